@@ -1,0 +1,277 @@
+// runtime.cpp -- device init, error reporting, weight residency, state mirrors.
+#include "runtime.h"
+
+#include <stdarg.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include <unordered_map>
+#include <vector>
+
+extern "C" int draco_repack(int code, const uint8_t* src, int n_out, int n_in, uint8_t* dst);
+
+namespace draco {
+
+namespace {
+
+struct MatEntry {
+    DracoMat m;
+    int code, n_out, n_in;
+    uint64_t fp;  // sampled fingerprint of the host bytes at registration
+};
+
+struct Mirror {
+    void* dev = nullptr;
+    size_t bytes = 0;
+};
+
+struct State {
+    bool inited = false;
+    int device = 0;
+    hipStream_t st = nullptr;
+    std::unordered_map<const void*, MatEntry> mats;
+    std::unordered_map<const void*, Mirror> mirrors;
+    std::vector<std::pair<void*, size_t>> scr;
+    std::vector<std::pair<void*, size_t>> pin;
+    size_t resident = 0;
+    std::string err;
+};
+
+State& S() {
+    static State* s = new State();  // never destroyed: device memory lives to process end
+    return *s;
+}
+
+// FNV-1a over 64 evenly spaced 8-byte samples plus the length.  Detects a
+// different buffer reusing a freed address; not a content hash.
+uint64_t fingerprint(const void* host, size_t bytes) {
+    const uint8_t* p = (const uint8_t*)host;
+    uint64_t h = 1469598103934665603ull ^ bytes;
+    if (bytes < 8) {
+        for (size_t i = 0; i < bytes; i++) h = (h ^ p[i]) * 1099511628211ull;
+        return h;
+    }
+    for (int i = 0; i < 64; i++) {
+        const size_t off = (bytes - 8) * (size_t)i / 63;
+        uint64_t w;
+        memcpy(&w, p + off, 8);
+        h = (h ^ w) * 1099511628211ull;
+    }
+    return h;
+}
+
+}  // namespace
+
+std::recursive_mutex& api_mutex() {
+    static std::recursive_mutex* m = new std::recursive_mutex();
+    return *m;
+}
+
+int fail(int rc, const char* fmt, ...) {
+    char buf[1024];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    S().err = buf;
+    if (getenv("DRACO_VERBOSE")) fprintf(stderr, "[draco] %s\n", buf);
+    return rc;
+}
+
+const char* last_error() { return S().err.c_str(); }
+
+int ensure_init() {
+    State& s = S();
+    if (s.inited) return 0;
+    const char* dv = getenv("DRACO_DEVICE");
+    s.device = dv ? atoi(dv) : 0;
+    int n = 0;
+    DRACO_HIP(hipGetDeviceCount(&n));
+    if (n <= s.device) return fail(-2, "no HIP device %d (count %d)", s.device, n);
+    DRACO_HIP(hipSetDevice(s.device));
+    DRACO_HIP(hipStreamCreateWithFlags(&s.st, hipStreamNonBlocking));
+    s.inited = true;
+    return 0;
+}
+
+hipStream_t stream() { return S().st; }
+
+const DracoMat* get_mat(const void* host, int code, int n_out, int n_in) {
+    State& s = S();
+    if (ensure_init()) return nullptr;
+    const size_t hb = draco_row_bytes(code, n_in) * (size_t)n_out;
+    if (hb == 0) {
+        fail(-1, "unsupported format code %d (n_in %d)", code, n_in);
+        return nullptr;
+    }
+    const uint64_t fp = fingerprint(host, hb);
+    auto it = s.mats.find(host);
+    if (it != s.mats.end()) {
+        MatEntry& e = it->second;
+        if (e.code == code && e.n_in == n_in && e.n_out >= n_out && e.fp == fingerprint(host, draco_row_bytes(code, n_in) * (size_t)e.n_out))
+            return &e.m;
+        hipFree(e.m.dev);
+        s.resident -= e.m.L.bytes;
+        s.mats.erase(it);
+    }
+    MatEntry e;
+    if (draco_layout(code, n_out, n_in, &e.m.L)) {
+        fail(-1, "no device layout for code %d shape %dx%d", code, n_out, n_in);
+        return nullptr;
+    }
+    e.code = code;
+    e.n_out = n_out;
+    e.n_in = n_in;
+    e.fp = fp;
+    hipError_t he = hipMalloc(&e.m.dev, e.m.L.bytes);
+    if (he != hipSuccess) {
+        fail(-2, "hipMalloc(%zu) for weights failed: %s", e.m.L.bytes, hipGetErrorString(he));
+        return nullptr;
+    }
+    uint8_t* stage = (uint8_t*)pinned(0, e.m.L.bytes);
+    if (!stage) return nullptr;
+    memset(stage, 0, e.m.L.bytes);
+    draco_repack(code, (const uint8_t*)host, n_out, n_in, stage);
+    he = hipMemcpyAsync(e.m.dev, stage, e.m.L.bytes, hipMemcpyHostToDevice, s.st);
+    if (he == hipSuccess) he = hipStreamSynchronize(s.st);
+    if (he != hipSuccess) {
+        hipFree(e.m.dev);
+        fail(-2, "weight upload failed: %s", hipGetErrorString(he));
+        return nullptr;
+    }
+    s.resident += e.m.L.bytes;
+    auto res = s.mats.emplace(host, e);
+    return &res.first->second.m;
+}
+
+int forget(const void* host) {
+    State& s = S();
+    int n = 0;
+    auto it = s.mats.find(host);
+    if (it != s.mats.end()) {
+        hipFree(it->second.m.dev);
+        s.resident -= it->second.m.L.bytes;
+        s.mats.erase(it);
+        n++;
+    }
+    auto mt = s.mirrors.find(host);
+    if (mt != s.mirrors.end()) {
+        hipFree(mt->second.dev);
+        s.mirrors.erase(mt);
+        n++;
+    }
+    return n;
+}
+
+void forget_all() {
+    State& s = S();
+    if (s.st) hipStreamSynchronize(s.st);
+    for (auto& kv : s.mats) hipFree(kv.second.m.dev);
+    s.mats.clear();
+    for (auto& kv : s.mirrors) hipFree(kv.second.dev);
+    s.mirrors.clear();
+    s.resident = 0;
+}
+
+size_t resident_bytes() { return S().resident; }
+
+void* get_mirror(const void* host, size_t bytes, bool* fresh) {
+    State& s = S();
+    if (ensure_init()) return nullptr;
+    auto it = s.mirrors.find(host);
+    if (it != s.mirrors.end() && it->second.bytes >= bytes && it->second.dev) {
+        if (fresh) *fresh = false;
+        return it->second.dev;
+    }
+    if (it != s.mirrors.end()) {
+        hipStreamSynchronize(s.st);
+        hipFree(it->second.dev);
+        s.mirrors.erase(it);
+    }
+    Mirror m;
+    hipError_t he = hipMalloc(&m.dev, bytes);
+    if (he != hipSuccess) {
+        fail(-2, "hipMalloc(%zu) for state mirror failed: %s", bytes, hipGetErrorString(he));
+        return nullptr;
+    }
+    m.bytes = bytes;
+    s.mirrors[host] = m;
+    if (fresh) *fresh = true;
+    return m.dev;
+}
+
+int mirror_invalidate(const void* host) {
+    State& s = S();
+    auto it = s.mirrors.find(host);
+    if (it == s.mirrors.end()) return 0;
+    hipStreamSynchronize(s.st);
+    hipFree(it->second.dev);
+    s.mirrors.erase(it);
+    return 1;
+}
+
+int mirror_pull(const void* host, size_t bytes) {
+    State& s = S();
+    auto it = s.mirrors.find(host);
+    if (it == s.mirrors.end()) return fail(-1, "no device mirror for host buffer %p", host);
+    if (bytes > it->second.bytes) bytes = it->second.bytes;
+    DRACO_HIP(hipMemcpyAsync((void*)host, it->second.dev, bytes, hipMemcpyDeviceToHost, s.st));
+    DRACO_HIP(hipStreamSynchronize(s.st));
+    return 0;
+}
+
+int mirror_push(const void* host, size_t bytes) {
+    bool fresh = false;
+    void* d = get_mirror(host, bytes, &fresh);
+    if (!d) return -2;
+    DRACO_HIP(hipMemcpyAsync(d, host, bytes, hipMemcpyHostToDevice, S().st));
+    DRACO_HIP(hipStreamSynchronize(S().st));
+    return 0;
+}
+
+void* scratch(int slot, size_t bytes) {
+    State& s = S();
+    if (ensure_init()) return nullptr;
+    if ((int)s.scr.size() <= slot) s.scr.resize(slot + 1, {nullptr, 0});
+    auto& e = s.scr[slot];
+    if (e.second < bytes) {
+        if (e.first) {
+            hipStreamSynchronize(s.st);
+            hipFree(e.first);
+        }
+        size_t cap = bytes < 4096 ? 4096 : bytes;
+        hipError_t he = hipMalloc(&e.first, cap);
+        if (he != hipSuccess) {
+            e = {nullptr, 0};
+            fail(-2, "hipMalloc(%zu) scratch failed: %s", cap, hipGetErrorString(he));
+            return nullptr;
+        }
+        e.second = cap;
+    }
+    return e.first;
+}
+
+void* pinned(int slot, size_t bytes) {
+    State& s = S();
+    if (ensure_init()) return nullptr;
+    if ((int)s.pin.size() <= slot) s.pin.resize(slot + 1, {nullptr, 0});
+    auto& e = s.pin[slot];
+    if (e.second < bytes) {
+        if (e.first) {
+            hipStreamSynchronize(s.st);
+            hipHostFree(e.first);
+        }
+        size_t cap = bytes < 65536 ? 65536 : bytes;
+        hipError_t he = hipHostMalloc(&e.first, cap, hipHostMallocDefault);
+        if (he != hipSuccess) {
+            e = {nullptr, 0};
+            fail(-2, "hipHostMalloc(%zu) failed: %s", cap, hipGetErrorString(he));
+            return nullptr;
+        }
+        e.second = cap;
+    }
+    return e.first;
+}
+
+}  // namespace draco

@@ -1,0 +1,113 @@
+"""ctypes binding of libdraco_hip.so (the HIP product library).
+
+Loading fails loudly when the library has not been built: there is no CPU
+fallback anywhere on the product path.
+"""
+import ctypes as ct
+import os
+
+import numpy as np
+
+PKG = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+LIB_PATH = os.environ.get("DRACO_HIP_SO", os.path.join(PKG, "lib", "libdraco_hip.so"))
+
+f32p = ct.POINTER(ct.c_float)
+u8p = ct.POINTER(ct.c_uint8)
+i32p = ct.POINTER(ct.c_int)
+
+_LIB = None
+
+
+def pf(a):
+    return a.ctypes.data_as(f32p)
+
+
+def pu8(a):
+    return a.ctypes.data_as(u8p)
+
+
+def pi32(a):
+    return a.ctypes.data_as(i32p)
+
+
+def vp(a):
+    return ct.c_void_p(a.ctypes.data)
+
+
+# name -> (restype, argtypes).  Mirrors include/draco_hip.h.
+SIGNATURES = {
+    # m5 kernel-library ABI (src/m5_kern_scalar.c:146-165)
+    "m5_scalar_supported": (ct.c_int, [ct.c_int]),
+    "m5_gemv": (ct.c_int, [ct.c_int, f32p, u8p, ct.c_int, ct.c_int, f32p]),
+    "m5_gemv_range": (ct.c_int, [ct.c_int, f32p, u8p, ct.c_int, ct.c_int, f32p, ct.c_int, ct.c_int]),
+    # library utilities
+    "draco_last_error": (ct.c_char_p, []),
+    "draco_forget": (ct.c_int, [ct.c_void_p]),
+    "draco_reset": (None, []),
+    "draco_resident_bytes": (ct.c_size_t, []),
+    "draco_version": (ct.c_char_p, []),
+    "draco_bench_gemv": (ct.c_int, [ct.c_int, u8p, ct.c_int, ct.c_int, ct.c_int, ct.c_int, f32p]),
+    "draco_bench_launch": (ct.c_int, [ct.c_int, f32p]),
+    "draco_quantize": (ct.c_int, [ct.c_int, f32p, ct.c_int, ct.c_int, u8p]),
+    "draco_layout_query": (ct.c_size_t, [ct.c_int, ct.c_int, ct.c_int, ct.POINTER(ct.c_size_t)]),
+    "draco_repack": (ct.c_int, [ct.c_int, u8p, ct.c_int, ct.c_int, u8p]),
+    "draco_unpack": (ct.c_int, [ct.c_int, u8p, ct.c_int, ct.c_int, u8p]),
+    "draco_rope_table": (None, [ct.c_int, ct.c_int, ct.c_float, f32p]),
+    "draco_f16_to_f32": (ct.c_float, [ct.c_uint16]),
+    "draco_f32_to_f16": (ct.c_uint16, [ct.c_float]),
+}
+
+
+def load():
+    """Return the loaded library (cached).  Raises if it is not built."""
+    global _LIB
+    if _LIB is not None:
+        return _LIB
+    if not os.path.exists(LIB_PATH):
+        raise RuntimeError(f"libdraco_hip.so not built at {LIB_PATH}: run __graft_entry__.build()")
+    lib = ct.CDLL(LIB_PATH)
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _LIB = lib
+    return lib
+
+
+def last_error():
+    return load().draco_last_error().decode(errors="replace")
+
+
+def check(rc, what="call"):
+    if rc != 0:
+        raise RuntimeError(f"{what} failed rc={rc}: {last_error()}")
+    return rc
+
+
+def quantize(code, x):
+    """Encode a 2-D float32 array into GGUF rows of `code` (0 Q8_0, 4 Q6_K, 5 Q4_K)."""
+    x = np.ascontiguousarray(x, np.float32)
+    if x.ndim == 1:
+        x = x[None, :]
+    n_rows, n_in = x.shape
+    out = np.empty(n_rows * row_bytes(code, n_in), np.uint8)
+    check(load().draco_quantize(code, pf(x), n_rows, n_in, pu8(out)), "draco_quantize")
+    return out
+
+
+def row_bytes(code, n_in):
+    return {0: (n_in // 32) * 34, 3: (n_in // 256) * 176, 4: (n_in // 256) * 210,
+            5: (n_in // 256) * 144, 7: n_in * 2, 9: n_in * 4}[code]
+
+
+def gemv(code, x, W, n_out, n_in, o0=None, o1=None):
+    """Host-pointer m5_gemv / m5_gemv_range through the C ABI; returns y."""
+    lib = load()
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.zeros(n_out, np.float32)
+    if o0 is None:
+        rc = lib.m5_gemv(code, pf(x), pu8(W), n_out, n_in, pf(y))
+    else:
+        rc = lib.m5_gemv_range(code, pf(x), pu8(W), n_out, n_in, pf(y), o0, o1)
+    check(rc, "m5_gemv")
+    return y

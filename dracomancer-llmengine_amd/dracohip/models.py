@@ -1,0 +1,143 @@
+"""Seeded synthetic models of the benchmark configurations, in GGUF byte format.
+
+Convention (the reference defines none; fixed here and used everywhere):
+  * one numpy Generator per model, np.random.default_rng(seed);
+  * tensors are drawn in GGUF tensor order -- token_embd, then per layer
+    attn_q, attn_k, attn_v, attn_output, ffn_gate, ffn_up, ffn_down, then
+    output (only when the head is not tied to the embedding);
+  * each tensor is rng.standard_normal((n_out, n_in), dtype=float32) * wscale
+    (0.02 for every benchmark configuration) and is encoded by draco_quantize (libdraco_hip.so, host code);
+  * every RMSNorm weight is 1.0;
+  * prompt ids: np.random.default_rng(seed + 1000).integers(0, vocab, n_prompt).
+
+The GPU path and the CPU oracle consume the same bytes, so the encoder only
+needs to be a valid GGUF encoder.
+"""
+import hashlib
+from dataclasses import dataclass, field
+
+import numpy as np
+
+from . import lib as _lib
+
+Q8_0, Q6_K, Q4_K, F16, F32 = 0, 4, 5, 7, 9
+
+
+@dataclass
+class LlamaConfig:
+    name: str
+    hidden: int
+    n_layer: int
+    n_head: int
+    n_kv: int
+    head_dim: int
+    n_ff: int
+    vocab: int
+    eps: float
+    rope_base: float
+    codes: dict  # tensor kind -> format code (q, k, v, o, gate, up, down, emb, out)
+    tied: bool = True
+    n_prompt: int = 32
+    n_gen: int = 64
+    max_t: int = 1024
+    chunk: int = 256
+    wscale: float = 0.02
+
+    @property
+    def rot(self):
+        return self.head_dim
+
+
+# configs[0] of BASELINE.json: SmolLM2-360M shape, all Q8_0, tied head.
+SMOL360M = LlamaConfig(
+    name="smollm2-360m-q8_0", hidden=960, n_layer=32, n_head=15, n_kv=5, head_dim=64, n_ff=2560,
+    vocab=49152, eps=1e-5, rope_base=100000.0,
+    codes=dict(q=Q8_0, k=Q8_0, v=Q8_0, o=Q8_0, gate=Q8_0, up=Q8_0, down=Q8_0, emb=Q8_0, out=Q8_0),
+    tied=True, n_prompt=32, n_gen=64, max_t=1024)
+
+# configs[2] of BASELINE.json: Llama-3.2-1B shape, Q4_K_M-style, tied head (Q6_K).
+LLAMA1B = LlamaConfig(
+    name="llama-3.2-1b-q4_k_m", hidden=2048, n_layer=16, n_head=32, n_kv=8, head_dim=64, n_ff=8192,
+    vocab=128256, eps=1e-5, rope_base=500000.0,
+    codes=dict(q=Q4_K, k=Q4_K, v=Q6_K, o=Q4_K, gate=Q4_K, up=Q4_K, down=Q6_K, emb=Q6_K, out=Q6_K),
+    tied=True, n_prompt=960, n_gen=64, max_t=1024)
+
+# small shapes for tests
+TINY_K = LlamaConfig(
+    name="tiny-kquant", hidden=512, n_layer=2, n_head=8, n_kv=2, head_dim=64, n_ff=1024, vocab=1000,
+    eps=1e-5, rope_base=10000.0,
+    codes=dict(q=Q4_K, k=Q4_K, v=Q6_K, o=Q4_K, gate=Q4_K, up=Q4_K, down=Q6_K, emb=Q6_K, out=Q6_K),
+    tied=True, n_prompt=8, n_gen=16, max_t=64, wscale=0.25)
+
+TINY_Q8 = LlamaConfig(
+    name="tiny-q8_0", hidden=192, n_layer=2, n_head=3, n_kv=1, head_dim=64, n_ff=256, vocab=600,
+    eps=1e-5, rope_base=100000.0,
+    codes=dict(q=Q8_0, k=Q8_0, v=Q8_0, o=Q8_0, gate=Q8_0, up=Q8_0, down=Q8_0, emb=Q8_0, out=Q8_0),
+    tied=True, n_prompt=8, n_gen=16, max_t=64, wscale=0.25)
+
+CONFIGS = {c.name: c for c in (SMOL360M, LLAMA1B, TINY_K, TINY_Q8)}
+
+
+@dataclass
+class LlamaModel:
+    cfg: LlamaConfig
+    seed: int
+    tensors: dict = field(default_factory=dict)  # name -> (uint8 bytes, code, n_out, n_in)
+    norms: dict = field(default_factory=dict)    # name -> float32
+
+    def head(self):
+        name = "token_embd.weight" if self.cfg.tied else "output.weight"
+        return self.tensors[name]
+
+    def digest(self):
+        h = hashlib.sha256()
+        for name in sorted(self.tensors):
+            h.update(name.encode())
+            h.update(self.tensors[name][0].tobytes())
+        return h.hexdigest()
+
+    def prompt(self, n=None):
+        n = self.cfg.n_prompt if n is None else n
+        return np.random.default_rng(self.seed + 1000).integers(0, self.cfg.vocab, n).astype(np.int32)
+
+    def nbytes(self):
+        return sum(t[0].nbytes for t in self.tensors.values())
+
+
+def _draw(rng, n_out, n_in, wscale):
+    w = rng.standard_normal((n_out, n_in), dtype=np.float32)
+    w *= np.float32(wscale)
+    return w
+
+
+def _tensor(rng, code, n_out, n_in, wscale=0.02, rows_per_chunk=16384):
+    out = np.empty(n_out * _lib.row_bytes(code, n_in), np.uint8)
+    rb = _lib.row_bytes(code, n_in)
+    # draw in row chunks (same stream order as one big draw) to bound memory
+    for r0 in range(0, n_out, rows_per_chunk):
+        r1 = min(n_out, r0 + rows_per_chunk)
+        w = _draw(rng, r1 - r0, n_in, wscale)
+        out[r0 * rb:r1 * rb] = _lib.quantize(code, w)
+    return out
+
+
+def build_llama(cfg, seed=0):
+    rng = np.random.default_rng(seed)
+    m = LlamaModel(cfg=cfg, seed=seed)
+    H, QD, KD = cfg.hidden, cfg.n_head * cfg.head_dim, cfg.n_kv * cfg.head_dim
+    c = cfg.codes
+    ws = cfg.wscale
+    m.tensors["token_embd.weight"] = (_tensor(rng, c["emb"], cfg.vocab, H, ws), c["emb"], cfg.vocab, H)
+    for il in range(cfg.n_layer):
+        p = f"blk.{il}."
+        for kind, n_out, n_in in (("q", QD, H), ("k", KD, H), ("v", KD, H), ("o", H, QD),
+                                  ("gate", cfg.n_ff, H), ("up", cfg.n_ff, H), ("down", H, cfg.n_ff)):
+            tname = {"q": "attn_q", "k": "attn_k", "v": "attn_v", "o": "attn_output",
+                     "gate": "ffn_gate", "up": "ffn_up", "down": "ffn_down"}[kind]
+            m.tensors[p + tname + ".weight"] = (_tensor(rng, c[kind], n_out, n_in, ws), c[kind], n_out, n_in)
+        m.norms[p + "attn_norm.weight"] = np.ones(H, np.float32)
+        m.norms[p + "ffn_norm.weight"] = np.ones(H, np.float32)
+    if not cfg.tied:
+        m.tensors["output.weight"] = (_tensor(rng, c["out"], cfg.vocab, H, ws), c["out"], cfg.vocab, H)
+    m.norms["output_norm.weight"] = np.ones(H, np.float32)
+    return m

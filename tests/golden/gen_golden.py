@@ -1,0 +1,265 @@
+"""Write the golden fixtures under tests/golden/ from the reference's own C.
+
+Runs only where the reference tree exists and `make -C oracle ref` built
+oracle/_ref/*.so (the reference's sources compiled in place).  Every output
+array here is produced by the compiled reference (src/m5_kern_scalar.c,
+src/m5/m5_batch8_k.c, src/m6_engine.c + m6_layer.c, src/m6_gdn_scan.c) on
+seeded inputs; the inputs are regenerated deterministically by the tests
+(weights via dracohip.models, vectors via numpy default_rng) or stored when
+small.
+
+usage: python tests/golden/gen_golden.py [--only NAME ...]
+"""
+import argparse
+import ctypes as ct
+import hashlib
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.dirname(os.path.dirname(os.path.abspath(__file__))))
+sys.path.insert(0, os.path.join(ROOT, "dracomancer-llmengine_amd"))
+sys.path.insert(0, ROOT)
+
+from dracohip import lib as dlib  # noqa: E402
+from dracohip import models  # noqa: E402
+from dracohip.driver import EngineLib, LlamaDriver  # noqa: E402
+from oracle.oracle import REF_DIR  # noqa: E402
+
+OUT = os.path.dirname(os.path.abspath(__file__))
+f32p = ct.POINTER(ct.c_float)
+u8p = ct.POINTER(ct.c_uint8)
+i32p = ct.POINTER(ct.c_int)
+
+
+def pf(a):
+    return a.ctypes.data_as(f32p)
+
+
+def pu8(a):
+    return a.ctypes.data_as(u8p)
+
+
+def ref(name):
+    return ct.CDLL(os.path.join(REF_DIR, f"libref_{name}.so"))
+
+
+# ---------------------------------------------------------------- inputs --
+GEMV_CASES = [  # (name, code, n_out, n_in)
+    ("q4k_48x512", 5, 48, 512), ("q4k_33x768", 5, 33, 768), ("q4k_5x2048", 5, 5, 2048),
+    ("q6k_48x512", 4, 48, 512), ("q6k_33x768", 4, 33, 768), ("q6k_5x2048", 4, 5, 2048),
+    ("q80_40x960", 0, 40, 960), ("q80_7x64", 0, 7, 64),
+    ("q5k_16x512", 3, 16, 512), ("f16_10x96", 7, 10, 96), ("f32_10x96", 9, 10, 96),
+]
+
+
+def gemv_inputs(code, n_out, n_in, seed):
+    """Seeded weight bytes + x.  Shared by the generator and the tests."""
+    rng = np.random.default_rng(seed)
+    if code in (0, 4, 5):
+        W = dlib.quantize(code, rng.standard_normal((n_out, n_in), dtype=np.float32) * np.float32(0.02))
+    elif code == 3:  # Q5_K: random qs/qh/scales with finite positive d, dmin
+        nb = n_in // 256
+        W = rng.integers(0, 256, n_out * nb * 176, dtype=np.uint8).reshape(-1, 176)
+        d = (rng.random(W.shape[0]) * 1e-3 + 1e-4).astype(np.float16).view(np.uint8).reshape(-1, 2)
+        dm = (rng.random(W.shape[0]) * 1e-3).astype(np.float16).view(np.uint8).reshape(-1, 2)
+        W[:, 0:2] = d
+        W[:, 2:4] = dm
+        W = W.reshape(-1)
+    elif code == 7:
+        W = (rng.standard_normal(n_out * n_in) * 0.1).astype(np.float16).view(np.uint8)
+    else:
+        W = (rng.standard_normal(n_out * n_in) * 0.1).astype(np.float32).view(np.uint8)
+    x = rng.standard_normal(n_in, dtype=np.float32)
+    return np.ascontiguousarray(W), x
+
+
+def gen_gemv():
+    L = ref("scalar")
+    L.m5_gemv.argtypes = [ct.c_int, f32p, u8p, ct.c_int, ct.c_int, f32p]
+    L.m5_gemv_range.argtypes = [ct.c_int, f32p, u8p, ct.c_int, ct.c_int, f32p, ct.c_int, ct.c_int]
+    L.m5_scalar_supported.argtypes = [ct.c_int]
+    out = {}
+    for i, (name, code, n_out, n_in) in enumerate(GEMV_CASES):
+        W, x = gemv_inputs(code, n_out, n_in, 100 + i)
+        y = np.zeros(n_out, np.float32)
+        assert L.m5_gemv(code, pf(x), pu8(W), n_out, n_in, pf(y)) == 0
+        yr = np.full(n_out, np.float32(-7.0))
+        o0, o1 = n_out // 3, n_out - 1
+        assert L.m5_gemv_range(code, pf(x), pu8(W), n_out, n_in, pf(yr), o0, o1) == 0
+        onehot = np.zeros(n_in, np.float32)
+        col = (n_in * 5) // 7
+        onehot[col] = 1.0
+        yc = np.zeros(n_out, np.float32)
+        assert L.m5_gemv(code, pf(onehot), pu8(W), n_out, n_in, pf(yc)) == 0
+        out[name + "_y"] = y
+        out[name + "_yrange"] = yr
+        out[name + "_meta"] = np.array([code, n_out, n_in, o0, o1, col], np.int64)
+        out[name + "_col"] = yc
+    out["supported"] = np.array([L.m5_scalar_supported(c) for c in range(12)], np.int32)
+    # rms norm (src/m6_engine.c:31-37)
+    E = ref("engine")
+    E.m6_rms_norm.argtypes = [f32p, f32p, ct.c_int, ct.c_float, f32p]
+    rng = np.random.default_rng(7)
+    for h in (960, 2048):
+        xx = rng.standard_normal(h, dtype=np.float32) * np.float32(3.0)
+        ww = rng.standard_normal(h, dtype=np.float32)
+        o = np.zeros(h, np.float32)
+        E.m6_rms_norm(pf(xx), pf(ww), h, ct.c_float(1e-5), pf(o))
+        out[f"rms{h}_x"], out[f"rms{h}_w"], out[f"rms{h}_y"] = xx, ww, o
+    np.savez_compressed(os.path.join(OUT, "gemv.npz"), **out)
+    print("gemv.npz", len(GEMV_CASES), "cases")
+
+
+BATCH8K_CASES = [  # (tag, code, x_stride_kind)
+    ("q4k_shared", 5, 0), ("q4k_perexp", 5, 1), ("q6k_shared", 4, 0), ("q6k_perexp", 4, 1),
+]
+
+
+def batch8k_inputs(code, perexp, seed):
+    """Seeded inputs of m5_gemvn_q4k/q6k: 5 experts of 100x512, idx [3,0,4]."""
+    rng = np.random.default_rng(seed)
+    n_exp_all, n_out_e, n_in = 5, 100, 512
+    W = dlib.quantize(code, rng.standard_normal((n_exp_all * n_out_e, n_in), dtype=np.float32)
+                      * np.float32(0.02))
+    idx = np.array([3, 0, 4], np.int32)
+    xstride = n_in if perexp else 0
+    x = rng.standard_normal((len(idx) if perexp else 1) * n_in, dtype=np.float32)
+    return W, x, idx, W.nbytes // n_exp_all, n_out_e, n_in, xstride
+
+
+def gen_batch8k():
+    B = ref("batch8k")
+    for fn in (B.m5_gemvn_q4k, B.m5_gemvn_q6k):
+        fn.argtypes = [f32p, ct.c_long, u8p, i32p, ct.c_long, ct.c_int, ct.c_int, ct.c_int, f32p]
+        fn.restype = ct.c_int
+    out = {}
+    for i, (tag, code, perexp) in enumerate(BATCH8K_CASES):
+        W, x, idx, per, n_out_e, n_in, xstride = batch8k_inputs(code, perexp, 40 + i)
+        fn = B.m5_gemvn_q4k if code == 5 else B.m5_gemvn_q6k
+        y = np.zeros(len(idx) * n_out_e, np.float32)
+        assert fn(pf(x), xstride, pu8(W), idx.ctypes.data_as(i32p), per, n_out_e, n_in, len(idx), pf(y)) == 0
+        out[tag + "_y"] = y
+    np.savez_compressed(os.path.join(OUT, "batch8k.npz"), **out)
+    print("batch8k.npz")
+
+
+def ref_engine():
+    E = ref("engine")
+    E.m6_init_dl.argtypes = [ct.c_char_p] * 5
+    E.m6_init_dl.restype = ct.c_int
+    sp = os.path.join(REF_DIR, "libref_scalar.so").encode()
+    rc = E.m6_init_dl(sp, sp, sp, sp, sp)  # the reference's own scalar mode (src/m5sel.py:13-14)
+    assert rc == 0, rc
+    return E
+
+
+def gen_llama(cfg, fname, seed=0, logit_steps=(0,)):
+    t0 = time.time()
+    model = models.build_llama(cfg, seed)
+    E = EngineLib(ref_engine(), name="ref")
+    drv = LlamaDriver(model, E)
+    prompt = model.prompt()
+    toks, hidden, lg = drv.greedy(prompt, cfg.n_gen, collect_logits=logit_steps)
+    out = dict(tokens=np.array(toks, np.int32), hidden=hidden, prompt=prompt,
+               digest=np.frombuffer(bytes.fromhex(model.digest()), np.uint8))
+    for s, v in lg.items():
+        # full logits only for small vocabularies; top-8 (ids + values) always
+        top = np.argsort(-v.astype(np.float64), kind="stable")[:8]
+        out[f"logits{s}_top_ids"] = top.astype(np.int32)
+        out[f"logits{s}_top_vals"] = v[top]
+        if cfg.vocab <= 4096:
+            out[f"logits{s}"] = v
+    np.savez_compressed(os.path.join(OUT, fname), **out)
+    print(fname, cfg.name, f"{time.time() - t0:.1f}s", "tokens", toks[:8], "...")
+
+
+def gen_moe():
+    """m6_granite_moe (src/m6_layer.c:771-802) on a small and a cfg4-shaped layer."""
+    E = ref_engine()
+    E.m6_granite_moe.argtypes = [f32p, ct.c_void_p, i32p, f32p, ct.c_int, ct.c_int, ct.c_int, ct.c_int,
+                                 ct.c_int, f32p, f32p]
+    out = {}
+    for tag, n_exp, n_used, inter, n_in, seed in (("small", 16, 4, 256, 512, 21), ("cfg4", 128, 8, 768, 2048, 22)):
+        rng = np.random.default_rng(seed)
+        gate_inp = (rng.standard_normal((n_exp, n_in), dtype=np.float32) * np.float32(0.02))
+        # expert bytes are regenerated by the test from the same seed stream
+        Wg = dlib.quantize(5, rng.standard_normal((n_exp * inter, n_in), dtype=np.float32) * np.float32(0.02))
+        Wu = dlib.quantize(5, rng.standard_normal((n_exp * inter, n_in), dtype=np.float32) * np.float32(0.02))
+        Wd = dlib.quantize(4, rng.standard_normal((n_exp * n_in, inter), dtype=np.float32) * np.float32(0.02))
+        x = rng.standard_normal(n_in, dtype=np.float32)
+        pg, pu, pd = Wg.nbytes // n_exp, Wu.nbytes // n_exp, Wd.nbytes // n_exp
+        ptrs = np.zeros(3 * n_exp, np.uint64)
+        codes = np.zeros(3 * n_exp, np.int32)
+        for e in range(n_exp):
+            ptrs[3 * e] = Wg.ctypes.data + e * pg
+            ptrs[3 * e + 1] = Wu.ctypes.data + e * pu
+            ptrs[3 * e + 2] = Wd.ctypes.data + e * pd
+            codes[3 * e:3 * e + 3] = (5, 5, 4)
+        scratch = np.zeros(3 * n_used * inter + n_used * n_in + 64, np.float32)
+        y = np.zeros(n_in, np.float32)
+        E.m6_granite_moe(pf(x), ct.c_void_p(ptrs.ctypes.data), codes.ctypes.data_as(i32p), pf(gate_inp),
+                         n_exp, n_used, inter, n_in, n_in, pf(scratch), pf(y))
+        out[f"{tag}_y"] = y
+        out[f"{tag}_meta"] = np.array([n_exp, n_used, inter, n_in, seed], np.int64)
+        out[f"{tag}_digest"] = np.frombuffer(hashlib.sha256(Wg.tobytes() + Wu.tobytes() + Wd.tobytes()).digest(), np.uint8)
+    np.savez_compressed(os.path.join(OUT, "moe.npz"), **out)
+    print("moe.npz")
+
+
+def gdn_inputs(T, n_vh, nhq, seed):
+    rng = np.random.default_rng(seed)
+    n_qkv = n_vh * 128 + 2 * nhq * 128
+    QKV = rng.standard_normal((T, n_qkv), dtype=np.float32)
+    Z = rng.standard_normal((T, n_vh * 128), dtype=np.float32)
+    B = (1.0 / (1.0 + np.exp(-rng.standard_normal((T, n_vh))))).astype(np.float32)
+    G = np.exp(-np.logaddexp(0.0, rng.standard_normal((T, n_vh)))).astype(np.float32)
+    conv = (rng.standard_normal((n_qkv, 4), dtype=np.float32) * np.float32(0.5))
+    ssm_norm = (1.0 + 0.1 * rng.standard_normal(128)).astype(np.float32)
+    tail = rng.standard_normal(n_qkv * 3, dtype=np.float32)
+    S = (rng.standard_normal(n_vh * 128 * 128, dtype=np.float32) * np.float32(0.05))
+    return n_qkv, QKV, Z, B, G, conv, ssm_norm, tail, S
+
+
+def gen_gdn():
+    L = ref("gdnscan")
+    L.m6_gdn_scan.argtypes = [f32p] * 8 + [ct.c_int] * 3 + [f32p, f32p]
+    out = {}
+    for tag, T, n_vh, nhq, seed in (("a", 6, 2, 1, 31), ("b", 5, 4, 2, 32)):
+        n_qkv, QKV, Z, B, G, conv, ssm_norm, tail, S = gdn_inputs(T, n_vh, nhq, seed)
+        ON = np.zeros((T, n_vh * 128), np.float32)
+        work = np.zeros(n_qkv, np.float32)
+        L.m6_gdn_scan(pf(QKV), pf(Z), pf(B), pf(G), pf(conv), pf(ssm_norm), pf(tail), pf(S),
+                      T, n_qkv, n_vh, pf(ON), pf(work))
+        out[f"{tag}_ON"] = ON
+        out[f"{tag}_S_sha"] = np.frombuffer(hashlib.sha256(S.tobytes()).digest(), np.uint8)
+        out[f"{tag}_tail_sha"] = np.frombuffer(hashlib.sha256(tail.tobytes()).digest(), np.uint8)
+        out[f"{tag}_S_sample"] = S[::997].copy()
+        out[f"{tag}_meta"] = np.array([T, n_vh, nhq, seed], np.int64)
+    np.savez_compressed(os.path.join(OUT, "gdn.npz"), **out)
+    print("gdn.npz")
+
+
+JOBS = {
+    "gemv": gen_gemv,
+    "batch8k": gen_batch8k,
+    "moe": gen_moe,
+    "gdn": gen_gdn,
+    "tiny_k": lambda: gen_llama(models.TINY_K, "llama_tiny_k.npz", logit_steps=(0, 15)),
+    "tiny_q8": lambda: gen_llama(models.TINY_Q8, "llama_tiny_q8.npz", logit_steps=(0, 15)),
+    "smol360m": lambda: gen_llama(models.SMOL360M, "smol360m.npz", logit_steps=(0, 63)),
+    "llama1b": lambda: gen_llama(models.LLAMA1B, "llama1b.npz", logit_steps=(0, 63)),
+}
+
+if __name__ == "__main__":
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--only", nargs="*", default=[k for k in JOBS if k != "llama1b"])
+    a = ap.parse_args()
+    for k in a.only:
+        JOBS[k]()
+    with open(os.path.join(OUT, "README.json"), "w") as f:
+        json.dump({k: "generated by gen_golden.py from oracle/_ref (the reference's C compiled in place)"
+                   for k in JOBS}, f, indent=1)

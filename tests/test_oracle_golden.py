@@ -1,0 +1,131 @@
+"""The CPU oracle (oracle/draco_oracle.c) against fixtures written by the
+reference's own C (tests/golden/gen_golden.py drives oracle/_ref).
+
+Bar: bit-identical outputs on identical inputs.
+"""
+import ctypes as ct
+
+import numpy as np
+import pytest
+
+from helpers import bits_equal, golden
+import gen_golden as gg
+from dracohip import models
+from dracohip.driver import EngineLib, LlamaDriver
+from oracle.oracle import pf, pu8, pi32
+
+
+@pytest.mark.parametrize("case", [c[0] for c in gg.GEMV_CASES])
+def test_gemv_matches_reference(oracle, case):
+    g = golden("gemv.npz")
+    i = [c[0] for c in gg.GEMV_CASES].index(case)
+    _, code, n_out, n_in = gg.GEMV_CASES[i]
+    W, x = gg.gemv_inputs(code, n_out, n_in, 100 + i)
+    y = oracle.gemv(code, x, W, n_out, n_in)
+    assert bits_equal(y, g[case + "_y"]), (case, np.max(np.abs(y - g[case + "_y"])))
+    code_, n_out_, n_in_, o0, o1, col = g[case + "_meta"]
+    yr = np.full(n_out, np.float32(-7.0))
+    oracle.gemv_range(code, x, W, n_out, n_in, int(o0), int(o1), yr)
+    assert bits_equal(yr, g[case + "_yrange"])  # rows outside [o0,o1) untouched
+    onehot = np.zeros(n_in, np.float32)
+    onehot[int(col)] = 1.0
+    assert bits_equal(oracle.gemv(code, onehot, W, n_out, n_in), g[case + "_col"])
+
+
+def test_supported_codes(oracle):
+    g = golden("gemv.npz")
+    assert [oracle.lib.or_supported(c) for c in range(12)] == list(g["supported"])
+
+
+@pytest.mark.parametrize("h", [960, 2048])
+def test_rms_norm(oracle, h):
+    g = golden("gemv.npz")
+    x, w = g[f"rms{h}_x"], g[f"rms{h}_w"]
+    o = np.zeros(h, np.float32)
+    oracle.lib.or_rms_norm(pf(x), pf(w), h, ct.c_float(1e-5), pf(o))
+    assert bits_equal(o, g[f"rms{h}_y"])
+
+
+@pytest.mark.parametrize("i", range(len(gg.BATCH8K_CASES)))
+def test_batch8k_lane_order(oracle, i):
+    """AVX-512 grouped GEMV (src/m5/m5_batch8_k.c) restated lane by lane."""
+    tag, code, perexp = gg.BATCH8K_CASES[i]
+    W, x, idx, per, n_out_e, n_in, xstride = gg.batch8k_inputs(code, perexp, 40 + i)
+    y = np.zeros(len(idx) * n_out_e, np.float32)
+    fn = oracle.lib.or_gemvn_q4k if code == 5 else oracle.lib.or_gemvn_q6k
+    assert fn(pf(x), xstride, pu8(W), pi32(idx), per, n_out_e, n_in, len(idx), pf(y)) == 0
+    assert bits_equal(y, golden("batch8k.npz")[tag + "_y"])
+
+
+@pytest.mark.parametrize("tag", ["a", "b"])
+def test_gdn_scan(oracle, tag):
+    import hashlib
+    g = golden("gdn.npz")
+    T, n_vh, nhq, seed = [int(v) for v in g[f"{tag}_meta"]]
+    n_qkv, QKV, Z, B, G, conv, ssm_norm, tail, S = gg.gdn_inputs(T, n_vh, nhq, seed)
+    ON = np.zeros((T, n_vh * 128), np.float32)
+    work = np.zeros(n_qkv, np.float32)
+    oracle.lib.or_gdn_scan(pf(QKV), pf(Z), pf(B), pf(G), pf(conv), pf(ssm_norm), pf(tail), pf(S),
+                           T, n_qkv, n_vh, pf(ON), pf(work))
+    assert bits_equal(ON, g[f"{tag}_ON"])
+    assert hashlib.sha256(S.tobytes()).digest() == g[f"{tag}_S_sha"].tobytes()
+    assert hashlib.sha256(tail.tobytes()).digest() == g[f"{tag}_tail_sha"].tobytes()
+
+
+@pytest.mark.parametrize("tag", ["small", "cfg4"])
+def test_granite_moe(oracle, tag):
+    import hashlib
+    from dracohip import lib as dlib
+    g = golden("moe.npz")
+    n_exp, n_used, inter, n_in, seed = [int(v) for v in g[f"{tag}_meta"]]
+    rng = np.random.default_rng(seed)
+    gate_inp = rng.standard_normal((n_exp, n_in), dtype=np.float32) * np.float32(0.02)
+    Wg = dlib.quantize(5, rng.standard_normal((n_exp * inter, n_in), dtype=np.float32) * np.float32(0.02))
+    Wu = dlib.quantize(5, rng.standard_normal((n_exp * inter, n_in), dtype=np.float32) * np.float32(0.02))
+    Wd = dlib.quantize(4, rng.standard_normal((n_exp * n_in, inter), dtype=np.float32) * np.float32(0.02))
+    x = rng.standard_normal(n_in, dtype=np.float32)
+    assert hashlib.sha256(Wg.tobytes() + Wu.tobytes() + Wd.tobytes()).digest() == g[f"{tag}_digest"].tobytes()
+    pg, pu, pd = Wg.nbytes // n_exp, Wu.nbytes // n_exp, Wd.nbytes // n_exp
+    ptrs = np.zeros(3 * n_exp, np.uint64)
+    codes = np.zeros(3 * n_exp, np.int32)
+    for e in range(n_exp):
+        ptrs[3 * e:3 * e + 3] = (Wg.ctypes.data + e * pg, Wu.ctypes.data + e * pu, Wd.ctypes.data + e * pd)
+        codes[3 * e:3 * e + 3] = (5, 5, 4)
+    scratch = np.zeros(3 * n_used * inter + n_used * n_in + 64, np.float32)
+    y = np.zeros(n_in, np.float32)
+    oracle.lib.or_granite_moe(pf(x), ct.c_void_p(ptrs.ctypes.data), pi32(codes), pf(gate_inp), n_exp,
+                              n_used, inter, n_in, n_in, pf(scratch), pf(y))
+    assert bits_equal(y, g[f"{tag}_y"])
+
+
+def oracle_engine(oracle):
+    return EngineLib(oracle.lib, forward="or_forward_token", head="or_head_op",
+                     attn="or_llama_attn_op", dense="or_dense_op", name="oracle")
+
+
+@pytest.mark.parametrize("cfgname,fname", [("tiny-kquant", "llama_tiny_k.npz"), ("tiny-q8_0", "llama_tiny_q8.npz")])
+def test_llama_decode_tiny(oracle, cfgname, fname):
+    """Token-serial prefill + greedy decode through the descriptor ABI, bitwise."""
+    g = golden(fname)
+    cfg = models.CONFIGS[cfgname]
+    model = models.build_llama(cfg, 0)
+    assert model.digest() == g["digest"].tobytes().hex()
+    drv = LlamaDriver(model, oracle_engine(oracle))
+    toks, hidden, lg = drv.greedy(model.prompt(), cfg.n_gen, collect_logits=(0, 15))
+    assert toks == list(g["tokens"])
+    assert bits_equal(hidden, g["hidden"])
+    assert bits_equal(lg[0], g["logits0"]) and bits_equal(lg[15], g["logits15"])
+
+
+@pytest.mark.slow
+def test_llama_decode_smol360m(oracle):
+    """SmolLM2-360M-shaped Q8_0, 32 prompt + 64 greedy tokens, bitwise."""
+    g = golden("smol360m.npz")
+    cfg = models.SMOL360M
+    model = models.build_llama(cfg, 0)
+    assert model.digest() == g["digest"].tobytes().hex()
+    drv = LlamaDriver(model, oracle_engine(oracle))
+    toks, hidden, lg = drv.greedy(model.prompt(), cfg.n_gen, collect_logits=(0, 63))
+    assert toks == list(g["tokens"])
+    assert bits_equal(hidden, g["hidden"])
+    assert bits_equal(lg[63][g["logits63_top_ids"]], g["logits63_top_vals"])
