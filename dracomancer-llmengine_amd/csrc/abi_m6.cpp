@@ -1,0 +1,695 @@
+// abi_m6.cpp -- the layer-engine ABI (drop-in for m6_engine.so's llama path).
+//
+// Reference: src/m6_engine.c:18-83 (descriptors, m6_forward_token),
+// :270-303 (M6DenseP, m6_dense_op), :373-391 (m6_head_op), :396-517
+// (M6LlamaAttnP, llama_attn_core, m6_llama_attn_op).  Struct layouts are the
+// reference's, field for field: Python callers allocate them through ctypes
+// (src/smol_engine.py:97-115).
+//
+// m6_forward_token recognises descriptors whose op pointers are this
+// library's own m6_llama_attn_op / m6_dense_op (Python takes them from the
+// same .so, src/smol_engine.py:117-118) and runs the whole token on the
+// device: weights resident (registry keyed by host address), KV caches as
+// device mirrors of the caller's kcache/vcache arrays, one host->device copy
+// of x in and one copy out.  The caller's tlen counters advance exactly as
+// the reference's do (src/m6_engine.c:510).
+#include <math.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <map>
+#include <unordered_map>
+#include <vector>
+
+#include "decode.h"
+#include "runtime.h"
+
+extern "C" {
+typedef void (*m6_attn_op)(const float* xn, void* p, int pos, float* out);
+typedef void (*m6_ffn_op)(const float* xn, void* p, float* out);
+
+typedef struct {
+    const float* attn_norm;
+    const float* ffn_norm;
+    m6_attn_op attn;
+    void* attn_p;
+    m6_ffn_op ffn;
+    void* ffn_p;
+} M6LayerDesc;
+
+typedef struct {
+    const uint8_t *wq, *wk, *wv, *wo;
+    int cq, ck, cv, co;
+    int n_head, n_kv, head_dim, hidden, rot;
+    float rope_base;
+    float* kcache;
+    float* vcache;
+    int* tlen;
+    int max_t;
+    float* work;
+} M6LlamaAttnP;
+
+typedef struct {
+    const uint8_t *g, *u, *d;
+    int cg, cu, cd, n_ff, h;
+} M6DenseP;
+
+void m6_llama_attn_op(const float* xn, void* p, int pos, float* out);
+void m6_dense_op(const float* xn, void* p, float* out);
+}
+
+using namespace draco;
+
+namespace {
+
+struct DevAttn {
+    uint64_t epoch = 0;
+    M6LlamaAttnP snap;
+    const DracoMat *wq, *wk, *wv, *wo;
+    float *kc, *vc;
+    int NH, NKV, HD, H, rot, max_t;
+    float base, scale;
+};
+
+struct DevFfn {
+    uint64_t epoch = 0;
+    M6DenseP snap;
+    const DracoMat *g, *u, *d;
+    int FF, H;
+};
+
+struct Work {
+    float *x = nullptr, *xn = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *att = nullptr,
+          *part = nullptr, *g = nullptr, *u = nullptr;
+    size_t cap_h = 0, cap_q = 0, cap_k = 0, cap_part = 0, cap_ff = 0;
+};
+
+struct DevModel {
+    uint64_t epoch = 0;
+    std::vector<M6LayerDesc> descs;
+    std::vector<DevAttn*> attn;
+    std::vector<DevFfn*> ffn;
+    std::vector<const float*> anorm, fnorm;
+    int h = 0, n_layer = 0;
+    Work w;
+    int* state = nullptr;   // device [1 + n_layer]
+    int* hstate = nullptr;  // pinned host mirror of state
+};
+
+struct RopeTab {
+    float* dev = nullptr;
+    int cap = 0;
+};
+
+std::unordered_map<const void*, DevAttn*>& attn_cache() {
+    static auto* m = new std::unordered_map<const void*, DevAttn*>();
+    return *m;
+}
+std::unordered_map<const void*, DevFfn*>& ffn_cache() {
+    static auto* m = new std::unordered_map<const void*, DevFfn*>();
+    return *m;
+}
+std::unordered_map<const void*, DevModel*>& model_cache() {
+    static auto* m = new std::unordered_map<const void*, DevModel*>();
+    return *m;
+}
+std::map<std::pair<int, float>, RopeTab>& rope_cache() {
+    static auto* m = new std::map<std::pair<int, float>, RopeTab>();
+    return *m;
+}
+struct NormEntry {
+    float* dev;
+    uint64_t epoch;
+};
+std::unordered_map<const void*, NormEntry>& norm_cache() {
+    static auto* m = new std::unordered_map<const void*, NormEntry>();
+    return *m;
+}
+
+extern "C" void draco_rope_table(int max_t, int rot, float base, float* tab);
+
+int report(int rc, const char* where) {
+    fprintf(stderr, "[draco_hip] %s failed (rc=%d): %s\n", where, rc, last_error());
+    return rc;
+}
+
+// device copy of a norm weight vector (immutable while registered)
+const float* norm_dev(const float* host, int h) {
+    if (!host) return nullptr;
+    auto& c = norm_cache();
+    auto it = c.find(host);
+    if (it != c.end() && it->second.epoch == epoch()) return it->second.dev;
+    float* d = it != c.end() ? it->second.dev : nullptr;
+    if (it != c.end()) {  // re-read after an eviction: the address may hold new data
+        hipStreamSynchronize(stream());
+        hipFree(d);
+        d = nullptr;
+    }
+    if (hipMalloc(&d, sizeof(float) * h) != hipSuccess) {
+        fail(-2, "hipMalloc for norm weights failed");
+        return nullptr;
+    }
+    if (hipMemcpy(d, host, sizeof(float) * h, hipMemcpyHostToDevice) != hipSuccess) {
+        fail(-2, "norm upload failed");
+        return nullptr;
+    }
+    c[host] = NormEntry{d, epoch()};
+    return d;
+}
+
+// rope angle table covering positions [0, need)
+const float* rope_dev(int rot, float base, int need) {
+    RopeTab& t = rope_cache()[{rot, base}];
+    if (t.cap >= need) return t.dev;
+    int cap = need < 1024 ? 1024 : need;
+    std::vector<float> h((size_t)cap * rot);
+    draco_rope_table(cap, rot, base, h.data());
+    if (t.dev) {
+        hipStreamSynchronize(stream());
+        hipFree(t.dev);
+    }
+    if (hipMalloc(&t.dev, sizeof(float) * h.size()) != hipSuccess) {
+        t = RopeTab();
+        fail(-2, "hipMalloc rope table failed");
+        return nullptr;
+    }
+    if (hipMemcpy(t.dev, h.data(), sizeof(float) * h.size(), hipMemcpyHostToDevice) != hipSuccess) {
+        fail(-2, "rope table upload failed");
+        return nullptr;
+    }
+    t.cap = cap;
+    return t.dev;
+}
+
+DevAttn* get_attn(const M6LlamaAttnP* p) {
+    auto& c = attn_cache();
+    auto it = c.find(p);
+    if (it != c.end() && it->second->epoch == epoch() && memcmp(&it->second->snap, p, sizeof(*p)) == 0)
+        return it->second;
+    const int NH = p->n_head, NKV = p->n_kv, HD = p->head_dim, H = p->hidden;
+    if (NH <= 0 || NKV <= 0 || NH % NKV || NH / NKV > 8 || (HD != 64 && HD != 128) || p->rot > HD ||
+        (p->rot & 1) || p->max_t <= 0) {
+        fail(-1, "m6_llama_attn_op: unsupported shape NH=%d NKV=%d HD=%d rot=%d", NH, NKV, HD, p->rot);
+        return nullptr;
+    }
+    DevAttn* a = (it != c.end()) ? it->second : new DevAttn();
+    a->snap = *p;
+    a->NH = NH; a->NKV = NKV; a->HD = HD; a->H = H; a->rot = p->rot; a->max_t = p->max_t;
+    a->base = p->rope_base;
+    a->scale = 1.0f / sqrtf((float)HD);
+    const int QD = NH * HD, KD = NKV * HD;
+    a->wq = get_mat(p->wq, p->cq, QD, H);
+    a->wk = get_mat(p->wk, p->ck, KD, H);
+    a->wv = get_mat(p->wv, p->cv, KD, H);
+    a->wo = get_mat(p->wo, p->co, H, QD);
+    if (!a->wq || !a->wk || !a->wv || !a->wo) return nullptr;
+    const size_t kvb = sizeof(float) * (size_t)p->max_t * KD;
+    bool fk = false, fv = false;
+    a->kc = (float*)get_mirror(p->kcache, kvb, &fk);
+    a->vc = (float*)get_mirror(p->vcache, kvb, &fv);
+    if (!a->kc || !a->vc) return nullptr;
+    const int T = p->tlen ? *p->tlen : 0;
+    if ((fk || fv) && T > 0) {  // state the caller already holds (CPU prefill, restored snapshot)
+        const size_t b = sizeof(float) * (size_t)T * KD;
+        if (hipMemcpy(a->kc, p->kcache, b, hipMemcpyHostToDevice) != hipSuccess ||
+            hipMemcpy(a->vc, p->vcache, b, hipMemcpyHostToDevice) != hipSuccess) {
+            fail(-2, "KV mirror upload failed");
+            return nullptr;
+        }
+    }
+    if (!rope_dev(a->rot, a->base, a->max_t)) return nullptr;
+    a->epoch = epoch();
+    c[p] = a;
+    return a;
+}
+
+DevFfn* get_ffn(const M6DenseP* p) {
+    auto& c = ffn_cache();
+    auto it = c.find(p);
+    if (it != c.end() && it->second->epoch == epoch() && memcmp(&it->second->snap, p, sizeof(*p)) == 0)
+        return it->second;
+    DevFfn* f = (it != c.end()) ? it->second : new DevFfn();
+    f->snap = *p;
+    f->FF = p->n_ff;
+    f->H = p->h;
+    f->g = get_mat(p->g, p->cg, p->n_ff, p->h);
+    f->u = get_mat(p->u, p->cu, p->n_ff, p->h);
+    f->d = get_mat(p->d, p->cd, p->h, p->n_ff);
+    if (!f->g || !f->u || !f->d) return nullptr;
+    f->epoch = epoch();
+    c[p] = f;
+    return f;
+}
+
+int grow(float** p, size_t* cap, size_t n) {
+    if (*cap >= n) return 0;
+    if (*p) {
+        hipStreamSynchronize(stream());
+        hipFree(*p);
+    }
+    DRACO_HIP(hipMalloc(p, sizeof(float) * n));
+    *cap = n;
+    return 0;
+}
+
+int ensure_work(Work& w, int H, int QD, int KD, int NH, int HD, int max_t, int FF) {
+    const size_t part = (size_t)NH * attn_nsplit(max_t) * (HD + 2);
+    if (grow(&w.x, &w.cap_h, H + 64)) return -2;
+    if (w.cap_h > 0 && !w.xn) DRACO_HIP(hipMalloc(&w.xn, sizeof(float) * w.cap_h));
+    if (w.cap_q < (size_t)QD) {
+        size_t c = w.cap_q;
+        if (grow(&w.q, &c, QD)) return -2;
+        size_t c2 = w.cap_q;
+        if (grow(&w.att, &c2, QD)) return -2;
+        w.cap_q = QD;
+    }
+    if (w.cap_k < (size_t)KD) {
+        size_t c = w.cap_k;
+        if (grow(&w.k, &c, KD)) return -2;
+        size_t c2 = w.cap_k;
+        if (grow(&w.v, &c2, KD)) return -2;
+        w.cap_k = KD;
+    }
+    if (grow(&w.part, &w.cap_part, part)) return -2;
+    if (w.cap_ff < (size_t)FF) {
+        size_t c = w.cap_ff;
+        if (grow(&w.g, &c, FF)) return -2;
+        size_t c2 = w.cap_ff;
+        if (grow(&w.u, &c2, FF)) return -2;
+        w.cap_ff = FF;
+    }
+    return 0;
+}
+
+DevModel* build_model(const M6LayerDesc* layers, int n_layer, int h);
+
+DevModel* resolve_model(const M6LayerDesc* layers, int n_layer, int h) {
+    // building may evict (a replaced weight bumps the epoch): retry until a
+    // build completes within one epoch
+    for (int tries = 0; tries < 3; tries++) {
+        const uint64_t e0 = epoch();
+        DevModel* m = build_model(layers, n_layer, h);
+        if (!m || m->epoch == epoch()) return m;
+        (void)e0;
+    }
+    fail(-2, "model residency kept changing while building");
+    return nullptr;
+}
+
+DevModel* build_model(const M6LayerDesc* layers, int n_layer, int h) {
+    auto& c = model_cache();
+    auto it = c.find(layers);
+    if (it != c.end()) {
+        DevModel* m = it->second;
+        bool ok = m->epoch == epoch() && m->n_layer == n_layer && m->h == h &&
+                  memcmp(m->descs.data(), layers, sizeof(M6LayerDesc) * n_layer) == 0;
+        for (int l = 0; ok && l < n_layer; l++)
+            ok = memcmp(&m->attn[l]->snap, layers[l].attn_p, sizeof(M6LlamaAttnP)) == 0 &&
+                 memcmp(&m->ffn[l]->snap, layers[l].ffn_p, sizeof(M6DenseP)) == 0 &&
+                 attn_cache().count(layers[l].attn_p) && attn_cache().at(layers[l].attn_p) == m->attn[l] &&
+                 ffn_cache().count(layers[l].ffn_p) && ffn_cache().at(layers[l].ffn_p) == m->ffn[l];
+        if (ok) return m;
+    }
+    DevModel* m = (it != c.end()) ? it->second : new DevModel();
+    m->descs.assign(layers, layers + n_layer);
+    m->attn.assign(n_layer, nullptr);
+    m->ffn.assign(n_layer, nullptr);
+    m->anorm.assign(n_layer, nullptr);
+    m->fnorm.assign(n_layer, nullptr);
+    m->h = h;
+    m->n_layer = n_layer;
+    for (int l = 0; l < n_layer; l++) {
+        const M6LayerDesc& L = layers[l];
+        if ((void*)L.attn != (void*)&m6_llama_attn_op || (void*)L.ffn != (void*)&m6_dense_op) {
+            fail(-1, "m6_forward_token: layer %d uses an op not served by this library", l);
+            return nullptr;
+        }
+        DevAttn* a = get_attn((const M6LlamaAttnP*)L.attn_p);
+        DevFfn* f = get_ffn((const M6DenseP*)L.ffn_p);
+        if (!a || !f) return nullptr;
+        if (a->H != h || f->H != h) {
+            fail(-1, "m6_forward_token: layer %d hidden size mismatch", l);
+            return nullptr;
+        }
+        m->attn[l] = a;
+        m->ffn[l] = f;
+        m->anorm[l] = norm_dev(L.attn_norm, h);
+        m->fnorm[l] = norm_dev(L.ffn_norm, h);
+        if ((L.attn_norm && !m->anorm[l]) || (L.ffn_norm && !m->fnorm[l])) return nullptr;
+        if (ensure_work(m->w, h, a->NH * a->HD, a->NKV * a->HD, a->NH, a->HD, a->max_t, f->FF)) return nullptr;
+    }
+    m->epoch = epoch();
+    if (!m->state) {
+        if (hipMalloc(&m->state, sizeof(int) * (1 + n_layer + 8)) != hipSuccess ||
+            hipHostMalloc(&m->hstate, sizeof(int) * (1 + n_layer + 8), hipHostMallocDefault) != hipSuccess) {
+            fail(-2, "state allocation failed");
+            return nullptr;
+        }
+    }
+    c[layers] = m;
+    return m;
+}
+
+// enqueue one llama layer on the device (x in w.x, updated in place)
+int enqueue_layer(DevModel* m, int l, float eps, hipStream_t st) {
+    DevAttn* a = m->attn[l];
+    DevFfn* f = m->ffn[l];
+    Work& w = m->w;
+    const int H = m->h;
+    dk_rmsnorm(w.x, m->anorm[l], w.xn, H, eps, st);
+    if (draco_gemv_launch(*a->wq, w.xn, w.q, nullptr, 0, a->wq->L.n_out, st)) return fail(-1, "gemv q");
+    if (draco_gemv_launch(*a->wk, w.xn, w.k, nullptr, 0, a->wk->L.n_out, st)) return fail(-1, "gemv k");
+    if (draco_gemv_launch(*a->wv, w.xn, w.v, nullptr, 0, a->wv->L.n_out, st)) return fail(-1, "gemv v");
+    const float* tab = rope_cache()[{a->rot, a->base}].dev;
+    dk_rope_append(w.q, w.k, w.v, a->kc, a->vc, tab, m->state, l, a->NH, a->NKV, a->HD, a->rot, st);
+    if (dk_attention(w.q, a->kc, a->vc, w.part, w.att, m->state, l, a->NH, a->NKV, a->HD, a->max_t, a->scale, st))
+        return fail(-1, "attention launch");
+    if (draco_gemv_launch(*a->wo, w.att, w.x, w.x, 0, H, st)) return fail(-1, "gemv o");
+    dk_rmsnorm(w.x, m->fnorm[l], w.xn, H, eps, st);
+    if (draco_gemv_launch(*f->g, w.xn, w.g, nullptr, 0, f->FF, st)) return fail(-1, "gemv gate");
+    if (draco_gemv_launch(*f->u, w.xn, w.u, nullptr, 0, f->FF, st)) return fail(-1, "gemv up");
+    dk_swiglu(w.g, w.u, f->FF, st);
+    if (draco_gemv_launch(*f->d, w.g, w.x, w.x, 0, H, st)) return fail(-1, "gemv down");
+    return 0;
+}
+
+int check_positions(DevModel* m, int pos, int n_steps) {
+    for (int l = 0; l < m->n_layer; l++) {
+        const int T = *m->attn[l]->snap.tlen;
+        if (T < 0 || T + n_steps > m->attn[l]->max_t)
+            return fail(-1, "layer %d: tlen %d + %d steps exceeds max_t %d", l, T, n_steps, m->attn[l]->max_t);
+    }
+    if (pos < 0) return fail(-1, "negative position %d", pos);
+    for (int l = 0; l < m->n_layer; l++)
+        if (!rope_dev(m->attn[l]->rot, m->attn[l]->base, pos + n_steps)) return -2;
+    return 0;
+}
+
+int upload_state(DevModel* m, int pos, hipStream_t st) {
+    m->hstate[0] = pos;
+    for (int l = 0; l < m->n_layer; l++) m->hstate[1 + l] = *m->attn[l]->snap.tlen;
+    DRACO_HIP(hipMemcpyAsync(m->state, m->hstate, sizeof(int) * (1 + m->n_layer), hipMemcpyHostToDevice, st));
+    return 0;
+}
+
+// state layout of a single directly-called op: [pos, tlen]
+int* op_state() {
+    static int* d = nullptr;
+    if (!d && hipMalloc(&d, sizeof(int) * 8) != hipSuccess) return nullptr;
+    return d;
+}
+
+}  // namespace
+
+extern "C" {
+
+// src/m6_engine.c:31-37
+void m6_rms_norm(const float* x, const float* w, int h, float eps, float* out) {
+    std::lock_guard<std::recursive_mutex> g(api_mutex());
+    if (int rc = ensure_init()) { report(rc, "m6_rms_norm"); return; }
+    hipStream_t st = stream();
+    float* dx = (float*)scratch(2, sizeof(float) * h * 3);
+    if (!dx) { report(-2, "m6_rms_norm"); return; }
+    float* dw = dx + h;
+    float* dout = dx + 2 * h;
+    hipMemcpyAsync(dx, x, sizeof(float) * h, hipMemcpyHostToDevice, st);
+    if (w) hipMemcpyAsync(dw, w, sizeof(float) * h, hipMemcpyHostToDevice, st);
+    dk_rmsnorm(dx, w ? dw : nullptr, dout, h, eps, st);
+    hipMemcpyAsync(out, dout, sizeof(float) * h, hipMemcpyDeviceToHost, st);
+    hipError_t e = hipStreamSynchronize(st);
+    if (e != hipSuccess) report(fail(-2, "m6_rms_norm: %s", hipGetErrorString(e)), "m6_rms_norm");
+}
+
+// src/m6_engine.c:40-54 (same table, including codes this library does not compute)
+size_t m6_rowbytes(int code, int n_in) {
+    switch (code) {
+    case 0: return (size_t)(n_in / 32) * 34;
+    case 1: return (size_t)(n_in / 32) * 18;
+    case 2: return (size_t)(n_in / 256) * 110;
+    case 3: return (size_t)(n_in / 256) * 176;
+    case 4: return (size_t)(n_in / 256) * 210;
+    case 5: return (size_t)(n_in / 256) * 144;
+    case 6: return (size_t)(n_in / 256) * 136;
+    case 7: return (size_t)n_in * 2;
+    case 8: return (size_t)(n_in / 32) * 22;
+    case 9: return (size_t)n_in * 4;
+    default: return 0;
+    }
+}
+
+const char* m6_engine_version(void) { return "m6_engine/1 draco_hip gfx950"; }
+
+// src/m6_layer.c:123-140.  The HIP library serves every format itself, so the
+// kernel-slot paths are accepted and ignored (0 = ok, as the reference).
+int m6_init_dl(const char* p012, const char* p3, const char* p4, const char* p56, const char* ps) {
+    (void)p012; (void)p3; (void)p4; (void)p56; (void)ps;
+    return 0;
+}
+
+// src/m6_layer.c:94-100 (Q5_0 slot).  Accepted; code 8 GEMVs fail loudly (-1).
+int m6_init_extra_dl(const char* p50) {
+    (void)p50;
+    return 0;
+}
+
+// src/m6_engine.c:61-83
+int m6_forward_token(float* x, int h, float eps, int pos, const M6LayerDesc* layers, int n_layer,
+                     float* scratch) {
+    (void)scratch;
+    std::lock_guard<std::recursive_mutex> g(api_mutex());
+    if (int rc = ensure_init()) return report(rc, "m6_forward_token");
+    DevModel* m = resolve_model(layers, n_layer, h);
+    if (!m) return report(-1, "m6_forward_token");
+    if (int rc = check_positions(m, pos, 1)) return report(rc, "m6_forward_token");
+    hipStream_t st = stream();
+    if (int rc = upload_state(m, pos, st)) return report(rc, "m6_forward_token");
+    if (hipMemcpyAsync(m->w.x, x, sizeof(float) * h, hipMemcpyHostToDevice, st) != hipSuccess)
+        return report(fail(-2, "x upload"), "m6_forward_token");
+    for (int l = 0; l < n_layer; l++)
+        if (int rc = enqueue_layer(m, l, eps, st)) return report(rc, "m6_forward_token");
+    hipMemcpyAsync(x, m->w.x, sizeof(float) * h, hipMemcpyDeviceToHost, st);
+    hipError_t e = hipStreamSynchronize(st);
+    if (e != hipSuccess) return report(fail(-2, "m6_forward_token: %s", hipGetErrorString(e)), "m6_forward_token");
+    for (int l = 0; l < n_layer; l++) *m->attn[l]->snap.tlen += 1;
+    return 0;
+}
+
+// src/m6_engine.c:373-391 (scratch receives the normalised x, as there)
+int m6_head_op(const float* x, const float* final_norm, int h, float eps, const uint8_t* head_w, int code,
+               int vocab, float* logits, float* scratch) {
+    std::lock_guard<std::recursive_mutex> g(api_mutex());
+    if (int rc = ensure_init()) return report(rc, "m6_head_op");
+    const DracoMat* hm = get_mat(head_w, code, vocab, h);
+    if (!hm) return report(-1, "m6_head_op");
+    const float* nw = norm_dev(final_norm, h);
+    if (final_norm && !nw) return report(-2, "m6_head_op");
+    hipStream_t st = stream();
+    float* dx = (float*)draco::scratch(3, sizeof(float) * (2 * (size_t)h + 64));
+    float* dl = (float*)draco::scratch(4, sizeof(float) * (size_t)vocab);
+    if (!dx || !dl) return report(-2, "m6_head_op");
+    float* dxn = dx + h + 32;
+    hipMemcpyAsync(dx, x, sizeof(float) * h, hipMemcpyHostToDevice, st);
+    dk_rmsnorm(dx, nw, dxn, h, eps, st);
+    draco_gemv_launch(*hm, dxn, dl, nullptr, 0, vocab, st);
+    hipMemcpyAsync(logits, dl, sizeof(float) * vocab, hipMemcpyDeviceToHost, st);
+    if (scratch) hipMemcpyAsync(scratch, dxn, sizeof(float) * h, hipMemcpyDeviceToHost, st);
+    hipError_t e = hipStreamSynchronize(st);
+    if (e != hipSuccess) return report(fail(-2, "m6_head_op: %s", hipGetErrorString(e)), "m6_head_op");
+    return 0;
+}
+
+// src/m6_engine.c:514-517 called directly (host xn in, host out).
+void m6_llama_attn_op(const float* xn, void* pv, int pos, float* out) {
+    std::lock_guard<std::recursive_mutex> g(api_mutex());
+    if (int rc = ensure_init()) { report(rc, "m6_llama_attn_op"); return; }
+    const M6LlamaAttnP* p = (const M6LlamaAttnP*)pv;
+    DevAttn* a = get_attn(p);
+    if (!a) { report(-1, "m6_llama_attn_op"); return; }
+    const int T = *p->tlen;
+    if (T < 0 || T >= a->max_t || pos < 0) { report(fail(-1, "tlen %d / pos %d out of range", T, pos), "m6_llama_attn_op"); return; }
+    if (!rope_dev(a->rot, a->base, pos + 1)) { report(-2, "m6_llama_attn_op"); return; }
+    static Work w;
+    if (ensure_work(w, a->H, a->NH * a->HD, a->NKV * a->HD, a->NH, a->HD, a->max_t, 1)) { report(-2, "m6_llama_attn_op"); return; }
+    int* ds = op_state();
+    static int* hs = nullptr;
+    if (!hs) hipHostMalloc(&hs, sizeof(int) * 8, hipHostMallocDefault);
+    hipStream_t st = stream();
+    hs[0] = pos;
+    hs[1] = T;
+    hipMemcpyAsync(ds, hs, sizeof(int) * 2, hipMemcpyHostToDevice, st);
+    hipMemcpyAsync(w.xn, xn, sizeof(float) * a->H, hipMemcpyHostToDevice, st);
+    draco_gemv_launch(*a->wq, w.xn, w.q, nullptr, 0, a->wq->L.n_out, st);
+    draco_gemv_launch(*a->wk, w.xn, w.k, nullptr, 0, a->wk->L.n_out, st);
+    draco_gemv_launch(*a->wv, w.xn, w.v, nullptr, 0, a->wv->L.n_out, st);
+    dk_rope_append(w.q, w.k, w.v, a->kc, a->vc, rope_cache()[{a->rot, a->base}].dev, ds, 0, a->NH, a->NKV, a->HD,
+                   a->rot, st);
+    dk_attention(w.q, a->kc, a->vc, w.part, w.att, ds, 0, a->NH, a->NKV, a->HD, a->max_t, a->scale, st);
+    draco_gemv_launch(*a->wo, w.att, w.x, nullptr, 0, a->H, st);
+    hipMemcpyAsync(out, w.x, sizeof(float) * a->H, hipMemcpyDeviceToHost, st);
+    hipError_t e = hipStreamSynchronize(st);
+    if (e != hipSuccess) { report(fail(-2, "m6_llama_attn_op: %s", hipGetErrorString(e)), "m6_llama_attn_op"); return; }
+    *p->tlen = T + 1;
+}
+
+// src/m6_engine.c:275-303 called directly.
+void m6_dense_op(const float* xn, void* pv, float* out) {
+    std::lock_guard<std::recursive_mutex> g(api_mutex());
+    if (int rc = ensure_init()) { report(rc, "m6_dense_op"); return; }
+    DevFfn* f = get_ffn((const M6DenseP*)pv);
+    if (!f) { report(-1, "m6_dense_op"); return; }
+    static Work w;
+    if (ensure_work(w, f->H, 1, 1, 1, 64, 64, f->FF)) { report(-2, "m6_dense_op"); return; }
+    hipStream_t st = stream();
+    hipMemcpyAsync(w.xn, xn, sizeof(float) * f->H, hipMemcpyHostToDevice, st);
+    draco_gemv_launch(*f->g, w.xn, w.g, nullptr, 0, f->FF, st);
+    draco_gemv_launch(*f->u, w.xn, w.u, nullptr, 0, f->FF, st);
+    dk_swiglu(w.g, w.u, f->FF, st);
+    draco_gemv_launch(*f->d, w.g, w.x, nullptr, 0, f->H, st);
+    hipMemcpyAsync(out, w.x, sizeof(float) * f->H, hipMemcpyDeviceToHost, st);
+    hipError_t e = hipStreamSynchronize(st);
+    if (e != hipSuccess) report(fail(-2, "m6_dense_op: %s", hipGetErrorString(e)), "m6_dense_op");
+}
+
+// ---- state sync hooks (no reference counterpart; the reference's state is
+// the host arrays themselves, src/draco_engine_server.py:907-922) ----
+
+// Copy every layer's device KV mirror into the caller's kcache/vcache arrays
+// (rows [0, tlen)), e.g. before snapshotting STATES.
+int draco_state_pull(const void* layers_v, int n_layer) {
+    std::lock_guard<std::recursive_mutex> g(api_mutex());
+    const M6LayerDesc* layers = (const M6LayerDesc*)layers_v;
+    for (int l = 0; l < n_layer; l++) {
+        const M6LlamaAttnP* p = (const M6LlamaAttnP*)layers[l].attn_p;
+        const size_t b = sizeof(float) * (size_t)(*p->tlen) * p->n_kv * p->head_dim;
+        if (b == 0) continue;
+        if (int rc = mirror_pull(p->kcache, b)) return rc;
+        if (int rc = mirror_pull(p->vcache, b)) return rc;
+    }
+    return 0;
+}
+
+// Upload the caller's kcache/vcache arrays into the device mirrors (rows
+// [0, tlen)), e.g. after restoring a snapshot into them.
+int draco_state_push(const void* layers_v, int n_layer) {
+    std::lock_guard<std::recursive_mutex> g(api_mutex());
+    if (int rc = ensure_init()) return rc;
+    const M6LayerDesc* layers = (const M6LayerDesc*)layers_v;
+    for (int l = 0; l < n_layer; l++) {
+        const M6LlamaAttnP* p = (const M6LlamaAttnP*)layers[l].attn_p;
+        DevAttn* a = get_attn(p);
+        if (!a) return -1;
+        const size_t b = sizeof(float) * (size_t)(*p->tlen) * p->n_kv * p->head_dim;
+        if (b == 0) continue;
+        DRACO_HIP(hipMemcpy(a->kc, p->kcache, b, hipMemcpyHostToDevice));
+        DRACO_HIP(hipMemcpy(a->vc, p->vcache, b, hipMemcpyHostToDevice));
+    }
+    return 0;
+}
+
+// ---- device-resident greedy generation (no reference counterpart: the
+// reference's loop is Python, src/smol_engine.py:203-213; this runs the same
+// steps without leaving the device) ----
+//
+// Feeds prompt[0..n_prompt) token-serially from the current tlen, then
+// generates n_gen tokens greedily (argmax, first index on ties).  Positions
+// are tlen-based: token i is at position tlen0 + i.  With use_graph != 0 one
+// prefill step and one decode step are captured as HIP graphs and replayed.
+// stats[0] = decode ms (n_gen steps), stats[1] = prefill ms.
+int draco_llama_generate(const void* layers_v, int n_layer, int h, float eps, const float* final_norm,
+                         const uint8_t* head_w, int head_code, int vocab, const uint8_t* emb_w, int emb_code,
+                         const int* prompt, int n_prompt, int n_gen, int use_graph, int* out_tokens,
+                         float* out_hidden, float* stats) {
+    std::lock_guard<std::recursive_mutex> g(api_mutex());
+    if (int rc = ensure_init()) return report(rc, "draco_llama_generate");
+    const M6LayerDesc* layers = (const M6LayerDesc*)layers_v;
+    if (n_prompt < 1 || n_gen < 1) return report(fail(-1, "need n_prompt >= 1 and n_gen >= 1"), "draco_llama_generate");
+    DevModel* m = resolve_model(layers, n_layer, h);
+    if (!m) return report(-1, "draco_llama_generate");
+    const DracoMat* hm = get_mat(head_w, head_code, vocab, h);
+    const DracoMat* em = get_mat(emb_w, emb_code, vocab, h);
+    const float* nw = norm_dev(final_norm, h);
+    if (!hm || !em || (final_norm && !nw)) return report(-1, "draco_llama_generate");
+    const int steps = n_prompt + n_gen - 1;
+    const int pos0 = *m->attn[0]->snap.tlen;
+    if (int rc = check_positions(m, pos0, steps)) return report(rc, "draco_llama_generate");
+    hipStream_t st = stream();
+    const int ntok = n_prompt + n_gen;
+    int* dtok = (int*)scratch(5, sizeof(int) * (ntok + 64));
+    float* dlog = (float*)scratch(6, sizeof(float) * (size_t)vocab);
+    float* dred = (float*)scratch(7, (sizeof(float) + sizeof(int)) * ARGMAX_BLOCKS + 64);
+    if (!dtok || !dlog || !dred) return report(-2, "draco_llama_generate");
+    int* cursor = dtok + ntok + 8;   // index of the token being fed
+    int* cur = dtok + ntok + 16;     // its id
+    int* dri = (int*)(dred + ARGMAX_BLOCKS);
+    std::vector<int> ht(ntok + 64, 0);
+    for (int i = 0; i < n_prompt; i++) ht[i] = prompt[i];
+    ht[ntok + 8] = 0;
+    DRACO_HIP(hipMemcpyAsync(dtok, ht.data(), sizeof(int) * (ntok + 64), hipMemcpyHostToDevice, st));
+    if (int rc = upload_state(m, pos0, st)) return report(rc, "draco_llama_generate");
+    auto step = [&](bool decode) -> int {
+        dk_pick_token(dtok, cursor, cur, st);
+        dk_embed(*em, cur, 0, m->w.x, st);
+        for (int l = 0; l < n_layer; l++)
+            if (int rc = enqueue_layer(m, l, eps, st)) return rc;
+        if (decode) {
+            dk_rmsnorm(m->w.x, nw, m->w.xn, h, eps, st);
+            if (draco_gemv_launch(*hm, m->w.xn, dlog, nullptr, 0, vocab, st)) return fail(-1, "head gemv");
+            // the argmax after feeding token `cursor` is token cursor+1
+            dk_argmax(dlog, vocab, dred, dri, dtok, cursor, 0, st);
+        }
+        dk_advance(m->state, n_layer, cursor, st);
+        return 0;
+    };
+    hipEvent_t e0, e1, e2;
+    DRACO_HIP(hipEventCreate(&e0));
+    DRACO_HIP(hipEventCreate(&e1));
+    DRACO_HIP(hipEventCreate(&e2));
+    hipGraphExec_t gx[2] = {nullptr, nullptr};
+    hipGraph_t gg[2] = {nullptr, nullptr};
+    if (use_graph) {
+        for (int k = 0; k < 2; k++) {
+            DRACO_HIP(hipStreamBeginCapture(st, hipStreamCaptureModeRelaxed));
+            int rc = step(k == 1);
+            hipGraph_t gr;
+            hipError_t ce = hipStreamEndCapture(st, &gr);
+            if (rc) return report(rc, "draco_llama_generate");
+            if (ce != hipSuccess) return report(fail(-2, "graph capture: %s", hipGetErrorString(ce)), "draco_llama_generate");
+            gg[k] = gr;
+            DRACO_HIP(hipGraphInstantiate(&gx[k], gr, nullptr, nullptr, 0));
+        }
+    }
+    DRACO_HIP(hipEventRecord(e0, st));
+    for (int i = 0; i < n_prompt - 1; i++) {
+        if (use_graph) DRACO_HIP(hipGraphLaunch(gx[0], st));
+        else if (int rc = step(false)) return report(rc, "draco_llama_generate");
+    }
+    DRACO_HIP(hipEventRecord(e1, st));
+    for (int i = 0; i < n_gen; i++) {
+        if (use_graph) DRACO_HIP(hipGraphLaunch(gx[1], st));
+        else if (int rc = step(true)) return report(rc, "draco_llama_generate");
+    }
+    DRACO_HIP(hipEventRecord(e2, st));
+    DRACO_HIP(hipMemcpyAsync(ht.data(), dtok, sizeof(int) * ntok, hipMemcpyDeviceToHost, st));
+    if (out_hidden) DRACO_HIP(hipMemcpyAsync(out_hidden, m->w.x, sizeof(float) * h, hipMemcpyDeviceToHost, st));
+    DRACO_HIP(hipStreamSynchronize(st));
+    float ms_pre = 0, ms_dec = 0;
+    hipEventElapsedTime(&ms_pre, e0, e1);
+    hipEventElapsedTime(&ms_dec, e1, e2);
+    if (stats) {
+        stats[0] = ms_dec;
+        stats[1] = ms_pre;
+    }
+    for (int i = 0; i < n_gen; i++) out_tokens[i] = ht[n_prompt + i];
+    for (int l = 0; l < n_layer; l++) *m->attn[l]->snap.tlen += steps;
+    // the attn snapshots hold the tlen pointer, not its value: still valid
+    for (int k = 0; k < 2; k++) {
+        if (gx[k]) hipGraphExecDestroy(gx[k]);
+        if (gg[k]) hipGraphDestroy(gg[k]);
+    }
+    hipEventDestroy(e0);
+    hipEventDestroy(e1);
+    hipEventDestroy(e2);
+    return 0;
+}
+
+}  // extern "C"

@@ -1,0 +1,26 @@
+// decode.h -- launchers of the decode-token kernels (decode.hip).
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include "gemv.h"
+
+constexpr int ARGMAX_BLOCKS = 256;
+
+// Number of T-splits of the decode attention for a cache of max_t rows
+// (about 64 rows per split at full length, at most 64 splits).
+static inline int attn_nsplit(int max_t) {
+    int n = (max_t + 63) / 64;
+    return n < 1 ? 1 : (n > 64 ? 64 : n);
+}
+
+void dk_rmsnorm(const float* x, const float* w, float* out, int h, float eps, hipStream_t st);
+void dk_rope_append(float* q, const float* k, const float* v, float* kc, float* vc, const float* tab,
+                    const int* state, int layer, int NH, int NKV, int HD, int rot, hipStream_t st);
+int dk_attention(const float* q, const float* kc, const float* vc, float* part, float* out, const int* state,
+                 int layer, int NH, int NKV, int HD, int max_t, float scale, hipStream_t st);
+void dk_swiglu(float* g, const float* u, int n, hipStream_t st);
+void dk_embed(const DracoMat& m, const int* tokp, int tok, float* out, hipStream_t st);
+// out[slotp ? *slotp + 1 : slot] = first index of max(x[0..n))
+void dk_argmax(const float* x, int n, float* pv, int* pi, int* out, const int* slotp, int slot, hipStream_t st);
+void dk_advance(int* state, int n_layer, int* tok_cursor, hipStream_t st);
+void dk_pick_token(const int* ids, const int* cursor, int* cur, hipStream_t st);

@@ -1,0 +1,378 @@
+// decode.hip -- the non-GEMV kernels of one llama decode token (gfx950).
+//
+// Reference semantics (src/m6_engine.c):
+//   rms_norm            :31-37    out = x * (1/sqrtf(mean(x^2)+eps)) * w
+//   consecutive-pair rope :134-143 (angles from a host table built with the
+//                        same libm calls, so they are bit-identical)
+//   KV append            :477-481  row T of the caches, after rope
+//   attention            :482-505  per q head h (kv head h/rep): softmax over
+//                        rows 0..T of (q.k_t)*scale, weighted sum of v_t
+//   SwiGLU               :289-302  g = g/(1+expf(-g)) * u
+//
+// Device "token state": st[0] = position, st[1 + l] = tlen of layer l before
+// this token.  Kernels read T and pos from it, so a captured graph of a
+// token can be replayed for every position (k_advance bumps it).
+#include <hip/hip_runtime.h>
+#include <math.h>
+
+#include "decode.h"
+#include "dev_common.h"
+
+namespace {
+
+// ------------------------------------------------------------- RMSNorm --
+// One block of 1024 threads; deterministic tree sum.
+__global__ __launch_bounds__(1024) void k_rmsnorm(const float* __restrict__ x, const float* __restrict__ w,
+                                                  float* __restrict__ out, int h, float eps) {
+    __shared__ float red[16];
+    float s = 0.f;
+    for (int i = threadIdx.x; i < h; i += blockDim.x) s = fmaf(x[i], x[i], s);
+    s = wave_sum(s);
+    const int wv = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    if ((threadIdx.x & 63) == 0) red[wv] = s;
+    __syncthreads();
+    float tot = 0.f;
+    for (int i = 0; i < nw; i++) tot += red[i];
+    const float inv = 1.f / sqrtf(tot / (float)h + eps);
+    for (int i = threadIdx.x; i < h; i += blockDim.x) out[i] = w ? x[i] * inv * w[i] : x[i] * inv;
+}
+
+// ---------------------------------------------------- rope + KV append --
+// q: [NH][HD], k,v: [NKV][HD]; rope on the first `rot` dims of every head.
+__global__ __launch_bounds__(256) void k_rope_append(float* __restrict__ q, const float* __restrict__ k,
+                                                     const float* __restrict__ v, float* __restrict__ kc,
+                                                     float* __restrict__ vc, const float* __restrict__ tab,
+                                                     const int* __restrict__ st, int layer, int NH, int NKV,
+                                                     int HD, int rot) {
+    const int pos = st[0];
+    const int T = st[1 + layer];
+    const int half = rot / 2;
+    const int KD = NKV * HD;
+    const float* ang = tab + (size_t)pos * half * 2;
+    const int n_q = NH * HD, n_k = KD;
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n_q + 2 * n_k; i += gridDim.x * blockDim.x) {
+        if (i < n_q) {  // q: rotate pairs in place (one thread per pair, even index)
+            const int d = i % HD;
+            if (d < rot && (d & 1) == 0) {
+                const float c = ang[d], s = ang[d + 1];  // pair index d/2 -> tab[(d/2)*2 + {0,1}]
+                const float a = q[i], b = q[i + 1];
+                q[i] = a * c - b * s;
+                q[i + 1] = a * s + b * c;
+            }
+        } else if (i < n_q + n_k) {
+            const int j = i - n_q, d = j % HD;
+            float* dst = kc + (size_t)T * KD;
+            if (d < rot) {
+                if ((d & 1) == 0) {
+                    const float c = ang[d], s = ang[d + 1];
+                    const float a = k[j], b = k[j + 1];
+                    dst[j] = a * c - b * s;
+                    dst[j + 1] = a * s + b * c;
+                }
+            } else {
+                dst[j] = k[j];
+            }
+        } else {
+            const int j = i - n_q - n_k;
+            vc[(size_t)T * KD + j] = v[j];
+        }
+    }
+}
+
+// ----------------------------------------------------------- attention --
+// Split-T decode attention.  Block (g, s) handles kv head g and rows
+// [t0, t1) of 0..T for all `rep` q heads that share it, writing an
+// unnormalised partial (o[HD], m, l) per (q head, split).
+constexpr int REPMAX = 8;
+
+template <int HD>
+__global__ __launch_bounds__(256) void k_attn_partial(const float* __restrict__ q, const float* __restrict__ kc,
+                                                      const float* __restrict__ vc, float* __restrict__ part,
+                                                      const int* __restrict__ st, int layer, int NH, int NKV,
+                                                      int nsplit, int chunk_max, float scale) {
+    extern __shared__ float sh[];
+    const int g = blockIdx.x, s = blockIdx.y;
+    const int rep = NH / NKV, KD = NKV * HD;
+    const int Tn = st[1 + layer] + 1;
+    const int chunk = (Tn + nsplit - 1) / nsplit;
+    const int t0 = s * chunk, t1 = min(Tn, t0 + chunk);
+    const int n = max(0, t1 - t0);
+    float* qs = sh;                    // [rep][HD]
+    float* sc = qs + rep * HD;         // [rep][chunk_max]
+    float* ml = sc + rep * chunk_max;  // [rep][2]
+    float* red = ml + 2 * REPMAX;      // [4][rep][HD]
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    for (int i = tid; i < rep * HD; i += 256) qs[i] = q[(size_t)g * rep * HD + i];
+    __syncthreads();
+    // scores: one row per thread
+    for (int t = tid; t < n; t += 256) {
+        const float* kt = kc + (size_t)(t0 + t) * KD + g * HD;
+        float acc[REPMAX];
+#pragma unroll
+        for (int j = 0; j < REPMAX; j++) acc[j] = 0.f;
+        for (int d = 0; d < HD; d += 4) {
+            const float4 kv = ld4(kt + d);
+#pragma unroll
+            for (int j = 0; j < REPMAX; j++) {
+                if (j < rep) {
+                    const float* qj = qs + j * HD + d;
+                    acc[j] = fmaf(qj[0], kv.x, acc[j]);
+                    acc[j] = fmaf(qj[1], kv.y, acc[j]);
+                    acc[j] = fmaf(qj[2], kv.z, acc[j]);
+                    acc[j] = fmaf(qj[3], kv.w, acc[j]);
+                }
+            }
+        }
+        for (int j = 0; j < rep; j++) sc[j * chunk_max + t] = acc[j] * scale;
+    }
+    __syncthreads();
+    // per head: max, exp, sum (wave j handles heads j, j+4, ...)
+    for (int j = wv; j < rep; j += 4) {
+        float m = -INFINITY;
+        for (int t = lane; t < n; t += 64) m = fmaxf(m, sc[j * chunk_max + t]);
+        m = wave_max(m);
+        float l = 0.f;
+        for (int t = lane; t < n; t += 64) {
+            const float p = n > 0 ? expf(sc[j * chunk_max + t] - m) : 0.f;
+            sc[j * chunk_max + t] = p;
+            l += p;
+        }
+        l = wave_sum(l);
+        if (lane == 0) {
+            ml[2 * j] = m;
+            ml[2 * j + 1] = l;
+        }
+    }
+    __syncthreads();
+    // P.V: wave wv takes rows wv, wv+4, ...; lanes span the head dims
+    constexpr int DPL = HD / 64;  // dims per lane
+    float o[REPMAX][DPL];
+#pragma unroll
+    for (int j = 0; j < REPMAX; j++)
+#pragma unroll
+        for (int e = 0; e < DPL; e++) o[j][e] = 0.f;
+    for (int t = wv; t < n; t += 4) {
+        const float* vt = vc + (size_t)(t0 + t) * KD + g * HD;
+        float vv[DPL];
+#pragma unroll
+        for (int e = 0; e < DPL; e++) vv[e] = vt[lane + 64 * e];
+#pragma unroll
+        for (int j = 0; j < REPMAX; j++)
+            if (j < rep) {
+                const float p = sc[j * chunk_max + t];
+#pragma unroll
+                for (int e = 0; e < DPL; e++) o[j][e] = fmaf(p, vv[e], o[j][e]);
+            }
+    }
+    for (int j = 0; j < rep; j++)
+#pragma unroll
+        for (int e = 0; e < DPL; e++) red[(wv * rep + j) * HD + lane + 64 * e] = o[j][e];
+    __syncthreads();
+    for (int i = tid; i < rep * HD; i += 256) {
+        const int j = i / HD, d = i % HD;
+        const float acc = red[(0 * rep + j) * HD + d] + red[(1 * rep + j) * HD + d] +
+                          red[(2 * rep + j) * HD + d] + red[(3 * rep + j) * HD + d];
+        const int h = g * rep + j;
+        float* pp = part + ((size_t)h * nsplit + s) * (HD + 2);
+        pp[d] = acc;
+        if (d == 0) {
+            pp[HD] = n > 0 ? ml[2 * j] : -INFINITY;
+            pp[HD + 1] = n > 0 ? ml[2 * j + 1] : 0.f;
+        }
+    }
+}
+
+// merge the splits of every q head: out[h][d] = sum_s o_s e^(m_s-M) / sum_s l_s e^(m_s-M)
+__global__ __launch_bounds__(128) void k_attn_combine(const float* __restrict__ part, float* __restrict__ out,
+                                                      int nsplit, int HD) {
+    const int h = blockIdx.x;
+    const float* ph = part + (size_t)h * nsplit * (HD + 2);
+    float M = -INFINITY;
+    for (int s = 0; s < nsplit; s++) M = fmaxf(M, ph[s * (HD + 2) + HD]);
+    float L = 0.f;
+    for (int s = 0; s < nsplit; s++) {
+        const float m = ph[s * (HD + 2) + HD];
+        if (m > -INFINITY) L += ph[s * (HD + 2) + HD + 1] * expf(m - M);
+    }
+    const float invL = 1.f / L;
+    for (int d = threadIdx.x; d < HD; d += blockDim.x) {
+        float acc = 0.f;
+        for (int s = 0; s < nsplit; s++) {
+            const float m = ph[s * (HD + 2) + HD];
+            if (m > -INFINITY) acc += ph[s * (HD + 2) + d] * expf(m - M);
+        }
+        out[(size_t)h * HD + d] = acc * invL;
+    }
+}
+
+// -------------------------------------------------------------- SwiGLU --
+__global__ __launch_bounds__(256) void k_swiglu(float* __restrict__ g, const float* __restrict__ u, int n) {
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
+        const float gv = g[i];
+        g[i] = (gv / (1.f + expf(-gv))) * u[i];
+    }
+}
+
+// ---------------------------------------------------------- embedding --
+// Dequantize row `tok` of a private-layout matrix into out[n_in]; values are
+// bit-identical to the host decoders ((d*sc)*q for Q6_K, d*sc*q - dmin*m for
+// Q4_K, q*d for Q8_0).
+__global__ __launch_bounds__(256) void k_embed(const uint8_t* __restrict__ base, DracoLayout L,
+                                               const int* __restrict__ tokp, int tok_host,
+                                               float* __restrict__ out) {
+    const int tok = tokp ? *tokp : tok_host;
+    const int n_in = L.n_in, nb = L.nb;
+    for (int p = blockIdx.x * blockDim.x + threadIdx.x; p < n_in; p += gridDim.x * blockDim.x) {
+        const size_t blk = (size_t)tok * nb + p / draco_block_values(L.code);
+        float val = 0.f;
+        if (L.code == DRACO_Q8_0) {
+            const int8_t q = (int8_t)base[L.off[0] + blk * 32 + (p & 31)];
+            const float d = h2f(*reinterpret_cast<const uint16_t*>(base + L.off[1] + blk * 2));
+            val = (float)q * d;
+        } else if (L.code == DRACO_Q6_K) {
+            const int i = p & 255;
+            const uint8_t lb = base[L.off[0] + blk * 128 + (i >> 7) * 64 + (i & 63)];
+            const int lo4 = ((i >> 6) & 1) ? (lb >> 4) : (lb & 0xF);
+            const int hi2 = (base[L.off[1] + blk * 64 + (i >> 7) * 32 + (i & 31)] >> (((i >> 5) & 3) * 2)) & 3;
+            const int8_t sc = (int8_t)base[L.off[2] + blk * 16 + (i >> 4)];
+            const float d = h2f(*reinterpret_cast<const uint16_t*>(base + L.off[3] + blk * 2));
+            val = (d * (float)sc) * (float)((lo4 | (hi2 << 4)) - 32);
+        } else if (L.code == DRACO_Q4_K) {
+            const int i = p & 255, j = i >> 5;
+            const uint8_t* hd = base + L.off[1] + blk * 16;
+            const float d = h2f(*reinterpret_cast<const uint16_t*>(hd)), dmin = h2f(*reinterpret_cast<const uint16_t*>(hd + 2));
+            const uint8_t* s = hd + 4;
+            int sc, m;
+            if (j < 4) {
+                sc = s[j] & 63;
+                m = s[j + 4] & 63;
+            } else {
+                sc = (s[j + 4] & 0xF) | ((s[j - 4] >> 6) << 4);
+                m = (s[j + 4] >> 4) | ((s[j] >> 6) << 4);
+            }
+            const uint8_t qb = base[L.off[0] + blk * 128 + (j >> 1) * 32 + (i & 31)];
+            const int q = (j & 1) ? (qb >> 4) : (qb & 0xF);
+            val = (d * (float)sc) * (float)q - dmin * (float)m;
+        } else if (L.code == DRACO_F32) {
+            val = reinterpret_cast<const float*>(base)[(size_t)tok * n_in + p];
+        } else if (L.code == DRACO_F16) {
+            val = h2f(reinterpret_cast<const uint16_t*>(base)[(size_t)tok * n_in + p]);
+        }
+        out[p] = val;
+    }
+}
+
+// -------------------------------------------------------------- argmax --
+// First index of the maximum (np.argmax semantics).  Stage 1: per-block
+// (value, index); stage 2: one block reduces the partials.
+__device__ __forceinline__ void am_merge(float& v, int& i, float v2, int i2) {
+    if (v2 > v || (v2 == v && i2 < i)) {
+        v = v2;
+        i = i2;
+    }
+}
+
+__global__ __launch_bounds__(256) void k_argmax_part(const float* __restrict__ x, int n, float* __restrict__ pv,
+                                                     int* __restrict__ pi) {
+    float v = -INFINITY;
+    int idx = 0x7fffffff;
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) am_merge(v, idx, x[i], i);
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) am_merge(v, idx, __shfl_xor(v, m, 64), __shfl_xor(idx, m, 64));
+    __shared__ float sv[4];
+    __shared__ int si[4];
+    if ((threadIdx.x & 63) == 0) {
+        sv[threadIdx.x >> 6] = v;
+        si[threadIdx.x >> 6] = idx;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < 4; w++) am_merge(v, idx, sv[w], si[w]);
+        pv[blockIdx.x] = v;
+        pi[blockIdx.x] = idx;
+    }
+}
+
+__global__ __launch_bounds__(64) void k_argmax_final(const float* __restrict__ pv, const int* __restrict__ pi,
+                                                     int nb, int* __restrict__ out, const int* __restrict__ slotp,
+                                                     int slot) {
+    float v = -INFINITY;
+    int idx = 0x7fffffff;
+    for (int i = threadIdx.x; i < nb; i += 64) am_merge(v, idx, pv[i], pi[i]);
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) am_merge(v, idx, __shfl_xor(v, m, 64), __shfl_xor(idx, m, 64));
+    if (threadIdx.x == 0) out[slotp ? slotp[0] + 1 : slot] = idx;
+}
+
+// ------------------------------------------------------ token advance --
+// After a token: pos += 1, every layer's tlen += 1, next token slot.
+__global__ void k_advance(int* st, int n_layer, int* tok_cursor) {
+    if (threadIdx.x == 0) {
+        st[0] += 1;
+        for (int l = 0; l < n_layer; l++) st[1 + l] += 1;
+        if (tok_cursor) tok_cursor[0] += 1;
+    }
+}
+
+// copy token ids[cursor] -> cur (used by the graph: embed reads cur)
+__global__ void k_pick_token(const int* ids, const int* cursor, int* cur) {
+    if (threadIdx.x == 0) cur[0] = ids[cursor[0]];
+}
+
+}  // namespace
+
+// ------------------------------------------------------------ launchers --
+void dk_rmsnorm(const float* x, const float* w, float* out, int h, float eps, hipStream_t st) {
+    hipLaunchKernelGGL(k_rmsnorm, dim3(1), dim3(1024), 0, st, x, w, out, h, eps);
+}
+
+void dk_rope_append(float* q, const float* k, const float* v, float* kc, float* vc, const float* tab,
+                    const int* state, int layer, int NH, int NKV, int HD, int rot, hipStream_t st) {
+    const int n = NH * HD + 2 * NKV * HD;
+    const int blocks = (n + 255) / 256;
+    hipLaunchKernelGGL(k_rope_append, dim3(blocks), dim3(256), 0, st, q, k, v, kc, vc, tab, state, layer, NH,
+                       NKV, HD, rot);
+}
+
+int dk_attention(const float* q, const float* kc, const float* vc, float* part, float* out, const int* state,
+                 int layer, int NH, int NKV, int HD, int max_t, float scale, hipStream_t st) {
+    const int rep = NH / NKV;
+    if (rep < 1 || rep > REPMAX || NH % NKV) return -1;
+    const int nsplit = attn_nsplit(max_t);
+    const int chunk_max = (max_t + nsplit - 1) / nsplit;
+    const size_t shm = sizeof(float) * (rep * HD + rep * chunk_max + 2 * REPMAX + 4 * rep * HD);
+    const dim3 grid(NKV, nsplit);
+    if (HD == 64)
+        hipLaunchKernelGGL(k_attn_partial<64>, grid, dim3(256), shm, st, q, kc, vc, part, state, layer, NH, NKV,
+                           nsplit, chunk_max, scale);
+    else if (HD == 128)
+        hipLaunchKernelGGL(k_attn_partial<128>, grid, dim3(256), shm, st, q, kc, vc, part, state, layer, NH, NKV,
+                           nsplit, chunk_max, scale);
+    else
+        return -1;
+    hipLaunchKernelGGL(k_attn_combine, dim3(NH), dim3(HD < 128 ? HD : 128), 0, st, part, out, nsplit, HD);
+    return 0;
+}
+
+void dk_swiglu(float* g, const float* u, int n, hipStream_t st) {
+    const int blocks = (n + 255) / 256 < 1024 ? (n + 255) / 256 : 1024;
+    hipLaunchKernelGGL(k_swiglu, dim3(blocks), dim3(256), 0, st, g, u, n);
+}
+
+void dk_embed(const DracoMat& m, const int* tokp, int tok, float* out, hipStream_t st) {
+    const int blocks = (m.L.n_in + 255) / 256;
+    hipLaunchKernelGGL(k_embed, dim3(blocks), dim3(256), 0, st, m.dev, m.L, tokp, tok, out);
+}
+
+void dk_argmax(const float* x, int n, float* pv, int* pi, int* out, const int* slotp, int slot, hipStream_t st) {
+    hipLaunchKernelGGL(k_argmax_part, dim3(ARGMAX_BLOCKS), dim3(256), 0, st, x, n, pv, pi);
+    hipLaunchKernelGGL(k_argmax_final, dim3(1), dim3(64), 0, st, pv, pi, ARGMAX_BLOCKS, out, slotp, slot);
+}
+
+void dk_advance(int* state, int n_layer, int* tok_cursor, hipStream_t st) {
+    hipLaunchKernelGGL(k_advance, dim3(1), dim3(64), 0, st, state, n_layer, tok_cursor);
+}
+
+void dk_pick_token(const int* ids, const int* cursor, int* cur, hipStream_t st) {
+    hipLaunchKernelGGL(k_pick_token, dim3(1), dim3(64), 0, st, ids, cursor, cur);
+}

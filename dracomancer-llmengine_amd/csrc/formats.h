@@ -13,6 +13,12 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#if defined(__HIPCC__)
+#define DRACO_HD __host__ __device__
+#else
+#define DRACO_HD
+#endif
+
 enum {
     DRACO_Q8_0 = 0,
     DRACO_Q5_K = 3,
@@ -24,7 +30,7 @@ enum {
 
 #define Q8K_BLOCK_BYTES 292  // { float d; int8 qs[256]; int16 bsums[16]; }
 
-static inline size_t draco_row_bytes(int code, int n_in) {
+DRACO_HD static inline size_t draco_row_bytes(int code, int n_in) {
     switch (code) {
     case DRACO_Q8_0: return (size_t)(n_in / 32) * 34;
     case DRACO_Q5_K: return (size_t)(n_in / 256) * 176;
@@ -36,7 +42,7 @@ static inline size_t draco_row_bytes(int code, int n_in) {
     }
 }
 
-static inline int draco_block_values(int code) {
+DRACO_HD static inline int draco_block_values(int code) {
     switch (code) {
     case DRACO_Q8_0: return 32;
     case DRACO_Q5_K:

@@ -35,6 +35,7 @@ struct State {
     std::vector<std::pair<void*, size_t>> scr;
     std::vector<std::pair<void*, size_t>> pin;
     size_t resident = 0;
+    uint64_t epoch = 1;
     std::string err;
 };
 
@@ -62,6 +63,8 @@ uint64_t fingerprint(const void* host, size_t bytes) {
 }
 
 }  // namespace
+
+uint64_t epoch() { return S().epoch; }
 
 std::recursive_mutex& api_mutex() {
     static std::recursive_mutex* m = new std::recursive_mutex();
@@ -109,11 +112,15 @@ const DracoMat* get_mat(const void* host, int code, int n_out, int n_in) {
     auto it = s.mats.find(host);
     if (it != s.mats.end()) {
         MatEntry& e = it->second;
-        if (e.code == code && e.n_in == n_in && e.n_out >= n_out && e.fp == fingerprint(host, draco_row_bytes(code, n_in) * (size_t)e.n_out))
+        if (e.code == code && e.n_in == n_in && e.n_out >= n_out &&
+            e.fp == fingerprint(host, draco_row_bytes(code, n_in) * (size_t)e.n_out))
             return &e.m;
+        // different bytes (or shape) at a known address: replace the device copy
+        hipStreamSynchronize(s.st);
         hipFree(e.m.dev);
+        e.m.dev = nullptr;
         s.resident -= e.m.L.bytes;
-        s.mats.erase(it);
+        s.epoch++;
     }
     MatEntry e;
     if (draco_layout(code, n_out, n_in, &e.m.L)) {
@@ -141,13 +148,16 @@ const DracoMat* get_mat(const void* host, int code, int n_out, int n_in) {
         return nullptr;
     }
     s.resident += e.m.L.bytes;
-    auto res = s.mats.emplace(host, e);
-    return &res.first->second.m;
+    MatEntry& slot = s.mats[host];  // node address stays stable for the process
+    slot = e;
+    return &slot.m;
 }
 
 int forget(const void* host) {
     State& s = S();
     int n = 0;
+    s.epoch++;
+    if (s.st) hipStreamSynchronize(s.st);
     auto it = s.mats.find(host);
     if (it != s.mats.end()) {
         hipFree(it->second.m.dev);
@@ -166,6 +176,7 @@ int forget(const void* host) {
 
 void forget_all() {
     State& s = S();
+    s.epoch++;
     if (s.st) hipStreamSynchronize(s.st);
     for (auto& kv : s.mats) hipFree(kv.second.m.dev);
     s.mats.clear();
@@ -188,6 +199,7 @@ void* get_mirror(const void* host, size_t bytes, bool* fresh) {
         hipStreamSynchronize(s.st);
         hipFree(it->second.dev);
         s.mirrors.erase(it);
+        s.epoch++;
     }
     Mirror m;
     hipError_t he = hipMalloc(&m.dev, bytes);
@@ -208,6 +220,7 @@ int mirror_invalidate(const void* host) {
     hipStreamSynchronize(s.st);
     hipFree(it->second.dev);
     s.mirrors.erase(it);
+    s.epoch++;
     return 1;
 }
 

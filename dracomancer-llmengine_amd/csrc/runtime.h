@@ -34,6 +34,11 @@ const char* last_error();
                                  __FILE__, __LINE__);                                      \
     } while (0)
 
+// Eviction epoch: bumped whenever a registered weight or mirror is dropped or
+// replaced.  Anything that caches DracoMat pointers or mirror addresses must
+// rebuild when the epoch it was built at is no longer current.
+uint64_t epoch();
+
 // Weight residency.  Returns nullptr (and records an error) on failure.
 // The host buffer must hold n_out rows of GGUF format `code`; its contents are
 // assumed immutable while registered (draco_forget drops an entry).

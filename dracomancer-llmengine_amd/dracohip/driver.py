@@ -156,6 +156,27 @@ class LlamaDriver:
             raise RuntimeError(f"m6_head_op rc={rc}")
         return self.logits
 
+    def generate_device(self, prompt, n_gen, use_graph=True):
+        """The same greedy loop run entirely on the device (draco_llama_generate).
+
+        Returns (tokens, final hidden x, stats) with stats = (decode ms, prefill ms).
+        Only valid with the HIP engine library."""
+        prompt = np.ascontiguousarray(prompt, np.int32)
+        toks = np.zeros(n_gen, np.int32)
+        hidden = np.zeros(self.H, np.float32)
+        stats = np.zeros(4, np.float32)
+        L = self.engine.cdll
+        rc = L.draco_llama_generate(
+            ct.cast(self.descs, ct.c_void_p), self.NL, self.H, np.float32(self.cfg.eps), pf(self.onorm),
+            ct.c_void_p(self.head_buf.ctypes.data), self.head_code, self.cfg.vocab,
+            ct.c_void_p(self.emb_buf.ctypes.data), self.emb_code,
+            prompt.ctypes.data_as(ct.POINTER(ct.c_int)), len(prompt), n_gen, int(use_graph),
+            toks.ctypes.data_as(ct.POINTER(ct.c_int)), pf(hidden), pf(stats))
+        if rc != 0:
+            raise RuntimeError(f"draco_llama_generate rc={rc}: {L.draco_last_error().decode()}")
+        self.x[:] = hidden
+        return [int(t) for t in toks], hidden, (float(stats[0]), float(stats[1]))
+
     def greedy(self, prompt, n_gen, collect_logits=()):
         """Token-serial prefill then greedy decode (src/smol_engine.py:203-213)."""
         for pos, t in enumerate(prompt):

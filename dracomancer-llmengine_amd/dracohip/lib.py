@@ -40,6 +40,21 @@ SIGNATURES = {
     "m5_scalar_supported": (ct.c_int, [ct.c_int]),
     "m5_gemv": (ct.c_int, [ct.c_int, f32p, u8p, ct.c_int, ct.c_int, f32p]),
     "m5_gemv_range": (ct.c_int, [ct.c_int, f32p, u8p, ct.c_int, ct.c_int, f32p, ct.c_int, ct.c_int]),
+    # m6 layer-engine ABI (src/m6_engine.c)
+    "m6_rms_norm": (None, [f32p, f32p, ct.c_int, ct.c_float, f32p]),
+    "m6_rowbytes": (ct.c_size_t, [ct.c_int, ct.c_int]),
+    "m6_engine_version": (ct.c_char_p, []),
+    "m6_init_dl": (ct.c_int, [ct.c_char_p] * 5),
+    "m6_init_extra_dl": (ct.c_int, [ct.c_char_p]),
+    "m6_forward_token": (ct.c_int, [f32p, ct.c_int, ct.c_float, ct.c_int, ct.c_void_p, ct.c_int, f32p]),
+    "m6_head_op": (ct.c_int, [f32p, f32p, ct.c_int, ct.c_float, ct.c_void_p, ct.c_int, ct.c_int, f32p, f32p]),
+    "m6_llama_attn_op": (None, [f32p, ct.c_void_p, ct.c_int, f32p]),
+    "m6_dense_op": (None, [f32p, ct.c_void_p, f32p]),
+    "draco_state_pull": (ct.c_int, [ct.c_void_p, ct.c_int]),
+    "draco_state_push": (ct.c_int, [ct.c_void_p, ct.c_int]),
+    "draco_llama_generate": (ct.c_int, [ct.c_void_p, ct.c_int, ct.c_int, ct.c_float, f32p, ct.c_void_p,
+                                        ct.c_int, ct.c_int, ct.c_void_p, ct.c_int, i32p, ct.c_int, ct.c_int,
+                                        ct.c_int, i32p, f32p, f32p]),
     # library utilities
     "draco_last_error": (ct.c_char_p, []),
     "draco_forget": (ct.c_int, [ct.c_void_p]),

@@ -39,6 +39,81 @@ int m5_gemv(int code, const float* x, const uint8_t* W, int n_out, int n_in, flo
 int m5_gemv_range(int code, const float* x, const uint8_t* W, int n_out, int n_in, float* y,
                   int o0, int o1);
 
+/* ---- layer-engine ABI (drop-in for m6_engine.so, llama path) ------------ */
+
+/* Descriptor and parameter structs, field for field src/m6_engine.c:21-28,
+ * :270-273 and :396-406 (ctypes mirrors: src/smol_engine.py:97-115). */
+typedef void (*m6_attn_op)(const float* xn, void* p, int pos, float* out);
+typedef void (*m6_ffn_op)(const float* xn, void* p, float* out);
+typedef struct {
+    const float* attn_norm;
+    const float* ffn_norm;
+    m6_attn_op attn;
+    void* attn_p;
+    m6_ffn_op ffn;
+    void* ffn_p;
+} M6LayerDesc;
+typedef struct {
+    const uint8_t *wq, *wk, *wv, *wo;
+    int cq, ck, cv, co;
+    int n_head, n_kv, head_dim, hidden, rot;
+    float rope_base;
+    float* kcache;
+    float* vcache;
+    int* tlen;
+    int max_t;
+    float* work;
+} M6LlamaAttnP;
+typedef struct {
+    const uint8_t *g, *u, *d;
+    int cg, cu, cd, n_ff, h;
+} M6DenseP;
+
+/* src/m6_engine.c:31-37 */
+void m6_rms_norm(const float* x, const float* w, int h, float eps, float* out);
+/* src/m6_engine.c:40-54 */
+size_t m6_rowbytes(int code, int n_in);
+/* src/m6_engine.c:85 */
+const char* m6_engine_version(void);
+/* src/m6_layer.c:123-140; kernel-slot paths accepted and ignored (returns 0). */
+int m6_init_dl(const char* p012, const char* p3, const char* p4, const char* p56, const char* ps);
+/* src/m6_layer.c:94-100; accepted (returns 0); Q5_0 (code 8) GEMVs return -1. */
+int m6_init_extra_dl(const char* p50);
+/* src/m6_engine.c:61-83.  x[h] updated in place; every layer's *tlen += 1.
+ * Layers whose ops are this library's m6_llama_attn_op / m6_dense_op run on
+ * the device (KV caches mirrored on the device, see draco_state_pull/push);
+ * any other op pointer returns -1. */
+int m6_forward_token(float* x, int h, float eps, int pos, const M6LayerDesc* layers, int n_layer,
+                     float* scratch);
+/* src/m6_engine.c:373-391.  scratch[h] receives the normalised x. */
+int m6_head_op(const float* x, const float* final_norm, int h, float eps, const uint8_t* head_w,
+               int code, int vocab, float* logits, float* scratch);
+/* src/m6_engine.c:514-517 (llama_attn_core, kq_scale 1/sqrt(head_dim)). */
+void m6_llama_attn_op(const float* xn, void* p, int pos, float* out);
+/* src/m6_engine.c:275-303 */
+void m6_dense_op(const float* xn, void* p, float* out);
+
+/* ---- state sync hooks (no reference counterpart: the reference's KV state
+ * is the host arrays themselves, src/draco_engine_server.py:907-922) ------ */
+
+/* device KV mirrors -> caller's kcache/vcache (rows [0, tlen)) */
+int draco_state_pull(const void* layers, int n_layer);
+/* caller's kcache/vcache (rows [0, tlen)) -> device KV mirrors */
+int draco_state_push(const void* layers, int n_layer);
+
+/* ---- device-resident greedy loop (no reference counterpart: the
+ * reference's loop is Python, src/smol_engine.py:203-213) ----------------
+ * Feeds prompt[0..n_prompt) from the current tlen, then generates n_gen
+ * tokens by argmax (first index on ties), all on the device; with use_graph
+ * one prefill step and one decode step are captured as HIP graphs and
+ * replayed.  out_hidden[h] = x after the last forward (nullable);
+ * stats[0] = decode ms, stats[1] = prefill ms (nullable). */
+int draco_llama_generate(const void* layers, int n_layer, int h, float eps,
+                         const float* final_norm, const uint8_t* head_w, int head_code, int vocab,
+                         const uint8_t* emb_w, int emb_code, const int* prompt, int n_prompt,
+                         int n_gen, int use_graph, int* out_tokens, float* out_hidden,
+                         float* stats);
+
 /* ---- library utilities (no reference counterpart) ----------------------- */
 
 const char* draco_last_error(void);

@@ -43,6 +43,8 @@ _SIGS = {
     "or_forward_token": (ct.c_int, [f32p, ct.c_int, ct.c_float, ct.c_int, ct.c_void_p, ct.c_int, f32p]),
     "or_head_op": (ct.c_int, [f32p, f32p, ct.c_int, ct.c_float, u8p, ct.c_int, ct.c_int, f32p, f32p]),
     "or_argmax": (ct.c_int, [f32p, ct.c_int]),
+    "or_llama_attn_op": (None, [f32p, ct.c_void_p, ct.c_int, f32p]),
+    "or_dense_op": (None, [f32p, ct.c_void_p, f32p]),
     "or_topk": (None, [f32p, ct.c_int, ct.c_int, i32p]),
     "or_moe_route": (None, [f32p, f32p, ct.c_int, ct.c_int, ct.c_int, f32p, i32p, f32p]),
     "or_granite_moe": (None, [f32p, ct.c_void_p, i32p, f32p, ct.c_int, ct.c_int, ct.c_int, ct.c_int,

@@ -16,6 +16,7 @@ def declared_symbols():
     for h in glob.glob(os.path.join(ROOT, "include", "*.h")):
         src = open(h).read()
         src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+        src = re.sub(r"typedef[^;]*;", "", src)  # function-pointer typedefs are not exports
         for m in re.finditer(r"^[A-Za-z_][\w \*]*?\b([a-z][a-z0-9_]*)\s*\(", src, flags=re.M):
             names.add(m.group(1))
     return names
