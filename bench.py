@@ -1,0 +1,220 @@
+"""Benchmark: decode tok/s at batch 1, context ~1024, on one MI355X.
+
+Workload: Llama-3.2-1B-shaped decoder, random-init
+N(0,0.02) from seed 0, Q4_K_M-style (Q4_K q/k/o/gate/up, Q6_K v/down/tied
+head), a 960-token random prompt, then greedy decode at positions 960..1023.
+One "step" is one decode token (embedding -> 16 layers -> head -> argmax),
+run by the device-resident loop (draco_llama_generate, graph-replayed); the
+prompt is fed untimed before every timed run.  value = timed tokens / timed
+seconds (HIP events on the decode stream).
+
+roofline: the Q4_K GEMV of configs[1] (W 14336x4096 from seed 1, fp32 x),
+timed live with per-launch HIP event pairs while rotating 10 distinct weight
+copies (330 MB > the 256 MB MALL).
+
+cpu_baseline: the reference's own C engine (src/m6_engine.c + the scalar
+kernels of src/m5_kern_scalar.c, compiled from source into oracle/_ref),
+decoding from the same context on this host's cores, in a child process.
+
+usage: python bench.py [--gpus 1] [--steps 64] [--warmup 8]
+"""
+import argparse
+import json
+import os
+import subprocess
+import sys
+import tempfile
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "dracomancer-llmengine_amd"))
+sys.path.insert(0, ROOT)
+
+import numpy as np  # noqa: E402
+
+PEAK_HBM_GBS = 8000.0
+CTX_START = 960
+MAX_DECODE = 64  # positions 960..1023 (max_t 1024)
+
+
+def log(*a):
+    print("[bench]", *a, file=sys.stderr, flush=True)
+
+
+def q4k_gemv_roofline(lib, n_copies=10, iters=200):
+    """configs[1] Q4_K GEMV 14336x4096, fp32 activations (the decode path's kernel)."""
+    n_out, n_in = 14336, 4096
+    rng = np.random.default_rng(1)
+    W = lib.quantize(5, rng.standard_normal((n_out, n_in), dtype=np.float32) * np.float32(0.02))
+    out = np.zeros(4, np.float32)
+    rc = lib.load().draco_bench_gemv(5, lib.pu8(W), n_out, n_in, n_copies, iters, lib.pf(out))
+    if rc != 0:
+        raise RuntimeError(lib.last_error())
+    us = float(out[0])
+    alg_bytes = W.nbytes + 4 * n_in + 4 * n_out  # weights + fp32 x + fp32 y
+    gbs = alg_bytes / us / 1e3
+    return {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+            "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None,
+            "kernel": "k_gemv_q4k (W 14336x4096 Q4_K, fp32 x, 10 rotating copies)",
+            "alg_bytes_per_launch": alg_bytes, "us_per_launch": round(us, 3),
+            "us_per_launch_median": round(float(out[3]), 3)}
+
+
+def cpu_baseline_worker(args):
+    """Child process: the reference engine decoding from context CTX_START."""
+    from dracohip import models
+    from dracohip.driver import EngineLib, LlamaDriver
+    from oracle.oracle import REF_DIR
+    import ctypes as ct
+    cfg = models.LLAMA1B
+    model = models.build_llama(cfg, 0)
+    E = ct.CDLL(os.path.join(REF_DIR, "libref_engine.so"))
+    E.m6_init_dl.argtypes = [ct.c_char_p] * 5
+    sp = os.path.join(REF_DIR, "libref_scalar.so").encode()
+    assert E.m6_init_dl(sp, sp, sp, sp, sp) == 0
+    drv = LlamaDriver(model, EngineLib(E, name="ref"))
+    kv = np.load(args.kv_file)
+    for l in range(cfg.n_layer):
+        drv.kc[l][:] = kv[f"k{l}"]
+        drv.vc[l][:] = kv[f"v{l}"]
+        drv.tl[l][0] = CTX_START
+    tok = int(kv["next_token"])
+    t0 = time.time()
+    n = 0
+    while n < args.cpu_tokens and (time.time() - t0) < args.cpu_seconds:
+        drv.forward(tok, CTX_START + n)
+        tok = int(np.argmax(drv.logits_of_x().astype(np.float64)))
+        n += 1
+    dt = time.time() - t0
+    print(json.dumps({"tokens": n, "seconds": dt, "threads": int(os.environ.get("OMP_NUM_THREADS", "0"))}))
+
+
+def run_cpu_baseline(drv, cfg, first_token, threads, cpu_tokens, cpu_seconds):
+    """Pull the GPU's KV at context CTX_START and time the reference engine from there."""
+    import ctypes as ct
+    from dracohip import lib
+    lib.load().draco_state_pull(ct.cast(drv.descs, ct.c_void_p), drv.NL)
+    n = CTX_START * cfg.n_kv * cfg.head_dim
+    fd, path = tempfile.mkstemp(suffix=".npz", dir="/dev/shm" if os.path.isdir("/dev/shm") else None)
+    os.close(fd)
+    try:
+        arrs = {f"k{l}": drv.kc[l].copy() for l in range(cfg.n_layer)}
+        arrs.update({f"v{l}": drv.vc[l].copy() for l in range(cfg.n_layer)})
+        for l in range(cfg.n_layer):
+            arrs[f"k{l}"][n:] = 0
+            arrs[f"v{l}"][n:] = 0
+        np.savez(path, next_token=np.int64(first_token), **arrs)
+        env = dict(os.environ, OMP_NUM_THREADS=str(threads), OMP_PROC_BIND="false")
+        cmd = [sys.executable, os.path.abspath(__file__), "--cpu-baseline-worker", "--kv-file", path,
+               "--cpu-tokens", str(cpu_tokens), "--cpu-seconds", str(cpu_seconds)]
+        r = subprocess.run(cmd, env=env, capture_output=True, text=True, timeout=600)
+        if r.returncode != 0:
+            log("cpu baseline failed:", r.stderr[-2000:])
+            return None
+        res = json.loads(r.stdout.strip().splitlines()[-1])
+    finally:
+        os.unlink(path)
+    return {"value": round(res["tokens"] / res["seconds"], 3), "unit": "tok/s", "cores": threads,
+            "kind": "reference",
+            "sample": f"{res['tokens']} greedy decode tokens of the same model from context {CTX_START} "
+                      f"(KV taken from the GPU prefill), reference m6_engine.c + m5_kern_scalar.c "
+                      f"(scalar kernels: the AVX-512 m5_kern*.so are not in the reference tree), "
+                      f"{res['seconds']:.1f}s"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=64)
+    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-threads", type=int, default=0)
+    ap.add_argument("--cpu-tokens", type=int, default=48)
+    ap.add_argument("--cpu-seconds", type=float, default=20.0)
+    ap.add_argument("--eager", action="store_true",
+                    help="run the decode loop without HIP graphs (for profilers that cannot trace graphs)")
+    ap.add_argument("--roofline-only", action="store_true", help="only the Q4_K GEMV roofline measurement")
+    ap.add_argument("--cpu-baseline-worker", action="store_true")
+    ap.add_argument("--kv-file")
+    args = ap.parse_args()
+    if args.cpu_baseline_worker:
+        return cpu_baseline_worker(args)
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py: this build runs on exactly one GPU (--gpus 1); multi-GPU runs are not part "
+              "of it", file=sys.stderr)
+        sys.exit(2)
+
+    import ctypes as ct
+    from dracohip import lib, models
+    from dracohip.driver import LlamaDriver, hip_engine_lib
+
+    if args.roofline_only:
+        roof = q4k_gemv_roofline(lib)
+        log(f"Q4_K GEMV 14336x4096: {roof['us_per_launch']} us/launch, {roof['achieved']} GB/s")
+        print(json.dumps({"roofline": roof}), flush=True)
+        return
+
+    cfg = models.LLAMA1B
+    t0 = time.time()
+    model = models.build_llama(cfg, 0)
+    prompt = model.prompt()
+    log(f"model {cfg.name} built in {time.time() - t0:.1f}s ({model.nbytes() / 1e6:.1f} MB)")
+    L = lib.load()
+    drv = LlamaDriver(model, hip_engine_lib())
+
+    def run(n_tok):
+        drv.reset()
+        L.draco_state_push(ct.cast(drv.descs, ct.c_void_p), drv.NL)
+        return drv.generate_device(prompt, n_tok, use_graph=not args.eager)
+
+    if args.warmup > 0:
+        run(min(args.warmup, MAX_DECODE))
+        log(f"warmup {args.warmup} decode steps done")
+    left, ms, toks_first = args.steps, 0.0, None
+    while left > 0:
+        k = min(left, MAX_DECODE)
+        toks, hidden, (dec_ms, pre_ms) = run(k)
+        if toks_first is None:
+            toks_first = toks
+        ms += dec_ms
+        left -= k
+        log(f"timed {k} decode steps: {dec_ms:.2f} ms (prefill {pre_ms:.1f} ms)")
+    tok_s = args.steps / (ms / 1e3)
+    match = None
+    gpath = os.path.join(ROOT, "tests", "golden", "llama1b.npz")
+    if os.path.exists(gpath):
+        g = np.load(gpath)
+        n = min(len(toks_first), len(g["tokens"]))
+        match = bool(list(g["tokens"][:n]) == toks_first[:n])
+    log(f"decode {tok_s:.1f} tok/s; greedy tokens match reference: {match}")
+
+    roof = q4k_gemv_roofline(lib)
+    log(f"Q4_K GEMV 14336x4096: {roof['us_per_launch']} us/launch, {roof['achieved']} GB/s")
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        threads = args.cpu_threads or min(16, os.cpu_count() or 1)
+        # first decode token after the prompt: feed it through the CPU engine from CTX_START
+        run(1)
+        cpu = run_cpu_baseline(drv, cfg, toks_first[0], threads, args.cpu_tokens, args.cpu_seconds)
+        if cpu:
+            log(f"cpu baseline {cpu['value']} tok/s on {threads} threads")
+
+    line = {
+        "metric": "decode tok/s bs1 @ctx1024; Q4_K GEMV achieved HBM GB/s as % of peak",
+        "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms / args.steps, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "fp32 activations x Q4_K/Q6_K weights",
+        "data": "synthetic: random-init N(0,0.02) weights from seed 0, random prompt ids",
+        "config": {"workload": "configs[2] llama-3.2-1b-shaped Q4_K_M decode, bs1, 960-token prompt, "
+                               "positions 960..1023", "global_batch": 1, "seq_len": 1024,
+                   "parallelism": "single GPU"},
+        "greedy_tokens_match_reference": match,
+        "roofline": roof,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

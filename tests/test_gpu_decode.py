@@ -146,3 +146,16 @@ def test_smol360m_dropin_per_token():
     assert toks == list(g["tokens"])
     assert np.max(np.abs(hidden - g["hidden"])) <= HID_TOL
     assert rel_err(lg[63][g["logits63_top_ids"]], g["logits63_top_vals"]) <= 1e-4
+
+
+def test_llama1b_device_generate():
+    """Llama-3.2-1B-shaped Q4_K_M, 960-token prompt + 64 greedy
+    tokens (positions up to 1023), token-identical to the reference engine."""
+    g = golden("llama1b.npz")
+    cfg, model, drv = _driver("llama-3.2-1b-q4_k_m")
+    assert model.digest() == g["digest"].tobytes().hex()
+    print("[decode] llama1b device generate", flush=True)
+    toks, hidden, st = drv.generate_device(model.prompt(), cfg.n_gen, use_graph=True)
+    print(f"[decode] llama1b decode {cfg.n_gen / (st[0] / 1e3):.1f} tok/s prefill {st[1]:.0f} ms", flush=True)
+    assert toks == list(g["tokens"])
+    assert np.max(np.abs(hidden - g["hidden"])) <= HID_TOL
