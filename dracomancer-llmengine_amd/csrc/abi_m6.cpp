@@ -81,6 +81,7 @@ struct DevFfn {
 struct Work {
     float *x = nullptr, *xn = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *att = nullptr,
           *part = nullptr, *g = nullptr, *u = nullptr;
+    unsigned* cnt = nullptr;  // attention merge counters (one per kv head), zero at rest
     size_t cap_h = 0, cap_q = 0, cap_k = 0, cap_part = 0, cap_ff = 0;
 };
 
@@ -254,6 +255,11 @@ int grow(float** p, size_t* cap, size_t n) {
 
 int ensure_work(Work& w, int H, int QD, int KD, int NH, int HD, int max_t, int FF) {
     const size_t part = (size_t)NH * attn_nsplit(max_t) * (HD + 2);
+    if (!w.cnt) {
+        DRACO_HIP(hipMalloc(&w.cnt, sizeof(unsigned) * 256));
+        DRACO_HIP(hipMemset(w.cnt, 0, sizeof(unsigned) * 256));
+        DRACO_HIP(hipDeviceSynchronize());
+    }
     if (grow(&w.x, &w.cap_h, H + 64)) return -2;
     if (w.cap_h > 0 && !w.xn) DRACO_HIP(hipMalloc(&w.xn, sizeof(float) * w.cap_h));
     if (w.cap_q < (size_t)QD) {
@@ -350,25 +356,93 @@ DevModel* build_model(const M6LayerDesc* layers, int n_layer, int h) {
     return m;
 }
 
-// enqueue one llama layer on the device (x in w.x, updated in place)
+SegDesc seg_of(const DracoMat* m, int epi, float* y, const float* yadd) {
+    SegDesc d = {};
+    d.base = m->dev;
+    d.L = m->L;
+    d.epi = epi;
+    d.y = y;
+    d.yadd = yadd;
+    return d;
+}
+
+// q/k/v projections of one attention op from input x (RMS-normalised in the
+// prologue when norm != 0), with rope on q/k and the KV append at row T as
+// epilogues (src/m6_engine.c:447-481).
+int enqueue_qkv(DevAttn* a, Work& w, const float* x, int norm, const float* norm_w, float eps,
+                const int* state, int layer, hipStream_t st) {
+    const SegDesc all[3] = {seg_of(a->wq, EPI_ROPE_Q, w.q, nullptr), seg_of(a->wk, EPI_ROPE_K, nullptr, nullptr),
+                            seg_of(a->wv, EPI_V_APPEND, nullptr, nullptr)};
+    bool done[3] = {false, false, false};
+    for (int i = 0; i < 3; i++) {
+        if (done[i]) continue;
+        SegLaunch s = {};
+        s.n_in = a->H;
+        s.x = x;
+        s.do_norm = norm;
+        s.norm_w = norm_w;
+        s.eps = eps;
+        for (int j = i; j < 3; j++)  // every not-yet-issued segment of this format
+            if (!done[j] && all[j].L.code == all[i].L.code) {
+                s.seg[s.nseg++] = all[j];
+                done[j] = true;
+            }
+        s.rope_tab = rope_cache()[{a->rot, a->base}].dev;
+        s.state = state;
+        s.layer = layer;
+        s.head_dim = a->HD;
+        s.rot = a->rot;
+        s.kv_dim = a->NKV * a->HD;
+        s.kc = a->kc;
+        s.vc = a->vc;
+        if (draco_seg_launch(s, st)) return fail(-1, "qkv launch rejected");
+    }
+    return 0;
+}
+
+// gate/up + SwiGLU into w.g (src/m6_engine.c:289-302), input normalised in the
+// prologue when norm != 0
+int enqueue_gateup(DevFfn* f, Work& w, const float* x, int norm, const float* norm_w, float eps,
+                   hipStream_t st) {
+    if (f->g->L.code == f->u->L.code) {
+        SegLaunch s = {};
+        s.nseg = 2;
+        s.n_in = f->H;
+        s.x = x;
+        s.do_norm = norm;
+        s.norm_w = norm_w;
+        s.eps = eps;
+        s.seg[0] = seg_of(f->g, EPI_SWIGLU, w.g, nullptr);
+        s.seg[1] = seg_of(f->u, EPI_STORE, nullptr, nullptr);
+        if (draco_seg_launch(s, st)) return fail(-1, "gate/up launch rejected");
+        return 0;
+    }
+    // mixed formats: two launches + the elementwise SwiGLU
+    const float* xin = x;
+    if (norm) {
+        dk_rmsnorm(x, norm_w, w.xn, f->H, eps, st);
+        xin = w.xn;
+    }
+    if (draco_gemv_launch(*f->g, xin, w.g, nullptr, 0, f->FF, st)) return fail(-1, "gemv gate");
+    if (draco_gemv_launch(*f->u, xin, w.u, nullptr, 0, f->FF, st)) return fail(-1, "gemv up");
+    dk_swiglu(w.g, w.u, f->FF, st);
+    return 0;
+}
+
+// enqueue one llama layer on the device (x in w.x, updated in place):
+// five launches -- qkv(+norm,+rope,+append), attention(+merge), wo(+residual),
+// gate/up(+norm,+SwiGLU), down(+residual)
 int enqueue_layer(DevModel* m, int l, float eps, hipStream_t st) {
     DevAttn* a = m->attn[l];
     DevFfn* f = m->ffn[l];
     Work& w = m->w;
     const int H = m->h;
-    dk_rmsnorm(w.x, m->anorm[l], w.xn, H, eps, st);
-    if (draco_gemv_launch(*a->wq, w.xn, w.q, nullptr, 0, a->wq->L.n_out, st)) return fail(-1, "gemv q");
-    if (draco_gemv_launch(*a->wk, w.xn, w.k, nullptr, 0, a->wk->L.n_out, st)) return fail(-1, "gemv k");
-    if (draco_gemv_launch(*a->wv, w.xn, w.v, nullptr, 0, a->wv->L.n_out, st)) return fail(-1, "gemv v");
-    const float* tab = rope_cache()[{a->rot, a->base}].dev;
-    dk_rope_append(w.q, w.k, w.v, a->kc, a->vc, tab, m->state, l, a->NH, a->NKV, a->HD, a->rot, st);
-    if (dk_attention(w.q, a->kc, a->vc, w.part, w.att, m->state, l, a->NH, a->NKV, a->HD, a->max_t, a->scale, st))
+    if (int rc = enqueue_qkv(a, w, w.x, 1, m->anorm[l], eps, m->state, l, st)) return rc;
+    if (dk_attention(w.q, a->kc, a->vc, w.part, w.cnt, w.att, m->state, l, a->NH, a->NKV, a->HD, a->max_t,
+                     a->scale, st))
         return fail(-1, "attention launch");
     if (draco_gemv_launch(*a->wo, w.att, w.x, w.x, 0, H, st)) return fail(-1, "gemv o");
-    dk_rmsnorm(w.x, m->fnorm[l], w.xn, H, eps, st);
-    if (draco_gemv_launch(*f->g, w.xn, w.g, nullptr, 0, f->FF, st)) return fail(-1, "gemv gate");
-    if (draco_gemv_launch(*f->u, w.xn, w.u, nullptr, 0, f->FF, st)) return fail(-1, "gemv up");
-    dk_swiglu(w.g, w.u, f->FF, st);
+    if (int rc = enqueue_gateup(f, w, w.x, 1, m->fnorm[l], eps, st)) return rc;
     if (draco_gemv_launch(*f->d, w.g, w.x, w.x, 0, H, st)) return fail(-1, "gemv down");
     return 0;
 }
@@ -489,8 +563,21 @@ int m6_head_op(const float* x, const float* final_norm, int h, float eps, const 
     if (!dx || !dl) return report(-2, "m6_head_op");
     float* dxn = dx + h + 32;
     hipMemcpyAsync(dx, x, sizeof(float) * h, hipMemcpyHostToDevice, st);
-    dk_rmsnorm(dx, nw, dxn, h, eps, st);
-    draco_gemv_launch(*hm, dxn, dl, nullptr, 0, vocab, st);
+    if (hm->L.code == DRACO_Q4_K || hm->L.code == DRACO_Q6_K || hm->L.code == DRACO_Q8_0) {
+        SegLaunch sl = {};
+        sl.nseg = 1;
+        sl.n_in = h;
+        sl.x = dx;
+        sl.do_norm = 1;
+        sl.norm_w = nw;
+        sl.eps = eps;
+        sl.xn_out = dxn;
+        sl.seg[0] = seg_of(hm, EPI_STORE, dl, nullptr);
+        if (draco_seg_launch(sl, st)) return report(fail(-1, "head launch rejected"), "m6_head_op");
+    } else {
+        dk_rmsnorm(dx, nw, dxn, h, eps, st);
+        draco_gemv_launch(*hm, dxn, dl, nullptr, 0, vocab, st);
+    }
     hipMemcpyAsync(logits, dl, sizeof(float) * vocab, hipMemcpyDeviceToHost, st);
     if (scratch) hipMemcpyAsync(scratch, dxn, sizeof(float) * h, hipMemcpyDeviceToHost, st);
     hipError_t e = hipStreamSynchronize(st);
@@ -518,12 +605,8 @@ void m6_llama_attn_op(const float* xn, void* pv, int pos, float* out) {
     hs[1] = T;
     hipMemcpyAsync(ds, hs, sizeof(int) * 2, hipMemcpyHostToDevice, st);
     hipMemcpyAsync(w.xn, xn, sizeof(float) * a->H, hipMemcpyHostToDevice, st);
-    draco_gemv_launch(*a->wq, w.xn, w.q, nullptr, 0, a->wq->L.n_out, st);
-    draco_gemv_launch(*a->wk, w.xn, w.k, nullptr, 0, a->wk->L.n_out, st);
-    draco_gemv_launch(*a->wv, w.xn, w.v, nullptr, 0, a->wv->L.n_out, st);
-    dk_rope_append(w.q, w.k, w.v, a->kc, a->vc, rope_cache()[{a->rot, a->base}].dev, ds, 0, a->NH, a->NKV, a->HD,
-                   a->rot, st);
-    dk_attention(w.q, a->kc, a->vc, w.part, w.att, ds, 0, a->NH, a->NKV, a->HD, a->max_t, a->scale, st);
+    if (enqueue_qkv(a, w, w.xn, 0, nullptr, 0.f, ds, 0, st)) { report(-1, "m6_llama_attn_op"); return; }
+    dk_attention(w.q, a->kc, a->vc, w.part, w.cnt, w.att, ds, 0, a->NH, a->NKV, a->HD, a->max_t, a->scale, st);
     draco_gemv_launch(*a->wo, w.att, w.x, nullptr, 0, a->H, st);
     hipMemcpyAsync(out, w.x, sizeof(float) * a->H, hipMemcpyDeviceToHost, st);
     hipError_t e = hipStreamSynchronize(st);
@@ -541,9 +624,7 @@ void m6_dense_op(const float* xn, void* pv, float* out) {
     if (ensure_work(w, f->H, 1, 1, 1, 64, 64, f->FF)) { report(-2, "m6_dense_op"); return; }
     hipStream_t st = stream();
     hipMemcpyAsync(w.xn, xn, sizeof(float) * f->H, hipMemcpyHostToDevice, st);
-    draco_gemv_launch(*f->g, w.xn, w.g, nullptr, 0, f->FF, st);
-    draco_gemv_launch(*f->u, w.xn, w.u, nullptr, 0, f->FF, st);
-    dk_swiglu(w.g, w.u, f->FF, st);
+    if (enqueue_gateup(f, w, w.xn, 0, nullptr, 0.f, st)) { report(-1, "m6_dense_op"); return; }
     draco_gemv_launch(*f->d, w.g, w.x, nullptr, 0, f->H, st);
     hipMemcpyAsync(out, w.x, sizeof(float) * f->H, hipMemcpyDeviceToHost, st);
     hipError_t e = hipStreamSynchronize(st);
@@ -616,27 +697,50 @@ int draco_llama_generate(const void* layers_v, int n_layer, int h, float eps, co
     const int ntok = n_prompt + n_gen;
     int* dtok = (int*)scratch(5, sizeof(int) * (ntok + 64));
     float* dlog = (float*)scratch(6, sizeof(float) * (size_t)vocab);
-    float* dred = (float*)scratch(7, (sizeof(float) + sizeof(int)) * ARGMAX_BLOCKS + 64);
+    // head argmax partials: one (value, index) per head block (8 rows per block) + a counter
+    const int hblocks = (vocab + 7) / 8;
+    float* dred = (float*)scratch(7, (sizeof(float) + sizeof(int)) * ((size_t)hblocks + 64) + 256);
     if (!dtok || !dlog || !dred) return report(-2, "draco_llama_generate");
     int* cursor = dtok + ntok + 8;   // index of the token being fed
     int* cur = dtok + ntok + 16;     // its id
-    int* dri = (int*)(dred + ARGMAX_BLOCKS);
+    int* dri = (int*)(dred + hblocks + 32);
+    const bool fused_head = hm->L.code == DRACO_Q4_K || hm->L.code == DRACO_Q6_K || hm->L.code == DRACO_Q8_0;
     std::vector<int> ht(ntok + 64, 0);
     for (int i = 0; i < n_prompt; i++) ht[i] = prompt[i];
     ht[ntok + 8] = 0;
     DRACO_HIP(hipMemcpyAsync(dtok, ht.data(), sizeof(int) * (ntok + 64), hipMemcpyHostToDevice, st));
     if (int rc = upload_state(m, pos0, st)) return report(rc, "draco_llama_generate");
+    (void)cur;
     auto step = [&](bool decode) -> int {
-        dk_pick_token(dtok, cursor, cur, st);
-        dk_embed(*em, cur, 0, m->w.x, st);
+        dk_embed(*em, dtok, cursor, m->w.x, st);
         for (int l = 0; l < n_layer; l++)
             if (int rc = enqueue_layer(m, l, eps, st)) return rc;
-        if (decode) {
-            dk_rmsnorm(m->w.x, nw, m->w.xn, h, eps, st);
-            if (draco_gemv_launch(*hm, m->w.xn, dlog, nullptr, 0, vocab, st)) return fail(-1, "head gemv");
-            // the argmax after feeding token `cursor` is token cursor+1
-            dk_argmax(dlog, vocab, dred, dri, dtok, cursor, 0, st);
+        if (!decode) {
+            dk_advance(m->state, n_layer, cursor, st);
+            return 0;
         }
+        if (fused_head) {
+            // final RMSNorm + vocab GEMV + argmax (-> token cursor+1) + state advance
+            SegLaunch sl = {};
+            sl.nseg = 1;
+            sl.n_in = h;
+            sl.x = m->w.x;
+            sl.do_norm = 1;
+            sl.norm_w = nw;
+            sl.eps = eps;
+            sl.seg[0] = seg_of(hm, EPI_ARGMAX, dlog, nullptr);
+            sl.am_val = dred;
+            sl.am_idx = dri;
+            sl.tokens = dtok;
+            sl.cursor = cursor;
+            sl.advance_state = m->state;
+            sl.advance_layers = n_layer;
+            if (draco_seg_launch(sl, st)) return fail(-1, "head launch rejected");
+            return 0;
+        }
+        dk_rmsnorm(m->w.x, nw, m->w.xn, h, eps, st);
+        if (draco_gemv_launch(*hm, m->w.xn, dlog, nullptr, 0, vocab, st)) return fail(-1, "head gemv");
+        dk_argmax(dlog, vocab, dred, dri, dtok, cursor, 0, st);
         dk_advance(m->state, n_layer, cursor, st);
         return 0;
     };

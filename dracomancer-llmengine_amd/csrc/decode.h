@@ -7,19 +7,22 @@
 constexpr int ARGMAX_BLOCKS = 256;
 
 // Number of T-splits of the decode attention for a cache of max_t rows
-// (about 64 rows per split at full length, at most 64 splits).
+// (about 32 rows per split at full length, at most 64 splits; the merge
+// kernel handles at most 64).
 static inline int attn_nsplit(int max_t) {
-    int n = (max_t + 63) / 64;
+    int n = (max_t + 31) / 32;
     return n < 1 ? 1 : (n > 64 ? 64 : n);
 }
 
 void dk_rmsnorm(const float* x, const float* w, float* out, int h, float eps, hipStream_t st);
 void dk_rope_append(float* q, const float* k, const float* v, float* kc, float* vc, const float* tab,
                     const int* state, int layer, int NH, int NKV, int HD, int rot, hipStream_t st);
-int dk_attention(const float* q, const float* kc, const float* vc, float* part, float* out, const int* state,
-                 int layer, int NH, int NKV, int HD, int max_t, float scale, hipStream_t st);
+// split-T partials + merge; `count` is unused (kept for the caller's buffer plumbing)
+int dk_attention(const float* q, const float* kc, const float* vc, float* part, unsigned* count, float* out,
+                 const int* state, int layer, int NH, int NKV, int HD, int max_t, float scale, hipStream_t st);
 void dk_swiglu(float* g, const float* u, int n, hipStream_t st);
-void dk_embed(const DracoMat& m, const int* tokp, int tok, float* out, hipStream_t st);
+// out[n_in] = dequantized row ids[cursor ? *cursor : 0] of m
+void dk_embed(const DracoMat& m, const int* ids, const int* cursor, float* out, hipStream_t st);
 // out[slotp ? *slotp + 1 : slot] = first index of max(x[0..n))
 void dk_argmax(const float* x, int n, float* pv, int* pi, int* out, const int* slotp, int slot, hipStream_t st);
 void dk_advance(int* state, int n_layer, int* tok_cursor, hipStream_t st);

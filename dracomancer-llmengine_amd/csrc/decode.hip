@@ -81,126 +81,112 @@ __global__ __launch_bounds__(256) void k_rope_append(float* __restrict__ q, cons
 
 // ----------------------------------------------------------- attention --
 // Split-T decode attention.  Block (g, s) handles kv head g and rows
-// [t0, t1) of 0..T for all `rep` q heads that share it, writing an
-// unnormalised partial (o[HD], m, l) per (q head, split).
+// [t0, t1) of 0..T for the `rep` q heads that share it (GQA: q head h reads
+// kv head h/rep, src/m6_engine.c:484).  The block first issues every load of
+// its K and V rows into LDS (one memory round trip), then computes scores,
+// the chunk softmax and P.V from LDS, and writes an unnormalised partial
+// (o[HD], m, l) per (q head, split).  k_attn_combine merges the splits:
+//   out[h] = sum_s o_s e^(m_s - M) / sum_s l_s e^(m_s - M),  M = max_s m_s
+// which equals the reference's single-pass softmax up to fp32 rounding.
 constexpr int REPMAX = 8;
 
 template <int HD>
-__global__ __launch_bounds__(256) void k_attn_partial(const float* __restrict__ q, const float* __restrict__ kc,
-                                                      const float* __restrict__ vc, float* __restrict__ part,
-                                                      const int* __restrict__ st, int layer, int NH, int NKV,
-                                                      int nsplit, int chunk_max, float scale) {
+__global__ __launch_bounds__(256) void k_attn_part(const float* __restrict__ q, const float* __restrict__ kc,
+                                                   const float* __restrict__ vc, float* __restrict__ part,
+                                                   const int* __restrict__ st, int layer, int NH, int NKV,
+                                                   int nsplit, int chunk_max, float scale) {
     extern __shared__ float sh[];
+    constexpr int KP = HD + 4;  // padded K row (LDS bank spread)
     const int g = blockIdx.x, s = blockIdx.y;
     const int rep = NH / NKV, KD = NKV * HD;
     const int Tn = st[1 + layer] + 1;
     const int chunk = (Tn + nsplit - 1) / nsplit;
     const int t0 = s * chunk, t1 = min(Tn, t0 + chunk);
     const int n = max(0, t1 - t0);
-    float* qs = sh;                    // [rep][HD]
-    float* sc = qs + rep * HD;         // [rep][chunk_max]
-    float* ml = sc + rep * chunk_max;  // [rep][2]
-    float* red = ml + 2 * REPMAX;      // [4][rep][HD]
+    float* qs = sh;                       // [rep][HD]
+    float* ks = qs + rep * HD;            // [chunk_max][KP]
+    float* vs = ks + chunk_max * KP;      // [chunk_max][HD]
+    float* sc = vs + chunk_max * HD;      // [rep][chunk_max]
+    float* ml = sc + rep * chunk_max;     // [rep][2]
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    for (int i = tid; i < rep * HD; i += 256) qs[i] = q[(size_t)g * rep * HD + i];
-    __syncthreads();
-    // scores: one row per thread
-    for (int t = tid; t < n; t += 256) {
-        const float* kt = kc + (size_t)(t0 + t) * KD + g * HD;
-        float acc[REPMAX];
-#pragma unroll
-        for (int j = 0; j < REPMAX; j++) acc[j] = 0.f;
-        for (int d = 0; d < HD; d += 4) {
-            const float4 kv = ld4(kt + d);
-#pragma unroll
-            for (int j = 0; j < REPMAX; j++) {
-                if (j < rep) {
-                    const float* qj = qs + j * HD + d;
-                    acc[j] = fmaf(qj[0], kv.x, acc[j]);
-                    acc[j] = fmaf(qj[1], kv.y, acc[j]);
-                    acc[j] = fmaf(qj[2], kv.z, acc[j]);
-                    acc[j] = fmaf(qj[3], kv.w, acc[j]);
-                }
-            }
-        }
-        for (int j = 0; j < rep; j++) sc[j * chunk_max + t] = acc[j] * scale;
+    constexpr int C4 = HD / 4;
+    for (int i = tid; i < rep * C4; i += 256) {
+        const float4 v = ld4(q + (size_t)g * rep * HD + 4 * i);
+        *reinterpret_cast<float4*>(qs + 4 * i) = v;
+    }
+    for (int i = tid; i < n * C4; i += 256) {
+        const int t = i / C4, c = i % C4;
+        const size_t off = (size_t)(t0 + t) * KD + g * HD + 4 * c;
+        const float4 kv = ld4(kc + off), vv = ld4(vc + off);
+        *reinterpret_cast<float4*>(ks + t * KP + 4 * c) = kv;
+        *reinterpret_cast<float4*>(vs + t * HD + 4 * c) = vv;
     }
     __syncthreads();
-    // per head: max, exp, sum (wave j handles heads j, j+4, ...)
+    for (int pr = tid; pr < n * rep; pr += 256) {
+        const int t = pr / rep, j = pr % rep;
+        const float* kt = ks + t * KP;
+        const float* qj = qs + j * HD;
+        float acc = 0.f;
+#pragma unroll 8
+        for (int d = 0; d < HD; d++) acc = fmaf(qj[d], kt[d], acc);
+        sc[j * chunk_max + t] = acc * scale;
+    }
+    __syncthreads();
     for (int j = wv; j < rep; j += 4) {
         float m = -INFINITY;
         for (int t = lane; t < n; t += 64) m = fmaxf(m, sc[j * chunk_max + t]);
         m = wave_max(m);
         float l = 0.f;
         for (int t = lane; t < n; t += 64) {
-            const float p = n > 0 ? expf(sc[j * chunk_max + t] - m) : 0.f;
+            const float p = expf(sc[j * chunk_max + t] - m);
             sc[j * chunk_max + t] = p;
             l += p;
         }
         l = wave_sum(l);
         if (lane == 0) {
-            ml[2 * j] = m;
+            ml[2 * j] = n > 0 ? m : -INFINITY;
             ml[2 * j + 1] = l;
         }
     }
     __syncthreads();
-    // P.V: wave wv takes rows wv, wv+4, ...; lanes span the head dims
-    constexpr int DPL = HD / 64;  // dims per lane
-    float o[REPMAX][DPL];
-#pragma unroll
-    for (int j = 0; j < REPMAX; j++)
-#pragma unroll
-        for (int e = 0; e < DPL; e++) o[j][e] = 0.f;
-    for (int t = wv; t < n; t += 4) {
-        const float* vt = vc + (size_t)(t0 + t) * KD + g * HD;
-        float vv[DPL];
-#pragma unroll
-        for (int e = 0; e < DPL; e++) vv[e] = vt[lane + 64 * e];
-#pragma unroll
-        for (int j = 0; j < REPMAX; j++)
-            if (j < rep) {
-                const float p = sc[j * chunk_max + t];
-#pragma unroll
-                for (int e = 0; e < DPL; e++) o[j][e] = fmaf(p, vv[e], o[j][e]);
-            }
-    }
-    for (int j = 0; j < rep; j++)
-#pragma unroll
-        for (int e = 0; e < DPL; e++) red[(wv * rep + j) * HD + lane + 64 * e] = o[j][e];
-    __syncthreads();
     for (int i = tid; i < rep * HD; i += 256) {
         const int j = i / HD, d = i % HD;
-        const float acc = red[(0 * rep + j) * HD + d] + red[(1 * rep + j) * HD + d] +
-                          red[(2 * rep + j) * HD + d] + red[(3 * rep + j) * HD + d];
-        const int h = g * rep + j;
-        float* pp = part + ((size_t)h * nsplit + s) * (HD + 2);
+        const float* pj = sc + j * chunk_max;
+        float acc = 0.f;
+        for (int t = 0; t < n; t++) acc = fmaf(pj[t], vs[t * HD + d], acc);
+        float* pp = part + ((size_t)(g * rep + j) * nsplit + s) * (HD + 2);
         pp[d] = acc;
         if (d == 0) {
-            pp[HD] = n > 0 ? ml[2 * j] : -INFINITY;
-            pp[HD + 1] = n > 0 ? ml[2 * j + 1] : 0.f;
+            pp[HD] = ml[2 * j];
+            pp[HD + 1] = ml[2 * j + 1];
         }
     }
 }
 
-// merge the splits of every q head: out[h][d] = sum_s o_s e^(m_s-M) / sum_s l_s e^(m_s-M)
+// one block per q head, one thread per head dim
 __global__ __launch_bounds__(128) void k_attn_combine(const float* __restrict__ part, float* __restrict__ out,
                                                       int nsplit, int HD) {
-    const int h = blockIdx.x;
+    __shared__ float wsp[64];
+    __shared__ float invL;
+    const int h = blockIdx.x, tid = threadIdx.x;
     const float* ph = part + (size_t)h * nsplit * (HD + 2);
-    float M = -INFINITY;
-    for (int s = 0; s < nsplit; s++) M = fmaxf(M, ph[s * (HD + 2) + HD]);
-    float L = 0.f;
-    for (int s = 0; s < nsplit; s++) {
-        const float m = ph[s * (HD + 2) + HD];
-        if (m > -INFINITY) L += ph[s * (HD + 2) + HD + 1] * expf(m - M);
-    }
-    const float invL = 1.f / L;
-    for (int d = threadIdx.x; d < HD; d += blockDim.x) {
-        float acc = 0.f;
-        for (int s = 0; s < nsplit; s++) {
-            const float m = ph[s * (HD + 2) + HD];
-            if (m > -INFINITY) acc += ph[s * (HD + 2) + d] * expf(m - M);
+    if (tid < 64) {
+        float M = -INFINITY;
+        for (int k = 0; k < nsplit; k++) M = fmaxf(M, ph[k * (HD + 2) + HD]);
+        float w = 0.f, l = 0.f;
+        if (tid < nsplit) {
+            const float m = ph[tid * (HD + 2) + HD];
+            w = m > -INFINITY ? expf(m - M) : 0.f;
+            l = ph[tid * (HD + 2) + HD + 1] * w;
+            wsp[tid] = w;
         }
+        l = wave_sum(l);
+        if (tid == 0) invL = 1.f / l;
+    }
+    __syncthreads();
+    for (int d = tid; d < HD; d += blockDim.x) {
+        float acc = 0.f;
+        for (int k = 0; k < nsplit; k++) acc = fmaf(ph[k * (HD + 2) + d], wsp[k], acc);
         out[(size_t)h * HD + d] = acc * invL;
     }
 }
@@ -218,9 +204,9 @@ __global__ __launch_bounds__(256) void k_swiglu(float* __restrict__ g, const flo
 // bit-identical to the host decoders ((d*sc)*q for Q6_K, d*sc*q - dmin*m for
 // Q4_K, q*d for Q8_0).
 __global__ __launch_bounds__(256) void k_embed(const uint8_t* __restrict__ base, DracoLayout L,
-                                               const int* __restrict__ tokp, int tok_host,
+                                               const int* __restrict__ ids, const int* __restrict__ cursor,
                                                float* __restrict__ out) {
-    const int tok = tokp ? *tokp : tok_host;
+    const int tok = ids[cursor ? cursor[0] : 0];
     const int n_in = L.n_in, nb = L.nb;
     for (int p = blockIdx.x * blockDim.x + threadIdx.x; p < n_in; p += gridDim.x * blockDim.x) {
         const size_t blk = (size_t)tok * nb + p / draco_block_values(L.code);
@@ -334,19 +320,22 @@ void dk_rope_append(float* q, const float* k, const float* v, float* kc, float* 
                        NKV, HD, rot);
 }
 
-int dk_attention(const float* q, const float* kc, const float* vc, float* part, float* out, const int* state,
-                 int layer, int NH, int NKV, int HD, int max_t, float scale, hipStream_t st) {
+int dk_attention(const float* q, const float* kc, const float* vc, float* part, unsigned* count, float* out,
+                 const int* state, int layer, int NH, int NKV, int HD, int max_t, float scale, hipStream_t st) {
+    (void)count;
     const int rep = NH / NKV;
     if (rep < 1 || rep > REPMAX || NH % NKV) return -1;
     const int nsplit = attn_nsplit(max_t);
     const int chunk_max = (max_t + nsplit - 1) / nsplit;
-    const size_t shm = sizeof(float) * (rep * HD + rep * chunk_max + 2 * REPMAX + 4 * rep * HD);
+    const size_t shm = sizeof(float) * ((size_t)rep * HD + (size_t)chunk_max * (HD + 4) + (size_t)chunk_max * HD +
+                                        (size_t)rep * chunk_max + 2 * REPMAX);
+    if (shm > 160 * 1024) return -1;
     const dim3 grid(NKV, nsplit);
     if (HD == 64)
-        hipLaunchKernelGGL(k_attn_partial<64>, grid, dim3(256), shm, st, q, kc, vc, part, state, layer, NH, NKV,
+        hipLaunchKernelGGL(k_attn_part<64>, grid, dim3(256), shm, st, q, kc, vc, part, state, layer, NH, NKV,
                            nsplit, chunk_max, scale);
     else if (HD == 128)
-        hipLaunchKernelGGL(k_attn_partial<128>, grid, dim3(256), shm, st, q, kc, vc, part, state, layer, NH, NKV,
+        hipLaunchKernelGGL(k_attn_part<128>, grid, dim3(256), shm, st, q, kc, vc, part, state, layer, NH, NKV,
                            nsplit, chunk_max, scale);
     else
         return -1;
@@ -359,9 +348,9 @@ void dk_swiglu(float* g, const float* u, int n, hipStream_t st) {
     hipLaunchKernelGGL(k_swiglu, dim3(blocks), dim3(256), 0, st, g, u, n);
 }
 
-void dk_embed(const DracoMat& m, const int* tokp, int tok, float* out, hipStream_t st) {
+void dk_embed(const DracoMat& m, const int* ids, const int* cursor, float* out, hipStream_t st) {
     const int blocks = (m.L.n_in + 255) / 256;
-    hipLaunchKernelGGL(k_embed, dim3(blocks), dim3(256), 0, st, m.dev, m.L, tokp, tok, out);
+    hipLaunchKernelGGL(k_embed, dim3(blocks), dim3(256), 0, st, m.dev, m.L, ids, cursor, out);
 }
 
 void dk_argmax(const float* x, int n, float* pv, int* pi, int* out, const int* slotp, int slot, hipStream_t st) {

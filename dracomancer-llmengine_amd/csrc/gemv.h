@@ -14,3 +14,59 @@ struct DracoMat {
 int draco_gemv_launch(const DracoMat& m, const float* x, float* y, const float* yadd, int row0,
                       int row1, hipStream_t st);
 int draco_gemv_supported(int code);
+
+// ---- fused segment GEMV --------------------------------------------------
+// One launch computes several matrices (segments) of ONE weight format that
+// share the input x.
+// Optional prologue: x <- x * (1/sqrt(mean(x^2)+eps)) * norm_w (RMSNorm,
+// src/m6_engine.c:31-37), computed by every block.  Per-segment epilogue:
+enum {
+    EPI_STORE = 0,      // y[r] = dot
+    EPI_RESID = 1,      // y[r] = yadd[r] + dot   (y may alias yadd)
+    EPI_ROPE_Q = 2,     // pairs (2i, 2i+1) rotated by the rope table -> y
+    EPI_ROPE_K = 3,     // rotated pairs -> kcache row T
+    EPI_V_APPEND = 4,   // -> vcache row T
+    EPI_SWIGLU = 5,     // dual segment: y[r] = silu(dot_gate) * dot_up  (seg i = gate, seg i+1 = up)
+    EPI_ARGMAX = 6,     // y[r] = dot, per-block argmax partials, then a finalize launch
+                        // writes tokens[*cursor + 1] and advances the token state
+};
+
+struct SegDesc {
+    const uint8_t* base;
+    DracoLayout L;
+    float* y;
+    const float* yadd;
+    int epi;
+    int first_block;  // first grid block of this segment
+    int n_blocks;
+};
+
+constexpr int SEG_MAX = 4;
+
+struct SegLaunch {
+    SegDesc seg[SEG_MAX];
+    int nseg;
+    int n_in;
+    const float* x;
+    const float* norm_w;  // nullable
+    int do_norm;
+    float eps;
+    float* xn_out;        // nullable: block 0 writes the normalised x here
+    // rope / KV epilogue context
+    const float* rope_tab;  // [pos][rot/2][cos, sin]
+    const int* state;       // [pos, tlen per layer ...]
+    int layer;
+    int head_dim, rot, kv_dim;
+    float* kc;
+    float* vc;
+    // argmax epilogue context
+    float* am_val;      // [n_blocks] partials
+    int* am_idx;
+    int* tokens;
+    const int* cursor;  // token written to tokens[*cursor + 1], then *cursor += 1
+    int* advance_state; // nullable: pos and every layer's tlen += 1
+    int advance_layers;
+};
+
+// Builds grid ranges for every segment and launches the fused kernel.
+int draco_seg_launch(SegLaunch& a, hipStream_t st);
