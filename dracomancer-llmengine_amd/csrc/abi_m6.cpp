@@ -382,8 +382,10 @@ int enqueue_qkv(DevAttn* a, Work& w, const float* x, int norm, const float* norm
         s.do_norm = norm;
         s.norm_w = norm_w;
         s.eps = eps;
-        for (int j = i; j < 3; j++)  // every not-yet-issued segment of this format
-            if (!done[j] && all[j].L.code == all[i].L.code) {
+        // every not-yet-issued segment of the same kernel family (Q4_K/Q6_K share one)
+        auto fam = [](int c) { return c == DRACO_Q8_0 ? 0 : 1; };
+        for (int j = i; j < 3; j++)
+            if (!done[j] && fam(all[j].L.code) == fam(all[i].L.code)) {
                 s.seg[s.nseg++] = all[j];
                 done[j] = true;
             }

@@ -16,8 +16,9 @@ int draco_gemv_launch(const DracoMat& m, const float* x, float* y, const float* 
 int draco_gemv_supported(int code);
 
 // ---- fused segment GEMV --------------------------------------------------
-// One launch computes several matrices (segments) of ONE weight format that
-// share the input x.
+// One launch computes several matrices (segments) that share the input x.
+// Q4_K and Q6_K segments may be mixed in one launch; Q8_0 segments must all be
+// Q8_0.
 // Optional prologue: x <- x * (1/sqrt(mean(x^2)+eps)) * norm_w (RMSNorm,
 // src/m6_engine.c:31-37), computed by every block.  Per-segment epilogue:
 enum {
@@ -37,8 +38,13 @@ struct SegDesc {
     float* y;
     const float* yadd;
     int epi;
-    int first_block;  // first grid block of this segment
+    int row0, row1;   // rows computed: [row0, row1); row1 == 0 means n_out
+    // filled by draco_seg_launch
+    int first_block;  // Q8_0 path: first grid block of this segment
     int n_blocks;
+    int first_tile;   // Q4_K/Q6_K path: first global tile index of this segment
+    int n_tiles;
+    int tile0;        // first 16-row tile of the row range
 };
 
 constexpr int SEG_MAX = 4;

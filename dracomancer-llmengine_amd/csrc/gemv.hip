@@ -1,27 +1,45 @@
-// gemv.hip -- fp32-activation GEMV over block-quantized weights (gfx950).
+// gemv.hip -- GEMV over block-quantized weights with fp32 activations (gfx950).
 //
 //   y[r] = sum_k W[r][k] * x[k]
 //
 // Reference semantics: dot_row / m5_gemv_range, src/m5_kern_scalar.c:48-165
 // (decoded weight w = d*sc*q - dmin*m for Q4_K, d*sc*(q-32) for Q6_K, d*q
-// for Q8_0).  The summation order differs from the reference's sequential
-// loop (a wave tree), so results agree to fp32 rounding, not bitwise.
+// for Q8_0).  Summation orders differ from the reference's sequential loop,
+// so results agree to fp32 rounding, not bitwise.
 //
-// Mapping: one wave64 owns R consecutive rows.  A row is cut into "units"
-// (16 quant bytes for Q4_K, 48 for Q6_K, one 32-value block for Q8_0); lane
-// l takes units l, l+64, ...  Each unit's x slice is loaded once and reused
-// for the wave's R rows (and for the paired row of a second matrix in the
-// SwiGLU dual mode).  The block scale is applied once per 16/32 values to an
-// inner dot of integer-valued weights:
-//   Q4_K: d*sc_j*(sum q*x) - dmin*m_j*(sum x)
-//   Q6_K: d*sc_g*((sum (q+32)*x) - 32*(sum x))
-//   Q8_0: d*(sum q*x)
-// which is the reference's per-weight expression regrouped.
+// Q4_K / Q6_K (k_dq): int8 MFMA on exact integer digits of x.
+//   x is cut into groups of 16 values.  Group G gets a power-of-two scale
+//   2^k, k = ilogb(max|x_G|) - 5, so |x|/2^k < 64, and X = rint(x*2^(21-k))
+//   is an integer below 2^27 in magnitude: X = d0*2^21 + d1*2^14 + d2*2^7 + d3
+//   with d0 in [-64,63] and d1..d3 in [0,127] -- four int8 digits, and
+//   |x - X*2^(k-21)| <= 2^(k-22), below half an fp32 ulp of the group maximum.
+//   One v_mfma_i32_16x16x64_i8 multiplies 16 weight rows (B: the raw 4- or
+//   6-bit quants, lane (j, g) holding 16 K values of row j) by the digits
+//   (A: block-diagonal, digit rows 4g..4g+3 non-zero only against lane group
+//   g's K values).  Lane (j, g) receives the four exact int32 digit dots of
+//   its (row, group); they fold to fp32 as (128*C0 + C1) + (128*C2 + C3)*2^-14
+//   times 2^(k-7), and the block scales apply per group:
+//     Q4_K: d*sc_j*(x.q) - dmin*m_j*(sum x)
+//     Q6_K: d*sc*(x.q - 32*(sum x))
+//   which is the reference's per-weight expression regrouped.
+//   The device layout is the 16-row tile layout of formats.h, so each of a
+//   lane's weight loads is one aligned 16-byte vector and every wave load
+//   instruction reads 1 KB contiguously.  The Q4_K high nibble is read with
+//   one AND thanks to the XOR 0x80 applied at repack: the byte then holds
+//   16*(u-8), so x.u = C/16 + 8*(sum x).
 //
-// The fused segment kernel (k_seg) adds an RMSNorm prologue and epilogues
-// (rope + KV append, residual add, SwiGLU, argmax) so a llama layer needs
-// five launches instead of thirteen.
+//   Mapping: a block of NW waves owns one 16-row tile at a time (tiles of all
+//   segments are numbered consecutively and visited grid-stride); wave w takes
+//   super-blocks w, w+NW, ... of the tile; every wave runs the same number of
+//   items per tile (padding items are skipped) so the per-tile reduction
+//   barrier is uniform.  The next item's weights are loaded before the current
+//   one is computed (two register buffers), and the first item's loads are in
+//   flight while the prologue (RMSNorm + digits into LDS) runs.
+//
+// Q8_0 (k_seg): one wave owns SEG_R rows; fp32 VALU dot per 32-value block.
 #include <hip/hip_runtime.h>
+
+#include <mutex>
 
 #include "dev_common.h"
 #include "formats.h"
@@ -29,130 +47,358 @@
 
 namespace {
 
-constexpr int SEG_R = 2;                  // rows per wave in k_seg
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+constexpr int SEG_R = 2;                  // rows per wave in k_seg (Q8_0)
 constexpr int SEG_ROWS = 4 * SEG_R;       // rows per block (4 waves)
+constexpr int XP_MAXV = 4;                // float4s of x per thread held by the prologue
 
-// ------------------------------------------------------------- traits --
-struct FQ4K {
-    static constexpr int UPB = 8;   // units per 256-value block
-    static constexpr int NX = 32;   // x values per unit
-    static constexpr int NS = 2;    // partial x sums per unit
-    __device__ static void xslice(const float* x, int u, float* xv, float* sx) {
-        const int b = u >> 3, j2 = (u & 7) >> 1, k0 = (u & 1) * 16;
-        const float* p = x + b * 256 + j2 * 64 + k0;
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const float4 a = ld4(p + 4 * i), c = ld4(p + 32 + 4 * i);
-            xv[4 * i] = a.x; xv[4 * i + 1] = a.y; xv[4 * i + 2] = a.z; xv[4 * i + 3] = a.w;
-            xv[16 + 4 * i] = c.x; xv[17 + 4 * i] = c.y; xv[18 + 4 * i] = c.z; xv[19 + 4 * i] = c.w;
-        }
-        sx[0] = sx[1] = 0.f;
-#pragma unroll
-        for (int i = 0; i < 16; i++) {
-            sx[0] += xv[i];
-            sx[1] += xv[16 + i];
-        }
-    }
-    __device__ static float dot(const uint8_t* base, const DracoLayout& L, int row, int u, const float* xv,
-                                const float* sx) {
-        const size_t blk = (size_t)row * L.nb + (u >> 3);
-        const uint4 q = ldu4(base + L.off[0] + blk * 128 + (size_t)(u & 7) * 16);
-        const uint4 h = ldu4(base + L.off[1] + blk * 16);
-        const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
-        float sl = 0.f, sh = 0.f;
-#pragma unroll
-        for (int dw = 0; dw < 4; dw++) {
-            const uint32_t lo = qw[dw] & 0x0F0F0F0Fu, hi = (qw[dw] >> 4) & 0x0F0F0F0Fu;
-#pragma unroll
-            for (int k = 0; k < 4; k++) {
-                sl = fmaf(ubyte_f(lo, k), xv[4 * dw + k], sl);
-                sh = fmaf(ubyte_f(hi, k), xv[16 + 4 * dw + k], sh);
-            }
-        }
-        // six-bit scales/mins of sub-blocks 2*j2 and 2*j2+1 (src/m5_kern_scalar.c:39-46)
-        const int j2 = (u & 7) >> 1;
-        const float d = h2f((uint16_t)(h.x & 0xFFFF)), dmin = h2f((uint16_t)(h.x >> 16));
-        const int s0 = 16 * (j2 & 1), s1 = s0 + 8;  // bit offsets of bytes (2*j2)&3, (2*j2+1)&3
-        int sc0, m0, sc1, m1;
-        if (j2 < 2) {
-            sc0 = (h.y >> s0) & 63;
-            m0 = (h.z >> s0) & 63;
-            sc1 = (h.y >> s1) & 63;
-            m1 = (h.z >> s1) & 63;
-        } else {
-            sc0 = ((h.w >> s0) & 15) | (((h.y >> (s0 + 6)) & 3) << 4);
-            m0 = ((h.w >> (s0 + 4)) & 15) | (((h.z >> (s0 + 6)) & 3) << 4);
-            sc1 = ((h.w >> s1) & 15) | (((h.y >> (s1 + 6)) & 3) << 4);
-            m1 = ((h.w >> (s1 + 4)) & 15) | (((h.z >> (s1 + 6)) & 3) << 4);
-        }
-        return (d * (float)sc0 * sl - dmin * (float)m0 * sx[0]) + (d * (float)sc1 * sh - dmin * (float)m1 * sx[1]);
-    }
+// ------------------------------------------------------------------ k_dq --
+struct Frag {
+    uint4 a, b, c;   // Q4_K: qs r=0, qs r=1, header.  Q6_K: ql A, ql B, qh
+    uint32_t sc, d;  // Q6_K: 4 scales, d
 };
 
-// unit (b, g, c) = ql[64g+16c..+16] (A), ql[64g+32+16c..+16] (B), qh[32g+16c..+16]:
-//   A.lo -> values 128g+16c+i      scale group 8g+c
-//   B.lo -> values 128g+32+16c+i   scale group 8g+c+2
-//   A.hi -> values 128g+64+16c+i   scale group 8g+c+4
-//   B.hi -> values 128g+96+16c+i   scale group 8g+c+6
-// (the GGUF bit map of src/m5_kern_scalar.c:115-142 regrouped by qh byte)
-struct FQ6K {
-    static constexpr int UPB = 4, NX = 64, NS = 4;
-    __device__ static void xslice(const float* x, int u, float* xv, float* sx) {
-        const int b = u >> 2, g = (u >> 1) & 1, c = u & 1;
-        const float* p = x + b * 256 + 128 * g + 16 * c;
-#pragma unroll
-        for (int run = 0; run < 4; run++) {
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const float4 a = ld4(p + 32 * run + 4 * i);
-                xv[16 * run + 4 * i] = a.x; xv[16 * run + 4 * i + 1] = a.y;
-                xv[16 * run + 4 * i + 2] = a.z; xv[16 * run + 4 * i + 3] = a.w;
-            }
-            float s = 0.f;
-#pragma unroll
-            for (int i = 0; i < 16; i++) s += xv[16 * run + i];
-            sx[run] = s;
-        }
-    }
-    __device__ static float dot(const uint8_t* base, const DracoLayout& L, int row, int u, const float* xv,
-                                const float* sx) {
-        const int g = (u >> 1) & 1, c = u & 1;
-        const size_t blk = (size_t)row * L.nb + (u >> 2);
-        const uint4 qa = ldu4(base + L.off[0] + blk * 128 + 64 * g + 16 * c);
-        const uint4 qb = ldu4(base + L.off[0] + blk * 128 + 64 * g + 32 + 16 * c);
-        const uint4 hv = ldu4(base + L.off[1] + blk * 64 + 32 * g + 16 * c);
-        const uint4 sv = ldu4(base + L.off[2] + blk * 16);
-        const float d = h2f(*reinterpret_cast<const uint16_t*>(base + L.off[3] + blk * 2));
-        const uint32_t A[4] = {qa.x, qa.y, qa.z, qa.w};
-        const uint32_t B[4] = {qb.x, qb.y, qb.z, qb.w};
-        const uint32_t H[4] = {hv.x, hv.y, hv.z, hv.w};
-        float s[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int dw = 0; dw < 4; dw++) {
-            const uint32_t v0 = (A[dw] & 0x0F0F0F0Fu) | ((H[dw] << 4) & 0x30303030u);
-            const uint32_t v1 = (B[dw] & 0x0F0F0F0Fu) | ((H[dw] << 2) & 0x30303030u);
-            const uint32_t v2 = ((A[dw] >> 4) & 0x0F0F0F0Fu) | (H[dw] & 0x30303030u);
-            const uint32_t v3 = ((B[dw] >> 4) & 0x0F0F0F0Fu) | ((H[dw] >> 2) & 0x30303030u);
-#pragma unroll
-            for (int k = 0; k < 4; k++) {
-                s[0] = fmaf(ubyte_f(v0, k), xv[4 * dw + k], s[0]);
-                s[1] = fmaf(ubyte_f(v1, k), xv[16 + 4 * dw + k], s[1]);
-                s[2] = fmaf(ubyte_f(v2, k), xv[32 + 4 * dw + k], s[2]);
-                s[3] = fmaf(ubyte_f(v3, k), xv[48 + 4 * dw + k], s[3]);
-            }
-        }
-        const uint32_t S[4] = {sv.x, sv.y, sv.z, sv.w};
-        float part = 0.f;
-#pragma unroll
-        for (int run = 0; run < 4; run++) {
-            const int gi = 8 * g + c + 2 * run;
-            const float dsc = d * (float)(int)(int8_t)(S[gi >> 2] >> (8 * (gi & 3)));
-            part += dsc * (s[run] - 32.f * sx[run]);
-        }
-        return part;
-    }
-};
+__device__ __forceinline__ void load_q4(const uint8_t* item, int lane, Frag& f) {
+    f.a = ldu4(item + 16 * lane);
+    f.b = ldu4(item + 1024 + 16 * lane);
+    f.c = ldu4(item + 2048 + 16 * (lane & 15));
+    f.sc = 0u;
+    f.d = 0u;
+}
 
+__device__ __forceinline__ void load_q6(const uint8_t* item, int lane, Frag& f) {
+    f.a = ldu4(item + 16 * lane);
+    f.b = ldu4(item + 1024 + 16 * lane);
+    f.c = ldu4(item + 2048 + 16 * lane);
+    f.sc = *reinterpret_cast<const uint32_t*>(item + 3072 + 4 * lane);
+    f.d = *reinterpret_cast<const uint16_t*>(item + 3328 + 2 * (lane & 15));
+}
+
+__device__ __forceinline__ float fold(const v4i C) {
+    const int i0 = (C[0] << 7) + C[1], i1 = (C[2] << 7) + C[3];
+    return fmaf((float)i1, 6.103515625e-05f, (float)i0);
+}
+
+// One Q4_K item: 16 rows x 256 values.  xa: this lane's A address for the
+// item's first group (or the zero region), xsm + gi: its (scale, sum) pairs.
+// Returns (d * sum_g sc*(x.q), dmin * sum_g m*(sum x)).
+__device__ __forceinline__ float2 dot_q4(const Frag& f, const int8_t* xa, const float2* xsm, int gi, int g) {
+    const int gh = g >> 1;
+    float sD = 0.f, sM = 0.f;
+#pragma unroll
+    for (int r = 0; r < 2; r++) {
+        const uint4 q = r ? f.b : f.a;
+#pragma unroll
+        for (int nib = 0; nib < 2; nib++) {
+            const uint32_t m = nib ? 0xF0F0F0F0u : 0x0F0F0F0Fu;
+            const v4i B = {(int)(q.x & m), (int)(q.y & m), (int)(q.z & m), (int)(q.w & m)};
+            const int go = 8 * r + 2 * nib;  // group offset of this MFMA (lane adds 4*gh + (g&1))
+            const v4i A = *reinterpret_cast<const v4i*>(xa + go * 64);
+            const v4i C = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, B, (v4i){0, 0, 0, 0}, 0, 0, 0);
+            const float fv = fold(C);
+            const float2 sm = xsm[gi + go];
+            // six-bit scale/min of sub-block 4r + 2gh + nib (src/m5_kern_scalar.c:39-46)
+            const int s0 = 2 * gh + nib;
+            int sc, mn;
+            if (r == 0) {
+                sc = (f.c.y >> (8 * s0)) & 63;
+                mn = (f.c.z >> (8 * s0)) & 63;
+            } else {
+                sc = ((f.c.w >> (8 * s0)) & 15) | (((f.c.y >> (8 * s0 + 6)) & 3) << 4);
+                mn = ((f.c.w >> (8 * s0 + 4)) & 15) | (((f.c.z >> (8 * s0 + 6)) & 3) << 4);
+            }
+            const float scf = (float)sc;
+            if (nib) {
+                sD = fmaf(scf, fv * (sm.x * 0.0625f), sD);
+                sD = fmaf(8.f * scf, sm.y, sD);
+            } else {
+                sD = fmaf(scf, fv * sm.x, sD);
+            }
+            sM = fmaf((float)mn, sm.y, sM);
+        }
+    }
+    return make_float2(h2f((uint16_t)(f.c.x & 0xFFFF)) * sD, h2f((uint16_t)(f.c.x >> 16)) * sM);
+}
+
+// One Q6_K item.  Fragment r (0..3) holds values 128*g2 + 32*r + 16*c + e
+// (g2 = g>>1, c = g&1), i.e. group 8*g2 + 2*r + c, with the GGUF bit map of
+// src/m5_kern_scalar.c:115-142: low nibble of ql A (r=0) / ql B (r=1), high
+// nibble of ql A (r=2) / ql B (r=3), and qh bits 2r.
+__device__ __forceinline__ float dot_q6(const Frag& f, const int8_t* xa, const float2* xsm, int gi) {
+    const uint32_t A4[4] = {f.a.x, f.a.y, f.a.z, f.a.w};
+    const uint32_t B4[4] = {f.b.x, f.b.y, f.b.z, f.b.w};
+    const uint32_t H4[4] = {f.c.x, f.c.y, f.c.z, f.c.w};
+    float s = 0.f;
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        v4i Bv;
+#pragma unroll
+        for (int w = 0; w < 4; w++) {
+            uint32_t v;
+            if (r == 0) v = (A4[w] & 0x0F0F0F0Fu) | ((H4[w] << 4) & 0x30303030u);
+            else if (r == 1) v = (B4[w] & 0x0F0F0F0Fu) | ((H4[w] << 2) & 0x30303030u);
+            else if (r == 2) v = ((A4[w] >> 4) & 0x0F0F0F0Fu) | (H4[w] & 0x30303030u);
+            else v = ((B4[w] >> 4) & 0x0F0F0F0Fu) | ((H4[w] >> 2) & 0x30303030u);
+            Bv[w] = (int)v;
+        }
+        const v4i A = *reinterpret_cast<const v4i*>(xa + r * 128);
+        const v4i C = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, Bv, (v4i){0, 0, 0, 0}, 0, 0, 0);
+        const float2 sm = xsm[gi + 2 * r];
+        const float scf = (float)(int)(int8_t)(f.sc >> (8 * r));
+        s = fmaf(scf, fmaf(-32.f, sm.y, fold(C) * sm.x), s);
+    }
+    return h2f((uint16_t)f.d) * s;
+}
+
+__device__ __forceinline__ void am_merge(float& v, int& i, float v2, int i2) {
+    if (v2 > v || (v2 == v && i2 < i)) {
+        v = v2;
+        i = i2;
+    }
+}
+
+__device__ __forceinline__ int seg_of_tile(const SegLaunch& a, int T) {
+    int si = 0;
+    for (int i = 1; i < a.nseg; i++)
+        if (T >= a.seg[i].first_tile) si = i;
+    return si;
+}
+
+// FM: 1 = Q4_K segments only, 2 = Q6_K only, 3 = both (per-tile switch).
+template <int NW, int FM, bool DUAL>
+__global__ __launch_bounds__(64 * NW) void k_dq(const SegLaunch a) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    constexpr int NT = 64 * NW;
+    const int n_in = a.n_in, nb = n_in >> 8, ng = n_in >> 4, n4 = n_in >> 2;
+    int8_t* xd = reinterpret_cast<int8_t*>(smem);                           // [ng][4 digits][16]
+    int8_t* zero = xd + (size_t)ng * 64;                                    // 1 KB of zeros
+    float2* xsm = reinterpret_cast<float2*>(smem + (size_t)ng * 64 + 1024);  // [ng] (2^(k-7), sum x)
+    float* red = reinterpret_cast<float*>(xsm + ng);                        // [2][NW][16]
+
+    const int tid = threadIdx.x, lane = tid & 63, j = lane & 15, g = lane >> 4;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int bx = blockIdx.x, G = gridDim.x;
+    int total = 0;
+    for (int i = 0; i < a.nseg; i++) total += a.seg[i].n_tiles;
+    const int ipt = (nb + NW - 1) / NW;
+    const int my_tiles = bx < total ? (total - bx + G - 1) / G : 0;
+    const int n_items = my_tiles * ipt;
+
+    auto is_q4 = [&](int T) -> bool {
+        if (FM != 3) return FM == 1;
+        return a.seg[seg_of_tile(a, T)].L.code == DRACO_Q4_K;
+    };
+    auto load = [&](int T, int b, Frag& f, Frag& f2) {
+        const int si = seg_of_tile(a, T);
+        const bool q4 = is_q4(T);
+        const size_t ib = q4 ? DRACO_Q4T_ITEM : DRACO_Q6T_ITEM;
+        const size_t off = ((size_t)(T - a.seg[si].first_tile + a.seg[si].tile0) * nb + b) * ib;
+        if (q4) load_q4(a.seg[si].base + off, lane, f);
+        else load_q6(a.seg[si].base + off, lane, f);
+        if (DUAL) {
+            if (q4) load_q4(a.seg[si + 1].base + off, lane, f2);
+            else load_q6(a.seg[si + 1].base + off, lane, f2);
+        }
+    };
+
+    // ---- prologue part 1: x (and norm weight) loads, then the first item's weights
+    float4 xv[XP_MAXV], wv[XP_MAXV];
+#pragma unroll
+    for (int q = 0; q < XP_MAXV; q++) {
+        const int i4 = tid + q * NT;
+        if (i4 < n4) {
+            xv[q] = ld4(a.x + 4 * i4);
+            if (a.do_norm && a.norm_w) wv[q] = ld4(a.norm_w + 4 * i4);
+        }
+    }
+    Frag P0, P1, Q0, Q1;
+    int ct = bx, cb = w, cp = 0;  // current item: tile, super-block, position in tile
+    if (n_items > 0 && cb < nb) load(ct, cb, P0, Q0);
+    for (int i = tid; i < 256; i += NT) reinterpret_cast<uint32_t*>(zero)[i] = 0u;
+
+    // ---- prologue part 2: RMSNorm (src/m6_engine.c:31-37) and digits into LDS
+    float inv = 1.f;
+    if (a.do_norm) {
+        float ss = 0.f;
+#pragma unroll
+        for (int q = 0; q < XP_MAXV; q++)
+            if (tid + q * NT < n4) {
+                const float4 v = xv[q];
+                ss = fmaf(v.x, v.x, ss);
+                ss = fmaf(v.y, v.y, ss);
+                ss = fmaf(v.z, v.z, ss);
+                ss = fmaf(v.w, v.w, ss);
+            }
+        ss = wave_sum(ss);
+        if (lane == 0) red[w] = ss;
+        __syncthreads();
+        float tot = 0.f;
+#pragma unroll
+        for (int i = 0; i < NW; i++) tot += red[i];
+        inv = 1.f / sqrtf(tot / (float)n_in + a.eps);
+    }
+#pragma unroll
+    for (int q = 0; q < XP_MAXV; q++) {
+        const int i4 = tid + q * NT;
+        if (i4 >= n4) break;
+        float4 v = xv[q];
+        if (a.do_norm) {
+            if (a.norm_w) {
+                const float4 nw = wv[q];
+                v.x = v.x * inv * nw.x; v.y = v.y * inv * nw.y; v.z = v.z * inv * nw.z; v.w = v.w * inv * nw.w;
+            } else {
+                v.x *= inv; v.y *= inv; v.z *= inv; v.w *= inv;
+            }
+            if (a.xn_out && bx == 0) *reinterpret_cast<float4*>(a.xn_out + 4 * i4) = v;
+        }
+        float am = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+        float sum = (v.x + v.y) + (v.z + v.w);
+        am = fmaxf(am, __shfl_xor(am, 1, 64));
+        am = fmaxf(am, __shfl_xor(am, 2, 64));
+        sum += __shfl_xor(sum, 1, 64);
+        sum += __shfl_xor(sum, 2, 64);
+        const int k = am > 0.f ? max(ilogbf(am) - 5, -100) : 0;
+        const float up = __builtin_bit_cast(float, (uint32_t)(127 + 21 - k) << 23);  // 2^(21-k)
+        const uint32_t X0 = (uint32_t)(int)rintf(v.x * up), X1 = (uint32_t)(int)rintf(v.y * up);
+        const uint32_t X2 = (uint32_t)(int)rintf(v.z * up), X3 = (uint32_t)(int)rintf(v.w * up);
+        const int grp = i4 >> 2, qq = i4 & 3;
+#pragma unroll
+        for (int dg = 0; dg < 4; dg++) {
+            const int sh = 21 - 7 * dg, wd = dg ? 7 : 8;
+            const uint32_t o = __builtin_amdgcn_ubfe(X0, sh, wd) | (__builtin_amdgcn_ubfe(X1, sh, wd) << 8) |
+                               (__builtin_amdgcn_ubfe(X2, sh, wd) << 16) | (__builtin_amdgcn_ubfe(X3, sh, wd) << 24);
+            *reinterpret_cast<uint32_t*>(xd + (grp * 4 + dg) * 16 + 4 * qq) = o;
+        }
+        if (qq == 0) xsm[grp] = make_float2(__builtin_bit_cast(float, (uint32_t)(127 + k - 7) << 23), sum);
+    }
+    __syncthreads();
+
+    // this lane's A row: digit (j&3) of its group, non-zero only when (j>>2) == g
+    const bool adig = (j >> 2) == g;
+    const int gl4 = 4 * (g >> 1) + (g & 1), gl6 = 8 * (g >> 1) + (g & 1);
+    float am_v = -INFINITY;
+    int am_i = 0x7fffffff;
+    float aD = 0.f, aM = 0.f, aD2 = 0.f, aM2 = 0.f;
+
+    auto step = [&](int i, Frag& cur, Frag& nxt, Frag& cur2, Frag& nxt2) {
+        int nt = ct, nbk = cb + NW, np = cp + 1;
+        if (np == ipt) {
+            np = 0;
+            nbk = w;
+            nt = ct + G;
+        }
+        if (i + 1 < n_items && nbk < nb) load(nt, nbk, nxt, nxt2);
+        if (cb < nb) {
+            float cD, cM, cD2 = 0.f, cM2 = 0.f;
+            if (is_q4(ct)) {
+                const int8_t* xa = adig ? xd + (size_t)cb * 1024 + (gl4 * 4 + (j & 3)) * 16 : zero;
+                const float2 r = dot_q4(cur, xa, xsm, cb * 16 + gl4, g);
+                cD = r.x;
+                cM = r.y;
+                if (DUAL) {
+                    const float2 r2 = dot_q4(cur2, xa, xsm, cb * 16 + gl4, g);
+                    cD2 = r2.x;
+                    cM2 = r2.y;
+                }
+            } else {
+                const int8_t* xa = adig ? xd + (size_t)cb * 1024 + (gl6 * 4 + (j & 3)) * 16 : zero;
+                cD = dot_q6(cur, xa, xsm, cb * 16 + gl6);
+                cM = 0.f;
+                if (DUAL) cD2 = dot_q6(cur2, xa, xsm, cb * 16 + gl6);
+            }
+            aD += cD;
+            aM += cM;
+            if (DUAL) {
+                aD2 += cD2;
+                aM2 += cM2;
+            }
+        }
+        if (cp == ipt - 1) {  // tile done: reduce lanes (g) and waves, run the epilogue
+            float acc = aD - aM, acc2 = aD2 - aM2;
+            acc += __shfl_xor(acc, 16, 64);
+            acc += __shfl_xor(acc, 32, 64);
+            if (DUAL) {
+                acc2 += __shfl_xor(acc2, 16, 64);
+                acc2 += __shfl_xor(acc2, 32, 64);
+            }
+            if (lane < 16) {
+                red[w * 16 + j] = acc;
+                if (DUAL) red[(NW + w) * 16 + j] = acc2;
+            }
+            __syncthreads();
+            if (tid < 16) {
+                float v = 0.f, v2 = 0.f;
+#pragma unroll
+                for (int q = 0; q < NW; q++) {
+                    v += red[q * 16 + tid];
+                    if (DUAL) v2 += red[(NW + q) * 16 + tid];
+                }
+                const SegDesc& s = a.seg[seg_of_tile(a, ct)];
+                const int row = (ct - s.first_tile + s.tile0) * 16 + tid;
+                const bool ok = row >= s.row0 && row < s.row1;
+                switch (s.epi) {
+                case EPI_STORE:
+                    if (ok) s.y[row] = v;
+                    break;
+                case EPI_RESID:
+                    if (ok) s.y[row] = s.yadd[row] + v;
+                    break;
+                case EPI_SWIGLU:
+                    if (ok) s.y[row] = (v / (1.f + expf(-v))) * v2;
+                    break;
+                case EPI_ROPE_Q:
+                case EPI_ROPE_K: {
+                    // pairs (2i, 2i+1) of a head, src/m6_engine.c:134-143
+                    const float pv = __shfl_xor(v, 1, 64);
+                    float o = v;
+                    const int d = row % a.head_dim;
+                    if (d < a.rot) {
+                        const float* ang = a.rope_tab + ((size_t)a.state[0] * (a.rot / 2) + d / 2) * 2;
+                        const float c = ang[0], sn = ang[1];
+                        o = (row & 1) ? pv * sn + v * c : v * c - pv * sn;
+                    }
+                    if (ok) {
+                        if (s.epi == EPI_ROPE_Q) s.y[row] = o;
+                        else a.kc[(size_t)a.state[1 + a.layer] * a.kv_dim + row] = o;
+                    }
+                    break;
+                }
+                case EPI_V_APPEND:
+                    if (ok) a.vc[(size_t)a.state[1 + a.layer] * a.kv_dim + row] = v;
+                    break;
+                case EPI_ARGMAX: {
+                    if (ok) s.y[row] = v;
+                    float bv = ok ? v : -INFINITY;
+                    int bi = ok ? row : 0x7fffffff;
+#pragma unroll
+                    for (int m = 8; m >= 1; m >>= 1) am_merge(bv, bi, __shfl_xor(bv, m, 64), __shfl_xor(bi, m, 64));
+                    am_merge(am_v, am_i, bv, bi);
+                    break;
+                }
+                default:
+                    break;
+                }
+            }
+            __syncthreads();
+            aD = aM = aD2 = aM2 = 0.f;
+        }
+        ct = nt;
+        cb = nbk;
+        cp = np;
+    };
+    for (int i = 0; i < n_items; i += 2) {
+        step(i, P0, P1, Q0, Q1);
+        if (i + 1 >= n_items) break;
+        step(i + 1, P1, P0, Q1, Q0);
+    }
+    if (a.seg[0].epi == EPI_ARGMAX && tid == 0) {
+        a.am_val[bx] = am_v;
+        a.am_idx[bx] = am_i;
+    }
+}
+
+// ------------------------------------------------------------------ Q8_0 --
 struct FQ80 {
     static constexpr int UPB = 1, NX = 32, NS = 1;
     __device__ static void xslice(const float* x, int u, float* xv, float* sx) {
@@ -199,16 +445,7 @@ __device__ __forceinline__ void rows_dot(const SegDesc& s, const SegDesc& s2, co
 }
 
 
-__device__ __forceinline__ void am_merge(float& v, int& i, float v2, int i2) {
-    if (v2 > v || (v2 == v && i2 < i)) {
-        v = v2;
-        i = i2;
-    }
-}
-
-// ------------------------------------------------------ fused segments --
-// One instantiation per weight format (all segments of a launch share it)
-// and per dual mode, so the register budget is that of one format.
+// Fused segment kernel for Q8_0 (one instantiation per dual mode).
 template <class F, bool DUAL>
 __global__ __launch_bounds__(256) void k_seg(const SegLaunch a) {
     extern __shared__ float xsh[];
@@ -392,13 +629,105 @@ __global__ __launch_bounds__(256) void k_gemv_plain(const uint8_t* __restrict__ 
 
 }  // namespace
 
-int draco_seg_launch(SegLaunch& a, hipStream_t st) {
-    if (a.nseg < 1 || a.nseg > SEG_MAX) return -1;
+namespace {
+
+int cu_count() {
+    static int n = 0;
+    static std::once_flag once;
+    std::call_once(once, [] {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+            n = 256;
+    });
+    return n;
+}
+
+size_t dq_lds_bytes(int n_in, int nw) { return (size_t)(n_in / 16) * 72 + 1024 + (size_t)2 * nw * 16 * 4; }
+
+template <int NW, int FM, bool DUAL>
+void launch_dq(SegLaunch& a, int grid, hipStream_t st) {
+    static std::once_flag once;
+    std::call_once(once, [] {
+        // allow LDS beyond 64 KB for long rows (n_in up to 16384 needs ~74 KB)
+        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&k_dq<NW, FM, DUAL>),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    });
+    hipLaunchKernelGGL((k_dq<NW, FM, DUAL>), dim3(grid), dim3(64 * NW), dq_lds_bytes(a.n_in, NW), st, a);
+}
+
+template <int NW>
+void launch_dq_nw(SegLaunch& a, int fm, bool dual, int grid, hipStream_t st) {
+    if (dual) {
+        if (fm == 1) launch_dq<NW, 1, true>(a, grid, st);
+        else launch_dq<NW, 2, true>(a, grid, st);
+    } else if (fm == 1) {
+        launch_dq<NW, 1, false>(a, grid, st);
+    } else if (fm == 2) {
+        launch_dq<NW, 2, false>(a, grid, st);
+    } else {
+        launch_dq<NW, 3, false>(a, grid, st);
+    }
+}
+
+// Q4_K / Q6_K segments: tile bookkeeping, instance choice, persistent grid.
+int seg_launch_dq(SegLaunch& a, hipStream_t st) {
+    const int n_in = a.n_in;
+    if (n_in % 256 || n_in > 16384) return -1;
+    const int nb = n_in / 256;
+    int tiles = 0, fm = 0;
+    bool dual = false;
+    for (int i = 0; i < a.nseg; i++) {
+        SegDesc& s = a.seg[i];
+        if (s.row1 <= 0) s.row1 = s.L.n_out;
+        if (s.row0 < 0 || s.row1 > s.L.n_out || s.row0 >= s.row1) return -1;
+        fm |= s.L.code == DRACO_Q4_K ? 1 : 2;
+        s.tile0 = s.row0 / 16;
+        s.first_tile = tiles;
+        s.n_tiles = (s.row1 + 15) / 16 - s.tile0;
+        if (s.epi == EPI_SWIGLU) {
+            if (i + 1 >= a.nseg) return -1;
+            SegDesc& u = a.seg[i + 1];
+            if (u.L.code != s.L.code || u.L.n_out != s.L.n_out || u.L.n_in != n_in) return -1;
+            u.row0 = s.row0;
+            u.row1 = s.row1;
+            u.tile0 = s.tile0;
+            u.first_tile = 1 << 30;  // never selected: computed with its gate
+            u.n_tiles = 0;
+            dual = true;
+            tiles += s.n_tiles;
+            i++;
+            continue;
+        }
+        if ((s.epi == EPI_ROPE_Q || s.epi == EPI_ROPE_K) && (a.head_dim & 1)) return -1;
+        if (s.epi == EPI_ARGMAX && a.nseg != 1) return -1;
+        tiles += s.n_tiles;
+    }
+    if (dual && (a.nseg != 2 || fm == 3)) return -1;
+    // waves per block: enough to split a row's super-blocks, and enough
+    // threads for the prologue's XP_MAXV float4s per thread
+    int nw = nb >= 32 ? 16 : (nb >= 8 ? 8 : 4);
+    while (n_in > XP_MAXV * 4 * 64 * nw) nw *= 2;
+    if (nw > 16) return -1;
+    const int cap = cu_count() * (nw == 4 ? 4 : (nw == 8 ? 2 : 1));
+    const int grid = tiles < cap ? tiles : cap;
+    if (grid <= 0) return 0;
+    if (nw == 4) launch_dq_nw<4>(a, fm, dual, grid, st);
+    else if (nw == 8) launch_dq_nw<8>(a, fm, dual, grid, st);
+    else launch_dq_nw<16>(a, fm, dual, grid, st);
+    if (a.seg[0].epi == EPI_ARGMAX)
+        hipLaunchKernelGGL(k_argmax_finalize, dim3(1), dim3(256), 0, st, a.am_val, a.am_idx, grid, a.tokens,
+                           const_cast<int*>(a.cursor), a.advance_state, a.advance_layers);
+    return 0;
+}
+
+// Q8_0 segments (k_seg).
+int seg_launch_q8(SegLaunch& a, hipStream_t st) {
     int blocks = 0;
     for (int i = 0; i < a.nseg; i++) {
         SegDesc& s = a.seg[i];
-        if (s.L.code != DRACO_Q4_K && s.L.code != DRACO_Q6_K && s.L.code != DRACO_Q8_0) return -1;
-        if (s.L.n_in != a.n_in) return -1;
+        if (s.row1 <= 0) s.row1 = s.L.n_out;
+        if (s.row0 != 0 || s.row1 != s.L.n_out) return -1;  // row ranges go through draco_gemv_launch
         s.first_block = blocks;
         s.n_blocks = (s.L.n_out + SEG_ROWS - 1) / SEG_ROWS;
         if (s.epi == EPI_SWIGLU) {
@@ -414,29 +743,33 @@ int draco_seg_launch(SegLaunch& a, hipStream_t st) {
         if ((s.epi == EPI_ROPE_Q || s.epi == EPI_ROPE_K) && ((s.L.n_out & 1) || (a.head_dim & 1))) return -1;
         blocks += s.n_blocks;
     }
-    const int code = a.seg[0].L.code;
     bool dual = false;
-    for (int i = 0; i < a.nseg; i++) {
-        if (a.seg[i].L.code != code) return -1;  // one format per launch
-        dual = dual || a.seg[i].epi == EPI_SWIGLU;
-    }
+    for (int i = 0; i < a.nseg; i++) dual = dual || a.seg[i].epi == EPI_SWIGLU;
     if (dual && a.nseg != 2) return -1;
     const size_t shm = a.do_norm ? sizeof(float) * (size_t)a.n_in : 0;
     const dim3 g(blocks), b(256);
-    if (code == DRACO_Q4_K) {
-        if (dual) hipLaunchKernelGGL((k_seg<FQ4K, true>), g, b, shm, st, a);
-        else hipLaunchKernelGGL((k_seg<FQ4K, false>), g, b, shm, st, a);
-    } else if (code == DRACO_Q6_K) {
-        if (dual) hipLaunchKernelGGL((k_seg<FQ6K, true>), g, b, shm, st, a);
-        else hipLaunchKernelGGL((k_seg<FQ6K, false>), g, b, shm, st, a);
-    } else {
-        if (dual) hipLaunchKernelGGL((k_seg<FQ80, true>), g, b, shm, st, a);
-        else hipLaunchKernelGGL((k_seg<FQ80, false>), g, b, shm, st, a);
-    }
+    if (dual) hipLaunchKernelGGL((k_seg<FQ80, true>), g, b, shm, st, a);
+    else hipLaunchKernelGGL((k_seg<FQ80, false>), g, b, shm, st, a);
     if (a.seg[0].epi == EPI_ARGMAX)
         hipLaunchKernelGGL(k_argmax_finalize, dim3(1), dim3(256), 0, st, a.am_val, a.am_idx, a.seg[0].n_blocks,
                            a.tokens, const_cast<int*>(a.cursor), a.advance_state, a.advance_layers);
     return 0;
+}
+
+}  // namespace
+
+int draco_seg_launch(SegLaunch& a, hipStream_t st) {
+    if (a.nseg < 1 || a.nseg > SEG_MAX) return -1;
+    bool kq = false, q8 = false;
+    for (int i = 0; i < a.nseg; i++) {
+        const int c = a.seg[i].L.code;
+        if (a.seg[i].L.n_in != a.n_in) return -1;
+        if (c == DRACO_Q4_K || c == DRACO_Q6_K) kq = true;
+        else if (c == DRACO_Q8_0) q8 = true;
+        else return -1;
+    }
+    if (kq && q8) return -1;
+    return kq ? seg_launch_dq(a, st) : seg_launch_q8(a, st);
 }
 
 int draco_gemv_launch(const DracoMat& m, const float* x, float* y, const float* yadd, int row0, int row1,
@@ -444,9 +777,23 @@ int draco_gemv_launch(const DracoMat& m, const float* x, float* y, const float* 
     if (row0 < 0 || row1 > m.L.n_out || row0 > row1) return -1;
     if (row0 == row1) return 0;
     const int code = m.L.code;
-    if (code == DRACO_Q4_K || code == DRACO_Q6_K || code == DRACO_Q8_0) {
-        // a row range is a segment over rows [row0, row1): shift the row origin by
-        // offsetting y and describing only those rows
+    if (code == DRACO_Q4_K || code == DRACO_Q6_K) {
+        SegLaunch a = {};
+        a.nseg = 1;
+        a.n_in = m.L.n_in;
+        a.x = x;
+        SegDesc& s = a.seg[0];
+        s.base = m.dev;
+        s.L = m.L;
+        s.row0 = row0;
+        s.row1 = row1;
+        s.y = y;
+        s.yadd = yadd;
+        s.epi = yadd ? EPI_RESID : EPI_STORE;
+        return draco_seg_launch(a, st);
+    }
+    if (code == DRACO_Q8_0) {
+        // a row range is a segment over rows [row0, row1): offset the region bases by row0 rows
         SegLaunch a = {};
         a.nseg = 1;
         a.n_in = m.L.n_in;
@@ -454,17 +801,10 @@ int draco_gemv_launch(const DracoMat& m, const float* x, float* y, const float* 
         SegDesc& s = a.seg[0];
         s.L = m.L;
         s.L.n_out = row1 - row0;
-        // rows start at row0: advance every region base by row0 rows
-        const size_t nb = (size_t)m.L.nb;
         s.base = m.dev;
-        if (row0) {
-            // regions are row-major [n_out][nb][...]: per-region offsets move by row0 rows
-            size_t per[4] = {0, 0, 0, 0};
-            if (code == DRACO_Q4_K) { per[0] = 128; per[1] = 16; }
-            else if (code == DRACO_Q6_K) { per[0] = 128; per[1] = 64; per[2] = 16; per[3] = 2; }
-            else { per[0] = 32; per[1] = 2; }
-            for (int i = 0; i < 4; i++) s.L.off[i] += per[i] * nb * (size_t)row0;
-        }
+        const size_t nb = (size_t)m.L.nb;
+        s.L.off[0] += 32 * nb * (size_t)row0;
+        s.L.off[1] += 2 * nb * (size_t)row0;
         s.y = y + row0;
         s.yadd = yadd ? yadd + row0 : nullptr;
         s.epi = yadd ? EPI_RESID : EPI_STORE;

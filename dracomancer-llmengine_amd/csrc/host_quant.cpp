@@ -192,21 +192,23 @@ int draco_repack(int code, const uint8_t* src, int n_out, int n_in, uint8_t* dst
         return 0;
     }
     if (code != DRACO_Q4_K && code != DRACO_Q6_K && code != DRACO_Q8_0) return -1;
+    if (code == DRACO_Q4_K || code == DRACO_Q6_K) memset(dst, 0, L.bytes);  // padding rows of the last tile
     #pragma omp parallel for schedule(static)
     for (int r = 0; r < n_out; r++) {
         for (int b = 0; b < nb; b++) {
-            const size_t i = (size_t)r * nb + b;
             if (code == DRACO_Q4_K) {
                 const uint8_t* blk = src + (size_t)r * rb + (size_t)b * 144;
-                memcpy(dst + L.off[0] + i * 128, blk + 16, 128);
-                memcpy(dst + L.off[1] + i * 16, blk, 16);
+                memcpy(dst + draco_q4t_hdr(nb, r, b), blk, 16);
+                for (int i = 0; i < 128; i += 16)  // 16-byte runs stay contiguous
+                    for (int e = 0; e < 16; e++) dst[draco_q4t_qs(nb, r, b, i) + e] = blk[16 + i + e] ^ 0x80;
             } else if (code == DRACO_Q6_K) {
                 const uint8_t* blk = src + (size_t)r * rb + (size_t)b * 210;
-                memcpy(dst + L.off[0] + i * 128, blk, 128);
-                memcpy(dst + L.off[1] + i * 64, blk + 128, 64);
-                memcpy(dst + L.off[2] + i * 16, blk + 192, 16);
-                memcpy(dst + L.off[3] + i * 2, blk + 208, 2);
+                for (int i = 0; i < 128; i += 16) memcpy(dst + draco_q6t_ql(nb, r, b, i), blk + i, 16);
+                for (int i = 0; i < 64; i += 16) memcpy(dst + draco_q6t_qh(nb, r, b, i), blk + 128 + i, 16);
+                for (int i = 0; i < 16; i++) dst[draco_q6t_sc(nb, r, b, i)] = blk[192 + i];
+                memcpy(dst + draco_q6t_d(nb, r, b), blk + 208, 2);
             } else {
+                const size_t i = (size_t)r * nb + b;
                 const uint8_t* blk = src + (size_t)r * rb + (size_t)b * 34;
                 memcpy(dst + L.off[0] + i * 32, blk + 2, 32);
                 memcpy(dst + L.off[1] + i * 2, blk, 2);
@@ -228,18 +230,18 @@ int draco_unpack(int code, const uint8_t* src, int n_out, int n_in, uint8_t* dst
     }
     for (int r = 0; r < n_out; r++)
         for (int b = 0; b < nb; b++) {
-            const size_t i = (size_t)r * nb + b;
             if (code == DRACO_Q4_K) {
                 uint8_t* blk = dst + (size_t)r * rb + (size_t)b * 144;
-                memcpy(blk + 16, src + L.off[0] + i * 128, 128);
-                memcpy(blk, src + L.off[1] + i * 16, 16);
+                memcpy(blk, src + draco_q4t_hdr(nb, r, b), 16);
+                for (int i = 0; i < 128; i++) blk[16 + i] = src[draco_q4t_qs(nb, r, b, i)] ^ 0x80;
             } else if (code == DRACO_Q6_K) {
                 uint8_t* blk = dst + (size_t)r * rb + (size_t)b * 210;
-                memcpy(blk, src + L.off[0] + i * 128, 128);
-                memcpy(blk + 128, src + L.off[1] + i * 64, 64);
-                memcpy(blk + 192, src + L.off[2] + i * 16, 16);
-                memcpy(blk + 208, src + L.off[3] + i * 2, 2);
+                for (int i = 0; i < 128; i++) blk[i] = src[draco_q6t_ql(nb, r, b, i)];
+                for (int i = 0; i < 64; i++) blk[128 + i] = src[draco_q6t_qh(nb, r, b, i)];
+                for (int i = 0; i < 16; i++) blk[192 + i] = src[draco_q6t_sc(nb, r, b, i)];
+                memcpy(blk + 208, src + draco_q6t_d(nb, r, b), 2);
             } else {
+                const size_t i = (size_t)r * nb + b;
                 uint8_t* blk = dst + (size_t)r * rb + (size_t)b * 34;
                 memcpy(blk + 2, src + L.off[0] + i * 32, 32);
                 memcpy(blk, src + L.off[1] + i * 2, 2);
