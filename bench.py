@@ -134,6 +134,7 @@ def main():
     ap.add_argument("--eager", action="store_true",
                     help="run the decode loop without HIP graphs (for profilers that cannot trace graphs)")
     ap.add_argument("--roofline-only", action="store_true", help="only the Q4_K GEMV roofline measurement")
+    ap.add_argument("--no-roofline", action="store_true", help="skip the GEMV roofline measurement (profiling runs)")
     ap.add_argument("--cpu-baseline-worker", action="store_true")
     ap.add_argument("--kv-file")
     args = ap.parse_args()
@@ -188,8 +189,10 @@ def main():
         match = bool(list(g["tokens"][:n]) == toks_first[:n])
     log(f"decode {tok_s:.1f} tok/s; greedy tokens match reference: {match}")
 
-    roof = q4k_gemv_roofline(lib)
-    log(f"Q4_K GEMV 14336x4096: {roof['us_per_launch']} us/launch, {roof['achieved']} GB/s")
+    roof = None
+    if not args.no_roofline:
+        roof = q4k_gemv_roofline(lib)
+        log(f"Q4_K GEMV 14336x4096: {roof['us_per_launch']} us/launch, {roof['achieved']} GB/s")
 
     cpu = None
     if not args.no_cpu_baseline:

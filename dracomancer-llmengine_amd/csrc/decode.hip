@@ -163,32 +163,29 @@ __global__ __launch_bounds__(256) void k_attn_part(const float* __restrict__ q, 
     }
 }
 
-// one block per q head, one thread per head dim
+// Merge the splits of one q head (block), one thread per head dim.  Lane k
+// of each wave holds split k's (m, l); the weights exp(m_k - M) are
+// broadcast with readlane, and all of a lane's partial loads are issued
+// before the first FMA, so the kernel costs two dependent L2 round trips.
+template <int MAXS>
 __global__ __launch_bounds__(128) void k_attn_combine(const float* __restrict__ part, float* __restrict__ out,
                                                       int nsplit, int HD) {
-    __shared__ float wsp[64];
-    __shared__ float invL;
-    const int h = blockIdx.x, tid = threadIdx.x;
+    const int h = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
     const float* ph = part + (size_t)h * nsplit * (HD + 2);
-    if (tid < 64) {
-        float M = -INFINITY;
-        for (int k = 0; k < nsplit; k++) M = fmaxf(M, ph[k * (HD + 2) + HD]);
-        float w = 0.f, l = 0.f;
-        if (tid < nsplit) {
-            const float m = ph[tid * (HD + 2) + HD];
-            w = m > -INFINITY ? expf(m - M) : 0.f;
-            l = ph[tid * (HD + 2) + HD + 1] * w;
-            wsp[tid] = w;
-        }
-        l = wave_sum(l);
-        if (tid == 0) invL = 1.f / l;
+    const float m = lane < nsplit ? ph[lane * (HD + 2) + HD] : -INFINITY;
+    const float lk = lane < nsplit ? ph[lane * (HD + 2) + HD + 1] : 0.f;
+    float pv[MAXS];
+#pragma unroll
+    for (int k = 0; k < MAXS; k++) pv[k] = (k < nsplit && tid < HD) ? ph[k * (HD + 2) + tid] : 0.f;
+    const float M = wave_max(m);
+    const float wk = m > -INFINITY ? expf(m - M) : 0.f;
+    const float L = wave_sum(lk * wk);
+    float acc = 0.f;
+#pragma unroll
+    for (int k = 0; k < MAXS; k++) {  // lanes k >= nsplit carry weight 0
+        acc = fmaf(pv[k], __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wk), k)), acc);
     }
-    __syncthreads();
-    for (int d = tid; d < HD; d += blockDim.x) {
-        float acc = 0.f;
-        for (int k = 0; k < nsplit; k++) acc = fmaf(ph[k * (HD + 2) + d], wsp[k], acc);
-        out[(size_t)h * HD + d] = acc * invL;
-    }
+    if (tid < HD) out[(size_t)h * HD + tid] = acc * (1.f / L);
 }
 
 // -------------------------------------------------------------- SwiGLU --
@@ -341,7 +338,10 @@ int dk_attention(const float* q, const float* kc, const float* vc, float* part, 
                            nsplit, chunk_max, scale);
     else
         return -1;
-    hipLaunchKernelGGL(k_attn_combine, dim3(NH), dim3(HD < 128 ? HD : 128), 0, st, part, out, nsplit, HD);
+    const dim3 cg(NH), cb(HD < 128 ? HD : 128);
+    if (nsplit <= 16) hipLaunchKernelGGL(k_attn_combine<16>, cg, cb, 0, st, part, out, nsplit, HD);
+    else if (nsplit <= 32) hipLaunchKernelGGL(k_attn_combine<32>, cg, cb, 0, st, part, out, nsplit, HD);
+    else hipLaunchKernelGGL(k_attn_combine<64>, cg, cb, 0, st, part, out, nsplit, HD);
     return 0;
 }
 

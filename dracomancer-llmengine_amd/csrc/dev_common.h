@@ -37,6 +37,17 @@ __device__ __forceinline__ int wave_sum_i(int v) {
     return v;
 }
 
+// Workgroup barrier that orders LDS only.  __syncthreads() carries a
+// workgroup fence over all address spaces, which on gfx9 waits for every
+// outstanding global load (vmcnt(0)); this one waits for LDS operations only,
+// so weight loads issued before it stay in flight.  Use it only where the
+// barrier protects LDS data.
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 __device__ __forceinline__ float4 ld4(const float* p) { return *reinterpret_cast<const float4*>(p); }
 
 __device__ __forceinline__ uint4 ldu4(const uint8_t* p) { return *reinterpret_cast<const uint4*>(p); }

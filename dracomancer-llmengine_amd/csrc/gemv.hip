@@ -214,7 +214,10 @@ __global__ __launch_bounds__(64 * NW) void k_dq(const SegLaunch a) {
     }
     Frag P0, P1, Q0, Q1;
     int ct = bx, cb = w, cp = 0;  // current item: tile, super-block, position in tile
-    if (n_items > 0 && cb < nb) load(ct, cb, P0, Q0);
+    // loads are issued unconditionally, at indices clamped to a real item:
+    // a skipped load would leave the wait-count analysis no choice but
+    // vmcnt(0) before every use, serialising the prefetch
+    load(ct < total ? ct : total - 1, cb < nb ? cb : nb - 1, P0, Q0);
     for (int i = tid; i < 256; i += NT) reinterpret_cast<uint32_t*>(zero)[i] = 0u;
 
     // ---- prologue part 2: RMSNorm (src/m6_engine.c:31-37) and digits into LDS
@@ -232,7 +235,7 @@ __global__ __launch_bounds__(64 * NW) void k_dq(const SegLaunch a) {
             }
         ss = wave_sum(ss);
         if (lane == 0) red[w] = ss;
-        __syncthreads();
+        lds_barrier();
         float tot = 0.f;
 #pragma unroll
         for (int i = 0; i < NW; i++) tot += red[i];
@@ -272,7 +275,7 @@ __global__ __launch_bounds__(64 * NW) void k_dq(const SegLaunch a) {
         }
         if (qq == 0) xsm[grp] = make_float2(__builtin_bit_cast(float, (uint32_t)(127 + k - 7) << 23), sum);
     }
-    __syncthreads();
+    lds_barrier();
 
     // this lane's A row: digit (j&3) of its group, non-zero only when (j>>2) == g
     const bool adig = (j >> 2) == g;
@@ -288,7 +291,7 @@ __global__ __launch_bounds__(64 * NW) void k_dq(const SegLaunch a) {
             nbk = w;
             nt = ct + G;
         }
-        if (i + 1 < n_items && nbk < nb) load(nt, nbk, nxt, nxt2);
+        load(i + 1 < n_items ? nt : ct, nbk < nb ? nbk : nb - 1, nxt, nxt2);
         if (cb < nb) {
             float cD, cM, cD2 = 0.f, cM2 = 0.f;
             if (is_q4(ct)) {
@@ -326,7 +329,7 @@ __global__ __launch_bounds__(64 * NW) void k_dq(const SegLaunch a) {
                 red[w * 16 + j] = acc;
                 if (DUAL) red[(NW + w) * 16 + j] = acc2;
             }
-            __syncthreads();
+            lds_barrier();
             if (tid < 16) {
                 float v = 0.f, v2 = 0.f;
 #pragma unroll
@@ -380,7 +383,7 @@ __global__ __launch_bounds__(64 * NW) void k_dq(const SegLaunch a) {
                     break;
                 }
             }
-            __syncthreads();
+            lds_barrier();
             aD = aM = aD2 = aM2 = 0.f;
         }
         ct = nt;
