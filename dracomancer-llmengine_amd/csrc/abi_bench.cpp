@@ -22,6 +22,10 @@ extern "C" {
 // out[0] mean us per launch from per-launch event pairs
 // out[1] us per launch from one event pair around the whole loop
 // out[2] min us, out[3] median us (per-launch pairs)
+// out[4] us per launch of the same `iters` launches captured in a HIP graph
+//        and replayed (one event pair around the replay): back-to-back
+//        kernels with no host gaps, the figure comparable to a profiler's
+//        per-kernel duration.  `out` holds at least 5 floats.
 int draco_bench_gemv(int code, const uint8_t* W, int n_out, int n_in, int n_copies, int iters,
                      float* out) {
     std::lock_guard<std::recursive_mutex> g(api_mutex());
@@ -66,12 +70,29 @@ int draco_bench_gemv(int code, const uint8_t* W, int n_out, int n_in, int n_copi
     }
     float tot = 0;
     DRACO_HIP(hipEventElapsedTime(&tot, ev[2 * iters], ev[2 * iters + 1]));
+    // graph replay of the same rotation
+    hipGraph_t graph;
+    hipGraphExec_t exec;
+    DRACO_HIP(hipStreamBeginCapture(st, hipStreamCaptureModeRelaxed));
+    for (int i = 0; i < iters; i++) draco_gemv_launch(mats[i % n_copies], dx, dy, nullptr, 0, n_out, st);
+    DRACO_HIP(hipStreamEndCapture(st, &graph));
+    DRACO_HIP(hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0));
+    DRACO_HIP(hipGraphLaunch(exec, st));  // warm
+    DRACO_HIP(hipEventRecord(ev[0], st));
+    DRACO_HIP(hipGraphLaunch(exec, st));
+    DRACO_HIP(hipEventRecord(ev[1], st));
+    DRACO_HIP(hipStreamSynchronize(st));
+    float gms = 0;
+    DRACO_HIP(hipEventElapsedTime(&gms, ev[0], ev[1]));
+    hipGraphExecDestroy(exec);
+    hipGraphDestroy(graph);
     std::vector<float> s = t;
     std::sort(s.begin(), s.end());
     out[0] = (float)(sum / iters);
     out[1] = tot * 1000.f / iters;
     out[2] = s[0];
     out[3] = s[iters / 2];
+    out[4] = gms * 1000.f / iters;
     for (auto& e : ev) hipEventDestroy(e);
     for (auto& m : mats) hipFree(m.dev);
     hipFree(dx);

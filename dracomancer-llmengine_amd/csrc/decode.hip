@@ -82,84 +82,85 @@ __global__ __launch_bounds__(256) void k_rope_append(float* __restrict__ q, cons
 // ----------------------------------------------------------- attention --
 // Split-T decode attention.  Block (g, s) handles kv head g and rows
 // [t0, t1) of 0..T for the `rep` q heads that share it (GQA: q head h reads
-// kv head h/rep, src/m6_engine.c:484).  The block first issues every load of
-// its K and V rows into LDS (one memory round trip), then computes scores,
-// the chunk softmax and P.V from LDS, and writes an unnormalised partial
-// (o[HD], m, l) per (q head, split).  k_attn_combine merges the splits:
+// kv head h/rep, src/m6_engine.c:484); wave j of the block is q head
+// g*rep + j.  A pass covers TPP = 64/LPT rows: LPT = HD/32 lanes share a row
+// (32 head dims each), so a lane's K slice is 8 float4 loads; lane d also
+// loads V[t][d] (and V[t][d+64] when HD = 128) for the pass's rows.  All of a
+// pass's K and V loads are issued before the first FMA; scores reduce over
+// the row's lanes with shuffles, the softmax over the wave, and P.V uses
+// readlane broadcasts -- no LDS and no barrier.  Passes are merged with the
+// online-softmax rescale.  Each (q head, split) writes an unnormalised
+// partial (o[HD], m, l); k_attn_combine merges the splits:
 //   out[h] = sum_s o_s e^(m_s - M) / sum_s l_s e^(m_s - M),  M = max_s m_s
 // which equals the reference's single-pass softmax up to fp32 rounding.
-constexpr int REPMAX = 8;
+constexpr int REPMAX = 16;
 
 template <int HD>
-__global__ __launch_bounds__(256) void k_attn_part(const float* __restrict__ q, const float* __restrict__ kc,
-                                                   const float* __restrict__ vc, float* __restrict__ part,
-                                                   const int* __restrict__ st, int layer, int NH, int NKV,
-                                                   int nsplit, int chunk_max, float scale) {
-    extern __shared__ float sh[];
-    constexpr int KP = HD + 4;  // padded K row (LDS bank spread)
+__global__ __launch_bounds__(1024) void k_attn_part(const float* __restrict__ q, const float* __restrict__ kc,
+                                                    const float* __restrict__ vc, float* __restrict__ part,
+                                                    const int* __restrict__ st, int layer, int NH, int NKV,
+                                                    int nsplit, float scale) {
+    constexpr int LPT = HD / 32, TPP = 64 / LPT, DV = HD / 64;
     const int g = blockIdx.x, s = blockIdx.y;
+    const int lane = threadIdx.x & 63, j = threadIdx.x >> 6;
     const int rep = NH / NKV, KD = NKV * HD;
+    const int h = g * rep + j;
     const int Tn = st[1 + layer] + 1;
     const int chunk = (Tn + nsplit - 1) / nsplit;
     const int t0 = s * chunk, t1 = min(Tn, t0 + chunk);
-    const int n = max(0, t1 - t0);
-    float* qs = sh;                       // [rep][HD]
-    float* ks = qs + rep * HD;            // [chunk_max][KP]
-    float* vs = ks + chunk_max * KP;      // [chunk_max][HD]
-    float* sc = vs + chunk_max * HD;      // [rep][chunk_max]
-    float* ml = sc + rep * chunk_max;     // [rep][2]
-    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    constexpr int C4 = HD / 4;
-    for (int i = tid; i < rep * C4; i += 256) {
-        const float4 v = ld4(q + (size_t)g * rep * HD + 4 * i);
-        *reinterpret_cast<float4*>(qs + 4 * i) = v;
-    }
-    for (int i = tid; i < n * C4; i += 256) {
-        const int t = i / C4, c = i % C4;
-        const size_t off = (size_t)(t0 + t) * KD + g * HD + 4 * c;
-        const float4 kv = ld4(kc + off), vv = ld4(vc + off);
-        *reinterpret_cast<float4*>(ks + t * KP + 4 * c) = kv;
-        *reinterpret_cast<float4*>(vs + t * HD + 4 * c) = vv;
-    }
-    __syncthreads();
-    for (int pr = tid; pr < n * rep; pr += 256) {
-        const int t = pr / rep, j = pr % rep;
-        const float* kt = ks + t * KP;
-        const float* qj = qs + j * HD;
-        float acc = 0.f;
-#pragma unroll 8
-        for (int d = 0; d < HD; d++) acc = fmaf(qj[d], kt[d], acc);
-        sc[j * chunk_max + t] = acc * scale;
-    }
-    __syncthreads();
-    for (int j = wv; j < rep; j += 4) {
-        float m = -INFINITY;
-        for (int t = lane; t < n; t += 64) m = fmaxf(m, sc[j * chunk_max + t]);
-        m = wave_max(m);
-        float l = 0.f;
-        for (int t = lane; t < n; t += 64) {
-            const float p = expf(sc[j * chunk_max + t] - m);
-            sc[j * chunk_max + t] = p;
-            l += p;
+    const int tt = lane / LPT, pt = lane % LPT;
+    float4 qv[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) qv[i] = ld4(q + (size_t)h * HD + 32 * pt + 4 * i);
+    float m_run = -INFINITY, l_run = 0.f, o[DV];
+#pragma unroll
+    for (int e = 0; e < DV; e++) o[e] = 0.f;
+    for (int pb = t0; pb < t1; pb += TPP) {
+        const int t = pb + tt;
+        const bool valid = t < t1;
+        const int tr = valid ? t : t0;  // clamped row: loads stay in bounds
+        float4 kv[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) kv[i] = ld4(kc + (size_t)tr * KD + g * HD + 32 * pt + 4 * i);
+        float vv[TPP][DV];
+#pragma unroll
+        for (int r = 0; r < TPP; r++) {
+            const int trr = pb + r < t1 ? pb + r : t0;
+#pragma unroll
+            for (int e = 0; e < DV; e++) vv[r][e] = vc[(size_t)trr * KD + g * HD + lane + 64 * e];
         }
-        l = wave_sum(l);
-        if (lane == 0) {
-            ml[2 * j] = n > 0 ? m : -INFINITY;
-            ml[2 * j + 1] = l;
+        float sc = 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            sc = fmaf(qv[i].x, kv[i].x, sc);
+            sc = fmaf(qv[i].y, kv[i].y, sc);
+            sc = fmaf(qv[i].z, kv[i].z, sc);
+            sc = fmaf(qv[i].w, kv[i].w, sc);
         }
+#pragma unroll
+        for (int m = 1; m < LPT; m <<= 1) sc += __shfl_xor(sc, m, 64);
+        sc = valid ? sc * scale : -INFINITY;
+        const float m_new = fmaxf(m_run, wave_max(sc));
+        const float corr = m_run > -INFINITY ? expf(m_run - m_new) : 0.f;
+        const float p = valid ? expf(sc - m_new) : 0.f;
+        l_run = l_run * corr + wave_sum(pt == 0 ? p : 0.f);
+#pragma unroll
+        for (int e = 0; e < DV; e++) {
+            float acc = o[e] * corr;
+#pragma unroll
+            for (int r = 0; r < TPP; r++)
+                acc = fmaf(__builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, p), r * LPT)),
+                           vv[r][e], acc);
+            o[e] = acc;
+        }
+        m_run = m_new;
     }
-    __syncthreads();
-    for (int i = tid; i < rep * HD; i += 256) {
-        const int j = i / HD, d = i % HD;
-        const float* pj = sc + j * chunk_max;
-        float acc = 0.f;
-        for (int t = 0; t < n; t++) acc = fmaf(pj[t], vs[t * HD + d], acc);
-        float* pp = part + ((size_t)(g * rep + j) * nsplit + s) * (HD + 2);
-        pp[d] = acc;
-        if (d == 0) {
-            pp[HD] = ml[2 * j];
-            pp[HD + 1] = ml[2 * j + 1];
-        }
+    float* pp = part + ((size_t)h * nsplit + s) * (HD + 2);
+#pragma unroll
+    for (int e = 0; e < DV; e++) pp[lane + 64 * e] = o[e];
+    if (lane == 0) {
+        pp[HD] = m_run;
+        pp[HD + 1] = l_run;
     }
 }
 
@@ -325,17 +326,12 @@ int dk_attention(const float* q, const float* kc, const float* vc, float* part, 
     const int rep = NH / NKV;
     if (rep < 1 || rep > REPMAX || NH % NKV) return -1;
     const int nsplit = attn_nsplit(max_t);
-    const int chunk_max = (max_t + nsplit - 1) / nsplit;
-    const size_t shm = sizeof(float) * ((size_t)rep * HD + (size_t)chunk_max * (HD + 4) + (size_t)chunk_max * HD +
-                                        (size_t)rep * chunk_max + 2 * REPMAX);
-    if (shm > 160 * 1024) return -1;
-    const dim3 grid(NKV, nsplit);
+    const dim3 grid(NKV, nsplit), block(64 * rep);
     if (HD == 64)
-        hipLaunchKernelGGL(k_attn_part<64>, grid, dim3(256), shm, st, q, kc, vc, part, state, layer, NH, NKV,
-                           nsplit, chunk_max, scale);
+        hipLaunchKernelGGL(k_attn_part<64>, grid, block, 0, st, q, kc, vc, part, state, layer, NH, NKV, nsplit, scale);
     else if (HD == 128)
-        hipLaunchKernelGGL(k_attn_part<128>, grid, dim3(256), shm, st, q, kc, vc, part, state, layer, NH, NKV,
-                           nsplit, chunk_max, scale);
+        hipLaunchKernelGGL(k_attn_part<128>, grid, block, 0, st, q, kc, vc, part, state, layer, NH, NKV, nsplit,
+                           scale);
     else
         return -1;
     const dim3 cg(NH), cb(HD < 128 ? HD : 128);

@@ -283,8 +283,28 @@ __global__ __launch_bounds__(64 * NW) void k_dq(const SegLaunch a) {
     float am_v = -INFINITY;
     int am_i = 0x7fffffff;
     float aD = 0.f, aM = 0.f, aD2 = 0.f, aM2 = 0.f;
+    // epilogue inputs, loaded when a tile starts so they are not a memory
+    // round trip after the tile's reduction
+    const int pos = a.state ? a.state[0] : 0;
+    const int kv_row = a.state ? a.state[1 + a.layer] : 0;
+    float ep0 = 0.f, ep1 = 0.f;
 
     auto step = [&](int i, Frag& cur, Frag& nxt, Frag& cur2, Frag& nxt2) {
+        if (cp == 0 && tid < 16) {
+            const SegDesc& s = a.seg[seg_of_tile(a, ct)];
+            const int row = (ct - s.first_tile + s.tile0) * 16 + tid;
+            const int rr = row < s.L.n_out ? row : s.L.n_out - 1;
+            const int epi = s.epi;
+            const float* src = nullptr;
+            if (epi == EPI_RESID) {
+                src = s.yadd + rr;
+            } else if ((epi == EPI_ROPE_Q || epi == EPI_ROPE_K) && rr % a.head_dim < a.rot) {
+                src = a.rope_tab + ((size_t)pos * (a.rot / 2) + (rr % a.head_dim) / 2) * 2;
+            }
+            const float2 e = src ? make_float2(src[0], epi == EPI_RESID ? 0.f : src[1]) : make_float2(0.f, 0.f);
+            ep0 = e.x;
+            ep1 = e.y;
+        }
         int nt = ct, nbk = cb + NW, np = cp + 1;
         if (np == ipt) {
             np = 0;
@@ -345,7 +365,7 @@ __global__ __launch_bounds__(64 * NW) void k_dq(const SegLaunch a) {
                     if (ok) s.y[row] = v;
                     break;
                 case EPI_RESID:
-                    if (ok) s.y[row] = s.yadd[row] + v;
+                    if (ok) s.y[row] = ep0 + v;
                     break;
                 case EPI_SWIGLU:
                     if (ok) s.y[row] = (v / (1.f + expf(-v))) * v2;
@@ -355,20 +375,18 @@ __global__ __launch_bounds__(64 * NW) void k_dq(const SegLaunch a) {
                     // pairs (2i, 2i+1) of a head, src/m6_engine.c:134-143
                     const float pv = __shfl_xor(v, 1, 64);
                     float o = v;
-                    const int d = row % a.head_dim;
-                    if (d < a.rot) {
-                        const float* ang = a.rope_tab + ((size_t)a.state[0] * (a.rot / 2) + d / 2) * 2;
-                        const float c = ang[0], sn = ang[1];
+                    if (row % a.head_dim < a.rot) {
+                        const float c = ep0, sn = ep1;
                         o = (row & 1) ? pv * sn + v * c : v * c - pv * sn;
                     }
                     if (ok) {
                         if (s.epi == EPI_ROPE_Q) s.y[row] = o;
-                        else a.kc[(size_t)a.state[1 + a.layer] * a.kv_dim + row] = o;
+                        else a.kc[(size_t)kv_row * a.kv_dim + row] = o;
                     }
                     break;
                 }
                 case EPI_V_APPEND:
-                    if (ok) a.vc[(size_t)a.state[1 + a.layer] * a.kv_dim + row] = v;
+                    if (ok) a.vc[(size_t)kv_row * a.kv_dim + row] = v;
                     break;
                 case EPI_ARGMAX: {
                     if (ok) s.y[row] = v;
