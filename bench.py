@@ -65,6 +65,29 @@ def q4k_gemv_roofline(lib, n_copies=10, iters=200):
             "us_per_launch_event_pairs": round(float(out[0]), 3)}
 
 
+def q8k_gemv_configs1(lib, n_copies=10, iters=200):
+    """Q4_K GEMV with on-device Q8_K activations, both FFN shapes, bs1 and bs8.
+
+    Algorithmic bytes per launch = Q4_K weights + Q8_K activation blocks + fp32 y.
+    """
+    out = {}
+    for n_out, n_in in ((14336, 4096), (4096, 14336)):
+        rng = np.random.default_rng(1)
+        W = lib.quantize(5, rng.standard_normal((n_out, n_in), dtype=np.float32) * np.float32(0.02))
+        for nvec in (1, 8):
+            o = np.zeros(4, np.float32)
+            rc = lib.load().draco_bench_gemv_q8k(5, lib.pu8(W), n_out, n_in, nvec, n_copies, iters, lib.pf(o))
+            if rc != 0:
+                raise RuntimeError(lib.last_error())
+            alg = W.nbytes + nvec * (n_in // 256) * 292 + 4 * nvec * n_out
+            us = float(o[0])
+            out[f"{n_out}x{n_in}_bs{nvec}"] = {
+                "us_per_launch": round(us, 3), "GB_s": round(alg / us / 1e3, 1),
+                "frac_of_peak": round(alg / us / 1e3 / PEAK_HBM_GBS, 4),
+                "us_quantize_plus_gemv": round(float(o[1]), 3), "alg_bytes": alg}
+    return out
+
+
 def cpu_baseline_worker(args):
     """Child process: the reference engine decoding from context CTX_START."""
     from dracohip import models
@@ -157,7 +180,10 @@ def main():
     if args.roofline_only:
         roof = q4k_gemv_roofline(lib)
         log(f"Q4_K GEMV 14336x4096: {roof['us_per_launch']} us/launch, {roof['achieved']} GB/s")
-        print(json.dumps({"roofline": roof}), flush=True)
+        q8 = q8k_gemv_configs1(lib)
+        for k, v in q8.items():
+            log(f"Q4_K x Q8_K GEMV {k}: {v['us_per_launch']} us, {v['GB_s']} GB/s")
+        print(json.dumps({"roofline": roof, "configs1_q8k_gemv": q8}), flush=True)
         return
 
     cfg = models.LLAMA1B
@@ -194,10 +220,13 @@ def main():
         match = bool(list(g["tokens"][:n]) == toks_first[:n])
     log(f"decode {tok_s:.1f} tok/s; greedy tokens match reference: {match}")
 
-    roof = None
+    roof = q8 = None
     if not args.no_roofline:
         roof = q4k_gemv_roofline(lib)
         log(f"Q4_K GEMV 14336x4096: {roof['us_per_launch']} us/launch, {roof['achieved']} GB/s")
+        q8 = q8k_gemv_configs1(lib)
+        for k, v in q8.items():
+            log(f"Q4_K x Q8_K GEMV {k}: {v['us_per_launch']} us, {v['GB_s']} GB/s")
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -219,6 +248,7 @@ def main():
                    "parallelism": "single GPU"},
         "greedy_tokens_match_reference": match,
         "roofline": roof,
+        "configs1_q8k_gemv": q8,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

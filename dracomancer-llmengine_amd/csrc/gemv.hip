@@ -44,42 +44,15 @@
 #include "dev_common.h"
 #include "formats.h"
 #include "gemv.h"
+#include "tile_frag.h"
 
 namespace {
-
-typedef int v4i __attribute__((ext_vector_type(4)));
 
 constexpr int SEG_R = 2;                  // rows per wave in k_seg (Q8_0)
 constexpr int SEG_ROWS = 4 * SEG_R;       // rows per block (4 waves)
 constexpr int XP_MAXV = 4;                // float4s of x per thread held by the prologue
 
 // ------------------------------------------------------------------ k_dq --
-struct Frag {
-    uint4 a, b, c;   // Q4_K: qs r=0, qs r=1, header.  Q6_K: ql A, ql B, qh
-    uint32_t sc, d;  // Q6_K: 4 scales, d
-};
-
-__device__ __forceinline__ void load_q4(const uint8_t* item, int lane, Frag& f) {
-    f.a = ldu4(item + 16 * lane);
-    f.b = ldu4(item + 1024 + 16 * lane);
-    f.c = ldu4(item + 2048 + 16 * (lane & 15));
-    f.sc = 0u;
-    f.d = 0u;
-}
-
-__device__ __forceinline__ void load_q6(const uint8_t* item, int lane, Frag& f) {
-    f.a = ldu4(item + 16 * lane);
-    f.b = ldu4(item + 1024 + 16 * lane);
-    f.c = ldu4(item + 2048 + 16 * lane);
-    f.sc = *reinterpret_cast<const uint32_t*>(item + 3072 + 4 * lane);
-    f.d = *reinterpret_cast<const uint16_t*>(item + 3328 + 2 * (lane & 15));
-}
-
-__device__ __forceinline__ float fold(const v4i C) {
-    const int i0 = (C[0] << 7) + C[1], i1 = (C[2] << 7) + C[3];
-    return fmaf((float)i1, 6.103515625e-05f, (float)i0);
-}
-
 // One Q4_K item: 16 rows x 256 values.  xa: this lane's A address for the
 // item's first group (or the zero region), xsm + gi: its (scale, sum) pairs.
 // Returns (d * sum_g sc*(x.q), dmin * sum_g m*(sum x)).

@@ -1,0 +1,26 @@
+// q8k.h -- internal interface of the Q8_K quantizer and the Q4_K/Q6_K x Q8_K
+// GEMV kernels (q8k.hip).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "formats.h"
+
+struct Q8Launch {
+    const uint8_t* base;  // weights, tile layout (formats.h)
+    DracoLayout L;
+    int n_in;
+    const uint8_t* xq;    // nvec * (n_in/256) Q8_K blocks, vector-major (device)
+    float* y;             // y[v * y_stride + row]
+    int y_stride;
+    int row0, row1;       // rows computed (row1 == 0: n_out)
+    int32_t* isc;         // optional (ISUMS launches): [n_out][nb] integer sums
+    int32_t* imn;
+    // filled by draco_gemv_q8k_launch
+    int tile0, n_tiles;
+};
+
+// Quantize nvec vectors of n floats (n % 256 == 0) into Q8_K blocks.
+int draco_q8k_quantize_launch(const float* x, int n, int nvec, uint8_t* out, hipStream_t st);
+// nvec in {1, 4, 8}; isums requires nvec == 1.
+int draco_gemv_q8k_launch(Q8Launch& a, int nvec, bool isums, hipStream_t st);

@@ -124,10 +124,32 @@ int draco_forget(const void* host);
 void draco_reset(void);
 size_t draco_resident_bytes(void);
 
+/* ---- Q8_K activations and the Q4_K / Q6_K x Q8_K GEMV --------------------
+ * No reference counterpart: the reference has no Q8_K path (nearest analogue:
+ * the Q8_0 x Q8_0 int8 dot of tests/i8dot_bench.c:63-183).  Block format
+ * {float d; int8 qs[256]; int16 bsums[16]} (292 bytes) and rounding of
+ * llama.cpp b10819 quantize_row_q8_K_ref.  Host pointers; weights are
+ * registered and kept resident like m5_gemv's.  0 ok, -1 unsupported, -2
+ * device error. */
+/* out: nvec * (n/256) blocks, vector-major. */
+int draco_q8k_quantize(const float* x, int n, int nvec, uint8_t* out);
+/* y[v * n_out + r] for v < nvec, nvec in {1, 4, 8}; xq as above. */
+int draco_gemv_q8k(int code, const uint8_t* xq, int nvec, const uint8_t* W, int n_out, int n_in, float* y);
+/* x fp32 (nvec vectors of n_in), quantized to Q8_K on the device first. */
+int draco_gemv_q8k_f32(int code, const float* x, int nvec, const uint8_t* W, int n_out, int n_in, float* y);
+/* Integer super-block sums of one vector: isc[r * nb + b], imn[r * nb + b]. */
+int draco_q8k_isums(int code, const uint8_t* xq, const uint8_t* W, int n_out, int n_in, int32_t* isc,
+                    int32_t* imn);
+/* out[0] us per Q8_K GEMV launch, out[1] us per (quantize + GEMV) pair, both
+ * from a graph replay of `iters` launches over n_copies weight copies. */
+int draco_bench_gemv_q8k(int code, const uint8_t* W, int n_out, int n_in, int nvec, int n_copies, int iters,
+                         float* out);
+
 /* Device timing probes (weights rotated over n_copies device copies so the
  * working set can exceed the 256 MB MALL).  out[0] mean us per launch from
  * per-launch event pairs, out[1] us per launch over the whole loop, out[2]
- * min, out[3] median. */
+ * min, out[3] median, out[4] us per launch from a graph replay of the same
+ * launches (out holds at least 5 floats). */
 int draco_bench_gemv(int code, const uint8_t* W, int n_out, int n_in, int n_copies, int iters,
                      float* out);
 /* out[0] us per empty-kernel launch in a stream, out[1] in a replayed graph. */
