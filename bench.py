@@ -33,6 +33,10 @@ sys.path.insert(0, ROOT)
 import numpy as np  # noqa: E402
 
 PEAK_HBM_GBS = 8000.0
+# HBM bytes per launch of the roofline kernel from the FETCH_SIZE / WRITE_SIZE
+# counter passes in profiles/gemv_q4k_14336x4096_roofline.md (scaled by a copy
+# of known size): 16282.0 * 2046.6 + 56.0 * 1024 bytes
+TRAFFIC_BYTES = 33379120
 CTX_START = 960
 MAX_DECODE = 64  # positions 960..1023 (max_t 1024)
 
@@ -59,7 +63,7 @@ def q4k_gemv_roofline(lib, n_copies=10, iters=200):
     alg_bytes = W.nbytes + 4 * n_in + 4 * n_out  # weights + fp32 x + fp32 y
     gbs = alg_bytes / us / 1e3
     return {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-            "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None,
+            "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": TRAFFIC_BYTES,
             "kernel": "k_dq<8,1,false> (W 14336x4096 Q4_K, fp32 x, 10 rotating copies)",
             "alg_bytes_per_launch": alg_bytes, "us_per_launch": round(us, 3),
             "us_per_launch_event_pairs": round(float(out[0]), 3)}

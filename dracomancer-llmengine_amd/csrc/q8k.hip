@@ -149,7 +149,10 @@ __global__ __launch_bounds__(64 * NW) void k_dq8(const Q8Launch a) {
             nbk = w;
             nt = ct + G;
         }
-        load(i + 1 < n_items ? nt : ct, nbk < nb ? nbk : nb - 1, nxt);
+        // a padding item (or the end) reloads this wave's first item of the
+        // current tile, already fetched, so it costs no HBM traffic
+        const bool real = i + 1 < n_items && nbk < nb;
+        load(real ? nt : ct, real ? nbk : (w < nb ? w : nb - 1), nxt);
         if (cb < nb) {
             int isc[NB], imn[NB];
 #pragma unroll
