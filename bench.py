@@ -92,6 +92,41 @@ def q8k_gemv_configs1(lib, n_copies=10, iters=200):
     return out
 
 
+def moe_ffn_configs3(lib, iters=100):
+    """configs[3] MoE FFN: hidden 2048, 128 experts (Q4_K gate/up/down, FFN 768), top-8, fp32 router.
+
+    One FFN = router GEMV + routed gate/up (+SwiGLU) + down (+weighted combine),
+    timed as a graph replay of `iters` FFNs.  Bytes per FFN = 8 experts' three
+    Q4_K matrices + the fp32 router.
+    """
+    import ctypes as ct
+    n_exp, n_used, inter, H = 128, 8, 768, 2048
+    rng = np.random.default_rng(3)
+    gate_inp = rng.standard_normal((n_exp, H), dtype=np.float32) * np.float32(0.02)
+    mats = []
+    for rows, cols in ((inter, H), (inter, H), (H, inter)):
+        chunks = [lib.quantize(5, rng.standard_normal((16 * rows, cols), dtype=np.float32) * np.float32(0.02))
+                  for _ in range(n_exp // 16)]
+        mats.append(np.concatenate(chunks))
+    per = [m.nbytes // n_exp for m in mats]
+    ptrs = np.zeros(3 * n_exp, np.uint64)
+    codes = np.full(3 * n_exp, 5, np.int32)
+    for e in range(n_exp):
+        for k in range(3):
+            ptrs[3 * e + k] = mats[k].ctypes.data + e * per[k]
+    x = rng.standard_normal(H).astype(np.float32)
+    o = np.zeros(4, np.float32)
+    rc = lib.load().draco_bench_granite_moe(lib.pf(x), ct.c_void_p(ptrs.ctypes.data), lib.pi32(codes),
+                                           lib.pf(gate_inp), n_exp, n_used, inter, H, H, iters, lib.pf(o))
+    if rc != 0:
+        raise RuntimeError(lib.last_error())
+    lib.load().draco_reset()
+    us, nbytes = float(o[0]), float(o[1])
+    return {"us_per_ffn": round(us, 3), "bytes_per_ffn": int(nbytes), "GB_s": round(nbytes / us / 1e3, 1),
+            "frac_of_peak": round(nbytes / us / 1e3 / PEAK_HBM_GBS, 4),
+            "shape": "128 experts top-8, FFN 768, hidden 2048, Q4_K experts, fp32 router"}
+
+
 def cpu_baseline_worker(args):
     """Child process: the reference engine decoding from context CTX_START."""
     from dracohip import models
@@ -187,7 +222,9 @@ def main():
         q8 = q8k_gemv_configs1(lib)
         for k, v in q8.items():
             log(f"Q4_K x Q8_K GEMV {k}: {v['us_per_launch']} us, {v['GB_s']} GB/s")
-        print(json.dumps({"roofline": roof, "configs1_q8k_gemv": q8}), flush=True)
+        moe = moe_ffn_configs3(lib)
+        log(f"MoE FFN configs[3]: {moe['us_per_ffn']} us, {moe['GB_s']} GB/s")
+        print(json.dumps({"roofline": roof, "configs1_q8k_gemv": q8, "configs3_moe_ffn": moe}), flush=True)
         return
 
     cfg = models.LLAMA1B
@@ -224,13 +261,15 @@ def main():
         match = bool(list(g["tokens"][:n]) == toks_first[:n])
     log(f"decode {tok_s:.1f} tok/s; greedy tokens match reference: {match}")
 
-    roof = q8 = None
+    roof = q8 = moe = None
     if not args.no_roofline:
         roof = q4k_gemv_roofline(lib)
         log(f"Q4_K GEMV 14336x4096: {roof['us_per_launch']} us/launch, {roof['achieved']} GB/s")
         q8 = q8k_gemv_configs1(lib)
         for k, v in q8.items():
             log(f"Q4_K x Q8_K GEMV {k}: {v['us_per_launch']} us, {v['GB_s']} GB/s")
+        moe = moe_ffn_configs3(lib)
+        log(f"MoE FFN configs[3]: {moe['us_per_ffn']} us, {moe['GB_s']} GB/s")
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -253,6 +292,7 @@ def main():
         "greedy_tokens_match_reference": match,
         "roofline": roof,
         "configs1_q8k_gemv": q8,
+        "configs3_moe_ffn": moe,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

@@ -1,0 +1,269 @@
+// abi_moe.cpp -- MoE entry points.
+//
+// m6_granite_moe: src/m6_layer.c:771-802 (called per layer by the qwen35
+// driver, src/qwen35_engine.py:294-307).  m5_gemvn_q4k / m5_gemvn_q6k:
+// src/m5/m5_batch8_k.c:80-183 (called by src/k2_engine.py:461-560).  All
+// pointers are caller-owned HOST pointers, as in the reference; expert
+// matrices are registered (uploaded once, kept resident) by host address.
+#include <stdio.h>
+#include <string.h>
+
+#include <map>
+#include <vector>
+
+#include "moe.h"
+#include "runtime.h"
+
+using namespace draco;
+
+namespace {
+
+int fm_of(int code) { return code == DRACO_Q4_K ? 1 : (code == DRACO_Q6_K ? 2 : 0); }
+
+// device pointer tables for one expert set, rebuilt when the registry epoch moves
+struct ExpertSet {
+    uint64_t epoch = 0;
+    const uint8_t** dev = nullptr;  // [3][n_exp]
+    int n_exp = 0;
+    int fm_gu = 0, fm_d = 0;
+    const DracoMat* router = nullptr;
+};
+
+std::map<const void*, ExpertSet>& sets() {
+    static std::map<const void*, ExpertSet> m;
+    return m;
+}
+
+ExpertSet* expert_set(const uint64_t* ptrs, const int* codes, const float* gate_inp, int n_exp, int inter,
+                      int n_in, int n_out, hipStream_t st) {
+    ExpertSet& s = sets()[ptrs];
+    if (s.dev && s.epoch == epoch() && s.n_exp == n_exp) {
+        s.router = get_mat(gate_inp, DRACO_F32, n_exp, n_in);
+        return s.router ? &s : nullptr;
+    }
+    const int fg = fm_of(codes[0]), fd = fm_of(codes[2]);
+    if (!fg || !fd) {
+        fail(-1, "m6_granite_moe: expert formats %d/%d not served (Q4_K, Q6_K)", codes[0], codes[2]);
+        return nullptr;
+    }
+    std::vector<const uint8_t*> tab(3 * (size_t)n_exp);
+    for (int e = 0; e < n_exp; e++) {
+        if (codes[3 * e] != codes[0] || codes[3 * e + 1] != codes[0] || codes[3 * e + 2] != codes[2]) {
+            fail(-1, "m6_granite_moe: mixed expert formats");
+            return nullptr;
+        }
+        const DracoMat* g = get_mat((const void*)(uintptr_t)ptrs[3 * e], codes[3 * e], inter, n_in);
+        const DracoMat* u = get_mat((const void*)(uintptr_t)ptrs[3 * e + 1], codes[3 * e + 1], inter, n_in);
+        const DracoMat* d = get_mat((const void*)(uintptr_t)ptrs[3 * e + 2], codes[3 * e + 2], n_out, inter);
+        if (!g || !u || !d) return nullptr;
+        tab[e] = g->dev;
+        tab[n_exp + e] = u->dev;
+        tab[2 * (size_t)n_exp + e] = d->dev;
+    }
+    if (s.dev && s.n_exp != n_exp) {
+        hipFree(s.dev);
+        s.dev = nullptr;
+    }
+    if (!s.dev && hipMalloc(&s.dev, sizeof(void*) * 3 * (size_t)n_exp) != hipSuccess) {
+        fail(-2, "m6_granite_moe: table allocation failed");
+        return nullptr;
+    }
+    if (hipMemcpyAsync(s.dev, tab.data(), sizeof(void*) * tab.size(), hipMemcpyHostToDevice, st) != hipSuccess ||
+        hipStreamSynchronize(st) != hipSuccess) {
+        fail(-2, "m6_granite_moe: table upload failed");
+        return nullptr;
+    }
+    s.n_exp = n_exp;
+    s.fm_gu = fg;
+    s.fm_d = fd;
+    s.router = get_mat(gate_inp, DRACO_F32, n_exp, n_in);
+    if (!s.router) return nullptr;
+    s.epoch = epoch();  // after every get_mat: a replacement above bumps it
+    return &s;
+}
+
+struct MoeWork {
+    float *x, *logits, *act, *out, *selw;
+    int* sel;
+    const uint8_t** seld;
+};
+
+int moe_work(MoeWork& w, int n_in, int n_exp, int n_used, int inter, int n_out) {
+    w.x = (float*)scratch(0, sizeof(float) * (size_t)n_in);
+    w.out = (float*)scratch(1, sizeof(float) * (size_t)n_out);
+    char* p = (char*)scratch(4, sizeof(float) * ((size_t)n_exp + (size_t)n_used * inter + 2 * MOE_USED_MAX) +
+                                    sizeof(void*) * MOE_USED_MAX + 256);
+    if (!w.x || !w.out || !p) return -2;
+    w.seld = (const uint8_t**)p;
+    w.logits = (float*)(p + sizeof(void*) * MOE_USED_MAX);
+    w.selw = w.logits + n_exp;
+    w.sel = (int*)(w.selw + MOE_USED_MAX);
+    w.act = (float*)(w.sel + MOE_USED_MAX);
+    return 0;
+}
+
+// enqueue router + routed gate/up + down/combine (x, out device pointers)
+int enqueue_moe(ExpertSet* s, const float* x, float* out, const float* resid, MoeWork& w, int n_exp, int n_used,
+                int inter, int n_in, int n_out, hipStream_t st) {
+    if (draco_moe_logits_launch(x, (const float*)s->router->dev, n_exp, n_in, w.logits, st))
+        return fail(-1, "moe router launch rejected");
+    MoeArgs a = {};
+    a.x = x;
+    a.n_in = n_in;
+    a.n_out_e = inter;
+    a.n_slots = n_used;
+    a.logits = w.logits;
+    a.n_exp = n_exp;
+    a.base0 = s->dev;
+    a.base1 = s->dev + n_exp;
+    a.base2 = s->dev + 2 * (size_t)n_exp;
+    a.sel = w.sel;
+    a.selw = w.selw;
+    a.seld = w.seld;
+    a.act = w.act;
+    if (draco_moe_grp_launch(a, s->fm_gu, true, false, true, st)) return fail(-1, "moe gate/up launch rejected");
+    a.inter = inter;
+    a.n_out = n_out;
+    a.out = out;
+    a.resid = resid;
+    if (draco_moe_down_launch(a, s->fm_d, st)) return fail(-1, "moe down launch rejected");
+    return 0;
+}
+
+int check_moe(int n_exp, int n_used, int inter, int n_in, int n_out) {
+    if (n_exp < 1 || n_exp > MOE_EXP_MAX || n_used < 1 || n_used > n_exp || n_used > 16)
+        return fail(-1, "m6_granite_moe: n_exp %d / n_used %d not served", n_exp, n_used);
+    if (inter % 256 || n_in % 256 || n_out % 16)
+        return fail(-1, "m6_granite_moe: shape inter %d n_in %d n_out %d not served", inter, n_in, n_out);
+    return 0;
+}
+
+int granite_moe(const float* x0, const uint64_t* ptrs, const int* codes, const float* gate_inp, int n_exp,
+                int n_used, int inter, int n_in, int n_out, float* out) {
+    if (int rc = check_moe(n_exp, n_used, inter, n_in, n_out)) return rc;
+    if (int rc = ensure_init()) return rc;
+    hipStream_t st = stream();
+    ExpertSet* s = expert_set(ptrs, codes, gate_inp, n_exp, inter, n_in, n_out, st);
+    if (!s) return -2;
+    MoeWork w;
+    if (moe_work(w, n_in, n_exp, n_used, inter, n_out)) return -2;
+    DRACO_HIP(hipMemcpyAsync(w.x, x0, sizeof(float) * (size_t)n_in, hipMemcpyHostToDevice, st));
+    if (int rc = enqueue_moe(s, w.x, w.out, nullptr, w, n_exp, n_used, inter, n_in, n_out, st)) return rc;
+    DRACO_HIP(hipGetLastError());
+    DRACO_HIP(hipMemcpyAsync(out, w.out, sizeof(float) * (size_t)n_out, hipMemcpyDeviceToHost, st));
+    DRACO_HIP(hipStreamSynchronize(st));
+    return 0;
+}
+
+int gemvn(int code, const float* x, long x_stride, const uint8_t* W, const int* idx, long per, int n_out_e,
+          int n_in, int n_exp, float* y) {
+    const int nb = n_in / 256;
+    if (nb <= 0 || n_in % 256 || nb > 256) return -1;  // the reference's own checks
+    if (n_exp < 1 || n_out_e < 1) return 0;
+    if (n_out_e % 16) return fail(-1, "m5_gemvn: n_out_e %d not a multiple of 16", n_out_e);
+    if (int rc = ensure_init()) return rc;
+    hipStream_t st = stream();
+    const size_t xf = x_stride ? (size_t)(n_exp - 1) * x_stride + n_in : (size_t)n_in;
+    float* dx = (float*)scratch(0, sizeof(float) * xf);
+    float* dy = (float*)scratch(1, sizeof(float) * (size_t)n_exp * n_out_e);
+    const uint8_t** db = (const uint8_t**)scratch(5, sizeof(void*) * (size_t)n_exp);
+    if (!dx || !dy || !db) return -2;
+    std::vector<const uint8_t*> tab(n_exp);
+    for (int e = 0; e < n_exp; e++) {
+        const DracoMat* m = get_mat(W + (int64_t)idx[e] * per, code, n_out_e, n_in);
+        if (!m) return -2;
+        tab[e] = m->dev;
+    }
+    DRACO_HIP(hipMemcpyAsync(db, tab.data(), sizeof(void*) * n_exp, hipMemcpyHostToDevice, st));
+    DRACO_HIP(hipMemcpyAsync(dx, x, sizeof(float) * xf, hipMemcpyHostToDevice, st));
+    // per-slot x: as many slots per launch as the prologue holds
+    const int per_launch = x_stride ? draco_moe_xper_slots(n_in) : MOE_USED_MAX;
+    if (per_launch < 1) return fail(-1, "m5_gemvn: n_in %d too long for per-expert x", n_in);
+    for (int e0 = 0; e0 < n_exp; e0 += per_launch) {
+        const int ns = n_exp - e0 < per_launch ? n_exp - e0 : per_launch;
+        MoeArgs a = {};
+        a.x = dx + (size_t)e0 * x_stride;
+        a.x_stride = x_stride;
+        a.n_in = n_in;
+        a.n_out_e = n_out_e;
+        a.n_slots = ns;
+        a.base0 = db + e0;
+        a.y = dy + (size_t)e0 * n_out_e;
+        if (draco_moe_grp_launch(a, fm_of(code), false, x_stride != 0, false, st))
+            return fail(-1, "m5_gemvn launch rejected");
+    }
+    DRACO_HIP(hipGetLastError());
+    DRACO_HIP(hipMemcpyAsync(y, dy, sizeof(float) * (size_t)n_exp * n_out_e, hipMemcpyDeviceToHost, st));
+    DRACO_HIP(hipStreamSynchronize(st));
+    return 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+void m6_granite_moe(const float* x0, const uint64_t* ptrs, const int* codes, const float* gate_inp, int n_exp,
+                    int n_used, int inter, int n_in, int n_out, float* scratch_unused, float* out) {
+    (void)scratch_unused;  // the device path needs no host scratch
+    std::lock_guard<std::recursive_mutex> g(api_mutex());
+    if (int rc = granite_moe(x0, ptrs, codes, gate_inp, n_exp, n_used, inter, n_in, n_out, out))
+        fprintf(stderr, "m6_granite_moe: rc %d: %s\n", rc, last_error());
+}
+
+int m5_gemvn_q4k(const float* x, long x_stride, const uint8_t* W, const int* idx, long per, int n_out_e,
+                 int n_in, int n_exp, float* y) {
+    std::lock_guard<std::recursive_mutex> g(api_mutex());
+    return gemvn(DRACO_Q4_K, x, x_stride, W, idx, per, n_out_e, n_in, n_exp, y);
+}
+
+int m5_gemvn_q6k(const float* x, long x_stride, const uint8_t* W, const int* idx, long per, int n_out_e,
+                 int n_in, int n_exp, float* y) {
+    std::lock_guard<std::recursive_mutex> g(api_mutex());
+    return gemvn(DRACO_Q6_K, x, x_stride, W, idx, per, n_out_e, n_in, n_exp, y);
+}
+
+// Same inputs as m6_granite_moe; returns 0 and out[0] = us per MoE FFN
+// (router + routed gate/up + down/combine) from a graph replay of `iters`
+// FFNs on the device (x fixed), out[1] = the routed experts' weight bytes per
+// FFN + router bytes.
+int draco_bench_granite_moe(const float* x0, const uint64_t* ptrs, const int* codes, const float* gate_inp,
+                            int n_exp, int n_used, int inter, int n_in, int n_out, int iters, float* out) {
+    std::lock_guard<std::recursive_mutex> g(api_mutex());
+    if (int rc = check_moe(n_exp, n_used, inter, n_in, n_out)) return rc;
+    if (int rc = ensure_init()) return rc;
+    hipStream_t st = stream();
+    ExpertSet* s = expert_set(ptrs, codes, gate_inp, n_exp, inter, n_in, n_out, st);
+    if (!s) return -2;
+    MoeWork w;
+    if (moe_work(w, n_in, n_exp, n_used, inter, n_out)) return -2;
+    DRACO_HIP(hipMemcpyAsync(w.x, x0, sizeof(float) * (size_t)n_in, hipMemcpyHostToDevice, st));
+    if (int rc = enqueue_moe(s, w.x, w.out, nullptr, w, n_exp, n_used, inter, n_in, n_out, st)) return rc;
+    DRACO_HIP(hipStreamSynchronize(st));
+    hipGraph_t graph;
+    hipGraphExec_t exec;
+    DRACO_HIP(hipStreamBeginCapture(st, hipStreamCaptureModeRelaxed));
+    for (int i = 0; i < iters; i++) enqueue_moe(s, w.x, w.out, nullptr, w, n_exp, n_used, inter, n_in, n_out, st);
+    DRACO_HIP(hipStreamEndCapture(st, &graph));
+    DRACO_HIP(hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0));
+    DRACO_HIP(hipGraphLaunch(exec, st));
+    hipEvent_t e0, e1;
+    DRACO_HIP(hipEventCreate(&e0));
+    DRACO_HIP(hipEventCreate(&e1));
+    DRACO_HIP(hipEventRecord(e0, st));
+    DRACO_HIP(hipGraphLaunch(exec, st));
+    DRACO_HIP(hipEventRecord(e1, st));
+    DRACO_HIP(hipStreamSynchronize(st));
+    float ms = 0;
+    DRACO_HIP(hipEventElapsedTime(&ms, e0, e1));
+    out[0] = ms * 1000.f / iters;
+    const double gu = (double)draco_row_bytes(codes[0], n_in) * inter * 2;
+    const double dn = (double)draco_row_bytes(codes[2], inter) * n_out;
+    out[1] = (float)(n_used * (gu + dn) + 4.0 * n_exp * n_in);
+    hipGraphExecDestroy(exec);
+    hipGraphDestroy(graph);
+    hipEventDestroy(e0);
+    hipEventDestroy(e1);
+    return 0;
+}
+
+}  // extern "C"

@@ -53,77 +53,6 @@ constexpr int SEG_ROWS = 4 * SEG_R;       // rows per block (4 waves)
 constexpr int XP_MAXV = 4;                // float4s of x per thread held by the prologue
 
 // ------------------------------------------------------------------ k_dq --
-// One Q4_K item: 16 rows x 256 values.  xa: this lane's A address for the
-// item's first group (or the zero region), xsm + gi: its (scale, sum) pairs.
-// Returns (d * sum_g sc*(x.q), dmin * sum_g m*(sum x)).
-__device__ __forceinline__ float2 dot_q4(const Frag& f, const int8_t* xa, const float2* xsm, int gi, int g) {
-    const int gh = g >> 1;
-    float sD = 0.f, sM = 0.f;
-#pragma unroll
-    for (int r = 0; r < 2; r++) {
-        const uint4 q = r ? f.b : f.a;
-#pragma unroll
-        for (int nib = 0; nib < 2; nib++) {
-            const uint32_t m = nib ? 0xF0F0F0F0u : 0x0F0F0F0Fu;
-            const v4i B = {(int)(q.x & m), (int)(q.y & m), (int)(q.z & m), (int)(q.w & m)};
-            const int go = 8 * r + 2 * nib;  // group offset of this MFMA (lane adds 4*gh + (g&1))
-            const v4i A = *reinterpret_cast<const v4i*>(xa + go * 64);
-            const v4i C = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, B, (v4i){0, 0, 0, 0}, 0, 0, 0);
-            const float fv = fold(C);
-            const float2 sm = xsm[gi + go];
-            // six-bit scale/min of sub-block 4r + 2gh + nib (src/m5_kern_scalar.c:39-46)
-            const int s0 = 2 * gh + nib;
-            int sc, mn;
-            if (r == 0) {
-                sc = (f.c.y >> (8 * s0)) & 63;
-                mn = (f.c.z >> (8 * s0)) & 63;
-            } else {
-                sc = ((f.c.w >> (8 * s0)) & 15) | (((f.c.y >> (8 * s0 + 6)) & 3) << 4);
-                mn = ((f.c.w >> (8 * s0 + 4)) & 15) | (((f.c.z >> (8 * s0 + 6)) & 3) << 4);
-            }
-            const float scf = (float)sc;
-            if (nib) {
-                sD = fmaf(scf, fv * (sm.x * 0.0625f), sD);
-                sD = fmaf(8.f * scf, sm.y, sD);
-            } else {
-                sD = fmaf(scf, fv * sm.x, sD);
-            }
-            sM = fmaf((float)mn, sm.y, sM);
-        }
-    }
-    return make_float2(h2f((uint16_t)(f.c.x & 0xFFFF)) * sD, h2f((uint16_t)(f.c.x >> 16)) * sM);
-}
-
-// One Q6_K item.  Fragment r (0..3) holds values 128*g2 + 32*r + 16*c + e
-// (g2 = g>>1, c = g&1), i.e. group 8*g2 + 2*r + c, with the GGUF bit map of
-// src/m5_kern_scalar.c:115-142: low nibble of ql A (r=0) / ql B (r=1), high
-// nibble of ql A (r=2) / ql B (r=3), and qh bits 2r.
-__device__ __forceinline__ float dot_q6(const Frag& f, const int8_t* xa, const float2* xsm, int gi) {
-    const uint32_t A4[4] = {f.a.x, f.a.y, f.a.z, f.a.w};
-    const uint32_t B4[4] = {f.b.x, f.b.y, f.b.z, f.b.w};
-    const uint32_t H4[4] = {f.c.x, f.c.y, f.c.z, f.c.w};
-    float s = 0.f;
-#pragma unroll
-    for (int r = 0; r < 4; r++) {
-        v4i Bv;
-#pragma unroll
-        for (int w = 0; w < 4; w++) {
-            uint32_t v;
-            if (r == 0) v = (A4[w] & 0x0F0F0F0Fu) | ((H4[w] << 4) & 0x30303030u);
-            else if (r == 1) v = (B4[w] & 0x0F0F0F0Fu) | ((H4[w] << 2) & 0x30303030u);
-            else if (r == 2) v = ((A4[w] >> 4) & 0x0F0F0F0Fu) | (H4[w] & 0x30303030u);
-            else v = ((B4[w] >> 4) & 0x0F0F0F0Fu) | ((H4[w] >> 2) & 0x30303030u);
-            Bv[w] = (int)v;
-        }
-        const v4i A = *reinterpret_cast<const v4i*>(xa + r * 128);
-        const v4i C = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, Bv, (v4i){0, 0, 0, 0}, 0, 0, 0);
-        const float2 sm = xsm[gi + 2 * r];
-        const float scf = (float)(int)(int8_t)(f.sc >> (8 * r));
-        s = fmaf(scf, fmaf(-32.f, sm.y, fold(C) * sm.x), s);
-    }
-    return h2f((uint16_t)f.d) * s;
-}
-
 __device__ __forceinline__ void am_merge(float& v, int& i, float v2, int i2) {
     if (v2 > v || (v2 == v && i2 < i)) {
         v = v2;
@@ -228,25 +157,7 @@ __global__ __launch_bounds__(64 * NW) void k_dq(const SegLaunch a) {
             }
             if (a.xn_out && bx == 0) *reinterpret_cast<float4*>(a.xn_out + 4 * i4) = v;
         }
-        float am = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-        float sum = (v.x + v.y) + (v.z + v.w);
-        am = fmaxf(am, __shfl_xor(am, 1, 64));
-        am = fmaxf(am, __shfl_xor(am, 2, 64));
-        sum += __shfl_xor(sum, 1, 64);
-        sum += __shfl_xor(sum, 2, 64);
-        const int k = am > 0.f ? max(ilogbf(am) - 5, -100) : 0;
-        const float up = __builtin_bit_cast(float, (uint32_t)(127 + 21 - k) << 23);  // 2^(21-k)
-        const uint32_t X0 = (uint32_t)(int)rintf(v.x * up), X1 = (uint32_t)(int)rintf(v.y * up);
-        const uint32_t X2 = (uint32_t)(int)rintf(v.z * up), X3 = (uint32_t)(int)rintf(v.w * up);
-        const int grp = i4 >> 2, qq = i4 & 3;
-#pragma unroll
-        for (int dg = 0; dg < 4; dg++) {
-            const int sh = 21 - 7 * dg, wd = dg ? 7 : 8;
-            const uint32_t o = __builtin_amdgcn_ubfe(X0, sh, wd) | (__builtin_amdgcn_ubfe(X1, sh, wd) << 8) |
-                               (__builtin_amdgcn_ubfe(X2, sh, wd) << 16) | (__builtin_amdgcn_ubfe(X3, sh, wd) << 24);
-            *reinterpret_cast<uint32_t*>(xd + (grp * 4 + dg) * 16 + 4 * qq) = o;
-        }
-        if (qq == 0) xsm[grp] = make_float2(__builtin_bit_cast(float, (uint32_t)(127 + k - 7) << 23), sum);
+        digits4(v, i4, xd, xsm);
     }
     lds_barrier();
 

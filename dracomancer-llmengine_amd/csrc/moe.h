@@ -1,0 +1,47 @@
+// moe.h -- internal interface of the MoE kernels (moe.hip).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "formats.h"
+
+constexpr int MOE_EXP_MAX = 512;   // experts in the router (the reference's lg[512])
+constexpr int MOE_USED_MAX = 64;   // selected experts / grouped slots per launch
+
+struct MoeArgs {
+    // activations
+    const float* x;          // shared x, or slot j at x + j * x_stride
+    long x_stride;           // floats (0: shared)
+    const float* norm_w;     // RMSNorm of x in the prologue (do_norm)
+    int do_norm;
+    float eps;
+    int n_in;                // rows' length of the grouped matrices
+    int n_out_e;             // rows per grouped matrix
+    int n_slots;             // selected experts (routed) or grouped slots
+    // routing (k_moe_grp ROUTE)
+    const float* logits;
+    int n_exp;
+    const uint8_t* const* base0;  // [n_exp] (routed) or [n_slots]: gate / grouped matrix bases (tile layout)
+    const uint8_t* const* base1;  // [n_exp] up bases
+    const uint8_t* const* base2;  // [n_exp] down bases
+    int* sel;                // published routing: expert ids [n_used]
+    float* selw;             // weights [n_used]
+    const uint8_t** seld;    // down bases of the selected experts [n_used]
+    // outputs
+    float* act;              // routed: [n_used][n_out_e] SwiGLU activations
+    float* y;                // grouped: [n_slots][n_out_e]
+    // down + combine (k_moe_down)
+    int inter;
+    int n_out;
+    float* out;
+    const float* resid;      // optional: out = resid + sum
+};
+
+int draco_moe_logits_launch(const float* x, const float* gate_inp, int n_exp, int n_in, float* logits,
+                            hipStream_t st);
+// fm: 1 = Q4_K, 2 = Q6_K.  route (+dual): gate/up of the routed experts;
+// otherwise the grouped GEMV (xper: per-slot x).
+int draco_moe_grp_launch(MoeArgs& a, int fm, bool dual, bool xper, bool route, hipStream_t st);
+int draco_moe_down_launch(MoeArgs& a, int fm, hipStream_t st);
+// slots per grouped launch when every slot has its own x of length n_in
+int draco_moe_xper_slots(int n_in);

@@ -1,0 +1,503 @@
+// moe.hip -- top-k MoE expert FFN for decode and the grouped expert GEMV (gfx950).
+//
+// Reference: m6_granite_moe / topk_idx / moe_experts, src/m6_layer.c:699-821:
+//   logits[e] = x . gate_inp[e]; probs = softmax(logits); idx = stable top-k
+//   (largest first, lowest index on ties); wtop = probs[idx] / max(sum, 2^-14);
+//   act_j = silu(W_gate[e_j] x) * (W_up[e_j] x); out = sum_j wtop_j * (W_down[e_j] act_j).
+// and the grouped expert GEMV m5_gemvn_q4k/q6k, src/m5/m5_batch8_k.c:80-183:
+//   y[j] = W[idx[j]] . x_j, x_j = x + j*x_stride.
+//
+// Launches for one MoE FFN:
+//   k_moe_logits   one wave per expert row of the fp32 router (wave-tree sum)
+//   k_moe_grp      ROUTE: every block recomputes softmax / top-k / weights from
+//                  the logits (one wave, ~0.3 us) and runs the selected experts'
+//                  gate and up tiles together (16 rows x 256 values per item,
+//                  int8 MFMA on the digits of x as in gemv.hip) with a SwiGLU
+//                  epilogue into act[j]; block 0 publishes the routing.
+//   k_moe_down     one output tile per block, wave j = selected expert j over
+//                  its act_j digits; the epilogue forms sum_j wtop_j * y_j in j
+//                  order, so the combine needs no extra pass.
+// k_moe_grp without ROUTE is the grouped GEMV (shared x, or per-expert x for up
+// to MOE_XPER_MAX experts per launch).
+//
+// Numerics: the router sums in a wave tree and the softmax sum in a wave tree
+// (the reference sums sequentially), so logits and weights agree to fp32
+// rounding; top-k can differ from the reference only when two probabilities
+// are within that rounding of each other.
+#include <hip/hip_runtime.h>
+
+#include <mutex>
+
+#include "moe.h"
+#include "tile_frag.h"
+
+namespace {
+
+constexpr int XP_MAXV = 4;
+
+__global__ __launch_bounds__(256) void k_moe_logits(const float* __restrict__ x, const float* __restrict__ gi,
+                                                    int n_exp, int n_in, float* __restrict__ logits) {
+    const int e = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (e >= n_exp) return;  // uniform per wave
+    const float* w = gi + (size_t)e * n_in;
+    float acc = 0.f;
+    for (int i = lane * 4; i < n_in; i += 256) {
+        const float4 a = ld4(x + i), b = ld4(w + i);
+        acc = fmaf(a.x, b.x, acc);
+        acc = fmaf(a.y, b.y, acc);
+        acc = fmaf(a.z, b.z, acc);
+        acc = fmaf(a.w, b.w, acc);
+    }
+    acc = wave_sum(acc);
+    if (lane == 0) logits[e] = acc;
+}
+
+// Softmax over n_exp (<= 512) logits, stable top-k and renormalised weights,
+// by one wave; results into sidx[n_used], swt[n_used] (LDS).
+__device__ __forceinline__ void route_wave(const float* __restrict__ logits, int n_exp, int n_used, int* sidx,
+                                           float* swt) {
+    constexpr int PER = MOE_EXP_MAX / 64;
+    const int lane = threadIdx.x & 63;
+    float p[PER];
+    float mx = -1e30f;
+#pragma unroll
+    for (int q = 0; q < PER; q++) {
+        const int e = lane + 64 * q;
+        p[q] = e < n_exp ? logits[e] : -1e30f;
+        mx = fmaxf(mx, p[q]);
+    }
+    mx = wave_max(mx);
+    float s = 0.f;
+#pragma unroll
+    for (int q = 0; q < PER; q++) {
+        const int e = lane + 64 * q;
+        if (e < n_exp) {
+            p[q] = expf(p[q] - mx);
+            s += p[q];
+        }
+    }
+    const float inv = 1.f / wave_sum(s);
+#pragma unroll
+    for (int q = 0; q < PER; q++) p[q] = lane + 64 * q < n_exp ? p[q] * inv : -2.f;  // -2: never selected
+    for (int t = 0; t < n_used; t++) {
+        float bv = -1.5f;
+        int bi = 0x7fffffff;
+#pragma unroll
+        for (int q = 0; q < PER; q++)
+            if (p[q] > bv) {  // q ascending = expert index ascending within the lane
+                bv = p[q];
+                bi = lane + 64 * q;
+            }
+#pragma unroll
+        for (int m = 32; m >= 1; m >>= 1) {
+            const float v2 = __shfl_xor(bv, m, 64);
+            const int i2 = __shfl_xor(bi, m, 64);
+            if (v2 > bv || (v2 == bv && i2 < bi)) {
+                bv = v2;
+                bi = i2;
+            }
+        }
+#pragma unroll
+        for (int q = 0; q < PER; q++)
+            if (lane + 64 * q == bi) p[q] = -2.f;
+        if (lane == 0) {
+            sidx[t] = bi;
+            swt[t] = bv;
+        }
+    }
+    if (lane == 0) {
+        float ws = 0.f;
+        for (int t = 0; t < n_used; t++) ws += swt[t];
+        if (ws < 6.103515625e-5f) ws = 6.103515625e-5f;
+        for (int t = 0; t < n_used; t++) swt[t] /= ws;
+    }
+}
+
+// Grouped expert GEMV over 16-row tiles: tile T -> slot s = T / tpe, local
+// tile T % tpe of expert e_s.  ROUTE: e_s from the routing prologue, gate/up
+// (DUAL) with SwiGLU into a.act; otherwise e_s = a.idx[s] and y[s][row].
+// XPER: slot s reads x + s * x_stride (digits of every slot in LDS).
+template <int NW, int FM, bool DUAL, bool XPER, bool ROUTE>
+__global__ __launch_bounds__(64 * NW) void k_moe_grp(const MoeArgs a) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    constexpr int NT = 64 * NW;
+    constexpr size_t IB = FM == 1 ? DRACO_Q4T_ITEM : DRACO_Q6T_ITEM;
+    const int n_in = a.n_in, nb = n_in >> 8, ng = n_in >> 4, n4 = n_in >> 2;
+    const int nx = XPER ? a.n_slots : 1;  // digit sets
+    int8_t* xd = reinterpret_cast<int8_t*>(smem);                            // [nx][ng][4][16]
+    int8_t* zero = xd + (size_t)nx * ng * 64;                                // 1 KB of zeros
+    float2* xsm = reinterpret_cast<float2*>(zero + 1024);                    // [nx][ng]
+    float* red = reinterpret_cast<float*>(xsm + (size_t)nx * ng);            // [2][NW][16] (+ norm)
+    int* sidx = reinterpret_cast<int*>(red + 2 * NW * 16 + 64);              // [MOE_USED_MAX]
+    float* swt = reinterpret_cast<float*>(sidx + MOE_USED_MAX);
+    const uint8_t** sb0 = reinterpret_cast<const uint8_t**>(swt + MOE_USED_MAX);  // [MOE_USED_MAX] bases
+    const uint8_t** sb1 = sb0 + MOE_USED_MAX;
+
+    const int tid = threadIdx.x, lane = tid & 63, j = lane & 15, g = lane >> 4;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int bx = blockIdx.x, G = gridDim.x;
+    const int n_slots = a.n_slots, tpe = a.n_out_e >> 4;
+    const int total = n_slots * tpe;
+    const int ipt = (nb + NW - 1) / NW;
+    const int my_tiles = bx < total ? (total - bx + G - 1) / G : 0;
+    const int n_items = my_tiles * ipt;
+
+    // x loads first (independent of the routing)
+    float4 xv[XP_MAXV], wv[XP_MAXV];
+    const int nvals4 = nx * n4;
+#pragma unroll
+    for (int q = 0; q < XP_MAXV; q++) {
+        const int i4 = tid + q * NT;
+        if (i4 < nvals4) {
+            const int s = XPER ? i4 / n4 : 0, o = i4 - s * n4;
+            xv[q] = ld4(a.x + (size_t)s * a.x_stride + 4 * o);
+            if (a.do_norm && a.norm_w) wv[q] = ld4(a.norm_w + 4 * o);
+        }
+    }
+    // routing / expert bases
+    if (ROUTE) {
+        if (w == 0) {
+            route_wave(a.logits, a.n_exp, n_slots, sidx, swt);
+            if (lane < n_slots) {
+                const int e = sidx[lane];
+                sb0[lane] = a.base0[e];
+                if (DUAL) sb1[lane] = a.base1[e];
+                if (bx == 0) {
+                    a.sel[lane] = e;
+                    a.selw[lane] = swt[lane];
+                    a.seld[lane] = a.base2[e];
+                }
+            }
+        }
+    } else if (tid < n_slots) {
+        sb0[tid] = a.base0[tid];
+        if (DUAL) sb1[tid] = a.base1[tid];
+    }
+    for (int i = tid; i < 256; i += NT) reinterpret_cast<uint32_t*>(zero)[i] = 0u;
+    lds_barrier();
+
+    auto load = [&](int T, int b, Frag& f, Frag& f2) {
+        const int s = T / tpe, lt = T - s * tpe;
+        const size_t off = ((size_t)lt * nb + b) * IB;
+        if (FM == 1) load_q4(sb0[s] + off, lane, f);
+        else load_q6(sb0[s] + off, lane, f);
+        if (DUAL) {
+            if (FM == 1) load_q4(sb1[s] + off, lane, f2);
+            else load_q6(sb1[s] + off, lane, f2);
+        }
+    };
+    Frag P0, P1, Q0, Q1;
+    int ct = bx, cb = w, cp = 0;
+    load(ct < total ? ct : total - 1, cb < nb ? cb : nb - 1, P0, Q0);
+
+    // digits (RMSNorm first when asked; one norm for the shared x)
+    float inv = 1.f;
+    if (a.do_norm) {
+        float ss = 0.f;
+#pragma unroll
+        for (int q = 0; q < XP_MAXV; q++)
+            if (tid + q * NT < n4) {
+                const float4 v = xv[q];
+                ss = fmaf(v.x, v.x, ss);
+                ss = fmaf(v.y, v.y, ss);
+                ss = fmaf(v.z, v.z, ss);
+                ss = fmaf(v.w, v.w, ss);
+            }
+        ss = wave_sum(ss);
+        if (lane == 0) red[2 * NW * 16 + w] = ss;
+        lds_barrier();
+        float tot = 0.f;
+#pragma unroll
+        for (int i = 0; i < NW; i++) tot += red[2 * NW * 16 + i];
+        inv = 1.f / sqrtf(tot / (float)n_in + a.eps);
+    }
+#pragma unroll
+    for (int q = 0; q < XP_MAXV; q++) {
+        const int i4 = tid + q * NT;
+        if (i4 >= nvals4) break;
+        float4 v = xv[q];
+        if (a.do_norm) {
+            if (a.norm_w) {
+                const float4 nw = wv[q];
+                v.x = v.x * inv * nw.x; v.y = v.y * inv * nw.y; v.z = v.z * inv * nw.z; v.w = v.w * inv * nw.w;
+            } else {
+                v.x *= inv; v.y *= inv; v.z *= inv; v.w *= inv;
+            }
+        }
+        const int s = XPER ? i4 / n4 : 0, o = i4 - s * n4;
+        digits4(v, o, xd + (size_t)s * ng * 64, xsm + (size_t)s * ng);
+    }
+    lds_barrier();
+
+    const bool adig = (j >> 2) == g;
+    const int gl4 = 4 * (g >> 1) + (g & 1), gl6 = 8 * (g >> 1) + (g & 1);
+    float aD = 0.f, aM = 0.f, aD2 = 0.f, aM2 = 0.f;
+    auto step = [&](int i, Frag& cur, Frag& nxt, Frag& cur2, Frag& nxt2) {
+        int nt = ct, nbk = cb + NW, np = cp + 1;
+        if (np == ipt) {
+            np = 0;
+            nbk = w;
+            nt = ct + G;
+        }
+        const bool real = i + 1 < n_items && nbk < nb;
+        load(real ? nt : ct, real ? nbk : (w < nb ? w : nb - 1), nxt, nxt2);
+        if (cb < nb) {
+            const int s = XPER ? ct / tpe : 0;
+            const int8_t* xs = xd + (size_t)s * ng * 64;
+            const float2* ms = xsm + (size_t)s * ng;
+            float cD, cM, cD2 = 0.f, cM2 = 0.f;
+            if (FM == 1) {
+                const int8_t* xa = adig ? xs + (size_t)cb * 1024 + (gl4 * 4 + (j & 3)) * 16 : zero;
+                const float2 r = dot_q4(cur, xa, ms, cb * 16 + gl4, g);
+                cD = r.x;
+                cM = r.y;
+                if (DUAL) {
+                    const float2 r2 = dot_q4(cur2, xa, ms, cb * 16 + gl4, g);
+                    cD2 = r2.x;
+                    cM2 = r2.y;
+                }
+            } else {
+                const int8_t* xa = adig ? xs + (size_t)cb * 1024 + (gl6 * 4 + (j & 3)) * 16 : zero;
+                cD = dot_q6(cur, xa, ms, cb * 16 + gl6);
+                cM = 0.f;
+                if (DUAL) cD2 = dot_q6(cur2, xa, ms, cb * 16 + gl6);
+            }
+            aD += cD;
+            aM += cM;
+            if (DUAL) {
+                aD2 += cD2;
+                aM2 += cM2;
+            }
+        }
+        if (cp == ipt - 1) {
+            float acc = aD - aM, acc2 = aD2 - aM2;
+            acc += __shfl_xor(acc, 16, 64);
+            acc += __shfl_xor(acc, 32, 64);
+            if (DUAL) {
+                acc2 += __shfl_xor(acc2, 16, 64);
+                acc2 += __shfl_xor(acc2, 32, 64);
+            }
+            if (lane < 16) {
+                red[w * 16 + j] = acc;
+                if (DUAL) red[(NW + w) * 16 + j] = acc2;
+            }
+            lds_barrier();
+            if (tid < 16) {
+                float v = 0.f, v2 = 0.f;
+#pragma unroll
+                for (int q = 0; q < NW; q++) {
+                    v += red[q * 16 + tid];
+                    if (DUAL) v2 += red[(NW + q) * 16 + tid];
+                }
+                const int s = ct / tpe, row = (ct - s * tpe) * 16 + tid;
+                float* y = (DUAL ? a.act : a.y) + (size_t)s * a.n_out_e;
+                if (DUAL) y[row] = (v / (1.f + expf(-v))) * v2;
+                else y[row] = v;
+            }
+            lds_barrier();
+            aD = aM = aD2 = aM2 = 0.f;
+        }
+        ct = nt;
+        cb = nbk;
+        cp = np;
+    };
+    for (int i = 0; i < n_items; i += 2) {
+        step(i, P0, P1, Q0, Q1);
+        if (i + 1 >= n_items) break;
+        step(i + 1, P1, P0, Q1, Q0);
+    }
+}
+
+// Down projection of the routed experts plus the weighted combine.  Block =
+// one 16-row output tile at a time; wave j (< n_used) = expert slot j, which
+// walks the nb super-blocks of its down rows over act_j's digits.
+template <int NW, int FM>
+__global__ __launch_bounds__(64 * NW) void k_moe_down(const MoeArgs a) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    constexpr int NT = 64 * NW;
+    constexpr size_t IB = FM == 1 ? DRACO_Q4T_ITEM : DRACO_Q6T_ITEM;
+    const int inter = a.inter, nb = inter >> 8, ng = inter >> 4, n4 = inter >> 2;
+    const int n_used = a.n_slots;
+    int8_t* xd = reinterpret_cast<int8_t*>(smem);                      // [n_used][ng][64]
+    int8_t* zero = xd + (size_t)n_used * ng * 64;
+    float2* xsm = reinterpret_cast<float2*>(zero + 1024);              // [n_used][ng]
+    float* red = reinterpret_cast<float*>(xsm + (size_t)n_used * ng);  // [NW][16]
+    float* swt = red + NW * 16;                                        // [MOE_USED_MAX]
+
+    const int tid = threadIdx.x, lane = tid & 63, j = lane & 15, g = lane >> 4;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int tiles = a.n_out >> 4;
+    const bool active = w < n_used;
+    // this wave's expert base (routing published by k_moe_grp)
+    const uint8_t* base = a.seld[active ? w : 0];
+    if (tid < n_used) swt[tid] = a.selw[tid];
+    for (int i = tid; i < 256; i += NT) reinterpret_cast<uint32_t*>(zero)[i] = 0u;
+    // act loads (all slots), then digits
+    const int nvals4 = n_used * n4;
+    for (int i4 = tid; i4 < nvals4; i4 += NT) {
+        const int s = i4 / n4, o = i4 - s * n4;
+        digits4(ld4(a.act + (size_t)s * inter + 4 * o), o, xd + (size_t)s * ng * 64, xsm + (size_t)s * ng);
+    }
+    lds_barrier();
+    const bool adig = (j >> 2) == g;
+    const int gl4 = 4 * (g >> 1) + (g & 1), gl6 = 8 * (g >> 1) + (g & 1);
+    const int8_t* xs = xd + (size_t)(active ? w : 0) * ng * 64;
+    const float2* ms = xsm + (size_t)(active ? w : 0) * ng;
+    for (int t = blockIdx.x; t < tiles; t += gridDim.x) {
+        float aD = 0.f, aM = 0.f;
+        if (active) {
+            Frag P0, P1;
+            auto ld = [&](int b, Frag& f) {
+                const uint8_t* p = base + ((size_t)t * nb + b) * IB;
+                if (FM == 1) load_q4(p, lane, f);
+                else load_q6(p, lane, f);
+            };
+            ld(0, P0);
+            for (int b = 0; b < nb; b += 2) {
+                ld(b + 1 < nb ? b + 1 : b, P1);
+                if (FM == 1) {
+                    const int8_t* xa = adig ? xs + (size_t)b * 1024 + (gl4 * 4 + (j & 3)) * 16 : zero;
+                    const float2 r = dot_q4(P0, xa, ms, b * 16 + gl4, g);
+                    aD += r.x;
+                    aM += r.y;
+                } else {
+                    const int8_t* xa = adig ? xs + (size_t)b * 1024 + (gl6 * 4 + (j & 3)) * 16 : zero;
+                    aD += dot_q6(P0, xa, ms, b * 16 + gl6);
+                }
+                if (b + 1 >= nb) break;
+                ld(b + 2 < nb ? b + 2 : b + 1, P0);
+                if (FM == 1) {
+                    const int8_t* xa = adig ? xs + (size_t)(b + 1) * 1024 + (gl4 * 4 + (j & 3)) * 16 : zero;
+                    const float2 r = dot_q4(P1, xa, ms, (b + 1) * 16 + gl4, g);
+                    aD += r.x;
+                    aM += r.y;
+                } else {
+                    const int8_t* xa = adig ? xs + (size_t)(b + 1) * 1024 + (gl6 * 4 + (j & 3)) * 16 : zero;
+                    aD += dot_q6(P1, xa, ms, (b + 1) * 16 + gl6);
+                }
+            }
+        }
+        float acc = aD - aM;
+        acc += __shfl_xor(acc, 16, 64);
+        acc += __shfl_xor(acc, 32, 64);
+        if (lane < 16) red[w * 16 + j] = acc;
+        lds_barrier();
+        if (tid < 16) {
+            float o = 0.f;
+            for (int s = 0; s < n_used; s++) o += swt[s] * red[s * 16 + tid];  // j order, like the reference
+            const int row = t * 16 + tid;
+            a.out[row] = a.resid ? a.resid[row] + o : o;
+        }
+        lds_barrier();
+    }
+}
+
+int cu_count() {
+    static int n = 0;
+    static std::once_flag once;
+    std::call_once(once, [] {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+            n = 256;
+    });
+    return n;
+}
+
+template <class K>
+void allow_big_lds(K kern) {
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                              160 * 1024);
+}
+
+template <int NW, int FM, bool DUAL, bool XPER, bool ROUTE>
+void launch_grp(const MoeArgs& a, int grid, size_t lds, hipStream_t st) {
+    static std::once_flag once;
+    std::call_once(once, [] { allow_big_lds(&k_moe_grp<NW, FM, DUAL, XPER, ROUTE>); });
+    hipLaunchKernelGGL((k_moe_grp<NW, FM, DUAL, XPER, ROUTE>), dim3(grid), dim3(64 * NW), lds, st, a);
+}
+
+template <int NW, int FM>
+void launch_down(const MoeArgs& a, int grid, size_t lds, hipStream_t st) {
+    static std::once_flag once;
+    std::call_once(once, [] { allow_big_lds(&k_moe_down<NW, FM>); });
+    hipLaunchKernelGGL((k_moe_down<NW, FM>), dim3(grid), dim3(64 * NW), lds, st, a);
+}
+
+int grp_nw(int n_in) {
+    const int nb = n_in / 256;
+    int nw = nb >= 8 ? 8 : 4;
+    while (n_in > XP_MAXV * 4 * 64 * nw && nw < 16) nw *= 2;
+    return nw;
+}
+
+template <int NW>
+int dispatch_grp(const MoeArgs& a, int fm, bool dual, bool xper, bool route, int grid, size_t lds, hipStream_t st) {
+    if (route) {
+        if (!dual) return -1;
+        if (fm == 1) launch_grp<NW, 1, true, false, true>(a, grid, lds, st);
+        else launch_grp<NW, 2, true, false, true>(a, grid, lds, st);
+        return 0;
+    }
+    if (dual) return -1;
+    if (fm == 1) {
+        if (xper) launch_grp<NW, 1, false, true, false>(a, grid, lds, st);
+        else launch_grp<NW, 1, false, false, false>(a, grid, lds, st);
+    } else {
+        if (xper) launch_grp<NW, 2, false, true, false>(a, grid, lds, st);
+        else launch_grp<NW, 2, false, false, false>(a, grid, lds, st);
+    }
+    return 0;
+}
+
+}  // namespace
+
+int draco_moe_logits_launch(const float* x, const float* gate_inp, int n_exp, int n_in, float* logits,
+                            hipStream_t st) {
+    if (n_exp < 1 || n_exp > MOE_EXP_MAX || n_in % 4) return -1;
+    hipLaunchKernelGGL(k_moe_logits, dim3((n_exp + 3) / 4), dim3(256), 0, st, x, gate_inp, n_exp, n_in, logits);
+    return 0;
+}
+
+// ROUTE + DUAL (gate/up of the routed experts) or the plain grouped GEMV.
+int draco_moe_grp_launch(MoeArgs& a, int fm, bool dual, bool xper, bool route, hipStream_t st) {
+    const int n_in = a.n_in;
+    if (n_in % 256 || a.n_out_e % 16 || a.n_slots < 1 || a.n_slots > MOE_USED_MAX) return -1;
+    if (route && (a.n_exp < a.n_slots || a.n_exp > MOE_EXP_MAX)) return -1;
+    const int nw = grp_nw(n_in);
+    const int nx = xper ? a.n_slots : 1;
+    if ((size_t)nx * (n_in / 4) > (size_t)XP_MAXV * 64 * nw) return -1;  // prologue capacity
+    const size_t lds = (size_t)nx * (n_in / 16) * 72 + 1024 + (2 * 16 * 16 + 64) * 4 + MOE_USED_MAX * 24;
+    if (lds > 160 * 1024) return -1;
+    const int total = a.n_slots * (a.n_out_e / 16);
+    const int cap = cu_count() * (nw == 4 ? 4 : (nw == 8 ? 2 : 1));
+    const int grid = total < cap ? total : cap;
+    if (nw == 4) return dispatch_grp<4>(a, fm, dual, xper, route, grid, lds, st);
+    if (nw == 8) return dispatch_grp<8>(a, fm, dual, xper, route, grid, lds, st);
+    return dispatch_grp<16>(a, fm, dual, xper, route, grid, lds, st);
+}
+
+int draco_moe_xper_slots(int n_in) {
+    if (n_in <= 0 || n_in % 256) return 0;
+    return (XP_MAXV * 64 * grp_nw(n_in) * 4) / n_in;
+}
+
+int draco_moe_down_launch(MoeArgs& a, int fm, hipStream_t st) {
+    if (a.inter % 256 || a.n_out % 16 || a.n_slots < 1 || a.n_slots > 16) return -1;
+    const int nw = a.n_slots <= 4 ? 4 : (a.n_slots <= 8 ? 8 : 16);
+    if (a.n_slots * (a.inter / 4) > 4096 * 4) return -1;
+    const size_t lds = (size_t)a.n_slots * (a.inter / 16) * 72 + 1024 + (size_t)nw * 16 * 4 + MOE_USED_MAX * 4;
+    if (lds > 160 * 1024) return -1;
+    const int tiles = a.n_out / 16;
+    if (nw == 4) {
+        if (fm == 1) launch_down<4, 1>(a, tiles, lds, st);
+        else launch_down<4, 2>(a, tiles, lds, st);
+    } else if (nw == 8) {
+        if (fm == 1) launch_down<8, 1>(a, tiles, lds, st);
+        else launch_down<8, 2>(a, tiles, lds, st);
+    } else {
+        if (fm == 1) launch_down<16, 1>(a, tiles, lds, st);
+        else launch_down<16, 2>(a, tiles, lds, st);
+    }
+    return 0;
+}

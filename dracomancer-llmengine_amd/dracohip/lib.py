@@ -63,6 +63,13 @@ SIGNATURES = {
     "draco_version": (ct.c_char_p, []),
     "draco_bench_gemv": (ct.c_int, [ct.c_int, u8p, ct.c_int, ct.c_int, ct.c_int, ct.c_int, f32p]),
     "draco_bench_launch": (ct.c_int, [ct.c_int, f32p]),
+    # MoE (src/m6_layer.c:771-802, src/m5/m5_batch8_k.c:80-183)
+    "m6_granite_moe": (None, [f32p, ct.c_void_p, i32p, f32p, ct.c_int, ct.c_int, ct.c_int, ct.c_int, ct.c_int,
+                              f32p, f32p]),
+    "m5_gemvn_q4k": (ct.c_int, [f32p, ct.c_long, u8p, i32p, ct.c_long, ct.c_int, ct.c_int, ct.c_int, f32p]),
+    "m5_gemvn_q6k": (ct.c_int, [f32p, ct.c_long, u8p, i32p, ct.c_long, ct.c_int, ct.c_int, ct.c_int, f32p]),
+    "draco_bench_granite_moe": (ct.c_int, [f32p, ct.c_void_p, i32p, f32p, ct.c_int, ct.c_int, ct.c_int, ct.c_int,
+                                           ct.c_int, ct.c_int, f32p]),
     # Q8_K activations (no reference counterpart)
     "draco_q8k_quantize": (ct.c_int, [f32p, ct.c_int, ct.c_int, u8p]),
     "draco_gemv_q8k": (ct.c_int, [ct.c_int, u8p, ct.c_int, u8p, ct.c_int, ct.c_int, f32p]),

@@ -124,6 +124,29 @@ int draco_forget(const void* host);
 void draco_reset(void);
 size_t draco_resident_bytes(void);
 
+/* ---- MoE ----------------------------------------------------------------
+ * m6_granite_moe: src/m6_layer.c:771-802 -- router (fp32 gate_inp
+ * [n_exp][n_in]) -> softmax -> stable top-n_used -> renormalised weights ->
+ * per expert silu(gate.x)*(up.x) -> down -> weighted sum into out[n_out].
+ * ptrs/codes: 3 per expert (gate, up, down), host pointers.  Served: Q4_K /
+ * Q6_K experts, n_exp <= 512, n_used <= 16, inter and n_in multiples of 256,
+ * n_out a multiple of 16.  `scratch` is not used (the reference's host scratch
+ * is not needed by the device path).  Errors are printed (void, as the
+ * reference). */
+void m6_granite_moe(const float* x0, const uint64_t* ptrs, const int* codes, const float* gate_inp, int n_exp,
+                    int n_used, int inter, int n_in, int n_out, float* scratch, float* out);
+/* m5_gemvn_q4k / m5_gemvn_q6k: src/m5/m5_batch8_k.c:80-183.  y[e * n_out_e + r]
+ * = (W + idx[e] * per)[r] . (x + e * x_stride) for e < n_exp.  Returns -1 for
+ * n_in % 256 != 0 (as the reference) or n_out_e % 16 != 0. */
+int m5_gemvn_q4k(const float* x, long x_stride, const uint8_t* W, const int* idx, long per, int n_out_e,
+                 int n_in, int n_exp, float* y);
+int m5_gemvn_q6k(const float* x, long x_stride, const uint8_t* W, const int* idx, long per, int n_out_e,
+                 int n_in, int n_exp, float* y);
+/* No reference counterpart: out[0] us per MoE FFN (router + routed gate/up +
+ * down/combine) from a graph replay of `iters` FFNs, out[1] bytes per FFN. */
+int draco_bench_granite_moe(const float* x0, const uint64_t* ptrs, const int* codes, const float* gate_inp,
+                            int n_exp, int n_used, int inter, int n_in, int n_out, int iters, float* out);
+
 /* ---- Q8_K activations and the Q4_K / Q6_K x Q8_K GEMV --------------------
  * No reference counterpart: the reference has no Q8_K path (nearest analogue:
  * the Q8_0 x Q8_0 int8 dot of tests/i8dot_bench.c:63-183).  Block format

@@ -1,0 +1,118 @@
+"""MoE on the GPU through the reference ABI: m6_granite_moe (src/m6_layer.c:771-802)
+and m5_gemvn_q4k / m5_gemvn_q6k (src/m5/m5_batch8_k.c:80-183).
+
+Checks: the compiled reference's own outputs (tests/golden/moe.npz, weights
+regenerated from the recorded seed and checked by digest), the oracle at the
+configs[3] shape with Q4_K experts, ties in the router, and the grouped GEMV
+with shared and per-expert x.  Bar: max|dy| <= 1e-5 * max|y_ref|.
+"""
+import ctypes as ct
+import hashlib
+
+import numpy as np
+import pytest
+
+from helpers import golden, rel_err
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-5
+
+
+def build_moe(n_exp, inter, n_in, n_out, seed, codes3=(5, 5, 4), digest_order=True):
+    from dracohip import lib
+    rng = np.random.default_rng(seed)
+    gate_inp = rng.standard_normal((n_exp, n_in), dtype=np.float32) * np.float32(0.02)
+    Wg = lib.quantize(codes3[0], rng.standard_normal((n_exp * inter, n_in), dtype=np.float32) * np.float32(0.02))
+    Wu = lib.quantize(codes3[1], rng.standard_normal((n_exp * inter, n_in), dtype=np.float32) * np.float32(0.02))
+    Wd = lib.quantize(codes3[2], rng.standard_normal((n_exp * n_out, inter), dtype=np.float32) * np.float32(0.02))
+    x = rng.standard_normal(n_in, dtype=np.float32)
+    pg, pu, pd = Wg.nbytes // n_exp, Wu.nbytes // n_exp, Wd.nbytes // n_exp
+    ptrs = np.zeros(3 * n_exp, np.uint64)
+    codes = np.zeros(3 * n_exp, np.int32)
+    for e in range(n_exp):
+        ptrs[3 * e:3 * e + 3] = (Wg.ctypes.data + e * pg, Wu.ctypes.data + e * pu, Wd.ctypes.data + e * pd)
+        codes[3 * e:3 * e + 3] = codes3
+    return dict(gate_inp=gate_inp, Wg=Wg, Wu=Wu, Wd=Wd, x=x, ptrs=ptrs, codes=codes)
+
+
+def run_hip(hip, M, n_exp, n_used, inter, n_in, n_out):
+    from dracohip import lib
+    y = np.zeros(n_out, np.float32)
+    scratch = np.zeros(8, np.float32)
+    hip.m6_granite_moe(lib.pf(M["x"]), ct.c_void_p(M["ptrs"].ctypes.data), lib.pi32(M["codes"]),
+                       lib.pf(M["gate_inp"]), n_exp, n_used, inter, n_in, n_out, lib.pf(scratch), lib.pf(y))
+    return y
+
+
+def run_oracle(oracle, M, n_exp, n_used, inter, n_in, n_out):
+    from dracohip import lib
+    y = np.zeros(n_out, np.float32)
+    scratch = np.zeros(3 * n_used * inter + n_used * n_out + 64, np.float32)
+    oracle.lib.or_granite_moe(lib.pf(M["x"]), ct.c_void_p(M["ptrs"].ctypes.data), lib.pi32(M["codes"]),
+                              lib.pf(M["gate_inp"]), n_exp, n_used, inter, n_in, n_out, lib.pf(scratch), lib.pf(y))
+    return y
+
+
+@pytest.mark.parametrize("tag", ["small", "cfg4"])
+def test_granite_moe_vs_reference_golden(hip, tag):
+    g = golden("moe.npz")
+    n_exp, n_used, inter, n_in, seed = [int(v) for v in g[f"{tag}_meta"]]
+    M = build_moe(n_exp, inter, n_in, n_in, seed)
+    assert hashlib.sha256(M["Wg"].tobytes() + M["Wu"].tobytes() + M["Wd"].tobytes()).digest() == \
+        g[f"{tag}_digest"].tobytes()
+    y = run_hip(hip, M, n_exp, n_used, inter, n_in, n_in)
+    assert rel_err(y, g[f"{tag}_y"]) <= TOL
+
+
+def test_granite_moe_configs3_q4k_experts(hip, oracle):
+    # hidden 2048, 128 experts, top-8, expert FFN 768, Q4_K experts
+    n_exp, n_used, inter, H = 128, 8, 768, 2048
+    M = build_moe(n_exp, inter, H, H, 33, codes3=(5, 5, 5))
+    for k in range(3):  # three tokens through the same registered experts
+        M["x"] = np.random.default_rng(100 + k).standard_normal(H).astype(np.float32)
+        y = run_hip(hip, M, n_exp, n_used, inter, H, H)
+        ref = run_oracle(oracle, M, n_exp, n_used, inter, H, H)
+        assert rel_err(y, ref) <= TOL
+
+
+def test_granite_moe_router_ties_pick_lowest_index(hip, oracle):
+    n_exp, n_used, inter, H = 16, 4, 256, 512
+    M = build_moe(n_exp, inter, H, H, 5)
+    gi = M["gate_inp"]
+    gi[3] = gi[11]  # experts 3 and 11 score identically; 5 and 6 too
+    gi[6] = gi[5]
+    gi[11] *= np.float32(4.0)  # make the tied pairs likely winners
+    gi[3] = gi[11]
+    y = run_hip(hip, M, n_exp, n_used, inter, H, H)
+    ref = run_oracle(oracle, M, n_exp, n_used, inter, H, H)
+    assert rel_err(y, ref) <= TOL
+
+
+@pytest.mark.parametrize("code", [4, 5])
+@pytest.mark.parametrize("per_expert_x", [False, True])
+def test_gemvn_grouped(hip, oracle, code, per_expert_x):
+    from dracohip import lib
+    n_tot, n_sel, n_out_e, n_in = 32, 8, 768, 2048
+    rng = np.random.default_rng(code + 2 * per_expert_x)
+    W = lib.quantize(code, rng.standard_normal((n_tot * n_out_e, n_in), dtype=np.float32) * np.float32(0.02))
+    per = W.nbytes // n_tot
+    idx = np.array(rng.choice(n_tot, n_sel, replace=False), np.int32)
+    x_stride = n_in if per_expert_x else 0
+    x = rng.standard_normal(n_sel * n_in if per_expert_x else n_in).astype(np.float32)
+    y = np.zeros(n_sel * n_out_e, np.float32)
+    fn = hip.m5_gemvn_q4k if code == 5 else hip.m5_gemvn_q6k
+    assert fn(lib.pf(x), x_stride, lib.pu8(W), lib.pi32(idx), per, n_out_e, n_in, n_sel, lib.pf(y)) == 0
+    ref = np.zeros_like(y)
+    ofn = oracle.lib.or_gemvn_q4k if code == 5 else oracle.lib.or_gemvn_q6k
+    assert ofn(lib.pf(x), x_stride, lib.pu8(W), lib.pi32(idx), per, n_out_e, n_in, n_sel, lib.pf(ref)) == 0
+    for e in range(n_sel):
+        assert rel_err(y[e * n_out_e:(e + 1) * n_out_e], ref[e * n_out_e:(e + 1) * n_out_e]) <= TOL
+
+
+def test_gemvn_rejects_like_reference(hip):
+    from dracohip import lib
+    x = np.zeros(512, np.float32)
+    W = np.zeros(144 * 2 * 16, np.uint8)
+    idx = np.zeros(1, np.int32)
+    y = np.zeros(16, np.float32)
+    assert hip.m5_gemvn_q4k(lib.pf(x), 0, lib.pu8(W), lib.pi32(idx), 0, 16, 300, 1, lib.pf(y)) == -1
