@@ -127,6 +127,31 @@ def moe_ffn_configs3(lib, iters=100):
             "shape": "128 experts top-8, FFN 768, hidden 2048, Q4_K experts, fp32 router"}
 
 
+def gdn_scan_configs4(lib):
+    """configs[4] GDN scan: 32 V heads / 16 q-k heads of 128, T = 4096 scanned in 64-token
+    launches, then 64 single-token (decode) steps; us per token, state bytes per token."""
+    T, n_vh, nhq = 4096, 32, 16
+    n_qkv = n_vh * 128 + 2 * nhq * 128
+    rng = np.random.default_rng(4)
+    QKV = rng.standard_normal((T, n_qkv), dtype=np.float32)
+    Z = rng.standard_normal((T, n_vh * 128), dtype=np.float32)
+    B = (1.0 / (1.0 + np.exp(-rng.standard_normal((T, n_vh))))).astype(np.float32)
+    G = np.exp(-np.logaddexp(0.0, rng.standard_normal((T, n_vh)))).astype(np.float32)
+    conv = rng.standard_normal((n_qkv, 4), dtype=np.float32) * np.float32(0.5)
+    ssm_norm = np.ones(128, np.float32)
+    tail = np.zeros(n_qkv * 3, np.float32)
+    S = np.zeros(n_vh * 128 * 128, np.float32)
+    o = np.zeros(4, np.float32)
+    rc = lib.load().draco_bench_gdn_scan(lib.pf(QKV), lib.pf(Z), lib.pf(B), lib.pf(G), lib.pf(conv),
+                                         lib.pf(ssm_norm), lib.pf(tail), lib.pf(S), T, n_qkv, n_vh, 64, 64,
+                                         lib.pf(o))
+    if rc != 0:
+        raise RuntimeError(lib.last_error())
+    return {"us_per_token_prefill_64chunks": round(float(o[0]), 3), "us_per_decode_step": round(float(o[1]), 3),
+            "prefill_tok_s_one_layer": round(1e6 / float(o[0]), 1),
+            "shape": "32 V heads, 16 q/k heads, head 128, T 4096 in 64-token launches + 64 decode steps"}
+
+
 def cpu_baseline_worker(args):
     """Child process: the reference engine decoding from context CTX_START."""
     from dracohip import models
@@ -224,7 +249,11 @@ def main():
             log(f"Q4_K x Q8_K GEMV {k}: {v['us_per_launch']} us, {v['GB_s']} GB/s")
         moe = moe_ffn_configs3(lib)
         log(f"MoE FFN configs[3]: {moe['us_per_ffn']} us, {moe['GB_s']} GB/s")
-        print(json.dumps({"roofline": roof, "configs1_q8k_gemv": q8, "configs3_moe_ffn": moe}), flush=True)
+        gdn = gdn_scan_configs4(lib)
+        log(f"GDN scan configs[4]: {gdn['us_per_token_prefill_64chunks']} us/token (64-token launches), "
+            f"{gdn['us_per_decode_step']} us/decode step")
+        print(json.dumps({"roofline": roof, "configs1_q8k_gemv": q8, "configs3_moe_ffn": moe,
+                          "configs4_gdn_scan": gdn}), flush=True)
         return
 
     cfg = models.LLAMA1B
@@ -261,7 +290,7 @@ def main():
         match = bool(list(g["tokens"][:n]) == toks_first[:n])
     log(f"decode {tok_s:.1f} tok/s; greedy tokens match reference: {match}")
 
-    roof = q8 = moe = None
+    roof = q8 = moe = gdn = None
     if not args.no_roofline:
         roof = q4k_gemv_roofline(lib)
         log(f"Q4_K GEMV 14336x4096: {roof['us_per_launch']} us/launch, {roof['achieved']} GB/s")
@@ -270,6 +299,9 @@ def main():
             log(f"Q4_K x Q8_K GEMV {k}: {v['us_per_launch']} us, {v['GB_s']} GB/s")
         moe = moe_ffn_configs3(lib)
         log(f"MoE FFN configs[3]: {moe['us_per_ffn']} us, {moe['GB_s']} GB/s")
+        gdn = gdn_scan_configs4(lib)
+        log(f"GDN scan configs[4]: {gdn['us_per_token_prefill_64chunks']} us/token (64-token launches), "
+            f"{gdn['us_per_decode_step']} us/decode step")
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -293,6 +325,7 @@ def main():
         "roofline": roof,
         "configs1_q8k_gemv": q8,
         "configs3_moe_ffn": moe,
+        "configs4_gdn_scan": gdn,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

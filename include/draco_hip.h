@@ -147,6 +147,22 @@ int m5_gemvn_q6k(const float* x, long x_stride, const uint8_t* W, const int* idx
 int draco_bench_granite_moe(const float* x0, const uint64_t* ptrs, const int* codes, const float* gate_inp,
                             int n_exp, int n_used, int inter, int n_in, int n_out, int iters, float* out);
 
+/* ---- Gated-DeltaNet scan ---------------------------------------------------
+ * m6_gdn_scan: src/m6_gdn_scan.c:18-93.  QKV[T*n_qkv] (q heads, k heads, v
+ * heads, 128 wide), Z[T*n_vh*128], B (beta) and G (= exp(alpha)) [T*n_vh],
+ * conv[n_qkv*4], ssm_norm[128]; tail[n_qkv*3] and S[n_vh*128*128] are updated
+ * in place; ON[T*n_vh*128].  Host pointers; `work` is not used. */
+void m6_gdn_scan(const float* QKV, const float* Z, const float* B, const float* G, const float* conv,
+                 const float* ssm_norm, float* tail, float* S, int T, int n_qkv, int n_vh, float* ON,
+                 float* work);
+/* No reference counterpart: device-resident timing with the same inputs (the
+ * caller's S and tail are not modified).  out[0] us per token scanning T tokens
+ * in launches of `chunk` tokens, out[1] us per single-token launch (n_dec
+ * steps). */
+int draco_bench_gdn_scan(const float* QKV, const float* Z, const float* B, const float* G, const float* conv,
+                         const float* ssm_norm, const float* tail, const float* S, int T, int n_qkv, int n_vh,
+                         int chunk, int n_dec, float* out);
+
 /* ---- Q8_K activations and the Q4_K / Q6_K x Q8_K GEMV --------------------
  * No reference counterpart: the reference has no Q8_K path (nearest analogue:
  * the Q8_0 x Q8_0 int8 dot of tests/i8dot_bench.c:63-183).  Block format
