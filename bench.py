@@ -152,6 +152,40 @@ def gdn_scan_configs4(lib):
             "shape": "32 V heads, 16 q/k heads, head 128, T 4096 in 64-token launches + 64 decode steps"}
 
 
+PEAK_INT8_TOPS = 5000.0
+
+
+def prefill_gemm_configs2(lib, T=256, n_copies=4, iters=20):
+    """configs[2] chunked prefill: one 256-token chunk through a Llama-1B layer's seven projections.
+
+    fp32-equivalent TFLOP/s = 2*T*n_out*n_in / time.  The int8 MFMA work issued
+    is 4x that (four digits of x) for Q4_K and 8x for Q6_K (A block-diagonal over
+    16-value halves); `mfma_util` = issued int8 ops / (time * 5.0 POP/s).
+    """
+    shapes = [("q", 5, 2048, 2048), ("k", 5, 512, 2048), ("v", 4, 512, 2048), ("o", 5, 2048, 2048),
+              ("gate", 5, 8192, 2048), ("up", 5, 8192, 2048), ("down", 4, 2048, 8192)]
+    rng = np.random.default_rng(2)
+    res, tot_us, tot_flop, tot_i8 = {}, 0.0, 0.0, 0.0
+    for name, code, n_out, n_in in shapes:
+        W = lib.quantize(code, rng.standard_normal((n_out, n_in), dtype=np.float32) * np.float32(0.02))
+        o = np.zeros(4, np.float32)
+        rc = lib.load().draco_bench_gemm(code, lib.pu8(W), n_out, n_in, T, n_copies, iters, lib.pf(o))
+        if rc != 0:
+            raise RuntimeError(lib.last_error())
+        us = float(o[0])
+        flop = 2.0 * T * n_out * n_in
+        i8 = flop * (4 if code == 5 else 8)
+        res[name] = {"us": round(us, 2), "us_kernel_only": round(float(o[1]), 2),
+                     "tflops_fp32_equiv": round(flop / us / 1e6, 1)}
+        tot_us += us
+        tot_flop += flop
+        tot_i8 += i8
+    return {"tokens": T, "us_per_layer_chunk": round(tot_us, 1),
+            "tflops_fp32_equiv": round(tot_flop / tot_us / 1e6, 1),
+            "mfma_util": round(tot_i8 / tot_us / 1e6 / PEAK_INT8_TOPS, 4),
+            "prefill_tok_s_16_layers": round(T / (16 * tot_us * 1e-6), 1), "per_matrix": res}
+
+
 def cpu_baseline_worker(args):
     """Child process: the reference engine decoding from context CTX_START."""
     from dracohip import models
@@ -252,8 +286,12 @@ def main():
         gdn = gdn_scan_configs4(lib)
         log(f"GDN scan configs[4]: {gdn['us_per_token_prefill_64chunks']} us/token (64-token launches), "
             f"{gdn['us_per_decode_step']} us/decode step")
+        pre = prefill_gemm_configs2(lib)
+        log(f"prefill GEMM configs[2] (256-token chunk, one layer): {pre['us_per_layer_chunk']} us, "
+            f"{pre['tflops_fp32_equiv']} TFLOP/s fp32-equiv, int8 MFMA util {pre['mfma_util']}")
         print(json.dumps({"roofline": roof, "configs1_q8k_gemv": q8, "configs3_moe_ffn": moe,
-                          "configs4_gdn_scan": gdn}), flush=True)
+                          "configs4_gdn_scan": gdn,
+        "configs2_prefill_gemm": pre, "configs2_prefill_gemm": pre}), flush=True)
         return
 
     cfg = models.LLAMA1B
@@ -290,7 +328,7 @@ def main():
         match = bool(list(g["tokens"][:n]) == toks_first[:n])
     log(f"decode {tok_s:.1f} tok/s; greedy tokens match reference: {match}")
 
-    roof = q8 = moe = gdn = None
+    roof = q8 = moe = gdn = pre = None
     if not args.no_roofline:
         roof = q4k_gemv_roofline(lib)
         log(f"Q4_K GEMV 14336x4096: {roof['us_per_launch']} us/launch, {roof['achieved']} GB/s")
@@ -302,6 +340,9 @@ def main():
         gdn = gdn_scan_configs4(lib)
         log(f"GDN scan configs[4]: {gdn['us_per_token_prefill_64chunks']} us/token (64-token launches), "
             f"{gdn['us_per_decode_step']} us/decode step")
+        pre = prefill_gemm_configs2(lib)
+        log(f"prefill GEMM configs[2] (256-token chunk, one layer): {pre['us_per_layer_chunk']} us, "
+            f"{pre['tflops_fp32_equiv']} TFLOP/s fp32-equiv, int8 MFMA util {pre['mfma_util']}")
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -326,6 +367,7 @@ def main():
         "configs1_q8k_gemv": q8,
         "configs3_moe_ffn": moe,
         "configs4_gdn_scan": gdn,
+        "configs2_prefill_gemm": pre,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

@@ -1,0 +1,146 @@
+// abi_gemm.cpp -- prefill GEMM entry points.
+//
+// m5_gemm_auto: src/m5/m5_gemm_fused.c:231-241 (0 = done, -1 = code not served,
+// the caller falls back); m5_gemm: src/m5/m5_gemm.c:249-272 (Y[T x n_out] =
+// X[T x n_in] . W^T).  Host pointers.  Q4_K / Q6_K run on the int8-MFMA GEMM
+// (gemm.hip); Q8_0 runs as one device GEMV per token.
+#include <string.h>
+
+#include <vector>
+
+#include "gemm.h"
+#include "runtime.h"
+
+extern "C" int draco_repack(int code, const uint8_t* src, int n_out, int n_in, uint8_t* dst);
+
+using namespace draco;
+
+namespace {
+
+bool served(int code) { return code == DRACO_Q4_K || code == DRACO_Q6_K || code == DRACO_Q8_0; }
+
+// X, Y device; enqueue Y = X . W^T
+int enqueue_gemm(const DracoMat& m, const float* X, int T, float* Y, uint8_t* digits, hipStream_t st) {
+    if (m.L.code == DRACO_Q8_0) {
+        for (int t = 0; t < T; t++)
+            if (draco_gemv_launch(m, X + (size_t)t * m.L.n_in, Y + (size_t)t * m.L.n_out, nullptr, 0, m.L.n_out, st))
+                return fail(-1, "gemm: gemv launch rejected");
+        return 0;
+    }
+    GemmArgs a = {};
+    if (draco_gemm_digits_launch(X, T, m.L.n_in, digits, a, st)) return fail(-1, "gemm: digits launch rejected");
+    a.W = m.dev;
+    a.L = m.L;
+    a.Y = Y;
+    a.ldy = m.L.n_out;
+    if (draco_gemm_launch(a, st)) return fail(-1, "gemm: launch rejected");
+    return 0;
+}
+
+int gemm_host(int code, const float* X, const uint8_t* W, int T, int n_out, int n_in, float* Y) {
+    if (!served(code)) return -1;
+    if (T < 0 || n_out <= 0 || n_in <= 0 || n_in % draco_block_values(code))
+        return fail(-1, "m5_gemm: bad shape T=%d %dx%d", T, n_out, n_in);
+    if (T == 0) return 0;
+    if (int rc = ensure_init()) return rc;
+    const DracoMat* m = get_mat(W, code, n_out, n_in);
+    if (!m) return -2;
+    hipStream_t st = stream();
+    float* dx = (float*)scratch(0, sizeof(float) * (size_t)T * n_in);
+    float* dy = (float*)scratch(1, sizeof(float) * (size_t)T * n_out);
+    uint8_t* dd = code == DRACO_Q8_0 ? nullptr : (uint8_t*)scratch(7, draco_gemm_digit_bytes(T, n_in));
+    if (!dx || !dy || (code != DRACO_Q8_0 && !dd)) return -2;
+    DRACO_HIP(hipMemcpyAsync(dx, X, sizeof(float) * (size_t)T * n_in, hipMemcpyHostToDevice, st));
+    if (int rc = enqueue_gemm(*m, dx, T, dy, dd, st)) return rc;
+    DRACO_HIP(hipGetLastError());
+    DRACO_HIP(hipMemcpyAsync(Y, dy, sizeof(float) * (size_t)T * n_out, hipMemcpyDeviceToHost, st));
+    DRACO_HIP(hipStreamSynchronize(st));
+    return 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+int m5_gemm_auto(int code, const float* X, const uint8_t* W, int c, int n_out, int n_in, float* Y) {
+    std::lock_guard<std::recursive_mutex> g(api_mutex());
+    return gemm_host(code, X, W, c, n_out, n_in, Y);
+}
+
+int m5_gemm(int code, const float* X, const uint8_t* W, int T, int n_out, int n_in, float* Y, float* wbuf) {
+    (void)wbuf;  // the device path needs no host row buffer
+    std::lock_guard<std::recursive_mutex> g(api_mutex());
+    return gemm_host(code, X, W, T, n_out, n_in, Y);
+}
+
+// Graph-replayed timing of the prefill GEMM on `n_copies` weight copies:
+// out[0] us per GEMM including the activation digitization, out[1] us per
+// GEMM kernel alone (digits computed once).
+int draco_bench_gemm(int code, const uint8_t* W, int n_out, int n_in, int T, int n_copies, int iters, float* out) {
+    std::lock_guard<std::recursive_mutex> g(api_mutex());
+    if (code != DRACO_Q4_K && code != DRACO_Q6_K) return fail(-1, "bench gemm: code %d not on the MFMA path", code);
+    if (int rc = ensure_init()) return rc;
+    DracoLayout L;
+    if (draco_layout(code, n_out, n_in, &L) || T < 1) return fail(-1, "bench gemm: bad shape");
+    if (n_copies < 1) n_copies = 1;
+    std::vector<uint8_t> host(L.bytes, 0);
+    draco_repack(code, W, n_out, n_in, host.data());
+    std::vector<DracoMat> mats(n_copies);
+    for (auto& m : mats) {
+        m.L = L;
+        DRACO_HIP(hipMalloc(&m.dev, L.bytes));
+        DRACO_HIP(hipMemcpy(m.dev, host.data(), L.bytes, hipMemcpyHostToDevice));
+    }
+    std::vector<float> xh((size_t)T * n_in);
+    for (size_t i = 0; i < xh.size(); i++) xh[i] = (float)((int)((i * 2654435761u) % 2001) - 1000) * 1e-3f;
+    float *dx, *dy;
+    uint8_t* dd;
+    DRACO_HIP(hipMalloc(&dx, sizeof(float) * xh.size()));
+    DRACO_HIP(hipMalloc(&dy, sizeof(float) * (size_t)T * n_out));
+    DRACO_HIP(hipMalloc(&dd, draco_gemm_digit_bytes(T, n_in)));
+    DRACO_HIP(hipMemcpy(dx, xh.data(), sizeof(float) * xh.size(), hipMemcpyHostToDevice));
+    hipStream_t st = stream();
+    GemmArgs a = {};
+    if (draco_gemm_digits_launch(dx, T, n_in, dd, a, st)) return fail(-1, "bench gemm: digits rejected");
+    hipEvent_t e0, e1;
+    DRACO_HIP(hipEventCreate(&e0));
+    DRACO_HIP(hipEventCreate(&e1));
+    for (int mode = 0; mode < 2; mode++) {
+        hipGraph_t graph;
+        hipGraphExec_t exec;
+        DRACO_HIP(hipStreamBeginCapture(st, hipStreamCaptureModeRelaxed));
+        for (int i = 0; i < iters; i++) {
+            if (mode == 0) {
+                enqueue_gemm(mats[i % n_copies], dx, T, dy, dd, st);
+            } else {
+                GemmArgs b = a;
+                b.W = mats[i % n_copies].dev;
+                b.L = L;
+                b.Y = dy;
+                b.ldy = n_out;
+                draco_gemm_launch(b, st);
+            }
+        }
+        DRACO_HIP(hipStreamEndCapture(st, &graph));
+        DRACO_HIP(hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0));
+        DRACO_HIP(hipGraphLaunch(exec, st));
+        DRACO_HIP(hipEventRecord(e0, st));
+        DRACO_HIP(hipGraphLaunch(exec, st));
+        DRACO_HIP(hipEventRecord(e1, st));
+        DRACO_HIP(hipStreamSynchronize(st));
+        float ms = 0;
+        DRACO_HIP(hipEventElapsedTime(&ms, e0, e1));
+        out[mode] = ms * 1000.f / iters;
+        hipGraphExecDestroy(exec);
+        hipGraphDestroy(graph);
+    }
+    hipEventDestroy(e0);
+    hipEventDestroy(e1);
+    for (auto& m : mats) hipFree(m.dev);
+    hipFree(dx);
+    hipFree(dy);
+    hipFree(dd);
+    return 0;
+}
+
+}  // extern "C"

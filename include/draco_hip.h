@@ -147,6 +147,18 @@ int m5_gemvn_q6k(const float* x, long x_stride, const uint8_t* W, const int* idx
 int draco_bench_granite_moe(const float* x0, const uint64_t* ptrs, const int* codes, const float* gate_inp,
                             int n_exp, int n_used, int inter, int n_in, int n_out, int iters, float* out);
 
+/* ---- Prefill GEMM: Y[T x n_out] = X[T x n_in] . W^T ----------------------
+ * m5_gemm_auto: src/m5/m5_gemm_fused.c:231-241 (0 done, -1 code not served:
+ * the caller falls back).  m5_gemm: src/m5/m5_gemm.c:249-272.  Host pointers.
+ * Served: Q4_K and Q6_K on int8 MFMA, Q8_0 as per-token device GEMVs.
+ * `wbuf` is not used. */
+int m5_gemm_auto(int code, const float* X, const uint8_t* W, int c, int n_out, int n_in, float* Y);
+int m5_gemm(int code, const float* X, const uint8_t* W, int T, int n_out, int n_in, float* Y, float* wbuf);
+/* No reference counterpart: out[0] us per GEMM including the activation
+ * digitization, out[1] us for the GEMM kernel alone (graph replays over
+ * n_copies weight copies). */
+int draco_bench_gemm(int code, const uint8_t* W, int n_out, int n_in, int T, int n_copies, int iters, float* out);
+
 /* ---- Gated-DeltaNet scan ---------------------------------------------------
  * m6_gdn_scan: src/m6_gdn_scan.c:18-93.  QKV[T*n_qkv] (q heads, k heads, v
  * heads, 128 wide), Z[T*n_vh*128], B (beta) and G (= exp(alpha)) [T*n_vh],

@@ -1,0 +1,57 @@
+"""Prefill GEMM on the GPU: m5_gemm / m5_gemm_auto (src/m5/m5_gemm.c:249-272,
+src/m5/m5_gemm_fused.c:231-241) vs the oracle's or_gemm (pinned as "equals
+stacked GEMVs").  Bar: max|dY| <= 1e-5 * max|Y_ref| over the whole output.
+"""
+import numpy as np
+import pytest
+
+from helpers import rel_err
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-5
+
+
+def _case(code, T, n_out, n_in, seed):
+    from dracohip import lib
+    rng = np.random.default_rng(seed)
+    W = lib.quantize(code, rng.standard_normal((n_out, n_in), dtype=np.float32) * np.float32(0.02))
+    X = rng.standard_normal((T, n_in)).astype(np.float32)
+    X[0, :7] = 0.0           # zeros, a large value and a tiny one in one super-block
+    if n_in > 300:
+        X[-1, 300] = 80.0
+        X[-1, 301] = 1e-30
+    return W, X
+
+
+@pytest.mark.parametrize("code", [5, 4, 0])
+@pytest.mark.parametrize("T,n_out,n_in", [(1, 16, 256), (7, 40, 512), (37, 96, 2048), (256, 2048, 2048),
+                                          (64, 8192, 2048), (100, 2048, 8192), (9, 48, 768)])
+def test_gemm_vs_oracle(hip, oracle, code, T, n_out, n_in):
+    from dracohip import lib
+    W, X = _case(code, T, n_out, n_in, T + n_out + code)
+    Y = np.zeros((T, n_out), np.float32)
+    wbuf = np.zeros(8, np.float32)
+    assert hip.m5_gemm(code, lib.pf(X), lib.pu8(W), T, n_out, n_in, lib.pf(Y), lib.pf(wbuf)) == 0, lib.last_error()
+    ref = np.zeros_like(Y)
+    assert oracle.lib.or_gemm(code, lib.pf(X), lib.pu8(W), T, n_out, n_in, lib.pf(ref)) == 0
+    assert rel_err(Y, ref) <= TOL
+    Y2 = np.zeros_like(Y)
+    assert hip.m5_gemm_auto(code, lib.pf(X), lib.pu8(W), T, n_out, n_in, lib.pf(Y2)) == 0
+    assert np.array_equal(Y, Y2)
+
+
+def test_gemm_equals_stacked_gemv(hip):
+    from dracohip import lib
+    W, X = _case(5, 24, 512, 2048, 3)
+    Y = np.zeros((24, 512), np.float32)
+    assert hip.m5_gemm_auto(5, lib.pf(X), lib.pu8(W), 24, 512, 2048, lib.pf(Y)) == 0
+    G = np.stack([lib.gemv(5, X[t], W, 512, 2048) for t in range(24)])
+    assert rel_err(Y, G) <= TOL
+
+
+def test_gemm_unsupported_code_returns_minus_one(hip):
+    from dracohip import lib
+    X = np.zeros((2, 256), np.float32)
+    W = np.zeros(4 * 110, np.uint8)
+    Y = np.zeros((2, 4), np.float32)
+    assert hip.m5_gemm_auto(2, lib.pf(X), lib.pu8(W), 2, 4, 256, lib.pf(Y)) == -1   # IQ3_S: caller falls back
