@@ -11,6 +11,8 @@
 #include <map>
 #include <vector>
 
+#include "decode.h"
+#include "gemm.h"
 #include "moe.h"
 #include "runtime.h"
 
@@ -198,9 +200,158 @@ int gemvn(int code, const float* x, long x_stride, const uint8_t* W, const int* 
     return 0;
 }
 
+// ---- token-batched MoE (prefill), src/m6_moe_tok.c:44-161 -----------------
+int moe_tok(const float* X, const int* order, const float* wtop, const uint64_t* ep, const int* ec, int T,
+            int n_used, int inter, int n_in, int n_out, int n_exp, float* out) {
+    if (T < 1 || n_used < 1 || n_exp < 1 || n_exp > MOE_EXP_MAX)
+        return fail(-1, "m6_moe_tok: T %d n_used %d n_exp %d not served", T, n_used, n_exp);
+    if (inter % 256 || n_in % 256 || n_out % 16)
+        return fail(-1, "m6_moe_tok: shape inter %d n_in %d n_out %d not served", inter, n_in, n_out);
+    // expert grouping (the reference's off/ilist/slot, segments padded to 8 tokens)
+    std::vector<int> cnt(n_exp, 0);
+    for (int i = 0; i < T * n_used; i++)
+        if (order[i] >= 0 && order[i] < n_exp) cnt[order[i]]++;
+    std::vector<int> oct0(n_exp, 0), active;
+    int n_oct = 0, max_oct = 0;
+    int cg = -1, cu = -1, cd = -1;
+    for (int e = 0; e < n_exp; e++) {
+        if (!cnt[e]) continue;
+        active.push_back(e);
+        oct0[e] = n_oct;
+        const int o = (cnt[e] + 7) / 8;
+        n_oct += o;
+        max_oct = o > max_oct ? o : max_oct;
+        if (cg < 0) {
+            cg = ec[3 * e];
+            cu = ec[3 * e + 1];
+            cd = ec[3 * e + 2];
+        }
+        if (ec[3 * e] != cg || ec[3 * e + 1] != cu || ec[3 * e + 2] != cd)
+            return fail(-1, "m6_moe_tok: mixed expert formats");
+    }
+    if (active.empty()) {
+        memset(out, 0, sizeof(float) * (size_t)T * n_out);
+        return 0;
+    }
+    if (!fm_of(cg) || !fm_of(cu) || !fm_of(cd) || cg != cu)
+        return fail(-1, "m6_moe_tok: expert formats %d/%d/%d not served", cg, cu, cd);
+    const int R = 8 * n_oct;
+    std::vector<int> src(R, -1), pos((size_t)T * n_used, -1), fill(n_exp, 0);
+    for (int i = 0; i < T * n_used; i++) {
+        const int e = order[i];
+        if (e < 0 || e >= n_exp) continue;
+        const int row = 8 * oct0[e] + fill[e]++;
+        src[row] = i / n_used;
+        pos[i] = row;
+    }
+    if (int rc = ensure_init()) return rc;
+    hipStream_t st = stream();
+    const int na = (int)active.size();
+    std::vector<GemmGroup> gg(na), gu(na), gd(na);
+    for (int k = 0; k < na; k++) {
+        const int e = active[k];
+        const DracoMat* g = get_mat((const void*)(uintptr_t)ep[3 * e], cg, inter, n_in);
+        const DracoMat* u = get_mat((const void*)(uintptr_t)ep[3 * e + 1], cu, inter, n_in);
+        const DracoMat* d = get_mat((const void*)(uintptr_t)ep[3 * e + 2], cd, n_out, inter);
+        if (!g || !u || !d) return -2;
+        const int o = (cnt[e] + 7) / 8;
+        gg[k] = {g->dev, oct0[e], o};
+        gu[k] = {u->dev, oct0[e], o};
+        gd[k] = {d->dev, oct0[e], o};
+    }
+    // device buffers (scratch slots 8..): inputs, gathered rows, digits, intermediates, tables
+    const size_t fX = (size_t)T * n_in, fXg = (size_t)R * n_in, fI = (size_t)R * inter, fY = (size_t)R * n_out,
+                 fO = (size_t)T * n_out;
+    float* dX = (float*)scratch(8, sizeof(float) * fX);
+    float* dXg = (float*)scratch(9, sizeof(float) * fXg);
+    float* dG = (float*)scratch(10, sizeof(float) * fI);
+    float* dU = (float*)scratch(11, sizeof(float) * fI);
+    float* dY = (float*)scratch(12, sizeof(float) * fY);
+    float* dO = (float*)scratch(13, sizeof(float) * fO);
+    const size_t dbytes = draco_gemm_digit_bytes(R, n_in > inter ? n_in : inter);
+    uint8_t* dD = (uint8_t*)scratch(14, dbytes);
+    const size_t tb = sizeof(int) * ((size_t)R + (size_t)T * n_used) + sizeof(float) * (size_t)T * n_used +
+                      sizeof(GemmGroup) * 3 * (size_t)na + 64;
+    char* dT = (char*)scratch(15, tb);
+    if (!dX || !dXg || !dG || !dU || !dY || !dO || !dD || !dT) return -2;
+    int* dsrc = (int*)dT;
+    int* dpos = dsrc + R;
+    float* dwt = (float*)(dpos + (size_t)T * n_used);
+    GemmGroup* dgr = (GemmGroup*)(((uintptr_t)(dwt + (size_t)T * n_used) + 15) & ~(uintptr_t)15);
+    std::vector<GemmGroup> allg;
+    allg.insert(allg.end(), gg.begin(), gg.end());
+    allg.insert(allg.end(), gu.begin(), gu.end());
+    allg.insert(allg.end(), gd.begin(), gd.end());
+    DRACO_HIP(hipMemcpyAsync(dX, X, sizeof(float) * fX, hipMemcpyHostToDevice, st));
+    DRACO_HIP(hipMemcpyAsync(dsrc, src.data(), sizeof(int) * R, hipMemcpyHostToDevice, st));
+    DRACO_HIP(hipMemcpyAsync(dpos, pos.data(), sizeof(int) * pos.size(), hipMemcpyHostToDevice, st));
+    DRACO_HIP(hipMemcpyAsync(dwt, wtop, sizeof(float) * (size_t)T * n_used, hipMemcpyHostToDevice, st));
+    DRACO_HIP(hipMemcpyAsync(dgr, allg.data(), sizeof(GemmGroup) * allg.size(), hipMemcpyHostToDevice, st));
+    if (draco_moe_gather_launch(dX, n_in, dsrc, R, dXg, st)) return fail(-1, "moe_tok gather rejected");
+    auto grouped = [&](const float* Xin, int k_in, int code, const GemmGroup* groups, int rows, float* Y) -> int {
+        DracoLayout L;
+        if (draco_layout(code, rows, k_in, &L)) return fail(-1, "moe_tok layout");
+        GemmArgs a = {};
+        if (draco_gemm_digits_launch(Xin, R, k_in, dD, a, st)) return fail(-1, "moe_tok digits rejected");
+        a.L = L;
+        a.Y = Y;
+        a.ldy = rows;
+        a.groups = groups;
+        a.n_groups = na;
+        a.max_oct = max_oct;
+        if (draco_gemm_grouped_launch(a, st)) return fail(-1, "moe_tok gemm rejected");
+        return 0;
+    };
+    if (int rc = grouped(dXg, n_in, cg, dgr, inter, dG)) return rc;
+    {
+        // the gate and up GEMMs share the digits of Xg: reuse them for up
+        DracoLayout L;
+        draco_layout(cu, inter, n_in, &L);
+        GemmArgs a = {};
+        const size_t oct = (size_t)R / 8;
+        a.xdig = reinterpret_cast<const int8_t*>(dD);
+        a.xsc = reinterpret_cast<const float*>(dD + oct * ((size_t)n_in / 32) * 1024);
+        a.xs32 = a.xsc + oct * ((size_t)n_in / 256) * 8;
+        a.xs16 = a.xs32 + oct * ((size_t)n_in / 32) * 8;
+        a.T = R;
+        a.n_in = n_in;
+        a.L = L;
+        a.Y = dU;
+        a.ldy = inter;
+        a.groups = dgr + na;
+        a.n_groups = na;
+        a.max_oct = max_oct;
+        if (draco_gemm_grouped_launch(a, st)) return fail(-1, "moe_tok up gemm rejected");
+    }
+    dk_swiglu(dG, dU, R * inter, st);
+    if (int rc = grouped(dG, inter, cd, dgr + 2 * na, n_out, dY)) return rc;
+    if (draco_moe_scatter_launch(dY, n_out, dpos, dwt, n_used, T, dO, st)) return fail(-1, "moe_tok scatter rejected");
+    DRACO_HIP(hipGetLastError());
+    DRACO_HIP(hipMemcpyAsync(out, dO, sizeof(float) * fO, hipMemcpyDeviceToHost, st));
+    DRACO_HIP(hipStreamSynchronize(st));
+    return 0;
+}
+
 }  // namespace
 
 extern "C" {
+
+typedef int (*draco_dequant_fn)(int, const uint8_t*, int, float*);
+typedef int (*draco_gemm_auto_fn)(int, const float*, const uint8_t*, int, int, int, float*);
+
+void m6_moe_tok(draco_dequant_fn DQ, draco_gemm_auto_fn GA, float* gwbuf, const float* X, const int* order,
+                const float* wtop, const uint64_t* ep, const int* ec, int T, int n_used, int inter, int n_in,
+                int n_out, int n_exp, float* out, float* work, int* iwork) {
+    (void)DQ;  // the device path uses its own kernels, not the caller's CPU callbacks
+    (void)GA;
+    (void)gwbuf;
+    (void)work;
+    (void)iwork;
+    std::lock_guard<std::recursive_mutex> g(api_mutex());
+    if (int rc = moe_tok(X, order, wtop, ep, ec, T, n_used, inter, n_in, n_out, n_exp, out))
+        fprintf(stderr, "m6_moe_tok: rc %d: %s\n", rc, last_error());
+}
+
 
 void m6_granite_moe(const float* x0, const uint64_t* ptrs, const int* codes, const float* gate_inp, int n_exp,
                     int n_used, int inter, int n_in, int n_out, float* scratch_unused, float* out) {

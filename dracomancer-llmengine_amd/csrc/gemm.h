@@ -5,6 +5,13 @@
 
 #include "formats.h"
 
+// One group of a grouped GEMM (e.g. one expert): its weights and its tokens,
+// octets [oct0, oct0 + n_oct) of the digit buffer.
+struct GemmGroup {
+    const uint8_t* W;
+    int oct0, n_oct;
+};
+
 struct GemmArgs {
     const uint8_t* W;   // weights, Q4_K / Q6_K tile layout
     DracoLayout L;
@@ -16,6 +23,10 @@ struct GemmArgs {
     const float* xs16;
     float* Y;           // Y[t * ldy + row]
     int ldy;
+    // grouped launch (nullptr: one group = W, all tokens)
+    const GemmGroup* groups;  // device array [n_groups]
+    int n_groups;
+    int max_oct;              // largest n_oct of any group
 };
 
 // device bytes of the digit buffer for T tokens of length n_in
@@ -23,3 +34,5 @@ size_t draco_gemm_digit_bytes(int T, int n_in);
 // digitize X[T][n_in] (device) into buf; fills a.xdig/xsc/xs32/xs16, a.T, a.n_in
 int draco_gemm_digits_launch(const float* X, int T, int n_in, uint8_t* buf, GemmArgs& a, hipStream_t st);
 int draco_gemm_launch(GemmArgs& a, hipStream_t st);
+// Y[t] for the tokens of every group against that group's W (same shape for all groups)
+int draco_gemm_grouped_launch(GemmArgs& a, hipStream_t st);

@@ -94,9 +94,13 @@ template <int NW, int RP>
 __global__ __launch_bounds__(64 * NW) void k_gemm_q4(const GemmArgs a) {
     const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int n = lane & 31, u = lane >> 5;
-    const int oc = blockIdx.y * NW + w;                 // token octet
-    const int n_oct = (a.T + 7) >> 3;
-    if (oc >= n_oct) return;                             // uniform per wave; no barriers below
+    // grouped launch: blockIdx.z selects the group (weights, token octets)
+    const GemmGroup* gp = a.groups ? a.groups + blockIdx.z : nullptr;
+    const uint8_t* Wb = gp ? gp->W : a.W;
+    const int oi = blockIdx.y * NW + w;
+    const int n_oct = gp ? gp->n_oct : (a.T + 7) >> 3;
+    if (oi >= n_oct) return;                             // uniform per wave; no barriers below
+    const int oc = (gp ? gp->oct0 : 0) + oi;             // token octet in the digit buffer
     const int nb = a.n_in >> 8, nc = a.n_in >> 5;
     const int p0 = blockIdx.x * RP;
     float y[RP][4];
@@ -120,7 +124,7 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_q4(const GemmArgs a) {
             const int tile = 2 * (p0 + p) + (n >> 4), j = n & 15;
             if (2 * (p0 + p) >= a.L.ntiles) break;       // uniform
             const int tl = tile < a.L.ntiles ? tile : a.L.ntiles - 1;
-            const uint8_t* item = a.W + ((size_t)tl * nb + b) * DRACO_Q4T_ITEM;
+            const uint8_t* item = Wb + ((size_t)tl * nb + b) * DRACO_Q4T_ITEM;
             uint4 q[2][2];
 #pragma unroll
             for (int r = 0; r < 2; r++)
@@ -190,9 +194,13 @@ template <int NW, int RP>
 __global__ __launch_bounds__(64 * NW) void k_gemm_q6(const GemmArgs a) {
     const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int n = lane & 31, u = lane >> 5;
-    const int oc = blockIdx.y * NW + w;
-    const int n_oct = (a.T + 7) >> 3;
-    if (oc >= n_oct) return;
+    // grouped launch: blockIdx.z selects the group (weights, token octets)
+    const GemmGroup* gp = a.groups ? a.groups + blockIdx.z : nullptr;
+    const uint8_t* Wb = gp ? gp->W : a.W;
+    const int oi = blockIdx.y * NW + w;
+    const int n_oct = gp ? gp->n_oct : (a.T + 7) >> 3;
+    if (oi >= n_oct) return;                             // uniform per wave; no barriers below
+    const int oc = (gp ? gp->oct0 : 0) + oi;             // token octet in the digit buffer
     const int nb = a.n_in >> 8, nc = a.n_in >> 5, ng = a.n_in >> 4;
     const int p0 = blockIdx.x * RP;
     // A-row role of this lane: m = lane & 31 = 16h + 4t4 + dg
@@ -211,7 +219,7 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_q6(const GemmArgs a) {
             if (2 * (p0 + p) >= a.L.ntiles) break;
             const int tile = 2 * (p0 + p) + (n >> 4), j = n & 15;
             const int tl = tile < a.L.ntiles ? tile : a.L.ntiles - 1;
-            const uint8_t* item = a.W + ((size_t)tl * nb + b) * DRACO_Q6T_ITEM;
+            const uint8_t* item = Wb + ((size_t)tl * nb + b) * DRACO_Q6T_ITEM;
             const float d = h2f(*reinterpret_cast<const uint16_t*>(item + 3328 + 2 * j));
 #pragma unroll 1
             for (int g2 = 0; g2 < 2; g2++) {
@@ -308,6 +316,18 @@ int draco_gemm_digits_launch(const float* X, int T, int n_in, uint8_t* buf, Gemm
     float* xs16 = xs32 + oct * ((size_t)n_in / 32) * 8;
     hipLaunchKernelGGL(k_gemm_digits, dim3(n_in / 256, (unsigned)(oct * 8)), dim3(64), 0, st, X, T, n_in, xdig, xsc,
                        xs32, xs16);
+    return 0;
+}
+
+int draco_gemm_grouped_launch(GemmArgs& a, hipStream_t st) {
+    constexpr int NW = 4, RP = 1;
+    const int code = a.L.code;
+    if (!a.groups || a.n_groups < 1 || a.max_oct < 1 || a.n_in != a.L.n_in) return -1;
+    const int pairs = (a.L.n_out + 31) / 32;
+    const dim3 grid((pairs + RP - 1) / RP, (a.max_oct + NW - 1) / NW, a.n_groups);
+    if (code == DRACO_Q4_K) hipLaunchKernelGGL((k_gemm_q4<NW, RP>), grid, dim3(64 * NW), 0, st, a);
+    else if (code == DRACO_Q6_K) hipLaunchKernelGGL((k_gemm_q6<NW, RP>), grid, dim3(64 * NW), 0, st, a);
+    else return -1;
     return 0;
 }
 

@@ -45,3 +45,8 @@ int draco_moe_grp_launch(MoeArgs& a, int fm, bool dual, bool xper, bool route, h
 int draco_moe_down_launch(MoeArgs& a, int fm, hipStream_t st);
 // slots per grouped launch when every slot has its own x of length n_in
 int draco_moe_xper_slots(int n_in);
+
+// token-batched MoE helpers
+int draco_moe_gather_launch(const float* X, int n_in, const int* src, int rows, float* Xg, hipStream_t st);
+int draco_moe_scatter_launch(const float* Yd, int n_out, const int* pos, const float* wt, int n_used, int T, float* out,
+                             hipStream_t st);

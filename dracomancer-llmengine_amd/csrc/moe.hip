@@ -392,6 +392,32 @@ __global__ __launch_bounds__(64 * NW) void k_moe_down(const MoeArgs a) {
     }
 }
 
+// Token-batched MoE (prefill): gather the token rows of every expert segment
+// (src[row] = token or -1 for padding), and the deterministic scatter
+// out[t] = sum_k w[t,k] * Yd[pos[t,k]] in k order (src/m6_moe_tok.c:148-159).
+__global__ __launch_bounds__(256) void k_moe_gather(const float* __restrict__ X, int n_in, const int* __restrict__ src,
+                                                    float* __restrict__ Xg) {
+    const int row = blockIdx.x, t = src[row];
+    for (int i = threadIdx.x * 4; i < n_in; i += 1024) {
+        const float4 v = t >= 0 ? ld4(X + (size_t)t * n_in + i) : make_float4(0.f, 0.f, 0.f, 0.f);
+        *reinterpret_cast<float4*>(Xg + (size_t)row * n_in + i) = v;
+    }
+}
+
+__global__ __launch_bounds__(256) void k_moe_scatter(const float* __restrict__ Yd, int n_out, const int* __restrict__ pos,
+                                                     const float* __restrict__ wt, int n_used, float* __restrict__ out) {
+    const int t = blockIdx.x;
+    for (int r = threadIdx.x; r < n_out; r += 256) {
+        float o = 0.f;
+        for (int k = 0; k < n_used; k++) {
+            const int p = pos[t * n_used + k];
+            if (p < 0) continue;
+            o += wt[t * n_used + k] * Yd[(size_t)p * n_out + r];
+        }
+        out[(size_t)t * n_out + r] = o;
+    }
+}
+
 int cu_count() {
     static int n = 0;
     static std::once_flag once;
@@ -499,5 +525,18 @@ int draco_moe_down_launch(MoeArgs& a, int fm, hipStream_t st) {
         if (fm == 1) launch_down<16, 1>(a, tiles, lds, st);
         else launch_down<16, 2>(a, tiles, lds, st);
     }
+    return 0;
+}
+
+int draco_moe_gather_launch(const float* X, int n_in, const int* src, int rows, float* Xg, hipStream_t st) {
+    if (n_in % 4 || rows < 1) return -1;
+    hipLaunchKernelGGL(k_moe_gather, dim3(rows), dim3(256), 0, st, X, n_in, src, Xg);
+    return 0;
+}
+
+int draco_moe_scatter_launch(const float* Yd, int n_out, const int* pos, const float* wt, int n_used, int T, float* out,
+                             hipStream_t st) {
+    if (T < 1) return -1;
+    hipLaunchKernelGGL(k_moe_scatter, dim3(T), dim3(256), 0, st, Yd, n_out, pos, wt, n_used, out);
     return 0;
 }

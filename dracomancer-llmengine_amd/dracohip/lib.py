@@ -66,6 +66,8 @@ SIGNATURES = {
     # MoE (src/m6_layer.c:771-802, src/m5/m5_batch8_k.c:80-183)
     "m6_granite_moe": (None, [f32p, ct.c_void_p, i32p, f32p, ct.c_int, ct.c_int, ct.c_int, ct.c_int, ct.c_int,
                               f32p, f32p]),
+    "m6_moe_tok": (None, [ct.c_void_p, ct.c_void_p, f32p, f32p, i32p, f32p, ct.c_void_p, i32p] + [ct.c_int] * 6
+                   + [f32p, f32p, i32p]),
     "m5_gemvn_q4k": (ct.c_int, [f32p, ct.c_long, u8p, i32p, ct.c_long, ct.c_int, ct.c_int, ct.c_int, f32p]),
     "m5_gemvn_q6k": (ct.c_int, [f32p, ct.c_long, u8p, i32p, ct.c_long, ct.c_int, ct.c_int, ct.c_int, f32p]),
     "draco_bench_granite_moe": (ct.c_int, [f32p, ct.c_void_p, i32p, f32p, ct.c_int, ct.c_int, ct.c_int, ct.c_int,

@@ -135,6 +135,17 @@ size_t draco_resident_bytes(void);
  * reference). */
 void m6_granite_moe(const float* x0, const uint64_t* ptrs, const int* codes, const float* gate_inp, int n_exp,
                     int n_used, int inter, int n_in, int n_out, float* scratch, float* out);
+/* m6_moe_tok: src/m6_moe_tok.c:44-161 -- token-batched MoE FFN for prefill:
+ * out[T][n_out] = sum over k (ascending) of wtop[t*n_used+k] * expert
+ * order[t*n_used+k] applied to X[t] (gate/up -> silu*up -> down).  ep/ec: 3
+ * host pointers / codes per expert.  Served: Q4_K / Q6_K experts (one format
+ * per role across experts), inter and n_in multiples of 256, n_out a
+ * multiple of 16.  DQ, GA, gwbuf, work and iwork are accepted and not used
+ * (the device path runs its own grouped GEMMs). */
+void m6_moe_tok(int (*DQ)(int, const uint8_t*, int, float*),
+                int (*GA)(int, const float*, const uint8_t*, int, int, int, float*), float* gwbuf, const float* X,
+                const int* order, const float* wtop, const uint64_t* ep, const int* ec, int T, int n_used, int inter,
+                int n_in, int n_out, int n_exp, float* out, float* work, int* iwork);
 /* m5_gemvn_q4k / m5_gemvn_q6k: src/m5/m5_batch8_k.c:80-183.  y[e * n_out_e + r]
  * = (W + idx[e] * per)[r] . (x + e * x_stride) for e < n_exp.  Returns -1 for
  * n_in % 256 != 0 (as the reference) or n_out_e % 16 != 0. */

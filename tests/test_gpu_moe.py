@@ -116,3 +116,27 @@ def test_gemvn_rejects_like_reference(hip):
     idx = np.zeros(1, np.int32)
     y = np.zeros(16, np.float32)
     assert hip.m5_gemvn_q4k(lib.pf(x), 0, lib.pu8(W), lib.pi32(idx), 0, 16, 300, 1, lib.pf(y)) == -1
+
+
+@pytest.mark.parametrize("n_exp,n_used,inter,H,T,codes3", [(16, 4, 256, 512, 20, (5, 5, 4)),
+                                                           (128, 8, 768, 2048, 48, (5, 5, 5))])
+def test_moe_tok_vs_oracle(hip, oracle, n_exp, n_used, inter, H, T, codes3):
+    from dracohip import lib
+    M = build_moe(n_exp, inter, H, H, 61 + T, codes3=codes3)
+    rng = np.random.default_rng(T)
+    X = rng.standard_normal((T, H)).astype(np.float32)
+    # routing as the caller would pass it: distinct experts per token, softmax-like weights;
+    # one invalid expert id (skipped by both) and experts with no tokens
+    order = np.stack([rng.choice(n_exp // 2, n_used, replace=False) for _ in range(T)]).astype(np.int32)
+    order[3, 1] = -1
+    wtop = rng.random((T, n_used)).astype(np.float32)
+    wtop /= wtop.sum(axis=1, keepdims=True)
+    y = np.zeros((T, H), np.float32)
+    z = np.zeros(8, np.float32)
+    zi = np.zeros(8, np.int32)
+    hip.m6_moe_tok(None, None, lib.pf(z), lib.pf(X), lib.pi32(order), lib.pf(wtop), ct.c_void_p(M["ptrs"].ctypes.data),
+                   lib.pi32(M["codes"]), T, n_used, inter, H, H, n_exp, lib.pf(y), lib.pf(z), lib.pi32(zi))
+    ref = np.zeros_like(y)
+    oracle.lib.or_moe_tok(lib.pf(X), lib.pi32(order), lib.pf(wtop), ct.c_void_p(M["ptrs"].ctypes.data),
+                          lib.pi32(M["codes"]), T, n_used, inter, H, H, n_exp, lib.pf(ref))
+    assert rel_err(y, ref) <= TOL
