@@ -18,8 +18,13 @@ void dk_rmsnorm(const float* x, const float* w, float* out, int h, float eps, hi
 void dk_rope_append(float* q, const float* k, const float* v, float* kc, float* vc, const float* tab,
                     const int* state, int layer, int NH, int NKV, int HD, int rot, hipStream_t st);
 // split-T partials + merge; `count` is unused (kept for the caller's buffer plumbing)
+// HD in {64, 128, 256}; NH / NKV <= 16.  gate (nullable): out[h][d] *= sigmoid(gate[h * gstride + d]).
 int dk_attention(const float* q, const float* kc, const float* vc, float* part, unsigned* count, float* out,
-                 const int* state, int layer, int NH, int NKV, int HD, int max_t, float scale, hipStream_t st);
+                 const int* state, int layer, int NH, int NKV, int HD, int max_t, float scale, hipStream_t st,
+                 const float* gate = nullptr, int gstride = 0);
+// qwen35 full attention q/k head RMSNorm + rope (NH q heads, 2 k heads of 256).
+void dk_fa_prep(const float* QG, float* Qr, const float* kin, float* kout, const float* qn, const float* kn,
+                const float* cs, int NH, hipStream_t st);
 void dk_swiglu(float* g, const float* u, int n, hipStream_t st);
 // out[n_in] = dequantized row ids[cursor ? *cursor : 0] of m
 void dk_embed(const DracoMat& m, const int* ids, const int* cursor, float* out, hipStream_t st);

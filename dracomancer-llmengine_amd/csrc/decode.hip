@@ -168,9 +168,12 @@ __global__ __launch_bounds__(1024) void k_attn_part(const float* __restrict__ q,
 // of each wave holds split k's (m, l); the weights exp(m_k - M) are
 // broadcast with readlane, and all of a lane's partial loads are issued
 // before the first FMA, so the kernel costs two dependent L2 round trips.
+// With `gate` set the result is multiplied by sigmoid(gate[h * gstride + d])
+// (qwen35 full attention, src/m6_layer.c:500-505).
 template <int MAXS>
-__global__ __launch_bounds__(128) void k_attn_combine(const float* __restrict__ part, float* __restrict__ out,
-                                                      int nsplit, int HD) {
+__global__ __launch_bounds__(256) void k_attn_combine(const float* __restrict__ part, float* __restrict__ out,
+                                                      int nsplit, int HD, const float* __restrict__ gate,
+                                                      int gstride) {
     const int h = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
     const float* ph = part + (size_t)h * nsplit * (HD + 2);
     const float m = lane < nsplit ? ph[lane * (HD + 2) + HD] : -INFINITY;
@@ -186,7 +189,40 @@ __global__ __launch_bounds__(128) void k_attn_combine(const float* __restrict__ 
     for (int k = 0; k < MAXS; k++) {  // lanes k >= nsplit carry weight 0
         acc = fmaf(pv[k], __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wk), k)), acc);
     }
-    if (tid < HD) out[(size_t)h * HD + tid] = acc * (1.f / L);
+    if (tid < HD) {
+        float r = acc * (1.f / L);
+        if (gate) r *= 1.f / (1.f + expf(-gate[(size_t)h * gstride + tid]));
+        out[(size_t)h * HD + tid] = r;
+    }
+}
+
+// qwen35 full attention, per-head RMSNorm over 256 dims and rope on the pairs
+// (t, t + 32), t < 32 (src/m6_layer.c:427-457).  Blocks 0..NH-1 normalise q
+// head b from QG[b * 512 .. + 256] into Qr[b * 256] as (x * r) * q_norm; blocks
+// NH, NH + 1 normalise k head kv from kin[kv * 256] into kout[kv * 256] as
+// x * (r * k_norm), the two association orders of the reference.  cs holds
+// [32][cos, sin] of pos0 * rope_inv[t].  Rope partners t and t + 32 are lanes
+// of wave 0 and swap values with one shuffle.
+__global__ __launch_bounds__(256) void k_fa_prep(const float* __restrict__ QG, float* __restrict__ Qr,
+                                                 const float* __restrict__ kin, float* __restrict__ kout,
+                                                 const float* __restrict__ qn, const float* __restrict__ kn,
+                                                 const float* __restrict__ cs, int NH) {
+    __shared__ float red[4];
+    const int b = blockIdx.x, t = threadIdx.x, lane = t & 63, w = t >> 6;
+    const bool isq = b < NH;
+    const float x = isq ? QG[(size_t)b * 512 + t] : kin[(b - NH) * 256 + t];
+    const float s = wave_sum(x * x);
+    if (lane == 0) red[w] = s;
+    __syncthreads();
+    const float n2 = (red[0] + red[1]) + (red[2] + red[3]);
+    const float r = 1.f / sqrtf(n2 / 256.f + 1e-6f);
+    float y = isq ? x * r * qn[t] : x * (r * kn[t]);
+    if (w == 0) {
+        const float o = __shfl_xor(y, 32, 64);
+        const float c = cs[2 * (lane & 31)], sn = cs[2 * (lane & 31) + 1];
+        y = lane < 32 ? y * c - o * sn : o * sn + y * c;
+    }
+    (isq ? Qr + (size_t)b * 256 : kout + (b - NH) * 256)[t] = y;
 }
 
 // -------------------------------------------------------------- SwiGLU --
@@ -321,7 +357,8 @@ void dk_rope_append(float* q, const float* k, const float* v, float* kc, float* 
 }
 
 int dk_attention(const float* q, const float* kc, const float* vc, float* part, unsigned* count, float* out,
-                 const int* state, int layer, int NH, int NKV, int HD, int max_t, float scale, hipStream_t st) {
+                 const int* state, int layer, int NH, int NKV, int HD, int max_t, float scale, hipStream_t st,
+                 const float* gate, int gstride) {
     (void)count;
     const int rep = NH / NKV;
     if (rep < 1 || rep > REPMAX || NH % NKV) return -1;
@@ -332,13 +369,21 @@ int dk_attention(const float* q, const float* kc, const float* vc, float* part, 
     else if (HD == 128)
         hipLaunchKernelGGL(k_attn_part<128>, grid, block, 0, st, q, kc, vc, part, state, layer, NH, NKV, nsplit,
                            scale);
+    else if (HD == 256)
+        hipLaunchKernelGGL(k_attn_part<256>, grid, block, 0, st, q, kc, vc, part, state, layer, NH, NKV, nsplit,
+                           scale);
     else
         return -1;
-    const dim3 cg(NH), cb(HD < 128 ? HD : 128);
-    if (nsplit <= 16) hipLaunchKernelGGL(k_attn_combine<16>, cg, cb, 0, st, part, out, nsplit, HD);
-    else if (nsplit <= 32) hipLaunchKernelGGL(k_attn_combine<32>, cg, cb, 0, st, part, out, nsplit, HD);
-    else hipLaunchKernelGGL(k_attn_combine<64>, cg, cb, 0, st, part, out, nsplit, HD);
+    const dim3 cg(NH), cb(HD);
+    if (nsplit <= 16) hipLaunchKernelGGL(k_attn_combine<16>, cg, cb, 0, st, part, out, nsplit, HD, gate, gstride);
+    else if (nsplit <= 32) hipLaunchKernelGGL(k_attn_combine<32>, cg, cb, 0, st, part, out, nsplit, HD, gate, gstride);
+    else hipLaunchKernelGGL(k_attn_combine<64>, cg, cb, 0, st, part, out, nsplit, HD, gate, gstride);
     return 0;
+}
+
+void dk_fa_prep(const float* QG, float* Qr, const float* kin, float* kout, const float* qn, const float* kn,
+                const float* cs, int NH, hipStream_t st) {
+    hipLaunchKernelGGL(k_fa_prep, dim3(NH + 2), dim3(256), 0, st, QG, Qr, kin, kout, qn, kn, cs, NH);
 }
 
 void dk_swiglu(float* g, const float* u, int n, hipStream_t st) {

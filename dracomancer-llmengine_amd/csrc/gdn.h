@@ -13,6 +13,18 @@ struct GdnArgs {
     float* S;               // [n_vh][128 k][128 v], updated
     float* ON;              // [T][n_vh*128]
     int T, n_qkv, n_vh, nhq;
+    // decode step only (draco_gdn_step_launch): B and G are computed in the
+    // kernel from the layer input, src/m6_layer.c:237-256
+    const float* h1;         // [H] layer input (before the attention RMSNorm)
+    const float* attn_norm;  // [H]
+    const float* bw;         // [n_vh][H] beta projection (the reference's [H][n_vh], transposed)
+    const float* aw;         // [n_vh][H] alpha projection
+    const float* ssm_a;      // [n_vh]
+    const float* ssm_dt;     // [n_vh]
+    int H;                   // <= 4096, multiple of 4
 };
 
 int draco_gdn_scan_launch(const GdnArgs& a, hipStream_t st);
+// One decode token (T must be 1): the scan step with beta = sigmoid(xn.bw),
+// decay = exp(softplus(xn.aw + dt) * a), xn = rms(h1) * attn_norm (eps 1e-6).
+int draco_gdn_step_launch(const GdnArgs& a, hipStream_t st);

@@ -33,6 +33,64 @@ constexpr float EPS = 1e-6f;
 
 __device__ __forceinline__ float silu(float a) { return a / (1.f + expf(-a)); }
 
+// Decode-step gates of V head h (src/m6_layer.c:237-256): every thread
+// returns beta and the decay exp(alpha).  xn = h1 * rms^-1 * attn_norm is
+// recomputed by each block (H floats, L2-resident after the first block);
+// the beta / alpha rows are contiguous [n_vh][H], read once per block.
+__device__ __forceinline__ void gdn_gates(const GdnArgs& a, int h, int tid, float* beta, float* gdec) {
+    __shared__ float pre[3][8];
+    const int lane = tid & 63, w = tid >> 6;
+    float4 hv[2], nv[2], bv[2], av[2];
+#pragma unroll
+    for (int k = 0; k < 2; k++) {  // clamped, unconditional loads; masked below
+        const int i = 4 * tid + 2048 * k;
+        const int ic = i < a.H ? i : 0;
+        hv[k] = ld4(a.h1 + ic);
+        nv[k] = ld4(a.attn_norm + ic);
+        bv[k] = ld4(a.bw + (size_t)h * a.H + ic);
+        av[k] = ld4(a.aw + (size_t)h * a.H + ic);
+    }
+    float ss = 0.f;
+#pragma unroll
+    for (int k = 0; k < 2; k++)
+        if (4 * tid + 2048 * k < a.H) ss += hv[k].x * hv[k].x + hv[k].y * hv[k].y + hv[k].z * hv[k].z + hv[k].w * hv[k].w;
+    ss = wave_sum(ss);
+    if (lane == 0) pre[0][w] = ss;
+    lds_barrier();
+    float tot = 0.f;
+#pragma unroll
+    for (int q = 0; q < 8; q++) tot += pre[0][q];
+    const float inv = 1.f / sqrtf(tot / (float)a.H + EPS);
+    float pb = 0.f, pa = 0.f;
+#pragma unroll
+    for (int k = 0; k < 2; k++) {
+        if (4 * tid + 2048 * k < a.H) {
+            const float x0 = hv[k].x * inv * nv[k].x, x1 = hv[k].y * inv * nv[k].y;
+            const float x2 = hv[k].z * inv * nv[k].z, x3 = hv[k].w * inv * nv[k].w;
+            pb += bv[k].x * x0 + bv[k].y * x1 + bv[k].z * x2 + bv[k].w * x3;
+            pa += av[k].x * x0 + av[k].y * x1 + av[k].z * x2 + av[k].w * x3;
+        }
+    }
+    pb = wave_sum(pb);
+    pa = wave_sum(pa);
+    if (lane == 0) {
+        pre[1][w] = pb;
+        pre[2][w] = pa;
+    }
+    lds_barrier();
+    float bacc = 0.f, aacc = 0.f;
+#pragma unroll
+    for (int q = 0; q < 8; q++) {
+        bacc += pre[1][q];
+        aacc += pre[2][q];
+    }
+    *beta = 1.f / (1.f + expf(-bacc));
+    const float avv = aacc + a.ssm_dt[h];
+    const float sp = avv > 0.f ? avv + log1pf(expf(-avv)) : log1pf(expf(avv));
+    *gdec = expf(sp * a.ssm_a[h]);
+}
+
+template <bool DEC>
 __global__ __launch_bounds__(512) void k_gdn_scan(const GdnArgs a) {
     __shared__ float cq[SV], ck[SV], cv[SV];   // conv outputs of this token (q, k normalised in place)
     __shared__ float red[2][8];
@@ -66,10 +124,16 @@ __global__ __launch_bounds__(512) void k_gdn_scan(const GdnArgs a) {
     // per-token inputs, prefetched one token ahead
     float xin = ch >= 0 && T > 0 ? a.QKV[ch] : 0.f;
     float zin = T > 0 ? a.Z[(size_t)h * SV + v] : 0.f;
-    float gin = T > 0 ? a.G[h] : 0.f, bin = T > 0 ? a.B[h] : 0.f;
+    float gin = 0.f, bin = 0.f;
+    if constexpr (DEC) {
+        gdn_gates(a, h, tid, &bin, &gin);
+    } else {
+        gin = T > 0 ? a.G[h] : 0.f;
+        bin = T > 0 ? a.B[h] : 0.f;
+    }
     for (int t = 0; t < T; t++) {
         const float x = xin, z = zin, g = gin, b = bin;
-        if (t + 1 < T) {
+        if (!DEC && t + 1 < T) {
             xin = ch >= 0 ? a.QKV[(size_t)(t + 1) * n_qkv + ch] : 0.f;
             zin = a.Z[(size_t)(t + 1) * n_vh * SV + (size_t)h * SV + v];
             gin = a.G[(size_t)(t + 1) * n_vh + h];
@@ -144,6 +208,14 @@ __global__ __launch_bounds__(512) void k_gdn_scan(const GdnArgs a) {
 int draco_gdn_scan_launch(const GdnArgs& a, hipStream_t st) {
     if (a.n_vh < 1 || a.nhq < 1 || a.n_qkv != a.n_vh * SV + 2 * a.nhq * SV || a.T < 0) return -1;
     if (a.T == 0) return 0;
-    hipLaunchKernelGGL(k_gdn_scan, dim3(a.n_vh), dim3(512), 0, st, a);
+    hipLaunchKernelGGL(k_gdn_scan<false>, dim3(a.n_vh), dim3(512), 0, st, a);
+    return 0;
+}
+
+int draco_gdn_step_launch(const GdnArgs& a, hipStream_t st) {
+    if (a.n_vh < 1 || a.nhq < 1 || a.n_qkv != a.n_vh * SV + 2 * a.nhq * SV || a.T != 1) return -1;
+    if (a.H < 4 || a.H > 4096 || a.H % 4 || !a.h1 || !a.attn_norm || !a.bw || !a.aw || !a.ssm_a || !a.ssm_dt)
+        return -1;
+    hipLaunchKernelGGL(k_gdn_scan<true>, dim3(a.n_vh), dim3(512), 0, st, a);
     return 0;
 }

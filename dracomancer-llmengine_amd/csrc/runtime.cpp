@@ -26,12 +26,20 @@ struct Mirror {
     size_t bytes = 0;
 };
 
+struct VecEntry {
+    float* dev = nullptr;
+    size_t n = 0;
+    int tcols = 0;
+    uint64_t fp = 0;
+};
+
 struct State {
     bool inited = false;
     int device = 0;
     hipStream_t st = nullptr;
     std::unordered_map<const void*, MatEntry> mats;
     std::unordered_map<const void*, Mirror> mirrors;
+    std::unordered_map<const void*, VecEntry> vecs;
     std::vector<std::pair<void*, size_t>> scr;
     std::vector<std::pair<void*, size_t>> pin;
     size_t resident = 0;
@@ -153,11 +161,66 @@ const DracoMat* get_mat(const void* host, int code, int n_out, int n_in) {
     return &slot.m;
 }
 
+const float* get_vec(const float* host, size_t n, int tcols) {
+    State& s = S();
+    if (ensure_init()) return nullptr;
+    if (!host || n == 0 || (tcols > 0 && n % (size_t)tcols)) {
+        fail(-1, "get_vec: bad vector (n %zu, tcols %d)", n, tcols);
+        return nullptr;
+    }
+    const uint64_t fp = fingerprint(host, n * sizeof(float));
+    auto it = s.vecs.find(host);
+    if (it != s.vecs.end()) {
+        VecEntry& e = it->second;
+        if (e.n == n && e.tcols == tcols && e.fp == fp) return e.dev;
+        hipStreamSynchronize(s.st);
+        hipFree(e.dev);
+        s.resident -= e.n * sizeof(float);
+        s.vecs.erase(it);
+        s.epoch++;
+    }
+    VecEntry e;
+    e.n = n;
+    e.tcols = tcols;
+    e.fp = fp;
+    hipError_t he = hipMalloc(&e.dev, n * sizeof(float));
+    if (he != hipSuccess) {
+        fail(-2, "hipMalloc(%zu) for a vector failed: %s", n * sizeof(float), hipGetErrorString(he));
+        return nullptr;
+    }
+    float* stage = (float*)pinned(0, n * sizeof(float));
+    if (!stage) return nullptr;
+    if (tcols > 0) {  // host [rows][tcols] -> device [tcols][rows]
+        const size_t rows = n / (size_t)tcols;
+        for (size_t r = 0; r < rows; r++)
+            for (int c = 0; c < tcols; c++) stage[(size_t)c * rows + r] = host[r * tcols + c];
+    } else {
+        memcpy(stage, host, n * sizeof(float));
+    }
+    he = hipMemcpyAsync(e.dev, stage, n * sizeof(float), hipMemcpyHostToDevice, s.st);
+    if (he == hipSuccess) he = hipStreamSynchronize(s.st);
+    if (he != hipSuccess) {
+        hipFree(e.dev);
+        fail(-2, "vector upload failed: %s", hipGetErrorString(he));
+        return nullptr;
+    }
+    s.resident += n * sizeof(float);
+    s.vecs[host] = e;
+    return e.dev;
+}
+
 int forget(const void* host) {
     State& s = S();
     int n = 0;
     s.epoch++;
     if (s.st) hipStreamSynchronize(s.st);
+    auto vt = s.vecs.find(host);
+    if (vt != s.vecs.end()) {
+        hipFree(vt->second.dev);
+        s.resident -= vt->second.n * sizeof(float);
+        s.vecs.erase(vt);
+        n++;
+    }
     auto it = s.mats.find(host);
     if (it != s.mats.end()) {
         hipFree(it->second.m.dev);
@@ -182,6 +245,8 @@ void forget_all() {
     s.mats.clear();
     for (auto& kv : s.mirrors) hipFree(kv.second.dev);
     s.mirrors.clear();
+    for (auto& kv : s.vecs) hipFree(kv.second.dev);
+    s.vecs.clear();
     s.resident = 0;
 }
 

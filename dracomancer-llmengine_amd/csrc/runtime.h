@@ -44,6 +44,10 @@ uint64_t epoch();
 // assumed immutable while registered (draco_forget drops an entry).
 const DracoMat* get_mat(const void* host, int code, int n_out, int n_in);
 int forget(const void* host);
+// Device copy of a caller-owned fp32 array of n floats (norm weights, conv
+// taps, ...), registered like a weight.  tcols > 0: the host array is
+// [n / tcols][tcols] and the device copy is its transpose [tcols][n / tcols].
+const float* get_vec(const float* host, size_t n, int tcols = 0);
 void forget_all();
 size_t resident_bytes();
 

@@ -186,6 +186,59 @@ int draco_bench_gdn_scan(const float* QKV, const float* Z, const float* B, const
                          const float* ssm_norm, const float* tail, const float* S, int T, int n_qkv, int n_vh,
                          int chunk, int n_dec, float* out);
 
+/* ---- qwen35 hybrid layers (decode, one token) ----------------------------
+ * Descriptors field for field src/m6_layer.c:189-202 (GdnW) and :375-387
+ * (FullW); ctypes twins src/qwen35_engine.py:137-157.  Hidden width 2048,
+ * 16 GDN q/k heads, head dims 128 (GDN) / 256 (full attention) and 2 KV heads
+ * are fixed, as in the reference.  Host pointers; the caller's state arrays
+ * (ssm, tail) are updated in place and Kr / Vc are read, as there.  Served
+ * projection formats: Q4_K, Q6_K, Q8_0 (fused launches) and F16 / F32.
+ * `buf` and `scores` are the reference's host scratch and are not used.
+ * Errors are printed (void, as the reference). */
+typedef struct {
+    const float* attn_norm;
+    const uint8_t* qkv_buf; int qkv_code;
+    const uint8_t* gate_buf; int gate_code;
+    const float* beta_wt;   /* [2048][n_vh] */
+    const float* alpha_wt;  /* [2048][n_vh] */
+    const float* ssm_a;
+    const float* ssm_dt;
+    const float* conv;      /* [n_qkv][4] */
+    const float* ssm_norm;  /* [128] */
+    const uint8_t* ssm_out_buf; int ssm_out_code;
+    const float* post_norm;
+    int n_qkv; int n_vh; int d_in;
+} GdnW;
+
+typedef struct {
+    const float* attn_norm;
+    const uint8_t* q_buf; int q_code;   /* nh*512 rows: per head q[256] | gate[256] */
+    const uint8_t* k_buf; int k_code;   /* 512 rows */
+    const uint8_t* v_buf; int v_code;   /* 512 rows */
+    const float* q_norm;                /* [256] */
+    const float* k_norm;                /* [256] */
+    const uint8_t* o_buf; int o_code;   /* 2048 rows, nh*256 wide */
+    const float* post_norm;
+    const float* rope_inv;              /* [32] */
+    int nh;                             /* even, <= 32 */
+} FullW;
+
+/* m6_gdn_attn: src/m6_layer.c:205-364.  h1[2048] -> x2n, x2_out; ssm
+ * [n_vh][128][128] and tail [n_qkv][3] updated in place. */
+void m6_gdn_attn(const float* h1, const GdnW* w, float* ssm, float* tail, float* buf, float* x2n,
+                 float* x2_out);
+/* m6_full_attn: src/m6_layer.c:389-518.  Kr / Vc: Told cached rows of
+ * [2][256]; kr_new / v_new receive the new row (k normed + roped). */
+void m6_full_attn(const float* h1, const FullW* w, const float* Kr, const float* Vc, int Told, int pos0,
+                  float* buf, float* scores, float* x2n, float* x2_out, float* kr_new, float* v_new);
+/* No reference counterpart: device-resident timing of one op (kind 0 GDN with
+ * w a GdnW*, state from ssm_or_kr / tail_or_vc; kind 1 full attention with w a
+ * FullW*, told cached rows from ssm_or_kr / tail_or_vc).  Host arrays are not
+ * modified.  out[0] us per op (graph replay of `iters` ops), out[1] weight
+ * bytes per op, out[2] algorithmic HBM bytes per op. */
+int draco_bench_qwen_op(int kind, const void* w, const float* h1, const float* ssm_or_kr, const float* tail_or_vc,
+                        int told, int iters, float* out);
+
 /* ---- Q8_K activations and the Q4_K / Q6_K x Q8_K GEMV --------------------
  * No reference counterpart: the reference has no Q8_K path (nearest analogue:
  * the Q8_0 x Q8_0 int8 dot of tests/i8dot_bench.c:63-183).  Block format

@@ -592,6 +592,205 @@ void or_gdn_scan(const float* QKV, const float* Z, const float* B, const float* 
 }
 
 /* ------------------------------------------------------------------ */
+/* a23  GDN decode op (qwen35 linear-attention layer, one token)       */
+/*      src/m6_layer.c:189-364.  Hidden width 2048 and 16 q/k heads    */
+/*      are fixed, as in the reference (src/m6_layer.c:11-13).         */
+/*      Struct layout = the reference's GdnW (src/m6_layer.c:189-202,  */
+/*      ctypes twin src/qwen35_engine.py:137-146).                     */
+/* ------------------------------------------------------------------ */
+#define QW_H 2048
+#define QW_NKH 16
+
+typedef struct {
+    const float* attn_norm;
+    const uint8_t* qkv_buf; int qkv_code;
+    const uint8_t* gate_buf; int gate_code;
+    const float* beta_wt;   /* [2048][n_vh] */
+    const float* alpha_wt;
+    const float* ssm_a;
+    const float* ssm_dt;
+    const float* conv;      /* [n_qkv][4] */
+    const float* ssm_norm;  /* [128] */
+    const uint8_t* ssm_out_buf; int ssm_out_code;
+    const float* post_norm;
+    int n_qkv; int n_vh; int d_in;
+} OrGdnW;
+
+/* x2_out = h1 + ssm_out(gated rms(delta rule(l2norm(conv(qkv(rms(h1))))))),
+ * x2n = rms(x2_out) * post_norm; ssm [n_vh][128][128] and tail [n_qkv][3]
+ * updated in place.  The reference sums the post-norm square in per-thread
+ * partials (src/m6_layer.c:343-361); this restatement sums sequentially, so
+ * x2n agrees to fp32 rounding, every other output bit for bit. */
+int or_gdn_attn(const float* h1, const OrGdnW* w, float* ssm, float* tail,
+                float* x2n, float* x2_out) {
+    const int NQKV = w->n_qkv, NVH = w->n_vh, DIN = w->d_in;
+    if (NVH < 1 || NVH > 64 || NQKV != 2 * QW_NKH * GDN_SV + NVH * GDN_SV || DIN != NVH * GDN_SV) return -1;
+    float* xn = (float*)malloc(sizeof(float) * (QW_H + 2 * (size_t)NQKV + 2 * (size_t)NVH * GDN_SV + QW_H));
+    float* qkv = xn + QW_H;
+    float* cout = qkv + NQKV;
+    float* z = cout + NQKV;
+    float* on = z + NVH * GDN_SV;
+    float* attn = on + NVH * GDN_SV;
+    float ms = 0.f;
+    for (int i = 0; i < QW_H; i++) ms += h1[i] * h1[i];
+    float inv = 1.f / sqrtf(ms / (float)QW_H + GDN_EPS);
+    for (int i = 0; i < QW_H; i++) xn[i] = h1[i] * inv * w->attn_norm[i];
+    or_gemv(w->qkv_code, xn, w->qkv_buf, NQKV, QW_H, qkv);
+    or_gemv(w->gate_code, xn, w->gate_buf, NVH * GDN_SV, QW_H, z);
+    /* beta = sigmoid(x.Wb), alpha = softplus(x.Wa + dt) * a  (:240-256) */
+    float beta[64], gdec[64], bacc[64], aacc[64];
+    for (int i = 0; i < NVH; i++) bacc[i] = aacc[i] = 0.f;
+    for (int t = 0; t < QW_H; t++) {
+        const float xt = xn[t];
+        for (int i = 0; i < NVH; i++) {
+            bacc[i] += w->beta_wt[(size_t)t * NVH + i] * xt;
+            aacc[i] += w->alpha_wt[(size_t)t * NVH + i] * xt;
+        }
+    }
+    for (int i = 0; i < NVH; i++) {
+        beta[i] = 1.f / (1.f + expf(-bacc[i]));
+        const float av = aacc[i] + w->ssm_dt[i];
+        const float sp = av > 0 ? av + log1pf(expf(-av)) : log1pf(expf(av));
+        gdec[i] = expf(sp * w->ssm_a[i]);
+    }
+    gdn_conv(qkv, w->conv, tail, cout, NQKV);                      /* :262-270 */
+    for (int j = 0; j < 2 * QW_NKH; j++) {                          /* :274-280 */
+        float* hv = cout + j * GDN_SV;
+        float n2 = 0.f;
+        for (int u = 0; u < GDN_SV; u++) n2 += hv[u] * hv[u];
+        const float r = 1.f / fmaxf(sqrtf(n2), GDN_EPS);
+        for (int u = 0; u < GDN_SV; u++) hv[u] *= r;
+    }
+    const float scale = 1.f / sqrtf((float)GDN_SV);
+    for (int h = 0; h < NVH; h++) {                                 /* :283-331 */
+        const int j = h % QW_NKH;
+        float oh[GDN_SV];
+        gdn_head_step(ssm + (size_t)h * GDN_SV * GDN_SV, cout + QW_NKH * GDN_SV + j * GDN_SV,
+                      cout + j * GDN_SV, cout + 2 * QW_NKH * GDN_SV + h * GDN_SV, gdec[h], beta[h], oh);
+        float ms2 = 0.f;
+        for (int vv = 0; vv < GDN_SV; vv++) { oh[vv] = oh[vv] * scale; ms2 += oh[vv] * oh[vv]; }
+        const float inv2 = 1.f / sqrtf(ms2 / GDN_SV + GDN_EPS);
+        for (int vv = 0; vv < GDN_SV; vv++) {
+            const float zv = z[h * GDN_SV + vv];
+            on[h * GDN_SV + vv] = oh[vv] * inv2 * w->ssm_norm[vv] * (zv / (1.f + expf(-zv)));
+        }
+    }
+    or_gemv(w->ssm_out_code, on, w->ssm_out_buf, QW_H, DIN, attn);  /* :332-340 */
+    ms = 0.f;
+    for (int i = 0; i < QW_H; i++) { x2_out[i] = h1[i] + attn[i]; ms += x2_out[i] * x2_out[i]; }
+    inv = 1.f / sqrtf(ms / (float)QW_H + GDN_EPS);
+    for (int i = 0; i < QW_H; i++) x2n[i] = x2_out[i] * inv * w->post_norm[i];
+    free(xn);
+    return 0;
+}
+
+/* ------------------------------------------------------------------ */
+/* a25  qwen35 full attention (one token)  src/m6_layer.c:375-518.     */
+/*      Head dim 256, 2 KV heads, rope on pairs (t, t+32), t < 32.     */
+/*      Struct layout = the reference's FullW (src/m6_layer.c:375-387, */
+/*      ctypes twin src/qwen35_engine.py:149-157).                     */
+/* ------------------------------------------------------------------ */
+typedef struct {
+    const float* attn_norm;
+    const uint8_t* q_buf; int q_code;   /* nh*512 rows: per head q[256] | gate[256] */
+    const uint8_t* k_buf; int k_code;   /* 512 rows */
+    const uint8_t* v_buf; int v_code;   /* 512 rows */
+    const float* q_norm;                /* [256] */
+    const float* k_norm;
+    const uint8_t* o_buf; int o_code;   /* 2048 rows, nh*256 wide */
+    const float* post_norm;
+    const float* rope_inv;              /* [32] */
+    int nh;
+} OrFullW;
+
+/* Kr/Vc: Told cached rows of [2][256]; the new row is computed here and
+ * returned in kr_new (normed + roped) / v_new.  Every output is bitwise the
+ * reference's on the same inputs (sequential sums throughout there too). */
+int or_full_attn(const float* h1, const OrFullW* w, const float* Kr, const float* Vc, int Told,
+                 int pos0, float* x2n, float* x2_out, float* kr_new, float* v_new) {
+    const int HD = 256, NKV = 2, HALF = 32, NH = w->nh;
+    if (NH < NKV || NH % NKV || NH > 64 || Told < 0) return -1;
+    const int NQG = NH * 2 * HD, T = Told + 1;
+    float* xn = (float*)malloc(sizeof(float) * ((size_t)QW_H * 2 + NQG + 2 * (size_t)NH * HD + T));
+    float* QG = xn + QW_H;
+    float* Qr = QG + NQG;
+    float* ao = Qr + NH * HD;
+    float* attn = ao + NH * HD;
+    float* sc = attn + QW_H;
+    float ms = 0.f;
+    for (int i = 0; i < QW_H; i++) ms += h1[i] * h1[i];
+    float inv = 1.f / sqrtf(ms / (float)QW_H + GDN_EPS);
+    for (int i = 0; i < QW_H; i++) xn[i] = h1[i] * inv * w->attn_norm[i];
+    or_gemv(w->q_code, xn, w->q_buf, NQG, QW_H, QG);
+    or_gemv(w->k_code, xn, w->k_buf, NKV * HD, QW_H, kr_new);
+    or_gemv(w->v_code, xn, w->v_buf, NKV * HD, QW_H, v_new);
+    for (int kv = 0; kv < NKV; kv++) {                    /* :427-441 k: x *= (r * w) */
+        float* kh = kr_new + kv * HD;
+        float n2 = 0.f;
+        for (int t = 0; t < HD; t++) n2 += kh[t] * kh[t];
+        n2 = 1.f / sqrtf(n2 / HD + GDN_EPS);
+        for (int t = 0; t < HD; t++) kh[t] *= n2 * w->k_norm[t];
+        for (int t = 0; t < HALF; t++) {
+            const float ang = (float)pos0 * w->rope_inv[t];
+            const float c = cosf(ang), s = sinf(ang);
+            const float a = kh[t], b = kh[t + HALF];
+            kh[t] = a * c - b * s;
+            kh[t + HALF] = a * s + b * c;
+        }
+    }
+    for (int h = 0; h < NH; h++) {                        /* :443-457 q: (x * r) * w */
+        const float* qh = QG + h * 2 * HD;
+        float* qo = Qr + h * HD;
+        float n2 = 0.f;
+        for (int t = 0; t < HD; t++) n2 += qh[t] * qh[t];
+        n2 = 1.f / sqrtf(n2 / HD + GDN_EPS);
+        for (int t = 0; t < HD; t++) qo[t] = qh[t] * n2 * w->q_norm[t];
+        for (int t = 0; t < HALF; t++) {
+            const float ang = (float)pos0 * w->rope_inv[t];
+            const float c = cosf(ang), s = sinf(ang);
+            const float a = qo[t], b = qo[t + HALF];
+            qo[t] = a * c - b * s;
+            qo[t + HALF] = a * s + b * c;
+        }
+    }
+    const float scale = 1.f / sqrtf((float)HD);
+    for (int h = 0; h < NH; h++) {                        /* :459-499 */
+        const int kv = h / (NH / NKV);
+        const float* qh = Qr + h * HD;
+        for (int t = 0; t < T; t++) {
+            const float* krow = t < Told ? Kr + (size_t)t * NKV * HD + kv * HD : kr_new + kv * HD;
+            float acc = 0.f;
+            for (int d = 0; d < HD; d++) acc += qh[d] * krow[d];
+            sc[t] = acc * scale;
+        }
+        float mx = sc[0];
+        for (int t = 1; t < T; t++) if (sc[t] > mx) mx = sc[t];
+        float sum = 0.f;
+        for (int t = 0; t < T; t++) { sc[t] = expf(sc[t] - mx); sum += sc[t]; }
+        const float rsum = 1.f / sum;
+        float* oh = ao + h * HD;
+        for (int d = 0; d < HD; d++) oh[d] = 0.f;
+        for (int t = 0; t < T; t++) {
+            const float p = sc[t] * rsum;
+            const float* vrow = t < Told ? Vc + (size_t)t * NKV * HD + kv * HD : v_new + kv * HD;
+            for (int d = 0; d < HD; d++) oh[d] += p * vrow[d];
+        }
+    }
+    for (int h = 0; h < NH; h++) {                        /* :500-505 sigmoid gate */
+        float* oh = ao + h * HD;
+        const float* gh = QG + h * 2 * HD + HD;
+        for (int d = 0; d < HD; d++) oh[d] *= 1.f / (1.f + expf(-gh[d]));
+    }
+    or_gemv(w->o_code, ao, w->o_buf, QW_H, NH * HD, attn);
+    ms = 0.f;
+    for (int i = 0; i < QW_H; i++) { x2_out[i] = h1[i] + attn[i]; ms += x2_out[i] * x2_out[i]; }
+    inv = 1.f / sqrtf(ms / (float)QW_H + GDN_EPS);
+    for (int i = 0; i < QW_H; i++) x2n[i] = x2_out[i] * inv * w->post_norm[i];
+    free(xn);
+    return 0;
+}
+
+/* ------------------------------------------------------------------ */
 /* a22  token-batched MoE  src/m6_moe_tok.c:44-161, restated with the  */
 /* per-token expert FFN of the decode path.  Pinned by the invariant   */
 /* "token-batched == token-serial" (the reference's own gate,          */

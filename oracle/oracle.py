@@ -53,6 +53,8 @@ _SIGS = {
                            ct.c_int, f32p, f32p]),
     "or_moe_tok": (None, [f32p, i32p, f32p, ct.c_void_p, i32p, ct.c_int, ct.c_int, ct.c_int,
                           ct.c_int, ct.c_int, ct.c_int, f32p]),
+    "or_gdn_attn": (ct.c_int, [f32p, ct.c_void_p, f32p, f32p, f32p, f32p]),
+    "or_full_attn": (ct.c_int, [f32p, ct.c_void_p, f32p, f32p, ct.c_int, ct.c_int, f32p, f32p, f32p, f32p]),
     "or_gemm": (ct.c_int, [ct.c_int, f32p, u8p, ct.c_int, ct.c_int, ct.c_int, f32p]),
     "or_gemvn_q4k": (ct.c_int, [f32p, ct.c_long, u8p, i32p, ct.c_long, ct.c_int, ct.c_int, ct.c_int, f32p]),
     "or_gemvn_q6k": (ct.c_int, [f32p, ct.c_long, u8p, i32p, ct.c_long, ct.c_int, ct.c_int, ct.c_int, f32p]),

@@ -243,11 +243,61 @@ def gen_gdn():
     print("gdn.npz")
 
 
+# qwen35 layer ops: (tag, n_vh, codes, seed) and (tag, nh, codes, seed, [(told, pos0), ...])
+QWEN_GDN_CASES = [("cfg5", 32, (5, 5, 5), 51), ("q80", 16, (0, 0, 0), 52), ("mixed", 16, (5, 4, 4), 53)]
+QWEN_FULL_CASES = [("cfg5", 16, (5, 5, 4, 5), 61, [(0, 0), (7, 7), (300, 300), (40, 45)]),
+                   ("q80", 8, (0, 0, 0, 0), 62, [(0, 0), (33, 33)])]
+GDN_STEPS = 3
+
+
+def gen_qwen35():
+    """m6_gdn_attn (src/m6_layer.c:205-364) over GDN_STEPS consecutive tokens
+    and m6_full_attn (src/m6_layer.c:389-518) at several cache lengths."""
+    from dracohip import qwen35 as Q
+    E = ref_engine()
+    E.m6_gdn_attn.argtypes = [f32p, ct.c_void_p, f32p, f32p, f32p, f32p, f32p]
+    E.m6_full_attn.argtypes = [f32p, ct.c_void_p, f32p, f32p, ct.c_int, ct.c_int, f32p, f32p, f32p, f32p,
+                               f32p, f32p]
+    out = {}
+    for tag, n_vh, codes, seed in QWEN_GDN_CASES:
+        L = Q.gdn_layer(seed, n_vh, codes)
+        ssm, tail = L.fresh_state()
+        h1 = Q.hidden(seed + 1000, GDN_STEPS)
+        buf = np.zeros(40000, np.float32)  # the reference's scratch (>= 28672, buf[39000] = 0)
+        for s in range(GDN_STEPS):
+            x2n = np.zeros(Q.H, np.float32)
+            x2o = np.zeros(Q.H, np.float32)
+            E.m6_gdn_attn(pf(h1[s]), L.ptr(), pf(ssm), pf(tail), pf(buf), pf(x2n), pf(x2o))
+            out[f"gdn_{tag}_x2n_{s}"] = x2n
+            out[f"gdn_{tag}_x2o_{s}"] = x2o
+        out[f"gdn_{tag}_ssm_sample"] = ssm[::61].copy()
+        out[f"gdn_{tag}_ssm_sha"] = np.frombuffer(hashlib.sha256(ssm.tobytes()).digest(), np.uint8)
+        out[f"gdn_{tag}_tail"] = tail.copy()
+        out[f"gdn_{tag}_meta"] = np.array([n_vh, *codes, seed, GDN_STEPS], np.int64)
+    for tag, nh, codes, seed, steps in QWEN_FULL_CASES:
+        L = Q.full_layer(seed, nh, codes)
+        for told, pos0 in steps:
+            Kr, Vc = Q.kv_rows(seed + told, told)
+            h1 = Q.hidden(seed + 2000 + told)[0]
+            buf = np.zeros(40000, np.float32)
+            scores = np.zeros(nh * (told + 1), np.float32)
+            x2n, x2o = np.zeros(Q.H, np.float32), np.zeros(Q.H, np.float32)
+            krn, vrn = np.zeros(512, np.float32), np.zeros(512, np.float32)
+            E.m6_full_attn(pf(h1), L.ptr(), pf(Kr), pf(Vc), told, pos0, pf(buf), pf(scores), pf(x2n), pf(x2o),
+                           pf(krn), pf(vrn))
+            k = f"full_{tag}_{told}_{pos0}"
+            out[k + "_x2n"], out[k + "_x2o"], out[k + "_krn"], out[k + "_vrn"] = x2n, x2o, krn, vrn
+        out[f"full_{tag}_meta"] = np.array([nh, *codes, seed], np.int64)
+    np.savez_compressed(os.path.join(OUT, "qwen35.npz"), **out)
+    print("qwen35.npz")
+
+
 JOBS = {
     "gemv": gen_gemv,
     "batch8k": gen_batch8k,
     "moe": gen_moe,
     "gdn": gen_gdn,
+    "qwen35": gen_qwen35,
     "tiny_k": lambda: gen_llama(models.TINY_K, "llama_tiny_k.npz", logit_steps=(0, 15)),
     "tiny_q8": lambda: gen_llama(models.TINY_Q8, "llama_tiny_q8.npz", logit_steps=(0, 15)),
     "smol360m": lambda: gen_llama(models.SMOL360M, "smol360m.npz", logit_steps=(0, 63)),

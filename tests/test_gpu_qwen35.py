@@ -1,0 +1,145 @@
+"""qwen35 hybrid-layer decode ops on the GPU through the C ABI:
+m6_gdn_attn (src/m6_layer.c:205-364) and m6_full_attn (src/m6_layer.c:389-518).
+
+Checks: the compiled reference's outputs (tests/golden/qwen35.npz) at the
+configs[4] layer shape (32 V heads, 16 q/k heads; full attention with 16 q
+heads of 256) and in Q8_0 / mixed-format variants, over consecutive GDN
+tokens (state carried through the caller's arrays) and several cache lengths;
+the oracle at a 1000-row cache.  Bar (normwise, max|a-b| / max|ref|): every
+output -- x2_out, x2n, kr_new, v_new, the recurrent state and the conv tail --
+within 1e-5, the GEMV bar (measured on MI355X: below 1e-6 throughout).
+"""
+import numpy as np
+import pytest
+
+import gen_golden as gg
+from helpers import golden, rel_err
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-5
+
+
+def _pf(a):
+    from dracohip import lib
+    return lib.pf(a)
+
+
+@pytest.mark.parametrize("tag", [c[0] for c in gg.QWEN_GDN_CASES])
+def test_gdn_attn_vs_reference(hip, oracle, tag):
+    from dracohip import qwen35 as Q
+    g = golden("qwen35.npz")
+    meta = [int(v) for v in g[f"gdn_{tag}_meta"]]
+    n_vh, codes, seed, steps = meta[0], tuple(meta[1:4]), meta[4], meta[5]
+    L = Q.gdn_layer(seed, n_vh, codes)
+    ssm, tail = L.fresh_state()
+    h1 = Q.hidden(seed + 1000, steps)
+    buf = np.zeros(16, np.float32)
+    worst = 0.0
+    for s in range(steps):
+        x2n, x2o = np.zeros(Q.H, np.float32), np.zeros(Q.H, np.float32)
+        print(f"[gdn_attn] case {tag} step {s}", flush=True)
+        hip.m6_gdn_attn(_pf(h1[s]), L.ptr(), _pf(ssm), _pf(tail), _pf(buf), _pf(x2n), _pf(x2o))
+        e1 = rel_err(x2o, g[f"gdn_{tag}_x2o_{s}"])
+        e2 = rel_err(x2n, g[f"gdn_{tag}_x2n_{s}"])
+        worst = max(worst, e1, e2)
+        assert e1 <= TOL and e2 <= TOL, (s, e1, e2)
+    # state after `steps` tokens against the oracle's (same seeded inputs)
+    so, to = L.fresh_state()
+    for s in range(steps):
+        x2n, x2o = np.zeros(Q.H, np.float32), np.zeros(Q.H, np.float32)
+        assert oracle.lib.or_gdn_attn(_pf(h1[s]), L.ptr(), _pf(so), _pf(to), _pf(x2n), _pf(x2o)) == 0
+    es = rel_err(ssm, so)
+    et = rel_err(tail, to)
+    print(f"[gdn_attn] {tag}: out {worst:.2e} state {es:.2e} tail {et:.2e}")
+    assert es <= TOL
+    assert rel_err(ssm[::61], g[f"gdn_{tag}_ssm_sample"]) <= TOL
+    assert et <= TOL
+    assert rel_err(tail, g[f"gdn_{tag}_tail"]) <= TOL
+
+
+@pytest.mark.parametrize("tag", [c[0] for c in gg.QWEN_FULL_CASES])
+def test_full_attn_vs_reference(hip, tag):
+    from dracohip import qwen35 as Q
+    _, nh, codes, seed, steps = [c for c in gg.QWEN_FULL_CASES if c[0] == tag][0]
+    g = golden("qwen35.npz")
+    L = Q.full_layer(seed, nh, codes)
+    buf = np.zeros(16, np.float32)
+    for told, pos0 in steps:
+        Kr, Vc = Q.kv_rows(seed + told, told)
+        h1 = Q.hidden(seed + 2000 + told)[0]
+        x2n, x2o = np.zeros(Q.H, np.float32), np.zeros(Q.H, np.float32)
+        krn, vrn = np.zeros(512, np.float32), np.zeros(512, np.float32)
+        scores = np.zeros(16, np.float32)
+        print(f"[full_attn] case {tag} told {told} pos0 {pos0}", flush=True)
+        hip.m6_full_attn(_pf(h1), L.ptr(), _pf(Kr), _pf(Vc), told, pos0, _pf(buf), _pf(scores), _pf(x2n),
+                         _pf(x2o), _pf(krn), _pf(vrn))
+        k = f"full_{tag}_{told}_{pos0}"
+        errs = {n: rel_err(v, g[k + "_" + n]) for n, v in
+                (("x2n", x2n), ("x2o", x2o), ("krn", krn), ("vrn", vrn))}
+        print(f"[full_attn] {tag} {told}/{pos0}: " + " ".join(f"{n} {e:.2e}" for n, e in errs.items()))
+        for n, e in errs.items():
+            assert e <= TOL, (told, pos0, n, e)
+
+
+def test_full_attn_long_cache_vs_oracle(hip, oracle):
+    """1000 cached rows (the split-T path with 32 splits) at the configs[4] shape."""
+    from dracohip import qwen35 as Q
+    L = Q.full_layer(63, 16, (5, 5, 4, 5))
+    told = 1000
+    Kr, Vc = Q.kv_rows(64, told)
+    h1 = Q.hidden(65)[0]
+    outs = []
+    for fn in ("hip", "oracle"):
+        x2n, x2o = np.zeros(Q.H, np.float32), np.zeros(Q.H, np.float32)
+        krn, vrn = np.zeros(512, np.float32), np.zeros(512, np.float32)
+        if fn == "hip":
+            print("[full_attn] long cache told 1000", flush=True)
+            buf = np.zeros(16, np.float32)
+            hip.m6_full_attn(_pf(h1), L.ptr(), _pf(Kr), _pf(Vc), told, told, _pf(buf), _pf(buf), _pf(x2n),
+                             _pf(x2o), _pf(krn), _pf(vrn))
+        else:
+            assert oracle.lib.or_full_attn(_pf(h1), L.ptr(), _pf(Kr), _pf(Vc), told, told, _pf(x2n), _pf(x2o),
+                                           _pf(krn), _pf(vrn)) == 0
+        outs.append((x2n, x2o, krn, vrn))
+    for a, b in zip(outs[0], outs[1]):
+        assert rel_err(a, b) <= TOL
+
+
+def test_gdn_attn_decay_closed_form(hip):
+    """All conv taps 0 => q = k = v = 0: the state only decays by
+    exp(softplus(xn.aw + dt) * a) (float64 recomputation) and x2_out = h1."""
+    from dracohip import qwen35 as Q
+    L = Q.gdn_layer(71, 16, (0, 0, 0))
+    a = L.arrays
+    a["conv"][:] = 0.0
+    S0 = L.ssm.copy()
+    h1 = Q.hidden(72)[0]
+    x2n, x2o = np.zeros(Q.H, np.float32), np.zeros(Q.H, np.float32)
+    buf = np.zeros(16, np.float32)
+    print("[gdn_attn] closed form", flush=True)
+    hip.m6_gdn_attn(_pf(h1), L.ptr(), _pf(L.ssm), _pf(L.tail), _pf(buf), _pf(x2n), _pf(x2o))
+    xn = h1.astype(np.float64) / np.sqrt(np.mean(h1.astype(np.float64) ** 2) + 1e-6) * a["attn_norm"]
+    av = xn @ a["alpha_wt"].astype(np.float64) + a["ssm_dt"]
+    gd = np.exp(np.logaddexp(0.0, av) * a["ssm_a"])
+    S1 = L.ssm.reshape(16, -1)
+    S0 = S0.reshape(16, -1)
+    for h in range(16):
+        np.testing.assert_allclose(S1[h], gd[h] * S0[h], rtol=2e-5, atol=1e-9)
+    np.testing.assert_array_equal(x2o, h1)
+
+
+@pytest.mark.parametrize("kind", [0, 1])
+def test_bench_qwen_op_runs(hip, kind):
+    from dracohip import lib, qwen35 as Q
+    out = np.zeros(4, np.float32)
+    h1 = Q.hidden(5)[0]
+    if kind == 0:
+        L = Q.gdn_layer(81, 32, (5, 5, 5))
+        rc = hip.draco_bench_qwen_op(0, L.ptr(), _pf(h1), _pf(L.ssm), _pf(L.tail), 0, 4, _pf(out))
+    else:
+        L = Q.full_layer(82, 16, (5, 5, 4, 5))
+        Kr, Vc = Q.kv_rows(83, 64)
+        rc = hip.draco_bench_qwen_op(1, L.ptr(), _pf(h1), _pf(Kr), _pf(Vc), 64, 4, _pf(out))
+    assert rc == 0, lib.load().draco_last_error()
+    print(f"[bench_qwen_op] kind {kind}: {out[0]:.2f} us, {out[2] / 1e6:.2f} MB")
+    assert out[0] > 0 and out[1] > 0 and out[2] >= out[1]
