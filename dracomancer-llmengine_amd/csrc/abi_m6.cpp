@@ -254,7 +254,7 @@ int grow(float** p, size_t* cap, size_t n) {
 }
 
 int ensure_work(Work& w, int H, int QD, int KD, int NH, int HD, int max_t, int FF) {
-    const size_t part = (size_t)NH * attn_nsplit(max_t) * (HD + 2);
+    const size_t part = (size_t)NH * attn_nsplit(max_t, NH, KD / HD, HD) * (HD + 2);
     if (!w.cnt) {
         DRACO_HIP(hipMalloc(&w.cnt, sizeof(unsigned) * 256));
         DRACO_HIP(hipMemset(w.cnt, 0, sizeof(unsigned) * 256));

@@ -25,6 +25,8 @@ int fm_of(int code) { return code == DRACO_Q4_K ? 1 : (code == DRACO_Q6_K ? 2 : 
 // device pointer tables for one expert set, rebuilt when the registry epoch moves
 struct ExpertSet {
     uint64_t epoch = 0;
+    std::vector<uint64_t> host_ptrs;  // the caller's table when the set was built
+    std::vector<int> host_codes;
     const uint8_t** dev = nullptr;  // [3][n_exp]
     int n_exp = 0;
     int fm_gu = 0, fm_d = 0;
@@ -39,7 +41,12 @@ std::map<const void*, ExpertSet>& sets() {
 ExpertSet* expert_set(const uint64_t* ptrs, const int* codes, const float* gate_inp, int n_exp, int inter,
                       int n_in, int n_out, hipStream_t st) {
     ExpertSet& s = sets()[ptrs];
-    if (s.dev && s.epoch == epoch() && s.n_exp == n_exp) {
+    // the table address alone does not identify the set: a new table can
+    // reuse a freed one's address, so its contents must match too
+    const bool same_table = s.n_exp == n_exp && s.host_ptrs.size() == 3 * (size_t)n_exp &&
+                            memcmp(s.host_ptrs.data(), ptrs, sizeof(uint64_t) * 3 * (size_t)n_exp) == 0 &&
+                            memcmp(s.host_codes.data(), codes, sizeof(int) * 3 * (size_t)n_exp) == 0;
+    if (s.dev && s.epoch == epoch() && same_table) {
         s.router = get_mat(gate_inp, DRACO_F32, n_exp, n_in);
         return s.router ? &s : nullptr;
     }
@@ -76,6 +83,8 @@ ExpertSet* expert_set(const uint64_t* ptrs, const int* codes, const float* gate_
         return nullptr;
     }
     s.n_exp = n_exp;
+    s.host_ptrs.assign(ptrs, ptrs + 3 * (size_t)n_exp);
+    s.host_codes.assign(codes, codes + 3 * (size_t)n_exp);
     s.fm_gu = fg;
     s.fm_d = fd;
     s.router = get_mat(gate_inp, DRACO_F32, n_exp, n_in);

@@ -280,7 +280,7 @@ int full_resolve(const FullW* w, FullDev& f) {
 
 // buffers for caches of up to max_t rows
 int full_bufs(const FullDev& f, int max_t, int slot, FullBufs& b) {
-    const int nsplit = attn_nsplit(max_t);
+    const int nsplit = attn_nsplit(max_t, f.nh, FNKV, FHD);
     const size_t kv = (size_t)max_t * FNKV * FHD;
     const size_t part = (size_t)f.nh * nsplit * (FHD + 2);
     const size_t n = 5 * (size_t)QH + (size_t)f.nh * 2 * FHD + 2 * (size_t)f.nh * FHD + FNKV * FHD + 2 * kv +

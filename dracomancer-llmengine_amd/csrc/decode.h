@@ -6,11 +6,30 @@
 
 constexpr int ARGMAX_BLOCKS = 256;
 
-// Number of T-splits of the decode attention for a cache of max_t rows
-// (about 32 rows per split at full length, at most 64 splits; the merge
-// kernel handles at most 64).
-static inline int attn_nsplit(int max_t) {
+// The group-shared attention kernel serves GQA groups of rep = NH / NKV q
+// heads with rep a power of two in [2, 16] and HD in {128, 256}; other shapes
+// run the per-head kernel.  (At HD 64 the per-head kernel is faster on MI355X:
+// its rows are 256 bytes, so the re-read K / V rows stay in L2 and the
+// per-row shuffle cost of the grouped kernel dominates.)
+static inline bool attn_grouped(int NH, int NKV, int HD) {
+    if (NKV < 1 || NH % NKV) return false;
+    const int rep = NH / NKV;
+    if (rep < 2 || rep > 16 || (rep & (rep - 1))) return false;
+    return HD == 128 || HD == 256;
+}
+
+// Number of T-splits of the decode attention for a cache of max_t rows.
+// Grouped kernel: about 32 rows per split at full length and at most ~512
+// blocks (NKV * nsplit), at most 256 splits.  Per-head kernel: about 32 rows
+// per split, at most 64 splits.  The split count is fixed by max_t so that a
+// captured decode step serves every cache length.
+static inline int attn_nsplit(int max_t, int NH, int NKV, int HD) {
     int n = (max_t + 31) / 32;
+    if (attn_grouped(NH, NKV, HD)) {
+        const int cap = (512 + NKV - 1) / NKV;
+        n = n < cap ? n : cap;
+        return n < 1 ? 1 : (n > 256 ? 256 : n);
+    }
     return n < 1 ? 1 : (n > 64 ? 64 : n);
 }
 

@@ -164,6 +164,191 @@ __global__ __launch_bounds__(1024) void k_attn_part(const float* __restrict__ q,
     }
 }
 
+// Group-shared split-T decode attention.  Block (g, s) handles kv head g
+// and rows [t0, t1) for all REP q heads of the group, so every K / V element
+// is read from memory once per block (the per-head kernel above reads it once
+// per q head).  Rows are processed in sub-chunks of GQ_CH:
+//   scores  wave w takes rows w, w + 4, ...; a lane holds DPL = HD/64 dims of
+//           K and of each group q head, forms REP partial dots and reduces
+//           them with a reduce-scatter (each halving shuffle stage leaves a
+//           lane half of the heads), so a row costs REP - 1 + 6 - log2(REP)
+//           shuffles instead of 6 * REP; scores go to LDS as [row][head]
+//   softmax per head over the sub-chunk, merged into a running (m, l) with
+//           the online rescale
+//   P.V     thread (d, head group) owns HPT = REP*HD/256 outputs of dim d,
+//           rescales them and accumulates p[row][head] * V[row][d]
+// Each (q head, split) writes (o[HD], m, l) for k_attn_merge.
+constexpr int GQ_CH = 32;
+
+template <int REP>
+__device__ __forceinline__ float group_reduce_scatter(float (&v)[REP], int lane, int* head) {
+    int hd = 0;
+#pragma unroll
+    for (int n = REP, m = 32; n > 1; n >>= 1, m >>= 1) {
+        const bool up = (lane & m) != 0;
+        hd += up ? n / 2 : 0;
+#pragma unroll
+        for (int i = 0; i < n / 2; i++) {
+            const float send = up ? v[i] : v[i + n / 2];
+            const float keep = up ? v[i + n / 2] : v[i];
+            v[i] = keep + __shfl_xor(send, m, 64);
+        }
+    }
+    float r = v[0];
+#pragma unroll
+    for (int m = 32 / REP; m >= 1; m >>= 1) r += __shfl_xor(r, m, 64);
+    *head = hd;
+    return r;
+}
+
+template <int HD, int REP>
+__global__ __launch_bounds__(256) void k_attn_gqa(const float* __restrict__ q, const float* __restrict__ kc,
+                                                  const float* __restrict__ vc, float* __restrict__ part,
+                                                  const int* __restrict__ st, int layer, int NKV, int nsplit,
+                                                  float scale) {
+    constexpr int DPL = HD / 64, HPT = REP * HD / 256, RPW = GQ_CH / 4;
+    __shared__ float sc[GQ_CH * REP];
+    __shared__ float mrun[REP], lrun[REP], corr[REP];
+    const int g = blockIdx.x, s = blockIdx.y, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int KD = NKV * HD;
+    const int Tn = st[1 + layer] + 1;
+    const int chunk = (Tn + nsplit - 1) / nsplit;
+    const int t0 = s * chunk, t1 = min(Tn, t0 + chunk);
+    float qv[REP][DPL];
+#pragma unroll
+    for (int h = 0; h < REP; h++)
+#pragma unroll
+        for (int e = 0; e < DPL; e++) qv[h][e] = q[(size_t)(g * REP + h) * HD + DPL * lane + e];
+    const int d = tid % HD, hg = tid / HD;
+    float o[HPT];
+#pragma unroll
+    for (int i = 0; i < HPT; i++) o[i] = 0.f;
+    if (tid < REP) {
+        mrun[tid] = -INFINITY;
+        lrun[tid] = 0.f;
+    }
+    const float* kg = kc + (size_t)g * HD + DPL * lane;
+    const float* vg = vc + (size_t)g * HD + d;
+    for (int c0 = t0; c0 < t1; c0 += GQ_CH) {
+        const int nr = min(GQ_CH, t1 - c0);
+        // all loads of the sub-chunk first: K for this wave's rows, V for this thread's dim
+        float kx[RPW][DPL];
+#pragma unroll
+        for (int i = 0; i < RPW; i++) {
+            const int t = min(c0 + w + 4 * i, t1 - 1);
+#pragma unroll
+            for (int e = 0; e < DPL; e++) kx[i][e] = kg[(size_t)t * KD + e];
+        }
+        float vv[GQ_CH];
+#pragma unroll
+        for (int r = 0; r < GQ_CH; r++) vv[r] = vg[(size_t)min(c0 + r, t1 - 1) * KD];
+#pragma unroll
+        for (int i = 0; i < RPW; i++) {
+            float pd[REP];
+#pragma unroll
+            for (int h = 0; h < REP; h++) {
+                float a = 0.f;
+#pragma unroll
+                for (int e = 0; e < DPL; e++) a = fmaf(qv[h][e], kx[i][e], a);
+                pd[h] = a;
+            }
+            int hs;
+            const float sres = group_reduce_scatter<REP>(pd, lane, &hs);
+            const int r = w + 4 * i;
+            if ((lane & (64 / REP - 1)) == 0) sc[r * REP + hs] = r < nr ? sres * scale : -INFINITY;
+        }
+        lds_barrier();
+        // softmax: wave w takes heads 2w (lanes 0-31) and 2w+1 (lanes 32-63), then +8
+        for (int h = 2 * w + (lane >> 5); h < REP; h += 8) {
+            const int r = lane & 31;
+            const float sv = sc[r * REP + h];
+            float cm = sv;
+#pragma unroll
+            for (int m = 16; m >= 1; m >>= 1) cm = fmaxf(cm, __shfl_xor(cm, m, 64));
+            const float mo = mrun[h];
+            const float mn = fmaxf(mo, cm);
+            const float cr = mo == -INFINITY ? 0.f : expf(mo - mn);
+            const float p = sv == -INFINITY ? 0.f : expf(sv - mn);
+            float ps = p;
+#pragma unroll
+            for (int m = 16; m >= 1; m >>= 1) ps += __shfl_xor(ps, m, 64);
+            sc[r * REP + h] = p;
+            if (r == 0) {
+                mrun[h] = mn;
+                lrun[h] = lrun[h] * cr + ps;
+                corr[h] = cr;
+            }
+        }
+        lds_barrier();
+#pragma unroll
+        for (int i = 0; i < HPT; i++) o[i] *= corr[hg * HPT + i];
+#pragma unroll
+        for (int r = 0; r < GQ_CH; r++) {
+#pragma unroll
+            for (int i = 0; i < HPT; i++) o[i] = fmaf(sc[r * REP + hg * HPT + i], vv[r], o[i]);
+        }
+        lds_barrier();  // sc / corr / mrun are rewritten by the next sub-chunk
+    }
+#pragma unroll
+    for (int i = 0; i < HPT; i++) part[((size_t)(g * REP + hg * HPT + i) * nsplit + s) * (HD + 2) + d] = o[i];
+    if (tid < REP) {
+        float* pp = part + ((size_t)(g * REP + tid) * nsplit + s) * (HD + 2);
+        pp[HD] = mrun[tid];
+        pp[HD + 1] = lrun[tid];
+    }
+}
+
+// Merge the splits of one q head (block of HD threads, one per head dim):
+//   out[h] = sum_s o_s e^(m_s - M) / sum_s l_s e^(m_s - M),  M = max_s m_s
+// The split weights go through LDS; the partial loads are unconditional
+// (indices clamped, weights of padding splits 0) and issued 32 at a time.
+constexpr int MERGE_MAXS = 256;
+
+template <int HD>
+__global__ __launch_bounds__(256) void k_attn_merge(const float* __restrict__ part, float* __restrict__ out,
+                                                    int nsplit, const float* __restrict__ gate, int gstride) {
+    __shared__ float wsh[MERGE_MAXS + 32];
+    __shared__ float red[2][4];
+    const int h = blockIdx.x, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    constexpr int NW = HD / 64;
+    const float* ph = part + (size_t)h * nsplit * (HD + 2);
+    float mloc = -INFINITY;
+    for (int k = tid; k < nsplit; k += HD) mloc = fmaxf(mloc, ph[(size_t)k * (HD + 2) + HD]);
+    mloc = wave_max(mloc);
+    if (lane == 0) red[0][w] = mloc;
+    __syncthreads();
+    float M = red[0][0];
+#pragma unroll
+    for (int i = 1; i < NW; i++) M = fmaxf(M, red[0][i]);
+    float lsum = 0.f;
+    for (int k = tid; k < MERGE_MAXS + 32; k += HD) {
+        float wk = 0.f;
+        if (k < nsplit) {
+            const float mk = ph[(size_t)k * (HD + 2) + HD];
+            wk = mk == -INFINITY ? 0.f : expf(mk - M);
+            lsum += ph[(size_t)k * (HD + 2) + HD + 1] * wk;
+        }
+        wsh[k] = wk;
+    }
+    lsum = wave_sum(lsum);
+    if (lane == 0) red[1][w] = lsum;
+    __syncthreads();
+    float L = 0.f;
+#pragma unroll
+    for (int i = 0; i < NW; i++) L += red[1][i];
+    float acc = 0.f;
+    for (int k0 = 0; k0 < nsplit; k0 += 32) {
+        float pv[32];
+#pragma unroll
+        for (int j = 0; j < 32; j++) pv[j] = ph[(size_t)min(k0 + j, nsplit - 1) * (HD + 2) + tid];
+#pragma unroll
+        for (int j = 0; j < 32; j++) acc = fmaf(pv[j], wsh[k0 + j], acc);
+    }
+    float r = acc * (1.f / L);
+    if (gate) r *= 1.f / (1.f + expf(-gate[(size_t)h * gstride + tid]));
+    out[(size_t)h * HD + tid] = r;
+}
+
 // Merge the splits of one q head (block), one thread per head dim.  Lane k
 // of each wave holds split k's (m, l); the weights exp(m_k - M) are
 // broadcast with readlane, and all of a lane's partial loads are issued
@@ -180,7 +365,7 @@ __global__ __launch_bounds__(256) void k_attn_combine(const float* __restrict__ 
     const float lk = lane < nsplit ? ph[lane * (HD + 2) + HD + 1] : 0.f;
     float pv[MAXS];
 #pragma unroll
-    for (int k = 0; k < MAXS; k++) pv[k] = (k < nsplit && tid < HD) ? ph[k * (HD + 2) + tid] : 0.f;
+    for (int k = 0; k < MAXS; k++) pv[k] = ph[min(k, nsplit - 1) * (HD + 2) + tid];  // unconditional: no vmcnt(0) per load
     const float M = wave_max(m);
     const float wk = m > -INFINITY ? expf(m - M) : 0.f;
     const float L = wave_sum(lk * wk);
@@ -362,7 +547,22 @@ int dk_attention(const float* q, const float* kc, const float* vc, float* part, 
     (void)count;
     const int rep = NH / NKV;
     if (rep < 1 || rep > REPMAX || NH % NKV) return -1;
-    const int nsplit = attn_nsplit(max_t);
+    const int nsplit = attn_nsplit(max_t, NH, NKV, HD);
+    if (attn_grouped(NH, NKV, HD)) {
+        const dim3 grid(NKV, nsplit);
+#define GQA_CASE(H_, R_)                                                                                  \
+    if (HD == H_ && rep == R_) {                                                                          \
+        hipLaunchKernelGGL((k_attn_gqa<H_, R_>), grid, dim3(256), 0, st, q, kc, vc, part, state, layer, NKV, \
+                           nsplit, scale);                                                                \
+    } else
+        GQA_CASE(64, 4) GQA_CASE(64, 8) GQA_CASE(64, 16) GQA_CASE(128, 2) GQA_CASE(128, 4) GQA_CASE(128, 8)
+        GQA_CASE(128, 16) GQA_CASE(256, 2) GQA_CASE(256, 4) GQA_CASE(256, 8) GQA_CASE(256, 16) return -1;
+#undef GQA_CASE
+        if (HD == 64) hipLaunchKernelGGL(k_attn_merge<64>, dim3(NH), dim3(64), 0, st, part, out, nsplit, gate, gstride);
+        else if (HD == 128) hipLaunchKernelGGL(k_attn_merge<128>, dim3(NH), dim3(128), 0, st, part, out, nsplit, gate, gstride);
+        else hipLaunchKernelGGL(k_attn_merge<256>, dim3(NH), dim3(256), 0, st, part, out, nsplit, gate, gstride);
+        return 0;
+    }
     const dim3 grid(NKV, nsplit), block(64 * rep);
     if (HD == 64)
         hipLaunchKernelGGL(k_attn_part<64>, grid, block, 0, st, q, kc, vc, part, state, layer, NH, NKV, nsplit, scale);
