@@ -52,6 +52,7 @@ constexpr int SEG_MAX = 4;
 struct SegLaunch {
     SegDesc seg[SEG_MAX];
     int nseg;
+    int total_tiles;      // filled by draco_seg_launch (Q4_K/Q6_K path)
     int n_in;
     const float* x;
     const float* norm_w;  // nullable

@@ -60,11 +60,22 @@ __device__ __forceinline__ void am_merge(float& v, int& i, float v2, int i2) {
     }
 }
 
+// Segment of global tile T.  Segment first tiles ascend; unused slots (and
+// the "up" half of a SwiGLU pair) hold 1 << 30, so three comparisons against
+// kernel-argument values (loaded once, kept in SGPRs) replace a loop.
 __device__ __forceinline__ int seg_of_tile(const SegLaunch& a, int T) {
-    int si = 0;
-    for (int i = 1; i < a.nseg; i++)
-        if (T >= a.seg[i].first_tile) si = i;
-    return si;
+    return (T >= a.seg[1].first_tile) + (T >= a.seg[2].first_tile) + (T >= a.seg[3].first_tile);
+}
+
+// Fields of segment si picked with selects over compile-time indices (no
+// dynamic indexing into the kernel arguments, which costs a scalar load).
+template <class F>
+__device__ __forceinline__ auto seg_pick(const SegLaunch& a, int si, F f) -> decltype(f(a.seg[0])) {
+    auto r = f(a.seg[0]);
+    if (si == 1) r = f(a.seg[1]);
+    if (si == 2) r = f(a.seg[2]);
+    if (si == 3) r = f(a.seg[3]);
+    return r;
 }
 
 // FM: 1 = Q4_K segments only, 2 = Q6_K only, 3 = both (per-tile switch).
@@ -81,26 +92,37 @@ __global__ __launch_bounds__(64 * NW) void k_dq(const SegLaunch a) {
     const int tid = threadIdx.x, lane = tid & 63, j = lane & 15, g = lane >> 4;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int bx = blockIdx.x, G = gridDim.x;
-    int total = 0;
-    for (int i = 0; i < a.nseg; i++) total += a.seg[i].n_tiles;
+    const int total = a.total_tiles;
     const int ipt = (nb + NW - 1) / NW;
     const int my_tiles = bx < total ? (total - bx + G - 1) / G : 0;
     const int n_items = my_tiles * ipt;
 
-    auto is_q4 = [&](int T) -> bool {
-        if (FM != 3) return FM == 1;
-        return a.seg[seg_of_tile(a, T)].L.code == DRACO_Q4_K;
+    // Item 0 of tile T (wave-uniform): base pointer(s) and format.  Items of
+    // a tile are contiguous, super-block b at + b * item bytes.
+    struct TileRef {
+        const uint8_t* p;
+        const uint8_t* p2;
+        bool q4;
     };
-    auto load = [&](int T, int b, Frag& f, Frag& f2) {
+    auto tile_ref = [&](int T) {
         const int si = seg_of_tile(a, T);
-        const bool q4 = is_q4(T);
+        const bool q4 = FM == 3 ? seg_pick(a, si, [](const SegDesc& d) { return d.L.code; }) == DRACO_Q4_K : FM == 1;
         const size_t ib = q4 ? DRACO_Q4T_ITEM : DRACO_Q6T_ITEM;
-        const size_t off = ((size_t)(T - a.seg[si].first_tile + a.seg[si].tile0) * nb + b) * ib;
-        if (q4) load_q4(a.seg[si].base + off, lane, f);
-        else load_q6(a.seg[si].base + off, lane, f);
+        const int tl = T - seg_pick(a, si, [](const SegDesc& d) { return d.first_tile; }) +
+                       seg_pick(a, si, [](const SegDesc& d) { return d.tile0; });
+        const size_t off = (size_t)tl * nb * ib;
+        TileRef r;
+        r.p = seg_pick(a, si, [](const SegDesc& d) { return d.base; }) + off;
+        r.p2 = DUAL ? seg_pick(a, si + 1, [](const SegDesc& d) { return d.base; }) + off : r.p;
+        r.q4 = q4;
+        return r;
+    };
+    auto load_at = [&](const uint8_t* p, const uint8_t* p2, bool q4, Frag& f, Frag& f2) {
+        if (q4) load_q4(p, lane, f);
+        else load_q6(p, lane, f);
         if (DUAL) {
-            if (q4) load_q4(a.seg[si + 1].base + off, lane, f2);
-            else load_q6(a.seg[si + 1].base + off, lane, f2);
+            if (q4) load_q4(p2, lane, f2);
+            else load_q6(p2, lane, f2);
         }
     };
 
@@ -115,11 +137,36 @@ __global__ __launch_bounds__(64 * NW) void k_dq(const SegLaunch a) {
         }
     }
     Frag P0, P1, Q0, Q1;
-    int ct = bx, cb = w, cp = 0;  // current item: tile, super-block, position in tile
-    // loads are issued unconditionally, at indices clamped to a real item:
-    // a skipped load would leave the wait-count analysis no choice but
-    // vmcnt(0) before every use, serialising the prefetch
-    load(ct < total ? ct : total - 1, cb < nb ? cb : nb - 1, P0, Q0);
+    // Load cursor (one item ahead of the compute cursor).  Loads are issued
+    // unconditionally: a padding item or a load past the wave's last item
+    // re-reads the last real item it loaded (already fetched or in flight,
+    // so no HBM traffic) -- a skipped load would leave the wait-count
+    // analysis no choice but vmcnt(0) before every use.
+    int lt = bx < total ? bx : total - 1, lb = w, lp = 0, li = 0;
+    TileRef lref = tile_ref(lt);
+    const size_t lib = lref.q4 ? DRACO_Q4T_ITEM : DRACO_Q6T_ITEM;
+    const uint8_t* lastp = lref.p + (size_t)(w < nb ? w : nb - 1) * lib;
+    const uint8_t* lastp2 = lref.p2 + (size_t)(w < nb ? w : nb - 1) * lib;
+    bool lastq4 = lref.q4;
+    auto load_next = [&](Frag& f, Frag& f2) {
+        if (li < n_items && lb < nb) {
+            const size_t ib = lref.q4 ? DRACO_Q4T_ITEM : DRACO_Q6T_ITEM;
+            lastp = lref.p + (size_t)lb * ib;
+            lastp2 = lref.p2 + (size_t)lb * ib;
+            lastq4 = lref.q4;
+        }
+        load_at(lastp, lastp2, lastq4, f, f2);
+        li++;
+        lp++;
+        lb += NW;
+        if (lp == ipt) {
+            lp = 0;
+            lb = w;
+            lt += G;
+            if (li < n_items) lref = tile_ref(lt);
+        }
+    };
+    load_next(P0, Q0);
     for (int i = tid; i < 256; i += NT) reinterpret_cast<uint32_t*>(zero)[i] = 0u;
 
     // ---- prologue part 2: RMSNorm (src/m6_engine.c:31-37) and digits into LDS
@@ -167,41 +214,45 @@ __global__ __launch_bounds__(64 * NW) void k_dq(const SegLaunch a) {
     float am_v = -INFINITY;
     int am_i = 0x7fffffff;
     float aD = 0.f, aM = 0.f, aD2 = 0.f, aM2 = 0.f;
-    // epilogue inputs, loaded when a tile starts so they are not a memory
-    // round trip after the tile's reduction
     const int pos = a.state ? a.state[0] : 0;
     const int kv_row = a.state ? a.state[1 + a.layer] : 0;
-    float ep0 = 0.f, ep1 = 0.f;
+    // compute cursor and the current tile's epilogue context (set at tile start)
+    int ct = bx, cb = w, cp = 0;
+    int c_epi = EPI_STORE, c_row = 0, c_r0 = 0, c_r1 = 0;
+    float* c_y = nullptr;
+    bool cq4 = FM != 2;
+    float ep0 = 0.f, ep1 = 0.f;  // epilogue inputs, loaded at tile start (off the tile-end critical path)
 
-    auto step = [&](int i, Frag& cur, Frag& nxt, Frag& cur2, Frag& nxt2) {
-        if (cp == 0 && tid < 16) {
-            const SegDesc& s = a.seg[seg_of_tile(a, ct)];
-            const int row = (ct - s.first_tile + s.tile0) * 16 + tid;
-            const int rr = row < s.L.n_out ? row : s.L.n_out - 1;
-            const int epi = s.epi;
-            const float* src = nullptr;
-            if (epi == EPI_RESID) {
-                src = s.yadd + rr;
-            } else if ((epi == EPI_ROPE_Q || epi == EPI_ROPE_K) && rr % a.head_dim < a.rot) {
-                src = a.rope_tab + ((size_t)pos * (a.rot / 2) + (rr % a.head_dim) / 2) * 2;
+    auto step = [&](Frag& cur, Frag& nxt, Frag& cur2, Frag& nxt2) {
+        if (cp == 0) {
+            const int si = seg_of_tile(a, ct);
+            c_epi = seg_pick(a, si, [](const SegDesc& d) { return d.epi; });
+            c_row = (ct - seg_pick(a, si, [](const SegDesc& d) { return d.first_tile; }) +
+                     seg_pick(a, si, [](const SegDesc& d) { return d.tile0; })) * 16;
+            c_r0 = seg_pick(a, si, [](const SegDesc& d) { return d.row0; });
+            c_r1 = seg_pick(a, si, [](const SegDesc& d) { return d.row1; });
+            c_y = seg_pick(a, si, [](const SegDesc& d) { return d.y; });
+            if (FM == 3) cq4 = seg_pick(a, si, [](const SegDesc& d) { return d.L.code; }) == DRACO_Q4_K;
+            if (tid < 16) {
+                const int n_out = seg_pick(a, si, [](const SegDesc& d) { return d.L.n_out; });
+                const int row = c_row + tid;
+                const int rr = row < n_out ? row : n_out - 1;
+                const float* src = nullptr;
+                if (c_epi == EPI_RESID) {
+                    src = seg_pick(a, si, [](const SegDesc& d) { return d.yadd; }) + rr;
+                } else if ((c_epi == EPI_ROPE_Q || c_epi == EPI_ROPE_K) && rr % a.head_dim < a.rot) {
+                    src = a.rope_tab + ((size_t)pos * (a.rot / 2) + (rr % a.head_dim) / 2) * 2;
+                }
+                const float2 e =
+                    src ? make_float2(src[0], c_epi == EPI_RESID ? 0.f : src[1]) : make_float2(0.f, 0.f);
+                ep0 = e.x;
+                ep1 = e.y;
             }
-            const float2 e = src ? make_float2(src[0], epi == EPI_RESID ? 0.f : src[1]) : make_float2(0.f, 0.f);
-            ep0 = e.x;
-            ep1 = e.y;
         }
-        int nt = ct, nbk = cb + NW, np = cp + 1;
-        if (np == ipt) {
-            np = 0;
-            nbk = w;
-            nt = ct + G;
-        }
-        // a padding item (or the end) reloads this wave's first item of the
-        // current tile, already fetched, so it costs no HBM traffic
-        const bool real = i + 1 < n_items && nbk < nb;
-        load(real ? nt : ct, real ? nbk : (w < nb ? w : nb - 1), nxt, nxt2);
+        load_next(nxt, nxt2);
         if (cb < nb) {
             float cD, cM, cD2 = 0.f, cM2 = 0.f;
-            if (is_q4(ct)) {
+            if (cq4) {
                 const int8_t* xa = adig ? xd + (size_t)cb * 1024 + (gl4 * 4 + (j & 3)) * 16 : zero;
                 const float2 r = dot_q4(cur, xa, xsm, cb * 16 + gl4, g);
                 cD = r.x;
@@ -244,18 +295,17 @@ __global__ __launch_bounds__(64 * NW) void k_dq(const SegLaunch a) {
                     v += red[q * 16 + tid];
                     if (DUAL) v2 += red[(NW + q) * 16 + tid];
                 }
-                const SegDesc& s = a.seg[seg_of_tile(a, ct)];
-                const int row = (ct - s.first_tile + s.tile0) * 16 + tid;
-                const bool ok = row >= s.row0 && row < s.row1;
-                switch (s.epi) {
+                const int row = c_row + tid;
+                const bool ok = row >= c_r0 && row < c_r1;
+                switch (c_epi) {
                 case EPI_STORE:
-                    if (ok) s.y[row] = v;
+                    if (ok) c_y[row] = v;
                     break;
                 case EPI_RESID:
-                    if (ok) s.y[row] = ep0 + v;
+                    if (ok) c_y[row] = ep0 + v;
                     break;
                 case EPI_SWIGLU:
-                    if (ok) s.y[row] = (v / (1.f + expf(-v))) * v2;
+                    if (ok) c_y[row] = (v / (1.f + expf(-v))) * v2;
                     break;
                 case EPI_ROPE_Q:
                 case EPI_ROPE_K: {
@@ -267,7 +317,7 @@ __global__ __launch_bounds__(64 * NW) void k_dq(const SegLaunch a) {
                         o = (row & 1) ? pv * sn + v * c : v * c - pv * sn;
                     }
                     if (ok) {
-                        if (s.epi == EPI_ROPE_Q) s.y[row] = o;
+                        if (c_epi == EPI_ROPE_Q) c_y[row] = o;
                         else a.kc[(size_t)kv_row * a.kv_dim + row] = o;
                     }
                     break;
@@ -276,7 +326,7 @@ __global__ __launch_bounds__(64 * NW) void k_dq(const SegLaunch a) {
                     if (ok) a.vc[(size_t)kv_row * a.kv_dim + row] = v;
                     break;
                 case EPI_ARGMAX: {
-                    if (ok) s.y[row] = v;
+                    if (ok) c_y[row] = v;
                     float bv = ok ? v : -INFINITY;
                     int bi = ok ? row : 0x7fffffff;
 #pragma unroll
@@ -291,14 +341,18 @@ __global__ __launch_bounds__(64 * NW) void k_dq(const SegLaunch a) {
             lds_barrier();
             aD = aM = aD2 = aM2 = 0.f;
         }
-        ct = nt;
-        cb = nbk;
-        cp = np;
+        cp++;
+        cb += NW;
+        if (cp == ipt) {
+            cp = 0;
+            cb = w;
+            ct += G;
+        }
     };
     for (int i = 0; i < n_items; i += 2) {
-        step(i, P0, P1, Q0, Q1);
+        step(P0, P1, Q0, Q1);
         if (i + 1 >= n_items) break;
-        step(i + 1, P1, P0, Q1, Q0);
+        step(P1, P0, Q1, Q0);
     }
     if (a.seg[0].epi == EPI_ARGMAX && tid == 0) {
         a.am_val[bx] = am_v;
@@ -612,6 +666,12 @@ int seg_launch_dq(SegLaunch& a, hipStream_t st) {
         tiles += s.n_tiles;
     }
     if (dual && (a.nseg != 2 || fm == 3)) return -1;
+    for (int i = a.nseg; i < SEG_MAX; i++) {  // unused slots: never selected by seg_of_tile
+        a.seg[i] = a.seg[a.nseg - 1];
+        a.seg[i].first_tile = 1 << 30;
+        a.seg[i].n_tiles = 0;
+    }
+    a.total_tiles = tiles;
     // waves per block: enough to split a row's super-blocks, and enough
     // threads for the prologue's XP_MAXV float4s per thread
     int nw = nb >= 32 ? 16 : (nb >= 8 ? 8 : 4);
