@@ -152,6 +152,36 @@ def gdn_scan_configs4(lib):
             "shape": "32 V heads, 16 q/k heads, head 128, T 4096 in 64-token launches + 64 decode steps"}
 
 
+def qwen35_ops_configs4(lib, told=4096, iters=50):
+    """configs[4] hybrid stack, one decode token per layer kind: the GDN layer op
+    (m6_gdn_attn: qkv+gate GEMVs, gates, conv, delta rule on the 32x128x128
+    state, gated rms, ssm_out GEMV + residual, post-norm) and the full-attention
+    op (m6_full_attn: q+gate/k/v GEMVs, q/k norm + rope, attention over `told`
+    cached rows + the new one, sigmoid gate, o GEMV + residual, post-norm), Q4_K
+    projections (v in Q6_K), graph replay with device-resident state."""
+    from dracohip import qwen35 as Q
+    L = lib.load()
+    h1 = Q.hidden(5)[0]
+    out = np.zeros(4, np.float32)
+    res = {}
+    G = Q.gdn_layer(81, 32, (5, 5, 5))
+    if L.draco_bench_qwen_op(0, G.ptr(), lib.pf(h1), lib.pf(G.ssm), lib.pf(G.tail), 0, iters, lib.pf(out)):
+        raise RuntimeError(lib.last_error())
+    res["gdn_op"] = {"us_per_token": round(float(out[0]), 3), "bytes_per_token": int(out[2]),
+                     "GB_s": round(float(out[2]) / float(out[0]) / 1e3, 1),
+                     "frac_of_peak": round(float(out[2]) / float(out[0]) / 1e3 / PEAK_HBM_GBS, 4)}
+    F = Q.full_layer(82, 16, (5, 5, 4, 5))
+    Kr, Vc = Q.kv_rows(83, told)
+    if L.draco_bench_qwen_op(1, F.ptr(), lib.pf(h1), lib.pf(Kr), lib.pf(Vc), told, iters, lib.pf(out)):
+        raise RuntimeError(lib.last_error())
+    res["full_attn_op"] = {"us_per_token": round(float(out[0]), 3), "bytes_per_token": int(out[2]),
+                           "cached_rows": told, "GB_s": round(float(out[2]) / float(out[0]) / 1e3, 1),
+                           "frac_of_peak": round(float(out[2]) / float(out[0]) / 1e3 / PEAK_HBM_GBS, 4)}
+    res["shape"] = ("GDN: 16 q/k + 32 V heads of 128, n_qkv 8192, hidden 2048; full attention: 16 q heads, "
+                    "2 KV heads of 256, hidden 2048")
+    return res
+
+
 PEAK_INT8_TOPS = 5000.0
 
 
@@ -289,9 +319,12 @@ def main():
         pre = prefill_gemm_configs2(lib)
         log(f"prefill GEMM configs[2] (256-token chunk, one layer): {pre['us_per_layer_chunk']} us, "
             f"{pre['tflops_fp32_equiv']} TFLOP/s fp32-equiv, int8 MFMA util {pre['mfma_util']}")
+        qw = qwen35_ops_configs4(lib)
+        log(f"qwen35 ops configs[4]: GDN layer {qw['gdn_op']['us_per_token']} us/token, full attention "
+            f"{qw['full_attn_op']['us_per_token']} us/token at 4096 cached rows")
         print(json.dumps({"roofline": roof, "configs1_q8k_gemv": q8, "configs3_moe_ffn": moe,
-                          "configs4_gdn_scan": gdn,
-        "configs2_prefill_gemm": pre, "configs2_prefill_gemm": pre}), flush=True)
+                          "configs4_gdn_scan": gdn, "configs4_layer_ops": qw,
+                          "configs2_prefill_gemm": pre}), flush=True)
         return
 
     cfg = models.LLAMA1B
@@ -328,7 +361,7 @@ def main():
         match = bool(list(g["tokens"][:n]) == toks_first[:n])
     log(f"decode {tok_s:.1f} tok/s; greedy tokens match reference: {match}")
 
-    roof = q8 = moe = gdn = pre = None
+    roof = q8 = moe = gdn = pre = qw = None
     if not args.no_roofline:
         roof = q4k_gemv_roofline(lib)
         log(f"Q4_K GEMV 14336x4096: {roof['us_per_launch']} us/launch, {roof['achieved']} GB/s")
@@ -343,6 +376,9 @@ def main():
         pre = prefill_gemm_configs2(lib)
         log(f"prefill GEMM configs[2] (256-token chunk, one layer): {pre['us_per_layer_chunk']} us, "
             f"{pre['tflops_fp32_equiv']} TFLOP/s fp32-equiv, int8 MFMA util {pre['mfma_util']}")
+        qw = qwen35_ops_configs4(lib)
+        log(f"qwen35 ops configs[4]: GDN layer {qw['gdn_op']['us_per_token']} us/token, full attention "
+            f"{qw['full_attn_op']['us_per_token']} us/token at 4096 cached rows")
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -367,6 +403,7 @@ def main():
         "configs1_q8k_gemv": q8,
         "configs3_moe_ffn": moe,
         "configs4_gdn_scan": gdn,
+        "configs4_layer_ops": qw,
         "configs2_prefill_gemm": pre,
         "cpu_baseline": cpu,
     }
