@@ -93,12 +93,23 @@ struct Proj {
     const float* yadd;  // nullable: y = yadd + W.x
 };
 
+// Post-projection RMSNorm request: out = RMSNorm(y) * w (eps QEPS), one
+// k_rmsnorm launch after the projection.  (A last-block-done finisher inside
+// the GEMV was measured slower on MI355X: the agent-scope release each block
+// needs before counting itself writes back its XCD's L2.)
+struct PostNorm {
+    const float* w;
+    float* out;
+};
+
 // GEMVs of several matrices sharing the input x (n_in wide), with x
 // RMS-normalised by norm_w in the kernels' prologue when norm_w is set.
 // Q4_K / Q6_K matrices share one launch, Q8_0 matrices another; any other
 // format runs through the plain GEMV on an explicitly normalised copy in xn.
+// With `post` (one matrix only) the output's RMSNorm is produced too.
 int enqueue_proj(const Proj* p, int n, const float* x, int n_in, const float* norm_w, float* xn,
-                 hipStream_t st) {
+                 hipStream_t st, const PostNorm* post = nullptr) {
+    if (post && n != 1) return fail(-1, "enqueue_proj: post-norm needs one matrix");
     bool done[SEG_MAX] = {};
     if (n > SEG_MAX) return fail(-1, "enqueue_proj: %d matrices", n);
     auto fam = [](int c) { return c == DRACO_Q8_0 ? 0 : (c == DRACO_Q4_K || c == DRACO_Q6_K ? 1 : 2); };
@@ -115,6 +126,7 @@ int enqueue_proj(const Proj* p, int n, const float* x, int n_in, const float* no
             }
             if (draco_gemv_launch(*p[i].m, xin, p[i].y, p[i].yadd, 0, p[i].m->L.n_out, st))
                 return fail(-1, "plain GEMV launch rejected (code %d)", p[i].m->L.code);
+            if (post) dk_rmsnorm(p[i].y, post->w, post->out, p[i].m->L.n_out, QEPS, st);
             done[i] = true;
             continue;
         }
@@ -136,6 +148,7 @@ int enqueue_proj(const Proj* p, int n, const float* x, int n_in, const float* no
             done[j] = true;
         }
         if (draco_seg_launch(s, st)) return fail(-1, "segment GEMV launch rejected");
+        if (post) dk_rmsnorm(p[i].y, post->w, post->out, p[i].m->L.n_out, QEPS, st);
     }
     return 0;
 }
@@ -222,9 +235,8 @@ int enqueue_gdn(const GdnDev& g, const GdnBufs& b, hipStream_t st) {
     a.H = QH;
     if (draco_gdn_step_launch(a, st)) return fail(-1, "gdn step launch rejected");
     const Proj out[1] = {{g.out, b.x2o, b.h1}};
-    if (int rc = enqueue_proj(out, 1, b.on, g.d_in, nullptr, b.xn, st)) return rc;
-    dk_rmsnorm(b.x2o, g.post_norm, b.x2n, QH, QEPS, st);
-    return 0;
+    const PostNorm pn = {g.post_norm, b.x2n};
+    return enqueue_proj(out, 1, b.on, g.d_in, nullptr, b.xn, st, &pn);
 }
 
 int gdn_host(const float* h1, const GdnW* w, float* ssm, float* tail, float* x2n, float* x2_out) {
@@ -329,9 +341,8 @@ int enqueue_full(const FullDev& f, const FullBufs& b, int told, hipStream_t st) 
                      1.f / sqrtf((float)FHD), st, b.QG + FHD, 2 * FHD))
         return fail(-1, "attention launch rejected");
     const Proj out[1] = {{f.o, b.x2o, b.h1}};
-    if (int rc = enqueue_proj(out, 1, b.ao, f.nh * FHD, nullptr, b.xn, st)) return rc;
-    dk_rmsnorm(b.x2o, f.post_norm, b.x2n, QH, QEPS, st);
-    return 0;
+    const PostNorm pn = {f.post_norm, b.x2n};
+    return enqueue_proj(out, 1, b.ao, f.nh * FHD, nullptr, b.xn, st, &pn);
 }
 
 int full_host(const float* h1, const FullW* w, const float* Kr, const float* Vc, int told, int pos0, float* x2n,

@@ -298,30 +298,37 @@ __global__ __launch_bounds__(256) void k_attn_gqa(const float* __restrict__ q, c
     }
 }
 
-// Merge the splits of one q head (block of HD threads, one per head dim):
+// Merge the splits of one q head:
 //   out[h] = sum_s o_s e^(m_s - M) / sum_s l_s e^(m_s - M),  M = max_s m_s
-// The split weights go through LDS; the partial loads are unconditional
-// (indices clamped, weights of padding splits 0) and issued 32 at a time.
+// Block (h, d0) of 4 waves covers head dims d0*64 .. d0*64+63; wave q sums the
+// splits q, q+4, ... for its lane's dim and the four partial sums meet in
+// LDS.  The partial loads of the first batch are issued before the split
+// statistics are reduced, so the kernel costs about one memory round trip;
+// loads are unconditional (indices clamped, weights of padding splits 0).
 constexpr int MERGE_MAXS = 256;
+constexpr int MERGE_BATCH = 32;
 
-template <int HD>
 __global__ __launch_bounds__(256) void k_attn_merge(const float* __restrict__ part, float* __restrict__ out,
-                                                    int nsplit, const float* __restrict__ gate, int gstride) {
-    __shared__ float wsh[MERGE_MAXS + 32];
+                                                    int nsplit, int HD, const float* __restrict__ gate,
+                                                    int gstride) {
+    __shared__ float wsh[MERGE_MAXS + 4 * MERGE_BATCH];
     __shared__ float red[2][4];
-    const int h = blockIdx.x, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    constexpr int NW = HD / 64;
+    __shared__ float accs[4][64];
+    const int h = blockIdx.x, tid = threadIdx.x, lane = tid & 63, q = tid >> 6;
+    const int d = blockIdx.y * 64 + lane;
     const float* ph = part + (size_t)h * nsplit * (HD + 2);
-    float mloc = -INFINITY;
-    for (int k = tid; k < nsplit; k += HD) mloc = fmaxf(mloc, ph[(size_t)k * (HD + 2) + HD]);
-    mloc = wave_max(mloc);
-    if (lane == 0) red[0][w] = mloc;
-    __syncthreads();
-    float M = red[0][0];
+    float pv[MERGE_BATCH];
 #pragma unroll
-    for (int i = 1; i < NW; i++) M = fmaxf(M, red[0][i]);
+    for (int j = 0; j < MERGE_BATCH; j++) pv[j] = ph[(size_t)min(q + 4 * j, nsplit - 1) * (HD + 2) + d];
+    // split statistics (threads k, k + 256, ...)
+    float mloc = -INFINITY;
+    for (int k = tid; k < nsplit; k += 256) mloc = fmaxf(mloc, ph[(size_t)k * (HD + 2) + HD]);
+    mloc = wave_max(mloc);
+    if (lane == 0) red[0][q] = mloc;
+    lds_barrier();
+    const float M = fmaxf(fmaxf(red[0][0], red[0][1]), fmaxf(red[0][2], red[0][3]));
     float lsum = 0.f;
-    for (int k = tid; k < MERGE_MAXS + 32; k += HD) {
+    for (int k = tid; k < MERGE_MAXS + 4 * MERGE_BATCH; k += 256) {
         float wk = 0.f;
         if (k < nsplit) {
             const float mk = ph[(size_t)k * (HD + 2) + HD];
@@ -331,22 +338,25 @@ __global__ __launch_bounds__(256) void k_attn_merge(const float* __restrict__ pa
         wsh[k] = wk;
     }
     lsum = wave_sum(lsum);
-    if (lane == 0) red[1][w] = lsum;
-    __syncthreads();
-    float L = 0.f;
-#pragma unroll
-    for (int i = 0; i < NW; i++) L += red[1][i];
+    if (lane == 0) red[1][q] = lsum;
+    lds_barrier();
+    const float L = (red[1][0] + red[1][1]) + (red[1][2] + red[1][3]);
     float acc = 0.f;
-    for (int k0 = 0; k0 < nsplit; k0 += 32) {
-        float pv[32];
 #pragma unroll
-        for (int j = 0; j < 32; j++) pv[j] = ph[(size_t)min(k0 + j, nsplit - 1) * (HD + 2) + tid];
+    for (int j = 0; j < MERGE_BATCH; j++) acc = fmaf(pv[j], wsh[q + 4 * j], acc);
+    for (int k0 = 4 * MERGE_BATCH; k0 < nsplit; k0 += 4 * MERGE_BATCH) {
 #pragma unroll
-        for (int j = 0; j < 32; j++) acc = fmaf(pv[j], wsh[k0 + j], acc);
+        for (int j = 0; j < MERGE_BATCH; j++) pv[j] = ph[(size_t)min(k0 + q + 4 * j, nsplit - 1) * (HD + 2) + d];
+#pragma unroll
+        for (int j = 0; j < MERGE_BATCH; j++) acc = fmaf(pv[j], wsh[k0 + q + 4 * j], acc);
     }
-    float r = acc * (1.f / L);
-    if (gate) r *= 1.f / (1.f + expf(-gate[(size_t)h * gstride + tid]));
-    out[(size_t)h * HD + tid] = r;
+    accs[q][lane] = acc;
+    lds_barrier();
+    if (q == 0) {
+        float r = ((accs[0][lane] + accs[1][lane]) + (accs[2][lane] + accs[3][lane])) * (1.f / L);
+        if (gate) r *= 1.f / (1.f + expf(-gate[(size_t)h * gstride + d]));
+        out[(size_t)h * HD + d] = r;
+    }
 }
 
 // Merge the splits of one q head (block), one thread per head dim.  Lane k
@@ -558,9 +568,7 @@ int dk_attention(const float* q, const float* kc, const float* vc, float* part, 
         GQA_CASE(64, 4) GQA_CASE(64, 8) GQA_CASE(64, 16) GQA_CASE(128, 2) GQA_CASE(128, 4) GQA_CASE(128, 8)
         GQA_CASE(128, 16) GQA_CASE(256, 2) GQA_CASE(256, 4) GQA_CASE(256, 8) GQA_CASE(256, 16) return -1;
 #undef GQA_CASE
-        if (HD == 64) hipLaunchKernelGGL(k_attn_merge<64>, dim3(NH), dim3(64), 0, st, part, out, nsplit, gate, gstride);
-        else if (HD == 128) hipLaunchKernelGGL(k_attn_merge<128>, dim3(NH), dim3(128), 0, st, part, out, nsplit, gate, gstride);
-        else hipLaunchKernelGGL(k_attn_merge<256>, dim3(NH), dim3(256), 0, st, part, out, nsplit, gate, gstride);
+        hipLaunchKernelGGL(k_attn_merge, dim3(NH, HD / 64), dim3(256), 0, st, part, out, nsplit, HD, gate, gstride);
         return 0;
     }
     const dim3 grid(NKV, nsplit), block(64 * rep);
