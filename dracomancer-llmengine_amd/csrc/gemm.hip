@@ -214,6 +214,8 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_q6(const GemmArgs a) {
 #pragma unroll
             for (int q = 0; q < 4; q++) y[p][s][q] = 0.f;
     for (int b = 0; b < nb; b++) {
+        // token scales of this octet's parity-u tokens (2^k per token, k per super-block)
+        const float4 xs = *reinterpret_cast<const float4*>(a.xsc + (((size_t)oc * nb + b) * 2 + u) * 4);
 #pragma unroll
         for (int p = 0; p < RP; p++) {
             if (2 * (p0 + p) >= a.L.ntiles) break;
@@ -221,16 +223,44 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_q6(const GemmArgs a) {
             const int tl = tile < a.L.ntiles ? tile : a.L.ntiles - 1;
             const uint8_t* item = Wb + ((size_t)tl * nb + b) * DRACO_Q6T_ITEM;
             const float d = h2f(*reinterpret_cast<const uint16_t*>(item + 3328 + 2 * j));
+            // per super-block: int32 sums of sc * C over the 8 chunks (exact), and the
+            // fp32 sums of sc * (16-value sums) for the -32 offset
+            int acc[2][16];
+            float off[2][2];
+#pragma unroll
+            for (int qs = 0; qs < 2; qs++) {
+#pragma unroll
+                for (int i = 0; i < 16; i++) acc[qs][i] = 0;
+                off[qs][0] = off[qs][1] = 0.f;
+            }
 #pragma unroll 1
             for (int g2 = 0; g2 < 2; g2++) {
                 const int ls = j + 16 * (2 * g2 + u);  // tile-layout lane slot of (row j, group pair g2, half u)
                 const uint4 qa = ldu4(item + 16 * ls), qb = ldu4(item + 1024 + 16 * ls), qh = ldu4(item + 2048 + 16 * ls);
                 const uint32_t sc4 = *reinterpret_cast<const uint32_t*>(item + 3072 + 4 * ls);
+                // every activation operand of the four 32-value chunks of this group pair,
+                // loaded before the first MFMA (one memory round trip per group pair)
+                v4i A[4][2];
+                float4 s16[4][2];
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const int c = b * 8 + 4 * g2 + r;  // 32-value chunk: values 128*g2 + 32r .. +31
+#pragma unroll
+                    for (int qs = 0; qs < 2; qs++) {
+                        // A: digits of token 4*qs + t4A, half hA, from the octet layout
+                        const int mo = 4 * (4 * qs + t4A) + dgA;  // octet A-row (4*token + digit)
+                        const v4i av = *reinterpret_cast<const v4i*>(a.xdig + (((size_t)oc * nc + c) * 64 + mo + 32 * hA) * 16);
+                        A[r][qs] = asup ? av : (v4i){0, 0, 0, 0};
+                    }
+#pragma unroll
+                    for (int h = 0; h < 2; h++)
+                        s16[r][h] = *reinterpret_cast<const float4*>(a.xs16 + (((size_t)oc * ng + 2 * c + h) * 2 + u) * 4);
+                }
                 // this lane's scale for chunk r is that of group 8*g2 + 2r + u; the other half's comes from lane^32
                 const uint32_t sc4o = (uint32_t)__shfl_xor((int)sc4, 32, 64);
                 const uint32_t A4[4] = {qa.x, qa.y, qa.z, qa.w}, B4[4] = {qb.x, qb.y, qb.z, qb.w};
                 const uint32_t H4[4] = {qh.x, qh.y, qh.z, qh.w};
-#pragma unroll 1
+#pragma unroll
                 for (int r = 0; r < 4; r++) {
                     v4i Bv;
 #pragma unroll
@@ -242,41 +272,39 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_q6(const GemmArgs a) {
                         else vv = ((B4[q] >> 4) & 0x0F0F0F0Fu) | ((H4[q] >> 2) & 0x30303030u);
                         Bv[q] = (int)vv;
                     }
-                    const int c = b * 8 + 4 * g2 + r;  // 32-value chunk: values 128*g2 + 32r .. +31
                     // group of half h: 16-value group 2c + h
                     const int sc_u = (int)(int8_t)(sc4 >> (8 * r));    // half u
                     const int sc_o = (int)(int8_t)(sc4o >> (8 * r));   // half 1-u
+                    const int sc0 = u == 0 ? sc_u : sc_o, sc1 = u == 1 ? sc_u : sc_o;  // halves 0, 1
 #pragma unroll
                     for (int qs = 0; qs < 2; qs++) {
-                        // A: digits of token 4*qs + t4A, half hA, from the octet layout
-                        const int mo = 4 * (4 * qs + t4A) + dgA;  // octet A-row (4*token + digit)
-                        v4i Av = {0, 0, 0, 0};
-                        const v4i av = *reinterpret_cast<const v4i*>(a.xdig + (((size_t)oc * nc + c) * 64 + mo + 32 * hA) * 16);
-                        if (asup) Av = av;
-                        const v16i C = __builtin_amdgcn_mfma_i32_32x32x32_i8(Av, Bv, (v16i){}, 0, 0, 0);
+                        const v16i C = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[r][qs], Bv, (v16i){}, 0, 0, 0);
                         // C[i]: h = i/8, t4 = 2*((i/4)&1) + u, digit i%4
 #pragma unroll
-                        for (int tq = 0; tq < 2; tq++) {
-                            const int t4 = 2 * tq + u, tok8 = 4 * qs + t4;
-                            const float4 xs = *reinterpret_cast<const float4*>(
-                                a.xsc + (((size_t)oc * nb + b) * 2 + (tok8 & 1)) * 4);
-                            const float xsq = (tok8 >> 1) == 0 ? xs.x : ((tok8 >> 1) == 1 ? xs.y : ((tok8 >> 1) == 2 ? xs.z : xs.w));
-                            float part = 0.f;
+                        for (int i = 0; i < 16; i++) acc[qs][i] += (i < 8 ? sc0 : sc1) * C[i];
 #pragma unroll
-                            for (int h = 0; h < 2; h++) {
-                                const int i0 = 8 * h + 4 * tq;
-                                const float f = fold4(C[i0], C[i0 + 1], C[i0 + 2], C[i0 + 3]);
-                                const float4 s16 = *reinterpret_cast<const float4*>(
-                                    a.xs16 + (((size_t)oc * ng + 2 * c + h) * 2 + (tok8 & 1)) * 4);
-                                const float sv = (tok8 >> 1) == 0 ? s16.x : ((tok8 >> 1) == 1 ? s16.y : ((tok8 >> 1) == 2 ? s16.z : s16.w));
-                                const float scf = (float)(h == u ? sc_u : sc_o);
-                                part = fmaf(scf, fmaf(-32.f, sv, f * xsq), part);
-                            }
-                            y[p][qs][tq] = fmaf(d, part, y[p][qs][tq]);
+                        for (int tq = 0; tq < 2; tq++) {
+                            const int tq2 = 2 * qs + tq;  // token 4*qs + 2*tq + u = 2*tq2 + u
+                            const float4 v0 = s16[r][0], v1 = s16[r][1];
+                            const float sv0 = tq2 == 0 ? v0.x : (tq2 == 1 ? v0.y : (tq2 == 2 ? v0.z : v0.w));
+                            const float sv1 = tq2 == 0 ? v1.x : (tq2 == 1 ? v1.y : (tq2 == 2 ? v1.z : v1.w));
+                            off[qs][tq] = fmaf((float)sc1, sv1, fmaf((float)sc0, sv0, off[qs][tq]));
                         }
                     }
                 }
             }
+            // fold once per super-block: both halves' digit sums, then the token scale
+#pragma unroll
+            for (int qs = 0; qs < 2; qs++)
+#pragma unroll
+                for (int tq = 0; tq < 2; tq++) {
+                    const int tq2 = 2 * qs + tq;
+                    const float xsq = tq2 == 0 ? xs.x : (tq2 == 1 ? xs.y : (tq2 == 2 ? xs.z : xs.w));
+                    const int i0 = 4 * tq;
+                    const float f = fold4(acc[qs][i0] + acc[qs][i0 + 8], acc[qs][i0 + 1] + acc[qs][i0 + 9],
+                                          acc[qs][i0 + 2] + acc[qs][i0 + 10], acc[qs][i0 + 3] + acc[qs][i0 + 11]);
+                    y[p][qs][tq] = fmaf(d, fmaf(-32.f, off[qs][tq], f * xsq), y[p][qs][tq]);
+                }
         }
     }
 #pragma unroll
