@@ -22,8 +22,9 @@ namespace {
 
 // ------------------------------------------------------------- RMSNorm --
 // One block of 1024 threads; deterministic tree sum.
-__global__ __launch_bounds__(1024) void k_rmsnorm(const float* __restrict__ x, const float* __restrict__ w,
-                                                  float* __restrict__ out, int h, float eps) {
+// Any h: two passes over x.
+__global__ __launch_bounds__(1024) void k_rmsnorm_loop(const float* __restrict__ x, const float* __restrict__ w,
+                                                       float* __restrict__ out, int h, float eps) {
     __shared__ float red[16];
     float s = 0.f;
     for (int i = threadIdx.x; i < h; i += blockDim.x) s = fmaf(x[i], x[i], s);
@@ -35,6 +36,34 @@ __global__ __launch_bounds__(1024) void k_rmsnorm(const float* __restrict__ x, c
     for (int i = 0; i < nw; i++) tot += red[i];
     const float inv = 1.f / sqrtf(tot / (float)h + eps);
     for (int i = threadIdx.x; i < h; i += blockDim.x) out[i] = w ? x[i] * inv * w[i] : x[i] * inv;
+}
+
+// h <= RMS_PER_THREAD * blockDim.x: x and w are read once, held in registers.
+constexpr int RMS_PER_THREAD = 8;
+__global__ __launch_bounds__(1024) void k_rmsnorm(const float* __restrict__ x, const float* __restrict__ w,
+                                                  float* __restrict__ out, int h, float eps) {
+    __shared__ float red[16];
+    float v[RMS_PER_THREAD], wv8[RMS_PER_THREAD];
+    float s = 0.f;
+#pragma unroll
+    for (int k = 0; k < RMS_PER_THREAD; k++) {
+        const int i = threadIdx.x + k * blockDim.x;
+        v[k] = i < h ? x[i] : 0.f;
+        wv8[k] = (w && i < h) ? w[i] : 1.f;
+        s = fmaf(v[k], v[k], s);
+    }
+    s = wave_sum(s);
+    const int wv = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    if ((threadIdx.x & 63) == 0) red[wv] = s;
+    __syncthreads();
+    float tot = 0.f;
+    for (int i = 0; i < nw; i++) tot += red[i];
+    const float inv = 1.f / sqrtf(tot / (float)h + eps);
+#pragma unroll
+    for (int k = 0; k < RMS_PER_THREAD; k++) {
+        const int i = threadIdx.x + k * blockDim.x;
+        if (i < h) out[i] = w ? v[k] * inv * wv8[k] : v[k] * inv;
+    }
 }
 
 // ---------------------------------------------------- rope + KV append --
@@ -180,27 +209,6 @@ __global__ __launch_bounds__(1024) void k_attn_part(const float* __restrict__ q,
 // Each (q head, split) writes (o[HD], m, l) for k_attn_merge.
 constexpr int GQ_CH = 32;
 
-template <int REP>
-__device__ __forceinline__ float group_reduce_scatter(float (&v)[REP], int lane, int* head) {
-    int hd = 0;
-#pragma unroll
-    for (int n = REP, m = 32; n > 1; n >>= 1, m >>= 1) {
-        const bool up = (lane & m) != 0;
-        hd += up ? n / 2 : 0;
-#pragma unroll
-        for (int i = 0; i < n / 2; i++) {
-            const float send = up ? v[i] : v[i + n / 2];
-            const float keep = up ? v[i + n / 2] : v[i];
-            v[i] = keep + __shfl_xor(send, m, 64);
-        }
-    }
-    float r = v[0];
-#pragma unroll
-    for (int m = 32 / REP; m >= 1; m >>= 1) r += __shfl_xor(r, m, 64);
-    *head = hd;
-    return r;
-}
-
 template <int HD, int REP>
 __global__ __launch_bounds__(256) void k_attn_gqa(const float* __restrict__ q, const float* __restrict__ kc,
                                                   const float* __restrict__ vc, float* __restrict__ part,
@@ -242,20 +250,40 @@ __global__ __launch_bounds__(256) void k_attn_gqa(const float* __restrict__ q, c
         float vv[GQ_CH];
 #pragma unroll
         for (int r = 0; r < GQ_CH; r++) vv[r] = vg[(size_t)min(c0 + r, t1 - 1) * KD];
+        // all of the wave's rows through each reduce-scatter stage together,
+        // so a stage's shuffles are issued back to back and waited for once
+        float pd[RPW][REP];
 #pragma unroll
-        for (int i = 0; i < RPW; i++) {
-            float pd[REP];
+        for (int i = 0; i < RPW; i++)
 #pragma unroll
             for (int h = 0; h < REP; h++) {
                 float a = 0.f;
 #pragma unroll
                 for (int e = 0; e < DPL; e++) a = fmaf(qv[h][e], kx[i][e], a);
-                pd[h] = a;
+                pd[i][h] = a;
             }
-            int hs;
-            const float sres = group_reduce_scatter<REP>(pd, lane, &hs);
+        int hs = 0;
+#pragma unroll
+        for (int n = REP, m = 32; n > 1; n >>= 1, m >>= 1) {
+            const bool up = (lane & m) != 0;
+            hs += up ? n / 2 : 0;
+#pragma unroll
+            for (int i = 0; i < RPW; i++)
+#pragma unroll
+                for (int k = 0; k < n / 2; k++) {
+                    const float send = up ? pd[i][k] : pd[i][k + n / 2];
+                    const float keep = up ? pd[i][k + n / 2] : pd[i][k];
+                    pd[i][k] = keep + __shfl_xor(send, m, 64);
+                }
+        }
+#pragma unroll
+        for (int m = 32 / REP; m >= 1; m >>= 1)
+#pragma unroll
+            for (int i = 0; i < RPW; i++) pd[i][0] += __shfl_xor(pd[i][0], m, 64);
+#pragma unroll
+        for (int i = 0; i < RPW; i++) {
             const int r = w + 4 * i;
-            if ((lane & (64 / REP - 1)) == 0) sc[r * REP + hs] = r < nr ? sres * scale : -INFINITY;
+            if ((lane & (64 / REP - 1)) == 0) sc[r * REP + hs] = r < nr ? pd[i][0] * scale : -INFINITY;
         }
         lds_barrier();
         // softmax: wave w takes heads 2w (lanes 0-31) and 2w+1 (lanes 32-63), then +8
@@ -540,7 +568,14 @@ __global__ void k_pick_token(const int* ids, const int* cursor, int* cur) {
 
 // ------------------------------------------------------------ launchers --
 void dk_rmsnorm(const float* x, const float* w, float* out, int h, float eps, hipStream_t st) {
-    hipLaunchKernelGGL(k_rmsnorm, dim3(1), dim3(1024), 0, st, x, w, out, h, eps);
+    // one block; enough threads that each holds at most RMS_PER_THREAD values
+    if (h > 1024 * RMS_PER_THREAD) {
+        hipLaunchKernelGGL(k_rmsnorm_loop, dim3(1), dim3(1024), 0, st, x, w, out, h, eps);
+        return;
+    }
+    int nt = 64;
+    while (nt < 1024 && nt * RMS_PER_THREAD < h) nt *= 2;
+    hipLaunchKernelGGL(k_rmsnorm, dim3(1), dim3(nt), 0, st, x, w, out, h, eps);
 }
 
 void dk_rope_append(float* q, const float* k, const float* v, float* kc, float* vc, const float* tab,
