@@ -10,7 +10,7 @@ constexpr int ARGMAX_BLOCKS = 256;
 // heads with rep a power of two in [2, 16] and HD in {128, 256}; other shapes
 // run the per-head kernel.  (At HD 64 the per-head kernel is faster on MI355X:
 // its rows are 256 bytes, so the re-read K / V rows stay in L2 and the
-// per-row shuffle cost of the grouped kernel dominates.)
+// per-row lane-exchange cost of the grouped kernel dominates.)
 static inline bool attn_grouped(int NH, int NKV, int HD) {
     if (NKV < 1 || NH % NKV) return false;
     const int rep = NH / NKV;

@@ -116,7 +116,7 @@ __global__ __launch_bounds__(256) void k_rope_append(float* __restrict__ q, cons
 // (32 head dims each), so a lane's K slice is 8 float4 loads; lane d also
 // loads V[t][d] (and V[t][d+64] when HD = 128) for the pass's rows.  All of a
 // pass's K and V loads are issued before the first FMA; scores reduce over
-// the row's lanes with shuffles, the softmax over the wave, and P.V uses
+// the row's lanes with DPP moves, the softmax over the wave, and P.V uses
 // readlane broadcasts -- no LDS and no barrier.  Passes are merged with the
 // online-softmax rescale.  Each (q head, split) writes an unnormalised
 // partial (o[HD], m, l); k_attn_combine merges the splits:
@@ -166,8 +166,7 @@ __global__ __launch_bounds__(1024) void k_attn_part(const float* __restrict__ q,
             sc = fmaf(qv[i].z, kv[i].z, sc);
             sc = fmaf(qv[i].w, kv[i].w, sc);
         }
-#pragma unroll
-        for (int m = 1; m < LPT; m <<= 1) sc += __shfl_xor(sc, m, 64);
+        sc = group_sum<LPT>(sc);
         sc = valid ? sc * scale : -INFINITY;
         const float m_new = fmaxf(m_run, wave_max(sc));
         const float corr = m_run > -INFINITY ? expf(m_run - m_new) : 0.f;
@@ -199,9 +198,9 @@ __global__ __launch_bounds__(1024) void k_attn_part(const float* __restrict__ q,
 // per q head).  Rows are processed in sub-chunks of GQ_CH:
 //   scores  wave w takes rows w, w + 4, ...; a lane holds DPL = HD/64 dims of
 //           K and of each group q head, forms REP partial dots and reduces
-//           them with a reduce-scatter (each halving shuffle stage leaves a
+//           them with a reduce-scatter (each halving lane-exchange stage leaves a
 //           lane half of the heads), so a row costs REP - 1 + 6 - log2(REP)
-//           shuffles instead of 6 * REP; scores go to LDS as [row][head]
+//           exchanges instead of 6 * REP; scores go to LDS as [row][head]
 //   softmax per head over the sub-chunk, merged into a running (m, l) with
 //           the online rescale
 //   P.V     thread (d, head group) owns HPT = REP*HD/256 outputs of dim d,
@@ -250,8 +249,9 @@ __global__ __launch_bounds__(256) void k_attn_gqa(const float* __restrict__ q, c
         float vv[GQ_CH];
 #pragma unroll
         for (int r = 0; r < GQ_CH; r++) vv[r] = vg[(size_t)min(c0 + r, t1 - 1) * KD];
-        // all of the wave's rows through each reduce-scatter stage together,
-        // so a stage's shuffles are issued back to back and waited for once
+        // reduce-scatter over the heads: each stage halves the heads a lane
+        // holds and pairs it (lane_flip) with a lane keeping the other half;
+        // the exchanges are DPP / permlane moves, no LDS traffic
         float pd[RPW][REP];
 #pragma unroll
         for (int i = 0; i < RPW; i++)
@@ -273,13 +273,11 @@ __global__ __launch_bounds__(256) void k_attn_gqa(const float* __restrict__ q, c
                 for (int k = 0; k < n / 2; k++) {
                     const float send = up ? pd[i][k] : pd[i][k + n / 2];
                     const float keep = up ? pd[i][k + n / 2] : pd[i][k];
-                    pd[i][k] = keep + __shfl_xor(send, m, 64);
+                    pd[i][k] = keep + lane_flip(send, m);
                 }
         }
 #pragma unroll
-        for (int m = 32 / REP; m >= 1; m >>= 1)
-#pragma unroll
-            for (int i = 0; i < RPW; i++) pd[i][0] += __shfl_xor(pd[i][0], m, 64);
+        for (int i = 0; i < RPW; i++) pd[i][0] = group_sum<64 / REP>(pd[i][0]);
 #pragma unroll
         for (int i = 0; i < RPW; i++) {
             const int r = w + 4 * i;
@@ -290,16 +288,12 @@ __global__ __launch_bounds__(256) void k_attn_gqa(const float* __restrict__ q, c
         for (int h = 2 * w + (lane >> 5); h < REP; h += 8) {
             const int r = lane & 31;
             const float sv = sc[r * REP + h];
-            float cm = sv;
-#pragma unroll
-            for (int m = 16; m >= 1; m >>= 1) cm = fmaxf(cm, __shfl_xor(cm, m, 64));
+            const float cm = group_max<32>(sv);
             const float mo = mrun[h];
             const float mn = fmaxf(mo, cm);
             const float cr = mo == -INFINITY ? 0.f : expf(mo - mn);
             const float p = sv == -INFINITY ? 0.f : expf(sv - mn);
-            float ps = p;
-#pragma unroll
-            for (int m = 16; m >= 1; m >>= 1) ps += __shfl_xor(ps, m, 64);
+            const float ps = group_sum<32>(p);
             sc[r * REP + h] = p;
             if (r == 0) {
                 mrun[h] = mn;
@@ -425,7 +419,7 @@ __global__ __launch_bounds__(256) void k_attn_combine(const float* __restrict__ 
 // NH, NH + 1 normalise k head kv from kin[kv * 256] into kout[kv * 256] as
 // x * (r * k_norm), the two association orders of the reference.  cs holds
 // [32][cos, sin] of pos0 * rope_inv[t].  Rope partners t and t + 32 are lanes
-// of wave 0 and swap values with one shuffle.
+// of wave 0 and swap values with one permlane32 swap.
 __global__ __launch_bounds__(256) void k_fa_prep(const float* __restrict__ QG, float* __restrict__ Qr,
                                                  const float* __restrict__ kin, float* __restrict__ kout,
                                                  const float* __restrict__ qn, const float* __restrict__ kn,
@@ -441,7 +435,7 @@ __global__ __launch_bounds__(256) void k_fa_prep(const float* __restrict__ QG, f
     const float r = 1.f / sqrtf(n2 / 256.f + 1e-6f);
     float y = isq ? x * r * qn[t] : x * (r * kn[t]);
     if (w == 0) {
-        const float o = __shfl_xor(y, 32, 64);
+        const float o = lane_xor32(y);
         const float c = cs[2 * (lane & 31)], sn = cs[2 * (lane & 31) + 1];
         y = lane < 32 ? y * c - o * sn : o * sn + y * c;
     }
@@ -510,20 +504,12 @@ __global__ __launch_bounds__(256) void k_embed(const uint8_t* __restrict__ base,
 // -------------------------------------------------------------- argmax --
 // First index of the maximum (np.argmax semantics).  Stage 1: per-block
 // (value, index); stage 2: one block reduces the partials.
-__device__ __forceinline__ void am_merge(float& v, int& i, float v2, int i2) {
-    if (v2 > v || (v2 == v && i2 < i)) {
-        v = v2;
-        i = i2;
-    }
-}
-
 __global__ __launch_bounds__(256) void k_argmax_part(const float* __restrict__ x, int n, float* __restrict__ pv,
                                                      int* __restrict__ pi) {
     float v = -INFINITY;
     int idx = 0x7fffffff;
     for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) am_merge(v, idx, x[i], i);
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) am_merge(v, idx, __shfl_xor(v, m, 64), __shfl_xor(idx, m, 64));
+    group_argmax<64>(v, idx);
     __shared__ float sv[4];
     __shared__ int si[4];
     if ((threadIdx.x & 63) == 0) {
@@ -544,8 +530,7 @@ __global__ __launch_bounds__(64) void k_argmax_final(const float* __restrict__ p
     float v = -INFINITY;
     int idx = 0x7fffffff;
     for (int i = threadIdx.x; i < nb; i += 64) am_merge(v, idx, pv[i], pi[i]);
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) am_merge(v, idx, __shfl_xor(v, m, 64), __shfl_xor(idx, m, 64));
+    group_argmax<64>(v, idx);
     if (threadIdx.x == 0) out[slotp ? slotp[0] + 1 : slot] = idx;
 }
 

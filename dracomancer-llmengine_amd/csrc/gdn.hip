@@ -14,7 +14,7 @@
 // (v_lo = lane>>2, kq = lane&3) holds S[32kq .. 32kq+31][16w + v_lo].  Each
 // lane applies the reference's per-element operations in k order within its
 // chunk (decay, multiply, add, unfused); the four chunks of a column combine
-// with lane shuffles, so the delta rule needs no LDS and no barrier.  The conv
+// with DPP moves, so the delta rule needs no LDS and no barrier.  The conv
 // runs on threads 0..383 (one channel each: q, k of head j and v of head h,
 // tail in registers); only the block that owns a channel writes its tail back
 // (q/k channels: the block with h < NHQ).  l2 norms and the gated rms reduce
@@ -170,8 +170,7 @@ __global__ __launch_bounds__(512) void k_gdn_scan(const GdnArgs a) {
             s[i] = s[i] * g;
             sk = sk + s[i] * ck[32 * kq + i];
         }
-        sk += __shfl_xor(sk, 1, 64);
-        sk += __shfl_xor(sk, 2, 64);
+        sk = group_sum<4>(sk);
         const float d = (cv[v] - sk) * b;
         float o = 0.f;
 #pragma unroll
@@ -179,8 +178,7 @@ __global__ __launch_bounds__(512) void k_gdn_scan(const GdnArgs a) {
             s[i] = s[i] + ck[32 * kq + i] * d;
             o = o + s[i] * cq[32 * kq + i];
         }
-        o += __shfl_xor(o, 1, 64);
-        o += __shfl_xor(o, 2, 64);
+        o = group_sum<4>(o);
         // (4) gated rms over the 128 columns
         o = o * scale;
         float o2 = kq == 0 ? o * o : 0.f;

@@ -74,10 +74,9 @@ __global__ __launch_bounds__(64) void k_gemm_digits(const float* __restrict__ X,
     }
     // 16- and 32-value sums (4 and 8 consecutive threads)
     float s = (v.x + v.y) + (v.z + v.w);
-    s += __shfl_xor(s, 1, 64);
-    s += __shfl_xor(s, 2, 64);
+    s = group_sum<4>(s);
     if ((i & 3) == 0) xs16[(((size_t)oc * ng + b * 16 + (i >> 2)) * 2 + u8) * 4 + q8] = s;
-    s += __shfl_xor(s, 4, 64);
+    s += dpp<DPP_MIRROR8>(s);  // the other 4 lanes of the 8, uniform after the step above
     if ((i & 7) == 0) xs32[(((size_t)oc * nc + c) * 2 + u8) * 4 + q8] = s;
     // the digit fold gives X / 2^21, and x = (X / 2^21) * 2^k
     if (i == 0) xsc[(((size_t)oc * nb + b) * 2 + u8) * 4 + q8] = __builtin_bit_cast(float, (uint32_t)(127 + k) << 23);
@@ -257,7 +256,7 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_q6(const GemmArgs a) {
                         s16[r][h] = *reinterpret_cast<const float4*>(a.xs16 + (((size_t)oc * ng + 2 * c + h) * 2 + u) * 4);
                 }
                 // this lane's scale for chunk r is that of group 8*g2 + 2r + u; the other half's comes from lane^32
-                const uint32_t sc4o = (uint32_t)__shfl_xor((int)sc4, 32, 64);
+                const uint32_t sc4o = lane_xor32(sc4);
                 const uint32_t A4[4] = {qa.x, qa.y, qa.z, qa.w}, B4[4] = {qb.x, qb.y, qb.z, qb.w};
                 const uint32_t H4[4] = {qh.x, qh.y, qh.z, qh.w};
 #pragma unroll

@@ -53,13 +53,6 @@ constexpr int SEG_ROWS = 4 * SEG_R;       // rows per block (4 waves)
 constexpr int XP_MAXV = 4;                // float4s of x per thread held by the prologue
 
 // ------------------------------------------------------------------ k_dq --
-__device__ __forceinline__ void am_merge(float& v, int& i, float v2, int i2) {
-    if (v2 > v || (v2 == v && i2 < i)) {
-        v = v2;
-        i = i2;
-    }
-}
-
 // Segment of global tile T.  Segment first tiles ascend; unused slots (and
 // the "up" half of a SwiGLU pair) hold 1 << 30, so three comparisons against
 // kernel-argument values (loaded once, kept in SGPRs) replace a loop.
@@ -277,12 +270,8 @@ __global__ __launch_bounds__(64 * NW) void k_dq(const SegLaunch a) {
         }
         if (cp == ipt - 1) {  // tile done: reduce lanes (g) and waves, run the epilogue
             float acc = aD - aM, acc2 = aD2 - aM2;
-            acc += __shfl_xor(acc, 16, 64);
-            acc += __shfl_xor(acc, 32, 64);
-            if (DUAL) {
-                acc2 += __shfl_xor(acc2, 16, 64);
-                acc2 += __shfl_xor(acc2, 32, 64);
-            }
+            acc = rows_sum(acc);
+            if (DUAL) acc2 = rows_sum(acc2);
             if (lane < 16) {
                 red[w * 16 + j] = acc;
                 if (DUAL) red[(NW + w) * 16 + j] = acc2;
@@ -310,7 +299,7 @@ __global__ __launch_bounds__(64 * NW) void k_dq(const SegLaunch a) {
                 case EPI_ROPE_Q:
                 case EPI_ROPE_K: {
                     // pairs (2i, 2i+1) of a head, src/m6_engine.c:134-143
-                    const float pv = __shfl_xor(v, 1, 64);
+                    const float pv = dpp<DPP_XOR1>(v);
                     float o = v;
                     if (row % a.head_dim < a.rot) {
                         const float c = ep0, sn = ep1;
@@ -329,8 +318,7 @@ __global__ __launch_bounds__(64 * NW) void k_dq(const SegLaunch a) {
                     if (ok) c_y[row] = v;
                     float bv = ok ? v : -INFINITY;
                     int bi = ok ? row : 0x7fffffff;
-#pragma unroll
-                    for (int m = 8; m >= 1; m >>= 1) am_merge(bv, bi, __shfl_xor(bv, m, 64), __shfl_xor(bi, m, 64));
+                    group_argmax<16>(bv, bi);
                     am_merge(am_v, am_i, bv, bi);
                     break;
                 }
@@ -538,8 +526,7 @@ __global__ __launch_bounds__(256) void k_argmax_finalize(const float* __restrict
     float v = -INFINITY;
     int idx = 0x7fffffff;
     for (int i = tid; i < nb; i += 256) am_merge(v, idx, pv[i], pi[i]);
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) am_merge(v, idx, __shfl_xor(v, m, 64), __shfl_xor(idx, m, 64));
+    group_argmax<64>(v, idx);
     if (lane == 0) {
         sv[wv] = v;
         si[wv] = idx;

@@ -88,15 +88,7 @@ __device__ __forceinline__ void route_wave(const float* __restrict__ logits, int
                 bv = p[q];
                 bi = lane + 64 * q;
             }
-#pragma unroll
-        for (int m = 32; m >= 1; m >>= 1) {
-            const float v2 = __shfl_xor(bv, m, 64);
-            const int i2 = __shfl_xor(bi, m, 64);
-            if (v2 > bv || (v2 == bv && i2 < bi)) {
-                bv = v2;
-                bi = i2;
-            }
-        }
+        group_argmax<64>(bv, bi);
 #pragma unroll
         for (int q = 0; q < PER; q++)
             if (lane + 64 * q == bi) p[q] = -2.f;
@@ -271,12 +263,8 @@ __global__ __launch_bounds__(64 * NW) void k_moe_grp(const MoeArgs a) {
         }
         if (cp == ipt - 1) {
             float acc = aD - aM, acc2 = aD2 - aM2;
-            acc += __shfl_xor(acc, 16, 64);
-            acc += __shfl_xor(acc, 32, 64);
-            if (DUAL) {
-                acc2 += __shfl_xor(acc2, 16, 64);
-                acc2 += __shfl_xor(acc2, 32, 64);
-            }
+            acc = rows_sum(acc);
+            if (DUAL) acc2 = rows_sum(acc2);
             if (lane < 16) {
                 red[w * 16 + j] = acc;
                 if (DUAL) red[(NW + w) * 16 + j] = acc2;
@@ -378,8 +366,7 @@ __global__ __launch_bounds__(64 * NW) void k_moe_down(const MoeArgs a) {
             }
         }
         float acc = aD - aM;
-        acc += __shfl_xor(acc, 16, 64);
-        acc += __shfl_xor(acc, 32, 64);
+        acc = rows_sum(acc);
         if (lane < 16) red[w * 16 + j] = acc;
         lds_barrier();
         if (tid < 16) {

@@ -41,15 +41,7 @@ __global__ __launch_bounds__(256) void k_q8k_quantize(const float* __restrict__ 
     // first index of the largest |x|
     float ax = fabsf(xv);
     int idx = t;
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) {
-        const float a2 = __shfl_xor(ax, m, 64);
-        const int i2 = __shfl_xor(idx, m, 64);
-        if (a2 > ax || (a2 == ax && i2 < idx)) {
-            ax = a2;
-            idx = i2;
-        }
-    }
+    group_argmax<64>(ax, idx);
     if (lane == 0) {
         wv[w] = ax;
         wi[w] = idx;
@@ -75,9 +67,7 @@ __global__ __launch_bounds__(256) void k_q8k_quantize(const float* __restrict__ 
         q = q < 127 ? q : 127;
         d = 1.f / iscale;
     }
-    int s = q;
-#pragma unroll
-    for (int m = 1; m < 16; m <<= 1) s += __shfl_xor(s, m, 64);
+    const int s = group_reduce<16>(q, OpAdd{});
     uint8_t* blk = out + ((size_t)v * (n / 256) + b) * Q8K_BLOCK_BYTES;
     blk[4 + t] = (uint8_t)(int8_t)q;
     if ((t & 15) == 0) *reinterpret_cast<int16_t*>(blk + 260 + 2 * (t >> 4)) = (int16_t)s;
@@ -222,10 +212,8 @@ __global__ __launch_bounds__(64 * NW) void k_dq8(const Q8Launch a) {
             }
             if (ISUMS) {
                 int s = isc[0], m = imn[0];
-                s += __shfl_xor(s, 16, 64);
-                s += __shfl_xor(s, 32, 64);
-                m += __shfl_xor(m, 16, 64);
-                m += __shfl_xor(m, 32, 64);
+                s = rows_sum_i(s);
+                m = rows_sum_i(m);
                 const int row = (ct + a.tile0) * 16 + j;
                 if (g == 0 && row >= a.row0 && row < a.row1) {
                     a.isc[(size_t)row * nb + cb] = s;
@@ -237,8 +225,7 @@ __global__ __launch_bounds__(64 * NW) void k_dq8(const Q8Launch a) {
 #pragma unroll
             for (int v = 0; v < NB; v++) {
                 float s = yacc[v];
-                s += __shfl_xor(s, 16, 64);
-                s += __shfl_xor(s, 32, 64);
+                s = rows_sum(s);
                 if (lane < 16) red[(v * NW + w) * 16 + j] = s;
                 yacc[v] = 0.f;
             }

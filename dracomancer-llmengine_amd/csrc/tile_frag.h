@@ -120,14 +120,12 @@ __device__ __forceinline__ float dot_q6(const Frag& f, const int8_t* xa, const f
 // k = ilogb(max |x| of the group) - 5 (clamped at -100).  X = rint(x*2^(21-k))
 // = d0*2^21 + d1*2^14 + d2*2^7 + d3, |X| < 2^27, d0 signed, d1..d3 in [0,127].
 // The four threads of a group (consecutive lanes, i4 % 4 = 0..3) must call it
-// together: the group maximum and sum use lane shuffles.
+// together: the group maximum and sum use DPP quad moves.
 __device__ __forceinline__ void digits4(float4 v, int i4, int8_t* xd, float2* xsm) {
     float am = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
     float sum = (v.x + v.y) + (v.z + v.w);
-    am = fmaxf(am, __shfl_xor(am, 1, 64));
-    am = fmaxf(am, __shfl_xor(am, 2, 64));
-    sum += __shfl_xor(sum, 1, 64);
-    sum += __shfl_xor(sum, 2, 64);
+    am = group_max<4>(am);
+    sum = group_sum<4>(sum);
     const int k = am > 0.f ? max(ilogbf(am) - 5, -100) : 0;
     const float up = __builtin_bit_cast(float, (uint32_t)(127 + 21 - k) << 23);  // 2^(21-k)
     const uint32_t X0 = (uint32_t)(int)rintf(v.x * up), X1 = (uint32_t)(int)rintf(v.y * up);
