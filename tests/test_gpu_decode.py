@@ -127,6 +127,38 @@ def test_direct_ops_match_oracle(oracle):
         assert rel_err(out, outr) <= 1e-5
 
 
+@pytest.mark.parametrize("hd,nh,nkv", [(128, 3, 1), (128, 2, 2), (64, 5, 1)])
+def test_attn_op_head_shapes_match_oracle(oracle, hd, nh, nkv):
+    """The per-head attention kernel and its last-block split merge at head
+    dim 128 (GQA ratios 3 and 1) and head dim 64 with ratio 5 (shapes the
+    grouped kernel does not take; m6_llama_attn_op takes head dims 64 and
+    128): 48 tokens through m6_llama_attn_op with a 256-row cache (8 splits),
+    against the oracle after every token."""
+    import dataclasses
+    from tests_oracle_engine import oracle_engine
+    from dracohip import lib
+    cfg = dataclasses.replace(models.TINY_Q8, name=f"attn-{hd}-{nh}-{nkv}", head_dim=hd, n_head=nh, n_kv=nkv,
+                              max_t=256)
+    model = models.build_llama(cfg, 0)
+    lib.load().draco_reset()
+    drv = LlamaDriver(model, hip_engine_lib())
+    ref = LlamaDriver(model, oracle_engine(oracle))
+    L = drv.engine.cdll
+    rng = np.random.default_rng(5)
+    worst = 0.0
+    for step in range(48):
+        xn = rng.standard_normal(cfg.hidden, dtype=np.float32)
+        out = np.zeros(cfg.hidden, np.float32)
+        outr = np.zeros(cfg.hidden, np.float32)
+        print(f"[attn_op] hd {hd} nh {nh} nkv {nkv} step {step}", flush=True)
+        L.m6_llama_attn_op(pf(xn), drv.descs[0].attn_p, step, pf(out))
+        oracle.lib.or_llama_attn_op(pf(xn), ref.descs[0].attn_p, step, pf(outr))
+        e = rel_err(out, outr)
+        worst = max(worst, e)
+        assert e <= 1e-5, (step, e)
+    print(f"[attn_op] hd {hd} nh {nh} nkv {nkv}: worst {worst:.2e}")
+
+
 def test_smol360m_device_generate():
     """SmolLM2-360M-shaped Q8_0, 32 prompt + 64 greedy tokens."""
     g = golden("smol360m.npz")
