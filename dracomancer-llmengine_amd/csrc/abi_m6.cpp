@@ -81,8 +81,9 @@ struct DevFfn {
 struct Work {
     float *x = nullptr, *xn = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *att = nullptr,
           *part = nullptr, *g = nullptr, *u = nullptr;
+    float* xe = nullptr;      // next token's embedding, written by the head's argmax (generation)
     unsigned* cnt = nullptr;  // attention merge counters (one per kv head), zero at rest
-    size_t cap_h = 0, cap_q = 0, cap_k = 0, cap_part = 0, cap_ff = 0;
+    size_t cap_h = 0, cap_xn = 0, cap_xe = 0, cap_q = 0, cap_k = 0, cap_part = 0, cap_ff = 0;
 };
 
 struct DevModel {
@@ -261,7 +262,8 @@ int ensure_work(Work& w, int H, int QD, int KD, int NH, int HD, int max_t, int F
         DRACO_HIP(hipDeviceSynchronize());
     }
     if (grow(&w.x, &w.cap_h, H + 64)) return -2;
-    if (w.cap_h > 0 && !w.xn) DRACO_HIP(hipMalloc(&w.xn, sizeof(float) * w.cap_h));
+    if (grow(&w.xn, &w.cap_xn, H + 64)) return -2;
+    if (grow(&w.xe, &w.cap_xe, H + 64)) return -2;
     if (w.cap_q < (size_t)QD) {
         size_t c = w.cap_q;
         if (grow(&w.q, &c, QD)) return -2;
@@ -431,19 +433,21 @@ int enqueue_gateup(DevFfn* f, Work& w, const float* x, int norm, const float* no
     return 0;
 }
 
-// enqueue one llama layer on the device (x in w.x, updated in place):
+// enqueue one llama layer on the device (x in w.x, updated in place; with
+// xin set the layer reads its input from xin and leaves its output in w.x):
 // five launches -- qkv(+norm,+rope,+append), attention(+merge), wo(+residual),
 // gate/up(+norm,+SwiGLU), down(+residual)
-int enqueue_layer(DevModel* m, int l, float eps, hipStream_t st) {
+int enqueue_layer(DevModel* m, int l, float eps, hipStream_t st, const float* xin = nullptr) {
     DevAttn* a = m->attn[l];
     DevFfn* f = m->ffn[l];
     Work& w = m->w;
     const int H = m->h;
-    if (int rc = enqueue_qkv(a, w, w.x, 1, m->anorm[l], eps, m->state, l, st)) return rc;
+    const float* x0 = xin ? xin : w.x;
+    if (int rc = enqueue_qkv(a, w, x0, 1, m->anorm[l], eps, m->state, l, st)) return rc;
     if (dk_attention(w.q, a->kc, a->vc, w.part, w.cnt, w.att, m->state, l, a->NH, a->NKV, a->HD, a->max_t,
                      a->scale, st))
         return fail(-1, "attention launch");
-    if (draco_gemv_launch(*a->wo, w.att, w.x, w.x, 0, H, st)) return fail(-1, "gemv o");
+    if (draco_gemv_launch(*a->wo, w.att, w.x, x0, 0, H, st)) return fail(-1, "gemv o");
     if (int rc = enqueue_gateup(f, w, w.x, 1, m->fnorm[l], eps, st)) return rc;
     if (draco_gemv_launch(*f->d, w.g, w.x, w.x, 0, H, st)) return fail(-1, "gemv down");
     return 0;
@@ -713,10 +717,14 @@ int draco_llama_generate(const void* layers_v, int n_layer, int h, float eps, co
     DRACO_HIP(hipMemcpyAsync(dtok, ht.data(), sizeof(int) * (ntok + 64), hipMemcpyHostToDevice, st));
     if (int rc = upload_state(m, pos0, st)) return report(rc, "draco_llama_generate");
     (void)cur;
+    // With the fused head, a decode step's input embedding was decoded by the
+    // previous step's argmax into w.xe (the first one by an embedding launch
+    // after the prompt), and layer 0 reads it from there.
     auto step = [&](bool decode) -> int {
-        dk_embed(*em, dtok, cursor, m->w.x, st);
+        const bool emb_ready = decode && fused_head;
+        if (!emb_ready) dk_embed(*em, dtok, cursor, m->w.x, st);
         for (int l = 0; l < n_layer; l++)
-            if (int rc = enqueue_layer(m, l, eps, st)) return rc;
+            if (int rc = enqueue_layer(m, l, eps, st, (emb_ready && l == 0) ? m->w.xe : nullptr)) return rc;
         if (!decode) {
             dk_advance(m->state, n_layer, cursor, st);
             return 0;
@@ -737,6 +745,9 @@ int draco_llama_generate(const void* layers_v, int n_layer, int h, float eps, co
             sl.cursor = cursor;
             sl.advance_state = m->state;
             sl.advance_layers = n_layer;
+            sl.emb = em->dev;
+            sl.emb_L = em->L;
+            sl.emb_out = m->w.xe;
             if (draco_seg_launch(sl, st)) return fail(-1, "head launch rejected");
             return 0;
         }
@@ -769,6 +780,7 @@ int draco_llama_generate(const void* layers_v, int n_layer, int h, float eps, co
         if (use_graph) DRACO_HIP(hipGraphLaunch(gx[0], st));
         else if (int rc = step(false)) return report(rc, "draco_llama_generate");
     }
+    if (fused_head) dk_embed(*em, dtok, cursor, m->w.xe, st);
     DRACO_HIP(hipEventRecord(e1, st));
     for (int i = 0; i < n_gen; i++) {
         if (use_graph) DRACO_HIP(hipGraphLaunch(gx[1], st));

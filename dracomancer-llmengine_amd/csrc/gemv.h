@@ -73,6 +73,9 @@ struct SegLaunch {
     const int* cursor;  // token written to tokens[*cursor + 1], then *cursor += 1
     int* advance_state; // nullable: pos and every layer's tlen += 1
     int advance_layers;
+    const uint8_t* emb; // with emb_out set: the new token's row of emb (layout emb_L) -> emb_out
+    DracoLayout emb_L;
+    float* emb_out;
 };
 
 // Builds grid ranges for every segment and launches the fused kernel.

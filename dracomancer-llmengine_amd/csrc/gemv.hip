@@ -42,6 +42,7 @@
 #include <mutex>
 
 #include "dev_common.h"
+#include "embed_dev.h"
 #include "formats.h"
 #include "gemv.h"
 #include "tile_frag.h"
@@ -52,18 +53,90 @@ constexpr int SEG_R = 2;                  // rows per wave in k_seg (Q8_0)
 constexpr int SEG_ROWS = 4 * SEG_R;       // rows per block (4 waves)
 constexpr int XP_MAXV = 4;                // float4s of x per thread held by the prologue
 
+// ------------------------------------------------------- kernel arguments --
+// What the kernels read of a SegLaunch, packed.  The launch cost on MI355X
+// grows with the kernel-argument size (80 bytes of padding measured at +0.2 to
+// +0.4 us per launch, same kernel code), so the host request -- four full
+// layouts and fields only the host or the finalize launch needs -- is not
+// passed as is.
+struct SegK {
+    const uint8_t* base;  // K-quant tiles; Q8_0: the quants (layout off[0])
+    const uint8_t* aux;   // Q8_0: the fp16 scales (layout off[1])
+    float* y;
+    const float* yadd;
+    int code, n_out, nb, epi;
+    int row0, row1;
+    int first;  // first global tile (K-quants) or first grid block (Q8_0)
+    int tile0;
+};
+
+struct SegKArgs {
+    SegK seg[SEG_MAX];
+    const float* x;
+    const float* norm_w;
+    float* xn_out;
+    const float* rope_tab;
+    const int* state;
+    float* kc;
+    float* vc;
+    float* am_val;
+    int* am_idx;
+    int nseg, total_tiles, n_in, do_norm;
+    float eps;
+    int layer, head_dim, rot, kv_dim;
+};
+
+SegKArgs seg_kargs(const SegLaunch& a, bool q80) {
+    SegKArgs k = {};
+    for (int i = 0; i < SEG_MAX; i++) {
+        const SegDesc& d = a.seg[i];
+        SegK& o = k.seg[i];
+        o.base = q80 && d.base ? d.base + d.L.off[0] : d.base;
+        o.aux = q80 && d.base ? d.base + d.L.off[1] : nullptr;
+        o.y = d.y;
+        o.yadd = d.yadd;
+        o.code = d.L.code;
+        o.n_out = d.L.n_out;
+        o.nb = d.L.nb;
+        o.epi = d.epi;
+        o.row0 = d.row0;
+        o.row1 = d.row1;
+        o.first = q80 ? d.first_block : d.first_tile;
+        o.tile0 = d.tile0;
+    }
+    k.x = a.x;
+    k.norm_w = a.norm_w;
+    k.xn_out = a.xn_out;
+    k.rope_tab = a.rope_tab;
+    k.state = a.state;
+    k.kc = a.kc;
+    k.vc = a.vc;
+    k.am_val = a.am_val;
+    k.am_idx = a.am_idx;
+    k.nseg = a.nseg;
+    k.total_tiles = a.total_tiles;
+    k.n_in = a.n_in;
+    k.do_norm = a.do_norm;
+    k.eps = a.eps;
+    k.layer = a.layer;
+    k.head_dim = a.head_dim;
+    k.rot = a.rot;
+    k.kv_dim = a.kv_dim;
+    return k;
+}
+
 // ------------------------------------------------------------------ k_dq --
 // Segment of global tile T.  Segment first tiles ascend; unused slots (and
 // the "up" half of a SwiGLU pair) hold 1 << 30, so three comparisons against
 // kernel-argument values (loaded once, kept in SGPRs) replace a loop.
-__device__ __forceinline__ int seg_of_tile(const SegLaunch& a, int T) {
-    return (T >= a.seg[1].first_tile) + (T >= a.seg[2].first_tile) + (T >= a.seg[3].first_tile);
+__device__ __forceinline__ int seg_of_tile(const SegKArgs& a, int T) {
+    return (T >= a.seg[1].first) + (T >= a.seg[2].first) + (T >= a.seg[3].first);
 }
 
 // Fields of segment si picked with selects over compile-time indices (no
 // dynamic indexing into the kernel arguments, which costs a scalar load).
 template <class F>
-__device__ __forceinline__ auto seg_pick(const SegLaunch& a, int si, F f) -> decltype(f(a.seg[0])) {
+__device__ __forceinline__ auto seg_pick(const SegKArgs& a, int si, F f) -> decltype(f(a.seg[0])) {
     auto r = f(a.seg[0]);
     if (si == 1) r = f(a.seg[1]);
     if (si == 2) r = f(a.seg[2]);
@@ -73,7 +146,7 @@ __device__ __forceinline__ auto seg_pick(const SegLaunch& a, int si, F f) -> dec
 
 // FM: 1 = Q4_K segments only, 2 = Q6_K only, 3 = both (per-tile switch).
 template <int NW, int FM, bool DUAL>
-__global__ __launch_bounds__(64 * NW) void k_dq(const SegLaunch a) {
+__global__ __launch_bounds__(64 * NW) void k_dq(const SegKArgs a) {
     extern __shared__ __align__(16) uint8_t smem[];
     constexpr int NT = 64 * NW;
     const int n_in = a.n_in, nb = n_in >> 8, ng = n_in >> 4, n4 = n_in >> 2;
@@ -99,14 +172,14 @@ __global__ __launch_bounds__(64 * NW) void k_dq(const SegLaunch a) {
     };
     auto tile_ref = [&](int T) {
         const int si = seg_of_tile(a, T);
-        const bool q4 = FM == 3 ? seg_pick(a, si, [](const SegDesc& d) { return d.L.code; }) == DRACO_Q4_K : FM == 1;
+        const bool q4 = FM == 3 ? seg_pick(a, si, [](const SegK& d) { return d.code; }) == DRACO_Q4_K : FM == 1;
         const size_t ib = q4 ? DRACO_Q4T_ITEM : DRACO_Q6T_ITEM;
-        const int tl = T - seg_pick(a, si, [](const SegDesc& d) { return d.first_tile; }) +
-                       seg_pick(a, si, [](const SegDesc& d) { return d.tile0; });
+        const int tl = T - seg_pick(a, si, [](const SegK& d) { return d.first; }) +
+                       seg_pick(a, si, [](const SegK& d) { return d.tile0; });
         const size_t off = (size_t)tl * nb * ib;
         TileRef r;
-        r.p = seg_pick(a, si, [](const SegDesc& d) { return d.base; }) + off;
-        r.p2 = DUAL ? seg_pick(a, si + 1, [](const SegDesc& d) { return d.base; }) + off : r.p;
+        r.p = seg_pick(a, si, [](const SegK& d) { return d.base; }) + off;
+        r.p2 = DUAL ? seg_pick(a, si + 1, [](const SegK& d) { return d.base; }) + off : r.p;
         r.q4 = q4;
         return r;
     };
@@ -219,20 +292,20 @@ __global__ __launch_bounds__(64 * NW) void k_dq(const SegLaunch a) {
     auto step = [&](Frag& cur, Frag& nxt, Frag& cur2, Frag& nxt2) {
         if (cp == 0) {
             const int si = seg_of_tile(a, ct);
-            c_epi = seg_pick(a, si, [](const SegDesc& d) { return d.epi; });
-            c_row = (ct - seg_pick(a, si, [](const SegDesc& d) { return d.first_tile; }) +
-                     seg_pick(a, si, [](const SegDesc& d) { return d.tile0; })) * 16;
-            c_r0 = seg_pick(a, si, [](const SegDesc& d) { return d.row0; });
-            c_r1 = seg_pick(a, si, [](const SegDesc& d) { return d.row1; });
-            c_y = seg_pick(a, si, [](const SegDesc& d) { return d.y; });
-            if (FM == 3) cq4 = seg_pick(a, si, [](const SegDesc& d) { return d.L.code; }) == DRACO_Q4_K;
+            c_epi = seg_pick(a, si, [](const SegK& d) { return d.epi; });
+            c_row = (ct - seg_pick(a, si, [](const SegK& d) { return d.first; }) +
+                     seg_pick(a, si, [](const SegK& d) { return d.tile0; })) * 16;
+            c_r0 = seg_pick(a, si, [](const SegK& d) { return d.row0; });
+            c_r1 = seg_pick(a, si, [](const SegK& d) { return d.row1; });
+            c_y = seg_pick(a, si, [](const SegK& d) { return d.y; });
+            if (FM == 3) cq4 = seg_pick(a, si, [](const SegK& d) { return d.code; }) == DRACO_Q4_K;
             if (tid < 16) {
-                const int n_out = seg_pick(a, si, [](const SegDesc& d) { return d.L.n_out; });
+                const int n_out = seg_pick(a, si, [](const SegK& d) { return d.n_out; });
                 const int row = c_row + tid;
                 const int rr = row < n_out ? row : n_out - 1;
                 const float* src = nullptr;
                 if (c_epi == EPI_RESID) {
-                    src = seg_pick(a, si, [](const SegDesc& d) { return d.yadd; }) + rr;
+                    src = seg_pick(a, si, [](const SegK& d) { return d.yadd; }) + rr;
                 } else if ((c_epi == EPI_ROPE_Q || c_epi == EPI_ROPE_K) && rr % a.head_dim < a.rot) {
                     src = a.rope_tab + ((size_t)pos * (a.rot / 2) + (rr % a.head_dim) / 2) * 2;
                 }
@@ -359,12 +432,11 @@ struct FQ80 {
         }
         sx[0] = 0.f;
     }
-    __device__ static float dot(const uint8_t* base, const DracoLayout& L, int row, int u, const float* xv,
-                                const float* sx) {
+    __device__ static float dot(const SegK& sg, int row, int u, const float* xv, const float* sx) {
         (void)sx;
-        const size_t blk = (size_t)row * L.nb + u;
-        const uint4 q0 = ldu4(base + L.off[0] + blk * 32), q1 = ldu4(base + L.off[0] + blk * 32 + 16);
-        const float d = h2f(*reinterpret_cast<const uint16_t*>(base + L.off[1] + blk * 2));
+        const size_t blk = (size_t)row * sg.nb + u;
+        const uint4 q0 = ldu4(sg.base + blk * 32), q1 = ldu4(sg.base + blk * 32 + 16);
+        const float d = h2f(*reinterpret_cast<const uint16_t*>(sg.aux + blk * 2));
         const uint32_t Q[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
         float s = 0.f;
 #pragma unroll
@@ -377,19 +449,18 @@ struct FQ80 {
 
 // R row dots of one wave (plus the same rows of a second matrix when DUAL)
 template <class F, int R, bool DUAL>
-__device__ __forceinline__ void rows_dot(const SegDesc& s, const SegDesc& s2, const float* xs, int r0,
-                                         float* acc) {
+__device__ __forceinline__ void rows_dot(const SegK& s, const SegK& s2, const float* xs, int r0, float* acc) {
     const int lane = threadIdx.x & 63;
-    const int U = s.L.nb * F::UPB;
-    const int n_out = s.L.n_out;
+    const int U = s.nb * F::UPB;
+    const int n_out = s.n_out;
     for (int u = lane; u < U; u += 64) {
         float xv[F::NX], sx[F::NS];
         F::xslice(xs, u, xv, sx);
 #pragma unroll
         for (int i = 0; i < R; i++)
             if (r0 + i < n_out) {
-                acc[i] += F::dot(s.base, s.L, r0 + i, u, xv, sx);
-                if (DUAL) acc[R + i] += F::dot(s2.base, s2.L, r0 + i, u, xv, sx);
+                acc[i] += F::dot(s, r0 + i, u, xv, sx);
+                if (DUAL) acc[R + i] += F::dot(s2, r0 + i, u, xv, sx);
             }
     }
 }
@@ -397,7 +468,7 @@ __device__ __forceinline__ void rows_dot(const SegDesc& s, const SegDesc& s2, co
 
 // Fused segment kernel for Q8_0 (one instantiation per dual mode).
 template <class F, bool DUAL>
-__global__ __launch_bounds__(256) void k_seg(const SegLaunch a) {
+__global__ __launch_bounds__(256) void k_seg(const SegKArgs a) {
     extern __shared__ float xsh[];
     __shared__ float red[4];
     __shared__ float amv[4 * SEG_R];
@@ -405,9 +476,9 @@ __global__ __launch_bounds__(256) void k_seg(const SegLaunch a) {
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     int si = 0;
     for (int i = 1; i < a.nseg; i++)
-        if ((int)blockIdx.x >= a.seg[i].first_block) si = i;
-    const SegDesc& s = a.seg[si];
-    const SegDesc& s2 = a.seg[DUAL ? si + 1 : si];
+        if ((int)blockIdx.x >= a.seg[i].first) si = i;
+    const SegK& s = a.seg[si];
+    const SegK& s2 = a.seg[DUAL ? si + 1 : si];
 
     // prologue: RMSNorm of x into LDS (every block; same order -> same result)
     const float* xs = a.x;
@@ -432,7 +503,7 @@ __global__ __launch_bounds__(256) void k_seg(const SegLaunch a) {
         xs = xsh;
     }
 
-    const int r0 = ((int)blockIdx.x - s.first_block) * SEG_ROWS + wv * SEG_R;
+    const int r0 = ((int)blockIdx.x - s.first) * SEG_ROWS + wv * SEG_R;
     float acc[2 * SEG_R];
 #pragma unroll
     for (int i = 0; i < 2 * SEG_R; i++) acc[i] = 0.f;
@@ -440,7 +511,7 @@ __global__ __launch_bounds__(256) void k_seg(const SegLaunch a) {
 #pragma unroll
     for (int i = 0; i < (DUAL ? 2 : 1) * SEG_R; i++) acc[i] = wave_sum(acc[i]);
 
-    const int n_out = s.L.n_out;
+    const int n_out = s.n_out;
     switch (s.epi) {
     case EPI_STORE:
     case EPI_ARGMAX:
@@ -508,7 +579,7 @@ __global__ __launch_bounds__(256) void k_seg(const SegLaunch a) {
         float v = amv[0];
         int idx = ami[0];
         for (int i = 1; i < 4 * SEG_R; i++) am_merge(v, idx, amv[i], ami[i]);
-        const int bi = (int)blockIdx.x - s.first_block;
+        const int bi = (int)blockIdx.x - s.first;
         a.am_val[bi] = v;
         a.am_idx[bi] = idx;
     }
@@ -516,13 +587,22 @@ __global__ __launch_bounds__(256) void k_seg(const SegLaunch a) {
 
 // Reduce the head's per-block argmax partials (np.argmax semantics: first
 // index of the maximum), write tokens[*cursor + 1] and advance the token
-// state.  One block; runs after k_seg in stream order.
+// state.  With emb_out set, also decode the new token's embedding row into
+// emb_out (the next token's input), so generation needs no embedding launch.
+// One block; runs after the head GEMV in stream order.
 __global__ __launch_bounds__(256) void k_argmax_finalize(const float* __restrict__ pv, const int* __restrict__ pi,
                                                          int nb, int* __restrict__ tokens, int* cursor,
-                                                         int* state, int n_layer) {
+                                                         int* state, int n_layer, const uint8_t* __restrict__ emb,
+                                                         DracoLayout emb_L, float* __restrict__ emb_out) {
     __shared__ float sv[4];
     __shared__ int si[4];
+    __shared__ int tok_s;
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    // position and per-layer lengths advance in parallel, one entry per
+    // thread (nothing in this launch reads them)
+    if (state)
+        for (int i = tid; i <= n_layer; i += 256) state[i] += 1;
+    const int cur = (tid == 0 && cursor) ? cursor[0] : -1;
     float v = -INFINITY;
     int idx = 0x7fffffff;
     for (int i = tid; i < nb; i += 256) am_merge(v, idx, pv[i], pi[i]);
@@ -534,14 +614,14 @@ __global__ __launch_bounds__(256) void k_argmax_finalize(const float* __restrict
     __syncthreads();
     if (tid == 0) {
         for (int w = 1; w < 4; w++) am_merge(v, idx, sv[w], si[w]);
-        const int cur = cursor ? cursor[0] : -1;
         tokens[cur + 1] = idx;
-        if (state) {
-            state[0] += 1;
-            for (int l = 0; l < n_layer; l++) state[1 + l] += 1;
-        }
-        if (cursor) cursor[0] += 1;
+        if (cursor) cursor[0] = cur + 1;
+        tok_s = idx;
     }
+    if (!emb_out) return;
+    __syncthreads();
+    const int tok = tok_s;
+    for (int p = tid; p < emb_L.n_in; p += 256) emb_out[p] = embed_value(emb, emb_L, tok, p);
 }
 
 // ------------------------------------------------------------ F32 / F16 --
@@ -602,7 +682,8 @@ void launch_dq(SegLaunch& a, int grid, hipStream_t st) {
         (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&k_dq<NW, FM, DUAL>),
                                   hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
     });
-    hipLaunchKernelGGL((k_dq<NW, FM, DUAL>), dim3(grid), dim3(64 * NW), dq_lds_bytes(a.n_in, NW), st, a);
+    hipLaunchKernelGGL((k_dq<NW, FM, DUAL>), dim3(grid), dim3(64 * NW), dq_lds_bytes(a.n_in, NW), st,
+                       seg_kargs(a, false));
 }
 
 template <int NW>
@@ -672,7 +753,8 @@ int seg_launch_dq(SegLaunch& a, hipStream_t st) {
     else launch_dq_nw<16>(a, fm, dual, grid, st);
     if (a.seg[0].epi == EPI_ARGMAX)
         hipLaunchKernelGGL(k_argmax_finalize, dim3(1), dim3(256), 0, st, a.am_val, a.am_idx, grid, a.tokens,
-                           const_cast<int*>(a.cursor), a.advance_state, a.advance_layers);
+                           const_cast<int*>(a.cursor), a.advance_state, a.advance_layers, a.emb, a.emb_L,
+                           a.emb_out);
     return 0;
 }
 
@@ -703,11 +785,13 @@ int seg_launch_q8(SegLaunch& a, hipStream_t st) {
     if (dual && a.nseg != 2) return -1;
     const size_t shm = a.do_norm ? sizeof(float) * (size_t)a.n_in : 0;
     const dim3 g(blocks), b(256);
-    if (dual) hipLaunchKernelGGL((k_seg<FQ80, true>), g, b, shm, st, a);
-    else hipLaunchKernelGGL((k_seg<FQ80, false>), g, b, shm, st, a);
+    const SegKArgs k = seg_kargs(a, true);
+    if (dual) hipLaunchKernelGGL((k_seg<FQ80, true>), g, b, shm, st, k);
+    else hipLaunchKernelGGL((k_seg<FQ80, false>), g, b, shm, st, k);
     if (a.seg[0].epi == EPI_ARGMAX)
         hipLaunchKernelGGL(k_argmax_finalize, dim3(1), dim3(256), 0, st, a.am_val, a.am_idx, a.seg[0].n_blocks,
-                           a.tokens, const_cast<int*>(a.cursor), a.advance_state, a.advance_layers);
+                           a.tokens, const_cast<int*>(a.cursor), a.advance_state, a.advance_layers, a.emb, a.emb_L,
+                           a.emb_out);
     return 0;
 }
 
