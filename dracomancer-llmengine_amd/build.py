@@ -23,6 +23,10 @@ COMMON = ["-O3", "-fPIC", "-std=c++17", f"--offload-arch={ARCH}", "-ffp-contract
 # Contraction is off everywhere: kernels call fmaf where they want a fused op, and
 # host code (rope table, encoders) must round every operation like the reference.
 DEVICE_CONTRACT = ["-fno-gpu-flush-denormals-to-zero"]
+# Per-file flags.  The prefill GEMM post-processes every MFMA result on the VALU;
+# the VGPR form of the MFMA writes them where the VALU reads them, instead of to
+# accumulation registers that each need a v_accvgpr_read first.
+FILE_FLAGS = {"gemm.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
 
 
 def _sources():
@@ -35,7 +39,7 @@ def _sources():
 
 def _compile(src):
     obj = os.path.join(OBJDIR, os.path.basename(src) + ".o")
-    cmd = [HIPCC] + COMMON + DEVICE_CONTRACT + ["-c", src, "-o", obj]
+    cmd = [HIPCC] + COMMON + DEVICE_CONTRACT + FILE_FLAGS.get(os.path.basename(src), []) + ["-c", src, "-o", obj]
     if src.endswith(".hip"):
         cmd[1:1] = ["-x", "hip"]
     r = subprocess.run(cmd, capture_output=True, text=True)

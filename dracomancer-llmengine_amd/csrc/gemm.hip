@@ -155,7 +155,7 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_q4(const GemmArgs a) {
                 const v16i C = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[sb], B, (v16i){}, 0, 0, 0);
                 const int scm = nib ? sc : 16 * sc;
 #pragma unroll
-                for (int i = 0; i < 16; i++) acc[i] += scm * C[i];
+                for (int i = 0; i < 16; i++) acc[i] += __mul24(scm, C[i]);  // |scm| < 2^10, |C| < 2^20: exact
             }
 #pragma unroll
             for (int qt = 0; qt < 4; qt++) {
@@ -280,7 +280,7 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_q6(const GemmArgs a) {
                         const v16i C = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[r][qs], Bv, (v16i){}, 0, 0, 0);
                         // C[i]: h = i/8, t4 = 2*((i/4)&1) + u, digit i%4
 #pragma unroll
-                        for (int i = 0; i < 16; i++) acc[qs][i] += (i < 8 ? sc0 : sc1) * C[i];
+                        for (int i = 0; i < 16; i++) acc[qs][i] += __mul24(i < 8 ? sc0 : sc1, C[i]);  // exact: < 2^27
 #pragma unroll
                         for (int tq = 0; tq < 2; tq++) {
                             const int tq2 = 2 * qs + tq;  // token 4*qs + 2*tq + u = 2*tq2 + u
