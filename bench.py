@@ -35,9 +35,9 @@ import numpy as np  # noqa: E402
 PEAK_HBM_GBS = 8000.0
 # HBM bytes per launch of the roofline kernel from the FETCH_SIZE / WRITE_SIZE
 # counter passes (rocprofv3 --pmc, scaled by a device copy of known size:
-# 2046.6 B per FETCH_SIZE unit, 1024 B per WRITE_SIZE unit): 16296.5 * 2046.6
+# 2046.6 B per FETCH_SIZE unit, 1024 B per WRITE_SIZE unit): 16282.5 * 2046.6
 # + 56.0 * 1024 bytes
-TRAFFIC_BYTES = 33409761
+TRAFFIC_BYTES = 33381109
 CTX_START = 960
 MAX_DECODE = 64  # positions 960..1023 (max_t 1024)
 
