@@ -145,7 +145,9 @@ __device__ __forceinline__ auto seg_pick(const SegKArgs& a, int si, F f) -> decl
 }
 
 // FM: 1 = Q4_K segments only, 2 = Q6_K only, 3 = both (per-tile switch).
-template <int NW, int FM, bool DUAL>
+// MULTI: more than one segment (a SwiGLU pair counts as one); without it the
+// segment of every tile is 0 at compile time and its selection code is gone.
+template <int NW, int FM, bool DUAL, bool MULTI>
 __global__ __launch_bounds__(64 * NW) void k_dq(const SegKArgs a) {
     extern __shared__ __align__(16) uint8_t smem[];
     constexpr int NT = 64 * NW;
@@ -171,7 +173,7 @@ __global__ __launch_bounds__(64 * NW) void k_dq(const SegKArgs a) {
         bool q4;
     };
     auto tile_ref = [&](int T) {
-        const int si = seg_of_tile(a, T);
+        const int si = MULTI ? seg_of_tile(a, T) : 0;
         const bool q4 = FM == 3 ? seg_pick(a, si, [](const SegK& d) { return d.code; }) == DRACO_Q4_K : FM == 1;
         const size_t ib = q4 ? DRACO_Q4T_ITEM : DRACO_Q6T_ITEM;
         const int tl = T - seg_pick(a, si, [](const SegK& d) { return d.first; }) +
@@ -291,7 +293,7 @@ __global__ __launch_bounds__(64 * NW) void k_dq(const SegKArgs a) {
 
     auto step = [&](Frag& cur, Frag& nxt, Frag& cur2, Frag& nxt2) {
         if (cp == 0) {
-            const int si = seg_of_tile(a, ct);
+            const int si = MULTI ? seg_of_tile(a, ct) : 0;
             c_epi = seg_pick(a, si, [](const SegK& d) { return d.epi; });
             c_row = (ct - seg_pick(a, si, [](const SegK& d) { return d.first; }) +
                      seg_pick(a, si, [](const SegK& d) { return d.tile0; })) * 16;
@@ -674,29 +676,36 @@ int cu_count() {
 
 size_t dq_lds_bytes(int n_in, int nw) { return (size_t)(n_in / 16) * 72 + 1024 + (size_t)2 * nw * 16 * 4; }
 
-template <int NW, int FM, bool DUAL>
+template <int NW, int FM, bool DUAL, bool MULTI>
 void launch_dq(SegLaunch& a, int grid, hipStream_t st) {
     static std::once_flag once;
     std::call_once(once, [] {
         // allow LDS beyond 64 KB for long rows (n_in up to 16384 needs ~74 KB)
-        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&k_dq<NW, FM, DUAL>),
+        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&k_dq<NW, FM, DUAL, MULTI>),
                                   hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
     });
-    hipLaunchKernelGGL((k_dq<NW, FM, DUAL>), dim3(grid), dim3(64 * NW), dq_lds_bytes(a.n_in, NW), st,
+    hipLaunchKernelGGL((k_dq<NW, FM, DUAL, MULTI>), dim3(grid), dim3(64 * NW), dq_lds_bytes(a.n_in, NW), st,
                        seg_kargs(a, false));
+}
+
+template <int NW, int FM, bool DUAL>
+void launch_dq_m(SegLaunch& a, bool multi, int grid, hipStream_t st) {
+    if (multi) launch_dq<NW, FM, DUAL, true>(a, grid, st);
+    else launch_dq<NW, FM, DUAL, false>(a, grid, st);
 }
 
 template <int NW>
 void launch_dq_nw(SegLaunch& a, int fm, bool dual, int grid, hipStream_t st) {
+    const bool multi = a.nseg > (dual ? 2 : 1);
     if (dual) {
-        if (fm == 1) launch_dq<NW, 1, true>(a, grid, st);
-        else launch_dq<NW, 2, true>(a, grid, st);
+        if (fm == 1) launch_dq_m<NW, 1, true>(a, multi, grid, st);
+        else launch_dq_m<NW, 2, true>(a, multi, grid, st);
     } else if (fm == 1) {
-        launch_dq<NW, 1, false>(a, grid, st);
+        launch_dq_m<NW, 1, false>(a, multi, grid, st);
     } else if (fm == 2) {
-        launch_dq<NW, 2, false>(a, grid, st);
+        launch_dq_m<NW, 2, false>(a, multi, grid, st);
     } else {
-        launch_dq<NW, 3, false>(a, grid, st);
+        launch_dq<NW, 3, false, true>(a, grid, st);
     }
 }
 
