@@ -147,7 +147,10 @@ __device__ __forceinline__ auto seg_pick(const SegKArgs& a, int si, F f) -> decl
 // FM: 1 = Q4_K segments only, 2 = Q6_K only, 3 = both (per-tile switch).
 // MULTI: more than one segment (a SwiGLU pair counts as one); without it the
 // segment of every tile is 0 at compile time and its selection code is gone.
-template <int NW, int FM, bool DUAL, bool MULTI>
+// EPI: the epilogue when it is fixed for the launch (single segment), or
+// EPI_RT to read it from the tile's segment.
+constexpr int EPI_RT = -1;
+template <int NW, int FM, bool DUAL, bool MULTI, int EPI>
 __global__ __launch_bounds__(64 * NW) void k_dq(const SegKArgs a) {
     extern __shared__ __align__(16) uint8_t smem[];
     constexpr int NT = 64 * NW;
@@ -294,7 +297,7 @@ __global__ __launch_bounds__(64 * NW) void k_dq(const SegKArgs a) {
     auto step = [&](Frag& cur, Frag& nxt, Frag& cur2, Frag& nxt2) {
         if (cp == 0) {
             const int si = MULTI ? seg_of_tile(a, ct) : 0;
-            c_epi = seg_pick(a, si, [](const SegK& d) { return d.epi; });
+            c_epi = EPI != EPI_RT ? EPI : seg_pick(a, si, [](const SegK& d) { return d.epi; });
             c_row = (ct - seg_pick(a, si, [](const SegK& d) { return d.first; }) +
                      seg_pick(a, si, [](const SegK& d) { return d.tile0; })) * 16;
             c_r0 = seg_pick(a, si, [](const SegK& d) { return d.row0; });
@@ -417,7 +420,7 @@ __global__ __launch_bounds__(64 * NW) void k_dq(const SegKArgs a) {
         if (i + 1 >= n_items) break;
         step(P1, P0, Q1, Q0);
     }
-    if (a.seg[0].epi == EPI_ARGMAX && tid == 0) {
+    if ((EPI != EPI_RT ? EPI : a.seg[0].epi) == EPI_ARGMAX && tid == 0) {
         a.am_val[bx] = am_v;
         a.am_idx[bx] = am_i;
     }
@@ -676,22 +679,31 @@ int cu_count() {
 
 size_t dq_lds_bytes(int n_in, int nw) { return (size_t)(n_in / 16) * 72 + 1024 + (size_t)2 * nw * 16 * 4; }
 
-template <int NW, int FM, bool DUAL, bool MULTI>
+template <int NW, int FM, bool DUAL, bool MULTI, int EPI>
 void launch_dq(SegLaunch& a, int grid, hipStream_t st) {
     static std::once_flag once;
     std::call_once(once, [] {
         // allow LDS beyond 64 KB for long rows (n_in up to 16384 needs ~74 KB)
-        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&k_dq<NW, FM, DUAL, MULTI>),
+        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&k_dq<NW, FM, DUAL, MULTI, EPI>),
                                   hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
     });
-    hipLaunchKernelGGL((k_dq<NW, FM, DUAL, MULTI>), dim3(grid), dim3(64 * NW), dq_lds_bytes(a.n_in, NW), st,
+    hipLaunchKernelGGL((k_dq<NW, FM, DUAL, MULTI, EPI>), dim3(grid), dim3(64 * NW), dq_lds_bytes(a.n_in, NW), st,
                        seg_kargs(a, false));
 }
 
+// single-segment launches get their epilogue at compile time (a SwiGLU pair
+// is always one); the rest read it per tile
 template <int NW, int FM, bool DUAL>
 void launch_dq_m(SegLaunch& a, bool multi, int grid, hipStream_t st) {
-    if (multi) launch_dq<NW, FM, DUAL, true>(a, grid, st);
-    else launch_dq<NW, FM, DUAL, false>(a, grid, st);
+    if constexpr (DUAL) {
+        launch_dq<NW, FM, true, false, EPI_SWIGLU>(a, grid, st);  // dual launches have exactly one pair
+    } else {
+        if (multi) launch_dq<NW, FM, false, true, EPI_RT>(a, grid, st);
+        else if (a.seg[0].epi == EPI_STORE) launch_dq<NW, FM, false, false, EPI_STORE>(a, grid, st);
+        else if (a.seg[0].epi == EPI_RESID) launch_dq<NW, FM, false, false, EPI_RESID>(a, grid, st);
+        else if (a.seg[0].epi == EPI_ARGMAX) launch_dq<NW, FM, false, false, EPI_ARGMAX>(a, grid, st);
+        else launch_dq<NW, FM, false, false, EPI_RT>(a, grid, st);
+    }
 }
 
 template <int NW>
@@ -705,7 +717,7 @@ void launch_dq_nw(SegLaunch& a, int fm, bool dual, int grid, hipStream_t st) {
     } else if (fm == 2) {
         launch_dq_m<NW, 2, false>(a, multi, grid, st);
     } else {
-        launch_dq<NW, 3, false, true>(a, grid, st);
+        launch_dq<NW, 3, false, true, EPI_RT>(a, grid, st);
     }
 }
 
