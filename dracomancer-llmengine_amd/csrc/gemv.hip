@@ -148,9 +148,10 @@ __device__ __forceinline__ auto seg_pick(const SegKArgs& a, int si, F f) -> decl
 // MULTI: more than one segment (a SwiGLU pair counts as one); without it the
 // segment of every tile is 0 at compile time and its selection code is gone.
 // EPI: the epilogue when it is fixed for the launch (single segment), or
-// EPI_RT to read it from the tile's segment.
+// EPI_RT to read it from the tile's segment.  NORM: the RMSNorm prologue
+// (the launch's do_norm).
 constexpr int EPI_RT = -1;
-template <int NW, int FM, bool DUAL, bool MULTI, int EPI>
+template <int NW, int FM, bool DUAL, bool MULTI, int EPI, bool NORM>
 __global__ __launch_bounds__(64 * NW) void k_dq(const SegKArgs a) {
     extern __shared__ __align__(16) uint8_t smem[];
     constexpr int NT = 64 * NW;
@@ -204,7 +205,7 @@ __global__ __launch_bounds__(64 * NW) void k_dq(const SegKArgs a) {
         const int i4 = tid + q * NT;
         if (i4 < n4) {
             xv[q] = ld4(a.x + 4 * i4);
-            if (a.do_norm && a.norm_w) wv[q] = ld4(a.norm_w + 4 * i4);
+            if (NORM && a.norm_w) wv[q] = ld4(a.norm_w + 4 * i4);
         }
     }
     Frag P0, P1, Q0, Q1;
@@ -242,7 +243,7 @@ __global__ __launch_bounds__(64 * NW) void k_dq(const SegKArgs a) {
 
     // ---- prologue part 2: RMSNorm (src/m6_engine.c:31-37) and digits into LDS
     float inv = 1.f;
-    if (a.do_norm) {
+    if (NORM) {
         float ss = 0.f;
 #pragma unroll
         for (int q = 0; q < XP_MAXV; q++)
@@ -266,7 +267,7 @@ __global__ __launch_bounds__(64 * NW) void k_dq(const SegKArgs a) {
         const int i4 = tid + q * NT;
         if (i4 >= n4) break;
         float4 v = xv[q];
-        if (a.do_norm) {
+        if (NORM) {
             if (a.norm_w) {
                 const float4 nw = wv[q];
                 v.x = v.x * inv * nw.x; v.y = v.y * inv * nw.y; v.z = v.z * inv * nw.z; v.w = v.w * inv * nw.w;
@@ -679,31 +680,37 @@ int cu_count() {
 
 size_t dq_lds_bytes(int n_in, int nw) { return (size_t)(n_in / 16) * 72 + 1024 + (size_t)2 * nw * 16 * 4; }
 
-template <int NW, int FM, bool DUAL, bool MULTI, int EPI>
+template <int NW, int FM, bool DUAL, bool MULTI, int EPI, bool NORM>
 void launch_dq(SegLaunch& a, int grid, hipStream_t st) {
     static std::once_flag once;
     std::call_once(once, [] {
         // allow LDS beyond 64 KB for long rows (n_in up to 16384 needs ~74 KB)
-        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&k_dq<NW, FM, DUAL, MULTI, EPI>),
+        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&k_dq<NW, FM, DUAL, MULTI, EPI, NORM>),
                                   hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
     });
-    hipLaunchKernelGGL((k_dq<NW, FM, DUAL, MULTI, EPI>), dim3(grid), dim3(64 * NW), dq_lds_bytes(a.n_in, NW), st,
-                       seg_kargs(a, false));
+    hipLaunchKernelGGL((k_dq<NW, FM, DUAL, MULTI, EPI, NORM>), dim3(grid), dim3(64 * NW), dq_lds_bytes(a.n_in, NW),
+                       st, seg_kargs(a, false));
 }
 
 // single-segment launches get their epilogue at compile time (a SwiGLU pair
 // is always one); the rest read it per tile
+template <int NW, int FM, bool DUAL, bool NORM>
+void launch_dq_e(SegLaunch& a, bool multi, int grid, hipStream_t st) {
+    if constexpr (DUAL) {
+        launch_dq<NW, FM, true, false, EPI_SWIGLU, NORM>(a, grid, st);  // dual launches have exactly one pair
+    } else {
+        if (multi) launch_dq<NW, FM, false, true, EPI_RT, NORM>(a, grid, st);
+        else if (a.seg[0].epi == EPI_STORE) launch_dq<NW, FM, false, false, EPI_STORE, NORM>(a, grid, st);
+        else if (a.seg[0].epi == EPI_RESID) launch_dq<NW, FM, false, false, EPI_RESID, NORM>(a, grid, st);
+        else if (a.seg[0].epi == EPI_ARGMAX) launch_dq<NW, FM, false, false, EPI_ARGMAX, NORM>(a, grid, st);
+        else launch_dq<NW, FM, false, false, EPI_RT, NORM>(a, grid, st);
+    }
+}
+
 template <int NW, int FM, bool DUAL>
 void launch_dq_m(SegLaunch& a, bool multi, int grid, hipStream_t st) {
-    if constexpr (DUAL) {
-        launch_dq<NW, FM, true, false, EPI_SWIGLU>(a, grid, st);  // dual launches have exactly one pair
-    } else {
-        if (multi) launch_dq<NW, FM, false, true, EPI_RT>(a, grid, st);
-        else if (a.seg[0].epi == EPI_STORE) launch_dq<NW, FM, false, false, EPI_STORE>(a, grid, st);
-        else if (a.seg[0].epi == EPI_RESID) launch_dq<NW, FM, false, false, EPI_RESID>(a, grid, st);
-        else if (a.seg[0].epi == EPI_ARGMAX) launch_dq<NW, FM, false, false, EPI_ARGMAX>(a, grid, st);
-        else launch_dq<NW, FM, false, false, EPI_RT>(a, grid, st);
-    }
+    if (a.do_norm) launch_dq_e<NW, FM, DUAL, true>(a, multi, grid, st);
+    else launch_dq_e<NW, FM, DUAL, false>(a, multi, grid, st);
 }
 
 template <int NW>
@@ -717,7 +724,8 @@ void launch_dq_nw(SegLaunch& a, int fm, bool dual, int grid, hipStream_t st) {
     } else if (fm == 2) {
         launch_dq_m<NW, 2, false>(a, multi, grid, st);
     } else {
-        launch_dq<NW, 3, false, true, EPI_RT>(a, grid, st);
+        if (a.do_norm) launch_dq<NW, 3, false, true, EPI_RT, true>(a, grid, st);
+        else launch_dq<NW, 3, false, true, EPI_RT, false>(a, grid, st);
     }
 }
 
