@@ -148,9 +148,10 @@ __device__ __forceinline__ auto seg_pick(const SegKArgs& a, int si, F f) -> decl
 // MULTI: more than one segment (a SwiGLU pair counts as one); without it the
 // segment of every tile is 0 at compile time and its selection code is gone.
 // EPI: the epilogue when it is fixed for the launch (single segment), or
-// EPI_RT to read it from the tile's segment.  NORM: the RMSNorm prologue
-// (the launch's do_norm).
-constexpr int EPI_RT = -1;
+// EPI_RT to read it from the tile's segment; EPI_QKV: the llama q/k/v launch
+// (segments 0, 1, 2 = rope q, rope k + KV append, V append).  NORM: the
+// RMSNorm prologue (the launch's do_norm).
+constexpr int EPI_RT = -1, EPI_QKV = -2;
 template <int NW, int FM, bool DUAL, bool MULTI, int EPI, bool NORM>
 __global__ __launch_bounds__(64 * NW) void k_dq(const SegKArgs a) {
     extern __shared__ __align__(16) uint8_t smem[];
@@ -298,7 +299,8 @@ __global__ __launch_bounds__(64 * NW) void k_dq(const SegKArgs a) {
     auto step = [&](Frag& cur, Frag& nxt, Frag& cur2, Frag& nxt2) {
         if (cp == 0) {
             const int si = MULTI ? seg_of_tile(a, ct) : 0;
-            c_epi = EPI != EPI_RT ? EPI : seg_pick(a, si, [](const SegK& d) { return d.epi; });
+            if constexpr (EPI == EPI_QKV) c_epi = si == 0 ? EPI_ROPE_Q : (si == 1 ? EPI_ROPE_K : EPI_V_APPEND);
+            else c_epi = EPI != EPI_RT ? EPI : seg_pick(a, si, [](const SegK& d) { return d.epi; });
             c_row = (ct - seg_pick(a, si, [](const SegK& d) { return d.first; }) +
                      seg_pick(a, si, [](const SegK& d) { return d.tile0; })) * 16;
             c_r0 = seg_pick(a, si, [](const SegK& d) { return d.row0; });
@@ -421,7 +423,7 @@ __global__ __launch_bounds__(64 * NW) void k_dq(const SegKArgs a) {
         if (i + 1 >= n_items) break;
         step(P1, P0, Q1, Q0);
     }
-    if ((EPI != EPI_RT ? EPI : a.seg[0].epi) == EPI_ARGMAX && tid == 0) {
+    if ((EPI >= 0 ? EPI : (EPI == EPI_QKV ? EPI_ROPE_Q : a.seg[0].epi)) == EPI_ARGMAX && tid == 0) {
         a.am_val[bx] = am_v;
         a.am_idx[bx] = am_i;
     }
@@ -724,7 +726,10 @@ void launch_dq_nw(SegLaunch& a, int fm, bool dual, int grid, hipStream_t st) {
     } else if (fm == 2) {
         launch_dq_m<NW, 2, false>(a, multi, grid, st);
     } else {
-        if (a.do_norm) launch_dq<NW, 3, false, true, EPI_RT, true>(a, grid, st);
+        const bool qkv = a.nseg == 3 && a.seg[0].epi == EPI_ROPE_Q && a.seg[1].epi == EPI_ROPE_K &&
+                         a.seg[2].epi == EPI_V_APPEND;
+        if (qkv && a.do_norm) launch_dq<NW, 3, false, true, EPI_QKV, true>(a, grid, st);
+        else if (a.do_norm) launch_dq<NW, 3, false, true, EPI_RT, true>(a, grid, st);
         else launch_dq<NW, 3, false, true, EPI_RT, false>(a, grid, st);
     }
 }
