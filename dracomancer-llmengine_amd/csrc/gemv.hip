@@ -152,7 +152,7 @@ __device__ __forceinline__ auto seg_pick(const SegKArgs& a, int si, F f) -> decl
 // (segments 0, 1, 2 = rope q, rope k + KV append, V append).  NORM: the
 // RMSNorm prologue (the launch's do_norm).
 constexpr int EPI_RT = -1, EPI_QKV = -2;
-template <int NW, int FM, bool DUAL, bool MULTI, int EPI, bool NORM>
+template <int NW, int FM, bool DUAL, bool MULTI, int EPI, bool NORM, bool IPT1>
 __global__ __launch_bounds__(64 * NW) void k_dq(const SegKArgs a) {
     extern __shared__ __align__(16) uint8_t smem[];
     constexpr int NT = 64 * NW;
@@ -166,7 +166,7 @@ __global__ __launch_bounds__(64 * NW) void k_dq(const SegKArgs a) {
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int bx = blockIdx.x, G = gridDim.x;
     const int total = a.total_tiles;
-    const int ipt = (nb + NW - 1) / NW;
+    const int ipt = IPT1 ? 1 : (nb + NW - 1) / NW;  // IPT1: the launch has one item per wave and tile
     const int my_tiles = bx < total ? (total - bx + G - 1) / G : 0;
     const int n_items = my_tiles * ipt;
 
@@ -682,16 +682,22 @@ int cu_count() {
 
 size_t dq_lds_bytes(int n_in, int nw) { return (size_t)(n_in / 16) * 72 + 1024 + (size_t)2 * nw * 16 * 4; }
 
-template <int NW, int FM, bool DUAL, bool MULTI, int EPI, bool NORM>
-void launch_dq(SegLaunch& a, int grid, hipStream_t st) {
+template <int NW, int FM, bool DUAL, bool MULTI, int EPI, bool NORM, bool IPT1>
+void launch_dq1(SegLaunch& a, int grid, hipStream_t st) {
     static std::once_flag once;
     std::call_once(once, [] {
         // allow LDS beyond 64 KB for long rows (n_in up to 16384 needs ~74 KB)
-        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&k_dq<NW, FM, DUAL, MULTI, EPI, NORM>),
+        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&k_dq<NW, FM, DUAL, MULTI, EPI, NORM, IPT1>),
                                   hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
     });
-    hipLaunchKernelGGL((k_dq<NW, FM, DUAL, MULTI, EPI, NORM>), dim3(grid), dim3(64 * NW), dq_lds_bytes(a.n_in, NW),
-                       st, seg_kargs(a, false));
+    hipLaunchKernelGGL((k_dq<NW, FM, DUAL, MULTI, EPI, NORM, IPT1>), dim3(grid), dim3(64 * NW),
+                       dq_lds_bytes(a.n_in, NW), st, seg_kargs(a, false));
+}
+
+template <int NW, int FM, bool DUAL, bool MULTI, int EPI, bool NORM>
+void launch_dq(SegLaunch& a, int grid, hipStream_t st) {
+    if ((a.n_in >> 8) <= NW) launch_dq1<NW, FM, DUAL, MULTI, EPI, NORM, true>(a, grid, st);
+    else launch_dq1<NW, FM, DUAL, MULTI, EPI, NORM, false>(a, grid, st);
 }
 
 // single-segment launches get their epilogue at compile time (a SwiGLU pair
