@@ -443,7 +443,7 @@ struct FQ80 {
     __device__ static float dot(const SegK& sg, int row, int u, const float* xv, const float* sx) {
         (void)sx;
         const size_t blk = (size_t)row * sg.nb + u;
-        const uint4 q0 = ldu4(sg.base + blk * 32), q1 = ldu4(sg.base + blk * 32 + 16);
+        const uint4 q0 = ldnt4(sg.base + blk * 32), q1 = ldnt4(sg.base + blk * 32 + 16);
         const float d = h2f(*reinterpret_cast<const uint16_t*>(sg.aux + blk * 2));
         const uint32_t Q[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
         float s = 0.f;

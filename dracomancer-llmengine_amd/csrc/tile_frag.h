@@ -17,17 +17,17 @@ struct Frag {
 };
 
 __device__ __forceinline__ void load_q4(const uint8_t* item, int lane, Frag& f) {
-    f.a = ldu4(item + 16 * lane);
-    f.b = ldu4(item + 1024 + 16 * lane);
-    f.c = ldu4(item + 2048 + 16 * (lane & 15));
+    f.a = ldnt4(item + 16 * lane);
+    f.b = ldnt4(item + 1024 + 16 * lane);
+    f.c = ldnt4(item + 2048 + 16 * (lane & 15));
     f.sc = 0u;
     f.d = 0u;
 }
 
 __device__ __forceinline__ void load_q6(const uint8_t* item, int lane, Frag& f) {
-    f.a = ldu4(item + 16 * lane);
-    f.b = ldu4(item + 1024 + 16 * lane);
-    f.c = ldu4(item + 2048 + 16 * lane);
+    f.a = ldnt4(item + 16 * lane);
+    f.b = ldnt4(item + 1024 + 16 * lane);
+    f.c = ldnt4(item + 2048 + 16 * lane);
     f.sc = *reinterpret_cast<const uint32_t*>(item + 3072 + 4 * lane);
     f.d = *reinterpret_cast<const uint16_t*>(item + 3328 + 2 * (lane & 15));
 }
