@@ -242,44 +242,58 @@ __global__ __launch_bounds__(64 * NW) void k_dq(const SegKArgs a) {
     load_next(P0, Q0);
     for (int i = tid; i < 256; i += NT) reinterpret_cast<uint32_t*>(zero)[i] = 0u;
 
-    // ---- prologue part 2: RMSNorm (src/m6_engine.c:31-37) and digits into LDS
-    float inv = 1.f;
-    if (NORM) {
-        float ss = 0.f;
-#pragma unroll
-        for (int q = 0; q < XP_MAXV; q++)
-            if (tid + q * NT < n4) {
-                const float4 v = xv[q];
-                ss = fmaf(v.x, v.x, ss);
-                ss = fmaf(v.y, v.y, ss);
-                ss = fmaf(v.z, v.z, ss);
-                ss = fmaf(v.w, v.w, ss);
-            }
-        ss = wave_sum(ss);
-        if (lane == 0) red[w] = ss;
-        lds_barrier();
-        float tot = 0.f;
-#pragma unroll
-        for (int i = 0; i < NW; i++) tot += red[i];
-        inv = 1.f / sqrtf(tot / (float)n_in + a.eps);
-    }
+    // ---- prologue part 2: digits into LDS, with the RMSNorm of
+    // src/m6_engine.c:31-37 split in two: the digits are those of x*w, and
+    // the scalar 1/rms (sum of squares reduced across waves through the same
+    // barrier) multiplies each finished row dot in the epilogue.  One barrier
+    // instead of two; the result differs from dotting (x*inv)*w only by fp32
+    // rounding.
+    float* ssp = red + 2 * NW * 16;  // [NW] per-wave sums of squares
+    float ss = 0.f;
 #pragma unroll
     for (int q = 0; q < XP_MAXV; q++) {
         const int i4 = tid + q * NT;
         if (i4 >= n4) break;
         float4 v = xv[q];
         if (NORM) {
+            ss = fmaf(v.x, v.x, ss);
+            ss = fmaf(v.y, v.y, ss);
+            ss = fmaf(v.z, v.z, ss);
+            ss = fmaf(v.w, v.w, ss);
             if (a.norm_w) {
                 const float4 nw = wv[q];
-                v.x = v.x * inv * nw.x; v.y = v.y * inv * nw.y; v.z = v.z * inv * nw.z; v.w = v.w * inv * nw.w;
-            } else {
-                v.x *= inv; v.y *= inv; v.z *= inv; v.w *= inv;
+                v.x *= nw.x; v.y *= nw.y; v.z *= nw.z; v.w *= nw.w;
             }
-            if (a.xn_out && bx == 0) *reinterpret_cast<float4*>(a.xn_out + 4 * i4) = v;
         }
         digits4(v, i4, xd, xsm);
     }
+    if (NORM) {
+        ss = wave_sum(ss);
+        if (lane == 0) ssp[w] = ss;
+    }
     lds_barrier();
+    float inv = 1.f;
+    if (NORM) {
+        float tot = 0.f;
+#pragma unroll
+        for (int i = 0; i < NW; i++) tot += ssp[i];
+        inv = 1.f / sqrtf(tot / (float)n_in + a.eps);
+        if (a.xn_out && bx == 0) {
+#pragma unroll
+            for (int q = 0; q < XP_MAXV; q++) {
+                const int i4 = tid + q * NT;
+                if (i4 >= n4) break;
+                float4 v = xv[q];
+                if (a.norm_w) {
+                    const float4 nw = wv[q];
+                    v.x = v.x * inv * nw.x; v.y = v.y * inv * nw.y; v.z = v.z * inv * nw.z; v.w = v.w * inv * nw.w;
+                } else {
+                    v.x *= inv; v.y *= inv; v.z *= inv; v.w *= inv;
+                }
+                *reinterpret_cast<float4*>(a.xn_out + 4 * i4) = v;
+            }
+        }
+    }
 
     // this lane's A row: digit (j&3) of its group, non-zero only when (j>>2) == g
     const bool adig = (j >> 2) == g;
@@ -364,6 +378,10 @@ __global__ __launch_bounds__(64 * NW) void k_dq(const SegKArgs a) {
                 for (int q = 0; q < NW; q++) {
                     v += red[q * 16 + tid];
                     if (DUAL) v2 += red[(NW + q) * 16 + tid];
+                }
+                if (NORM) {
+                    v *= inv;
+                    v2 *= inv;
                 }
                 const int row = c_row + tid;
                 const bool ok = row >= c_r0 && row < c_r1;
@@ -680,7 +698,7 @@ int cu_count() {
     return n;
 }
 
-size_t dq_lds_bytes(int n_in, int nw) { return (size_t)(n_in / 16) * 72 + 1024 + (size_t)2 * nw * 16 * 4; }
+size_t dq_lds_bytes(int n_in, int nw) { return (size_t)(n_in / 16) * 72 + 1024 + (size_t)2 * nw * 16 * 4 + (size_t)nw * 4; }
 
 template <int NW, int FM, bool DUAL, bool MULTI, int EPI, bool NORM, bool IPT1>
 void launch_dq1(SegLaunch& a, int grid, hipStream_t st) {
