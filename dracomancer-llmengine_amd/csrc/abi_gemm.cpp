@@ -15,26 +15,41 @@ extern "C" int draco_repack(int code, const uint8_t* src, int n_out, int n_in, u
 
 using namespace draco;
 
-namespace {
-
-bool served(int code) { return code == DRACO_Q4_K || code == DRACO_Q6_K || code == DRACO_Q8_0; }
-
-// X, Y device; enqueue Y = X . W^T
-int enqueue_gemm(const DracoMat& m, const float* X, int T, float* Y, uint8_t* digits, hipStream_t st) {
-    if (m.L.code == DRACO_Q8_0) {
+int draco_enqueue_gemm(const DracoMat& m, const float* X, int T, float* Y, uint8_t* digits, bool have_digits,
+                       hipStream_t st) {
+    if (m.L.code != DRACO_Q4_K && m.L.code != DRACO_Q6_K) {  // Q8_0 and the plain formats: one GEMV per token
         for (int t = 0; t < T; t++)
             if (draco_gemv_launch(m, X + (size_t)t * m.L.n_in, Y + (size_t)t * m.L.n_out, nullptr, 0, m.L.n_out, st))
                 return fail(-1, "gemm: gemv launch rejected");
         return 0;
     }
     GemmArgs a = {};
-    if (draco_gemm_digits_launch(X, T, m.L.n_in, digits, a, st)) return fail(-1, "gemm: digits launch rejected");
+    if (have_digits) {
+        // the launch only fills the buffer views; enqueue nothing
+        const size_t oct = (size_t)(T + 7) / 8;
+        a.xdig = reinterpret_cast<int8_t*>(digits);
+        a.xsc = reinterpret_cast<float*>(digits + oct * ((size_t)m.L.n_in / 32) * 1024);
+        a.xs32 = a.xsc + oct * ((size_t)m.L.n_in / 256) * 8;
+        a.xs16 = a.xs32 + oct * ((size_t)m.L.n_in / 32) * 8;
+        a.T = T;
+        a.n_in = m.L.n_in;
+    } else if (draco_gemm_digits_launch(X, T, m.L.n_in, digits, a, st)) {
+        return fail(-1, "gemm: digits launch rejected");
+    }
     a.W = m.dev;
     a.L = m.L;
     a.Y = Y;
     a.ldy = m.L.n_out;
     if (draco_gemm_launch(a, st)) return fail(-1, "gemm: launch rejected");
     return 0;
+}
+
+namespace {
+
+bool served(int code) { return code == DRACO_Q4_K || code == DRACO_Q6_K || code == DRACO_Q8_0; }
+
+int enqueue_gemm(const DracoMat& m, const float* X, int T, float* Y, uint8_t* digits, hipStream_t st) {
+    return draco_enqueue_gemm(m, X, T, Y, digits, false, st);
 }
 
 int gemm_host(int code, const float* X, const uint8_t* W, int T, int n_out, int n_in, float* Y) {

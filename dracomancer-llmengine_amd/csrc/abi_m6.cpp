@@ -17,11 +17,14 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <algorithm>
 #include <map>
 #include <unordered_map>
 #include <vector>
 
 #include "decode.h"
+#include "gemm.h"
+#include "prefill.h"
 #include "runtime.h"
 
 extern "C" {
@@ -86,8 +89,19 @@ struct Work {
     size_t cap_h = 0, cap_xn = 0, cap_xe = 0, cap_q = 0, cap_k = 0, cap_part = 0, cap_ff = 0;
 };
 
+// Chunked-prefill buffers, token-major, for up to `cap` tokens per chunk.
+struct PfBufs {
+    float *X = nullptr, *Xn = nullptr, *Q = nullptr, *K = nullptr, *V = nullptr, *O = nullptr, *G = nullptr,
+          *U = nullptr, *Y = nullptr, *part = nullptr;
+    uint8_t* dig = nullptr;
+    int* ids = nullptr;
+    int cap = 0, H = 0, QD = 0, KD = 0, FF = 0;
+    size_t part_n = 0, dig_n = 0;
+};
+
 struct DevModel {
     uint64_t epoch = 0;
+    PfBufs pf;
     std::vector<M6LayerDesc> descs;
     std::vector<DevAttn*> attn;
     std::vector<DevFfn*> ffn;
@@ -453,6 +467,112 @@ int enqueue_layer(DevModel* m, int l, float eps, hipStream_t st, const float* xi
     return 0;
 }
 
+// ---- chunked prefill (configs of the reference's forward_chunk,
+// src/qwen35_prefill.py:209-239, for the llama family) ----
+
+int g_prefill_chunk = 256;  // tokens per chunk; 0 = token-serial prefill
+
+int ensure_pf(DevModel* m, int cap) {
+    PfBufs& b = m->pf;
+    int QD = 0, KD = 0, FF = 0, NH = 0, HD = 0, max_t = 0;
+    for (int l = 0; l < m->n_layer; l++) {
+        const DevAttn* a = m->attn[l];
+        QD = std::max(QD, a->NH * a->HD);
+        KD = std::max(KD, a->NKV * a->HD);
+        NH = std::max(NH, a->NH);
+        HD = std::max(HD, a->HD);
+        max_t = std::max(max_t, a->max_t);
+        FF = std::max(FF, m->ffn[l]->FF);
+    }
+    const size_t part_n = pf_part_floats(NH, cap, HD, pf_attn_nsplit(max_t, cap));
+    const int win = std::max(std::max(m->h, QD), FF);
+    const size_t dig_n = draco_gemm_digit_bytes(cap, ((win + 255) / 256) * 256);
+    if (b.cap >= cap && b.H == m->h && b.QD >= QD && b.KD >= KD && b.FF >= FF && b.part_n >= part_n && b.dig_n >= dig_n)
+        return 0;
+    DRACO_HIP(hipStreamSynchronize(stream()));
+    float** fl[] = {&b.X, &b.Xn, &b.Q, &b.K, &b.V, &b.O, &b.G, &b.U, &b.Y, &b.part};
+    for (float** f : fl)
+        if (*f) {
+            DRACO_HIP(hipFree(*f));
+            *f = nullptr;
+        }
+    if (b.dig) DRACO_HIP(hipFree(b.dig));
+    if (b.ids) DRACO_HIP(hipFree(b.ids));
+    b = PfBufs();
+    const size_t c = (size_t)cap;
+    DRACO_HIP(hipMalloc(&b.X, sizeof(float) * c * m->h));
+    DRACO_HIP(hipMalloc(&b.Xn, sizeof(float) * c * m->h));
+    DRACO_HIP(hipMalloc(&b.Q, sizeof(float) * c * QD));
+    DRACO_HIP(hipMalloc(&b.K, sizeof(float) * c * KD));
+    DRACO_HIP(hipMalloc(&b.V, sizeof(float) * c * KD));
+    DRACO_HIP(hipMalloc(&b.O, sizeof(float) * c * QD));
+    DRACO_HIP(hipMalloc(&b.G, sizeof(float) * c * FF));
+    DRACO_HIP(hipMalloc(&b.U, sizeof(float) * c * FF));
+    DRACO_HIP(hipMalloc(&b.Y, sizeof(float) * c * m->h));
+    DRACO_HIP(hipMalloc(&b.part, sizeof(float) * part_n));
+    DRACO_HIP(hipMalloc(&b.dig, dig_n));
+    DRACO_HIP(hipMalloc(&b.ids, sizeof(int) * c));
+    b.cap = cap;
+    b.H = m->h;
+    b.QD = QD;
+    b.KD = KD;
+    b.FF = FF;
+    b.part_n = part_n;
+    b.dig_n = dig_n;
+    return 0;
+}
+
+// Layer l for the T tokens whose hidden rows are in pf.X: the same steps as
+// enqueue_layer (src/m6_engine.c:61-83 with llama_attn_core and
+// m6_dense_op), token rows batched.  Token t sits at rope position pos0 + t
+// and cache row row0 + t.
+int enqueue_prefill_layer(DevModel* m, int l, int T, int pos0, int row0, float eps, hipStream_t st) {
+    PfBufs& b = m->pf;
+    DevAttn* a = m->attn[l];
+    DevFfn* f = m->ffn[l];
+    const int H = m->h;
+    const float* tab = rope_dev(a->rot, a->base, pos0 + T);
+    if (!tab) return -2;
+    if (pf_rms(b.X, m->anorm[l], b.Xn, T, H, eps, st)) return fail(-1, "prefill: rms rejected");
+    // the digits of Xn are written by the first K-quant product and reused by the others
+    auto kquant = [](const DracoMat* x) { return x->L.code == DRACO_Q4_K || x->L.code == DRACO_Q6_K; };
+    if (draco_enqueue_gemm(*a->wq, b.Xn, T, b.Q, b.dig, false, st)) return -1;
+    if (draco_enqueue_gemm(*a->wk, b.Xn, T, b.K, b.dig, kquant(a->wq), st)) return -1;
+    if (draco_enqueue_gemm(*a->wv, b.Xn, T, b.V, b.dig, kquant(a->wq) || kquant(a->wk), st)) return -1;
+    if (pf_rope_append(b.Q, b.K, b.V, a->kc, a->vc, tab, pos0, row0, T, a->NH, a->NKV, a->HD, a->rot, st))
+        return fail(-1, "prefill: rope rejected");
+    if (pf_attention(b.Q, a->kc, a->vc, b.part, b.O, row0, T, a->NH, a->NKV, a->HD, a->scale, st))
+        return fail(-1, "prefill: attention shape NH=%d NKV=%d HD=%d not served", a->NH, a->NKV, a->HD);
+    if (draco_enqueue_gemm(*a->wo, b.O, T, b.Y, b.dig, false, st)) return -1;
+    pf_add(b.X, b.Y, (size_t)T * H, st);
+    if (pf_rms(b.X, m->fnorm[l], b.Xn, T, H, eps, st)) return fail(-1, "prefill: rms rejected");
+    if (draco_enqueue_gemm(*f->g, b.Xn, T, b.G, b.dig, false, st)) return -1;
+    if (draco_enqueue_gemm(*f->u, b.Xn, T, b.U, b.dig, kquant(f->g), st)) return -1;
+    dk_swiglu(b.G, b.U, T * f->FF, st);
+    if (draco_enqueue_gemm(*f->d, b.G, T, b.Y, b.dig, false, st)) return -1;
+    pf_add(b.X, b.Y, (size_t)T * H, st);
+    return 0;
+}
+
+// Tokens ids[0..n) (device) through every layer in chunks of g_prefill_chunk:
+// token i at position pos0 + i and cache row tlen_l + i of layer l (the
+// host tlen counters are not advanced here).  The last token's hidden state
+// is left in pf.X row (last chunk's T - 1); returns that T (0 on error).
+int enqueue_prefill(DevModel* m, const DracoMat* em, const int* ids, int n, int pos0, float eps, hipStream_t st) {
+    const int C = g_prefill_chunk;
+    if (C < 1 || n < 1) return 0;
+    if (ensure_pf(m, C)) return 0;
+    int last = 0;
+    for (int c0 = 0; c0 < n; c0 += C) {
+        const int T = std::min(C, n - c0);
+        if (pf_embed(em->dev, em->L, ids + c0, T, m->pf.X, st)) return 0;
+        for (int l = 0; l < m->n_layer; l++)
+            if (enqueue_prefill_layer(m, l, T, pos0 + c0, *m->attn[l]->snap.tlen + c0, eps, st)) return 0;
+        last = T;
+    }
+    return last;
+}
+
 int check_positions(DevModel* m, int pos, int n_steps) {
     for (int l = 0; l < m->n_layer; l++) {
         const int T = *m->attn[l]->snap.tlen;
@@ -465,9 +585,10 @@ int check_positions(DevModel* m, int pos, int n_steps) {
     return 0;
 }
 
-int upload_state(DevModel* m, int pos, hipStream_t st) {
+// device state = [pos, tlen_l + add for each layer]
+int upload_state(DevModel* m, int pos, hipStream_t st, int add = 0) {
     m->hstate[0] = pos;
-    for (int l = 0; l < m->n_layer; l++) m->hstate[1 + l] = *m->attn[l]->snap.tlen;
+    for (int l = 0; l < m->n_layer; l++) m->hstate[1 + l] = *m->attn[l]->snap.tlen + add;
     DRACO_HIP(hipMemcpyAsync(m->state, m->hstate, sizeof(int) * (1 + m->n_layer), hipMemcpyHostToDevice, st));
     return 0;
 }
@@ -677,11 +798,14 @@ int draco_state_push(const void* layers_v, int n_layer) {
 // reference's loop is Python, src/smol_engine.py:203-213; this runs the same
 // steps without leaving the device) ----
 //
-// Feeds prompt[0..n_prompt) token-serially from the current tlen, then
-// generates n_gen tokens greedily (argmax, first index on ties).  Positions
-// are tlen-based: token i is at position tlen0 + i.  With use_graph != 0 one
-// prefill step and one decode step are captured as HIP graphs and replayed.
-// stats[0] = decode ms (n_gen steps), stats[1] = prefill ms.
+// Feeds prompt[0..n_prompt) from the current tlen, then generates n_gen
+// tokens greedily (argmax, first index on ties).  Positions are tlen-based:
+// token i is at position tlen0 + i.  prompt[0..n_prompt-1) goes through the
+// chunked prefill (draco_set_prefill_chunk; token-serial decode steps when it
+// is 0), the last prompt token through the first decode step.  With use_graph
+// != 0 the token-serial prefill step and the decode step are captured as HIP
+// graphs and replayed.  stats[0] = decode ms (n_gen steps), stats[1] =
+// prefill ms (the n_prompt - 1 tokens before the first decode step).
 int draco_llama_generate(const void* layers_v, int n_layer, int h, float eps, const float* final_norm,
                          const uint8_t* head_w, int head_code, int vocab, const uint8_t* emb_w, int emb_code,
                          const int* prompt, int n_prompt, int n_gen, int use_graph, int* out_tokens,
@@ -690,6 +814,9 @@ int draco_llama_generate(const void* layers_v, int n_layer, int h, float eps, co
     if (int rc = ensure_init()) return report(rc, "draco_llama_generate");
     const M6LayerDesc* layers = (const M6LayerDesc*)layers_v;
     if (n_prompt < 1 || n_gen < 1) return report(fail(-1, "need n_prompt >= 1 and n_gen >= 1"), "draco_llama_generate");
+    for (int i = 0; i < n_prompt; i++)
+        if (prompt[i] < 0 || prompt[i] >= vocab)
+            return report(fail(-1, "prompt token id %d out of range", prompt[i]), "draco_llama_generate");
     DevModel* m = resolve_model(layers, n_layer, h);
     if (!m) return report(-1, "draco_llama_generate");
     const DracoMat* hm = get_mat(head_w, head_code, vocab, h);
@@ -713,9 +840,13 @@ int draco_llama_generate(const void* layers_v, int n_layer, int h, float eps, co
     const bool fused_head = hm->L.code == DRACO_Q4_K || hm->L.code == DRACO_Q6_K || hm->L.code == DRACO_Q8_0;
     std::vector<int> ht(ntok + 64, 0);
     for (int i = 0; i < n_prompt; i++) ht[i] = prompt[i];
-    ht[ntok + 8] = 0;
+    // prompt[0 .. n_prompt - 1) goes through the chunked prefill when enabled
+    // (the last prompt token goes through the first decode step, which also
+    // runs the head); the token cursor then starts past those tokens
+    const int n_chunked = (g_prefill_chunk > 0 && n_prompt - 1 >= 2) ? n_prompt - 1 : 0;
+    if (n_chunked && ensure_pf(m, g_prefill_chunk)) return report(-2, "draco_llama_generate (prefill buffers)");
+    ht[ntok + 8] = n_chunked;
     DRACO_HIP(hipMemcpyAsync(dtok, ht.data(), sizeof(int) * (ntok + 64), hipMemcpyHostToDevice, st));
-    if (int rc = upload_state(m, pos0, st)) return report(rc, "draco_llama_generate");
     (void)cur;
     // With the fused head, a decode step's input embedding was decoded by the
     // previous step's argmax into w.xe (the first one by an embedding launch
@@ -776,7 +907,10 @@ int draco_llama_generate(const void* layers_v, int n_layer, int h, float eps, co
         }
     }
     DRACO_HIP(hipEventRecord(e0, st));
-    for (int i = 0; i < n_prompt - 1; i++) {
+    if (n_chunked && enqueue_prefill(m, em, dtok, n_chunked, pos0, eps, st) <= 0)
+        return report(-1, "draco_llama_generate (chunked prefill)");
+    if (int rc = upload_state(m, pos0 + n_chunked, st, n_chunked)) return report(rc, "draco_llama_generate");
+    for (int i = n_chunked; i < n_prompt - 1; i++) {
         if (use_graph) DRACO_HIP(hipGraphLaunch(gx[0], st));
         else if (int rc = step(false)) return report(rc, "draco_llama_generate");
     }
@@ -807,6 +941,65 @@ int draco_llama_generate(const void* layers_v, int n_layer, int h, float eps, co
     hipEventDestroy(e0);
     hipEventDestroy(e1);
     hipEventDestroy(e2);
+    return 0;
+}
+
+
+// ---- chunked prefill of the llama family (the reference's forward_chunk
+// contract, src/qwen35_prefill.py:209-210 and src/draco_engine_server.py:836-842:
+// the engine state afterwards equals that of forward(ids[i], pos + i) run
+// token by token) ----
+
+// Tokens per chunk of the chunked prefill (draco_llama_prefill and the
+// prompt of draco_llama_generate); 0 makes draco_llama_generate feed its
+// prompt token by token.  Returns the previous value; n < 0 only queries.
+int draco_set_prefill_chunk(int n) {
+    std::lock_guard<std::recursive_mutex> g(api_mutex());
+    const int old = g_prefill_chunk;
+    if (n >= 0) g_prefill_chunk = n > 4096 ? 4096 : n;
+    return old;
+}
+
+// ids[0..n) (host) at positions pos .. pos + n - 1: the KV rows of every layer
+// are appended at rows tlen .. tlen + n - 1 (device mirrors) and every tlen
+// advances by n, as n calls of m6_forward_token would leave them; out_x (h
+// floats, host) receives the last token's hidden state after the last layer.
+int draco_llama_prefill(const void* layers_v, int n_layer, int h, float eps, const uint8_t* emb_w, int emb_code,
+                        int vocab, const int* ids, int n, int pos, float* out_x) {
+    std::lock_guard<std::recursive_mutex> g(api_mutex());
+    if (int rc = ensure_init()) return report(rc, "draco_llama_prefill");
+    const M6LayerDesc* layers = (const M6LayerDesc*)layers_v;
+    if (n < 1 || pos < 0) return report(fail(-1, "need n >= 1 and pos >= 0"), "draco_llama_prefill");
+    for (int i = 0; i < n; i++)
+        if (ids[i] < 0 || ids[i] >= vocab) return report(fail(-1, "token id %d out of range", ids[i]), "draco_llama_prefill");
+    DevModel* m = resolve_model(layers, n_layer, h);
+    if (!m) return report(-1, "draco_llama_prefill");
+    const DracoMat* em = get_mat(emb_w, emb_code, vocab, h);
+    if (!em) return report(-1, "draco_llama_prefill");
+    for (int l = 0; l < n_layer; l++) {
+        const int T = *m->attn[l]->snap.tlen;
+        if (T < 0 || T + n > m->attn[l]->max_t)
+            return report(fail(-1, "layer %d: tlen %d + %d tokens exceeds max_t %d", l, T, n, m->attn[l]->max_t),
+                          "draco_llama_prefill");
+    }
+    const int C = g_prefill_chunk > 0 ? g_prefill_chunk : 256;
+    const int saved = g_prefill_chunk;
+    g_prefill_chunk = C;
+    hipStream_t st = stream();
+    int* dids = (int*)scratch(5, sizeof(int) * ((size_t)n + 64));
+    if (!dids) {
+        g_prefill_chunk = saved;
+        return report(-2, "draco_llama_prefill");
+    }
+    DRACO_HIP(hipMemcpyAsync(dids, ids, sizeof(int) * n, hipMemcpyHostToDevice, st));
+    const int last = enqueue_prefill(m, em, dids, n, pos, eps, st);
+    g_prefill_chunk = saved;
+    if (last <= 0) return report(-1, "draco_llama_prefill");
+    if (out_x)
+        DRACO_HIP(hipMemcpyAsync(out_x, m->pf.X + (size_t)(last - 1) * h, sizeof(float) * h, hipMemcpyDeviceToHost, st));
+    hipError_t e = hipStreamSynchronize(st);
+    if (e != hipSuccess) return report(fail(-2, "draco_llama_prefill: %s", hipGetErrorString(e)), "draco_llama_prefill");
+    for (int l = 0; l < n_layer; l++) *m->attn[l]->snap.tlen += n;
     return 0;
 }
 

@@ -34,5 +34,13 @@ size_t draco_gemm_digit_bytes(int T, int n_in);
 // digitize X[T][n_in] (device) into buf; fills a.xdig/xsc/xs32/xs16, a.T, a.n_in
 int draco_gemm_digits_launch(const float* X, int T, int n_in, uint8_t* buf, GemmArgs& a, hipStream_t st);
 int draco_gemm_launch(GemmArgs& a, hipStream_t st);
+
+struct DracoMat;
+// Y[t][row] = X[t] . W[row] for T token rows (X, Y device, token-major).
+// Q4_K / Q6_K: digits of X into `digits` (draco_gemm_digit_bytes(T, n_in)),
+// skipped when have_digits says they are already there for this X; other
+// formats (Q8_0, F32, F16): one GEMV per token.
+int draco_enqueue_gemm(const DracoMat& m, const float* X, int T, float* Y, uint8_t* digits, bool have_digits,
+                       hipStream_t st);
 // Y[t] for the tokens of every group against that group's W (same shape for all groups)
 int draco_gemm_grouped_launch(GemmArgs& a, hipStream_t st);

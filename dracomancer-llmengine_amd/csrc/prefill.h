@@ -1,0 +1,26 @@
+// prefill.h -- launchers of the chunked-prefill kernels (prefill.hip).
+// All pointers are device pointers; rows are token-major ([T][width]).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "formats.h"
+
+// key splits of the chunk attention and the partial buffer it needs (floats)
+int pf_attn_nsplit(int row0, int T);
+size_t pf_part_floats(int NH, int T, int HD, int nspl);
+
+// X[t] = embedding row ids[t] (private layout of an embedding matrix)
+int pf_embed(const uint8_t* base, const DracoLayout& L, const int* ids, int T, float* X, hipStream_t st);
+// Xn[t] = (X[t] * inv_rms) * w, h <= 4096
+int pf_rms(const float* X, const float* w, float* Xn, int T, int h, float eps, hipStream_t st);
+// rope of Q[t] / K[t] at position pos0 + t; K, V rows into cache row row0 + t
+int pf_rope_append(float* Q, const float* K, const float* V, float* kc, float* vc, const float* tab, int pos0,
+                   int row0, int T, int NH, int NKV, int HD, int rot, hipStream_t st);
+// O[t] = causal attention of query row row0 + t over cache rows [0, row0 + t]
+// (NH / NKV <= 8, HD 64 or 128); part holds pf_part_floats(...) floats
+int pf_attention(const float* Q, const float* kc, const float* vc, float* part, float* O, int row0, int T, int NH,
+                 int NKV, int HD, float scale, hipStream_t st);
+// X += Y over n floats
+int pf_add(float* X, const float* Y, size_t n, hipStream_t st);

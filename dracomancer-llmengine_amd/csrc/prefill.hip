@@ -1,0 +1,274 @@
+// prefill.hip -- chunked prefill of the llama family (gfx950): the T tokens
+// of a chunk go through each layer together, with the weight products on the
+// int8-MFMA GEMM (gemm.hip) and these row-parallel kernels around them:
+//
+//   k_pf_embed          X[t] = embedding row ids[t]
+//   k_pf_rms            Xn[t] = RMSNorm(X[t]) * w            (src/m6_engine.c:31-37)
+//   k_pf_rope_append    rope on Q[t] and K[t] at position pos0 + t, K/V rows
+//                       appended at cache row row0 + t       (src/m6_engine.c:456-481)
+//   k_pf_attn, k_pf_merge
+//                       causal attention: token t attends cache rows
+//                       [0, row0 + t]                        (src/m6_engine.c:482-505)
+//   k_pf_add            X += Y (residual)
+//
+// The result equals running the tokens one by one through m6_forward_token
+// up to fp32 rounding (summation orders differ; the softmax is the split
+// online form, exact in exact arithmetic).
+#include <hip/hip_runtime.h>
+
+#include "dev_common.h"
+#include "embed_dev.h"
+#include "formats.h"
+#include "prefill.h"
+
+namespace {
+
+__global__ __launch_bounds__(256) void k_pf_embed(const uint8_t* __restrict__ base, DracoLayout L,
+                                                  const int* __restrict__ ids, float* __restrict__ X) {
+    const int t = blockIdx.y, p = blockIdx.x * 256 + threadIdx.x;
+    if (p < L.n_in) X[(size_t)t * L.n_in + p] = embed_value(base, L, ids[t], p);
+}
+
+// one block of 256 threads per token row; x held in registers (h <= 256 * PF_RMS_PT)
+constexpr int PF_RMS_PT = 16;
+__global__ __launch_bounds__(256) void k_pf_rms(const float* __restrict__ X, const float* __restrict__ w,
+                                                float* __restrict__ Xn, int h, float eps) {
+    __shared__ float red[4];
+    const float* x = X + (size_t)blockIdx.x * h;
+    float* o = Xn + (size_t)blockIdx.x * h;
+    float v[PF_RMS_PT];
+    float s = 0.f;
+#pragma unroll
+    for (int k = 0; k < PF_RMS_PT; k++) {
+        const int i = threadIdx.x + 256 * k;
+        v[k] = i < h ? x[i] : 0.f;
+        s = fmaf(v[k], v[k], s);
+    }
+    s = wave_sum(s);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
+    __syncthreads();
+    const float tot = (red[0] + red[1]) + (red[2] + red[3]);
+    const float inv = 1.f / sqrtf(tot / (float)h + eps);
+#pragma unroll
+    for (int k = 0; k < PF_RMS_PT; k++) {
+        const int i = threadIdx.x + 256 * k;
+        if (i < h) o[i] = w ? v[k] * inv * w[i] : v[k] * inv;
+    }
+}
+
+// Q [T][NH*HD] rotated in place; K [T][KD] rotated into kc row row0 + t; V
+// [T][KD] copied into vc row row0 + t.  One thread per even index of a pair
+// (pairs (2i, 2i+1) of a head, the GGML "normal" rope, src/m6_engine.c:134-143).
+__global__ __launch_bounds__(256) void k_pf_rope_append(float* __restrict__ Q, const float* __restrict__ K,
+                                                        const float* __restrict__ V, float* __restrict__ kc,
+                                                        float* __restrict__ vc, const float* __restrict__ tab,
+                                                        int pos0, int row0, int NH, int NKV, int HD, int rot) {
+    const int t = blockIdx.y, i = blockIdx.x * 256 + threadIdx.x;
+    const int QD = NH * HD, KD = NKV * HD, half = rot / 2;
+    const float* ang = tab + (size_t)(pos0 + t) * half * 2;
+    if (i < QD) {
+        const int d = i % HD;
+        float* q = Q + (size_t)t * QD;
+        if (d < rot && (d & 1) == 0) {
+            const float c = ang[d], s = ang[d + 1];
+            const float a = q[i], b = q[i + 1];
+            q[i] = a * c - b * s;
+            q[i + 1] = a * s + b * c;
+        }
+    } else if (i < QD + KD) {
+        const int j = i - QD, d = j % HD;
+        const float* k = K + (size_t)t * KD;
+        float* dst = kc + (size_t)(row0 + t) * KD;
+        if (d < rot) {
+            if ((d & 1) == 0) {
+                const float c = ang[d], s = ang[d + 1];
+                const float a = k[j], b = k[j + 1];
+                dst[j] = a * c - b * s;
+                dst[j + 1] = a * s + b * c;
+            }
+        } else {
+            dst[j] = k[j];
+        }
+    } else if (i < QD + 2 * KD) {
+        const int j = i - QD - KD;
+        vc[(size_t)(row0 + t) * KD + j] = V[(size_t)t * KD + j];
+    }
+}
+
+// Causal attention of a chunk, split over the key rows.  Block (g, qt, s):
+// kv head g, queries qt*64 .. qt*64+63 of the chunk (lane = query), key split
+// s of rows [0, row0 + last query of the tile].  Wave j is q head g*rep + j;
+// the rep waves share the K / V rows, staged in LDS 64 rows at a time and
+// read by every lane at the same address (broadcast).  Keys go in groups of
+// 16: scores, one online-softmax rescale, then P.V.  Writes the unnormalised
+// (o[HD], m, l) of (head, query, split) for k_pf_merge.
+constexpr int PF_QT = 64, PF_KT = 64, PF_KG = 16;
+
+template <int HD>
+__global__ __launch_bounds__(512) void k_pf_attn(const float* __restrict__ Q, const float* __restrict__ kc,
+                                                 const float* __restrict__ vc, float* __restrict__ part, int row0,
+                                                 int T, int NH, int NKV, int nspl, float scale) {
+    extern __shared__ __align__(16) float sm[];
+    float* Ks = sm;
+    float* Vs = sm + PF_KT * HD;
+    const int g = blockIdx.x, qt = blockIdx.y, s = blockIdx.z;
+    const int tid = threadIdx.x, lane = tid & 63, j = tid >> 6;
+    const int rep = NH / NKV, h = g * rep + j, KD = NKV * HD, QD = NH * HD;
+    const int t = qt * PF_QT + lane, qrow = row0 + t;
+    const bool live = t < T;
+    const int kend = row0 + min(T, (qt + 1) * PF_QT);
+    const int chunk = (kend + nspl - 1) / nspl;
+    const int k0 = min(kend, s * chunk), k1 = min(kend, k0 + chunk);
+    float q[HD], o[HD];
+#pragma unroll
+    for (int d = 0; d < HD; d += 4) {
+        const float4 v = live ? ld4(Q + (size_t)t * QD + h * HD + d) : make_float4(0.f, 0.f, 0.f, 0.f);
+        q[d] = v.x; q[d + 1] = v.y; q[d + 2] = v.z; q[d + 3] = v.w;
+        o[d] = o[d + 1] = o[d + 2] = o[d + 3] = 0.f;
+    }
+    float m = -INFINITY, l = 0.f;
+    for (int kb = k0; kb < k1; kb += PF_KT) {
+        const int nr = min(PF_KT, k1 - kb);
+        for (int i = tid; i < nr * (HD / 4); i += blockDim.x) {
+            const int r = i / (HD / 4), c = 4 * (i % (HD / 4));
+            *reinterpret_cast<float4*>(Ks + r * HD + c) = ld4(kc + (size_t)(kb + r) * KD + g * HD + c);
+            *reinterpret_cast<float4*>(Vs + r * HD + c) = ld4(vc + (size_t)(kb + r) * KD + g * HD + c);
+        }
+        __syncthreads();
+        for (int c0 = 0; c0 < nr; c0 += PF_KG) {
+            const int ng = min(PF_KG, nr - c0);
+            float sc[PF_KG];
+            float cm = -INFINITY;
+#pragma unroll
+            for (int jj = 0; jj < PF_KG; jj++) {
+                sc[jj] = -INFINITY;
+                if (jj < ng) {
+                    const float* kr = Ks + (c0 + jj) * HD;
+                    float acc = 0.f;
+#pragma unroll
+                    for (int d = 0; d < HD; d += 4) {
+                        const float4 kv = *reinterpret_cast<const float4*>(kr + d);
+                        acc = fmaf(q[d], kv.x, acc);
+                        acc = fmaf(q[d + 1], kv.y, acc);
+                        acc = fmaf(q[d + 2], kv.z, acc);
+                        acc = fmaf(q[d + 3], kv.w, acc);
+                    }
+                    if (live && kb + c0 + jj <= qrow) sc[jj] = acc * scale;
+                    cm = fmaxf(cm, sc[jj]);
+                }
+            }
+            const float mn = fmaxf(m, cm);
+            if (mn > -INFINITY) {
+                const float corr = m > -INFINITY ? expf(m - mn) : 0.f;
+                l *= corr;
+#pragma unroll
+                for (int d = 0; d < HD; d++) o[d] *= corr;
+#pragma unroll
+                for (int jj = 0; jj < PF_KG; jj++) {
+                    if (jj < ng) {
+                        const float p = sc[jj] > -INFINITY ? expf(sc[jj] - mn) : 0.f;
+                        l += p;
+                        const float* vr = Vs + (c0 + jj) * HD;
+#pragma unroll
+                        for (int d = 0; d < HD; d += 4) {
+                            const float4 vv = *reinterpret_cast<const float4*>(vr + d);
+                            o[d] = fmaf(p, vv.x, o[d]);
+                            o[d + 1] = fmaf(p, vv.y, o[d + 1]);
+                            o[d + 2] = fmaf(p, vv.z, o[d + 2]);
+                            o[d + 3] = fmaf(p, vv.w, o[d + 3]);
+                        }
+                    }
+                }
+                m = mn;
+            }
+        }
+        __syncthreads();
+    }
+    if (!live) return;
+    float* pp = part + (((size_t)h * T + t) * nspl + s) * (HD + 2);
+#pragma unroll
+    for (int d = 0; d < HD; d++) pp[d] = o[d];
+    pp[HD] = m;
+    pp[HD + 1] = l;
+}
+
+// out[t][h*HD + d] = sum_s o_s[d] e^(m_s - M) / sum_s l_s e^(m_s - M)
+__global__ __launch_bounds__(256) void k_pf_merge(const float* __restrict__ part, float* __restrict__ O, int T,
+                                                  int NH, int HD, int nspl) {
+    const int t = blockIdx.x, h = blockIdx.y, d = threadIdx.x;
+    if (d >= HD) return;
+    const float* pp = part + ((size_t)h * T + t) * nspl * (HD + 2);
+    float M = -INFINITY;
+    for (int s = 0; s < nspl; s++) M = fmaxf(M, pp[s * (HD + 2) + HD]);
+    float num = 0.f, den = 0.f;
+    for (int s = 0; s < nspl; s++) {
+        const float ms = pp[s * (HD + 2) + HD];
+        if (ms == -INFINITY) continue;
+        const float e = expf(ms - M);
+        den = fmaf(pp[s * (HD + 2) + HD + 1], e, den);
+        num = fmaf(pp[s * (HD + 2) + d], e, num);
+    }
+    O[(size_t)t * NH * HD + h * HD + d] = num / den;
+}
+
+__global__ __launch_bounds__(256) void k_pf_add(float* __restrict__ X, const float* __restrict__ Y, size_t n) {
+    for (size_t i = blockIdx.x * (size_t)256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) X[i] += Y[i];
+}
+
+}  // namespace
+
+int pf_attn_nsplit(int row0, int T) {
+    // about 64 key rows per split at the tile holding the chunk's last query
+    const int n = (row0 + T + 63) / 64;
+    return n < 1 ? 1 : (n > 64 ? 64 : n);
+}
+
+size_t pf_part_floats(int NH, int T, int HD, int nspl) { return (size_t)NH * T * nspl * (HD + 2); }
+
+int pf_embed(const uint8_t* base, const DracoLayout& L, const int* ids, int T, float* X, hipStream_t st) {
+    if (T < 1) return -1;
+    hipLaunchKernelGGL(k_pf_embed, dim3((L.n_in + 255) / 256, T), dim3(256), 0, st, base, L, ids, X);
+    return 0;
+}
+
+int pf_rms(const float* X, const float* w, float* Xn, int T, int h, float eps, hipStream_t st) {
+    if (T < 1 || h > 256 * PF_RMS_PT) return -1;
+    hipLaunchKernelGGL(k_pf_rms, dim3(T), dim3(256), 0, st, X, w, Xn, h, eps);
+    return 0;
+}
+
+int pf_rope_append(float* Q, const float* K, const float* V, float* kc, float* vc, const float* tab, int pos0,
+                   int row0, int T, int NH, int NKV, int HD, int rot, hipStream_t st) {
+    if (T < 1 || (rot & 1) || rot > HD) return -1;
+    const int n = NH * HD + 2 * NKV * HD;
+    hipLaunchKernelGGL(k_pf_rope_append, dim3((n + 255) / 256, T), dim3(256), 0, st, Q, K, V, kc, vc, tab, pos0,
+                       row0, NH, NKV, HD, rot);
+    return 0;
+}
+
+int pf_attention(const float* Q, const float* kc, const float* vc, float* part, float* O, int row0, int T, int NH,
+                 int NKV, int HD, float scale, hipStream_t st) {
+    if (T < 1 || NKV < 1 || NH % NKV || NH / NKV > 8 || (HD != 64 && HD != 128)) return -1;
+    const int nspl = pf_attn_nsplit(row0, T);
+    const dim3 grid(NKV, (T + PF_QT - 1) / PF_QT, nspl), block(64 * (NH / NKV));
+    const size_t lds = sizeof(float) * 2 * PF_KT * HD;
+    if (HD == 64) {
+        hipLaunchKernelGGL(k_pf_attn<64>, grid, block, lds, st, Q, kc, vc, part, row0, T, NH, NKV, nspl, scale);
+    } else {
+        static bool attr = false;
+        if (!attr) {
+            (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&k_pf_attn<128>),
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, 64 * 1024);
+            attr = true;
+        }
+        hipLaunchKernelGGL(k_pf_attn<128>, grid, block, lds, st, Q, kc, vc, part, row0, T, NH, NKV, nspl, scale);
+    }
+    hipLaunchKernelGGL(k_pf_merge, dim3(T, NH), dim3(HD), 0, st, part, O, T, NH, HD, nspl);
+    return 0;
+}
+
+int pf_add(float* X, const float* Y, size_t n, hipStream_t st) {
+    const size_t blocks = (n + 255) / 256;
+    hipLaunchKernelGGL(k_pf_add, dim3(blocks < 2048 ? (unsigned)blocks : 2048u), dim3(256), 0, st, X, Y, n);
+    return 0;
+}

@@ -177,6 +177,20 @@ class LlamaDriver:
         self.x[:] = hidden
         return [int(t) for t in toks], hidden, (float(stats[0]), float(stats[1]))
 
+    def prefill_chunk(self, ids, pos0):
+        """Chunked prefill (the forward_chunk contract of src/qwen35_prefill.py:209-239
+        and src/draco_engine_server.py:836-842, here for the llama family): leaves
+        the engine state of forward(ids[i], pos0 + i) run token by token and
+        returns the last position's logits.  Only valid with the HIP engine."""
+        ids = np.ascontiguousarray(ids, np.int32)
+        L = self.engine.cdll
+        rc = L.draco_llama_prefill(ct.cast(self.descs, ct.c_void_p), self.NL, self.H, np.float32(self.cfg.eps),
+                                   ct.c_void_p(self.emb_buf.ctypes.data), self.emb_code, self.cfg.vocab,
+                                   ids.ctypes.data_as(ct.POINTER(ct.c_int)), len(ids), int(pos0), pf(self.x))
+        if rc != 0:
+            raise RuntimeError(f"draco_llama_prefill rc={rc}: {L.draco_last_error().decode()}")
+        return self.logits_of_x()
+
     def greedy(self, prompt, n_gen, collect_logits=()):
         """Token-serial prefill then greedy decode (src/smol_engine.py:203-213)."""
         for pos, t in enumerate(prompt):

@@ -55,6 +55,9 @@ SIGNATURES = {
     "draco_llama_generate": (ct.c_int, [ct.c_void_p, ct.c_int, ct.c_int, ct.c_float, f32p, ct.c_void_p,
                                         ct.c_int, ct.c_int, ct.c_void_p, ct.c_int, i32p, ct.c_int, ct.c_int,
                                         ct.c_int, i32p, f32p, f32p]),
+    "draco_set_prefill_chunk": (ct.c_int, [ct.c_int]),
+    "draco_llama_prefill": (ct.c_int, [ct.c_void_p, ct.c_int, ct.c_int, ct.c_float, ct.c_void_p, ct.c_int, ct.c_int,
+                                       i32p, ct.c_int, ct.c_int, f32p]),
     # qwen35 hybrid layers (src/m6_layer.c:189-518)
     "m6_gdn_attn": (None, [f32p, ct.c_void_p, f32p, f32p, f32p, f32p, f32p]),
     "m6_full_attn": (None, [f32p, ct.c_void_p, f32p, f32p, ct.c_int, ct.c_int, f32p, f32p, f32p, f32p,

@@ -104,15 +104,34 @@ int draco_state_push(const void* layers, int n_layer);
 /* ---- device-resident greedy loop (no reference counterpart: the
  * reference's loop is Python, src/smol_engine.py:203-213) ----------------
  * Feeds prompt[0..n_prompt) from the current tlen, then generates n_gen
- * tokens by argmax (first index on ties), all on the device; with use_graph
- * one prefill step and one decode step are captured as HIP graphs and
- * replayed.  out_hidden[h] = x after the last forward (nullable);
- * stats[0] = decode ms, stats[1] = prefill ms (nullable). */
+ * tokens by argmax (first index on ties), all on the device.
+ * prompt[0..n_prompt-1) goes through the chunked prefill below (token-serial
+ * decode steps when the chunk size is 0); the last prompt token goes through
+ * the first decode step.  With use_graph the token-serial prefill step and
+ * the decode step are captured as HIP graphs and replayed.
+ * out_hidden[h] = x after the last forward (nullable); stats[0] = decode ms,
+ * stats[1] = prefill ms of the n_prompt - 1 tokens (nullable). */
 int draco_llama_generate(const void* layers, int n_layer, int h, float eps,
                          const float* final_norm, const uint8_t* head_w, int head_code, int vocab,
                          const uint8_t* emb_w, int emb_code, const int* prompt, int n_prompt,
                          int n_gen, int use_graph, int* out_tokens, float* out_hidden,
                          float* stats);
+
+/* ---- chunked prefill of the llama family: the reference's forward_chunk
+ * contract (src/qwen35_prefill.py:209-210, src/draco_engine_server.py:836-842:
+ * afterwards the engine state is that of forward(ids[i], pos + i) run token
+ * by token), which the reference implements for qwen35 only ----------------
+ * ids[0..n) at positions pos .. pos + n - 1, in chunks of the chunk size:
+ * per layer one RMSNorm, the q/k/v, o, gate/up and down products as int8-MFMA
+ * GEMMs over the chunk's tokens, rope + KV append at rows tlen .. tlen + n - 1
+ * (device mirrors) and causal attention; every tlen advances by n.
+ * out_x[h] (host, nullable) = hidden state of the last token after the last
+ * layer (the x m6_forward_token leaves).  0 = ok. */
+int draco_llama_prefill(const void* layers, int n_layer, int h, float eps, const uint8_t* emb_w, int emb_code,
+                        int vocab, const int* ids, int n, int pos, float* out_x);
+/* tokens per prefill chunk (default 256; 0 = draco_llama_generate feeds its
+ * prompt token by token).  Returns the previous value; n < 0 only queries. */
+int draco_set_prefill_chunk(int n);
 
 /* ---- library utilities (no reference counterpart) ----------------------- */
 
