@@ -615,7 +615,8 @@ __global__ __launch_bounds__(256) void k_seg(const SegKArgs a) {
 // index of the maximum), write tokens[*cursor + 1] and advance the token
 // state.  With emb_out set, also decode the new token's embedding row into
 // emb_out (the next token's input), so generation needs no embedding launch.
-// One block; runs after the head GEMV in stream order.
+// Runs after the head GEMV in stream order: one block, or with emb_out one
+// block per 256 embedding values (at most 64).
 __global__ __launch_bounds__(256) void k_argmax_finalize(const float* __restrict__ pv, const int* __restrict__ pi,
                                                          int nb, int* __restrict__ tokens, int* cursor,
                                                          int* state, int n_layer, const uint8_t* __restrict__ emb,
@@ -624,11 +625,15 @@ __global__ __launch_bounds__(256) void k_argmax_finalize(const float* __restrict
     __shared__ int si[4];
     __shared__ int tok_s;
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const bool lead = blockIdx.x == 0;
     // position and per-layer lengths advance in parallel, one entry per
     // thread (nothing in this launch reads them)
-    if (state)
+    if (state && lead)
         for (int i = tid; i <= n_layer; i += 256) state[i] += 1;
-    const int cur = (tid == 0 && cursor) ? cursor[0] : -1;
+    const int cur = (lead && tid == 0 && cursor) ? cursor[0] : -1;
+    // every block reduces the same partials in the same order (same winner);
+    // block 0 records the token, every block decodes its slice of the next
+    // token's embedding row
     float v = -INFINITY;
     int idx = 0x7fffffff;
     for (int i = tid; i < nb; i += 256) am_merge(v, idx, pv[i], pi[i]);
@@ -640,14 +645,20 @@ __global__ __launch_bounds__(256) void k_argmax_finalize(const float* __restrict
     __syncthreads();
     if (tid == 0) {
         for (int w = 1; w < 4; w++) am_merge(v, idx, sv[w], si[w]);
-        tokens[cur + 1] = idx;
-        if (cursor) cursor[0] = cur + 1;
+        if (lead) {
+            tokens[cur + 1] = idx;
+            if (cursor) cursor[0] = cur + 1;
+        }
         tok_s = idx;
     }
     if (!emb_out) return;
     __syncthreads();
     const int tok = tok_s;
-    for (int p = tid; p < emb_L.n_in; p += 256) emb_out[p] = embed_value(emb, emb_L, tok, p);
+    for (int p = blockIdx.x * 256 + tid; p < emb_L.n_in; p += gridDim.x * 256) emb_out[p] = embed_value(emb, emb_L, tok, p);
+}
+
+unsigned finalize_blocks(const float* emb_out, int n_in) {
+    return emb_out ? (unsigned)((n_in + 255) / 256 < 64 ? (n_in + 255) / 256 : 64) : 1u;
 }
 
 // ------------------------------------------------------------ F32 / F16 --
@@ -812,7 +823,7 @@ int seg_launch_dq(SegLaunch& a, hipStream_t st) {
     else if (nw == 8) launch_dq_nw<8>(a, fm, dual, grid, st);
     else launch_dq_nw<16>(a, fm, dual, grid, st);
     if (a.seg[0].epi == EPI_ARGMAX)
-        hipLaunchKernelGGL(k_argmax_finalize, dim3(1), dim3(256), 0, st, a.am_val, a.am_idx, grid, a.tokens,
+        hipLaunchKernelGGL(k_argmax_finalize, dim3(finalize_blocks(a.emb_out, a.emb_L.n_in)), dim3(256), 0, st, a.am_val, a.am_idx, grid, a.tokens,
                            const_cast<int*>(a.cursor), a.advance_state, a.advance_layers, a.emb, a.emb_L,
                            a.emb_out);
     return 0;
@@ -849,7 +860,7 @@ int seg_launch_q8(SegLaunch& a, hipStream_t st) {
     if (dual) hipLaunchKernelGGL((k_seg<FQ80, true>), g, b, shm, st, k);
     else hipLaunchKernelGGL((k_seg<FQ80, false>), g, b, shm, st, k);
     if (a.seg[0].epi == EPI_ARGMAX)
-        hipLaunchKernelGGL(k_argmax_finalize, dim3(1), dim3(256), 0, st, a.am_val, a.am_idx, a.seg[0].n_blocks,
+        hipLaunchKernelGGL(k_argmax_finalize, dim3(finalize_blocks(a.emb_out, a.emb_L.n_in)), dim3(256), 0, st, a.am_val, a.am_idx, a.seg[0].n_blocks,
                            a.tokens, const_cast<int*>(a.cursor), a.advance_state, a.advance_layers, a.emb, a.emb_L,
                            a.emb_out);
     return 0;
