@@ -2,11 +2,13 @@
 
 Workload: Llama-3.2-1B-shaped decoder, random-init
 N(0,0.02) from seed 0, Q4_K_M-style (Q4_K q/k/o/gate/up, Q6_K v/down/tied
-head), a 960-token random prompt, then greedy decode at positions 960..1023.
-One "step" is one decode token (embedding -> 16 layers -> head -> argmax),
-run by the device-resident loop (draco_llama_generate, graph-replayed); the
-prompt is fed untimed before every timed run.  value = timed tokens / timed
-seconds (HIP events on the decode stream).
+head), a 960-token random prompt through the 256-token chunked prefill, then
+greedy decode at positions 960..1023.  One "step" is one decode token
+(embedding -> 16 layers -> head -> argmax), run by the device-resident loop
+(draco_llama_generate, graph-replayed); the prompt is fed before every timed
+run and is not part of `value`.  value = timed tokens / timed seconds (HIP
+events on the decode stream).  configs2_prefill reports the prompt's chunked
+prefill time (and the token-serial time of the same prompt for scale).
 
 roofline: the Q4_K GEMV of configs[1] (W 14336x4096 from seed 1, fp32 x),
 timed live with per-launch HIP event pairs while rotating 10 distinct weight
@@ -35,9 +37,9 @@ import numpy as np  # noqa: E402
 PEAK_HBM_GBS = 8000.0
 # HBM bytes per launch of the roofline kernel from the FETCH_SIZE / WRITE_SIZE
 # counter passes (rocprofv3 --pmc, scaled by a device copy of known size:
-# 2046.6 B per FETCH_SIZE unit, 1024 B per WRITE_SIZE unit): 16282.5 * 2046.6
+# 2046.6 B per FETCH_SIZE unit, 1024 B per WRITE_SIZE unit): 16318.4 * 2046.6
 # + 56.0 * 1024 bytes
-TRAFFIC_BYTES = 33381109
+TRAFFIC_BYTES = 33454581
 CTX_START = 960
 MAX_DECODE = 64  # positions 960..1023 (max_t 1024)
 
@@ -344,16 +346,29 @@ def main():
     if args.warmup > 0:
         run(min(args.warmup, MAX_DECODE))
         log(f"warmup {args.warmup} decode steps done")
-    left, ms, toks_first = args.steps, 0.0, None
+    left, ms, toks_first, pre_list = args.steps, 0.0, None, []
     while left > 0:
         k = min(left, MAX_DECODE)
         toks, hidden, (dec_ms, pre_ms) = run(k)
         if toks_first is None:
             toks_first = toks
         ms += dec_ms
+        pre_list.append(pre_ms)
         left -= k
         log(f"timed {k} decode steps: {dec_ms:.2f} ms (prefill {pre_ms:.1f} ms)")
     tok_s = args.steps / (ms / 1e3)
+    # the prompt (all but its last token, which the first decode step takes)
+    # through the 256-token chunked prefill, and once token by token for scale
+    n_pre = len(prompt) - 1
+    chunk = L.draco_set_prefill_chunk(-1)
+    L.draco_set_prefill_chunk(0)
+    _, _, (_, serial_ms) = run(1)
+    L.draco_set_prefill_chunk(chunk)
+    pre_ms = float(np.median(pre_list))
+    prefill = {"prompt_tokens": n_pre, "chunk": chunk, "ms": round(pre_ms, 3),
+               "tok_s": round(n_pre / (pre_ms / 1e3), 1), "token_serial_ms": round(serial_ms, 3),
+               "token_serial_tok_s": round(n_pre / (serial_ms / 1e3), 1)}
+    log(f"prefill {n_pre} tokens: chunked {pre_ms:.1f} ms, token-serial {serial_ms:.1f} ms")
     match = None
     gpath = os.path.join(ROOT, "tests", "golden", "llama1b.npz")
     if os.path.exists(gpath):
@@ -400,6 +415,7 @@ def main():
                                "positions 960..1023", "global_batch": 1, "seq_len": 1024,
                    "parallelism": "single GPU"},
         "greedy_tokens_match_reference": match,
+        "configs2_prefill": prefill,
         "roofline": roof,
         "configs1_q8k_gemv": q8,
         "configs3_moe_ffn": moe,
