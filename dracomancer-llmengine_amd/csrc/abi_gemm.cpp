@@ -23,6 +23,7 @@ int draco_enqueue_gemm(const DracoMat& m, const float* X, int T, float* Y, uint8
                 return fail(-1, "gemm: gemv launch rejected");
         return 0;
     }
+#ifdef DRACO_GEMM_INT8
     GemmArgs a = {};
     if (have_digits) {
         // the launch only fills the buffer views; enqueue nothing
@@ -42,6 +43,26 @@ int draco_enqueue_gemm(const DracoMat& m, const float* X, int T, float* Y, uint8
     a.ldy = m.L.n_out;
     if (draco_gemm_launch(a, st)) return fail(-1, "gemm: launch rejected");
     return 0;
+#else
+    if (!have_digits && draco_gemmh_x_launch(X, T, m.L.n_in, digits, st))
+        return fail(-1, "gemm: activation launch rejected");
+    GemmHArgs a = {};
+    a.W = m.dev;
+    a.L = m.L;
+    a.n_in = m.L.n_in;
+    a.T = T;
+    a.xh = digits;
+    a.Y = Y;
+    a.ldy = m.L.n_out;
+    const size_t pf = draco_gemmh_part_floats(m.L, T, a.ldy);
+    if (pf) {
+        // grow-only; callers that capture graphs enqueue once before capturing
+        a.part = (float*)scratch(12, sizeof(float) * pf);
+        if (!a.part) return -2;
+    }
+    if (draco_gemmh_launch(a, st)) return fail(-1, "gemm: launch rejected");
+    return 0;
+#endif
 }
 
 namespace {
@@ -115,8 +136,16 @@ int draco_bench_gemm(int code, const uint8_t* W, int n_out, int n_in, int T, int
     DRACO_HIP(hipMalloc(&dd, draco_gemm_digit_bytes(T, n_in)));
     DRACO_HIP(hipMemcpy(dx, xh.data(), sizeof(float) * xh.size(), hipMemcpyHostToDevice));
     hipStream_t st = stream();
+    // one eager product first: it sizes the K-split scratch outside the capture
+    if (enqueue_gemm(mats[0], dx, T, dy, dd, st)) return -1;
+    DRACO_HIP(hipStreamSynchronize(st));
+#ifdef DRACO_GEMM_INT8
     GemmArgs a = {};
     if (draco_gemm_digits_launch(dx, T, n_in, dd, a, st)) return fail(-1, "bench gemm: digits rejected");
+#else
+    float* part = (float*)scratch(12, sizeof(float) * (draco_gemmh_part_floats(L, T, n_out) + 1));
+    if (!part) return -2;
+#endif
     hipEvent_t e0, e1;
     DRACO_HIP(hipEventCreate(&e0));
     DRACO_HIP(hipEventCreate(&e1));
@@ -128,12 +157,25 @@ int draco_bench_gemm(int code, const uint8_t* W, int n_out, int n_in, int T, int
             if (mode == 0) {
                 enqueue_gemm(mats[i % n_copies], dx, T, dy, dd, st);
             } else {
+#ifdef DRACO_GEMM_INT8
                 GemmArgs b = a;
                 b.W = mats[i % n_copies].dev;
                 b.L = L;
                 b.Y = dy;
                 b.ldy = n_out;
                 draco_gemm_launch(b, st);
+#else
+                GemmHArgs b = {};
+                b.W = mats[i % n_copies].dev;
+                b.L = L;
+                b.n_in = n_in;
+                b.T = T;
+                b.xh = dd;
+                b.Y = dy;
+                b.ldy = n_out;
+                b.part = part;
+                draco_gemmh_launch(b, st);
+#endif
             }
         }
         DRACO_HIP(hipStreamEndCapture(st, &graph));

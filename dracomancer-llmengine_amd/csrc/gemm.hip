@@ -324,8 +324,11 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_q6(const GemmArgs a) {
 
 size_t draco_gemm_digit_bytes(int T, int n_in) {
     const size_t oct = (size_t)(T + 7) / 8;
-    return oct * ((size_t)n_in / 32) * 1024 + oct * ((size_t)n_in / 256) * 32 + oct * ((size_t)n_in / 32) * 32 +
-           oct * ((size_t)n_in / 16) * 32 + 256;
+    const size_t dig = oct * ((size_t)n_in / 32) * 1024 + oct * ((size_t)n_in / 256) * 32 +
+                       oct * ((size_t)n_in / 32) * 32 + oct * ((size_t)n_in / 16) * 32 + 256;
+    // the buffer also holds the f16 GEMM's activation operands (draco_enqueue_gemm)
+    const size_t xh = draco_gemmh_x_bytes(T, n_in);
+    return dig > xh ? dig : xh;
 }
 
 int draco_gemm_digits_launch(const float* X, int T, int n_in, uint8_t* buf, GemmArgs& a, hipStream_t st) {
