@@ -185,15 +185,16 @@ def qwen35_ops_configs4(lib, told=4096, iters=50):
     return res
 
 
-PEAK_INT8_TOPS = 5000.0
+PEAK_F16_TFLOPS = 2500.0  # MI355X dense f16 MFMA
 
 
 def prefill_gemm_configs2(lib, T=256, n_copies=4, iters=20):
     """configs[2] chunked prefill: one 256-token chunk through a Llama-1B layer's seven projections.
 
-    fp32-equivalent TFLOP/s = 2*T*n_out*n_in / time.  The int8 MFMA work issued
-    is 4x that (four digits of x) for Q4_K and 8x for Q6_K (A block-diagonal over
-    16-value halves); `mfma_util` = issued int8 ops / (time * 5.0 POP/s).
+    fp32-equivalent TFLOP/s = 2*T*n_out*n_in / time.  The f16 MFMA work issued
+    is 2x that for Q4_K (hi and lo halves of x; plus 1/8 for the min term on a
+    K-padded 16-slot MFMA) and 4x for Q6_K (hi/lo x the two scale parts);
+    `mfma_util` = issued f16 MFMA flops / (time * 2.5 PFLOP/s dense f16).
     """
     shapes = [("q", 5, 2048, 2048), ("k", 5, 512, 2048), ("v", 4, 512, 2048), ("o", 5, 2048, 2048),
               ("gate", 5, 8192, 2048), ("up", 5, 8192, 2048), ("down", 4, 2048, 8192)]
@@ -207,7 +208,7 @@ def prefill_gemm_configs2(lib, T=256, n_copies=4, iters=20):
             raise RuntimeError(lib.last_error())
         us = float(o[0])
         flop = 2.0 * T * n_out * n_in
-        i8 = flop * (4 if code == 5 else 8)
+        i8 = flop * (2.0 * 34.0 / 32.0 if code == 5 else 4.0)
         res[name] = {"us": round(us, 2), "us_kernel_only": round(float(o[1]), 2),
                      "tflops_fp32_equiv": round(flop / us / 1e6, 1)}
         tot_us += us
@@ -215,7 +216,7 @@ def prefill_gemm_configs2(lib, T=256, n_copies=4, iters=20):
         tot_i8 += i8
     return {"tokens": T, "us_per_layer_chunk": round(tot_us, 1),
             "tflops_fp32_equiv": round(tot_flop / tot_us / 1e6, 1),
-            "mfma_util": round(tot_i8 / tot_us / 1e6 / PEAK_INT8_TOPS, 4),
+            "mfma_util": round(tot_i8 / tot_us / 1e6 / PEAK_F16_TFLOPS, 4),
             "prefill_tok_s_16_layers": round(T / (16 * tot_us * 1e-6), 1), "per_matrix": res}
 
 
@@ -321,7 +322,7 @@ def main():
             f"{gdn['us_per_decode_step']} us/decode step")
         pre = prefill_gemm_configs2(lib)
         log(f"prefill GEMM configs[2] (256-token chunk, one layer): {pre['us_per_layer_chunk']} us, "
-            f"{pre['tflops_fp32_equiv']} TFLOP/s fp32-equiv, int8 MFMA util {pre['mfma_util']}")
+            f"{pre['tflops_fp32_equiv']} TFLOP/s fp32-equiv, f16 MFMA util {pre['mfma_util']}")
         qw = qwen35_ops_configs4(lib)
         log(f"qwen35 ops configs[4]: GDN layer {qw['gdn_op']['us_per_token']} us/token, full attention "
             f"{qw['full_attn_op']['us_per_token']} us/token at 4096 cached rows")
@@ -391,7 +392,7 @@ def main():
             f"{gdn['us_per_decode_step']} us/decode step")
         pre = prefill_gemm_configs2(lib)
         log(f"prefill GEMM configs[2] (256-token chunk, one layer): {pre['us_per_layer_chunk']} us, "
-            f"{pre['tflops_fp32_equiv']} TFLOP/s fp32-equiv, int8 MFMA util {pre['mfma_util']}")
+            f"{pre['tflops_fp32_equiv']} TFLOP/s fp32-equiv, f16 MFMA util {pre['mfma_util']}")
         qw = qwen35_ops_configs4(lib)
         log(f"qwen35 ops configs[4]: GDN layer {qw['gdn_op']['us_per_token']} us/token, full attention "
             f"{qw['full_attn_op']['us_per_token']} us/token at 4096 cached rows")

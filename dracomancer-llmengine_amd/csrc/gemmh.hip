@@ -142,7 +142,133 @@ __device__ __forceinline__ void stage_store(uint8_t* dst, const uint4 (&r)[9], i
 }
 
 // ------------------------------------------------------------------ GEMM --
-// FM 1 = Q4_K, 2 = Q6_K.  Grid (row blocks of 4*RW*32 rows, token tiles, K splits).
+// Raw weight registers of one (32-row tile, super-block) for lane (n, u).
+template <int FM>
+struct WFrag;
+template <>
+struct WFrag<1> {  // Q4_K: quant vectors (r, gh) = (v>>1, v&1), the row header
+    uint4 qv[4], h;
+};
+template <>
+struct WFrag<2> {  // Q6_K: ql A, ql B, qh and 4 scales of lane slots g2 = 0, 1; d
+    uint4 qa[2], qb[2], qh[2];
+    uint32_t sc4[2];
+    uint32_t d;
+};
+
+__device__ __forceinline__ void wload(const uint8_t* item, int j, int u, WFrag<1>& f) {
+#pragma unroll
+    for (int v = 0; v < 4; v++) f.qv[v] = ldnt4(item + (v >> 1) * 1024 + 16 * (j + 16 * (2 * (v & 1) + u)));
+    f.h = ldnt4(item + 2048 + 16 * j);
+}
+__device__ __forceinline__ void wload(const uint8_t* item, int j, int u, WFrag<2>& f) {
+#pragma unroll
+    for (int g2 = 0; g2 < 2; g2++) {
+        const int ls = j + 16 * (2 * g2 + u);
+        f.qa[g2] = ldnt4(item + 16 * ls);
+        f.qb[g2] = ldnt4(item + 1024 + 16 * ls);
+        f.qh[g2] = ldnt4(item + 2048 + 16 * ls);
+        f.sc4[g2] = *reinterpret_cast<const uint32_t*>(item + 3072 + 4 * ls);
+    }
+    f.d = *reinterpret_cast<const uint16_t*>(item + 3328 + 2 * j);
+}
+
+// One (32-row tile, super-block) against the staged activations `cur`:
+// returns the tile's contribution before the token scale, per C element.
+__device__ __forceinline__ void tile_q4(const WFrag<1>& f, const uint8_t* cur, int lane, int u, float (&part)[16]) {
+    v16f P = {}, Q = {};
+    const float dd = h2f((uint16_t)(f.h.x & 0xFFFF)), dm = h2f((uint16_t)(f.h.x >> 16));
+    // 6-bit scales and mins of the 8 sub-blocks (src/m5_kern_scalar.c:39-46)
+    int sc[8], mn[8];
+#pragma unroll
+    for (int s8 = 0; s8 < 8; s8++) {
+        if (s8 < 4) {
+            sc[s8] = (f.h.y >> (8 * s8)) & 63;
+            mn[s8] = (f.h.z >> (8 * s8)) & 63;
+        } else {
+            const int s0 = s8 - 4;
+            sc[s8] = ((f.h.w >> (8 * s0)) & 15) | (((f.h.y >> (8 * s0 + 6)) & 3) << 4);
+            mn[s8] = ((f.h.w >> (8 * s0 + 4)) & 15) | (((f.h.z >> (8 * s0 + 6)) & 3) << 4);
+        }
+    }
+#pragma unroll
+    for (int s = 0; s < 16; s++) {
+        const int v = s >> 2, nib = (s >> 1) & 1, bh = s & 1;
+        const int sbk = 4 * (s >> 3) + ((s >> 1) & 3);  // sub-block of this K-step
+        const uint4 q = f.qv[v];
+        uint32_t w0 = bh ? q.z : q.x, w1 = bh ? q.w : q.y;
+        if (nib) {
+            w0 = ((w0 >> 4) & 0x0F0F0F0Fu) ^ 0x08080808u;  // stored XOR 0x80: high nibble u ^ 8
+            w1 = ((w1 >> 4) & 0x0F0F0F0Fu) ^ 0x08080808u;
+        } else {
+            w0 &= 0x0F0F0F0Fu;
+            w1 &= 0x0F0F0F0Fu;
+        }
+        const _Float16 c = (_Float16)sc[sbk], o = (_Float16)(-1024.f * (float)sc[sbk]);
+        uint32_t p0, p1, p2, p3;
+        nib2h(w0, (v2h){c, c}, (v2h){o, o}, p0, p1);
+        nib2h(w1, (v2h){c, c}, (v2h){o, o}, p2, p3);
+        const v8h B = pack8(p0, p1, p2, p3);
+        P = __builtin_amdgcn_mfma_f32_32x32x16_f16(lds8(cur + ((size_t)(2 * s) * 64 + lane) * 16), B, P, 0, 0, 0);
+        P = __builtin_amdgcn_mfma_f32_32x32x16_f16(lds8(cur + ((size_t)(2 * s + 1) * 64 + lane) * 16), B, P, 0, 0, 0);
+    }
+    // min term: B lane (n, 0) = m_0..m_7 of row n, lanes (n, 1) zero
+    v8h Bm;
+#pragma unroll
+    for (int i = 0; i < 8; i++) Bm[i] = u ? (_Float16)0.f : (_Float16)mn[i];
+    Q = __builtin_amdgcn_mfma_f32_32x32x16_f16(lds8(cur + XH_A + (size_t)lane * 16), Bm, Q, 0, 0, 0);
+    Q = __builtin_amdgcn_mfma_f32_32x32x16_f16(lds8(cur + XH_A + 1024 + (size_t)lane * 16), Bm, Q, 0, 0, 0);
+    const float dm32 = -32.f * dm;
+#pragma unroll
+    for (int i = 0; i < 16; i++) part[i] = fmaf(dd, P[i], dm32 * Q[i]);
+}
+
+__device__ __forceinline__ void tile_q6(const WFrag<2>& f, const uint8_t* cur, int lane, float (&part)[16]) {
+    v16f P = {}, Q = {};
+    const float dd = h2f((uint16_t)f.d);
+#pragma unroll
+    for (int s = 0; s < 16; s++) {
+        const int g2 = s >> 3, r6 = (s >> 1) & 3, bh = s & 1;
+        const uint4 A4 = f.qa[g2], B4 = f.qb[g2], H4 = f.qh[g2];
+        uint32_t wq[2];
+#pragma unroll
+        for (int k = 0; k < 2; k++) {
+            const int qd = 2 * bh + k;  // dword of the 16-byte vectors
+            const uint32_t av = qd == 0 ? A4.x : (qd == 1 ? A4.y : (qd == 2 ? A4.z : A4.w));
+            const uint32_t bv = qd == 0 ? B4.x : (qd == 1 ? B4.y : (qd == 2 ? B4.z : B4.w));
+            const uint32_t hv = qd == 0 ? H4.x : (qd == 1 ? H4.y : (qd == 2 ? H4.z : H4.w));
+            // the GGUF 6-bit map of src/m5_kern_scalar.c:115-142 (as the GEMV's dot_q6)
+            if (r6 == 0) wq[k] = (av & 0x0F0F0F0Fu) | ((hv << 4) & 0x30303030u);
+            else if (r6 == 1) wq[k] = (bv & 0x0F0F0F0Fu) | ((hv << 2) & 0x30303030u);
+            else if (r6 == 2) wq[k] = ((av >> 4) & 0x0F0F0F0Fu) | (hv & 0x30303030u);
+            else wq[k] = ((bv >> 4) & 0x0F0F0F0Fu) | ((hv >> 2) & 0x30303030u);
+        }
+        const int scv = (int)(int8_t)(f.sc4[g2] >> (8 * r6));
+        const int shv = scv >> 3, slv = scv & 7;  // sc = 8*sh + sl
+        const _Float16 ch = (_Float16)shv, cl = (_Float16)slv;
+        const _Float16 oh = (_Float16)(-1056.f * (float)shv), ol = (_Float16)(-1056.f * (float)slv);
+        uint32_t p0, p1, p2, p3;
+        nib2h(wq[0], (v2h){ch, ch}, (v2h){oh, oh}, p0, p1);
+        nib2h(wq[1], (v2h){ch, ch}, (v2h){oh, oh}, p2, p3);
+        const v8h Bh = pack8(p0, p1, p2, p3);
+        nib2h(wq[0], (v2h){cl, cl}, (v2h){ol, ol}, p0, p1);
+        nib2h(wq[1], (v2h){cl, cl}, (v2h){ol, ol}, p2, p3);
+        const v8h Bl = pack8(p0, p1, p2, p3);
+        const v8h Ahi = lds8(cur + ((size_t)(2 * s) * 64 + lane) * 16);
+        const v8h Alo = lds8(cur + ((size_t)(2 * s + 1) * 64 + lane) * 16);
+        P = __builtin_amdgcn_mfma_f32_32x32x16_f16(Ahi, Bh, P, 0, 0, 0);
+        P = __builtin_amdgcn_mfma_f32_32x32x16_f16(Alo, Bh, P, 0, 0, 0);
+        Q = __builtin_amdgcn_mfma_f32_32x32x16_f16(Ahi, Bl, Q, 0, 0, 0);
+        Q = __builtin_amdgcn_mfma_f32_32x32x16_f16(Alo, Bl, Q, 0, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < 16; i++) part[i] = dd * fmaf(8.f, P[i], Q[i]);
+}
+
+// FM 1 = Q4_K, 2 = Q6_K.  Grid (row blocks of 4*RW*32 rows, token tiles, K
+// splits).  The next super-block's weights are loaded into registers while
+// the current one is computed, as are its activations (then written to the
+// other LDS buffer).
 template <int FM, int RW>
 __global__ __launch_bounds__(256) void k_gemmh(const GemmHArgs a) {
     extern __shared__ __align__(16) uint8_t sm[];  // [2][XH_SB]
@@ -152,139 +278,51 @@ __global__ __launch_bounds__(256) void k_gemmh(const GemmHArgs a) {
     const int per = (nb + gridDim.z - 1) / gridDim.z;
     const int b0 = blockIdx.z * per, b1 = min(nb, b0 + per);
     const int rt0 = (4 * blockIdx.x + w) * RW;  // this wave's first 32-row tile
+    constexpr size_t IB = FM == 1 ? DRACO_Q4T_ITEM : DRACO_Q6T_ITEM;
     const uint8_t* xsrc = a.xh + (size_t)tt * nb * XH_SB;
     float y[RW][16];
+    const uint8_t* wrow[RW];  // item 0 of each row tile (tile index clamped in bounds)
 #pragma unroll
-    for (int r = 0; r < RW; r++)
+    for (int r = 0; r < RW; r++) {
 #pragma unroll
         for (int i = 0; i < 16; i++) y[r][i] = 0.f;
-
-    uint4 stg[9];
-    if (b0 < b1) {
-        stage_load(xsrc + (size_t)b0 * XH_SB, stg, tid);
-        stage_store(sm, stg, tid);
+        const int tile = min(2 * (rt0 + r) + (n >> 4), a.L.ntiles - 1);
+        wrow[r] = a.W + (size_t)tile * nb * IB;
     }
+    if (b0 >= b1) return;  // uniform per block (empty K split)
+
+    WFrag<FM> wc[RW], wn[RW];
+#pragma unroll
+    for (int r = 0; r < RW; r++) wload(wrow[r] + (size_t)b0 * IB, j, u, wc[r]);
+    uint4 stg[9];
+    stage_load(xsrc + (size_t)b0 * XH_SB, stg, tid);
+    stage_store(sm, stg, tid);
     __syncthreads();
     for (int b = b0; b < b1; b++) {
         const uint8_t* cur = sm + (size_t)((b - b0) & 1) * XH_SB;
         uint8_t* nxt = sm + (size_t)((b - b0 + 1) & 1) * XH_SB;
-        if (b + 1 < b1) stage_load(xsrc + (size_t)(b + 1) * XH_SB, stg, tid);
+        const int bn = b + 1 < b1 ? b + 1 : b;  // the last step reloads its own (cached) data
+        stage_load(xsrc + (size_t)bn * XH_SB, stg, tid);
+#pragma unroll
+        for (int r = 0; r < RW; r++) wload(wrow[r] + (size_t)bn * IB, j, u, wn[r]);
         float4 ts4[4];  // token scales of this lane's C rows 8q + 4u .. +3
 #pragma unroll
         for (int q = 0; q < 4; q++) ts4[q] = *reinterpret_cast<const float4*>(cur + XH_A + XH_M + 4 * (8 * q + 4 * u));
 #pragma unroll
         for (int r = 0; r < RW; r++) {
-            const int rt = rt0 + r;
-            if (32 * rt >= a.L.n_out) break;  // uniform per wave; no barrier inside
-            const int tile = min(2 * rt + (n >> 4), a.L.ntiles - 1);
-            v16f P = {}, Q = {};
-            float dd, dm = 0.f;
-            if (FM == 1) {
-                const uint8_t* item = a.W + ((size_t)tile * nb + b) * DRACO_Q4T_ITEM;
-                uint4 qv[4];
-#pragma unroll
-                for (int v = 0; v < 4; v++) qv[v] = ldnt4(item + (v >> 1) * 1024 + 16 * (j + 16 * (2 * (v & 1) + u)));
-                const uint4 h = ldnt4(item + 2048 + 16 * j);
-                dd = h2f((uint16_t)(h.x & 0xFFFF));
-                dm = h2f((uint16_t)(h.x >> 16));
-                // 6-bit scales and mins of the 8 sub-blocks (src/m5_kern_scalar.c:39-46)
-                int sc[8], mn[8];
-#pragma unroll
-                for (int s8 = 0; s8 < 8; s8++) {
-                    if (s8 < 4) {
-                        sc[s8] = (h.y >> (8 * s8)) & 63;
-                        mn[s8] = (h.z >> (8 * s8)) & 63;
-                    } else {
-                        const int s0 = s8 - 4;
-                        sc[s8] = ((h.w >> (8 * s0)) & 15) | (((h.y >> (8 * s0 + 6)) & 3) << 4);
-                        mn[s8] = ((h.w >> (8 * s0 + 4)) & 15) | (((h.z >> (8 * s0 + 6)) & 3) << 4);
-                    }
-                }
-#pragma unroll
-                for (int s = 0; s < 16; s++) {
-                    const int v = s >> 2, nib = (s >> 1) & 1, bh = s & 1;
-                    const int sbk = 4 * (s >> 3) + ((s >> 1) & 3);  // sub-block of this K-step
-                    const uint4 q = qv[v];
-                    uint32_t w0 = bh ? q.z : q.x, w1 = bh ? q.w : q.y;
-                    if (nib) {
-                        w0 = ((w0 >> 4) & 0x0F0F0F0Fu) ^ 0x08080808u;  // stored XOR 0x80: high nibble u ^ 8
-                        w1 = ((w1 >> 4) & 0x0F0F0F0Fu) ^ 0x08080808u;
-                    } else {
-                        w0 &= 0x0F0F0F0Fu;
-                        w1 &= 0x0F0F0F0Fu;
-                    }
-                    const _Float16 c = (_Float16)sc[sbk];
-                    const v2h c2 = {c, c}, o2 = {(_Float16)(-1024.f * (float)sc[sbk]), (_Float16)(-1024.f * (float)sc[sbk])};
-                    uint32_t p0, p1, p2, p3;
-                    nib2h(w0, c2, o2, p0, p1);
-                    nib2h(w1, c2, o2, p2, p3);
-                    const v8h B = pack8(p0, p1, p2, p3);
-                    P = __builtin_amdgcn_mfma_f32_32x32x16_f16(lds8(cur + ((size_t)(2 * s) * 64 + lane) * 16), B, P, 0, 0, 0);
-                    P = __builtin_amdgcn_mfma_f32_32x32x16_f16(lds8(cur + ((size_t)(2 * s + 1) * 64 + lane) * 16), B, P, 0, 0, 0);
-                }
-                // min term: B lane (n, 0) = m_0..m_7 of row n, lanes (n, 1) zero
-                v8h Bm;
-#pragma unroll
-                for (int i = 0; i < 8; i++) Bm[i] = u ? (_Float16)0.f : (_Float16)mn[i];
-                Q = __builtin_amdgcn_mfma_f32_32x32x16_f16(lds8(cur + XH_A + (size_t)lane * 16), Bm, Q, 0, 0, 0);
-                Q = __builtin_amdgcn_mfma_f32_32x32x16_f16(lds8(cur + XH_A + 1024 + (size_t)lane * 16), Bm, Q, 0, 0, 0);
-            } else {
-                const uint8_t* item = a.W + ((size_t)tile * nb + b) * DRACO_Q6T_ITEM;
-                dd = h2f(*reinterpret_cast<const uint16_t*>(item + 3328 + 2 * j));
-                uint4 qa[2], qb[2], qh[2];
-                uint32_t sc4[2];
-#pragma unroll
-                for (int g2 = 0; g2 < 2; g2++) {
-                    const int ls = j + 16 * (2 * g2 + u);
-                    qa[g2] = ldnt4(item + 16 * ls);
-                    qb[g2] = ldnt4(item + 1024 + 16 * ls);
-                    qh[g2] = ldnt4(item + 2048 + 16 * ls);
-                    sc4[g2] = *reinterpret_cast<const uint32_t*>(item + 3072 + 4 * ls);
-                }
-#pragma unroll
-                for (int s = 0; s < 16; s++) {
-                    const int g2 = s >> 3, r6 = (s >> 1) & 3, bh = s & 1;
-                    const uint4 A4 = qa[g2], B4 = qb[g2], H4 = qh[g2];
-                    uint32_t wq[2];
-#pragma unroll
-                    for (int k = 0; k < 2; k++) {
-                        const int qd = 2 * bh + k;  // dword of the 16-byte vectors
-                        const uint32_t av = qd == 0 ? A4.x : (qd == 1 ? A4.y : (qd == 2 ? A4.z : A4.w));
-                        const uint32_t bv = qd == 0 ? B4.x : (qd == 1 ? B4.y : (qd == 2 ? B4.z : B4.w));
-                        const uint32_t hv = qd == 0 ? H4.x : (qd == 1 ? H4.y : (qd == 2 ? H4.z : H4.w));
-                        // the GGUF 6-bit map of src/m5_kern_scalar.c:115-142 (as the GEMV's dot_q6)
-                        if (r6 == 0) wq[k] = (av & 0x0F0F0F0Fu) | ((hv << 4) & 0x30303030u);
-                        else if (r6 == 1) wq[k] = (bv & 0x0F0F0F0Fu) | ((hv << 2) & 0x30303030u);
-                        else if (r6 == 2) wq[k] = ((av >> 4) & 0x0F0F0F0Fu) | (hv & 0x30303030u);
-                        else wq[k] = ((bv >> 4) & 0x0F0F0F0Fu) | ((hv >> 2) & 0x30303030u);
-                    }
-                    const int scv = (int)(int8_t)(sc4[g2] >> (8 * r6));
-                    const int shv = scv >> 3, slv = scv & 7;  // sc = 8*sh + sl
-                    const _Float16 ch = (_Float16)shv, cl = (_Float16)slv;
-                    const _Float16 oh = (_Float16)(-1056.f * (float)shv), ol = (_Float16)(-1056.f * (float)slv);
-                    uint32_t p0, p1, p2, p3;
-                    nib2h(wq[0], (v2h){ch, ch}, (v2h){oh, oh}, p0, p1);
-                    nib2h(wq[1], (v2h){ch, ch}, (v2h){oh, oh}, p2, p3);
-                    const v8h Bh = pack8(p0, p1, p2, p3);
-                    nib2h(wq[0], (v2h){cl, cl}, (v2h){ol, ol}, p0, p1);
-                    nib2h(wq[1], (v2h){cl, cl}, (v2h){ol, ol}, p2, p3);
-                    const v8h Bl = pack8(p0, p1, p2, p3);
-                    const v8h Ahi = lds8(cur + ((size_t)(2 * s) * 64 + lane) * 16);
-                    const v8h Alo = lds8(cur + ((size_t)(2 * s + 1) * 64 + lane) * 16);
-                    P = __builtin_amdgcn_mfma_f32_32x32x16_f16(Ahi, Bh, P, 0, 0, 0);
-                    P = __builtin_amdgcn_mfma_f32_32x32x16_f16(Alo, Bh, P, 0, 0, 0);
-                    Q = __builtin_amdgcn_mfma_f32_32x32x16_f16(Ahi, Bl, Q, 0, 0, 0);
-                    Q = __builtin_amdgcn_mfma_f32_32x32x16_f16(Alo, Bl, Q, 0, 0, 0);
-                }
-            }
+            if (32 * (rt0 + r) >= a.L.n_out) break;  // uniform per wave; no barrier inside
+            float part[16];
+            if constexpr (FM == 1) tile_q4(wc[r], cur, lane, u, part);
+            else tile_q6(wc[r], cur, lane, part);
 #pragma unroll
             for (int i = 0; i < 16; i++) {
                 const float4 t4 = ts4[i >> 2];
                 const float tsc = (i & 3) == 0 ? t4.x : ((i & 3) == 1 ? t4.y : ((i & 3) == 2 ? t4.z : t4.w));
-                const float part = FM == 1 ? fmaf(dd, P[i], -32.f * dm * Q[i]) : dd * fmaf(8.f, P[i], Q[i]);
-                y[r][i] = fmaf(tsc, part, y[r][i]);
+                y[r][i] = fmaf(tsc, part[i], y[r][i]);
             }
         }
+#pragma unroll
+        for (int r = 0; r < RW; r++) wc[r] = wn[r];
         if (b + 1 < b1) stage_store(nxt, stg, tid);
         __syncthreads();
     }
