@@ -14,6 +14,7 @@ The GPU path and the CPU oracle consume the same bytes, so the encoder only
 needs to be a valid GGUF encoder.
 """
 import hashlib
+import os
 from dataclasses import dataclass, field
 
 import numpy as np
@@ -140,4 +141,71 @@ def build_llama(cfg, seed=0):
     if not cfg.tied:
         m.tensors["output.weight"] = (_tensor(rng, c["out"], cfg.vocab, H, ws), c["out"], cfg.vocab, H)
     m.norms["output_norm.weight"] = np.ones(H, np.float32)
+    return m
+
+
+# ------------------------------------------------------------ GGUF files --
+# Metadata keys are the llama family's, as the reference driver reads them
+# (src/smol_engine.py:26-40: llama.block_count, .embedding_length,
+# .attention.head_count(_kv), .attention.layer_norm_rms_epsilon,
+# .rope.dimension_count, .rope.freq_base, .feed_forward_length, .vocab_size).
+
+def save_llama_gguf(model, path):
+    """Write a LlamaModel as a GGUF v3 file (tensor data as stored, norms as F32)."""
+    from . import gguf
+    cfg = model.cfg
+    fields = {
+        "general.architecture": "llama", "general.name": cfg.name,
+        "llama.block_count": cfg.n_layer, "llama.embedding_length": cfg.hidden,
+        "llama.attention.head_count": cfg.n_head, "llama.attention.head_count_kv": cfg.n_kv,
+        "llama.attention.layer_norm_rms_epsilon": float(cfg.eps), "llama.rope.dimension_count": cfg.rot,
+        "llama.rope.freq_base": float(cfg.rope_base), "llama.feed_forward_length": cfg.n_ff,
+        "llama.vocab_size": cfg.vocab, "llama.context_length": cfg.max_t,
+        "dracomancer.seed": int(model.seed), "dracomancer.n_prompt": cfg.n_prompt, "dracomancer.n_gen": cfg.n_gen,
+    }
+    tensors = []
+    for name, (buf, code, n_out, n_in) in model.tensors.items():
+        tensors.append((name, gguf.GGML_OF_M5[code], (n_in, n_out), buf))
+    for name, w in model.norms.items():
+        tensors.append((name, "F32", (w.size,), np.ascontiguousarray(w, np.float32)))
+    gguf.write_gguf(path, fields, tensors)
+
+
+def load_llama_gguf(path, max_t=None):
+    """A LlamaModel whose tensors are zero-copy views of the mapped file
+    (the engine registers them by those addresses)."""
+    from . import gguf
+    r = gguf.FastGGUF(path)
+
+    def kv(key, default=None):
+        f = r.fields.get("llama." + key)
+        return default if f is None else f.contents()
+
+    T = {t.name: t for t in r.tensors}
+    kind = {"attn_q": "q", "attn_k": "k", "attn_v": "v", "attn_output": "o", "ffn_gate": "gate",
+            "ffn_up": "up", "ffn_down": "down"}
+    codes = {"emb": gguf.M5_CODE[T["token_embd.weight"].tensor_type.name]}
+    for tname, k in kind.items():
+        codes[k] = gguf.M5_CODE[T["blk.0." + tname + ".weight"].tensor_type.name]
+    tied = "output.weight" not in T
+    codes["out"] = codes["emb"] if tied else gguf.M5_CODE[T["output.weight"].tensor_type.name]
+    seed_f = r.fields.get("dracomancer.seed")
+    np_f, ng_f = r.fields.get("dracomancer.n_prompt"), r.fields.get("dracomancer.n_gen")
+    gen = r.fields.get("general.name")
+    H, NH = int(kv("embedding_length")), int(kv("attention.head_count"))
+    cfg = LlamaConfig(
+        name=gen.contents() if gen else os.path.basename(path), hidden=H, n_layer=int(kv("block_count")),
+        n_head=NH, n_kv=int(kv("attention.head_count_kv")), head_dim=H // NH, n_ff=int(kv("feed_forward_length")),
+        vocab=int(kv("vocab_size", T["token_embd.weight"].shape[1])),
+        eps=float(kv("attention.layer_norm_rms_epsilon")), rope_base=float(kv("rope.freq_base")), codes=codes,
+        tied=tied, n_prompt=int(np_f.contents()) if np_f else 32, n_gen=int(ng_f.contents()) if ng_f else 64,
+        max_t=int(max_t or kv("context_length", 1024)))
+    if int(kv("rope.dimension_count", cfg.head_dim)) != cfg.head_dim:
+        raise ValueError("partial rope (rope.dimension_count != head_dim) is not served by this driver")
+    m = LlamaModel(cfg=cfg, seed=int(seed_f.contents()) if seed_f else 0)
+    for name, t in T.items():
+        if t.tensor_type.name == "F32" and len(t.shape) == 1:
+            m.norms[name] = t.data
+        else:
+            m.tensors[name] = (t.data.reshape(-1), gguf.M5_CODE[t.tensor_type.name], int(t.shape[1]), int(t.shape[0]))
     return m

@@ -191,3 +191,23 @@ def test_llama1b_device_generate():
     print(f"[decode] llama1b decode {cfg.n_gen / (st[0] / 1e3):.1f} tok/s prefill {st[1]:.0f} ms", flush=True)
     assert toks == list(g["tokens"])
     assert np.max(np.abs(hidden - g["hidden"])) <= HID_TOL
+
+
+@pytest.mark.parametrize("cfgname,fname", TINY)
+def test_device_generate_from_gguf_file(tmp_path, cfgname, fname):
+    """The on-disk path: the model written as a GGUF file, mapped back
+    (dracohip/gguf.py, the reference's FastGGUF interface), its tensors
+    registered by their addresses in the mapping, then decoded: the golden
+    tokens of the same model built in memory."""
+    g = golden(fname)
+    cfg = models.CONFIGS[cfgname]
+    path = tmp_path / f"{cfgname}.gguf"
+    models.save_llama_gguf(models.build_llama(cfg, 0), path)
+    model = models.load_llama_gguf(path)
+    from dracohip import lib
+    lib.load().draco_reset()
+    drv = LlamaDriver(model, hip_engine_lib())
+    print(f"[decode] from gguf {cfgname}", flush=True)
+    toks, hidden, _ = drv.generate_device(model.prompt(), cfg.n_gen, use_graph=True)
+    assert toks == list(g["tokens"])
+    assert np.max(np.abs(hidden - g["hidden"])) <= hid_tol(g["hidden"])
