@@ -2,8 +2,9 @@
 //
 // m5_gemm_auto: src/m5/m5_gemm_fused.c:231-241 (0 = done, -1 = code not served,
 // the caller falls back); m5_gemm: src/m5/m5_gemm.c:249-272 (Y[T x n_out] =
-// X[T x n_in] . W^T).  Host pointers.  Q4_K / Q6_K run on the int8-MFMA GEMM
-// (gemm.hip); Q8_0 runs as one device GEMV per token.
+// X[T x n_in] . W^T).  Host pointers.  Q4_K / Q6_K run on the f16-MFMA GEMM
+// (gemmh.hip; the int8-MFMA GEMM of gemm.hip when built with DRACO_GEMM_INT8);
+// Q8_0 runs as one device GEMV per token.
 #include <string.h>
 
 #include <vector>

@@ -526,14 +526,14 @@ int ensure_pf(DevModel* m, int cap) {
 // enqueue_layer (src/m6_engine.c:61-83 with llama_attn_core and
 // m6_dense_op), token rows batched.  Token t sits at rope position pos0 + t
 // and cache row row0 + t.
-int enqueue_prefill_layer(DevModel* m, int l, int T, int pos0, int row0, float eps, hipStream_t st) {
+int enqueue_prefill_layer(DevModel* m, int l, int T, int pos0, int row0, float eps, hipStream_t st, bool xn_ready) {
     PfBufs& b = m->pf;
     DevAttn* a = m->attn[l];
     DevFfn* f = m->ffn[l];
     const int H = m->h;
     const float* tab = rope_dev(a->rot, a->base, pos0 + T);
     if (!tab) return -2;
-    if (pf_rms(b.X, m->anorm[l], b.Xn, T, H, eps, st)) return fail(-1, "prefill: rms rejected");
+    if (!xn_ready && pf_rms(b.X, m->anorm[l], b.Xn, T, H, eps, st)) return fail(-1, "prefill: rms rejected");
     // the digits of Xn are written by the first K-quant product and reused by the others
     auto kquant = [](const DracoMat* x) { return x->L.code == DRACO_Q4_K || x->L.code == DRACO_Q6_K; };
     if (draco_enqueue_gemm(*a->wq, b.Xn, T, b.Q, b.dig, false, st)) return -1;
@@ -544,13 +544,17 @@ int enqueue_prefill_layer(DevModel* m, int l, int T, int pos0, int row0, float e
     if (pf_attention(b.Q, a->kc, a->vc, b.part, b.O, row0, T, a->NH, a->NKV, a->HD, a->scale, st))
         return fail(-1, "prefill: attention shape NH=%d NKV=%d HD=%d not served", a->NH, a->NKV, a->HD);
     if (draco_enqueue_gemm(*a->wo, b.O, T, b.Y, b.dig, false, st)) return -1;
-    pf_add(b.X, b.Y, (size_t)T * H, st);
-    if (pf_rms(b.X, m->fnorm[l], b.Xn, T, H, eps, st)) return fail(-1, "prefill: rms rejected");
+    if (pf_add_rms(b.X, b.Y, m->fnorm[l], b.Xn, T, H, eps, st)) return fail(-1, "prefill: rms rejected");
     if (draco_enqueue_gemm(*f->g, b.Xn, T, b.G, b.dig, false, st)) return -1;
     if (draco_enqueue_gemm(*f->u, b.Xn, T, b.U, b.dig, kquant(f->g), st)) return -1;
     dk_swiglu(b.G, b.U, T * f->FF, st);
     if (draco_enqueue_gemm(*f->d, b.G, T, b.Y, b.dig, false, st)) return -1;
-    pf_add(b.X, b.Y, (size_t)T * H, st);
+    // the residual; fused with the next layer's input RMSNorm when there is one
+    if (l + 1 < m->n_layer) {
+        if (pf_add_rms(b.X, b.Y, m->anorm[l + 1], b.Xn, T, H, eps, st)) return fail(-1, "prefill: rms rejected");
+    } else {
+        pf_add(b.X, b.Y, (size_t)T * H, st);
+    }
     return 0;
 }
 
@@ -567,7 +571,7 @@ int enqueue_prefill(DevModel* m, const DracoMat* em, const int* ids, int n, int 
         const int T = std::min(C, n - c0);
         if (pf_embed(em->dev, em->L, ids + c0, T, m->pf.X, st)) return 0;
         for (int l = 0; l < m->n_layer; l++)
-            if (enqueue_prefill_layer(m, l, T, pos0 + c0, *m->attn[l]->snap.tlen + c0, eps, st)) return 0;
+            if (enqueue_prefill_layer(m, l, T, pos0 + c0, *m->attn[l]->snap.tlen + c0, eps, st, l > 0)) return 0;
         last = T;
     }
     return last;

@@ -15,6 +15,8 @@ size_t pf_part_floats(int NH, int T, int HD, int nspl);
 int pf_embed(const uint8_t* base, const DracoLayout& L, const int* ids, int T, float* X, hipStream_t st);
 // Xn[t] = (X[t] * inv_rms) * w, h <= 4096
 int pf_rms(const float* X, const float* w, float* Xn, int T, int h, float eps, hipStream_t st);
+// X[t] += Y[t], then Xn[t] = (X[t] * inv_rms) * w (h <= 4096)
+int pf_add_rms(float* X, const float* Y, const float* w, float* Xn, int T, int h, float eps, hipStream_t st);
 // rope of Q[t] / K[t] at position pos0 + t; K, V rows into cache row row0 + t
 int pf_rope_append(float* Q, const float* K, const float* V, float* kc, float* vc, const float* tab, int pos0,
                    int row0, int T, int NH, int NKV, int HD, int rot, hipStream_t st);

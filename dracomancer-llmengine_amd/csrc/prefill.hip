@@ -1,9 +1,10 @@
 // prefill.hip -- chunked prefill of the llama family (gfx950): the T tokens
 // of a chunk go through each layer together, with the weight products on the
-// int8-MFMA GEMM (gemm.hip) and these row-parallel kernels around them:
+// f16-MFMA GEMM (gemmh.hip) and these row-parallel kernels around them:
 //
 //   k_pf_embed          X[t] = embedding row ids[t]
 //   k_pf_rms            Xn[t] = RMSNorm(X[t]) * w            (src/m6_engine.c:31-37)
+//   k_pf_add_rms        X[t] += Y[t], then the RMSNorm of the sum
 //   k_pf_rope_append    rope on Q[t] and K[t] at position pos0 + t, K/V rows
 //                       appended at cache row row0 + t       (src/m6_engine.c:456-481)
 //   k_pf_attn, k_pf_merge
@@ -42,6 +43,39 @@ __global__ __launch_bounds__(256) void k_pf_rms(const float* __restrict__ X, con
     for (int k = 0; k < PF_RMS_PT; k++) {
         const int i = threadIdx.x + 256 * k;
         v[k] = i < h ? x[i] : 0.f;
+        s = fmaf(v[k], v[k], s);
+    }
+    s = wave_sum(s);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
+    __syncthreads();
+    const float tot = (red[0] + red[1]) + (red[2] + red[3]);
+    const float inv = 1.f / sqrtf(tot / (float)h + eps);
+#pragma unroll
+    for (int k = 0; k < PF_RMS_PT; k++) {
+        const int i = threadIdx.x + 256 * k;
+        if (i < h) o[i] = w ? v[k] * inv * w[i] : v[k] * inv;
+    }
+}
+
+// X[t] += Y[t] (the residual), then Xn[t] = (X[t] * inv_rms) * w: one block
+// per token row, the sum held in registers between the two steps
+__global__ __launch_bounds__(256) void k_pf_add_rms(float* __restrict__ X, const float* __restrict__ Y,
+                                                    const float* __restrict__ w, float* __restrict__ Xn, int h,
+                                                    float eps) {
+    __shared__ float red[4];
+    float* x = X + (size_t)blockIdx.x * h;
+    const float* y = Y + (size_t)blockIdx.x * h;
+    float* o = Xn + (size_t)blockIdx.x * h;
+    float v[PF_RMS_PT];
+    float s = 0.f;
+#pragma unroll
+    for (int k = 0; k < PF_RMS_PT; k++) {
+        const int i = threadIdx.x + 256 * k;
+        v[k] = 0.f;
+        if (i < h) {
+            v[k] = x[i] + y[i];
+            x[i] = v[k];
+        }
         s = fmaf(v[k], v[k], s);
     }
     s = wave_sum(s);
@@ -234,6 +268,12 @@ int pf_embed(const uint8_t* base, const DracoLayout& L, const int* ids, int T, f
 int pf_rms(const float* X, const float* w, float* Xn, int T, int h, float eps, hipStream_t st) {
     if (T < 1 || h > 256 * PF_RMS_PT) return -1;
     hipLaunchKernelGGL(k_pf_rms, dim3(T), dim3(256), 0, st, X, w, Xn, h, eps);
+    return 0;
+}
+
+int pf_add_rms(float* X, const float* Y, const float* w, float* Xn, int T, int h, float eps, hipStream_t st) {
+    if (T < 1 || h > 256 * PF_RMS_PT) return -1;
+    hipLaunchKernelGGL(k_pf_add_rms, dim3(T), dim3(256), 0, st, X, Y, w, Xn, h, eps);
     return 0;
 }
 
