@@ -130,6 +130,33 @@ def moe_ffn_configs3(lib, iters=100):
             "shape": "128 experts top-8, FFN 768, hidden 2048, Q4_K experts, fp32 router"}
 
 
+def shexp_qwen35moe(lib, iters=200, n_copies=160):
+    """qwen35moe shared expert (m6_granite_shexp) at hidden 2048, FFN 512: Q4_K
+    gate/up, Q6_K down, fp32 gate row.  One call = gate/up (+SwiGLU) + gate row
+    + down + sigmoid scale, graph-replayed with the weights rotated over
+    n_copies device copies (~2.05 MB each, 330 MB in all: past the MALL)."""
+    import ctypes as ct
+    shi, H = 512, 2048
+    rng = np.random.default_rng(5)
+    ws = [lib.quantize(5, rng.standard_normal((shi, H), dtype=np.float32) * np.float32(0.02)),
+          lib.quantize(5, rng.standard_normal((shi, H), dtype=np.float32) * np.float32(0.02)),
+          lib.quantize(4, rng.standard_normal((H, shi), dtype=np.float32) * np.float32(0.02)),
+          (rng.standard_normal(H, dtype=np.float32) * np.float32(0.02)).view(np.uint8)]
+    ptrs = np.array([w.ctypes.data for w in ws], np.uint64)
+    codes = np.array([5, 5, 4, 9], np.int32)
+    x = rng.standard_normal(H).astype(np.float32)
+    o = np.zeros(2, np.float32)
+    rc = lib.load().draco_bench_shexp(lib.pf(x), ct.c_void_p(ptrs.ctypes.data), lib.pi32(codes), shi, H, n_copies,
+                                      iters, lib.pf(o))
+    if rc != 0:
+        raise RuntimeError(lib.last_error())
+    lib.load().draco_reset()
+    us, nbytes = float(o[0]), float(o[1])
+    return {"us_per_call": round(us, 3), "bytes_per_call": int(nbytes), "GB_s": round(nbytes / us / 1e3, 1),
+            "frac_of_peak": round(nbytes / us / 1e3 / PEAK_HBM_GBS, 4), "launches": 4,
+            "shape": "shared expert FFN 512, hidden 2048, Q4_K gate/up, Q6_K down, fp32 gate row"}
+
+
 def gdn_scan_configs4(lib):
     """configs[4] GDN scan: 32 V heads / 16 q-k heads of 128, T = 4096 scanned in 64-token
     launches, then 64 single-token (decode) steps; us per token, state bytes per token."""
@@ -317,6 +344,8 @@ def main():
             log(f"Q4_K x Q8_K GEMV {k}: {v['us_per_launch']} us, {v['GB_s']} GB/s")
         moe = moe_ffn_configs3(lib)
         log(f"MoE FFN configs[3]: {moe['us_per_ffn']} us, {moe['GB_s']} GB/s")
+        shx = shexp_qwen35moe(lib)
+        log(f"qwen35moe shared expert: {shx['us_per_call']} us, {shx['GB_s']} GB/s")
         gdn = gdn_scan_configs4(lib)
         log(f"GDN scan configs[4]: {gdn['us_per_token_prefill_64chunks']} us/token (64-token launches), "
             f"{gdn['us_per_decode_step']} us/decode step")
@@ -378,7 +407,7 @@ def main():
         match = bool(list(g["tokens"][:n]) == toks_first[:n])
     log(f"decode {tok_s:.1f} tok/s; greedy tokens match reference: {match}")
 
-    roof = q8 = moe = gdn = pre = qw = None
+    roof = q8 = moe = shx = gdn = pre = qw = None
     if not args.no_roofline:
         roof = q4k_gemv_roofline(lib)
         log(f"Q4_K GEMV 14336x4096: {roof['us_per_launch']} us/launch, {roof['achieved']} GB/s")
@@ -387,6 +416,8 @@ def main():
             log(f"Q4_K x Q8_K GEMV {k}: {v['us_per_launch']} us, {v['GB_s']} GB/s")
         moe = moe_ffn_configs3(lib)
         log(f"MoE FFN configs[3]: {moe['us_per_ffn']} us, {moe['GB_s']} GB/s")
+        shx = shexp_qwen35moe(lib)
+        log(f"qwen35moe shared expert: {shx['us_per_call']} us, {shx['GB_s']} GB/s")
         gdn = gdn_scan_configs4(lib)
         log(f"GDN scan configs[4]: {gdn['us_per_token_prefill_64chunks']} us/token (64-token launches), "
             f"{gdn['us_per_decode_step']} us/decode step")
@@ -420,6 +451,7 @@ def main():
         "roofline": roof,
         "configs1_q8k_gemv": q8,
         "configs3_moe_ffn": moe,
+        "qwen35moe_shared_expert": shx,
         "configs4_gdn_scan": gdn,
         "configs4_layer_ops": qw,
         "configs2_prefill_gemm": pre,

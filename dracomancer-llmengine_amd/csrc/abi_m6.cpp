@@ -762,6 +762,127 @@ void m6_dense_op(const float* xn, void* pv, float* out) {
     if (e != hipSuccess) report(fail(-2, "m6_dense_op: %s", hipGetErrorString(e)), "m6_dense_op");
 }
 
+// qwen35moe shared expert, src/m6_engine.c:1111-1127: out = down(SwiGLU(gate
+// x, up x)) * sigmoid(gate_inp_shexp . x); shp/shc = {gate, up, down,
+// gate_inp} (gate/up shi x h, down h x shi, gate_inp 1 x h).  Like the
+// reference it returns nothing; on return out[h] holds the gated output,
+// shg[h] the ungated down product, sg[0] the gate logit and sh[0, shi) the
+// SwiGLU activation (sh[shi, 2 shi) is scratch and is not written).
+void m6_granite_shexp(const float* x, const uint64_t* shp, const int* shc, float* sg, float* sh, float* shg,
+                      float* out, int shi, int h) {
+    std::lock_guard<std::recursive_mutex> g(api_mutex());
+    if (int rc = ensure_init()) { report(rc, "m6_granite_shexp"); return; }
+    if (shi <= 0 || h <= 0) { report(fail(-1, "m6_granite_shexp: shape shi %d h %d", shi, h), "m6_granite_shexp"); return; }
+    // the gate/up/down triple resolves through the dense-op cache, keyed by a
+    // descriptor that is refreshed per call (re-resolved only when it changes)
+    static M6DenseP key;
+    key.g = (const uint8_t*)(uintptr_t)shp[0];
+    key.u = (const uint8_t*)(uintptr_t)shp[1];
+    key.d = (const uint8_t*)(uintptr_t)shp[2];
+    key.cg = shc[0];
+    key.cu = shc[1];
+    key.cd = shc[2];
+    key.n_ff = shi;
+    key.h = h;
+    DevFfn* f = get_ffn(&key);
+    const DracoMat* gi = get_mat((const void*)(uintptr_t)shp[3], shc[3], 1, h);
+    if (!f || !gi) { report(-1, "m6_granite_shexp"); return; }
+    static Work w;
+    if (ensure_work(w, h, h, 1, 1, 64, 64, shi)) { report(-2, "m6_granite_shexp"); return; }
+    hipStream_t st = stream();
+    hipMemcpyAsync(w.xn, x, sizeof(float) * h, hipMemcpyHostToDevice, st);
+    if (enqueue_gateup(f, w, w.xn, 0, nullptr, 0.f, st) || draco_gemv_launch(*gi, w.xn, w.k, nullptr, 0, 1, st) ||
+        draco_gemv_launch(*f->d, w.g, w.x, nullptr, 0, h, st)) {
+        report(-1, "m6_granite_shexp");
+        return;
+    }
+    dk_sigmoid_scale(w.x, w.k, w.q, h, st);
+    hipMemcpyAsync(out, w.q, sizeof(float) * h, hipMemcpyDeviceToHost, st);
+    hipMemcpyAsync(shg, w.x, sizeof(float) * h, hipMemcpyDeviceToHost, st);
+    hipMemcpyAsync(sg, w.k, sizeof(float), hipMemcpyDeviceToHost, st);
+    hipMemcpyAsync(sh, w.g, sizeof(float) * shi, hipMemcpyDeviceToHost, st);
+    hipError_t e = hipStreamSynchronize(st);
+    if (e != hipSuccess) report(fail(-2, "m6_granite_shexp: %s", hipGetErrorString(e)), "m6_granite_shexp");
+}
+
+// Graph-replayed timing of m6_granite_shexp's device work (gate/up + SwiGLU,
+// gate row, down, sigmoid scale) with x resident, the four weights rotated
+// over n_copies device copies so that the replay streams from HBM once
+// n_copies x the weight bytes exceeds the 256 MB MALL: out[0] = us per call,
+// out[1] = weight bytes per call.
+int draco_bench_shexp(const float* x, const uint64_t* shp, const int* shc, int shi, int h, int n_copies, int iters,
+                      float* out) {
+    std::lock_guard<std::recursive_mutex> g(api_mutex());
+    if (int rc = ensure_init()) return rc;
+    if (shi <= 0 || h <= 0 || n_copies < 1 || iters < 1) return fail(-1, "bench shexp: bad arguments");
+    static M6DenseP key;
+    key = M6DenseP{(const uint8_t*)(uintptr_t)shp[0], (const uint8_t*)(uintptr_t)shp[1],
+                   (const uint8_t*)(uintptr_t)shp[2], shc[0], shc[1], shc[2], shi, h};
+    DevFfn* f = get_ffn(&key);
+    const DracoMat* gi = get_mat((const void*)(uintptr_t)shp[3], shc[3], 1, h);
+    if (!f || !gi) return -1;
+    static Work w;
+    if (ensure_work(w, h, h, 1, 1, 64, 64, shi)) return -2;
+    hipStream_t st = stream();
+    const DracoMat* src[4] = {f->g, f->u, f->d, gi};
+    std::vector<DracoMat> cp(4 * (size_t)n_copies);
+    for (int c = 0; c < n_copies; c++)
+        for (int k = 0; k < 4; k++) {
+            DracoMat& m = cp[4 * (size_t)c + k];
+            m = *src[k];
+            DRACO_HIP(hipMalloc(&m.dev, m.L.bytes));
+            DRACO_HIP(hipMemcpyAsync(m.dev, src[k]->dev, m.L.bytes, hipMemcpyDeviceToDevice, st));
+        }
+    std::vector<DevFfn> fs(n_copies);
+    for (int c = 0; c < n_copies; c++) {
+        fs[c].g = &cp[4 * (size_t)c];
+        fs[c].u = &cp[4 * (size_t)c + 1];
+        fs[c].d = &cp[4 * (size_t)c + 2];
+        fs[c].FF = shi;
+        fs[c].H = h;
+    }
+    DRACO_HIP(hipMemcpyAsync(w.xn, x, sizeof(float) * h, hipMemcpyHostToDevice, st));
+    auto enq = [&](int c) {
+        if (enqueue_gateup(&fs[c], w, w.xn, 0, nullptr, 0.f, st) ||
+            draco_gemv_launch(cp[4 * (size_t)c + 3], w.xn, w.k, nullptr, 0, 1, st) ||
+            draco_gemv_launch(cp[4 * (size_t)c + 2], w.g, w.x, nullptr, 0, h, st))
+            return -1;
+        dk_sigmoid_scale(w.x, w.k, w.q, h, st);
+        return 0;
+    };
+    int rc = enq(0);
+    DRACO_HIP(hipStreamSynchronize(st));
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    if (!rc) {
+        DRACO_HIP(hipStreamBeginCapture(st, hipStreamCaptureModeRelaxed));
+        for (int i = 0; i < iters && !rc; i++) rc = enq(i % n_copies);
+        DRACO_HIP(hipStreamEndCapture(st, &graph));
+    }
+    if (!rc) {
+        DRACO_HIP(hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0));
+        DRACO_HIP(hipEventCreate(&e0));
+        DRACO_HIP(hipEventCreate(&e1));
+        DRACO_HIP(hipGraphLaunch(exec, st));
+        DRACO_HIP(hipEventRecord(e0, st));
+        DRACO_HIP(hipGraphLaunch(exec, st));
+        DRACO_HIP(hipEventRecord(e1, st));
+        DRACO_HIP(hipStreamSynchronize(st));
+        float ms = 0;
+        DRACO_HIP(hipEventElapsedTime(&ms, e0, e1));
+        out[0] = ms * 1000.f / iters;
+        const double gu = (double)(draco_row_bytes(shc[0], h) + draco_row_bytes(shc[1], h)) * shi;
+        out[1] = (float)(gu + (double)draco_row_bytes(shc[2], shi) * h + (double)draco_row_bytes(shc[3], h));
+        hipEventDestroy(e0);
+        hipEventDestroy(e1);
+        hipGraphExecDestroy(exec);
+    }
+    if (graph) hipGraphDestroy(graph);
+    for (auto& m : cp) hipFree(m.dev);
+    return rc ? fail(-1, "bench shexp: launch rejected") : 0;
+}
+
 // ---- state sync hooks (no reference counterpart; the reference's state is
 // the host arrays themselves, src/draco_engine_server.py:907-922) ----
 

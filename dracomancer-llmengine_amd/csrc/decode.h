@@ -45,6 +45,8 @@ int dk_attention(const float* q, const float* kc, const float* vc, float* part, 
 void dk_fa_prep(const float* QG, float* Qr, const float* kin, float* kout, const float* qn, const float* kn,
                 const float* cs, int NH, hipStream_t st);
 void dk_swiglu(float* g, const float* u, int n, hipStream_t st);
+// out[i] = y[i] * sigmoid(g[0]) (n floats; g is one device float)
+void dk_sigmoid_scale(const float* y, const float* g, float* out, int n, hipStream_t st);
 // out[n_in] = dequantized row ids[cursor ? *cursor : 0] of m
 void dk_embed(const DracoMat& m, const int* ids, const int* cursor, float* out, hipStream_t st);
 // out[slotp ? *slotp + 1 : slot] = first index of max(x[0..n))

@@ -451,6 +451,14 @@ __global__ __launch_bounds__(256) void k_swiglu(float* __restrict__ g, const flo
     }
 }
 
+// out[i] = y[i] * sigmoid(g[0]): the shared expert's scalar gate
+// (src/m6_engine.c:1125-1126)
+__global__ __launch_bounds__(256) void k_sigmoid_scale(const float* __restrict__ y, const float* __restrict__ g,
+                                                       float* __restrict__ out, int n) {
+    const float s = 1.0f / (1.0f + expf(-g[0]));
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) out[i] = y[i] * s;
+}
+
 // ---------------------------------------------------------- embedding --
 // Dequantize row `tok` of a private-layout matrix into out[n_in]
 // (embed_value, embed_dev.h).
@@ -578,6 +586,11 @@ void dk_fa_prep(const float* QG, float* Qr, const float* kin, float* kout, const
 void dk_swiglu(float* g, const float* u, int n, hipStream_t st) {
     const int blocks = (n + 255) / 256 < 1024 ? (n + 255) / 256 : 1024;
     hipLaunchKernelGGL(k_swiglu, dim3(blocks), dim3(256), 0, st, g, u, n);
+}
+
+void dk_sigmoid_scale(const float* y, const float* g, float* out, int n, hipStream_t st) {
+    const int blocks = (n + 255) / 256 < 1024 ? (n + 255) / 256 : 1024;
+    hipLaunchKernelGGL(k_sigmoid_scale, dim3(blocks), dim3(256), 0, st, y, g, out, n);
 }
 
 void dk_embed(const DracoMat& m, const int* ids, const int* cursor, float* out, hipStream_t st) {

@@ -50,6 +50,8 @@ SIGNATURES = {
     "m6_head_op": (ct.c_int, [f32p, f32p, ct.c_int, ct.c_float, ct.c_void_p, ct.c_int, ct.c_int, f32p, f32p]),
     "m6_llama_attn_op": (None, [f32p, ct.c_void_p, ct.c_int, f32p]),
     "m6_dense_op": (None, [f32p, ct.c_void_p, f32p]),
+    "m6_granite_shexp": (None, [f32p, ct.c_void_p, i32p, f32p, f32p, f32p, f32p, ct.c_int, ct.c_int]),
+    "draco_bench_shexp": (ct.c_int, [f32p, ct.c_void_p, i32p, ct.c_int, ct.c_int, ct.c_int, ct.c_int, f32p]),
     "draco_state_pull": (ct.c_int, [ct.c_void_p, ct.c_int]),
     "draco_state_push": (ct.c_int, [ct.c_void_p, ct.c_int]),
     "draco_llama_generate": (ct.c_int, [ct.c_void_p, ct.c_int, ct.c_int, ct.c_float, f32p, ct.c_void_p,

@@ -92,6 +92,17 @@ int m6_head_op(const float* x, const float* final_norm, int h, float eps, const 
 void m6_llama_attn_op(const float* xn, void* p, int pos, float* out);
 /* src/m6_engine.c:275-303 */
 void m6_dense_op(const float* xn, void* p, float* out);
+/* src/m6_engine.c:1111-1127 (qwen35moe shared expert).  shp/shc = {gate,
+ * up, down, gate_inp}: out[h] = down(SwiGLU(gate.x, up.x)) *
+ * sigmoid(gate_inp.x).  Also leaves shg[h] (ungated), sg[0] (gate logit) and
+ * sh[0, shi) (activation); sh[shi, 2 shi) is scratch. */
+void m6_granite_shexp(const float* x, const uint64_t* shp, const int* shc, float* sg, float* sh, float* shg,
+                      float* out, int shi, int h);
+/* Timing (no reference counterpart): m6_granite_shexp's device work
+ * graph-replayed `iters` times, weights rotated over n_copies device copies;
+ * out[0] = us per call, out[1] = weight bytes per call. */
+int draco_bench_shexp(const float* x, const uint64_t* shp, const int* shc, int shi, int h, int n_copies,
+                      int iters, float* out);
 
 /* ---- state sync hooks (no reference counterpart: the reference's KV state
  * is the host arrays themselves, src/draco_engine_server.py:907-922) ------ */

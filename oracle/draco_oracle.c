@@ -512,6 +512,51 @@ void or_granite_moe(const float* x0, const uint64_t* ptrs, const int* codes,
     }
 }
 
+/* gemv_any's inline F32 branch, src/m6_layer.c:148-174: four 16-lane fma
+ * accumulators over 64-value steps (a 16-value tail into the first), the
+ * lane sums (a0+a1)+(a2+a3), GCC's _mm512_reduce_add_ps tree, then the
+ * scalar tail.  Every other code goes to the scalar kernels (or_gemv). */
+static float hsum16(const float* a);
+static void or_gemv_any(int code, const float* x, const uint8_t* buf, int n_out, int n_in, float* y) {
+    if (code != 9) {
+        or_gemv(code, x, buf, n_out, n_in, y);
+        return;
+    }
+    const float* w = (const float*)buf;
+    for (int r = 0; r < n_out; r++) {
+        const float* wr = w + (size_t)r * n_in;
+        float a[4][16] = {{0}};
+        int i = 0;
+        for (; i + 63 < n_in; i += 64)
+            for (int q = 0; q < 4; q++)
+                for (int l = 0; l < 16; l++) a[q][l] = fmaf(wr[i + 16 * q + l], x[i + 16 * q + l], a[q][l]);
+        for (; i + 15 < n_in; i += 16)
+            for (int l = 0; l < 16; l++) a[0][l] = fmaf(wr[i + l], x[i + l], a[0][l]);
+        float t[16];
+        for (int l = 0; l < 16; l++) t[l] = (a[0][l] + a[1][l]) + (a[2][l] + a[3][l]);
+        float s = hsum16(t);
+        for (; i < n_in; i++) s = fmaf(wr[i], x[i], s);
+        y[r] = s;
+    }
+}
+
+/* a21  qwen35moe shared expert  src/m6_engine.c:1111-1127: SwiGLU FFN
+ * scaled by sigmoid of the one-row gate product.  shp/shc = {gate, up, down,
+ * gate_inp}; sh holds [gate | up] and then the activation in its first half. */
+void or_granite_shexp(const float* x, const uint64_t* shp, const int* shc, float* sg, float* sh,
+                      float* shg, float* out, int shi, int h) {
+    or_gemv_any(shc[3], x, (const uint8_t*)(uintptr_t)shp[3], 1, h, sg);
+    or_gemv_any(shc[0], x, (const uint8_t*)(uintptr_t)shp[0], shi, h, sh);
+    or_gemv_any(shc[1], x, (const uint8_t*)(uintptr_t)shp[1], shi, h, sh + shi);
+    for (int i = 0; i < shi; i++) {
+        const float gv = sh[i];
+        sh[i] = (gv / (1.f + expf(-gv))) * sh[shi + i];
+    }
+    or_gemv_any(shc[2], sh, (const uint8_t*)(uintptr_t)shp[2], h, shi, shg);
+    const float gate = 1.f / (1.f + expf(-sg[0]));
+    for (int i = 0; i < h; i++) out[i] = shg[i] * gate;
+}
+
 /* ------------------------------------------------------------------ */
 /* a24  GDN token-serial scan  src/m6_gdn_scan.c:18-93                 */
 /* ------------------------------------------------------------------ */

@@ -49,6 +49,7 @@ _SIGS = {
     "or_moe_route": (None, [f32p, f32p, ct.c_int, ct.c_int, ct.c_int, f32p, i32p, f32p]),
     "or_granite_moe": (None, [f32p, ct.c_void_p, i32p, f32p, ct.c_int, ct.c_int, ct.c_int, ct.c_int,
                               ct.c_int, f32p, f32p]),
+    "or_granite_shexp": (None, [f32p, ct.c_void_p, i32p, f32p, f32p, f32p, f32p, ct.c_int, ct.c_int]),
     "or_gdn_scan": (None, [f32p, f32p, f32p, f32p, f32p, f32p, f32p, f32p, ct.c_int, ct.c_int,
                            ct.c_int, f32p, f32p]),
     "or_moe_tok": (None, [f32p, i32p, f32p, ct.c_void_p, i32p, ct.c_int, ct.c_int, ct.c_int,

@@ -210,6 +210,54 @@ def gen_moe():
     print("moe.npz")
 
 
+SHEXP_CASES = [  # (tag, shi, h, codes {gate, up, down, gate_inp}, seed)
+    ("small", 256, 512, (5, 5, 4, 9), 51),
+    ("q35", 512, 2048, (5, 5, 4, 9), 52),
+    ("mixed", 128, 256, (5, 0, 0, 7), 53),
+]
+
+
+def shexp_inputs(shi, h, codes, seed):
+    """Shared-expert weights {gate, up, down, gate_inp} encoded in `codes`
+    (F32 / F16 rows as raw little-endian values) and x, from one rng stream."""
+    rng = np.random.default_rng(seed)
+
+    def enc(code, w):
+        if code == 9:
+            return np.ascontiguousarray(w, np.float32).view(np.uint8).ravel()
+        if code == 7:
+            return np.ascontiguousarray(w.astype(np.float16)).view(np.uint8).ravel()
+        return dlib.quantize(code, w)
+    shapes = [(shi, h), (shi, h), (h, shi), (1, h)]
+    ws = [enc(c, rng.standard_normal(s, dtype=np.float32) * np.float32(0.02)) for c, s in zip(codes, shapes)]
+    x = rng.standard_normal(h, dtype=np.float32)
+    ptrs = np.array([w.ctypes.data for w in ws], np.uint64)
+    return ws, x, ptrs, np.array(codes, np.int32)
+
+
+def gen_shexp():
+    """m6_granite_shexp (src/m6_engine.c:1111-1127) at three shapes / format mixes."""
+    E = ref_engine()
+    E.m6_granite_shexp.argtypes = [f32p, ct.c_void_p, i32p, f32p, f32p, f32p, f32p, ct.c_int, ct.c_int]
+    E.m6_granite_shexp.restype = None
+    out = {}
+    for tag, shi, h, codes, seed in SHEXP_CASES:
+        ws, x, ptrs, cds = shexp_inputs(shi, h, codes, seed)
+        sg = np.zeros(1, np.float32)
+        sh = np.zeros(2 * shi, np.float32)
+        shg = np.zeros(h, np.float32)
+        y = np.zeros(h, np.float32)
+        E.m6_granite_shexp(pf(x), ct.c_void_p(ptrs.ctypes.data), cds.ctypes.data_as(i32p), pf(sg), pf(sh), pf(shg),
+                           pf(y), shi, h)
+        out[f"{tag}_out"] = y
+        out[f"{tag}_shg"] = shg
+        out[f"{tag}_sg"] = sg
+        out[f"{tag}_act"] = sh[:shi].copy()
+        out[f"{tag}_digest"] = np.frombuffer(hashlib.sha256(b"".join(w.tobytes() for w in ws)).digest(), np.uint8)
+    np.savez_compressed(os.path.join(OUT, "shexp.npz"), **out)
+    print("shexp.npz")
+
+
 def gdn_inputs(T, n_vh, nhq, seed):
     rng = np.random.default_rng(seed)
     n_qkv = n_vh * 128 + 2 * nhq * 128
@@ -296,6 +344,7 @@ JOBS = {
     "gemv": gen_gemv,
     "batch8k": gen_batch8k,
     "moe": gen_moe,
+    "shexp": gen_shexp,
     "gdn": gen_gdn,
     "qwen35": gen_qwen35,
     "tiny_k": lambda: gen_llama(models.TINY_K, "llama_tiny_k.npz", logit_steps=(0, 15)),

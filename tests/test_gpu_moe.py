@@ -1,4 +1,5 @@
-"""MoE on the GPU through the reference ABI: m6_granite_moe (src/m6_layer.c:771-802)
+"""MoE on the GPU through the reference ABI: m6_granite_moe (src/m6_layer.c:771-802),
+the qwen35moe shared expert m6_granite_shexp (src/m6_engine.c:1111-1127)
 and m5_gemvn_q4k / m5_gemvn_q6k (src/m5/m5_batch8_k.c:80-183).
 
 Checks: the compiled reference's own outputs (tests/golden/moe.npz, weights
@@ -140,3 +141,31 @@ def test_moe_tok_vs_oracle(hip, oracle, n_exp, n_used, inter, H, T, codes3):
     oracle.lib.or_moe_tok(lib.pf(X), lib.pi32(order), lib.pf(wtop), ct.c_void_p(M["ptrs"].ctypes.data),
                           lib.pi32(M["codes"]), T, n_used, inter, H, H, n_exp, lib.pf(ref))
     assert rel_err(y, ref) <= TOL
+
+
+def run_shexp(fn, ptrs, cds, x, shi, h):
+    from dracohip import lib
+    sg, sh, shg, y = (np.zeros(1, np.float32), np.zeros(2 * shi, np.float32), np.zeros(h, np.float32),
+                      np.zeros(h, np.float32))
+    fn(lib.pf(x), ct.c_void_p(ptrs.ctypes.data), lib.pi32(cds), lib.pf(sg), lib.pf(sh), lib.pf(shg), lib.pf(y),
+       shi, h)
+    return y, shg, sg, sh[:shi]
+
+
+@pytest.mark.parametrize("tag", ["small", "q35", "mixed", "small"])
+def test_granite_shexp_vs_reference_golden(hip, oracle, tag):
+    """Golden from the compiled reference (Q4_K/Q6_K with an F32 gate row, and
+    a Q4_K/Q8_0 mix with an F16 gate row); "small" runs again after the other
+    shapes so the cached descriptor is re-resolved."""
+    import gen_golden as gg
+    g = golden("shexp.npz")
+    _, shi, h, codes, seed = [c for c in gg.SHEXP_CASES if c[0] == tag][0]
+    ws, x, ptrs, cds = gg.shexp_inputs(shi, h, codes, seed)
+    assert hashlib.sha256(b"".join(w.tobytes() for w in ws)).digest() == g[f"{tag}_digest"].tobytes()
+    y, shg, sg, act = run_shexp(hip.m6_granite_shexp, ptrs, cds, x, shi, h)
+    assert rel_err(y, g[f"{tag}_out"]) <= TOL, rel_err(y, g[f"{tag}_out"])
+    assert rel_err(shg, g[f"{tag}_shg"]) <= TOL
+    assert abs(float(sg[0]) - float(g[f"{tag}_sg"][0])) <= TOL * max(1.0, abs(float(g[f"{tag}_sg"][0])))
+    assert rel_err(act, g[f"{tag}_act"]) <= TOL
+    yo, _, _, _ = run_shexp(oracle.lib.or_granite_shexp, ptrs, cds, x, shi, h)
+    assert rel_err(y, yo) <= TOL

@@ -98,6 +98,23 @@ def test_granite_moe(oracle, tag):
     assert bits_equal(y, g[f"{tag}_y"])
 
 
+@pytest.mark.parametrize("case", gg.SHEXP_CASES, ids=[c[0] for c in gg.SHEXP_CASES])
+def test_granite_shexp(oracle, case):
+    """qwen35moe shared expert (src/m6_engine.c:1111-1127): every array the
+    reference writes (gated output, ungated product, gate logit, activation)."""
+    import hashlib
+    tag, shi, h, codes, seed = case
+    g = golden("shexp.npz")
+    ws, x, ptrs, cds = gg.shexp_inputs(shi, h, codes, seed)
+    assert hashlib.sha256(b"".join(w.tobytes() for w in ws)).digest() == g[f"{tag}_digest"].tobytes()
+    sg, sh, shg, y = (np.zeros(1, np.float32), np.zeros(2 * shi, np.float32), np.zeros(h, np.float32),
+                      np.zeros(h, np.float32))
+    oracle.lib.or_granite_shexp(pf(x), ct.c_void_p(ptrs.ctypes.data), pi32(cds), pf(sg), pf(sh), pf(shg), pf(y),
+                                shi, h)
+    assert bits_equal(y, g[f"{tag}_out"]) and bits_equal(shg, g[f"{tag}_shg"])
+    assert bits_equal(sg, g[f"{tag}_sg"]) and bits_equal(sh[:shi], g[f"{tag}_act"])
+
+
 def oracle_engine(oracle):
     return EngineLib(oracle.lib, forward="or_forward_token", head="or_head_op",
                      attn="or_llama_attn_op", dense="or_dense_op", name="oracle")
