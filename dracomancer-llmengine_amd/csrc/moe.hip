@@ -8,9 +8,10 @@
 //   y[j] = W[idx[j]] . x_j, x_j = x + j*x_stride.
 //
 // Launches for one MoE FFN:
-//   k_moe_logits   one wave per expert row of the fp32 router (wave-tree sum)
+//   k_moe_logits   one block per expert row of the fp32 router (tree sum)
 //   k_moe_grp      ROUTE: every block recomputes softmax / top-k / weights from
-//                  the logits (one wave, ~0.3 us) and runs the selected experts'
+//                  the logits (softmax by one wave, top-k as a parallel rank of
+//                  every expert, the bases read ahead) and runs the selected experts'
 //                  gate and up tiles together (16 rows x 256 values per item,
 //                  int8 MFMA on the digits of x as in gemv.hip) with a SwiGLU
 //                  epilogue into act[j]; block 0 publishes the routing.
@@ -35,27 +36,46 @@ namespace {
 
 constexpr int XP_MAXV = 4;
 
+// One block per router row: every thread's loads are issued together (up to
+// 4 float4 pairs per step), then a wave-tree sum and the 4 wave sums in order.
 __global__ __launch_bounds__(256) void k_moe_logits(const float* __restrict__ x, const float* __restrict__ gi,
                                                     int n_exp, int n_in, float* __restrict__ logits) {
-    const int e = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
-    if (e >= n_exp) return;  // uniform per wave
+    __shared__ float part[4];
+    constexpr int U = 4;
+    const int e = blockIdx.x, tid = threadIdx.x;
     const float* w = gi + (size_t)e * n_in;
     float acc = 0.f;
-    for (int i = lane * 4; i < n_in; i += 256) {
-        const float4 a = ld4(x + i), b = ld4(w + i);
-        acc = fmaf(a.x, b.x, acc);
-        acc = fmaf(a.y, b.y, acc);
-        acc = fmaf(a.z, b.z, acc);
-        acc = fmaf(a.w, b.w, acc);
+    for (int i0 = tid * 4; i0 < n_in; i0 += U * 1024) {
+        float4 a[U], b[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int i = i0 + u * 1024;
+            a[u] = i < n_in ? ld4(x + i) : make_float4(0.f, 0.f, 0.f, 0.f);
+            b[u] = i < n_in ? ld4(w + i) : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            acc = fmaf(a[u].x, b[u].x, acc);
+            acc = fmaf(a[u].y, b[u].y, acc);
+            acc = fmaf(a[u].z, b[u].z, acc);
+            acc = fmaf(a[u].w, b[u].w, acc);
+        }
     }
     acc = wave_sum(acc);
-    if (lane == 0) logits[e] = acc;
+    if ((tid & 63) == 0) part[tid >> 6] = acc;
+    lds_barrier();
+    if (tid == 0) logits[e] = (part[0] + part[1]) + (part[2] + part[3]);
 }
 
-// Softmax over n_exp (<= 512) logits, stable top-k and renormalised weights,
-// by one wave; results into sidx[n_used], swt[n_used] (LDS).
-__device__ __forceinline__ void route_wave(const float* __restrict__ logits, int n_exp, int n_used, int* sidx,
-                                           float* swt) {
+// Routing (src/m6_layer.c:774-821) in two parallel steps instead of n_used
+// sequential argmax rounds.  softmax_wave: one wave turns the logits into
+// probabilities sp[0, n_exp) (max and sum by wave trees; sp[n_exp, 512) =
+// -1, below every probability).  rank_slot: the rank of expert e is the
+// number of experts ahead of it in the reference's stable order (higher
+// probability, or the same probability and a lower index); the ranks are a
+// permutation of [0, n_exp), so the experts of rank < n_used are exactly the
+// sequential top-k, rank = slot.
+__device__ __forceinline__ void softmax_wave(const float* __restrict__ logits, int n_exp, float* sp) {
     constexpr int PER = MOE_EXP_MAX / 64;
     const int lane = threadIdx.x & 63;
     float p[PER];
@@ -78,31 +98,19 @@ __device__ __forceinline__ void route_wave(const float* __restrict__ logits, int
     }
     const float inv = 1.f / wave_sum(s);
 #pragma unroll
-    for (int q = 0; q < PER; q++) p[q] = lane + 64 * q < n_exp ? p[q] * inv : -2.f;  // -2: never selected
-    for (int t = 0; t < n_used; t++) {
-        float bv = -1.5f;
-        int bi = 0x7fffffff;
-#pragma unroll
-        for (int q = 0; q < PER; q++)
-            if (p[q] > bv) {  // q ascending = expert index ascending within the lane
-                bv = p[q];
-                bi = lane + 64 * q;
-            }
-        group_argmax<64>(bv, bi);
-#pragma unroll
-        for (int q = 0; q < PER; q++)
-            if (lane + 64 * q == bi) p[q] = -2.f;
-        if (lane == 0) {
-            sidx[t] = bi;
-            swt[t] = bv;
-        }
+    for (int q = 0; q < PER; q++) sp[lane + 64 * q] = lane + 64 * q < n_exp ? p[q] * inv : -1.f;
+}
+
+__device__ __forceinline__ int rank_slot(const float* sp, int n_exp, int e) {
+    const float pe = sp[e];
+    const float4* s4 = reinterpret_cast<const float4*>(sp);
+    int r = 0;
+    for (int f = 0; f < n_exp; f += 4) {
+        const float4 v = s4[f >> 2];
+        r += (v.x > pe || (v.x == pe && f < e)) + (v.y > pe || (v.y == pe && f + 1 < e)) +
+             (v.z > pe || (v.z == pe && f + 2 < e)) + (v.w > pe || (v.w == pe && f + 3 < e));
     }
-    if (lane == 0) {
-        float ws = 0.f;
-        for (int t = 0; t < n_used; t++) ws += swt[t];
-        if (ws < 6.103515625e-5f) ws = 6.103515625e-5f;
-        for (int t = 0; t < n_used; t++) swt[t] /= ws;
-    }
+    return r;
 }
 
 // Grouped expert GEMV over 16-row tiles: tile T -> slot s = T / tpe, local
@@ -124,6 +132,7 @@ __global__ __launch_bounds__(64 * NW) void k_moe_grp(const MoeArgs a) {
     float* swt = reinterpret_cast<float*>(sidx + MOE_USED_MAX);
     const uint8_t** sb0 = reinterpret_cast<const uint8_t**>(swt + MOE_USED_MAX);  // [MOE_USED_MAX] bases
     const uint8_t** sb1 = sb0 + MOE_USED_MAX;
+    float* sp = reinterpret_cast<float*>(sb1 + MOE_USED_MAX);                      // [MOE_EXP_MAX] probabilities
 
     const int tid = threadIdx.x, lane = tid & 63, j = lane & 15, g = lane >> 4;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -148,16 +157,35 @@ __global__ __launch_bounds__(64 * NW) void k_moe_grp(const MoeArgs a) {
     }
     // routing / expert bases
     if (ROUTE) {
-        if (w == 0) {
-            route_wave(a.logits, a.n_exp, n_slots, sidx, swt);
-            if (lane < n_slots) {
-                const int e = sidx[lane];
-                sb0[lane] = a.base0[e];
-                if (DUAL) sb1[lane] = a.base1[e];
-                if (bx == 0) {
-                    a.sel[lane] = e;
-                    a.selw[lane] = swt[lane];
-                    a.seld[lane] = a.base2[e];
+        // this thread's experts' bases, read while wave 0 reads the logits;
+        // slots default to expert 0 (every slot is overwritten below unless
+        // the probabilities hold a NaN, which then cannot index out of range)
+        const uint8_t* rb0[2];
+        const uint8_t* rb1[2];
+#pragma unroll
+        for (int k = 0; k < 2; k++) {
+            const int e = tid + k * NT;
+            rb0[k] = e < a.n_exp ? a.base0[e] : nullptr;
+            rb1[k] = (DUAL && e < a.n_exp) ? a.base1[e] : nullptr;
+        }
+        if (tid < n_slots) {
+            sidx[tid] = 0;
+            swt[tid] = 0.f;
+            sb0[tid] = a.base0[0];
+            if (DUAL) sb1[tid] = a.base1[0];
+        }
+        if (w == 0) softmax_wave(a.logits, a.n_exp, sp);
+        lds_barrier();
+#pragma unroll
+        for (int k = 0; k < 2; k++) {
+            const int e = tid + k * NT;
+            if (e < a.n_exp) {
+                const int r = rank_slot(sp, a.n_exp, e);
+                if (r < n_slots) {
+                    sidx[r] = e;
+                    swt[r] = sp[e];
+                    sb0[r] = rb0[k];
+                    if (DUAL) sb1[r] = rb1[k];
                 }
             }
         }
@@ -167,6 +195,15 @@ __global__ __launch_bounds__(64 * NW) void k_moe_grp(const MoeArgs a) {
     }
     for (int i = tid; i < 256; i += NT) reinterpret_cast<uint32_t*>(zero)[i] = 0u;
     lds_barrier();
+    if (ROUTE && bx == 0 && tid < n_slots) {  // publish the routing: weights renormalised in slot order
+        float ws = 0.f;
+        for (int t = 0; t < n_slots; t++) ws += swt[t];
+        if (ws < 6.103515625e-5f) ws = 6.103515625e-5f;
+        const int e = sidx[tid];
+        a.sel[tid] = e;
+        a.selw[tid] = swt[tid] / ws;
+        a.seld[tid] = a.base2[e];
+    }
 
     auto load = [&](int T, int b, Frag& f, Frag& f2) {
         const int s = T / tpe, lt = T - s * tpe;
@@ -298,7 +335,9 @@ __global__ __launch_bounds__(64 * NW) void k_moe_grp(const MoeArgs a) {
 
 // Down projection of the routed experts plus the weighted combine.  Block =
 // one 16-row output tile at a time; wave j (< n_used) = expert slot j, which
-// walks the nb super-blocks of its down rows over act_j's digits.
+// walks the nb super-blocks of its down rows over act_j's digits, three
+// super-blocks in flight; the first three are requested before act_j is
+// read and digitized.
 template <int NW, int FM>
 __global__ __launch_bounds__(64 * NW) void k_moe_down(const MoeArgs a) {
     extern __shared__ __align__(16) uint8_t smem[];
@@ -318,6 +357,19 @@ __global__ __launch_bounds__(64 * NW) void k_moe_down(const MoeArgs a) {
     const bool active = w < n_used;
     // this wave's expert base (routing published by k_moe_grp)
     const uint8_t* base = a.seld[active ? w : 0];
+    // item b of tile t (b clamped: a repeated item is already in flight)
+    auto ld = [&](int t, int b, Frag& f) {
+        const uint8_t* p = base + ((size_t)t * nb + (b < nb ? b : nb - 1)) * IB;
+        if (FM == 1) load_q4(p, lane, f);
+        else load_q6(p, lane, f);
+    };
+    Frag P0, P1, P2;
+    int t = blockIdx.x;
+    if (active && t < tiles) {
+        ld(t, 0, P0);
+        ld(t, 1, P1);
+        ld(t, 2, P2);
+    }
     if (tid < n_used) swt[tid] = a.selw[tid];
     for (int i = tid; i < 256; i += NT) reinterpret_cast<uint32_t*>(zero)[i] = 0u;
     // act loads (all slots), then digits
@@ -331,37 +383,34 @@ __global__ __launch_bounds__(64 * NW) void k_moe_down(const MoeArgs a) {
     const int gl4 = 4 * (g >> 1) + (g & 1), gl6 = 8 * (g >> 1) + (g & 1);
     const int8_t* xs = xd + (size_t)(active ? w : 0) * ng * 64;
     const float2* ms = xsm + (size_t)(active ? w : 0) * ng;
-    for (int t = blockIdx.x; t < tiles; t += gridDim.x) {
+    for (; t < tiles; t += gridDim.x) {
         float aD = 0.f, aM = 0.f;
         if (active) {
-            Frag P0, P1;
-            auto ld = [&](int b, Frag& f) {
-                const uint8_t* p = base + ((size_t)t * nb + b) * IB;
-                if (FM == 1) load_q4(p, lane, f);
-                else load_q6(p, lane, f);
-            };
-            ld(0, P0);
-            for (int b = 0; b < nb; b += 2) {
-                ld(b + 1 < nb ? b + 1 : b, P1);
+            auto dot = [&](const Frag& f, int b) {
                 if (FM == 1) {
                     const int8_t* xa = adig ? xs + (size_t)b * 1024 + (gl4 * 4 + (j & 3)) * 16 : zero;
-                    const float2 r = dot_q4(P0, xa, ms, b * 16 + gl4, g);
+                    const float2 r = dot_q4(f, xa, ms, b * 16 + gl4, g);
                     aD += r.x;
                     aM += r.y;
                 } else {
                     const int8_t* xa = adig ? xs + (size_t)b * 1024 + (gl6 * 4 + (j & 3)) * 16 : zero;
-                    aD += dot_q6(P0, xa, ms, b * 16 + gl6);
+                    aD += dot_q6(f, xa, ms, b * 16 + gl6);
                 }
-                if (b + 1 >= nb) break;
-                ld(b + 2 < nb ? b + 2 : b + 1, P0);
-                if (FM == 1) {
-                    const int8_t* xa = adig ? xs + (size_t)(b + 1) * 1024 + (gl4 * 4 + (j & 3)) * 16 : zero;
-                    const float2 r = dot_q4(P1, xa, ms, (b + 1) * 16 + gl4, g);
-                    aD += r.x;
-                    aM += r.y;
-                } else {
-                    const int8_t* xa = adig ? xs + (size_t)(b + 1) * 1024 + (gl6 * 4 + (j & 3)) * 16 : zero;
-                    aD += dot_q6(P1, xa, ms, (b + 1) * 16 + gl6);
+            };
+            const int tn = t + (int)gridDim.x;  // the next tile's first items follow this tile's last
+            for (int b = 0; b < nb; b += 3) {
+                dot(P0, b);
+                if (b + 3 < nb) ld(t, b + 3, P0);
+                else if (tn < tiles) ld(tn, 0, P0);
+                if (b + 1 < nb) {
+                    dot(P1, b + 1);
+                    if (b + 4 < nb) ld(t, b + 4, P1);
+                    else if (tn < tiles) ld(tn, 1, P1);
+                }
+                if (b + 2 < nb) {
+                    dot(P2, b + 2);
+                    if (b + 5 < nb) ld(t, b + 5, P2);
+                    else if (tn < tiles) ld(tn, 2, P2);
                 }
             }
         }
@@ -468,7 +517,7 @@ int dispatch_grp(const MoeArgs& a, int fm, bool dual, bool xper, bool route, int
 int draco_moe_logits_launch(const float* x, const float* gate_inp, int n_exp, int n_in, float* logits,
                             hipStream_t st) {
     if (n_exp < 1 || n_exp > MOE_EXP_MAX || n_in % 4) return -1;
-    hipLaunchKernelGGL(k_moe_logits, dim3((n_exp + 3) / 4), dim3(256), 0, st, x, gate_inp, n_exp, n_in, logits);
+    hipLaunchKernelGGL(k_moe_logits, dim3(n_exp), dim3(256), 0, st, x, gate_inp, n_exp, n_in, logits);
     return 0;
 }
 
@@ -480,7 +529,8 @@ int draco_moe_grp_launch(MoeArgs& a, int fm, bool dual, bool xper, bool route, h
     const int nw = grp_nw(n_in);
     const int nx = xper ? a.n_slots : 1;
     if ((size_t)nx * (n_in / 4) > (size_t)XP_MAXV * 64 * nw) return -1;  // prologue capacity
-    const size_t lds = (size_t)nx * (n_in / 16) * 72 + 1024 + (2 * 16 * 16 + 64) * 4 + MOE_USED_MAX * 24;
+    const size_t lds = (size_t)nx * (n_in / 16) * 72 + 1024 + (2 * 16 * 16 + 64) * 4 + MOE_USED_MAX * 24 +
+                       MOE_EXP_MAX * 4;
     if (lds > 160 * 1024) return -1;
     const int total = a.n_slots * (a.n_out_e / 16);
     const int cap = cu_count() * (nw == 4 ? 4 : (nw == 8 ? 2 : 1));
