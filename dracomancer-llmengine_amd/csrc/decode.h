@@ -47,6 +47,9 @@ void dk_fa_prep(const float* QG, float* Qr, const float* kin, float* kout, const
 void dk_swiglu(float* g, const float* u, int n, hipStream_t st);
 // out[i] = y[i] * sigmoid(g[0]) (n floats; g is one device float)
 void dk_sigmoid_scale(const float* y, const float* g, float* out, int n, hipStream_t st);
+// out[i] = y[i] * sigmoid(x . g) for a one-row F32 / F16 matrix g of n values
+// (n % 4 == 0), gdot[0] = x . g; -1 for any other g
+int dk_gate_scale(const float* x, const DracoMat& g, const float* y, float* out, float* gdot, int n, hipStream_t st);
 // out[n_in] = dequantized row ids[cursor ? *cursor : 0] of m
 void dk_embed(const DracoMat& m, const int* ids, const int* cursor, float* out, hipStream_t st);
 // out[slotp ? *slotp + 1 : slot] = first index of max(x[0..n))

@@ -459,6 +459,39 @@ __global__ __launch_bounds__(256) void k_sigmoid_scale(const float* __restrict__
     for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) out[i] = y[i] * s;
 }
 
+// out[i] = y[i] * sigmoid(x . g) for a one-row fp32 / fp16 gate g of n
+// values (n % 4 == 0): every block forms the dot (tree sum, 4 wave sums in
+// order) and scales its slice; block 0 also stores the dot in gdot[0].
+__global__ __launch_bounds__(256) void k_gate_scale(const float* __restrict__ x, const void* __restrict__ g,
+                                                    int f16, const float* __restrict__ y, float* __restrict__ out,
+                                                    float* __restrict__ gdot, int n) {
+    typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+    __shared__ float red[4];
+    const int tid = threadIdx.x;
+    float acc = 0.f;
+    for (int i = tid * 4; i < n; i += 1024) {
+        const float4 a = ld4(x + i);
+        float4 b;
+        if (f16) {
+            const h4 v = *reinterpret_cast<const h4*>(reinterpret_cast<const _Float16*>(g) + i);
+            b = make_float4((float)v.x, (float)v.y, (float)v.z, (float)v.w);
+        } else {
+            b = ld4(reinterpret_cast<const float*>(g) + i);
+        }
+        acc = fmaf(a.x, b.x, acc);
+        acc = fmaf(a.y, b.y, acc);
+        acc = fmaf(a.z, b.z, acc);
+        acc = fmaf(a.w, b.w, acc);
+    }
+    acc = wave_sum(acc);
+    if ((tid & 63) == 0) red[tid >> 6] = acc;
+    lds_barrier();
+    const float d = (red[0] + red[1]) + (red[2] + red[3]);
+    const float sgm = 1.0f / (1.0f + expf(-d));
+    if (blockIdx.x == 0 && tid == 0) gdot[0] = d;
+    for (int i = blockIdx.x * 256 + tid; i < n; i += gridDim.x * 256) out[i] = y[i] * sgm;
+}
+
 // ---------------------------------------------------------- embedding --
 // Dequantize row `tok` of a private-layout matrix into out[n_in]
 // (embed_value, embed_dev.h).
@@ -591,6 +624,14 @@ void dk_swiglu(float* g, const float* u, int n, hipStream_t st) {
 void dk_sigmoid_scale(const float* y, const float* g, float* out, int n, hipStream_t st) {
     const int blocks = (n + 255) / 256 < 1024 ? (n + 255) / 256 : 1024;
     hipLaunchKernelGGL(k_sigmoid_scale, dim3(blocks), dim3(256), 0, st, y, g, out, n);
+}
+
+int dk_gate_scale(const float* x, const DracoMat& g, const float* y, float* out, float* gdot, int n, hipStream_t st) {
+    if ((g.L.code != DRACO_F32 && g.L.code != DRACO_F16) || g.L.n_out != 1 || g.L.n_in != n || n % 4) return -1;
+    const int blocks = (n + 255) / 256 < 64 ? (n + 255) / 256 : 64;
+    hipLaunchKernelGGL(k_gate_scale, dim3(blocks), dim3(256), 0, st, x, (const void*)g.dev, g.L.code == DRACO_F16 ? 1 : 0,
+                       y, out, gdot, n);
+    return 0;
 }
 
 void dk_embed(const DracoMat& m, const int* ids, const int* cursor, float* out, hipStream_t st) {
