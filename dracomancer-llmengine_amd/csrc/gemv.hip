@@ -240,7 +240,12 @@ __global__ __launch_bounds__(64 * NW) void k_dq(const SegKArgs a) {
         }
     };
     load_next(P0, Q0);
-    for (int i = tid; i < 256; i += NT) reinterpret_cast<uint32_t*>(zero)[i] = 0u;
+    // the zero page: written by the block before its barrier, or without the
+    // barrier (no RMSNorm) by every wave for itself (identical values)
+    if (NORM)
+        for (int i = tid; i < 256; i += NT) reinterpret_cast<uint32_t*>(zero)[i] = 0u;
+    else
+        for (int i = lane; i < 256; i += 64) reinterpret_cast<uint32_t*>(zero)[i] = 0u;
 
     // ---- prologue part 2: digits into LDS, with the RMSNorm of
     // src/m6_engine.c:31-37 split in two: the digits are those of x*w, and
@@ -270,8 +275,18 @@ __global__ __launch_bounds__(64 * NW) void k_dq(const SegKArgs a) {
     if (NORM) {
         ss = wave_sum(ss);
         if (lane == 0) ssp[w] = ss;
+        lds_barrier();
+    } else {
+        // Wave w digitizes exactly the super-blocks it multiplies (float4 i4 =
+        // tid + q * NT lies in super-block w + q * NW, and its items are
+        // w, w + NW, ...), so without the RMSNorm no wave reads another
+        // wave's LDS before the first tile reduction: its own writes are
+        // ordered before its reads and the block barrier is skipped
+        // (decode 1995 -> 2009 tok/s same-box; deferring 1/rms past the
+        // barrier in the RMSNorm instances was slower, 2004 -> 1983).
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
     }
-    lds_barrier();
     float inv = 1.f;
     if (NORM) {
         float tot = 0.f;
