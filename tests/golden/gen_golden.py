@@ -214,6 +214,7 @@ SHEXP_CASES = [  # (tag, shi, h, codes {gate, up, down, gate_inp}, seed)
     ("small", 256, 512, (5, 5, 4, 9), 51),
     ("q35", 512, 2048, (5, 5, 4, 9), 52),
     ("mixed", 128, 256, (5, 0, 0, 7), 53),
+    ("q8gate", 256, 512, (0, 5, 4, 0), 54),
 ]
 
 

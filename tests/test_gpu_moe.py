@@ -152,11 +152,13 @@ def run_shexp(fn, ptrs, cds, x, shi, h):
     return y, shg, sg, sh[:shi]
 
 
-@pytest.mark.parametrize("tag", ["small", "q35", "mixed", "small"])
+@pytest.mark.parametrize("tag", ["small", "q35", "mixed", "q8gate", "small"])
 def test_granite_shexp_vs_reference_golden(hip, oracle, tag):
-    """Golden from the compiled reference (Q4_K/Q6_K with an F32 gate row, and
-    a Q4_K/Q8_0 mix with an F16 gate row); "small" runs again after the other
-    shapes so the cached descriptor is re-resolved."""
+    """Golden from the compiled reference (Q4_K/Q6_K with an F32 gate row; a
+    Q4_K/Q8_0 mix with an F16 gate row; Q8_0 gate with Q4_K up, which takes
+    the two-launch gate/up path, and a Q8_0 gate row, which takes the one-row
+    GEMV before the scale); "small" runs again after the other shapes so the
+    cached descriptor is re-resolved."""
     import gen_golden as gg
     g = golden("shexp.npz")
     _, shi, h, codes, seed = [c for c in gg.SHEXP_CASES if c[0] == tag][0]
