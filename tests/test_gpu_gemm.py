@@ -25,7 +25,11 @@ def _case(code, T, n_out, n_in, seed):
 
 @pytest.mark.parametrize("code", [5, 4, 0])
 @pytest.mark.parametrize("T,n_out,n_in", [(1, 16, 256), (7, 40, 512), (37, 96, 2048), (256, 2048, 2048),
-                                          (64, 8192, 2048), (100, 2048, 8192), (9, 48, 768)])
+                                          (64, 8192, 2048), (100, 2048, 8192), (9, 48, 768),
+                                          # the ragged last prefill chunk on the K-split products, 3 super-blocks
+                                          # per row with n_out off the 16-row tile, n_in at the 16384 cap
+                                          (191, 512, 2048), (191, 2048, 8192), (33, 1000, 768), (255, 130, 4096),
+                                          (32, 16, 16384)])
 def test_gemm_vs_oracle(hip, oracle, code, T, n_out, n_in):
     from dracohip import lib
     W, X = _case(code, T, n_out, n_in, T + n_out + code)

@@ -1,8 +1,12 @@
 """HIP GEMV through the m5 C ABI against the CPU oracle (same bytes, same x).
 
 Bar: fp32 GEMV within 1e-5 relative error,
-measured normwise as max|y_gpu - y_ref| / max|y_ref|.  Range calls must
-leave rows outside [o0,o1) untouched.
+measured normwise as max|y_gpu - y_ref| / max|y_ref|.  With a single output
+row the normwise error is the elementwise one, which cancellation can make
+arbitrarily large (a 32-term Q8_0 dot of 2.0e-4 out of terms summing to 0.34
+in magnitude: condition number ~1700); there the error is taken against the
+dot product's absolute sum sum_i |w_i x_i|, the scale of its fp32 forward
+error bound.  Range calls must leave rows outside [o0,o1) untouched.
 """
 import numpy as np
 import pytest
@@ -21,7 +25,14 @@ def _check(oracle, code, n_out, n_in, seed, W=None, x=None):
     print(f"[gemv] code={code} shape={n_out}x{n_in} seed={seed}", flush=True)
     y = lib.gemv(code, x, W, n_out, n_in)
     yr = oracle.gemv(code, x, W, n_out, n_in)
-    e = rel_err(y, yr)
+    if n_out == 1:
+        from oracle.oracle import pf, pu8
+        row = np.zeros(n_in, np.float32)
+        assert oracle.lib.or_dequant_row(code, pu8(W), n_in, pf(row)) == 0
+        scale = float(np.abs(row.astype(np.float64) * x.astype(np.float64)).sum())
+        e = float(np.max(np.abs(y.astype(np.float64) - yr))) / max(scale, 1e-30)
+    else:
+        e = rel_err(y, yr)
     assert e <= TOL, (code, n_out, n_in, e)
     return W, x, y
 
@@ -36,6 +47,8 @@ def test_gemv_golden_shapes(oracle, i):
     (5, 2048, 2048), (5, 512, 2048), (5, 8192, 2048), (4, 512, 2048), (4, 2048, 8192),
     (5, 4096, 14336), (5, 14336, 4096), (0, 960, 960), (0, 2560, 960), (0, 960, 2560),
     (0, 320, 960), (4, 3000, 2048), (5, 768, 2048), (4, 2048, 768),
+    # one row, rows off the 16-row tile, n_in at the 16384 cap, a single super-block / Q8_0 block
+    (5, 1, 4096), (5, 17, 16384), (4, 33, 256), (0, 1, 32), (4, 5, 16384),
 ])
 def test_gemv_model_shapes(oracle, code, n_out, n_in):
     _check(oracle, code, n_out, n_in, 7 + n_out + n_in)
