@@ -76,6 +76,18 @@ def test_granite_moe_configs3_q4k_experts(hip, oracle):
         assert rel_err(y, ref) <= TOL
 
 
+@pytest.mark.parametrize("n_exp,n_used", [(300, 6), (512, 16), (512, 1), (40, 8)])
+def test_granite_moe_expert_counts(hip, oracle, n_exp, n_used):
+    """Routers wider than the routing block (256 threads at n_in 512, so
+    experts 256 and up are ranked in a second pass), the 512-expert limit,
+    the largest top-k the down kernel serves (16) and top-1."""
+    inter, H = 256, 512
+    M = build_moe(n_exp, inter, H, H, 40 + n_used)
+    y = run_hip(hip, M, n_exp, n_used, inter, H, H)
+    ref = run_oracle(oracle, M, n_exp, n_used, inter, H, H)
+    assert rel_err(y, ref) <= TOL, rel_err(y, ref)
+
+
 def test_granite_moe_router_ties_pick_lowest_index(hip, oracle):
     n_exp, n_used, inter, H = 16, 4, 256, 512
     M = build_moe(n_exp, inter, H, H, 5)
