@@ -47,8 +47,20 @@ ExpertSet* expert_set(const uint64_t* ptrs, const int* codes, const float* gate_
                             memcmp(s.host_ptrs.data(), ptrs, sizeof(uint64_t) * 3 * (size_t)n_exp) == 0 &&
                             memcmp(s.host_codes.data(), codes, sizeof(int) * 3 * (size_t)n_exp) == 0;
     if (s.dev && s.epoch == epoch() && same_table) {
-        s.router = get_mat(gate_inp, DRACO_F32, n_exp, n_in);
-        return s.router ? &s : nullptr;
+        // the same pointers can now hold other bytes (new expert buffers at
+        // freed addresses): every expert goes through the registry's
+        // fingerprint check; a replaced matrix moves the epoch and the table
+        // is rebuilt below
+        for (int e = 0; e < n_exp; e++)
+            if (!get_mat((const void*)(uintptr_t)ptrs[3 * e], codes[3 * e], inter, n_in) ||
+                !get_mat((const void*)(uintptr_t)ptrs[3 * e + 1], codes[3 * e + 1], inter, n_in) ||
+                !get_mat((const void*)(uintptr_t)ptrs[3 * e + 2], codes[3 * e + 2], n_out, inter))
+                return nullptr;
+        if (s.epoch == epoch()) {
+            s.router = get_mat(gate_inp, DRACO_F32, n_exp, n_in);
+            if (s.router && s.epoch == epoch()) return &s;
+            if (!s.router) return nullptr;
+        }
     }
     const int fg = fm_of(codes[0]), fd = fm_of(codes[2]);
     if (!fg || !fd) {
