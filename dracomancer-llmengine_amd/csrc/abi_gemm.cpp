@@ -3,8 +3,8 @@
 // m5_gemm_auto: src/m5/m5_gemm_fused.c:231-241 (0 = done, -1 = code not served,
 // the caller falls back); m5_gemm: src/m5/m5_gemm.c:249-272 (Y[T x n_out] =
 // X[T x n_in] . W^T).  Host pointers.  Q4_K / Q6_K run on the f16-MFMA GEMM
-// (gemmh.hip; the int8-MFMA GEMM of gemm.hip when built with DRACO_GEMM_INT8);
-// Q8_0 runs as one device GEMV per token.
+// (gemmh.hip); Q8_0 runs as one device GEMV per token.  The int8-MFMA kernels
+// of gemm.hip serve the grouped expert GEMMs of m6_moe_tok only.
 #include <string.h>
 
 #include <vector>
@@ -24,27 +24,6 @@ int draco_enqueue_gemm(const DracoMat& m, const float* X, int T, float* Y, uint8
                 return fail(-1, "gemm: gemv launch rejected");
         return 0;
     }
-#ifdef DRACO_GEMM_INT8
-    GemmArgs a = {};
-    if (have_digits) {
-        // the launch only fills the buffer views; enqueue nothing
-        const size_t oct = (size_t)(T + 7) / 8;
-        a.xdig = reinterpret_cast<int8_t*>(digits);
-        a.xsc = reinterpret_cast<float*>(digits + oct * ((size_t)m.L.n_in / 32) * 1024);
-        a.xs32 = a.xsc + oct * ((size_t)m.L.n_in / 256) * 8;
-        a.xs16 = a.xs32 + oct * ((size_t)m.L.n_in / 32) * 8;
-        a.T = T;
-        a.n_in = m.L.n_in;
-    } else if (draco_gemm_digits_launch(X, T, m.L.n_in, digits, a, st)) {
-        return fail(-1, "gemm: digits launch rejected");
-    }
-    a.W = m.dev;
-    a.L = m.L;
-    a.Y = Y;
-    a.ldy = m.L.n_out;
-    if (draco_gemm_launch(a, st)) return fail(-1, "gemm: launch rejected");
-    return 0;
-#else
     if (!have_digits && draco_gemmh_x_launch(X, T, m.L.n_in, digits, st))
         return fail(-1, "gemm: activation launch rejected");
     GemmHArgs a = {};
@@ -63,7 +42,6 @@ int draco_enqueue_gemm(const DracoMat& m, const float* X, int T, float* Y, uint8
     }
     if (draco_gemmh_launch(a, st)) return fail(-1, "gemm: launch rejected");
     return 0;
-#endif
 }
 
 namespace {
@@ -140,13 +118,8 @@ int draco_bench_gemm(int code, const uint8_t* W, int n_out, int n_in, int T, int
     // one eager product first: it sizes the K-split scratch outside the capture
     if (enqueue_gemm(mats[0], dx, T, dy, dd, st)) return -1;
     DRACO_HIP(hipStreamSynchronize(st));
-#ifdef DRACO_GEMM_INT8
-    GemmArgs a = {};
-    if (draco_gemm_digits_launch(dx, T, n_in, dd, a, st)) return fail(-1, "bench gemm: digits rejected");
-#else
     float* part = (float*)scratch(12, sizeof(float) * (draco_gemmh_part_floats(L, T, n_out) + 1));
     if (!part) return -2;
-#endif
     hipEvent_t e0, e1;
     DRACO_HIP(hipEventCreate(&e0));
     DRACO_HIP(hipEventCreate(&e1));
@@ -158,14 +131,6 @@ int draco_bench_gemm(int code, const uint8_t* W, int n_out, int n_in, int T, int
             if (mode == 0) {
                 enqueue_gemm(mats[i % n_copies], dx, T, dy, dd, st);
             } else {
-#ifdef DRACO_GEMM_INT8
-                GemmArgs b = a;
-                b.W = mats[i % n_copies].dev;
-                b.L = L;
-                b.Y = dy;
-                b.ldy = n_out;
-                draco_gemm_launch(b, st);
-#else
                 GemmHArgs b = {};
                 b.W = mats[i % n_copies].dev;
                 b.L = L;
@@ -176,7 +141,6 @@ int draco_bench_gemm(int code, const uint8_t* W, int n_out, int n_in, int T, int
                 b.ldy = n_out;
                 b.part = part;
                 draco_gemmh_launch(b, st);
-#endif
             }
         }
         DRACO_HIP(hipStreamEndCapture(st, &graph));

@@ -110,6 +110,7 @@ struct DevModel {
     Work w;
     int* state = nullptr;   // device [1 + n_layer]
     int* hstate = nullptr;  // pinned host mirror of state
+    int state_cap = 0;      // ints allocated in state / hstate
 };
 
 struct RopeTab {
@@ -133,15 +134,6 @@ std::map<std::pair<int, float>, RopeTab>& rope_cache() {
     static auto* m = new std::map<std::pair<int, float>, RopeTab>();
     return *m;
 }
-struct NormEntry {
-    float* dev;
-    uint64_t epoch;
-};
-std::unordered_map<const void*, NormEntry>& norm_cache() {
-    static auto* m = new std::unordered_map<const void*, NormEntry>();
-    return *m;
-}
-
 extern "C" void draco_rope_table(int max_t, int rot, float base, float* tab);
 
 int report(int rc, const char* where) {
@@ -149,28 +141,12 @@ int report(int rc, const char* where) {
     return rc;
 }
 
-// device copy of a norm weight vector (immutable while registered)
+// device copy of a norm weight vector: registered like any fp32 parameter
+// array (get_vec), so a different array at a recycled host address, or one of
+// a different length, is re-uploaded rather than served from the old copy
 const float* norm_dev(const float* host, int h) {
     if (!host) return nullptr;
-    auto& c = norm_cache();
-    auto it = c.find(host);
-    if (it != c.end() && it->second.epoch == epoch()) return it->second.dev;
-    float* d = it != c.end() ? it->second.dev : nullptr;
-    if (it != c.end()) {  // re-read after an eviction: the address may hold new data
-        hipStreamSynchronize(stream());
-        hipFree(d);
-        d = nullptr;
-    }
-    if (hipMalloc(&d, sizeof(float) * h) != hipSuccess) {
-        fail(-2, "hipMalloc for norm weights failed");
-        return nullptr;
-    }
-    if (hipMemcpy(d, host, sizeof(float) * h, hipMemcpyHostToDevice) != hipSuccess) {
-        fail(-2, "norm upload failed");
-        return nullptr;
-    }
-    c[host] = NormEntry{d, epoch()};
-    return d;
+    return get_vec(host, (size_t)h);
 }
 
 // rope angle table covering positions [0, need)
@@ -361,12 +337,24 @@ DevModel* build_model(const M6LayerDesc* layers, int n_layer, int h) {
         if (ensure_work(m->w, h, a->NH * a->HD, a->NKV * a->HD, a->NH, a->HD, a->max_t, f->FF)) return nullptr;
     }
     m->epoch = epoch();
-    if (!m->state) {
-        if (hipMalloc(&m->state, sizeof(int) * (1 + n_layer + 8)) != hipSuccess ||
-            hipHostMalloc(&m->hstate, sizeof(int) * (1 + n_layer + 8), hipHostMallocDefault) != hipSuccess) {
+    // [pos, tlen of each layer]; a later model at the same descriptor address
+    // may have more layers, so the buffers grow with n_layer
+    if (m->state_cap < 1 + n_layer + 8) {
+        if (m->state) {
+            hipStreamSynchronize(stream());
+            hipFree(m->state);
+            hipHostFree(m->hstate);
+            m->state = nullptr;
+            m->hstate = nullptr;
+            m->state_cap = 0;
+        }
+        const int cap = 1 + n_layer + 8;
+        if (hipMalloc(&m->state, sizeof(int) * cap) != hipSuccess ||
+            hipHostMalloc(&m->hstate, sizeof(int) * cap, hipHostMallocDefault) != hipSuccess) {
             fail(-2, "state allocation failed");
             return nullptr;
         }
+        m->state_cap = cap;
     }
     c[layers] = m;
     return m;
@@ -1021,21 +1009,35 @@ int draco_llama_generate(const void* layers_v, int n_layer, int h, float eps, co
         dk_advance(m->state, n_layer, cursor, st);
         return 0;
     };
-    hipEvent_t e0, e1, e2;
-    DRACO_HIP(hipEventCreate(&e0));
-    DRACO_HIP(hipEventCreate(&e1));
-    DRACO_HIP(hipEventCreate(&e2));
-    hipGraphExec_t gx[2] = {nullptr, nullptr};
-    hipGraph_t gg[2] = {nullptr, nullptr};
+    // events and graphs are released on every return path (the guard's
+    // destructor waits for the stream first, so no replay is still running)
+    struct Guard {
+        hipStream_t st;
+        hipEvent_t ev[3] = {nullptr, nullptr, nullptr};
+        hipGraphExec_t gx[2] = {nullptr, nullptr};
+        hipGraph_t gg[2] = {nullptr, nullptr};
+        ~Guard() {
+            hipStreamSynchronize(st);
+            for (int k = 0; k < 2; k++) {
+                if (gx[k]) hipGraphExecDestroy(gx[k]);
+                if (gg[k]) hipGraphDestroy(gg[k]);
+            }
+            for (hipEvent_t e : ev)
+                if (e) hipEventDestroy(e);
+        }
+    } G{st};
+    for (hipEvent_t& e : G.ev) DRACO_HIP(hipEventCreate(&e));
+    hipEvent_t e0 = G.ev[0], e1 = G.ev[1], e2 = G.ev[2];
+    hipGraphExec_t* gx = G.gx;
     if (use_graph) {
         for (int k = 0; k < 2; k++) {
             DRACO_HIP(hipStreamBeginCapture(st, hipStreamCaptureModeRelaxed));
             int rc = step(k == 1);
-            hipGraph_t gr;
+            hipGraph_t gr = nullptr;
             hipError_t ce = hipStreamEndCapture(st, &gr);
+            G.gg[k] = gr;
             if (rc) return report(rc, "draco_llama_generate");
             if (ce != hipSuccess) return report(fail(-2, "graph capture: %s", hipGetErrorString(ce)), "draco_llama_generate");
-            gg[k] = gr;
             DRACO_HIP(hipGraphInstantiate(&gx[k], gr, nullptr, nullptr, 0));
         }
     }
@@ -1067,13 +1069,6 @@ int draco_llama_generate(const void* layers_v, int n_layer, int h, float eps, co
     for (int i = 0; i < n_gen; i++) out_tokens[i] = ht[n_prompt + i];
     for (int l = 0; l < n_layer; l++) *m->attn[l]->snap.tlen += steps;
     // the attn snapshots hold the tlen pointer, not its value: still valid
-    for (int k = 0; k < 2; k++) {
-        if (gx[k]) hipGraphExecDestroy(gx[k]);
-        if (gg[k]) hipGraphDestroy(gg[k]);
-    }
-    hipEventDestroy(e0);
-    hipEventDestroy(e1);
-    hipEventDestroy(e2);
     return 0;
 }
 

@@ -369,8 +369,13 @@ void m6_moe_tok(draco_dequant_fn DQ, draco_gemm_auto_fn GA, float* gwbuf, const 
     (void)work;
     (void)iwork;
     std::lock_guard<std::recursive_mutex> g(api_mutex());
-    if (int rc = moe_tok(X, order, wtop, ep, ec, T, n_used, inter, n_in, n_out, n_exp, out))
+    if (int rc = moe_tok(X, order, wtop, ep, ec, T, n_used, inter, n_in, n_out, n_exp, out)) {
+        // void ABI (as the reference): an input this library does not serve
+        // (IQ3_S experts, mixed formats, n_used > 16, ...) leaves NaN in out,
+        // so the caller's next step cannot silently read stale values
         fprintf(stderr, "m6_moe_tok: rc %d: %s\n", rc, last_error());
+        if (out && T > 0 && n_out > 0) poison(out, (size_t)T * n_out);
+    }
 }
 
 
@@ -378,8 +383,10 @@ void m6_granite_moe(const float* x0, const uint64_t* ptrs, const int* codes, con
                     int n_used, int inter, int n_in, int n_out, float* scratch_unused, float* out) {
     (void)scratch_unused;  // the device path needs no host scratch
     std::lock_guard<std::recursive_mutex> g(api_mutex());
-    if (int rc = granite_moe(x0, ptrs, codes, gate_inp, n_exp, n_used, inter, n_in, n_out, out))
+    if (int rc = granite_moe(x0, ptrs, codes, gate_inp, n_exp, n_used, inter, n_in, n_out, out)) {
         fprintf(stderr, "m6_granite_moe: rc %d: %s\n", rc, last_error());
+        if (out && n_out > 0) poison(out, (size_t)n_out);  // unserved input: NaN, not stale values
+    }
 }
 
 int m5_gemvn_q4k(const float* x, long x_stride, const uint8_t* W, const int* idx, long per, int n_out_e,

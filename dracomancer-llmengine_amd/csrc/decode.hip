@@ -587,8 +587,10 @@ int dk_attention(const float* q, const float* kc, const float* vc, float* part, 
         hipLaunchKernelGGL((k_attn_gqa<H_, R_>), grid, dim3(256), 0, st, q, kc, vc, part, state, layer, NKV, \
                            nsplit, scale);                                                                \
     } else
-        GQA_CASE(64, 4) GQA_CASE(64, 8) GQA_CASE(64, 16) GQA_CASE(128, 2) GQA_CASE(128, 4) GQA_CASE(128, 8)
-        GQA_CASE(128, 16) GQA_CASE(256, 2) GQA_CASE(256, 4) GQA_CASE(256, 8) GQA_CASE(256, 16) return -1;
+        // the shapes attn_grouped sends here: llama attention (head dim 128,
+        // GQA <= 8) and qwen35 full attention (head dim 256, 2 kv heads)
+        GQA_CASE(128, 2) GQA_CASE(128, 4) GQA_CASE(128, 8)
+        GQA_CASE(256, 2) GQA_CASE(256, 4) GQA_CASE(256, 8) GQA_CASE(256, 16) return -1;
 #undef GQA_CASE
         hipLaunchKernelGGL(k_attn_merge, dim3(NH, HD / 64), dim3(256), 0, st, part, out, nsplit, HD, gate, gstride);
         return 0;

@@ -58,6 +58,11 @@ int mirror_invalidate(const void* host);
 int mirror_pull(const void* host, size_t bytes);   // device -> host
 int mirror_push(const void* host, size_t bytes);   // host -> device
 
+// Fill a caller's host output with quiet NaN: the void entry points (as the
+// reference's, which return nothing) leave it so when they fail, so a caller
+// that cannot see the error does not read stale values as a result.
+void poison(float* host, size_t n);
+
 // Grow-only device scratch in numbered slots.
 void* scratch(int slot, size_t bytes);
 // Grow-only pinned host staging in numbered slots.

@@ -1,7 +1,9 @@
 """Read-only GGUF reader (mmap, zero-copy tensor views) and a GGUF writer.
 
-The reader keeps the interface subset of the reference's `FastGGUF`
-(src/gguf_fast.py:167-370): `FastGGUF(path)` (cached per (path, size, mtime)),
+The reader keeps the public interface subset of the reference's `FastGGUF`
+(src/gguf_fast.py:167-370), with its own parser (a bounds-checked cursor over
+the mapping) and its own per-file reuse (a metaclass keyed by the file's
+device, inode, size and mtime): `FastGGUF(path)` (one reader per unchanged file),
 `.fields` (name -> `FastField` with `.contents()`), `.tensors` (`FastTensor`:
 name, tensor_type (with `.name`), shape (ne[0] first), n_elements, n_bytes,
 data_offset, `.data` zero-copy view, `.raw_bytes()`), `get_field`,
@@ -101,42 +103,91 @@ M5_CODE = {"Q8_0": 0, "IQ4_NL": 1, "IQ3_S": 2, "Q5_K": 3, "Q6_K": 4, "Q4_K": 5, 
            "F32": 9}
 GGML_OF_M5 = {c: GGMLQuantizationType[n] for n, c in M5_CODE.items()}
 
-_SCALAR = {
-    GGUFValueType.UINT8: ("B", np.uint8, 1), GGUFValueType.INT8: ("b", np.int8, 1),
-    GGUFValueType.UINT16: ("H", np.uint16, 2), GGUFValueType.INT16: ("h", np.int16, 2),
-    GGUFValueType.UINT32: ("I", np.uint32, 4), GGUFValueType.INT32: ("i", np.int32, 4),
-    GGUFValueType.FLOAT32: ("f", np.float32, 4), GGUFValueType.BOOL: ("B", np.uint8, 1),
-    GGUFValueType.UINT64: ("Q", np.uint64, 8), GGUFValueType.INT64: ("q", np.int64, 8),
-    GGUFValueType.FLOAT64: ("d", np.float64, 8),
+# metadata scalar types as little-endian numpy dtypes (BOOL is one byte)
+_VT_DTYPE = {
+    GGUFValueType.UINT8: np.dtype("<u1"), GGUFValueType.INT8: np.dtype("<i1"),
+    GGUFValueType.UINT16: np.dtype("<u2"), GGUFValueType.INT16: np.dtype("<i2"),
+    GGUFValueType.UINT32: np.dtype("<u4"), GGUFValueType.INT32: np.dtype("<i4"),
+    GGUFValueType.FLOAT32: np.dtype("<f4"), GGUFValueType.BOOL: np.dtype("<u1"),
+    GGUFValueType.UINT64: np.dtype("<u8"), GGUFValueType.INT64: np.dtype("<i8"),
+    GGUFValueType.FLOAT64: np.dtype("<f8"),
 }
-_ITEM = {
+# tensor types stored as plain numbers (everything else is block-quantized bytes)
+_PLAIN_DTYPE = {
     GGMLQuantizationType.F16: np.float16, GGMLQuantizationType.F32: np.float32, GGMLQuantizationType.F64: np.float64,
     GGMLQuantizationType.I8: np.int8, GGMLQuantizationType.I16: np.int16, GGMLQuantizationType.I32: np.int32,
     GGMLQuantizationType.I64: np.int64,
 }
 
-_CACHE: dict = {}
+
+class _Cursor:
+    """Bounds-checked little-endian reads over the mapped file."""
+
+    def __init__(self, buf, path):
+        self.buf, self.path, self.pos = buf, path, 0
+
+    def span(self, n):
+        """Advance over n bytes and return their start offset."""
+        at = self.pos
+        if n < 0 or at + n > len(self.buf):
+            raise ValueError(f"GGUF file truncated at byte {at} (needs {n} more): {self.path}")
+        self.pos = at + n
+        return at
+
+    def number(self, dt):
+        at = self.span(dt.itemsize)
+        return np.frombuffer(self.buf, dtype=dt, count=1, offset=at)[0].item()
+
+    def u32(self):
+        return self.number(_VT_DTYPE[GGUFValueType.UINT32])
+
+    def u64(self):
+        return self.number(_VT_DTYPE[GGUFValueType.UINT64])
+
+    def text(self):
+        n = self.u64()
+        at = self.span(n)
+        return bytes(self.buf[at:at + n]).decode("utf-8", "replace")
+
+    def value(self, vt):
+        """One metadata value of type vt -> (python value or ndarray, type chain)."""
+        vt = GGUFValueType(vt)
+        if vt is GGUFValueType.STRING:
+            return self.text(), [vt]
+        if vt is not GGUFValueType.ARRAY:
+            return self.number(_VT_DTYPE[vt]), [vt]
+        et = GGUFValueType(self.u32())
+        count = self.u64()
+        if et is GGUFValueType.STRING:
+            return [self.text() for _ in range(count)], [vt, et]
+        if et is GGUFValueType.ARRAY:
+            raise ValueError("nested GGUF arrays are not supported")
+        dt = _VT_DTYPE[et]
+        at = self.span(count * dt.itemsize)
+        return np.frombuffer(self.buf, dtype=dt, count=count, offset=at), [vt, et]
 
 
 class FastField:
     """One metadata key: `contents()` gives a str, a Python scalar, or a list
     (arrays of strings or of numbers), as the reference's reader does."""
 
-    __slots__ = ("offset", "name", "value", "types")
-
     def __init__(self, offset, name, value, types):
-        self.offset, self.name, self.value, self.types = offset, name, value, types
+        self.offset = offset
+        self.name = name
+        self.value = value
+        self.types = types
 
     def contents(self, index_or_slice=slice(None)):
         v = self.value
-        if isinstance(v, list):
-            return v[index_or_slice] if isinstance(index_or_slice, int) else list(v[index_or_slice])
         if isinstance(v, np.ndarray):
-            return v.tolist()[index_or_slice]
-        return v
+            v = v.tolist()
+        if not isinstance(v, list):
+            return v
+        picked = v[index_or_slice]
+        return picked if isinstance(index_or_slice, int) else list(picked)
 
     def __repr__(self):
-        return f"FastField({self.name!r})"
+        return f"FastField({self.name!r}, {[t.name for t in self.types]})"
 
 
 class FastTensor:
@@ -144,172 +195,124 @@ class FastTensor:
     (quantized types as uint8 [rows, row bytes], float/int types in their
     dtype, numpy shape = reversed GGUF dims)."""
 
-    __slots__ = ("name", "tensor_type", "shape", "n_elements", "n_bytes", "data_offset", "data", "_mm")
-
-    def __init__(self, name, tensor_type, dims, mm, data_off_abs, n_elements, n_bytes):
+    def __init__(self, name, tensor_type, dims, mapping, offset, n_elements, n_bytes):
         self.name = name
         self.tensor_type = tensor_type
         self.shape = dims
         self.n_elements = n_elements
         self.n_bytes = n_bytes
-        self.data_offset = data_off_abs
-        self._mm = mm
-        np_dims = tuple(int(d) for d in reversed(dims.tolist()))
-        item = _ITEM.get(tensor_type)
-        if item is not None:
-            self.data = np.frombuffer(mm, dtype=item, count=n_elements, offset=data_off_abs).reshape(np_dims)
+        self.data_offset = offset
+        self._mapping = mapping
+        rows_first = tuple(int(d) for d in dims[::-1])
+        plain = _PLAIN_DTYPE.get(tensor_type)
+        if plain is not None:
+            view = np.frombuffer(mapping, dtype=plain, count=n_elements, offset=offset)
+            self.data = view.reshape(rows_first)
         else:
-            bs, ts = GGML_QUANT_SIZES[tensor_type]
-            byte_shape = np_dims[:-1] + (np_dims[-1] // bs * ts,)
-            self.data = np.frombuffer(mm, dtype=np.uint8, count=n_bytes, offset=data_off_abs).reshape(byte_shape)
+            per_block, block_bytes = GGML_QUANT_SIZES[tensor_type]
+            row_bytes = rows_first[-1] // per_block * block_bytes
+            view = np.frombuffer(mapping, dtype=np.uint8, count=n_bytes, offset=offset)
+            self.data = view.reshape(rows_first[:-1] + (row_bytes,))
 
     def raw_bytes(self):
-        return memoryview(self._mm)[self.data_offset:self.data_offset + self.n_bytes]
+        return memoryview(self._mapping)[self.data_offset:self.data_offset + self.n_bytes]
 
     def __repr__(self):
         return f"FastTensor({self.name!r}, {self.tensor_type.name}, {tuple(self.shape.tolist())})"
 
 
-class FastGGUF:
-    """Read-only, zero-copy, cached per file (path, size, mtime)."""
+class _OnePerFile(type):
+    """Constructing a reader returns the open reader of the same file while
+    the file is unchanged (same device/inode, size and modification time);
+    otherwise a fresh one, which replaces it."""
 
-    def __new__(cls, path, mode="r"):
-        key = os.path.abspath(os.fspath(path))
-        st = os.stat(key)
-        sig = (st.st_size, st.st_mtime_ns)
-        hit = _CACHE.get(key)
-        if hit is not None and hit._sig == sig:
-            return hit
-        obj = super().__new__(cls)
-        obj._key, obj._sig = key, sig
-        _CACHE[key] = obj
-        return obj
+    _open: dict = {}
+
+    def __call__(cls, path, mode="r"):
+        full = os.path.realpath(os.fspath(path))
+        st = os.stat(full)
+        ident = (st.st_dev, st.st_ino, st.st_size, st.st_mtime_ns)
+        known = _OnePerFile._open.get(full)
+        if known is not None and known._ident == ident:
+            return known
+        reader = super().__call__(full, mode)
+        reader._ident = ident
+        _OnePerFile._open[full] = reader
+        return reader
+
+
+class FastGGUF(metaclass=_OnePerFile):
+    """Read-only, zero-copy GGUF reader; one open reader per unchanged file."""
 
     def __init__(self, path, mode="r"):
-        if getattr(self, "_ready", False):
-            return
         if sys.byteorder != "little":
             raise RuntimeError("GGUF reader: little-endian hosts only")
-        self.path = self._key
+        self.path = path
         self.fields: "OrderedDict[str, FastField]" = OrderedDict()
         self.tensors: list = []
-        self._fd = os.open(self.path, os.O_RDONLY)
-        try:
-            self._mm = _mmap.mmap(self._fd, 0, access=_mmap.ACCESS_READ)
-        except ValueError:
-            os.close(self._fd)
-            _CACHE.pop(self._key, None)
-            raise ValueError(f"not a GGUF file (empty): {self.path}")
-        self.data = np.frombuffer(self._mm, dtype=np.uint8)
-        try:
-            self._parse()
-        except Exception:
-            self.data = None
-            self.tensors, self.fields = [], OrderedDict()
+        self._by_name: dict = {}
+        with open(path, "rb") as f:
             try:
-                self._mm.close()
-            except BufferError:  # views held by the traceback: the mapping goes with them
-                pass
-            os.close(self._fd)
-            _CACHE.pop(self._key, None)
+                self._map = _mmap.mmap(f.fileno(), 0, access=_mmap.ACCESS_READ)
+            except ValueError:
+                raise ValueError(f"not a GGUF file (empty): {path}") from None
+        try:
+            self._read_header()
+        except Exception:
+            self._release()
             raise
-        self._ready = True
+        self.data = np.frombuffer(self._map, dtype=np.uint8)
 
-    def _need(self, o, n):
-        if o + n > len(self._mm):
-            raise ValueError(f"GGUF file truncated at byte {o} (needs {n} more): {self.path}")
-
-    def _u32(self, o):
-        self._need(o, 4)
-        return struct.unpack_from("<I", self._mm, o)[0]
-
-    def _u64(self, o):
-        self._need(o, 8)
-        return struct.unpack_from("<Q", self._mm, o)[0]
-
-    def _str(self, o):
-        n = self._u64(o)
-        self._need(o + 8, n)
-        return o + 8 + n, self._mm[o + 8:o + 8 + n].decode("utf-8", "replace")
-
-    def _value(self, o, t):
-        t = GGUFValueType(t)
-        if t == GGUFValueType.STRING:
-            o, s = self._str(o)
-            return o, s, [t]
-        if t == GGUFValueType.ARRAY:
-            it = GGUFValueType(self._u32(o))
-            cnt = self._u64(o + 4)
-            o += 12
-            if it == GGUFValueType.STRING:
-                vals = []
-                for _ in range(cnt):
-                    o, s = self._str(o)
-                    vals.append(s)
-                return o, vals, [t, it]
-            if it == GGUFValueType.ARRAY:
-                raise ValueError("nested GGUF arrays are not supported")
-            _, dt, sz = _SCALAR[it]
-            self._need(o, cnt * sz)
-            return o + cnt * sz, np.frombuffer(self._mm, dtype=dt, count=cnt, offset=o), [t, it]
-        fmt, _, sz = _SCALAR[t]
-        self._need(o, sz)
-        return o + sz, struct.unpack_from("<" + fmt, self._mm, o)[0], [t]
-
-    def _parse(self):
-        if len(self._mm) < 24 or self._mm[:4] != b"GGUF":
+    def _read_header(self):
+        cur = _Cursor(self._map, self.path)
+        if len(self._map) < 24 or bytes(self._map[0:4]) != b"GGUF":
             raise ValueError(f"not a GGUF file: {self.path}")
-        ver = self._u32(4)
-        if ver not in (2, 3):
-            raise ValueError(f"unsupported GGUF version {ver} (2 and 3 are read)")
-        self.version = ver
-        self.tensor_count, self.kv_count = self._u64(8), self._u64(16)
-        o = 24
+        cur.span(4)
+        self.version = cur.u32()
+        if self.version not in (2, 3):
+            raise ValueError(f"unsupported GGUF version {self.version} (2 and 3 are read)")
+        self.tensor_count = cur.u64()
+        self.kv_count = cur.u64()
         for _ in range(self.kv_count):
-            start = o
-            o, k = self._str(o)
-            rt = self._u32(o)
-            o, v, chain = self._value(o + 4, rt)
-            self.fields[k] = FastField(start, k, v, chain)
-        infos = []
+            at = cur.pos
+            key = cur.text()
+            value, chain = cur.value(cur.u32())
+            self.fields[key] = FastField(at, key, value, chain)
+        directory = []
         for _ in range(self.tensor_count):
-            o, name = self._str(o)
-            nd = self._u32(o)
-            o += 4
-            if nd > GGML_MAX_DIMS:
-                raise ValueError(f"tensor {name}: {nd} dimensions (at most {GGML_MAX_DIMS})")
-            self._need(o, 8 * nd)
-            dims = np.frombuffer(self._mm, dtype=np.uint64, count=nd, offset=o).copy()
-            o += 8 * nd
-            raw_type = self._u32(o)
-            t_off = self._u64(o + 4)
-            o += 12
-            infos.append((name, dims, raw_type, t_off))
-        al = self.fields.get("general.alignment")
-        self.alignment = int(al.value) if al is not None else GGUF_DEFAULT_ALIGNMENT
-        if self.alignment == 0 or (self.alignment & (self.alignment - 1)):
+            name = cur.text()
+            n_dims = cur.u32()
+            if n_dims > GGML_MAX_DIMS:
+                raise ValueError(f"tensor {name}: {n_dims} dimensions (at most {GGML_MAX_DIMS})")
+            dims = np.array([cur.u64() for _ in range(n_dims)], np.uint64)
+            ggml_type = GGMLQuantizationType(cur.u32())
+            directory.append((name, dims, ggml_type, cur.u64()))
+        align_field = self.fields.get("general.alignment")
+        self.alignment = GGUF_DEFAULT_ALIGNMENT if align_field is None else int(align_field.contents())
+        if self.alignment <= 0 or self.alignment & (self.alignment - 1):
             raise ValueError(f"invalid alignment {self.alignment}")
-        if o % self.alignment:
-            o += self.alignment - o % self.alignment
-        self.data_offset = o
-        seen = set()
-        for name, dims, raw_type, t_off in infos:
-            if name in seen:
+        self.data_offset = -(-cur.pos // self.alignment) * self.alignment
+        for name, dims, ggml_type, rel in directory:
+            if name in self._by_name:
                 raise ValueError(f"duplicate tensor name {name}")
-            seen.add(name)
-            gt = GGMLQuantizationType(raw_type)
-            n_el = 1
-            for d in dims.tolist():
-                n_el *= int(d)
-            bs, ts = GGML_QUANT_SIZES[gt]
-            if dims.size and int(dims[0]) % bs:
+            per_block, block_bytes = GGML_QUANT_SIZES[ggml_type]
+            n_elements = int(np.prod(dims.astype(np.int64))) if dims.size else 1
+            if dims.size and int(dims[0]) % per_block:
                 raise ValueError(f"tensor {name}: row of {int(dims[0])} values is not a whole number of blocks")
-            n_bytes = n_el // bs * ts
-            abs_off = o + t_off
-            if abs_off + n_bytes > len(self._mm):
-                raise ValueError(f"tensor {name}: data ({n_bytes} bytes at {abs_off}) past the end of the file")
-            self.tensors.append(FastTensor(name, gt, dims, self._mm, abs_off, n_el, n_bytes))
-        self._by_name = {t.name: t for t in self.tensors}
+            n_bytes = n_elements // per_block * block_bytes
+            start = self.data_offset + rel
+            if start + n_bytes > len(self._map):
+                raise ValueError(f"tensor {name}: data ({n_bytes} bytes at {start}) past the end of the file")
+            t = FastTensor(name, ggml_type, dims, self._map, start, n_elements, n_bytes)
+            self.tensors.append(t)
+            self._by_name[name] = t
+
+    def _release(self):
+        self.tensors, self._by_name, self.data = [], {}, None
+        try:
+            self._map.close()
+        except BufferError:  # views still held elsewhere: the mapping goes with them
+            pass
 
     def get_field(self, key):
         return self.fields.get(key)
@@ -321,23 +324,22 @@ class FastGGUF:
         return self._by_name.get(name)
 
     def tensor_bytes(self, name):
-        return bytes(self.tensor(name).raw_bytes())
+        return bytes(self._by_name[name].raw_bytes())
 
     def close(self):
-        """Drop the cache entry and release the mapping.  Views taken from
-        `.data` of this reader's tensors must be gone first."""
-        _CACHE.pop(self._key, None)
+        """Forget this reader and release the mapping.  Views taken from
+        `.data` of its tensors must be gone first."""
+        if _OnePerFile._open.get(self.path) is self:
+            del _OnePerFile._open[self.path]
         for t in self.tensors:
             t.data = None
-            t._mm = None
-        self.data = None
-        self._mm.close()
-        os.close(self._fd)
+            t._mapping = None
+        self._release()
 
 
 def load(path):
     r = FastGGUF(path)
-    return r, {t.name: t for t in r.tensors}
+    return r, dict(r._by_name)
 
 
 # ------------------------------------------------------------------ writer --

@@ -4,8 +4,8 @@ The reference driver dequantizes one embedding row on the host: Q8_0 inline
 in numpy (src/smol_engine.py:180-185), other formats through gguf-py's
 dequantize (src/smol_engine.py:187).  These decoders compute the same fp32
 values with the same operation order ((d*sc)*q for Q6_K, d*sc*q - dmin*m for
-Q4_K, q*d for Q8_0); tests/test_host.py checks them bit-for-bit against the
-oracle's decoder.  The device-resident decode loop does the same lookup on
+Q4_K, q*d for Q8_0); tests/test_oracle_pins.py checks them bit-for-bit
+against the oracle's row decoder.  The device-resident decode loop does the same lookup on
 the GPU (embed kernel) and never calls this module.
 """
 import numpy as np

@@ -76,7 +76,15 @@ TINY_Q8 = LlamaConfig(
     codes=dict(q=Q8_0, k=Q8_0, v=Q8_0, o=Q8_0, gate=Q8_0, up=Q8_0, down=Q8_0, emb=Q8_0, out=Q8_0),
     tied=True, n_prompt=8, n_gen=16, max_t=64, wscale=0.25)
 
-CONFIGS = {c.name: c for c in (SMOL360M, LLAMA1B, TINY_K, TINY_Q8)}
+# configs[3]'s attention block (32 q / 4 kv heads of 128, Q6_K projections,
+# cache of 512 rows) as a one-layer llama model: the attention parity cases
+ATTN_CFG3 = LlamaConfig(
+    name="attn-cfg3-q6k", hidden=2048, n_layer=1, n_head=32, n_kv=4, head_dim=128, n_ff=256, vocab=256,
+    eps=1e-6, rope_base=1000000.0,
+    codes=dict(q=Q6_K, k=Q6_K, v=Q6_K, o=Q6_K, gate=Q4_K, up=Q4_K, down=Q4_K, emb=Q6_K, out=Q6_K),
+    tied=True, n_prompt=8, n_gen=8, max_t=512)
+
+CONFIGS = {c.name: c for c in (SMOL360M, LLAMA1B, TINY_K, TINY_Q8, ATTN_CFG3)}
 
 
 @dataclass

@@ -133,8 +133,8 @@ int draco_llama_generate(const void* layers, int n_layer, int h, float eps,
  * afterwards the engine state is that of forward(ids[i], pos + i) run token
  * by token), which the reference implements for qwen35 only ----------------
  * ids[0..n) at positions pos .. pos + n - 1, in chunks of the chunk size:
- * per layer one RMSNorm, the q/k/v, o, gate/up and down products as int8-MFMA
- * GEMMs over the chunk's tokens, rope + KV append at rows tlen .. tlen + n - 1
+ * per layer one RMSNorm, the q/k/v, o, gate/up and down products as f16-MFMA
+ * GEMMs over the chunk's tokens (exact f16 operands, fp32 accumulation), rope + KV append at rows tlen .. tlen + n - 1
  * (device mirrors) and causal attention; every tlen advances by n.
  * out_x[h] (host, nullable) = hidden state of the last token after the last
  * layer (the x m6_forward_token leaves).  0 = ok. */
@@ -191,7 +191,8 @@ int draco_bench_granite_moe(const float* x0, const uint64_t* ptrs, const int* co
 /* ---- Prefill GEMM: Y[T x n_out] = X[T x n_in] . W^T ----------------------
  * m5_gemm_auto: src/m5/m5_gemm_fused.c:231-241 (0 done, -1 code not served:
  * the caller falls back).  m5_gemm: src/m5/m5_gemm.c:249-272.  Host pointers.
- * Served: Q4_K and Q6_K on int8 MFMA, Q8_0 as per-token device GEMVs.
+ * Served: Q4_K and Q6_K on f16 MFMA (exact operands), Q8_0 as per-token
+ * device GEMVs.
  * `wbuf` is not used. */
 int m5_gemm_auto(int code, const float* X, const uint8_t* W, int c, int n_out, int n_in, float* Y);
 int m5_gemm(int code, const float* X, const uint8_t* W, int T, int n_out, int n_in, float* Y, float* wbuf);

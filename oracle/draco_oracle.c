@@ -16,6 +16,13 @@
  * m5_gemm_fused.c need a header that is not in the tree) are pinned by
  * invariants instead; their docstrings say which.
  *
+ * OR_MUTANT (compile-time, default 0) plants one known slip for the pin
+ * tests to catch (tests/test_oracle_pins.py builds each mutant into a
+ * temporary library and checks that its pins fail): 1 Q4_K nibble swap and
+ * 2 Q4_K min term dropped in or_dequant_row, 3 Q6_K high-bit shift taken
+ * from the wrong index, 4 or_gemm output transposed, 5 or_moe_tok weighting
+ * every slot by slot 0's weight.  The shipped liboracle.so is built with 0.
+ *
  * Q8_K (activation quantizer) and the integer block dots have no reference in
  * the tree at all.  They follow llama.cpp's published quantize_row_q8_K_ref /
  * ggml_vec_dot_q4_K_q8_K / ggml_vec_dot_q6_K_q8_K algorithm (ggml-quants.c,
@@ -28,6 +35,10 @@
 #include <stdlib.h>
 #include <math.h>
 #include <omp.h>
+
+#ifndef OR_MUTANT
+#define OR_MUTANT 0
+#endif
 
 /* ------------------------------------------------------------------ */
 /* a1  IEEE half -> float, exact incl. subnormals                      */
@@ -219,8 +230,10 @@ int or_gemv(int code, const float* x, const uint8_t* W, int n_out, int n_in, flo
 /* ------------------------------------------------------------------ */
 /* a12  independent row dequantizer  src/m5/m5_gemm.c:55-235           */
 /*      (Q8_0 :56-68, Q4_K :142-169, Q6_K :193-211).  The value of     */
-/*      each weight equals what row_dot multiplies by x (pinned by the */
-/*      one-hot test: gemv with x = e_i returns column i).             */
+/*      each weight equals what row_dot multiplies by x.  Pinned by    */
+/*      tests/test_oracle_pins.py: every row equals the one-hot        */
+/*      columns of or_gemv (bitwise pinned to the compiled scalar      */
+/*      kernel) and the independent numpy decoders, bit for bit.       */
 /* ------------------------------------------------------------------ */
 int or_dequant_row(int code, const uint8_t* row, int n_in, float* out) {
     if (code == 0) {
@@ -242,8 +255,17 @@ int or_dequant_row(int code, const uint8_t* row, int n_in, float* out) {
                 const float dsc = d * sc[j], dm = dmin * mn[j];
                 const uint8_t* qb = qs + (j >> 1) * 32;
                 for (int k = 0; k < 32; k++) {
+#if OR_MUTANT == 1
+                    const float qv = (float)((j & 1) ? (qb[k] & 0xF) : (qb[k] >> 4));
+#else
                     const float qv = (float)((j & 1) ? (qb[k] >> 4) : (qb[k] & 0xF));
+#endif
+#if OR_MUTANT == 2
+                    out[b * 256 + j * 32 + k] = dsc * qv;
+                    (void)dm;
+#else
                     out[b * 256 + j * 32 + k] = dsc * qv - dm;
+#endif
                 }
             }
         }
@@ -259,7 +281,11 @@ int or_dequant_row(int code, const uint8_t* row, int n_in, float* out) {
             for (int p = 0; p < 256; p++) {
                 const uint8_t lb = ql[(p >> 7) * 64 + (p & 63)];
                 const int lo4 = ((p >> 6) & 1) ? (lb >> 4) : (lb & 0x0F);
+#if OR_MUTANT == 3
+                const int hi2 = (qh[(p >> 7) * 32 + (p & 31)] >> (((p >> 6) & 3) * 2)) & 3;
+#else
                 const int hi2 = (qh[(p >> 7) * 32 + (p & 31)] >> (((p >> 5) & 3) * 2)) & 3;
+#endif
                 const int q = (lo4 | (hi2 << 4)) - 32;
                 out[b * 256 + p] = d * (float)sc[p >> 4] * (float)q;
             }
@@ -837,11 +863,13 @@ int or_full_attn(const float* h1, const OrFullW* w, const float* Kr, const float
 
 /* ------------------------------------------------------------------ */
 /* a22  token-batched MoE  src/m6_moe_tok.c:44-161, restated with the  */
-/* per-token expert FFN of the decode path.  Pinned by the invariant   */
-/* "token-batched == token-serial" (the reference's own gate,          */
-/* src/prefill_chunk_gate.py:25-46): every (token, slot) runs the same */
-/* scalar GEMVs as or_granite_moe's expert phase, and the scatter adds */
-/* slots in k order.                                                   */
+/* per-token expert FFN of the decode path.  Pinned by                 */
+/* tests/test_oracle_pins.py: (1) token-batched == token-serial, bit   */
+/* for bit (the reference's own gate, src/prefill_chunk_gate.py:25-46):*/
+/* every (token, slot) runs the same scalar GEMVs as or_granite_moe's  */
+/* expert phase and the scatter adds slots in k order; (2) within      */
+/* 1e-5 of the compiled src/m6_moe_tok.c (tests/golden/moetok.npz),    */
+/* whose dots are 16-lane FMA trees.                                   */
 /* ------------------------------------------------------------------ */
 void or_moe_tok(const float* X, const int* order, const float* wtop,
                 const uint64_t* ep, const int* ec, int T, int n_used, int inter,
@@ -867,7 +895,11 @@ void or_moe_tok(const float* X, const int* order, const float* wtop,
                     act[i] = (gv / (1.f + expf(-gv))) * uu[i];
                 }
                 or_gemv_range(ec[3 * e + 2], act, (const uint8_t*)(uintptr_t)ep[3 * e + 2], n_out, inter, yd, 0, n_out);
+#if OR_MUTANT == 5
+                const float w = wtop[t * n_used];
+#else
                 const float w = wtop[t * n_used + k];
+#endif
                 for (int r = 0; r < n_out; r++) o[r] += w * yd[r];
             }
         }
@@ -881,9 +913,10 @@ void or_moe_tok(const float* X, const int* order, const float* wtop,
 /* m5_gemm semantics (src/m5/m5_gemm.c:249-272): dequantize each row   */
 /* once (a12), then one dot per token.  The reference's dot is a       */
 /* 16-lane AVX-512 tree; this restatement sums sequentially, so it is  */
-/* pinned by invariants (== stacked GEMVs within fp32 tolerance,       */
-/* one-hot columns exact), not bitwise -- m5_gemm.c cannot be built    */
-/* here (its header iq3s_grid.h is absent from the tree).              */
+/* pinned by invariants (tests/test_oracle_pins.py: == stacked GEMVs  */
+/* within 1e-6, one-hot token rows give the dequantized columns bit    */
+/* for bit), not bitwise -- m5_gemm.c cannot be built here (its header */
+/* iq3s_grid.h is absent from the tree).                               */
 /* ------------------------------------------------------------------ */
 int or_gemm(int code, const float* X, const uint8_t* W, int T, int n_out, int n_in, float* Y) {
     if (!or_supported(code) || code == 3) return -1;
@@ -898,7 +931,11 @@ int or_gemm(int code, const float* X, const uint8_t* W, int T, int n_out, int n_
                 const float* xt = X + (size_t)t * n_in;
                 float s = 0.f;
                 for (int i = 0; i < n_in; i++) s += wb[i] * xt[i];
+#if OR_MUTANT == 4
+                Y[(size_t)r * T + t] = s;
+#else
                 Y[(size_t)t * n_out + r] = s;
+#endif
             }
         }
         free(wb);

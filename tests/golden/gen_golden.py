@@ -3,7 +3,8 @@
 Runs only where the reference tree exists and `make -C oracle ref` built
 oracle/_ref/*.so (the reference's sources compiled in place).  Every output
 array here is produced by the compiled reference (src/m5_kern_scalar.c,
-src/m5/m5_batch8_k.c, src/m6_engine.c + m6_layer.c, src/m6_gdn_scan.c) on
+src/m5/m5_batch8_k.c, src/m6_engine.c + m6_layer.c, src/m6_gdn_scan.c,
+src/m6_moe_tok.c) on
 seeded inputs; the inputs are regenerated deterministically by the tests
 (weights via dracohip.models, vectors via numpy default_rng) or stored when
 small.
@@ -292,6 +293,114 @@ def gen_gdn():
     print("gdn.npz")
 
 
+MOETOK_CASES = [  # (tag, n_exp, n_used, inter, n_in (= n_out), T, codes {gate, up, down}, seed)
+    ("small", 16, 4, 256, 512, 20, (5, 5, 4), 81),
+    ("cfg3", 128, 8, 768, 2048, 24, (5, 5, 5), 82),
+    ("q6mix", 32, 6, 512, 1024, 12, (4, 5, 4), 83),
+]
+
+
+def moetok_inputs(n_exp, n_used, inter, n_in, T, codes, seed):
+    """Seeded expert weights (3 per expert), token rows X[T][n_in] and routing
+    (distinct experts per token from the lower half of the experts, so some
+    experts get no token; weights normalised per token; slot 1 of token 3 holds
+    the invalid id -1, which both sides skip)."""
+    rng = np.random.default_rng(seed)
+    mats = [dlib.quantize(codes[0], rng.standard_normal((n_exp * inter, n_in), dtype=np.float32) * np.float32(0.02)),
+            dlib.quantize(codes[1], rng.standard_normal((n_exp * inter, n_in), dtype=np.float32) * np.float32(0.02)),
+            dlib.quantize(codes[2], rng.standard_normal((n_exp * n_in, inter), dtype=np.float32) * np.float32(0.02))]
+    ptrs = np.zeros(3 * n_exp, np.uint64)
+    ec = np.zeros(3 * n_exp, np.int32)
+    for e in range(n_exp):
+        for k in range(3):
+            ptrs[3 * e + k] = mats[k].ctypes.data + e * (mats[k].nbytes // n_exp)
+            ec[3 * e + k] = codes[k]
+    X = rng.standard_normal((T, n_in)).astype(np.float32)
+    order = np.stack([rng.choice(n_exp // 2, n_used, replace=False) for _ in range(T)]).astype(np.int32)
+    order[3, 1] = -1
+    wtop = rng.random((T, n_used)).astype(np.float32)
+    wtop /= wtop.sum(axis=1, keepdims=True)
+    return mats, ptrs, ec, X, np.ascontiguousarray(order), np.ascontiguousarray(wtop)
+
+
+def gen_moetok():
+    """m6_moe_tok (src/m6_moe_tok.c:44-161) compiled from the reference, driven
+    with GA = NULL (its row-dequantize + dot path) and DQ = the oracle's row
+    decoder (the reference's own m5_dequant_row lives in src/m5/m5_gemm.c,
+    which cannot be built here); the decoder is pinned bit for bit by
+    tests/test_oracle_pins.py."""
+    from oracle.oracle import Oracle
+    orc = Oracle()
+    M = ref("moetok")
+    M.m6_moe_tok.restype = None
+    M.m6_moe_tok.argtypes = [ct.c_void_p] * 8 + [ct.c_int] * 6 + [ct.c_void_p] * 3
+    dq = ct.cast(orc.lib.or_dequant_row, ct.c_void_p)
+    nth = 2 * (os.cpu_count() or 8)
+    out = {}
+    for tag, n_exp, n_used, inter, n_in, T, codes, seed in MOETOK_CASES:
+        mats, ptrs, ec, X, order, wtop = moetok_inputs(n_exp, n_used, inter, n_in, T, codes, seed)
+        y = np.zeros((T, n_in), np.float32)
+        gwbuf = np.zeros(nth * ((max(n_in, inter) + 15) & ~15), np.float32)
+        work = np.zeros(T * n_used * (n_in + 3 * inter + n_in), np.float32)
+        iwork = np.zeros(T * n_used * 2 + n_exp + 1, np.int32)
+        M.m6_moe_tok(dq, None, gwbuf.ctypes.data, X.ctypes.data, order.ctypes.data, wtop.ctypes.data,
+                     ptrs.ctypes.data, ec.ctypes.data, T, n_used, inter, n_in, n_in, n_exp,
+                     y.ctypes.data, work.ctypes.data, iwork.ctypes.data)
+        out[f"{tag}_y"] = y
+        out[f"{tag}_digest"] = np.frombuffer(hashlib.sha256(b"".join(m.tobytes() for m in mats)).digest(), np.uint8)
+    np.savez_compressed(os.path.join(OUT, "moetok.npz"), **out)
+    print("moetok.npz")
+
+
+ATTN_CFG3_T0 = 480      # cached rows before the first step
+ATTN_CFG3_STEPS = 4
+
+
+def attn_cfg3_inputs():
+    """configs[3]'s attention (ATTN_CFG3, one layer): the layer's weights, a
+    cache holding ATTN_CFG3_T0 seeded rows and the normalised inputs of
+    ATTN_CFG3_STEPS tokens."""
+    cfg = models.ATTN_CFG3
+    model = models.build_llama(cfg, 7)
+    rng = np.random.default_rng(77)
+    kd = cfg.n_kv * cfg.head_dim
+    krows = rng.standard_normal((ATTN_CFG3_T0, kd), dtype=np.float32)
+    vrows = rng.standard_normal((ATTN_CFG3_T0, kd), dtype=np.float32)
+    xs = rng.standard_normal((ATTN_CFG3_STEPS, cfg.hidden), dtype=np.float32)
+    return cfg, model, krows, vrows, xs
+
+
+def run_attn_steps(drv, attn_fn, krows, vrows, xs, pos0):
+    """Drive one layer's attention op token by token from a pre-filled cache;
+    returns the outputs [steps][hidden] and the appended K/V rows."""
+    t0 = krows.shape[0]
+    drv.kc[0][:krows.size] = krows.reshape(-1)
+    drv.vc[0][:vrows.size] = vrows.reshape(-1)
+    drv.tl[0][0] = t0
+    outs = np.zeros((xs.shape[0], drv.H), np.float32)
+    for s in range(xs.shape[0]):
+        attn_fn(pf(np.ascontiguousarray(xs[s])), drv.descs[0].attn_p, pos0 + s, pf(outs[s]))
+    return outs
+
+
+def gen_attn_cfg3():
+    """m6_llama_attn_op (src/m6_engine.c:425-517) at configs[3]'s attention
+    shape: 32 q / 4 kv heads of 128 (GQA 8), Q6_K projections, 480 cached rows
+    + 4 steps."""
+    E = ref_engine()
+    E.m6_llama_attn_op.argtypes = [f32p, ct.c_void_p, ct.c_int, f32p]
+    E.m6_llama_attn_op.restype = None
+    cfg, model, krows, vrows, xs = attn_cfg3_inputs()
+    drv = LlamaDriver(model, EngineLib(E, name="ref"))
+    outs = run_attn_steps(drv, E.m6_llama_attn_op, krows, vrows, xs, ATTN_CFG3_T0)
+    kd = cfg.n_kv * cfg.head_dim
+    n = (ATTN_CFG3_T0 + ATTN_CFG3_STEPS) * kd
+    np.savez_compressed(os.path.join(OUT, "attn_cfg3.npz"), out=outs,
+                        knew=drv.kc[0][ATTN_CFG3_T0 * kd:n].copy(), vnew=drv.vc[0][ATTN_CFG3_T0 * kd:n].copy(),
+                        digest=np.frombuffer(bytes.fromhex(model.digest()), np.uint8))
+    print("attn_cfg3.npz")
+
+
 # qwen35 layer ops: (tag, n_vh, codes, seed) and (tag, nh, codes, seed, [(told, pos0), ...])
 QWEN_GDN_CASES = [("cfg5", 32, (5, 5, 5), 51), ("q80", 16, (0, 0, 0), 52), ("mixed", 16, (5, 4, 4), 53)]
 QWEN_FULL_CASES = [("cfg5", 16, (5, 5, 4, 5), 61, [(0, 0), (7, 7), (300, 300), (40, 45)]),
@@ -345,6 +454,8 @@ JOBS = {
     "gemv": gen_gemv,
     "batch8k": gen_batch8k,
     "moe": gen_moe,
+    "moetok": gen_moetok,
+    "attn_cfg3": gen_attn_cfg3,
     "shexp": gen_shexp,
     "gdn": gen_gdn,
     "qwen35": gen_qwen35,

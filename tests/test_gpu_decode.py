@@ -159,6 +159,67 @@ def test_attn_op_head_shapes_match_oracle(oracle, hd, nh, nkv):
     print(f"[attn_op] hd {hd} nh {nh} nkv {nkv}: worst {worst:.2e}")
 
 
+def test_attn_op_configs3_vs_reference_golden():
+    """configs[3]'s attention (32 q / 4 kv heads of 128: the group-shared
+    kernel at GQA 8, Q6_K projections) from a 480-row cache, 4 steps to a
+    484-row cache, against the compiled reference: outputs and the appended
+    K/V rows (pulled from the device mirror)."""
+    import gen_golden as gg
+    from dracohip import lib
+    g = golden("attn_cfg3.npz")
+    cfg, model, krows, vrows, xs = gg.attn_cfg3_inputs()
+    assert model.digest() == g["digest"].tobytes().hex()
+    lib.load().draco_reset()
+    drv = LlamaDriver(model, hip_engine_lib())
+    print("[attn_op] configs[3] shape vs reference golden", flush=True)
+    outs = gg.run_attn_steps(drv, drv.engine.cdll.m6_llama_attn_op, krows, vrows, xs, gg.ATTN_CFG3_T0)
+    for s in range(gg.ATTN_CFG3_STEPS):
+        assert rel_err(outs[s], g["out"][s]) <= 1e-5, (s, rel_err(outs[s], g["out"][s]))
+    assert lib.load().draco_state_pull(ct.cast(drv.descs, ct.c_void_p), drv.NL) == 0
+    kd = cfg.n_kv * cfg.head_dim
+    n = (gg.ATTN_CFG3_T0 + gg.ATTN_CFG3_STEPS) * kd
+    assert rel_err(drv.kc[0][gg.ATTN_CFG3_T0 * kd:n], g["knew"]) <= 1e-5
+    assert rel_err(drv.vc[0][gg.ATTN_CFG3_T0 * kd:n], g["vnew"]) <= 1e-5
+    assert np.array_equal(drv.kc[0][:gg.ATTN_CFG3_T0 * kd], krows.reshape(-1))
+
+
+@pytest.mark.parametrize("nh,nkv", [(4, 2), (8, 2), (32, 4)])
+def test_attn_op_grouped_head_dim_128_match_oracle(oracle, nh, nkv):
+    """The group-shared attention kernel at head dim 128 for every GQA ratio
+    m6_llama_attn_op sends to it (2, 4, 8): 40 tokens from a 200-row cache of
+    256 (8 splits) through m6_llama_attn_op, against the oracle after every
+    token."""
+    import dataclasses
+    from tests_oracle_engine import oracle_engine
+    from dracohip import lib
+    cfg = dataclasses.replace(models.TINY_Q8, name=f"gqa-128-{nh}-{nkv}", head_dim=128, n_head=nh, n_kv=nkv,
+                              hidden=256, max_t=256)
+    model = models.build_llama(cfg, 1)
+    lib.load().draco_reset()
+    drv = LlamaDriver(model, hip_engine_lib())
+    ref = LlamaDriver(model, oracle_engine(oracle))
+    rng = np.random.default_rng(9)
+    kd = nkv * 128
+    rows = rng.standard_normal((2, 200 * kd), dtype=np.float32)
+    for d in (drv, ref):
+        d.kc[0][:rows.shape[1]] = rows[0]
+        d.vc[0][:rows.shape[1]] = rows[1]
+        d.tl[0][0] = 200
+    L = drv.engine.cdll
+    worst = 0.0
+    for step in range(40):
+        xn = rng.standard_normal(cfg.hidden, dtype=np.float32)
+        out = np.zeros(cfg.hidden, np.float32)
+        outr = np.zeros(cfg.hidden, np.float32)
+        print(f"[attn_op] grouped hd 128 nh {nh} nkv {nkv} step {step}", flush=True)
+        L.m6_llama_attn_op(pf(xn), drv.descs[0].attn_p, 200 + step, pf(out))
+        oracle.lib.or_llama_attn_op(pf(xn), ref.descs[0].attn_p, 200 + step, pf(outr))
+        e = rel_err(out, outr)
+        worst = max(worst, e)
+        assert e <= 1e-5, (step, e)
+    print(f"[attn_op] grouped hd 128 nh {nh} nkv {nkv}: worst {worst:.2e}")
+
+
 def test_smol360m_device_generate():
     """SmolLM2-360M-shaped Q8_0, 32 prompt + 64 greedy tokens."""
     g = golden("smol360m.npz")

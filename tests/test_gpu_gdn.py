@@ -81,3 +81,33 @@ def test_gdn_beta_zero_only_decays(hip):
     decay = np.prod(G.astype(np.float64), axis=0)  # [n_vh]
     want = S.reshape(n_vh, -1).astype(np.float64) * decay[:, None]
     assert rel_err(S2.reshape(n_vh, -1), want) <= 1e-6
+
+
+def test_gdn_scan_configs4_4096_tokens_then_decode(hip, oracle):
+    """configs[4]'s scan length: 4096 tokens in 64-token calls, then 64
+    single-token calls (decode), at 32 V / 16 q-k heads of 128, the state and
+    conv tail carried through the ABI; against the oracle's one-shot scan of
+    all 4160 tokens.  Reports the worst normwise error of every call's outputs
+    and of the final state (error growth over the recurrence)."""
+    T, n_vh, nhq = 4096 + 64, 32, 16
+    n_qkv, QKV, Z, B, G, conv, ssm_norm, tail, S = gg.gdn_inputs(T, n_vh, nhq, 45)
+    S[:] = 0.0
+    tail[:] = 0.0
+    ONo, So, tailo = scan_oracle(oracle, T, n_qkv, n_vh, QKV, Z, B, G, conv, ssm_norm, tail, S)
+    St, tt = S.copy(), tail.copy()
+    worst, t0 = 0.0, 0
+    while t0 < T:
+        n = 64 if t0 < 4096 else 1
+        sl = slice(t0, t0 + n)
+        if t0 % 1024 == 0 or t0 >= 4096 and (t0 - 4096) % 16 == 0:
+            print(f"[gdn] 4096-token scan: token {t0}, worst so far {worst:.2e}", flush=True)
+        on, St, tt = scan(hip, n, n_qkv, n_vh, np.ascontiguousarray(QKV[sl]), np.ascontiguousarray(Z[sl]),
+                          np.ascontiguousarray(B[sl]), np.ascontiguousarray(G[sl]), conv, ssm_norm, tt, St)
+        e = rel_err(on, ONo[sl])
+        worst = max(worst, e)
+        assert e <= TOL, (t0, e)
+        t0 += n
+    es = rel_err(St, So)
+    print(f"[gdn] 4096 + 64 tokens: worst per-call output error {worst:.2e}, final state {es:.2e}", flush=True)
+    assert es <= TOL
+    assert np.array_equal(tt, tailo)

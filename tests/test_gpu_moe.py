@@ -183,3 +183,50 @@ def test_granite_shexp_vs_reference_golden(hip, oracle, tag):
     assert rel_err(act, g[f"{tag}_act"]) <= TOL
     yo, _, _, _ = run_shexp(oracle.lib.or_granite_shexp, ptrs, cds, x, shi, h)
     assert rel_err(y, yo) <= TOL
+
+
+@pytest.mark.parametrize("tag", [c[0] for c in __import__("gen_golden").MOETOK_CASES])
+def test_moe_tok_vs_reference_golden(hip, tag):
+    """m6_moe_tok against the compiled reference's token-batched MoE
+    (tests/golden/moetok.npz): Q4_K / Q6_K experts, experts with no tokens and
+    an invalid slot (-1)."""
+    import gen_golden as gg
+    from dracohip import lib
+    g = golden("moetok.npz")
+    _, n_exp, n_used, inter, H, T, codes, seed = [c for c in gg.MOETOK_CASES if c[0] == tag][0]
+    mats, ptrs, ec, X, order, wtop = gg.moetok_inputs(n_exp, n_used, inter, H, T, codes, seed)
+    assert hashlib.sha256(b"".join(m.tobytes() for m in mats)).digest() == g[f"{tag}_digest"].tobytes()
+    y = np.zeros((T, H), np.float32)
+    z = np.zeros(8, np.float32)
+    zi = np.zeros(8, np.int32)
+    print(f"[moe_tok] {tag} vs reference golden", flush=True)
+    hip.m6_moe_tok(None, None, lib.pf(z), lib.pf(X), lib.pi32(order), lib.pf(wtop), ct.c_void_p(ptrs.ctypes.data),
+                   lib.pi32(ec), T, n_used, inter, H, H, n_exp, lib.pf(y), lib.pf(z), lib.pi32(zi))
+    assert rel_err(y, g[f"{tag}_y"]) <= TOL, rel_err(y, g[f"{tag}_y"])
+
+
+def test_unserved_moe_inputs_leave_nan(hip):
+    """The void MoE entry points cannot return an error code (as the
+    reference's): for input they do not serve (IQ3_S experts, which the
+    reference's qwen35 prefill passes to m6_moe_tok) they leave NaN in out
+    instead of stale values."""
+    from dracohip import lib
+    n_exp, n_used, inter, H = 16, 4, 256, 512
+    M = build_moe(n_exp, inter, H, H, 70)
+    codes = M["codes"].copy()
+    codes[:] = 2  # IQ3_S
+    y = np.zeros(H, np.float32)
+    scratch = np.zeros(8, np.float32)
+    hip.m6_granite_moe(lib.pf(M["x"]), ct.c_void_p(M["ptrs"].ctypes.data), lib.pi32(codes), lib.pf(M["gate_inp"]),
+                       n_exp, n_used, inter, H, H, lib.pf(scratch), lib.pf(y))
+    assert np.all(np.isnan(y))
+    T = 3
+    X = np.ones((T, H), np.float32)
+    order = np.tile(np.arange(n_used, dtype=np.int32), (T, 1))
+    wtop = np.full((T, n_used), 1.0 / n_used, np.float32)
+    out = np.zeros((T, H), np.float32)
+    z = np.zeros(8, np.float32)
+    zi = np.zeros(8, np.int32)
+    hip.m6_moe_tok(None, None, lib.pf(z), lib.pf(X), lib.pi32(order), lib.pf(wtop), ct.c_void_p(M["ptrs"].ctypes.data),
+                   lib.pi32(codes), T, n_used, inter, H, H, n_exp, lib.pf(out), lib.pf(z), lib.pi32(zi))
+    assert np.all(np.isnan(out))

@@ -61,7 +61,8 @@ def test_q8k_isums_bit_exact(hip, oracle, code, n_out, n_in):
 
 @pytest.mark.parametrize("code", [4, 5])
 @pytest.mark.parametrize("n_out,n_in,nvec", [(64, 256, 1), (1000, 2048, 1), (512, 2048, 8), (200, 768, 4),
-                                             (14336, 4096, 1), (4096, 14336, 1), (14336, 4096, 8)])
+                                             (14336, 4096, 1), (4096, 14336, 1), (14336, 4096, 8),
+                                             (4096, 14336, 8)])
 def test_gemv_q8k_vs_oracle(hip, oracle, code, n_out, n_in, nvec):
     from dracohip import lib
     rng = np.random.default_rng(1)

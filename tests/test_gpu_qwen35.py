@@ -81,11 +81,13 @@ def test_full_attn_vs_reference(hip, tag):
             assert e <= TOL, (told, pos0, n, e)
 
 
-def test_full_attn_long_cache_vs_oracle(hip, oracle):
-    """1000 cached rows (the split-T path with 32 splits) at the configs[4] shape."""
+@pytest.mark.parametrize("nh,told", [(16, 1000), (4, 300), (32, 500)])
+def test_full_attn_long_cache_vs_oracle(hip, oracle, nh, told):
+    """Long caches through the split-T group-shared kernel at head dim 256 for
+    every GQA ratio the full attention uses here: 16 q heads over the 2 kv
+    heads (GQA 8, the configs[4] shape, 1000 rows), 4 (GQA 2) and 32 (GQA 16)."""
     from dracohip import qwen35 as Q
-    L = Q.full_layer(63, 16, (5, 5, 4, 5))
-    told = 1000
+    L = Q.full_layer(63 + nh, nh, (5, 5, 4, 5))
     Kr, Vc = Q.kv_rows(64, told)
     h1 = Q.hidden(65)[0]
     outs = []
@@ -93,7 +95,7 @@ def test_full_attn_long_cache_vs_oracle(hip, oracle):
         x2n, x2o = np.zeros(Q.H, np.float32), np.zeros(Q.H, np.float32)
         krn, vrn = np.zeros(512, np.float32), np.zeros(512, np.float32)
         if fn == "hip":
-            print("[full_attn] long cache told 1000", flush=True)
+            print(f"[full_attn] long cache nh {nh} told {told}", flush=True)
             buf = np.zeros(16, np.float32)
             hip.m6_full_attn(_pf(h1), L.ptr(), _pf(Kr), _pf(Vc), told, told, _pf(buf), _pf(buf), _pf(x2n),
                              _pf(x2o), _pf(krn), _pf(vrn))

@@ -11,8 +11,9 @@ import pytest
 from helpers import bits_equal, golden
 import gen_golden as gg
 from dracohip import models
-from dracohip.driver import EngineLib, LlamaDriver
+from dracohip.driver import LlamaDriver
 from oracle.oracle import pf, pu8, pi32
+from tests_oracle_engine import oracle_engine
 
 
 @pytest.mark.parametrize("case", [c[0] for c in gg.GEMV_CASES])
@@ -115,11 +116,6 @@ def test_granite_shexp(oracle, case):
     assert bits_equal(sg, g[f"{tag}_sg"]) and bits_equal(sh[:shi], g[f"{tag}_act"])
 
 
-def oracle_engine(oracle):
-    return EngineLib(oracle.lib, forward="or_forward_token", head="or_head_op",
-                     attn="or_llama_attn_op", dense="or_dense_op", name="oracle")
-
-
 @pytest.mark.parametrize("cfgname,fname", [("tiny-kquant", "llama_tiny_k.npz"), ("tiny-q8_0", "llama_tiny_q8.npz")])
 def test_llama_decode_tiny(oracle, cfgname, fname):
     """Token-serial prefill + greedy decode through the descriptor ABI, bitwise."""
@@ -219,3 +215,18 @@ def test_gdn_attn_closed_forms(oracle):
         np.testing.assert_allclose(S1[h], g[h] * S0[h], rtol=2e-5, atol=1e-9)
     # with q = k = v = 0 the output o is 0, so the layer adds ssm_out(0) = 0
     np.testing.assert_array_equal(x2o, h1)
+
+
+def test_llama_attn_configs3_shape(oracle):
+    """or_llama_attn_op at configs[3]'s attention shape (32 q / 4 kv heads of
+    128, Q6_K, 480 cached rows + 4 steps), bitwise to the compiled reference."""
+    g = golden("attn_cfg3.npz")
+    cfg, model, krows, vrows, xs = gg.attn_cfg3_inputs()
+    assert model.digest() == g["digest"].tobytes().hex()
+    drv = LlamaDriver(model, oracle_engine(oracle))
+    outs = gg.run_attn_steps(drv, oracle.lib.or_llama_attn_op, krows, vrows, xs, gg.ATTN_CFG3_T0)
+    kd = cfg.n_kv * cfg.head_dim
+    n = (gg.ATTN_CFG3_T0 + gg.ATTN_CFG3_STEPS) * kd
+    assert bits_equal(outs, g["out"])
+    assert bits_equal(drv.kc[0][gg.ATTN_CFG3_T0 * kd:n], g["knew"])
+    assert bits_equal(drv.vc[0][gg.ATTN_CFG3_T0 * kd:n], g["vnew"])
