@@ -107,6 +107,7 @@ int ensure_init() {
     if (n <= s.device) return fail(-2, "no HIP device %d (count %d)", s.device, n);
     DRACO_HIP(hipSetDevice(s.device));
     DRACO_HIP(hipStreamCreateWithFlags(&s.st, hipStreamNonBlocking));
+    if (int rc = noalloc_setup(s.device)) return rc;  // the no-alloc entry point's staging address
     s.inited = true;
     return 0;
 }

@@ -21,6 +21,9 @@ std::recursive_mutex& api_mutex();
 // Initialise device + stream on first use.  0 = ok.
 int ensure_init();
 hipStream_t stream();
+// Device address of the no-alloc entry point's static staging array on
+// `device` (noalloc.hip); called by ensure_init with that device current.
+int noalloc_setup(int device);
 
 // Record an error message (readable through draco_last_error()).
 int fail(int rc, const char* fmt, ...);

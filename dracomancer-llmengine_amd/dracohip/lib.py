@@ -95,6 +95,9 @@ SIGNATURES = {
     "draco_gemv_q8k_f32": (ct.c_int, [ct.c_int, f32p, ct.c_int, u8p, ct.c_int, ct.c_int, f32p]),
     "draco_q8k_isums": (ct.c_int, [ct.c_int, u8p, u8p, ct.c_int, ct.c_int, i32p, i32p]),
     "draco_bench_gemv_q8k": (ct.c_int, [ct.c_int, u8p, ct.c_int, ct.c_int, ct.c_int, ct.c_int, ct.c_int, f32p]),
+    "draco_gemv_q8k_f32_noalloc": (ct.c_int, [ct.c_int, ct.c_void_p, ct.c_int, ct.c_void_p, ct.c_int, ct.c_int,
+                                              ct.c_void_p, ct.c_void_p]),
+    "draco_noalloc_capacity": (ct.c_size_t, []),
     "draco_quantize": (ct.c_int, [ct.c_int, f32p, ct.c_int, ct.c_int, u8p]),
     "draco_layout_query": (ct.c_size_t, [ct.c_int, ct.c_int, ct.c_int, ct.POINTER(ct.c_size_t)]),
     "draco_repack": (ct.c_int, [ct.c_int, u8p, ct.c_int, ct.c_int, u8p]),

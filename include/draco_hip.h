@@ -171,7 +171,9 @@ void m6_granite_moe(const float* x0, const uint64_t* ptrs, const int* codes, con
  * host pointers / codes per expert.  Served: Q4_K / Q6_K experts (one format
  * per role across experts), inter and n_in multiples of 256, n_out a
  * multiple of 16.  DQ, GA, gwbuf, work and iwork are accepted and not used
- * (the device path runs its own grouped GEMMs). */
+ * (the device path runs its own grouped GEMMs).  Unserved input (e.g. IQ3_S
+ * experts) is reported on stderr and leaves NaN in out (void, as the
+ * reference; m6_granite_moe does the same). */
 void m6_moe_tok(int (*DQ)(int, const uint8_t*, int, float*),
                 int (*GA)(int, const float*, const uint8_t*, int, int, int, float*), float* gwbuf, const float* X,
                 const int* order, const float* wtop, const uint64_t* ep, const int* ec, int T, int n_used, int inter,
@@ -286,6 +288,19 @@ int draco_gemv_q8k_f32(int code, const float* x, int nvec, const uint8_t* W, int
 /* Integer super-block sums of one vector: isc[r * nb + b], imn[r * nb + b]. */
 int draco_q8k_isums(int code, const uint8_t* xq, const uint8_t* W, int n_out, int n_in, int32_t* isc,
                     int32_t* imn);
+/* No reference counterpart.  For callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc): draco_gemv_q8k_f32 with DEVICE pointers and no allocation.
+ * x [nvec][n_in] fp32, W the weights already in this library's device layout
+ * (draco_repack of the GGUF rows; draco_layout_query bytes), y [nvec][n_out]
+ * fp32.  The Q8_K blocks of x are staged in a static device array of
+ * draco_noalloc_capacity() bytes (1 MiB: nvec * n_in / 256 * 292 bytes at
+ * most; larger requests return -1).  Enqueued on `stream` (a hipStream_t;
+ * NULL = the library's stream) and not waited for.  Every call on one GPU
+ * shares that GPU's staging array: calls that overlap on one GPU race. */
+int draco_gemv_q8k_f32_noalloc(int code, const float* x, int nvec, const uint8_t* W, int n_out, int n_in, float* y,
+                               void* stream);
+size_t draco_noalloc_capacity(void);
 /* out[0] us per Q8_K GEMV launch, out[1] us per (quantize + GEMV) pair, both
  * from a graph replay of `iters` launches over n_copies weight copies. */
 int draco_bench_gemv_q8k(int code, const uint8_t* W, int n_out, int n_in, int nvec, int n_copies, int iters,
