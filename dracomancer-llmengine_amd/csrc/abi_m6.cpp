@@ -24,6 +24,7 @@
 
 #include "decode.h"
 #include "gemm.h"
+#include "moe.h"
 #include "prefill.h"
 #include "runtime.h"
 
@@ -59,6 +60,7 @@ typedef struct {
 
 void m6_llama_attn_op(const float* xn, void* p, int pos, float* out);
 void m6_dense_op(const float* xn, void* p, float* out);
+void draco_moe_ffn_op(const float* xn, void* p, float* out);  // abi_moe.cpp
 }
 
 using namespace draco;
@@ -104,7 +106,9 @@ struct DevModel {
     PfBufs pf;
     std::vector<M6LayerDesc> descs;
     std::vector<DevAttn*> attn;
-    std::vector<DevFfn*> ffn;
+    std::vector<DevFfn*> ffn;          // dense FFN layers (m6_dense_op), else null
+    std::vector<MoeLayer*> moe;        // MoE FFN layers (draco_moe_ffn_op), else null
+    std::vector<DracoMoeP> moe_snap;   // their parameter structs when built
     std::vector<const float*> anorm, fnorm;
     int h = 0, n_layer = 0;
     Work w;
@@ -301,40 +305,67 @@ DevModel* build_model(const M6LayerDesc* layers, int n_layer, int h) {
         DevModel* m = it->second;
         bool ok = m->epoch == epoch() && m->n_layer == n_layer && m->h == h &&
                   memcmp(m->descs.data(), layers, sizeof(M6LayerDesc) * n_layer) == 0;
-        for (int l = 0; ok && l < n_layer; l++)
+        for (int l = 0; ok && l < n_layer; l++) {
             ok = memcmp(&m->attn[l]->snap, layers[l].attn_p, sizeof(M6LlamaAttnP)) == 0 &&
-                 memcmp(&m->ffn[l]->snap, layers[l].ffn_p, sizeof(M6DenseP)) == 0 &&
-                 attn_cache().count(layers[l].attn_p) && attn_cache().at(layers[l].attn_p) == m->attn[l] &&
-                 ffn_cache().count(layers[l].ffn_p) && ffn_cache().at(layers[l].ffn_p) == m->ffn[l];
-        if (ok) return m;
+                 attn_cache().count(layers[l].attn_p) && attn_cache().at(layers[l].attn_p) == m->attn[l];
+            if (ok && m->moe[l])  // MoE layer: the op's parameter struct unchanged, its experts current
+                ok = memcmp(&m->moe_snap[l], layers[l].ffn_p, sizeof(DracoMoeP)) == 0 &&
+                     draco_moe_layer((const DracoMoeP*)layers[l].ffn_p) == m->moe[l];
+            else if (ok)
+                ok = memcmp(&m->ffn[l]->snap, layers[l].ffn_p, sizeof(M6DenseP)) == 0 &&
+                     ffn_cache().count(layers[l].ffn_p) && ffn_cache().at(layers[l].ffn_p) == m->ffn[l];
+        }
+        if (ok && m->epoch == epoch()) return m;
     }
     DevModel* m = (it != c.end()) ? it->second : new DevModel();
     m->descs.assign(layers, layers + n_layer);
     m->attn.assign(n_layer, nullptr);
     m->ffn.assign(n_layer, nullptr);
+    m->moe.assign(n_layer, nullptr);
+    m->moe_snap.assign(n_layer, DracoMoeP{});
     m->anorm.assign(n_layer, nullptr);
     m->fnorm.assign(n_layer, nullptr);
     m->h = h;
     m->n_layer = n_layer;
     for (int l = 0; l < n_layer; l++) {
         const M6LayerDesc& L = layers[l];
-        if ((void*)L.attn != (void*)&m6_llama_attn_op || (void*)L.ffn != (void*)&m6_dense_op) {
+        const bool dense = (void*)L.ffn == (void*)&m6_dense_op;
+        const bool moe = (void*)L.ffn == (void*)&draco_moe_ffn_op;
+        if ((void*)L.attn != (void*)&m6_llama_attn_op || (!dense && !moe)) {
             fail(-1, "m6_forward_token: layer %d uses an op not served by this library", l);
             return nullptr;
         }
         DevAttn* a = get_attn((const M6LlamaAttnP*)L.attn_p);
-        DevFfn* f = get_ffn((const M6DenseP*)L.ffn_p);
-        if (!a || !f) return nullptr;
-        if (a->H != h || f->H != h) {
+        if (!a) return nullptr;
+        int FF = 1;
+        if (dense) {
+            DevFfn* f = get_ffn((const M6DenseP*)L.ffn_p);
+            if (!f) return nullptr;
+            if (f->H != h) {
+                fail(-1, "m6_forward_token: layer %d hidden size mismatch", l);
+                return nullptr;
+            }
+            m->ffn[l] = f;
+            FF = f->FF;
+        } else {
+            const DracoMoeP* mp = (const DracoMoeP*)L.ffn_p;
+            if (mp->n_in != h || mp->n_out != h) {
+                fail(-1, "m6_forward_token: layer %d MoE width %d/%d != hidden %d", l, mp->n_in, mp->n_out, h);
+                return nullptr;
+            }
+            m->moe[l] = draco_moe_layer(mp);
+            if (!m->moe[l]) return nullptr;
+            m->moe_snap[l] = *mp;
+        }
+        if (a->H != h) {
             fail(-1, "m6_forward_token: layer %d hidden size mismatch", l);
             return nullptr;
         }
         m->attn[l] = a;
-        m->ffn[l] = f;
         m->anorm[l] = norm_dev(L.attn_norm, h);
         m->fnorm[l] = norm_dev(L.ffn_norm, h);
         if ((L.attn_norm && !m->anorm[l]) || (L.ffn_norm && !m->fnorm[l])) return nullptr;
-        if (ensure_work(m->w, h, a->NH * a->HD, a->NKV * a->HD, a->NH, a->HD, a->max_t, f->FF)) return nullptr;
+        if (ensure_work(m->w, h, a->NH * a->HD, a->NKV * a->HD, a->NH, a->HD, a->max_t, FF)) return nullptr;
     }
     m->epoch = epoch();
     // [pos, tlen of each layer]; a later model at the same descriptor address
@@ -462,9 +493,17 @@ int enqueue_layer(DevModel* m, int l, float eps, hipStream_t st, const float* xi
                      a->scale, st))
         return fail(-1, "attention launch");
     if (draco_gemv_launch(*a->wo, w.att, w.x, x0, 0, H, st)) return fail(-1, "gemv o");
+    if (m->moe[l])  // RMSNorm, router, routed gate/up + SwiGLU, down + weighted combine + residual
+        return draco_moe_layer_enqueue(m->moe[l], w.x, m->fnorm[l], eps, w.x, w.x, st);
     if (int rc = enqueue_gateup(f, w, w.x, 1, m->fnorm[l], eps, st)) return rc;
     if (draco_gemv_launch(*f->d, w.g, w.x, w.x, 0, H, st)) return fail(-1, "gemv down");
     return 0;
+}
+
+bool has_moe(const DevModel* m) {
+    for (const MoeLayer* p : m->moe)
+        if (p) return true;
+    return false;
 }
 
 // ---- chunked prefill (configs of the reference's forward_chunk,
@@ -482,7 +521,7 @@ int ensure_pf(DevModel* m, int cap) {
         NH = std::max(NH, a->NH);
         HD = std::max(HD, a->HD);
         max_t = std::max(max_t, a->max_t);
-        FF = std::max(FF, m->ffn[l]->FF);
+        if (m->ffn[l]) FF = std::max(FF, m->ffn[l]->FF);
     }
     const size_t part_n = pf_part_floats(NH, cap, HD, pf_attn_nsplit(max_t, cap));
     const int win = std::max(std::max(m->h, QD), FF);
@@ -563,6 +602,10 @@ int enqueue_prefill_layer(DevModel* m, int l, int T, int pos0, int row0, float e
 // host tlen counters are not advanced here).  The last token's hidden state
 // is left in pf.X row (last chunk's T - 1); returns that T (0 on error).
 int enqueue_prefill(DevModel* m, const DracoMat* em, const int* ids, int n, int pos0, float eps, hipStream_t st) {
+    if (has_moe(m)) {
+        fail(-1, "chunked prefill: MoE layers are fed token by token (draco_llama_generate does so)");
+        return 0;
+    }
     const int C = g_prefill_chunk;
     if (C < 1 || n < 1) return 0;
     if (ensure_pf(m, C)) return 0;
@@ -964,7 +1007,8 @@ int draco_llama_generate(const void* layers_v, int n_layer, int h, float eps, co
     // prompt[0 .. n_prompt - 1) goes through the chunked prefill when enabled
     // (the last prompt token goes through the first decode step, which also
     // runs the head); the token cursor then starts past those tokens
-    const int n_chunked = (g_prefill_chunk > 0 && n_prompt - 1 >= 2) ? n_prompt - 1 : 0;
+    // (MoE models feed the prompt through token-serial decode steps)
+    const int n_chunked = (g_prefill_chunk > 0 && n_prompt - 1 >= 2 && !has_moe(m)) ? n_prompt - 1 : 0;
     if (n_chunked && ensure_pf(m, g_prefill_chunk)) return report(-2, "draco_llama_generate (prefill buffers)");
     ht[ntok + 8] = n_chunked;
     DRACO_HIP(hipMemcpyAsync(dtok, ht.data(), sizeof(int) * (ntok + 64), hipMemcpyHostToDevice, st));

@@ -254,7 +254,9 @@ int moe_tok(const float* X, const int* order, const float* wtop, const uint64_t*
         memset(out, 0, sizeof(float) * (size_t)T * n_out);
         return 0;
     }
-    if (!fm_of(cg) || !fm_of(cu) || !fm_of(cd) || cg != cu)
+    // gate and up may differ in format: the up product reuses the gate's
+    // activation digits, which do not depend on the weight format
+    if (!fm_of(cg) || !fm_of(cu) || !fm_of(cd))
         return fail(-1, "m6_moe_tok: expert formats %d/%d/%d not served", cg, cu, cd);
     const int R = 8 * n_oct;
     std::vector<int> src(R, -1), pos((size_t)T * n_used, -1), fill(n_exp, 0);
@@ -353,9 +355,85 @@ int moe_tok(const float* X, const int* order, const float* wtop, const uint64_t*
     return 0;
 }
 
+std::map<const void*, MoeLayer*>& moe_layers() {
+    static auto* m = new std::map<const void*, MoeLayer*>();
+    return *m;
+}
+
 }  // namespace
 
+// ---- the MoE FFN of one layer inside the device decode loop --------------
+struct MoeLayer {
+    DracoMoeP snap;
+    ExpertSet* set = nullptr;
+    uint64_t epoch = 0;
+    MoeWork w = {};
+    float* xn = nullptr;
+    char* buf = nullptr;  // own allocation behind w (router logits, activations, routing)
+};
+
+MoeLayer* draco_moe_layer(const DracoMoeP* p) {
+    if (!p) {
+        fail(-1, "moe layer: null parameters");
+        return nullptr;
+    }
+    MoeLayer*& slot = moe_layers()[p];
+    if (slot && slot->epoch == epoch() && memcmp(&slot->snap, p, sizeof(*p)) == 0) return slot;
+    if (check_moe(p->n_exp, p->n_used, p->inter, p->n_in, p->n_out)) return nullptr;
+    if (ensure_init()) return nullptr;
+    if (!slot) slot = new MoeLayer();
+    MoeLayer* m = slot;
+    m->set = expert_set(p->ptrs, p->codes, p->gate_inp, p->n_exp, p->inter, p->n_in, p->n_out, stream());
+    if (!m->set) return nullptr;
+    // own buffers: captured graphs keep these addresses, so nothing shared
+    // with the host-pointer entry points (whose scratch can be regrown)
+    const size_t bytes = sizeof(float) * ((size_t)p->n_in + 64) + sizeof(void*) * MOE_USED_MAX +
+                         sizeof(float) * ((size_t)p->n_exp + (size_t)p->n_used * p->inter + 2 * MOE_USED_MAX) + 256;
+    if (m->buf) {
+        hipStreamSynchronize(stream());
+        hipFree(m->buf);
+        m->buf = nullptr;
+    }
+    if (hipMalloc(&m->buf, bytes) != hipSuccess) {
+        fail(-2, "moe layer: work allocation failed");
+        return nullptr;
+    }
+    m->xn = (float*)m->buf;
+    char* q = m->buf + sizeof(float) * ((size_t)p->n_in + 64);
+    m->w.seld = (const uint8_t**)q;
+    m->w.logits = (float*)(q + sizeof(void*) * MOE_USED_MAX);
+    m->w.selw = m->w.logits + p->n_exp;
+    m->w.sel = (int*)(m->w.selw + MOE_USED_MAX);
+    m->w.act = (float*)(m->w.sel + MOE_USED_MAX);
+    m->snap = *p;
+    m->epoch = m->set->epoch;
+    return m;
+}
+
+int draco_moe_layer_enqueue(MoeLayer* m, const float* x, const float* norm_w, float eps, float* out,
+                            const float* resid, hipStream_t st) {
+    const DracoMoeP& p = m->snap;
+    dk_rmsnorm(x, norm_w, m->xn, p.n_in, eps, st);
+    return enqueue_moe(m->set, m->xn, out, resid, m->w, p.n_exp, p.n_used, p.inter, p.n_in, p.n_out, st);
+}
+
 extern "C" {
+
+// The MoE FFN as an m6 ffn op (no reference counterpart as an op: the
+// reference's qwen35 driver calls m6_granite_moe per layer from Python,
+// src/qwen35_engine.py:293-307): out[n_out] = m6_granite_moe(xn, ...) with
+// the arguments packed in DracoMoeP.  Called directly it runs like
+// m6_granite_moe; inside M6LayerDesc it lets m6_forward_token and the device
+// decode loop run MoE layers (src/m6_engine.c:61-83 with this op as ffn).
+void draco_moe_ffn_op(const float* xn, void* pv, float* out) {
+    const DracoMoeP* p = (const DracoMoeP*)pv;
+    std::lock_guard<std::recursive_mutex> g(api_mutex());
+    if (int rc = granite_moe(xn, p->ptrs, p->codes, p->gate_inp, p->n_exp, p->n_used, p->inter, p->n_in, p->n_out,
+                             out)) {
+        fprintf(stderr, "draco_moe_ffn_op: rc %d: %s\n", rc, last_error());
+        if (out && p->n_out > 0) poison(out, (size_t)p->n_out);
+    }
+}
 
 typedef int (*draco_dequant_fn)(int, const uint8_t*, int, float*);
 typedef int (*draco_gemm_auto_fn)(int, const float*, const uint8_t*, int, int, int, float*);

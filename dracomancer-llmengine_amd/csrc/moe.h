@@ -46,6 +46,26 @@ int draco_moe_down_launch(MoeArgs& a, int fm, hipStream_t st);
 // slots per grouped launch when every slot has its own x of length n_in
 int draco_moe_xper_slots(int n_in);
 
+// The MoE FFN as an m6 ffn op's parameters (include/draco_hip.h DracoMoeP):
+// m6_granite_moe's arguments (src/m6_layer.c:771) in one struct.
+struct DracoMoeP {
+    const uint64_t* ptrs;   // [3 * n_exp] host pointers: gate, up, down per expert
+    const int* codes;       // [3 * n_exp]
+    const float* gate_inp;  // [n_exp][n_in] fp32 router
+    int n_exp, n_used, inter, n_in, n_out;
+    float* scratch;         // the reference op's host scratch (unused here)
+};
+
+// One decoder layer's MoE FFN for the device decode loop (abi_m6.cpp): the
+// expert set resolved once, per-layer work buffers of its own (a captured
+// graph keeps pointing at them).  nullptr + fail() on error.
+struct MoeLayer;
+MoeLayer* draco_moe_layer(const DracoMoeP* p);
+// out = resid + MoE(RMSNorm(x) * norm_w), device pointers; out may alias x
+// and resid (x is read by the norm launch before anything is written).
+int draco_moe_layer_enqueue(MoeLayer* m, const float* x, const float* norm_w, float eps, float* out,
+                            const float* resid, hipStream_t st);
+
 // token-batched MoE helpers
 int draco_moe_gather_launch(const float* X, int n_in, const int* src, int rows, float* Xg, hipStream_t st);
 int draco_moe_scatter_launch(const float* Yd, int n_out, const int* pos, const float* wt, int n_used, int T, float* out,

@@ -47,11 +47,21 @@ class M6DenseP(ct.Structure):
                 ("n_ff", ct.c_int), ("h", ct.c_int)]
 
 
+class DracoMoeP(ct.Structure):
+    """Parameters of the MoE FFN op (include/draco_hip.h DracoMoeP): the
+    arguments of m6_granite_moe (src/m6_layer.c:771) in one struct."""
+    _fields_ = [("ptrs", ct.c_void_p), ("codes", ct.c_void_p), ("gate_inp", f32p),
+                ("n_exp", ct.c_int), ("n_used", ct.c_int), ("inter", ct.c_int), ("n_in", ct.c_int),
+                ("n_out", ct.c_int), ("scratch", f32p)]
+
+
 class EngineLib:
-    """An m6-ABI library: forward_token, head_op and the two op pointers."""
+    """An m6-ABI library: forward_token, head_op and the op pointers (the MoE
+    FFN op is optional: `moe=None` for libraries without one; a caller may set
+    `moe_ptr` to a callback of its own)."""
 
     def __init__(self, cdll, forward="m6_forward_token", head="m6_head_op",
-                 attn="m6_llama_attn_op", dense="m6_dense_op", name="hip"):
+                 attn="m6_llama_attn_op", dense="m6_dense_op", name="hip", moe="draco_moe_ffn_op"):
         self.cdll = cdll
         self.name = name
         self.forward_token = getattr(cdll, forward)
@@ -63,6 +73,7 @@ class EngineLib:
         self.head_op.restype = ct.c_int
         self.attn_ptr = ct.cast(getattr(cdll, attn), ct.c_void_p).value
         self.dense_ptr = ct.cast(getattr(cdll, dense), ct.c_void_p).value
+        self.moe_ptr = ct.cast(getattr(cdll, moe), ct.c_void_p).value if moe and hasattr(cdll, moe) else None
 
 
 def hip_engine_lib():
@@ -110,6 +121,9 @@ class LlamaDriver:
             self.tl.append(tl)
             self.descs[il].attn = engine.attn_ptr
             self.descs[il].attn_p = ct.cast(ct.pointer(a), ct.c_void_p)
+            if cfg.moe:
+                self._moe_layer(il, p, T, engine)
+                continue
             d = M6DenseP()
             for fld, cfld, tname in (("g", "cg", "ffn_gate"), ("u", "cu", "ffn_up"), ("d", "cd", "ffn_down")):
                 buf, code = T[p + tname + ".weight"][:2]
@@ -128,6 +142,31 @@ class LlamaDriver:
         self.x = np.zeros(self.H, np.float32)
         self.logits = np.zeros(cfg.vocab, np.float32)
         self.hrms = np.zeros(self.H, np.float32)
+
+    def _moe_layer(self, il, p, T, engine):
+        """The MoE FFN of layer il as the descriptor's ffn op: the expert
+        table as src/qwen35_engine.py:262-275 builds it (3 host pointers and
+        codes per expert into the 3-D expert tensors), the fp32 router."""
+        if engine.moe_ptr is None:
+            raise RuntimeError(f"engine {engine.name} has no MoE FFN op")
+        cfg = self.cfg
+        E, F = cfg.n_exp, cfg.exp_ff
+        ptrs = np.zeros(3 * E, np.uint64)
+        codes = np.zeros(3 * E, np.int32)
+        for k, tname in enumerate(("ffn_gate_exps", "ffn_up_exps", "ffn_down_exps")):
+            buf, code = T[p + tname + ".weight"][:2]
+            per = buf.nbytes // E
+            ptrs[k::3] = buf.ctypes.data + per * np.arange(E, dtype=np.uint64)
+            codes[k::3] = code
+        gi = T[p + "ffn_gate_inp.weight"][0].view(np.float32)
+        scratch = np.zeros(3 * cfg.n_used * F + cfg.n_used * self.H + 64, np.float32)
+        mp = DracoMoeP()
+        mp.ptrs, mp.codes, mp.gate_inp = ptrs.ctypes.data, codes.ctypes.data, pf(gi)
+        mp.n_exp, mp.n_used, mp.inter, mp.n_in, mp.n_out = E, cfg.n_used, F, self.H, self.H
+        mp.scratch = pf(scratch)
+        self.keep += [ptrs, codes, gi, scratch, mp]
+        self.descs[il].ffn = engine.moe_ptr
+        self.descs[il].ffn_p = ct.cast(ct.pointer(mp), ct.c_void_p)
 
     def reset(self):
         """src/draco_engine_server.py:125-132: zero the state arrays and tlen."""

@@ -43,10 +43,20 @@ class LlamaConfig:
     max_t: int = 1024
     chunk: int = 256
     wscale: float = 0.02
+    # MoE FFN (n_exp > 0): softmax router over n_exp experts, top n_used,
+    # experts of exp_ff SwiGLU rows (m6_granite_moe semantics) instead of the
+    # dense gate/up/down
+    n_exp: int = 0
+    n_used: int = 0
+    exp_ff: int = 0
 
     @property
     def rot(self):
         return self.head_dim
+
+    @property
+    def moe(self):
+        return self.n_exp > 0
 
 
 # configs[0] of BASELINE.json: SmolLM2-360M shape, all Q8_0, tied head.
@@ -84,7 +94,25 @@ ATTN_CFG3 = LlamaConfig(
     codes=dict(q=Q6_K, k=Q6_K, v=Q6_K, o=Q6_K, gate=Q4_K, up=Q4_K, down=Q4_K, emb=Q6_K, out=Q6_K),
     tied=True, n_prompt=8, n_gen=8, max_t=512)
 
-CONFIGS = {c.name: c for c in (SMOL360M, LLAMA1B, TINY_K, TINY_Q8, ATTN_CFG3)}
+# configs[3] of BASELINE.json: Qwen3-30B-A3B-shaped MoE stack -- 48 layers of
+# attention (32 q / 4 kv heads of 128, Q6_K) + MoE FFN (128 experts, top 8,
+# expert FFN 768, Q4_K experts, fp32 router N(0, 0.02)), hidden 2048, decode
+# at context 512.  The configuration names no vocabulary; Qwen3's 151936 with
+# an untied Q6_K head (Q4_K embedding) gives the greedy loop its tokens.
+QWEN3_MOE = LlamaConfig(
+    name="qwen3-30b-a3b-moe-stack", hidden=2048, n_layer=48, n_head=32, n_kv=4, head_dim=128, n_ff=0,
+    vocab=151936, eps=1e-6, rope_base=1000000.0,
+    codes=dict(q=Q6_K, k=Q6_K, v=Q6_K, o=Q6_K, gate=Q4_K, up=Q4_K, down=Q4_K, emb=Q4_K, out=Q6_K),
+    tied=False, n_prompt=448, n_gen=64, max_t=512, n_exp=128, n_used=8, exp_ff=768)
+
+# the same layer shape in two layers with a small vocabulary: MoE parity cases
+MOE_TINY = LlamaConfig(
+    name="moe-tiny", hidden=2048, n_layer=2, n_head=32, n_kv=4, head_dim=128, n_ff=0, vocab=1024, eps=1e-6,
+    rope_base=1000000.0,
+    codes=dict(q=Q6_K, k=Q6_K, v=Q6_K, o=Q6_K, gate=Q4_K, up=Q4_K, down=Q4_K, emb=Q4_K, out=Q6_K),
+    tied=False, n_prompt=8, n_gen=16, max_t=64, n_exp=128, n_used=8, exp_ff=768)
+
+CONFIGS = {c.name: c for c in (SMOL360M, LLAMA1B, TINY_K, TINY_Q8, ATTN_CFG3, QWEN3_MOE, MOE_TINY)}
 
 
 @dataclass
@@ -130,6 +158,24 @@ def _tensor(rng, code, n_out, n_in, wscale=0.02, rows_per_chunk=16384):
     return out
 
 
+def _random_q4k(rng, n_rows, n_in, wscale):
+    """Random Q4_K rows without drawing floats: every byte of each 144-byte
+    super-block uniform (nibbles q, 6-bit scales sc and mins m), then d and
+    dmin set so that w = d*sc*q - dmin*m has mean ~0 (dmin = 7.5 d) and
+    standard deviation ~wscale (about 255 d for uniform q, sc, m).  Used for
+    MoE experts, whose N(0, wscale) draws would take minutes at the configs[3]
+    size (29 G values); the kernels' work and bytes do not depend on the
+    values, and GPU and CPU consume the same bytes."""
+    nblk = n_rows * (n_in // 256)
+    words = rng.bit_generator.random_raw((nblk * 144 + 7) // 8)  # uniform 64-bit words of the generator
+    blk = words.view(np.uint8)[:nblk * 144].reshape(nblk, 144)
+    d = np.float16(wscale / 255.0)
+    dmin = np.float16(7.5 * float(d))
+    blk[:, 0:2] = np.frombuffer(d.tobytes(), np.uint8)
+    blk[:, 2:4] = np.frombuffer(dmin.tobytes(), np.uint8)
+    return blk.reshape(-1)
+
+
 def build_llama(cfg, seed=0):
     rng = np.random.default_rng(seed)
     m = LlamaModel(cfg=cfg, seed=seed)
@@ -137,13 +183,27 @@ def build_llama(cfg, seed=0):
     c = cfg.codes
     ws = cfg.wscale
     m.tensors["token_embd.weight"] = (_tensor(rng, c["emb"], cfg.vocab, H, ws), c["emb"], cfg.vocab, H)
+    names = {"q": "attn_q", "k": "attn_k", "v": "attn_v", "o": "attn_output",
+             "gate": "ffn_gate", "up": "ffn_up", "down": "ffn_down"}
     for il in range(cfg.n_layer):
         p = f"blk.{il}."
-        for kind, n_out, n_in in (("q", QD, H), ("k", KD, H), ("v", KD, H), ("o", H, QD),
-                                  ("gate", cfg.n_ff, H), ("up", cfg.n_ff, H), ("down", H, cfg.n_ff)):
-            tname = {"q": "attn_q", "k": "attn_k", "v": "attn_v", "o": "attn_output",
-                     "gate": "ffn_gate", "up": "ffn_up", "down": "ffn_down"}[kind]
-            m.tensors[p + tname + ".weight"] = (_tensor(rng, c[kind], n_out, n_in, ws), c[kind], n_out, n_in)
+        for kind, n_out, n_in in (("q", QD, H), ("k", KD, H), ("v", KD, H), ("o", H, QD)):
+            m.tensors[p + names[kind] + ".weight"] = (_tensor(rng, c[kind], n_out, n_in, ws), c[kind], n_out, n_in)
+        if cfg.moe:
+            # router fp32 [n_exp][H] N(0, wscale); experts as random Q4_K blocks,
+            # each 3-D tensor [n_exp][rows][cols] stored as n_exp * rows rows
+            E, F = cfg.n_exp, cfg.exp_ff
+            gi = _draw(rng, E, H, ws)
+            m.tensors[p + "ffn_gate_inp.weight"] = (gi.view(np.uint8).reshape(-1), F32, E, H)
+            for kind, rows, n_in in (("gate", F, H), ("up", F, H), ("down", H, F)):
+                if c[kind] != Q4_K:
+                    raise ValueError("MoE experts are generated as Q4_K")
+                m.tensors[p + names[kind] + "_exps.weight"] = (_random_q4k(rng, E * rows, n_in, ws), c[kind],
+                                                               E * rows, n_in)
+        else:
+            for kind, n_out, n_in in (("gate", cfg.n_ff, H), ("up", cfg.n_ff, H), ("down", H, cfg.n_ff)):
+                m.tensors[p + names[kind] + ".weight"] = (_tensor(rng, c[kind], n_out, n_in, ws), c[kind], n_out,
+                                                          n_in)
         m.norms[p + "attn_norm.weight"] = np.ones(H, np.float32)
         m.norms[p + "ffn_norm.weight"] = np.ones(H, np.float32)
     if not cfg.tied:

@@ -538,6 +538,24 @@ void or_granite_moe(const float* x0, const uint64_t* ptrs, const int* codes,
     }
 }
 
+/* The MoE FFN as an m6 ffn op (OrLayerDesc.ffn): m6_granite_moe's arguments
+ * packed in one struct (the product's DracoMoeP, field for field), as the
+ * reference's qwen35 driver passes them per layer (src/qwen35_engine.py:
+ * 293-307, the MoE half of _ffn).  scratch >= 3*n_used*inter + n_used*n_out. */
+typedef struct {
+    const uint64_t* ptrs;
+    const int* codes;
+    const float* gate_inp;
+    int n_exp, n_used, inter, n_in, n_out;
+    float* scratch;
+} OrMoeP;
+
+void or_moe_ffn_op(const float* xn, void* pv, float* out) {
+    const OrMoeP* p = (const OrMoeP*)pv;
+    or_granite_moe(xn, p->ptrs, p->codes, p->gate_inp, p->n_exp, p->n_used, p->inter, p->n_in, p->n_out,
+                   p->scratch, out);
+}
+
 /* gemv_any's inline F32 branch, src/m6_layer.c:148-174: four 16-lane fma
  * accumulators over 64-value steps (a 16-value tail into the first), the
  * lane sums (a0+a1)+(a2+a3), GCC's _mm512_reduce_add_ps tree, then the

@@ -45,6 +45,7 @@ _SIGS = {
     "or_argmax": (ct.c_int, [f32p, ct.c_int]),
     "or_llama_attn_op": (None, [f32p, ct.c_void_p, ct.c_int, f32p]),
     "or_dense_op": (None, [f32p, ct.c_void_p, f32p]),
+    "or_moe_ffn_op": (None, [f32p, ct.c_void_p, f32p]),
     "or_topk": (None, [f32p, ct.c_int, ct.c_int, i32p]),
     "or_moe_route": (None, [f32p, f32p, ct.c_int, ct.c_int, ct.c_int, f32p, i32p, f32p]),
     "or_granite_moe": (None, [f32p, ct.c_void_p, i32p, f32p, ct.c_int, ct.c_int, ct.c_int, ct.c_int,
@@ -82,6 +83,7 @@ class Oracle:
         # op function pointers usable inside descriptor arrays
         self.attn_op = ct.cast(self.lib.or_llama_attn_op, ct.c_void_p).value
         self.dense_op = ct.cast(self.lib.or_dense_op, ct.c_void_p).value
+        self.moe_op = ct.cast(self.lib.or_moe_ffn_op, ct.c_void_p).value
 
     def gemv(self, code, x, W, n_out, n_in):
         y = np.zeros(n_out, np.float32)

@@ -158,10 +158,34 @@ def ref_engine():
     return E
 
 
+_MOE_CALLBACKS = []  # keep the ctypes callbacks alive
+
+
+def ref_engine_lib(E):
+    """The compiled reference engine as an EngineLib.  Its MoE layers run the
+    reference's own m6_granite_moe (src/m6_layer.c:771-802) through an ffn-op
+    callback, as src/qwen35_engine.py:293-307 calls it per layer."""
+    from dracohip.driver import DracoMoeP
+    E.m6_granite_moe.argtypes = [f32p, ct.c_void_p, ct.c_void_p, f32p, ct.c_int, ct.c_int, ct.c_int, ct.c_int,
+                                 ct.c_int, f32p, f32p]
+    E.m6_granite_moe.restype = None
+
+    @ct.CFUNCTYPE(None, f32p, ct.c_void_p, f32p)
+    def moe_op(xn, pv, out):
+        p = ct.cast(pv, ct.POINTER(DracoMoeP)).contents
+        E.m6_granite_moe(xn, p.ptrs, p.codes, p.gate_inp, p.n_exp, p.n_used, p.inter, p.n_in, p.n_out, p.scratch,
+                         out)
+
+    _MOE_CALLBACKS.append(moe_op)
+    lib = EngineLib(E, name="ref", moe=None)
+    lib.moe_ptr = ct.cast(moe_op, ct.c_void_p).value
+    return lib
+
+
 def gen_llama(cfg, fname, seed=0, logit_steps=(0,)):
     t0 = time.time()
     model = models.build_llama(cfg, seed)
-    E = EngineLib(ref_engine(), name="ref")
+    E = ref_engine_lib(ref_engine())
     drv = LlamaDriver(model, E)
     prompt = model.prompt()
     toks, hidden, lg = drv.greedy(prompt, cfg.n_gen, collect_logits=logit_steps)
@@ -463,6 +487,7 @@ JOBS = {
     "tiny_q8": lambda: gen_llama(models.TINY_Q8, "llama_tiny_q8.npz", logit_steps=(0, 15)),
     "smol360m": lambda: gen_llama(models.SMOL360M, "smol360m.npz", logit_steps=(0, 63)),
     "llama1b": lambda: gen_llama(models.LLAMA1B, "llama1b.npz", logit_steps=(0, 63)),
+    "moe_tiny": lambda: gen_llama(models.MOE_TINY, "moe_tiny.npz", logit_steps=(0, 15)),
 }
 
 if __name__ == "__main__":

@@ -220,6 +220,34 @@ def test_attn_op_grouped_head_dim_128_match_oracle(oracle, nh, nkv):
     print(f"[attn_op] grouped hd 128 nh {nh} nkv {nkv}: worst {worst:.2e}")
 
 
+def test_moe_stack_dropin_per_token():
+    """configs[3]'s layer in two layers (attention 32 q / 4 kv x 128 Q6_K, MoE
+    FFN of 128 experts, top 8, FFN 768) driven per token through
+    m6_forward_token (the MoE FFN as the descriptors' ffn op) and m6_head_op,
+    against the compiled reference engine running its own m6_granite_moe."""
+    g = golden("moe_tiny.npz")
+    cfg, model, drv = _driver("moe-tiny")
+    assert model.digest() == g["digest"].tobytes().hex()
+    print("[decode] moe stack drop-in", flush=True)
+    toks, hidden, lg = drv.greedy(model.prompt(), cfg.n_gen, collect_logits=(0, 15))
+    assert toks == list(g["tokens"])
+    assert np.max(np.abs(hidden - g["hidden"])) <= hid_tol(g["hidden"])
+    assert rel_err(lg[0], g["logits0"]) <= 1e-5
+    assert rel_err(lg[15], g["logits15"]) <= 1e-4
+
+
+@pytest.mark.parametrize("use_graph", [False, True])
+def test_moe_stack_device_generate(use_graph):
+    """The same model through the device-resident loop (prompt token by token,
+    greedy decode, graph-replayed or eager)."""
+    g = golden("moe_tiny.npz")
+    cfg, model, drv = _driver("moe-tiny")
+    print(f"[decode] moe stack device generate graph={use_graph}", flush=True)
+    toks, hidden, _ = drv.generate_device(model.prompt(), cfg.n_gen, use_graph=use_graph)
+    assert toks == list(g["tokens"])
+    assert np.max(np.abs(hidden - g["hidden"])) <= hid_tol(g["hidden"])
+
+
 def test_smol360m_device_generate():
     """SmolLM2-360M-shaped Q8_0, 32 prompt + 64 greedy tokens."""
     g = golden("smol360m.npz")

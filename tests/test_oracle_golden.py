@@ -230,3 +230,19 @@ def test_llama_attn_configs3_shape(oracle):
     assert bits_equal(outs, g["out"])
     assert bits_equal(drv.kc[0][gg.ATTN_CFG3_T0 * kd:n], g["knew"])
     assert bits_equal(drv.vc[0][gg.ATTN_CFG3_T0 * kd:n], g["vnew"])
+
+
+def test_moe_stack_decode_tiny(oracle):
+    """configs[3]'s layer (attention 32 q / 4 kv x 128 Q6_K + MoE FFN: 128
+    experts, top 8, FFN 768) in two layers: token-serial prompt + greedy
+    decode through the descriptor ABI with the MoE FFN as the layer's ffn op,
+    bitwise to the compiled reference engine running its own m6_granite_moe."""
+    g = golden("moe_tiny.npz")
+    cfg = models.MOE_TINY
+    model = models.build_llama(cfg, 0)
+    assert model.digest() == g["digest"].tobytes().hex()
+    drv = LlamaDriver(model, oracle_engine(oracle))
+    toks, hidden, lg = drv.greedy(model.prompt(), cfg.n_gen, collect_logits=(0, 15))
+    assert toks == list(g["tokens"])
+    assert bits_equal(hidden, g["hidden"])
+    assert bits_equal(lg[0], g["logits0"]) and bits_equal(lg[15], g["logits15"])
