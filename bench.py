@@ -212,6 +212,55 @@ def qwen35_ops_configs4(lib, told=4096, iters=50):
     return res
 
 
+def moe_stack_configs3(lib, seed=3):
+    """the 48-layer Qwen3-30B-A3B-shaped MoE stack (attention 32 q /
+    4 kv heads of 128, Q6_K; MoE FFN 128 experts, top 8, FFN 768, Q4_K experts,
+    fp32 router) decoding at context 512: a 448-token prompt fed token by token
+    through the graph-replayed decode step, then 64 greedy tokens (positions
+    448..511) timed with HIP events.  Bytes per token = attention weights +
+    the 8 routed experts' three matrices + the router, per layer, + the K/V rows
+    read (mean over the decode positions) + the head and one embedding row."""
+    import ctypes as ct
+    from dracohip import models
+    from dracohip.driver import LlamaDriver, hip_engine_lib
+    cfg = models.QWEN3_MOE
+    t0 = time.time()
+    model = models.build_llama(cfg, seed)
+    log(f"configs[3] model built in {time.time() - t0:.1f}s ({model.nbytes() / 1e9:.2f} GB)")
+    L = lib.load()
+    drv = LlamaDriver(model, hip_engine_lib())
+    t0 = time.time()
+    toks, _, (dec_ms, pre_ms) = drv.generate_device(model.prompt(), cfg.n_gen, use_graph=True)
+    log(f"configs[3] first run (upload + prompt + decode) {time.time() - t0:.1f}s")
+    drv.reset()
+    L.draco_state_push(ct.cast(drv.descs, ct.c_void_p), drv.NL)
+    toks2, _, (dec_ms, pre_ms) = drv.generate_device(model.prompt(), cfg.n_gen, use_graph=True)
+    T = model.tensors
+    H, E, F, KD = cfg.hidden, cfg.n_exp, cfg.exp_ff, cfg.n_kv * cfg.head_dim
+    attn = sum(T[f"blk.0.{n}.weight"][0].nbytes for n in ("attn_q", "attn_k", "attn_v", "attn_output"))
+    experts = sum(T[f"blk.0.{n}.weight"][0].nbytes // E for n in ("ffn_gate_exps", "ffn_up_exps", "ffn_down_exps"))
+    router = E * H * 4
+    # decode step i runs at tlen n_prompt - 1 + i and reads that many rows + its own
+    rows = np.arange(cfg.n_prompt - 1, cfg.n_prompt - 1 + cfg.n_gen) + 1
+    kv = 2 * KD * 4 * float(rows.mean())
+    head = model.head()[0].nbytes
+    emb_row = T["token_embd.weight"][0].nbytes // cfg.vocab
+    per_tok = cfg.n_layer * (attn + cfg.n_used * experts + router + kv) + head + emb_row
+    stack = cfg.n_layer * (attn + cfg.n_used * experts + router + kv)
+    tok_s = cfg.n_gen / (dec_ms / 1e3)
+    res = {"tok_s": round(tok_s, 1), "ms_per_token": round(dec_ms / cfg.n_gen, 4),
+           "bytes_per_token": int(per_tok), "GB_s": round(per_tok * tok_s / 1e9, 1),
+           "frac_of_peak": round(per_tok * tok_s / 1e9 / PEAK_HBM_GBS, 4),
+           "stack_bytes_per_token_no_head": int(stack), "roof_tok_s": round(PEAK_HBM_GBS * 1e9 / per_tok, 1),
+           "prompt_tokens": cfg.n_prompt, "prompt_ms_token_serial": round(pre_ms, 1),
+           "greedy_tokens_repeat": toks == toks2,
+           "shape": "48 layers: attention 32q/4kv x 128 Q6_K + MoE 128 experts top-8 FFN 768 Q4_K, fp32 router; "
+                    "hidden 2048, vocab 151936 (untied Q6_K head), decode at positions 448..511"}
+    del drv, model
+    L.draco_reset()
+    return res
+
+
 PEAK_F16_TFLOPS = 2500.0  # MI355X dense f16 MFMA
 
 
@@ -322,6 +371,7 @@ def main():
                     help="run the decode loop without HIP graphs (for profilers that cannot trace graphs)")
     ap.add_argument("--roofline-only", action="store_true", help="only the Q4_K GEMV roofline measurement")
     ap.add_argument("--no-roofline", action="store_true", help="skip the GEMV roofline measurement (profiling runs)")
+    ap.add_argument("--no-stacks", action="store_true", help="skip the configs[3] / configs[4] layer stacks")
     ap.add_argument("--cpu-baseline-worker", action="store_true")
     ap.add_argument("--kv-file")
     args = ap.parse_args()
@@ -437,6 +487,12 @@ def main():
         if cpu:
             log(f"cpu baseline {cpu['value']} tok/s on {threads} threads")
 
+    moe_stack = None
+    if not args.no_stacks:
+        moe_stack = moe_stack_configs3(lib)
+        log(f"configs[3] MoE stack: {moe_stack['tok_s']} tok/s, {moe_stack['GB_s']} GB/s "
+            f"({moe_stack['frac_of_peak']} of peak)")
+
     line = {
         "metric": "decode tok/s bs1 @ctx1024; Q4_K GEMV achieved HBM GB/s as % of peak",
         "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
@@ -455,6 +511,7 @@ def main():
         "configs4_gdn_scan": gdn,
         "configs4_layer_ops": qw,
         "configs2_prefill_gemm": pre,
+        "configs3_moe_stack": moe_stack,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
