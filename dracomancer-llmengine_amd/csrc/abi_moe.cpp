@@ -417,6 +417,11 @@ int draco_moe_layer_enqueue(MoeLayer* m, const float* x, const float* norm_w, fl
     return enqueue_moe(m->set, m->xn, out, resid, m->w, p.n_exp, p.n_used, p.inter, p.n_in, p.n_out, st);
 }
 
+int draco_moe_layer_enqueue_xn(MoeLayer* m, const float* xn, float* out, const float* resid, hipStream_t st) {
+    const DracoMoeP& p = m->snap;
+    return enqueue_moe(m->set, xn, out, resid, m->w, p.n_exp, p.n_used, p.inter, p.n_in, p.n_out, st);
+}
+
 extern "C" {
 
 // The MoE FFN as an m6 ffn op (no reference counterpart as an op: the

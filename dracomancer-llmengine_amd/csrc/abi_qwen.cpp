@@ -25,11 +25,16 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <algorithm>
+#include <map>
 #include <vector>
 
 #include "decode.h"
 #include "gdn.h"
+#include "gemm.h"
 #include "gemv.h"
+#include "moe.h"
+#include "prefill.h"
 #include "runtime.h"
 
 using namespace draco;
@@ -72,6 +77,12 @@ typedef struct {
     const float* rope_inv;
     int nh;
 } FullW;
+
+// the dense FFN op's parameters (src/m6_engine.c:270-273), as in abi_m6.cpp
+typedef struct {
+    const uint8_t *g, *u, *d;
+    int cg, cu, cd, n_ff, h;
+} M6DenseP;
 
 namespace {
 
@@ -410,6 +421,407 @@ int time_graph(int iters, F enq, float* us) {
     return 0;
 }
 
+// ================================================ the hybrid stack ======
+// One qwen35 token as the reference's driver composes it per layer
+// (src/qwen35_engine.py:310-327): the layer op (m6_gdn_attn or m6_full_attn)
+// leaves x2_out = x + attn and x2n = RMSNorm(x2_out) * post_norm; the FFN of
+// x2n (none, dense m6_dense_op, or MoE m6_granite_moe) is added to x2_out.
+// Here every layer's state lives on the device: the recurrent state and
+// conv tail of a GDN layer, the K / V rows of a full-attention layer (device
+// mirrors of the caller's arrays, keyed by their host addresses; the state
+// hooks move them), so a token moves no state over PCIe.
+
+constexpr int QFFN_NONE = 0, QFFN_DENSE = 1, QFFN_MOE = 2;
+constexpr int QCHUNK_MAX = 256;
+
+struct QStackLayer {
+    int kind = 0;
+    const void* w = nullptr;
+    float* state0 = nullptr;  // host: GDN ssm / full Kr
+    float* state1 = nullptr;  // host: GDN tail / full Vc
+    int max_t = 0;
+    int ffn_kind = 0;
+    const void* ffn = nullptr;
+};
+
+struct QLayer {
+    QStackLayer desc;
+    GdnW gw = {};
+    FullW fw = {};
+    M6DenseP dp = {};
+    DracoMoeP mp = {};
+    GdnDev g = {};
+    FullDev f = {};
+    float *S = nullptr, *tail = nullptr;  // GDN device state
+    float *kc = nullptr, *vc = nullptr;   // full-attention device cache rows
+    const float* cs = nullptr;            // full attention: rope cos / sin table [max_t][64]
+    const DracoMat *fg = nullptr, *fu = nullptr, *fd = nullptr;  // dense FFN
+    int FF = 0;
+    MoeLayer* moe = nullptr;
+};
+
+struct QStack {
+    uint64_t epoch = 0;
+    std::vector<QStackLayer> descs;
+    std::vector<QLayer> L;
+    int n_layer = 0, max_qkv = 0, max_din = 0, max_nh = 0, max_t = 0, max_ff = 0, max_vh = 0;
+    // one token
+    float *x = nullptr, *x2n = nullptr, *xn = nullptr, *qkv = nullptr, *z = nullptr, *on = nullptr, *QG = nullptr,
+          *Qr = nullptr, *kraw = nullptr, *vraw = nullptr, *ao = nullptr, *part = nullptr, *fg = nullptr,
+          *fu = nullptr, *xe = nullptr;
+    int* state = nullptr;   // device [pos, told]
+    int* hstate = nullptr;  // pinned
+    // a prefill chunk of up to pf_cap tokens
+    int pf_cap = 0;
+    float *X = nullptr, *Xn = nullptr, *QKV = nullptr, *Z = nullptr, *B = nullptr, *G = nullptr, *ON = nullptr,
+          *Y = nullptr, *PQG = nullptr, *PQr = nullptr, *PK = nullptr, *PV = nullptr, *AO = nullptr, *Ppart = nullptr,
+          *PG = nullptr, *PU = nullptr;
+    uint8_t* dig = nullptr;
+    int* ids = nullptr;
+    std::vector<void*> allocs, pf_allocs;
+};
+
+std::map<const void*, QStack*>& qstacks() {
+    static auto* m = new std::map<const void*, QStack*>();
+    return *m;
+}
+
+// rope cos / sin of positions [0, rows) for one rope_inv table, computed as
+// the reference does per token ((float)pos * rope_inv[t], cosf / sinf,
+// src/m6_layer.c:434-440); device copy cached per (host table, rows)
+const float* rope_rows(const float* rope_inv, int rows) {
+    struct Tab {
+        float* dev = nullptr;
+        int rows = 0;
+        std::vector<float> inv;
+    };
+    static auto* tabs = new std::map<const float*, Tab>();
+    Tab& t = (*tabs)[rope_inv];
+    const bool same = t.inv.size() == 32 && memcmp(t.inv.data(), rope_inv, sizeof(float) * 32) == 0;
+    if (t.dev && same && t.rows >= rows) return t.dev;
+    std::vector<float> h((size_t)rows * 64);
+    for (int p = 0; p < rows; p++) rope_cs(rope_inv, p, h.data() + (size_t)p * 64);
+    if (t.dev) {
+        hipStreamSynchronize(stream());
+        hipFree(t.dev);
+        t.dev = nullptr;
+    }
+    if (hipMalloc(&t.dev, sizeof(float) * h.size()) != hipSuccess ||
+        hipMemcpy(t.dev, h.data(), sizeof(float) * h.size(), hipMemcpyHostToDevice) != hipSuccess) {
+        fail(-2, "qwen stack: rope table upload failed");
+        t = Tab();
+        return nullptr;
+    }
+    t.rows = rows;
+    t.inv.assign(rope_inv, rope_inv + 32);
+    return t.dev;
+}
+
+// device state of one layer: a mirror of the caller's array, uploaded when
+// the mirror is new (the caller's array holds the state to start from)
+float* state_mirror(float* host, size_t floats) {
+    bool fresh = false;
+    float* d = (float*)get_mirror(host, sizeof(float) * floats, &fresh);
+    if (d && fresh && hipMemcpy(d, host, sizeof(float) * floats, hipMemcpyHostToDevice) != hipSuccess) {
+        fail(-2, "qwen stack: state upload failed");
+        return nullptr;
+    }
+    return d;
+}
+
+size_t gdn_state_floats(const GdnDev& g) { return (size_t)g.n_vh * QSV * QSV; }
+size_t gdn_tail_floats(const GdnDev& g) { return (size_t)g.n_qkv * 3; }
+size_t full_cache_floats(int max_t) { return (size_t)max_t * FNKV * FHD; }
+
+int qstack_alloc(std::vector<void*>& keep, float** p, size_t floats) {
+    if (hipMalloc(p, sizeof(float) * (floats + 64)) != hipSuccess) return fail(-2, "qwen stack: allocation failed");
+    keep.push_back(*p);
+    return 0;
+}
+
+QStack* build_qstack(const QStackLayer* layers, int n_layer, int h) {
+    if (h != QH) {
+        fail(-1, "qwen stack: hidden %d (the qwen35 ops fix it at %d)", h, QH);
+        return nullptr;
+    }
+    if (n_layer < 1) {
+        fail(-1, "qwen stack: no layers");
+        return nullptr;
+    }
+    QStack*& slot = qstacks()[layers];
+    if (slot && slot->epoch == epoch() && slot->n_layer == n_layer &&
+        memcmp(slot->descs.data(), layers, sizeof(QStackLayer) * n_layer) == 0) {
+        bool same = true;
+        for (int l = 0; same && l < n_layer; l++) {
+            const QLayer& q = slot->L[l];
+            same = q.desc.kind == 0 ? memcmp(&q.gw, q.desc.w, sizeof(GdnW)) == 0
+                                    : memcmp(&q.fw, q.desc.w, sizeof(FullW)) == 0;
+            if (same && q.desc.ffn_kind == QFFN_DENSE) same = memcmp(&q.dp, q.desc.ffn, sizeof(M6DenseP)) == 0;
+            if (same && q.desc.ffn_kind == QFFN_MOE)
+                same = memcmp(&q.mp, q.desc.ffn, sizeof(DracoMoeP)) == 0 &&
+                       draco_moe_layer((const DracoMoeP*)q.desc.ffn) == q.moe;
+        }
+        if (same && slot->epoch == epoch()) return slot;
+    }
+    if (slot) {  // rebuild: release the old token buffers (mirrors stay registered)
+        hipStreamSynchronize(stream());
+        for (void* p : slot->allocs) hipFree(p);
+        for (void* p : slot->pf_allocs) hipFree(p);
+        delete slot;
+        slot = nullptr;
+    }
+    QStack* s = new QStack();
+    s->descs.assign(layers, layers + n_layer);
+    s->L.resize(n_layer);
+    s->n_layer = n_layer;
+    for (int l = 0; l < n_layer; l++) {
+        QLayer& q = s->L[l];
+        q.desc = layers[l];
+        if (q.desc.kind == 0) {
+            q.gw = *(const GdnW*)q.desc.w;
+            if (gdn_resolve(&q.gw, q.g)) return nullptr;
+            q.S = state_mirror(q.desc.state0, gdn_state_floats(q.g));
+            q.tail = state_mirror(q.desc.state1, gdn_tail_floats(q.g));
+            if (!q.S || !q.tail) return nullptr;
+            s->max_qkv = std::max(s->max_qkv, q.g.n_qkv);
+            s->max_din = std::max(s->max_din, q.g.d_in);
+            s->max_vh = std::max(s->max_vh, q.g.n_vh);
+        } else if (q.desc.kind == 1) {
+            q.fw = *(const FullW*)q.desc.w;
+            if (full_resolve(&q.fw, q.f)) return nullptr;
+            if (q.desc.max_t < 1) {
+                fail(-1, "qwen stack: layer %d: full attention needs max_t >= 1", l);
+                return nullptr;
+            }
+            q.kc = state_mirror(q.desc.state0, full_cache_floats(q.desc.max_t));
+            q.vc = state_mirror(q.desc.state1, full_cache_floats(q.desc.max_t));
+            q.cs = rope_rows(q.fw.rope_inv, q.desc.max_t);
+            if (!q.kc || !q.vc || !q.cs) return nullptr;
+            s->max_nh = std::max(s->max_nh, q.f.nh);
+            s->max_t = std::max(s->max_t, q.desc.max_t);
+        } else {
+            fail(-1, "qwen stack: layer %d kind %d (0 GDN, 1 full attention)", l, q.desc.kind);
+            return nullptr;
+        }
+        if (q.desc.ffn_kind == QFFN_DENSE) {
+            q.dp = *(const M6DenseP*)q.desc.ffn;
+            if (q.dp.h != QH) {
+                fail(-1, "qwen stack: layer %d dense FFN width %d", l, q.dp.h);
+                return nullptr;
+            }
+            q.FF = q.dp.n_ff;
+            q.fg = get_mat(q.dp.g, q.dp.cg, q.FF, QH);
+            q.fu = get_mat(q.dp.u, q.dp.cu, q.FF, QH);
+            q.fd = get_mat(q.dp.d, q.dp.cd, QH, q.FF);
+            if (!q.fg || !q.fu || !q.fd) return nullptr;
+            s->max_ff = std::max(s->max_ff, q.FF);
+        } else if (q.desc.ffn_kind == QFFN_MOE) {
+            q.mp = *(const DracoMoeP*)q.desc.ffn;
+            if (q.mp.n_in != QH || q.mp.n_out != QH) {
+                fail(-1, "qwen stack: layer %d MoE width %d/%d", l, q.mp.n_in, q.mp.n_out);
+                return nullptr;
+            }
+            q.moe = draco_moe_layer((const DracoMoeP*)q.desc.ffn);
+            if (!q.moe) return nullptr;
+        } else if (q.desc.ffn_kind != QFFN_NONE) {
+            fail(-1, "qwen stack: layer %d FFN kind %d (0 none, 1 dense, 2 MoE)", l, q.desc.ffn_kind);
+            return nullptr;
+        }
+    }
+    const int nsplit = s->max_nh ? attn_nsplit(s->max_t, s->max_nh, FNKV, FHD) : 1;
+    auto& k = s->allocs;
+    if (qstack_alloc(k, &s->x, QH) || qstack_alloc(k, &s->x2n, QH) || qstack_alloc(k, &s->xn, QH) ||
+        qstack_alloc(k, &s->xe, QH) || qstack_alloc(k, &s->qkv, std::max(s->max_qkv, 1)) ||
+        qstack_alloc(k, &s->z, std::max(s->max_din, 1)) || qstack_alloc(k, &s->on, std::max(s->max_din, 1)) ||
+        qstack_alloc(k, &s->QG, (size_t)std::max(s->max_nh, 1) * 2 * FHD) ||
+        qstack_alloc(k, &s->Qr, (size_t)std::max(s->max_nh, 1) * FHD) ||
+        qstack_alloc(k, &s->ao, (size_t)std::max(s->max_nh, 1) * FHD) || qstack_alloc(k, &s->kraw, FNKV * FHD) ||
+        qstack_alloc(k, &s->vraw, FNKV * FHD) ||
+        qstack_alloc(k, &s->part, (size_t)std::max(s->max_nh, 1) * nsplit * (FHD + 2)) ||
+        qstack_alloc(k, &s->fg, std::max(s->max_ff, 1)) || qstack_alloc(k, &s->fu, std::max(s->max_ff, 1)))
+        return nullptr;
+    if (hipMalloc(&s->state, sizeof(int) * 16) != hipSuccess ||
+        hipHostMalloc(&s->hstate, sizeof(int) * 16, hipHostMallocDefault) != hipSuccess) {
+        fail(-2, "qwen stack: state allocation failed");
+        return nullptr;
+    }
+    k.push_back(s->state);
+    s->epoch = epoch();
+    slot = s;
+    return s;
+}
+
+// prefill chunk buffers for up to cap tokens
+int qstack_pf(QStack* s, int cap) {
+    if (s->pf_cap >= cap) return 0;
+    hipStreamSynchronize(stream());
+    for (void* p : s->pf_allocs) hipFree(p);
+    s->pf_allocs.clear();
+    const size_t c = (size_t)cap;
+    const int nh = std::max(s->max_nh, 1);
+    auto& k = s->pf_allocs;
+    const int win = std::max(std::max(QH, std::max(s->max_din, nh * FHD)), s->max_ff);
+    const size_t nspl = pf_attn_nsplit(s->max_t, cap);
+    if (qstack_alloc(k, &s->X, c * QH) || qstack_alloc(k, &s->Xn, c * QH) ||
+        qstack_alloc(k, &s->QKV, c * std::max(s->max_qkv, 1)) || qstack_alloc(k, &s->Z, c * std::max(s->max_din, 1)) ||
+        qstack_alloc(k, &s->B, c * std::max(s->max_vh, 1)) || qstack_alloc(k, &s->G, c * std::max(s->max_vh, 1)) ||
+        qstack_alloc(k, &s->ON, c * std::max(s->max_din, 1)) || qstack_alloc(k, &s->Y, c * QH) ||
+        qstack_alloc(k, &s->PQG, c * nh * 2 * FHD) || qstack_alloc(k, &s->PQr, c * nh * FHD) ||
+        qstack_alloc(k, &s->PK, c * FNKV * FHD) || qstack_alloc(k, &s->PV, c * FNKV * FHD) ||
+        qstack_alloc(k, &s->AO, c * nh * FHD) || qstack_alloc(k, &s->Ppart, pf_part_floats(nh, cap, FHD, nspl)) ||
+        qstack_alloc(k, &s->PG, c * std::max(s->max_ff, 1)) || qstack_alloc(k, &s->PU, c * std::max(s->max_ff, 1)))
+        return -2;
+    if (hipMalloc(&s->dig, draco_gemm_digit_bytes(cap, ((win + 255) / 256) * 256)) != hipSuccess ||
+        hipMalloc(&s->ids, sizeof(int) * c) != hipSuccess)
+        return fail(-2, "qwen stack: prefill allocation failed");
+    k.push_back(s->dig);
+    k.push_back(s->ids);
+    s->pf_cap = cap;
+    return 0;
+}
+
+// the FFN of one token: x += FFN(x2n) (x holds x2_out)
+int enqueue_qffn(QStack* s, QLayer& q, hipStream_t st) {
+    if (q.desc.ffn_kind == QFFN_NONE) return 0;
+    if (q.desc.ffn_kind == QFFN_MOE) return draco_moe_layer_enqueue_xn(q.moe, s->x2n, s->x, s->x, st);
+    const Proj gu[2] = {{q.fg, s->fg, nullptr}, {q.fu, s->fu, nullptr}};
+    if (int rc = enqueue_proj(gu, 2, s->x2n, QH, nullptr, s->xn, st)) return rc;
+    dk_swiglu(s->fg, s->fu, q.FF, st);
+    const Proj dn[1] = {{q.fd, s->x, s->x}};
+    return enqueue_proj(dn, 1, s->fg, q.FF, nullptr, s->xn, st);
+}
+
+// one token through every layer: x (device) in place, or, with xin, layer 0
+// reads its input from xin and every layer leaves its output in x; position
+// and told from s->state ([pos, told], told = pos as the reference's driver
+// passes them)
+int enqueue_qtoken(QStack* s, hipStream_t st, float* xin = nullptr) {
+    for (int l = 0; l < s->n_layer; l++) {
+        QLayer& q = s->L[l];
+        float* x0 = (l == 0 && xin) ? xin : s->x;
+        if (q.desc.kind == 0) {
+            GdnBufs b = {};
+            b.h1 = x0;
+            b.qkv = s->qkv;
+            b.z = s->z;
+            b.on = s->on;
+            b.x2o = s->x;  // in place: the ssm_out projection adds its residual row by row
+            b.x2n = s->x2n;
+            b.xn = s->xn;
+            b.S = q.S;
+            b.tail = q.tail;
+            if (int rc = enqueue_gdn(q.g, b, st)) return rc;
+        } else {
+            const FullDev& f = q.f;
+            const Proj in[3] = {{f.q, s->QG, nullptr}, {f.k, s->kraw, nullptr}, {f.v, s->vraw, nullptr}};
+            if (int rc = enqueue_proj(in, 3, x0, QH, f.attn_norm, s->xn, st)) return rc;
+            dk_fa_prep_rows(s->QG, f.nh * 2 * FHD, s->Qr, s->kraw, s->vraw, q.kc, q.vc, f.q_norm, f.k_norm, q.cs,
+                            s->state, 0, 0, f.nh, 1, st);
+            if (dk_attention(s->Qr, q.kc, q.vc, s->part, nullptr, s->ao, s->state, 0, f.nh, FNKV, FHD, q.desc.max_t,
+                             1.f / sqrtf((float)FHD), st, s->QG + FHD, 2 * FHD))
+                return fail(-1, "qwen stack: attention launch rejected");
+            const Proj out[1] = {{f.o, s->x, x0}};
+            const PostNorm pn = {f.post_norm, s->x2n};
+            if (int rc = enqueue_proj(out, 1, s->ao, f.nh * FHD, nullptr, s->xn, st, &pn)) return rc;
+        }
+        if (int rc = enqueue_qffn(s, q, st)) return rc;
+    }
+    return 0;
+}
+
+int qstack_positions(QStack* s, int pos0, int n) {
+    if (pos0 < 0) return fail(-1, "qwen stack: negative position %d", pos0);
+    for (int l = 0; l < s->n_layer; l++)
+        if (s->L[l].desc.kind == 1 && pos0 + n > s->L[l].desc.max_t)
+            return fail(-1, "qwen stack: layer %d: position %d + %d tokens exceeds max_t %d", l, pos0, n,
+                        s->L[l].desc.max_t);
+    return 0;
+}
+
+// T tokens whose hidden rows are in s->X (positions pos0 .. pos0 + T - 1)
+// through every layer: the chunked form the reference runs in
+// src/qwen35_prefill.py:209-239 (_gdn :110-135, _full :137-168), with the
+// projections as f16-MFMA GEMMs over the chunk and the scan token-serial
+int enqueue_qchunk(QStack* s, int T, int pos0, hipStream_t st) {
+    auto kq = [](const DracoMat* m) { return m->L.code == DRACO_Q4_K || m->L.code == DRACO_Q6_K; };
+    for (int l = 0; l < s->n_layer; l++) {
+        QLayer& q = s->L[l];
+        if (q.desc.kind == 0) {
+            const GdnDev& g = q.g;
+            if (pf_rms(s->X, g.attn_norm, s->Xn, T, QH, QEPS, st)) return fail(-1, "qwen prefill: rms rejected");
+            if (draco_enqueue_gemm(*g.qkv, s->Xn, T, s->QKV, s->dig, false, st)) return -1;
+            if (draco_enqueue_gemm(*g.gate, s->Xn, T, s->Z, s->dig, kq(g.qkv), st)) return -1;
+            if (pf_gdn_gates(s->Xn, T, QH, g.bw, g.aw, g.ssm_dt, g.ssm_a, s->B, s->G, g.n_vh, st))
+                return fail(-1, "qwen prefill: gates rejected");
+            GdnArgs a = {};
+            a.QKV = s->QKV;
+            a.Z = s->Z;
+            a.B = s->B;
+            a.G = s->G;
+            a.conv = g.conv;
+            a.ssm_norm = g.ssm_norm;
+            a.tail = q.tail;
+            a.S = q.S;
+            a.ON = s->ON;
+            a.T = T;
+            a.n_qkv = g.n_qkv;
+            a.n_vh = g.n_vh;
+            a.nhq = QNKH;
+            if (draco_gdn_scan_launch(a, st)) return fail(-1, "qwen prefill: scan rejected");
+            if (draco_enqueue_gemm(*g.out, s->ON, T, s->Y, s->dig, false, st)) return -1;
+            if (pf_add_rms(s->X, s->Y, g.post_norm, s->Xn, T, QH, QEPS, st)) return fail(-1, "qwen prefill: rms");
+        } else {
+            const FullDev& f = q.f;
+            if (pf_rms(s->X, f.attn_norm, s->Xn, T, QH, QEPS, st)) return fail(-1, "qwen prefill: rms rejected");
+            if (draco_enqueue_gemm(*f.q, s->Xn, T, s->PQG, s->dig, false, st)) return -1;
+            if (draco_enqueue_gemm(*f.k, s->Xn, T, s->PK, s->dig, kq(f.q), st)) return -1;
+            if (draco_enqueue_gemm(*f.v, s->Xn, T, s->PV, s->dig, kq(f.q) || kq(f.k), st)) return -1;
+            dk_fa_prep_rows(s->PQG, f.nh * 2 * FHD, s->PQr, s->PK, s->PV, q.kc, q.vc, f.q_norm, f.k_norm, q.cs,
+                            nullptr, pos0, pos0, f.nh, T, st);
+            if (pf_attention256(s->PQr, q.kc, q.vc, s->Ppart, s->AO, pos0, T, f.nh, FNKV, 1.f / sqrtf((float)FHD),
+                                s->PQG + FHD, f.nh * 2 * FHD, 2 * FHD, st))
+                return fail(-1, "qwen prefill: attention rejected");
+            if (draco_enqueue_gemm(*f.o, s->AO, T, s->Y, s->dig, false, st)) return -1;
+            if (pf_add_rms(s->X, s->Y, f.post_norm, s->Xn, T, QH, QEPS, st)) return fail(-1, "qwen prefill: rms");
+        }
+        // FFN of the chunk (input Xn = x2n rows, residual into X)
+        if (q.desc.ffn_kind == QFFN_DENSE) {
+            if (draco_enqueue_gemm(*q.fg, s->Xn, T, s->PG, s->dig, false, st)) return -1;
+            if (draco_enqueue_gemm(*q.fu, s->Xn, T, s->PU, s->dig, kq(q.fg), st)) return -1;
+            dk_swiglu(s->PG, s->PU, T * q.FF, st);
+            if (draco_enqueue_gemm(*q.fd, s->PG, T, s->Y, s->dig, false, st)) return -1;
+            pf_add(s->X, s->Y, (size_t)T * QH, st);
+        } else if (q.desc.ffn_kind == QFFN_MOE) {
+            return fail(-1, "qwen prefill: MoE FFN layers are fed token by token");
+        }
+    }
+    return 0;
+}
+
+bool qstack_has_moe(const QStack* s) {
+    for (const QLayer& q : s->L)
+        if (q.desc.ffn_kind == QFFN_MOE) return true;
+    return false;
+}
+
+int g_qwen_chunk = 64;
+
+// ids (device) [0, n) at positions pos0 .. through the chunked prefill;
+// leaves the last token's hidden row in s->X row (returned T - 1)
+int enqueue_qprefill(QStack* s, const DracoMat* em, const int* ids, int n, int pos0, hipStream_t st) {
+    const int C = g_qwen_chunk;
+    if (C < 1 || n < 1) return 0;
+    if (qstack_pf(s, C)) return 0;
+    int last = 0;
+    for (int c0 = 0; c0 < n; c0 += C) {
+        const int T = std::min(C, n - c0);
+        if (pf_embed(em->dev, em->L, ids + c0, T, s->X, st)) return 0;
+        if (enqueue_qchunk(s, T, pos0 + c0, st)) return 0;
+        last = T;
+    }
+    return last;
+}
+
 }  // namespace
 
 extern "C" {
@@ -486,6 +898,260 @@ int draco_bench_qwen_op(int kind, const void* w, const float* h1, const float* s
         return 0;
     }
     return fail(-1, "bench qwen: kind %d", kind);
+}
+
+// ---- the qwen35 hybrid stack (no reference counterpart as one call: the
+// reference's driver composes the per-layer ops in Python,
+// src/qwen35_engine.py:310-327 for a token, src/qwen35_prefill.py:209-239 for
+// a chunk) ----
+
+// One token through every layer (x[h] host, in / out: the X the reference's
+// forward leaves before its head), at position pos (= the full-attention
+// layers' Told, as the reference passes them).  Layer state stays on the
+// device (draco_qwen_state_pull / push move it).
+int draco_qwen_forward(float* x, int h, int pos, const void* layers, int n_layer) {
+    std::lock_guard<std::recursive_mutex> g(api_mutex());
+    if (int rc = ensure_init()) return report(rc, "draco_qwen_forward");
+    QStack* s = build_qstack((const QStackLayer*)layers, n_layer, h);
+    if (!s) return report(-1, "draco_qwen_forward");
+    if (int rc = qstack_positions(s, pos, 1)) return report(rc, "draco_qwen_forward");
+    hipStream_t st = stream();
+    s->hstate[0] = pos;
+    s->hstate[1] = pos;
+    if (hipMemcpyAsync(s->state, s->hstate, sizeof(int) * 2, hipMemcpyHostToDevice, st) != hipSuccess ||
+        hipMemcpyAsync(s->x, x, sizeof(float) * QH, hipMemcpyHostToDevice, st) != hipSuccess)
+        return report(fail(-2, "upload failed"), "draco_qwen_forward");
+    if (int rc = enqueue_qtoken(s, st)) return report(rc, "draco_qwen_forward");
+    if (hipMemcpyAsync(x, s->x, sizeof(float) * QH, hipMemcpyDeviceToHost, st) != hipSuccess)
+        return report(fail(-2, "download failed"), "draco_qwen_forward");
+    hipError_t e = hipStreamSynchronize(st);
+    if (e != hipSuccess) return report(fail(-2, "draco_qwen_forward: %s", hipGetErrorString(e)), "draco_qwen_forward");
+    return 0;
+}
+
+// The forward_chunk contract for the stack (src/qwen35_prefill.py:209-239):
+// ids[0..n) at positions pos0 .. pos0 + n - 1 in chunks of the qwen chunk
+// size; afterwards the state is that of n token-serial forwards.  out_x (h
+// floats, host, nullable) = the last token's hidden row.
+int draco_qwen_prefill(const void* layers, int n_layer, int h, const uint8_t* emb_w, int emb_code, int vocab,
+                       const int* ids, int n, int pos0, float* out_x) {
+    std::lock_guard<std::recursive_mutex> g(api_mutex());
+    if (int rc = ensure_init()) return report(rc, "draco_qwen_prefill");
+    if (n < 1) return report(fail(-1, "need n >= 1"), "draco_qwen_prefill");
+    for (int i = 0; i < n; i++)
+        if (ids[i] < 0 || ids[i] >= vocab) return report(fail(-1, "token id %d out of range", ids[i]), "draco_qwen_prefill");
+    QStack* s = build_qstack((const QStackLayer*)layers, n_layer, h);
+    if (!s) return report(-1, "draco_qwen_prefill");
+    if (qstack_has_moe(s)) return report(fail(-1, "MoE FFN layers are fed token by token"), "draco_qwen_prefill");
+    const DracoMat* em = get_mat(emb_w, emb_code, vocab, h);
+    if (!em) return report(-1, "draco_qwen_prefill");
+    if (int rc = qstack_positions(s, pos0, n)) return report(rc, "draco_qwen_prefill");
+    hipStream_t st = stream();
+    int* dids = (int*)scratch(5, sizeof(int) * ((size_t)n + 64));
+    if (!dids) return report(-2, "draco_qwen_prefill");
+    DRACO_HIP(hipMemcpyAsync(dids, ids, sizeof(int) * n, hipMemcpyHostToDevice, st));
+    const int last = enqueue_qprefill(s, em, dids, n, pos0, st);
+    if (last <= 0) return report(-1, "draco_qwen_prefill");
+    if (out_x) DRACO_HIP(hipMemcpyAsync(out_x, s->X + (size_t)(last - 1) * QH, sizeof(float) * QH, hipMemcpyDeviceToHost, st));
+    hipError_t e = hipStreamSynchronize(st);
+    if (e != hipSuccess) return report(fail(-2, "draco_qwen_prefill: %s", hipGetErrorString(e)), "draco_qwen_prefill");
+    return 0;
+}
+
+// Tokens per chunk of draco_qwen_prefill and of draco_qwen_generate's prompt
+// (default 64, at most 256; 0 = the prompt goes token by token).  Returns the
+// previous value; n < 0 only queries.
+int draco_set_qwen_chunk(int n) {
+    std::lock_guard<std::recursive_mutex> g(api_mutex());
+    const int old = g_qwen_chunk;
+    if (n >= 0) g_qwen_chunk = n > QCHUNK_MAX ? QCHUNK_MAX : n;
+    return old;
+}
+
+// Greedy generation on the device from position pos0: prompt[0..n_prompt-1)
+// through the chunked prefill (token-serial decode steps when the chunk size
+// is 0 or a layer has a MoE FFN), the last prompt token through the first
+// decode step, then n_gen tokens by argmax (first index on ties).  With
+// use_graph the token step is captured once and replayed.  out_hidden[h] = x
+// after the last forward (nullable); stats[0] = decode ms, stats[1] = prefill
+// ms (nullable).
+int draco_qwen_generate(const void* layers, int n_layer, int h, float eps, const float* final_norm,
+                        const uint8_t* head_w, int head_code, int vocab, const uint8_t* emb_w, int emb_code, int pos0,
+                        const int* prompt, int n_prompt, int n_gen, int use_graph, int* out_tokens, float* out_hidden,
+                        float* stats) {
+    std::lock_guard<std::recursive_mutex> g(api_mutex());
+    if (int rc = ensure_init()) return report(rc, "draco_qwen_generate");
+    if (n_prompt < 1 || n_gen < 1) return report(fail(-1, "need n_prompt >= 1 and n_gen >= 1"), "draco_qwen_generate");
+    for (int i = 0; i < n_prompt; i++)
+        if (prompt[i] < 0 || prompt[i] >= vocab)
+            return report(fail(-1, "prompt token id %d out of range", prompt[i]), "draco_qwen_generate");
+    QStack* s = build_qstack((const QStackLayer*)layers, n_layer, h);
+    if (!s) return report(-1, "draco_qwen_generate");
+    const DracoMat* hm = get_mat(head_w, head_code, vocab, h);
+    const DracoMat* em = get_mat(emb_w, emb_code, vocab, h);
+    const float* nw = final_norm ? get_vec(final_norm, (size_t)h) : nullptr;
+    if (!hm || !em || (final_norm && !nw)) return report(-1, "draco_qwen_generate");
+    // get_mat / get_vec may have moved the epoch: the stack's cached pointers must be current
+    s = build_qstack((const QStackLayer*)layers, n_layer, h);
+    if (!s) return report(-1, "draco_qwen_generate");
+    const int steps = n_prompt + n_gen - 1;
+    if (int rc = qstack_positions(s, pos0, steps)) return report(rc, "draco_qwen_generate");
+    hipStream_t st = stream();
+    const int ntok = n_prompt + n_gen;
+    int* dtok = (int*)scratch(5, sizeof(int) * (ntok + 64));
+    const int hblocks = (vocab + 7) / 8;
+    float* dred = (float*)scratch(7, (sizeof(float) + sizeof(int)) * ((size_t)hblocks + 64) + 256);
+    float* dlog = (float*)scratch(6, sizeof(float) * (size_t)vocab);
+    if (!dtok || !dred || !dlog) return report(-2, "draco_qwen_generate");
+    int* cursor = dtok + ntok + 8;
+    int* dri = (int*)(dred + hblocks + 32);
+    const bool fused_head = hm->L.code == DRACO_Q4_K || hm->L.code == DRACO_Q6_K || hm->L.code == DRACO_Q8_0;
+    const int n_chunked = (g_qwen_chunk > 0 && n_prompt - 1 >= 2 && !qstack_has_moe(s)) ? n_prompt - 1 : 0;
+    if (n_chunked && qstack_pf(s, g_qwen_chunk)) return report(-2, "draco_qwen_generate (prefill buffers)");
+    std::vector<int> ht(ntok + 64, 0);
+    for (int i = 0; i < n_prompt; i++) ht[i] = prompt[i];
+    ht[ntok + 8] = n_chunked;
+    DRACO_HIP(hipMemcpyAsync(dtok, ht.data(), sizeof(int) * (ntok + 64), hipMemcpyHostToDevice, st));
+    auto step = [&](bool decode) -> int {
+        const bool emb_ready = decode && fused_head;
+        if (!emb_ready) dk_embed(*em, dtok, cursor, s->x, st);
+        if (int rc = enqueue_qtoken(s, st, emb_ready ? s->xe : nullptr)) return rc;
+        if (!decode) {
+            dk_advance(s->state, 1, cursor, st);
+            return 0;
+        }
+        if (fused_head) {
+            SegLaunch sl = {};
+            sl.nseg = 1;
+            sl.n_in = h;
+            sl.x = s->x;
+            sl.do_norm = 1;
+            sl.norm_w = nw;
+            sl.eps = eps;
+            SegDesc d = {};
+            d.base = hm->dev;
+            d.L = hm->L;
+            d.epi = EPI_ARGMAX;
+            d.y = dlog;
+            sl.seg[0] = d;
+            sl.am_val = dred;
+            sl.am_idx = dri;
+            sl.tokens = dtok;
+            sl.cursor = cursor;
+            sl.advance_state = s->state;
+            sl.advance_layers = 1;
+            sl.emb = em->dev;
+            sl.emb_L = em->L;
+            sl.emb_out = s->xe;
+            if (draco_seg_launch(sl, st)) return fail(-1, "head launch rejected");
+            return 0;
+        }
+        dk_rmsnorm(s->x, nw, s->xn, h, eps, st);
+        if (draco_gemv_launch(*hm, s->xn, dlog, nullptr, 0, vocab, st)) return fail(-1, "head gemv");
+        dk_argmax(dlog, vocab, dred, dri, dtok, cursor, 0, st);
+        dk_advance(s->state, 1, cursor, st);
+        return 0;
+    };
+    struct Guard {
+        hipStream_t st;
+        hipEvent_t ev[3] = {nullptr, nullptr, nullptr};
+        hipGraphExec_t gx[2] = {nullptr, nullptr};
+        hipGraph_t gg[2] = {nullptr, nullptr};
+        ~Guard() {
+            hipStreamSynchronize(st);
+            for (int k = 0; k < 2; k++) {
+                if (gx[k]) hipGraphExecDestroy(gx[k]);
+                if (gg[k]) hipGraphDestroy(gg[k]);
+            }
+            for (hipEvent_t e : ev)
+                if (e) hipEventDestroy(e);
+        }
+    } G{st};
+    for (hipEvent_t& e : G.ev) DRACO_HIP(hipEventCreate(&e));
+    if (use_graph) {
+        for (int k = 0; k < 2; k++) {
+            if (k == 0 && n_chunked == n_prompt - 1) continue;  // no token-serial prompt step to capture
+            DRACO_HIP(hipStreamBeginCapture(st, hipStreamCaptureModeRelaxed));
+            const int rc = step(k == 1);
+            hipGraph_t gr = nullptr;
+            const hipError_t ce = hipStreamEndCapture(st, &gr);
+            G.gg[k] = gr;
+            if (rc) return report(rc, "draco_qwen_generate");
+            if (ce != hipSuccess) return report(fail(-2, "graph capture: %s", hipGetErrorString(ce)), "draco_qwen_generate");
+            DRACO_HIP(hipGraphInstantiate(&G.gx[k], gr, nullptr, nullptr, 0));
+        }
+    }
+    DRACO_HIP(hipEventRecord(G.ev[0], st));
+    if (n_chunked && enqueue_qprefill(s, em, dtok, n_chunked, pos0, st) <= 0)
+        return report(-1, "draco_qwen_generate (chunked prefill)");
+    s->hstate[0] = pos0 + n_chunked;
+    s->hstate[1] = pos0 + n_chunked;
+    DRACO_HIP(hipMemcpyAsync(s->state, s->hstate, sizeof(int) * 2, hipMemcpyHostToDevice, st));
+    for (int i = n_chunked; i < n_prompt - 1; i++) {
+        if (use_graph) DRACO_HIP(hipGraphLaunch(G.gx[0], st));
+        else if (int rc = step(false)) return report(rc, "draco_qwen_generate");
+    }
+    if (fused_head) dk_embed(*em, dtok, cursor, s->xe, st);
+    DRACO_HIP(hipEventRecord(G.ev[1], st));
+    for (int i = 0; i < n_gen; i++) {
+        if (use_graph) DRACO_HIP(hipGraphLaunch(G.gx[1], st));
+        else if (int rc = step(true)) return report(rc, "draco_qwen_generate");
+    }
+    DRACO_HIP(hipEventRecord(G.ev[2], st));
+    DRACO_HIP(hipMemcpyAsync(ht.data(), dtok, sizeof(int) * ntok, hipMemcpyDeviceToHost, st));
+    if (out_hidden) DRACO_HIP(hipMemcpyAsync(out_hidden, s->x, sizeof(float) * h, hipMemcpyDeviceToHost, st));
+    DRACO_HIP(hipStreamSynchronize(st));
+    float ms_pre = 0.f, ms_dec = 0.f;
+    hipEventElapsedTime(&ms_pre, G.ev[0], G.ev[1]);
+    hipEventElapsedTime(&ms_dec, G.ev[1], G.ev[2]);
+    if (stats) {
+        stats[0] = ms_dec;
+        stats[1] = ms_pre;
+    }
+    for (int i = 0; i < n_gen; i++) out_tokens[i] = ht[n_prompt + i];
+    return 0;
+}
+
+// Device state of every layer -> the caller's arrays (GDN ssm and tail in
+// full; full-attention Kr / Vc rows [0, rows)), e.g. before a snapshot.
+int draco_qwen_state_pull(const void* layers_v, int n_layer, int rows) {
+    std::lock_guard<std::recursive_mutex> g(api_mutex());
+    const QStackLayer* layers = (const QStackLayer*)layers_v;
+    for (int l = 0; l < n_layer; l++) {
+        const QStackLayer& d = layers[l];
+        if (d.kind == 0) {
+            const GdnW* w = (const GdnW*)d.w;
+            if (int rc = mirror_pull(d.state0, sizeof(float) * (size_t)w->n_vh * QSV * QSV)) return rc;
+            if (int rc = mirror_pull(d.state1, sizeof(float) * (size_t)w->n_qkv * 3)) return rc;
+        } else if (rows > 0) {
+            const size_t b = sizeof(float) * full_cache_floats(std::min(rows, d.max_t));
+            if (int rc = mirror_pull(d.state0, b)) return rc;
+            if (int rc = mirror_pull(d.state1, b)) return rc;
+        }
+    }
+    return 0;
+}
+
+// The caller's arrays -> device state of every layer (after a reset that
+// zeroed them, or a restored snapshot): GDN ssm and tail in full,
+// full-attention rows [0, rows).
+int draco_qwen_state_push(const void* layers_v, int n_layer, int rows) {
+    std::lock_guard<std::recursive_mutex> g(api_mutex());
+    if (int rc = ensure_init()) return rc;
+    const QStackLayer* layers = (const QStackLayer*)layers_v;
+    for (int l = 0; l < n_layer; l++) {
+        const QStackLayer& d = layers[l];
+        if (d.kind == 0) {
+            const GdnW* w = (const GdnW*)d.w;
+            if (int rc = mirror_push(d.state0, sizeof(float) * (size_t)w->n_vh * QSV * QSV)) return rc;
+            if (int rc = mirror_push(d.state1, sizeof(float) * (size_t)w->n_qkv * 3)) return rc;
+        } else if (rows > 0) {
+            const size_t b = sizeof(float) * full_cache_floats(std::min(rows, d.max_t));
+            if (int rc = mirror_push(d.state0, b)) return rc;
+            if (int rc = mirror_push(d.state1, b)) return rc;
+        }
+    }
+    return 0;
 }
 
 }  // extern "C"

@@ -44,6 +44,12 @@ int dk_attention(const float* q, const float* kc, const float* vc, float* part, 
 // qwen35 full attention q/k head RMSNorm + rope (NH q heads, 2 k heads of 256).
 void dk_fa_prep(const float* QG, float* Qr, const float* kin, float* kout, const float* qn, const float* kn,
                 const float* cs, int NH, hipStream_t st);
+// The same for T tokens at positions (state ? state[0] : pos0) + t, K / V rows
+// into cache rows (state ? state[1] : row0) + t (kc / vc rows of 2 x 256);
+// QG rows qg_stride apart, kin / vin rows of 512, cs_tab [position][64].
+void dk_fa_prep_rows(const float* QG, int qg_stride, float* Qr, const float* kin, const float* vin, float* kc,
+                     float* vc, const float* qn, const float* kn, const float* cs_tab, const int* state, int pos0,
+                     int row0, int NH, int T, hipStream_t st);
 void dk_swiglu(float* g, const float* u, int n, hipStream_t st);
 // out[i] = y[i] * sigmoid(g[0]) (n floats; g is one device float)
 void dk_sigmoid_scale(const float* y, const float* g, float* out, int n, hipStream_t st);

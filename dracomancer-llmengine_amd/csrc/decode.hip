@@ -443,6 +443,44 @@ __global__ __launch_bounds__(256) void k_fa_prep(const float* __restrict__ QG, f
     (isq ? Qr + (size_t)b * 256 : kout + (b - NH) * 256)[t] = y;
 }
 
+// The same head norms and rope for T tokens whose positions and cache rows
+// come from the device (graph-replayable): token t sits at position
+// p = (state ? state[0] : pos0) + t and cache row r = (state ? state[1] : row0)
+// + t.  Block (b, t): b < NH normalises + ropes q head b of QG[t] (row
+// stride qg_stride) into Qr[t]; b = NH + g normalises + ropes k head g of
+// kin[t] into kc row r and copies v head g of vin[t] into vc row r.  The
+// rope's cos / sin come from cs_tab row p (64 floats: the reference's
+// (float)pos * rope_inv[t] angle, computed on the host).
+__global__ __launch_bounds__(256) void k_fa_prep_rows(const float* __restrict__ QG, int qg_stride,
+                                                      float* __restrict__ Qr, const float* __restrict__ kin,
+                                                      const float* __restrict__ vin, float* __restrict__ kc,
+                                                      float* __restrict__ vc, const float* __restrict__ qn,
+                                                      const float* __restrict__ kn,
+                                                      const float* __restrict__ cs_tab, const int* __restrict__ state,
+                                                      int pos0, int row0, int NH) {
+    __shared__ float red[4];
+    const int b = blockIdx.x, tok = blockIdx.y, t = threadIdx.x, lane = t & 63, w = t >> 6;
+    const int pos = (state ? state[0] : pos0) + tok, row = (state ? state[1] : row0) + tok;
+    const bool isq = b < NH;
+    const int g = b - NH;
+    const float x = isq ? QG[(size_t)tok * qg_stride + (size_t)b * 512 + t] : kin[(size_t)tok * 512 + g * 256 + t];
+    if (!isq) vc[(size_t)row * 512 + g * 256 + t] = vin[(size_t)tok * 512 + g * 256 + t];
+    const float s = wave_sum(x * x);
+    if (lane == 0) red[w] = s;
+    __syncthreads();
+    const float n2 = (red[0] + red[1]) + (red[2] + red[3]);
+    const float r = 1.f / sqrtf(n2 / 256.f + 1e-6f);
+    float y = isq ? x * r * qn[t] : x * (r * kn[t]);
+    if (w == 0) {
+        const float* cs = cs_tab + (size_t)pos * 64;
+        const float o = lane_xor32(y);
+        const float c = cs[2 * (lane & 31)], sn = cs[2 * (lane & 31) + 1];
+        y = lane < 32 ? y * c - o * sn : o * sn + y * c;
+    }
+    if (isq) Qr[(size_t)tok * NH * 256 + (size_t)b * 256 + t] = y;
+    else kc[(size_t)row * 512 + g * 256 + t] = y;
+}
+
 // -------------------------------------------------------------- SwiGLU --
 __global__ __launch_bounds__(256) void k_swiglu(float* __restrict__ g, const float* __restrict__ u, int n) {
     for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
@@ -616,6 +654,13 @@ int dk_attention(const float* q, const float* kc, const float* vc, float* part, 
 void dk_fa_prep(const float* QG, float* Qr, const float* kin, float* kout, const float* qn, const float* kn,
                 const float* cs, int NH, hipStream_t st) {
     hipLaunchKernelGGL(k_fa_prep, dim3(NH + 2), dim3(256), 0, st, QG, Qr, kin, kout, qn, kn, cs, NH);
+}
+
+void dk_fa_prep_rows(const float* QG, int qg_stride, float* Qr, const float* kin, const float* vin, float* kc,
+                     float* vc, const float* qn, const float* kn, const float* cs_tab, const int* state, int pos0,
+                     int row0, int NH, int T, hipStream_t st) {
+    hipLaunchKernelGGL(k_fa_prep_rows, dim3(NH + 2, T), dim3(256), 0, st, QG, qg_stride, Qr, kin, vin, kc, vc, qn, kn,
+                       cs_tab, state, pos0, row0, NH);
 }
 
 void dk_swiglu(float* g, const float* u, int n, hipStream_t st) {

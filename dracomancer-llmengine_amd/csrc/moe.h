@@ -65,6 +65,9 @@ MoeLayer* draco_moe_layer(const DracoMoeP* p);
 // and resid (x is read by the norm launch before anything is written).
 int draco_moe_layer_enqueue(MoeLayer* m, const float* x, const float* norm_w, float eps, float* out,
                             const float* resid, hipStream_t st);
+// out = resid + MoE(xn) for an input that is already normalised (the qwen35
+// FFN input x2n, src/qwen35_engine.py:325)
+int draco_moe_layer_enqueue_xn(MoeLayer* m, const float* xn, float* out, const float* resid, hipStream_t st);
 
 // token-batched MoE helpers
 int draco_moe_gather_launch(const float* X, int n_in, const int* src, int rows, float* Xg, hipStream_t st);

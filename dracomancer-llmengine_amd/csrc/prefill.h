@@ -24,5 +24,13 @@ int pf_rope_append(float* Q, const float* K, const float* V, float* kc, float* v
 // (NH / NKV <= 8, HD 64 or 128); part holds pf_part_floats(...) floats
 int pf_attention(const float* Q, const float* kc, const float* vc, float* part, float* O, int row0, int T, int NH,
                  int NKV, int HD, float scale, hipStream_t st);
+// The same at head dim 256 (NH / NKV <= 16) with the qwen35 output gate:
+// O[t][h*256 + d] = attention * sigmoid(gate[t * g_row + h * g_head + d])
+int pf_attention256(const float* Q, const float* kc, const float* vc, float* part, float* O, int row0, int T, int NH,
+                    int NKV, float scale, const float* gate, int g_row, int g_head, hipStream_t st);
+// GDN gates of T tokens: B[t][e] = sigmoid(Xn[t] . bw[e]), G[t][e] =
+// exp(softplus(Xn[t] . aw[e] + dt[e]) * sa[e]); bw / aw [n_vh][H]
+int pf_gdn_gates(const float* Xn, int T, int H, const float* bw, const float* aw, const float* dt, const float* sa,
+                 float* B, float* G, int n_vh, hipStream_t st);
 // X += Y over n floats
 int pf_add(float* X, const float* Y, size_t n, hipStream_t st);

@@ -245,6 +245,163 @@ __global__ __launch_bounds__(256) void k_pf_merge(const float* __restrict__ part
     O[(size_t)t * NH * HD + h * HD + d] = num / den;
 }
 
+// Causal chunk attention at head dim 256 (qwen35 full attention, the chunked
+// form of src/m6_layer.c:455-500 that src/qwen35_prefill.py:137-168 runs).
+// Block (g, qt, s): kv head g, queries qt*8 .. qt*8+7 of the chunk, key split
+// s; wave j = q head g*rep + j.  Eight lanes share a query: lane = 8*query +
+// k holds the dims 4*(k + 8*i) .. +3 (i < 8) of q and of the output, so the
+// eight lanes of a query read one 128-byte run of a staged K / V row
+// (conflict-free) and a score is the sum over those eight lanes.  K / V rows
+// are staged in LDS 32 at a time; keys go in groups of 16 (scores, one
+// online-softmax rescale, P.V).  Writes (o[256], m, l) per (head, query,
+// split) for k_pf_merge256.
+constexpr int PF256_QT = 8, PF256_KT = 32;
+
+__global__ __launch_bounds__(1024) void k_pf_attn256(const float* __restrict__ Q, const float* __restrict__ kc,
+                                                     const float* __restrict__ vc, float* __restrict__ part,
+                                                     int row0, int T, int NH, int NKV, int nspl, float scale) {
+    constexpr int HD = 256;
+    __shared__ __align__(16) float Ks[PF256_KT * HD];
+    __shared__ __align__(16) float Vs[PF256_KT * HD];
+    const int g = blockIdx.x, qt = blockIdx.y, s = blockIdx.z;
+    const int tid = threadIdx.x, lane = tid & 63, j = tid >> 6, k = lane & 7;
+    const int rep = NH / NKV, h = g * rep + j, KD = NKV * HD, QD = NH * HD;
+    const int t = qt * PF256_QT + (lane >> 3), qrow = row0 + t;
+    const bool live = t < T;
+    const int kend = row0 + min(T, (qt + 1) * PF256_QT);
+    const int chunk = (kend + nspl - 1) / nspl;
+    const int k0 = min(kend, s * chunk), k1 = min(kend, k0 + chunk);
+    float q[32], o[32];
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const float4 v = live ? ld4(Q + (size_t)t * QD + h * HD + 4 * (k + 8 * i)) : make_float4(0.f, 0.f, 0.f, 0.f);
+        q[4 * i] = v.x; q[4 * i + 1] = v.y; q[4 * i + 2] = v.z; q[4 * i + 3] = v.w;
+        o[4 * i] = o[4 * i + 1] = o[4 * i + 2] = o[4 * i + 3] = 0.f;
+    }
+    float m = -INFINITY, l = 0.f;
+    for (int kb = k0; kb < k1; kb += PF256_KT) {
+        const int nr = min(PF256_KT, k1 - kb);
+        for (int i = tid; i < nr * (HD / 4); i += blockDim.x) {
+            const int r = i / (HD / 4), c = 4 * (i % (HD / 4));
+            *reinterpret_cast<float4*>(Ks + r * HD + c) = ld4(kc + (size_t)(kb + r) * KD + g * HD + c);
+            *reinterpret_cast<float4*>(Vs + r * HD + c) = ld4(vc + (size_t)(kb + r) * KD + g * HD + c);
+        }
+        __syncthreads();
+        for (int c0 = 0; c0 < nr; c0 += 16) {
+            const int ng = min(16, nr - c0);
+            float sc[16];
+            float cm = -INFINITY;
+#pragma unroll
+            for (int jj = 0; jj < 16; jj++) {
+                float acc = 0.f;
+                if (jj < ng) {
+                    const float* kr = Ks + (c0 + jj) * HD;
+#pragma unroll
+                    for (int i = 0; i < 8; i++) {
+                        const float4 kv = *reinterpret_cast<const float4*>(kr + 4 * (k + 8 * i));
+                        acc = fmaf(q[4 * i], kv.x, acc);
+                        acc = fmaf(q[4 * i + 1], kv.y, acc);
+                        acc = fmaf(q[4 * i + 2], kv.z, acc);
+                        acc = fmaf(q[4 * i + 3], kv.w, acc);
+                    }
+                }
+                acc = group_sum<8>(acc);
+                sc[jj] = (jj < ng && live && kb + c0 + jj <= qrow) ? acc * scale : -INFINITY;
+                cm = fmaxf(cm, sc[jj]);
+            }
+            const float mn = fmaxf(m, cm);
+            if (mn > -INFINITY) {
+                const float corr = m > -INFINITY ? expf(m - mn) : 0.f;
+                l *= corr;
+#pragma unroll
+                for (int d = 0; d < 32; d++) o[d] *= corr;
+#pragma unroll
+                for (int jj = 0; jj < 16; jj++) {
+                    if (jj < ng) {
+                        const float p = sc[jj] > -INFINITY ? expf(sc[jj] - mn) : 0.f;
+                        l += p;
+                        const float* vr = Vs + (c0 + jj) * HD;
+#pragma unroll
+                        for (int i = 0; i < 8; i++) {
+                            const float4 vv = *reinterpret_cast<const float4*>(vr + 4 * (k + 8 * i));
+                            o[4 * i] = fmaf(p, vv.x, o[4 * i]);
+                            o[4 * i + 1] = fmaf(p, vv.y, o[4 * i + 1]);
+                            o[4 * i + 2] = fmaf(p, vv.z, o[4 * i + 2]);
+                            o[4 * i + 3] = fmaf(p, vv.w, o[4 * i + 3]);
+                        }
+                    }
+                }
+                m = mn;
+            }
+        }
+        __syncthreads();
+    }
+    if (!live) return;
+    float* pp = part + (((size_t)h * T + t) * nspl + s) * (HD + 2);
+#pragma unroll
+    for (int i = 0; i < 8; i++)
+        *reinterpret_cast<float4*>(pp + 4 * (k + 8 * i)) = make_float4(o[4 * i], o[4 * i + 1], o[4 * i + 2], o[4 * i + 3]);
+    if (k == 0) {
+        pp[HD] = m;
+        pp[HD + 1] = l;
+    }
+}
+
+// k_pf_merge with the qwen35 output gate: O[t][h*HD + d] *= sigmoid(gate
+// row t, h*gstride_h + d) (the reference's attn * sigmoid(q gate half),
+// src/qwen35_prefill.py:164-166 / src/m6_layer.c:497).
+__global__ __launch_bounds__(256) void k_pf_merge_gate(const float* __restrict__ part, float* __restrict__ O, int T,
+                                                       int NH, int HD, int nspl, const float* __restrict__ gate,
+                                                       int g_row, int g_head) {
+    const int t = blockIdx.x, h = blockIdx.y, d = threadIdx.x;
+    if (d >= HD) return;
+    const float* pp = part + ((size_t)h * T + t) * nspl * (HD + 2);
+    float M = -INFINITY;
+    for (int s = 0; s < nspl; s++) M = fmaxf(M, pp[s * (HD + 2) + HD]);
+    float num = 0.f, den = 0.f;
+    for (int s = 0; s < nspl; s++) {
+        const float ms = pp[s * (HD + 2) + HD];
+        if (ms == -INFINITY) continue;
+        const float e = expf(ms - M);
+        den = fmaf(pp[s * (HD + 2) + HD + 1], e, den);
+        num = fmaf(pp[s * (HD + 2) + d], e, num);
+    }
+    const float gv = gate[(size_t)t * g_row + (size_t)h * g_head + d];
+    O[(size_t)t * NH * HD + h * HD + d] = (num / den) * (1.f / (1.f + expf(-gv)));
+}
+
+// GDN gates of a chunk (src/qwen35_prefill.py:118-123): for token t and V
+// head e, B = sigmoid(Xn[t] . bw[e]) and G = exp(softplus(Xn[t] . aw[e] +
+// dt[e]) * a[e]); bw / aw stored [n_vh][H].  Block (t, e), 256 threads.
+__global__ __launch_bounds__(256) void k_pf_gdn_gates(const float* __restrict__ Xn, int H,
+                                                      const float* __restrict__ bw, const float* __restrict__ aw,
+                                                      const float* __restrict__ dt, const float* __restrict__ sa,
+                                                      float* __restrict__ B, float* __restrict__ G, int n_vh) {
+    __shared__ float red[2][4];
+    const int t = blockIdx.x, e = blockIdx.y, tid = threadIdx.x;
+    const float* x = Xn + (size_t)t * H;
+    float sb = 0.f, sa_ = 0.f;
+    for (int i = tid * 4; i < H; i += 1024) {
+        const float4 xv = ld4(x + i), bv = ld4(bw + (size_t)e * H + i), av = ld4(aw + (size_t)e * H + i);
+        sb = fmaf(xv.x, bv.x, sb); sb = fmaf(xv.y, bv.y, sb); sb = fmaf(xv.z, bv.z, sb); sb = fmaf(xv.w, bv.w, sb);
+        sa_ = fmaf(xv.x, av.x, sa_); sa_ = fmaf(xv.y, av.y, sa_); sa_ = fmaf(xv.z, av.z, sa_); sa_ = fmaf(xv.w, av.w, sa_);
+    }
+    sb = wave_sum(sb);
+    sa_ = wave_sum(sa_);
+    if ((tid & 63) == 0) {
+        red[0][tid >> 6] = sb;
+        red[1][tid >> 6] = sa_;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        const float b = (red[0][0] + red[0][1]) + (red[0][2] + red[0][3]);
+        const float a = (red[1][0] + red[1][1]) + (red[1][2] + red[1][3]) + dt[e];
+        const float sp = a > 0.f ? a + log1pf(expf(-a)) : log1pf(expf(a));  // softplus, src/m6_layer.c:253
+        B[(size_t)t * n_vh + e] = 1.f / (1.f + expf(-b));
+        G[(size_t)t * n_vh + e] = expf(sp * sa[e]);
+    }
+}
+
 __global__ __launch_bounds__(256) void k_pf_add(float* __restrict__ X, const float* __restrict__ Y, size_t n) {
     for (size_t i = blockIdx.x * (size_t)256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) X[i] += Y[i];
 }
@@ -304,6 +461,23 @@ int pf_attention(const float* Q, const float* kc, const float* vc, float* part, 
         hipLaunchKernelGGL(k_pf_attn<128>, grid, block, lds, st, Q, kc, vc, part, row0, T, NH, NKV, nspl, scale);
     }
     hipLaunchKernelGGL(k_pf_merge, dim3(T, NH), dim3(HD), 0, st, part, O, T, NH, HD, nspl);
+    return 0;
+}
+
+int pf_attention256(const float* Q, const float* kc, const float* vc, float* part, float* O, int row0, int T, int NH,
+                    int NKV, float scale, const float* gate, int g_row, int g_head, hipStream_t st) {
+    if (T < 1 || NKV < 1 || NH % NKV || NH / NKV > 16 || !gate) return -1;
+    const int nspl = pf_attn_nsplit(row0, T);
+    const dim3 grid(NKV, (T + PF256_QT - 1) / PF256_QT, nspl), block(64 * (NH / NKV));
+    hipLaunchKernelGGL(k_pf_attn256, grid, block, 0, st, Q, kc, vc, part, row0, T, NH, NKV, nspl, scale);
+    hipLaunchKernelGGL(k_pf_merge_gate, dim3(T, NH), dim3(256), 0, st, part, O, T, NH, 256, nspl, gate, g_row, g_head);
+    return 0;
+}
+
+int pf_gdn_gates(const float* Xn, int T, int H, const float* bw, const float* aw, const float* dt, const float* sa,
+                 float* B, float* G, int n_vh, hipStream_t st) {
+    if (T < 1 || H % 4 || n_vh < 1) return -1;
+    hipLaunchKernelGGL(k_pf_gdn_gates, dim3(T, n_vh), dim3(256), 0, st, Xn, H, bw, aw, dt, sa, B, G, n_vh);
     return 0;
 }
 

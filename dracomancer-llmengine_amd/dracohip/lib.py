@@ -65,6 +65,17 @@ SIGNATURES = {
     "m6_full_attn": (None, [f32p, ct.c_void_p, f32p, f32p, ct.c_int, ct.c_int, f32p, f32p, f32p, f32p,
                             f32p, f32p]),
     "draco_bench_qwen_op": (ct.c_int, [ct.c_int, ct.c_void_p, f32p, f32p, f32p, ct.c_int, ct.c_int, f32p]),
+    # qwen35 hybrid stack on the device (no reference counterpart as one call)
+    "draco_qwen_forward": (ct.c_int, [f32p, ct.c_int, ct.c_int, ct.c_void_p, ct.c_int]),
+    "draco_qwen_prefill": (ct.c_int, [ct.c_void_p, ct.c_int, ct.c_int, ct.c_void_p, ct.c_int, ct.c_int, i32p, ct.c_int,
+                                      ct.c_int, f32p]),
+    "draco_set_qwen_chunk": (ct.c_int, [ct.c_int]),
+    "draco_qwen_generate": (ct.c_int, [ct.c_void_p, ct.c_int, ct.c_int, ct.c_float, f32p, ct.c_void_p, ct.c_int,
+                                       ct.c_int, ct.c_void_p, ct.c_int, ct.c_int, i32p, ct.c_int, ct.c_int, ct.c_int,
+                                       i32p, f32p, f32p]),
+    "draco_qwen_state_pull": (ct.c_int, [ct.c_void_p, ct.c_int, ct.c_int]),
+    "draco_qwen_state_push": (ct.c_int, [ct.c_void_p, ct.c_int, ct.c_int]),
+    "draco_moe_ffn_op": (None, [f32p, ct.c_void_p, f32p]),
     # library utilities
     "draco_last_error": (ct.c_char_p, []),
     "draco_forget": (ct.c_int, [ct.c_void_p]),

@@ -185,6 +185,22 @@ int m5_gemvn_q4k(const float* x, long x_stride, const uint8_t* W, const int* idx
                  int n_in, int n_exp, float* y);
 int m5_gemvn_q6k(const float* x, long x_stride, const uint8_t* W, const int* idx, long per, int n_out_e,
                  int n_in, int n_exp, float* y);
+/* The MoE FFN as an m6 ffn op (no reference counterpart as an op: the
+ * reference's qwen35 driver calls m6_granite_moe per layer from Python,
+ * src/qwen35_engine.py:293-307): the arguments of m6_granite_moe in one
+ * struct.  In an M6LayerDesc it lets m6_forward_token and
+ * draco_llama_generate run MoE layers on the device (the configs[3] stack);
+ * called directly it is m6_granite_moe(xn, ...) into out[n_out].  scratch
+ * is the reference op's host scratch (3*n_used*inter + n_used*n_out floats;
+ * not used by the device path). */
+typedef struct {
+    const uint64_t* ptrs;   /* [3 * n_exp] gate, up, down per expert */
+    const int* codes;       /* [3 * n_exp] */
+    const float* gate_inp;  /* [n_exp][n_in] fp32 router */
+    int n_exp, n_used, inter, n_in, n_out;
+    float* scratch;
+} DracoMoeP;
+void draco_moe_ffn_op(const float* xn, void* p, float* out);
 /* No reference counterpart: out[0] us per MoE FFN (router + routed gate/up +
  * down/combine) from a graph replay of `iters` FFNs, out[1] bytes per FFN. */
 int draco_bench_granite_moe(const float* x0, const uint64_t* ptrs, const int* codes, const float* gate_inp,
@@ -271,6 +287,53 @@ void m6_full_attn(const float* h1, const FullW* w, const float* Kr, const float*
  * bytes per op, out[2] algorithmic HBM bytes per op. */
 int draco_bench_qwen_op(int kind, const void* w, const float* h1, const float* ssm_or_kr, const float* tail_or_vc,
                         int told, int iters, float* out);
+
+/* ---- the qwen35 hybrid stack on the device --------------------------------
+ * No reference counterpart as one call: the reference's driver composes the
+ * per-layer ops in Python (src/qwen35_engine.py:310-327 per token,
+ * src/qwen35_prefill.py:209-239 per chunk).  One DracoQwenLayer per layer:
+ * the layer op (kind 0 m6_gdn_attn with a GdnW, kind 1 m6_full_attn with a
+ * FullW), its state arrays (GDN: ssm [n_vh][128][128] and tail [n_qkv][3];
+ * full attention: Kr and Vc [max_t][2][256]) and the FFN of x2n added to
+ * x2_out (ffn_kind 0 none, 1 dense with an M6DenseP, 2 MoE with a
+ * DracoMoeP).  Token t of a sequence sits at position pos0 + t and writes
+ * cache row pos0 + t (Told = pos, as the reference passes them).  The state
+ * lives on the device (mirrors keyed by the state arrays' addresses, loaded
+ * from them when first seen); draco_qwen_state_pull / push move it to and
+ * from the caller's arrays (snapshot, or after zeroing them for a reset). */
+typedef struct {
+    int kind;            /* 0 GDN, 1 full attention */
+    const void* w;       /* const GdnW* / const FullW* */
+    float* state0;       /* GDN ssm / full-attention Kr */
+    float* state1;       /* GDN tail / full-attention Vc */
+    int max_t;           /* full attention: rows of Kr / Vc */
+    int ffn_kind;        /* 0 none, 1 dense, 2 MoE */
+    const void* ffn;     /* const M6DenseP* / const DracoMoeP* */
+} DracoQwenLayer;
+
+/* One token: x[2048] (host, in / out) through every layer at position pos. */
+int draco_qwen_forward(float* x, int h, int pos, const void* layers, int n_layer);
+/* forward_chunk: ids[0..n) at positions pos0 .. pos0 + n - 1 in chunks
+ * (draco_set_qwen_chunk, default 64): projections as f16-MFMA GEMMs over the
+ * chunk, the GDN scan token-serial, causal gated attention over the cache;
+ * out_x[2048] (host, nullable) = the last token's hidden row.  Layers with a
+ * MoE FFN are not served here (-1; draco_qwen_generate feeds them token by
+ * token). */
+int draco_qwen_prefill(const void* layers, int n_layer, int h, const uint8_t* emb_w, int emb_code, int vocab,
+                       const int* ids, int n, int pos0, float* out_x);
+int draco_set_qwen_chunk(int n);
+/* Greedy generation from position pos0 (prompt through the chunked prefill
+ * except its last token, then n_gen argmax tokens; graph-replayed steps with
+ * use_graph); the head is RMSNorm(final_norm, eps) + head_w, as m6_head_op.
+ * stats[0] = decode ms, stats[1] = prompt ms (nullable). */
+int draco_qwen_generate(const void* layers, int n_layer, int h, float eps, const float* final_norm,
+                        const uint8_t* head_w, int head_code, int vocab, const uint8_t* emb_w, int emb_code, int pos0,
+                        const int* prompt, int n_prompt, int n_gen, int use_graph, int* out_tokens, float* out_hidden,
+                        float* stats);
+/* device state -> caller's arrays (GDN in full; Kr / Vc rows [0, rows)) */
+int draco_qwen_state_pull(const void* layers, int n_layer, int rows);
+/* caller's arrays -> device state */
+int draco_qwen_state_push(const void* layers, int n_layer, int rows);
 
 /* ---- Q8_K activations and the Q4_K / Q6_K x Q8_K GEMV --------------------
  * No reference counterpart: the reference has no Q8_K path (nearest analogue:

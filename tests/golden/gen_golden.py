@@ -474,6 +474,47 @@ def gen_qwen35():
     print("qwen35.npz")
 
 
+def ref_qwen_ops(E, max_t):
+    """The compiled reference's qwen35 per-layer ops (src/m6_layer.c:205-518,
+    src/m6_engine.c:275-303 and :373-391, m6_granite_moe through the MoE
+    callback) as a QwenStackDriver op table, with the host scratch they need
+    (buf >= 40000 floats with buf[39000] = 0, scores [nh][max_t])."""
+    from dracohip import qwen35 as Q
+    E.m6_gdn_attn.argtypes = [f32p, ct.c_void_p, f32p, f32p, f32p, f32p, f32p]
+    E.m6_gdn_attn.restype = None
+    E.m6_full_attn.argtypes = [f32p, ct.c_void_p, f32p, f32p, ct.c_int, ct.c_int, f32p, f32p, f32p, f32p, f32p, f32p]
+    E.m6_full_attn.restype = None
+    E.m6_dense_op.argtypes = [f32p, ct.c_void_p, f32p]
+    E.m6_dense_op.restype = None
+    lib = ref_engine_lib(E)
+    buf = np.zeros(40000, np.float32)
+    scores = np.zeros(32 * max_t, np.float32)
+    moe = ct.cast(lib.moe_ptr, ct.CFUNCTYPE(None, f32p, ct.c_void_p, f32p))
+    return {"gdn": lambda h1, w, ssm, tail, x2n, x2o: E.m6_gdn_attn(h1, w, ssm, tail, pf(buf), x2n, x2o),
+            "full": lambda h1, w, Kr, Vc, told, pos0, x2n, x2o, krn, vrn:
+                E.m6_full_attn(h1, w, Kr, Vc, told, pos0, pf(buf), pf(scores), x2n, x2o, krn, vrn),
+            "dense": E.m6_dense_op, "moe": moe, "head": lib.head_op, "_keep": (buf, scores, lib)}
+
+
+def gen_qwen_stack(name, fname, logit_steps):
+    """A qwen35 stack (dracohip.qwen35 STACKS[name]) decoded token by token
+    through the compiled reference's per-layer ops exactly as
+    src/qwen35_engine.py:310-327 composes them (the caller appends KRN / VRN
+    to its caches), then greedy tokens."""
+    from dracohip import qwen35 as Q
+    t0 = time.time()
+    cfg = Q.STACKS[name]
+    stack = Q.build_stack(cfg, 0)
+    ops = ref_qwen_ops(ref_engine(), cfg.max_t)
+    drv = Q.QwenStackDriver(stack, ops)
+    toks, hidden, lg = drv.greedy(stack.prompt(), cfg.n_gen, collect_logits=logit_steps)
+    out = dict(tokens=np.array(toks, np.int32), hidden=hidden, prompt=stack.prompt())
+    for s, v in lg.items():
+        out[f"logits{s}"] = v
+    np.savez_compressed(os.path.join(OUT, fname), **out)
+    print(fname, name, f"{time.time() - t0:.1f}s", "tokens", toks[:8], "...")
+
+
 JOBS = {
     "gemv": gen_gemv,
     "batch8k": gen_batch8k,
@@ -488,6 +529,8 @@ JOBS = {
     "smol360m": lambda: gen_llama(models.SMOL360M, "smol360m.npz", logit_steps=(0, 63)),
     "llama1b": lambda: gen_llama(models.LLAMA1B, "llama1b.npz", logit_steps=(0, 63)),
     "moe_tiny": lambda: gen_llama(models.MOE_TINY, "moe_tiny.npz", logit_steps=(0, 15)),
+    "qwen_tiny": lambda: gen_qwen_stack("qwen35-tiny", "qwen_tiny.npz", logit_steps=(0, 15)),
+    "qwen_tiny_moe": lambda: gen_qwen_stack("qwen35-tiny-moe", "qwen_tiny_moe.npz", logit_steps=(0, 7)),
 }
 
 if __name__ == "__main__":
