@@ -261,6 +261,61 @@ def moe_stack_configs3(lib, seed=3):
     return res
 
 
+def qwen_stack_configs4(lib, seed=4):
+    """the 48-layer qwen35 hybrid stack (36 GDN layers of 16 q/k
+    and 32 V heads of 128, 12 full-attention layers of 16 q / 2 KV heads of
+    256, 3:1 interleave, Q4_K projections, hidden 2048): a 4096-token prompt,
+    all but its last token through the chunked prefill in 64-token chunks, then
+    64 greedy decode steps (positions 4095..4158), graph-replayed.  Bytes per
+    decode token = every layer's projection weights + the GDN state read and
+    written + the beta / alpha rows + the full-attention K / V rows read (mean
+    over the decode positions) + the head and one embedding row."""
+    import ctypes as ct
+    from dracohip import qwen35 as Q
+    cfg = Q.QWEN35_GDN48
+    t0 = time.time()
+    stack = Q.build_stack(cfg, seed)
+    log(f"configs[4] stack built in {time.time() - t0:.1f}s ({stack.nbytes() / 1e9:.2f} GB)")
+    L = lib.load()
+    drv = Q.QwenStackDriver(stack, Q.hip_ops(L), lib=L)
+    old = L.draco_set_qwen_chunk(64)
+    prompt = stack.prompt()
+    t0 = time.time()
+    toks, _, _ = drv.generate_device(prompt, cfg.n_gen)
+    log(f"configs[4] first run (upload + prompt + decode) {time.time() - t0:.1f}s")
+    drv.reset()
+    toks2, _, (dec_ms, pre_ms) = drv.generate_device(prompt, cfg.n_gen)
+    L.draco_set_qwen_chunk(old)
+    gdn_w = full_w = 0
+    for il, layer in enumerate(stack.layers):
+        a = layer.arrays
+        if isinstance(layer, Q.FullLayer):
+            full_w += a["q"].nbytes + a["k"].nbytes + a["v"].nbytes + a["o"].nbytes
+        else:
+            gdn_w += a["qkv"].nbytes + a["gate"].nbytes + a["ssm_out"].nbytes
+    n_gdn = sum(1 for layer in stack.layers if isinstance(layer, Q.GdnLayer))
+    n_full = cfg.n_layer - n_gdn
+    n_qkv = 2 * Q.NKH * Q.SV + cfg.n_vh * Q.SV
+    gdn_state = n_gdn * (2 * cfg.n_vh * Q.SV * Q.SV * 4 + 2 * Q.H * cfg.n_vh * 4 + 2 * n_qkv * 3 * 4 + n_qkv * 16)
+    rows = np.arange(cfg.n_prompt - 1, cfg.n_prompt - 1 + cfg.n_gen) + 1
+    kv = n_full * 2 * Q.NKV_A * Q.HD_A * 4 * float(rows.mean())
+    per_tok = gdn_w + full_w + gdn_state + kv + stack.head.nbytes + stack.emb.nbytes // cfg.vocab
+    tok_s = cfg.n_gen / (dec_ms / 1e3)
+    n_pre = len(prompt) - 1
+    res = {"decode_tok_s": round(tok_s, 1), "ms_per_token": round(dec_ms / cfg.n_gen, 4),
+           "bytes_per_token": int(per_tok), "GB_s": round(per_tok * tok_s / 1e9, 1),
+           "frac_of_peak": round(per_tok * tok_s / 1e9 / PEAK_HBM_GBS, 4),
+           "roof_tok_s": round(PEAK_HBM_GBS * 1e9 / per_tok, 1),
+           "prefill_tokens": n_pre, "prefill_chunk": 64, "prefill_ms": round(pre_ms, 1),
+           "prefill_tok_s": round(n_pre / (pre_ms / 1e3), 1), "greedy_tokens_repeat": toks == toks2,
+           "shape": "48 layers 3:1 GDN (16 q/k + 32 V heads of 128) : full attention (16 q / 2 kv heads of 256), "
+                    "Q4_K projections, hidden 2048, no FFN (the configuration's mixers), vocab 151936 untied Q6_K "
+                    "head; 4095-token chunked prefill, decode at positions 4095..4158"}
+    del drv, stack
+    L.draco_reset()
+    return res
+
+
 PEAK_F16_TFLOPS = 2500.0  # MI355X dense f16 MFMA
 
 
@@ -487,11 +542,14 @@ def main():
         if cpu:
             log(f"cpu baseline {cpu['value']} tok/s on {threads} threads")
 
-    moe_stack = None
+    moe_stack = qwen_stack = None
     if not args.no_stacks:
         moe_stack = moe_stack_configs3(lib)
         log(f"configs[3] MoE stack: {moe_stack['tok_s']} tok/s, {moe_stack['GB_s']} GB/s "
             f"({moe_stack['frac_of_peak']} of peak)")
+        qwen_stack = qwen_stack_configs4(lib)
+        log(f"configs[4] qwen35 stack: decode {qwen_stack['decode_tok_s']} tok/s ({qwen_stack['frac_of_peak']} of "
+            f"peak), prefill {qwen_stack['prefill_tok_s']} tok/s")
 
     line = {
         "metric": "decode tok/s bs1 @ctx1024; Q4_K GEMV achieved HBM GB/s as % of peak",
@@ -512,6 +570,7 @@ def main():
         "configs4_layer_ops": qw,
         "configs2_prefill_gemm": pre,
         "configs3_moe_stack": moe_stack,
+        "configs4_qwen_stack": qwen_stack,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
