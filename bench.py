@@ -212,6 +212,49 @@ def qwen35_ops_configs4(lib, told=4096, iters=50):
     return res
 
 
+def llama_bytes_per_token(model, first_pos, n_gen):
+    """Algorithmic HBM bytes of one decode token of a llama-family model: every
+    layer matrix and the head once, one embedding row, and the K / V rows read
+    (mean over positions first_pos .. first_pos + n_gen - 1, rows 0..pos)."""
+    cfg = model.cfg
+    T = model.tensors
+    layers = sum(v[0].nbytes for k, v in T.items() if k.startswith("blk."))
+    head = model.head()[0].nbytes
+    emb_row = T["token_embd.weight"][0].nbytes // cfg.vocab
+    rows = np.arange(first_pos, first_pos + n_gen) + 1
+    kv = cfg.n_layer * 2 * cfg.n_kv * cfg.head_dim * 4 * float(rows.mean())
+    return layers + head + emb_row + kv
+
+
+def smol_decode_configs0(lib):
+    """SmolLM2-360M-shaped Q8_0, 32-token prompt + 64 greedy tokens
+    on the device loop (graph-replayed); tokens checked against the reference
+    golden; tok/s and GB/s against the HBM roof."""
+    import ctypes as ct
+    from dracohip import models
+    from dracohip.driver import LlamaDriver, hip_engine_lib
+    cfg = models.SMOL360M
+    model = models.build_llama(cfg, 0)
+    L = lib.load()
+    drv = LlamaDriver(model, hip_engine_lib())
+    drv.generate_device(model.prompt(), cfg.n_gen)
+    drv.reset()
+    L.draco_state_push(ct.cast(drv.descs, ct.c_void_p), drv.NL)
+    toks, _, (dec_ms, _) = drv.generate_device(model.prompt(), cfg.n_gen)
+    gpath = os.path.join(ROOT, "tests", "golden", "smol360m.npz")
+    match = bool(list(np.load(gpath)["tokens"]) == toks) if os.path.exists(gpath) else None
+    per_tok = llama_bytes_per_token(model, cfg.n_prompt - 1, cfg.n_gen)
+    tok_s = cfg.n_gen / (dec_ms / 1e3)
+    res = {"tok_s": round(tok_s, 1), "ms_per_token": round(dec_ms / cfg.n_gen, 4), "bytes_per_token": int(per_tok),
+           "GB_s": round(per_tok * tok_s / 1e9, 1), "frac_of_peak": round(per_tok * tok_s / 1e9 / PEAK_HBM_GBS, 4),
+           "roof_tok_s": round(PEAK_HBM_GBS * 1e9 / per_tok, 1), "greedy_tokens_match_reference": match,
+           "shape": "SmolLM2-360M: hidden 960, 32 layers, 15/5 x 64, FFN 2560, vocab 49152, all Q8_0; "
+                    "32-token prompt, 64 greedy tokens"}
+    del drv, model
+    L.draco_reset()
+    return res
+
+
 def moe_stack_configs3(lib, seed=3):
     """the 48-layer Qwen3-30B-A3B-shaped MoE stack (attention 32 q /
     4 kv heads of 128, Q6_K; MoE FFN 128 experts, top 8, FFN 768, Q4_K experts,
@@ -380,6 +423,75 @@ def cpu_baseline_worker(args):
     print(json.dumps({"tokens": n, "seconds": dt, "threads": int(os.environ.get("OMP_NUM_THREADS", "0"))}))
 
 
+def cpu_gemv_worker(args):
+    """Child process: the reference's AVX-512 Q4_K row kernel (m5_gemvn_q4k,
+    src/m5/m5_batch8_k.c:80-114, compiled from source into oracle/_ref) on the
+    configs[1] shapes at batch 1.  Its row loop ignores the row-block bounds
+    it is handed (every OpenMP unit would recompute all rows), so the matrix
+    is passed as 64-row slices, one slice per "expert" with x shared: each
+    unit computes its own 64 rows once.  Weights rotate over copies totalling
+    more than any host L3; median of 15 timed calls after 5 warm-ups."""
+    import ctypes as ct
+    from dracohip import lib
+    from oracle.oracle import REF_DIR
+    B = ct.CDLL(os.path.join(REF_DIR, "libref_batch8k.so"))
+    fn = B.m5_gemvn_q4k
+    fn.restype = ct.c_int
+    fn.argtypes = [ct.c_void_p, ct.c_long, ct.c_void_p, ct.c_void_p, ct.c_long, ct.c_int, ct.c_int, ct.c_int,
+                   ct.c_void_p]
+    out = {}
+    for n_out, n_in in ((14336, 4096), (4096, 14336)):
+        rng = np.random.default_rng(1)
+        W = lib.quantize(5, rng.standard_normal((n_out, n_in), dtype=np.float32) * np.float32(0.02))
+        copies = [W] + [W.copy() for _ in range(11)]  # 12 x 33 MB
+        x = rng.standard_normal(n_in).astype(np.float32)
+        y = np.zeros(n_out, np.float32)
+        rows = 64
+        idx = np.arange(n_out // rows, dtype=np.int32)
+        per = rows * (n_in // 256) * 144
+        times = []
+        for i in range(20):
+            w = copies[i % len(copies)]
+            t0 = time.perf_counter()
+            rc = fn(x.ctypes.data, 0, w.ctypes.data, idx.ctypes.data, per, rows, n_in, len(idx), y.ctypes.data)
+            dt = time.perf_counter() - t0
+            assert rc == 0
+            if i >= 5:
+                times.append(dt)
+        t = float(np.median(times))
+        out[f"{n_out}x{n_in}"] = {"us": round(t * 1e6, 1), "GB_s": round(W.nbytes / t / 1e9, 2)}
+    print(json.dumps(out))
+
+
+def cpu_host_info():
+    info = {"nproc": os.cpu_count(), "affinity_cpus": len(os.sched_getaffinity(0))}
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    info["cpu_model"] = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    for path in ("/sys/devices/system/cpu/cpu0/cpufreq/scaling_governor",):
+        try:
+            with open(path) as f:
+                info["governor"] = f.read().strip()
+        except OSError:
+            info["governor"] = "unavailable"
+    return info
+
+
+def run_cpu_gemv(threads):
+    env = dict(os.environ, OMP_NUM_THREADS=str(threads), OMP_PROC_BIND="false")
+    cmd = [sys.executable, os.path.abspath(__file__), "--cpu-gemv-worker"]
+    r = subprocess.run(cmd, env=env, capture_output=True, text=True, timeout=600)
+    if r.returncode != 0:
+        log("cpu gemv baseline failed:", r.stderr[-2000:])
+        return None
+    return json.loads(r.stdout.strip().splitlines()[-1])
+
+
 def run_cpu_baseline(drv, cfg, first_token, threads, cpu_tokens, cpu_seconds):
     """Pull the GPU's KV at context CTX_START and time the reference engine from there."""
     import ctypes as ct
@@ -428,10 +540,13 @@ def main():
     ap.add_argument("--no-roofline", action="store_true", help="skip the GEMV roofline measurement (profiling runs)")
     ap.add_argument("--no-stacks", action="store_true", help="skip the configs[3] / configs[4] layer stacks")
     ap.add_argument("--cpu-baseline-worker", action="store_true")
+    ap.add_argument("--cpu-gemv-worker", action="store_true")
     ap.add_argument("--kv-file")
     args = ap.parse_args()
     if args.cpu_baseline_worker:
         return cpu_baseline_worker(args)
+    if args.cpu_gemv_worker:
+        return cpu_gemv_worker(args)
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build runs on exactly one GPU (--gpus 1); multi-GPU runs are not part "
               "of it", file=sys.stderr)
@@ -511,6 +626,12 @@ def main():
         n = min(len(toks_first), len(g["tokens"]))
         match = bool(list(g["tokens"][:n]) == toks_first[:n])
     log(f"decode {tok_s:.1f} tok/s; greedy tokens match reference: {match}")
+    # the decode path against the HBM roof: algorithmic bytes of one token
+    # (every weight once, one embedding row, the K / V rows read) x tok/s
+    per_tok = llama_bytes_per_token(model, CTX_START - 1, min(args.steps, MAX_DECODE))
+    decode_roof = {"bound": "hbm", "bytes_per_token": int(per_tok), "achieved_GB_s": round(per_tok * tok_s / 1e9, 1),
+                   "peak_GB_s": PEAK_HBM_GBS, "frac": round(per_tok * tok_s / 1e9 / PEAK_HBM_GBS, 4),
+                   "roof_tok_s": round(PEAK_HBM_GBS * 1e9 / per_tok, 1)}
 
     roof = q8 = moe = shx = gdn = pre = qw = None
     if not args.no_roofline:
@@ -535,15 +656,27 @@ def main():
 
     cpu = None
     if not args.no_cpu_baseline:
-        threads = args.cpu_threads or min(16, os.cpu_count() or 1)
+        # all the cores this process may use (the GPU box grants 16), and one
+        threads = args.cpu_threads or min(16, len(os.sched_getaffinity(0)) or 1)
         # first decode token after the prompt: feed it through the CPU engine from CTX_START
         run(1)
         cpu = run_cpu_baseline(drv, cfg, toks_first[0], threads, args.cpu_tokens, args.cpu_seconds)
         if cpu:
             log(f"cpu baseline {cpu['value']} tok/s on {threads} threads")
+            one = run_cpu_baseline(drv, cfg, toks_first[0], 1, args.cpu_tokens, args.cpu_seconds / 2)
+            if one:
+                cpu["one_thread"] = {"value": one["value"], "unit": "tok/s", "sample": one["sample"]}
+                log(f"cpu baseline {one['value']} tok/s on 1 thread")
+            gemv = {f"threads_{t}": run_cpu_gemv(t) for t in (threads, 1)}
+            cpu["gemv_q4k_avx512_bs1"] = gemv
+            cpu["host"] = cpu_host_info()
+            log(f"cpu AVX-512 Q4_K GEMV: {gemv}")
 
-    moe_stack = qwen_stack = None
+    moe_stack = qwen_stack = smol = None
     if not args.no_stacks:
+        smol = smol_decode_configs0(lib)
+        log(f"configs[0] SmolLM2-360M decode: {smol['tok_s']} tok/s ({smol['frac_of_peak']} of peak), tokens match "
+            f"reference: {smol['greedy_tokens_match_reference']}")
         moe_stack = moe_stack_configs3(lib)
         log(f"configs[3] MoE stack: {moe_stack['tok_s']} tok/s, {moe_stack['GB_s']} GB/s "
             f"({moe_stack['frac_of_peak']} of peak)")
@@ -561,6 +694,8 @@ def main():
                                "positions 960..1023", "global_batch": 1, "seq_len": 1024,
                    "parallelism": "single GPU"},
         "greedy_tokens_match_reference": match,
+        "decode_roofline": decode_roof,
+        "configs0_decode": smol,
         "configs2_prefill": prefill,
         "roofline": roof,
         "configs1_q8k_gemv": q8,
