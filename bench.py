@@ -538,7 +538,9 @@ def main():
                     help="run the decode loop without HIP graphs (for profilers that cannot trace graphs)")
     ap.add_argument("--roofline-only", action="store_true", help="only the Q4_K GEMV roofline measurement")
     ap.add_argument("--no-roofline", action="store_true", help="skip the GEMV roofline measurement (profiling runs)")
-    ap.add_argument("--no-stacks", action="store_true", help="skip the configs[3] / configs[4] layer stacks")
+    ap.add_argument("--no-stacks", action="store_true", help="skip the configs[0] / [3] / [4] decode legs")
+    ap.add_argument("--no-serial-prefill", action="store_true",
+                    help="skip the token-serial prompt run (the chunked prefill is the measured one)")
     ap.add_argument("--cpu-baseline-worker", action="store_true")
     ap.add_argument("--cpu-gemv-worker", action="store_true")
     ap.add_argument("--kv-file")
@@ -611,14 +613,17 @@ def main():
     # through the 256-token chunked prefill, and once token by token for scale
     n_pre = len(prompt) - 1
     chunk = L.draco_set_prefill_chunk(-1)
-    L.draco_set_prefill_chunk(0)
-    _, _, (_, serial_ms) = run(1)
-    L.draco_set_prefill_chunk(chunk)
+    serial_ms = None
+    if not args.no_serial_prefill:
+        L.draco_set_prefill_chunk(0)
+        _, _, (_, serial_ms) = run(1)
+        L.draco_set_prefill_chunk(chunk)
     pre_ms = float(np.median(pre_list))
     prefill = {"prompt_tokens": n_pre, "chunk": chunk, "ms": round(pre_ms, 3),
-               "tok_s": round(n_pre / (pre_ms / 1e3), 1), "token_serial_ms": round(serial_ms, 3),
-               "token_serial_tok_s": round(n_pre / (serial_ms / 1e3), 1)}
-    log(f"prefill {n_pre} tokens: chunked {pre_ms:.1f} ms, token-serial {serial_ms:.1f} ms")
+               "tok_s": round(n_pre / (pre_ms / 1e3), 1),
+               "token_serial_ms": round(serial_ms, 3) if serial_ms else None,
+               "token_serial_tok_s": round(n_pre / (serial_ms / 1e3), 1) if serial_ms else None}
+    log(f"prefill {n_pre} tokens: chunked {pre_ms:.1f} ms, token-serial {serial_ms} ms")
     match = None
     gpath = os.path.join(ROOT, "tests", "golden", "llama1b.npz")
     if os.path.exists(gpath):

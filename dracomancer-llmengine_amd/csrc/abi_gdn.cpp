@@ -22,7 +22,8 @@ int gdn_host(const float* QKV, const float* Z, const float* B, const float* G, c
     hipStream_t st = stream();
     const size_t nq = (size_t)T * n_qkv, nz = (size_t)T * n_vh * 128, nbg = (size_t)T * n_vh,
                  ns = (size_t)n_vh * 128 * 128, nt = (size_t)n_qkv * 3, nc = (size_t)n_qkv * 4;
-    float* d = (float*)scratch(6, sizeof(float) * (nq + 2 * nz + 2 * nbg + ns + nt + nc + 128));
+    const size_t npss = (size_t)T * n_vh * 8;
+    float* d = (float*)scratch(6, sizeof(float) * (nq + 2 * nz + 2 * nbg + ns + nt + nc + 128 + npss));
     if (!d) return -2;
     GdnArgs a = {};
     float* p = d;
@@ -34,6 +35,7 @@ int gdn_host(const float* QKV, const float* Z, const float* B, const float* G, c
     float* dn = p; p += 128;
     float* dt = p; p += nt;
     float* ds = p; p += ns;
+    float* dpss = p; p += npss;
     float* don = p;
     DRACO_HIP(hipMemcpyAsync(dq, QKV, sizeof(float) * nq, hipMemcpyHostToDevice, st));
     DRACO_HIP(hipMemcpyAsync(dz, Z, sizeof(float) * nz, hipMemcpyHostToDevice, st));
@@ -56,6 +58,8 @@ int gdn_host(const float* QKV, const float* Z, const float* B, const float* G, c
     a.n_qkv = n_qkv;
     a.n_vh = n_vh;
     a.nhq = (n_qkv - n_vh * 128) / 256;
+    a.nspl = draco_gdn_split(T == 1);  // one token: the decode step's split
+    a.PSS = dpss;
     if (draco_gdn_scan_launch(a, st)) return fail(-1, "gdn scan launch rejected");
     DRACO_HIP(hipGetLastError());
     DRACO_HIP(hipMemcpyAsync(ON, don, sizeof(float) * nz, hipMemcpyDeviceToHost, st));
@@ -94,7 +98,8 @@ int draco_bench_gdn_scan(const float* QKV, const float* Z, const float* B, const
     hipStream_t st = stream();
     const size_t nq = (size_t)T * n_qkv, nz = (size_t)T * n_vh * 128, nbg = (size_t)T * n_vh,
                  ns = (size_t)n_vh * 128 * 128, nt = (size_t)n_qkv * 3, nc = (size_t)n_qkv * 4;
-    float *dq, *dz, *db, *dg, *dc, *dn, *dt, *ds, *don;
+    float *dq, *dz, *db, *dg, *dc, *dn, *dt, *ds, *don, *dpss;
+    DRACO_HIP(hipMalloc(&dpss, sizeof(float) * (size_t)(chunk > 1 ? chunk : 1) * n_vh * 8));
     DRACO_HIP(hipMalloc(&dq, sizeof(float) * nq));
     DRACO_HIP(hipMalloc(&dz, sizeof(float) * nz));
     DRACO_HIP(hipMalloc(&db, sizeof(float) * nbg));
@@ -127,6 +132,8 @@ int draco_bench_gdn_scan(const float* QKV, const float* Z, const float* B, const
         a.n_qkv = n_qkv;
         a.n_vh = n_vh;
         a.nhq = (n_qkv - n_vh * 128) / 256;
+        a.nspl = draco_gdn_split(n == 1);
+        a.PSS = dpss;
         return a;
     };
     hipEvent_t e0, e1;
@@ -160,7 +167,7 @@ int draco_bench_gdn_scan(const float* QKV, const float* Z, const float* B, const
     }
     hipEventDestroy(e0);
     hipEventDestroy(e1);
-    for (float* p : {dq, dz, db, dg, dc, dn, dt, ds, don}) hipFree(p);
+    for (float* p : {dq, dz, db, dg, dc, dn, dt, ds, don, dpss}) hipFree(p);
     return 0;
 }
 

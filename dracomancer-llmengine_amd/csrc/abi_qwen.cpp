@@ -172,7 +172,7 @@ struct GdnDev {
 };
 
 struct GdnBufs {
-    float *h1, *qkv, *z, *on, *x2o, *x2n, *xn, *S, *tail;
+    float *h1, *qkv, *z, *on, *x2o, *x2n, *xn, *S, *tail, *pss;
 };
 
 int gdn_resolve(const GdnW* w, GdnDev& g) {
@@ -202,7 +202,7 @@ int gdn_resolve(const GdnW* w, GdnDev& g) {
 
 int gdn_bufs(const GdnDev& g, int slot, GdnBufs& b) {
     const size_t ns = (size_t)g.n_vh * QSV * QSV, nt = (size_t)g.n_qkv * 3;
-    const size_t n = 5 * (size_t)QH + g.n_qkv + 2 * (size_t)g.d_in + ns + nt + 16 * 64;  // + carve slack
+    const size_t n = 5 * (size_t)QH + g.n_qkv + 2 * (size_t)g.d_in + ns + nt + (size_t)g.n_vh * 8 + 16 * 64;  // + carve slack
     float* p = (float*)scratch(slot, sizeof(float) * n);
     if (!p) return -2;
     auto take = [&](size_t k) {  // 256-byte aligned carve
@@ -219,10 +219,13 @@ int gdn_bufs(const GdnDev& g, int slot, GdnBufs& b) {
     b.on = take(g.d_in);
     b.S = take(ns);
     b.tail = take(nt);
+    b.pss = take((size_t)g.n_vh * 8);
     return 0;
 }
 
-int enqueue_gdn(const GdnDev& g, const GdnBufs& b, hipStream_t st) {
+// post_norm false: x2n is not produced (a stack whose FFN normalises x2_out
+// itself, or has none)
+int enqueue_gdn(const GdnDev& g, const GdnBufs& b, hipStream_t st, bool post_norm = true) {
     const Proj in[2] = {{g.qkv, b.qkv, nullptr}, {g.gate, b.z, nullptr}};
     if (int rc = enqueue_proj(in, 2, b.h1, QH, g.attn_norm, b.xn, st)) return rc;
     GdnArgs a = {};
@@ -244,10 +247,12 @@ int enqueue_gdn(const GdnDev& g, const GdnBufs& b, hipStream_t st) {
     a.ssm_a = g.ssm_a;
     a.ssm_dt = g.ssm_dt;
     a.H = QH;
+    a.nspl = draco_gdn_split(true);
+    a.PSS = b.pss;
     if (draco_gdn_step_launch(a, st)) return fail(-1, "gdn step launch rejected");
     const Proj out[1] = {{g.out, b.x2o, b.h1}};
     const PostNorm pn = {g.post_norm, b.x2n};
-    return enqueue_proj(out, 1, b.on, g.d_in, nullptr, b.xn, st, &pn);
+    return enqueue_proj(out, 1, b.on, g.d_in, nullptr, b.xn, st, post_norm ? &pn : nullptr);
 }
 
 int gdn_host(const float* h1, const GdnW* w, float* ssm, float* tail, float* x2n, float* x2_out) {
@@ -468,14 +473,14 @@ struct QStack {
     // one token
     float *x = nullptr, *x2n = nullptr, *xn = nullptr, *qkv = nullptr, *z = nullptr, *on = nullptr, *QG = nullptr,
           *Qr = nullptr, *kraw = nullptr, *vraw = nullptr, *ao = nullptr, *part = nullptr, *fg = nullptr,
-          *fu = nullptr, *xe = nullptr;
+          *fu = nullptr, *xe = nullptr, *pss = nullptr;
     int* state = nullptr;   // device [pos, told]
     int* hstate = nullptr;  // pinned
     // a prefill chunk of up to pf_cap tokens
     int pf_cap = 0;
     float *X = nullptr, *Xn = nullptr, *QKV = nullptr, *Z = nullptr, *B = nullptr, *G = nullptr, *ON = nullptr,
           *Y = nullptr, *PQG = nullptr, *PQr = nullptr, *PK = nullptr, *PV = nullptr, *AO = nullptr, *Ppart = nullptr,
-          *PG = nullptr, *PU = nullptr;
+          *PG = nullptr, *PU = nullptr, *PPSS = nullptr;
     uint8_t* dig = nullptr;
     int* ids = nullptr;
     std::vector<void*> allocs, pf_allocs;
@@ -638,7 +643,8 @@ QStack* build_qstack(const QStackLayer* layers, int n_layer, int h) {
         qstack_alloc(k, &s->ao, (size_t)std::max(s->max_nh, 1) * FHD) || qstack_alloc(k, &s->kraw, FNKV * FHD) ||
         qstack_alloc(k, &s->vraw, FNKV * FHD) ||
         qstack_alloc(k, &s->part, (size_t)std::max(s->max_nh, 1) * nsplit * (FHD + 2)) ||
-        qstack_alloc(k, &s->fg, std::max(s->max_ff, 1)) || qstack_alloc(k, &s->fu, std::max(s->max_ff, 1)))
+        qstack_alloc(k, &s->fg, std::max(s->max_ff, 1)) || qstack_alloc(k, &s->fu, std::max(s->max_ff, 1)) ||
+        qstack_alloc(k, &s->pss, (size_t)std::max(s->max_vh, 1) * 8))
         return nullptr;
     if (hipMalloc(&s->state, sizeof(int) * 16) != hipSuccess ||
         hipHostMalloc(&s->hstate, sizeof(int) * 16, hipHostMallocDefault) != hipSuccess) {
@@ -669,7 +675,8 @@ int qstack_pf(QStack* s, int cap) {
         qstack_alloc(k, &s->PQG, c * nh * 2 * FHD) || qstack_alloc(k, &s->PQr, c * nh * FHD) ||
         qstack_alloc(k, &s->PK, c * FNKV * FHD) || qstack_alloc(k, &s->PV, c * FNKV * FHD) ||
         qstack_alloc(k, &s->AO, c * nh * FHD) || qstack_alloc(k, &s->Ppart, pf_part_floats(nh, cap, FHD, nspl)) ||
-        qstack_alloc(k, &s->PG, c * std::max(s->max_ff, 1)) || qstack_alloc(k, &s->PU, c * std::max(s->max_ff, 1)))
+        qstack_alloc(k, &s->PG, c * std::max(s->max_ff, 1)) || qstack_alloc(k, &s->PU, c * std::max(s->max_ff, 1)) ||
+        qstack_alloc(k, &s->PPSS, c * std::max(s->max_vh, 1) * 8))
         return -2;
     if (hipMalloc(&s->dig, draco_gemm_digit_bytes(cap, ((win + 255) / 256) * 256)) != hipSuccess ||
         hipMalloc(&s->ids, sizeof(int) * c) != hipSuccess)
@@ -680,12 +687,15 @@ int qstack_pf(QStack* s, int cap) {
     return 0;
 }
 
-// the FFN of one token: x += FFN(x2n) (x holds x2_out)
+// the FFN of one token: x += FFN(x2n), x2n = RMSNorm(x2_out) * post_norm
+// formed by the FFN's own first launch (x holds x2_out): the MoE's norm
+// launch, or the gate/up GEMV's RMSNorm prologue
 int enqueue_qffn(QStack* s, QLayer& q, hipStream_t st) {
     if (q.desc.ffn_kind == QFFN_NONE) return 0;
-    if (q.desc.ffn_kind == QFFN_MOE) return draco_moe_layer_enqueue_xn(q.moe, s->x2n, s->x, s->x, st);
+    const float* pn = q.desc.kind == 0 ? q.g.post_norm : q.f.post_norm;
+    if (q.desc.ffn_kind == QFFN_MOE) return draco_moe_layer_enqueue(q.moe, s->x, pn, QEPS, s->x, s->x, st);
     const Proj gu[2] = {{q.fg, s->fg, nullptr}, {q.fu, s->fu, nullptr}};
-    if (int rc = enqueue_proj(gu, 2, s->x2n, QH, nullptr, s->xn, st)) return rc;
+    if (int rc = enqueue_proj(gu, 2, s->x, QH, pn, s->xn, st)) return rc;
     dk_swiglu(s->fg, s->fu, q.FF, st);
     const Proj dn[1] = {{q.fd, s->x, s->x}};
     return enqueue_proj(dn, 1, s->fg, q.FF, nullptr, s->xn, st);
@@ -710,7 +720,8 @@ int enqueue_qtoken(QStack* s, hipStream_t st, float* xin = nullptr) {
             b.xn = s->xn;
             b.S = q.S;
             b.tail = q.tail;
-            if (int rc = enqueue_gdn(q.g, b, st)) return rc;
+            b.pss = s->pss;
+            if (int rc = enqueue_gdn(q.g, b, st, false)) return rc;
         } else {
             const FullDev& f = q.f;
             const Proj in[3] = {{f.q, s->QG, nullptr}, {f.k, s->kraw, nullptr}, {f.v, s->vraw, nullptr}};
@@ -721,8 +732,7 @@ int enqueue_qtoken(QStack* s, hipStream_t st, float* xin = nullptr) {
                              1.f / sqrtf((float)FHD), st, s->QG + FHD, 2 * FHD))
                 return fail(-1, "qwen stack: attention launch rejected");
             const Proj out[1] = {{f.o, s->x, x0}};
-            const PostNorm pn = {f.post_norm, s->x2n};
-            if (int rc = enqueue_proj(out, 1, s->ao, f.nh * FHD, nullptr, s->xn, st, &pn)) return rc;
+            if (int rc = enqueue_proj(out, 1, s->ao, f.nh * FHD, nullptr, s->xn, st)) return rc;
         }
         if (int rc = enqueue_qffn(s, q, st)) return rc;
     }
@@ -767,6 +777,8 @@ int enqueue_qchunk(QStack* s, int T, int pos0, hipStream_t st) {
             a.n_qkv = g.n_qkv;
             a.n_vh = g.n_vh;
             a.nhq = QNKH;
+            a.nspl = draco_gdn_split(T == 1);
+            a.PSS = s->PPSS;
             if (draco_gdn_scan_launch(a, st)) return fail(-1, "qwen prefill: scan rejected");
             if (draco_enqueue_gemm(*g.out, s->ON, T, s->Y, s->dig, false, st)) return -1;
             if (pf_add_rms(s->X, s->Y, g.post_norm, s->Xn, T, QH, QEPS, st)) return fail(-1, "qwen prefill: rms");

@@ -22,7 +22,15 @@ struct GdnArgs {
     const float* ssm_a;      // [n_vh]
     const float* ssm_dt;     // [n_vh]
     int H;                   // <= 4096, multiple of 4
+    // column split: nspl blocks per V head (1, 2, 4 or 8; 0 = 1).  Above 1
+    // the gated rms runs in a second launch and needs PSS [T][n_vh][8] floats.
+    int nspl;
+    float* PSS;
 };
+
+// blocks per V head for the decode step / for scans of several tokens
+// (draco_set_gdn_split changes them)
+int draco_gdn_split(bool decode);
 
 int draco_gdn_scan_launch(const GdnArgs& a, hipStream_t st);
 // One decode token (T must be 1): the scan step with beta = sigmoid(xn.bw),

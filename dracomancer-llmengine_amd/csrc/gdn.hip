@@ -9,18 +9,30 @@
 //   on = (o/sqrt(128)) * rsqrt(mean(o^2)+1e-6) * ssm_norm * silu(z)
 // S is [k][v] (row k), 128 x 128 fp32 per V head.
 //
-// Mapping: one block of 8 waves per V head for the whole scan; the state
-// lives in registers.  Wave w owns columns v = 16w .. 16w+15; lane
-// (v_lo = lane>>2, kq = lane&3) holds S[32kq .. 32kq+31][16w + v_lo].  Each
-// lane applies the reference's per-element operations in k order within its
-// chunk (decay, multiply, add, unfused); the four chunks of a column combine
-// with DPP moves, so the delta rule needs no LDS and no barrier.  The conv
-// runs on threads 0..383 (one channel each: q, k of head j and v of head h,
-// tail in registers); only the block that owns a channel writes its tail back
-// (q/k channels: the block with h < NHQ).  l2 norms and the gated rms reduce
-// across waves through LDS.  Results agree with the reference to fp32
-// rounding: the per-column sums are split in four chunks and the l2 / rms sums
-// use a tree.
+// Mapping: the 128 columns of a V head's state are split over NSPL = 8 / NW
+// blocks of NW waves (grid n_vh x NSPL); every block keeps its columns of the
+// state in registers for the whole scan.  Wave w of split sp owns columns
+// v = 16 (sp NW + w) .. +15; lane (v_lo = lane>>2, kq = lane&3) holds
+// S[32kq .. 32kq+31][v].  Each lane applies the reference's per-element
+// operations in k order within its chunk (decay, multiply, add, unfused); the
+// four chunks of a column combine with DPP moves, so the delta rule needs no
+// LDS and no barrier.  The conv runs on the block's threads, channel c =
+// tid + r * threads (q and k of head j in every block: the l2 norms need
+// them whole; v only for the block's columns), the tails in registers; only
+// the block that owns a channel writes its tail back (q/k channels: split 0
+// of a head with h < NHQ).  The l2 norms reduce across the block's waves
+// through LDS.  The gated rms needs all 128 columns of a head: with one
+// block per head (NW = 8) it is finished in the block; split across blocks,
+// each wave writes its columns' o / sqrt(128) to ON and the sum of their
+// squares to a partial buffer, and k_gdn_gnorm applies the rms, the norm
+// weight and the gate in place.  Results agree with the reference to fp32
+// rounding: the per-column sums are split in four chunks and the l2 / rms
+// sums use a tree.
+//
+// The split spreads each head's 64 KB of state over NSPL CUs (the state load
+// and store at the ends of a launch run NSPL-wide) and gives a long scan one
+// in-block barrier per token fewer with fewer waves behind each (the rms
+// needs none when split); the defaults below are the measured best.
 #include <hip/hip_runtime.h>
 
 #include "dev_common.h"
@@ -37,38 +49,64 @@ __device__ __forceinline__ float silu(float a) { return a / (1.f + expf(-a)); }
 // returns beta and the decay exp(alpha).  xn = h1 * rms^-1 * attn_norm is
 // recomputed by each block (H floats, L2-resident after the first block);
 // the beta / alpha rows are contiguous [n_vh][H], read once per block.
+template <int NW>
 __device__ __forceinline__ void gdn_gates(const GdnArgs& a, int h, int tid, float* beta, float* gdec) {
-    __shared__ float pre[3][8];
+    constexpr int NT = 64 * NW;
+    // float4 per thread covering H <= 4096; wide blocks hold them in
+    // registers, narrow ones (NV > 2) stream them in two passes
+    constexpr int NV = (4096 + 4 * NT - 1) / (4 * NT);
+    constexpr int NR = NV <= 2 ? NV : 1;
+    __shared__ float pre[3][NW];
     const int lane = tid & 63, w = tid >> 6;
-    float4 hv[2], nv[2], bv[2], av[2];
-#pragma unroll
-    for (int k = 0; k < 2; k++) {  // clamped, unconditional loads; masked below
-        const int i = 4 * tid + 2048 * k;
+    float4 hv[NR], nv[NR], bv[NR], av[NR];
+    auto load = [&](int k, int slot) {  // clamped, unconditional loads; masked below
+        const int i = 4 * tid + 4 * NT * k;
         const int ic = i < a.H ? i : 0;
-        hv[k] = ld4(a.h1 + ic);
-        nv[k] = ld4(a.attn_norm + ic);
-        bv[k] = ld4(a.bw + (size_t)h * a.H + ic);
-        av[k] = ld4(a.aw + (size_t)h * a.H + ic);
-    }
+        hv[slot] = ld4(a.h1 + ic);
+        nv[slot] = ld4(a.attn_norm + ic);
+        bv[slot] = ld4(a.bw + (size_t)h * a.H + ic);
+        av[slot] = ld4(a.aw + (size_t)h * a.H + ic);
+    };
     float ss = 0.f;
+    if constexpr (NR == NV) {
 #pragma unroll
-    for (int k = 0; k < 2; k++)
-        if (4 * tid + 2048 * k < a.H) ss += hv[k].x * hv[k].x + hv[k].y * hv[k].y + hv[k].z * hv[k].z + hv[k].w * hv[k].w;
+        for (int k = 0; k < NV; k++) load(k, k);
+#pragma unroll
+        for (int k = 0; k < NV; k++)
+            if (4 * tid + 4 * NT * k < a.H)
+                ss += hv[k].x * hv[k].x + hv[k].y * hv[k].y + hv[k].z * hv[k].z + hv[k].w * hv[k].w;
+    } else {
+        for (int k = 0; k < NV; k++) {
+            const int i = 4 * tid + 4 * NT * k;
+            if (i < a.H) {
+                const float4 x = ld4(a.h1 + i);
+                ss += x.x * x.x + x.y * x.y + x.z * x.z + x.w * x.w;
+            }
+        }
+    }
     ss = wave_sum(ss);
     if (lane == 0) pre[0][w] = ss;
     lds_barrier();
     float tot = 0.f;
 #pragma unroll
-    for (int q = 0; q < 8; q++) tot += pre[0][q];
+    for (int q = 0; q < NW; q++) tot += pre[0][q];
     const float inv = 1.f / sqrtf(tot / (float)a.H + EPS);
     float pb = 0.f, pa = 0.f;
+    auto acc = [&](int k, int slot) {
+        if (4 * tid + 4 * NT * k < a.H) {
+            const float x0 = hv[slot].x * inv * nv[slot].x, x1 = hv[slot].y * inv * nv[slot].y;
+            const float x2 = hv[slot].z * inv * nv[slot].z, x3 = hv[slot].w * inv * nv[slot].w;
+            pb += bv[slot].x * x0 + bv[slot].y * x1 + bv[slot].z * x2 + bv[slot].w * x3;
+            pa += av[slot].x * x0 + av[slot].y * x1 + av[slot].z * x2 + av[slot].w * x3;
+        }
+    };
+    if constexpr (NR == NV) {
 #pragma unroll
-    for (int k = 0; k < 2; k++) {
-        if (4 * tid + 2048 * k < a.H) {
-            const float x0 = hv[k].x * inv * nv[k].x, x1 = hv[k].y * inv * nv[k].y;
-            const float x2 = hv[k].z * inv * nv[k].z, x3 = hv[k].w * inv * nv[k].w;
-            pb += bv[k].x * x0 + bv[k].y * x1 + bv[k].z * x2 + bv[k].w * x3;
-            pa += av[k].x * x0 + av[k].y * x1 + av[k].z * x2 + av[k].w * x3;
+        for (int k = 0; k < NV; k++) acc(k, k);
+    } else {
+        for (int k = 0; k < NV; k++) {
+            load(k, 0);
+            acc(k, 0);
         }
     }
     pb = wave_sum(pb);
@@ -80,7 +118,7 @@ __device__ __forceinline__ void gdn_gates(const GdnArgs& a, int h, int tid, floa
     lds_barrier();
     float bacc = 0.f, aacc = 0.f;
 #pragma unroll
-    for (int q = 0; q < 8; q++) {
+    for (int q = 0; q < NW; q++) {
         bacc += pre[1][q];
         aacc += pre[2][q];
     }
@@ -90,30 +128,43 @@ __device__ __forceinline__ void gdn_gates(const GdnArgs& a, int h, int tid, floa
     *gdec = expf(sp * a.ssm_a[h]);
 }
 
-template <bool DEC>
-__global__ __launch_bounds__(512) void k_gdn_scan(const GdnArgs a) {
-    __shared__ float cq[SV], ck[SV], cv[SV];   // conv outputs of this token (q, k normalised in place)
-    __shared__ float red[2][8];
-    __shared__ float ored[8];
-    const int h = blockIdx.x, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+template <bool DEC, int NW>
+__global__ __launch_bounds__(64 * NW) void k_gdn_scan(const GdnArgs a) {
+    constexpr int NT = 64 * NW, NSPL = 8 / NW, NC = 16 * NW;  // threads, splits per head, columns per block
+    constexpr int CH = 2 * SV + NC;                            // conv channels of a block
+    constexpr int R = (CH + NT - 1) / NT;                      // channels per thread
+    __shared__ float cq[SV], ck[SV], cv[NC];  // conv outputs of this token (q, k normalised in place)
+    __shared__ float red[2][NW];
+    __shared__ float ored[NW];
+    const int h = blockIdx.x, sp = blockIdx.y, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int NHQ = a.nhq, n_qkv = a.n_qkv, n_vh = a.n_vh, T = a.T;
     const int j = h % NHQ;
-    // conv channel of this thread: 0..127 q_j, 128..255 k_j, 256..383 v_h
-    int ch = -1;
-    if (tid < SV) ch = j * SV + tid;
-    else if (tid < 2 * SV) ch = NHQ * SV + j * SV + (tid - SV);
-    else if (tid < 3 * SV) ch = 2 * NHQ * SV + h * SV + (tid - 2 * SV);
-    const bool owner = tid >= 2 * SV ? true : (h < NHQ);
-    float w0 = 0.f, w1 = 0.f, w2 = 0.f, w3 = 0.f, t0 = 0.f, t1 = 0.f, t2 = 0.f;
-    if (ch >= 0) {
-        const float4 cw = ld4(a.conv + (size_t)ch * 4);
-        w0 = cw.x; w1 = cw.y; w2 = cw.z; w3 = cw.w;
-        t0 = a.tail[(size_t)ch * 3];
-        t1 = a.tail[(size_t)ch * 3 + 1];
-        t2 = a.tail[(size_t)ch * 3 + 2];
+    const int col0 = sp * NC;  // this block's first column of the head
+    // conv channels of this thread: local c = tid + r * NT; 0..127 q_j,
+    // 128..255 k_j, 256.. v_h columns col0 ..
+    int ch[R];
+    bool own[R];
+    float w0[R], w1[R], w2[R], w3[R], t0[R], t1[R], t2[R], xin[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        const int c = tid + r * NT;
+        ch[r] = -1;
+        if (c < SV) ch[r] = j * SV + c;
+        else if (c < 2 * SV) ch[r] = NHQ * SV + j * SV + (c - SV);
+        else if (c < CH) ch[r] = 2 * NHQ * SV + h * SV + col0 + (c - 2 * SV);
+        own[r] = c >= 2 * SV ? true : (h < NHQ && sp == 0);
+        w0[r] = w1[r] = w2[r] = w3[r] = t0[r] = t1[r] = t2[r] = xin[r] = 0.f;
+        if (ch[r] >= 0) {
+            const float4 cw = ld4(a.conv + (size_t)ch[r] * 4);
+            w0[r] = cw.x; w1[r] = cw.y; w2[r] = cw.z; w3[r] = cw.w;
+            t0[r] = a.tail[(size_t)ch[r] * 3];
+            t1[r] = a.tail[(size_t)ch[r] * 3 + 1];
+            t2[r] = a.tail[(size_t)ch[r] * 3 + 2];
+            if (T > 0) xin[r] = a.QKV[ch[r]];
+        }
     }
     // state slice
-    const int vl = lane >> 2, kq = lane & 3, v = 16 * w + vl;
+    const int vl = lane >> 2, kq = lane & 3, vloc = 16 * w + vl, v = col0 + vloc;
     float* Sh = a.S + (size_t)h * SV * SV;
     float s[32];
 #pragma unroll
@@ -122,45 +173,65 @@ __global__ __launch_bounds__(512) void k_gdn_scan(const GdnArgs a) {
     const float scale = 1.f / sqrtf((float)SV);
 
     // per-token inputs, prefetched one token ahead
-    float xin = ch >= 0 && T > 0 ? a.QKV[ch] : 0.f;
     float zin = T > 0 ? a.Z[(size_t)h * SV + v] : 0.f;
     float gin = 0.f, bin = 0.f;
     if constexpr (DEC) {
-        gdn_gates(a, h, tid, &bin, &gin);
+        gdn_gates<NW>(a, h, tid, &bin, &gin);
     } else {
         gin = T > 0 ? a.G[h] : 0.f;
         bin = T > 0 ? a.B[h] : 0.f;
     }
     for (int t = 0; t < T; t++) {
-        const float x = xin, z = zin, g = gin, b = bin;
+        const float z = zin, g = gin, b = bin;
+        float x[R];
+#pragma unroll
+        for (int r = 0; r < R; r++) x[r] = xin[r];
         if (!DEC && t + 1 < T) {
-            xin = ch >= 0 ? a.QKV[(size_t)(t + 1) * n_qkv + ch] : 0.f;
+#pragma unroll
+            for (int r = 0; r < R; r++)
+                if (ch[r] >= 0) xin[r] = a.QKV[(size_t)(t + 1) * n_qkv + ch[r]];
             zin = a.Z[(size_t)(t + 1) * n_vh * SV + (size_t)h * SV + v];
             gin = a.G[(size_t)(t + 1) * n_vh + h];
             bin = a.B[(size_t)(t + 1) * n_vh + h];
         }
-        // (1) conv + silu (src/m6_gdn_scan.c:30-38)
-        float c = 0.f;
-        if (ch >= 0) {
-            const float acc = w0 * t0 + w1 * t1 + w2 * t2 + w3 * x;
-            c = silu(acc);
-            t0 = t1;
-            t1 = t2;
-            t2 = x;
+        // (1) conv + silu (src/m6_gdn_scan.c:30-38); (2) squares for the l2 norms
+        float c[R];
+        float sqq = 0.f, sqk = 0.f;
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            c[r] = 0.f;
+            if (ch[r] >= 0) {
+                const float acc = w0[r] * t0[r] + w1[r] * t1[r] + w2[r] * t2[r] + w3[r] * x[r];
+                c[r] = silu(acc);
+                t0[r] = t1[r];
+                t1[r] = t2[r];
+                t2[r] = x[r];
+            }
+            const int cl = tid + r * NT;
+            if (cl < SV) sqq += c[r] * c[r];
+            else if (cl < 2 * SV) sqk += c[r] * c[r];
         }
-        // (2) l2 norms of q (waves 0,1) and k (waves 2,3)
-        float sq = tid < 2 * SV ? c * c : 0.f;
-        sq = wave_sum(sq);
-        if (lane == 0 && w < 4) red[w >> 1][w & 1] = sq;
+        sqq = wave_sum(sqq);
+        sqk = wave_sum(sqk);
+        if (lane == 0) {
+            red[0][w] = sqq;
+            red[1][w] = sqk;
+        }
         lds_barrier();
-        if (tid < 2 * SV) {
-            const float n2 = red[w >> 1][0] + red[w >> 1][1];
-            const float nr = sqrtf(n2);
-            const float inv = 1.f / (nr > EPS ? nr : EPS);
-            if (tid < SV) cq[tid] = c * inv;
-            else ck[tid - SV] = c * inv;
-        } else if (tid < 3 * SV) {
-            cv[tid - 2 * SV] = c;
+        float nq = 0.f, nk = 0.f;
+#pragma unroll
+        for (int q = 0; q < NW; q++) {
+            nq += red[0][q];
+            nk += red[1][q];
+        }
+        const float rq = sqrtf(nq), rk = sqrtf(nk);
+        const float iq = 1.f / (rq > EPS ? rq : EPS), ik = 1.f / (rk > EPS ? rk : EPS);
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const int cl = tid + r * NT;
+            if (cl < SV) cq[cl] = c[r] * iq;
+            else if (cl < 2 * SV) ck[cl - SV] = c[r] * ik;
+            else if (cl < CH) cv[cl - 2 * SV] = c[r];
         }
         lds_barrier();
         // (3) delta rule on this lane's 32 rows of column v
@@ -171,7 +242,7 @@ __global__ __launch_bounds__(512) void k_gdn_scan(const GdnArgs a) {
             sk = sk + s[i] * ck[32 * kq + i];
         }
         sk = group_sum<4>(sk);
-        const float d = (cv[v] - sk) * b;
+        const float d = (cv[vloc] - sk) * b;
         float o = 0.f;
 #pragma unroll
         for (int i = 0; i < 32; i++) {
@@ -183,37 +254,93 @@ __global__ __launch_bounds__(512) void k_gdn_scan(const GdnArgs a) {
         o = o * scale;
         float o2 = kq == 0 ? o * o : 0.f;
         o2 = wave_sum(o2);
-        if (lane == 0) ored[w] = o2;
-        lds_barrier();
-        float ms2 = 0.f;
+        if constexpr (NSPL == 1) {
+            if (lane == 0) ored[w] = o2;
+            lds_barrier();
+            float ms2 = 0.f;
 #pragma unroll
-        for (int q = 0; q < 8; q++) ms2 += ored[q];
-        const float inv2 = 1.f / sqrtf(ms2 / SV + EPS);
-        if (kq == 0) a.ON[(size_t)t * n_vh * SV + (size_t)h * SV + v] = o * inv2 * nw * silu(z);
+            for (int q = 0; q < NW; q++) ms2 += ored[q];
+            const float inv2 = 1.f / sqrtf(ms2 / SV + EPS);
+            if (kq == 0) a.ON[(size_t)t * n_vh * SV + (size_t)h * SV + v] = o * inv2 * nw * silu(z);
+        } else {
+            // o / sqrt(128) and this wave's sum of squares; k_gdn_gnorm finishes
+            if (kq == 0) a.ON[(size_t)t * n_vh * SV + (size_t)h * SV + v] = o;
+            if (lane == 0) a.PSS[((size_t)t * n_vh + h) * 8 + sp * NW + w] = o2;
+        }
         lds_barrier();  // cq/ck/cv/red/ored are rewritten by the next token
     }
 #pragma unroll
     for (int i = 0; i < 32; i++) Sh[(size_t)(32 * kq + i) * SV + v] = s[i];
-    if (ch >= 0 && owner) {
-        a.tail[(size_t)ch * 3] = t0;
-        a.tail[(size_t)ch * 3 + 1] = t1;
-        a.tail[(size_t)ch * 3 + 2] = t2;
-    }
+#pragma unroll
+    for (int r = 0; r < R; r++)
+        if (ch[r] >= 0 && own[r]) {
+            a.tail[(size_t)ch[r] * 3] = t0[r];
+            a.tail[(size_t)ch[r] * 3 + 1] = t1[r];
+            a.tail[(size_t)ch[r] * 3 + 2] = t2[r];
+        }
 }
 
+// The gated rms of split scans, in place: for token t and V head h,
+// ON[t][h][v] = o * rsqrt(sum of the 8 wave partials / 128 + eps) *
+// ssm_norm[v] * silu(Z[t][h][v]), the reference's order (src/m6_layer.c:
+// 320-331).  Block (t, h), 128 threads.
+__global__ __launch_bounds__(128) void k_gdn_gnorm(const GdnArgs a) {
+    const int t = blockIdx.x, h = blockIdx.y, v = threadIdx.x;
+    const float* ps = a.PSS + ((size_t)t * a.n_vh + h) * 8;
+    float ms2 = 0.f;
+#pragma unroll
+    for (int q = 0; q < 8; q++) ms2 += ps[q];
+    const float inv2 = 1.f / sqrtf(ms2 / SV + EPS);
+    const size_t i = (size_t)t * a.n_vh * SV + (size_t)h * SV + v;
+    a.ON[i] = a.ON[i] * inv2 * a.ssm_norm[v] * silu(a.Z[i]);
+}
+
+template <bool DEC>
+int launch_scan(const GdnArgs& a, int nspl, hipStream_t st) {
+    if (nspl > 1 && !a.PSS) return -1;
+    switch (nspl) {
+    case 1: hipLaunchKernelGGL((k_gdn_scan<DEC, 8>), dim3(a.n_vh, 1), dim3(512), 0, st, a); return 0;
+    case 2: hipLaunchKernelGGL((k_gdn_scan<DEC, 4>), dim3(a.n_vh, 2), dim3(256), 0, st, a); break;
+    case 4: hipLaunchKernelGGL((k_gdn_scan<DEC, 2>), dim3(a.n_vh, 4), dim3(128), 0, st, a); break;
+    case 8: hipLaunchKernelGGL((k_gdn_scan<DEC, 1>), dim3(a.n_vh, 8), dim3(64), 0, st, a); break;
+    default: return -1;
+    }
+    hipLaunchKernelGGL(k_gdn_gnorm, dim3(a.T, a.n_vh), dim3(SV), 0, st, a);
+    return 0;
+}
+
+// Measured on MI355X (configs[4] heads, 32 V heads): a decode step takes
+// 6.9 us unsplit and 6.4-6.5 us split 4-way, less than the second launch the
+// split needs, so single tokens stay unsplit; a 64-token scan takes 1.73
+// us/token unsplit, 1.45 split 2-way (two waves per block: cheaper barriers
+// in the per-token chain), 1.95 4-way and 2.27 8-way.
+int g_split_dec = 1;
+int g_split_scan = 2;
+
 }  // namespace
+
+int draco_gdn_split(bool decode) { return decode ? g_split_dec : g_split_scan; }
+
+// Blocks per V head of the GDN decode step and of multi-token scans (1, 2, 4
+// or 8; a negative argument keeps the setting).  Returns the previous values
+// as decode * 16 + scan.
+extern "C" int draco_set_gdn_split(int decode_split, int scan_split) {
+    const int old = g_split_dec * 16 + g_split_scan;
+    auto ok = [](int n) { return n == 1 || n == 2 || n == 4 || n == 8; };
+    if (ok(decode_split)) g_split_dec = decode_split;
+    if (ok(scan_split)) g_split_scan = scan_split;
+    return old;
+}
 
 int draco_gdn_scan_launch(const GdnArgs& a, hipStream_t st) {
     if (a.n_vh < 1 || a.nhq < 1 || a.n_qkv != a.n_vh * SV + 2 * a.nhq * SV || a.T < 0) return -1;
     if (a.T == 0) return 0;
-    hipLaunchKernelGGL(k_gdn_scan<false>, dim3(a.n_vh), dim3(512), 0, st, a);
-    return 0;
+    return launch_scan<false>(a, a.nspl < 1 ? 1 : a.nspl, st);
 }
 
 int draco_gdn_step_launch(const GdnArgs& a, hipStream_t st) {
     if (a.n_vh < 1 || a.nhq < 1 || a.n_qkv != a.n_vh * SV + 2 * a.nhq * SV || a.T != 1) return -1;
     if (a.H < 4 || a.H > 4096 || a.H % 4 || !a.h1 || !a.attn_norm || !a.bw || !a.aw || !a.ssm_a || !a.ssm_dt)
         return -1;
-    hipLaunchKernelGGL(k_gdn_scan<true>, dim3(a.n_vh), dim3(512), 0, st, a);
-    return 0;
+    return launch_scan<true>(a, a.nspl < 1 ? 1 : a.nspl, st);
 }

@@ -70,6 +70,7 @@ SIGNATURES = {
     "draco_qwen_prefill": (ct.c_int, [ct.c_void_p, ct.c_int, ct.c_int, ct.c_void_p, ct.c_int, ct.c_int, i32p, ct.c_int,
                                       ct.c_int, f32p]),
     "draco_set_qwen_chunk": (ct.c_int, [ct.c_int]),
+    "draco_set_gdn_split": (ct.c_int, [ct.c_int, ct.c_int]),
     "draco_qwen_generate": (ct.c_int, [ct.c_void_p, ct.c_int, ct.c_int, ct.c_float, f32p, ct.c_void_p, ct.c_int,
                                        ct.c_int, ct.c_void_p, ct.c_int, ct.c_int, i32p, ct.c_int, ct.c_int, ct.c_int,
                                        i32p, f32p, f32p]),

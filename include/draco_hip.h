@@ -322,6 +322,12 @@ int draco_qwen_forward(float* x, int h, int pos, const void* layers, int n_layer
 int draco_qwen_prefill(const void* layers, int n_layer, int h, const uint8_t* emb_w, int emb_code, int vocab,
                        const int* ids, int n, int pos0, float* out_x);
 int draco_set_qwen_chunk(int n);
+/* No reference counterpart: blocks per V head of the GDN scan (1, 2, 4 or 8;
+ * negative keeps a setting) for single-token steps and for multi-token scans
+ * (defaults 4 and 1).  Split above 1, each head's 128 state columns spread
+ * over that many workgroups and the gated rms runs as a second launch.
+ * Returns the previous values as decode * 16 + scan. */
+int draco_set_gdn_split(int decode_split, int scan_split);
 /* Greedy generation from position pos0 (prompt through the chunked prefill
  * except its last token, then n_gen argmax tokens; graph-replayed steps with
  * use_graph); the head is RMSNorm(final_norm, eps) + head_w, as m6_head_op.

@@ -111,3 +111,22 @@ def test_gdn_scan_configs4_4096_tokens_then_decode(hip, oracle):
     print(f"[gdn] 4096 + 64 tokens: worst per-call output error {worst:.2e}, final state {es:.2e}", flush=True)
     assert es <= TOL
     assert np.array_equal(tt, tailo)
+
+
+@pytest.mark.parametrize("split", [1, 2, 4, 8])
+@pytest.mark.parametrize("T", [1, 20])
+def test_gdn_scan_column_split(hip, oracle, split, T):
+    """The scan with each head's 128 state columns split over 1, 2, 4 or 8
+    workgroups (the gated rms then in a second launch) against the oracle at
+    the configs[4] head shape: outputs, state and tail."""
+    old = hip.draco_set_gdn_split(split, split)
+    try:
+        n_qkv, QKV, Z, B, G, conv, ssm_norm, tail, S = gg.gdn_inputs(T, 32, 16, 46 + T)
+        print(f"[gdn] column split {split}, T {T}", flush=True)
+        ON, S2, tail2 = scan(hip, T, n_qkv, 32, QKV, Z, B, G, conv, ssm_norm, tail, S)
+    finally:
+        hip.draco_set_gdn_split(old // 16, old % 16)
+    ONo, So, tailo = scan_oracle(oracle, T, n_qkv, 32, QKV, Z, B, G, conv, ssm_norm, tail, S)
+    assert rel_err(ON, ONo) <= TOL
+    assert rel_err(S2, So) <= TOL
+    assert np.array_equal(tail2, tailo)
