@@ -255,6 +255,44 @@ int enqueue_gdn(const GdnDev& g, const GdnBufs& b, hipStream_t st, bool post_nor
     return enqueue_proj(out, 1, b.on, g.d_in, nullptr, b.xn, st, post_norm ? &pn : nullptr);
 }
 
+// ---- state residency of the per-layer ops ----
+// m6_gdn_attn and m6_full_attn keep the caller's state arrays on the device:
+// the GDN recurrent state and conv tail and the full-attention K / V rows
+// live in mirrors keyed by the arrays' host addresses (the same mirrors the
+// qwen stack entry points use), so a call moves h1 in and x2n / x2_out
+// (+ kr_new / v_new) out.  The caller's arrays are not kept current
+// (draco_array_pull copies a mirror back, draco_array_push forces an
+// upload).  A write of the caller's own is detected:
+//  - GDN: after every call the first QSAMP floats of the device state are
+//    written into the caller's ssm.  If at the next call they are not there
+//    bit for bit (a reset that zeroed the arrays, a restored snapshot), the
+//    state and tail are uploaded from the caller's arrays.
+//  - full attention: the caller appends kr_new / v_new to its own rows (the
+//    reference's driver, src/qwen35_engine.py:317-323), so its rows equal
+//    the device's.  The first float of every row the device holds is kept
+//    here; up to 17 rows of [0, Told) are compared per call, and a mismatch
+//    uploads rows [0, Told).  Rows the device never held are uploaded too.
+constexpr int QSAMP = 128;
+
+struct OpState {
+    const void* dev = nullptr;     // the mirror these records describe
+    std::vector<uint32_t> samp;    // GDN: written-back state floats
+    int rows = 0;                  // full attention: leading rows the device holds
+    int cap = 0;                   // full attention: rows the mirrors were sized for
+    std::vector<uint32_t> shk, shv;  // full attention: first float of each held row
+};
+
+std::map<const void*, OpState>& op_states() {
+    static auto* m = new std::map<const void*, OpState>();
+    return *m;
+}
+
+uint32_t fbits(float f) {
+    uint32_t u;
+    memcpy(&u, &f, 4);
+    return u;
+}
+
 int gdn_host(const float* h1, const GdnW* w, float* ssm, float* tail, float* x2n, float* x2_out) {
     if (int rc = ensure_init()) return rc;
     GdnDev g;
@@ -263,16 +301,35 @@ int gdn_host(const float* h1, const GdnW* w, float* ssm, float* tail, float* x2n
     if (gdn_bufs(g, 20, b)) return -2;
     hipStream_t st = stream();
     const size_t ns = (size_t)g.n_vh * QSV * QSV, nt = (size_t)g.n_qkv * 3;
-    DRACO_HIP(hipMemcpyAsync(b.h1, h1, sizeof(float) * QH, hipMemcpyHostToDevice, st));
-    DRACO_HIP(hipMemcpyAsync(b.S, ssm, sizeof(float) * ns, hipMemcpyHostToDevice, st));
-    DRACO_HIP(hipMemcpyAsync(b.tail, tail, sizeof(float) * nt, hipMemcpyHostToDevice, st));
+    bool fs = false, ft = false;
+    b.S = (float*)get_mirror(ssm, sizeof(float) * ns, &fs);
+    b.tail = (float*)get_mirror(tail, sizeof(float) * nt, &ft);
+    if (!b.S || !b.tail) return -2;
+    OpState& os = op_states()[ssm];
+    bool upload = fs || ft || os.dev != b.S || os.samp.size() != QSAMP;
+    for (int i = 0; !upload && i < QSAMP; i++) upload = fbits(ssm[i]) != os.samp[i];
+    if (upload) {
+        DRACO_HIP(hipMemcpyAsync(b.S, ssm, sizeof(float) * ns, hipMemcpyHostToDevice, st));
+        DRACO_HIP(hipMemcpyAsync(b.tail, tail, sizeof(float) * nt, hipMemcpyHostToDevice, st));
+    }
+    // pinned staging: h1 in; x2_out, x2n (adjacent on the device) and the
+    // state sample out
+    float* hp = (float*)pinned(5, sizeof(float) * (3 * QH + QSAMP));
+    if (!hp) return -2;
+    memcpy(hp, h1, sizeof(float) * QH);
+    DRACO_HIP(hipMemcpyAsync(b.h1, hp, sizeof(float) * QH, hipMemcpyHostToDevice, st));
     if (int rc = enqueue_gdn(g, b, st)) return rc;
     DRACO_HIP(hipGetLastError());
-    DRACO_HIP(hipMemcpyAsync(x2n, b.x2n, sizeof(float) * QH, hipMemcpyDeviceToHost, st));
-    DRACO_HIP(hipMemcpyAsync(x2_out, b.x2o, sizeof(float) * QH, hipMemcpyDeviceToHost, st));
-    DRACO_HIP(hipMemcpyAsync(ssm, b.S, sizeof(float) * ns, hipMemcpyDeviceToHost, st));
-    DRACO_HIP(hipMemcpyAsync(tail, b.tail, sizeof(float) * nt, hipMemcpyDeviceToHost, st));
+    float* ho = hp + QH;
+    DRACO_HIP(hipMemcpyAsync(ho, b.x2o, sizeof(float) * 2 * QH, hipMemcpyDeviceToHost, st));
+    DRACO_HIP(hipMemcpyAsync(ho + 2 * QH, b.S, sizeof(float) * QSAMP, hipMemcpyDeviceToHost, st));
     DRACO_HIP(hipStreamSynchronize(st));
+    memcpy(x2_out, ho, sizeof(float) * QH);
+    memcpy(x2n, ho + QH, sizeof(float) * QH);
+    memcpy(ssm, ho + 2 * QH, sizeof(float) * QSAMP);
+    os.dev = b.S;
+    os.samp.resize(QSAMP);
+    for (int i = 0; i < QSAMP; i++) os.samp[i] = fbits(ho[2 * QH + i]);
     return 0;
 }
 
@@ -306,10 +363,11 @@ int full_resolve(const FullW* w, FullDev& f) {
     return 0;
 }
 
-// buffers for caches of up to max_t rows
-int full_bufs(const FullDev& f, int max_t, int slot, FullBufs& b) {
+// buffers for caches of up to max_t rows (with cache false, kc / vc are left
+// null: the caller's mirrors hold the rows)
+int full_bufs(const FullDev& f, int max_t, int slot, FullBufs& b, bool cache = true) {
     const int nsplit = attn_nsplit(max_t, f.nh, FNKV, FHD);
-    const size_t kv = (size_t)max_t * FNKV * FHD;
+    const size_t kv = cache ? (size_t)max_t * FNKV * FHD : 0;
     const size_t part = (size_t)f.nh * nsplit * (FHD + 2);
     const size_t n = 5 * (size_t)QH + (size_t)f.nh * 2 * FHD + 2 * (size_t)f.nh * FHD + FNKV * FHD + 2 * kv +
                      part + 64 + 64 + 16 * 64;
@@ -320,7 +378,11 @@ int full_bufs(const FullDev& f, int max_t, int slot, FullBufs& b) {
         p += (k + 63) & ~(size_t)63;
         return r;
     };
+    // h1, cs, state adjacent (one upload), then x2_out, x2n adjacent (one
+    // download)
     b.h1 = take(QH);
+    b.cs = take(64);
+    b.state = (int*)take(64);
     b.x2o = take(QH);
     b.x2n = take(QH);
     b.xn = take(QH);
@@ -328,11 +390,9 @@ int full_bufs(const FullDev& f, int max_t, int slot, FullBufs& b) {
     b.Qr = take((size_t)f.nh * FHD);
     b.ao = take((size_t)f.nh * FHD);
     b.kraw = take(FNKV * FHD);
-    b.kc = take(kv);
-    b.vc = take(kv);
+    b.kc = cache ? take(kv) : nullptr;
+    b.vc = cache ? take(kv) : nullptr;
     b.part = take(part);
-    b.cs = take(64);
-    b.state = (int*)take(64);
     return 0;
 }
 
@@ -368,29 +428,65 @@ int full_host(const float* h1, const FullW* w, const float* Kr, const float* Vc,
     FullDev f;
     if (int rc = full_resolve(w, f)) return rc;
     FullBufs b;
-    if (full_bufs(f, told + 1, 21, b)) return -2;
-    float* hs = (float*)pinned(5, sizeof(float) * 128);
-    if (!hs) return -2;
-    rope_cs(w->rope_inv, pos0, hs);
-    int* hi = (int*)(hs + 64);
+    if (full_bufs(f, told + 1, 21, b, false)) return -2;
+    hipStream_t st = stream();
+    const size_t rowf = (size_t)FNKV * FHD, rowb = sizeof(float) * rowf;
+    // K / V mirrors of at least told + 1 rows, grown by doubling (the held
+    // rows move with them)
+    OpState& os = op_states()[Kr];
+    if (!os.dev) os.cap = os.rows = 0;
+    const int need = told + 1;
+    const bool grow = need > os.cap;
+    if (grow) os.cap = std::max(std::max(need, 2 * os.cap), 256);
+    const size_t keep = rowb * (size_t)std::min(os.rows, told);
+    bool fk = false, fv = false;
+    b.kc = (float*)grow_mirror(Kr, rowb * os.cap, keep, &fk);
+    b.vc = (float*)grow_mirror(Vc, rowb * os.cap, keep, &fv);
+    if (!b.kc || !b.vc) return -2;
+    if (fk || fv || (b.kc != os.dev && !(grow && os.dev))) os.rows = 0;
+    os.dev = b.kc;
+    if (os.shk.size() < (size_t)os.cap) {
+        os.shk.resize(os.cap);
+        os.shv.resize(os.cap);
+    }
+    int held = std::min(os.rows, told);
+    for (int i = 0; held > 0 && i <= 16; i++) {
+        const int r = i == 16 ? held - 1 : (int)((int64_t)i * held / 16);
+        if (fbits(Kr[(size_t)r * rowf]) != os.shk[r] || fbits(Vc[(size_t)r * rowf]) != os.shv[r]) held = 0;
+    }
+    if (held < told) {
+        const size_t n = rowb * (size_t)(told - held);
+        DRACO_HIP(hipMemcpyAsync(b.kc + (size_t)held * rowf, Kr + (size_t)held * rowf, n, hipMemcpyHostToDevice, st));
+        DRACO_HIP(hipMemcpyAsync(b.vc + (size_t)held * rowf, Vc + (size_t)held * rowf, n, hipMemcpyHostToDevice, st));
+        for (int r = held; r < told; r++) {
+            os.shk[r] = fbits(Kr[(size_t)r * rowf]);
+            os.shv[r] = fbits(Vc[(size_t)r * rowf]);
+        }
+    }
+    // pinned staging: h1, rope cos / sin, [pos0, told] in (adjacent on the
+    // device); x2_out and x2n (adjacent), kr_new, v_new out
+    float* hp = (float*)pinned(5, sizeof(float) * (QH + 128 + 2 * QH + 2 * rowf));
+    if (!hp) return -2;
+    memcpy(hp, h1, sizeof(float) * QH);
+    rope_cs(w->rope_inv, pos0, hp + QH);
+    int* hi = (int*)(hp + QH + 64);
     hi[0] = pos0;
     hi[1] = told;
-    hipStream_t st = stream();
-    const size_t rowf = (size_t)FNKV * FHD;
-    DRACO_HIP(hipMemcpyAsync(b.h1, h1, sizeof(float) * QH, hipMemcpyHostToDevice, st));
-    DRACO_HIP(hipMemcpyAsync(b.cs, hs, sizeof(float) * 64, hipMemcpyHostToDevice, st));
-    DRACO_HIP(hipMemcpyAsync(b.state, hi, sizeof(int) * 2, hipMemcpyHostToDevice, st));
-    if (told > 0) {
-        DRACO_HIP(hipMemcpyAsync(b.kc, Kr, sizeof(float) * rowf * told, hipMemcpyHostToDevice, st));
-        DRACO_HIP(hipMemcpyAsync(b.vc, Vc, sizeof(float) * rowf * told, hipMemcpyHostToDevice, st));
-    }
+    DRACO_HIP(hipMemcpyAsync(b.h1, hp, sizeof(float) * (QH + 64 + 2), hipMemcpyHostToDevice, st));
     if (int rc = enqueue_full(f, b, told, st)) return rc;
     DRACO_HIP(hipGetLastError());
-    DRACO_HIP(hipMemcpyAsync(x2n, b.x2n, sizeof(float) * QH, hipMemcpyDeviceToHost, st));
-    DRACO_HIP(hipMemcpyAsync(x2_out, b.x2o, sizeof(float) * QH, hipMemcpyDeviceToHost, st));
-    DRACO_HIP(hipMemcpyAsync(kr_new, b.kc + rowf * told, sizeof(float) * rowf, hipMemcpyDeviceToHost, st));
-    DRACO_HIP(hipMemcpyAsync(v_new, b.vc + rowf * told, sizeof(float) * rowf, hipMemcpyDeviceToHost, st));
+    float* ho = hp + QH + 128;
+    DRACO_HIP(hipMemcpyAsync(ho, b.x2o, sizeof(float) * 2 * QH, hipMemcpyDeviceToHost, st));
+    DRACO_HIP(hipMemcpyAsync(ho + 2 * QH, b.kc + rowf * told, rowb, hipMemcpyDeviceToHost, st));
+    DRACO_HIP(hipMemcpyAsync(ho + 2 * QH + rowf, b.vc + rowf * told, rowb, hipMemcpyDeviceToHost, st));
     DRACO_HIP(hipStreamSynchronize(st));
+    memcpy(x2_out, ho, sizeof(float) * QH);
+    memcpy(x2n, ho + QH, sizeof(float) * QH);
+    memcpy(kr_new, ho + 2 * QH, rowb);
+    memcpy(v_new, ho + 2 * QH + rowf, rowb);
+    os.shk[told] = fbits(kr_new[0]);
+    os.shv[told] = fbits(v_new[0]);
+    os.rows = told + 1;
     return 0;
 }
 
@@ -1122,6 +1218,24 @@ int draco_qwen_generate(const void* layers, int n_layer, int h, float eps, const
     }
     for (int i = 0; i < n_gen; i++) out_tokens[i] = ht[n_prompt + i];
     return 0;
+}
+
+// One state array's device mirror -> the caller's array (its first `bytes`):
+// a GDN ssm or tail, or the leading rows of a full-attention Kr / Vc, as the
+// per-layer ops left them.
+int draco_array_pull(void* host, size_t bytes) {
+    std::lock_guard<std::recursive_mutex> g(api_mutex());
+    return mirror_pull(host, bytes);
+}
+
+// The caller's array (its first `bytes`) -> its device mirror, e.g. after
+// restoring a snapshot into it; the per-layer ops re-read it on their next
+// call.
+int draco_array_push(const void* host, size_t bytes) {
+    std::lock_guard<std::recursive_mutex> g(api_mutex());
+    if (int rc = ensure_init()) return rc;
+    op_states().erase(host);
+    return mirror_push(host, bytes);
 }
 
 // Device state of every layer -> the caller's arrays (GDN ssm and tail in

@@ -6,6 +6,7 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <algorithm>
 #include <unordered_map>
 #include <vector>
 
@@ -281,6 +282,35 @@ void* get_mirror(const void* host, size_t bytes, bool* fresh) {
     m.bytes = bytes;
     s.mirrors[host] = m;
     if (fresh) *fresh = true;
+    return m.dev;
+}
+
+void* grow_mirror(const void* host, size_t bytes, size_t keep, bool* fresh) {
+    State& s = S();
+    if (ensure_init()) return nullptr;
+    auto it = s.mirrors.find(host);
+    if (it != s.mirrors.end() && it->second.bytes >= bytes && it->second.dev) {
+        *fresh = false;
+        return it->second.dev;
+    }
+    Mirror m;
+    hipError_t he = hipMalloc(&m.dev, bytes);
+    if (he != hipSuccess) {
+        fail(-2, "hipMalloc(%zu) for state mirror failed: %s", bytes, hipGetErrorString(he));
+        return nullptr;
+    }
+    m.bytes = bytes;
+    *fresh = true;
+    if (it != s.mirrors.end()) {
+        keep = std::min(keep, it->second.bytes);
+        if (keep && hipMemcpyAsync(m.dev, it->second.dev, keep, hipMemcpyDeviceToDevice, s.st) == hipSuccess)
+            *fresh = false;
+        hipStreamSynchronize(s.st);
+        hipFree(it->second.dev);
+        s.mirrors.erase(it);
+        s.epoch++;
+    }
+    s.mirrors[host] = m;
     return m.dev;
 }
 

@@ -57,6 +57,9 @@ size_t resident_bytes();
 // Device mirror of a caller-owned host array (KV caches and other state).
 // `fresh` is set when the mirror was (re)allocated and holds no data yet.
 void* get_mirror(const void* host, size_t bytes, bool* fresh);
+// The same, but a mirror too small for `bytes` is replaced by a larger one
+// that keeps its first `keep` bytes (`fresh` is then false).
+void* grow_mirror(const void* host, size_t bytes, size_t keep, bool* fresh);
 int mirror_invalidate(const void* host);
 int mirror_pull(const void* host, size_t bytes);   // device -> host
 int mirror_push(const void* host, size_t bytes);   // host -> device

@@ -65,6 +65,8 @@ SIGNATURES = {
     "m6_full_attn": (None, [f32p, ct.c_void_p, f32p, f32p, ct.c_int, ct.c_int, f32p, f32p, f32p, f32p,
                             f32p, f32p]),
     "draco_bench_qwen_op": (ct.c_int, [ct.c_int, ct.c_void_p, f32p, f32p, f32p, ct.c_int, ct.c_int, f32p]),
+    "draco_array_pull": (ct.c_int, [ct.c_void_p, ct.c_size_t]),
+    "draco_array_push": (ct.c_int, [ct.c_void_p, ct.c_size_t]),
     # qwen35 hybrid stack on the device (no reference counterpart as one call)
     "draco_qwen_forward": (ct.c_int, [f32p, ct.c_int, ct.c_int, ct.c_void_p, ct.c_int]),
     "draco_qwen_prefill": (ct.c_int, [ct.c_void_p, ct.c_int, ct.c_int, ct.c_void_p, ct.c_int, ct.c_int, i32p, ct.c_int,

@@ -272,12 +272,21 @@ typedef struct {
     int nh;                             /* even, <= 32 */
 } FullW;
 
-/* m6_gdn_attn: src/m6_layer.c:205-364.  h1[2048] -> x2n, x2_out; ssm
- * [n_vh][128][128] and tail [n_qkv][3] updated in place. */
+/* m6_gdn_attn: src/m6_layer.c:205-364.  h1[2048] -> x2n, x2_out; the state
+ * ssm [n_vh][128][128] and tail [n_qkv][3] advances in device mirrors keyed by
+ * the arrays' addresses (loaded from them when first seen).  Each call writes
+ * the first 128 state floats back into ssm; when the caller's ssm no longer
+ * holds them bit for bit at the next call (a reset that zeroed the arrays, a
+ * restored snapshot), both arrays are loaded again.  draco_array_pull copies
+ * the state back in full. */
 void m6_gdn_attn(const float* h1, const GdnW* w, float* ssm, float* tail, float* buf, float* x2n,
                  float* x2_out);
 /* m6_full_attn: src/m6_layer.c:389-518.  Kr / Vc: Told cached rows of
- * [2][256]; kr_new / v_new receive the new row (k normed + roped). */
+ * [2][256]; kr_new / v_new receive the new row (k normed + roped), which the
+ * caller appends at row Told as the reference's driver does.  The rows live
+ * in device mirrors keyed by Kr / Vc: rows the device has not held are
+ * uploaded, and up to 17 held rows are compared with the caller's (first
+ * float of each) per call, a mismatch reloading rows [0, Told). */
 void m6_full_attn(const float* h1, const FullW* w, const float* Kr, const float* Vc, int Told, int pos0,
                   float* buf, float* scores, float* x2n, float* x2_out, float* kr_new, float* v_new);
 /* No reference counterpart: device-resident timing of one op (kind 0 GDN with
@@ -287,6 +296,11 @@ void m6_full_attn(const float* h1, const FullW* w, const float* Kr, const float*
  * bytes per op, out[2] algorithmic HBM bytes per op. */
 int draco_bench_qwen_op(int kind, const void* w, const float* h1, const float* ssm_or_kr, const float* tail_or_vc,
                         int told, int iters, float* out);
+/* No reference counterpart (the reference's state arrays are host memory):
+ * a state array's device mirror -> its first `bytes` (pull), and the caller's
+ * array -> the mirror (push, e.g. after restoring a snapshot into it). */
+int draco_array_pull(void* host, size_t bytes);
+int draco_array_push(const void* host, size_t bytes);
 
 /* ---- the qwen35 hybrid stack on the device --------------------------------
  * No reference counterpart as one call: the reference's driver composes the
@@ -324,7 +338,7 @@ int draco_qwen_prefill(const void* layers, int n_layer, int h, const uint8_t* em
 int draco_set_qwen_chunk(int n);
 /* No reference counterpart: blocks per V head of the GDN scan (1, 2, 4 or 8;
  * negative keeps a setting) for single-token steps and for multi-token scans
- * (defaults 4 and 1).  Split above 1, each head's 128 state columns spread
+ * (defaults 1 and 2).  Split above 1, each head's 128 state columns spread
  * over that many workgroups and the gated rms runs as a second launch.
  * Returns the previous values as decode * 16 + scan. */
 int draco_set_gdn_split(int decode_split, int scan_split);
