@@ -11,12 +11,16 @@ events on the decode stream).  configs2_prefill reports the prompt's chunked
 prefill time (and the token-serial time of the same prompt for scale).
 
 roofline: the Q4_K GEMV of configs[1] (W 14336x4096 from seed 1, fp32 x),
-timed live with per-launch HIP event pairs while rotating 10 distinct weight
-copies (330 MB > the 256 MB MALL).
+one HIP event pair around a graph replay of 200 launches rotating 10
+distinct weight copies (330 MB > the 256 MB MALL).  decode_roofline: the
+configs[2] decode's bytes per token x tok/s against the same HBM peak.
+Further legs: configs[0], [1], [3] and [4] (see each function).
 
 cpu_baseline: the reference's own C engine (src/m6_engine.c + the scalar
 kernels of src/m5_kern_scalar.c, compiled from source into oracle/_ref),
-decoding from the same context on this host's cores, in a child process.
+decoding from the same context on this host's cores (all granted, and one),
+in a child process; plus the reference's AVX-512 Q4_K row kernel
+(src/m5/m5_batch8_k.c) at the configs[1] shapes.
 
 usage: python bench.py [--gpus 1] [--steps 64] [--warmup 8]
 """
@@ -226,7 +230,7 @@ def llama_bytes_per_token(model, first_pos, n_gen):
     return layers + head + emb_row + kv
 
 
-def smol_decode_configs0(lib):
+def smol_decode_configs0(lib, use_graph=True):
     """SmolLM2-360M-shaped Q8_0, 32-token prompt + 64 greedy tokens
     on the device loop (graph-replayed); tokens checked against the reference
     golden; tok/s and GB/s against the HBM roof."""
@@ -237,10 +241,10 @@ def smol_decode_configs0(lib):
     model = models.build_llama(cfg, 0)
     L = lib.load()
     drv = LlamaDriver(model, hip_engine_lib())
-    drv.generate_device(model.prompt(), cfg.n_gen)
+    drv.generate_device(model.prompt(), cfg.n_gen, use_graph=use_graph)
     drv.reset()
     L.draco_state_push(ct.cast(drv.descs, ct.c_void_p), drv.NL)
-    toks, _, (dec_ms, _) = drv.generate_device(model.prompt(), cfg.n_gen)
+    toks, _, (dec_ms, _) = drv.generate_device(model.prompt(), cfg.n_gen, use_graph=use_graph)
     gpath = os.path.join(ROOT, "tests", "golden", "smol360m.npz")
     match = bool(list(np.load(gpath)["tokens"]) == toks) if os.path.exists(gpath) else None
     per_tok = llama_bytes_per_token(model, cfg.n_prompt - 1, cfg.n_gen)
@@ -255,7 +259,7 @@ def smol_decode_configs0(lib):
     return res
 
 
-def moe_stack_configs3(lib, seed=3):
+def moe_stack_configs3(lib, seed=3, use_graph=True):
     """the 48-layer Qwen3-30B-A3B-shaped MoE stack (attention 32 q /
     4 kv heads of 128, Q6_K; MoE FFN 128 experts, top 8, FFN 768, Q4_K experts,
     fp32 router) decoding at context 512: a 448-token prompt fed token by token
@@ -273,11 +277,11 @@ def moe_stack_configs3(lib, seed=3):
     L = lib.load()
     drv = LlamaDriver(model, hip_engine_lib())
     t0 = time.time()
-    toks, _, (dec_ms, pre_ms) = drv.generate_device(model.prompt(), cfg.n_gen, use_graph=True)
+    toks, _, (dec_ms, pre_ms) = drv.generate_device(model.prompt(), cfg.n_gen, use_graph=use_graph)
     log(f"configs[3] first run (upload + prompt + decode) {time.time() - t0:.1f}s")
     drv.reset()
     L.draco_state_push(ct.cast(drv.descs, ct.c_void_p), drv.NL)
-    toks2, _, (dec_ms, pre_ms) = drv.generate_device(model.prompt(), cfg.n_gen, use_graph=True)
+    toks2, _, (dec_ms, pre_ms) = drv.generate_device(model.prompt(), cfg.n_gen, use_graph=use_graph)
     T = model.tensors
     H, E, F, KD = cfg.hidden, cfg.n_exp, cfg.exp_ff, cfg.n_kv * cfg.head_dim
     attn = sum(T[f"blk.0.{n}.weight"][0].nbytes for n in ("attn_q", "attn_k", "attn_v", "attn_output"))
@@ -304,7 +308,7 @@ def moe_stack_configs3(lib, seed=3):
     return res
 
 
-def qwen_stack_configs4(lib, seed=4):
+def qwen_stack_configs4(lib, seed=4, use_graph=True):
     """the 48-layer qwen35 hybrid stack (36 GDN layers of 16 q/k
     and 32 V heads of 128, 12 full-attention layers of 16 q / 2 KV heads of
     256, 3:1 interleave, Q4_K projections, hidden 2048): a 4096-token prompt,
@@ -324,10 +328,10 @@ def qwen_stack_configs4(lib, seed=4):
     old = L.draco_set_qwen_chunk(64)
     prompt = stack.prompt()
     t0 = time.time()
-    toks, _, _ = drv.generate_device(prompt, cfg.n_gen)
+    toks, _, _ = drv.generate_device(prompt, cfg.n_gen, use_graph=use_graph)
     log(f"configs[4] first run (upload + prompt + decode) {time.time() - t0:.1f}s")
     drv.reset()
-    toks2, _, (dec_ms, pre_ms) = drv.generate_device(prompt, cfg.n_gen)
+    toks2, _, (dec_ms, pre_ms) = drv.generate_device(prompt, cfg.n_gen, use_graph=use_graph)
     L.draco_set_qwen_chunk(old)
     gdn_w = full_w = 0
     for il, layer in enumerate(stack.layers):
@@ -541,6 +545,8 @@ def main():
     ap.add_argument("--no-stacks", action="store_true", help="skip the configs[0] / [3] / [4] decode legs")
     ap.add_argument("--no-serial-prefill", action="store_true",
                     help="skip the token-serial prompt run (the chunked prefill is the measured one)")
+    ap.add_argument("--leg", choices=["configs0", "configs3", "configs4"],
+                    help="run only this decode leg and print its record (profiling runs)")
     ap.add_argument("--cpu-baseline-worker", action="store_true")
     ap.add_argument("--cpu-gemv-worker", action="store_true")
     ap.add_argument("--kv-file")
@@ -557,6 +563,13 @@ def main():
     import ctypes as ct
     from dracohip import lib, models
     from dracohip.driver import LlamaDriver, hip_engine_lib
+
+    if args.leg:
+        fn = {"configs0": smol_decode_configs0, "configs3": moe_stack_configs3, "configs4": qwen_stack_configs4}
+        res = fn[args.leg](lib, use_graph=not args.eager)
+        log(f"{args.leg}: {res}")
+        print(json.dumps({args.leg: res}), flush=True)
+        return
 
     if args.roofline_only:
         roof = q4k_gemv_roofline(lib)
@@ -679,13 +692,13 @@ def main():
 
     moe_stack = qwen_stack = smol = None
     if not args.no_stacks:
-        smol = smol_decode_configs0(lib)
+        smol = smol_decode_configs0(lib, use_graph=not args.eager)
         log(f"configs[0] SmolLM2-360M decode: {smol['tok_s']} tok/s ({smol['frac_of_peak']} of peak), tokens match "
             f"reference: {smol['greedy_tokens_match_reference']}")
-        moe_stack = moe_stack_configs3(lib)
+        moe_stack = moe_stack_configs3(lib, use_graph=not args.eager)
         log(f"configs[3] MoE stack: {moe_stack['tok_s']} tok/s, {moe_stack['GB_s']} GB/s "
             f"({moe_stack['frac_of_peak']} of peak)")
-        qwen_stack = qwen_stack_configs4(lib)
+        qwen_stack = qwen_stack_configs4(lib, use_graph=not args.eager)
         log(f"configs[4] qwen35 stack: decode {qwen_stack['decode_tok_s']} tok/s ({qwen_stack['frac_of_peak']} of "
             f"peak), prefill {qwen_stack['prefill_tok_s']} tok/s")
 

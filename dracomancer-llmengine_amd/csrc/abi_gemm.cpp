@@ -5,10 +5,12 @@
 // X[T x n_in] . W^T).  Host pointers.  Q4_K / Q6_K run on the f16-MFMA GEMM
 // (gemmh.hip); Q8_0 runs as one device GEMV per token.  The int8-MFMA kernels
 // of gemm.hip serve the grouped expert GEMMs of m6_moe_tok only.
+// m5_dequant_row: src/m5/m5_gemm.c:55-235, the GEMM library's row decoder.
 #include <string.h>
 
 #include <vector>
 
+#include "decode.h"
 #include "gemm.h"
 #include "runtime.h"
 
@@ -86,6 +88,50 @@ int m5_gemm(int code, const float* X, const uint8_t* W, int T, int n_out, int n_
     (void)wbuf;  // the device path needs no host row buffer
     std::lock_guard<std::recursive_mutex> g(api_mutex());
     return gemm_host(code, X, W, T, n_out, n_in, Y);
+}
+
+// src/m5/m5_gemm.c:55-235: one GGUF row -> out[n_in] fp32 (0 done, -1 code
+// not served).  Served: Q8_0, Q4_K, Q6_K, F16 (the reference also serves
+// Q5_K and the IQ formats, which no path here carries).  The row is decoded
+// on the device by the embedding decoder: from the resident copy when the
+// row lies inside a registered matrix, else from the row's own bytes put in
+// the private layout.
+int m5_dequant_row(int code, const uint8_t* row, int n_in, float* out) {
+    std::lock_guard<std::recursive_mutex> g(api_mutex());
+    if (code != DRACO_Q8_0 && code != DRACO_Q4_K && code != DRACO_Q6_K && code != DRACO_F16) return -1;
+    if (!row || !out || n_in <= 0 || n_in % draco_block_values(code)) {
+        fail(-1, "m5_dequant_row: n_in %d is not a whole number of blocks", n_in);
+        return -1;
+    }
+    if (ensure_init()) return -1;
+    hipStream_t st = stream();
+    int r = 0;
+    DracoMat m;
+    if (const DracoMat* rm = find_row(row, code, n_in, &r)) {
+        m = *rm;
+    } else {
+        if (draco_layout(code, 1, n_in, &m.L)) return fail(-1, "m5_dequant_row: no layout for n_in %d", n_in);
+        uint8_t* stage = (uint8_t*)pinned(0, m.L.bytes);
+        m.dev = (uint8_t*)scratch(30, m.L.bytes);
+        if (!stage || !m.dev) return -1;
+        memset(stage, 0, m.L.bytes);
+        draco_repack(code, row, 1, n_in, stage);
+        if (hipMemcpyAsync(m.dev, stage, m.L.bytes, hipMemcpyHostToDevice, st) != hipSuccess)
+            return fail(-1, "m5_dequant_row: upload failed");
+    }
+    int* ids = (int*)scratch(31, sizeof(float) * ((size_t)n_in + 64));
+    float* hp = (float*)pinned(6, sizeof(float) * ((size_t)n_in + 64));
+    if (!ids || !hp) return -1;
+    float* dout = (float*)(ids + 64);
+    *(int*)hp = r;
+    if (hipMemcpyAsync(ids, hp, sizeof(int), hipMemcpyHostToDevice, st) != hipSuccess)
+        return fail(-1, "m5_dequant_row: upload failed");
+    dk_embed(m, ids, nullptr, dout, st);
+    if (hipMemcpyAsync(hp, dout, sizeof(float) * n_in, hipMemcpyDeviceToHost, st) != hipSuccess ||
+        hipStreamSynchronize(st) != hipSuccess)
+        return fail(-1, "m5_dequant_row: decode failed");
+    memcpy(out, hp, sizeof(float) * n_in);
+    return 0;
 }
 
 // Graph-replayed timing of the prefill GEMM on `n_copies` weight copies:

@@ -1,15 +1,14 @@
 // abi_qwen.cpp -- qwen35 hybrid-layer decode ops: m6_gdn_attn (Gated-DeltaNet
 // layer) and m6_full_attn (gated full attention), src/m6_layer.c:189-518.
 //
-// Host pointers in and out, as in the reference: the recurrent state (ssm,
-// tail) and the cached K / V rows are the caller's arrays.  Each call uploads
-// them, runs the layer on the device and downloads every output the reference
-// writes (the state in place, kr_new / v_new for the caller's cache append).
-// Weights and fp32 parameter arrays are registered by host address and stay
-// resident.  The reference's scratch arguments (buf, scores) are accepted and
-// not used.
+// Host pointers in and out, as in the reference.  The recurrent state (ssm,
+// tail) and the cached K / V rows stay in device mirrors of the caller's
+// arrays between calls (the residency rules are next to gdn_host below), so
+// a call moves h1 in and the outputs out.  Weights and fp32 parameter arrays
+// are registered by host address and stay resident.  The reference's scratch
+// arguments (buf, scores) are accepted and not used.
 //
-// Device work per GDN token (5 launches):
+// Device work per GDN token (4 launches):
 //   k_dq      qkv + gate projections, attention RMSNorm in the prologue
 //   k_gdn     per V head: beta / decay from xn, conv + silu, l2 norms, delta
 //             rule on the register-resident state, gated rms   -> on
@@ -18,8 +17,9 @@
 // Device work per full-attention token (6 launches):
 //   k_dq        q+gate, k, v projections (v straight into cache row Told)
 //   k_fa_prep   q / k head RMSNorm + rope (k into cache row Told)
-//   k_attn_part split-T attention over Told + 1 rows, then k_attn_combine
-//               with the sigmoid gate
+//   k_attn_gqa  split-T attention over Told + 1 rows, each K / V row read
+//               once per GQA group; k_attn_merge merges the splits and
+//               applies the sigmoid gate
 //   k_dq        o projection + residual; k_rmsnorm               -> x2n
 #include <math.h>
 #include <stdio.h>

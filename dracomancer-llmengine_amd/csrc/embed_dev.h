@@ -8,6 +8,7 @@
 // Value p of row `tok` of a private-layout matrix; bit-identical to the host
 // decoders: (d*sc)*q for Q6_K, d*sc*q - dmin*m for Q4_K, q*d for Q8_0.
 __device__ __forceinline__ float embed_value(const uint8_t* __restrict__ base, const DracoLayout& L, int tok, int p) {
+#pragma clang fp contract(off)  // each product rounded on its own, as the host decoders
     const int n_in = L.n_in, nb = L.nb;
     const size_t blk = (size_t)tok * nb + p / draco_block_values(L.code);
     float val = 0.f;

@@ -216,6 +216,20 @@ const float* get_vec(const float* host, size_t n, int tcols) {
     return e.dev;
 }
 
+const DracoMat* find_row(const void* row, int code, int n_in, int* r) {
+    const uint8_t* p = (const uint8_t*)row;
+    for (auto& kv : S().mats) {
+        const MatEntry& e = kv.second;
+        if (e.code != code || e.n_in != n_in || !e.m.dev) continue;
+        const uint8_t* base = (const uint8_t*)kv.first;
+        const size_t rb = draco_row_bytes(code, n_in);
+        if (p < base || p >= base + rb * (size_t)e.n_out || (size_t)(p - base) % rb) continue;
+        *r = (int)((size_t)(p - base) / rb);
+        return &e.m;
+    }
+    return nullptr;
+}
+
 int forget(const void* host) {
     State& s = S();
     int n = 0;

@@ -47,6 +47,9 @@ uint64_t epoch();
 // assumed immutable while registered (draco_forget drops an entry).
 const DracoMat* get_mat(const void* host, int code, int n_out, int n_in);
 int forget(const void* host);
+// The registered matrix (format code, n_in) whose host rows hold `row` at a
+// row start; *r = the row's index.  nullptr when none does.
+const DracoMat* find_row(const void* row, int code, int n_in, int* r);
 // Device copy of a caller-owned fp32 array of n floats (norm weights, conv
 // taps, ...), registered like a weight.  tcols > 0: the host array is
 // [n / tcols][tcols] and the device copy is its transpose [tcols][n / tcols].

@@ -99,6 +99,7 @@ SIGNATURES = {
     # prefill GEMM (src/m5/m5_gemm_fused.c:231-241, src/m5/m5_gemm.c:249-272)
     "m5_gemm_auto": (ct.c_int, [ct.c_int, f32p, u8p, ct.c_int, ct.c_int, ct.c_int, f32p]),
     "m5_gemm": (ct.c_int, [ct.c_int, f32p, u8p, ct.c_int, ct.c_int, ct.c_int, f32p, f32p]),
+    "m5_dequant_row": (ct.c_int, [ct.c_int, u8p, ct.c_int, f32p]),
     "draco_bench_gemm": (ct.c_int, [ct.c_int, u8p, ct.c_int, ct.c_int, ct.c_int, ct.c_int, ct.c_int, f32p]),
     # Gated-DeltaNet scan (src/m6_gdn_scan.c:18-93)
     "m6_gdn_scan": (None, [f32p] * 8 + [ct.c_int] * 3 + [f32p, f32p]),

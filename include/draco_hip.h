@@ -214,6 +214,12 @@ int draco_bench_granite_moe(const float* x0, const uint64_t* ptrs, const int* co
  * `wbuf` is not used. */
 int m5_gemm_auto(int code, const float* X, const uint8_t* W, int c, int n_out, int n_in, float* Y);
 int m5_gemm(int code, const float* X, const uint8_t* W, int T, int n_out, int n_in, float* Y, float* wbuf);
+/* m5_dequant_row: src/m5/m5_gemm.c:55-235 -- one GGUF row (host) ->
+ * out[n_in] fp32, decoded on the device (from the resident copy when the row
+ * lies inside a registered matrix).  0 done, -1 code not served: served are
+ * Q8_0, Q4_K, Q6_K and F16 (the reference also decodes Q5_K and the IQ
+ * formats). */
+int m5_dequant_row(int code, const uint8_t* row, int n_in, float* out);
 /* No reference counterpart: out[0] us per GEMM including the activation
  * digitization, out[1] us for the GEMM kernel alone (graph replays over
  * n_copies weight copies). */
