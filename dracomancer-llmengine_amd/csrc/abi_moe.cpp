@@ -126,12 +126,15 @@ int moe_work(MoeWork& w, int n_in, int n_exp, int n_used, int inter, int n_out) 
 }
 
 // enqueue router + routed gate/up + down/combine (x, out device pointers)
+// norm_w set: x is the layer input, normalised by the router launch into xn
+// (RMSNorm with norm_w, eps), which the expert launches read
 int enqueue_moe(ExpertSet* s, const float* x, float* out, const float* resid, MoeWork& w, int n_exp, int n_used,
-                int inter, int n_in, int n_out, hipStream_t st) {
-    if (draco_moe_logits_launch(x, (const float*)s->router->dev, n_exp, n_in, w.logits, st))
+                int inter, int n_in, int n_out, hipStream_t st, const float* norm_w = nullptr, float eps = 0.f,
+                float* xn = nullptr) {
+    if (draco_moe_logits_launch(x, (const float*)s->router->dev, n_exp, n_in, w.logits, st, norm_w, eps, xn))
         return fail(-1, "moe router launch rejected");
     MoeArgs a = {};
-    a.x = x;
+    a.x = norm_w ? xn : x;
     a.n_in = n_in;
     a.n_out_e = inter;
     a.n_slots = n_used;
@@ -413,8 +416,12 @@ MoeLayer* draco_moe_layer(const DracoMoeP* p) {
 int draco_moe_layer_enqueue(MoeLayer* m, const float* x, const float* norm_w, float eps, float* out,
                             const float* resid, hipStream_t st) {
     const DracoMoeP& p = m->snap;
-    dk_rmsnorm(x, norm_w, m->xn, p.n_in, eps, st);
-    return enqueue_moe(m->set, m->xn, out, resid, m->w, p.n_exp, p.n_used, p.inter, p.n_in, p.n_out, st);
+    if (p.n_in > 4096 || !norm_w) {  // wider than the router's norm prologue, or no norm weight
+        dk_rmsnorm(x, norm_w, m->xn, p.n_in, eps, st);
+        return enqueue_moe(m->set, m->xn, out, resid, m->w, p.n_exp, p.n_used, p.inter, p.n_in, p.n_out, st);
+    }
+    return enqueue_moe(m->set, x, out, resid, m->w, p.n_exp, p.n_used, p.inter, p.n_in, p.n_out, st, norm_w, eps,
+                       m->xn);
 }
 
 int draco_moe_layer_enqueue_xn(MoeLayer* m, const float* xn, float* out, const float* resid, hipStream_t st) {

@@ -46,87 +46,95 @@ constexpr float EPS = 1e-6f;
 __device__ __forceinline__ float silu(float a) { return a / (1.f + expf(-a)); }
 
 // Decode-step gates of V head h (src/m6_layer.c:237-256): every thread
-// returns beta and the decay exp(alpha).  xn = h1 * rms^-1 * attn_norm is
+// gets beta and the decay exp(alpha).  xn = h1 * rms^-1 * attn_norm is
 // recomputed by each block (H floats, L2-resident after the first block);
 // the beta / alpha rows are contiguous [n_vh][H], read once per block.
+// issue() requests the operands (blocks of 512 threads hold them in
+// registers) so the kernel can put them ahead of its state loads; finish()
+// computes, streaming them in two passes when the block is narrower.
 template <int NW>
-__device__ __forceinline__ void gdn_gates(const GdnArgs& a, int h, int tid, float* beta, float* gdec) {
-    constexpr int NT = 64 * NW;
-    // float4 per thread covering H <= 4096; wide blocks hold them in
-    // registers, narrow ones (NV > 2) stream them in two passes
-    constexpr int NV = (4096 + 4 * NT - 1) / (4 * NT);
-    constexpr int NR = NV <= 2 ? NV : 1;
-    __shared__ float pre[3][NW];
-    const int lane = tid & 63, w = tid >> 6;
+struct GdnGates {
+    static constexpr int NT = 64 * NW;
+    static constexpr int NV = (4096 + 4 * NT - 1) / (4 * NT);  // float4 per thread covering H <= 4096
+    static constexpr int NR = NV <= 2 ? NV : 1;
     float4 hv[NR], nv[NR], bv[NR], av[NR];
-    auto load = [&](int k, int slot) {  // clamped, unconditional loads; masked below
-        const int i = 4 * tid + 4 * NT * k;
+
+    __device__ __forceinline__ void load(const GdnArgs& a, int h, int tid, int k, int slot) {
+        const int i = 4 * tid + 4 * NT * k;  // clamped, unconditional loads; masked in finish()
         const int ic = i < a.H ? i : 0;
         hv[slot] = ld4(a.h1 + ic);
         nv[slot] = ld4(a.attn_norm + ic);
         bv[slot] = ld4(a.bw + (size_t)h * a.H + ic);
         av[slot] = ld4(a.aw + (size_t)h * a.H + ic);
-    };
-    float ss = 0.f;
-    if constexpr (NR == NV) {
+    }
+    __device__ __forceinline__ void issue(const GdnArgs& a, int h, int tid) {
+        if constexpr (NR == NV) {
 #pragma unroll
-        for (int k = 0; k < NV; k++) load(k, k);
+            for (int k = 0; k < NV; k++) load(a, h, tid, k, k);
+        }
+    }
+    __device__ __forceinline__ void finish(const GdnArgs& a, int h, int tid, float* beta, float* gdec) {
+        __shared__ float pre[3][NW];
+        const int lane = tid & 63, w = tid >> 6;
+        float ss = 0.f;
+        if constexpr (NR == NV) {
 #pragma unroll
-        for (int k = 0; k < NV; k++)
-            if (4 * tid + 4 * NT * k < a.H)
-                ss += hv[k].x * hv[k].x + hv[k].y * hv[k].y + hv[k].z * hv[k].z + hv[k].w * hv[k].w;
-    } else {
-        for (int k = 0; k < NV; k++) {
-            const int i = 4 * tid + 4 * NT * k;
-            if (i < a.H) {
-                const float4 x = ld4(a.h1 + i);
-                ss += x.x * x.x + x.y * x.y + x.z * x.z + x.w * x.w;
+            for (int k = 0; k < NV; k++)
+                if (4 * tid + 4 * NT * k < a.H)
+                    ss += hv[k].x * hv[k].x + hv[k].y * hv[k].y + hv[k].z * hv[k].z + hv[k].w * hv[k].w;
+        } else {
+            for (int k = 0; k < NV; k++) {
+                const int i = 4 * tid + 4 * NT * k;
+                if (i < a.H) {
+                    const float4 x = ld4(a.h1 + i);
+                    ss += x.x * x.x + x.y * x.y + x.z * x.z + x.w * x.w;
+                }
             }
         }
-    }
-    ss = wave_sum(ss);
-    if (lane == 0) pre[0][w] = ss;
-    lds_barrier();
-    float tot = 0.f;
+        ss = wave_sum(ss);
+        if (lane == 0) pre[0][w] = ss;
+        lds_barrier();
+        float tot = 0.f;
 #pragma unroll
-    for (int q = 0; q < NW; q++) tot += pre[0][q];
-    const float inv = 1.f / sqrtf(tot / (float)a.H + EPS);
-    float pb = 0.f, pa = 0.f;
-    auto acc = [&](int k, int slot) {
-        if (4 * tid + 4 * NT * k < a.H) {
-            const float x0 = hv[slot].x * inv * nv[slot].x, x1 = hv[slot].y * inv * nv[slot].y;
-            const float x2 = hv[slot].z * inv * nv[slot].z, x3 = hv[slot].w * inv * nv[slot].w;
-            pb += bv[slot].x * x0 + bv[slot].y * x1 + bv[slot].z * x2 + bv[slot].w * x3;
-            pa += av[slot].x * x0 + av[slot].y * x1 + av[slot].z * x2 + av[slot].w * x3;
+        for (int q = 0; q < NW; q++) tot += pre[0][q];
+        const float inv = 1.f / sqrtf(tot / (float)a.H + EPS);
+        float pb = 0.f, pa = 0.f;
+        auto acc = [&](int k, int slot) {
+            if (4 * tid + 4 * NT * k < a.H) {
+                const float x0 = hv[slot].x * inv * nv[slot].x, x1 = hv[slot].y * inv * nv[slot].y;
+                const float x2 = hv[slot].z * inv * nv[slot].z, x3 = hv[slot].w * inv * nv[slot].w;
+                pb += bv[slot].x * x0 + bv[slot].y * x1 + bv[slot].z * x2 + bv[slot].w * x3;
+                pa += av[slot].x * x0 + av[slot].y * x1 + av[slot].z * x2 + av[slot].w * x3;
+            }
+        };
+        if constexpr (NR == NV) {
+#pragma unroll
+            for (int k = 0; k < NV; k++) acc(k, k);
+        } else {
+            for (int k = 0; k < NV; k++) {
+                load(a, h, tid, k, 0);
+                acc(k, 0);
+            }
         }
-    };
-    if constexpr (NR == NV) {
-#pragma unroll
-        for (int k = 0; k < NV; k++) acc(k, k);
-    } else {
-        for (int k = 0; k < NV; k++) {
-            load(k, 0);
-            acc(k, 0);
+        pb = wave_sum(pb);
+        pa = wave_sum(pa);
+        if (lane == 0) {
+            pre[1][w] = pb;
+            pre[2][w] = pa;
         }
-    }
-    pb = wave_sum(pb);
-    pa = wave_sum(pa);
-    if (lane == 0) {
-        pre[1][w] = pb;
-        pre[2][w] = pa;
-    }
-    lds_barrier();
-    float bacc = 0.f, aacc = 0.f;
+        lds_barrier();
+        float bacc = 0.f, aacc = 0.f;
 #pragma unroll
-    for (int q = 0; q < NW; q++) {
-        bacc += pre[1][q];
-        aacc += pre[2][q];
+        for (int q = 0; q < NW; q++) {
+            bacc += pre[1][q];
+            aacc += pre[2][q];
+        }
+        *beta = 1.f / (1.f + expf(-bacc));
+        const float avv = aacc + a.ssm_dt[h];
+        const float sp = avv > 0.f ? avv + log1pf(expf(-avv)) : log1pf(expf(avv));
+        *gdec = expf(sp * a.ssm_a[h]);
     }
-    *beta = 1.f / (1.f + expf(-bacc));
-    const float avv = aacc + a.ssm_dt[h];
-    const float sp = avv > 0.f ? avv + log1pf(expf(-avv)) : log1pf(expf(avv));
-    *gdec = expf(sp * a.ssm_a[h]);
-}
+};
 
 template <bool DEC, int NW>
 __global__ __launch_bounds__(64 * NW) void k_gdn_scan(const GdnArgs a) {
@@ -140,6 +148,10 @@ __global__ __launch_bounds__(64 * NW) void k_gdn_scan(const GdnArgs a) {
     const int NHQ = a.nhq, n_qkv = a.n_qkv, n_vh = a.n_vh, T = a.T;
     const int j = h % NHQ;
     const int col0 = sp * NC;  // this block's first column of the head
+    // decode: the gates' operands are requested first, then the conv inputs
+    // and the state, so the gate arithmetic runs while the state arrives
+    GdnGates<NW> gates;
+    if constexpr (DEC) gates.issue(a, h, tid);
     // conv channels of this thread: local c = tid + r * NT; 0..127 q_j,
     // 128..255 k_j, 256.. v_h columns col0 ..
     int ch[R];
@@ -166,17 +178,17 @@ __global__ __launch_bounds__(64 * NW) void k_gdn_scan(const GdnArgs a) {
     // state slice
     const int vl = lane >> 2, kq = lane & 3, vloc = 16 * w + vl, v = col0 + vloc;
     float* Sh = a.S + (size_t)h * SV * SV;
+    const float nw = a.ssm_norm[v];
+    // per-token inputs, prefetched one token ahead
+    float zin = T > 0 ? a.Z[(size_t)h * SV + v] : 0.f;
     float s[32];
 #pragma unroll
     for (int i = 0; i < 32; i++) s[i] = Sh[(size_t)(32 * kq + i) * SV + v];
-    const float nw = a.ssm_norm[v];
     const float scale = 1.f / sqrtf((float)SV);
 
-    // per-token inputs, prefetched one token ahead
-    float zin = T > 0 ? a.Z[(size_t)h * SV + v] : 0.f;
     float gin = 0.f, bin = 0.f;
     if constexpr (DEC) {
-        gdn_gates<NW>(a, h, tid, &bin, &gin);
+        gates.finish(a, h, tid, &bin, &gin);
     } else {
         gin = T > 0 ? a.G[h] : 0.f;
         bin = T > 0 ? a.B[h] : 0.f;

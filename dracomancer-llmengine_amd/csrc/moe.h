@@ -37,8 +37,11 @@ struct MoeArgs {
     const float* resid;      // optional: out = resid + sum
 };
 
+// norm_w set (n_in <= 4096): x is normalised first, xn = (x * rms^-1) * norm_w
+// (eps), and stored to xn_out for the expert launches.
 int draco_moe_logits_launch(const float* x, const float* gate_inp, int n_exp, int n_in, float* logits,
-                            hipStream_t st);
+                            hipStream_t st, const float* norm_w = nullptr, float eps = 0.f,
+                            float* xn_out = nullptr);
 // fm: 1 = Q4_K, 2 = Q6_K.  route (+dual): gate/up of the routed experts;
 // otherwise the grouped GEMV (xper: per-slot x).
 int draco_moe_grp_launch(MoeArgs& a, int fm, bool dual, bool xper, bool route, hipStream_t st);

@@ -8,7 +8,8 @@
 //   y[j] = W[idx[j]] . x_j, x_j = x + j*x_stride.
 //
 // Launches for one MoE FFN:
-//   k_moe_logits   one block per expert row of the fp32 router (tree sum)
+//   k_moe_logits   one block per expert row of the fp32 router (tree sum);
+//                  optionally the layer's RMSNorm first (xn stored by block 0)
 //   k_moe_grp      ROUTE: every block recomputes softmax / top-k / weights from
 //                  the logits (softmax by one wave, top-k as a parallel rank of
 //                  every expert, the bases read ahead) and runs the selected experts'
@@ -38,20 +39,51 @@ constexpr int XP_MAXV = 4;
 
 // One block per router row: every thread's loads are issued together (up to
 // 4 float4 pairs per step), then a wave-tree sum and the 4 wave sums in order.
+// NORM (n_in <= 4096, one step): x is the layer input and every block first
+// forms xn = (x * rms^-1) * norm_w itself (the same sums in every block, so
+// every block gets the same xn); block 0 also stores xn for the expert
+// launches, which then need no RMSNorm launch of their own.
+template <bool NORM>
 __global__ __launch_bounds__(256) void k_moe_logits(const float* __restrict__ x, const float* __restrict__ gi,
-                                                    int n_exp, int n_in, float* __restrict__ logits) {
-    __shared__ float part[4];
+                                                    int n_exp, int n_in, float* __restrict__ logits,
+                                                    const float* __restrict__ norm_w, float eps,
+                                                    float* __restrict__ xn_out) {
+    __shared__ float part[4], sq[4];
     constexpr int U = 4;
     const int e = blockIdx.x, tid = threadIdx.x;
     const float* w = gi + (size_t)e * n_in;
     float acc = 0.f;
     for (int i0 = tid * 4; i0 < n_in; i0 += U * 1024) {
-        float4 a[U], b[U];
+        float4 a[U], b[U], nw[U];
 #pragma unroll
         for (int u = 0; u < U; u++) {
             const int i = i0 + u * 1024;
             a[u] = i < n_in ? ld4(x + i) : make_float4(0.f, 0.f, 0.f, 0.f);
             b[u] = i < n_in ? ld4(w + i) : make_float4(0.f, 0.f, 0.f, 0.f);
+            if (NORM) nw[u] = i < n_in ? ld4(norm_w + i) : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+        if (NORM) {
+            float ss = 0.f;
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                ss = fmaf(a[u].x, a[u].x, ss);
+                ss = fmaf(a[u].y, a[u].y, ss);
+                ss = fmaf(a[u].z, a[u].z, ss);
+                ss = fmaf(a[u].w, a[u].w, ss);
+            }
+            ss = wave_sum(ss);
+            if ((tid & 63) == 0) sq[tid >> 6] = ss;
+            lds_barrier();
+            const float inv = 1.f / sqrtf(((sq[0] + sq[1]) + (sq[2] + sq[3])) / (float)n_in + eps);
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                a[u].x = a[u].x * inv * nw[u].x;
+                a[u].y = a[u].y * inv * nw[u].y;
+                a[u].z = a[u].z * inv * nw[u].z;
+                a[u].w = a[u].w * inv * nw[u].w;
+                const int i = i0 + u * 1024;
+                if (e == 0 && i < n_in) *reinterpret_cast<float4*>(xn_out + i) = a[u];
+            }
         }
 #pragma unroll
         for (int u = 0; u < U; u++) {
@@ -515,9 +547,16 @@ int dispatch_grp(const MoeArgs& a, int fm, bool dual, bool xper, bool route, int
 }  // namespace
 
 int draco_moe_logits_launch(const float* x, const float* gate_inp, int n_exp, int n_in, float* logits,
-                            hipStream_t st) {
+                            hipStream_t st, const float* norm_w, float eps, float* xn_out) {
     if (n_exp < 1 || n_exp > MOE_EXP_MAX || n_in % 4) return -1;
-    hipLaunchKernelGGL(k_moe_logits, dim3(n_exp), dim3(256), 0, st, x, gate_inp, n_exp, n_in, logits);
+    if (norm_w) {
+        if (n_in > 4096 || !xn_out) return -1;
+        hipLaunchKernelGGL(k_moe_logits<true>, dim3(n_exp), dim3(256), 0, st, x, gate_inp, n_exp, n_in, logits,
+                           norm_w, eps, xn_out);
+        return 0;
+    }
+    hipLaunchKernelGGL(k_moe_logits<false>, dim3(n_exp), dim3(256), 0, st, x, gate_inp, n_exp, n_in, logits,
+                       nullptr, 0.f, nullptr);
     return 0;
 }
 
