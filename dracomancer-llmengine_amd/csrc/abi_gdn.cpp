@@ -58,7 +58,7 @@ int gdn_host(const float* QKV, const float* Z, const float* B, const float* G, c
     a.n_qkv = n_qkv;
     a.n_vh = n_vh;
     a.nhq = (n_qkv - n_vh * 128) / 256;
-    a.nspl = draco_gdn_split(T == 1);  // one token: the decode step's split
+    a.nspl = T == 1 ? 1 : draco_gdn_split(false);  // one token: nothing to take the split's rms
     a.PSS = dpss;
     if (draco_gdn_scan_launch(a, st)) return fail(-1, "gdn scan launch rejected");
     DRACO_HIP(hipGetLastError());
@@ -132,7 +132,7 @@ int draco_bench_gdn_scan(const float* QKV, const float* Z, const float* B, const
         a.n_qkv = n_qkv;
         a.n_vh = n_vh;
         a.nhq = (n_qkv - n_vh * 128) / 256;
-        a.nspl = draco_gdn_split(n == 1);
+        a.nspl = n == 1 ? 1 : draco_gdn_split(false);
         a.PSS = dpss;
         return a;
     };

@@ -247,9 +247,32 @@ int enqueue_gdn(const GdnDev& g, const GdnBufs& b, hipStream_t st, bool post_nor
     a.ssm_a = g.ssm_a;
     a.ssm_dt = g.ssm_dt;
     a.H = QH;
-    a.nspl = draco_gdn_split(true);
     a.PSS = b.pss;
+    // split over several blocks per V head only when the ssm_out GEMV can
+    // take the gated rms into its prologue (Q4_K / Q6_K): the split's extra
+    // k_gdn_gnorm launch costs more than the split saves
+    const bool kq = g.out->L.code == DRACO_Q4_K || g.out->L.code == DRACO_Q6_K;
+    a.nspl = kq ? draco_gdn_split(true) : 1;
+    a.defer_gnorm = a.nspl > 1;
     if (draco_gdn_step_launch(a, st)) return fail(-1, "gdn step launch rejected");
+    if (a.defer_gnorm) {
+        SegLaunch s = {};
+        s.nseg = 1;
+        s.n_in = g.d_in;
+        s.x = b.on;
+        s.do_norm = 2;
+        s.eps = QEPS;
+        s.kc = b.pss;
+        SegDesc& d = s.seg[0];
+        d.base = g.out->dev;
+        d.L = g.out->L;
+        d.epi = EPI_RESID;
+        d.y = b.x2o;
+        d.yadd = b.h1;
+        if (draco_seg_launch(s, st)) return fail(-1, "gdn ssm_out launch rejected");
+        if (post_norm) dk_rmsnorm(b.x2o, g.post_norm, b.x2n, QH, QEPS, st);
+        return 0;
+    }
     const Proj out[1] = {{g.out, b.x2o, b.h1}};
     const PostNorm pn = {g.post_norm, b.x2n};
     return enqueue_proj(out, 1, b.on, g.d_in, nullptr, b.xn, st, post_norm ? &pn : nullptr);
@@ -873,7 +896,7 @@ int enqueue_qchunk(QStack* s, int T, int pos0, hipStream_t st) {
             a.n_qkv = g.n_qkv;
             a.n_vh = g.n_vh;
             a.nhq = QNKH;
-            a.nspl = draco_gdn_split(T == 1);
+            a.nspl = T == 1 ? 1 : draco_gdn_split(false);
             a.PSS = s->PPSS;
             if (draco_gdn_scan_launch(a, st)) return fail(-1, "qwen prefill: scan rejected");
             if (draco_enqueue_gemm(*g.out, s->ON, T, s->Y, s->dig, false, st)) return -1;

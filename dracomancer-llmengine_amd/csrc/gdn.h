@@ -26,6 +26,10 @@ struct GdnArgs {
     // the gated rms runs in a second launch and needs PSS [T][n_vh][8] floats.
     int nspl;
     float* PSS;
+    // split only: leave ON = (o / sqrt(128)) * ssm_norm * silu(z) and PSS
+    // for the consumer, which scales each head by its rms itself (the
+    // ssm_out GEMV's GNORM prologue) instead of a k_gdn_gnorm launch
+    bool defer_gnorm;
 };
 
 // blocks per V head for the decode step / for scans of several tokens

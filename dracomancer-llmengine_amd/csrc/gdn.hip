@@ -46,17 +46,19 @@ constexpr float EPS = 1e-6f;
 __device__ __forceinline__ float silu(float a) { return a / (1.f + expf(-a)); }
 
 // Decode-step gates of V head h (src/m6_layer.c:237-256): every thread
-// gets beta and the decay exp(alpha).  xn = h1 * rms^-1 * attn_norm is
-// recomputed by each block (H floats, L2-resident after the first block);
-// the beta / alpha rows are contiguous [n_vh][H], read once per block.
-// issue() requests the operands (blocks of 512 threads hold them in
-// registers) so the kernel can put them ahead of its state loads; finish()
-// computes, streaming them in two passes when the block is narrower.
+// gets beta and the decay exp(alpha).  xn = h1 * rms^-1 * attn_norm: the
+// block reduces the sum of squares of h1 and the two dots of (h1 * attn_norm)
+// with its head's beta / alpha rows through one barrier, and applies rms^-1
+// to the dots (the reference scales each element first; the results differ
+// by fp32 rounding).  h1 and attn_norm are L2-resident after the first
+// block; the rows are contiguous [n_vh][H].  issue() requests every operand
+// (up to 8 float4 per array and thread, so blocks of 128 threads and more
+// hold them in registers) ahead of the kernel's state loads; finish() reduces.
 template <int NW>
 struct GdnGates {
     static constexpr int NT = 64 * NW;
     static constexpr int NV = (4096 + 4 * NT - 1) / (4 * NT);  // float4 per thread covering H <= 4096
-    static constexpr int NR = NV <= 2 ? NV : 1;
+    static constexpr int NR = NV <= 8 ? NV : 1;
     float4 hv[NR], nv[NR], bv[NR], av[NR];
 
     __device__ __forceinline__ void load(const GdnArgs& a, int h, int tid, int k, int slot) {
@@ -76,35 +78,14 @@ struct GdnGates {
     __device__ __forceinline__ void finish(const GdnArgs& a, int h, int tid, float* beta, float* gdec) {
         __shared__ float pre[3][NW];
         const int lane = tid & 63, w = tid >> 6;
-        float ss = 0.f;
-        if constexpr (NR == NV) {
-#pragma unroll
-            for (int k = 0; k < NV; k++)
-                if (4 * tid + 4 * NT * k < a.H)
-                    ss += hv[k].x * hv[k].x + hv[k].y * hv[k].y + hv[k].z * hv[k].z + hv[k].w * hv[k].w;
-        } else {
-            for (int k = 0; k < NV; k++) {
-                const int i = 4 * tid + 4 * NT * k;
-                if (i < a.H) {
-                    const float4 x = ld4(a.h1 + i);
-                    ss += x.x * x.x + x.y * x.y + x.z * x.z + x.w * x.w;
-                }
-            }
-        }
-        ss = wave_sum(ss);
-        if (lane == 0) pre[0][w] = ss;
-        lds_barrier();
-        float tot = 0.f;
-#pragma unroll
-        for (int q = 0; q < NW; q++) tot += pre[0][q];
-        const float inv = 1.f / sqrtf(tot / (float)a.H + EPS);
-        float pb = 0.f, pa = 0.f;
+        float ss = 0.f, pb = 0.f, pa = 0.f;
         auto acc = [&](int k, int slot) {
             if (4 * tid + 4 * NT * k < a.H) {
-                const float x0 = hv[slot].x * inv * nv[slot].x, x1 = hv[slot].y * inv * nv[slot].y;
-                const float x2 = hv[slot].z * inv * nv[slot].z, x3 = hv[slot].w * inv * nv[slot].w;
-                pb += bv[slot].x * x0 + bv[slot].y * x1 + bv[slot].z * x2 + bv[slot].w * x3;
-                pa += av[slot].x * x0 + av[slot].y * x1 + av[slot].z * x2 + av[slot].w * x3;
+                const float4 x = hv[slot], n = nv[slot], b = bv[slot], al = av[slot];
+                ss += x.x * x.x + x.y * x.y + x.z * x.z + x.w * x.w;
+                const float x0 = x.x * n.x, x1 = x.y * n.y, x2 = x.z * n.z, x3 = x.w * n.w;
+                pb += b.x * x0 + b.y * x1 + b.z * x2 + b.w * x3;
+                pa += al.x * x0 + al.y * x1 + al.z * x2 + al.w * x3;
             }
         };
         if constexpr (NR == NV) {
@@ -116,21 +97,25 @@ struct GdnGates {
                 acc(k, 0);
             }
         }
+        ss = wave_sum(ss);
         pb = wave_sum(pb);
         pa = wave_sum(pa);
         if (lane == 0) {
+            pre[0][w] = ss;
             pre[1][w] = pb;
             pre[2][w] = pa;
         }
         lds_barrier();
-        float bacc = 0.f, aacc = 0.f;
+        float tot = 0.f, bacc = 0.f, aacc = 0.f;
 #pragma unroll
         for (int q = 0; q < NW; q++) {
+            tot += pre[0][q];
             bacc += pre[1][q];
             aacc += pre[2][q];
         }
-        *beta = 1.f / (1.f + expf(-bacc));
-        const float avv = aacc + a.ssm_dt[h];
+        const float inv = 1.f / sqrtf(tot / (float)a.H + EPS);
+        *beta = 1.f / (1.f + expf(-(bacc * inv)));
+        const float avv = aacc * inv + a.ssm_dt[h];
         const float sp = avv > 0.f ? avv + log1pf(expf(-avv)) : log1pf(expf(avv));
         *gdec = expf(sp * a.ssm_a[h]);
     }
@@ -276,7 +261,8 @@ __global__ __launch_bounds__(64 * NW) void k_gdn_scan(const GdnArgs a) {
             if (kq == 0) a.ON[(size_t)t * n_vh * SV + (size_t)h * SV + v] = o * inv2 * nw * silu(z);
         } else {
             // o / sqrt(128) and this wave's sum of squares; k_gdn_gnorm finishes
-            if (kq == 0) a.ON[(size_t)t * n_vh * SV + (size_t)h * SV + v] = o;
+            // (deferred: o * ssm_norm * silu(z), and the consumer applies the rms)
+            if (kq == 0) a.ON[(size_t)t * n_vh * SV + (size_t)h * SV + v] = a.defer_gnorm ? o * nw * silu(z) : o;
             if (lane == 0) a.PSS[((size_t)t * n_vh + h) * 8 + sp * NW + w] = o2;
         }
         lds_barrier();  // cq/ck/cv/red/ored are rewritten by the next token
@@ -317,16 +303,19 @@ int launch_scan(const GdnArgs& a, int nspl, hipStream_t st) {
     case 8: hipLaunchKernelGGL((k_gdn_scan<DEC, 1>), dim3(a.n_vh, 8), dim3(64), 0, st, a); break;
     default: return -1;
     }
-    hipLaunchKernelGGL(k_gdn_gnorm, dim3(a.T, a.n_vh), dim3(SV), 0, st, a);
+    if (!a.defer_gnorm) hipLaunchKernelGGL(k_gdn_gnorm, dim3(a.T, a.n_vh), dim3(SV), 0, st, a);
     return 0;
 }
 
-// Measured on MI355X (configs[4] heads, 32 V heads): a decode step takes
-// 6.9 us unsplit and 6.4-6.5 us split 4-way, less than the second launch the
-// split needs, so single tokens stay unsplit; a 64-token scan takes 1.73
+// Measured on MI355X (configs[4] heads, 32 V heads, graph-replayed): the
+// decode step with its gates takes 8.3 us in one block per head and 6.1 us
+// split 4 ways (6.3 two ways, 7.4 eight ways); the split's gated rms then
+// costs 0.5 us in the ssm_out GEMV's prologue (a k_gdn_gnorm launch would
+// cost more than the split saves): the 48-layer configs[4] stack decodes at
+// 974 tok/s split 4 against 922 unsplit.  A 64-token scan takes 1.73
 // us/token unsplit, 1.45 split 2-way (two waves per block: cheaper barriers
 // in the per-token chain), 1.95 4-way and 2.27 8-way.
-int g_split_dec = 1;
+int g_split_dec = 4;
 int g_split_scan = 2;
 
 }  // namespace

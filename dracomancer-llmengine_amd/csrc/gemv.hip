@@ -150,9 +150,11 @@ __device__ __forceinline__ auto seg_pick(const SegKArgs& a, int si, F f) -> decl
 // EPI: the epilogue when it is fixed for the launch (single segment), or
 // EPI_RT to read it from the tile's segment; EPI_QKV: the llama q/k/v launch
 // (segments 0, 1, 2 = rope q, rope k + KV append, V append).  NORM: the
-// RMSNorm prologue (the launch's do_norm).
+// launch's do_norm: 1 the RMSNorm prologue; 2 the GDN gated rms of 128-wide
+// groups (x, already gated by the scan, scaled per group by rsqrt(sum of
+// its 8 partial sums of squares / 128 + eps); see GNORM below).
 constexpr int EPI_RT = -1, EPI_QKV = -2;
-template <int NW, int FM, bool DUAL, bool MULTI, int EPI, bool NORM, bool IPT1>
+template <int NW, int FM, bool DUAL, bool MULTI, int EPI, int NORM, bool IPT1>
 __global__ __launch_bounds__(64 * NW) void k_dq(const SegKArgs a) {
     extern __shared__ __align__(16) uint8_t smem[];
     constexpr int NT = 64 * NW;
@@ -201,12 +203,18 @@ __global__ __launch_bounds__(64 * NW) void k_dq(const SegKArgs a) {
 
     // ---- prologue part 1: x (and norm weight) loads, then the first item's weights
     float4 xv[XP_MAXV], wv[XP_MAXV];
+    // NORM 2 (GNORM): the group partials [n_in / 128][8] = a.kc
+    float4 pv0[NORM == 2 ? XP_MAXV : 1], pv1[NORM == 2 ? XP_MAXV : 1];
 #pragma unroll
     for (int q = 0; q < XP_MAXV; q++) {
         const int i4 = tid + q * NT;
         if (i4 < n4) {
             xv[q] = ld4(a.x + 4 * i4);
-            if (NORM && a.norm_w) wv[q] = ld4(a.norm_w + 4 * i4);
+            if (NORM == 1 && a.norm_w) wv[q] = ld4(a.norm_w + 4 * i4);
+            if constexpr (NORM == 2) {
+                pv0[q] = ld4(a.kc + ((4 * i4) >> 7) * 8);
+                pv1[q] = ld4(a.kc + ((4 * i4) >> 7) * 8 + 4);
+            }
         }
     }
     Frag P0, P1, Q0, Q1;
@@ -242,7 +250,7 @@ __global__ __launch_bounds__(64 * NW) void k_dq(const SegKArgs a) {
     load_next(P0, Q0);
     // the zero page: written by the block before its barrier, or without the
     // barrier (no RMSNorm) by every wave for itself (identical values)
-    if (NORM)
+    if (NORM == 1)
         for (int i = tid; i < 256; i += NT) reinterpret_cast<uint32_t*>(zero)[i] = 0u;
     else
         for (int i = lane; i < 256; i += 64) reinterpret_cast<uint32_t*>(zero)[i] = 0u;
@@ -260,7 +268,17 @@ __global__ __launch_bounds__(64 * NW) void k_dq(const SegKArgs a) {
         const int i4 = tid + q * NT;
         if (i4 >= n4) break;
         float4 v = xv[q];
-        if (NORM) {
+        if constexpr (NORM == 2) {
+            // GNORM (src/m6_layer.c:320-331): the group's 8 partial sums in
+            // order (as k_gdn_gnorm), x = (o * norm_w * silu(z)) * rsqrt(.)
+            const float4 p0 = pv0[q], p1 = pv1[q];
+            float ms2 = 0.f;
+            ms2 += p0.x; ms2 += p0.y; ms2 += p0.z; ms2 += p0.w;
+            ms2 += p1.x; ms2 += p1.y; ms2 += p1.z; ms2 += p1.w;
+            const float inv2 = 1.f / sqrtf(ms2 / 128.f + a.eps);
+            v.x *= inv2; v.y *= inv2; v.z *= inv2; v.w *= inv2;
+        }
+        if (NORM == 1) {
             ss = fmaf(v.x, v.x, ss);
             ss = fmaf(v.y, v.y, ss);
             ss = fmaf(v.z, v.z, ss);
@@ -272,7 +290,7 @@ __global__ __launch_bounds__(64 * NW) void k_dq(const SegKArgs a) {
         }
         digits4(v, i4, xd, xsm);
     }
-    if (NORM) {
+    if (NORM == 1) {
         ss = wave_sum(ss);
         if (lane == 0) ssp[w] = ss;
         lds_barrier();
@@ -288,7 +306,7 @@ __global__ __launch_bounds__(64 * NW) void k_dq(const SegKArgs a) {
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
     }
     float inv = 1.f;
-    if (NORM) {
+    if (NORM == 1) {
         float tot = 0.f;
 #pragma unroll
         for (int i = 0; i < NW; i++) tot += ssp[i];
@@ -394,7 +412,7 @@ __global__ __launch_bounds__(64 * NW) void k_dq(const SegKArgs a) {
                     v += red[q * 16 + tid];
                     if (DUAL) v2 += red[(NW + q) * 16 + tid];
                 }
-                if (NORM) {
+                if (NORM == 1) {
                     v *= inv;
                     v2 *= inv;
                 }
@@ -726,7 +744,7 @@ int cu_count() {
 
 size_t dq_lds_bytes(int n_in, int nw) { return (size_t)(n_in / 16) * 72 + 1024 + (size_t)2 * nw * 16 * 4 + (size_t)nw * 4; }
 
-template <int NW, int FM, bool DUAL, bool MULTI, int EPI, bool NORM, bool IPT1>
+template <int NW, int FM, bool DUAL, bool MULTI, int EPI, int NORM, bool IPT1>
 void launch_dq1(SegLaunch& a, int grid, hipStream_t st) {
     static std::once_flag once;
     std::call_once(once, [] {
@@ -738,7 +756,7 @@ void launch_dq1(SegLaunch& a, int grid, hipStream_t st) {
                        dq_lds_bytes(a.n_in, NW), st, seg_kargs(a, false));
 }
 
-template <int NW, int FM, bool DUAL, bool MULTI, int EPI, bool NORM>
+template <int NW, int FM, bool DUAL, bool MULTI, int EPI, int NORM>
 void launch_dq(SegLaunch& a, int grid, hipStream_t st) {
     if ((a.n_in >> 8) <= NW) launch_dq1<NW, FM, DUAL, MULTI, EPI, NORM, true>(a, grid, st);
     else launch_dq1<NW, FM, DUAL, MULTI, EPI, NORM, false>(a, grid, st);
@@ -746,7 +764,7 @@ void launch_dq(SegLaunch& a, int grid, hipStream_t st) {
 
 // single-segment launches get their epilogue at compile time (a SwiGLU pair
 // is always one); the rest read it per tile
-template <int NW, int FM, bool DUAL, bool NORM>
+template <int NW, int FM, bool DUAL, int NORM>
 void launch_dq_e(SegLaunch& a, bool multi, int grid, hipStream_t st) {
     if constexpr (DUAL) {
         launch_dq<NW, FM, true, false, EPI_SWIGLU, NORM>(a, grid, st);  // dual launches have exactly one pair
@@ -761,8 +779,13 @@ void launch_dq_e(SegLaunch& a, bool multi, int grid, hipStream_t st) {
 
 template <int NW, int FM, bool DUAL>
 void launch_dq_m(SegLaunch& a, bool multi, int grid, hipStream_t st) {
-    if (a.do_norm) launch_dq_e<NW, FM, DUAL, true>(a, multi, grid, st);
-    else launch_dq_e<NW, FM, DUAL, false>(a, multi, grid, st);
+    if (a.do_norm == 2) {  // GNORM: one residual segment (checked by seg_launch_dq)
+        if constexpr (!DUAL) launch_dq<NW, FM, false, false, EPI_RESID, 2>(a, grid, st);
+    } else if (a.do_norm) {
+        launch_dq_e<NW, FM, DUAL, 1>(a, multi, grid, st);
+    } else {
+        launch_dq_e<NW, FM, DUAL, 0>(a, multi, grid, st);
+    }
 }
 
 template <int NW>
@@ -778,9 +801,9 @@ void launch_dq_nw(SegLaunch& a, int fm, bool dual, int grid, hipStream_t st) {
     } else {
         const bool qkv = a.nseg == 3 && a.seg[0].epi == EPI_ROPE_Q && a.seg[1].epi == EPI_ROPE_K &&
                          a.seg[2].epi == EPI_V_APPEND;
-        if (qkv && a.do_norm) launch_dq<NW, 3, false, true, EPI_QKV, true>(a, grid, st);
-        else if (a.do_norm) launch_dq<NW, 3, false, true, EPI_RT, true>(a, grid, st);
-        else launch_dq<NW, 3, false, true, EPI_RT, false>(a, grid, st);
+        if (qkv && a.do_norm) launch_dq<NW, 3, false, true, EPI_QKV, 1>(a, grid, st);
+        else if (a.do_norm) launch_dq<NW, 3, false, true, EPI_RT, 1>(a, grid, st);
+        else launch_dq<NW, 3, false, true, EPI_RT, 0>(a, grid, st);
     }
 }
 
@@ -818,6 +841,8 @@ int seg_launch_dq(SegLaunch& a, hipStream_t st) {
         tiles += s.n_tiles;
     }
     if (dual && (a.nseg != 2 || fm == 3)) return -1;
+    // GNORM prologue: one residual segment over whole 128-wide groups
+    if (a.do_norm == 2 && (a.nseg != 1 || a.seg[0].epi != EPI_RESID || n_in % 128 || !a.kc)) return -1;
     for (int i = a.nseg; i < SEG_MAX; i++) {  // unused slots: never selected by seg_of_tile
         a.seg[i] = a.seg[a.nseg - 1];
         a.seg[i].first_tile = 1 << 30;
@@ -894,6 +919,7 @@ int draco_seg_launch(SegLaunch& a, hipStream_t st) {
         else return -1;
     }
     if (kq && q8) return -1;
+    if (a.do_norm == 2 && !kq) return -1;  // the GNORM prologue is k_dq's only
     return kq ? seg_launch_dq(a, st) : seg_launch_q8(a, st);
 }
 

@@ -343,9 +343,12 @@ int draco_qwen_prefill(const void* layers, int n_layer, int h, const uint8_t* em
                        const int* ids, int n, int pos0, float* out_x);
 int draco_set_qwen_chunk(int n);
 /* No reference counterpart: blocks per V head of the GDN scan (1, 2, 4 or 8;
- * negative keeps a setting) for single-token steps and for multi-token scans
- * (defaults 1 and 2).  Split above 1, each head's 128 state columns spread
- * over that many workgroups and the gated rms runs as a second launch.
+ * negative keeps a setting) for the decode step of the layer ops and stacks
+ * and for multi-token scans (defaults 4 and 2).  Split above 1, each head's
+ * 128 state columns spread over that many workgroups and the gated rms runs
+ * after them: in the ssm_out GEMV's prologue for decode steps with a Q4_K /
+ * Q6_K ssm_out (other formats keep one workgroup per head), as a second
+ * launch for scans.  A single-token m6_gdn_scan runs unsplit.
  * Returns the previous values as decode * 16 + scan. */
 int draco_set_gdn_split(int decode_split, int scan_split);
 /* Greedy generation from position pos0 (prompt through the chunked prefill

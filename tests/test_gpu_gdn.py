@@ -114,11 +114,12 @@ def test_gdn_scan_configs4_4096_tokens_then_decode(hip, oracle):
 
 
 @pytest.mark.parametrize("split", [1, 2, 4, 8])
-@pytest.mark.parametrize("T", [1, 20])
+@pytest.mark.parametrize("T", [2, 20])
 def test_gdn_scan_column_split(hip, oracle, split, T):
     """The scan with each head's 128 state columns split over 1, 2, 4 or 8
     workgroups (the gated rms then in a second launch) against the oracle at
-    the configs[4] head shape: outputs, state and tail."""
+    the configs[4] head shape: outputs, state and tail.  (Single-token scans
+    run unsplit; the split decode step is tested through m6_gdn_attn.)"""
     old = hip.draco_set_gdn_split(split, split)
     try:
         n_qkv, QKV, Z, B, G, conv, ssm_norm, tail, S = gg.gdn_inputs(T, 32, 16, 46 + T)

@@ -28,6 +28,23 @@ def _pf(a):
 
 @pytest.mark.parametrize("tag", [c[0] for c in gg.QWEN_GDN_CASES])
 def test_gdn_attn_vs_reference(hip, oracle, tag):
+    _gdn_attn_case(hip, oracle, tag)
+
+
+@pytest.mark.parametrize("split", [2, 4, 8])
+@pytest.mark.parametrize("tag", [c[0] for c in gg.QWEN_GDN_CASES])
+def test_gdn_attn_decode_split(hip, oracle, tag, split):
+    """The decode step with each V head's state columns over 2, 4 or 8
+    blocks; the gated rms then runs in the ssm_out GEMV's prologue (Q4_K /
+    Q6_K ssm_out; other formats keep one block per head)."""
+    old = hip.draco_set_gdn_split(split, -1)
+    try:
+        _gdn_attn_case(hip, oracle, tag)
+    finally:
+        hip.draco_set_gdn_split(old // 16, old % 16)
+
+
+def _gdn_attn_case(hip, oracle, tag):
     from dracohip import qwen35 as Q
     g = golden("qwen35.npz")
     meta = [int(v) for v in g[f"gdn_{tag}_meta"]]
