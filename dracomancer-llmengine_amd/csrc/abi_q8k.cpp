@@ -85,17 +85,19 @@ int draco_gemv_q8k_f32(int code, const float* x, int nvec, const uint8_t* W, int
     const DracoMat* m = get_mat(W, code, n_out, n_in);
     if (!m) return -2;
     float* dx = (float*)scratch(0, sizeof(float) * (size_t)n_in * nvec);
-    uint8_t* dq = (uint8_t*)scratch(2, q8k_bytes(n_in, nvec));
+    uint8_t* dq = (uint8_t*)scratch(2, q8k_bytes(n_in, nvec) + Q8K_IMAGE_PAD);
     float* dy = (float*)scratch(1, sizeof(float) * (size_t)n_out * nvec);
     if (!dx || !dq || !dy) return -2;
     hipStream_t st = stream();
     DRACO_HIP(hipMemcpyAsync(dx, x, sizeof(float) * (size_t)n_in * nvec, hipMemcpyHostToDevice, st));
-    if (draco_q8k_quantize_launch(dx, n_in, nvec, dq, st)) return fail(-1, "q8k quantize launch rejected");
+    // the quantizer writes the GEMV's image of the blocks (same values)
+    if (draco_q8k_quantize_launch(dx, n_in, nvec, dq, st, true)) return fail(-1, "q8k quantize launch rejected");
     Q8Launch a = {};
     a.base = m->dev;
     a.L = m->L;
     a.n_in = n_in;
     a.xq = dq;
+    a.img = true;
     a.y = dy;
     a.y_stride = n_out;
     if (draco_gemv_q8k_launch(a, nvec, false, st)) return fail(-1, "q8k gemv launch rejected");
@@ -165,20 +167,21 @@ int draco_bench_gemv_q8k(int code, const uint8_t* W, int n_out, int n_in, int nv
     uint8_t* dq;
     DRACO_HIP(hipMalloc(&dx, sizeof(float) * xh.size()));
     DRACO_HIP(hipMalloc(&dy, sizeof(float) * (size_t)n_out * nvec));
-    DRACO_HIP(hipMalloc(&dq, q8k_bytes(n_in, nvec)));
+    DRACO_HIP(hipMalloc(&dq, q8k_bytes(n_in, nvec) + Q8K_IMAGE_PAD));
     DRACO_HIP(hipMemcpy(dx, xh.data(), sizeof(float) * xh.size(), hipMemcpyHostToDevice));
     hipStream_t st = stream();
-    auto gemv = [&](int i) {
+    auto gemv = [&](int i) {  // as draco_gemv_q8k_f32: the quantizer's GEMV image
         Q8Launch a = {};
         a.base = dev[i % n_copies];
         a.L = L;
         a.n_in = n_in;
         a.xq = dq;
+        a.img = true;
         a.y = dy;
         a.y_stride = n_out;
         return draco_gemv_q8k_launch(a, nvec, false, st);
     };
-    if (draco_q8k_quantize_launch(dx, n_in, nvec, dq, st)) return fail(-1, "bench: quantize rejected");
+    if (draco_q8k_quantize_launch(dx, n_in, nvec, dq, st, true)) return fail(-1, "bench: quantize rejected");
     for (int i = 0; i < n_copies; i++)
         if (gemv(i)) return fail(-1, "bench: gemv rejected");
     DRACO_HIP(hipStreamSynchronize(st));
@@ -190,7 +193,7 @@ int draco_bench_gemv_q8k(int code, const uint8_t* W, int n_out, int n_in, int nv
         hipGraphExec_t exec;
         DRACO_HIP(hipStreamBeginCapture(st, hipStreamCaptureModeRelaxed));
         for (int i = 0; i < iters; i++) {
-            if (mode == 1) draco_q8k_quantize_launch(dx, n_in, nvec, dq, st);
+            if (mode == 1) draco_q8k_quantize_launch(dx, n_in, nvec, dq, st, true);
             gemv(i);
         }
         DRACO_HIP(hipStreamEndCapture(st, &graph));

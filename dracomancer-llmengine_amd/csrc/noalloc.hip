@@ -19,7 +19,7 @@
 #include "q8k.h"
 #include "runtime.h"
 
-constexpr size_t NOALLOC_Q8K_BYTES = 1u << 20;  // 1 MiB: nvec * (n_in / 256) * 292 bytes at most
+constexpr size_t NOALLOC_Q8K_BYTES = 1u << 20;  // 1 MiB: nvec * (n_in / 256) * 292 + 16 bytes at most
 constexpr int NOALLOC_MAX_DEVICES = 64;
 
 // The staging array.  File scope, outside any namespace: the compiler gives a
@@ -70,7 +70,7 @@ int draco_gemv_q8k_f32_noalloc(int code, const float* x, int nvec, const uint8_t
     if (n_out <= 0 || n_in <= 0 || n_in % 256) return fail(-1, "noalloc q8k gemv: bad shape %dx%d", n_out, n_in);
     if (nvec != 1 && nvec != 4 && nvec != 8) return fail(-1, "noalloc q8k gemv: nvec %d not in {1, 4, 8}", nvec);
     if (!x || !W || !y) return fail(-1, "noalloc q8k gemv: null pointer");
-    const size_t need = (size_t)nvec * (size_t)(n_in / 256) * Q8K_BLOCK_BYTES;
+    const size_t need = (size_t)nvec * (size_t)(n_in / 256) * Q8K_BLOCK_BYTES + Q8K_IMAGE_PAD;
     if (need > NOALLOC_Q8K_BYTES)
         return fail(-1, "noalloc q8k gemv: %zu bytes of Q8_K staging exceed the %zu-byte static array", need,
                     NOALLOC_Q8K_BYTES);
@@ -84,12 +84,13 @@ int draco_gemv_q8k_f32_noalloc(int code, const float* x, int nvec, const uint8_t
     DracoLayout L;
     if (draco_layout(code, n_out, n_in, &L)) return fail(-1, "noalloc q8k gemv: no layout for %dx%d", n_out, n_in);
     hipStream_t st = stream ? (hipStream_t)stream : draco::stream();
-    if (draco_q8k_quantize_launch(x, n_in, nvec, stage, st)) return fail(-1, "noalloc q8k quantize rejected");
+    if (draco_q8k_quantize_launch(x, n_in, nvec, stage, st, true)) return fail(-1, "noalloc q8k quantize rejected");
     Q8Launch a = {};
     a.base = W;
     a.L = L;
     a.n_in = n_in;
     a.xq = stage;
+    a.img = true;
     a.y = y;
     a.y_stride = n_out;
     if (draco_gemv_q8k_launch(a, nvec, false, st)) return fail(-1, "noalloc q8k gemv launch rejected");

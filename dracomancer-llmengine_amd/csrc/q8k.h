@@ -10,7 +10,9 @@ struct Q8Launch {
     const uint8_t* base;  // weights, tile layout (formats.h)
     DracoLayout L;
     int n_in;
-    const uint8_t* xq;    // nvec * (n_in/256) Q8_K blocks, vector-major (device)
+    const uint8_t* xq;    // nvec * (n_in/256) Q8_K blocks, vector-major (device);
+                          // with img: the GEMV image of those blocks (below)
+    bool img;
     float* y;             // y[v * y_stride + row]
     int y_stride;
     int row0, row1;       // rows computed (row1 == 0: n_out)
@@ -20,7 +22,12 @@ struct Q8Launch {
     int tile0, n_tiles;
 };
 
-// Quantize nvec vectors of n floats (n % 256 == 0) into Q8_K blocks.
-int draco_q8k_quantize_launch(const float* x, int n, int nvec, uint8_t* out, hipStream_t st);
+// Quantize nvec vectors of n floats (n % 256 == 0) into Q8_K blocks.  With
+// image, out receives the same values as the GEMV's LDS image instead of
+// blocks: q8 [nvec][n] int8, bsums [n/16][nvec] int16, d [n/256][nvec]
+// float, contiguous (the same byte count as the blocks; buffers for it need
+// Q8K_IMAGE_PAD bytes more, which the GEMV's 16-byte copy may read).
+constexpr int Q8K_IMAGE_PAD = 16;
+int draco_q8k_quantize_launch(const float* x, int n, int nvec, uint8_t* out, hipStream_t st, bool image = false);
 // nvec in {1, 4, 8}; isums requires nvec == 1.
 int draco_gemv_q8k_launch(Q8Launch& a, int nvec, bool isums, hipStream_t st);

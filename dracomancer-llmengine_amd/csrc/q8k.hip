@@ -32,6 +32,8 @@ namespace {
 
 // ------------------------------------------------------------ quantizer --
 // grid (n/256, nvec), 256 threads: thread t owns value t of the block.
+// IMG: the values go to the GEMV image (q8k.h) instead of the block.
+template <bool IMG>
 __global__ __launch_bounds__(256) void k_q8k_quantize(const float* __restrict__ x, int n, uint8_t* __restrict__ out) {
     __shared__ float wv[4];
     __shared__ int wi[4];
@@ -68,6 +70,15 @@ __global__ __launch_bounds__(256) void k_q8k_quantize(const float* __restrict__ 
         d = 1.f / iscale;
     }
     const int s = group_reduce<16>(q, OpAdd{});
+    if (IMG) {
+        const int nv = gridDim.y;
+        out[(size_t)v * n + (size_t)b * 256 + t] = (uint8_t)(int8_t)q;
+        int16_t* bs = reinterpret_cast<int16_t*>(out + (size_t)nv * n);
+        if ((t & 15) == 0) bs[(size_t)(b * 16 + (t >> 4)) * nv + v] = (int16_t)s;
+        float* dd = reinterpret_cast<float*>(bs + (size_t)(n / 16) * nv);
+        if (t == 0) dd[(size_t)b * nv + v] = d;
+        return;
+    }
     uint8_t* blk = out + ((size_t)v * (n / 256) + b) * Q8K_BLOCK_BYTES;
     blk[4 + t] = (uint8_t)(int8_t)q;
     if ((t & 15) == 0) *reinterpret_cast<int16_t*>(blk + 260 + 2 * (t >> 4)) = (int16_t)s;
@@ -76,17 +87,21 @@ __global__ __launch_bounds__(256) void k_q8k_quantize(const float* __restrict__ 
 
 // ----------------------------------------------------------------- GEMV --
 // FM: 1 = Q4_K, 2 = Q6_K.  NB: activation vectors (1, 4 or 8).  ISUMS: also
-// write each (row, super-block)'s integer sums (NB == 1).
-template <int NW, int FM, int NB, bool ISUMS>
+// write each (row, super-block)'s integer sums (NB == 1).  IMG: xq is the
+// GEMV image (q8 [NB][n_in], bsums [ng][NB], d [nb][NB]), which is the LDS
+// layout itself, so the prologue is a flat 16-byte copy; otherwise the
+// prologue scatters the Q8_K blocks into that layout.
+template <int NW, int FM, int NB, bool ISUMS, bool IMG>
 __global__ __launch_bounds__(64 * NW) void k_dq8(const Q8Launch a) {
     extern __shared__ __align__(16) uint8_t smem[];
     constexpr int NT = 64 * NW, NH = NB >= 4 ? NB / 4 : 1;
     const int n_in = a.n_in, nb = n_in >> 8, ng = n_in >> 4;
-    int8_t* q8 = reinterpret_cast<int8_t*>(smem);                        // [NB][n_in]
-    int8_t* zero = q8 + (size_t)NB * n_in;                               // 1 KB of zeros
-    int16_t* bsum = reinterpret_cast<int16_t*>(zero + 1024);             // [ng][NB]
-    float* d8 = reinterpret_cast<float*>(bsum + (size_t)ng * NB);      // [nb][NB] (ng % 16 == 0: aligned)
-    float* red = d8 + (size_t)nb * NB;                                   // [NB][NW][16]
+    const size_t img = (size_t)NB * nb * Q8K_BLOCK_BYTES;                   // image bytes
+    int8_t* q8 = reinterpret_cast<int8_t*>(smem);                           // [NB][n_in]
+    int16_t* bsum = reinterpret_cast<int16_t*>(q8 + (size_t)NB * n_in);     // [ng][NB]
+    float* d8 = reinterpret_cast<float*>(bsum + (size_t)ng * NB);         // [nb][NB] (ng % 16 == 0: aligned)
+    int8_t* zero = reinterpret_cast<int8_t*>(smem + ((img + 15) & ~(size_t)15));  // 1 KB of zeros
+    float* red = reinterpret_cast<float*>(zero + 1024);                     // [NB][NW][16]
 
     const int tid = threadIdx.x, lane = tid & 63, j = lane & 15, g = lane >> 4;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -108,7 +123,13 @@ __global__ __launch_bounds__(64 * NW) void k_dq8(const Q8Launch a) {
 
     // prologue: Q8_K blocks -> LDS (q8 bytes, bsums, d)
     for (int i = tid; i < 256; i += NT) reinterpret_cast<uint32_t*>(zero)[i] = 0u;
-    const int ndw = NB * nb * (Q8K_BLOCK_BYTES / 4);
+    if (IMG) {
+        const int n16 = (int)((img + 15) >> 4);
+        const uint4* src = reinterpret_cast<const uint4*>(a.xq);
+        uint4* dst = reinterpret_cast<uint4*>(smem);
+        for (int i = tid; i < n16; i += NT) dst[i] = src[i];
+    }
+    const int ndw = IMG ? 0 : NB * nb * (Q8K_BLOCK_BYTES / 4);
     for (int i = tid; i < ndw; i += NT) {
         const int blk = i / (Q8K_BLOCK_BYTES / 4), k = i % (Q8K_BLOCK_BYTES / 4);
         const int v = blk / nb, b = blk % nb;
@@ -263,14 +284,20 @@ int cu_count() {
     return n;
 }
 
-template <int NW, int FM, int NB, bool IS>
-void launch_dq8(const Q8Launch& a, int grid, size_t lds, hipStream_t st) {
+template <int NW, int FM, int NB, bool IS, bool IMG>
+void launch_dq8i(const Q8Launch& a, int grid, size_t lds, hipStream_t st) {
     static std::once_flag once;
     std::call_once(once, [] {
-        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&k_dq8<NW, FM, NB, IS>),
+        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&k_dq8<NW, FM, NB, IS, IMG>),
                                   hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
     });
-    hipLaunchKernelGGL((k_dq8<NW, FM, NB, IS>), dim3(grid), dim3(64 * NW), lds, st, a);
+    hipLaunchKernelGGL((k_dq8<NW, FM, NB, IS, IMG>), dim3(grid), dim3(64 * NW), lds, st, a);
+}
+
+template <int NW, int FM, int NB, bool IS>
+void launch_dq8(const Q8Launch& a, int grid, size_t lds, hipStream_t st) {
+    if (a.img && !IS) launch_dq8i<NW, FM, NB, false, true>(a, grid, lds, st);
+    else launch_dq8i<NW, FM, NB, IS, false>(a, grid, lds, st);
 }
 
 template <int NW, int FM>
@@ -292,9 +319,10 @@ int launch_nb(const Q8Launch& a, int nb_vec, bool isums, int grid, size_t lds, h
 
 }  // namespace
 
-int draco_q8k_quantize_launch(const float* x, int n, int nvec, uint8_t* out, hipStream_t st) {
+int draco_q8k_quantize_launch(const float* x, int n, int nvec, uint8_t* out, hipStream_t st, bool image) {
     if (n <= 0 || n % 256 || nvec < 1) return -1;
-    hipLaunchKernelGGL(k_q8k_quantize, dim3(n / 256, nvec), dim3(256), 0, st, x, n, out);
+    if (image) hipLaunchKernelGGL(k_q8k_quantize<true>, dim3(n / 256, nvec), dim3(256), 0, st, x, n, out);
+    else hipLaunchKernelGGL(k_q8k_quantize<false>, dim3(n / 256, nvec), dim3(256), 0, st, x, n, out);
     return 0;
 }
 
@@ -313,9 +341,11 @@ int draco_gemv_q8k_launch(Q8Launch& a, int nvec, bool isums, hipStream_t st) {
         // vectors beyond nvec are read from the caller's buffer: require the padded count
         return -1;
     }
+    if (a.img && isums) return -1;
     const int nw = nb >= 32 ? 16 : (nb >= 8 ? 8 : 4);
-    const size_t lds = (size_t)NBp * n_in + 1024 + (size_t)ng * NBp * 2 + (size_t)nb * NBp * 4 +
-                       (size_t)NBp * nw * 16 * 4;
+    const size_t img = (size_t)NBp * nb * Q8K_BLOCK_BYTES;  // = NBp * n_in + ng * NBp * 2 + nb * NBp * 4
+    const size_t lds = ((img + 15) & ~(size_t)15) + 1024 + (size_t)NBp * nw * 16 * 4;
+    (void)ng;
     if (lds > 160 * 1024) return -1;
     const int cap = cu_count() * (nw == 4 ? 4 : (nw == 8 ? 2 : 1));
     const int grid = a.n_tiles < cap ? a.n_tiles : cap;

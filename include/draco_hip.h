@@ -385,9 +385,9 @@ int draco_q8k_isums(int code, const uint8_t* xq, const uint8_t* W, int n_out, in
  * hipMalloc): draco_gemv_q8k_f32 with DEVICE pointers and no allocation.
  * x [nvec][n_in] fp32, W the weights already in this library's device layout
  * (draco_repack of the GGUF rows; draco_layout_query bytes), y [nvec][n_out]
- * fp32.  The Q8_K blocks of x are staged in a static device array of
- * draco_noalloc_capacity() bytes (1 MiB: nvec * n_in / 256 * 292 bytes at
- * most; larger requests return -1).  Enqueued on `stream` (a hipStream_t;
+ * fp32.  The Q8_K values of x are staged in a static device array of
+ * draco_noalloc_capacity() bytes (1 MiB: nvec * n_in / 256 * 292 + 16 bytes
+ * at most; larger requests return -1).  Enqueued on `stream` (a hipStream_t;
  * NULL = the library's stream) and not waited for.  Every call on one GPU
  * shares that GPU's staging array: calls that overlap on one GPU race. */
 int draco_gemv_q8k_f32_noalloc(int code, const float* x, int nvec, const uint8_t* W, int n_out, int n_in, float* y,
