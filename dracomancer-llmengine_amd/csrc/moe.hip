@@ -102,11 +102,12 @@ __global__ __launch_bounds__(256) void k_moe_logits(const float* __restrict__ x,
 // Routing (src/m6_layer.c:774-821) in two parallel steps instead of n_used
 // sequential argmax rounds.  softmax_wave: one wave turns the logits into
 // probabilities sp[0, n_exp) (max and sum by wave trees; sp[n_exp, 512) =
-// -1, below every probability).  rank_slot: the rank of expert e is the
+// -1, below every probability).  rank_part: the rank of expert e is the
 // number of experts ahead of it in the reference's stable order (higher
 // probability, or the same probability and a lower index); the ranks are a
 // permutation of [0, n_exp), so the experts of rank < n_used are exactly the
-// sequential top-k, rank = slot.
+// sequential top-k, rank = slot.  Four adjacent lanes count one expert's
+// rank over a quarter of the experts each and add their counts with DPP.
 __device__ __forceinline__ void softmax_wave(const float* __restrict__ logits, int n_exp, float* sp) {
     constexpr int PER = MOE_EXP_MAX / 64;
     const int lane = threadIdx.x & 63;
@@ -133,11 +134,14 @@ __device__ __forceinline__ void softmax_wave(const float* __restrict__ logits, i
     for (int q = 0; q < PER; q++) sp[lane + 64 * q] = lane + 64 * q < n_exp ? p[q] * inv : -1.f;
 }
 
-__device__ __forceinline__ int rank_slot(const float* sp, int n_exp, int e) {
+// experts ahead of e among sp[f0, f0 + span) (span a multiple of 4; entries
+// past n_exp are -1 and never ahead)
+__device__ __forceinline__ int rank_part(const float* sp, int e, int f0, int span) {
     const float pe = sp[e];
     const float4* s4 = reinterpret_cast<const float4*>(sp);
     int r = 0;
-    for (int f = 0; f < n_exp; f += 4) {
+#pragma unroll 4
+    for (int f = f0; f < f0 + span; f += 4) {
         const float4 v = s4[f >> 2];
         r += (v.x > pe || (v.x == pe && f < e)) + (v.y > pe || (v.y == pe && f + 1 < e)) +
              (v.z > pe || (v.z == pe && f + 2 < e)) + (v.w > pe || (v.w == pe && f + 3 < e));
@@ -189,16 +193,20 @@ __global__ __launch_bounds__(64 * NW) void k_moe_grp(const MoeArgs a) {
     }
     // routing / expert bases
     if (ROUTE) {
-        // this thread's experts' bases, read while wave 0 reads the logits;
-        // slots default to expert 0 (every slot is overwritten below unless
+        // expert e = tid / 4 + k * EPP is ranked by lanes 4e'..4e'+3 (part
+        // tid % 4); part 0 reads its bases while wave 0 reads the logits.
+        // Slots default to expert 0 (every slot is overwritten below unless
         // the probabilities hold a NaN, which then cannot index out of range)
-        const uint8_t* rb0[2];
-        const uint8_t* rb1[2];
+        constexpr int EPP = NT / 4, NPASS = (MOE_EXP_MAX + EPP - 1) / EPP;
+        const int part = tid & 3;
+        const uint8_t* rb0[NPASS];
+        const uint8_t* rb1[NPASS];
 #pragma unroll
-        for (int k = 0; k < 2; k++) {
-            const int e = tid + k * NT;
-            rb0[k] = e < a.n_exp ? a.base0[e] : nullptr;
-            rb1[k] = (DUAL && e < a.n_exp) ? a.base1[e] : nullptr;
+        for (int k = 0; k < NPASS; k++) {
+            const int e = (tid >> 2) + k * EPP;
+            const bool mine = part == 0 && e < a.n_exp;
+            rb0[k] = mine ? a.base0[e] : nullptr;
+            rb1[k] = (DUAL && mine) ? a.base1[e] : nullptr;
         }
         if (tid < n_slots) {
             sidx[tid] = 0;
@@ -208,17 +216,18 @@ __global__ __launch_bounds__(64 * NW) void k_moe_grp(const MoeArgs a) {
         }
         if (w == 0) softmax_wave(a.logits, a.n_exp, sp);
         lds_barrier();
+        const int span = ((a.n_exp + 15) >> 4) << 2;  // a quarter, rounded up to whole float4s
 #pragma unroll
-        for (int k = 0; k < 2; k++) {
-            const int e = tid + k * NT;
-            if (e < a.n_exp) {
-                const int r = rank_slot(sp, a.n_exp, e);
-                if (r < n_slots) {
-                    sidx[r] = e;
-                    swt[r] = sp[e];
-                    sb0[r] = rb0[k];
-                    if (DUAL) sb1[r] = rb1[k];
-                }
+        for (int k = 0; k < NPASS; k++) {
+            if (k * EPP >= a.n_exp) break;  // uniform
+            const int e = (tid >> 2) + k * EPP;
+            int r = e < a.n_exp ? rank_part(sp, e, part * span, span) : 0;
+            r = group_reduce<4>(r, OpAdd{});
+            if (part == 0 && e < a.n_exp && r < n_slots) {
+                sidx[r] = e;
+                swt[r] = sp[e];
+                sb0[r] = rb0[k];
+                if (DUAL) sb1[r] = rb1[k];
             }
         }
     } else if (tid < n_slots) {
