@@ -22,7 +22,7 @@ int gdn_host(const float* QKV, const float* Z, const float* B, const float* G, c
     hipStream_t st = stream();
     const size_t nq = (size_t)T * n_qkv, nz = (size_t)T * n_vh * 128, nbg = (size_t)T * n_vh,
                  ns = (size_t)n_vh * 128 * 128, nt = (size_t)n_qkv * 3, nc = (size_t)n_qkv * 4;
-    const size_t npss = (size_t)T * n_vh * 8;
+    const size_t npss = (size_t)T * n_vh * GDN_PSS_STRIDE;
     float* d = (float*)scratch(6, sizeof(float) * (nq + 2 * nz + 2 * nbg + ns + nt + nc + 128 + npss));
     if (!d) return -2;
     GdnArgs a = {};
@@ -99,7 +99,7 @@ int draco_bench_gdn_scan(const float* QKV, const float* Z, const float* B, const
     const size_t nq = (size_t)T * n_qkv, nz = (size_t)T * n_vh * 128, nbg = (size_t)T * n_vh,
                  ns = (size_t)n_vh * 128 * 128, nt = (size_t)n_qkv * 3, nc = (size_t)n_qkv * 4;
     float *dq, *dz, *db, *dg, *dc, *dn, *dt, *ds, *don, *dpss;
-    DRACO_HIP(hipMalloc(&dpss, sizeof(float) * (size_t)(chunk > 1 ? chunk : 1) * n_vh * 8));
+    DRACO_HIP(hipMalloc(&dpss, sizeof(float) * (size_t)(chunk > 1 ? chunk : 1) * n_vh * GDN_PSS_STRIDE));
     DRACO_HIP(hipMalloc(&dq, sizeof(float) * nq));
     DRACO_HIP(hipMalloc(&dz, sizeof(float) * nz));
     DRACO_HIP(hipMalloc(&db, sizeof(float) * nbg));

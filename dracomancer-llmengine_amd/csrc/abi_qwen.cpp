@@ -202,7 +202,8 @@ int gdn_resolve(const GdnW* w, GdnDev& g) {
 
 int gdn_bufs(const GdnDev& g, int slot, GdnBufs& b) {
     const size_t ns = (size_t)g.n_vh * QSV * QSV, nt = (size_t)g.n_qkv * 3;
-    const size_t n = 5 * (size_t)QH + g.n_qkv + 2 * (size_t)g.d_in + ns + nt + (size_t)g.n_vh * 8 + 16 * 64;  // + carve slack
+    const size_t n = 5 * (size_t)QH + g.n_qkv + 2 * (size_t)g.d_in + ns + nt + (size_t)g.n_vh * GDN_PSS_STRIDE +
+                     16 * 64;  // + carve slack
     float* p = (float*)scratch(slot, sizeof(float) * n);
     if (!p) return -2;
     auto take = [&](size_t k) {  // 256-byte aligned carve
@@ -219,7 +220,7 @@ int gdn_bufs(const GdnDev& g, int slot, GdnBufs& b) {
     b.on = take(g.d_in);
     b.S = take(ns);
     b.tail = take(nt);
-    b.pss = take((size_t)g.n_vh * 8);
+    b.pss = take((size_t)g.n_vh * GDN_PSS_STRIDE);
     return 0;
 }
 
@@ -763,7 +764,7 @@ QStack* build_qstack(const QStackLayer* layers, int n_layer, int h) {
         qstack_alloc(k, &s->vraw, FNKV * FHD) ||
         qstack_alloc(k, &s->part, (size_t)std::max(s->max_nh, 1) * nsplit * (FHD + 2)) ||
         qstack_alloc(k, &s->fg, std::max(s->max_ff, 1)) || qstack_alloc(k, &s->fu, std::max(s->max_ff, 1)) ||
-        qstack_alloc(k, &s->pss, (size_t)std::max(s->max_vh, 1) * 8))
+        qstack_alloc(k, &s->pss, (size_t)std::max(s->max_vh, 1) * GDN_PSS_STRIDE))
         return nullptr;
     if (hipMalloc(&s->state, sizeof(int) * 16) != hipSuccess ||
         hipHostMalloc(&s->hstate, sizeof(int) * 16, hipHostMallocDefault) != hipSuccess) {
@@ -795,7 +796,7 @@ int qstack_pf(QStack* s, int cap) {
         qstack_alloc(k, &s->PK, c * FNKV * FHD) || qstack_alloc(k, &s->PV, c * FNKV * FHD) ||
         qstack_alloc(k, &s->AO, c * nh * FHD) || qstack_alloc(k, &s->Ppart, pf_part_floats(nh, cap, FHD, nspl)) ||
         qstack_alloc(k, &s->PG, c * std::max(s->max_ff, 1)) || qstack_alloc(k, &s->PU, c * std::max(s->max_ff, 1)) ||
-        qstack_alloc(k, &s->PPSS, c * std::max(s->max_vh, 1) * 8))
+        qstack_alloc(k, &s->PPSS, c * std::max(s->max_vh, 1) * GDN_PSS_STRIDE))
         return -2;
     if (hipMalloc(&s->dig, draco_gemm_digit_bytes(cap, ((win + 255) / 256) * 256)) != hipSuccess ||
         hipMalloc(&s->ids, sizeof(int) * c) != hipSuccess)

@@ -2,6 +2,10 @@
 #pragma once
 #include <hip/hip_runtime.h>
 
+// floats per (token, V head) in GdnArgs::PSS (one per wave of the head's
+// blocks); a split decode step fills 8
+constexpr int GDN_PSS_STRIDE = 64;
+
 struct GdnArgs {
     const float* QKV;       // [T][n_qkv]   (q heads, k heads, v heads; 128 each)
     const float* Z;         // [T][n_vh*128]
@@ -23,7 +27,8 @@ struct GdnArgs {
     const float* ssm_dt;     // [n_vh]
     int H;                   // <= 4096, multiple of 4
     // column split: nspl blocks per V head (1, 2, 4 or 8; 0 = 1).  Above 1
-    // the gated rms runs in a second launch and needs PSS [T][n_vh][8] floats.
+    // the gated rms runs in a second launch (or in the consumer) and needs
+    // PSS [T][n_vh][GDN_PSS_STRIDE] floats (the waves' partial sums).
     int nspl;
     float* PSS;
     // split only: leave ON = (o / sqrt(128)) * ssm_norm * silu(z) and PSS

@@ -9,13 +9,14 @@
 //   on = (o/sqrt(128)) * rsqrt(mean(o^2)+1e-6) * ssm_norm * silu(z)
 // S is [k][v] (row k), 128 x 128 fp32 per V head.
 //
-// Mapping: the 128 columns of a V head's state are split over NSPL = 8 / NW
-// blocks of NW waves (grid n_vh x NSPL); every block keeps its columns of the
-// state in registers for the whole scan.  Wave w of split sp owns columns
-// v = 16 (sp NW + w) .. +15; lane (v_lo = lane>>2, kq = lane&3) holds
-// S[32kq .. 32kq+31][v].  Each lane applies the reference's per-element
+// Mapping: the 128 columns of a V head's state are split over NSPL blocks
+// of NW waves (grid n_vh x NSPL); every block keeps its columns of the state
+// in registers for the whole scan.  Wave w of split sp owns CPW = 128 /
+// (NSPL NW) columns, v = CPW (sp NW + w) + v_lo; lane (v_lo = lane / KQ,
+// kq = lane % KQ, KQ = 64 / CPW) holds rows RPL kq .. RPL kq + RPL - 1 of
+// column v (RPL = 128 / KQ).  Each lane applies the reference's per-element
 // operations in k order within its chunk (decay, multiply, add, unfused); the
-// four chunks of a column combine with DPP moves, so the delta rule needs no
+// KQ chunks of a column combine with DPP moves, so the delta rule needs no
 // LDS and no barrier.  The conv runs on the block's threads, channel c =
 // tid + r * threads (q and k of head j in every block: the l2 norms need
 // them whole; v only for the block's columns), the tails in registers; only
@@ -26,7 +27,7 @@
 // each wave writes its columns' o / sqrt(128) to ON and the sum of their
 // squares to a partial buffer, and k_gdn_gnorm applies the rms, the norm
 // weight and the gate in place.  Results agree with the reference to fp32
-// rounding: the per-column sums are split in four chunks and the l2 / rms
+// rounding: the per-column sums are split in KQ chunks and the l2 / rms
 // sums use a tree.
 //
 // The split spreads each head's 64 KB of state over NSPL CUs (the state load
@@ -121,9 +122,14 @@ struct GdnGates {
     }
 };
 
-template <bool DEC, int NW>
+// NW waves per block, NSPL blocks per V head: a wave owns CPW = 128 /
+// (NSPL * NW) columns, KQ = 64 / CPW lanes share a column and each lane
+// holds RPL = 128 / KQ of its rows.
+template <bool DEC, int NW, int NSPL>
 __global__ __launch_bounds__(64 * NW) void k_gdn_scan(const GdnArgs a) {
-    constexpr int NT = 64 * NW, NSPL = 8 / NW, NC = 16 * NW;  // threads, splits per head, columns per block
+    constexpr int NT = 64 * NW, NC = SV / NSPL;  // threads, columns per block
+    constexpr int CPW = NC / NW, KQ = 64 / CPW, RPL = SV / KQ;
+    static_assert(CPW * NW * NSPL == SV && KQ * CPW == 64 && NSPL * NW <= GDN_PSS_STRIDE, "scan shape");
     constexpr int CH = 2 * SV + NC;                            // conv channels of a block
     constexpr int R = (CH + NT - 1) / NT;                      // channels per thread
     __shared__ float cq[SV], ck[SV], cv[NC];  // conv outputs of this token (q, k normalised in place)
@@ -161,14 +167,14 @@ __global__ __launch_bounds__(64 * NW) void k_gdn_scan(const GdnArgs a) {
         }
     }
     // state slice
-    const int vl = lane >> 2, kq = lane & 3, vloc = 16 * w + vl, v = col0 + vloc;
+    const int vl = lane / KQ, kq = lane % KQ, vloc = CPW * w + vl, v = col0 + vloc;
     float* Sh = a.S + (size_t)h * SV * SV;
     const float nw = a.ssm_norm[v];
     // per-token inputs, prefetched one token ahead
     float zin = T > 0 ? a.Z[(size_t)h * SV + v] : 0.f;
-    float s[32];
+    float s[RPL];
 #pragma unroll
-    for (int i = 0; i < 32; i++) s[i] = Sh[(size_t)(32 * kq + i) * SV + v];
+    for (int i = 0; i < RPL; i++) s[i] = Sh[(size_t)(RPL * kq + i) * SV + v];
     const float scale = 1.f / sqrtf((float)SV);
 
     float gin = 0.f, bin = 0.f;
@@ -234,19 +240,19 @@ __global__ __launch_bounds__(64 * NW) void k_gdn_scan(const GdnArgs a) {
         // (3) delta rule on this lane's 32 rows of column v
         float sk = 0.f;
 #pragma unroll
-        for (int i = 0; i < 32; i++) {
+        for (int i = 0; i < RPL; i++) {
             s[i] = s[i] * g;
-            sk = sk + s[i] * ck[32 * kq + i];
+            sk = sk + s[i] * ck[RPL * kq + i];
         }
-        sk = group_sum<4>(sk);
+        sk = group_sum<KQ>(sk);
         const float d = (cv[vloc] - sk) * b;
         float o = 0.f;
 #pragma unroll
-        for (int i = 0; i < 32; i++) {
-            s[i] = s[i] + ck[32 * kq + i] * d;
-            o = o + s[i] * cq[32 * kq + i];
+        for (int i = 0; i < RPL; i++) {
+            s[i] = s[i] + ck[RPL * kq + i] * d;
+            o = o + s[i] * cq[RPL * kq + i];
         }
-        o = group_sum<4>(o);
+        o = group_sum<KQ>(o);
         // (4) gated rms over the 128 columns
         o = o * scale;
         float o2 = kq == 0 ? o * o : 0.f;
@@ -263,12 +269,12 @@ __global__ __launch_bounds__(64 * NW) void k_gdn_scan(const GdnArgs a) {
             // o / sqrt(128) and this wave's sum of squares; k_gdn_gnorm finishes
             // (deferred: o * ssm_norm * silu(z), and the consumer applies the rms)
             if (kq == 0) a.ON[(size_t)t * n_vh * SV + (size_t)h * SV + v] = a.defer_gnorm ? o * nw * silu(z) : o;
-            if (lane == 0) a.PSS[((size_t)t * n_vh + h) * 8 + sp * NW + w] = o2;
+            if (lane == 0) a.PSS[((size_t)t * n_vh + h) * GDN_PSS_STRIDE + sp * NW + w] = o2;
         }
         lds_barrier();  // cq/ck/cv/red/ored are rewritten by the next token
     }
 #pragma unroll
-    for (int i = 0; i < 32; i++) Sh[(size_t)(32 * kq + i) * SV + v] = s[i];
+    for (int i = 0; i < RPL; i++) Sh[(size_t)(RPL * kq + i) * SV + v] = s[i];
 #pragma unroll
     for (int r = 0; r < R; r++)
         if (ch[r] >= 0 && own[r]) {
@@ -279,31 +285,50 @@ __global__ __launch_bounds__(64 * NW) void k_gdn_scan(const GdnArgs a) {
 }
 
 // The gated rms of split scans, in place: for token t and V head h,
-// ON[t][h][v] = o * rsqrt(sum of the 8 wave partials / 128 + eps) *
+// ON[t][h][v] = o * rsqrt(sum of the NP wave partials / 128 + eps) *
 // ssm_norm[v] * silu(Z[t][h][v]), the reference's order (src/m6_layer.c:
 // 320-331).  Block (t, h), 128 threads.
+template <int NP>
 __global__ __launch_bounds__(128) void k_gdn_gnorm(const GdnArgs a) {
     const int t = blockIdx.x, h = blockIdx.y, v = threadIdx.x;
-    const float* ps = a.PSS + ((size_t)t * a.n_vh + h) * 8;
+    const float* ps = a.PSS + ((size_t)t * a.n_vh + h) * GDN_PSS_STRIDE;
     float ms2 = 0.f;
 #pragma unroll
-    for (int q = 0; q < 8; q++) ms2 += ps[q];
+    for (int q = 0; q < NP; q++) ms2 += ps[q];
     const float inv2 = 1.f / sqrtf(ms2 / SV + EPS);
     const size_t i = (size_t)t * a.n_vh * SV + (size_t)h * SV + v;
     a.ON[i] = a.ON[i] * inv2 * a.ssm_norm[v] * silu(a.Z[i]);
 }
 
+// Decode steps keep NSPL * NW = 8 (8 partials: the ssm_out GEMV's GNORM
+// prologue reads 8); scans of several tokens use 8 waves per block.
 template <bool DEC>
 int launch_scan(const GdnArgs& a, int nspl, hipStream_t st) {
     if (nspl > 1 && !a.PSS) return -1;
-    switch (nspl) {
-    case 1: hipLaunchKernelGGL((k_gdn_scan<DEC, 8>), dim3(a.n_vh, 1), dim3(512), 0, st, a); return 0;
-    case 2: hipLaunchKernelGGL((k_gdn_scan<DEC, 4>), dim3(a.n_vh, 2), dim3(256), 0, st, a); break;
-    case 4: hipLaunchKernelGGL((k_gdn_scan<DEC, 2>), dim3(a.n_vh, 4), dim3(128), 0, st, a); break;
-    case 8: hipLaunchKernelGGL((k_gdn_scan<DEC, 1>), dim3(a.n_vh, 8), dim3(64), 0, st, a); break;
-    default: return -1;
+    const dim3 g(a.n_vh, nspl);
+    int np = 8;
+    if (DEC || nspl == 1) {
+        switch (nspl) {
+        case 1: hipLaunchKernelGGL((k_gdn_scan<DEC, 8, 1>), g, dim3(512), 0, st, a); return 0;
+        case 2: hipLaunchKernelGGL((k_gdn_scan<DEC, 4, 2>), g, dim3(256), 0, st, a); break;
+        case 4: hipLaunchKernelGGL((k_gdn_scan<DEC, 2, 4>), g, dim3(128), 0, st, a); break;
+        case 8: hipLaunchKernelGGL((k_gdn_scan<DEC, 1, 8>), g, dim3(64), 0, st, a); break;
+        default: return -1;
+        }
+    } else {
+        switch (nspl) {
+        case 2: hipLaunchKernelGGL((k_gdn_scan<DEC, 8, 2>), g, dim3(512), 0, st, a); np = 16; break;
+        case 4: hipLaunchKernelGGL((k_gdn_scan<DEC, 8, 4>), g, dim3(512), 0, st, a); np = 32; break;
+        case 8: hipLaunchKernelGGL((k_gdn_scan<DEC, 8, 8>), g, dim3(512), 0, st, a); np = 64; break;
+        default: return -1;
+        }
     }
-    if (!a.defer_gnorm) hipLaunchKernelGGL(k_gdn_gnorm, dim3(a.T, a.n_vh), dim3(SV), 0, st, a);
+    if (a.defer_gnorm) return np == 8 ? 0 : -1;
+    const dim3 gg(a.T, a.n_vh);
+    if (np == 8) hipLaunchKernelGGL(k_gdn_gnorm<8>, gg, dim3(SV), 0, st, a);
+    else if (np == 16) hipLaunchKernelGGL(k_gdn_gnorm<16>, gg, dim3(SV), 0, st, a);
+    else if (np == 32) hipLaunchKernelGGL(k_gdn_gnorm<32>, gg, dim3(SV), 0, st, a);
+    else hipLaunchKernelGGL(k_gdn_gnorm<64>, gg, dim3(SV), 0, st, a);
     return 0;
 }
 
@@ -312,11 +337,13 @@ int launch_scan(const GdnArgs& a, int nspl, hipStream_t st) {
 // split 4 ways (6.3 two ways, 7.4 eight ways); the split's gated rms then
 // costs 0.5 us in the ssm_out GEMV's prologue (a k_gdn_gnorm launch would
 // cost more than the split saves): the 48-layer configs[4] stack decodes at
-// 974 tok/s split 4 against 922 unsplit.  A 64-token scan takes 1.73
-// us/token unsplit, 1.45 split 2-way (two waves per block: cheaper barriers
-// in the per-token chain), 1.95 4-way and 2.27 8-way.
+// 974 tok/s split 4 against 922 unsplit.  A 64-token scan (the kernel
+// alone) takes 1.43 us/token in 2 blocks of 4 waves per head, 1.09 in 8
+// blocks of 4 waves, 1.17 / 1.00 / 0.96 in 2 / 4 / 8 blocks of 8 waves
+// (more lanes per column: shorter per-lane chains, every wave busy on its
+// SIMD) and 1.39 / 1.27 in 2 / 4 blocks of 16 waves.
 int g_split_dec = 4;
-int g_split_scan = 2;
+int g_split_scan = 8;
 
 }  // namespace
 

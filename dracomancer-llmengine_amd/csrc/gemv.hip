@@ -203,7 +203,7 @@ __global__ __launch_bounds__(64 * NW) void k_dq(const SegKArgs a) {
 
     // ---- prologue part 1: x (and norm weight) loads, then the first item's weights
     float4 xv[XP_MAXV], wv[XP_MAXV];
-    // NORM 2 (GNORM): the group partials [n_in / 128][8] = a.kc
+    // NORM 2 (GNORM): the group partials [n_in / 128][64] = a.kc (8 used)
     float4 pv0[NORM == 2 ? XP_MAXV : 1], pv1[NORM == 2 ? XP_MAXV : 1];
 #pragma unroll
     for (int q = 0; q < XP_MAXV; q++) {
@@ -212,8 +212,8 @@ __global__ __launch_bounds__(64 * NW) void k_dq(const SegKArgs a) {
             xv[q] = ld4(a.x + 4 * i4);
             if (NORM == 1 && a.norm_w) wv[q] = ld4(a.norm_w + 4 * i4);
             if constexpr (NORM == 2) {
-                pv0[q] = ld4(a.kc + ((4 * i4) >> 7) * 8);
-                pv1[q] = ld4(a.kc + ((4 * i4) >> 7) * 8 + 4);
+                pv0[q] = ld4(a.kc + ((4 * i4) >> 7) * 64);
+                pv1[q] = ld4(a.kc + ((4 * i4) >> 7) * 64 + 4);
             }
         }
     }
