@@ -3,7 +3,7 @@
 #include <hip/hip_runtime.h>
 
 // floats per (token, V head) in GdnArgs::PSS (one per wave of the head's
-// blocks); a split decode step fills 8
+// blocks); a split decode step fills 16
 constexpr int GDN_PSS_STRIDE = 64;
 
 struct GdnArgs {

@@ -300,19 +300,19 @@ __global__ __launch_bounds__(128) void k_gdn_gnorm(const GdnArgs a) {
     a.ON[i] = a.ON[i] * inv2 * a.ssm_norm[v] * silu(a.Z[i]);
 }
 
-// Decode steps keep NSPL * NW = 8 (8 partials: the ssm_out GEMV's GNORM
-// prologue reads 8); scans of several tokens use 8 waves per block.
+// A split decode step leaves NSPL * NW = 16 partials (the ssm_out GEMV's
+// GNORM prologue reads 16); scans of several tokens use 8 waves per block.
 template <bool DEC>
 int launch_scan(const GdnArgs& a, int nspl, hipStream_t st) {
     if (nspl > 1 && !a.PSS) return -1;
     const dim3 g(a.n_vh, nspl);
-    int np = 8;
+    int np = 16;
     if (DEC || nspl == 1) {
         switch (nspl) {
         case 1: hipLaunchKernelGGL((k_gdn_scan<DEC, 8, 1>), g, dim3(512), 0, st, a); return 0;
-        case 2: hipLaunchKernelGGL((k_gdn_scan<DEC, 4, 2>), g, dim3(256), 0, st, a); break;
-        case 4: hipLaunchKernelGGL((k_gdn_scan<DEC, 2, 4>), g, dim3(128), 0, st, a); break;
-        case 8: hipLaunchKernelGGL((k_gdn_scan<DEC, 1, 8>), g, dim3(64), 0, st, a); break;
+        case 2: hipLaunchKernelGGL((k_gdn_scan<DEC, 8, 2>), g, dim3(512), 0, st, a); break;
+        case 4: hipLaunchKernelGGL((k_gdn_scan<DEC, 4, 4>), g, dim3(256), 0, st, a); break;
+        case 8: hipLaunchKernelGGL((k_gdn_scan<DEC, 2, 8>), g, dim3(128), 0, st, a); break;
         default: return -1;
         }
     } else {
@@ -323,26 +323,27 @@ int launch_scan(const GdnArgs& a, int nspl, hipStream_t st) {
         default: return -1;
         }
     }
-    if (a.defer_gnorm) return np == 8 ? 0 : -1;
+    if (a.defer_gnorm) return np == 16 ? 0 : -1;
     const dim3 gg(a.T, a.n_vh);
-    if (np == 8) hipLaunchKernelGGL(k_gdn_gnorm<8>, gg, dim3(SV), 0, st, a);
-    else if (np == 16) hipLaunchKernelGGL(k_gdn_gnorm<16>, gg, dim3(SV), 0, st, a);
+    if (np == 16) hipLaunchKernelGGL(k_gdn_gnorm<16>, gg, dim3(SV), 0, st, a);
     else if (np == 32) hipLaunchKernelGGL(k_gdn_gnorm<32>, gg, dim3(SV), 0, st, a);
     else hipLaunchKernelGGL(k_gdn_gnorm<64>, gg, dim3(SV), 0, st, a);
     return 0;
 }
 
 // Measured on MI355X (configs[4] heads, 32 V heads, graph-replayed): the
-// decode step with its gates takes 8.3 us in one block per head and 6.1 us
-// split 4 ways (6.3 two ways, 7.4 eight ways); the split's gated rms then
+// decode step with its gates (kernel alone) takes 8.3 us in one block of 8
+// waves per head, split 4 ways 6.2 us in blocks of 2 waves, 5.8 in blocks of
+// 4 (7.3 of 8), split 8 ways 5.9 in blocks of 4; the split's gated rms then
 // costs 0.5 us in the ssm_out GEMV's prologue (a k_gdn_gnorm launch would
 // cost more than the split saves): the 48-layer configs[4] stack decodes at
-// 974 tok/s split 4 against 922 unsplit.  A 64-token scan (the kernel
+// 974 tok/s split 4 (2-wave blocks) against 922 unsplit, 964 split 4 in
+// 4-wave blocks and 998 split 8 in 2-wave blocks (same box, +-2%).  A 64-token scan (the kernel
 // alone) takes 1.43 us/token in 2 blocks of 4 waves per head, 1.09 in 8
 // blocks of 4 waves, 1.17 / 1.00 / 0.96 in 2 / 4 / 8 blocks of 8 waves
 // (more lanes per column: shorter per-lane chains, every wave busy on its
 // SIMD) and 1.39 / 1.27 in 2 / 4 blocks of 16 waves.
-int g_split_dec = 4;
+int g_split_dec = 8;
 int g_split_scan = 8;
 
 }  // namespace

@@ -58,7 +58,7 @@ struct SegLaunch {
     const float* norm_w;  // nullable
     // 0 none; 1 RMSNorm of x (norm_w, eps); 2 (Q4_K / Q6_K, one EPI_RESID
     // segment) the GDN gated rms of 128-wide groups: x = the scan's gated
-    // output, scaled per group by rsqrt(sum of the group's 8 partial sums of
+    // output, scaled per group by rsqrt(sum of the group's 16 partial sums of
     // squares in kc [group][64] / 128 + eps)
     int do_norm;
     float eps;

@@ -152,7 +152,7 @@ __device__ __forceinline__ auto seg_pick(const SegKArgs& a, int si, F f) -> decl
 // (segments 0, 1, 2 = rope q, rope k + KV append, V append).  NORM: the
 // launch's do_norm: 1 the RMSNorm prologue; 2 the GDN gated rms of 128-wide
 // groups (x, already gated by the scan, scaled per group by rsqrt(sum of
-// its 8 partial sums of squares / 128 + eps); see GNORM below).
+// its 16 partial sums of squares / 128 + eps); see GNORM below).
 constexpr int EPI_RT = -1, EPI_QKV = -2;
 template <int NW, int FM, bool DUAL, bool MULTI, int EPI, int NORM, bool IPT1>
 __global__ __launch_bounds__(64 * NW) void k_dq(const SegKArgs a) {
@@ -203,8 +203,9 @@ __global__ __launch_bounds__(64 * NW) void k_dq(const SegKArgs a) {
 
     // ---- prologue part 1: x (and norm weight) loads, then the first item's weights
     float4 xv[XP_MAXV], wv[XP_MAXV];
-    // NORM 2 (GNORM): the group partials [n_in / 128][64] = a.kc (8 used)
-    float4 pv0[NORM == 2 ? XP_MAXV : 1], pv1[NORM == 2 ? XP_MAXV : 1];
+    // NORM 2 (GNORM): the group partials [n_in / 128][64] = a.kc (16 used)
+    float4 pv0[NORM == 2 ? XP_MAXV : 1], pv1[NORM == 2 ? XP_MAXV : 1], pv2[NORM == 2 ? XP_MAXV : 1],
+        pv3[NORM == 2 ? XP_MAXV : 1];
 #pragma unroll
     for (int q = 0; q < XP_MAXV; q++) {
         const int i4 = tid + q * NT;
@@ -212,8 +213,11 @@ __global__ __launch_bounds__(64 * NW) void k_dq(const SegKArgs a) {
             xv[q] = ld4(a.x + 4 * i4);
             if (NORM == 1 && a.norm_w) wv[q] = ld4(a.norm_w + 4 * i4);
             if constexpr (NORM == 2) {
-                pv0[q] = ld4(a.kc + ((4 * i4) >> 7) * 64);
-                pv1[q] = ld4(a.kc + ((4 * i4) >> 7) * 64 + 4);
+                const float* pp = a.kc + ((4 * i4) >> 7) * 64;
+                pv0[q] = ld4(pp);
+                pv1[q] = ld4(pp + 4);
+                pv2[q] = ld4(pp + 8);
+                pv3[q] = ld4(pp + 12);
             }
         }
     }
@@ -269,12 +273,14 @@ __global__ __launch_bounds__(64 * NW) void k_dq(const SegKArgs a) {
         if (i4 >= n4) break;
         float4 v = xv[q];
         if constexpr (NORM == 2) {
-            // GNORM (src/m6_layer.c:320-331): the group's 8 partial sums in
+            // GNORM (src/m6_layer.c:320-331): the group's 16 partial sums in
             // order (as k_gdn_gnorm), x = (o * norm_w * silu(z)) * rsqrt(.)
-            const float4 p0 = pv0[q], p1 = pv1[q];
+            const float4 p0 = pv0[q], p1 = pv1[q], p2 = pv2[q], p3 = pv3[q];
             float ms2 = 0.f;
             ms2 += p0.x; ms2 += p0.y; ms2 += p0.z; ms2 += p0.w;
             ms2 += p1.x; ms2 += p1.y; ms2 += p1.z; ms2 += p1.w;
+            ms2 += p2.x; ms2 += p2.y; ms2 += p2.z; ms2 += p2.w;
+            ms2 += p3.x; ms2 += p3.y; ms2 += p3.z; ms2 += p3.w;
             const float inv2 = 1.f / sqrtf(ms2 / 128.f + a.eps);
             v.x *= inv2; v.y *= inv2; v.z *= inv2; v.w *= inv2;
         }

@@ -344,7 +344,7 @@ int draco_qwen_prefill(const void* layers, int n_layer, int h, const uint8_t* em
 int draco_set_qwen_chunk(int n);
 /* No reference counterpart: blocks per V head of the GDN scan (1, 2, 4 or 8;
  * negative keeps a setting) for the decode step of the layer ops and stacks
- * and for multi-token scans (defaults 4 and 8).  Split above 1, each head's
+ * and for multi-token scans (defaults 8 and 8).  Split above 1, each head's
  * 128 state columns spread over that many workgroups and the gated rms runs
  * after them: in the ssm_out GEMV's prologue for decode steps with a Q4_K /
  * Q6_K ssm_out (other formats keep one workgroup per head), as a second
