@@ -24,9 +24,10 @@ struct Q8Launch {
 
 // Quantize nvec vectors of n floats (n % 256 == 0) into Q8_K blocks.  With
 // image, out receives the same values as the GEMV's LDS image instead of
-// blocks: q8 [nvec][n] int8, bsums [n/16][nvec] int16, d [n/256][nvec]
-// float, contiguous (the same byte count as the blocks; buffers for it need
-// Q8K_IMAGE_PAD bytes more, which the GEMV's 16-byte copy may read).
+// blocks: q8 [nvec][n] int8, the group sums [n/256][nvec][16] as f16 (exact:
+// |sum| <= 2032), d [n/256][nvec] float, contiguous (the same byte count as
+// the blocks; buffers for it need Q8K_IMAGE_PAD bytes more, which the GEMV's
+// 16-byte copy may read).
 constexpr int Q8K_IMAGE_PAD = 16;
 int draco_q8k_quantize_launch(const float* x, int n, int nvec, uint8_t* out, hipStream_t st, bool image = false);
 // nvec in {1, 4, 8}; isums requires nvec == 1.

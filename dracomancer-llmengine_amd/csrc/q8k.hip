@@ -73,8 +73,9 @@ __global__ __launch_bounds__(256) void k_q8k_quantize(const float* __restrict__ 
     if (IMG) {
         const int nv = gridDim.y;
         out[(size_t)v * n + (size_t)b * 256 + t] = (uint8_t)(int8_t)q;
-        int16_t* bs = reinterpret_cast<int16_t*>(out + (size_t)nv * n);
-        if ((t & 15) == 0) bs[(size_t)(b * 16 + (t >> 4)) * nv + v] = (int16_t)s;
+        // group sums as f16 (|s| <= 16 * 127 < 2^11: exact), [block][vector][16]
+        _Float16* bs = reinterpret_cast<_Float16*>(out + (size_t)nv * n);
+        if ((t & 15) == 0) bs[((size_t)b * nv + v) * 16 + (t >> 4)] = (_Float16)s;
         float* dd = reinterpret_cast<float*>(bs + (size_t)(n / 16) * nv);
         if (t == 0) dd[(size_t)b * nv + v] = d;
         return;
@@ -88,22 +89,46 @@ __global__ __launch_bounds__(256) void k_q8k_quantize(const float* __restrict__ 
 // ----------------------------------------------------------------- GEMV --
 // FM: 1 = Q4_K, 2 = Q6_K.  NB: activation vectors (1, 4 or 8).  ISUMS: also
 // write each (row, super-block)'s integer sums (NB == 1).  IMG: xq is the
-// GEMV image (q8 [NB][n_in], bsums [ng][NB], d [nb][NB]), which is the LDS
-// layout itself, so the prologue is a flat 16-byte copy; otherwise the
-// prologue scatters the Q8_K blocks into that layout.
+// GEMV image (q8 [NB][n_in], bsums [nb][NB][16] f16, d [nb][NB]), which is
+// the LDS layout itself, so the prologue is a flat 16-byte copy; otherwise
+// the prologue scatters the Q8_K blocks into that layout.
+//
+// Per item (16 rows x one super-block) and lane (row j, lane group g) the
+// int8 MFMAs give the exact group dots C of the lane's four groups with every
+// vector; a lane adds c * C per (group, vector) into I, where c is a small
+// integer of the group's scale.  The terms that couple a weight scale with
+// an activation group sum -- the Q4_K mins, the Q4_K high nibble's bias
+// (the stored byte is 16(u - 8), so its C is 16 t - 128 bsum) and the Q6_K
+// offset (C - 32 bsum) -- are one f16 MFMA each per super-block over the 16
+// group sums of every vector (coefficients and sums are integers below 2^11,
+// every partial sum below 2^24: exact in the fp32 accumulator):
+//   Q4_K: 16 isc = I + 16 Tb, Tb = sum_{hi groups} 8 sc bsum, imn = Tm = sum m bsum
+//         y += d8 (dw (I / 16 + Tb) - dmin Tm)
+//   Q6_K: isc = I - 32 Tb, Tb = sum_g sc bsum,  y += d8 dw (I - 32 Tb)
+// which are the oracle's or_q8k_block_isums regrouped (exact integers).  The
+// f16 MFMA leaves vector 4g' + i's T in lane (j, g') element i; those are
+// added to the row sums once per tile.
+typedef _Float16 v4h __attribute__((ext_vector_type(4)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ uint32_t pk_h2(float a, float b) {
+    return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)a) |
+           ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)b) << 16);
+}
+
 template <int NW, int FM, int NB, bool ISUMS, bool IMG>
 __global__ __launch_bounds__(64 * NW) void k_dq8(const Q8Launch a) {
     extern __shared__ __align__(16) uint8_t smem[];
     constexpr int NT = 64 * NW, NH = NB >= 4 ? NB / 4 : 1;
-    const int n_in = a.n_in, nb = n_in >> 8, ng = n_in >> 4;
+    const int n_in = a.n_in, nb = n_in >> 8;
     const size_t img = (size_t)NB * nb * Q8K_BLOCK_BYTES;                   // image bytes
     int8_t* q8 = reinterpret_cast<int8_t*>(smem);                           // [NB][n_in]
-    int16_t* bsum = reinterpret_cast<int16_t*>(q8 + (size_t)NB * n_in);     // [ng][NB]
-    float* d8 = reinterpret_cast<float*>(bsum + (size_t)ng * NB);         // [nb][NB] (ng % 16 == 0: aligned)
+    uint16_t* bsf = reinterpret_cast<uint16_t*>(q8 + (size_t)NB * n_in);    // [nb][NB][16] f16
+    float* d8 = reinterpret_cast<float*>(bsf + (size_t)nb * NB * 16);      // [nb][NB]
     int8_t* zero = reinterpret_cast<int8_t*>(smem + ((img + 15) & ~(size_t)15));  // 1 KB of zeros
     float* red = reinterpret_cast<float*>(zero + 1024);                     // [NB][NW][16]
 
-    const int tid = threadIdx.x, lane = tid & 63, j = lane & 15, g = lane >> 4;
+    const int tid = threadIdx.x, lane = tid & 63, j = lane & 15, g = lane >> 4, gh = g >> 1;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int bx = blockIdx.x, G = gridDim.x;
     const int total = a.n_tiles;
@@ -121,7 +146,7 @@ __global__ __launch_bounds__(64 * NW) void k_dq8(const Q8Launch a) {
     int ct = bx, cb = w, cp = 0;
     load(ct < total ? ct : total - 1, cb < nb ? cb : nb - 1, P0);
 
-    // prologue: Q8_K blocks -> LDS (q8 bytes, bsums, d)
+    // prologue: Q8_K blocks -> LDS (q8 bytes, f16 bsums, d)
     for (int i = tid; i < 256; i += NT) reinterpret_cast<uint32_t*>(zero)[i] = 0u;
     if (IMG) {
         const int n16 = (int)((img + 15) >> 4);
@@ -139,19 +164,30 @@ __global__ __launch_bounds__(64 * NW) void k_dq8(const Q8Launch a) {
         } else if (k <= 64) {
             *reinterpret_cast<uint32_t*>(q8 + (size_t)v * n_in + b * 256 + 4 * (k - 1)) = val;
         } else {
-            const int gi = b * 16 + 2 * (k - 65);
-            bsum[(size_t)gi * NB + v] = (int16_t)(val & 0xFFFF);
-            bsum[(size_t)(gi + 1) * NB + v] = (int16_t)(val >> 16);
+            const int gi = 2 * (k - 65);  // groups gi, gi + 1 of super-block b
+            *reinterpret_cast<uint32_t*>(bsf + ((size_t)b * NB + v) * 16 + gi) =
+                pk_h2((float)(int16_t)(val & 0xFFFF), (float)(int16_t)(val >> 16));
         }
     }
     lds_barrier();
 
-    // A rows: lane (j, g) supplies vector (4h + (j&3)) for group slot g when (j>>2) == g
-    const bool arow = (j >> 2) == g && (NB > 1 || (j & 3) == 0);
-    const int av = NB > 1 ? (j & 3) : 0;
-    float yacc[NB];
+    // int8 A rows.  Q6_K: lane (j, g) supplies vector (4h + (j&3)) for group
+    // slot g when (j>>2) == g.  Q4_K: the two groups of a sub-block (one
+    // scale) share a 32-value K slot: row 8k + v is vector v over slot k
+    // (lane groups 2k, 2k + 1), so one MFMA serves 8 vectors and lane (j, g)
+    // receives vectors 4(g&1) + i of the sub-block of its own slot g >> 1.
+    const bool arow = FM == 1 ? ((j >> 3) == gh && (j & 7) < NB) : ((j >> 2) == g && (NB > 1 || (j & 3) == 0));
+    const int av = FM == 1 ? (j & 7) : (NB > 1 ? (j & 3) : 0);
+    // f16 A rows: lane (j, g) supplies vector j's group sums (vectors past NB: zeros)
+    const bool brow = j < NB;
+    // Q4_K: a lane accumulates its 4 vectors 4(g&1) + i (NV = min(NB, 4) of them)
+    constexpr int NV = FM == 1 ? (NB < 4 ? NB : 4) : NB;
+    const int vb = FM == 1 && NB > 4 ? 4 * (g & 1) : 0;  // first vector of a Q4_K lane
+    float yacc[NV], yT[4];
 #pragma unroll
-    for (int v = 0; v < NB; v++) yacc[v] = 0.f;
+    for (int v = 0; v < NV; v++) yacc[v] = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; i++) yT[i] = 0.f;
 
     auto step = [&](int i, Frag& cur, Frag& nxt) {
         int nt = ct, nbk = cb + NW, np = cp + 1;
@@ -165,21 +201,26 @@ __global__ __launch_bounds__(64 * NW) void k_dq8(const Q8Launch a) {
         const bool real = i + 1 < n_items && nbk < nb;
         load(real ? nt : ct, real ? nbk : (w < nb ? w : nb - 1), nxt);
         if (cb < nb) {
-            int isc[NB], imn[NB];
+            int I[NV];
 #pragma unroll
-            for (int v = 0; v < NB; v++) isc[v] = imn[v] = 0;
+            for (int v = 0; v < NV; v++) I[v] = 0;
+            int scs[4], mns[4];
+            // Q4_K A base of this item (fragment offsets are immediates; lanes
+            // without a row read the zero page)
+            const int8_t* ab = arow ? q8 + (size_t)av * n_in + cb * 256 + (4 * gh + (g & 1)) * 16 : zero;
             // one fragment = one group slot per lane; FM 1: 4 fragments (r, nib), FM 2: 4 (r)
 #pragma unroll
             for (int fr = 0; fr < 4; fr++) {
                 v4i B;
-                int grp, sc, mn = 0;
+                int grp, cf;
                 if (FM == 1) {
-                    const int r = fr >> 1, nib = fr & 1, gh = g >> 1;
+                    const int r = fr >> 1, nib = fr & 1;
                     const uint4 q = r ? cur.b : cur.a;
                     const uint32_t m = nib ? 0xF0F0F0F0u : 0x0F0F0F0Fu;
                     B = (v4i){(int)(q.x & m), (int)(q.y & m), (int)(q.z & m), (int)(q.w & m)};
                     grp = 8 * r + 4 * gh + 2 * nib + (g & 1);
-                    const int s0 = 2 * gh + nib;
+                    const int s0 = 2 * gh + nib;  // six-bit scale/min of sub-block 4r + s0
+                    int sc, mn;
                     if (r == 0) {
                         sc = (cur.c.y >> (8 * s0)) & 63;
                         mn = (cur.c.z >> (8 * s0)) & 63;
@@ -187,6 +228,9 @@ __global__ __launch_bounds__(64 * NW) void k_dq8(const Q8Launch a) {
                         sc = ((cur.c.w >> (8 * s0)) & 15) | (((cur.c.y >> (8 * s0 + 6)) & 3) << 4);
                         mn = ((cur.c.w >> (8 * s0 + 4)) & 15) | (((cur.c.z >> (8 * s0 + 6)) & 3) << 4);
                     }
+                    scs[fr] = sc;
+                    mns[fr] = mn;
+                    cf = nib ? sc : 16 * sc;
                 } else {
                     const int r = fr;
                     const uint32_t A4[4] = {cur.a.x, cur.a.y, cur.a.z, cur.a.w};
@@ -201,55 +245,117 @@ __global__ __launch_bounds__(64 * NW) void k_dq8(const Q8Launch a) {
                         else vv = ((B4[q] >> 4) & 0x0F0F0F0Fu) | ((H4[q] >> 2) & 0x30303030u);
                         B[q] = (int)vv;
                     }
-                    grp = 8 * (g >> 1) + 2 * r + (g & 1);
-                    sc = (int)(int8_t)(cur.sc >> (8 * r));
+                    grp = 8 * gh + 2 * r + (g & 1);
+                    cf = (int)(int8_t)(cur.sc >> (8 * r));
+                    scs[fr] = cf;
+                    mns[fr] = 0;
                 }
-                const int gg = cb * 16 + grp;  // this lane's group in the row
-                // bsums of this group for the lane's output vectors
-                int bs[NB];
+                // |C| < 2^19 and |cf| <= 1008: the full-rate 24-bit multiply is exact
+                // (a 32-bit v_mul_lo is quarter rate)
+                if (FM == 1) {
+                    const int r = fr >> 1, nib = fr & 1;
+                    const v4i C = __builtin_amdgcn_mfma_i32_16x16x64_i8(lds_v4i(ab + (8 * r + 2 * nib) * 16), B,
+                                                                       (v4i){0, 0, 0, 0}, 0, 0, 0);
 #pragma unroll
-                for (int v = 0; v < NB; v++) bs[v] = bsum[(size_t)gg * NB + v];
+                    for (int vv = 0; vv < NV; vv++) I[vv] += __mul24(cf, C[vv]);
+                } else {
+                    const int gg = cb * 16 + grp;  // this lane's group in the row
 #pragma unroll
-                for (int h = 0; h < NH; h++) {
-                    const int8_t* ap = arow ? q8 + (size_t)(4 * h + av) * n_in + gg * 16 : zero;
-                    const v4i C = __builtin_amdgcn_mfma_i32_16x16x64_i8(lds_v4i(ap), B, (v4i){0, 0, 0, 0}, 0, 0, 0);
+                    for (int h = 0; h < NH; h++) {
+                        const int8_t* ap = arow ? q8 + (size_t)(4 * h + av) * n_in + gg * 16 : zero;
+                        const v4i C = __builtin_amdgcn_mfma_i32_16x16x64_i8(lds_v4i(ap), B, (v4i){0, 0, 0, 0}, 0, 0, 0);
 #pragma unroll
-                    for (int vv = 0; vv < (NB > 1 ? 4 : 1); vv++) {
-                        const int v = NB > 1 ? 4 * h + vv : 0;
-                        int t;
-                        if (FM == 1) t = (fr & 1) ? (C[vv] + 128 * bs[v]) >> 4 : C[vv];
-                        else t = C[vv] - 32 * bs[v];
-                        isc[v] += sc * t;
-                        if (FM == 1) imn[v] += mn * bs[v];
+                        for (int vv = 0; vv < (NB > 1 ? 4 : 1); vv++)
+                            I[NB > 1 ? 4 * h + vv : 0] += __mul24(cf, C[vv]);
                     }
                 }
             }
+            // group-sum terms: lane (j, g) holds the scales of its fragments' groups
+            const uint16_t* bsb = bsf + ((size_t)cb * NB + (brow ? j : 0)) * 16;
+            v4f Tb, Tm = (v4f){0.f, 0.f, 0.f, 0.f};
+            if (FM == 1) {
+                // Tm: K slot 4g + e = group of the lane's sub-blocks (g 0: groups 0-3,
+                // 1: 8-11, 2: 4-7, 3: 12-15); slots of g's pair share their scales
+                const int gm = ((g & 1) ? 8 : 0) + 4 * gh;
+                const int mlo = (g & 1) ? mns[2] : mns[0], mhi = (g & 1) ? mns[3] : mns[1];
+                const uint2 bm = brow ? *reinterpret_cast<const uint2*>(bsb + gm) : make_uint2(0u, 0u);
+                const uint32_t cm0 = pk_h2((float)mlo, (float)mlo), cm1 = pk_h2((float)mhi, (float)mhi);
+                Tm = __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(v4h, bm),
+                                                             __builtin_bit_cast(v4h, make_uint2(cm0, cm1)), Tm, 0, 0, 0);
+                // Tb: lanes of g 0 / 2 supply the high-nibble groups {2,3,10,11} + 4gh
+                // with coefficient 8 sc; lanes of g 1 / 3 supply zeros
+                const bool bl = (g & 1) == 0 && brow;
+                const uint32_t b0 = bl ? *reinterpret_cast<const uint32_t*>(bsb + 4 * gh + 2) : 0u;
+                const uint32_t b1 = bl ? *reinterpret_cast<const uint32_t*>(bsb + 4 * gh + 10) : 0u;
+                const float c1 = (g & 1) ? 0.f : (float)(8 * scs[1]), c3 = (g & 1) ? 0.f : (float)(8 * scs[3]);
+                Tb = __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(v4h, make_uint2(b0, b1)),
+                                                             __builtin_bit_cast(v4h, make_uint2(pk_h2(c1, c1), pk_h2(c3, c3))),
+                                                             (v4f){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+            } else {
+                // Tb: K slot 4g + r = group 8gh + 2r + (g & 1), coefficient sc_r
+                const uint4 bq = brow ? *reinterpret_cast<const uint4*>(bsb + 8 * gh) : make_uint4(0u, 0u, 0u, 0u);
+                const uint32_t sel = (g & 1) ? 0x07060302u : 0x05040100u;  // odd / even halves of each dword pair
+                const uint32_t a0 = __builtin_amdgcn_perm(bq.y, bq.x, sel), a1 = __builtin_amdgcn_perm(bq.w, bq.z, sel);
+                Tb = __builtin_amdgcn_mfma_f32_16x16x16f16(
+                    __builtin_bit_cast(v4h, make_uint2(a0, a1)),
+                    __builtin_bit_cast(v4h, make_uint2(pk_h2((float)scs[0], (float)scs[1]), pk_h2((float)scs[2], (float)scs[3]))),
+                    (v4f){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+            }
             const float dw = FM == 1 ? h2f((uint16_t)(cur.c.x & 0xFFFF)) : h2f((uint16_t)cur.d);
             const float dm = FM == 1 ? h2f((uint16_t)(cur.c.x >> 16)) : 0.f;
+            const float ds = FM == 1 ? dw * 0.0625f : dw;
 #pragma unroll
-            for (int v = 0; v < NB; v++) {
-                const float dx = d8[cb * NB + v];
-                yacc[v] += (dx * dw) * (float)isc[v] - (dx * dm) * (float)imn[v];
+            for (int v = 0; v < NV; v++) yacc[v] = fmaf(d8[cb * NB + vb + v] * ds, (float)I[v], yacc[v]);
+            // T of vector 4g + i (lanes g >= NB / 4 hold zero rows)
+            if (4 * g < NB) {
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    if (4 * g + e >= NB) break;
+                    const float dx = d8[cb * NB + 4 * g + e];
+                    const float t = FM == 1 ? dw * Tb[e] - dm * Tm[e] : -32.f * dw * Tb[e];
+                    yT[e] = fmaf(dx, t, yT[e]);
+                }
             }
             if (ISUMS) {
-                int s = isc[0], m = imn[0];
-                s = rows_sum_i(s);
-                m = rows_sum_i(m);
+                // NB == 1: vector 0's T sits in the lanes of g 0
+                int s = rows_sum_i(I[0]);
                 const int row = (ct + a.tile0) * 16 + j;
                 if (g == 0 && row >= a.row0 && row < a.row1) {
-                    a.isc[(size_t)row * nb + cb] = s;
-                    a.imn[(size_t)row * nb + cb] = m;
+                    const int tb = (int)Tb[0], tm = (int)Tm[0];
+                    a.isc[(size_t)row * nb + cb] = FM == 1 ? (s + 16 * tb) / 16 : s - 32 * tb;
+                    a.imn[(size_t)row * nb + cb] = FM == 1 ? tm : 0;
                 }
             }
         }
         if (cp == ipt - 1) {  // tile done
+            if constexpr (FM == 1) {
+                // lane (j, g) holds vectors 4(g&1) + i (its T terms too when g < 2);
+                // lanes g and g ^ 2 hold the same vectors: one permlane32 swap per
+                // pair of them leaves the lower lanes vectors vb + k, the upper
+                // lanes vb + 2 + k, each summed over both lanes
+                float h[4];
 #pragma unroll
-            for (int v = 0; v < NB; v++) {
-                float s = yacc[v];
-                s = rows_sum(s);
-                if (lane < 16) red[(v * NW + w) * 16 + j] = s;
-                yacc[v] = 0.f;
+                for (int i = 0; i < 4; i++) h[i] = (i < NV ? yacc[i < NV ? i : 0] : 0.f) + (g < 2 ? yT[i] : 0.f);
+#pragma unroll
+                for (int k = 0; k < 2; k++) {
+                    const int b0 = __builtin_bit_cast(int, h[k]), b1 = __builtin_bit_cast(int, h[2 + k]);
+                    const auto p = __builtin_amdgcn_permlane32_swap(b0, b1, false, false);
+                    const float t = __builtin_bit_cast(float, (int)p[0]) + __builtin_bit_cast(float, (int)p[1]);
+                    const int v = 4 * (g & 1) + (g >= 2 ? 2 : 0) + k;  // lanes of odd g hold vectors 4-7
+                    if (v < NB) red[(v * NW + w) * 16 + j] = t;
+                }
+            } else {
+#pragma unroll
+                for (int v = 0; v < NB; v++) {
+                    float s = (g == (v >> 2) ? yT[v & 3] : 0.f) + yacc[v];
+                    s = rows_sum(s);
+                    if (lane < 16) red[(v * NW + w) * 16 + j] = s;
+                }
             }
+#pragma unroll
+            for (int v = 0; v < NV; v++) yacc[v] = 0.f;
+#pragma unroll
+            for (int e = 0; e < 4; e++) yT[e] = 0.f;
             lds_barrier();
             for (int o = tid; o < 16 * NB; o += NT) {
                 const int v = o >> 4, jj = o & 15;

@@ -183,6 +183,51 @@ def test_attn_op_configs3_vs_reference_golden():
     assert np.array_equal(drv.kc[0][:gg.ATTN_CFG3_T0 * kd], krows.reshape(-1))
 
 
+@pytest.mark.parametrize("hd,nh,nkv,max_t,ocode", [
+    (64, 32, 8, 1024, models.Q4_K),   # Llama-1B's attention: 32 splits
+    (64, 32, 8, 2048, models.Q4_K),   # 64 splits (the cap) of 32 rows
+    (128, 6, 2, 512, models.Q6_K),    # head dim 128, GQA 3, Q6_K projections
+    (64, 8, 8, 960, models.Q6_K),     # GQA 1, 30 splits
+])
+def test_attn_op_long_cache_match_oracle(oracle, hd, nh, nkv, max_t, ocode):
+    """The per-head attention kernel and the split merge over long caches
+    (up to the 64-split cap): from a cache filled to 24 rows short of max_t,
+    24 tokens through m6_llama_attn_op to a full cache, against the oracle
+    after every token."""
+    import dataclasses
+    from tests_oracle_engine import oracle_engine
+    from dracohip import lib
+    codes = dict(models.LLAMA1B.codes, o=ocode, q=ocode, k=ocode, v=ocode)
+    cfg = dataclasses.replace(models.LLAMA1B, name=f"longcache-{hd}-{nh}-{nkv}-{max_t}", head_dim=hd, n_head=nh,
+                              n_kv=nkv, hidden=max(256, nh * hd), n_layer=1, n_ff=256, vocab=256, max_t=max_t,
+                              codes=codes)
+    model = models.build_llama(cfg, 2)
+    lib.load().draco_reset()
+    drv = LlamaDriver(model, hip_engine_lib())
+    ref = LlamaDriver(model, oracle_engine(oracle))
+    rng = np.random.default_rng(11)
+    kd = nkv * hd
+    t0 = max_t - 24
+    rows = rng.standard_normal((2, t0 * kd), dtype=np.float32)
+    for d in (drv, ref):
+        d.kc[0][:rows.shape[1]] = rows[0]
+        d.vc[0][:rows.shape[1]] = rows[1]
+        d.tl[0][0] = t0
+    L = drv.engine.cdll
+    worst = 0.0
+    for step in range(24):
+        xn = rng.standard_normal(cfg.hidden, dtype=np.float32)
+        out = np.zeros(cfg.hidden, np.float32)
+        outr = np.zeros(cfg.hidden, np.float32)
+        print(f"[attn_op] long cache hd {hd} nh {nh} nkv {nkv} max_t {max_t} step {step}", flush=True)
+        L.m6_llama_attn_op(pf(xn), drv.descs[0].attn_p, t0 + step, pf(out))
+        oracle.lib.or_llama_attn_op(pf(xn), ref.descs[0].attn_p, t0 + step, pf(outr))
+        e = rel_err(out, outr)
+        worst = max(worst, e)
+        assert e <= 1e-5, (step, e)
+    print(f"[attn_op] long cache hd {hd} nh {nh} nkv {nkv} max_t {max_t}: worst {worst:.2e}")
+
+
 @pytest.mark.parametrize("nh,nkv", [(4, 2), (8, 2), (32, 4)])
 def test_attn_op_grouped_head_dim_128_match_oracle(oracle, nh, nkv):
     """The group-shared attention kernel at head dim 128 for every GQA ratio
