@@ -571,7 +571,8 @@ __global__ __launch_bounds__(64) void k_argmax_final(const float* __restrict__ p
     int idx = 0x7fffffff;
     for (int i = threadIdx.x; i < nb; i += 64) am_merge(v, idx, pv[i], pi[i]);
     group_argmax<64>(v, idx);
-    if (threadIdx.x == 0) out[slotp ? slotp[0] + 1 : slot] = idx;
+    // every value NaN: token 0 (a first-index '>' scan), never an out-of-range row
+    if (threadIdx.x == 0) out[slotp ? slotp[0] + 1 : slot] = idx == 0x7fffffff ? 0 : idx;
 }
 
 // ------------------------------------------------------ token advance --
