@@ -87,8 +87,12 @@ struct Work {
     float *x = nullptr, *xn = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *att = nullptr,
           *part = nullptr, *g = nullptr, *u = nullptr;
     float* xe = nullptr;      // next token's embedding, written by the head's argmax (generation)
+    // a pending residual after a split-K down projection: the layer output is
+    // x + pd[0..H) + pd[H..2H), materialised into xs by the next q/k/v launch
+    float *pd = nullptr, *xs = nullptr;
     unsigned* cnt = nullptr;  // attention merge counters (one per kv head), zero at rest
-    size_t cap_h = 0, cap_xn = 0, cap_xe = 0, cap_q = 0, cap_k = 0, cap_part = 0, cap_ff = 0;
+    size_t cap_h = 0, cap_xn = 0, cap_xe = 0, cap_q = 0, cap_k = 0, cap_part = 0, cap_ff = 0, cap_pd = 0,
+           cap_xs = 0;
 };
 
 // Chunked-prefill buffers, token-major, for up to `cap` tokens per chunk.
@@ -258,6 +262,8 @@ int ensure_work(Work& w, int H, int QD, int KD, int NH, int HD, int max_t, int F
     if (grow(&w.x, &w.cap_h, H + 64)) return -2;
     if (grow(&w.xn, &w.cap_xn, H + 64)) return -2;
     if (grow(&w.xe, &w.cap_xe, H + 64)) return -2;
+    if (grow(&w.pd, &w.cap_pd, 2 * (size_t)H + 64)) return -2;
+    if (grow(&w.xs, &w.cap_xs, H + 64)) return -2;
     if (w.cap_q < (size_t)QD) {
         size_t c = w.cap_q;
         if (grow(&w.q, &c, QD)) return -2;
@@ -405,7 +411,7 @@ SegDesc seg_of(const DracoMat* m, int epi, float* y, const float* yadd) {
 // prologue when norm != 0), with rope on q/k and the KV append at row T as
 // epilogues (src/m6_engine.c:447-481).
 int enqueue_qkv(DevAttn* a, Work& w, const float* x, int norm, const float* norm_w, float eps,
-                const int* state, int layer, hipStream_t st) {
+                const int* state, int layer, hipStream_t st, bool pending = false) {
     const SegDesc all[3] = {seg_of(a->wq, EPI_ROPE_Q, w.q, nullptr), seg_of(a->wk, EPI_ROPE_K, nullptr, nullptr),
                             seg_of(a->wv, EPI_V_APPEND, nullptr, nullptr)};
     bool done[3] = {false, false, false};
@@ -417,6 +423,11 @@ int enqueue_qkv(DevAttn* a, Work& w, const float* x, int norm, const float* norm
         s.do_norm = norm;
         s.norm_w = norm_w;
         s.eps = eps;
+        if (pending) {  // x + the split-K partials, normalised; the sum kept in w.xs
+            s.do_norm = 3;
+            s.am_val = w.pd;
+            s.xn_out = w.xs;
+        }
         // every not-yet-issued segment of the same kernel family (Q4_K/Q6_K share one)
         auto fam = [](int c) { return c == DRACO_Q8_0 ? 0 : 1; };
         for (int j = i; j < 3; j++)
@@ -478,24 +489,60 @@ int enqueue_shexp_tail(const DracoMat& gi, const DracoMat& down, Work& w, int h,
     return 0;
 }
 
+// Whether layer l's dense down projection runs split-K, leaving its residual
+// add to the next layer's q/k/v launch: a short wide matrix (half the CUs or
+// fewer with one tile each, 16 or 32 super-blocks per row) followed by a
+// layer whose q/k/v are all K-quants (the launch that takes the pending sum).
+// A 2048x8192 Q6_K GEMV takes 5.73 us, the same bytes as 4096x4096 4.59 us.
+bool ksplit_down(const DevModel* m, int l) {
+    if (l + 1 >= m->n_layer || !m->ffn[l] || m->moe[l]) return false;
+    const DracoMat& d = *m->ffn[l]->d;
+    const int nb = d.L.n_in / 256;
+    if ((d.L.code != DRACO_Q4_K && d.L.code != DRACO_Q6_K) || d.L.n_in % 256 || (nb != 16 && nb != 32) ||
+        (d.L.n_out + 15) / 16 > 128)
+        return false;
+    const DevAttn* n = m->attn[l + 1];
+    auto kq = [](const DracoMat* x) { return x->L.code == DRACO_Q4_K || x->L.code == DRACO_Q6_K; };
+    return kq(n->wq) && kq(n->wk) && kq(n->wv);
+}
+
 // enqueue one llama layer on the device (x in w.x, updated in place; with
 // xin set the layer reads its input from xin and leaves its output in w.x):
-// five launches -- qkv(+norm,+rope,+append), attention(+merge), wo(+residual),
-// gate/up(+norm,+SwiGLU), down(+residual)
+// qkv(+norm,+rope,+append), attention, merge, wo(+residual),
+// gate/up(+norm,+SwiGLU), down(+residual).  After a split-K down the output
+// is pending (w.x + the partials in w.pd) and the next layer's qkv launch
+// forms it (into w.xs), which wo then takes as its residual.
 int enqueue_layer(DevModel* m, int l, float eps, hipStream_t st, const float* xin = nullptr) {
     DevAttn* a = m->attn[l];
     DevFfn* f = m->ffn[l];
     Work& w = m->w;
     const int H = m->h;
     const float* x0 = xin ? xin : w.x;
-    if (int rc = enqueue_qkv(a, w, x0, 1, m->anorm[l], eps, m->state, l, st)) return rc;
+    const bool pending = !xin && l > 0 && ksplit_down(m, l - 1);
+    if (int rc = enqueue_qkv(a, w, x0, 1, m->anorm[l], eps, m->state, l, st, pending)) return rc;
     if (dk_attention(w.q, a->kc, a->vc, w.part, w.cnt, w.att, m->state, l, a->NH, a->NKV, a->HD, a->max_t,
                      a->scale, st))
         return fail(-1, "attention launch");
-    if (draco_gemv_launch(*a->wo, w.att, w.x, x0, 0, H, st)) return fail(-1, "gemv o");
+    if (draco_gemv_launch(*a->wo, w.att, w.x, pending ? w.xs : x0, 0, H, st)) return fail(-1, "gemv o");
     if (m->moe[l])  // RMSNorm, router, routed gate/up + SwiGLU, down + weighted combine + residual
         return draco_moe_layer_enqueue(m->moe[l], w.x, m->fnorm[l], eps, w.x, w.x, st);
     if (int rc = enqueue_gateup(f, w, w.x, 1, m->fnorm[l], eps, st)) return rc;
+    if (ksplit_down(m, l)) {
+        SegLaunch s = {};
+        s.nseg = 1;
+        s.n_in = f->d->L.n_in;
+        s.x = w.g;
+        s.ksplit = 2;
+        SegDesc& d = s.seg[0];
+        d.base = f->d->dev;
+        d.L = f->d->L;
+        d.row0 = 0;
+        d.row1 = H;
+        d.y = w.pd;
+        d.epi = EPI_STORE;
+        if (draco_seg_launch(s, st)) return fail(-1, "gemv down (split-K)");
+        return 0;
+    }
     if (draco_gemv_launch(*f->d, w.g, w.x, w.x, 0, H, st)) return fail(-1, "gemv down");
     return 0;
 }

@@ -152,9 +152,13 @@ __device__ __forceinline__ auto seg_pick(const SegKArgs& a, int si, F f) -> decl
 // (segments 0, 1, 2 = rope q, rope k + KV append, V append).  NORM: the
 // launch's do_norm: 1 the RMSNorm prologue; 2 the GDN gated rms of 128-wide
 // groups (x, already gated by the scan, scaled per group by rsqrt(sum of
-// its 16 partial sums of squares / 128 + eps); see GNORM below).
+// its 16 partial sums of squares / 128 + eps); see GNORM below); 3 the
+// RMSNorm of a pending residual x + p0 + p1 (PRES below).
+// KS: split-K launch (one EPI_STORE segment, no prologue norm): tiles
+// [0, a.rot) multiply the first half of every row's super-blocks and store
+// to y, tiles [a.rot, 2 a.rot) the second half and store to y + a.kv_dim.
 constexpr int EPI_RT = -1, EPI_QKV = -2;
-template <int NW, int FM, bool DUAL, bool MULTI, int EPI, int NORM, bool IPT1>
+template <int NW, int FM, bool DUAL, bool MULTI, int EPI, int NORM, bool IPT1, bool KS = false>
 __global__ __launch_bounds__(64 * NW) void k_dq(const SegKArgs a) {
     extern __shared__ __align__(16) uint8_t smem[];
     constexpr int NT = 64 * NW;
@@ -168,7 +172,10 @@ __global__ __launch_bounds__(64 * NW) void k_dq(const SegKArgs a) {
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int bx = blockIdx.x, G = gridDim.x;
     const int total = a.total_tiles;
-    const int ipt = IPT1 ? 1 : (nb + NW - 1) / NW;  // IPT1: the launch has one item per wave and tile
+    const int ipt = IPT1 ? 1 : (KS ? (nb >> 1) / NW : (nb + NW - 1) / NW);  // IPT1: one item per wave and tile
+    // KS: the half of tile T (0 or 1) and its first super-block
+    auto khalf = [&](int T) { return KS && T >= a.rot ? 1 : 0; };
+    auto kfirst = [&](int T) { return KS ? khalf(T) * (nb >> 1) : 0; };
     const int my_tiles = bx < total ? (total - bx + G - 1) / G : 0;
     const int n_items = my_tiles * ipt;
 
@@ -180,6 +187,7 @@ __global__ __launch_bounds__(64 * NW) void k_dq(const SegKArgs a) {
         bool q4;
     };
     auto tile_ref = [&](int T) {
+        if (KS) T -= khalf(T) * a.rot;
         const int si = MULTI ? seg_of_tile(a, T) : 0;
         const bool q4 = FM == 3 ? seg_pick(a, si, [](const SegK& d) { return d.code; }) == DRACO_Q4_K : FM == 1;
         const size_t ib = q4 ? DRACO_Q4T_ITEM : DRACO_Q6T_ITEM;
@@ -204,14 +212,20 @@ __global__ __launch_bounds__(64 * NW) void k_dq(const SegKArgs a) {
     // ---- prologue part 1: x (and norm weight) loads, then the first item's weights
     float4 xv[XP_MAXV], wv[XP_MAXV];
     // NORM 2 (GNORM): the group partials [n_in / 128][64] = a.kc (16 used)
-    float4 pv0[NORM == 2 ? XP_MAXV : 1], pv1[NORM == 2 ? XP_MAXV : 1], pv2[NORM == 2 ? XP_MAXV : 1],
+    // NORM 3 (PRES): the pending residual's two split-K partials at a.am_val
+    // ([2][n_in]); x = (x + p0) + p1, written to a.xn_out by block 0
+    float4 pv0[NORM >= 2 ? XP_MAXV : 1], pv1[NORM >= 2 ? XP_MAXV : 1], pv2[NORM == 2 ? XP_MAXV : 1],
         pv3[NORM == 2 ? XP_MAXV : 1];
 #pragma unroll
     for (int q = 0; q < XP_MAXV; q++) {
         const int i4 = tid + q * NT;
         if (i4 < n4) {
             xv[q] = ld4(a.x + 4 * i4);
-            if (NORM == 1 && a.norm_w) wv[q] = ld4(a.norm_w + 4 * i4);
+            if ((NORM == 1 || NORM == 3) && a.norm_w) wv[q] = ld4(a.norm_w + 4 * i4);
+            if constexpr (NORM == 3) {
+                pv0[q] = ld4(a.am_val + 4 * i4);
+                pv1[q] = ld4(a.am_val + n_in + 4 * i4);
+            }
             if constexpr (NORM == 2) {
                 const float* pp = a.kc + ((4 * i4) >> 7) * 64;
                 pv0[q] = ld4(pp);
@@ -227,7 +241,7 @@ __global__ __launch_bounds__(64 * NW) void k_dq(const SegKArgs a) {
     // re-reads the last real item it loaded (already fetched or in flight,
     // so no HBM traffic) -- a skipped load would leave the wait-count
     // analysis no choice but vmcnt(0) before every use.
-    int lt = bx < total ? bx : total - 1, lb = w, lp = 0, li = 0;
+    int lt = bx < total ? bx : total - 1, lb = w + kfirst(lt), lp = 0, li = 0;
     TileRef lref = tile_ref(lt);
     const size_t lib = lref.q4 ? DRACO_Q4T_ITEM : DRACO_Q6T_ITEM;
     const uint8_t* lastp = lref.p + (size_t)(w < nb ? w : nb - 1) * lib;
@@ -246,15 +260,15 @@ __global__ __launch_bounds__(64 * NW) void k_dq(const SegKArgs a) {
         lb += NW;
         if (lp == ipt) {
             lp = 0;
-            lb = w;
             lt += G;
+            lb = w + kfirst(lt);
             if (li < n_items) lref = tile_ref(lt);
         }
     };
     load_next(P0, Q0);
     // the zero page: written by the block before its barrier, or without the
     // barrier (no RMSNorm) by every wave for itself (identical values)
-    if (NORM == 1)
+    if (NORM == 1 || NORM == 3)
         for (int i = tid; i < 256; i += NT) reinterpret_cast<uint32_t*>(zero)[i] = 0u;
     else
         for (int i = lane; i < 256; i += 64) reinterpret_cast<uint32_t*>(zero)[i] = 0u;
@@ -272,6 +286,12 @@ __global__ __launch_bounds__(64 * NW) void k_dq(const SegKArgs a) {
         const int i4 = tid + q * NT;
         if (i4 >= n4) break;
         float4 v = xv[q];
+        if constexpr (NORM == 3) {
+            const float4 p = pv0[q], p2 = pv1[q];
+            v.x = (v.x + p.x) + p2.x; v.y = (v.y + p.y) + p2.y; v.z = (v.z + p.z) + p2.z; v.w = (v.w + p.w) + p2.w;
+            xv[q] = v;
+            if (a.xn_out && bx == 0) *reinterpret_cast<float4*>(a.xn_out + 4 * i4) = v;
+        }
         if constexpr (NORM == 2) {
             // GNORM (src/m6_layer.c:320-331): the group's 16 partial sums in
             // order (as k_gdn_gnorm), x = (o * norm_w * silu(z)) * rsqrt(.)
@@ -284,7 +304,7 @@ __global__ __launch_bounds__(64 * NW) void k_dq(const SegKArgs a) {
             const float inv2 = 1.f / sqrtf(ms2 / 128.f + a.eps);
             v.x *= inv2; v.y *= inv2; v.z *= inv2; v.w *= inv2;
         }
-        if (NORM == 1) {
+        if (NORM == 1 || NORM == 3) {
             ss = fmaf(v.x, v.x, ss);
             ss = fmaf(v.y, v.y, ss);
             ss = fmaf(v.z, v.z, ss);
@@ -296,7 +316,7 @@ __global__ __launch_bounds__(64 * NW) void k_dq(const SegKArgs a) {
         }
         digits4(v, i4, xd, xsm);
     }
-    if (NORM == 1) {
+    if (NORM == 1 || NORM == 3) {
         ss = wave_sum(ss);
         if (lane == 0) ssp[w] = ss;
         lds_barrier();
@@ -312,12 +332,12 @@ __global__ __launch_bounds__(64 * NW) void k_dq(const SegKArgs a) {
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
     }
     float inv = 1.f;
-    if (NORM == 1) {
+    if (NORM == 1 || NORM == 3) {
         float tot = 0.f;
 #pragma unroll
         for (int i = 0; i < NW; i++) tot += ssp[i];
         inv = 1.f / sqrtf(tot / (float)n_in + a.eps);
-        if (a.xn_out && bx == 0) {
+        if (NORM == 1 && a.xn_out && bx == 0) {
 #pragma unroll
             for (int q = 0; q < XP_MAXV; q++) {
                 const int i4 = tid + q * NT;
@@ -343,7 +363,7 @@ __global__ __launch_bounds__(64 * NW) void k_dq(const SegKArgs a) {
     const int pos = a.state ? a.state[0] : 0;
     const int kv_row = a.state ? a.state[1 + a.layer] : 0;
     // compute cursor and the current tile's epilogue context (set at tile start)
-    int ct = bx, cb = w, cp = 0;
+    int ct = bx, cb = w + kfirst(bx), cp = 0;
     int c_epi = EPI_STORE, c_row = 0, c_r0 = 0, c_r1 = 0;
     float* c_y = nullptr;
     bool cq4 = FM != 2;
@@ -354,11 +374,11 @@ __global__ __launch_bounds__(64 * NW) void k_dq(const SegKArgs a) {
             const int si = MULTI ? seg_of_tile(a, ct) : 0;
             if constexpr (EPI == EPI_QKV) c_epi = si == 0 ? EPI_ROPE_Q : (si == 1 ? EPI_ROPE_K : EPI_V_APPEND);
             else c_epi = EPI != EPI_RT ? EPI : seg_pick(a, si, [](const SegK& d) { return d.epi; });
-            c_row = (ct - seg_pick(a, si, [](const SegK& d) { return d.first; }) +
+            c_row = (ct - khalf(ct) * a.rot - seg_pick(a, si, [](const SegK& d) { return d.first; }) +
                      seg_pick(a, si, [](const SegK& d) { return d.tile0; })) * 16;
             c_r0 = seg_pick(a, si, [](const SegK& d) { return d.row0; });
             c_r1 = seg_pick(a, si, [](const SegK& d) { return d.row1; });
-            c_y = seg_pick(a, si, [](const SegK& d) { return d.y; });
+            c_y = seg_pick(a, si, [](const SegK& d) { return d.y; }) + (KS ? (size_t)khalf(ct) * a.kv_dim : 0);
             if (FM == 3) cq4 = seg_pick(a, si, [](const SegK& d) { return d.code; }) == DRACO_Q4_K;
             if (tid < 16) {
                 const int n_out = seg_pick(a, si, [](const SegK& d) { return d.n_out; });
@@ -418,7 +438,7 @@ __global__ __launch_bounds__(64 * NW) void k_dq(const SegKArgs a) {
                     v += red[q * 16 + tid];
                     if (DUAL) v2 += red[(NW + q) * 16 + tid];
                 }
-                if (NORM == 1) {
+                if (NORM == 1 || NORM == 3) {
                     v *= inv;
                     v2 *= inv;
                 }
@@ -471,8 +491,8 @@ __global__ __launch_bounds__(64 * NW) void k_dq(const SegKArgs a) {
         cb += NW;
         if (cp == ipt) {
             cp = 0;
-            cb = w;
             ct += G;
+            cb = w + kfirst(ct);
         }
     };
     for (int i = 0; i < n_items; i += 2) {
@@ -753,15 +773,15 @@ int cu_count() {
 
 size_t dq_lds_bytes(int n_in, int nw) { return (size_t)(n_in / 16) * 72 + 1024 + (size_t)2 * nw * 16 * 4 + (size_t)nw * 4; }
 
-template <int NW, int FM, bool DUAL, bool MULTI, int EPI, int NORM, bool IPT1>
+template <int NW, int FM, bool DUAL, bool MULTI, int EPI, int NORM, bool IPT1, bool KS = false>
 void launch_dq1(SegLaunch& a, int grid, hipStream_t st) {
     static std::once_flag once;
     std::call_once(once, [] {
         // allow LDS beyond 64 KB for long rows (n_in up to 16384 needs ~74 KB)
-        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&k_dq<NW, FM, DUAL, MULTI, EPI, NORM, IPT1>),
+        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&k_dq<NW, FM, DUAL, MULTI, EPI, NORM, IPT1, KS>),
                                   hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
     });
-    hipLaunchKernelGGL((k_dq<NW, FM, DUAL, MULTI, EPI, NORM, IPT1>), dim3(grid), dim3(64 * NW),
+    hipLaunchKernelGGL((k_dq<NW, FM, DUAL, MULTI, EPI, NORM, IPT1, KS>), dim3(grid), dim3(64 * NW),
                        dq_lds_bytes(a.n_in, NW), st, seg_kargs(a, false));
 }
 
@@ -790,6 +810,8 @@ template <int NW, int FM, bool DUAL>
 void launch_dq_m(SegLaunch& a, bool multi, int grid, hipStream_t st) {
     if (a.do_norm == 2) {  // GNORM: one residual segment (checked by seg_launch_dq)
         if constexpr (!DUAL) launch_dq<NW, FM, false, false, EPI_RESID, 2>(a, grid, st);
+    } else if (a.do_norm == 3) {  // PRES: per-tile epilogues (checked by seg_launch_dq)
+        if constexpr (!DUAL) launch_dq<NW, FM, false, true, EPI_RT, 3>(a, grid, st);
     } else if (a.do_norm) {
         launch_dq_e<NW, FM, DUAL, 1>(a, multi, grid, st);
     } else {
@@ -810,7 +832,9 @@ void launch_dq_nw(SegLaunch& a, int fm, bool dual, int grid, hipStream_t st) {
     } else {
         const bool qkv = a.nseg == 3 && a.seg[0].epi == EPI_ROPE_Q && a.seg[1].epi == EPI_ROPE_K &&
                          a.seg[2].epi == EPI_V_APPEND;
-        if (qkv && a.do_norm) launch_dq<NW, 3, false, true, EPI_QKV, 1>(a, grid, st);
+        if (qkv && a.do_norm == 3) launch_dq<NW, 3, false, true, EPI_QKV, 3>(a, grid, st);
+        else if (a.do_norm == 3) launch_dq<NW, 3, false, true, EPI_RT, 3>(a, grid, st);
+        else if (qkv && a.do_norm) launch_dq<NW, 3, false, true, EPI_QKV, 1>(a, grid, st);
         else if (a.do_norm) launch_dq<NW, 3, false, true, EPI_RT, 1>(a, grid, st);
         else launch_dq<NW, 3, false, true, EPI_RT, 0>(a, grid, st);
     }
@@ -852,6 +876,16 @@ int seg_launch_dq(SegLaunch& a, hipStream_t st) {
     if (dual && (a.nseg != 2 || fm == 3)) return -1;
     // GNORM prologue: one residual segment over whole 128-wide groups
     if (a.do_norm == 2 && (a.nseg != 1 || a.seg[0].epi != EPI_RESID || n_in % 128 || !a.kc)) return -1;
+    // PRES prologue: the partials of the pending residual; no SwiGLU pair
+    if (a.do_norm == 3 && (dual || !a.am_val)) return -1;
+    // split-K: one whole-matrix store segment, no prologue norm, halves of
+    // NW-divisible super-block counts on the 8-wave kernel
+    if (a.ksplit) {
+        const SegDesc& s0 = a.seg[0];
+        if (a.ksplit != 2 || a.nseg != 1 || dual || a.do_norm || s0.epi != EPI_STORE || s0.row0 != 0 ||
+            s0.row1 != s0.L.n_out || nb < 16 || nb > 32 || (nb / 2) % 8)
+            return -1;
+    }
     for (int i = a.nseg; i < SEG_MAX; i++) {  // unused slots: never selected by seg_of_tile
         a.seg[i] = a.seg[a.nseg - 1];
         a.seg[i].first_tile = 1 << 30;
@@ -876,6 +910,16 @@ int seg_launch_dq(SegLaunch& a, hipStream_t st) {
     // with fewer tiles than that keep one per block (halving the qkv or wo
     // grid was slower: 2108 -> 1917 / 1821 tok/s).
     if (nb <= nw && tiles >= 2 * cu_count() && tiles <= cap) grid = (tiles + 1) / 2;
+    if (a.ksplit) {
+        // tiles [0, tiles) take each row's first half, [tiles, 2 tiles) the second
+        a.rot = tiles;
+        a.kv_dim = a.seg[0].L.n_out;
+        a.total_tiles = 2 * tiles;
+        grid = 2 * tiles < cap ? 2 * tiles : cap;
+        if (fm == 1) launch_dq1<8, 1, false, false, EPI_STORE, 0, false, true>(a, grid, st);
+        else launch_dq1<8, 2, false, false, EPI_STORE, 0, false, true>(a, grid, st);
+        return 0;
+    }
     if (grid <= 0) return 0;
     if (nw == 4) launch_dq_nw<4>(a, fm, dual, grid, st);
     else if (nw == 8) launch_dq_nw<8>(a, fm, dual, grid, st);
