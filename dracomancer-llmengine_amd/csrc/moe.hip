@@ -581,7 +581,9 @@ int draco_moe_grp_launch(MoeArgs& a, int fm, bool dual, bool xper, bool route, h
                        MOE_EXP_MAX * 4;
     if (lds > 160 * 1024) return -1;
     const int total = a.n_slots * (a.n_out_e / 16);
-    const int cap = cu_count() * (nw == 4 ? 4 : (nw == 8 ? 2 : 1));
+    // ROUTE: every block repeats the routing (softmax + rank of the experts),
+    // so at most one block per CU (configs[3] FFN, 384 tiles: 16.3 -> 15.7 us)
+    const int cap = route ? cu_count() : cu_count() * (nw == 4 ? 4 : (nw == 8 ? 2 : 1));
     const int grid = total < cap ? total : cap;
     if (nw == 4) return dispatch_grp<4>(a, fm, dual, xper, route, grid, lds, st);
     if (nw == 8) return dispatch_grp<8>(a, fm, dual, xper, route, grid, lds, st);
