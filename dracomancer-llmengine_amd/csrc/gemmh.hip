@@ -28,8 +28,8 @@
 // Blocking.  Block = 4 waves on 32 tokens x 4*RW row tiles of 32 rows; the
 // activation operands of one super-block (34944 B: 16 K-steps x hi/lo x 1 KB,
 // the min-term operands, the 32 token scales) are staged in LDS, double
-// buffered, and read by all four waves; each wave runs RW row tiles against
-// each A read.  Weights stream from global memory (non-temporal loads).
+// buffered, and read by all four waves; each wave reads a K-step's A once and
+// runs it against its RW row tiles (independent accumulator chains).  Weights stream from global memory (non-temporal loads).
 // Tall-K products split K across blockIdx.z and a reduce kernel sums the
 // partials in a fixed order.
 #include <hip/hip_runtime.h>
@@ -173,96 +173,127 @@ __device__ __forceinline__ void wload(const uint8_t* item, int j, int u, WFrag<2
     f.d = *reinterpret_cast<const uint16_t*>(item + 3328 + 2 * j);
 }
 
-// One (32-row tile, super-block) against the staged activations `cur`:
-// returns the tile's contribution before the token scale, per C element.
-__device__ __forceinline__ void tile_q4(const WFrag<1>& f, const uint8_t* cur, int lane, int u, float (&part)[16]) {
-    v16f P = {}, Q = {};
-    const float dd = h2f((uint16_t)(f.h.x & 0xFFFF)), dm = h2f((uint16_t)(f.h.x >> 16));
-    // 6-bit scales and mins of the 8 sub-blocks (src/m5_kern_scalar.c:39-46)
-    int sc[8], mn[8];
+// RW (32-row tile, super-block) items against the staged activations `cur`:
+// each K-step reads its A operands (hi, lo) from LDS once and runs them
+// against every tile's B, so the LDS traffic per MFMA falls with RW and the
+// RW accumulator chains are independent.  Returns each tile's contribution
+// before the token scale, per C element.
+template <int RW>
+__device__ __forceinline__ void tiles_q4(const WFrag<1> (&f)[RW], const uint8_t* cur, int lane, int u,
+                                         float (&part)[RW][16]) {
+    v16f P[RW], Q[RW];
+    int sc[RW][8];
+    v8h Bm[RW];
 #pragma unroll
-    for (int s8 = 0; s8 < 8; s8++) {
-        if (s8 < 4) {
-            sc[s8] = (f.h.y >> (8 * s8)) & 63;
-            mn[s8] = (f.h.z >> (8 * s8)) & 63;
-        } else {
-            const int s0 = s8 - 4;
-            sc[s8] = ((f.h.w >> (8 * s0)) & 15) | (((f.h.y >> (8 * s0 + 6)) & 3) << 4);
-            mn[s8] = ((f.h.w >> (8 * s0 + 4)) & 15) | (((f.h.z >> (8 * s0 + 6)) & 3) << 4);
+    for (int r = 0; r < RW; r++) {
+        P[r] = (v16f){};
+        Q[r] = (v16f){};
+        // 6-bit scales and mins of the 8 sub-blocks (src/m5_kern_scalar.c:39-46)
+#pragma unroll
+        for (int s8 = 0; s8 < 8; s8++) {
+            int mn;
+            if (s8 < 4) {
+                sc[r][s8] = (f[r].h.y >> (8 * s8)) & 63;
+                mn = (f[r].h.z >> (8 * s8)) & 63;
+            } else {
+                const int s0 = s8 - 4;
+                sc[r][s8] = ((f[r].h.w >> (8 * s0)) & 15) | (((f[r].h.y >> (8 * s0 + 6)) & 3) << 4);
+                mn = ((f[r].h.w >> (8 * s0 + 4)) & 15) | (((f[r].h.z >> (8 * s0 + 6)) & 3) << 4);
+            }
+            // min term: B lane (n, 0) = m_0..m_7 of row n, lanes (n, 1) zero
+            Bm[r][s8] = u ? (_Float16)0.f : (_Float16)mn;
         }
     }
 #pragma unroll
     for (int s = 0; s < 16; s++) {
         const int v = s >> 2, nib = (s >> 1) & 1, bh = s & 1;
         const int sbk = 4 * (s >> 3) + ((s >> 1) & 3);  // sub-block of this K-step
-        const uint4 q = f.qv[v];
-        uint32_t w0 = bh ? q.z : q.x, w1 = bh ? q.w : q.y;
-        if (nib) {
-            w0 = ((w0 >> 4) & 0x0F0F0F0Fu) ^ 0x08080808u;  // stored XOR 0x80: high nibble u ^ 8
-            w1 = ((w1 >> 4) & 0x0F0F0F0Fu) ^ 0x08080808u;
-        } else {
-            w0 &= 0x0F0F0F0Fu;
-            w1 &= 0x0F0F0F0Fu;
+        const v8h Ahi = lds8(cur + ((size_t)(2 * s) * 64 + lane) * 16);
+        const v8h Alo = lds8(cur + ((size_t)(2 * s + 1) * 64 + lane) * 16);
+#pragma unroll
+        for (int r = 0; r < RW; r++) {
+            const uint4 q = f[r].qv[v];
+            uint32_t w0 = bh ? q.z : q.x, w1 = bh ? q.w : q.y;
+            if (nib) {
+                w0 = ((w0 >> 4) & 0x0F0F0F0Fu) ^ 0x08080808u;  // stored XOR 0x80: high nibble u ^ 8
+                w1 = ((w1 >> 4) & 0x0F0F0F0Fu) ^ 0x08080808u;
+            } else {
+                w0 &= 0x0F0F0F0Fu;
+                w1 &= 0x0F0F0F0Fu;
+            }
+            const _Float16 c = (_Float16)sc[r][sbk], o = (_Float16)(-1024.f * (float)sc[r][sbk]);
+            uint32_t p0, p1, p2, p3;
+            nib2h(w0, (v2h){c, c}, (v2h){o, o}, p0, p1);
+            nib2h(w1, (v2h){c, c}, (v2h){o, o}, p2, p3);
+            const v8h B = pack8(p0, p1, p2, p3);
+            P[r] = __builtin_amdgcn_mfma_f32_32x32x16_f16(Ahi, B, P[r], 0, 0, 0);
+            P[r] = __builtin_amdgcn_mfma_f32_32x32x16_f16(Alo, B, P[r], 0, 0, 0);
         }
-        const _Float16 c = (_Float16)sc[sbk], o = (_Float16)(-1024.f * (float)sc[sbk]);
-        uint32_t p0, p1, p2, p3;
-        nib2h(w0, (v2h){c, c}, (v2h){o, o}, p0, p1);
-        nib2h(w1, (v2h){c, c}, (v2h){o, o}, p2, p3);
-        const v8h B = pack8(p0, p1, p2, p3);
-        P = __builtin_amdgcn_mfma_f32_32x32x16_f16(lds8(cur + ((size_t)(2 * s) * 64 + lane) * 16), B, P, 0, 0, 0);
-        P = __builtin_amdgcn_mfma_f32_32x32x16_f16(lds8(cur + ((size_t)(2 * s + 1) * 64 + lane) * 16), B, P, 0, 0, 0);
     }
-    // min term: B lane (n, 0) = m_0..m_7 of row n, lanes (n, 1) zero
-    v8h Bm;
+    const v8h Mhi = lds8(cur + XH_A + (size_t)lane * 16), Mlo = lds8(cur + XH_A + 1024 + (size_t)lane * 16);
 #pragma unroll
-    for (int i = 0; i < 8; i++) Bm[i] = u ? (_Float16)0.f : (_Float16)mn[i];
-    Q = __builtin_amdgcn_mfma_f32_32x32x16_f16(lds8(cur + XH_A + (size_t)lane * 16), Bm, Q, 0, 0, 0);
-    Q = __builtin_amdgcn_mfma_f32_32x32x16_f16(lds8(cur + XH_A + 1024 + (size_t)lane * 16), Bm, Q, 0, 0, 0);
-    const float dm32 = -32.f * dm;
+    for (int r = 0; r < RW; r++) {
+        Q[r] = __builtin_amdgcn_mfma_f32_32x32x16_f16(Mhi, Bm[r], Q[r], 0, 0, 0);
+        Q[r] = __builtin_amdgcn_mfma_f32_32x32x16_f16(Mlo, Bm[r], Q[r], 0, 0, 0);
+        const float dd = h2f((uint16_t)(f[r].h.x & 0xFFFF)), dm32 = -32.f * h2f((uint16_t)(f[r].h.x >> 16));
 #pragma unroll
-    for (int i = 0; i < 16; i++) part[i] = fmaf(dd, P[i], dm32 * Q[i]);
+        for (int i = 0; i < 16; i++) part[r][i] = fmaf(dd, P[r][i], dm32 * Q[r][i]);
+    }
 }
 
-__device__ __forceinline__ void tile_q6(const WFrag<2>& f, const uint8_t* cur, int lane, float (&part)[16]) {
-    v16f P = {}, Q = {};
-    const float dd = h2f((uint16_t)f.d);
+template <int RW>
+__device__ __forceinline__ void tiles_q6(const WFrag<2> (&f)[RW], const uint8_t* cur, int lane,
+                                         float (&part)[RW][16]) {
+    v16f P[RW], Q[RW];
+#pragma unroll
+    for (int r = 0; r < RW; r++) {
+        P[r] = (v16f){};
+        Q[r] = (v16f){};
+    }
 #pragma unroll
     for (int s = 0; s < 16; s++) {
         const int g2 = s >> 3, r6 = (s >> 1) & 3, bh = s & 1;
-        const uint4 A4 = f.qa[g2], B4 = f.qb[g2], H4 = f.qh[g2];
-        uint32_t wq[2];
-#pragma unroll
-        for (int k = 0; k < 2; k++) {
-            const int qd = 2 * bh + k;  // dword of the 16-byte vectors
-            const uint32_t av = qd == 0 ? A4.x : (qd == 1 ? A4.y : (qd == 2 ? A4.z : A4.w));
-            const uint32_t bv = qd == 0 ? B4.x : (qd == 1 ? B4.y : (qd == 2 ? B4.z : B4.w));
-            const uint32_t hv = qd == 0 ? H4.x : (qd == 1 ? H4.y : (qd == 2 ? H4.z : H4.w));
-            // the GGUF 6-bit map of src/m5_kern_scalar.c:115-142 (as the GEMV's dot_q6)
-            if (r6 == 0) wq[k] = (av & 0x0F0F0F0Fu) | ((hv << 4) & 0x30303030u);
-            else if (r6 == 1) wq[k] = (bv & 0x0F0F0F0Fu) | ((hv << 2) & 0x30303030u);
-            else if (r6 == 2) wq[k] = ((av >> 4) & 0x0F0F0F0Fu) | (hv & 0x30303030u);
-            else wq[k] = ((bv >> 4) & 0x0F0F0F0Fu) | ((hv >> 2) & 0x30303030u);
-        }
-        const int scv = (int)(int8_t)(f.sc4[g2] >> (8 * r6));
-        const int shv = scv >> 3, slv = scv & 7;  // sc = 8*sh + sl
-        const _Float16 ch = (_Float16)shv, cl = (_Float16)slv;
-        const _Float16 oh = (_Float16)(-1056.f * (float)shv), ol = (_Float16)(-1056.f * (float)slv);
-        uint32_t p0, p1, p2, p3;
-        nib2h(wq[0], (v2h){ch, ch}, (v2h){oh, oh}, p0, p1);
-        nib2h(wq[1], (v2h){ch, ch}, (v2h){oh, oh}, p2, p3);
-        const v8h Bh = pack8(p0, p1, p2, p3);
-        nib2h(wq[0], (v2h){cl, cl}, (v2h){ol, ol}, p0, p1);
-        nib2h(wq[1], (v2h){cl, cl}, (v2h){ol, ol}, p2, p3);
-        const v8h Bl = pack8(p0, p1, p2, p3);
         const v8h Ahi = lds8(cur + ((size_t)(2 * s) * 64 + lane) * 16);
         const v8h Alo = lds8(cur + ((size_t)(2 * s + 1) * 64 + lane) * 16);
-        P = __builtin_amdgcn_mfma_f32_32x32x16_f16(Ahi, Bh, P, 0, 0, 0);
-        P = __builtin_amdgcn_mfma_f32_32x32x16_f16(Alo, Bh, P, 0, 0, 0);
-        Q = __builtin_amdgcn_mfma_f32_32x32x16_f16(Ahi, Bl, Q, 0, 0, 0);
-        Q = __builtin_amdgcn_mfma_f32_32x32x16_f16(Alo, Bl, Q, 0, 0, 0);
+#pragma unroll
+        for (int r = 0; r < RW; r++) {
+            const uint4 A4 = f[r].qa[g2], B4 = f[r].qb[g2], H4 = f[r].qh[g2];
+            uint32_t wq[2];
+#pragma unroll
+            for (int k = 0; k < 2; k++) {
+                const int qd = 2 * bh + k;  // dword of the 16-byte vectors
+                const uint32_t av = qd == 0 ? A4.x : (qd == 1 ? A4.y : (qd == 2 ? A4.z : A4.w));
+                const uint32_t bv = qd == 0 ? B4.x : (qd == 1 ? B4.y : (qd == 2 ? B4.z : B4.w));
+                const uint32_t hv = qd == 0 ? H4.x : (qd == 1 ? H4.y : (qd == 2 ? H4.z : H4.w));
+                // the GGUF 6-bit map of src/m5_kern_scalar.c:115-142 (as the GEMV's dot_q6)
+                if (r6 == 0) wq[k] = (av & 0x0F0F0F0Fu) | ((hv << 4) & 0x30303030u);
+                else if (r6 == 1) wq[k] = (bv & 0x0F0F0F0Fu) | ((hv << 2) & 0x30303030u);
+                else if (r6 == 2) wq[k] = ((av >> 4) & 0x0F0F0F0Fu) | (hv & 0x30303030u);
+                else wq[k] = ((bv >> 4) & 0x0F0F0F0Fu) | ((hv >> 2) & 0x30303030u);
+            }
+            const int scv = (int)(int8_t)(f[r].sc4[g2] >> (8 * r6));
+            const int shv = scv >> 3, slv = scv & 7;  // sc = 8*sh + sl
+            const _Float16 ch = (_Float16)shv, cl = (_Float16)slv;
+            const _Float16 oh = (_Float16)(-1056.f * (float)shv), ol = (_Float16)(-1056.f * (float)slv);
+            uint32_t p0, p1, p2, p3;
+            nib2h(wq[0], (v2h){ch, ch}, (v2h){oh, oh}, p0, p1);
+            nib2h(wq[1], (v2h){ch, ch}, (v2h){oh, oh}, p2, p3);
+            const v8h Bh = pack8(p0, p1, p2, p3);
+            nib2h(wq[0], (v2h){cl, cl}, (v2h){ol, ol}, p0, p1);
+            nib2h(wq[1], (v2h){cl, cl}, (v2h){ol, ol}, p2, p3);
+            const v8h Bl = pack8(p0, p1, p2, p3);
+            P[r] = __builtin_amdgcn_mfma_f32_32x32x16_f16(Ahi, Bh, P[r], 0, 0, 0);
+            P[r] = __builtin_amdgcn_mfma_f32_32x32x16_f16(Alo, Bh, P[r], 0, 0, 0);
+            Q[r] = __builtin_amdgcn_mfma_f32_32x32x16_f16(Ahi, Bl, Q[r], 0, 0, 0);
+            Q[r] = __builtin_amdgcn_mfma_f32_32x32x16_f16(Alo, Bl, Q[r], 0, 0, 0);
+        }
     }
 #pragma unroll
-    for (int i = 0; i < 16; i++) part[i] = dd * fmaf(8.f, P[i], Q[i]);
+    for (int r = 0; r < RW; r++) {
+        const float dd = h2f((uint16_t)f[r].d);
+#pragma unroll
+        for (int i = 0; i < 16; i++) part[r][i] = dd * fmaf(8.f, P[r][i], Q[r][i]);
+    }
 }
 
 // FM 1 = Q4_K, 2 = Q6_K.  Grid (row blocks of 4*RW*32 rows, token tiles, K
@@ -308,18 +339,19 @@ __global__ __launch_bounds__(256) void k_gemmh(const GemmHArgs a) {
         float4 ts4[4];  // token scales of this lane's C rows 8q + 4u .. +3
 #pragma unroll
         for (int q = 0; q < 4; q++) ts4[q] = *reinterpret_cast<const float4*>(cur + XH_A + XH_M + 4 * (8 * q + 4 * u));
+        if (32 * rt0 < a.L.n_out) {  // uniform per wave; no barrier inside.  Tiles past n_out
+                                     // (clamped loads) are computed and not stored.
+            float part[RW][16];
+            if constexpr (FM == 1) tiles_q4<RW>(wc, cur, lane, u, part);
+            else tiles_q6<RW>(wc, cur, lane, part);
 #pragma unroll
-        for (int r = 0; r < RW; r++) {
-            if (32 * (rt0 + r) >= a.L.n_out) break;  // uniform per wave; no barrier inside
-            float part[16];
-            if constexpr (FM == 1) tile_q4(wc[r], cur, lane, u, part);
-            else tile_q6(wc[r], cur, lane, part);
+            for (int r = 0; r < RW; r++)
 #pragma unroll
-            for (int i = 0; i < 16; i++) {
-                const float4 t4 = ts4[i >> 2];
-                const float tsc = (i & 3) == 0 ? t4.x : ((i & 3) == 1 ? t4.y : ((i & 3) == 2 ? t4.z : t4.w));
-                y[r][i] = fmaf(tsc, part[i], y[r][i]);
-            }
+                for (int i = 0; i < 16; i++) {
+                    const float4 t4 = ts4[i >> 2];
+                    const float tsc = (i & 3) == 0 ? t4.x : ((i & 3) == 1 ? t4.y : ((i & 3) == 2 ? t4.z : t4.w));
+                    y[r][i] = fmaf(tsc, part[r][i], y[r][i]);
+                }
         }
 #pragma unroll
         for (int r = 0; r < RW; r++) wc[r] = wn[r];
@@ -372,12 +404,15 @@ int draco_gemmh_x_launch(const float* X, int T, int n_in, uint8_t* buf, hipStrea
     return 0;
 }
 
-// Row blocks of 128 rows (one tile per wave) unless the product has row
-// tiles to spare; K split so that about 256 blocks run, each over at least
-// 2 super-blocks.  part: kspl * T * ldy floats (draco_gemmh_part_floats).
+// Row blocks of 256 rows (two tiles per wave, sharing each A read) for
+// products of at least 64 row tiles, else 128 rows; K split so that about
+// 256 blocks run, each over at least 2 super-blocks.  Measured on the
+// configs[2] chunk (256 tokens): q / o 17.0 -> 15.4 us, down 55.5 -> 51 us
+// with two tiles per wave; k / v (16 row tiles) slower with them.  part:
+// kspl * T * ldy floats (draco_gemmh_part_floats).
 static void plan(const DracoLayout& L, int T, int& rw, int& kspl) {
     const int nb = L.n_in / 256, tiles32 = (L.n_out + 31) / 32, ntt = (T + 31) / 32;
-    rw = tiles32 >= 4 * 2 * 64 ? 2 : 1;
+    rw = tiles32 >= 64 ? 2 : 1;
     const int blocks = ((tiles32 + 4 * rw - 1) / (4 * rw)) * ntt;
     kspl = 1;
     while (blocks * kspl * 2 <= 256 && nb / (kspl * 2) >= 2) kspl *= 2;
