@@ -517,36 +517,66 @@ struct FQ80 {
         }
         sx[0] = 0.f;
     }
-    __device__ static float dot(const SegK& sg, int row, int u, const float* xv, const float* sx) {
-        (void)sx;
+    struct W {  // one block's quants and scale
+        uint4 q0, q1;
+        uint16_t d;
+    };
+    __device__ static W load(const SegK& sg, int row, int u) {
         const size_t blk = (size_t)row * sg.nb + u;
-        const uint4 q0 = ldnt4(sg.base + blk * 32), q1 = ldnt4(sg.base + blk * 32 + 16);
-        const float d = h2f(*reinterpret_cast<const uint16_t*>(sg.aux + blk * 2));
-        const uint32_t Q[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+        W w;
+        w.q0 = ldnt4(sg.base + blk * 32);
+        w.q1 = ldnt4(sg.base + blk * 32 + 16);
+        w.d = *reinterpret_cast<const uint16_t*>(sg.aux + blk * 2);
+        return w;
+    }
+    __device__ static float dotw(const W& w, const float* xv, const float* sx) {
+        (void)sx;
+        const uint32_t Q[8] = {w.q0.x, w.q0.y, w.q0.z, w.q0.w, w.q1.x, w.q1.y, w.q1.z, w.q1.w};
         float s = 0.f;
 #pragma unroll
         for (int dw = 0; dw < 8; dw++)
 #pragma unroll
             for (int k = 0; k < 4; k++) s = fmaf(sbyte_f(Q[dw], k), xv[4 * dw + k], s);
-        return d * s;
+        return h2f(w.d) * s;
     }
 };
 
-// R row dots of one wave (plus the same rows of a second matrix when DUAL)
+// R row dots of one wave (plus the same rows of a second matrix when DUAL).
+// The wave's lanes cover (row, block) pairs p = i * U + u, so rows of fewer
+// than 64 blocks still occupy every lane (SmolLM2's 960-wide rows are 30
+// blocks: two rows per pass instead of 30 of 64 lanes); each lane adds its
+// pair's dot to its row's accumulator, and the caller sums the lanes.  The
+// first pass's weights (w0, w02) were requested by the caller before the x
+// prologue (first_pair).
+template <class F, int R>
+__device__ __forceinline__ bool first_pair(const SegK& s, int r0, int& i, int& u) {
+    const int lane = threadIdx.x & 63, U = s.nb * F::UPB;
+    i = lane / U;
+    u = lane - i * U;
+    return lane < R * U && r0 + i < s.n_out;
+}
+
 template <class F, int R, bool DUAL>
-__device__ __forceinline__ void rows_dot(const SegK& s, const SegK& s2, const float* xs, int r0, float* acc) {
+__device__ __forceinline__ void rows_dot(const SegK& s, const SegK& s2, const float* xs, int r0, float* acc,
+                                         const typename F::W& w0, const typename F::W& w02) {
     const int lane = threadIdx.x & 63;
     const int U = s.nb * F::UPB;
     const int n_out = s.n_out;
-    for (int u = lane; u < U; u += 64) {
+    for (int p = lane; p < R * U; p += 64) {
+        const int i = p / U, u = p - i * U;
         float xv[F::NX], sx[F::NS];
         F::xslice(xs, u, xv, sx);
+        if (r0 + i < n_out) {
+            const bool first = p == lane;
+            const float d = F::dotw(first ? w0 : F::load(s, r0 + i, u), xv, sx);
+            const float d2 = DUAL ? F::dotw(first ? w02 : F::load(s2, r0 + i, u), xv, sx) : 0.f;
 #pragma unroll
-        for (int i = 0; i < R; i++)
-            if (r0 + i < n_out) {
-                acc[i] += F::dot(s, r0 + i, u, xv, sx);
-                if (DUAL) acc[R + i] += F::dot(s2, r0 + i, u, xv, sx);
-            }
+            for (int k = 0; k < R; k++)
+                if (k == i) {
+                    acc[k] += d;
+                    if (DUAL) acc[R + k] += d2;
+                }
+        }
     }
 }
 
@@ -564,6 +594,17 @@ __global__ __launch_bounds__(256) void k_seg(const SegKArgs a) {
         if ((int)blockIdx.x >= a.seg[i].first) si = i;
     const SegK& s = a.seg[si];
     const SegK& s2 = a.seg[DUAL ? si + 1 : si];
+    const int r0 = ((int)blockIdx.x - s.first) * SEG_ROWS + wv * SEG_R;
+
+    // this lane's first (row, block) weights, requested before the x prologue
+    typename F::W w0 = {}, w02 = {};
+    {
+        int i0, u0;
+        if (first_pair<F, SEG_R>(s, r0, i0, u0)) {
+            w0 = F::load(s, r0 + i0, u0);
+            if (DUAL) w02 = F::load(s2, r0 + i0, u0);
+        }
+    }
 
     // prologue: RMSNorm of x into LDS (every block; same order -> same result)
     const float* xs = a.x;
@@ -576,7 +617,7 @@ __global__ __launch_bounds__(256) void k_seg(const SegKArgs a) {
         }
         ss = wave_sum(ss);
         if (lane == 0) red[wv] = ss;
-        __syncthreads();
+        lds_barrier();  // LDS only: the weight loads above stay in flight
         const float tot = (red[0] + red[1]) + (red[2] + red[3]);
         const float inv = 1.f / sqrtf(tot / (float)a.n_in + a.eps);
         for (int i = tid; i < a.n_in; i += 256) {
@@ -584,15 +625,14 @@ __global__ __launch_bounds__(256) void k_seg(const SegKArgs a) {
             xsh[i] = v;
             if (a.xn_out && blockIdx.x == 0) a.xn_out[i] = v;
         }
-        __syncthreads();
+        lds_barrier();
         xs = xsh;
     }
 
-    const int r0 = ((int)blockIdx.x - s.first) * SEG_ROWS + wv * SEG_R;
     float acc[2 * SEG_R];
 #pragma unroll
     for (int i = 0; i < 2 * SEG_R; i++) acc[i] = 0.f;
-    rows_dot<F, SEG_R, DUAL>(s, s2, xs, r0, acc);
+    rows_dot<F, SEG_R, DUAL>(s, s2, xs, r0, acc, w0, w02);
 #pragma unroll
     for (int i = 0; i < (DUAL ? 2 : 1) * SEG_R; i++) acc[i] = wave_sum(acc[i]);
 
