@@ -448,7 +448,11 @@ int draco_gemv_q8k_launch(Q8Launch& a, int nvec, bool isums, hipStream_t st) {
         return -1;
     }
     if (a.img && isums) return -1;
-    const int nw = nb >= 32 ? 16 : (nb >= 8 ? 8 : 4);
+    // 16 waves for long rows unless that leaves padding items (a padding item
+    // re-reads its wave's first item, which the non-temporal weight loads may
+    // already have evicted: 56 super-blocks over 16 waves fetched 11% more
+    // than the matrix); 8 waves divide 56
+    const int nw = nb >= 32 && nb % 16 == 0 ? 16 : (nb >= 8 ? 8 : 4);
     const size_t img = (size_t)NBp * nb * Q8K_BLOCK_BYTES;  // = NBp * n_in + ng * NBp * 2 + nb * NBp * 4
     const size_t lds = ((img + 15) & ~(size_t)15) + 1024 + (size_t)NBp * nw * 16 * 4;
     (void)ng;
