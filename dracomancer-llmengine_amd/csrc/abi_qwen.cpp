@@ -118,8 +118,12 @@ struct PostNorm {
 // Q4_K / Q6_K matrices share one launch, Q8_0 matrices another; any other
 // format runs through the plain GEMV on an explicitly normalised copy in xn.
 // With `post` (one matrix only) the output's RMSNorm is produced too.
+// With `pend` (a pending residual, x + pend[0..n_in) + pend[n_in..2 n_in))
+// every matrix must be a K-quant (one launch): its prologue forms the sum,
+// normalises it and stores it to pend_sum.
 int enqueue_proj(const Proj* p, int n, const float* x, int n_in, const float* norm_w, float* xn,
-                 hipStream_t st, const PostNorm* post = nullptr) {
+                 hipStream_t st, const PostNorm* post = nullptr, const float* pend = nullptr,
+                 float* pend_sum = nullptr) {
     if (post && n != 1) return fail(-1, "enqueue_proj: post-norm needs one matrix");
     bool done[SEG_MAX] = {};
     if (n > SEG_MAX) return fail(-1, "enqueue_proj: %d matrices", n);
@@ -147,6 +151,12 @@ int enqueue_proj(const Proj* p, int n, const float* x, int n_in, const float* no
         s.do_norm = norm_w ? 1 : 0;
         s.norm_w = norm_w;
         s.eps = QEPS;
+        if (pend) {
+            if (f != 1 || !norm_w || !pend_sum) return fail(-1, "enqueue_proj: a pending residual needs K-quants");
+            s.do_norm = 3;
+            s.am_val = const_cast<float*>(pend);
+            s.xn_out = pend_sum;
+        }
         for (int j = i; j < n; j++) {
             if (done[j] || fam(p[j].m->L.code) != f) continue;
             SegDesc d = {};
@@ -159,9 +169,47 @@ int enqueue_proj(const Proj* p, int n, const float* x, int n_in, const float* no
             done[j] = true;
         }
         if (draco_seg_launch(s, st)) return fail(-1, "segment GEMV launch rejected");
+        if (pend) {
+            for (int j = 0; j < n; j++)
+                if (!done[j]) return fail(-1, "enqueue_proj: a pending residual needs one launch");
+        }
         if (post) dk_rmsnorm(p[i].y, post->w, post->out, p[i].m->L.n_out, QEPS, st);
     }
     return 0;
+}
+
+// A split-K projection of x (n_in wide) into the two partials pd[0..n_out) and
+// pd[n_out..2 n_out) (SegLaunch.ksplit), optionally with the GDN gated-rms
+// prologue (gnorm_pss: its partial sums of squares).
+int enqueue_proj_ks(const DracoMat* m, const float* x, int n_in, float* pd, const float* gnorm_pss,
+                    hipStream_t st) {
+    SegLaunch s = {};
+    s.nseg = 1;
+    s.n_in = n_in;
+    s.x = x;
+    s.ksplit = 2;
+    if (gnorm_pss) {
+        s.do_norm = 2;
+        s.eps = QEPS;
+        s.kc = const_cast<float*>(gnorm_pss);
+    }
+    SegDesc& d = s.seg[0];
+    d.base = m->dev;
+    d.L = m->L;
+    d.row0 = 0;
+    d.row1 = m->L.n_out;
+    d.y = pd;
+    d.epi = EPI_STORE;
+    if (draco_seg_launch(s, st)) return fail(-1, "split-K projection launch rejected");
+    return 0;
+}
+
+// Whether a projection can run split-K (rows of 16 or 32 super-blocks, at
+// most 128 row tiles: the launches that leave CUs idle otherwise).
+bool ks_ok(const DracoMat* m) {
+    const int nb = m->L.n_in / 256;
+    return (m->L.code == DRACO_Q4_K || m->L.code == DRACO_Q6_K) && m->L.n_in % 256 == 0 && (nb == 16 || nb == 32) &&
+           (m->L.n_out + 15) / 16 <= 128;
 }
 
 // ------------------------------------------------------------------ GDN --
@@ -173,6 +221,13 @@ struct GdnDev {
 
 struct GdnBufs {
     float *h1, *qkv, *z, *on, *x2o, *x2n, *xn, *S, *tail, *pss;
+    // the stack's pending residual: the layer input is h1 + pend[0..H) +
+    // pend[H..2H), formed into pend_sum by the in-projection (then the
+    // layer's input for the scan's gates and the residual); with ks_out the
+    // ssm_out projection runs split-K into ks_out instead of adding its
+    // residual into x2o
+    const float* pend;
+    float *pend_sum, *ks_out;
 };
 
 int gdn_resolve(const GdnW* w, GdnDev& g) {
@@ -221,6 +276,9 @@ int gdn_bufs(const GdnDev& g, int slot, GdnBufs& b) {
     b.S = take(ns);
     b.tail = take(nt);
     b.pss = take((size_t)g.n_vh * GDN_PSS_STRIDE);
+    b.pend = nullptr;
+    b.pend_sum = nullptr;
+    b.ks_out = nullptr;
     return 0;
 }
 
@@ -228,7 +286,8 @@ int gdn_bufs(const GdnDev& g, int slot, GdnBufs& b) {
 // itself, or has none)
 int enqueue_gdn(const GdnDev& g, const GdnBufs& b, hipStream_t st, bool post_norm = true) {
     const Proj in[2] = {{g.qkv, b.qkv, nullptr}, {g.gate, b.z, nullptr}};
-    if (int rc = enqueue_proj(in, 2, b.h1, QH, g.attn_norm, b.xn, st)) return rc;
+    if (int rc = enqueue_proj(in, 2, b.h1, QH, g.attn_norm, b.xn, st, nullptr, b.pend, b.pend_sum)) return rc;
+    const float* h1 = b.pend ? b.pend_sum : b.h1;
     GdnArgs a = {};
     a.QKV = b.qkv;
     a.Z = b.z;
@@ -241,7 +300,7 @@ int enqueue_gdn(const GdnDev& g, const GdnBufs& b, hipStream_t st, bool post_nor
     a.n_qkv = g.n_qkv;
     a.n_vh = g.n_vh;
     a.nhq = QNKH;
-    a.h1 = b.h1;
+    a.h1 = h1;
     a.attn_norm = g.attn_norm;
     a.bw = g.bw;
     a.aw = g.aw;
@@ -256,6 +315,8 @@ int enqueue_gdn(const GdnDev& g, const GdnBufs& b, hipStream_t st, bool post_nor
     a.nspl = kq ? draco_gdn_split(true) : 1;
     a.defer_gnorm = a.nspl > 1;
     if (draco_gdn_step_launch(a, st)) return fail(-1, "gdn step launch rejected");
+    if (b.ks_out && !a.defer_gnorm) return fail(-1, "gdn: split-K ssm_out needs the gated-rms prologue");
+    if (b.ks_out) return enqueue_proj_ks(g.out, b.on, g.d_in, b.ks_out, b.pss, st);
     if (a.defer_gnorm) {
         SegLaunch s = {};
         s.nseg = 1;
@@ -269,12 +330,12 @@ int enqueue_gdn(const GdnDev& g, const GdnBufs& b, hipStream_t st, bool post_nor
         d.L = g.out->L;
         d.epi = EPI_RESID;
         d.y = b.x2o;
-        d.yadd = b.h1;
+        d.yadd = h1;
         if (draco_seg_launch(s, st)) return fail(-1, "gdn ssm_out launch rejected");
         if (post_norm) dk_rmsnorm(b.x2o, g.post_norm, b.x2n, QH, QEPS, st);
         return 0;
     }
-    const Proj out[1] = {{g.out, b.x2o, b.h1}};
+    const Proj out[1] = {{g.out, b.x2o, h1}};
     const PostNorm pn = {g.post_norm, b.x2n};
     return enqueue_proj(out, 1, b.on, g.d_in, nullptr, b.xn, st, post_norm ? &pn : nullptr);
 }
@@ -594,6 +655,7 @@ struct QStack {
     float *x = nullptr, *x2n = nullptr, *xn = nullptr, *qkv = nullptr, *z = nullptr, *on = nullptr, *QG = nullptr,
           *Qr = nullptr, *kraw = nullptr, *vraw = nullptr, *ao = nullptr, *part = nullptr, *fg = nullptr,
           *fu = nullptr, *xe = nullptr, *pss = nullptr;
+    float *xs = nullptr, *pd = nullptr;  // pending residual: its materialised sum and the split-K partials [2][H]
     int* state = nullptr;   // device [pos, told]
     int* hstate = nullptr;  // pinned
     // a prefill chunk of up to pf_cap tokens
@@ -764,7 +826,8 @@ QStack* build_qstack(const QStackLayer* layers, int n_layer, int h) {
         qstack_alloc(k, &s->vraw, FNKV * FHD) ||
         qstack_alloc(k, &s->part, (size_t)std::max(s->max_nh, 1) * nsplit * (FHD + 2)) ||
         qstack_alloc(k, &s->fg, std::max(s->max_ff, 1)) || qstack_alloc(k, &s->fu, std::max(s->max_ff, 1)) ||
-        qstack_alloc(k, &s->pss, (size_t)std::max(s->max_vh, 1) * GDN_PSS_STRIDE))
+        qstack_alloc(k, &s->pss, (size_t)std::max(s->max_vh, 1) * GDN_PSS_STRIDE) ||
+        qstack_alloc(k, &s->xs, QH) || qstack_alloc(k, &s->pd, 2 * QH))
         return nullptr;
     if (hipMalloc(&s->state, sizeof(int) * 16) != hipSuccess ||
         hipHostMalloc(&s->hstate, sizeof(int) * 16, hipHostMallocDefault) != hipSuccess) {
@@ -821,39 +884,82 @@ int enqueue_qffn(QStack* s, QLayer& q, hipStream_t st) {
     return enqueue_proj(dn, 1, s->fg, q.FF, nullptr, s->xn, st);
 }
 
+// Whether layer l's output projection runs split-K, leaving its residual add
+// to layer l + 1's in-projection: a layer without FFN (its projection's
+// output is the layer output) followed by a layer whose in-projection is all
+// K-quants; GDN layers only on the gated-rms prologue path.
+bool qks(const QStack* s, int l) {
+    if (l + 1 >= s->n_layer) return false;
+    const QLayer& q = s->L[l];
+    if (q.desc.ffn_kind != QFFN_NONE) return false;
+    auto kq = [](const DracoMat* m) { return m->L.code == DRACO_Q4_K || m->L.code == DRACO_Q6_K; };
+    if (q.desc.kind == 0) {
+        if (!ks_ok(q.g.out) || draco_gdn_split(true) <= 1) return false;
+    } else if (!ks_ok(q.f.o)) {
+        return false;
+    }
+    const QLayer& n = s->L[l + 1];
+    if (n.desc.kind == 0) return kq(n.g.qkv) && kq(n.g.gate);
+    return kq(n.f.q) && kq(n.f.k) && kq(n.f.v);
+}
+
 // one token through every layer: x (device) in place, or, with xin, layer 0
 // reads its input from xin and every layer leaves its output in x; position
 // and told from s->state ([pos, told], told = pos as the reference's driver
-// passes them)
+// passes them).  After a split-K output projection (qks) the layer output is
+// pending: base + the partials in s->pd, which the next layer's in-projection
+// forms into the other of s->x / s->xs (its input from then on).
 int enqueue_qtoken(QStack* s, hipStream_t st, float* xin = nullptr) {
+    float* base = s->x;   // the current layer's materialised input (or pending base)
+    bool pending = false;
     for (int l = 0; l < s->n_layer; l++) {
         QLayer& q = s->L[l];
-        float* x0 = (l == 0 && xin) ? xin : s->x;
+        float* x0 = (l == 0 && xin) ? xin : base;
+        float* alt = base == s->x ? s->xs : s->x;  // where a pending sum is formed
+        const bool ks = qks(s, l);
+        float* in = pending ? alt : x0;  // this layer's input once formed
         if (q.desc.kind == 0) {
             GdnBufs b = {};
             b.h1 = x0;
             b.qkv = s->qkv;
             b.z = s->z;
             b.on = s->on;
-            b.x2o = s->x;  // in place: the ssm_out projection adds its residual row by row
+            b.x2o = s->x;  // in place (or from the formed input): the ssm_out projection adds its residual row by row
             b.x2n = s->x2n;
             b.xn = s->xn;
             b.S = q.S;
             b.tail = q.tail;
             b.pss = s->pss;
+            b.pend = pending ? s->pd : nullptr;
+            b.pend_sum = pending ? alt : nullptr;
+            b.ks_out = ks ? s->pd : nullptr;
             if (int rc = enqueue_gdn(q.g, b, st, false)) return rc;
         } else {
             const FullDev& f = q.f;
-            const Proj in[3] = {{f.q, s->QG, nullptr}, {f.k, s->kraw, nullptr}, {f.v, s->vraw, nullptr}};
-            if (int rc = enqueue_proj(in, 3, x0, QH, f.attn_norm, s->xn, st)) return rc;
+            const Proj in3[3] = {{f.q, s->QG, nullptr}, {f.k, s->kraw, nullptr}, {f.v, s->vraw, nullptr}};
+            if (int rc = enqueue_proj(in3, 3, x0, QH, f.attn_norm, s->xn, st, nullptr, pending ? s->pd : nullptr,
+                                      pending ? alt : nullptr))
+                return rc;
             dk_fa_prep_rows(s->QG, f.nh * 2 * FHD, s->Qr, s->kraw, s->vraw, q.kc, q.vc, f.q_norm, f.k_norm, q.cs,
                             s->state, 0, 0, f.nh, 1, st);
             if (dk_attention(s->Qr, q.kc, q.vc, s->part, nullptr, s->ao, s->state, 0, f.nh, FNKV, FHD, q.desc.max_t,
                              1.f / sqrtf((float)FHD), st, s->QG + FHD, 2 * FHD))
                 return fail(-1, "qwen stack: attention launch rejected");
-            const Proj out[1] = {{f.o, s->x, x0}};
-            if (int rc = enqueue_proj(out, 1, s->ao, f.nh * FHD, nullptr, s->xn, st)) return rc;
+            if (ks) {
+                if (int rc = enqueue_proj_ks(f.o, s->ao, f.nh * FHD, s->pd, nullptr, st)) return rc;
+            } else {
+                const Proj out[1] = {{f.o, s->x, in}};
+                if (int rc = enqueue_proj(out, 1, s->ao, f.nh * FHD, nullptr, s->xn, st)) return rc;
+            }
         }
+        if (ks) {
+            // the layer output is in + the partials: the next layer forms it
+            base = in;
+            pending = true;
+            continue;
+        }
+        base = s->x;
+        pending = false;
         if (int rc = enqueue_qffn(s, q, st)) return rc;
     }
     return 0;

@@ -405,14 +405,15 @@ int draco_gemmh_x_launch(const float* X, int T, int n_in, uint8_t* buf, hipStrea
 }
 
 // Row blocks of 256 rows (two tiles per wave, sharing each A read) for
-// products of at least 64 row tiles, else 128 rows; K split so that about
-// 256 blocks run, each over at least 2 super-blocks.  Measured on the
-// configs[2] chunk (256 tokens): q / o 17.0 -> 15.4 us, down 55.5 -> 51 us
-// with two tiles per wave; k / v (16 row tiles) slower with them.  part:
-// kspl * T * ldy floats (draco_gemmh_part_floats).
+// products of at least 64 row tiles over at least 4 token tiles, else 128
+// rows; K split so that about 256 blocks run, each over at least 2
+// super-blocks.  Measured on the configs[2] chunk (256 tokens): q / o 17.0 ->
+// 15.4 us, down 55.5 -> 51 us with two tiles per wave; k / v (16 row tiles)
+// slower with them, and so was the configs[4] prefill's 64-token chunk
+// (9610 -> 9385 tok/s).  part: kspl * T * ldy floats (draco_gemmh_part_floats).
 static void plan(const DracoLayout& L, int T, int& rw, int& kspl) {
     const int nb = L.n_in / 256, tiles32 = (L.n_out + 31) / 32, ntt = (T + 31) / 32;
-    rw = tiles32 >= 64 ? 2 : 1;
+    rw = tiles32 >= 64 && ntt >= 4 ? 2 : 1;
     const int blocks = ((tiles32 + 4 * rw - 1) / (4 * rw)) * ntt;
     kspl = 1;
     while (blocks * kspl * 2 <= 256 && nb / (kspl * 2) >= 2) kspl *= 2;

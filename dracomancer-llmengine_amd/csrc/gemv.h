@@ -64,7 +64,7 @@ struct SegLaunch {
     // partials p at am_val ([2][n_in]), the sum stored to xn_out by block 0
     int do_norm;
     // 2: split-K (Q4_K / Q6_K, one EPI_STORE segment over the whole matrix,
-    // do_norm 0, 16 or 32 super-blocks per row):
+    // do_norm 0 or 2, 16 or 32 super-blocks per row):
     // y[r] = the first half's dot, y[n_out + r] = the second half's
     int ksplit;
     float eps;

@@ -914,16 +914,18 @@ int seg_launch_dq(SegLaunch& a, hipStream_t st) {
         tiles += s.n_tiles;
     }
     if (dual && (a.nseg != 2 || fm == 3)) return -1;
-    // GNORM prologue: one residual segment over whole 128-wide groups
-    if (a.do_norm == 2 && (a.nseg != 1 || a.seg[0].epi != EPI_RESID || n_in % 128 || !a.kc)) return -1;
+    // GNORM prologue: one residual segment (a store segment when split-K) over whole 128-wide groups
+    if (a.do_norm == 2 && (a.nseg != 1 || a.seg[0].epi != (a.ksplit ? EPI_STORE : EPI_RESID) || n_in % 128 || !a.kc))
+        return -1;
     // PRES prologue: the partials of the pending residual; no SwiGLU pair
     if (a.do_norm == 3 && (dual || !a.am_val)) return -1;
-    // split-K: one whole-matrix store segment, no prologue norm, halves of
-    // NW-divisible super-block counts on the 8-wave kernel
+    // split-K: one whole-matrix store segment, no prologue norm or the
+    // per-wave GNORM one, halves of NW-divisible super-block counts on the
+    // 8-wave kernel
     if (a.ksplit) {
         const SegDesc& s0 = a.seg[0];
-        if (a.ksplit != 2 || a.nseg != 1 || dual || a.do_norm || s0.epi != EPI_STORE || s0.row0 != 0 ||
-            s0.row1 != s0.L.n_out || nb < 16 || nb > 32 || (nb / 2) % 8)
+        if (a.ksplit != 2 || a.nseg != 1 || dual || (a.do_norm != 0 && a.do_norm != 2) || s0.epi != EPI_STORE ||
+            s0.row0 != 0 || s0.row1 != s0.L.n_out || nb < 16 || nb > 32 || (nb / 2) % 8)
             return -1;
     }
     for (int i = a.nseg; i < SEG_MAX; i++) {  // unused slots: never selected by seg_of_tile
@@ -956,8 +958,14 @@ int seg_launch_dq(SegLaunch& a, hipStream_t st) {
         a.kv_dim = a.seg[0].L.n_out;
         a.total_tiles = 2 * tiles;
         grid = 2 * tiles < cap ? 2 * tiles : cap;
-        if (fm == 1) launch_dq1<8, 1, false, false, EPI_STORE, 0, false, true>(a, grid, st);
-        else launch_dq1<8, 2, false, false, EPI_STORE, 0, false, true>(a, grid, st);
+        if (a.do_norm == 2) {
+            if (fm == 1) launch_dq1<8, 1, false, false, EPI_STORE, 2, false, true>(a, grid, st);
+            else launch_dq1<8, 2, false, false, EPI_STORE, 2, false, true>(a, grid, st);
+        } else if (fm == 1) {
+            launch_dq1<8, 1, false, false, EPI_STORE, 0, false, true>(a, grid, st);
+        } else {
+            launch_dq1<8, 2, false, false, EPI_STORE, 0, false, true>(a, grid, st);
+        }
         return 0;
     }
     if (grid <= 0) return 0;
