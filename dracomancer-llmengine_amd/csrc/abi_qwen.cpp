@@ -121,9 +121,21 @@ struct PostNorm {
 // With `pend` (a pending residual, x + pend[0..n_in) + pend[n_in..2 n_in))
 // every matrix must be a K-quant (one launch): its prologue forms the sum,
 // normalises it and stores it to pend_sum.
+// With `gd` the K-quant launch also dots gd->n rows of gd->w0 and of gd->w1
+// ([n][n_in] fp32) with the normalised x into gd->out[0 .. 2n), when it can;
+// gd->done says whether it did.
+struct GateDots {
+    const float* w0;
+    const float* w1;
+    int n;
+    float* out;
+    bool done;
+};
+
 int enqueue_proj(const Proj* p, int n, const float* x, int n_in, const float* norm_w, float* xn,
                  hipStream_t st, const PostNorm* post = nullptr, const float* pend = nullptr,
-                 float* pend_sum = nullptr) {
+                 float* pend_sum = nullptr, GateDots* gd = nullptr) {
+    if (gd) gd->done = false;
     if (post && n != 1) return fail(-1, "enqueue_proj: post-norm needs one matrix");
     bool done[SEG_MAX] = {};
     if (n > SEG_MAX) return fail(-1, "enqueue_proj: %d matrices", n);
@@ -157,6 +169,12 @@ int enqueue_proj(const Proj* p, int n, const float* x, int n_in, const float* no
             s.am_val = const_cast<float*>(pend);
             s.xn_out = pend_sum;
         }
+        if (gd && f == 1 && norm_w && gd->out) {
+            s.gdot_w0 = gd->w0;
+            s.gdot_w1 = gd->w1;
+            s.gdot_out = gd->out;
+            s.gdot_n = gd->n;
+        }
         for (int j = i; j < n; j++) {
             if (done[j] || fam(p[j].m->L.code) != f) continue;
             SegDesc d = {};
@@ -169,6 +187,7 @@ int enqueue_proj(const Proj* p, int n, const float* x, int n_in, const float* no
             done[j] = true;
         }
         if (draco_seg_launch(s, st)) return fail(-1, "segment GEMV launch rejected");
+        if (gd && s.gdot_done) gd->done = true;
         if (pend) {
             for (int j = 0; j < n; j++)
                 if (!done[j]) return fail(-1, "enqueue_proj: a pending residual needs one launch");
@@ -228,6 +247,8 @@ struct GdnBufs {
     // residual into x2o
     const float* pend;
     float *pend_sum, *ks_out;
+    // nullable: [2 n_vh] for the gates' dots formed by the in-projection
+    float* glog;
 };
 
 int gdn_resolve(const GdnW* w, GdnDev& g) {
@@ -258,7 +279,7 @@ int gdn_resolve(const GdnW* w, GdnDev& g) {
 int gdn_bufs(const GdnDev& g, int slot, GdnBufs& b) {
     const size_t ns = (size_t)g.n_vh * QSV * QSV, nt = (size_t)g.n_qkv * 3;
     const size_t n = 5 * (size_t)QH + g.n_qkv + 2 * (size_t)g.d_in + ns + nt + (size_t)g.n_vh * GDN_PSS_STRIDE +
-                     16 * 64;  // + carve slack
+                     2 * (size_t)g.n_vh + 16 * 64;  // + carve slack
     float* p = (float*)scratch(slot, sizeof(float) * n);
     if (!p) return -2;
     auto take = [&](size_t k) {  // 256-byte aligned carve
@@ -276,6 +297,7 @@ int gdn_bufs(const GdnDev& g, int slot, GdnBufs& b) {
     b.S = take(ns);
     b.tail = take(nt);
     b.pss = take((size_t)g.n_vh * GDN_PSS_STRIDE);
+    b.glog = take(2 * (size_t)g.n_vh);
     b.pend = nullptr;
     b.pend_sum = nullptr;
     b.ks_out = nullptr;
@@ -286,7 +308,12 @@ int gdn_bufs(const GdnDev& g, int slot, GdnBufs& b) {
 // itself, or has none)
 int enqueue_gdn(const GdnDev& g, const GdnBufs& b, hipStream_t st, bool post_norm = true) {
     const Proj in[2] = {{g.qkv, b.qkv, nullptr}, {g.gate, b.z, nullptr}};
-    if (int rc = enqueue_proj(in, 2, b.h1, QH, g.attn_norm, b.xn, st, nullptr, b.pend, b.pend_sum)) return rc;
+    // the gates' dots (xn.beta_wt, xn.alpha_wt rows) ride on the in-projection
+    // when it is one K-quant launch with blocks to spare
+    GateDots gd = {g.bw, g.aw, g.n_vh, b.glog, false};
+    if (int rc = enqueue_proj(in, 2, b.h1, QH, g.attn_norm, b.xn, st, nullptr, b.pend, b.pend_sum,
+                              b.glog ? &gd : nullptr))
+        return rc;
     const float* h1 = b.pend ? b.pend_sum : b.h1;
     GdnArgs a = {};
     a.QKV = b.qkv;
@@ -307,6 +334,7 @@ int enqueue_gdn(const GdnDev& g, const GdnBufs& b, hipStream_t st, bool post_nor
     a.ssm_a = g.ssm_a;
     a.ssm_dt = g.ssm_dt;
     a.H = QH;
+    a.glog = b.glog && gd.done ? b.glog : nullptr;
     a.PSS = b.pss;
     // split over several blocks per V head only when the ssm_out GEMV can
     // take the gated rms into its prologue (Q4_K / Q6_K): the split's extra
@@ -656,6 +684,7 @@ struct QStack {
           *Qr = nullptr, *kraw = nullptr, *vraw = nullptr, *ao = nullptr, *part = nullptr, *fg = nullptr,
           *fu = nullptr, *xe = nullptr, *pss = nullptr;
     float *xs = nullptr, *pd = nullptr;  // pending residual: its materialised sum and the split-K partials [2][H]
+    float* glog = nullptr;               // GDN gates' dots [2][max_vh]
     int* state = nullptr;   // device [pos, told]
     int* hstate = nullptr;  // pinned
     // a prefill chunk of up to pf_cap tokens
@@ -827,7 +856,8 @@ QStack* build_qstack(const QStackLayer* layers, int n_layer, int h) {
         qstack_alloc(k, &s->part, (size_t)std::max(s->max_nh, 1) * nsplit * (FHD + 2)) ||
         qstack_alloc(k, &s->fg, std::max(s->max_ff, 1)) || qstack_alloc(k, &s->fu, std::max(s->max_ff, 1)) ||
         qstack_alloc(k, &s->pss, (size_t)std::max(s->max_vh, 1) * GDN_PSS_STRIDE) ||
-        qstack_alloc(k, &s->xs, QH) || qstack_alloc(k, &s->pd, 2 * QH))
+        qstack_alloc(k, &s->xs, QH) || qstack_alloc(k, &s->pd, 2 * QH) ||
+        qstack_alloc(k, &s->glog, 2 * (size_t)std::max(s->max_vh, 1)))
         return nullptr;
     if (hipMalloc(&s->state, sizeof(int) * 16) != hipSuccess ||
         hipHostMalloc(&s->hstate, sizeof(int) * 16, hipHostMallocDefault) != hipSuccess) {
@@ -930,6 +960,7 @@ int enqueue_qtoken(QStack* s, hipStream_t st, float* xin = nullptr) {
             b.S = q.S;
             b.tail = q.tail;
             b.pss = s->pss;
+            b.glog = s->glog;
             b.pend = pending ? s->pd : nullptr;
             b.pend_sum = pending ? alt : nullptr;
             b.ks_out = ks ? s->pd : nullptr;

@@ -26,6 +26,10 @@ struct GdnArgs {
     const float* ssm_a;      // [n_vh]
     const float* ssm_dt;     // [n_vh]
     int H;                   // <= 4096, multiple of 4
+    // nullable: the gates' two dots already formed ([n_vh] xn.beta_wt rows,
+    // then [n_vh] xn.alpha_wt rows, by the in-projection launch); the kernel
+    // then reads them instead of dotting h1 with bw / aw itself
+    const float* glog;
     // column split: nspl blocks per V head (1, 2, 4 or 8; 0 = 1).  Above 1
     // the gated rms runs in a second launch (or in the consumer) and needs
     // PSS [T][n_vh][GDN_PSS_STRIDE] floats (the waves' partial sums).

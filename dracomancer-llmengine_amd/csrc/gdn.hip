@@ -115,8 +115,13 @@ struct GdnGates {
             aacc += pre[2][q];
         }
         const float inv = 1.f / sqrtf(tot / (float)a.H + EPS);
-        *beta = 1.f / (1.f + expf(-(bacc * inv)));
-        const float avv = aacc * inv + a.ssm_dt[h];
+        gates_of(a, h, bacc * inv, aacc * inv, beta, gdec);
+    }
+    // beta = sigmoid(xn.bw), decay = exp(softplus(xn.aw + dt) * a) from the two dots
+    static __device__ __forceinline__ void gates_of(const GdnArgs& a, int h, float db, float da, float* beta,
+                                                    float* gdec) {
+        *beta = 1.f / (1.f + expf(-db));
+        const float avv = da + a.ssm_dt[h];
         const float sp = avv > 0.f ? avv + log1pf(expf(-avv)) : log1pf(expf(avv));
         *gdec = expf(sp * a.ssm_a[h]);
     }
@@ -142,7 +147,15 @@ __global__ __launch_bounds__(64 * NW) void k_gdn_scan(const GdnArgs a) {
     // decode: the gates' operands are requested first, then the conv inputs
     // and the state, so the gate arithmetic runs while the state arrives
     GdnGates<NW> gates;
-    if constexpr (DEC) gates.issue(a, h, tid);
+    float gdb = 0.f, gda = 0.f;  // the gates' dots when the in-projection formed them
+    if constexpr (DEC) {
+        if (a.glog) {
+            gdb = a.glog[h];
+            gda = a.glog[n_vh + h];
+        } else {
+            gates.issue(a, h, tid);
+        }
+    }
     // conv channels of this thread: local c = tid + r * NT; 0..127 q_j,
     // 128..255 k_j, 256.. v_h columns col0 ..
     int ch[R];
@@ -179,7 +192,8 @@ __global__ __launch_bounds__(64 * NW) void k_gdn_scan(const GdnArgs a) {
 
     float gin = 0.f, bin = 0.f;
     if constexpr (DEC) {
-        gates.finish(a, h, tid, &bin, &gin);
+        if (a.glog) GdnGates<NW>::gates_of(a, h, gdb, gda, &bin, &gin);
+        else gates.finish(a, h, tid, &bin, &gin);
     } else {
         gin = T > 0 ? a.G[h] : 0.f;
         bin = T > 0 ? a.B[h] : 0.f;

@@ -86,6 +86,20 @@ struct SegLaunch {
     const uint8_t* emb; // with emb_out set: the new token's row of emb (layout emb_L) -> emb_out
     DracoLayout emb_L;
     float* emb_out;
+    // Row dots riding on a normalising launch (do_norm 1 or 3, two or more
+    // Q4_K / Q6_K store or residual segments, no SwiGLU pair, not split-K,
+    // rows of 8 to 16 super-blocks): the last
+    // 2 gdot_n blocks of the grid each dot one fp32 row -- rows [0, gdot_n)
+    // of gdot_w0, then [0, gdot_n) of gdot_w1, n_in wide, contiguous -- with
+    // the normalised x (x * norm_w * 1/rms) into gdot_out[0 .. 2 gdot_n).
+    // draco_seg_launch sets gdot_done when the launch computed them (a
+    // launch that cannot -- too few blocks, n_in above 8 floats per thread,
+    // another epilogue -- leaves it 0 and the caller computes them itself).
+    const float* gdot_w0;
+    const float* gdot_w1;
+    float* gdot_out;
+    int gdot_n;
+    int gdot_done;
 };
 
 // Builds grid ranges for every segment and launches the fused kernel.

@@ -84,6 +84,10 @@ struct SegKArgs {
     int nseg, total_tiles, n_in, do_norm;
     float eps;
     int layer, head_dim, rot, kv_dim;
+    // row dots (SegLaunch.gdot_*): launches that carry them have no rope or
+    // KV epilogue and no GNORM prologue, so their rows ride in rope_tab (w0)
+    // and kc (w1) and the dots go to vc (the argument block stays 368 bytes)
+    int gdot;
 };
 
 SegKArgs seg_kargs(const SegLaunch& a, bool q80) {
@@ -122,6 +126,12 @@ SegKArgs seg_kargs(const SegLaunch& a, bool q80) {
     k.head_dim = a.head_dim;
     k.rot = a.rot;
     k.kv_dim = a.kv_dim;
+    if (!q80 && a.gdot_done) {
+        k.rope_tab = a.gdot_w0;
+        k.kc = const_cast<float*>(a.gdot_w1);
+        k.vc = a.gdot_out;
+        k.gdot = a.gdot_n;
+    }
     return k;
 }
 
@@ -158,7 +168,8 @@ __device__ __forceinline__ auto seg_pick(const SegKArgs& a, int si, F f) -> decl
 // [0, a.rot) multiply the first half of every row's super-blocks and store
 // to y, tiles [a.rot, 2 a.rot) the second half and store to y + a.kv_dim.
 constexpr int EPI_RT = -1, EPI_QKV = -2;
-template <int NW, int FM, bool DUAL, bool MULTI, int EPI, int NORM, bool IPT1, bool KS = false>
+// GD: the launch carries row dots (a.gdot, RMSNorm prologues only).
+template <int NW, int FM, bool DUAL, bool MULTI, int EPI, int NORM, bool IPT1, bool KS = false, bool GD = false>
 __global__ __launch_bounds__(64 * NW) void k_dq(const SegKArgs a) {
     extern __shared__ __align__(16) uint8_t smem[];
     constexpr int NT = 64 * NW;
@@ -235,6 +246,23 @@ __global__ __launch_bounds__(64 * NW) void k_dq(const SegKArgs a) {
             }
         }
     }
+    // row dots (GD): block G - 2 a.gdot + r dots row r of [w0; w1] with the
+    // normalised x, up to 2 float4 per thread.  Every block loads (the other
+    // blocks re-read row 0, an L2 hit): a load under a block-dependent
+    // branch leaves the wait-count analysis no choice but to wait for it
+    // before the first weights are used.
+    static_assert(!GD || NORM == 1 || NORM == 3, "row dots ride on the RMSNorm prologue");
+    const int gr = GD ? bx - (G - 2 * a.gdot) : -1;
+    float4 gv[2];
+    if constexpr (GD) {
+        const int r = gr >= 0 ? gr : 0;
+        const float* row = r < a.gdot ? a.rope_tab + (size_t)r * n_in : a.kc + (size_t)(r - a.gdot) * n_in;
+#pragma unroll
+        for (int q = 0; q < 2; q++) {
+            const int i4 = tid + q * NT;
+            if (i4 < n4) gv[q] = ld4(row + 4 * i4);
+        }
+    }
     Frag P0, P1, Q0, Q1;
     // Load cursor (one item ahead of the compute cursor).  Loads are issued
     // unconditionally: a padding item or a load past the wave's last item
@@ -280,7 +308,8 @@ __global__ __launch_bounds__(64 * NW) void k_dq(const SegKArgs a) {
     // instead of two; the result differs from dotting (x*inv)*w only by fp32
     // rounding.
     float* ssp = red + 2 * NW * 16;  // [NW] per-wave sums of squares
-    float ss = 0.f;
+    float* gsp = ssp + NW;           // [NW] per-wave row-dot partials
+    float ss = 0.f, gp = 0.f;
 #pragma unroll
     for (int q = 0; q < XP_MAXV; q++) {
         const int i4 = tid + q * NT;
@@ -313,12 +342,23 @@ __global__ __launch_bounds__(64 * NW) void k_dq(const SegKArgs a) {
                 const float4 nw = wv[q];
                 v.x *= nw.x; v.y *= nw.y; v.z *= nw.z; v.w *= nw.w;
             }
+            if (GD && q < 2) {
+                const float4 r = gv[q < 2 ? q : 0];
+                gp = fmaf(v.x, r.x, gp);
+                gp = fmaf(v.y, r.y, gp);
+                gp = fmaf(v.z, r.z, gp);
+                gp = fmaf(v.w, r.w, gp);
+            }
         }
         digits4(v, i4, xd, xsm);
     }
     if (NORM == 1 || NORM == 3) {
         ss = wave_sum(ss);
-        if (lane == 0) ssp[w] = ss;
+        if (GD && gr >= 0) gp = wave_sum(gp);
+        if (lane == 0) {
+            ssp[w] = ss;
+            if (GD) gsp[w] = gp;
+        }
         lds_barrier();
     } else {
         // Wave w digitizes exactly the super-blocks it multiplies (float4 i4 =
@@ -337,6 +377,12 @@ __global__ __launch_bounds__(64 * NW) void k_dq(const SegKArgs a) {
 #pragma unroll
         for (int i = 0; i < NW; i++) tot += ssp[i];
         inv = 1.f / sqrtf(tot / (float)n_in + a.eps);
+        if (GD && gr >= 0 && tid == 0) {
+            float d = 0.f;
+#pragma unroll
+            for (int i = 0; i < NW; i++) d += gsp[i];
+            a.vc[gr] = d * inv;
+        }
         if (NORM == 1 && a.xn_out && bx == 0) {
 #pragma unroll
             for (int q = 0; q < XP_MAXV; q++) {
@@ -811,18 +857,33 @@ int cu_count() {
     return n;
 }
 
-size_t dq_lds_bytes(int n_in, int nw) { return (size_t)(n_in / 16) * 72 + 1024 + (size_t)2 * nw * 16 * 4 + (size_t)nw * 4; }
+size_t dq_lds_bytes(int n_in, int nw) { return (size_t)(n_in / 16) * 72 + 1024 + (size_t)2 * nw * 16 * 4 + (size_t)nw * 8; }
 
-template <int NW, int FM, bool DUAL, bool MULTI, int EPI, int NORM, bool IPT1, bool KS = false>
+template <int NW, int FM, bool DUAL, bool MULTI, int EPI, int NORM, bool IPT1, bool KS = false, bool GD = false>
 void launch_dq1(SegLaunch& a, int grid, hipStream_t st) {
     static std::once_flag once;
     std::call_once(once, [] {
         // allow LDS beyond 64 KB for long rows (n_in up to 16384 needs ~74 KB)
-        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&k_dq<NW, FM, DUAL, MULTI, EPI, NORM, IPT1, KS>),
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+        (void)hipFuncSetAttribute(
+            reinterpret_cast<const void*>(&k_dq<NW, FM, DUAL, MULTI, EPI, NORM, IPT1, KS, GD>),
+            hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
     });
-    hipLaunchKernelGGL((k_dq<NW, FM, DUAL, MULTI, EPI, NORM, IPT1, KS>), dim3(grid), dim3(64 * NW),
+    hipLaunchKernelGGL((k_dq<NW, FM, DUAL, MULTI, EPI, NORM, IPT1, KS, GD>), dim3(grid), dim3(64 * NW),
                        dq_lds_bytes(a.n_in, NW), st, seg_kargs(a, false));
+}
+
+// launches carrying row dots: 8 waves, several store / residual segments
+template <int FM, int NORM>
+void launch_dq_gd1(SegLaunch& a, int grid, hipStream_t st) {
+    if ((a.n_in >> 8) <= 8) launch_dq1<8, FM, false, true, EPI_RT, NORM, true, false, true>(a, grid, st);
+    else launch_dq1<8, FM, false, true, EPI_RT, NORM, false, false, true>(a, grid, st);
+}
+
+template <int NORM>
+void launch_dq_gd(SegLaunch& a, int fm, int grid, hipStream_t st) {
+    if (fm == 1) launch_dq_gd1<1, NORM>(a, grid, st);
+    else if (fm == 2) launch_dq_gd1<2, NORM>(a, grid, st);
+    else launch_dq_gd1<3, NORM>(a, grid, st);
 }
 
 template <int NW, int FM, bool DUAL, bool MULTI, int EPI, int NORM>
@@ -952,6 +1013,13 @@ int seg_launch_dq(SegLaunch& a, hipStream_t st) {
     // with fewer tiles than that keep one per block (halving the qkv or wo
     // grid was slower: 2108 -> 1917 / 1821 tok/s).
     if (nb <= nw && tiles >= 2 * cu_count() && tiles <= cap) grid = (tiles + 1) / 2;
+    a.gdot_done = 0;
+    if (a.gdot_n > 0 && !a.ksplit && !dual && a.nseg >= 2 && nw == 8 && (a.do_norm == 1 || a.do_norm == 3) &&
+        a.gdot_w0 && a.gdot_w1 && a.gdot_out && grid >= 2 * a.gdot_n && n_in <= 8 * 64 * nw) {
+        bool ok = true;
+        for (int i = 0; i < a.nseg; i++) ok = ok && (a.seg[i].epi == EPI_STORE || a.seg[i].epi == EPI_RESID);
+        a.gdot_done = ok ? 1 : 0;
+    }
     if (a.ksplit) {
         // tiles [0, tiles) take each row's first half, [tiles, 2 tiles) the second
         a.rot = tiles;
@@ -969,6 +1037,11 @@ int seg_launch_dq(SegLaunch& a, hipStream_t st) {
         return 0;
     }
     if (grid <= 0) return 0;
+    if (a.gdot_done) {
+        if (a.do_norm == 3) launch_dq_gd<3>(a, fm, grid, st);
+        else launch_dq_gd<1>(a, fm, grid, st);
+        return 0;
+    }
     if (nw == 4) launch_dq_nw<4>(a, fm, dual, grid, st);
     else if (nw == 8) launch_dq_nw<8>(a, fm, dual, grid, st);
     else launch_dq_nw<16>(a, fm, dual, grid, st);
