@@ -587,50 +587,21 @@ struct FQ80 {
     }
 };
 
-// R row dots of one wave (plus the same rows of a second matrix when DUAL).
-// The wave's lanes cover (row, block) pairs p = i * U + u, so rows of fewer
+// Fused segment kernel for Q8_0 (one instantiation per dual mode, preload
+// depth NP and RMSNorm prologue).  A wave owns SEG_R rows; its lanes cover (row, block)
+// pairs p = i * U + u (U blocks per row) in passes of 64, so rows of fewer
 // than 64 blocks still occupy every lane (SmolLM2's 960-wide rows are 30
-// blocks: two rows per pass instead of 30 of 64 lanes); each lane adds its
-// pair's dot to its row's accumulator, and the caller sums the lanes.  The
-// first pass's weights (w0, w02) were requested by the caller before the x
-// prologue (first_pair).
-template <class F, int R>
-__device__ __forceinline__ bool first_pair(const SegK& s, int r0, int& i, int& u) {
-    const int lane = threadIdx.x & 63, U = s.nb * F::UPB;
-    i = lane / U;
-    u = lane - i * U;
-    return lane < R * U && r0 + i < s.n_out;
-}
-
-template <class F, int R, bool DUAL>
-__device__ __forceinline__ void rows_dot(const SegK& s, const SegK& s2, const float* xs, int r0, float* acc,
-                                         const typename F::W& w0, const typename F::W& w02) {
-    const int lane = threadIdx.x & 63;
-    const int U = s.nb * F::UPB;
-    const int n_out = s.n_out;
-    for (int p = lane; p < R * U; p += 64) {
-        const int i = p / U, u = p - i * U;
-        float xv[F::NX], sx[F::NS];
-        F::xslice(xs, u, xv, sx);
-        if (r0 + i < n_out) {
-            const bool first = p == lane;
-            const float d = F::dotw(first ? w0 : F::load(s, r0 + i, u), xv, sx);
-            const float d2 = DUAL ? F::dotw(first ? w02 : F::load(s2, r0 + i, u), xv, sx) : 0.f;
-#pragma unroll
-            for (int k = 0; k < R; k++)
-                if (k == i) {
-                    acc[k] += d;
-                    if (DUAL) acc[R + k] += d2;
-                }
-        }
-    }
-}
-
-
-// Fused segment kernel for Q8_0 (one instantiation per dual mode).
-template <class F, bool DUAL>
+// blocks: two rows per pass instead of 30 of 64 lanes).  Each lane adds its
+// pair's dot to its row's accumulator in pass order, and the wave sums the
+// lanes.  Latency: the weights of the first NP passes are requested first
+// (pairs past the end re-read the last real pair, rows past the end the last
+// row, so every load is unconditional and in bounds), then x with all of a
+// thread's float4s in flight together, staged in LDS (RMS-normalised when
+// do_norm) behind LDS-only barriers; one memory round trip before the first
+// dot.  Passes beyond NP load one pass ahead.
+template <class F, bool DUAL, int NP, bool NORM>
 __global__ __launch_bounds__(256) void k_seg(const SegKArgs a) {
-    extern __shared__ float xsh[];
+    extern __shared__ float xsh[];  // the block's x, n_in floats (normalised when do_norm)
     __shared__ float red[4];
     __shared__ float amv[4 * SEG_R];
     __shared__ int ami[4 * SEG_R];
@@ -641,48 +612,120 @@ __global__ __launch_bounds__(256) void k_seg(const SegKArgs a) {
     const SegK& s = a.seg[si];
     const SegK& s2 = a.seg[DUAL ? si + 1 : si];
     const int r0 = ((int)blockIdx.x - s.first) * SEG_ROWS + wv * SEG_R;
-
-    // this lane's first (row, block) weights, requested before the x prologue
-    typename F::W w0 = {}, w02 = {};
-    {
-        int i0, u0;
-        if (first_pair<F, SEG_R>(s, r0, i0, u0)) {
-            w0 = F::load(s, r0 + i0, u0);
-            if (DUAL) w02 = F::load(s2, r0 + i0, u0);
-        }
+    const int n_out = s.n_out, U = s.nb * F::UPB, npair = SEG_R * U, passes = (npair + 63) / 64;
+    // pass k of this lane: row index i within the wave's rows, block u; live
+    // when the pair exists and its row is in range
+    auto pair = [&](int k, int& i, int& u) {
+        const int p0 = lane + 64 * k;
+        const int p = p0 < npair ? p0 : npair - 1;
+        i = p / U;
+        u = p - i * U;
+        return p0 < npair && r0 + i < n_out;
+    };
+    auto row_of = [&](int i) { return r0 + i < n_out ? r0 + i : n_out - 1; };
+    typename F::W wa[NP], wb[NP];
+#pragma unroll
+    for (int k = 0; k < NP; k++) {
+        int i, u;
+        pair(k, i, u);
+        wa[k] = F::load(s, row_of(i), u);
+        if (DUAL) wb[k] = F::load(s2, row_of(i), u);
     }
 
-    // prologue: RMSNorm of x into LDS (every block; same order -> same result)
-    const float* xs = a.x;
-    if (a.do_norm) {
-        float ss = 0.f;
-        for (int i = tid; i < a.n_in; i += 256) {
-            const float v = a.x[i];
-            xsh[i] = v;
-            ss = fmaf(v, v, ss);
+    // prologue: x into LDS, RMS-normalised when NORM (every block, same
+    // order -> same result): (x * 1/rms) * w.  The first XB float4s of every
+    // thread (n_in <= 4096) are requested together and unconditionally
+    // (clamped index; a null norm weight re-reads x), so the wait for them
+    // does not wait for the weights; longer rows take further batches.
+    const int n4 = a.n_in >> 2;
+    constexpr int XB = 4;  // float4s per thread per batch
+    const float* nwp = a.norm_w ? a.norm_w : a.x;
+    float4 xv[XB], nv[XB];
+#pragma unroll
+    for (int q = 0; q < XB; q++) {
+        const int i4 = tid + q * 256, ic = i4 < n4 ? i4 : n4 - 1;
+        xv[q] = ld4(a.x + 4 * ic);
+        if (NORM) nv[q] = ld4(nwp + 4 * ic);
+    }
+    float ss = 0.f;
+    auto stage = [&](int i4, const float4 v) {
+        *reinterpret_cast<float4*>(xsh + 4 * i4) = v;
+        if (NORM) {
+            ss = fmaf(v.x, v.x, ss);
+            ss = fmaf(v.y, v.y, ss);
+            ss = fmaf(v.z, v.z, ss);
+            ss = fmaf(v.w, v.w, ss);
         }
+    };
+#pragma unroll
+    for (int q = 0; q < XB; q++)
+        if (tid + q * 256 < n4) stage(tid + q * 256, xv[q]);
+    for (int i4 = tid + XB * 256; i4 < n4; i4 += 256) stage(i4, ld4(a.x + 4 * i4));
+    if (NORM) {
         ss = wave_sum(ss);
         if (lane == 0) red[wv] = ss;
         lds_barrier();  // LDS only: the weight loads above stay in flight
         const float tot = (red[0] + red[1]) + (red[2] + red[3]);
         const float inv = 1.f / sqrtf(tot / (float)a.n_in + a.eps);
-        for (int i = tid; i < a.n_in; i += 256) {
-            const float v = a.norm_w ? xsh[i] * inv * a.norm_w[i] : xsh[i] * inv;
-            xsh[i] = v;
-            if (a.xn_out && blockIdx.x == 0) a.xn_out[i] = v;
-        }
-        lds_barrier();
-        xs = xsh;
+        // each thread rescales the float4s it staged
+        auto scale = [&](int i4, const float4 w) {
+            float4 v = *reinterpret_cast<const float4*>(xsh + 4 * i4);
+            if (a.norm_w) {
+                v.x = v.x * inv * w.x; v.y = v.y * inv * w.y; v.z = v.z * inv * w.z; v.w = v.w * inv * w.w;
+            } else {
+                v.x *= inv; v.y *= inv; v.z *= inv; v.w *= inv;
+            }
+            *reinterpret_cast<float4*>(xsh + 4 * i4) = v;
+            if (a.xn_out && blockIdx.x == 0) *reinterpret_cast<float4*>(a.xn_out + 4 * i4) = v;
+        };
+#pragma unroll
+        for (int q = 0; q < XB; q++)
+            if (tid + q * 256 < n4) scale(tid + q * 256, nv[q]);
+        for (int i4 = tid + XB * 256; i4 < n4; i4 += 256) scale(i4, ld4(nwp + 4 * i4));
     }
+    lds_barrier();
 
     float acc[2 * SEG_R];
 #pragma unroll
     for (int i = 0; i < 2 * SEG_R; i++) acc[i] = 0.f;
-    rows_dot<F, SEG_R, DUAL>(s, s2, xs, r0, acc, w0, w02);
+    auto dot_pass = [&](int k, const typename F::W& w, const typename F::W& w2) {
+        int i, u;
+        const bool live = pair(k, i, u);
+        float xv[F::NX], sx[F::NS];
+        F::xslice(xsh, u, xv, sx);
+        const float d = F::dotw(w, xv, sx);
+        const float d2 = DUAL ? F::dotw(w2, xv, sx) : 0.f;
+#pragma unroll
+        for (int r = 0; r < SEG_R; r++)
+            if (live && r == i) {
+                acc[r] += d;
+                if (DUAL) acc[SEG_R + r] += d2;
+            }
+    };
+#pragma unroll
+    for (int k = 0; k < NP; k++)
+        if (k < passes) dot_pass(k, wa[k], wb[k]);
+    if (passes > NP) {
+        typename F::W c = wa[0], c2 = wb[0];
+        {
+            int i, u;
+            pair(NP, i, u);
+            c = F::load(s, row_of(i), u);
+            if (DUAL) c2 = F::load(s2, row_of(i), u);
+        }
+        for (int k = NP; k < passes; k++) {
+            int i, u;
+            pair(k + 1, i, u);  // clamped: past the last pass it re-reads a real pair
+            const typename F::W n = F::load(s, row_of(i), u);
+            const typename F::W n2 = DUAL ? F::load(s2, row_of(i), u) : n;
+            dot_pass(k, c, c2);
+            c = n;
+            c2 = n2;
+        }
+    }
 #pragma unroll
     for (int i = 0; i < (DUAL ? 2 : 1) * SEG_R; i++) acc[i] = wave_sum(acc[i]);
 
-    const int n_out = s.n_out;
     switch (s.epi) {
     case EPI_STORE:
     case EPI_ARGMAX:
@@ -1052,6 +1095,23 @@ int seg_launch_dq(SegLaunch& a, hipStream_t st) {
     return 0;
 }
 
+template <bool DUAL, int NP, bool NORM>
+void launch_seg1(dim3 g, size_t shm, hipStream_t st, const SegKArgs& k) {
+    static std::once_flag once;
+    std::call_once(once, [] {
+        // 128 KB of x (the kernel's static LDS and this stay below the CU's 160 KB)
+        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&k_seg<FQ80, DUAL, NP, NORM>),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, 128 * 1024);
+    });
+    hipLaunchKernelGGL((k_seg<FQ80, DUAL, NP, NORM>), g, dim3(256), shm, st, k);
+}
+
+template <bool DUAL, int NP>
+void launch_seg(dim3 g, size_t shm, hipStream_t st, const SegKArgs& k) {
+    if (k.do_norm) launch_seg1<DUAL, NP, true>(g, shm, st, k);
+    else launch_seg1<DUAL, NP, false>(g, shm, st, k);
+}
+
 // Q8_0 segments (k_seg).
 int seg_launch_q8(SegLaunch& a, hipStream_t st) {
     int blocks = 0;
@@ -1077,11 +1137,21 @@ int seg_launch_q8(SegLaunch& a, hipStream_t st) {
     bool dual = false;
     for (int i = 0; i < a.nseg; i++) dual = dual || a.seg[i].epi == EPI_SWIGLU;
     if (dual && a.nseg != 2) return -1;
-    const size_t shm = a.do_norm ? sizeof(float) * (size_t)a.n_in : 0;
+    // x is staged in LDS: up to 32768 floats (128 KB, above the default 64 KB)
+    if (a.n_in % 32 || a.n_in > 32768) return -1;
+    const size_t shm = sizeof(float) * (size_t)a.n_in;
     const dim3 g(blocks), b(256);
     const SegKArgs k = seg_kargs(a, true);
-    if (dual) hipLaunchKernelGGL((k_seg<FQ80, true>), g, b, shm, st, k);
-    else hipLaunchKernelGGL((k_seg<FQ80, false>), g, b, shm, st, k);
+    // passes of 64 (row, block) pairs per wave; the first NP preloaded
+    const int passes = (SEG_R * (a.n_in / 32) + 63) / 64;
+    if (dual) {
+        if (passes <= 1) launch_seg<true, 1>(g, shm, st, k);
+        else launch_seg<true, 2>(g, shm, st, k);
+    } else {
+        if (passes <= 1) launch_seg<false, 1>(g, shm, st, k);
+        else if (passes <= 2) launch_seg<false, 2>(g, shm, st, k);
+        else launch_seg<false, 4>(g, shm, st, k);
+    }
     if (a.seg[0].epi == EPI_ARGMAX)
         hipLaunchKernelGGL(k_argmax_finalize, dim3(finalize_blocks(a.emb_out, a.emb_L.n_in)), dim3(256), 0, st, a.am_val, a.am_idx, a.seg[0].n_blocks,
                            a.tokens, const_cast<int*>(a.cursor), a.advance_state, a.advance_layers, a.emb, a.emb_L,
