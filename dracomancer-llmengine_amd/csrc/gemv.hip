@@ -49,8 +49,7 @@
 
 namespace {
 
-constexpr int SEG_R = 2;                  // rows per wave in k_seg (Q8_0)
-constexpr int SEG_ROWS = 4 * SEG_R;       // rows per block (4 waves)
+constexpr int SEG_R = 2;                  // rows per wave in k_seg (Q8_0; 1 for wide rows without rope or norm)
 constexpr int XP_MAXV = 4;                // float4s of x per thread held by the prologue
 
 // ------------------------------------------------------- kernel arguments --
@@ -588,7 +587,9 @@ struct FQ80 {
 };
 
 // Fused segment kernel for Q8_0 (one instantiation per dual mode, preload
-// depth NP and RMSNorm prologue).  A wave owns SEG_R rows; its lanes cover (row, block)
+// depth NP, RMSNorm prologue and rows per wave R).  A wave owns R rows (2:
+// the rope epilogue's pairs, and short rows fill the wave; 1 for rows wider
+// than 32 blocks without rope, so each wave runs half the passes); its lanes cover (row, block)
 // pairs p = i * U + u (U blocks per row) in passes of 64, so rows of fewer
 // than 64 blocks still occupy every lane (SmolLM2's 960-wide rows are 30
 // blocks: two rows per pass instead of 30 of 64 lanes).  Each lane adds its
@@ -599,20 +600,20 @@ struct FQ80 {
 // thread's float4s in flight together, staged in LDS (RMS-normalised when
 // do_norm) behind LDS-only barriers; one memory round trip before the first
 // dot.  Passes beyond NP load one pass ahead.
-template <class F, bool DUAL, int NP, bool NORM>
+template <class F, bool DUAL, int NP, bool NORM, int R>
 __global__ __launch_bounds__(256) void k_seg(const SegKArgs a) {
     extern __shared__ float xsh[];  // the block's x, n_in floats (normalised when do_norm)
     __shared__ float red[4];
-    __shared__ float amv[4 * SEG_R];
-    __shared__ int ami[4 * SEG_R];
+    __shared__ float amv[4 * R];
+    __shared__ int ami[4 * R];
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     int si = 0;
     for (int i = 1; i < a.nseg; i++)
         if ((int)blockIdx.x >= a.seg[i].first) si = i;
     const SegK& s = a.seg[si];
     const SegK& s2 = a.seg[DUAL ? si + 1 : si];
-    const int r0 = ((int)blockIdx.x - s.first) * SEG_ROWS + wv * SEG_R;
-    const int n_out = s.n_out, U = s.nb * F::UPB, npair = SEG_R * U, passes = (npair + 63) / 64;
+    const int r0 = ((int)blockIdx.x - s.first) * (4 * R) + wv * R;
+    const int n_out = s.n_out, U = s.nb * F::UPB, npair = R * U, passes = (npair + 63) / 64;
     // pass k of this lane: row index i within the wave's rows, block u; live
     // when the pair exists and its row is in range
     auto pair = [&](int k, int& i, int& u) {
@@ -632,11 +633,14 @@ __global__ __launch_bounds__(256) void k_seg(const SegKArgs a) {
         if (DUAL) wb[k] = F::load(s2, row_of(i), u);
     }
 
-    // prologue: x into LDS, RMS-normalised when NORM (every block, same
-    // order -> same result): (x * 1/rms) * w.  The first XB float4s of every
-    // thread (n_in <= 4096) are requested together and unconditionally
-    // (clamped index; a null norm weight re-reads x), so the wait for them
-    // does not wait for the weights; longer rows take further batches.
+    // prologue: x into LDS, every block the same way.  With the RMSNorm the
+    // block stages x * w and reduces the sum of squares of x through the same
+    // LDS-only barrier; 1/rms multiplies every finished row dot (one barrier
+    // instead of two; the result differs from dotting (x / rms) * w by fp32
+    // rounding only).  The first XB float4s of every thread (n_in <= 4096)
+    // are requested together and unconditionally (clamped index; a null norm
+    // weight re-reads x), so the wait for them does not wait for the
+    // weights; longer rows take further batches.
     const int n4 = a.n_in >> 2;
     constexpr int XB = 4;  // float4s per thread per batch
     const float* nwp = a.norm_w ? a.norm_w : a.x;
@@ -648,46 +652,50 @@ __global__ __launch_bounds__(256) void k_seg(const SegKArgs a) {
         if (NORM) nv[q] = ld4(nwp + 4 * ic);
     }
     float ss = 0.f;
-    auto stage = [&](int i4, const float4 v) {
-        *reinterpret_cast<float4*>(xsh + 4 * i4) = v;
+    auto stage = [&](int i4, float4 v, const float4 w) {
         if (NORM) {
             ss = fmaf(v.x, v.x, ss);
             ss = fmaf(v.y, v.y, ss);
             ss = fmaf(v.z, v.z, ss);
             ss = fmaf(v.w, v.w, ss);
+            if (a.norm_w) {
+                v.x *= w.x; v.y *= w.y; v.z *= w.z; v.w *= w.w;
+            }
         }
+        *reinterpret_cast<float4*>(xsh + 4 * i4) = v;
     };
 #pragma unroll
     for (int q = 0; q < XB; q++)
-        if (tid + q * 256 < n4) stage(tid + q * 256, xv[q]);
-    for (int i4 = tid + XB * 256; i4 < n4; i4 += 256) stage(i4, ld4(a.x + 4 * i4));
+        if (tid + q * 256 < n4) stage(tid + q * 256, xv[q], nv[q]);
+    for (int i4 = tid + XB * 256; i4 < n4; i4 += 256) stage(i4, ld4(a.x + 4 * i4), NORM ? ld4(nwp + 4 * i4) : xv[0]);
+    float inv = 1.f;
     if (NORM) {
         ss = wave_sum(ss);
         if (lane == 0) red[wv] = ss;
-        lds_barrier();  // LDS only: the weight loads above stay in flight
-        const float tot = (red[0] + red[1]) + (red[2] + red[3]);
-        const float inv = 1.f / sqrtf(tot / (float)a.n_in + a.eps);
-        // each thread rescales the float4s it staged
-        auto scale = [&](int i4, const float4 w) {
-            float4 v = *reinterpret_cast<const float4*>(xsh + 4 * i4);
-            if (a.norm_w) {
-                v.x = v.x * inv * w.x; v.y = v.y * inv * w.y; v.z = v.z * inv * w.z; v.w = v.w * inv * w.w;
-            } else {
-                v.x *= inv; v.y *= inv; v.z *= inv; v.w *= inv;
-            }
-            *reinterpret_cast<float4*>(xsh + 4 * i4) = v;
-            if (a.xn_out && blockIdx.x == 0) *reinterpret_cast<float4*>(a.xn_out + 4 * i4) = v;
-        };
-#pragma unroll
-        for (int q = 0; q < XB; q++)
-            if (tid + q * 256 < n4) scale(tid + q * 256, nv[q]);
-        for (int i4 = tid + XB * 256; i4 < n4; i4 += 256) scale(i4, ld4(nwp + 4 * i4));
     }
-    lds_barrier();
-
-    float acc[2 * SEG_R];
+    lds_barrier();  // LDS only: the weight loads above stay in flight
+    if (NORM) {
+        const float tot = (red[0] + red[1]) + (red[2] + red[3]);
+        inv = 1.f / sqrtf(tot / (float)a.n_in + a.eps);
+        if (a.xn_out && blockIdx.x == 0) {  // the normalised x, (x / rms) * w as the reference
+            auto put = [&](int i4, float4 v, const float4 w) {
+                if (a.norm_w) {
+                    v.x = v.x * inv * w.x; v.y = v.y * inv * w.y; v.z = v.z * inv * w.z; v.w = v.w * inv * w.w;
+                } else {
+                    v.x *= inv; v.y *= inv; v.z *= inv; v.w *= inv;
+                }
+                *reinterpret_cast<float4*>(a.xn_out + 4 * i4) = v;
+            };
 #pragma unroll
-    for (int i = 0; i < 2 * SEG_R; i++) acc[i] = 0.f;
+            for (int q = 0; q < XB; q++)
+                if (tid + q * 256 < n4) put(tid + q * 256, xv[q], nv[q]);
+            for (int i4 = tid + XB * 256; i4 < n4; i4 += 256) put(i4, ld4(a.x + 4 * i4), ld4(nwp + 4 * i4));
+        }
+    }
+
+    float acc[2 * R];
+#pragma unroll
+    for (int i = 0; i < 2 * R; i++) acc[i] = 0.f;
     auto dot_pass = [&](int k, const typename F::W& w, const typename F::W& w2) {
         int i, u;
         const bool live = pair(k, i, u);
@@ -696,10 +704,10 @@ __global__ __launch_bounds__(256) void k_seg(const SegKArgs a) {
         const float d = F::dotw(w, xv, sx);
         const float d2 = DUAL ? F::dotw(w2, xv, sx) : 0.f;
 #pragma unroll
-        for (int r = 0; r < SEG_R; r++)
+        for (int r = 0; r < R; r++)
             if (live && r == i) {
                 acc[r] += d;
-                if (DUAL) acc[SEG_R + r] += d2;
+                if (DUAL) acc[R + r] += d2;
             }
     };
 #pragma unroll
@@ -724,26 +732,26 @@ __global__ __launch_bounds__(256) void k_seg(const SegKArgs a) {
         }
     }
 #pragma unroll
-    for (int i = 0; i < (DUAL ? 2 : 1) * SEG_R; i++) acc[i] = wave_sum(acc[i]);
+    for (int i = 0; i < (DUAL ? 2 : 1) * R; i++) acc[i] = wave_sum(acc[i]) * inv;
 
     switch (s.epi) {
     case EPI_STORE:
     case EPI_ARGMAX:
         if (lane == 0)
-            for (int i = 0; i < SEG_R; i++)
+            for (int i = 0; i < R; i++)
                 if (r0 + i < n_out) s.y[r0 + i] = acc[i];
         break;
     case EPI_RESID:
         if (lane == 0)
-            for (int i = 0; i < SEG_R; i++)
+            for (int i = 0; i < R; i++)
                 if (r0 + i < n_out) s.y[r0 + i] = s.yadd[r0 + i] + acc[i];
         break;
     case EPI_SWIGLU:
         if (lane == 0)
-            for (int i = 0; i < SEG_R; i++)
+            for (int i = 0; i < R; i++)
                 if (r0 + i < n_out) {
                     const float g = acc[i];
-                    s.y[r0 + i] = (g / (1.f + expf(-g))) * acc[SEG_R + i];
+                    s.y[r0 + i] = (g / (1.f + expf(-g))) * acc[R + i];
                 }
         break;
     case EPI_ROPE_Q:
@@ -773,7 +781,7 @@ __global__ __launch_bounds__(256) void k_seg(const SegKArgs a) {
     case EPI_V_APPEND:
         if (lane == 0) {
             float* dst = a.vc + (size_t)a.state[1 + a.layer] * a.kv_dim;
-            for (int i = 0; i < SEG_R; i++)
+            for (int i = 0; i < R; i++)
                 if (r0 + i < n_out) dst[r0 + i] = acc[i];
         }
         break;
@@ -784,15 +792,15 @@ __global__ __launch_bounds__(256) void k_seg(const SegKArgs a) {
     if (s.epi != EPI_ARGMAX) return;
     // per-block argmax partial; k_argmax_finalize (next launch) reduces them
     if (lane == 0)
-        for (int i = 0; i < SEG_R; i++) {
-            amv[wv * SEG_R + i] = (r0 + i < n_out) ? acc[i] : -INFINITY;
-            ami[wv * SEG_R + i] = (r0 + i < n_out) ? r0 + i : 0x7fffffff;
+        for (int i = 0; i < R; i++) {
+            amv[wv * R + i] = (r0 + i < n_out) ? acc[i] : -INFINITY;
+            ami[wv * R + i] = (r0 + i < n_out) ? r0 + i : 0x7fffffff;
         }
     __syncthreads();
     if (tid == 0) {
         float v = amv[0];
         int idx = ami[0];
-        for (int i = 1; i < 4 * SEG_R; i++) am_merge(v, idx, amv[i], ami[i]);
+        for (int i = 1; i < 4 * R; i++) am_merge(v, idx, amv[i], ami[i]);
         const int bi = (int)blockIdx.x - s.first;
         a.am_val[bi] = v;
         a.am_idx[bi] = idx;
@@ -1095,15 +1103,15 @@ int seg_launch_dq(SegLaunch& a, hipStream_t st) {
     return 0;
 }
 
-template <bool DUAL, int NP, bool NORM>
+template <bool DUAL, int NP, bool NORM, int R = SEG_R>
 void launch_seg1(dim3 g, size_t shm, hipStream_t st, const SegKArgs& k) {
     static std::once_flag once;
     std::call_once(once, [] {
         // 128 KB of x (the kernel's static LDS and this stay below the CU's 160 KB)
-        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&k_seg<FQ80, DUAL, NP, NORM>),
+        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&k_seg<FQ80, DUAL, NP, NORM, R>),
                                   hipFuncAttributeMaxDynamicSharedMemorySize, 128 * 1024);
     });
-    hipLaunchKernelGGL((k_seg<FQ80, DUAL, NP, NORM>), g, dim3(256), shm, st, k);
+    hipLaunchKernelGGL((k_seg<FQ80, DUAL, NP, NORM, R>), g, dim3(256), shm, st, k);
 }
 
 template <bool DUAL, int NP>
@@ -1114,13 +1122,20 @@ void launch_seg(dim3 g, size_t shm, hipStream_t st, const SegKArgs& k) {
 
 // Q8_0 segments (k_seg).
 int seg_launch_q8(SegLaunch& a, hipStream_t st) {
+    // one row per wave for rows wider than 32 blocks when no segment needs
+    // the rope epilogue's row pairs and x is not normalised (the o and down
+    // projections): twice the waves, half the passes each
+    bool pairs = a.do_norm != 0;
+    for (int i = 0; i < a.nseg; i++)
+        pairs = pairs || a.seg[i].epi == EPI_SWIGLU || a.seg[i].epi == EPI_ROPE_Q || a.seg[i].epi == EPI_ROPE_K;
+    const int R = !pairs && a.n_in > 1024 ? 1 : SEG_R;
     int blocks = 0;
     for (int i = 0; i < a.nseg; i++) {
         SegDesc& s = a.seg[i];
         if (s.row1 <= 0) s.row1 = s.L.n_out;
         if (s.row0 != 0 || s.row1 != s.L.n_out) return -1;  // row ranges go through draco_gemv_launch
         s.first_block = blocks;
-        s.n_blocks = (s.L.n_out + SEG_ROWS - 1) / SEG_ROWS;
+        s.n_blocks = (s.L.n_out + 4 * R - 1) / (4 * R);
         if (s.epi == EPI_SWIGLU) {
             if (i + 1 >= a.nseg) return -1;
             const SegDesc& u = a.seg[i + 1];
@@ -1143,8 +1158,12 @@ int seg_launch_q8(SegLaunch& a, hipStream_t st) {
     const dim3 g(blocks), b(256);
     const SegKArgs k = seg_kargs(a, true);
     // passes of 64 (row, block) pairs per wave; the first NP preloaded
-    const int passes = (SEG_R * (a.n_in / 32) + 63) / 64;
-    if (dual) {
+    const int passes = (R * (a.n_in / 32) + 63) / 64;
+    if (R == 1) {
+        if (passes <= 1) launch_seg1<false, 1, false, 1>(g, shm, st, k);
+        else if (passes <= 2) launch_seg1<false, 2, false, 1>(g, shm, st, k);
+        else launch_seg1<false, 4, false, 1>(g, shm, st, k);
+    } else if (dual) {
         if (passes <= 1) launch_seg<true, 1>(g, shm, st, k);
         else launch_seg<true, 2>(g, shm, st, k);
     } else {
