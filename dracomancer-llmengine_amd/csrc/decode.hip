@@ -343,23 +343,20 @@ __global__ __launch_bounds__(256) void k_attn_merge(const float* __restrict__ pa
     float pv[MERGE_BATCH];
 #pragma unroll
     for (int j = 0; j < MERGE_BATCH; j++) pv[j] = ph[(size_t)min(q + 4 * j, nsplit - 1) * (HD + 2) + d];
-    // split statistics (threads k, k + 256, ...)
-    float mloc = -INFINITY;
-    for (int k = tid; k < nsplit; k += 256) mloc = fmaxf(mloc, ph[(size_t)k * (HD + 2) + HD]);
+    // split statistics: thread k holds split k's (m, l) (nsplit <= 256),
+    // requested with the partials above
+    const int kc = min(tid, nsplit - 1);
+    const float mk0 = ph[(size_t)kc * (HD + 2) + HD], lk0 = ph[(size_t)kc * (HD + 2) + HD + 1];
+    const bool ks = tid < nsplit;
+    float mloc = ks ? mk0 : -INFINITY;
     mloc = wave_max(mloc);
     if (lane == 0) red[0][q] = mloc;
     lds_barrier();
     const float M = fmaxf(fmaxf(red[0][0], red[0][1]), fmaxf(red[0][2], red[0][3]));
-    float lsum = 0.f;
-    for (int k = tid; k < MERGE_MAXS + 4 * MERGE_BATCH; k += 256) {
-        float wk = 0.f;
-        if (k < nsplit) {
-            const float mk = ph[(size_t)k * (HD + 2) + HD];
-            wk = mk == -INFINITY ? 0.f : expf(mk - M);
-            lsum += ph[(size_t)k * (HD + 2) + HD + 1] * wk;
-        }
-        wsh[k] = wk;
-    }
+    const float wk = !ks || mk0 == -INFINITY ? 0.f : expf(mk0 - M);
+    float lsum = ks ? lk0 * wk : 0.f;
+    wsh[tid] = wk;
+    if (tid < 4 * MERGE_BATCH) wsh[MERGE_MAXS + tid] = 0.f;  // padding splits of the last batch
     lsum = wave_sum(lsum);
     if (lane == 0) red[1][q] = lsum;
     lds_barrier();
@@ -394,11 +391,15 @@ __global__ __launch_bounds__(256) void k_attn_combine(const float* __restrict__ 
                                                       int gstride) {
     const int h = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
     const float* ph = part + (size_t)h * nsplit * (HD + 2);
-    const float m = lane < nsplit ? ph[lane * (HD + 2) + HD] : -INFINITY;
-    const float lk = lane < nsplit ? ph[lane * (HD + 2) + HD + 1] : 0.f;
+    // every load unconditional (clamped split index), so all of them are in
+    // flight together: one memory round trip
+    const int kl = min(lane, nsplit - 1);
+    const float m0 = ph[kl * (HD + 2) + HD], l0 = ph[kl * (HD + 2) + HD + 1];
     float pv[MAXS];
 #pragma unroll
-    for (int k = 0; k < MAXS; k++) pv[k] = ph[min(k, nsplit - 1) * (HD + 2) + tid];  // unconditional: no vmcnt(0) per load
+    for (int k = 0; k < MAXS; k++) pv[k] = ph[min(k, nsplit - 1) * (HD + 2) + tid];
+    const float m = lane < nsplit ? m0 : -INFINITY;
+    const float lk = lane < nsplit ? l0 : 0.f;
     const float M = wave_max(m);
     const float wk = m > -INFINITY ? expf(m - M) : 0.f;
     const float L = wave_sum(lk * wk);
@@ -407,11 +408,11 @@ __global__ __launch_bounds__(256) void k_attn_combine(const float* __restrict__ 
     for (int k = 0; k < MAXS; k++) {  // lanes k >= nsplit carry weight 0
         acc = fmaf(pv[k], __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wk), k)), acc);
     }
-    if (tid < HD) {
-        float r = acc * (1.f / L);
-        if (gate) r *= 1.f / (1.f + expf(-gate[(size_t)h * gstride + tid]));
-        out[(size_t)h * HD + tid] = r;
-    }
+    // the block is HD threads (no guard: a store under a thread test would let
+    // the compiler sink the partial loads below the statistics' reductions)
+    float r = acc * (1.f / L);
+    if (gate) r *= 1.f / (1.f + expf(-gate[(size_t)h * gstride + tid]));
+    out[(size_t)h * HD + tid] = r;
 }
 
 // qwen35 full attention, per-head RMSNorm over 256 dims and rope on the pairs

@@ -832,7 +832,23 @@ __global__ __launch_bounds__(256) void k_argmax_finalize(const float* __restrict
     // token's embedding row
     float v = -INFINITY;
     int idx = 0x7fffffff;
-    for (int i = tid; i < nb; i += 256) am_merge(v, idx, pv[i], pi[i]);
+    // the partials in batches of 8 per thread, each batch's loads issued
+    // together (clamped index; the merge is order-independent: larger value,
+    // then lower index)
+    constexpr int MB = 8;
+    for (int i0 = tid; i0 < nb; i0 += 256 * MB) {
+        float bv[MB];
+        int bi[MB];
+#pragma unroll
+        for (int k = 0; k < MB; k++) {
+            const int i = i0 + 256 * k, ic = i < nb ? i : nb - 1;
+            bv[k] = pv[ic];
+            bi[k] = pi[ic];
+        }
+#pragma unroll
+        for (int k = 0; k < MB; k++)
+            if (i0 + 256 * k < nb) am_merge(v, idx, bv[k], bi[k]);
+    }
     group_argmax<64>(v, idx);
     if (lane == 0) {
         sv[wv] = v;
