@@ -464,18 +464,23 @@ __global__ __launch_bounds__(256) void k_fa_prep_rows(const float* __restrict__ 
     const int pos = (state ? state[0] : pos0) + tok, row = (state ? state[1] : row0) + tok;
     const bool isq = b < NH;
     const int g = b - NH;
-    const float x = isq ? QG[(size_t)tok * qg_stride + (size_t)b * 512 + t] : kin[(size_t)tok * 512 + g * 256 + t];
-    if (!isq) vc[(size_t)row * 512 + g * 256 + t] = vin[(size_t)tok * 512 + g * 256 + t];
+    // every operand requested before the first wait (one memory round trip):
+    // the head's value, its norm weight, the rope row (every wave; wave 0
+    // uses it) and, for q blocks too, a v value (k blocks copy it)
+    const float* xp = isq ? QG + (size_t)tok * qg_stride + (size_t)b * 512 : kin + (size_t)tok * 512 + g * 256;
+    const float* vp = vin + (size_t)tok * 512 + (isq ? 0 : g * 256);
+    const float* cs = cs_tab + (size_t)pos * 64;
+    const float x = xp[t], nwt = (isq ? qn : kn)[t], vv = vp[t];
+    const float c = cs[2 * (lane & 31)], sn = cs[2 * (lane & 31) + 1];
+    if (!isq) vc[(size_t)row * 512 + g * 256 + t] = vv;
     const float s = wave_sum(x * x);
     if (lane == 0) red[w] = s;
-    __syncthreads();
+    lds_barrier();
     const float n2 = (red[0] + red[1]) + (red[2] + red[3]);
     const float r = 1.f / sqrtf(n2 / 256.f + 1e-6f);
-    float y = isq ? x * r * qn[t] : x * (r * kn[t]);
+    float y = isq ? x * r * nwt : x * (r * nwt);
     if (w == 0) {
-        const float* cs = cs_tab + (size_t)pos * 64;
         const float o = lane_xor32(y);
-        const float c = cs[2 * (lane & 31)], sn = cs[2 * (lane & 31) + 1];
         y = lane < 32 ? y * c - o * sn : o * sn + y * c;
     }
     if (isq) Qr[(size_t)tok * NH * 256 + (size_t)b * 256 + t] = y;

@@ -161,30 +161,38 @@ __global__ __launch_bounds__(64 * NW) void k_gdn_scan(const GdnArgs a) {
     int ch[R];
     bool own[R];
     float w0[R], w1[R], w2[R], w3[R], t0[R], t1[R], t2[R], xin[R];
+    // Every load of the prologue is unconditional (a thread past the block's
+    // channels reads channel j * 128 and discards it; the launchers never
+    // start a scan of 0 tokens), so the conv inputs and the state below are
+    // all in flight before the first wait.
 #pragma unroll
     for (int r = 0; r < R; r++) {
         const int c = tid + r * NT;
-        ch[r] = -1;
-        if (c < SV) ch[r] = j * SV + c;
-        else if (c < 2 * SV) ch[r] = NHQ * SV + j * SV + (c - SV);
-        else if (c < CH) ch[r] = 2 * NHQ * SV + h * SV + col0 + (c - 2 * SV);
+        int cc = j * SV;
+        if (c < SV) cc = j * SV + c;
+        else if (c < 2 * SV) cc = NHQ * SV + j * SV + (c - SV);
+        else if (c < CH) cc = 2 * NHQ * SV + h * SV + col0 + (c - 2 * SV);
+        const bool live = c < CH;
+        ch[r] = live ? cc : -1;
         own[r] = c >= 2 * SV ? true : (h < NHQ && sp == 0);
-        w0[r] = w1[r] = w2[r] = w3[r] = t0[r] = t1[r] = t2[r] = xin[r] = 0.f;
-        if (ch[r] >= 0) {
-            const float4 cw = ld4(a.conv + (size_t)ch[r] * 4);
-            w0[r] = cw.x; w1[r] = cw.y; w2[r] = cw.z; w3[r] = cw.w;
-            t0[r] = a.tail[(size_t)ch[r] * 3];
-            t1[r] = a.tail[(size_t)ch[r] * 3 + 1];
-            t2[r] = a.tail[(size_t)ch[r] * 3 + 2];
-            if (T > 0) xin[r] = a.QKV[ch[r]];
-        }
+        const float4 cw = ld4(a.conv + (size_t)cc * 4);
+        const float ta = a.tail[(size_t)cc * 3], tb = a.tail[(size_t)cc * 3 + 1], tc = a.tail[(size_t)cc * 3 + 2];
+        const float xi = a.QKV[cc];
+        w0[r] = live ? cw.x : 0.f;
+        w1[r] = live ? cw.y : 0.f;
+        w2[r] = live ? cw.z : 0.f;
+        w3[r] = live ? cw.w : 0.f;
+        t0[r] = live ? ta : 0.f;
+        t1[r] = live ? tb : 0.f;
+        t2[r] = live ? tc : 0.f;
+        xin[r] = live ? xi : 0.f;
     }
     // state slice
     const int vl = lane / KQ, kq = lane % KQ, vloc = CPW * w + vl, v = col0 + vloc;
     float* Sh = a.S + (size_t)h * SV * SV;
     const float nw = a.ssm_norm[v];
     // per-token inputs, prefetched one token ahead
-    float zin = T > 0 ? a.Z[(size_t)h * SV + v] : 0.f;
+    float zin = a.Z[(size_t)h * SV + v];
     float s[RPL];
 #pragma unroll
     for (int i = 0; i < RPL; i++) s[i] = Sh[(size_t)(RPL * kq + i) * SV + v];
@@ -195,8 +203,8 @@ __global__ __launch_bounds__(64 * NW) void k_gdn_scan(const GdnArgs a) {
         if (a.glog) GdnGates<NW>::gates_of(a, h, gdb, gda, &bin, &gin);
         else gates.finish(a, h, tid, &bin, &gin);
     } else {
-        gin = T > 0 ? a.G[h] : 0.f;
-        bin = T > 0 ? a.B[h] : 0.f;
+        gin = a.G[h];
+        bin = a.B[h];
     }
     for (int t = 0; t < T; t++) {
         const float z = zin, g = gin, b = bin;
