@@ -173,7 +173,15 @@ __device__ __forceinline__ uint4 ldu4(const uint8_t* p) { return *reinterpret_ca
 // does not push activations, KV rows and other reused data out of L2.
 // Measured on the decode chain: 1919 -> 1943 tok/s.
 typedef unsigned int v4u32 __attribute__((ext_vector_type(4)));
+// Weight streams live in global memory.  A pointer read from memory (an
+// expert table) is generic to the compiler, and a generic (flat) load also
+// counts against the LDS wait counter, so every LDS barrier behind it would
+// wait for the weights; the cast makes it a global load.
+template <class T>
+__device__ __forceinline__ const __attribute__((address_space(1))) T* gptr(const void* p) {
+    return (const __attribute__((address_space(1))) T*)p;
+}
 __device__ __forceinline__ uint4 ldnt4(const uint8_t* p) {
-    const v4u32 v = __builtin_nontemporal_load(reinterpret_cast<const v4u32*>(p));
+    const v4u32 v = __builtin_nontemporal_load(gptr<v4u32>(p));
     return make_uint4(v.x, v.y, v.z, v.w);
 }

@@ -168,7 +168,8 @@ __global__ __launch_bounds__(64 * NW) void k_moe_grp(const MoeArgs a) {
     float* swt = reinterpret_cast<float*>(sidx + MOE_USED_MAX);
     const uint8_t** sb0 = reinterpret_cast<const uint8_t**>(swt + MOE_USED_MAX);  // [MOE_USED_MAX] bases
     const uint8_t** sb1 = sb0 + MOE_USED_MAX;
-    float* sp = reinterpret_cast<float*>(sb1 + MOE_USED_MAX);                      // [MOE_EXP_MAX] probabilities
+    const uint8_t** sb2 = sb1 + MOE_USED_MAX;  // block 0: the selected experts' down bases (published)
+    float* sp = reinterpret_cast<float*>(sb2 + MOE_USED_MAX);                      // [MOE_EXP_MAX] probabilities
 
     const int tid = threadIdx.x, lane = tid & 63, j = lane & 15, g = lane >> 4;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -199,20 +200,25 @@ __global__ __launch_bounds__(64 * NW) void k_moe_grp(const MoeArgs a) {
         // the probabilities hold a NaN, which then cannot index out of range)
         constexpr int EPP = NT / 4, NPASS = (MOE_EXP_MAX + EPP - 1) / EPP;
         const int part = tid & 3;
+        // Block 0 also reads the down bases it publishes, with the others (a
+        // read after the ranking would add a memory round trip to block 0)
         const uint8_t* rb0[NPASS];
         const uint8_t* rb1[NPASS];
+        const uint8_t* rb2[NPASS];
 #pragma unroll
         for (int k = 0; k < NPASS; k++) {
             const int e = (tid >> 2) + k * EPP;
             const bool mine = part == 0 && e < a.n_exp;
             rb0[k] = mine ? a.base0[e] : nullptr;
             rb1[k] = (DUAL && mine) ? a.base1[e] : nullptr;
+            rb2[k] = (bx == 0 && mine) ? a.base2[e] : nullptr;
         }
         if (tid < n_slots) {
             sidx[tid] = 0;
             swt[tid] = 0.f;
             sb0[tid] = a.base0[0];
             if (DUAL) sb1[tid] = a.base1[0];
+            if (bx == 0) sb2[tid] = a.base2[0];
         }
         if (w == 0) softmax_wave(a.logits, a.n_exp, sp);
         lds_barrier();
@@ -228,6 +234,7 @@ __global__ __launch_bounds__(64 * NW) void k_moe_grp(const MoeArgs a) {
                 swt[r] = sp[e];
                 sb0[r] = rb0[k];
                 if (DUAL) sb1[r] = rb1[k];
+                if (bx == 0) sb2[r] = rb2[k];
             }
         }
     } else if (tid < n_slots) {
@@ -236,15 +243,6 @@ __global__ __launch_bounds__(64 * NW) void k_moe_grp(const MoeArgs a) {
     }
     for (int i = tid; i < 256; i += NT) reinterpret_cast<uint32_t*>(zero)[i] = 0u;
     lds_barrier();
-    if (ROUTE && bx == 0 && tid < n_slots) {  // publish the routing: weights renormalised in slot order
-        float ws = 0.f;
-        for (int t = 0; t < n_slots; t++) ws += swt[t];
-        if (ws < 6.103515625e-5f) ws = 6.103515625e-5f;
-        const int e = sidx[tid];
-        a.sel[tid] = e;
-        a.selw[tid] = swt[tid] / ws;
-        a.seld[tid] = a.base2[e];
-    }
 
     auto load = [&](int T, int b, Frag& f, Frag& f2) {
         const int s = T / tpe, lt = T - s * tpe;
@@ -372,6 +370,17 @@ __global__ __launch_bounds__(64 * NW) void k_moe_grp(const MoeArgs a) {
         if (i + 1 >= n_items) break;
         step(i + 1, P1, P0, Q1, Q0);
     }
+    // publish the routing (weights renormalised in slot order) for the down
+    // launch, last: stores before the first weight requests would make them
+    // wait for the stores (the LDS routing tables are not rewritten above)
+    if (ROUTE && bx == 0 && tid < n_slots) {
+        float ws = 0.f;
+        for (int t = 0; t < n_slots; t++) ws += swt[t];
+        if (ws < 6.103515625e-5f) ws = 6.103515625e-5f;
+        a.sel[tid] = sidx[tid];
+        a.selw[tid] = swt[tid] / ws;
+        a.seld[tid] = sb2[tid];
+    }
 }
 
 // Down projection of the routed experts plus the weighted combine.  Block =
@@ -404,21 +413,45 @@ __global__ __launch_bounds__(64 * NW) void k_moe_down(const MoeArgs a) {
         if (FM == 1) load_q4(p, lane, f);
         else load_q6(p, lane, f);
     };
+    // act loads (all slots; every float4 of a batch requested together,
+    // clamped index) and the combine weight before the expert weights: the
+    // act arrives first, so the digits are formed while the weights stream
+    const int nvals4 = n_used * n4;
+    constexpr int AB = 4;
+    float4 av[AB];
+    auto act_batch = [&](int b0) {
+#pragma unroll
+        for (int k = 0; k < AB; k++) {
+            const int i4 = b0 + tid + k * NT, ic = i4 < nvals4 ? i4 : nvals4 - 1;
+            const int s = ic / n4, o = ic - s * n4;
+            av[k] = ld4(a.act + (size_t)s * inter + 4 * o);
+        }
+    };
+    act_batch(0);
+    const float swv = a.selw[tid < n_used ? tid : n_used - 1];
+    // requested unconditionally (a wave past the used slots or a block past
+    // the tiles re-reads real items), so the act waits above count exactly
     Frag P0, P1, P2;
     int t = blockIdx.x;
-    if (active && t < tiles) {
-        ld(t, 0, P0);
-        ld(t, 1, P1);
-        ld(t, 2, P2);
+    {
+        const int tl = t < tiles ? t : tiles - 1;
+        ld(tl, 0, P0);
+        ld(tl, 1, P1);
+        ld(tl, 2, P2);
     }
-    if (tid < n_used) swt[tid] = a.selw[tid];
     for (int i = tid; i < 256; i += NT) reinterpret_cast<uint32_t*>(zero)[i] = 0u;
-    // act loads (all slots), then digits
-    const int nvals4 = n_used * n4;
-    for (int i4 = tid; i4 < nvals4; i4 += NT) {
-        const int s = i4 / n4, o = i4 - s * n4;
-        digits4(ld4(a.act + (size_t)s * inter + 4 * o), o, xd + (size_t)s * ng * 64, xsm + (size_t)s * ng);
+    for (int b0 = 0; b0 < nvals4; b0 += AB * NT) {
+        if (b0 > 0) act_batch(b0);
+#pragma unroll
+        for (int k = 0; k < AB; k++) {
+            const int i4 = b0 + tid + k * NT;
+            if (i4 < nvals4) {
+                const int s = i4 / n4, o = i4 - s * n4;
+                digits4(av[k], o, xd + (size_t)s * ng * 64, xsm + (size_t)s * ng);
+            }
+        }
     }
+    if (tid < n_used) swt[tid] = swv;
     lds_barrier();
     const bool adig = (j >> 2) == g;
     const int gl4 = 4 * (g >> 1) + (g & 1), gl6 = 8 * (g >> 1) + (g & 1);
@@ -577,7 +610,7 @@ int draco_moe_grp_launch(MoeArgs& a, int fm, bool dual, bool xper, bool route, h
     const int nw = grp_nw(n_in);
     const int nx = xper ? a.n_slots : 1;
     if ((size_t)nx * (n_in / 4) > (size_t)XP_MAXV * 64 * nw) return -1;  // prologue capacity
-    const size_t lds = (size_t)nx * (n_in / 16) * 72 + 1024 + (2 * 16 * 16 + 64) * 4 + MOE_USED_MAX * 24 +
+    const size_t lds = (size_t)nx * (n_in / 16) * 72 + 1024 + (2 * 16 * 16 + 64) * 4 + MOE_USED_MAX * 32 +
                        MOE_EXP_MAX * 4;
     if (lds > 160 * 1024) return -1;
     const int total = a.n_slots * (a.n_out_e / 16);

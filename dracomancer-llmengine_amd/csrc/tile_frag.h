@@ -28,8 +28,8 @@ __device__ __forceinline__ void load_q6(const uint8_t* item, int lane, Frag& f) 
     f.a = ldnt4(item + 16 * lane);
     f.b = ldnt4(item + 1024 + 16 * lane);
     f.c = ldnt4(item + 2048 + 16 * lane);
-    f.sc = *reinterpret_cast<const uint32_t*>(item + 3072 + 4 * lane);
-    f.d = *reinterpret_cast<const uint16_t*>(item + 3328 + 2 * (lane & 15));
+    f.sc = *gptr<uint32_t>(item + 3072 + 4 * lane);
+    f.d = *gptr<uint16_t>(item + 3328 + 2 * (lane & 15));
 }
 
 __device__ __forceinline__ float fold(const v4i C) {
