@@ -159,6 +159,10 @@ __global__ __launch_bounds__(1024) void k_attn_part(const float* __restrict__ q,
 #pragma unroll
             for (int e = 0; e < DV; e++) vv[r][e] = vc[(size_t)trr * KD + g * HD + lane + 64 * e];
         }
+        // every K and V request of the pass leaves before the first wait (the
+        // scheduler would otherwise start the scores between them, and the
+        // wait for the first K rows would hold back the remaining V requests)
+        __builtin_amdgcn_sched_barrier(0);
         float sc = 0.f;
 #pragma unroll
         for (int i = 0; i < 8; i++) {
@@ -250,6 +254,7 @@ __global__ __launch_bounds__(256) void k_attn_gqa(const float* __restrict__ q, c
         float vv[GQ_CH];
 #pragma unroll
         for (int r = 0; r < GQ_CH; r++) vv[r] = vg[(size_t)min(c0 + r, t1 - 1) * KD];
+        __builtin_amdgcn_sched_barrier(0);  // every request of the sub-chunk before the first wait
         // reduce-scatter over the heads: each stage halves the heads a lane
         // holds and pairs it (lane_flip) with a lane keeping the other half;
         // the exchanges are DPP / permlane moves, no LDS traffic

@@ -166,7 +166,6 @@ __device__ __forceinline__ void lds_barrier() {
 
 __device__ __forceinline__ float4 ld4(const float* p) { return *reinterpret_cast<const float4*>(p); }
 
-__device__ __forceinline__ uint4 ldu4(const uint8_t* p) { return *reinterpret_cast<const uint4*>(p); }
 
 // Streaming load of data read once per launch (quantized weights): the
 // non-temporal hint marks the lines for early eviction, so a weight stream
@@ -180,6 +179,11 @@ typedef unsigned int v4u32 __attribute__((ext_vector_type(4)));
 template <class T>
 __device__ __forceinline__ const __attribute__((address_space(1))) T* gptr(const void* p) {
     return (const __attribute__((address_space(1))) T*)p;
+}
+// 16 weight bytes through the global address space (the grouped expert GEMMs' items)
+__device__ __forceinline__ uint4 ldu4(const uint8_t* p) {
+    const v4u32 v = *gptr<v4u32>(p);
+    return make_uint4(v.x, v.y, v.z, v.w);
 }
 __device__ __forceinline__ uint4 ldnt4(const uint8_t* p) {
     const v4u32 v = __builtin_nontemporal_load(gptr<v4u32>(p));

@@ -221,7 +221,7 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_q6(const GemmArgs a) {
             const int tile = 2 * (p0 + p) + (n >> 4), j = n & 15;
             const int tl = tile < a.L.ntiles ? tile : a.L.ntiles - 1;
             const uint8_t* item = Wb + ((size_t)tl * nb + b) * DRACO_Q6T_ITEM;
-            const float d = h2f(*reinterpret_cast<const uint16_t*>(item + 3328 + 2 * j));
+            const float d = h2f(*gptr<uint16_t>(item + 3328 + 2 * j));
             // per super-block: int32 sums of sc * C over the 8 chunks (exact), and the
             // fp32 sums of sc * (16-value sums) for the -32 offset
             int acc[2][16];
@@ -236,7 +236,7 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_q6(const GemmArgs a) {
             for (int g2 = 0; g2 < 2; g2++) {
                 const int ls = j + 16 * (2 * g2 + u);  // tile-layout lane slot of (row j, group pair g2, half u)
                 const uint4 qa = ldu4(item + 16 * ls), qb = ldu4(item + 1024 + 16 * ls), qh = ldu4(item + 2048 + 16 * ls);
-                const uint32_t sc4 = *reinterpret_cast<const uint32_t*>(item + 3072 + 4 * ls);
+                const uint32_t sc4 = *gptr<uint32_t>(item + 3072 + 4 * ls);
                 // every activation operand of the four 32-value chunks of this group pair,
                 // loaded before the first MFMA (one memory round trip per group pair)
                 v4i A[4][2];
