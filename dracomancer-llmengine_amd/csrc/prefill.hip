@@ -37,23 +37,31 @@ __global__ __launch_bounds__(256) void k_pf_rms(const float* __restrict__ X, con
     __shared__ float red[4];
     const float* x = X + (size_t)blockIdx.x * h;
     float* o = Xn + (size_t)blockIdx.x * h;
-    float v[PF_RMS_PT];
+    // every load (the row and its norm weights, clamped index) before the
+    // first wait; a null weight re-reads the row
+    const float* wp = w ? w : x;
+    float v[PF_RMS_PT], wv[PF_RMS_PT];
+#pragma unroll
+    for (int k = 0; k < PF_RMS_PT; k++) {
+        const int i = threadIdx.x + 256 * k, ic = i < h ? i : h - 1;
+        v[k] = x[ic];
+        wv[k] = wp[ic];
+    }
     float s = 0.f;
 #pragma unroll
     for (int k = 0; k < PF_RMS_PT; k++) {
-        const int i = threadIdx.x + 256 * k;
-        v[k] = i < h ? x[i] : 0.f;
+        if (threadIdx.x + 256 * k >= h) v[k] = 0.f;
         s = fmaf(v[k], v[k], s);
     }
     s = wave_sum(s);
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
-    __syncthreads();
+    lds_barrier();
     const float tot = (red[0] + red[1]) + (red[2] + red[3]);
     const float inv = 1.f / sqrtf(tot / (float)h + eps);
 #pragma unroll
     for (int k = 0; k < PF_RMS_PT; k++) {
         const int i = threadIdx.x + 256 * k;
-        if (i < h) o[i] = w ? v[k] * inv * w[i] : v[k] * inv;
+        if (i < h) o[i] = w ? v[k] * inv * wv[k] : v[k] * inv;
     }
 }
 
@@ -66,27 +74,34 @@ __global__ __launch_bounds__(256) void k_pf_add_rms(float* __restrict__ X, const
     float* x = X + (size_t)blockIdx.x * h;
     const float* y = Y + (size_t)blockIdx.x * h;
     float* o = Xn + (size_t)blockIdx.x * h;
-    float v[PF_RMS_PT];
+    // every load (row, residual, norm weights; clamped index) before the
+    // first wait and the first store; a null weight re-reads the row
+    const float* wp = w ? w : x;
+    float v[PF_RMS_PT], yv[PF_RMS_PT], wv[PF_RMS_PT];
+#pragma unroll
+    for (int k = 0; k < PF_RMS_PT; k++) {
+        const int i = threadIdx.x + 256 * k, ic = i < h ? i : h - 1;
+        v[k] = x[ic];
+        yv[k] = y[ic];
+        wv[k] = wp[ic];
+    }
     float s = 0.f;
 #pragma unroll
     for (int k = 0; k < PF_RMS_PT; k++) {
         const int i = threadIdx.x + 256 * k;
-        v[k] = 0.f;
-        if (i < h) {
-            v[k] = x[i] + y[i];
-            x[i] = v[k];
-        }
+        v[k] = i < h ? v[k] + yv[k] : 0.f;
+        if (i < h) x[i] = v[k];
         s = fmaf(v[k], v[k], s);
     }
     s = wave_sum(s);
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
-    __syncthreads();
+    lds_barrier();
     const float tot = (red[0] + red[1]) + (red[2] + red[3]);
     const float inv = 1.f / sqrtf(tot / (float)h + eps);
 #pragma unroll
     for (int k = 0; k < PF_RMS_PT; k++) {
         const int i = threadIdx.x + 256 * k;
-        if (i < h) o[i] = w ? v[k] * inv * w[i] : v[k] * inv;
+        if (i < h) o[i] = w ? v[k] * inv * wv[k] : v[k] * inv;
     }
 }
 
@@ -138,6 +153,36 @@ __global__ __launch_bounds__(256) void k_pf_rope_append(float* __restrict__ Q, c
 // (o[HD], m, l) of (head, query, split) for k_pf_merge.
 constexpr int PF_QT = 64, PF_KT = 64, PF_KG = 16;
 
+// K and V rows [kb, kb + nr) of kv head g into LDS (row-major, HD wide):
+// each thread requests up to 4 float4s of each array together (clamped
+// index; the stores skip the clamped ones), so a tile costs one memory round
+// trip per 4 float4s per thread instead of one per float4.
+template <int HD>
+__device__ __forceinline__ void stage_kv(float* Ks, float* Vs, const float* __restrict__ kc,
+                                         const float* __restrict__ vc, int kb, int nr, int KD, int g) {
+    constexpr int SB = 4;
+    const int n = nr * (HD / 4), nt = blockDim.x, tid = threadIdx.x;
+    for (int b0 = 0; b0 < n; b0 += SB * nt) {
+        float4 kv[SB], vv[SB];
+#pragma unroll
+        for (int u = 0; u < SB; u++) {
+            const int i = b0 + tid + u * nt, ic = i < n ? i : n - 1;
+            const int r = ic / (HD / 4), c = 4 * (ic % (HD / 4));
+            kv[u] = ld4(kc + (size_t)(kb + r) * KD + g * HD + c);
+            vv[u] = ld4(vc + (size_t)(kb + r) * KD + g * HD + c);
+        }
+#pragma unroll
+        for (int u = 0; u < SB; u++) {
+            const int i = b0 + tid + u * nt;
+            if (i < n) {
+                const int r = i / (HD / 4), c = 4 * (i % (HD / 4));
+                *reinterpret_cast<float4*>(Ks + r * HD + c) = kv[u];
+                *reinterpret_cast<float4*>(Vs + r * HD + c) = vv[u];
+            }
+        }
+    }
+}
+
 template <int HD>
 __global__ __launch_bounds__(512) void k_pf_attn(const float* __restrict__ Q, const float* __restrict__ kc,
                                                  const float* __restrict__ vc, float* __restrict__ part, int row0,
@@ -154,20 +199,17 @@ __global__ __launch_bounds__(512) void k_pf_attn(const float* __restrict__ Q, co
     const int chunk = (kend + nspl - 1) / nspl;
     const int k0 = min(kend, s * chunk), k1 = min(kend, k0 + chunk);
     float q[HD], o[HD];
+    const int tq = live ? t : 0;  // a query past the chunk reads row 0 and discards it
 #pragma unroll
     for (int d = 0; d < HD; d += 4) {
-        const float4 v = live ? ld4(Q + (size_t)t * QD + h * HD + d) : make_float4(0.f, 0.f, 0.f, 0.f);
-        q[d] = v.x; q[d + 1] = v.y; q[d + 2] = v.z; q[d + 3] = v.w;
+        const float4 v = ld4(Q + (size_t)tq * QD + h * HD + d);
+        q[d] = live ? v.x : 0.f; q[d + 1] = live ? v.y : 0.f; q[d + 2] = live ? v.z : 0.f; q[d + 3] = live ? v.w : 0.f;
         o[d] = o[d + 1] = o[d + 2] = o[d + 3] = 0.f;
     }
     float m = -INFINITY, l = 0.f;
     for (int kb = k0; kb < k1; kb += PF_KT) {
         const int nr = min(PF_KT, k1 - kb);
-        for (int i = tid; i < nr * (HD / 4); i += blockDim.x) {
-            const int r = i / (HD / 4), c = 4 * (i % (HD / 4));
-            *reinterpret_cast<float4*>(Ks + r * HD + c) = ld4(kc + (size_t)(kb + r) * KD + g * HD + c);
-            *reinterpret_cast<float4*>(Vs + r * HD + c) = ld4(vc + (size_t)(kb + r) * KD + g * HD + c);
-        }
+        stage_kv<HD>(Ks, Vs, kc, vc, kb, nr, KD, g);
         __syncthreads();
         for (int c0 = 0; c0 < nr; c0 += PF_KG) {
             const int ng = min(PF_KG, nr - c0);
@@ -272,20 +314,18 @@ __global__ __launch_bounds__(1024) void k_pf_attn256(const float* __restrict__ Q
     const int chunk = (kend + nspl - 1) / nspl;
     const int k0 = min(kend, s * chunk), k1 = min(kend, k0 + chunk);
     float q[32], o[32];
+    const int tq = live ? t : 0;  // a query past the chunk reads row 0 and discards it
 #pragma unroll
     for (int i = 0; i < 8; i++) {
-        const float4 v = live ? ld4(Q + (size_t)t * QD + h * HD + 4 * (k + 8 * i)) : make_float4(0.f, 0.f, 0.f, 0.f);
-        q[4 * i] = v.x; q[4 * i + 1] = v.y; q[4 * i + 2] = v.z; q[4 * i + 3] = v.w;
+        const float4 v = ld4(Q + (size_t)tq * QD + h * HD + 4 * (k + 8 * i));
+        q[4 * i] = live ? v.x : 0.f; q[4 * i + 1] = live ? v.y : 0.f;
+        q[4 * i + 2] = live ? v.z : 0.f; q[4 * i + 3] = live ? v.w : 0.f;
         o[4 * i] = o[4 * i + 1] = o[4 * i + 2] = o[4 * i + 3] = 0.f;
     }
     float m = -INFINITY, l = 0.f;
     for (int kb = k0; kb < k1; kb += PF256_KT) {
         const int nr = min(PF256_KT, k1 - kb);
-        for (int i = tid; i < nr * (HD / 4); i += blockDim.x) {
-            const int r = i / (HD / 4), c = 4 * (i % (HD / 4));
-            *reinterpret_cast<float4*>(Ks + r * HD + c) = ld4(kc + (size_t)(kb + r) * KD + g * HD + c);
-            *reinterpret_cast<float4*>(Vs + r * HD + c) = ld4(vc + (size_t)(kb + r) * KD + g * HD + c);
-        }
+        stage_kv<HD>(Ks, Vs, kc, vc, kb, nr, KD, g);
         __syncthreads();
         for (int c0 = 0; c0 < nr; c0 += 16) {
             const int ng = min(16, nr - c0);
