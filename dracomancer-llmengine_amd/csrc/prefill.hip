@@ -268,23 +268,50 @@ __global__ __launch_bounds__(512) void k_pf_attn(const float* __restrict__ Q, co
     pp[HD + 1] = l;
 }
 
+// The split merge of one (query, head, dim): M = max_s m_s, then num / den
+// with den = sum_s l_s e^(m_s - M), num = sum_s o_s[d] e^(m_s - M) in split
+// order.  Loads go in batches of 16 splits, all of a batch requested together
+// (clamped split index; the merge skips the clamped ones), instead of one
+// dependent round trip per split.
+__device__ __forceinline__ float pf_merge_one(const float* __restrict__ pp, int HD, int nspl, int d) {
+    constexpr int MB = 16;
+    float M = -INFINITY;
+    for (int s0 = 0; s0 < nspl; s0 += MB) {
+        float mv[MB];
+#pragma unroll
+        for (int k = 0; k < MB; k++) mv[k] = pp[(size_t)min(s0 + k, nspl - 1) * (HD + 2) + HD];
+#pragma unroll
+        for (int k = 0; k < MB; k++)
+            if (s0 + k < nspl) M = fmaxf(M, mv[k]);
+    }
+    float num = 0.f, den = 0.f;
+    for (int s0 = 0; s0 < nspl; s0 += MB) {
+        float mv[MB], lv[MB], ov[MB];
+#pragma unroll
+        for (int k = 0; k < MB; k++) {
+            const float* q = pp + (size_t)min(s0 + k, nspl - 1) * (HD + 2);
+            mv[k] = q[HD];
+            lv[k] = q[HD + 1];
+            ov[k] = q[d];
+        }
+#pragma unroll
+        for (int k = 0; k < MB; k++) {
+            if (s0 + k >= nspl || mv[k] == -INFINITY) continue;
+            const float e = expf(mv[k] - M);
+            den = fmaf(lv[k], e, den);
+            num = fmaf(ov[k], e, num);
+        }
+    }
+    return num / den;
+}
+
 // out[t][h*HD + d] = sum_s o_s[d] e^(m_s - M) / sum_s l_s e^(m_s - M)
 __global__ __launch_bounds__(256) void k_pf_merge(const float* __restrict__ part, float* __restrict__ O, int T,
                                                   int NH, int HD, int nspl) {
     const int t = blockIdx.x, h = blockIdx.y, d = threadIdx.x;
     if (d >= HD) return;
     const float* pp = part + ((size_t)h * T + t) * nspl * (HD + 2);
-    float M = -INFINITY;
-    for (int s = 0; s < nspl; s++) M = fmaxf(M, pp[s * (HD + 2) + HD]);
-    float num = 0.f, den = 0.f;
-    for (int s = 0; s < nspl; s++) {
-        const float ms = pp[s * (HD + 2) + HD];
-        if (ms == -INFINITY) continue;
-        const float e = expf(ms - M);
-        den = fmaf(pp[s * (HD + 2) + HD + 1], e, den);
-        num = fmaf(pp[s * (HD + 2) + d], e, num);
-    }
-    O[(size_t)t * NH * HD + h * HD + d] = num / den;
+    O[(size_t)t * NH * HD + h * HD + d] = pf_merge_one(pp, HD, nspl, d);
 }
 
 // Causal chunk attention at head dim 256 (qwen35 full attention, the chunked
@@ -396,18 +423,8 @@ __global__ __launch_bounds__(256) void k_pf_merge_gate(const float* __restrict__
     const int t = blockIdx.x, h = blockIdx.y, d = threadIdx.x;
     if (d >= HD) return;
     const float* pp = part + ((size_t)h * T + t) * nspl * (HD + 2);
-    float M = -INFINITY;
-    for (int s = 0; s < nspl; s++) M = fmaxf(M, pp[s * (HD + 2) + HD]);
-    float num = 0.f, den = 0.f;
-    for (int s = 0; s < nspl; s++) {
-        const float ms = pp[s * (HD + 2) + HD];
-        if (ms == -INFINITY) continue;
-        const float e = expf(ms - M);
-        den = fmaf(pp[s * (HD + 2) + HD + 1], e, den);
-        num = fmaf(pp[s * (HD + 2) + d], e, num);
-    }
     const float gv = gate[(size_t)t * g_row + (size_t)h * g_head + d];
-    O[(size_t)t * NH * HD + h * HD + d] = (num / den) * (1.f / (1.f + expf(-gv)));
+    O[(size_t)t * NH * HD + h * HD + d] = pf_merge_one(pp, HD, nspl, d) * (1.f / (1.f + expf(-gv)));
 }
 
 // GDN gates of a chunk (src/qwen35_prefill.py:118-123): for token t and V
