@@ -90,9 +90,12 @@ struct Work {
     // a pending residual after a split-K down projection: the layer output is
     // x + pd[0..H) + pd[H..2H), materialised into xs by the next q/k/v launch
     float *pd = nullptr, *xs = nullptr;
+    // a MoE layer after a split-K o projection: its input (the layer input +
+    // the partials in pd), materialised by the router launch
+    float* xm = nullptr;
     unsigned* cnt = nullptr;  // attention merge counters (one per kv head), zero at rest
     size_t cap_h = 0, cap_xn = 0, cap_xe = 0, cap_q = 0, cap_k = 0, cap_part = 0, cap_ff = 0, cap_pd = 0,
-           cap_xs = 0;
+           cap_xs = 0, cap_xm = 0;
 };
 
 // Chunked-prefill buffers, token-major, for up to `cap` tokens per chunk.
@@ -264,6 +267,7 @@ int ensure_work(Work& w, int H, int QD, int KD, int NH, int HD, int max_t, int F
     if (grow(&w.xe, &w.cap_xe, H + 64)) return -2;
     if (grow(&w.pd, &w.cap_pd, 2 * (size_t)H + 64)) return -2;
     if (grow(&w.xs, &w.cap_xs, H + 64)) return -2;
+    if (grow(&w.xm, &w.cap_xm, H + 64)) return -2;
     if (w.cap_q < (size_t)QD) {
         size_t c = w.cap_q;
         if (grow(&w.q, &c, QD)) return -2;
@@ -506,6 +510,18 @@ bool ksplit_down(const DevModel* m, int l) {
     return kq(n->wq) && kq(n->wk) && kq(n->wv);
 }
 
+// Whether layer l's o projection runs split-K, leaving its residual add to
+// the MoE router launch (k_moe_logits with a pending residual): a MoE layer
+// whose router takes the RMSNorm prologue and an o projection of 16 or 32
+// super-blocks per row and at most 128 tiles (configs[3]: 2048x4096 Q6_K).
+bool ksplit_o(const DevModel* m, int l) {
+    if (!m->moe[l] || !draco_moe_layer_pend_ok(m->moe[l], m->fnorm[l])) return false;
+    const DracoMat& o = *m->attn[l]->wo;
+    const int nb = o.L.n_in / 256;
+    return (o.L.code == DRACO_Q4_K || o.L.code == DRACO_Q6_K) && o.L.n_in % 256 == 0 && (nb == 16 || nb == 32) &&
+           (o.L.n_out + 15) / 16 <= 128;
+}
+
 // enqueue one llama layer on the device (x in w.x, updated in place; with
 // xin set the layer reads its input from xin and leaves its output in w.x):
 // qkv(+norm,+rope,+append), attention, merge, wo(+residual),
@@ -523,7 +539,26 @@ int enqueue_layer(DevModel* m, int l, float eps, hipStream_t st, const float* xi
     if (dk_attention(w.q, a->kc, a->vc, w.part, w.cnt, w.att, m->state, l, a->NH, a->NKV, a->HD, a->max_t,
                      a->scale, st))
         return fail(-1, "attention launch");
-    if (draco_gemv_launch(*a->wo, w.att, w.x, pending ? w.xs : x0, 0, H, st)) return fail(-1, "gemv o");
+    const float* base = pending ? w.xs : x0;  // this layer's input
+    if (m->moe[l] && ksplit_o(m, l)) {
+        // o split-K into w.pd; the router forms base + the partials into w.xm
+        // (its RMSNorm input and the down launch's residual)
+        SegLaunch s = {};
+        s.nseg = 1;
+        s.n_in = a->wo->L.n_in;
+        s.x = w.att;
+        s.ksplit = 2;
+        SegDesc& d = s.seg[0];
+        d.base = a->wo->dev;
+        d.L = a->wo->L;
+        d.row0 = 0;
+        d.row1 = H;
+        d.y = w.pd;
+        d.epi = EPI_STORE;
+        if (draco_seg_launch(s, st)) return fail(-1, "gemv o (split-K)");
+        return draco_moe_layer_enqueue(m->moe[l], base, m->fnorm[l], eps, w.x, nullptr, st, w.pd, w.xm);
+    }
+    if (draco_gemv_launch(*a->wo, w.att, w.x, base, 0, H, st)) return fail(-1, "gemv o");
     if (m->moe[l])  // RMSNorm, router, routed gate/up + SwiGLU, down + weighted combine + residual
         return draco_moe_layer_enqueue(m->moe[l], w.x, m->fnorm[l], eps, w.x, w.x, st);
     if (int rc = enqueue_gateup(f, w, w.x, 1, m->fnorm[l], eps, st)) return rc;

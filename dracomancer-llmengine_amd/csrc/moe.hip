@@ -43,24 +43,44 @@ constexpr int XP_MAXV = 4;
 // forms xn = (x * rms^-1) * norm_w itself (the same sums in every block, so
 // every block gets the same xn); block 0 also stores xn for the expert
 // launches, which then need no RMSNorm launch of their own.
-template <bool NORM>
+// PRES (with NORM): x is a pending residual, x + pend[0..n_in) +
+// pend[n_in..2 n_in) (the split-K partials of the o projection), formed in
+// every block in that order; block 0 also stores the sum to xs_out (the
+// residual of the expert down launch).
+template <bool NORM, bool PRES = false>
 __global__ __launch_bounds__(256) void k_moe_logits(const float* __restrict__ x, const float* __restrict__ gi,
                                                     int n_exp, int n_in, float* __restrict__ logits,
                                                     const float* __restrict__ norm_w, float eps,
-                                                    float* __restrict__ xn_out) {
+                                                    float* __restrict__ xn_out, const float* __restrict__ pend,
+                                                    float* __restrict__ xs_out) {
     __shared__ float part[4], sq[4];
     constexpr int U = 4;
     const int e = blockIdx.x, tid = threadIdx.x;
     const float* w = gi + (size_t)e * n_in;
     float acc = 0.f;
     for (int i0 = tid * 4; i0 < n_in; i0 += U * 1024) {
-        float4 a[U], b[U], nw[U];
+        float4 a[U], b[U], nw[U], p0[U], p1[U];
 #pragma unroll
         for (int u = 0; u < U; u++) {
             const int i = i0 + u * 1024;
             a[u] = i < n_in ? ld4(x + i) : make_float4(0.f, 0.f, 0.f, 0.f);
             b[u] = i < n_in ? ld4(w + i) : make_float4(0.f, 0.f, 0.f, 0.f);
             if (NORM) nw[u] = i < n_in ? ld4(norm_w + i) : make_float4(0.f, 0.f, 0.f, 0.f);
+            if (PRES) {
+                p0[u] = i < n_in ? ld4(pend + i) : make_float4(0.f, 0.f, 0.f, 0.f);
+                p1[u] = i < n_in ? ld4(pend + n_in + i) : make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+        }
+        if (PRES) {
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                a[u].x = (a[u].x + p0[u].x) + p1[u].x;
+                a[u].y = (a[u].y + p0[u].y) + p1[u].y;
+                a[u].z = (a[u].z + p0[u].z) + p1[u].z;
+                a[u].w = (a[u].w + p0[u].w) + p1[u].w;
+                const int i = i0 + u * 1024;
+                if (e == 0 && i < n_in) *reinterpret_cast<float4*>(xs_out + i) = a[u];
+            }
         }
         if (NORM) {
             float ss = 0.f;
@@ -589,16 +609,22 @@ int dispatch_grp(const MoeArgs& a, int fm, bool dual, bool xper, bool route, int
 }  // namespace
 
 int draco_moe_logits_launch(const float* x, const float* gate_inp, int n_exp, int n_in, float* logits,
-                            hipStream_t st, const float* norm_w, float eps, float* xn_out) {
+                            hipStream_t st, const float* norm_w, float eps, float* xn_out, const float* pend,
+                            float* xs_out) {
     if (n_exp < 1 || n_exp > MOE_EXP_MAX || n_in % 4) return -1;
+    if (pend && (!norm_w || !xs_out)) return -1;
     if (norm_w) {
         if (n_in > 4096 || !xn_out) return -1;
-        hipLaunchKernelGGL(k_moe_logits<true>, dim3(n_exp), dim3(256), 0, st, x, gate_inp, n_exp, n_in, logits,
-                           norm_w, eps, xn_out);
+        if (pend)
+            hipLaunchKernelGGL((k_moe_logits<true, true>), dim3(n_exp), dim3(256), 0, st, x, gate_inp, n_exp, n_in,
+                               logits, norm_w, eps, xn_out, pend, xs_out);
+        else
+            hipLaunchKernelGGL((k_moe_logits<true>), dim3(n_exp), dim3(256), 0, st, x, gate_inp, n_exp, n_in, logits,
+                               norm_w, eps, xn_out, nullptr, nullptr);
         return 0;
     }
-    hipLaunchKernelGGL(k_moe_logits<false>, dim3(n_exp), dim3(256), 0, st, x, gate_inp, n_exp, n_in, logits,
-                       nullptr, 0.f, nullptr);
+    hipLaunchKernelGGL((k_moe_logits<false>), dim3(n_exp), dim3(256), 0, st, x, gate_inp, n_exp, n_in, logits,
+                       nullptr, 0.f, nullptr, nullptr, nullptr);
     return 0;
 }
 
