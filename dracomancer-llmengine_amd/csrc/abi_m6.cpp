@@ -454,16 +454,25 @@ int enqueue_qkv(DevAttn* a, Work& w, const float* x, int norm, const float* norm
 
 // gate/up + SwiGLU into w.g (src/m6_engine.c:289-302), input normalised in the
 // prologue when norm != 0
+// With pend (a pending residual: the input is x + pend[0..H) + pend[H..2H),
+// the o projection's split-K partials) the gate/up launch forms the input in
+// its RMSNorm prologue and stores it to pend_sum (one launch, same formats).
 int enqueue_gateup(DevFfn* f, Work& w, const float* x, int norm, const float* norm_w, float eps,
-                   hipStream_t st) {
+                   hipStream_t st, const float* pend = nullptr, float* pend_sum = nullptr) {
+    if (pend && (f->g->L.code != f->u->L.code || !norm || !pend_sum))
+        return fail(-1, "gate/up: a pending residual needs one launch with the RMSNorm prologue");
     if (f->g->L.code == f->u->L.code) {
         SegLaunch s = {};
         s.nseg = 2;
         s.n_in = f->H;
         s.x = x;
-        s.do_norm = norm;
+        s.do_norm = pend ? 3 : norm;
         s.norm_w = norm_w;
         s.eps = eps;
+        if (pend) {
+            s.am_val = const_cast<float*>(pend);
+            s.xn_out = pend_sum;
+        }
         s.seg[0] = seg_of(f->g, EPI_SWIGLU, w.g, nullptr);
         s.seg[1] = seg_of(f->u, EPI_STORE, nullptr, nullptr);
         if (draco_seg_launch(s, st)) return fail(-1, "gate/up launch rejected");
@@ -522,12 +531,31 @@ bool ksplit_o(const DevModel* m, int l) {
            (o.L.n_out + 15) / 16 <= 128;
 }
 
+// Whether dense layer l's o projection runs split-K, leaving its residual
+// add to the gate/up launch (which forms the input plus the partials in its
+// RMSNorm prologue and stores it to w.xm): an o projection of 8 to 32
+// super-blocks per row (halves divisible by 4) and at most 128 tiles, and a
+// gate/up pair of one K-quant format (configs[2]: 2048x2048 Q4_K, the 4-wave
+// split-K launch).
+bool ksplit_o_dense(const DevModel* m, int l) {
+    const DevFfn* f = m->ffn[l];
+    if (!f || m->moe[l] || f->g->L.code != f->u->L.code) return false;
+    auto kq = [](const DracoMat* x) { return x->L.code == DRACO_Q4_K || x->L.code == DRACO_Q6_K; };
+    const DracoMat& o = *m->attn[l]->wo;
+    const int nb = o.L.n_in / 256;
+    return kq(f->g) && kq(&o) && o.L.n_in % 256 == 0 && nb >= 8 && nb <= 32 && (nb / 2) % 4 == 0 &&
+           (o.L.n_out + 15) / 16 <= 128;
+}
+
 // enqueue one llama layer on the device (x in w.x, updated in place; with
 // xin set the layer reads its input from xin and leaves its output in w.x):
 // qkv(+norm,+rope,+append), attention, merge, wo(+residual),
 // gate/up(+norm,+SwiGLU), down(+residual).  After a split-K down the output
 // is pending (w.x + the partials in w.pd) and the next layer's qkv launch
-// forms it (into w.xs), which wo then takes as its residual.
+// forms it (into w.xs), which wo then takes as its residual.  After a
+// split-K o projection (ksplit_o_dense) the gate/up launch forms the FFN
+// input into w.xm, the down projection's residual: the layer output is then
+// w.xm + the down's partials when the down is split-K too.
 int enqueue_layer(DevModel* m, int l, float eps, hipStream_t st, const float* xin = nullptr) {
     DevAttn* a = m->attn[l];
     DevFfn* f = m->ffn[l];
@@ -535,7 +563,9 @@ int enqueue_layer(DevModel* m, int l, float eps, hipStream_t st, const float* xi
     const int H = m->h;
     const float* x0 = xin ? xin : w.x;
     const bool pending = !xin && l > 0 && ksplit_down(m, l - 1);
-    if (int rc = enqueue_qkv(a, w, x0, 1, m->anorm[l], eps, m->state, l, st, pending)) return rc;
+    // a pending input's materialised part: w.xm after a split-K o projection
+    const float* xq = pending && ksplit_o_dense(m, l - 1) ? w.xm : x0;
+    if (int rc = enqueue_qkv(a, w, xq, 1, m->anorm[l], eps, m->state, l, st, pending)) return rc;
     if (dk_attention(w.q, a->kc, a->vc, w.part, w.cnt, w.att, m->state, l, a->NH, a->NKV, a->HD, a->max_t,
                      a->scale, st))
         return fail(-1, "attention launch");
@@ -558,10 +588,30 @@ int enqueue_layer(DevModel* m, int l, float eps, hipStream_t st, const float* xi
         if (draco_seg_launch(s, st)) return fail(-1, "gemv o (split-K)");
         return draco_moe_layer_enqueue(m->moe[l], base, m->fnorm[l], eps, w.x, nullptr, st, w.pd, w.xm);
     }
-    if (draco_gemv_launch(*a->wo, w.att, w.x, base, 0, H, st)) return fail(-1, "gemv o");
-    if (m->moe[l])  // RMSNorm, router, routed gate/up + SwiGLU, down + weighted combine + residual
-        return draco_moe_layer_enqueue(m->moe[l], w.x, m->fnorm[l], eps, w.x, w.x, st);
-    if (int rc = enqueue_gateup(f, w, w.x, 1, m->fnorm[l], eps, st)) return rc;
+    const bool kso = !m->moe[l] && ksplit_o_dense(m, l);
+    if (kso) {
+        // o split-K into w.pd (free: this layer's qkv consumed the down's)
+        SegLaunch s = {};
+        s.nseg = 1;
+        s.n_in = a->wo->L.n_in;
+        s.x = w.att;
+        s.ksplit = 2;
+        SegDesc& d = s.seg[0];
+        d.base = a->wo->dev;
+        d.L = a->wo->L;
+        d.row0 = 0;
+        d.row1 = H;
+        d.y = w.pd;
+        d.epi = EPI_STORE;
+        if (draco_seg_launch(s, st)) return fail(-1, "gemv o (split-K)");
+        if (int rc = enqueue_gateup(f, w, base, 1, m->fnorm[l], eps, st, w.pd, w.xm)) return rc;
+    } else {
+        if (draco_gemv_launch(*a->wo, w.att, w.x, base, 0, H, st)) return fail(-1, "gemv o");
+        if (m->moe[l])  // RMSNorm, router, routed gate/up + SwiGLU, down + weighted combine + residual
+            return draco_moe_layer_enqueue(m->moe[l], w.x, m->fnorm[l], eps, w.x, w.x, st);
+        if (int rc = enqueue_gateup(f, w, w.x, 1, m->fnorm[l], eps, st)) return rc;
+    }
+    const float* mid = kso ? w.xm : w.x;  // the FFN's input, the down's residual
     if (ksplit_down(m, l)) {
         SegLaunch s = {};
         s.nseg = 1;
@@ -578,7 +628,7 @@ int enqueue_layer(DevModel* m, int l, float eps, hipStream_t st, const float* xi
         if (draco_seg_launch(s, st)) return fail(-1, "gemv down (split-K)");
         return 0;
     }
-    if (draco_gemv_launch(*f->d, w.g, w.x, w.x, 0, H, st)) return fail(-1, "gemv down");
+    if (draco_gemv_launch(*f->d, w.g, w.x, mid, 0, H, st)) return fail(-1, "gemv down");
     return 0;
 }
 

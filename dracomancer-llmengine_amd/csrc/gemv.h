@@ -59,12 +59,13 @@ struct SegLaunch {
     // 0 none; 1 RMSNorm of x (norm_w, eps); 2 (Q4_K / Q6_K, one EPI_RESID
     // segment) the GDN gated rms of 128-wide groups: x = the scan's gated
     // output, scaled per group by rsqrt(sum of the group's 16 partial sums of
-    // squares in kc [group][64] / 128 + eps); 3 (Q4_K / Q6_K, no SwiGLU
-    // pair) RMSNorm of the pending residual x + p0 + p1, the two split-K
+    // squares in kc [group][64] / 128 + eps); 3 (Q4_K / Q6_K) RMSNorm of
+    // the pending residual x + p0 + p1, the two split-K
     // partials p at am_val ([2][n_in]), the sum stored to xn_out by block 0
     int do_norm;
     // 2: split-K (Q4_K / Q6_K, one EPI_STORE segment over the whole matrix,
-    // do_norm 0 or 2, 16 or 32 super-blocks per row):
+    // do_norm 0 or 2, 8 to 32 super-blocks per row with halves divisible by
+    // 8, or by 4 without the GNORM prologue):
     // y[r] = the first half's dot, y[n_out + r] = the second half's
     int ksplit;
     float eps;

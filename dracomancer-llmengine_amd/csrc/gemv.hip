@@ -978,8 +978,9 @@ template <int NW, int FM, bool DUAL>
 void launch_dq_m(SegLaunch& a, bool multi, int grid, hipStream_t st) {
     if (a.do_norm == 2) {  // GNORM: one residual segment (checked by seg_launch_dq)
         if constexpr (!DUAL) launch_dq<NW, FM, false, false, EPI_RESID, 2>(a, grid, st);
-    } else if (a.do_norm == 3) {  // PRES: per-tile epilogues (checked by seg_launch_dq)
-        if constexpr (!DUAL) launch_dq<NW, FM, false, true, EPI_RT, 3>(a, grid, st);
+    } else if (a.do_norm == 3) {  // PRES: per-tile epilogues, or the SwiGLU pair
+        if constexpr (DUAL) launch_dq<NW, FM, true, false, EPI_SWIGLU, 3>(a, grid, st);
+        else launch_dq<NW, FM, false, true, EPI_RT, 3>(a, grid, st);
     } else if (a.do_norm) {
         launch_dq_e<NW, FM, DUAL, 1>(a, multi, grid, st);
     } else {
@@ -1045,15 +1046,16 @@ int seg_launch_dq(SegLaunch& a, hipStream_t st) {
     // GNORM prologue: one residual segment (a store segment when split-K) over whole 128-wide groups
     if (a.do_norm == 2 && (a.nseg != 1 || a.seg[0].epi != (a.ksplit ? EPI_STORE : EPI_RESID) || n_in % 128 || !a.kc))
         return -1;
-    // PRES prologue: the partials of the pending residual; no SwiGLU pair
-    if (a.do_norm == 3 && (dual || !a.am_val)) return -1;
+    // PRES prologue: the partials of the pending residual
+    if (a.do_norm == 3 && !a.am_val) return -1;
     // split-K: one whole-matrix store segment, no prologue norm or the
-    // per-wave GNORM one, halves of NW-divisible super-block counts on the
-    // 8-wave kernel
+    // per-wave GNORM one; halves of 8-divisible super-block counts on the
+    // 8-wave kernel, of 4-divisible ones (no GNORM) on the 4-wave kernel
+    const int ks_nw = (nb / 2) % 8 == 0 ? 8 : ((nb / 2) % 4 == 0 && a.do_norm == 0 ? 4 : 0);
     if (a.ksplit) {
         const SegDesc& s0 = a.seg[0];
         if (a.ksplit != 2 || a.nseg != 1 || dual || (a.do_norm != 0 && a.do_norm != 2) || s0.epi != EPI_STORE ||
-            s0.row0 != 0 || s0.row1 != s0.L.n_out || nb < 16 || nb > 32 || (nb / 2) % 8)
+            s0.row0 != 0 || s0.row1 != s0.L.n_out || nb < 8 || nb > 32 || !ks_nw)
             return -1;
     }
     for (int i = a.nseg; i < SEG_MAX; i++) {  // unused slots: never selected by seg_of_tile
@@ -1092,6 +1094,13 @@ int seg_launch_dq(SegLaunch& a, hipStream_t st) {
         a.rot = tiles;
         a.kv_dim = a.seg[0].L.n_out;
         a.total_tiles = 2 * tiles;
+        if (ks_nw == 4) {  // 4-wave blocks: four per CU
+            const int cap4 = cu_count() * 4;
+            grid = 2 * tiles < cap4 ? 2 * tiles : cap4;
+            if (fm == 1) launch_dq1<4, 1, false, false, EPI_STORE, 0, false, true>(a, grid, st);
+            else launch_dq1<4, 2, false, false, EPI_STORE, 0, false, true>(a, grid, st);
+            return 0;
+        }
         grid = 2 * tiles < cap ? 2 * tiles : cap;
         if (a.do_norm == 2) {
             if (fm == 1) launch_dq1<8, 1, false, false, EPI_STORE, 2, false, true>(a, grid, st);
