@@ -157,7 +157,7 @@ def test_direct_ops_match_oracle(oracle):
 
 @pytest.mark.parametrize("hd,nh,nkv", [(128, 3, 1), (128, 2, 2), (64, 5, 1)])
 def test_attn_op_head_shapes_match_oracle(oracle, hd, nh, nkv):
-    """The per-head attention kernel and its last-block split merge at head
+    """The per-head attention kernel and its split merge kernel at head
     dim 128 (GQA ratios 3 and 1) and head dim 64 with ratio 5 (shapes the
     grouped kernel does not take; m6_llama_attn_op takes head dims 64 and
     128): 48 tokens through m6_llama_attn_op with a 256-row cache (8 splits),
