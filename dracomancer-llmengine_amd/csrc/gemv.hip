@@ -226,10 +226,15 @@ __global__ __launch_bounds__(64 * NW) void k_dq(const SegKArgs a) {
     // ([2][n_in]); x = (x + p0) + p1, written to a.xn_out by block 0
     float4 pv0[NORM >= 2 ? XP_MAXV : 1], pv1[NORM >= 2 ? XP_MAXV : 1], pv2[NORM == 2 ? XP_MAXV : 1],
         pv3[NORM == 2 ? XP_MAXV : 1];
+    // KS with one tile per block: the block multiplies one half of x only,
+    // so only that half is loaded and digitised (chunks q of NT float4s;
+    // chunk q holds super-blocks [q NW, q NW + NW), and NW divides the half)
+    const bool kown = KS && G == total;
+    const int kq_n = kown ? (nb >> 1) / NW : XP_MAXV, kq_lo = kown ? khalf(bx) * kq_n : 0;
 #pragma unroll
     for (int q = 0; q < XP_MAXV; q++) {
         const int i4 = tid + q * NT;
-        if (i4 < n4) {
+        if (i4 < n4 && q >= kq_lo && q < kq_lo + kq_n) {
             xv[q] = ld4(a.x + 4 * i4);
             if ((NORM == 1 || NORM == 3) && a.norm_w) wv[q] = ld4(a.norm_w + 4 * i4);
             if constexpr (NORM == 3) {
@@ -313,6 +318,7 @@ __global__ __launch_bounds__(64 * NW) void k_dq(const SegKArgs a) {
     for (int q = 0; q < XP_MAXV; q++) {
         const int i4 = tid + q * NT;
         if (i4 >= n4) break;
+        if (q < kq_lo || q >= kq_lo + kq_n) continue;
         float4 v = xv[q];
         if constexpr (NORM == 3) {
             const float4 p = pv0[q], p2 = pv1[q];
