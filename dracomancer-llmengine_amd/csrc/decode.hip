@@ -390,11 +390,17 @@ __global__ __launch_bounds__(256) void k_attn_merge(const float* __restrict__ pa
 // before the first FMA, so the kernel costs two dependent L2 round trips.
 // With `gate` set the result is multiplied by sigmoid(gate[h * gstride + d])
 // (qwen35 full attention, src/m6_layer.c:500-505).
+// Block b merges q head h = (b % NKV) rep + b / NKV.  Blocks are dispatched
+// round-robin over the XCDs, and k_attn_part's block (g, s) is linear block
+// g + NKV s, so with NKV = 8 every split of kv head g ran on XCD g; this
+// order puts the merges of g's q heads on XCD g too, where the partials are
+// still in L2.
 template <int MAXS>
 __global__ __launch_bounds__(256) void k_attn_combine(const float* __restrict__ part, float* __restrict__ out,
                                                       int nsplit, int HD, const float* __restrict__ gate,
-                                                      int gstride) {
-    const int h = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
+                                                      int gstride, int NKV) {
+    const int b = blockIdx.x, rep = gridDim.x / NKV;
+    const int h = (b % NKV) * rep + b / NKV, tid = threadIdx.x, lane = tid & 63;
     const float* ph = part + (size_t)h * nsplit * (HD + 2);
     // every load unconditional (clamped split index), so all of them are in
     // flight together: one memory round trip
@@ -657,9 +663,12 @@ int dk_attention(const float* q, const float* kc, const float* vc, float* part, 
     else
         return -1;
     const dim3 cg(NH), cb(HD);
-    if (nsplit <= 16) hipLaunchKernelGGL(k_attn_combine<16>, cg, cb, 0, st, part, out, nsplit, HD, gate, gstride);
-    else if (nsplit <= 32) hipLaunchKernelGGL(k_attn_combine<32>, cg, cb, 0, st, part, out, nsplit, HD, gate, gstride);
-    else hipLaunchKernelGGL(k_attn_combine<64>, cg, cb, 0, st, part, out, nsplit, HD, gate, gstride);
+    if (nsplit <= 16)
+        hipLaunchKernelGGL(k_attn_combine<16>, cg, cb, 0, st, part, out, nsplit, HD, gate, gstride, NKV);
+    else if (nsplit <= 32)
+        hipLaunchKernelGGL(k_attn_combine<32>, cg, cb, 0, st, part, out, nsplit, HD, gate, gstride, NKV);
+    else
+        hipLaunchKernelGGL(k_attn_combine<64>, cg, cb, 0, st, part, out, nsplit, HD, gate, gstride, NKV);
     return 0;
 }
 
