@@ -1219,9 +1219,13 @@ int draco_llama_generate(const void* layers_v, int n_layer, int h, float eps, co
         }
         // GEN_STEPS generated tokens in one graph (the state advances on the
         // device, so consecutive steps capture as they run): one graph launch
-        // per GEN_STEPS tokens instead of per token (configs[2] 2,228 -> 2,249
-        // tok/s same-box with 16; 4: 2,244)
-        if (n_gen >= GEN_STEPS) {
+        // per GEN_STEPS tokens instead of per token (configs[2], 98 kernels a
+        // step: 2,219 -> 2,243 tok/s same-box).  Steps of more kernels keep one
+        // graph per token: configs[0] (194 a step) and configs[3] were 0.1-0.2%
+        // slower with 16-step graphs.
+        size_t step_nodes = 0;
+        DRACO_HIP(hipGraphGetNodes(G.gg[1], nullptr, &step_nodes));
+        if (n_gen >= GEN_STEPS && step_nodes * GEN_STEPS <= 2048) {
             DRACO_HIP(hipStreamBeginCapture(st, hipStreamCaptureModeRelaxed));
             int rc = 0;
             for (int k = 0; k < GEN_STEPS && !rc; k++) rc = step(true);
