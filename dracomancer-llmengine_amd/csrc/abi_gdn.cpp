@@ -37,14 +37,24 @@ int gdn_host(const float* QKV, const float* Z, const float* B, const float* G, c
     float* ds = p; p += ns;
     float* dpss = p; p += npss;
     float* don = p;
+    // a state the per-layer GDN op holds on the device is scanned in place
+    // there (the caller's arrays hold only its sample); any other is uploaded
+    float *rs = nullptr, *rt = nullptr;
+    const bool resident = draco_gdn_state_current(S, tail, ns, nt, &rs, &rt);
+    if (resident) {
+        ds = rs;
+        dt = rt;
+    }
     DRACO_HIP(hipMemcpyAsync(dq, QKV, sizeof(float) * nq, hipMemcpyHostToDevice, st));
     DRACO_HIP(hipMemcpyAsync(dz, Z, sizeof(float) * nz, hipMemcpyHostToDevice, st));
     DRACO_HIP(hipMemcpyAsync(db, B, sizeof(float) * nbg, hipMemcpyHostToDevice, st));
     DRACO_HIP(hipMemcpyAsync(dg, G, sizeof(float) * nbg, hipMemcpyHostToDevice, st));
     DRACO_HIP(hipMemcpyAsync(dc, conv, sizeof(float) * nc, hipMemcpyHostToDevice, st));
     DRACO_HIP(hipMemcpyAsync(dn, ssm_norm, sizeof(float) * 128, hipMemcpyHostToDevice, st));
-    DRACO_HIP(hipMemcpyAsync(dt, tail, sizeof(float) * nt, hipMemcpyHostToDevice, st));
-    DRACO_HIP(hipMemcpyAsync(ds, S, sizeof(float) * ns, hipMemcpyHostToDevice, st));
+    if (!resident) {
+        DRACO_HIP(hipMemcpyAsync(dt, tail, sizeof(float) * nt, hipMemcpyHostToDevice, st));
+        DRACO_HIP(hipMemcpyAsync(ds, S, sizeof(float) * ns, hipMemcpyHostToDevice, st));
+    }
     a.QKV = dq;
     a.Z = dz;
     a.B = db;
@@ -66,6 +76,8 @@ int gdn_host(const float* QKV, const float* Z, const float* B, const float* G, c
     DRACO_HIP(hipMemcpyAsync(S, ds, sizeof(float) * ns, hipMemcpyDeviceToHost, st));
     DRACO_HIP(hipMemcpyAsync(tail, dt, sizeof(float) * nt, hipMemcpyDeviceToHost, st));
     DRACO_HIP(hipStreamSynchronize(st));
+    // the caller's arrays now hold the whole state, as the mirrors do
+    if (resident) draco_gdn_state_written(S, ds);
     return 0;
 }
 

@@ -190,7 +190,9 @@ DevAttn* get_attn(const M6LlamaAttnP* p) {
     if (it != c.end() && it->second->epoch == epoch() && memcmp(&it->second->snap, p, sizeof(*p)) == 0)
         return it->second;
     const int NH = p->n_head, NKV = p->n_kv, HD = p->head_dim, H = p->hidden;
-    if (NH <= 0 || NKV <= 0 || NH % NKV || NH / NKV > 8 || (HD != 64 && HD != 128) || p->rot > HD ||
+    // src/m6_engine.c:425-511 takes any GQA ratio and head dim; the device
+    // attention serves every even head dim up to 512 (decode.h)
+    if (NH <= 0 || NKV <= 0 || NH % NKV || HD < 2 || HD > 512 || (HD & 1) || p->rot < 0 || p->rot > HD ||
         (p->rot & 1) || p->max_t <= 0) {
         fail(-1, "m6_llama_attn_op: unsupported shape NH=%d NKV=%d HD=%d rot=%d", NH, NKV, HD, p->rot);
         return nullptr;
@@ -512,7 +514,7 @@ bool ksplit_down(const DevModel* m, int l) {
     const DracoMat& d = *m->ffn[l]->d;
     const int nb = d.L.n_in / 256;
     if ((d.L.code != DRACO_Q4_K && d.L.code != DRACO_Q6_K) || d.L.n_in % 256 || (nb != 16 && nb != 32) ||
-        (d.L.n_out + 15) / 16 > 128)
+        !draco_dq_ksplit_waves(d.L.n_in, 0) || (d.L.n_out + 15) / 16 > 128)
         return false;
     const DevAttn* n = m->attn[l + 1];
     auto kq = [](const DracoMat* x) { return x->L.code == DRACO_Q4_K || x->L.code == DRACO_Q6_K; };
@@ -528,23 +530,21 @@ bool ksplit_o(const DevModel* m, int l) {
     const DracoMat& o = *m->attn[l]->wo;
     const int nb = o.L.n_in / 256;
     return (o.L.code == DRACO_Q4_K || o.L.code == DRACO_Q6_K) && o.L.n_in % 256 == 0 && (nb == 16 || nb == 32) &&
-           (o.L.n_out + 15) / 16 <= 128;
+           draco_dq_ksplit_waves(o.L.n_in, 0) && (o.L.n_out + 15) / 16 <= 128;
 }
 
 // Whether dense layer l's o projection runs split-K, leaving its residual
 // add to the gate/up launch (which forms the input plus the partials in its
-// RMSNorm prologue and stores it to w.xm): an o projection of 8 to 32
-// super-blocks per row (halves divisible by 4) and at most 128 tiles, and a
-// gate/up pair of one K-quant format (configs[2]: 2048x2048 Q4_K, the 4-wave
-// split-K launch).
+// RMSNorm prologue and stores it to w.xm): an o projection whose rows a
+// split-K instance covers (draco_dq_ksplit_waves: 8, 16 or 32 super-blocks)
+// and at most 128 tiles, and a gate/up pair of one K-quant format
+// (configs[2]: 2048x2048 Q4_K, the 4-wave split-K launch).
 bool ksplit_o_dense(const DevModel* m, int l) {
     const DevFfn* f = m->ffn[l];
     if (!f || m->moe[l] || f->g->L.code != f->u->L.code) return false;
     auto kq = [](const DracoMat* x) { return x->L.code == DRACO_Q4_K || x->L.code == DRACO_Q6_K; };
     const DracoMat& o = *m->attn[l]->wo;
-    const int nb = o.L.n_in / 256;
-    return kq(f->g) && kq(&o) && o.L.n_in % 256 == 0 && nb >= 8 && nb <= 32 && (nb / 2) % 4 == 0 &&
-           (o.L.n_out + 15) / 16 <= 128;
+    return kq(f->g) && kq(&o) && draco_dq_ksplit_waves(o.L.n_in, 0) && (o.L.n_out + 15) / 16 <= 128;
 }
 
 // enqueue one llama layer on the device (x in w.x, updated in place; with
@@ -636,6 +636,16 @@ bool has_moe(const DevModel* m) {
     for (const MoeLayer* p : m->moe)
         if (p) return true;
     return false;
+}
+
+// Whether the model's tokens can go through the batched (chunked) prefill:
+// dense FFNs and attention shapes its kernel serves; other models feed
+// their prompts through token-serial decode steps.
+bool chunk_ok(const DevModel* m) {
+    if (has_moe(m)) return false;
+    for (int l = 0; l < m->n_layer; l++)
+        if (!pf_attention_ok(m->attn[l]->NH, m->attn[l]->NKV, m->attn[l]->HD)) return false;
+    return true;
 }
 
 // ---- chunked prefill (configs of the reference's forward_chunk,
@@ -734,8 +744,8 @@ int enqueue_prefill_layer(DevModel* m, int l, int T, int pos0, int row0, float e
 // host tlen counters are not advanced here).  The last token's hidden state
 // is left in pf.X row (last chunk's T - 1); returns that T (0 on error).
 int enqueue_prefill(DevModel* m, const DracoMat* em, const int* ids, int n, int pos0, float eps, hipStream_t st) {
-    if (has_moe(m)) {
-        fail(-1, "chunked prefill: MoE layers are fed token by token (draco_llama_generate does so)");
+    if (!chunk_ok(m)) {
+        fail(-1, "chunked prefill: MoE layers and attention shapes outside the batched kernel go token by token");
         return 0;
     }
     const int C = g_prefill_chunk;
@@ -1139,8 +1149,9 @@ int draco_llama_generate(const void* layers_v, int n_layer, int h, float eps, co
     // prompt[0 .. n_prompt - 1) goes through the chunked prefill when enabled
     // (the last prompt token goes through the first decode step, which also
     // runs the head); the token cursor then starts past those tokens
-    // (MoE models feed the prompt through token-serial decode steps)
-    const int n_chunked = (g_prefill_chunk > 0 && n_prompt - 1 >= 2 && !has_moe(m)) ? n_prompt - 1 : 0;
+    // (MoE models and attention shapes outside the batched prefill kernel
+    // feed the prompt through token-serial decode steps)
+    const int n_chunked = (g_prefill_chunk > 0 && n_prompt - 1 >= 2 && chunk_ok(m)) ? n_prompt - 1 : 0;
     if (n_chunked && ensure_pf(m, g_prefill_chunk)) return report(-2, "draco_llama_generate (prefill buffers)");
     ht[ntok + 8] = n_chunked;
     DRACO_HIP(hipMemcpyAsync(dtok, ht.data(), sizeof(int) * (ntok + 64), hipMemcpyHostToDevice, st));
@@ -1321,11 +1332,31 @@ int draco_llama_prefill(const void* layers_v, int n_layer, int h, float eps, con
         return report(-2, "draco_llama_prefill");
     }
     DRACO_HIP(hipMemcpyAsync(dids, ids, sizeof(int) * n, hipMemcpyHostToDevice, st));
-    const int last = enqueue_prefill(m, em, dids, n, pos, eps, st);
-    g_prefill_chunk = saved;
-    if (last <= 0) return report(-1, "draco_llama_prefill");
-    if (out_x)
-        DRACO_HIP(hipMemcpyAsync(out_x, m->pf.X + (size_t)(last - 1) * h, sizeof(float) * h, hipMemcpyDeviceToHost, st));
+    if (!chunk_ok(m)) {
+        // token by token through the decode layers (the state of n
+        // m6_forward_token calls): embedding of ids[cursor], every layer,
+        // then the cursor and every tlen advance
+        g_prefill_chunk = saved;
+        int* cursor = dids + n + 8;
+        const int zero = 0;
+        DRACO_HIP(hipMemcpyAsync(cursor, &zero, sizeof(int), hipMemcpyHostToDevice, st));
+        if (int rc = check_positions(m, pos, n)) return report(rc, "draco_llama_prefill");
+        if (int rc = upload_state(m, pos, st)) return report(rc, "draco_llama_prefill");
+        for (int i = 0; i < n; i++) {
+            dk_embed(*em, dids, cursor, m->w.x, st);
+            for (int l = 0; l < n_layer; l++)
+                if (int rc = enqueue_layer(m, l, eps, st)) return report(rc, "draco_llama_prefill");
+            dk_advance(m->state, n_layer, cursor, st);
+        }
+        if (out_x) DRACO_HIP(hipMemcpyAsync(out_x, m->w.x, sizeof(float) * h, hipMemcpyDeviceToHost, st));
+    } else {
+        const int last = enqueue_prefill(m, em, dids, n, pos, eps, st);
+        g_prefill_chunk = saved;
+        if (last <= 0) return report(-1, "draco_llama_prefill");
+        if (out_x)
+            DRACO_HIP(hipMemcpyAsync(out_x, m->pf.X + (size_t)(last - 1) * h, sizeof(float) * h,
+                                     hipMemcpyDeviceToHost, st));
+    }
     hipError_t e = hipStreamSynchronize(st);
     if (e != hipSuccess) return report(fail(-2, "draco_llama_prefill: %s", hipGetErrorString(e)), "draco_llama_prefill");
     for (int l = 0; l < n_layer; l++) *m->attn[l]->snap.tlen += n;

@@ -159,7 +159,7 @@ int enqueue_moe(ExpertSet* s, const float* x, float* out, const float* resid, Mo
 }
 
 int check_moe(int n_exp, int n_used, int inter, int n_in, int n_out) {
-    if (n_exp < 1 || n_exp > MOE_EXP_MAX || n_used < 1 || n_used > n_exp || n_used > 16)
+    if (n_exp < 1 || n_exp > MOE_EXP_MAX || n_used < 1 || n_used > n_exp || n_used > MOE_USED_MAX)
         return fail(-1, "m6_granite_moe: n_exp %d / n_used %d not served", n_exp, n_used);
     if (inter % 256 || n_in % 256 || n_out % 16)
         return fail(-1, "m6_granite_moe: shape inter %d n_in %d n_out %d not served", inter, n_in, n_out);

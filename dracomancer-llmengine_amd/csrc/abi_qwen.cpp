@@ -228,7 +228,7 @@ int enqueue_proj_ks(const DracoMat* m, const float* x, int n_in, float* pd, cons
 bool ks_ok(const DracoMat* m) {
     const int nb = m->L.n_in / 256;
     return (m->L.code == DRACO_Q4_K || m->L.code == DRACO_Q6_K) && m->L.n_in % 256 == 0 && (nb == 16 || nb == 32) &&
-           (m->L.n_out + 15) / 16 <= 128;
+           draco_dq_ksplit_waves(m->L.n_in, 2) && (m->L.n_out + 15) / 16 <= 128;
 }
 
 // ------------------------------------------------------------------ GDN --
@@ -755,6 +755,17 @@ int qstack_alloc(std::vector<void*>& keep, float** p, size_t floats) {
     return 0;
 }
 
+// Frees a stack's device buffers and pinned state (its mirrors stay
+// registered: they hold the caller's state).
+void release_qstack(QStack* s) {
+    if (!s) return;
+    hipStreamSynchronize(stream());
+    for (void* p : s->allocs) hipFree(p);
+    for (void* p : s->pf_allocs) hipFree(p);
+    if (s->hstate) hipHostFree(s->hstate);
+    delete s;
+}
+
 QStack* build_qstack(const QStackLayer* layers, int n_layer, int h) {
     if (h != QH) {
         fail(-1, "qwen stack: hidden %d (the qwen35 ops fix it at %d)", h, QH);
@@ -780,13 +791,15 @@ QStack* build_qstack(const QStackLayer* layers, int n_layer, int h) {
         if (same && slot->epoch == epoch()) return slot;
     }
     if (slot) {  // rebuild: release the old token buffers (mirrors stay registered)
-        hipStreamSynchronize(stream());
-        for (void* p : slot->allocs) hipFree(p);
-        for (void* p : slot->pf_allocs) hipFree(p);
-        delete slot;
+        release_qstack(slot);
         slot = nullptr;
     }
-    QStack* s = new QStack();
+    // a stack that fails part-way is released on the way out
+    struct Building {
+        QStack* s;
+        ~Building() { release_qstack(s); }
+    } building{new QStack()};
+    QStack* s = building.s;
     s->descs.assign(layers, layers + n_layer);
     s->L.resize(n_layer);
     s->n_layer = n_layer;
@@ -859,13 +872,19 @@ QStack* build_qstack(const QStackLayer* layers, int n_layer, int h) {
         qstack_alloc(k, &s->xs, QH) || qstack_alloc(k, &s->pd, 2 * QH) ||
         qstack_alloc(k, &s->glog, 2 * (size_t)std::max(s->max_vh, 1)))
         return nullptr;
-    if (hipMalloc(&s->state, sizeof(int) * 16) != hipSuccess ||
-        hipHostMalloc(&s->hstate, sizeof(int) * 16, hipHostMallocDefault) != hipSuccess) {
+    if (hipMalloc(&s->state, sizeof(int) * 16) != hipSuccess) {
+        s->state = nullptr;
         fail(-2, "qwen stack: state allocation failed");
         return nullptr;
     }
     k.push_back(s->state);
+    if (hipHostMalloc(&s->hstate, sizeof(int) * 16, hipHostMallocDefault) != hipSuccess) {
+        s->hstate = nullptr;
+        fail(-2, "qwen stack: state allocation failed");
+        return nullptr;
+    }
     s->epoch = epoch();
+    building.s = nullptr;
     slot = s;
     return s;
 }
@@ -1092,6 +1111,32 @@ int enqueue_qprefill(QStack* s, const DracoMat* em, const int* ids, int n, int p
 }
 
 }  // namespace
+
+bool draco_gdn_state_current(const float* ssm, const float* tail, size_t ns, size_t nt, float** dS, float** dT) {
+    *dS = *dT = nullptr;
+    auto it = op_states().find(ssm);
+    if (it == op_states().end()) return false;
+    OpState& os = it->second;
+    bool ok = os.samp.size() == QSAMP && ns >= QSAMP;
+    for (int i = 0; ok && i < QSAMP; i++) ok = fbits(ssm[i]) == os.samp[i];
+    bool fs = true, ft = true;
+    float* s = ok ? (float*)get_mirror(ssm, sizeof(float) * ns, &fs) : nullptr;
+    float* t = ok ? (float*)get_mirror(tail, sizeof(float) * nt, &ft) : nullptr;
+    if (!s || !t || fs || ft || s != os.dev) {
+        op_states().erase(it);
+        return false;
+    }
+    *dS = s;
+    *dT = t;
+    return true;
+}
+
+void draco_gdn_state_written(const float* ssm, const float* dS) {
+    OpState& os = op_states()[ssm];
+    os.dev = dS;
+    os.samp.resize(QSAMP);
+    for (int i = 0; i < QSAMP; i++) os.samp[i] = fbits(ssm[i]);
+}
 
 extern "C" {
 

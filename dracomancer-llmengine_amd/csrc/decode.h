@@ -7,15 +7,20 @@
 constexpr int ARGMAX_BLOCKS = 256;
 
 // The group-shared attention kernel serves GQA groups of rep = NH / NKV q
-// heads with rep a power of two in [2, 16] and HD in {128, 256}; other shapes
-// run the per-head kernel.  (At HD 64 the per-head kernel is faster on MI355X:
-// its rows are 256 bytes, so the re-read K / V rows stay in L2 and the
-// per-row lane-exchange cost of the grouped kernel dominates.)
+// heads with rep a power of two in [2, 8] at HD 128 and in [2, 16] at HD 256;
+// the per-head kernel serves HD in {64, 128, 256} with rep up to 16; every
+// other shape (any head dim up to 512, any rep) runs the generic kernel.  (At
+// HD 64 the per-head kernel is faster on MI355X: its rows are 256 bytes, so
+// the re-read K / V rows stay in L2 and the per-row lane-exchange cost of the
+// grouped kernel dominates.)
 static inline bool attn_grouped(int NH, int NKV, int HD) {
     if (NKV < 1 || NH % NKV) return false;
     const int rep = NH / NKV;
-    if (rep < 2 || rep > 16 || (rep & (rep - 1))) return false;
-    return HD == 128 || HD == 256;
+    if (rep < 2 || (rep & (rep - 1))) return false;
+    return (HD == 128 && rep <= 8) || (HD == 256 && rep <= 16);
+}
+static inline bool attn_per_head(int NH, int NKV, int HD) {
+    return NKV >= 1 && NH % NKV == 0 && NH / NKV <= 16 && (HD == 64 || HD == 128 || HD == 256);
 }
 
 // Number of T-splits of the decode attention for a cache of max_t rows.
@@ -37,7 +42,8 @@ void dk_rmsnorm(const float* x, const float* w, float* out, int h, float eps, hi
 void dk_rope_append(float* q, const float* k, const float* v, float* kc, float* vc, const float* tab,
                     const int* state, int layer, int NH, int NKV, int HD, int rot, hipStream_t st);
 // split-T partials + merge; `count` is unused (kept for the caller's buffer plumbing)
-// HD in {64, 128, 256}; NH / NKV <= 16.  gate (nullable): out[h][d] *= sigmoid(gate[h * gstride + d]).
+// Any NH divisible by NKV and any even HD up to 512.  gate (nullable):
+// out[h][d] *= sigmoid(gate[h * gstride + d]).
 int dk_attention(const float* q, const float* kc, const float* vc, float* part, unsigned* count, float* out,
                  const int* state, int layer, int NH, int NKV, int HD, int max_t, float scale, hipStream_t st,
                  const float* gate = nullptr, int gstride = 0);

@@ -123,8 +123,6 @@ __global__ __launch_bounds__(256) void k_rope_append(float* __restrict__ q, cons
 // partial (o[HD], m, l); k_attn_combine merges the splits:
 //   out[h] = sum_s o_s e^(m_s - M) / sum_s l_s e^(m_s - M),  M = max_s m_s
 // which equals the reference's single-pass softmax up to fp32 rounding.
-constexpr int REPMAX = 16;
-
 template <int HD>
 __global__ __launch_bounds__(1024) void k_attn_part(const float* __restrict__ q, const float* __restrict__ kc,
                                                     const float* __restrict__ vc, float* __restrict__ part,
@@ -194,6 +192,66 @@ __global__ __launch_bounds__(1024) void k_attn_part(const float* __restrict__ q,
     if (lane == 0) {
         pp[HD] = m_run;
         pp[HD + 1] = l_run;
+    }
+}
+
+// Any head dim (even, up to 512) and any GQA ratio: block h is q head h
+// (kv head h / rep, src/m6_engine.c:482-505), 256 threads over the whole row
+// range.  Rows go in sub-chunks of ATT_ANY_CH: wave w scores rows w, w + 4,
+// ... (lanes stride the head dims, then a wave sum) into LDS; the
+// sub-chunk's maximum rescales the running (m, l) and output (online
+// softmax); thread d accumulates p V[t][d] for dims d and d + 256.  It
+// writes the normalised output (times the optional gate) directly: this is
+// the fallback for shapes the tuned kernels above and below do not serve.
+constexpr int ATT_ANY_CH = 64;
+
+__global__ __launch_bounds__(256) void k_attn_any(const float* __restrict__ q, const float* __restrict__ kc,
+                                                  const float* __restrict__ vc, float* __restrict__ out,
+                                                  const int* __restrict__ st, int layer, int NH, int NKV, int HD,
+                                                  float scale, const float* __restrict__ gate, int gstride) {
+    __shared__ float qs[512];
+    __shared__ float sc[ATT_ANY_CH];
+    const int h = blockIdx.x, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int rep = NH / NKV, g = h / rep, KD = NKV * HD;
+    const int Tn = st[1 + layer] + 1;
+    for (int d = tid; d < HD; d += 256) qs[d] = q[(size_t)h * HD + d];
+    __syncthreads();
+    float m_run = -INFINITY, l_run = 0.f, o0 = 0.f, o1 = 0.f;
+    for (int c0 = 0; c0 < Tn; c0 += ATT_ANY_CH) {
+        const int nr = min(ATT_ANY_CH, Tn - c0);
+        for (int r = w; r < nr; r += 4) {
+            const float* kr = kc + (size_t)(c0 + r) * KD + (size_t)g * HD;
+            float acc = 0.f;
+            for (int d = lane; d < HD; d += 64) acc = fmaf(qs[d], kr[d], acc);
+            acc = wave_sum(acc);
+            if (lane == 0) sc[r] = acc * scale;
+        }
+        __syncthreads();
+        float cm = -INFINITY;
+        for (int r = 0; r < nr; r++) cm = fmaxf(cm, sc[r]);
+        const float mn = fmaxf(m_run, cm);
+        const float corr = m_run > -INFINITY ? expf(m_run - mn) : 0.f;
+        float ls = 0.f;
+        o0 *= corr;
+        o1 *= corr;
+        for (int r = 0; r < nr; r++) {
+            const float p = expf(sc[r] - mn);
+            ls += p;
+            const float* vr = vc + (size_t)(c0 + r) * KD + (size_t)g * HD;
+            if (tid < HD) o0 = fmaf(p, vr[tid], o0);
+            if (tid + 256 < HD) o1 = fmaf(p, vr[tid + 256], o1);
+        }
+        l_run = l_run * corr + ls;
+        m_run = mn;
+        __syncthreads();  // sc is rewritten by the next sub-chunk
+    }
+    const float il = 1.f / l_run;
+    for (int k = 0; k < 2; k++) {
+        const int d = tid + 256 * k;
+        if (d >= HD) break;
+        float r = (k ? o1 : o0) * il;
+        if (gate) r *= 1.f / (1.f + expf(-gate[(size_t)h * gstride + d]));
+        out[(size_t)h * HD + d] = r;
     }
 }
 
@@ -588,7 +646,7 @@ __global__ __launch_bounds__(64) void k_argmax_final(const float* __restrict__ p
     int idx = 0x7fffffff;
     for (int i = threadIdx.x; i < nb; i += 64) am_merge(v, idx, pv[i], pi[i]);
     group_argmax<64>(v, idx);
-    // every value NaN: token 0 (a first-index '>' scan), never an out-of-range row
+    // no partial at all: token 0, never an out-of-range row
     if (threadIdx.x == 0) out[slotp ? slotp[0] + 1 : slot] = idx == 0x7fffffff ? 0 : idx;
 }
 
@@ -633,8 +691,13 @@ int dk_attention(const float* q, const float* kc, const float* vc, float* part, 
                  const int* state, int layer, int NH, int NKV, int HD, int max_t, float scale, hipStream_t st,
                  const float* gate, int gstride) {
     (void)count;
+    if (NKV < 1 || NH < NKV || NH % NKV || HD < 2 || HD > 512 || (HD & 1)) return -1;
     const int rep = NH / NKV;
-    if (rep < 1 || rep > REPMAX || NH % NKV) return -1;
+    if (!attn_grouped(NH, NKV, HD) && !attn_per_head(NH, NKV, HD)) {
+        hipLaunchKernelGGL(k_attn_any, dim3(NH), dim3(256), 0, st, q, kc, vc, out, state, layer, NH, NKV, HD, scale,
+                           gate, gstride);
+        return 0;
+    }
     const int nsplit = attn_nsplit(max_t, NH, NKV, HD);
     if (attn_grouped(NH, NKV, HD)) {
         const dim3 grid(NKV, nsplit);
@@ -643,8 +706,9 @@ int dk_attention(const float* q, const float* kc, const float* vc, float* part, 
         hipLaunchKernelGGL((k_attn_gqa<H_, R_>), grid, dim3(256), 0, st, q, kc, vc, part, state, layer, NKV, \
                            nsplit, scale);                                                                \
     } else
-        // the shapes attn_grouped sends here: llama attention (head dim 128,
-        // GQA <= 8) and qwen35 full attention (head dim 256, 2 kv heads)
+        // the shapes attn_grouped sends here: head dim 128 with GQA <= 8
+        // (llama attention) and head dim 256 with GQA <= 16 (qwen35 full
+        // attention)
         GQA_CASE(128, 2) GQA_CASE(128, 4) GQA_CASE(128, 8)
         GQA_CASE(256, 2) GQA_CASE(256, 4) GQA_CASE(256, 8) GQA_CASE(256, 16) return -1;
 #undef GQA_CASE

@@ -136,8 +136,12 @@ __device__ __forceinline__ int rows_sum_i(int v) { return rows_reduce(v, OpAdd{}
 
 // (value, index) maximum over each aligned group of G lanes, ties to the lower
 // index (the first maximum in index order, whatever order the pairs meet in).
+// NaN ranks above every number, as in np.argmax (src/smol_engine.py:212):
+// any NaN makes the result the first NaN's index.
 __device__ __forceinline__ void am_merge(float& v, int& i, float v2, int i2) {
-    if (v2 > v || (v2 == v && i2 < i)) {
+    const bool n1 = v != v, n2 = v2 != v2;
+    const bool take = n2 ? (!n1 || i2 < i) : (!n1 && (v2 > v || (v2 == v && i2 < i)));
+    if (take) {
         v = v2;
         i = i2;
     }

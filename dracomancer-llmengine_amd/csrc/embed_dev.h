@@ -9,6 +9,9 @@
 // decoders: (d*sc)*q for Q6_K, d*sc*q - dmin*m for Q4_K, q*d for Q8_0.
 __device__ __forceinline__ float embed_value(const uint8_t* __restrict__ base, const DracoLayout& L, int tok, int p) {
 #pragma clang fp contract(off)  // each product rounded on its own, as the host decoders
+    // a row outside the matrix reads row 0 (host entry points reject such ids;
+    // this keeps a device-produced index from addressing past the weights)
+    if ((unsigned)tok >= (unsigned)L.n_out) tok = 0;
     const int n_in = L.n_in, nb = L.nb;
     const size_t blk = (size_t)tok * nb + p / draco_block_values(L.code);
     float val = 0.f;

@@ -49,3 +49,15 @@ int draco_gdn_scan_launch(const GdnArgs& a, hipStream_t st);
 // One decode token (T must be 1): the scan step with beta = sigmoid(xn.bw),
 // decay = exp(softplus(xn.aw + dt) * a), xn = rms(h1) * attn_norm (eps 1e-6).
 int draco_gdn_step_launch(const GdnArgs& a, hipStream_t st);
+
+// State residency shared by m6_gdn_attn (abi_qwen.cpp) and m6_gdn_scan
+// (abi_gdn.cpp).  The per-layer GDN op keeps the caller's ssm / tail on the
+// device and writes back only a sample of the state; a scan on the same
+// arrays must start from the device state.  draco_gdn_state_current returns
+// true with the mirrors when the caller's ssm still carries the op's last
+// written-back sample (the device holds the current state); otherwise false,
+// and the op's record is dropped so that its next call uploads the caller's
+// arrays.  draco_gdn_state_written records, after a scan on those mirrors
+// wrote the whole state back to the caller, the sample the caller now holds.
+bool draco_gdn_state_current(const float* ssm, const float* tail, size_t ns, size_t nt, float** dS, float** dT);
+void draco_gdn_state_written(const float* ssm, const float* dS);

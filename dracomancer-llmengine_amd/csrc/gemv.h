@@ -64,8 +64,7 @@ struct SegLaunch {
     // partials p at am_val ([2][n_in]), the sum stored to xn_out by block 0
     int do_norm;
     // 2: split-K (Q4_K / Q6_K, one EPI_STORE segment over the whole matrix,
-    // do_norm 0 or 2, 8 to 32 super-blocks per row with halves divisible by
-    // 8, or by 4 without the GNORM prologue):
+    // do_norm 0 or 2, row widths draco_dq_ksplit_waves accepts):
     // y[r] = the first half's dot, y[n_out + r] = the second half's
     int ksplit;
     float eps;
@@ -105,3 +104,26 @@ struct SegLaunch {
 
 // Builds grid ranges for every segment and launches the fused kernel.
 int draco_seg_launch(SegLaunch& a, hipStream_t st);
+
+// Launch shape of a Q4_K / Q6_K segment launch (k_dq), chosen on the host
+// from the row width, the tile count and the variant.  Every shape returned
+// keeps the kernel's coverage invariants: the prologue digitises (and
+// normalises) every input value an item multiplies, the items of a tile (or
+// of a split-K half) cover every super-block of its rows exactly once, the
+// row-dot loads cover n_in, and the LDS image fits a CU.
+struct DqShape {
+    int nw;      // waves per block
+    int grid;    // blocks
+    int ipt1;    // one item per wave and tile (rows of at most nw super-blocks)
+    int ks;      // split-K launch (halves of each row)
+    int gd;      // row dots ride on the launch
+    int xp_max;  // float4s of x per thread the prologue holds
+};
+// variant: dual = SwiGLU pair; ksplit = 2 for split-K; do_norm as SegLaunch;
+// gd_n = rows per weight of the row dots the caller asks for (0: none;
+// segment kinds already checked); cus = compute units of the device.
+// Returns 0 with the shape, or -1 when no k_dq instance serves the request.
+int draco_dq_shape(int n_in, int tiles, bool dual, int ksplit, int do_norm, int gd_n, int cus, DqShape& s);
+// Waves of the split-K instance for rows n_in wide (do_norm 0 or 2), 0 if
+// none covers them; callers that plan a split-K launch ask this first.
+int draco_dq_ksplit_waves(int n_in, int do_norm);

@@ -863,8 +863,8 @@ __global__ __launch_bounds__(256) void k_argmax_finalize(const float* __restrict
     __syncthreads();
     if (tid == 0) {
         for (int w = 1; w < 4; w++) am_merge(v, idx, sv[w], si[w]);
-        // no value compared greater than -inf (every logit NaN): token 0, as a
-        // first-index scan with '>' returns, never an out-of-range row
+        // no partial at all: token 0, never an out-of-range row (every real
+        // value, -inf and NaN included, beats the padding's index)
         if (idx == 0x7fffffff) idx = 0;
         if (lead) {
             tokens[cur + 1] = idx;
@@ -1054,61 +1054,39 @@ int seg_launch_dq(SegLaunch& a, hipStream_t st) {
         return -1;
     // PRES prologue: the partials of the pending residual
     if (a.do_norm == 3 && !a.am_val) return -1;
-    // split-K: one whole-matrix store segment, no prologue norm or the
-    // per-wave GNORM one; halves of 8-divisible super-block counts on the
-    // 8-wave kernel, of 4-divisible ones (no GNORM) on the 4-wave kernel
-    const int ks_nw = (nb / 2) % 8 == 0 ? 8 : ((nb / 2) % 4 == 0 && a.do_norm == 0 ? 4 : 0);
+    // split-K: one whole-matrix store segment (the row widths and prologues
+    // it serves are draco_dq_shape's to decide)
     if (a.ksplit) {
         const SegDesc& s0 = a.seg[0];
-        if (a.ksplit != 2 || a.nseg != 1 || dual || (a.do_norm != 0 && a.do_norm != 2) || s0.epi != EPI_STORE ||
-            s0.row0 != 0 || s0.row1 != s0.L.n_out || nb < 8 || nb > 32 || !ks_nw)
-            return -1;
+        if (a.nseg != 1 || s0.epi != EPI_STORE || s0.row0 != 0 || s0.row1 != s0.L.n_out) return -1;
     }
+    // row dots: store / residual segments only, on a normalising launch
+    int gd_n = 0;
+    if (a.gdot_n > 0 && !a.ksplit && !dual && a.nseg >= 2 && (a.do_norm == 1 || a.do_norm == 3) && a.gdot_w0 &&
+        a.gdot_w1 && a.gdot_out) {
+        bool ok = true;
+        for (int i = 0; i < a.nseg; i++) ok = ok && (a.seg[i].epi == EPI_STORE || a.seg[i].epi == EPI_RESID);
+        gd_n = ok ? a.gdot_n : 0;
+    }
+    DqShape sh;
+    if (draco_dq_shape(n_in, tiles, dual, a.ksplit, a.do_norm, gd_n, cu_count(), sh)) return -1;
     for (int i = a.nseg; i < SEG_MAX; i++) {  // unused slots: never selected by seg_of_tile
         a.seg[i] = a.seg[a.nseg - 1];
         a.seg[i].first_tile = 1 << 30;
         a.seg[i].n_tiles = 0;
     }
     a.total_tiles = tiles;
-    // waves per block: enough to split a row's super-blocks, and enough
-    // threads for the prologue's XP_MAXV float4s per thread
-    // (8 waves up to 63 super-blocks per row: measured faster than 16 for the
-    // decode down projection, n_in 8192)
-    int nw = nb >= 64 ? 16 : (nb >= 8 ? 8 : 4);
-    while (n_in > XP_MAXV * 4 * 64 * nw) nw *= 2;
-    if (nw > 16) return -1;
-    const int cap = cu_count() * (16 / nw);
-    int grid = tiles < cap ? tiles : cap;
-    // One item per wave and one tile per block (a row of at most NW
-    // super-blocks, at least two tiles per CU): blocks of two tiles instead,
-    // one per CU, so every wave keeps its second item's loads in flight while
-    // it computes the first, and half the blocks repeat the x prologue.
-    // Measured on the configs[2] decode (the gate/up SwiGLU launch, 512 tiles):
-    // 2008 -> 2108 tok/s; an 8192x2048 Q4_K GEMV 4.07 -> 3.83 us.  Launches
-    // with fewer tiles than that keep one per block (halving the qkv or wo
-    // grid was slower: 2108 -> 1917 / 1821 tok/s).
-    if (nb <= nw && tiles >= 2 * cu_count() && tiles <= cap) grid = (tiles + 1) / 2;
-    a.gdot_done = 0;
-    if (a.gdot_n > 0 && !a.ksplit && !dual && a.nseg >= 2 && nw == 8 && (a.do_norm == 1 || a.do_norm == 3) &&
-        a.gdot_w0 && a.gdot_w1 && a.gdot_out && grid >= 2 * a.gdot_n && n_in <= 8 * 64 * nw) {
-        bool ok = true;
-        for (int i = 0; i < a.nseg; i++) ok = ok && (a.seg[i].epi == EPI_STORE || a.seg[i].epi == EPI_RESID);
-        a.gdot_done = ok ? 1 : 0;
-    }
-    if (a.ksplit) {
+    const int grid = sh.grid;
+    a.gdot_done = sh.gd;
+    if (sh.ks) {
         // tiles [0, tiles) take each row's first half, [tiles, 2 tiles) the second
         a.rot = tiles;
         a.kv_dim = a.seg[0].L.n_out;
         a.total_tiles = 2 * tiles;
-        if (ks_nw == 4) {  // 4-wave blocks: four per CU
-            const int cap4 = cu_count() * 4;
-            grid = 2 * tiles < cap4 ? 2 * tiles : cap4;
+        if (sh.nw == 4) {
             if (fm == 1) launch_dq1<4, 1, false, false, EPI_STORE, 0, false, true>(a, grid, st);
             else launch_dq1<4, 2, false, false, EPI_STORE, 0, false, true>(a, grid, st);
-            return 0;
-        }
-        grid = 2 * tiles < cap ? 2 * tiles : cap;
-        if (a.do_norm == 2) {
+        } else if (a.do_norm == 2) {
             if (fm == 1) launch_dq1<8, 1, false, false, EPI_STORE, 2, false, true>(a, grid, st);
             else launch_dq1<8, 2, false, false, EPI_STORE, 2, false, true>(a, grid, st);
         } else if (fm == 1) {
@@ -1118,6 +1096,7 @@ int seg_launch_dq(SegLaunch& a, hipStream_t st) {
         }
         return 0;
     }
+    const int nw = sh.nw;
     if (grid <= 0) return 0;
     if (a.gdot_done) {
         if (a.do_norm == 3) launch_dq_gd<3>(a, fm, grid, st);
@@ -1211,6 +1190,65 @@ int seg_launch_q8(SegLaunch& a, hipStream_t st) {
 
 }  // namespace
 
+int draco_dq_ksplit_waves(int n_in, int do_norm) {
+    if (n_in <= 0 || n_in % 512) return 0;
+    const int nb = n_in / 256, half = nb / 2;
+    if (nb < 8 || nb > 32) return 0;
+    // the split-K instances: 8 waves (prologue none or GNORM), 4 waves (none).
+    // A half splits into whole items per wave, and with one tile per block
+    // (kown) chunk q of the prologue holds super-blocks [q nw, q nw + nw), so
+    // the second half's last chunk nb / nw - 1 must lie below XP_MAXV.
+    if (half % 8 == 0 && nb <= XP_MAXV * 8) return 8;
+    if (do_norm == 0 && half % 4 == 0 && nb <= XP_MAXV * 4) return 4;
+    return 0;
+}
+
+int draco_dq_shape(int n_in, int tiles, bool dual, int ksplit, int do_norm, int gd_n, int cus, DqShape& s) {
+    s = DqShape{};
+    s.xp_max = XP_MAXV;
+    if (n_in <= 0 || n_in % 256 || n_in > 16384 || tiles <= 0 || cus <= 0) return -1;
+    const int nb = n_in / 256;
+    if (ksplit) {
+        if (ksplit != 2 || dual || (do_norm != 0 && do_norm != 2)) return -1;
+        const int nw = draco_dq_ksplit_waves(n_in, do_norm);
+        if (!nw) return -1;
+        const int cap = cus * (16 / nw);  // 4-wave blocks: four per CU; 8-wave: two
+        s.nw = nw;
+        s.ks = 1;
+        s.grid = 2 * tiles < cap ? 2 * tiles : cap;
+    } else {
+        // waves per block: enough to split a row's super-blocks, and enough
+        // threads for the prologue's XP_MAXV float4s per thread (8 waves up
+        // to 63 super-blocks per row: measured faster than 16 for the decode
+        // down projection, n_in 8192)
+        int nw = nb >= 64 ? 16 : (nb >= 8 ? 8 : 4);
+        while (n_in > XP_MAXV * 4 * 64 * nw) nw *= 2;
+        if (nw > 16) return -1;
+        const int cap = cus * (16 / nw);
+        int grid = tiles < cap ? tiles : cap;
+        // One item per wave and one tile per block (a row of at most NW
+        // super-blocks, at least two tiles per CU): blocks of two tiles
+        // instead, one per CU, so every wave keeps its second item's loads in
+        // flight while it computes the first, and half the blocks repeat the
+        // x prologue.  Measured on the configs[2] decode (the gate/up SwiGLU
+        // launch, 512 tiles): 2008 -> 2108 tok/s; an 8192x2048 Q4_K GEMV
+        // 4.07 -> 3.83 us.  Launches with fewer tiles than that keep one per
+        // block (halving the qkv or wo grid was slower: 2108 -> 1917 / 1821
+        // tok/s).
+        if (nb <= nw && tiles >= 2 * cus && tiles <= cap) grid = (tiles + 1) / 2;
+        s.nw = nw;
+        s.grid = grid;
+        s.ipt1 = nb <= nw;
+        // row dots: the 8-wave instances, two float4 of the row per thread,
+        // 2 gd_n blocks at the end of the grid
+        if (gd_n > 0 && !dual && nw == 8 && (do_norm == 1 || do_norm == 3) && grid >= 2 * gd_n &&
+            n_in <= 2 * 4 * 64 * nw)
+            s.gd = 1;
+    }
+    if (dq_lds_bytes(n_in, s.nw) > 160 * 1024) return -1;
+    return 0;
+}
+
 int draco_seg_launch(SegLaunch& a, hipStream_t st) {
     if (a.nseg < 1 || a.nseg > SEG_MAX) return -1;
     bool kq = false, q8 = false;
@@ -1279,4 +1317,20 @@ int draco_gemv_launch(const DracoMat& m, const float* x, float* y, const float* 
 int draco_gemv_supported(int code) {
     return code == DRACO_Q4_K || code == DRACO_Q6_K || code == DRACO_Q8_0 || code == DRACO_F32 ||
            code == DRACO_F16;
+}
+
+// Host-side launch planning, exported so tests can enumerate shapes without a
+// GPU: out = {nw, grid, ipt1, ks, gd, xp_max}.  Returns draco_dq_shape's code.
+extern "C" int draco_dq_plan(int n_in, int tiles, int dual, int ksplit, int do_norm, int gd_n, int cus, int* out) {
+    DqShape s;
+    const int rc = draco_dq_shape(n_in, tiles, dual != 0, ksplit, do_norm, gd_n, cus, s);
+    if (out) {
+        out[0] = s.nw;
+        out[1] = s.grid;
+        out[2] = s.ipt1;
+        out[3] = s.ks;
+        out[4] = s.gd;
+        out[5] = s.xp_max;
+    }
+    return rc;
 }

@@ -654,8 +654,10 @@ int draco_moe_xper_slots(int n_in) {
     return (XP_MAXV * 64 * grp_nw(n_in) * 4) / n_in;
 }
 
-int draco_moe_down_launch(MoeArgs& a, int fm, hipStream_t st) {
-    if (a.inter % 256 || a.n_out % 16 || a.n_slots < 1 || a.n_slots > 16) return -1;
+namespace {
+
+// One k_moe_down launch over at most 16 slots (a wave per slot).
+int moe_down_chunk(const MoeArgs& a, int fm, hipStream_t st) {
     const int nw = a.n_slots <= 4 ? 4 : (a.n_slots <= 8 ? 8 : 16);
     if (a.n_slots * (a.inter / 4) > 4096 * 4) return -1;
     const size_t lds = (size_t)a.n_slots * (a.inter / 16) * 72 + 1024 + (size_t)nw * 16 * 4 + MOE_USED_MAX * 4;
@@ -670,6 +672,27 @@ int draco_moe_down_launch(MoeArgs& a, int fm, hipStream_t st) {
     } else {
         if (fm == 1) launch_down<16, 1>(a, tiles, lds, st);
         else launch_down<16, 2>(a, tiles, lds, st);
+    }
+    return 0;
+}
+
+}  // namespace
+
+// More than 16 selected experts (the reference serves up to 64,
+// src/m6_layer.c:797): launches of 16 slots each, in slot order, the first
+// adding the residual and each later one adding its sum to the output
+// (out = ((resid + S_0..15) + S_16..31) + ...).
+int draco_moe_down_launch(MoeArgs& a, int fm, hipStream_t st) {
+    if (a.inter % 256 || a.n_out % 16 || a.n_slots < 1 || a.n_slots > MOE_USED_MAX) return -1;
+    for (int c0 = 0; c0 < a.n_slots; c0 += 16) {
+        MoeArgs c = a;
+        c.n_slots = a.n_slots - c0 < 16 ? a.n_slots - c0 : 16;
+        c.sel = a.sel + c0;
+        c.selw = a.selw + c0;
+        c.seld = a.seld + c0;
+        c.act = a.act + (size_t)c0 * a.inter;
+        if (c0 > 0) c.resid = a.out;
+        if (int rc = moe_down_chunk(c, fm, st)) return rc;
     }
     return 0;
 }

@@ -19,7 +19,10 @@
 #include "q8k.h"
 #include "runtime.h"
 
-constexpr size_t NOALLOC_Q8K_BYTES = 1u << 20;  // 1 MiB: nvec * (n_in / 256) * 292 + 16 bytes at most
+// 1 MiB: nvec * (n_in / 256) * 292 + 16 bytes at most.  The shapes served
+// are bounded more tightly by the GEMV, whose LDS holds the same image (at
+// most about 150 KiB of it: n_in up to 16896 at nvec 8, 67584 at nvec 1).
+constexpr size_t NOALLOC_Q8K_BYTES = 1u << 20;
 constexpr int NOALLOC_MAX_DEVICES = 64;
 
 // The staging array.  File scope, outside any namespace: the compiler gives a
@@ -55,7 +58,10 @@ using namespace draco;
 
 extern "C" {
 
-// Bytes of the static staging array (the largest nvec * (n_in / 256) * 292).
+// Bytes of the static staging array (the largest nvec * (n_in / 256) * 292 +
+// 16).  A request within it can still exceed the GEMV's LDS image (160 KiB
+// for the image and the block's reduction space); such calls return -1
+// before anything is enqueued.
 size_t draco_noalloc_capacity(void) { return NOALLOC_Q8K_BYTES; }
 
 // draco_gemv_q8k_f32 with device pointers and no allocation: x [nvec][n_in]
@@ -74,6 +80,9 @@ int draco_gemv_q8k_f32_noalloc(int code, const float* x, int nvec, const uint8_t
     if (need > NOALLOC_Q8K_BYTES)
         return fail(-1, "noalloc q8k gemv: %zu bytes of Q8_K staging exceed the %zu-byte static array", need,
                     NOALLOC_Q8K_BYTES);
+    // the GEMV's own limits first: nothing is enqueued for a call it would refuse
+    if (!draco_gemv_q8k_shape_ok(code, n_in, nvec, true, false))
+        return fail(-1, "noalloc q8k gemv: rows of %d values at nvec %d exceed the GEMV's LDS image", n_in, nvec);
     if (int rc = ensure_init()) return rc;
     int dev = 0;
     DRACO_HIP(hipGetDevice(&dev));

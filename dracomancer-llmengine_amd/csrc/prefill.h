@@ -21,7 +21,10 @@ int pf_add_rms(float* X, const float* Y, const float* w, float* Xn, int T, int h
 int pf_rope_append(float* Q, const float* K, const float* V, float* kc, float* vc, const float* tab, int pos0,
                    int row0, int T, int NH, int NKV, int HD, int rot, hipStream_t st);
 // O[t] = causal attention of query row row0 + t over cache rows [0, row0 + t]
-// (NH / NKV <= 8, HD 64 or 128); part holds pf_part_floats(...) floats
+// (the shapes pf_attention_ok accepts); part holds pf_part_floats(...) floats
+static inline bool pf_attention_ok(int NH, int NKV, int HD) {
+    return NKV >= 1 && NH % NKV == 0 && NH / NKV <= 8 && (HD == 64 || HD == 128);
+}
 int pf_attention(const float* Q, const float* kc, const float* vc, float* part, float* O, int row0, int T, int NH,
                  int NKV, int HD, float scale, hipStream_t st);
 // The same at head dim 256 (NH / NKV <= 16) with the qwen35 output gate:

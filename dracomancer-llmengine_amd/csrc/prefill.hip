@@ -502,7 +502,7 @@ int pf_rope_append(float* Q, const float* K, const float* V, float* kc, float* v
 
 int pf_attention(const float* Q, const float* kc, const float* vc, float* part, float* O, int row0, int T, int NH,
                  int NKV, int HD, float scale, hipStream_t st) {
-    if (T < 1 || NKV < 1 || NH % NKV || NH / NKV > 8 || (HD != 64 && HD != 128)) return -1;
+    if (T < 1 || !pf_attention_ok(NH, NKV, HD)) return -1;
     const int nspl = pf_attn_nsplit(row0, T);
     const dim3 grid(NKV, (T + PF_QT - 1) / PF_QT, nspl), block(64 * (NH / NKV));
     const size_t lds = sizeof(float) * 2 * PF_KT * HD;

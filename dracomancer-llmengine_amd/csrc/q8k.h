@@ -32,3 +32,7 @@ constexpr int Q8K_IMAGE_PAD = 16;
 int draco_q8k_quantize_launch(const float* x, int n, int nvec, uint8_t* out, hipStream_t st, bool image = false);
 // nvec in {1, 4, 8}; isums requires nvec == 1.
 int draco_gemv_q8k_launch(Q8Launch& a, int nvec, bool isums, hipStream_t st);
+// Whether draco_gemv_q8k_launch serves rows n_in wide for nvec vectors (the
+// Q8_K image of x and the block's reduction space fit the CU's 160 KiB of
+// LDS), checked before anything is enqueued.
+int draco_gemv_q8k_shape_ok(int code, int n_in, int nvec, bool img, bool isums);

@@ -432,31 +432,48 @@ int draco_q8k_quantize_launch(const float* x, int n, int nvec, uint8_t* out, hip
     return 0;
 }
 
-int draco_gemv_q8k_launch(Q8Launch& a, int nvec, bool isums, hipStream_t st) {
-    const int code = a.L.code;
+namespace {
+
+// Waves per block and LDS bytes of a Q8_K GEMV over rows n_in wide for nvec
+// vectors; -1 when no instance serves the request.
+int q8k_shape(int code, int n_in, int nvec, bool img, bool isums, int* nw_out, size_t* lds_out) {
     if (code != DRACO_Q4_K && code != DRACO_Q6_K) return -1;
-    const int n_in = a.n_in;
-    if (n_in != a.L.n_in || n_in % 256 || nvec < 1 || nvec > 8) return -1;
-    if (a.row1 <= 0) a.row1 = a.L.n_out;
-    if (a.row0 < 0 || a.row1 > a.L.n_out || a.row0 >= a.row1) return -1;
-    a.tile0 = a.row0 / 16;
-    a.n_tiles = (a.row1 + 15) / 16 - a.tile0;
-    const int nb = n_in / 256, ng = n_in / 16;
-    const int NBp = nvec == 1 ? 1 : (nvec <= 4 ? 4 : 8);
-    if (NBp != nvec) {
-        // vectors beyond nvec are read from the caller's buffer: require the padded count
-        return -1;
-    }
-    if (a.img && isums) return -1;
+    // vectors beyond nvec would be read from the caller's buffer: only the
+    // instance counts 1, 4 and 8 are served
+    if (n_in <= 0 || n_in % 256 || (nvec != 1 && nvec != 4 && nvec != 8)) return -1;
+    if (img && isums) return -1;
+    const int nb = n_in / 256;
     // 16 waves for long rows unless that leaves padding items (a padding item
     // re-reads its wave's first item, which the non-temporal weight loads may
     // already have evicted: 56 super-blocks over 16 waves fetched 11% more
     // than the matrix); 8 waves divide 56
     const int nw = nb >= 32 && nb % 16 == 0 ? 16 : (nb >= 8 ? 8 : 4);
-    const size_t img = (size_t)NBp * nb * Q8K_BLOCK_BYTES;  // = NBp * n_in + ng * NBp * 2 + nb * NBp * 4
-    const size_t lds = ((img + 15) & ~(size_t)15) + 1024 + (size_t)NBp * nw * 16 * 4;
-    (void)ng;
+    const size_t image = (size_t)nvec * nb * Q8K_BLOCK_BYTES;  // = nvec * n_in + n_in / 16 * nvec * 2 + nb * nvec * 4
+    const size_t lds = ((image + 15) & ~(size_t)15) + 1024 + (size_t)nvec * nw * 16 * 4;
     if (lds > 160 * 1024) return -1;
+    *nw_out = nw;
+    *lds_out = lds;
+    return 0;
+}
+
+}  // namespace
+
+int draco_gemv_q8k_shape_ok(int code, int n_in, int nvec, bool img, bool isums) {
+    int nw;
+    size_t lds;
+    return q8k_shape(code, n_in, nvec, img, isums, &nw, &lds) == 0;
+}
+
+int draco_gemv_q8k_launch(Q8Launch& a, int nvec, bool isums, hipStream_t st) {
+    const int code = a.L.code;
+    const int n_in = a.n_in;
+    int nw;
+    size_t lds;
+    if (n_in != a.L.n_in || q8k_shape(code, n_in, nvec, a.img, isums, &nw, &lds)) return -1;
+    if (a.row1 <= 0) a.row1 = a.L.n_out;
+    if (a.row0 < 0 || a.row1 > a.L.n_out || a.row0 >= a.row1) return -1;
+    a.tile0 = a.row0 / 16;
+    a.n_tiles = (a.row1 + 15) / 16 - a.tile0;
     const int cap = cu_count() * (nw == 4 ? 4 : (nw == 8 ? 2 : 1));
     const int grid = a.n_tiles < cap ? a.n_tiles : cap;
     const int fm = code == DRACO_Q4_K ? 1 : 2;

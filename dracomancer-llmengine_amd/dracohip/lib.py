@@ -87,6 +87,7 @@ SIGNATURES = {
     "draco_version": (ct.c_char_p, []),
     "draco_bench_gemv": (ct.c_int, [ct.c_int, u8p, ct.c_int, ct.c_int, ct.c_int, ct.c_int, f32p]),
     "draco_bench_launch": (ct.c_int, [ct.c_int, f32p]),
+    "draco_dq_plan": (ct.c_int, [ct.c_int] * 7 + [i32p]),
     # MoE (src/m6_layer.c:771-802, src/m5/m5_batch8_k.c:80-183)
     "m6_granite_moe": (None, [f32p, ct.c_void_p, i32p, f32p, ct.c_int, ct.c_int, ct.c_int, ct.c_int, ct.c_int,
                               f32p, f32p]),

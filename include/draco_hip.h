@@ -387,7 +387,9 @@ int draco_q8k_isums(int code, const uint8_t* xq, const uint8_t* W, int n_out, in
  * (draco_repack of the GGUF rows; draco_layout_query bytes), y [nvec][n_out]
  * fp32.  The Q8_K values of x are staged in a static device array of
  * draco_noalloc_capacity() bytes (1 MiB: nvec * n_in / 256 * 292 + 16 bytes
- * at most; larger requests return -1).  Enqueued on `stream` (a hipStream_t;
+ * at most; larger requests return -1, as do rows whose Q8_K image does not
+ * fit the GEMV's 160 KiB of LDS -- n_in above 16896 at nvec 8 -- both before
+ * anything is enqueued).  Enqueued on `stream` (a hipStream_t;
  * NULL = the library's stream) and not waited for.  Every call on one GPU
  * shares that GPU's staging array: calls that overlap on one GPU race. */
 int draco_gemv_q8k_f32_noalloc(int code, const float* x, int nvec, const uint8_t* W, int n_out, int n_in, float* y,
@@ -407,6 +409,16 @@ int draco_bench_gemv(int code, const uint8_t* W, int n_out, int n_in, int n_copi
                      float* out);
 /* out[0] us per empty-kernel launch in a stream, out[1] in a replayed graph. */
 int draco_bench_launch(int iters, float* out);
+
+/* Launch planning of the Q4_K / Q6_K segment GEMV (no reference counterpart;
+ * pure host logic, callable without a GPU, for tests): the shape the library
+ * would launch for rows n_in wide in `tiles` 16-row tiles -- dual = SwiGLU
+ * pair, ksplit 2 = split-K, do_norm = prologue kind (0 none, 1 RMSNorm, 2 GDN
+ * gated rms, 3 RMSNorm of a pending residual), gd_n = row dots requested, cus
+ * = compute units.  out[6] = {waves per block, grid, one item per wave,
+ * split-K, row dots, float4s of x per thread in the prologue}.  Returns 0, or
+ * -1 when no instance covers the request. */
+int draco_dq_plan(int n_in, int tiles, int dual, int ksplit, int do_norm, int gd_n, int cus, int* out);
 
 /* Host-side byte work (pure CPU, callable without a GPU). */
 int draco_quantize(int code, const float* x, int n_rows, int n_in, uint8_t* out);

@@ -456,8 +456,11 @@ int or_head_op(const float* x, const float* final_norm, int h, float eps,
 }
 
 /* a19  greedy pick: np.argmax over a float64 copy (src/smol_engine.py:212,
- * src/draco_engine_server.py:754) -- first index wins ties. */
+ * src/draco_engine_server.py:754) -- first index wins ties, and numpy ranks
+ * NaN above every number, so the first NaN's index is the result when any
+ * value is NaN. */
 int or_argmax(const float* v, int n) {
+    for (int i = 0; i < n; i++) if (v[i] != v[i]) return i;
     int best = 0;
     for (int i = 1; i < n; i++) if (v[i] > v[best]) best = i;
     return best;

@@ -76,11 +76,13 @@ def test_granite_moe_configs3_q4k_experts(hip, oracle):
         assert rel_err(y, ref) <= TOL
 
 
-@pytest.mark.parametrize("n_exp,n_used", [(300, 6), (512, 16), (512, 1), (40, 8)])
+@pytest.mark.parametrize("n_exp,n_used", [(300, 6), (512, 16), (512, 1), (40, 8), (128, 24), (512, 64), (64, 64)])
 def test_granite_moe_expert_counts(hip, oracle, n_exp, n_used):
     """Routers wider than the routing block (256 threads at n_in 512, so
     experts 256 and up are ranked in a second pass), the 512-expert limit,
-    the largest top-k the down kernel serves (16) and top-1."""
+    the largest top-k one down launch serves (16), top-1, and top-k above 16
+    up to the reference's 64 (src/m6_layer.c:797: down launches of 16 slots
+    chained in slot order), including every expert selected."""
     inter, H = 256, 512
     M = build_moe(n_exp, inter, H, H, 40 + n_used)
     y = run_hip(hip, M, n_exp, n_used, inter, H, H)

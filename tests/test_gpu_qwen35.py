@@ -266,3 +266,50 @@ def test_full_attn_cache_residency(hip, oracle):
     Kr[100 * W:101 * W] *= -1.0
     assert hip.draco_array_push(Kr.ctypes.data, 291 * W * 4) == 0
     check(290, 98)
+
+
+def test_gdn_scan_after_device_decode_steps(hip, oracle):
+    """The reference's qwen35 adapter mixes per-token m6_gdn_attn calls with
+    forward_chunk, whose m6_gdn_scan reads and updates the same ssm / tail
+    arrays (src/qwen35_prefill.py:128-133).  The per-layer op keeps that
+    state on the device and writes back only a sample, so the scan must
+    start from the device state: decode steps, a 64-token scan chunk with no
+    explicit pull, then more decode steps, all against the oracle run on
+    host arrays; the scan leaves the whole state in the caller's arrays."""
+    from dracohip import qwen35 as Q
+    L = Q.gdn_layer(97, 32, (5, 5, 5))
+    ssm, tail = L.fresh_state()
+    so, to = L.fresh_state()
+    h1 = Q.hidden(98, 6)
+    n_qkv, n_vh, T = L.n_qkv, L.n_vh, 64
+    rng = np.random.default_rng(99)
+    QKV = rng.standard_normal((T, n_qkv), dtype=np.float32)
+    Z = rng.standard_normal((T, n_vh * 128), dtype=np.float32)
+    B = (1.0 / (1.0 + np.exp(-rng.standard_normal((T, n_vh))))).astype(np.float32)
+    G = np.exp(-np.logaddexp(0.0, rng.standard_normal((T, n_vh)))).astype(np.float32)
+    conv, snorm = L.arrays["conv"], L.arrays["ssm_norm"]
+
+    def oracle_step(s):
+        x2n, x2o = np.zeros(Q.H, np.float32), np.zeros(Q.H, np.float32)
+        assert oracle.lib.or_gdn_attn(_pf(h1[s]), L.ptr(), _pf(so), _pf(to), _pf(x2n), _pf(x2o)) == 0
+        return np.concatenate([x2o, x2n])
+
+    for s in range(3):
+        print(f"[gdn_attn] decode step {s} before the scan", flush=True)
+        assert rel_err(_gdn_call(hip, L, ssm, tail, h1[s]), oracle_step(s)) <= TOL, s
+    print("[gdn_scan] 64-token chunk on the op's arrays", flush=True)
+    ON = np.zeros((T, n_vh * 128), np.float32)
+    work = np.zeros(8, np.float32)
+    hip.m6_gdn_scan(_pf(QKV), _pf(Z), _pf(B), _pf(G), _pf(conv), _pf(snorm), _pf(tail), _pf(ssm), T, n_qkv, n_vh,
+                    _pf(ON), _pf(work))
+    ONr = np.zeros((T, n_vh * 128), np.float32)
+    oracle.lib.or_gdn_scan(_pf(QKV), _pf(Z), _pf(B), _pf(G), _pf(conv), _pf(snorm), _pf(to), _pf(so), T, n_qkv,
+                           n_vh, _pf(ONr), _pf(np.zeros(n_qkv, np.float32)))
+    assert rel_err(ON, ONr) <= TOL
+    assert rel_err(ssm, so) <= TOL  # the whole state is back in the caller's array
+    assert rel_err(tail, to) <= TOL
+    for s in range(3, 6):
+        print(f"[gdn_attn] decode step {s} after the scan", flush=True)
+        assert rel_err(_gdn_call(hip, L, ssm, tail, h1[s]), oracle_step(s)) <= TOL, s
+    assert hip.draco_array_pull(ssm.ctypes.data, ssm.nbytes) == 0
+    assert rel_err(ssm, so) <= TOL

@@ -153,3 +153,22 @@ def test_pins_catch_planted_slips(tmp_path, mutant, check):
                     f"-DOR_MUTANT={mutant}", "-o", so, src, "-lm"], check=True)
     with pytest.raises(AssertionError):
         check(Oracle(so))
+
+
+def test_argmax_matches_numpy(oracle):
+    """or_argmax is np.argmax over a float64 copy (src/smol_engine.py:212):
+    the first maximum, and the first NaN whenever a value is NaN."""
+    rng = np.random.default_rng(7)
+    cases = [np.array([1.0, 3.0, 3.0, 2.0], np.float32), np.full(5, -np.inf, np.float32),
+             np.full(4, np.nan, np.float32), np.array([np.inf, 1.0, np.inf], np.float32),
+             np.array([-np.inf, np.nan, 5.0, np.nan], np.float32), np.array([2.0, np.inf, np.nan], np.float32)]
+    for _ in range(200):
+        v = rng.standard_normal(int(rng.integers(1, 300))).astype(np.float32)
+        v[rng.integers(0, len(v), 3)] = v.max()  # ties of the maximum
+        if rng.random() < 0.5:
+            v[rng.integers(0, len(v), int(rng.integers(1, 3)))] = np.nan
+        if rng.random() < 0.3:
+            v[rng.integers(0, len(v))] = rng.choice([np.inf, -np.inf])
+        cases.append(v)
+    for v in cases:
+        assert oracle.lib.or_argmax(pf(v), len(v)) == int(np.argmax(v.astype(np.float64))), v
