@@ -3,9 +3,10 @@
 // m5_gemm_auto: src/m5/m5_gemm_fused.c:231-241 (0 = done, -1 = code not served,
 // the caller falls back); m5_gemm: src/m5/m5_gemm.c:249-272 (Y[T x n_out] =
 // X[T x n_in] . W^T).  Host pointers.  Q4_K / Q6_K run on the f16-MFMA GEMM
-// (gemmh.hip); Q8_0 runs as one device GEMV per token.  The int8-MFMA kernels
+// (gemmh.hip); Q8_0 and Q5_K run as one device GEMV per token.  The int8-MFMA kernels
 // of gemm.hip serve the grouped expert GEMMs of m6_moe_tok only.
 // m5_dequant_row: src/m5/m5_gemm.c:55-235, the GEMM library's row decoder.
+#include <stdio.h>
 #include <string.h>
 
 #include <vector>
@@ -48,7 +49,9 @@ int draco_enqueue_gemm(const DracoMat& m, const float* X, int T, float* Y, uint8
 
 namespace {
 
-bool served(int code) { return code == DRACO_Q4_K || code == DRACO_Q6_K || code == DRACO_Q8_0; }
+bool served(int code) {
+    return code == DRACO_Q4_K || code == DRACO_Q6_K || code == DRACO_Q8_0 || code == DRACO_Q5_K;
+}
 
 int enqueue_gemm(const DracoMat& m, const float* X, int T, float* Y, uint8_t* digits, hipStream_t st) {
     return draco_enqueue_gemm(m, X, T, Y, digits, false, st);
@@ -75,6 +78,16 @@ int gemm_host(int code, const float* X, const uint8_t* W, int T, int n_out, int 
     return 0;
 }
 
+// the void fused-GEMM entries' body (below)
+void gemm_void(const char* name, int code, const float* X, const uint8_t* W, int c, int n_out, int n_in, float* Y) {
+    std::lock_guard<std::recursive_mutex> g(api_mutex());
+    int rc = served(code) ? gemm_host(code, X, W, c, n_out, n_in, Y)
+                          : fail(-1, "%s: format code %d is not carried by this library", name, code);
+    if (rc) {
+        fprintf(stderr, "%s: rc %d: %s\n", name, rc, last_error());
+        if (Y && c > 0 && n_out > 0) poison(Y, (size_t)c * n_out);
+    }
+}
 }  // namespace
 
 extern "C" {
@@ -90,15 +103,43 @@ int m5_gemm(int code, const float* X, const uint8_t* W, int T, int n_out, int n_
     return gemm_host(code, X, W, T, n_out, n_in, Y);
 }
 
+// The per-format fused GEMM entries (the FUSED3 instances and m5_gemm_iq3s,
+// src/m5/m5_gemm_fused.c:78,211-228), Y[c x n_out] = X[c x n_in] . W^T.  The
+// reference's prefill driver looks all six up when it starts and calls them
+// by format instead of m5_gemm_auto (src/qwen35_prefill.py:76-80,100-104).
+// They return nothing, as the reference's: a format this library does not
+// carry (IQ4_XS, IQ3_S) or a failed call leaves NaN in Y and the error on
+// stderr, never stale values.
+
+void m5_gemm_q80(const float* X, const uint8_t* W, int c, int n_out, int n_in, float* Y) {
+    gemm_void("m5_gemm_q80", DRACO_Q8_0, X, W, c, n_out, n_in, Y);
+}
+void m5_gemm_q6k(const float* X, const uint8_t* W, int c, int n_out, int n_in, float* Y) {
+    gemm_void("m5_gemm_q6k", DRACO_Q6_K, X, W, c, n_out, n_in, Y);
+}
+void m5_gemm_q5k(const float* X, const uint8_t* W, int c, int n_out, int n_in, float* Y) {
+    gemm_void("m5_gemm_q5k", DRACO_Q5_K, X, W, c, n_out, n_in, Y);
+}
+void m5_gemm_q4k(const float* X, const uint8_t* W, int c, int n_out, int n_in, float* Y) {
+    gemm_void("m5_gemm_q4k", DRACO_Q4_K, X, W, c, n_out, n_in, Y);
+}
+void m5_gemm_iq4xs(const float* X, const uint8_t* W, int c, int n_out, int n_in, float* Y) {
+    gemm_void("m5_gemm_iq4xs", 6, X, W, c, n_out, n_in, Y);
+}
+void m5_gemm_iq3s(const float* X, const uint8_t* W, int c, int n_out, int n_in, float* Y) {
+    gemm_void("m5_gemm_iq3s", 2, X, W, c, n_out, n_in, Y);
+}
+
 // src/m5/m5_gemm.c:55-235: one GGUF row -> out[n_in] fp32 (0 done, -1 code
-// not served).  Served: Q8_0, Q4_K, Q6_K, F16 (the reference also serves
-// Q5_K and the IQ formats, which no path here carries).  The row is decoded
+// not served).  Served: Q8_0, Q4_K, Q5_K, Q6_K, F16 (the reference also
+// serves the IQ formats, which no path here carries).  The row is decoded
 // on the device by the embedding decoder: from the resident copy when the
 // row lies inside a registered matrix, else from the row's own bytes put in
 // the private layout.
 int m5_dequant_row(int code, const uint8_t* row, int n_in, float* out) {
     std::lock_guard<std::recursive_mutex> g(api_mutex());
-    if (code != DRACO_Q8_0 && code != DRACO_Q4_K && code != DRACO_Q6_K && code != DRACO_F16) return -1;
+    if (code != DRACO_Q8_0 && code != DRACO_Q4_K && code != DRACO_Q5_K && code != DRACO_Q6_K && code != DRACO_F16)
+        return -1;
     if (!row || !out || n_in <= 0 || n_in % draco_block_values(code)) {
         fail(-1, "m5_dequant_row: n_in %d is not a whole number of blocks", n_in);
         return -1;

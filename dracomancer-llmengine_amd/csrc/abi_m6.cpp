@@ -434,8 +434,9 @@ int enqueue_qkv(DevAttn* a, Work& w, const float* x, int norm, const float* norm
             s.am_val = w.pd;
             s.xn_out = w.xs;
         }
-        // every not-yet-issued segment of the same kernel family (Q4_K/Q6_K share one)
-        auto fam = [](int c) { return c == DRACO_Q8_0 ? 0 : 1; };
+        // every not-yet-issued segment of the same kernel family (Q4_K/Q6_K
+        // share one; Q5_K launches hold Q5_K segments only)
+        auto fam = [](int c) { return c == DRACO_Q8_0 ? 0 : (c == DRACO_Q5_K ? 2 : 1); };
         for (int j = i; j < 3; j++)
             if (!done[j] && fam(all[j].L.code) == fam(all[i].L.code)) {
                 s.seg[s.nseg++] = all[j];
@@ -842,6 +843,16 @@ int m6_init_extra_dl(const char* p50) {
     return 0;
 }
 
+// src/m6_layer.c:108-120, the opt-in IQ3_S integer kernel slot
+// (src/qwen35_engine.py:103-108 binds it when DRACO_IQ3_FAST=1).  IQ3_S is
+// not carried by this library: returns 1 ("could not load"), which the
+// driver reports before going on without the fast path.
+int m6_init_iq3_dl(const char* p12) {
+    (void)p12;
+    fail(-1, "m6_init_iq3_dl: IQ3_S is not carried by this library");
+    return 1;
+}
+
 // src/m6_engine.c:61-83
 int m6_forward_token(float* x, int h, float eps, int pos, const M6LayerDesc* layers, int n_layer,
                      float* scratch) {
@@ -1143,7 +1154,8 @@ int draco_llama_generate(const void* layers_v, int n_layer, int h, float eps, co
     int* cursor = dtok + ntok + 8;   // index of the token being fed
     int* cur = dtok + ntok + 16;     // its id
     int* dri = (int*)(dred + hblocks + 32);
-    const bool fused_head = hm->L.code == DRACO_Q4_K || hm->L.code == DRACO_Q6_K || hm->L.code == DRACO_Q8_0;
+    const bool fused_head = hm->L.code == DRACO_Q4_K || hm->L.code == DRACO_Q5_K || hm->L.code == DRACO_Q6_K ||
+                            hm->L.code == DRACO_Q8_0;
     std::vector<int> ht(ntok + 64, 0);
     for (int i = 0; i < n_prompt; i++) ht[i] = prompt[i];
     // prompt[0 .. n_prompt - 1) goes through the chunked prefill when enabled

@@ -365,6 +365,71 @@ std::map<const void*, MoeLayer*>& moe_layers() {
     return *m;
 }
 
+// m6_moe_batch4 (src/m6_layer.c:656-690): n given experts, no router --
+// out = sum_j wtop[j] * down_j(silu(gate_j x0) * up_j x0) in j order, the
+// caller's weights as they are (no renormalisation).  The routed launches
+// with the slots fixed by the host: gate/up + SwiGLU over the n slots, then
+// the down + weighted combine.
+int moe_batch(const float* x0, const uint64_t* ptrs, const int* codes, const float* wtop, int n, int inter,
+              int n_in, int n_out, float* out) {
+    if (n < 1 || n > MOE_USED_MAX) return fail(-1, "m6_moe_batch4: %d experts (1..%d served)", n, MOE_USED_MAX);
+    if (inter % 256 || n_in % 256 || n_out % 16)
+        return fail(-1, "m6_moe_batch4: shape inter %d n_in %d n_out %d not served", inter, n_in, n_out);
+    const int fg = fm_of(codes[0]), fd = fm_of(codes[2]);
+    for (int j = 0; j < n; j++)
+        if (codes[3 * j] != codes[0] || codes[3 * j + 1] != codes[0] || codes[3 * j + 2] != codes[2] || !fg || !fd)
+            return fail(-1, "m6_moe_batch4: expert formats not served (one of Q4_K / Q6_K per role)");
+    if (int rc = ensure_init()) return rc;
+    hipStream_t st = stream();
+    // device table [gate n][up n][down n] bases, then the n weights, x, act, out
+    const size_t tb = sizeof(void*) * 3 * (size_t)n;
+    char* d = (char*)scratch(16, tb + sizeof(float) * ((size_t)n + n_in + (size_t)n * inter + n_out) + 256);
+    char* h = (char*)pinned(7, tb + sizeof(float) * ((size_t)n + n_in));
+    if (!d || !h) return -2;
+    const uint8_t** tab = (const uint8_t**)h;
+    for (int j = 0; j < n; j++) {
+        const DracoMat* g = get_mat((const void*)(uintptr_t)ptrs[3 * j], codes[3 * j], inter, n_in);
+        const DracoMat* u = get_mat((const void*)(uintptr_t)ptrs[3 * j + 1], codes[3 * j + 1], inter, n_in);
+        const DracoMat* dn = get_mat((const void*)(uintptr_t)ptrs[3 * j + 2], codes[3 * j + 2], n_out, inter);
+        if (!g || !u || !dn) return -2;
+        tab[j] = g->dev;
+        tab[n + j] = u->dev;
+        tab[2 * n + j] = dn->dev;
+    }
+    float* hw = (float*)(h + tb);
+    memcpy(hw, wtop, sizeof(float) * n);
+    memcpy(hw + n, x0, sizeof(float) * n_in);
+    const uint8_t** dtab = (const uint8_t**)d;
+    float* dw = (float*)(d + tb);
+    float* dx = dw + n;
+    float* dact = dx + n_in;
+    float* dout = dact + (size_t)n * inter;
+    DRACO_HIP(hipMemcpyAsync(d, h, tb + sizeof(float) * ((size_t)n + n_in), hipMemcpyHostToDevice, st));
+    MoeArgs a = {};
+    a.x = dx;
+    a.n_in = n_in;
+    a.n_out_e = inter;
+    a.n_slots = n;
+    a.base0 = dtab;
+    a.base1 = dtab + n;
+    a.act = dact;
+    if (draco_moe_grp_launch(a, fg, true, false, false, st)) return fail(-1, "moe batch gate/up launch rejected");
+    a.inter = inter;
+    a.n_out = n_out;
+    a.out = dout;
+    a.resid = nullptr;
+    a.seld = dtab + 2 * n;
+    a.selw = dw;
+    if (draco_moe_down_launch(a, fd, st)) return fail(-1, "moe batch down launch rejected");
+    DRACO_HIP(hipGetLastError());
+    float* ho = (float*)pinned(8, sizeof(float) * (size_t)n_out);
+    if (!ho) return -2;
+    DRACO_HIP(hipMemcpyAsync(ho, dout, sizeof(float) * n_out, hipMemcpyDeviceToHost, st));
+    DRACO_HIP(hipStreamSynchronize(st));
+    memcpy(out, ho, sizeof(float) * n_out);
+    return 0;
+}
+
 }  // namespace
 
 // ---- the MoE FFN of one layer inside the device decode loop --------------
@@ -450,6 +515,18 @@ void draco_moe_ffn_op(const float* xn, void* pv, float* out) {
                              out)) {
         fprintf(stderr, "draco_moe_ffn_op: rc %d: %s\n", rc, last_error());
         if (out && p->n_out > 0) poison(out, (size_t)p->n_out);
+    }
+}
+
+// src/m6_layer.c:656-690 (bound by the reference's llama driver at import,
+// src/smol_engine.py:81).  scratch is accepted and not used.
+void m6_moe_batch4(const float* x0, const uint64_t* ptrs, const int* codes, const float* wtop, int n_exp, int inter,
+                   int n_in, int n_out, float* scratch, float* out) {
+    (void)scratch;
+    std::lock_guard<std::recursive_mutex> g(api_mutex());
+    if (int rc = moe_batch(x0, ptrs, codes, wtop, n_exp, inter, n_in, n_out, out)) {
+        fprintf(stderr, "m6_moe_batch4: rc %d: %s\n", rc, last_error());
+        if (out && n_out > 0) poison(out, (size_t)n_out);  // unserved input: NaN, not stale values
     }
 }
 

@@ -1319,7 +1319,8 @@ int draco_qwen_generate(const void* layers, int n_layer, int h, float eps, const
     if (!dtok || !dred || !dlog) return report(-2, "draco_qwen_generate");
     int* cursor = dtok + ntok + 8;
     int* dri = (int*)(dred + hblocks + 32);
-    const bool fused_head = hm->L.code == DRACO_Q4_K || hm->L.code == DRACO_Q6_K || hm->L.code == DRACO_Q8_0;
+    const bool fused_head = hm->L.code == DRACO_Q4_K || hm->L.code == DRACO_Q5_K || hm->L.code == DRACO_Q6_K ||
+                            hm->L.code == DRACO_Q8_0;
     const int n_chunked = (g_qwen_chunk > 0 && n_prompt - 1 >= 2 && !qstack_has_moe(s)) ? n_prompt - 1 : 0;
     if (n_chunked && qstack_pf(s, g_qwen_chunk)) return report(-2, "draco_qwen_generate (prefill buffers)");
     std::vector<int> ht(ntok + 64, 0);

@@ -6,7 +6,8 @@
 #include "formats.h"
 
 // Value p of row `tok` of a private-layout matrix; bit-identical to the host
-// decoders: (d*sc)*q for Q6_K, d*sc*q - dmin*m for Q4_K, q*d for Q8_0.
+// decoders: (d*sc)*q for Q6_K, d*sc*q - dmin*m for Q4_K, (q*d)*sc - dmin*m
+// for Q5_K, q*d for Q8_0.
 __device__ __forceinline__ float embed_value(const uint8_t* __restrict__ base, const DracoLayout& L, int tok, int p) {
 #pragma clang fp contract(off)  // each product rounded on its own, as the host decoders
     // a row outside the matrix reads row 0 (host entry points reject such ids;
@@ -45,6 +46,24 @@ __device__ __forceinline__ float embed_value(const uint8_t* __restrict__ base, c
         const uint8_t qb = base[draco_q4t_qs(nb, tok, b, (j >> 1) * 32 + (i & 31))] ^ 0x80;
         const int q = (j & 1) ? (qb >> 4) : (qb & 0xF);
         val = (d * (float)sc) * (float)q - dmin * (float)m;
+    } else if (L.code == DRACO_Q5_K) {
+        // the row decoder's order, (q*d)*sc - dmin*m (src/m5/m5_gemm.c:212-231)
+        const int i = p & 255, j = i >> 5, b = p >> 8;
+        const uint8_t* hd = base + draco_q5t_hdr(nb, tok, b);
+        const float d = h2f(*reinterpret_cast<const uint16_t*>(hd)), dmin = h2f(*reinterpret_cast<const uint16_t*>(hd + 2));
+        const uint8_t* s = hd + 4;
+        int sc, m;
+        if (j < 4) {
+            sc = s[j] & 63;
+            m = s[j + 4] & 63;
+        } else {
+            sc = (s[j + 4] & 0xF) | ((s[j - 4] >> 6) << 4);
+            m = (s[j + 4] >> 4) | ((s[j] >> 6) << 4);
+        }
+        const uint8_t qb = base[draco_q5t_qs(nb, tok, b, (j >> 1) * 32 + (i & 31))];
+        const int nib = (j & 1) ? (qb >> 4) : (qb & 0xF);
+        const int top = (base[draco_q5t_qh(nb, tok, b, i & 31)] >> j) & 1;
+        val = (float)(nib | (top << 4)) * d * (float)sc - dmin * (float)m;
     } else if (L.code == DRACO_F32) {
         val = reinterpret_cast<const float*>(base)[(size_t)tok * n_in + p];
     } else if (L.code == DRACO_F16) {

@@ -56,7 +56,7 @@ DRACO_HD static inline int draco_block_values(int code) {
 
 // Private device layout of one matrix.
 //
-// Q4_K and Q6_K use a tile layout built for the int8 MFMA GEMV: rows are
+// Q4_K, Q5_K and Q6_K use a tile layout built for the int8 MFMA GEMV: rows are
 // grouped in tiles of 16, and for every (tile, super-block) "item" the 16
 // rows' blocks are stored together, ordered so that lane l = j + 16*g of a
 // wave (row j of the tile, lane group g = 0..3) finds each of its operands as
@@ -77,6 +77,13 @@ DRACO_HD static inline int draco_block_values(int code) {
 //     [3072,3328) lane l: sc[8*g2 + c + 2*r], r = 0..3 (4 bytes)
 //     [3328,3360) row j: d (f16)
 //
+//   Q5_K item, 2816 B (the Q4_K item's qs and header, then the high bits):
+//     [   0,1024) lane l: qs[(g>>1)*32 + (g&1)*16 + e] of row j (not XORed)
+//     [1024,2048) lane l: qs[64 + (g>>1)*32 + (g&1)*16 + e] of row j
+//     [2048,2304) row j: the 16-byte header (d, dmin, scales[12])
+//     [2304,2816) 16 bytes per (row j, half c): qh[16*c + e], e = 0..15, at
+//                 2304 + 16*(j + 16*c); lane l reads the half c = g&1
+//     (bit s of qh[k] is the fifth bit of value 32*s + k)
 //   Q8_0 : structure of arrays, [0] qs n_out*nb*32, [1] d n_out*nb*2 (f16)
 //   F16/F32 : [0] the GGUF rows unchanged
 // The repack only moves bytes (and flips the Q4_K bit 7); it is a bijection
@@ -90,6 +97,7 @@ struct DracoLayout {
 
 #define DRACO_Q4T_ITEM 2304
 #define DRACO_Q6T_ITEM 3360
+#define DRACO_Q5T_ITEM 2816
 
 // Byte offsets inside the tile layouts (row r, super-block b, byte index i of
 // the GGUF field).
@@ -102,6 +110,16 @@ DRACO_HD static inline size_t draco_q4t_qs(int nb, int r, int b, int i) {  // i 
 }
 DRACO_HD static inline size_t draco_q4t_hdr(int nb, int r, int b) {
     return draco_item(nb, r, b, DRACO_Q4T_ITEM) + 2048 + 16 * (r & 15);
+}
+DRACO_HD static inline size_t draco_q5t_qs(int nb, int r, int b, int i) {  // i in [0,128)
+    const int j2 = i >> 5, k = i & 31, g = ((j2 & 1) << 1) | (k >> 4);
+    return draco_item(nb, r, b, DRACO_Q5T_ITEM) + (size_t)(j2 >> 1) * 1024 + 16 * ((r & 15) + 16 * g) + (k & 15);
+}
+DRACO_HD static inline size_t draco_q5t_hdr(int nb, int r, int b) {
+    return draco_item(nb, r, b, DRACO_Q5T_ITEM) + 2048 + 16 * (r & 15);
+}
+DRACO_HD static inline size_t draco_q5t_qh(int nb, int r, int b, int i) {  // i in [0,32)
+    return draco_item(nb, r, b, DRACO_Q5T_ITEM) + 2304 + 16 * ((r & 15) + 16 * (i >> 4)) + (i & 15);
 }
 DRACO_HD static inline size_t draco_q6t_ql(int nb, int r, int b, int i) {  // i in [0,128)
     const int g2 = i >> 6, h = (i >> 5) & 1, c = (i >> 4) & 1, g = 2 * g2 + c;
@@ -138,6 +156,9 @@ static inline int draco_layout(int code, int n_out, int n_in, DracoLayout* L) {
         break;
     case DRACO_Q6_K:
         o = draco_align256((size_t)L->ntiles * L->nb * DRACO_Q6T_ITEM);
+        break;
+    case DRACO_Q5_K:
+        o = draco_align256((size_t)L->ntiles * L->nb * DRACO_Q5T_ITEM);
         break;
     case DRACO_Q8_0:
         L->off[0] = o; o = draco_align256(o + nbl * 32);

@@ -153,7 +153,8 @@ __device__ __forceinline__ auto seg_pick(const SegKArgs& a, int si, F f) -> decl
     return r;
 }
 
-// FM: 1 = Q4_K segments only, 2 = Q6_K only, 3 = both (per-tile switch).
+// FM: 1 = Q4_K segments only, 2 = Q6_K only, 3 = both (per-tile switch),
+// 4 = Q5_K only (Q5_K never shares a launch with the other formats).
 // MULTI: more than one segment (a SwiGLU pair counts as one); without it the
 // segment of every tile is 0 at compile time and its selection code is gone.
 // EPI: the epilogue when it is fixed for the launch (single segment), or
@@ -200,7 +201,7 @@ __global__ __launch_bounds__(64 * NW) void k_dq(const SegKArgs a) {
         if (KS) T -= khalf(T) * a.rot;
         const int si = MULTI ? seg_of_tile(a, T) : 0;
         const bool q4 = FM == 3 ? seg_pick(a, si, [](const SegK& d) { return d.code; }) == DRACO_Q4_K : FM == 1;
-        const size_t ib = q4 ? DRACO_Q4T_ITEM : DRACO_Q6T_ITEM;
+        const size_t ib = FM == 4 ? DRACO_Q5T_ITEM : (q4 ? DRACO_Q4T_ITEM : DRACO_Q6T_ITEM);
         const int tl = T - seg_pick(a, si, [](const SegK& d) { return d.first; }) +
                        seg_pick(a, si, [](const SegK& d) { return d.tile0; });
         const size_t off = (size_t)tl * nb * ib;
@@ -211,10 +212,12 @@ __global__ __launch_bounds__(64 * NW) void k_dq(const SegKArgs a) {
         return r;
     };
     auto load_at = [&](const uint8_t* p, const uint8_t* p2, bool q4, Frag& f, Frag& f2) {
-        if (q4) load_q4(p, lane, f);
+        if (FM == 4) load_q5(p, lane, f);
+        else if (q4) load_q4(p, lane, f);
         else load_q6(p, lane, f);
         if (DUAL) {
-            if (q4) load_q4(p2, lane, f2);
+            if (FM == 4) load_q5(p2, lane, f2);
+            else if (q4) load_q4(p2, lane, f2);
             else load_q6(p2, lane, f2);
         }
     };
@@ -275,13 +278,13 @@ __global__ __launch_bounds__(64 * NW) void k_dq(const SegKArgs a) {
     // analysis no choice but vmcnt(0) before every use.
     int lt = bx < total ? bx : total - 1, lb = w + kfirst(lt), lp = 0, li = 0;
     TileRef lref = tile_ref(lt);
-    const size_t lib = lref.q4 ? DRACO_Q4T_ITEM : DRACO_Q6T_ITEM;
+    const size_t lib = FM == 4 ? DRACO_Q5T_ITEM : (lref.q4 ? DRACO_Q4T_ITEM : DRACO_Q6T_ITEM);
     const uint8_t* lastp = lref.p + (size_t)(w < nb ? w : nb - 1) * lib;
     const uint8_t* lastp2 = lref.p2 + (size_t)(w < nb ? w : nb - 1) * lib;
     bool lastq4 = lref.q4;
     auto load_next = [&](Frag& f, Frag& f2) {
         if (li < n_items && lb < nb) {
-            const size_t ib = lref.q4 ? DRACO_Q4T_ITEM : DRACO_Q6T_ITEM;
+            const size_t ib = FM == 4 ? DRACO_Q5T_ITEM : (lref.q4 ? DRACO_Q4T_ITEM : DRACO_Q6T_ITEM);
             lastp = lref.p + (size_t)lb * ib;
             lastp2 = lref.p2 + (size_t)lb * ib;
             lastq4 = lref.q4;
@@ -450,7 +453,17 @@ __global__ __launch_bounds__(64 * NW) void k_dq(const SegKArgs a) {
         load_next(nxt, nxt2);
         if (cb < nb) {
             float cD, cM, cD2 = 0.f, cM2 = 0.f;
-            if (cq4) {
+            if constexpr (FM == 4) {
+                const int8_t* xa = adig ? xd + (size_t)cb * 1024 + (gl4 * 4 + (j & 3)) * 16 : zero;
+                const float2 r = dot_q5(cur, xa, xsm, cb * 16 + gl4, g);
+                cD = r.x;
+                cM = r.y;
+                if (DUAL) {
+                    const float2 r2 = dot_q5(cur2, xa, xsm, cb * 16 + gl4, g);
+                    cD2 = r2.x;
+                    cM2 = r2.y;
+                }
+            } else if (cq4) {
                 const int8_t* xa = adig ? xd + (size_t)cb * 1024 + (gl4 * 4 + (j & 3)) * 16 : zero;
                 const float2 r = dot_q4(cur, xa, xsm, cb * 16 + gl4, g);
                 cD = r.x;
@@ -1015,7 +1028,21 @@ void launch_dq_nw(SegLaunch& a, int fm, bool dual, int grid, hipStream_t st) {
     }
 }
 
-// Q4_K / Q6_K segments: tile bookkeeping, instance choice, persistent grid.
+// Q5_K launches: the SwiGLU pair or per-tile epilogues read at run time, the
+// RMSNorm prologue or none (a smaller instance set than Q4_K / Q6_K's)
+template <int NW>
+void launch_dq_q5(SegLaunch& a, bool dual, int grid, hipStream_t st) {
+    if (dual) {
+        if (a.do_norm) launch_dq<NW, 4, true, false, EPI_SWIGLU, 1>(a, grid, st);
+        else launch_dq<NW, 4, true, false, EPI_SWIGLU, 0>(a, grid, st);
+    } else if (a.do_norm) {
+        launch_dq<NW, 4, false, true, EPI_RT, 1>(a, grid, st);
+    } else {
+        launch_dq<NW, 4, false, true, EPI_RT, 0>(a, grid, st);
+    }
+}
+
+// Q4_K / Q5_K / Q6_K segments: tile bookkeeping, instance choice, persistent grid.
 int seg_launch_dq(SegLaunch& a, hipStream_t st) {
     const int n_in = a.n_in;
     if (n_in % 256 || n_in > 16384) return -1;
@@ -1026,7 +1053,7 @@ int seg_launch_dq(SegLaunch& a, hipStream_t st) {
         SegDesc& s = a.seg[i];
         if (s.row1 <= 0) s.row1 = s.L.n_out;
         if (s.row0 < 0 || s.row1 > s.L.n_out || s.row0 >= s.row1) return -1;
-        fm |= s.L.code == DRACO_Q4_K ? 1 : 2;
+        fm |= s.L.code == DRACO_Q4_K ? 1 : (s.L.code == DRACO_Q6_K ? 2 : 4);
         s.tile0 = s.row0 / 16;
         s.first_tile = tiles;
         s.n_tiles = (s.row1 + 15) / 16 - s.tile0;
@@ -1049,6 +1076,9 @@ int seg_launch_dq(SegLaunch& a, hipStream_t st) {
         tiles += s.n_tiles;
     }
     if (dual && (a.nseg != 2 || fm == 3)) return -1;
+    // Q5_K: launches of Q5_K segments only, with the RMSNorm prologue or none
+    // (its layers never take a split-K half, a pending residual or row dots)
+    if ((fm & 4) && (fm != 4 || a.ksplit || a.do_norm > 1)) return -1;
     // GNORM prologue: one residual segment (a store segment when split-K) over whole 128-wide groups
     if (a.do_norm == 2 && (a.nseg != 1 || a.seg[0].epi != (a.ksplit ? EPI_STORE : EPI_RESID) || n_in % 128 || !a.kc))
         return -1;
@@ -1062,7 +1092,7 @@ int seg_launch_dq(SegLaunch& a, hipStream_t st) {
     }
     // row dots: store / residual segments only, on a normalising launch
     int gd_n = 0;
-    if (a.gdot_n > 0 && !a.ksplit && !dual && a.nseg >= 2 && (a.do_norm == 1 || a.do_norm == 3) && a.gdot_w0 &&
+    if (a.gdot_n > 0 && fm != 4 && !a.ksplit && !dual && a.nseg >= 2 && (a.do_norm == 1 || a.do_norm == 3) && a.gdot_w0 &&
         a.gdot_w1 && a.gdot_out) {
         bool ok = true;
         for (int i = 0; i < a.nseg; i++) ok = ok && (a.seg[i].epi == EPI_STORE || a.seg[i].epi == EPI_RESID);
@@ -1103,9 +1133,17 @@ int seg_launch_dq(SegLaunch& a, hipStream_t st) {
         else launch_dq_gd<1>(a, fm, grid, st);
         return 0;
     }
-    if (nw == 4) launch_dq_nw<4>(a, fm, dual, grid, st);
-    else if (nw == 8) launch_dq_nw<8>(a, fm, dual, grid, st);
-    else launch_dq_nw<16>(a, fm, dual, grid, st);
+    if (fm == 4) {
+        if (nw == 4) launch_dq_q5<4>(a, dual, grid, st);
+        else if (nw == 8) launch_dq_q5<8>(a, dual, grid, st);
+        else launch_dq_q5<16>(a, dual, grid, st);
+    } else if (nw == 4) {
+        launch_dq_nw<4>(a, fm, dual, grid, st);
+    } else if (nw == 8) {
+        launch_dq_nw<8>(a, fm, dual, grid, st);
+    } else {
+        launch_dq_nw<16>(a, fm, dual, grid, st);
+    }
     if (a.seg[0].epi == EPI_ARGMAX)
         hipLaunchKernelGGL(k_argmax_finalize, dim3(finalize_blocks(a.emb_out, a.emb_L.n_in)), dim3(256), 0, st, a.am_val, a.am_idx, grid, a.tokens,
                            const_cast<int*>(a.cursor), a.advance_state, a.advance_layers, a.emb, a.emb_L,
@@ -1255,7 +1293,7 @@ int draco_seg_launch(SegLaunch& a, hipStream_t st) {
     for (int i = 0; i < a.nseg; i++) {
         const int c = a.seg[i].L.code;
         if (a.seg[i].L.n_in != a.n_in) return -1;
-        if (c == DRACO_Q4_K || c == DRACO_Q6_K) kq = true;
+        if (c == DRACO_Q4_K || c == DRACO_Q6_K || c == DRACO_Q5_K) kq = true;
         else if (c == DRACO_Q8_0) q8 = true;
         else return -1;
     }
@@ -1269,7 +1307,7 @@ int draco_gemv_launch(const DracoMat& m, const float* x, float* y, const float* 
     if (row0 < 0 || row1 > m.L.n_out || row0 > row1) return -1;
     if (row0 == row1) return 0;
     const int code = m.L.code;
-    if (code == DRACO_Q4_K || code == DRACO_Q6_K) {
+    if (code == DRACO_Q4_K || code == DRACO_Q6_K || code == DRACO_Q5_K) {
         SegLaunch a = {};
         a.nseg = 1;
         a.n_in = m.L.n_in;
@@ -1315,8 +1353,8 @@ int draco_gemv_launch(const DracoMat& m, const float* x, float* y, const float* 
 }
 
 int draco_gemv_supported(int code) {
-    return code == DRACO_Q4_K || code == DRACO_Q6_K || code == DRACO_Q8_0 || code == DRACO_F32 ||
-           code == DRACO_F16;
+    return code == DRACO_Q4_K || code == DRACO_Q5_K || code == DRACO_Q6_K || code == DRACO_Q8_0 ||
+           code == DRACO_F32 || code == DRACO_F16;
 }
 
 // Host-side launch planning, exported so tests can enumerate shapes without a

@@ -2,8 +2,8 @@
 // models, the one-time repack into the private device layout, and the rope
 // angle table.  Pure CPU code (no HIP calls), so it is testable without a GPU.
 //
-// The encoders write valid GGUF Q8_0 / Q4_K / Q6_K blocks (layouts as read by
-// src/m5_kern_scalar.c:58-142).  Any valid encoder is acceptable for the
+// The encoders write valid GGUF Q8_0 / Q4_K / Q5_K / Q6_K blocks (layouts as
+// read by src/m5_kern_scalar.c:58-142).  Any valid encoder is acceptable for the
 // benchmark configurations: the GPU path and the CPU oracle consume the same
 // bytes.  Rounding is round-half-even everywhere (rintf), so the bytes are
 // reproducible on every IEEE host.
@@ -120,6 +120,53 @@ static void enc_q4_k(const float* x, uint8_t* blk) {
     }
 }
 
+// ---- Q5_K: [d f16][dmin f16][scales 12][qh 32][qs 128]; w = d*sc_j*q - dmin*m_j,
+// q = nibble | (bit j of qh[k]) << 4 for value 32 j + k ----
+static void enc_q5_k(const float* x, uint8_t* blk) {
+    float scale[8], minv[8];
+    for (int j = 0; j < 8; j++) {
+        float lo = 0.f, hi = -INFINITY;
+        for (int k = 0; k < 32; k++) {
+            lo = fminf(lo, x[j * 32 + k]);
+            hi = fmaxf(hi, x[j * 32 + k]);
+        }
+        if (hi < lo) hi = lo;
+        scale[j] = (hi - lo) / 31.f;
+        minv[j] = -lo;
+    }
+    float ms = 0.f, mm = 0.f;
+    for (int j = 0; j < 8; j++) {
+        ms = fmaxf(ms, scale[j]);
+        mm = fmaxf(mm, minv[j]);
+    }
+    const uint16_t hd = f32_to_f16(ms / 63.f), hm = f32_to_f16(mm / 63.f);
+    const float d = f16_to_f32(hd), dmin = f16_to_f32(hm);
+    int sc[8], mn[8];
+    for (int j = 0; j < 8; j++) {
+        sc[j] = d > 0.f ? (int)clampf(rintf(scale[j] / d), 0.f, 63.f) : 0;
+        mn[j] = dmin > 0.f ? (int)clampf(rintf(minv[j] / dmin), 0.f, 63.f) : 0;
+    }
+    memcpy(blk, &hd, 2);
+    memcpy(blk + 2, &hm, 2);
+    uint8_t* s = blk + 4;
+    for (int i = 0; i < 4; i++) {
+        s[i] = (uint8_t)(sc[i] | ((sc[4 + i] >> 4) << 6));
+        s[4 + i] = (uint8_t)(mn[i] | ((mn[4 + i] >> 4) << 6));
+        s[8 + i] = (uint8_t)((sc[4 + i] & 0xF) | ((mn[4 + i] & 0xF) << 4));
+    }
+    uint8_t* qh = blk + 16;
+    uint8_t* qs = blk + 48;
+    memset(qh, 0, 32 + 128);
+    for (int j = 0; j < 8; j++) {
+        const float S = d * (float)sc[j], M = dmin * (float)mn[j];
+        for (int k = 0; k < 32; k++) {
+            const int q = S > 0.f ? (int)clampf(rintf((x[j * 32 + k] + M) / S), 0.f, 31.f) : 0;
+            qs[(j >> 1) * 32 + k] |= (uint8_t)((q & 15) << ((j & 1) * 4));
+            qh[k] |= (uint8_t)((q >> 4) << j);
+        }
+    }
+}
+
 // ---- Q6_K: [ql 128][qh 64][sc 16 x int8][d f16]; w = d*sc_g*(q-32) ----
 static void enc_q6_k(const float* x, uint8_t* blk) {
     float gs[16];
@@ -159,8 +206,8 @@ int draco_quantize(int code, const float* x, int n_rows, int n_in, uint8_t* out)
     const size_t rb = draco_row_bytes(code, n_in);
     const int nb = n_in / bv;
     const int64_t total = (int64_t)n_rows * nb;
-    const int bb = code == DRACO_Q8_0 ? 34 : (code == DRACO_Q4_K ? 144 : 210);
-    if (code != DRACO_Q8_0 && code != DRACO_Q4_K && code != DRACO_Q6_K) return -1;
+    const int bb = (int)draco_row_bytes(code, bv);
+    if (code != DRACO_Q8_0 && code != DRACO_Q4_K && code != DRACO_Q5_K && code != DRACO_Q6_K) return -1;
     #pragma omp parallel for schedule(static)
     for (int64_t i = 0; i < total; i++) {
         const int64_t r = i / nb, b = i % nb;
@@ -168,6 +215,7 @@ int draco_quantize(int code, const float* x, int n_rows, int n_in, uint8_t* out)
         uint8_t* dst = out + r * (int64_t)rb + b * bb;
         if (code == DRACO_Q8_0) enc_q8_0(src, dst);
         else if (code == DRACO_Q4_K) enc_q4_k(src, dst);
+        else if (code == DRACO_Q5_K) enc_q5_k(src, dst);
         else enc_q6_k(src, dst);
     }
     return 0;
@@ -191,8 +239,8 @@ int draco_repack(int code, const uint8_t* src, int n_out, int n_in, uint8_t* dst
         memcpy(dst, src, rb * (size_t)n_out);
         return 0;
     }
-    if (code != DRACO_Q4_K && code != DRACO_Q6_K && code != DRACO_Q8_0) return -1;
-    if (code == DRACO_Q4_K || code == DRACO_Q6_K) memset(dst, 0, L.bytes);  // padding rows of the last tile
+    if (code != DRACO_Q4_K && code != DRACO_Q5_K && code != DRACO_Q6_K && code != DRACO_Q8_0) return -1;
+    if (code != DRACO_Q8_0) memset(dst, 0, L.bytes);  // padding rows of the last tile
     #pragma omp parallel for schedule(static)
     for (int r = 0; r < n_out; r++) {
         for (int b = 0; b < nb; b++) {
@@ -201,6 +249,11 @@ int draco_repack(int code, const uint8_t* src, int n_out, int n_in, uint8_t* dst
                 memcpy(dst + draco_q4t_hdr(nb, r, b), blk, 16);
                 for (int i = 0; i < 128; i += 16)  // 16-byte runs stay contiguous
                     for (int e = 0; e < 16; e++) dst[draco_q4t_qs(nb, r, b, i) + e] = blk[16 + i + e] ^ 0x80;
+            } else if (code == DRACO_Q5_K) {
+                const uint8_t* blk = src + (size_t)r * rb + (size_t)b * 176;
+                memcpy(dst + draco_q5t_hdr(nb, r, b), blk, 16);
+                for (int i = 0; i < 32; i += 16) memcpy(dst + draco_q5t_qh(nb, r, b, i), blk + 16 + i, 16);
+                for (int i = 0; i < 128; i += 16) memcpy(dst + draco_q5t_qs(nb, r, b, i), blk + 48 + i, 16);
             } else if (code == DRACO_Q6_K) {
                 const uint8_t* blk = src + (size_t)r * rb + (size_t)b * 210;
                 for (int i = 0; i < 128; i += 16) memcpy(dst + draco_q6t_ql(nb, r, b, i), blk + i, 16);
@@ -234,6 +287,11 @@ int draco_unpack(int code, const uint8_t* src, int n_out, int n_in, uint8_t* dst
                 uint8_t* blk = dst + (size_t)r * rb + (size_t)b * 144;
                 memcpy(blk, src + draco_q4t_hdr(nb, r, b), 16);
                 for (int i = 0; i < 128; i++) blk[16 + i] = src[draco_q4t_qs(nb, r, b, i)] ^ 0x80;
+            } else if (code == DRACO_Q5_K) {
+                uint8_t* blk = dst + (size_t)r * rb + (size_t)b * 176;
+                memcpy(blk, src + draco_q5t_hdr(nb, r, b), 16);
+                for (int i = 0; i < 32; i++) blk[16 + i] = src[draco_q5t_qh(nb, r, b, i)];
+                for (int i = 0; i < 128; i++) blk[48 + i] = src[draco_q5t_qs(nb, r, b, i)];
             } else if (code == DRACO_Q6_K) {
                 uint8_t* blk = dst + (size_t)r * rb + (size_t)b * 210;
                 for (int i = 0; i < 128; i++) blk[i] = src[draco_q6t_ql(nb, r, b, i)];

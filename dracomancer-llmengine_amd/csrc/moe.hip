@@ -595,7 +595,12 @@ int dispatch_grp(const MoeArgs& a, int fm, bool dual, bool xper, bool route, int
         else launch_grp<NW, 2, true, false, true>(a, grid, lds, st);
         return 0;
     }
-    if (dual) return -1;
+    if (dual) {  // gate/up + SwiGLU of slots fixed by the host (m6_moe_batch4)
+        if (xper) return -1;
+        if (fm == 1) launch_grp<NW, 1, true, false, false>(a, grid, lds, st);
+        else launch_grp<NW, 2, true, false, false>(a, grid, lds, st);
+        return 0;
+    }
     if (fm == 1) {
         if (xper) launch_grp<NW, 1, false, true, false>(a, grid, lds, st);
         else launch_grp<NW, 1, false, false, false>(a, grid, lds, st);

@@ -12,7 +12,8 @@
 typedef int v4i __attribute__((ext_vector_type(4)));
 
 struct Frag {
-    uint4 a, b, c;   // Q4_K: qs r=0, qs r=1, header.  Q6_K: ql A, ql B, qh
+    uint4 a, b, c;   // Q4_K / Q5_K: qs r=0, qs r=1, header.  Q6_K: ql A, ql B, qh
+    uint4 h;         // Q5_K: 16 qh bytes (the fifth bits)
     uint32_t sc, d;  // Q6_K: 4 scales, d
 };
 
@@ -20,6 +21,15 @@ __device__ __forceinline__ void load_q4(const uint8_t* item, int lane, Frag& f) 
     f.a = ldnt4(item + 16 * lane);
     f.b = ldnt4(item + 1024 + 16 * lane);
     f.c = ldnt4(item + 2048 + 16 * (lane & 15));
+    f.sc = 0u;
+    f.d = 0u;
+}
+
+__device__ __forceinline__ void load_q5(const uint8_t* item, int lane, Frag& f) {
+    f.a = ldnt4(item + 16 * lane);
+    f.b = ldnt4(item + 1024 + 16 * lane);
+    f.c = ldnt4(item + 2048 + 16 * (lane & 15));
+    f.h = ldnt4(item + 2304 + 16 * ((lane & 15) + 16 * ((lane >> 4) & 1)));
     f.sc = 0u;
     f.d = 0u;
 }
@@ -77,6 +87,49 @@ __device__ __forceinline__ float2 dot_q4(const Frag& f, const int8_t* xa, const 
             } else {
                 sD = fmaf(scf, fv * sm.x, sD);
             }
+            sM = fmaf((float)mn, sm.y, sM);
+        }
+    }
+    return make_float2(h2f((uint16_t)(f.c.x & 0xFFFF)) * sD, h2f((uint16_t)(f.c.x >> 16)) * sM);
+}
+
+// One Q5_K item: the Q4_K item's groups, each B byte the 5-bit quant
+// nibble | (fifth bit << 4) in [0, 31] (src/m5_kern_scalar.c:91-114: bit s of
+// qh[k] tops value 32*s + k), so a group's dot is (x.q5) and the weights
+// regroup as d*sc_s*(x.q5) - dmin*m_s*(sum x), as for Q4_K.
+// Returns (d * sum_g sc*(x.q), dmin * sum_g m*(sum x)).
+__device__ __forceinline__ float2 dot_q5(const Frag& f, const int8_t* xa, const float2* xsm, int gi, int g) {
+    const int gh = g >> 1;
+    const uint32_t H4[4] = {f.h.x, f.h.y, f.h.z, f.h.w};
+    float sD = 0.f, sM = 0.f;
+#pragma unroll
+    for (int r = 0; r < 2; r++) {
+        const uint4 q = r ? f.b : f.a;
+        const uint32_t Q4[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+        for (int nib = 0; nib < 2; nib++) {
+            const int s = 4 * r + 2 * gh + nib;  // sub-block of this lane's values
+            v4i B;
+#pragma unroll
+            for (int w = 0; w < 4; w++) {
+                const uint32_t lo = nib ? (Q4[w] >> 4) & 0x0F0F0F0Fu : Q4[w] & 0x0F0F0F0Fu;
+                B[w] = (int)(lo | (((H4[w] >> s) & 0x01010101u) << 4));
+            }
+            const int go = 8 * r + 2 * nib;
+            const v4i A = *reinterpret_cast<const v4i*>(xa + go * 64);
+            const v4i C = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, B, (v4i){0, 0, 0, 0}, 0, 0, 0);
+            const float fv = fold(C);
+            const float2 sm = xsm[gi + go];
+            const int s0 = 2 * gh + nib;
+            int sc, mn;
+            if (r == 0) {
+                sc = (f.c.y >> (8 * s0)) & 63;
+                mn = (f.c.z >> (8 * s0)) & 63;
+            } else {
+                sc = ((f.c.w >> (8 * s0)) & 15) | (((f.c.y >> (8 * s0 + 6)) & 3) << 4);
+                mn = ((f.c.w >> (8 * s0 + 4)) & 15) | (((f.c.z >> (8 * s0 + 6)) & 3) << 4);
+            }
+            sD = fmaf((float)sc, fv * sm.x, sD);
             sM = fmaf((float)mn, sm.y, sM);
         }
     }

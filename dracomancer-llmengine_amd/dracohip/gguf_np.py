@@ -47,6 +47,25 @@ def dequant_q4_k(row):
     return (dsc * q - dm).reshape(-1)
 
 
+def dequant_q5_k(row):
+    """(q*d)*sc - dmin*m, q = nibble | fifth bit << 4, the order of the
+    reference's row decoder (src/m5/m5_gemm.c:212-231)."""
+    blk = row.reshape(-1, 176)
+    nb = blk.shape[0]
+    d = _f16(blk[:, 0:2])
+    dmin = _f16(blk[:, 2:4])
+    sc, mn = _kscales(blk[:, 4:16])
+    qh = blk[:, 16:48]
+    qs = blk[:, 48:].reshape(nb, 4, 32)
+    q = np.empty((nb, 8, 32), np.int32)
+    q[:, 0::2, :] = qs & 0xF
+    q[:, 1::2, :] = qs >> 4
+    for j in range(8):
+        q[:, j, :] |= ((qh >> j) & 1).astype(np.int32) << 4
+    qd = q.astype(np.float32) * d[:, :, None]
+    return (qd * sc[:, :, None] - (dmin * mn)[:, :, None]).reshape(-1)
+
+
 def dequant_q6_k(row):
     blk = row.reshape(-1, 210)
     nb = blk.shape[0]
@@ -71,6 +90,8 @@ def dequant_row(code, row):
         return dequant_q4_k(row)
     if code == 4:
         return dequant_q6_k(row)
+    if code == 3:
+        return dequant_q5_k(row)
     if code == 9:
         return row.copy().view(np.float32)
     if code == 7:

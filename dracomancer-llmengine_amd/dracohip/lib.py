@@ -46,6 +46,7 @@ SIGNATURES = {
     "m6_engine_version": (ct.c_char_p, []),
     "m6_init_dl": (ct.c_int, [ct.c_char_p] * 5),
     "m6_init_extra_dl": (ct.c_int, [ct.c_char_p]),
+    "m6_init_iq3_dl": (ct.c_int, [ct.c_char_p]),
     "m6_forward_token": (ct.c_int, [f32p, ct.c_int, ct.c_float, ct.c_int, ct.c_void_p, ct.c_int, f32p]),
     "m6_head_op": (ct.c_int, [f32p, f32p, ct.c_int, ct.c_float, ct.c_void_p, ct.c_int, ct.c_int, f32p, f32p]),
     "m6_llama_attn_op": (None, [f32p, ct.c_void_p, ct.c_int, f32p]),
@@ -94,6 +95,7 @@ SIGNATURES = {
     "m6_moe_tok": (None, [ct.c_void_p, ct.c_void_p, f32p, f32p, i32p, f32p, ct.c_void_p, i32p] + [ct.c_int] * 6
                    + [f32p, f32p, i32p]),
     "m5_gemvn_q4k": (ct.c_int, [f32p, ct.c_long, u8p, i32p, ct.c_long, ct.c_int, ct.c_int, ct.c_int, f32p]),
+    "m6_moe_batch4": (None, [f32p, ct.c_void_p, i32p, f32p, ct.c_int, ct.c_int, ct.c_int, ct.c_int, f32p, f32p]),
     "m5_gemvn_q6k": (ct.c_int, [f32p, ct.c_long, u8p, i32p, ct.c_long, ct.c_int, ct.c_int, ct.c_int, f32p]),
     "draco_bench_granite_moe": (ct.c_int, [f32p, ct.c_void_p, i32p, f32p, ct.c_int, ct.c_int, ct.c_int, ct.c_int,
                                            ct.c_int, ct.c_int, f32p]),
@@ -101,6 +103,8 @@ SIGNATURES = {
     "m5_gemm_auto": (ct.c_int, [ct.c_int, f32p, u8p, ct.c_int, ct.c_int, ct.c_int, f32p]),
     "m5_gemm": (ct.c_int, [ct.c_int, f32p, u8p, ct.c_int, ct.c_int, ct.c_int, f32p, f32p]),
     "m5_dequant_row": (ct.c_int, [ct.c_int, u8p, ct.c_int, f32p]),
+    **{f"m5_gemm_{f}": (None, [f32p, u8p, ct.c_int, ct.c_int, ct.c_int, f32p])
+       for f in ("q80", "q6k", "q5k", "q4k", "iq4xs", "iq3s")},
     "draco_bench_gemm": (ct.c_int, [ct.c_int, u8p, ct.c_int, ct.c_int, ct.c_int, ct.c_int, ct.c_int, f32p]),
     # Gated-DeltaNet scan (src/m6_gdn_scan.c:18-93)
     "m6_gdn_scan": (None, [f32p] * 8 + [ct.c_int] * 3 + [f32p, f32p]),

@@ -21,7 +21,7 @@ import numpy as np
 
 from . import lib as _lib
 
-Q8_0, Q6_K, Q4_K, F16, F32 = 0, 4, 5, 7, 9
+Q8_0, Q5_K, Q6_K, Q4_K, F16, F32 = 0, 3, 4, 5, 7, 9
 
 
 @dataclass
@@ -86,6 +86,14 @@ TINY_Q8 = LlamaConfig(
     codes=dict(q=Q8_0, k=Q8_0, v=Q8_0, o=Q8_0, gate=Q8_0, up=Q8_0, down=Q8_0, emb=Q8_0, out=Q8_0),
     tied=True, n_prompt=8, n_gen=16, max_t=64, wscale=0.25)
 
+# Q5_K_M-style mix (Q5_K for q/k/o/gate/up and the embedding, Q6_K for
+# v/down and the untied head): the Q5_K parity cases
+TINY_Q5 = LlamaConfig(
+    name="tiny-q5_k_m", hidden=512, n_layer=2, n_head=8, n_kv=2, head_dim=64, n_ff=1024, vocab=1000,
+    eps=1e-5, rope_base=10000.0,
+    codes=dict(q=Q5_K, k=Q5_K, v=Q6_K, o=Q5_K, gate=Q5_K, up=Q5_K, down=Q6_K, emb=Q5_K, out=Q6_K),
+    tied=False, n_prompt=8, n_gen=16, max_t=64, wscale=0.25)
+
 # configs[3]'s attention block (32 q / 4 kv heads of 128, Q6_K projections,
 # cache of 512 rows) as a one-layer llama model: the attention parity cases
 ATTN_CFG3 = LlamaConfig(
@@ -112,7 +120,7 @@ MOE_TINY = LlamaConfig(
     codes=dict(q=Q6_K, k=Q6_K, v=Q6_K, o=Q6_K, gate=Q4_K, up=Q4_K, down=Q4_K, emb=Q4_K, out=Q6_K),
     tied=False, n_prompt=8, n_gen=16, max_t=64, n_exp=128, n_used=8, exp_ff=768)
 
-CONFIGS = {c.name: c for c in (SMOL360M, LLAMA1B, TINY_K, TINY_Q8, ATTN_CFG3, QWEN3_MOE, MOE_TINY)}
+CONFIGS = {c.name: c for c in (SMOL360M, LLAMA1B, TINY_K, TINY_Q8, TINY_Q5, ATTN_CFG3, QWEN3_MOE, MOE_TINY)}
 
 
 @dataclass

@@ -27,8 +27,8 @@ extern "C" {
 
 /* ---- per-format kernel-library ABI (drop-in for m5_kern*.so) ----------- */
 
-/* src/m5_kern_scalar.c:146-148.  1 if `code` is served (0 Q8_0, 4 Q6_K,
- * 5 Q4_K, 7 F16, 9 F32). */
+/* src/m5_kern_scalar.c:146-148.  1 if `code` is served (0 Q8_0, 3 Q5_K,
+ * 4 Q6_K, 5 Q4_K, 7 F16, 9 F32: the reference scalar kernel's set). */
 int m5_scalar_supported(int code);
 
 /* src/m5_kern_scalar.c:150-156.  y[n_out] = W[n_out x n_in] . x */
@@ -79,6 +79,10 @@ const char* m6_engine_version(void);
 int m6_init_dl(const char* p012, const char* p3, const char* p4, const char* p56, const char* ps);
 /* src/m6_layer.c:94-100; accepted (returns 0); Q5_0 (code 8) GEMVs return -1. */
 int m6_init_extra_dl(const char* p50);
+/* src/m6_layer.c:108-120 (the opt-in IQ3_S kernel slot, bound by
+ * src/qwen35_engine.py:103-108 when DRACO_IQ3_FAST=1).  IQ3_S is not carried:
+ * returns 1 ("could not load"), which the driver reports and goes on. */
+int m6_init_iq3_dl(const char* p12);
 /* src/m6_engine.c:61-83.  x[h] updated in place; every layer's *tlen += 1.
  * Layers whose ops are this library's m6_llama_attn_op / m6_dense_op run on
  * the device (KV caches mirrored on the device, see draco_state_pull/push);
@@ -159,7 +163,7 @@ size_t draco_resident_bytes(void);
  * [n_exp][n_in]) -> softmax -> stable top-n_used -> renormalised weights ->
  * per expert silu(gate.x)*(up.x) -> down -> weighted sum into out[n_out].
  * ptrs/codes: 3 per expert (gate, up, down), host pointers.  Served: Q4_K /
- * Q6_K experts, n_exp <= 512, n_used <= 16, inter and n_in multiples of 256,
+ * Q6_K experts, n_exp <= 512, n_used <= 64, inter and n_in multiples of 256,
  * n_out a multiple of 16.  `scratch` is not used (the reference's host scratch
  * is not needed by the device path).  Errors are printed (void, as the
  * reference). */
@@ -183,6 +187,15 @@ void m6_moe_tok(int (*DQ)(int, const uint8_t*, int, float*),
  * n_in % 256 != 0 (as the reference) or n_out_e % 16 != 0. */
 int m5_gemvn_q4k(const float* x, long x_stride, const uint8_t* W, const int* idx, long per, int n_out_e,
                  int n_in, int n_exp, float* y);
+/* m6_moe_batch4: src/m6_layer.c:656-690 (bound at import by the reference's
+ * llama driver, src/smol_engine.py:81) -- n_exp given experts, no router:
+ * out[n_out] = sum over j (ascending) of wtop[j] * down_j(silu(gate_j x0) *
+ * (up_j x0)), the weights as given.  ptrs/codes: 3 per expert (host).
+ * Served: Q4_K / Q6_K (one format per role), n_exp <= 64, inter and n_in
+ * multiples of 256, n_out a multiple of 16; anything else prints the error
+ * and leaves NaN in out (void, as the reference).  scratch is not used. */
+void m6_moe_batch4(const float* x0, const uint64_t* ptrs, const int* codes, const float* wtop, int n_exp, int inter,
+                   int n_in, int n_out, float* scratch, float* out);
 int m5_gemvn_q6k(const float* x, long x_stride, const uint8_t* W, const int* idx, long per, int n_out_e,
                  int n_in, int n_exp, float* y);
 /* The MoE FFN as an m6 ffn op (no reference counterpart as an op: the
@@ -209,15 +222,27 @@ int draco_bench_granite_moe(const float* x0, const uint64_t* ptrs, const int* co
 /* ---- Prefill GEMM: Y[T x n_out] = X[T x n_in] . W^T ----------------------
  * m5_gemm_auto: src/m5/m5_gemm_fused.c:231-241 (0 done, -1 code not served:
  * the caller falls back).  m5_gemm: src/m5/m5_gemm.c:249-272.  Host pointers.
- * Served: Q4_K and Q6_K on f16 MFMA (exact operands), Q8_0 as per-token
- * device GEMVs.
+ * Served: Q4_K and Q6_K on f16 MFMA (exact operands), Q8_0 and Q5_K as
+ * per-token device GEMVs.
  * `wbuf` is not used. */
 int m5_gemm_auto(int code, const float* X, const uint8_t* W, int c, int n_out, int n_in, float* Y);
 int m5_gemm(int code, const float* X, const uint8_t* W, int T, int n_out, int n_in, float* Y, float* wbuf);
+/* The per-format fused GEMMs of src/m5/m5_gemm_fused.c:78,211-228 (the
+ * FUSED3 instances and m5_gemm_iq3s), which the reference's prefill driver
+ * looks up by name (src/qwen35_prefill.py:76-80) and calls per format
+ * (:100-104): Y[c x n_out] = X[c x n_in] . W^T, as m5_gemm_auto for their
+ * code.  void, as the reference's: IQ4_XS and IQ3_S (not carried here) and
+ * failures print the error and leave NaN in Y. */
+void m5_gemm_q80(const float* X, const uint8_t* W, int c, int n_out, int n_in, float* Y);
+void m5_gemm_q6k(const float* X, const uint8_t* W, int c, int n_out, int n_in, float* Y);
+void m5_gemm_q5k(const float* X, const uint8_t* W, int c, int n_out, int n_in, float* Y);
+void m5_gemm_q4k(const float* X, const uint8_t* W, int c, int n_out, int n_in, float* Y);
+void m5_gemm_iq4xs(const float* X, const uint8_t* W, int c, int n_out, int n_in, float* Y);
+void m5_gemm_iq3s(const float* X, const uint8_t* W, int c, int n_out, int n_in, float* Y);
 /* m5_dequant_row: src/m5/m5_gemm.c:55-235 -- one GGUF row (host) ->
  * out[n_in] fp32, decoded on the device (from the resident copy when the row
  * lies inside a registered matrix).  0 done, -1 code not served: served are
- * Q8_0, Q4_K, Q6_K and F16 (the reference also decodes Q5_K and the IQ
+ * Q8_0, Q4_K, Q5_K, Q6_K and F16 (the reference also decodes the IQ
  * formats). */
 int m5_dequant_row(int code, const uint8_t* row, int n_in, float* out);
 /* No reference counterpart: out[0] us per GEMM including the activation

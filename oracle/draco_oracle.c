@@ -292,6 +292,24 @@ int or_dequant_row(int code, const uint8_t* row, int n_in, float* out) {
         }
         return 0;
     }
+    if (code == 3) {  /* Q5_K, src/m5/m5_gemm.c:212-231: (q*d)*sc - dmin*m */
+        for (int b = 0; b < n_in / 256; b++) {
+            const uint8_t* blk = row + (size_t)b * 176;
+            const float d = ld_f16(blk), dmin = ld_f16(blk + 2);
+            float sc[8], mn[8];
+            kq_scales(blk + 4, sc, mn);
+            const uint8_t* qh = blk + 16;
+            const uint8_t* qs = blk + 48;
+            for (int p = 0; p < 256; p++) {
+                const uint8_t qsb = qs[(p >> 6) * 32 + (p & 31)];
+                const int nib = ((p >> 5) & 1) ? (qsb >> 4) : (qsb & 0x0F);
+                const int bit = (qh[p & 31] >> (p >> 5)) & 1;
+                const int g = p >> 5;
+                out[b * 256 + p] = (float)(nib + (bit ? 16 : 0)) * d * sc[g] - dmin * mn[g];
+            }
+        }
+        return 0;
+    }
     if (code == 7) {
         for (int i = 0; i < n_in; i++) out[i] = ld_f16(row + (size_t)i * 2);
         return 0;
@@ -940,7 +958,7 @@ void or_moe_tok(const float* X, const int* order, const float* wtop,
 /* iq3s_grid.h is absent from the tree).                               */
 /* ------------------------------------------------------------------ */
 int or_gemm(int code, const float* X, const uint8_t* W, int T, int n_out, int n_in, float* Y) {
-    if (!or_supported(code) || code == 3) return -1;
+    if (!or_supported(code)) return -1;
     const size_t rs = or_rowbytes(code, n_in);
     #pragma omp parallel
     {

@@ -235,6 +235,51 @@ def gen_moe():
     print("moe.npz")
 
 
+MOE_BATCH4_CASES = [  # (tag, n experts, inter, n_in, n_out, codes (gate, up, down), seed)
+    ("b8", 8, 256, 512, 512, (5, 5, 4), 61),
+    ("b3q6", 3, 768, 2048, 2048, (4, 4, 5), 62),
+    ("b20", 20, 256, 256, 256, (5, 5, 5), 63),
+]
+
+
+def moe_batch4_inputs(n, inter, n_in, n_out, codes, seed):
+    """Expert bytes, their pointer / code tables, x and the (unnormalised)
+    weights of one m6_moe_batch4 case, from one rng stream."""
+    rng = np.random.default_rng(seed)
+    Wg = dlib.quantize(codes[0], rng.standard_normal((n * inter, n_in), dtype=np.float32) * np.float32(0.02))
+    Wu = dlib.quantize(codes[1], rng.standard_normal((n * inter, n_in), dtype=np.float32) * np.float32(0.02))
+    Wd = dlib.quantize(codes[2], rng.standard_normal((n * n_out, inter), dtype=np.float32) * np.float32(0.02))
+    x = rng.standard_normal(n_in, dtype=np.float32)
+    wtop = (rng.random(n) * 0.5 + 0.05).astype(np.float32)
+    pg, pu, pd = Wg.nbytes // n, Wu.nbytes // n, Wd.nbytes // n
+    ptrs = np.zeros(3 * n, np.uint64)
+    cds = np.zeros(3 * n, np.int32)
+    for e in range(n):
+        ptrs[3 * e:3 * e + 3] = (Wg.ctypes.data + e * pg, Wu.ctypes.data + e * pu, Wd.ctypes.data + e * pd)
+        cds[3 * e:3 * e + 3] = codes
+    return dict(Wg=Wg, Wu=Wu, Wd=Wd, x=x, wtop=wtop, ptrs=ptrs, codes=cds)
+
+
+def gen_moe_batch4():
+    """m6_moe_batch4 (src/m6_layer.c:656-690): given experts and weights."""
+    E = ref_engine()
+    # the C signature (src/m6_layer.c:656-658): 4 pointers, 4 ints, 2 pointers
+    E.m6_moe_batch4.argtypes = [ct.c_void_p] * 4 + [ct.c_int] * 4 + [ct.c_void_p] * 2
+    E.m6_moe_batch4.restype = None
+    out = {}
+    for tag, n, inter, n_in, n_out, codes, seed in MOE_BATCH4_CASES:
+        M = moe_batch4_inputs(n, inter, n_in, n_out, codes, seed)
+        scratch = np.zeros(3 * n * inter + n * n_out + 64, np.float32)
+        y = np.full(n_out, np.nan, np.float32)
+        E.m6_moe_batch4(M["x"].ctypes.data, M["ptrs"].ctypes.data, M["codes"].ctypes.data, M["wtop"].ctypes.data,
+                        n, inter, n_in, n_out, scratch.ctypes.data, y.ctypes.data)
+        out[f"{tag}_y"] = y
+        out[f"{tag}_digest"] = np.frombuffer(hashlib.sha256(M["Wg"].tobytes() + M["Wu"].tobytes() +
+                                                            M["Wd"].tobytes()).digest(), np.uint8)
+    np.savez_compressed(os.path.join(OUT, "moe_batch4.npz"), **out)
+    print("moe_batch4.npz")
+
+
 SHEXP_CASES = [  # (tag, shi, h, codes {gate, up, down, gate_inp}, seed)
     ("small", 256, 512, (5, 5, 4, 9), 51),
     ("q35", 512, 2048, (5, 5, 4, 9), 52),
@@ -519,6 +564,8 @@ JOBS = {
     "gemv": gen_gemv,
     "batch8k": gen_batch8k,
     "moe": gen_moe,
+    "moe_batch4": gen_moe_batch4,
+    "tiny_q5": lambda: gen_llama(models.TINY_Q5, "llama_tiny_q5.npz", logit_steps=(0, 15)),
     "moetok": gen_moetok,
     "attn_cfg3": gen_attn_cfg3,
     "shexp": gen_shexp,

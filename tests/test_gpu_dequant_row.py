@@ -1,6 +1,6 @@
 """m5_dequant_row (src/m5/m5_gemm.c:55-235) on the GPU through the C ABI.
 
-Rows of Q8_0 / Q4_K / Q6_K / F16 matrices are decoded on the device twice:
+Rows of Q8_0 / Q4_K / Q5_K / Q6_K / F16 matrices are decoded on the device twice:
 from the row's own bytes (matrix not registered) and from the resident copy
 of a registered matrix (the embedding decoder of the device decode loop).
 Both equal the oracle's or_dequant_row bit for bit; the oracle's decoder is
@@ -13,7 +13,8 @@ import pytest
 
 pytestmark = pytest.mark.gpu
 
-CASES = [(0, 8, 2048), (5, 8, 2048), (4, 8, 2048), (7, 4, 512), (5, 3, 14336), (4, 2, 4096), (0, 5, 960)]
+CASES = [(0, 8, 2048), (5, 8, 2048), (4, 8, 2048), (7, 4, 512), (5, 3, 14336), (4, 2, 4096), (0, 5, 960),
+         (3, 8, 2048), (3, 3, 14336)]
 
 
 def _matrix(code, n_out, n_in, seed):
@@ -48,5 +49,5 @@ def test_dequant_row_codes_not_served(hip):
     from dracohip import lib
     row = np.zeros(256, np.uint8)
     out = np.zeros(256, np.float32)
-    for code in (1, 2, 3, 6, 9, 13, 99):
+    for code in (1, 2, 6, 9, 13, 99):
         assert hip.m5_dequant_row(code, lib.pu8(row), 256, lib.pf(out)) == -1

@@ -23,7 +23,7 @@ def _case(code, T, n_out, n_in, seed):
     return W, X
 
 
-@pytest.mark.parametrize("code", [5, 4, 0])
+@pytest.mark.parametrize("code", [5, 4, 0, 3])
 @pytest.mark.parametrize("T,n_out,n_in", [(1, 16, 256), (7, 40, 512), (37, 96, 2048), (256, 2048, 2048),
                                           (64, 8192, 2048), (100, 2048, 8192), (9, 48, 768),
                                           # the ragged last prefill chunk on the K-split products, 3 super-blocks
@@ -59,3 +59,28 @@ def test_gemm_unsupported_code_returns_minus_one(hip):
     W = np.zeros(4 * 110, np.uint8)
     Y = np.zeros((2, 4), np.float32)
     assert hip.m5_gemm_auto(2, lib.pf(X), lib.pu8(W), 2, 4, 256, lib.pf(Y)) == -1   # IQ3_S: caller falls back
+
+
+@pytest.mark.parametrize("fname,code", [("q4k", 5), ("q6k", 4), ("q80", 0), ("q5k", 3)])
+def test_fused_entries_equal_gemm_auto(hip, fname, code):
+    """The per-format entries src/qwen35_prefill.py:76-80 looks up
+    (src/m5/m5_gemm_fused.c:211-228) compute what m5_gemm_auto does."""
+    from dracohip import lib
+    T, n_out, n_in = 40, 96, 512
+    W, X = _case(code, T, n_out, n_in, 77 + code)
+    Y = np.full((T, n_out), np.nan, np.float32)
+    getattr(hip, f"m5_gemm_{fname}")(lib.pf(X), lib.pu8(W), T, n_out, n_in, lib.pf(Y))
+    Y2 = np.zeros_like(Y)
+    assert hip.m5_gemm_auto(code, lib.pf(X), lib.pu8(W), T, n_out, n_in, lib.pf(Y2)) == 0
+    assert np.array_equal(Y, Y2)
+
+
+@pytest.mark.parametrize("fname", ["iq4xs", "iq3s"])
+def test_fused_entries_not_carried_leave_nan(hip, fname):
+    from dracohip import lib
+    X = np.ones((2, 256), np.float32)
+    W = np.zeros(4 * 136, np.uint8)
+    Y = np.zeros((2, 4), np.float32)
+    getattr(hip, f"m5_gemm_{fname}")(lib.pf(X), lib.pu8(W), 2, 4, 256, lib.pf(Y))
+    assert np.isnan(Y).all()
+

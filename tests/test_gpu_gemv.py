@@ -37,7 +37,7 @@ def _check(oracle, code, n_out, n_in, seed, W=None, x=None):
     return W, x, y
 
 
-@pytest.mark.parametrize("i", [i for i, c in enumerate(gg.GEMV_CASES) if c[1] in (0, 4, 5, 7, 9)])
+@pytest.mark.parametrize("i", [i for i, c in enumerate(gg.GEMV_CASES) if c[1] in (0, 3, 4, 5, 7, 9)])
 def test_gemv_golden_shapes(oracle, i):
     name, code, n_out, n_in = gg.GEMV_CASES[i]
     _check(oracle, code, n_out, n_in, 100 + i)
@@ -49,12 +49,14 @@ def test_gemv_golden_shapes(oracle, i):
     (0, 320, 960), (4, 3000, 2048), (5, 768, 2048), (4, 2048, 768),
     # one row, rows off the 16-row tile, n_in at the 16384 cap, a single super-block / Q8_0 block
     (5, 1, 4096), (5, 17, 16384), (4, 33, 256), (0, 1, 32), (4, 5, 16384),
+    # Q5_K (src/m5_kern_scalar.c:91-114): model shapes, one row, ragged tiles, the cap
+    (3, 2048, 2048), (3, 14336, 4096), (3, 4096, 14336), (3, 1, 4096), (3, 33, 256), (3, 17, 16384),
 ])
 def test_gemv_model_shapes(oracle, code, n_out, n_in):
     _check(oracle, code, n_out, n_in, 7 + n_out + n_in)
 
 
-@pytest.mark.parametrize("code", [0, 4, 5])
+@pytest.mark.parametrize("code", [0, 3, 4, 5])
 def test_gemv_range_absolute_rows(oracle, code):
     from dracohip import lib
     n_out, n_in = 300, 512 if code else 512
@@ -68,7 +70,7 @@ def test_gemv_range_absolute_rows(oracle, code):
     assert rel_err(y[37:250], yr[37:250]) <= TOL
 
 
-@pytest.mark.parametrize("code", [0, 4, 5])
+@pytest.mark.parametrize("code", [0, 3, 4, 5])
 def test_gemv_onehot_is_exact_column(oracle, code):
     """x = e_i returns column i of the decoded matrix exactly (the reference's
     own block-layout check, ROADMAP.md:568-580)."""
@@ -91,6 +93,8 @@ def test_unsupported_code_fails_loudly():
     y = np.zeros(4, np.float32)
     assert L.m5_gemv(2, lib.pf(x), lib.pu8(W), 4, 256, lib.pf(y)) == -1
     assert L.m5_scalar_supported(2) == 0 and L.m5_scalar_supported(5) == 1
+    # the reference's scalar kernel serves 0, 3, 4, 5, 7, 9 (src/m5_kern_scalar.c:146-148)
+    assert [c for c in range(10) if L.m5_scalar_supported(c)] == [0, 3, 4, 5, 7, 9]
 
 
 def test_reregistered_address_is_not_stale(oracle):

@@ -13,6 +13,7 @@ import hashlib
 import numpy as np
 import pytest
 
+import gen_golden as gg
 from helpers import golden, rel_err
 
 pytestmark = pytest.mark.gpu
@@ -232,3 +233,34 @@ def test_unserved_moe_inputs_leave_nan(hip):
     hip.m6_moe_tok(None, None, lib.pf(z), lib.pf(X), lib.pi32(order), lib.pf(wtop), ct.c_void_p(M["ptrs"].ctypes.data),
                    lib.pi32(codes), T, n_used, inter, H, H, n_exp, lib.pf(out), lib.pf(z), lib.pi32(zi))
     assert np.all(np.isnan(out))
+
+
+@pytest.mark.parametrize("tag", [c[0] for c in gg.MOE_BATCH4_CASES])
+def test_moe_batch4_vs_reference_golden(hip, tag):
+    """m6_moe_batch4 (src/m6_layer.c:656-690): given experts and weights,
+    against the compiled reference's output on the same bytes."""
+    from dracohip import lib
+    g = golden("moe_batch4.npz")
+    tag_, n, inter, n_in, n_out, codes, seed = [c for c in gg.MOE_BATCH4_CASES if c[0] == tag][0]
+    M = gg.moe_batch4_inputs(n, inter, n_in, n_out, codes, seed)
+    assert hashlib.sha256(M["Wg"].tobytes() + M["Wu"].tobytes() + M["Wd"].tobytes()).digest() == \
+        g[f"{tag}_digest"].tobytes()
+    y = np.full(n_out, np.nan, np.float32)
+    print(f"[moe_batch4] {tag}: {n} experts {inter}x{n_in} -> {n_out}", flush=True)
+    for _ in range(2):  # the second call reuses the registered experts
+        hip.m6_moe_batch4(lib.pf(M["x"]), ct.c_void_p(M["ptrs"].ctypes.data), lib.pi32(M["codes"]), lib.pf(M["wtop"]),
+                          n, inter, n_in, n_out, lib.pf(np.zeros(4, np.float32)), lib.pf(y))
+        assert rel_err(y, g[f"{tag}_y"]) <= TOL
+
+
+def test_moe_batch4_unserved_leaves_nan(hip):
+    """More experts than the device path serves, or IQ formats: NaN, not stale values."""
+    from dracohip import lib
+    M = gg.moe_batch4_inputs(8, 256, 512, 512, (5, 5, 4), 70)
+    y = np.zeros(512, np.float32)
+    bad = M["codes"].copy()
+    bad[2::3] = 2  # IQ3_S down projections
+    hip.m6_moe_batch4(lib.pf(M["x"]), ct.c_void_p(M["ptrs"].ctypes.data), lib.pi32(bad), lib.pf(M["wtop"]),
+                      8, 256, 512, 512, lib.pf(np.zeros(4, np.float32)), lib.pf(y))
+    assert np.isnan(y).all()
+

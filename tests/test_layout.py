@@ -9,7 +9,7 @@ the C offset helpers.
 import numpy as np
 import pytest
 
-Q4T_ITEM, Q6T_ITEM = 2304, 3360
+Q4T_ITEM, Q6T_ITEM, Q5T_ITEM = 2304, 3360, 2816
 
 
 def _layout(lib, code, n_out, n_in, rng):
@@ -23,7 +23,7 @@ def _layout(lib, code, n_out, n_in, rng):
     return W, dev
 
 
-@pytest.mark.parametrize("code", [0, 4, 5])
+@pytest.mark.parametrize("code", [0, 3, 4, 5])
 @pytest.mark.parametrize("n_out,n_in", [(1, 256), (17, 512), (48, 768), (100, 256), (33, 2048)])
 def test_repack_roundtrip(code, n_out, n_in):
     from dracohip import lib
@@ -57,6 +57,50 @@ def test_q4k_tile_positions(n_out, n_in):
         for j in range(n_out % 16, 16):
             it = items[ntiles - 1]
             assert not it[:, 2048 + 16 * j: 2048 + 16 * j + 16].any()
+
+
+@pytest.mark.parametrize("n_out,n_in", [(16, 256), (37, 768)])
+def test_q5k_tile_positions(n_out, n_in):
+    """Q5_K items: the Q4_K positions for qs (not XORed) and the header,
+    then qh[16 c + e] of row j at 2304 + 16 (j + 16 c)."""
+    from dracohip import lib
+    W, dev = _layout(lib, 3, n_out, n_in, np.random.default_rng(3))
+    nb = n_in // 256
+    blocks = W.reshape(n_out, nb, 176)
+    ntiles = (n_out + 15) // 16
+    items = dev[: ntiles * nb * Q5T_ITEM].reshape(ntiles, nb, Q5T_ITEM)
+    for r in range(n_out):
+        t, j = divmod(r, 16)
+        for b in range(nb):
+            blk, it = blocks[r, b], items[t, b]
+            assert np.array_equal(it[2048 + 16 * j: 2048 + 16 * j + 16], blk[:16])
+            for c in range(2):
+                assert np.array_equal(it[2304 + 16 * (j + 16 * c): 2320 + 16 * (j + 16 * c)], blk[16 + 16 * c:][:16])
+            for g in range(4):
+                l = j + 16 * g
+                for half in range(2):
+                    src = blk[48 + 64 * half + (g >> 1) * 32 + (g & 1) * 16:][:16]
+                    assert np.array_equal(it[1024 * half + 16 * l: 1024 * half + 16 * l + 16], src)
+
+
+def test_q5k_encoder_error_bound():
+    """The Q5_K encoder's values decode (numpy, the reference's row decoder
+    order) to within one quantization step of the input: per sub-block the
+    step is d*sc, and the offset dmin*m is within d*sc of -min(x) by
+    construction, so |w - x| <= 1.5 d sc + dmin / 2."""
+    from dracohip import lib, gguf_np
+    rng = np.random.default_rng(55)
+    x = rng.standard_normal((8, 512), dtype=np.float32) * np.float32(0.02)
+    W = lib.quantize(3, x)
+    rb = len(W) // 8
+    for r in range(8):
+        w = gguf_np.dequant_row(3, W[r * rb:(r + 1) * rb])
+        blk = W[r * rb:(r + 1) * rb].reshape(-1, 176)
+        d = blk[:, 0:2].copy().view(np.float16).astype(np.float32)[:, 0]
+        dmin = blk[:, 2:4].copy().view(np.float16).astype(np.float32)[:, 0]
+        step = np.repeat(d * 63, 256) * 1.5 + np.repeat(dmin, 256) * 0.5
+        assert np.all(np.abs(w - x[r]) <= step + 1e-7)
+        assert np.abs(w - x[r]).max() < 0.01 * np.abs(x[r]).max() * 10
 
 
 @pytest.mark.parametrize("n_out,n_in", [(16, 256), (21, 512)])

@@ -116,7 +116,8 @@ def test_granite_shexp(oracle, case):
     assert bits_equal(sg, g[f"{tag}_sg"]) and bits_equal(sh[:shi], g[f"{tag}_act"])
 
 
-@pytest.mark.parametrize("cfgname,fname", [("tiny-kquant", "llama_tiny_k.npz"), ("tiny-q8_0", "llama_tiny_q8.npz")])
+@pytest.mark.parametrize("cfgname,fname", [("tiny-kquant", "llama_tiny_k.npz"), ("tiny-q8_0", "llama_tiny_q8.npz"),
+                                          ("tiny-q5_k_m", "llama_tiny_q5.npz")])
 def test_llama_decode_tiny(oracle, cfgname, fname):
     """Token-serial prefill + greedy decode through the descriptor ABI, bitwise."""
     g = golden(fname)

@@ -21,7 +21,18 @@ from helpers import bits_equal, golden, rel_err
 from dracohip import gguf_np
 from oracle.oracle import HERE as ORACLE_DIR, Oracle, pf, pi32, pu8
 
-DEQUANT_CODES = (0, 4, 5, 7, 9)
+DEQUANT_CODES = (0, 3, 4, 5, 7, 9)
+
+
+def _same(code, a, b):
+    """Bit for bit, except Q5_K: the reference's row decoder rounds
+    (q*d)*sc - dmin*m (src/m5/m5_gemm.c:212-231) where its GEMV rounds
+    (d*sc)*q - dmin*m (src/m5_kern_scalar.c:91-114), so the two agree to a
+    couple of ulps of the product, not bitwise."""
+    if code != 3:
+        return bits_equal(a, b)
+    a, b = np.asarray(a, np.float64), np.asarray(b, np.float64)
+    return bool(np.all(np.abs(a - b) <= 2.0 ** -21 * np.maximum(np.abs(a), np.abs(b)) + 1e-30))
 
 
 def check_dequant_row(orc):
@@ -41,15 +52,15 @@ def check_dequant_row(orc):
             e[c] = 1.0
             cols[c] = orc.gemv(code, e, W, n_out, n_in)
             e[c] = 0.0
-        assert bits_equal(np.ascontiguousarray(cols.T), D), (name, "one-hot columns")
+        assert _same(code, np.ascontiguousarray(cols.T), D), (name, "one-hot columns")
         col = int(g[name + "_meta"][5])
-        assert bits_equal(np.ascontiguousarray(D[:, col]), g[name + "_col"]), (name, "reference column")
+        assert _same(code, np.ascontiguousarray(D[:, col]), g[name + "_col"]), (name, "reference column")
         rb = len(W) // n_out
         for r in range(n_out):
             assert bits_equal(gguf_np.dequant_row(code, W[r * rb:(r + 1) * rb]), D[r]), (name, "numpy row", r)
 
 
-GEMM_CASES = [(5, 48, 512, 7), (4, 33, 768, 5), (0, 40, 960, 9), (5, 5, 2048, 3)]  # code, n_out, n_in, T
+GEMM_CASES = [(5, 48, 512, 7), (4, 33, 768, 5), (0, 40, 960, 9), (5, 5, 2048, 3), (3, 24, 512, 4)]  # code, n_out, n_in, T
 
 
 def _gemm(orc, code, X, W, n_out, n_in):
@@ -85,7 +96,7 @@ def check_gemm(orc):
         Y1 = _gemm(orc, code, E, W, n_out, n_in)
         for t in range(T):
             col = orc.gemv(code, E[t], W, n_out, n_in)
-            assert bits_equal(Y1[t], col), (code, "one-hot", t)
+            assert _same(code, Y1[t], col), (code, "one-hot", t)
 
 
 def _moe_tok(orc, T, n_used, inter, n_in, n_exp, X, order, wtop, ptrs, ec):
