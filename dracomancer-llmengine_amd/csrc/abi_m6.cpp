@@ -93,9 +93,11 @@ struct Work {
     // a MoE layer after a split-K o projection: its input (the layer input +
     // the partials in pd), materialised by the router launch
     float* xm = nullptr;
+    // the fused attention merge + o projection's partials, [QD / 256][H]
+    float* po = nullptr;
     unsigned* cnt = nullptr;  // attention merge counters (one per kv head), zero at rest
     size_t cap_h = 0, cap_xn = 0, cap_xe = 0, cap_q = 0, cap_k = 0, cap_part = 0, cap_ff = 0, cap_pd = 0,
-           cap_xs = 0, cap_xm = 0;
+           cap_xs = 0, cap_xm = 0, cap_po = 0;
 };
 
 // Chunked-prefill buffers, token-major, for up to `cap` tokens per chunk.
@@ -270,6 +272,7 @@ int ensure_work(Work& w, int H, int QD, int KD, int NH, int HD, int max_t, int F
     if (grow(&w.pd, &w.cap_pd, 2 * (size_t)H + 64)) return -2;
     if (grow(&w.xs, &w.cap_xs, H + 64)) return -2;
     if (grow(&w.xm, &w.cap_xm, H + 64)) return -2;
+    if (grow(&w.po, &w.cap_po, (size_t)(QD / 256 > 0 ? QD / 256 : 1) * H + 64)) return -2;
     if (w.cap_q < (size_t)QD) {
         size_t c = w.cap_q;
         if (grow(&w.q, &c, QD)) return -2;
@@ -461,7 +464,7 @@ int enqueue_qkv(DevAttn* a, Work& w, const float* x, int norm, const float* norm
 // the o projection's split-K partials) the gate/up launch forms the input in
 // its RMSNorm prologue and stores it to pend_sum (one launch, same formats).
 int enqueue_gateup(DevFfn* f, Work& w, const float* x, int norm, const float* norm_w, float eps,
-                   hipStream_t st, const float* pend = nullptr, float* pend_sum = nullptr) {
+                   hipStream_t st, const float* pend = nullptr, float* pend_sum = nullptr, int npend = 2) {
     if (pend && (f->g->L.code != f->u->L.code || !norm || !pend_sum))
         return fail(-1, "gate/up: a pending residual needs one launch with the RMSNorm prologue");
     if (f->g->L.code == f->u->L.code) {
@@ -469,7 +472,7 @@ int enqueue_gateup(DevFfn* f, Work& w, const float* x, int norm, const float* no
         s.nseg = 2;
         s.n_in = f->H;
         s.x = x;
-        s.do_norm = pend ? 3 : norm;
+        s.do_norm = pend ? (npend == 8 ? 4 : 3) : norm;
         s.norm_w = norm_w;
         s.eps = eps;
         if (pend) {
@@ -548,6 +551,31 @@ bool ksplit_o_dense(const DevModel* m, int l) {
     return kq(f->g) && kq(&o) && draco_dq_ksplit_waves(o.L.n_in, 0) && (o.L.n_out + 15) / 16 <= 128;
 }
 
+// The attention split merge fused with the o projection (dk_attn_o), on by
+// default; draco_set_attn_o_fusion switches it.
+int g_attn_o_fusion = 1;
+
+// Whether dense layer l's attention split merge rides on its o projection
+// (dk_attn_o: one launch fewer per layer) and the o projection's eight
+// partials on the gate/up launch (the PRES8 prologue forms the FFN input into
+// w.xm): the per-head attention kernel at head dim 64 with 32 q heads (eight
+// 256-wide input chunks of four heads: configs[2]), a K-quant o projection
+// and a gate/up pair of one K-quant format whose rows the PRES8 prologue
+// covers.
+bool fused_o(const DevModel* m, int l) {
+    if (!g_attn_o_fusion) return false;
+    const DevFfn* f = m->ffn[l];
+    const DevAttn* a = m->attn[l];
+    if (!f || m->moe[l] || f->g->L.code != f->u->L.code) return false;
+    auto kq = [](const DracoMat* x) { return x->L.code == DRACO_Q4_K || x->L.code == DRACO_Q6_K; };
+    if (!kq(f->g) || !kq(a->wo) || a->HD != 64 || a->NH != 32 || a->wo->L.n_in != 2048) return false;
+    if (!attn_per_head(a->NH, a->NKV, a->HD) || attn_grouped(a->NH, a->NKV, a->HD) ||
+        attn_nsplit(a->max_t, a->NH, a->NKV, a->HD) > 64)
+        return false;
+    DqShape sh;
+    return draco_dq_shape(f->H, (f->FF + 15) / 16, true, 0, 4, 0, 256, sh) == 0;
+}
+
 // enqueue one llama layer on the device (x in w.x, updated in place; with
 // xin set the layer reads its input from xin and leaves its output in w.x):
 // qkv(+norm,+rope,+append), attention, merge, wo(+residual),
@@ -564,13 +592,24 @@ int enqueue_layer(DevModel* m, int l, float eps, hipStream_t st, const float* xi
     const int H = m->h;
     const float* x0 = xin ? xin : w.x;
     const bool pending = !xin && l > 0 && ksplit_down(m, l - 1);
-    // a pending input's materialised part: w.xm after a split-K o projection
-    const float* xq = pending && ksplit_o_dense(m, l - 1) ? w.xm : x0;
+    // a pending input's materialised part: w.xm after a split-K or fused o
+    // projection (the previous layer's FFN input)
+    const float* xq = pending && (fused_o(m, l - 1) || ksplit_o_dense(m, l - 1)) ? w.xm : x0;
     if (int rc = enqueue_qkv(a, w, xq, 1, m->anorm[l], eps, m->state, l, st, pending)) return rc;
-    if (dk_attention(w.q, a->kc, a->vc, w.part, w.cnt, w.att, m->state, l, a->NH, a->NKV, a->HD, a->max_t,
-                     a->scale, st))
-        return fail(-1, "attention launch");
     const float* base = pending ? w.xs : x0;  // this layer's input
+    const bool fo = fused_o(m, l);
+    if (fo) {
+        // split partials, then their merge + the o projection into eight
+        // partials, which the gate/up launch adds to the input (into w.xm)
+        if (dk_attention_parts(w.q, a->kc, a->vc, w.part, m->state, l, a->NH, a->NKV, a->HD, a->max_t, a->scale,
+                               st))
+            return fail(-1, "attention launch");
+        if (dk_attn_o(w.part, a->NH, a->NKV, a->max_t, *a->wo, w.po, st)) return fail(-1, "attention o launch");
+        if (int rc = enqueue_gateup(f, w, base, 1, m->fnorm[l], eps, st, w.po, w.xm, 8)) return rc;
+    } else if (dk_attention(w.q, a->kc, a->vc, w.part, w.cnt, w.att, m->state, l, a->NH, a->NKV, a->HD, a->max_t,
+                            a->scale, st)) {
+        return fail(-1, "attention launch");
+    }
     if (m->moe[l] && ksplit_o(m, l)) {
         // o split-K into w.pd; the router forms base + the partials into w.xm
         // (its RMSNorm input and the down launch's residual)
@@ -589,8 +628,10 @@ int enqueue_layer(DevModel* m, int l, float eps, hipStream_t st, const float* xi
         if (draco_seg_launch(s, st)) return fail(-1, "gemv o (split-K)");
         return draco_moe_layer_enqueue(m->moe[l], base, m->fnorm[l], eps, w.x, nullptr, st, w.pd, w.xm);
     }
-    const bool kso = !m->moe[l] && ksplit_o_dense(m, l);
-    if (kso) {
+    const bool kso = !fo && !m->moe[l] && ksplit_o_dense(m, l);
+    if (fo) {
+        // (launched above)
+    } else if (kso) {
         // o split-K into w.pd (free: this layer's qkv consumed the down's)
         SegLaunch s = {};
         s.nseg = 1;
@@ -612,7 +653,7 @@ int enqueue_layer(DevModel* m, int l, float eps, hipStream_t st, const float* xi
             return draco_moe_layer_enqueue(m->moe[l], w.x, m->fnorm[l], eps, w.x, w.x, st);
         if (int rc = enqueue_gateup(f, w, w.x, 1, m->fnorm[l], eps, st)) return rc;
     }
-    const float* mid = kso ? w.xm : w.x;  // the FFN's input, the down's residual
+    const float* mid = (kso || fo) ? w.xm : w.x;  // the FFN's input, the down's residual
     if (ksplit_down(m, l)) {
         SegLaunch s = {};
         s.nseg = 1;
@@ -1301,6 +1342,17 @@ int draco_llama_generate(const void* layers_v, int n_layer, int h, float eps, co
 // contract, src/qwen35_prefill.py:209-210 and src/draco_engine_server.py:836-842:
 // the engine state afterwards equals that of forward(ids[i], pos + i) run
 // token by token) ----
+
+// The fused attention merge + o projection of the llama decode layers (1 =
+// on, the default; 0 = the split merge and the o projection as two launches).
+// Returns the previous setting; on < 0 only queries.  Captured decode graphs
+// are per call, so a change applies to the next call.
+int draco_set_attn_o_fusion(int on) {
+    std::lock_guard<std::recursive_mutex> g(api_mutex());
+    const int old = g_attn_o_fusion;
+    if (on >= 0) g_attn_o_fusion = on ? 1 : 0;
+    return old;
+}
 
 // Tokens per chunk of the chunked prefill (draco_llama_prefill and the
 // prompt of draco_llama_generate); 0 makes draco_llama_generate feed its

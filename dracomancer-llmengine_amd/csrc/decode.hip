@@ -18,6 +18,7 @@
 #include "decode.h"
 #include "dev_common.h"
 #include "embed_dev.h"
+#include "tile_frag.h"
 
 namespace {
 
@@ -484,6 +485,73 @@ __global__ __launch_bounds__(256) void k_attn_combine(const float* __restrict__ 
     out[(size_t)h * HD + tid] = r;
 }
 
+// The per-head kernel's split merge fused with the o projection (head dim
+// 64: q heads 4c .. 4c+3 are input super-block c of the o rows; Q4_K / Q6_K
+// tile layout).  Block b takes chunk c = b % NC and row tiles 4 (b / NC) ..
+// +3.  Wave w first requests its tile's item c (the weights stream while the
+// merge runs), then merges the splits of head 4c + w as k_attn_combine does
+// (statistics and partials in one round trip); wave 0 digitises the 256
+// merged values (as k_dq's prologue) and every wave multiplies its tile:
+//   po[c][row] = W[row, 256c .. 256c + 255] . att[256c .. 256c + 255]
+// so the o projection's output is sum_c po[c] (the gate/up launch's PRES8
+// prologue forms it with the residual).  With NC = 8 kv groups of 4 heads
+// (configs[2]) block b runs on XCD b mod 8, the XCD that ran the splits of
+// kv head c (k_attn_part's block (c, s) is linear block c + 8 s), so the
+// partials it reads are in that XCD's L2.
+template <int FM, int MAXS>
+__global__ __launch_bounds__(256) void k_attn_o(const float* __restrict__ part, int nsplit,
+                                                const uint8_t* __restrict__ wo, int nb, int n_out, int NC,
+                                                float* __restrict__ po) {
+    constexpr int HD = 64;
+    constexpr size_t IB = FM == 1 ? DRACO_Q4T_ITEM : DRACO_Q6T_ITEM;
+    __shared__ __align__(16) float att[256];
+    __shared__ __align__(16) int8_t xd[1024];
+    __shared__ __align__(16) int8_t zero[1024];
+    __shared__ float2 xsm[16];
+    const int b = blockIdx.x, c = b % NC, rr = b / NC;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, j = lane & 15, g = lane >> 4;
+    const int ntiles = (n_out + 15) >> 4;
+    const int T = rr * 4 + w, Tc = T < ntiles ? T : ntiles - 1;
+    Frag f;
+    const uint8_t* item = wo + ((size_t)Tc * nb + c) * IB;
+    if (FM == 1) load_q4(item, lane, f);
+    else load_q6(item, lane, f);
+    // merge head 4c + w: every load unconditional (clamped split index)
+    const float* ph = part + (size_t)(4 * c + w) * nsplit * (HD + 2);
+    const int kl = min(lane, nsplit - 1);
+    const float m0 = ph[kl * (HD + 2) + HD], l0 = ph[kl * (HD + 2) + HD + 1];
+    float pv[MAXS];
+#pragma unroll
+    for (int k = 0; k < MAXS; k++) pv[k] = ph[min(k, nsplit - 1) * (HD + 2) + lane];
+    reinterpret_cast<uint32_t*>(zero)[tid] = 0u;
+    const float m = lane < nsplit ? m0 : -INFINITY;
+    const float lk = lane < nsplit ? l0 : 0.f;
+    const float M = wave_max(m);
+    const float wk = m > -INFINITY ? expf(m - M) : 0.f;
+    const float L = wave_sum(lk * wk);
+    float acc = 0.f;
+#pragma unroll
+    for (int k = 0; k < MAXS; k++)  // lanes k >= nsplit carry weight 0
+        acc = fmaf(pv[k], __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wk), k)), acc);
+    att[w * HD + lane] = acc * (1.f / L);
+    lds_barrier();
+    if (w == 0) digits4(reinterpret_cast<const float4*>(att)[lane], lane, xd, xsm);
+    lds_barrier();
+    const bool adig = (j >> 2) == g;
+    float v;
+    if (FM == 1) {
+        const int gl4 = 4 * (g >> 1) + (g & 1);
+        const float2 r = dot_q4(f, adig ? xd + (gl4 * 4 + (j & 3)) * 16 : zero, xsm, gl4, g);
+        v = r.x - r.y;
+    } else {
+        const int gl6 = 8 * (g >> 1) + (g & 1);
+        v = dot_q6(f, adig ? xd + (gl6 * 4 + (j & 3)) * 16 : zero, xsm, gl6);
+    }
+    v = rows_sum(v);
+    const int row = T * 16 + j;
+    if (lane < 16 && T < ntiles && row < n_out) po[(size_t)c * n_out + row] = v;
+}
+
 // qwen35 full attention, per-head RMSNorm over 256 dims and rope on the pairs
 // (t, t + 32), t < 32 (src/m6_layer.c:427-457).  Blocks 0..NH-1 normalise q
 // head b from QG[b * 512 .. + 256] into Qr[b * 256] as (x * r) * q_norm; blocks
@@ -733,6 +801,39 @@ int dk_attention(const float* q, const float* kc, const float* vc, float* part, 
         hipLaunchKernelGGL(k_attn_combine<32>, cg, cb, 0, st, part, out, nsplit, HD, gate, gstride, NKV);
     else
         hipLaunchKernelGGL(k_attn_combine<64>, cg, cb, 0, st, part, out, nsplit, HD, gate, gstride, NKV);
+    return 0;
+}
+
+int dk_attention_parts(const float* q, const float* kc, const float* vc, float* part, const int* state, int layer,
+                       int NH, int NKV, int HD, int max_t, float scale, hipStream_t st) {
+    if (HD != 64 || !attn_per_head(NH, NKV, HD) || attn_grouped(NH, NKV, HD)) return -1;
+    const int nsplit = attn_nsplit(max_t, NH, NKV, HD);
+    const dim3 grid(NKV, nsplit), block(64 * (NH / NKV));
+    hipLaunchKernelGGL(k_attn_part<64>, grid, block, 0, st, q, kc, vc, part, state, layer, NH, NKV, nsplit, scale);
+    return 0;
+}
+
+int dk_attn_o(const float* part, int NH, int NKV, int max_t, const DracoMat& wo, float* po, hipStream_t st) {
+    const int nsplit = attn_nsplit(max_t, NH, NKV, 64);
+    const int NC = NH / 4;
+    if (NH % 4 || wo.L.n_in != NH * 64 || wo.L.nb != NC || nsplit > 64 ||
+        (wo.L.code != DRACO_Q4_K && wo.L.code != DRACO_Q6_K))
+        return -1;
+    const int ntiles = (wo.L.n_out + 15) / 16;
+    const dim3 grid(NC * ((ntiles + 3) / 4)), block(256);
+    const bool q4 = wo.L.code == DRACO_Q4_K;
+#define AO_CASE(S_)                                                                                              \
+    if (q4) hipLaunchKernelGGL((k_attn_o<1, S_>), grid, block, 0, st, part, nsplit, wo.dev, wo.L.nb, wo.L.n_out, NC, \
+                               po);                                                                              \
+    else hipLaunchKernelGGL((k_attn_o<2, S_>), grid, block, 0, st, part, nsplit, wo.dev, wo.L.nb, wo.L.n_out, NC, po);
+    if (nsplit <= 16) {
+        AO_CASE(16)
+    } else if (nsplit <= 32) {
+        AO_CASE(32)
+    } else {
+        AO_CASE(64)
+    }
+#undef AO_CASE
     return 0;
 }
 

@@ -163,7 +163,9 @@ __device__ __forceinline__ auto seg_pick(const SegKArgs& a, int si, F f) -> decl
 // launch's do_norm: 1 the RMSNorm prologue; 2 the GDN gated rms of 128-wide
 // groups (x, already gated by the scan, scaled per group by rsqrt(sum of
 // its 16 partial sums of squares / 128 + eps); see GNORM below); 3 the
-// RMSNorm of a pending residual x + p0 + p1 (PRES below).
+// RMSNorm of a pending residual x + p0 + p1 (PRES below); 4 the same with
+// eight partials x + p0 + ... + p7 (the fused attention-merge + o
+// projection's, one per 256-wide input chunk), one float4 of x per thread.
 // KS: split-K launch (one EPI_STORE segment, no prologue norm): tiles
 // [0, a.rot) multiply the first half of every row's super-blocks and store
 // to y, tiles [a.rot, 2 a.rot) the second half and store to y + a.kv_dim.
@@ -223,23 +225,31 @@ __global__ __launch_bounds__(64 * NW) void k_dq(const SegKArgs a) {
     };
 
     // ---- prologue part 1: x (and norm weight) loads, then the first item's weights
-    float4 xv[XP_MAXV], wv[XP_MAXV];
+    constexpr bool RMS = NORM == 1 || NORM == 3 || NORM == 4;  // the RMSNorm prologue
+    constexpr int XPV = NORM == 4 ? 1 : XP_MAXV;               // float4s of x per thread
+    float4 xv[XPV], wv[XPV];
+    // NORM 4 (PRES8): the eight partials at a.am_val ([8][n_in])
+    float4 pq[NORM == 4 ? 8 : 1];
     // NORM 2 (GNORM): the group partials [n_in / 128][64] = a.kc (16 used)
     // NORM 3 (PRES): the pending residual's two split-K partials at a.am_val
     // ([2][n_in]); x = (x + p0) + p1, written to a.xn_out by block 0
-    float4 pv0[NORM >= 2 ? XP_MAXV : 1], pv1[NORM >= 2 ? XP_MAXV : 1], pv2[NORM == 2 ? XP_MAXV : 1],
-        pv3[NORM == 2 ? XP_MAXV : 1];
+    float4 pv0[NORM == 2 || NORM == 3 ? XP_MAXV : 1], pv1[NORM == 2 || NORM == 3 ? XP_MAXV : 1],
+        pv2[NORM == 2 ? XP_MAXV : 1], pv3[NORM == 2 ? XP_MAXV : 1];
     // KS with one tile per block: the block multiplies one half of x only,
     // so only that half is loaded and digitised (chunks q of NT float4s;
     // chunk q holds super-blocks [q NW, q NW + NW), and NW divides the half)
     const bool kown = KS && G == total;
-    const int kq_n = kown ? (nb >> 1) / NW : XP_MAXV, kq_lo = kown ? khalf(bx) * kq_n : 0;
+    const int kq_n = kown ? (nb >> 1) / NW : XPV, kq_lo = kown ? khalf(bx) * kq_n : 0;
 #pragma unroll
-    for (int q = 0; q < XP_MAXV; q++) {
+    for (int q = 0; q < XPV; q++) {
         const int i4 = tid + q * NT;
         if (i4 < n4 && q >= kq_lo && q < kq_lo + kq_n) {
             xv[q] = ld4(a.x + 4 * i4);
-            if ((NORM == 1 || NORM == 3) && a.norm_w) wv[q] = ld4(a.norm_w + 4 * i4);
+            if (RMS && a.norm_w) wv[q] = ld4(a.norm_w + 4 * i4);
+            if constexpr (NORM == 4) {
+#pragma unroll
+                for (int p = 0; p < 8; p++) pq[p] = ld4(a.am_val + (size_t)p * n_in + 4 * i4);
+            }
             if constexpr (NORM == 3) {
                 pv0[q] = ld4(a.am_val + 4 * i4);
                 pv1[q] = ld4(a.am_val + n_in + 4 * i4);
@@ -259,6 +269,7 @@ __global__ __launch_bounds__(64 * NW) void k_dq(const SegKArgs a) {
     // branch leaves the wait-count analysis no choice but to wait for it
     // before the first weights are used.
     static_assert(!GD || NORM == 1 || NORM == 3, "row dots ride on the RMSNorm prologue");
+    static_assert(NORM != 4 || !KS, "PRES8 launches are not split-K");
     const int gr = GD ? bx - (G - 2 * a.gdot) : -1;
     float4 gv[2];
     if constexpr (GD) {
@@ -303,7 +314,7 @@ __global__ __launch_bounds__(64 * NW) void k_dq(const SegKArgs a) {
     load_next(P0, Q0);
     // the zero page: written by the block before its barrier, or without the
     // barrier (no RMSNorm) by every wave for itself (identical values)
-    if (NORM == 1 || NORM == 3)
+    if (RMS)
         for (int i = tid; i < 256; i += NT) reinterpret_cast<uint32_t*>(zero)[i] = 0u;
     else
         for (int i = lane; i < 256; i += 64) reinterpret_cast<uint32_t*>(zero)[i] = 0u;
@@ -318,11 +329,19 @@ __global__ __launch_bounds__(64 * NW) void k_dq(const SegKArgs a) {
     float* gsp = ssp + NW;           // [NW] per-wave row-dot partials
     float ss = 0.f, gp = 0.f;
 #pragma unroll
-    for (int q = 0; q < XP_MAXV; q++) {
+    for (int q = 0; q < XPV; q++) {
         const int i4 = tid + q * NT;
         if (i4 >= n4) break;
         if (q < kq_lo || q >= kq_lo + kq_n) continue;
         float4 v = xv[q];
+        if constexpr (NORM == 4) {
+#pragma unroll
+            for (int p = 0; p < 8; p++) {
+                v.x += pq[p].x; v.y += pq[p].y; v.z += pq[p].z; v.w += pq[p].w;
+            }
+            xv[q] = v;
+            if (a.xn_out && bx == 0) *reinterpret_cast<float4*>(a.xn_out + 4 * i4) = v;
+        }
         if constexpr (NORM == 3) {
             const float4 p = pv0[q], p2 = pv1[q];
             v.x = (v.x + p.x) + p2.x; v.y = (v.y + p.y) + p2.y; v.z = (v.z + p.z) + p2.z; v.w = (v.w + p.w) + p2.w;
@@ -341,7 +360,7 @@ __global__ __launch_bounds__(64 * NW) void k_dq(const SegKArgs a) {
             const float inv2 = 1.f / sqrtf(ms2 / 128.f + a.eps);
             v.x *= inv2; v.y *= inv2; v.z *= inv2; v.w *= inv2;
         }
-        if (NORM == 1 || NORM == 3) {
+        if (RMS) {
             ss = fmaf(v.x, v.x, ss);
             ss = fmaf(v.y, v.y, ss);
             ss = fmaf(v.z, v.z, ss);
@@ -360,7 +379,7 @@ __global__ __launch_bounds__(64 * NW) void k_dq(const SegKArgs a) {
         }
         digits4(v, i4, xd, xsm);
     }
-    if (NORM == 1 || NORM == 3) {
+    if (RMS) {
         ss = wave_sum(ss);
         if (GD && gr >= 0) gp = wave_sum(gp);
         if (lane == 0) {
@@ -380,7 +399,7 @@ __global__ __launch_bounds__(64 * NW) void k_dq(const SegKArgs a) {
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
     }
     float inv = 1.f;
-    if (NORM == 1 || NORM == 3) {
+    if (RMS) {
         float tot = 0.f;
 #pragma unroll
         for (int i = 0; i < NW; i++) tot += ssp[i];
@@ -393,7 +412,7 @@ __global__ __launch_bounds__(64 * NW) void k_dq(const SegKArgs a) {
         }
         if (NORM == 1 && a.xn_out && bx == 0) {
 #pragma unroll
-            for (int q = 0; q < XP_MAXV; q++) {
+            for (int q = 0; q < XPV; q++) {
                 const int i4 = tid + q * NT;
                 if (i4 >= n4) break;
                 float4 v = xv[q];
@@ -502,7 +521,7 @@ __global__ __launch_bounds__(64 * NW) void k_dq(const SegKArgs a) {
                     v += red[q * 16 + tid];
                     if (DUAL) v2 += red[(NW + q) * 16 + tid];
                 }
-                if (NORM == 1 || NORM == 3) {
+                if (RMS) {
                     v *= inv;
                     v2 *= inv;
                 }
@@ -1000,6 +1019,8 @@ void launch_dq_m(SegLaunch& a, bool multi, int grid, hipStream_t st) {
     } else if (a.do_norm == 3) {  // PRES: per-tile epilogues, or the SwiGLU pair
         if constexpr (DUAL) launch_dq<NW, FM, true, false, EPI_SWIGLU, 3>(a, grid, st);
         else launch_dq<NW, FM, false, true, EPI_RT, 3>(a, grid, st);
+    } else if (a.do_norm == 4) {  // PRES8: the SwiGLU pair (checked by draco_dq_shape)
+        if constexpr (DUAL) launch_dq<NW, FM, true, false, EPI_SWIGLU, 4>(a, grid, st);
     } else if (a.do_norm) {
         launch_dq_e<NW, FM, DUAL, 1>(a, multi, grid, st);
     } else {
@@ -1082,8 +1103,8 @@ int seg_launch_dq(SegLaunch& a, hipStream_t st) {
     // GNORM prologue: one residual segment (a store segment when split-K) over whole 128-wide groups
     if (a.do_norm == 2 && (a.nseg != 1 || a.seg[0].epi != (a.ksplit ? EPI_STORE : EPI_RESID) || n_in % 128 || !a.kc))
         return -1;
-    // PRES prologue: the partials of the pending residual
-    if (a.do_norm == 3 && !a.am_val) return -1;
+    // PRES prologues: the partials of the pending residual
+    if ((a.do_norm == 3 || a.do_norm == 4) && !a.am_val) return -1;
     // split-K: one whole-matrix store segment (the row widths and prologues
     // it serves are draco_dq_shape's to decide)
     if (a.ksplit) {
@@ -1243,7 +1264,10 @@ int draco_dq_ksplit_waves(int n_in, int do_norm) {
 
 int draco_dq_shape(int n_in, int tiles, bool dual, int ksplit, int do_norm, int gd_n, int cus, DqShape& s) {
     s = DqShape{};
-    s.xp_max = XP_MAXV;
+    // the PRES8 prologue (do_norm 4) holds one float4 of x per thread
+    const int xp = do_norm == 4 ? 1 : XP_MAXV;
+    s.xp_max = xp;
+    if (do_norm == 4 && (ksplit || !dual)) return -1;
     if (n_in <= 0 || n_in % 256 || n_in > 16384 || tiles <= 0 || cus <= 0) return -1;
     const int nb = n_in / 256;
     if (ksplit) {
@@ -1260,7 +1284,7 @@ int draco_dq_shape(int n_in, int tiles, bool dual, int ksplit, int do_norm, int 
         // to 63 super-blocks per row: measured faster than 16 for the decode
         // down projection, n_in 8192)
         int nw = nb >= 64 ? 16 : (nb >= 8 ? 8 : 4);
-        while (n_in > XP_MAXV * 4 * 64 * nw) nw *= 2;
+        while (n_in > xp * 4 * 64 * nw) nw *= 2;
         if (nw > 16) return -1;
         const int cap = cus * (16 / nw);
         int grid = tiles < cap ? tiles : cap;

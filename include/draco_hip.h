@@ -147,6 +147,11 @@ int draco_llama_prefill(const void* layers, int n_layer, int h, float eps, const
 /* tokens per prefill chunk (default 256; 0 = draco_llama_generate feeds its
  * prompt token by token).  Returns the previous value; n < 0 only queries. */
 int draco_set_prefill_chunk(int n);
+/* No reference counterpart: the llama decode layers' attention split merge
+ * fused with the o projection (1, the default, where the shape allows: head
+ * dim 64, 32 q heads, K-quant o and gate/up) or run as two launches (0).
+ * Returns the previous setting; on < 0 only queries. */
+int draco_set_attn_o_fusion(int on);
 
 /* ---- library utilities (no reference counterpart) ----------------------- */
 

@@ -85,6 +85,7 @@ VARIANTS = [  # (name, dual, ksplit, do_norm, gd_n, barrier after the prologue)
     ("plain+pres", 0, 0, 3, 0, True),
     ("gnorm", 0, 0, 2, 0, False),
     ("swiglu+rms", 1, 0, 1, 0, True),
+    ("swiglu+pres8", 1, 0, 4, 0, True),
     ("rowdots", 0, 0, 1, 16, True),
     ("splitk", 0, 2, 0, 0, False),
     ("splitk+gnorm", 0, 2, 2, 0, False),
