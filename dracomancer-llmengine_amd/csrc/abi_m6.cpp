@@ -93,11 +93,9 @@ struct Work {
     // a MoE layer after a split-K o projection: its input (the layer input +
     // the partials in pd), materialised by the router launch
     float* xm = nullptr;
-    // the fused attention merge + o projection's partials, [QD / 256][H]
-    float* po = nullptr;
     unsigned* cnt = nullptr;  // attention merge counters (one per kv head), zero at rest
     size_t cap_h = 0, cap_xn = 0, cap_xe = 0, cap_q = 0, cap_k = 0, cap_part = 0, cap_ff = 0, cap_pd = 0,
-           cap_xs = 0, cap_xm = 0, cap_po = 0;
+           cap_xs = 0, cap_xm = 0;
 };
 
 // Chunked-prefill buffers, token-major, for up to `cap` tokens per chunk.
@@ -124,6 +122,13 @@ struct DevModel {
     int* state = nullptr;   // device [1 + n_layer]
     int* hstate = nullptr;  // pinned host mirror of state
     int state_cap = 0;      // ints allocated in state / hstate
+    // layers whose attention merge rides on the o projection (fused_o), each
+    // with the previous such layer (cyclically: the accumulator it clears),
+    // and their int64 accumulators ([n_layer][oacc_stride])
+    std::vector<char> fo;
+    std::vector<int> fo_prev;
+    unsigned long long* oacc = nullptr;
+    size_t oacc_stride = 0, oacc_n = 0;
 };
 
 struct RopeTab {
@@ -272,7 +277,6 @@ int ensure_work(Work& w, int H, int QD, int KD, int NH, int HD, int max_t, int F
     if (grow(&w.pd, &w.cap_pd, 2 * (size_t)H + 64)) return -2;
     if (grow(&w.xs, &w.cap_xs, H + 64)) return -2;
     if (grow(&w.xm, &w.cap_xm, H + 64)) return -2;
-    if (grow(&w.po, &w.cap_po, (size_t)(QD / 256 > 0 ? QD / 256 : 1) * H + 64)) return -2;
     if (w.cap_q < (size_t)QD) {
         size_t c = w.cap_q;
         if (grow(&w.q, &c, QD)) return -2;
@@ -562,7 +566,7 @@ int g_attn_o_fusion = 1;
 // 256-wide input chunks of four heads: configs[2]), a K-quant o projection
 // and a gate/up pair of one K-quant format whose rows the PRES8 prologue
 // covers.
-bool fused_o(const DevModel* m, int l) {
+bool fused_o_shape(const DevModel* m, int l) {
     if (!g_attn_o_fusion) return false;
     const DevFfn* f = m->ffn[l];
     const DevAttn* a = m->attn[l];
@@ -575,6 +579,42 @@ bool fused_o(const DevModel* m, int l) {
     DqShape sh;
     return draco_dq_shape(f->H, (f->FF + 15) / 16, true, 0, 4, 0, 256, sh) == 0;
 }
+
+// The fused layers of a model for this call, and their accumulators, all
+// cleared on the stream (before any capture): each fused layer's launch
+// clears the previous fused layer's accumulator (its consumer, the gate/up
+// launch, ran before), so every accumulator is zero when its layer starts,
+// call after call; fewer than two fused layers run unfused (a layer cannot
+// clear its own).  Called by every entry point before it enqueues layers.
+int plan_fusion(DevModel* m, hipStream_t st) {
+    const int L = m->n_layer;
+    m->fo.assign(L, 0);
+    m->fo_prev.assign(L, -1);
+    std::vector<int> ls;
+    for (int l = 0; l < L; l++)
+        if (fused_o_shape(m, l)) ls.push_back(l);
+    if (ls.size() < 2) return 0;
+    for (size_t i = 0; i < ls.size(); i++) {
+        m->fo[ls[i]] = 1;
+        m->fo_prev[ls[i]] = ls[(i + ls.size() - 1) % ls.size()];
+    }
+    const size_t stride = ((size_t)m->h + 1 + 63) / 64 * 64;
+    const size_t n = stride * L;
+    if (m->oacc_n < n) {
+        if (m->oacc) {
+            DRACO_HIP(hipStreamSynchronize(st));
+            DRACO_HIP(hipFree(m->oacc));
+            m->oacc = nullptr;
+        }
+        DRACO_HIP(hipMalloc(&m->oacc, sizeof(unsigned long long) * n));
+        m->oacc_n = n;
+    }
+    m->oacc_stride = stride;
+    DRACO_HIP(hipMemsetAsync(m->oacc, 0, sizeof(unsigned long long) * n, st));
+    return 0;
+}
+
+bool fused_o(const DevModel* m, int l) { return l >= 0 && l < (int)m->fo.size() && m->fo[l]; }
 
 // enqueue one llama layer on the device (x in w.x, updated in place; with
 // xin set the layer reads its input from xin and leaves its output in w.x):
@@ -604,8 +644,12 @@ int enqueue_layer(DevModel* m, int l, float eps, hipStream_t st, const float* xi
         if (dk_attention_parts(w.q, a->kc, a->vc, w.part, m->state, l, a->NH, a->NKV, a->HD, a->max_t, a->scale,
                                st))
             return fail(-1, "attention launch");
-        if (dk_attn_o(w.part, a->NH, a->NKV, a->max_t, *a->wo, w.po, st)) return fail(-1, "attention o launch");
-        if (int rc = enqueue_gateup(f, w, base, 1, m->fnorm[l], eps, st, w.po, w.xm, 8)) return rc;
+        unsigned long long* acc = m->oacc + (size_t)l * m->oacc_stride;
+        unsigned long long* zacc = m->oacc + (size_t)m->fo_prev[l] * m->oacc_stride;
+        if (dk_attn_o(w.part, a->NH, a->NKV, a->max_t, *a->wo, acc, zacc, (int)m->oacc_stride, st))
+            return fail(-1, "attention o launch");
+        if (int rc = enqueue_gateup(f, w, base, 1, m->fnorm[l], eps, st, reinterpret_cast<const float*>(acc), w.xm, 8))
+            return rc;
     } else if (dk_attention(w.q, a->kc, a->vc, w.part, w.cnt, w.att, m->state, l, a->NH, a->NKV, a->HD, a->max_t,
                             a->scale, st)) {
         return fail(-1, "attention launch");
@@ -902,6 +946,7 @@ int m6_forward_token(float* x, int h, float eps, int pos, const M6LayerDesc* lay
     if (int rc = ensure_init()) return report(rc, "m6_forward_token");
     DevModel* m = resolve_model(layers, n_layer, h);
     if (!m) return report(-1, "m6_forward_token");
+    if (int rc = plan_fusion(m, stream())) return report(rc, "m6_forward_token");
     if (int rc = check_positions(m, pos, 1)) return report(rc, "m6_forward_token");
     hipStream_t st = stream();
     if (int rc = upload_state(m, pos, st)) return report(rc, "m6_forward_token");
@@ -1177,6 +1222,7 @@ int draco_llama_generate(const void* layers_v, int n_layer, int h, float eps, co
             return report(fail(-1, "prompt token id %d out of range", prompt[i]), "draco_llama_generate");
     DevModel* m = resolve_model(layers, n_layer, h);
     if (!m) return report(-1, "draco_llama_generate");
+    if (int rc = plan_fusion(m, stream())) return report(rc, "draco_llama_generate");
     const DracoMat* hm = get_mat(head_w, head_code, vocab, h);
     const DracoMat* em = get_mat(emb_w, emb_code, vocab, h);
     const float* nw = norm_dev(final_norm, h);
@@ -1378,6 +1424,7 @@ int draco_llama_prefill(const void* layers_v, int n_layer, int h, float eps, con
         if (ids[i] < 0 || ids[i] >= vocab) return report(fail(-1, "token id %d out of range", ids[i]), "draco_llama_prefill");
     DevModel* m = resolve_model(layers, n_layer, h);
     if (!m) return report(-1, "draco_llama_prefill");
+    if (int rc = plan_fusion(m, stream())) return report(rc, "draco_llama_prefill");
     const DracoMat* em = get_mat(emb_w, emb_code, vocab, h);
     if (!em) return report(-1, "draco_llama_prefill");
     for (int l = 0; l < n_layer; l++) {

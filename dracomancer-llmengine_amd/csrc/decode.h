@@ -52,9 +52,12 @@ int dk_attention(const float* q, const float* kc, const float* vc, float* part, 
 int dk_attention_parts(const float* q, const float* kc, const float* vc, float* part, const int* state, int layer,
                        int NH, int NKV, int HD, int max_t, float scale, hipStream_t st);
 // Their merge fused with the o projection wo (Q4_K / Q6_K, n_in = NH * 64,
-// one 256-wide input chunk per 4 heads): po[c][0 .. n_out) = the chunk-c
-// share of wo . att, c < NH / 4; -1 for another shape.
-int dk_attn_o(const float* part, int NH, int NKV, int max_t, const DracoMat& wo, float* po, hipStream_t st);
+// one 256-wide input chunk per 4 heads): acc[row] += round(2^32 * wo . att)
+// over the chunks (int64 fixed point; acc must start at zero), acc[n_out]
+// set when a contribution is not finite; zacc[0 .. zn) is cleared.  -1 for
+// another shape.
+int dk_attn_o(const float* part, int NH, int NKV, int max_t, const DracoMat& wo, unsigned long long* acc,
+              unsigned long long* zacc, int zn, hipStream_t st);
 // qwen35 full attention q/k head RMSNorm + rope (NH q heads, 2 k heads of 256).
 void dk_fa_prep(const float* QG, float* Qr, const float* kin, float* kout, const float* qn, const float* kn,
                 const float* cs, int NH, hipStream_t st);

@@ -491,17 +491,23 @@ __global__ __launch_bounds__(256) void k_attn_combine(const float* __restrict__ 
 // +3.  Wave w first requests its tile's item c (the weights stream while the
 // merge runs), then merges the splits of head 4c + w as k_attn_combine does
 // (statistics and partials in one round trip); wave 0 digitises the 256
-// merged values (as k_dq's prologue) and every wave multiplies its tile:
-//   po[c][row] = W[row, 256c .. 256c + 255] . att[256c .. 256c + 255]
-// so the o projection's output is sum_c po[c] (the gate/up launch's PRES8
-// prologue forms it with the residual).  With NC = 8 kv groups of 4 heads
-// (configs[2]) block b runs on XCD b mod 8, the XCD that ran the splits of
-// kv head c (k_attn_part's block (c, s) is linear block c + 8 s), so the
-// partials it reads are in that XCD's L2.
+// merged values (as k_dq's prologue) and every wave multiplies its tile.
+// The chunks' contributions W[row, 256c .. 256c + 255] . att[256c ..] meet
+// in acc[row] as 64-bit fixed point (round(v * 2^32), agent-scope atomic
+// adds): integer addition is associative, so the sum is the same bit for
+// bit whatever order the blocks arrive in, and the consumer (the gate/up
+// launch's PRES8 prologue) reads one vector instead of NC.  A non-finite or
+// out-of-range contribution sets acc[n_out] instead, which makes the
+// consumer's input NaN, as the reference's fp32 sum would be.  The grid also
+// clears zacc[0 .. zn) (the previous fused layer's accumulator, consumed
+// before this launch).  With NC = 8 kv groups of 4 heads block b
+// runs on XCD b mod 8, the XCD that ran the splits of kv head c (k_attn_part's
+// block (c, s) is linear block c + 8 s).
 template <int FM, int MAXS>
 __global__ __launch_bounds__(256) void k_attn_o(const float* __restrict__ part, int nsplit,
                                                 const uint8_t* __restrict__ wo, int nb, int n_out, int NC,
-                                                float* __restrict__ po) {
+                                                unsigned long long* __restrict__ acc,
+                                                unsigned long long* __restrict__ zacc, int zn) {
     constexpr int HD = 64;
     constexpr size_t IB = FM == 1 ? DRACO_Q4T_ITEM : DRACO_Q6T_ITEM;
     __shared__ __align__(16) float att[256];
@@ -524,16 +530,17 @@ __global__ __launch_bounds__(256) void k_attn_o(const float* __restrict__ part, 
 #pragma unroll
     for (int k = 0; k < MAXS; k++) pv[k] = ph[min(k, nsplit - 1) * (HD + 2) + lane];
     reinterpret_cast<uint32_t*>(zero)[tid] = 0u;
+    for (int i = b * 256 + tid; i < zn; i += gridDim.x * 256) zacc[i] = 0ull;
     const float m = lane < nsplit ? m0 : -INFINITY;
     const float lk = lane < nsplit ? l0 : 0.f;
     const float M = wave_max(m);
     const float wk = m > -INFINITY ? expf(m - M) : 0.f;
     const float L = wave_sum(lk * wk);
-    float acc = 0.f;
+    float s = 0.f;
 #pragma unroll
     for (int k = 0; k < MAXS; k++)  // lanes k >= nsplit carry weight 0
-        acc = fmaf(pv[k], __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wk), k)), acc);
-    att[w * HD + lane] = acc * (1.f / L);
+        s = fmaf(pv[k], __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wk), k)), s);
+    att[w * HD + lane] = s * (1.f / L);
     lds_barrier();
     if (w == 0) digits4(reinterpret_cast<const float4*>(att)[lane], lane, xd, xsm);
     lds_barrier();
@@ -549,7 +556,14 @@ __global__ __launch_bounds__(256) void k_attn_o(const float* __restrict__ part, 
     }
     v = rows_sum(v);
     const int row = T * 16 + j;
-    if (lane < 16 && T < ntiles && row < n_out) po[(size_t)c * n_out + row] = v;
+    if (lane < 16 && T < ntiles && row < n_out) {
+        const float sv = v * 4294967296.f;  // 2^32
+        if (fabsf(sv) < 9.0e18f) {          // |round(sv)| < 2^63, and not NaN
+            atomicAdd(acc + row, (unsigned long long)(long long)rintf(sv));
+        } else {
+            atomicOr(acc + n_out, 1ull);
+        }
+    }
 }
 
 // qwen35 full attention, per-head RMSNorm over 256 dims and rope on the pairs
@@ -813,7 +827,8 @@ int dk_attention_parts(const float* q, const float* kc, const float* vc, float* 
     return 0;
 }
 
-int dk_attn_o(const float* part, int NH, int NKV, int max_t, const DracoMat& wo, float* po, hipStream_t st) {
+int dk_attn_o(const float* part, int NH, int NKV, int max_t, const DracoMat& wo, unsigned long long* acc,
+              unsigned long long* zacc, int zn, hipStream_t st) {
     const int nsplit = attn_nsplit(max_t, NH, NKV, 64);
     const int NC = NH / 4;
     if (NH % 4 || wo.L.n_in != NH * 64 || wo.L.nb != NC || nsplit > 64 ||
@@ -824,8 +839,9 @@ int dk_attn_o(const float* part, int NH, int NKV, int max_t, const DracoMat& wo,
     const bool q4 = wo.L.code == DRACO_Q4_K;
 #define AO_CASE(S_)                                                                                              \
     if (q4) hipLaunchKernelGGL((k_attn_o<1, S_>), grid, block, 0, st, part, nsplit, wo.dev, wo.L.nb, wo.L.n_out, NC, \
-                               po);                                                                              \
-    else hipLaunchKernelGGL((k_attn_o<2, S_>), grid, block, 0, st, part, nsplit, wo.dev, wo.L.nb, wo.L.n_out, NC, po);
+                               acc, zacc, zn);                                                                   \
+    else hipLaunchKernelGGL((k_attn_o<2, S_>), grid, block, 0, st, part, nsplit, wo.dev, wo.L.nb, wo.L.n_out, NC, \
+                            acc, zacc, zn);
     if (nsplit <= 16) {
         AO_CASE(16)
     } else if (nsplit <= 32) {

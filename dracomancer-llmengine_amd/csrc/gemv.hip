@@ -164,8 +164,8 @@ __device__ __forceinline__ auto seg_pick(const SegKArgs& a, int si, F f) -> decl
 // groups (x, already gated by the scan, scaled per group by rsqrt(sum of
 // its 16 partial sums of squares / 128 + eps); see GNORM below); 3 the
 // RMSNorm of a pending residual x + p0 + p1 (PRES below); 4 the same with
-// eight partials x + p0 + ... + p7 (the fused attention-merge + o
-// projection's, one per 256-wide input chunk), one float4 of x per thread.
+// the fused attention-merge + o projection's accumulator (PRES8 below: x +
+// acc * 2^-32, acc int64 fixed point), one float4 of x per thread.
 // KS: split-K launch (one EPI_STORE segment, no prologue norm): tiles
 // [0, a.rot) multiply the first half of every row's super-blocks and store
 // to y, tiles [a.rot, 2 a.rot) the second half and store to y + a.kv_dim.
@@ -228,8 +228,11 @@ __global__ __launch_bounds__(64 * NW) void k_dq(const SegKArgs a) {
     constexpr bool RMS = NORM == 1 || NORM == 3 || NORM == 4;  // the RMSNorm prologue
     constexpr int XPV = NORM == 4 ? 1 : XP_MAXV;               // float4s of x per thread
     float4 xv[XPV], wv[XPV];
-    // NORM 4 (PRES8): the eight partials at a.am_val ([8][n_in])
-    float4 pq[NORM == 4 ? 8 : 1];
+    // NORM 4 (PRES8): the pending residual's int64 fixed-point accumulator at
+    // a.am_val ([n_in] sums of round(2^32 p), then a flag at [n_in], set when
+    // a contribution was not finite)
+    longlong2 pq[NORM == 4 ? 2 : 1];
+    long long pflag = 0;
     // NORM 2 (GNORM): the group partials [n_in / 128][64] = a.kc (16 used)
     // NORM 3 (PRES): the pending residual's two split-K partials at a.am_val
     // ([2][n_in]); x = (x + p0) + p1, written to a.xn_out by block 0
@@ -247,8 +250,10 @@ __global__ __launch_bounds__(64 * NW) void k_dq(const SegKArgs a) {
             xv[q] = ld4(a.x + 4 * i4);
             if (RMS && a.norm_w) wv[q] = ld4(a.norm_w + 4 * i4);
             if constexpr (NORM == 4) {
-#pragma unroll
-                for (int p = 0; p < 8; p++) pq[p] = ld4(a.am_val + (size_t)p * n_in + 4 * i4);
+                const longlong2* A = reinterpret_cast<const longlong2*>(a.am_val) + 2 * i4;
+                pq[0] = A[0];
+                pq[1] = A[1];
+                pflag = reinterpret_cast<const long long*>(a.am_val)[n_in];
             }
             if constexpr (NORM == 3) {
                 pv0[q] = ld4(a.am_val + 4 * i4);
@@ -335,9 +340,12 @@ __global__ __launch_bounds__(64 * NW) void k_dq(const SegKArgs a) {
         if (q < kq_lo || q >= kq_lo + kq_n) continue;
         float4 v = xv[q];
         if constexpr (NORM == 4) {
-#pragma unroll
-            for (int p = 0; p < 8; p++) {
-                v.x += pq[p].x; v.y += pq[p].y; v.z += pq[p].z; v.w += pq[p].w;
+            constexpr float S = 2.3283064365386963e-10f;  // 2^-32
+            if (pflag) {
+                v.x = v.y = v.z = v.w = __builtin_nanf("");
+            } else {
+                v.x += (float)pq[0].x * S; v.y += (float)pq[0].y * S;
+                v.z += (float)pq[1].x * S; v.w += (float)pq[1].y * S;
             }
             xv[q] = v;
             if (a.xn_out && bx == 0) *reinterpret_cast<float4*>(a.xn_out + 4 * i4) = v;

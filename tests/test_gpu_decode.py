@@ -126,6 +126,31 @@ def test_attn_o_fusion_matches_oracle(oracle, fusion, use_graph):
         L.draco_set_attn_o_fusion(old)
 
 
+def test_attn_o_fusion_is_deterministic():
+    """The fused o projection's chunks meet in int64 fixed point (atomic
+    adds in any order): graph-replayed and eager runs, repeated, give the
+    same tokens and the same hidden state bit for bit."""
+    import ctypes as ct
+    import dataclasses
+    from dracohip import lib
+    cfg = dataclasses.replace(models.LLAMA1B, name="cfg2-layers", n_layer=3, n_ff=4096, vocab=1024, n_prompt=12,
+                              n_gen=8, max_t=64)
+    model = models.build_llama(cfg, 32)
+    L = lib.load()
+    assert L.draco_set_attn_o_fusion(-1) == 1
+    L.draco_reset()
+    drv = LlamaDriver(model, hip_engine_lib())
+    outs = []
+    for use_graph in (True, False, True, True):
+        drv.reset()
+        L.draco_state_push(ct.cast(drv.descs, ct.c_void_p), drv.NL)
+        toks, hidden, _ = drv.generate_device(model.prompt(), cfg.n_gen, use_graph=use_graph)
+        outs.append((toks, hidden.copy()))
+    for t, h in outs[1:]:
+        assert t == outs[0][0]
+        assert np.array_equal(h, outs[0][1])
+
+
 def test_graph_replays_match_eager():
     """Graph replays are checked against eager runs (several in a row)."""
     cfg, model, drv = _driver("tiny-kquant")
