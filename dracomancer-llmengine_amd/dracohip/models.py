@@ -113,6 +113,14 @@ QWEN3_MOE = LlamaConfig(
     codes=dict(q=Q6_K, k=Q6_K, v=Q6_K, o=Q6_K, gate=Q4_K, up=Q4_K, down=Q4_K, emb=Q4_K, out=Q6_K),
     tied=False, n_prompt=448, n_gen=64, max_t=512, n_exp=128, n_used=8, exp_ff=768)
 
+# configs[3]'s first 8 layers (the same layer weights: seed 3 draws them first)
+# with a short prompt: the deeper MoE parity case against the compiled reference
+QWEN3_MOE8 = LlamaConfig(
+    name="qwen3-moe-stack-8", hidden=2048, n_layer=8, n_head=32, n_kv=4, head_dim=128, n_ff=0,
+    vocab=151936, eps=1e-6, rope_base=1000000.0,
+    codes=dict(q=Q6_K, k=Q6_K, v=Q6_K, o=Q6_K, gate=Q4_K, up=Q4_K, down=Q4_K, emb=Q4_K, out=Q6_K),
+    tied=False, n_prompt=8, n_gen=8, max_t=64, n_exp=128, n_used=8, exp_ff=768)
+
 # the same layer shape in two layers with a small vocabulary: MoE parity cases
 MOE_TINY = LlamaConfig(
     name="moe-tiny", hidden=2048, n_layer=2, n_head=32, n_kv=4, head_dim=128, n_ff=0, vocab=1024, eps=1e-6,
@@ -120,7 +128,8 @@ MOE_TINY = LlamaConfig(
     codes=dict(q=Q6_K, k=Q6_K, v=Q6_K, o=Q6_K, gate=Q4_K, up=Q4_K, down=Q4_K, emb=Q4_K, out=Q6_K),
     tied=False, n_prompt=8, n_gen=16, max_t=64, n_exp=128, n_used=8, exp_ff=768)
 
-CONFIGS = {c.name: c for c in (SMOL360M, LLAMA1B, TINY_K, TINY_Q8, TINY_Q5, ATTN_CFG3, QWEN3_MOE, MOE_TINY)}
+CONFIGS = {c.name: c for c in (SMOL360M, LLAMA1B, TINY_K, TINY_Q8, TINY_Q5, ATTN_CFG3, QWEN3_MOE, MOE_TINY,
+                                QWEN3_MOE8)}
 
 
 @dataclass

@@ -229,7 +229,12 @@ QWEN35_TINY = QwenStackConfig(name="qwen35-tiny", n_layer=4, vocab=1024, max_t=6
 QWEN35_TINY_MOE = QwenStackConfig(name="qwen35-tiny-moe", n_layer=4, vocab=1024, max_t=64, n_prompt=12, n_gen=8,
                                   ffn=FFN_MOE, n_exp=32, n_used=4, exp_ff=512)
 
-STACKS = {c.name: c for c in (QWEN35_GDN48, QWEN35_TINY, QWEN35_TINY_MOE)}
+# the same 48 layers (the same weights: seed 0) with a short prompt: the
+# full-depth parity case against the compiled reference
+QWEN35_GDN48_SHORT = QwenStackConfig(name="qwen35-gdn-stack-48-short", n_layer=48, vocab=151936, max_t=64,
+                                     n_prompt=8, n_gen=8)
+
+STACKS = {c.name: c for c in (QWEN35_GDN48, QWEN35_TINY, QWEN35_TINY_MOE, QWEN35_GDN48_SHORT)}
 
 
 @dataclass
@@ -352,6 +357,10 @@ class QwenStackDriver:
         self.logits = np.zeros(cfg.vocab, np.float32)
         self.hsc = np.zeros(H, np.float32)
         self.emb_row = stack.emb.nbytes // cfg.vocab
+        # layers after which forward() keeps a copy of the hidden state
+        # (depth[il]: the last token's), for per-depth comparisons
+        self.record = ()
+        self.depth = {}
 
     # -- the reference's per-token forward, op by op (host state) --
     def embed(self, tok):
@@ -378,6 +387,8 @@ class QwenStackDriver:
             else:
                 self.ffo[:] = 0.0
             self.x[:] = self.x2o + self.ffo
+            if il in self.record:
+                self.depth[il] = self.x.copy()
         return self.x
 
     def logits_of_x(self, x=None):

@@ -541,21 +541,29 @@ def ref_qwen_ops(E, max_t):
             "dense": E.m6_dense_op, "moe": moe, "head": lib.head_op, "_keep": (buf, scores, lib)}
 
 
-def gen_qwen_stack(name, fname, logit_steps):
+def gen_qwen_stack(name, fname, logit_steps, record=()):
     """A qwen35 stack (dracohip.qwen35 STACKS[name]) decoded token by token
     through the compiled reference's per-layer ops exactly as
     src/qwen35_engine.py:310-327 composes them (the caller appends KRN / VRN
-    to its caches), then greedy tokens."""
+    to its caches), then greedy tokens.  `record`: layers after which the
+    last token's hidden state is kept (depth{il})."""
     from dracohip import qwen35 as Q
     t0 = time.time()
     cfg = Q.STACKS[name]
     stack = Q.build_stack(cfg, 0)
     ops = ref_qwen_ops(ref_engine(), cfg.max_t)
     drv = Q.QwenStackDriver(stack, ops)
+    drv.record = tuple(record)
     toks, hidden, lg = drv.greedy(stack.prompt(), cfg.n_gen, collect_logits=logit_steps)
     out = dict(tokens=np.array(toks, np.int32), hidden=hidden, prompt=stack.prompt())
+    for il, v in drv.depth.items():
+        out[f"depth{il}"] = v
     for s, v in lg.items():
-        out[f"logits{s}"] = v
+        if cfg.vocab <= 4096:
+            out[f"logits{s}"] = v
+        top = np.argsort(-v.astype(np.float64), kind="stable")[:8]
+        out[f"logits{s}_top_ids"] = top.astype(np.int32)
+        out[f"logits{s}_top_vals"] = v[top]
     np.savez_compressed(os.path.join(OUT, fname), **out)
     print(fname, name, f"{time.time() - t0:.1f}s", "tokens", toks[:8], "...")
 
@@ -578,6 +586,9 @@ JOBS = {
     "moe_tiny": lambda: gen_llama(models.MOE_TINY, "moe_tiny.npz", logit_steps=(0, 15)),
     "qwen_tiny": lambda: gen_qwen_stack("qwen35-tiny", "qwen_tiny.npz", logit_steps=(0, 15)),
     "qwen_tiny_moe": lambda: gen_qwen_stack("qwen35-tiny-moe", "qwen_tiny_moe.npz", logit_steps=(0, 7)),
+    "qwen48": lambda: gen_qwen_stack("qwen35-gdn-stack-48-short", "qwen48_short.npz", logit_steps=(0, 7),
+                                     record=range(3, 48, 4)),
+    "moe8": lambda: gen_llama(models.QWEN3_MOE8, "moe_stack8.npz", seed=3, logit_steps=(0, 7)),
 }
 
 if __name__ == "__main__":
