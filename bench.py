@@ -468,13 +468,28 @@ def cpu_gemv_worker(args):
 
 
 def cpu_host_info():
+    """The host the CPU baseline ran on: core counts, the CPU's identification
+    fields as /proc/cpuinfo gives them (the model-name string of a virtualised
+    host can be as short as "AMD EPYC", so family / model / stepping and the
+    vector extensions the reference's kernels use are recorded too), the
+    sockets and the frequency governor."""
     info = {"nproc": os.cpu_count(), "affinity_cpus": len(os.sched_getaffinity(0))}
     try:
+        fields, sockets = {}, set()
         with open("/proc/cpuinfo") as f:
             for line in f:
-                if line.startswith("model name"):
-                    info["cpu_model"] = line.split(":", 1)[1].strip()
-                    break
+                k, _, v = line.partition(":")
+                k, v = k.strip(), v.strip()
+                if k == "physical id":
+                    sockets.add(v)
+                if k in ("model name", "vendor_id", "cpu family", "model", "stepping", "cpu MHz", "flags") \
+                        and k not in fields:
+                    fields[k] = v
+        info["cpu_model"] = fields.get("model name")
+        info["cpu_id"] = {k: fields.get(k) for k in ("vendor_id", "cpu family", "model", "stepping", "cpu MHz")}
+        flags = set(fields.get("flags", "").split())
+        info["cpu_vector_ext"] = sorted(x for x in flags if x.startswith(("avx512", "avx2", "fma", "f16c")))
+        info["sockets"] = len(sockets) or None
     except OSError:
         pass
     for path in ("/sys/devices/system/cpu/cpu0/cpufreq/scaling_governor",):
