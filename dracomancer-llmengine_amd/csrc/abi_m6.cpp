@@ -560,22 +560,27 @@ bool ksplit_o_dense(const DevModel* m, int l) {
 int g_attn_o_fusion = 1;
 
 // Whether dense layer l's attention split merge rides on its o projection
-// (dk_attn_o: one launch fewer per layer) and the o projection's eight
-// partials on the gate/up launch (the PRES8 prologue forms the FFN input into
-// w.xm): the per-head attention kernel at head dim 64 with 32 q heads (eight
-// 256-wide input chunks of four heads: configs[2]), a K-quant o projection
-// and a gate/up pair of one K-quant format whose rows the PRES8 prologue
-// covers.
+// (dk_attn_o: one launch fewer per layer) and the o projection's chunk sums
+// on the gate/up launch (its pending-residual prologue forms the FFN input
+// into w.xm): the per-head attention kernel at head dim 64, and either a
+// K-quant o projection of 32 q heads (eight 256-wide input chunks of four
+// heads: configs[2]) with a gate/up pair of one K-quant format whose rows the
+// PRES8 prologue covers, or a Q8_0 o projection of at most 4 q heads per kv
+// head (one chunk per kv group: configs[0]) with a Q8_0 gate/up pair.
 bool fused_o_shape(const DevModel* m, int l) {
     if (!g_attn_o_fusion) return false;
     const DevFfn* f = m->ffn[l];
     const DevAttn* a = m->attn[l];
     if (!f || m->moe[l] || f->g->L.code != f->u->L.code) return false;
-    auto kq = [](const DracoMat* x) { return x->L.code == DRACO_Q4_K || x->L.code == DRACO_Q6_K; };
-    if (!kq(f->g) || !kq(a->wo) || a->HD != 64 || a->NH != 32 || a->wo->L.n_in != 2048) return false;
-    if (!attn_per_head(a->NH, a->NKV, a->HD) || attn_grouped(a->NH, a->NKV, a->HD) ||
-        attn_nsplit(a->max_t, a->NH, a->NKV, a->HD) > 64)
+    if (a->HD != 64 || !attn_per_head(a->NH, a->NKV, a->HD) || attn_grouped(a->NH, a->NKV, a->HD) ||
+        attn_nsplit(a->max_t, a->NH, a->NKV, a->HD) > 64 || a->wo->L.n_in != a->NH * 64)
         return false;
+    // Q8_0: chunks of one kv group of at most 4 heads, a Q8_0
+    // gate/up pair whose rows one prologue batch holds (k_seg PEND)
+    if (a->wo->L.code == DRACO_Q8_0)
+        return f->g->L.code == DRACO_Q8_0 && a->NH / a->NKV <= 4 && f->H <= 4096;
+    auto kq = [](const DracoMat* x) { return x->L.code == DRACO_Q4_K || x->L.code == DRACO_Q6_K; };
+    if (!kq(f->g) || !kq(a->wo) || a->NH != 32 || a->wo->L.n_in != 2048) return false;
     DqShape sh;
     return draco_dq_shape(f->H, (f->FF + 15) / 16, true, 0, 4, 0, 256, sh) == 0;
 }

@@ -51,11 +51,12 @@ int dk_attention(const float* q, const float* kc, const float* vc, float* part, 
 // per-head kernel serves); -1 otherwise.  part as dk_attention.
 int dk_attention_parts(const float* q, const float* kc, const float* vc, float* part, const int* state, int layer,
                        int NH, int NKV, int HD, int max_t, float scale, hipStream_t st);
-// Their merge fused with the o projection wo (Q4_K / Q6_K, n_in = NH * 64,
-// one 256-wide input chunk per 4 heads): acc[row] += round(2^32 * wo . att)
-// over the chunks (int64 fixed point; acc must start at zero), acc[n_out]
-// set when a contribution is not finite; zacc[0 .. zn) is cleared.  -1 for
-// another shape.
+// Their merge fused with the o projection wo (n_in = NH * 64; Q4_K / Q6_K:
+// one 256-wide input chunk per 4 heads; Q8_0: one chunk per kv group of
+// NH / NKV <= 4 heads): acc[row] += round(2^32 * wo . att) over the chunks
+// (int64 fixed point; acc must start at zero), acc[n_out] set when a
+// contribution is not finite; zacc[0 .. zn) is cleared.  -1 for another
+// shape.
 int dk_attn_o(const float* part, int NH, int NKV, int max_t, const DracoMat& wo, unsigned long long* acc,
               unsigned long long* zacc, int zn, hipStream_t st);
 // qwen35 full attention q/k head RMSNorm + rope (NH q heads, 2 k heads of 256).

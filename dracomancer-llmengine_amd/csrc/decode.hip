@@ -566,6 +566,78 @@ __global__ __launch_bounds__(256) void k_attn_o(const float* __restrict__ part, 
     }
 }
 
+// The same fusion for a Q8_0 o projection (head dim 64, REP q heads per kv
+// head, REP <= 4).  Chunk c is kv group c: q heads c REP .. c REP + REP - 1,
+// the 2 REP blocks [2 c REP, 2 c REP + 2 REP) of every o row.  Block b takes
+// chunk c = b % NC and rows 32 (b / NC) .. + 31; wave w < REP merges the
+// splits of head c REP + w (k_attn_combine's single memory round trip) into
+// LDS, while every wave's lanes (r, k) = (lane >> 3, lane & 7) already hold
+// row 32 (b / NC) + 8 w + r's block 2 c REP + k (k < 2 REP; the other lanes
+// re-read a real block and contribute nothing), requested first.  Each lane
+// dots its 32 quants with the 32 merged values of its block, the 8 lanes of
+// a row sum, and the row's contribution meets the other chunks' in acc[row]
+// as 64-bit fixed point (as k_attn_o: order-independent integer sums, a
+// flag at acc[n_out] for a non-finite or out-of-range value).  The merged
+// values sit in LDS with a 36-float stride per 32-value block, so the 8
+// blocks a row's lanes read fall in different banks.
+template <int MAXS, int REP>
+__global__ __launch_bounds__(256) void k_attn_o8(const float* __restrict__ part, int nsplit,
+                                                 const uint8_t* __restrict__ qs, const uint8_t* __restrict__ ds,
+                                                 int nb, int n_out, int NC, unsigned long long* __restrict__ acc,
+                                                 unsigned long long* __restrict__ zacc, int zn) {
+    constexpr int HD = 64, KB = 2 * REP;  // blocks of the chunk
+    __shared__ __align__(16) float att[8 * 36];
+    const int b = blockIdx.x, c = b % NC, rb = b / NC;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, r = lane >> 3, k = lane & 7;
+    const int row = rb * 32 + w * 8 + r, rc = row < n_out ? row : n_out - 1;
+    const int kc = k < KB ? k : KB - 1;
+    const size_t blk = (size_t)rc * nb + (size_t)c * KB + kc;
+    const uint4 q0 = ldnt4(qs + blk * 32), q1 = ldnt4(qs + blk * 32 + 16);
+    const uint16_t dh = *reinterpret_cast<const uint16_t*>(ds + blk * 2);
+    // merge head c REP + w (waves w < REP): every load unconditional
+    const int hw = w < REP ? w : REP - 1;
+    const float* ph = part + (size_t)(c * REP + hw) * nsplit * (HD + 2);
+    const int kl = min(lane, nsplit - 1);
+    const float m0 = ph[kl * (HD + 2) + HD], l0 = ph[kl * (HD + 2) + HD + 1];
+    float pv[MAXS];
+#pragma unroll
+    for (int s = 0; s < MAXS; s++) pv[s] = ph[min(s, nsplit - 1) * (HD + 2) + lane];
+    for (int i = b * 256 + tid; i < zn; i += gridDim.x * 256) zacc[i] = 0ull;
+    const float m = lane < nsplit ? m0 : -INFINITY;
+    const float lk = lane < nsplit ? l0 : 0.f;
+    const float M = wave_max(m);
+    const float wk = m > -INFINITY ? expf(m - M) : 0.f;
+    const float L = wave_sum(lk * wk);
+    float sacc = 0.f;
+#pragma unroll
+    for (int s = 0; s < MAXS; s++)  // lanes s >= nsplit carry weight 0
+        sacc = fmaf(pv[s], __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wk), s)), sacc);
+    // head w's dims 0..31 are chunk block 2w, 32..63 block 2w + 1
+    if (w < REP) att[(2 * w + (lane >> 5)) * 36 + (lane & 31)] = sacc * (1.f / L);
+    lds_barrier();
+    const float* xa = att + kc * 36;
+    const uint32_t Q[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+    float d = 0.f;
+#pragma unroll
+    for (int dw = 0; dw < 8; dw++) {
+        const float4 x4 = *reinterpret_cast<const float4*>(xa + 4 * dw);
+        d = fmaf(sbyte_f(Q[dw], 0), x4.x, d);
+        d = fmaf(sbyte_f(Q[dw], 1), x4.y, d);
+        d = fmaf(sbyte_f(Q[dw], 2), x4.z, d);
+        d = fmaf(sbyte_f(Q[dw], 3), x4.w, d);
+    }
+    float v = k < KB ? h2f(dh) * d : 0.f;
+    v = group_sum<8>(v);
+    if (k == 0 && row < n_out) {
+        const float sv = v * 4294967296.f;  // 2^32
+        if (fabsf(sv) < 9.0e18f) {          // |round(sv)| < 2^63, and not NaN
+            atomicAdd(acc + row, (unsigned long long)(long long)rintf(sv));
+        } else {
+            atomicOr(acc + n_out, 1ull);
+        }
+    }
+}
+
 // qwen35 full attention, per-head RMSNorm over 256 dims and rope on the pairs
 // (t, t + 32), t < 32 (src/m6_layer.c:427-457).  Blocks 0..NH-1 normalise q
 // head b from QG[b * 512 .. + 256] into Qr[b * 256] as (x * r) * q_norm; blocks
@@ -830,6 +902,32 @@ int dk_attention_parts(const float* q, const float* kc, const float* vc, float* 
 int dk_attn_o(const float* part, int NH, int NKV, int max_t, const DracoMat& wo, unsigned long long* acc,
               unsigned long long* zacc, int zn, hipStream_t st) {
     const int nsplit = attn_nsplit(max_t, NH, NKV, 64);
+    if (wo.L.code == DRACO_Q8_0) {
+        // chunks = kv groups of REP q heads, 2 REP blocks of every o row
+        const int REP = NKV > 0 && NH % NKV == 0 ? NH / NKV : 0;
+        if (REP < 1 || REP > 4 || wo.L.n_in != NH * 64 || wo.L.nb != 2 * NH || nsplit > 64) return -1;
+        const dim3 grid(NKV * ((wo.L.n_out + 31) / 32)), block(256);
+        const uint8_t* qs = wo.dev + wo.L.off[0];
+        const uint8_t* ds = wo.dev + wo.L.off[1];
+#define AO8_CASE(S_, R_)                                                                                        \
+    hipLaunchKernelGGL((k_attn_o8<S_, R_>), grid, block, 0, st, part, nsplit, qs, ds, wo.L.nb, wo.L.n_out, NKV, acc, \
+                       zacc, zn)
+#define AO8_REP(S_)            \
+    if (REP == 1) AO8_CASE(S_, 1); \
+    else if (REP == 2) AO8_CASE(S_, 2); \
+    else if (REP == 3) AO8_CASE(S_, 3); \
+    else AO8_CASE(S_, 4);
+        if (nsplit <= 16) {
+            AO8_REP(16)
+        } else if (nsplit <= 32) {
+            AO8_REP(32)
+        } else {
+            AO8_REP(64)
+        }
+#undef AO8_REP
+#undef AO8_CASE
+        return 0;
+    }
     const int NC = NH / 4;
     if (NH % 4 || wo.L.n_in != NH * 64 || wo.L.nb != NC || nsplit > 64 ||
         (wo.L.code != DRACO_Q4_K && wo.L.code != DRACO_Q6_K))

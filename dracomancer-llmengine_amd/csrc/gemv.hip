@@ -646,7 +646,12 @@ struct FQ80 {
 // thread's float4s in flight together, staged in LDS (RMS-normalised when
 // do_norm) behind LDS-only barriers; one memory round trip before the first
 // dot.  Passes beyond NP load one pass ahead.
-template <class F, bool DUAL, int NP, bool NORM, int R>
+// PEND (with NORM; rows of at most 4096 values): the input is x plus a
+// pending residual held as 64-bit fixed point at a.am_val ([n_in] sums of
+// round(2^32 p), then a flag at [n_in], set when a contribution was not
+// finite: the input is then NaN), the fused attention merge + o projection's
+// output; block 0 stores the sum (not normalised) to a.xn_out.
+template <class F, bool DUAL, int NP, bool NORM, int R, bool PEND = false>
 __global__ __launch_bounds__(256) void k_seg(const SegKArgs a) {
     extern __shared__ float xsh[];  // the block's x, n_in floats (normalised when do_norm)
     __shared__ float red[4];
@@ -691,11 +696,35 @@ __global__ __launch_bounds__(256) void k_seg(const SegKArgs a) {
     constexpr int XB = 4;  // float4s per thread per batch
     const float* nwp = a.norm_w ? a.norm_w : a.x;
     float4 xv[XB], nv[XB];
+    longlong2 pa[PEND ? XB : 1], pb[PEND ? XB : 1];
+    long long pflag = 0;
 #pragma unroll
     for (int q = 0; q < XB; q++) {
         const int i4 = tid + q * 256, ic = i4 < n4 ? i4 : n4 - 1;
         xv[q] = ld4(a.x + 4 * ic);
         if (NORM) nv[q] = ld4(nwp + 4 * ic);
+        if constexpr (PEND) {
+            const longlong2* A = reinterpret_cast<const longlong2*>(a.am_val) + 2 * ic;
+            pa[q] = A[0];
+            pb[q] = A[1];
+        }
+    }
+    if constexpr (PEND) {
+        pflag = reinterpret_cast<const long long*>(a.am_val)[a.n_in];
+#pragma unroll
+        for (int q = 0; q < XB; q++) {
+            constexpr float S = 2.3283064365386963e-10f;  // 2^-32
+            float4 v = xv[q];
+            if (pflag) {
+                v.x = v.y = v.z = v.w = __builtin_nanf("");
+            } else {
+                v.x += (float)pa[q].x * S; v.y += (float)pa[q].y * S;
+                v.z += (float)pb[q].x * S; v.w += (float)pb[q].y * S;
+            }
+            xv[q] = v;
+            if (a.xn_out && blockIdx.x == 0 && tid + q * 256 < n4)
+                *reinterpret_cast<float4*>(a.xn_out + 4 * (tid + q * 256)) = v;
+        }
     }
     float ss = 0.f;
     auto stage = [&](int i4, float4 v, const float4 w) {
@@ -723,7 +752,7 @@ __global__ __launch_bounds__(256) void k_seg(const SegKArgs a) {
     if (NORM) {
         const float tot = (red[0] + red[1]) + (red[2] + red[3]);
         inv = 1.f / sqrtf(tot / (float)a.n_in + a.eps);
-        if (a.xn_out && blockIdx.x == 0) {  // the normalised x, (x / rms) * w as the reference
+        if (!PEND && a.xn_out && blockIdx.x == 0) {  // the normalised x, (x / rms) * w as the reference
             auto put = [&](int i4, float4 v, const float4 w) {
                 if (a.norm_w) {
                     v.x = v.x * inv * w.x; v.y = v.y * inv * w.y; v.z = v.z * inv * w.z; v.w = v.w * inv * w.w;
@@ -1180,21 +1209,26 @@ int seg_launch_dq(SegLaunch& a, hipStream_t st) {
     return 0;
 }
 
-template <bool DUAL, int NP, bool NORM, int R = SEG_R>
+template <bool DUAL, int NP, bool NORM, int R = SEG_R, bool PEND = false>
 void launch_seg1(dim3 g, size_t shm, hipStream_t st, const SegKArgs& k) {
     static std::once_flag once;
     std::call_once(once, [] {
         // 128 KB of x (the kernel's static LDS and this stay below the CU's 160 KB)
-        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&k_seg<FQ80, DUAL, NP, NORM, R>),
+        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&k_seg<FQ80, DUAL, NP, NORM, R, PEND>),
                                   hipFuncAttributeMaxDynamicSharedMemorySize, 128 * 1024);
     });
-    hipLaunchKernelGGL((k_seg<FQ80, DUAL, NP, NORM, R>), g, dim3(256), shm, st, k);
+    hipLaunchKernelGGL((k_seg<FQ80, DUAL, NP, NORM, R, PEND>), g, dim3(256), shm, st, k);
 }
 
 template <bool DUAL, int NP>
 void launch_seg(dim3 g, size_t shm, hipStream_t st, const SegKArgs& k) {
-    if (k.do_norm) launch_seg1<DUAL, NP, true>(g, shm, st, k);
-    else launch_seg1<DUAL, NP, false>(g, shm, st, k);
+    if (k.do_norm == 4) {  // the pending residual's fixed-point accumulator (SwiGLU pairs only)
+        if constexpr (DUAL) launch_seg1<true, NP, true, SEG_R, true>(g, shm, st, k);
+    } else if (k.do_norm) {
+        launch_seg1<DUAL, NP, true>(g, shm, st, k);
+    } else {
+        launch_seg1<DUAL, NP, false>(g, shm, st, k);
+    }
 }
 
 // Q8_0 segments (k_seg).
@@ -1229,6 +1263,10 @@ int seg_launch_q8(SegLaunch& a, hipStream_t st) {
     bool dual = false;
     for (int i = 0; i < a.nseg; i++) dual = dual || a.seg[i].epi == EPI_SWIGLU;
     if (dual && a.nseg != 2) return -1;
+    // the fixed-point pending residual: a SwiGLU pair whose rows fit one
+    // batch of the prologue (4 float4s per thread), with its accumulator
+    if (a.do_norm == 4 && (!dual || a.n_in > 4096 || !a.am_val)) return -1;
+    if (a.do_norm == 2 || a.do_norm == 3) return -1;
     // x is staged in LDS: up to 32768 floats (128 KB, above the default 64 KB)
     if (a.n_in % 32 || a.n_in > 32768) return -1;
     const size_t shm = sizeof(float) * (size_t)a.n_in;

@@ -126,6 +126,48 @@ def test_attn_o_fusion_matches_oracle(oracle, fusion, use_graph):
         L.draco_set_attn_o_fusion(old)
 
 
+Q8_FUSED_SHAPES = [  # (q heads, kv heads, hidden, max_t): REP = 3, 4, 2, 1; 2, 32, 64 splits
+    (15, 5, 960, 1024), (8, 2, 512, 64), (8, 4, 512, 2048), (4, 4, 256, 64)]
+
+
+@pytest.mark.parametrize("shape", Q8_FUSED_SHAPES, ids=[f"{s[0]}q{s[1]}kv-t{s[3]}" for s in Q8_FUSED_SHAPES])
+@pytest.mark.parametrize("use_graph", [False, True])
+def test_attn_o8_fusion_matches_oracle(oracle, shape, use_graph):
+    """Q8_0 layers (configs[0]'s formats) with the attention split merge fused
+    with the o projection (one chunk per kv group of 1-4 heads, int64 fixed
+    point into the gate/up launch's prologue), at 2, 32 and 64 attention
+    splits: the device loop (graph-replayed and eager) and the per-token
+    drop-in path give the oracle engine's greedy tokens, hidden state within
+    the decode bar.  The configs[0] shape also runs with the fusion off."""
+    import dataclasses
+    from tests_oracle_engine import oracle_engine
+    from dracohip import lib
+    nh, nkv, hidden, max_t = shape
+    cfg = dataclasses.replace(models.SMOL360M, name=f"q8-fused-{nh}-{nkv}", hidden=hidden, n_head=nh, n_kv=nkv,
+                              n_layer=3, n_ff=2560 if hidden == 960 else 1024, vocab=1024, n_prompt=12, n_gen=8,
+                              max_t=max_t, wscale=0.25 if hidden < 960 else 0.02)
+    model = models.build_llama(cfg, 41)
+    ref = LlamaDriver(model, oracle_engine(oracle))
+    rt, rh, _ = ref.greedy(model.prompt(), cfg.n_gen)
+    L = lib.load()
+    for fusion in ([1, 0] if hidden == 960 else [1]):
+        old = L.draco_set_attn_o_fusion(fusion)
+        try:
+            L.draco_reset()
+            drv = LlamaDriver(model, hip_engine_lib())
+            print(f"[decode] q8 attn-o fusion {fusion} {shape} graph={use_graph}", flush=True)
+            toks, hidden_dev, _ = drv.generate_device(model.prompt(), cfg.n_gen, use_graph=use_graph)
+            assert toks == rt
+            assert np.max(np.abs(hidden_dev - rh)) <= hid_tol(rh)
+            L.draco_reset()
+            drv2 = LlamaDriver(model, hip_engine_lib())
+            t2, h2, _ = drv2.greedy(model.prompt(), cfg.n_gen)
+            assert t2 == rt
+            assert np.max(np.abs(h2 - rh)) <= hid_tol(rh)
+        finally:
+            L.draco_set_attn_o_fusion(old)
+
+
 def test_attn_o_fusion_is_deterministic():
     """The fused o projection's chunks meet in int64 fixed point (atomic
     adds in any order): graph-replayed and eager runs, repeated, give the
