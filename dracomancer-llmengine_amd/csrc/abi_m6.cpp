@@ -571,7 +571,18 @@ bool fused_o_shape(const DevModel* m, int l) {
     if (!g_attn_o_fusion) return false;
     const DevFfn* f = m->ffn[l];
     const DevAttn* a = m->attn[l];
-    if (!f || m->moe[l] || f->g->L.code != f->u->L.code) return false;
+    auto kq = [](const DracoMat* x) { return x->L.code == DRACO_Q4_K || x->L.code == DRACO_Q6_K; };
+    if (m->moe[l]) {
+        // MoE layers: a K-quant o projection of whole 256-wide
+        // chunks at head dim 64 / 128 / 256, the grouped or per-head
+        // attention kernel, and a router whose RMSNorm prologue can form the
+        // pending input
+        const int HD = a->HD;
+        return kq(a->wo) && (HD == 64 || HD == 128 || HD == 256) && (a->NH * HD) % 256 == 0 &&
+               a->wo->L.n_in == a->NH * HD && (attn_grouped(a->NH, a->NKV, HD) || attn_per_head(a->NH, a->NKV, HD)) &&
+               attn_nsplit(a->max_t, a->NH, a->NKV, HD) <= 64 && draco_moe_layer_pend_ok(m->moe[l], m->fnorm[l]);
+    }
+    if (!f || f->g->L.code != f->u->L.code) return false;
     if (a->HD != 64 || !attn_per_head(a->NH, a->NKV, a->HD) || attn_grouped(a->NH, a->NKV, a->HD) ||
         attn_nsplit(a->max_t, a->NH, a->NKV, a->HD) > 64 || a->wo->L.n_in != a->NH * 64)
         return false;
@@ -579,7 +590,6 @@ bool fused_o_shape(const DevModel* m, int l) {
     // gate/up pair whose rows one prologue batch holds (k_seg PEND)
     if (a->wo->L.code == DRACO_Q8_0)
         return f->g->L.code == DRACO_Q8_0 && a->NH / a->NKV <= 4 && f->H <= 4096;
-    auto kq = [](const DracoMat* x) { return x->L.code == DRACO_Q4_K || x->L.code == DRACO_Q6_K; };
     if (!kq(f->g) || !kq(a->wo) || a->NH != 32 || a->wo->L.n_in != 2048) return false;
     DqShape sh;
     return draco_dq_shape(f->H, (f->FF + 15) / 16, true, 0, 4, 0, 256, sh) == 0;
@@ -651,8 +661,11 @@ int enqueue_layer(DevModel* m, int l, float eps, hipStream_t st, const float* xi
             return fail(-1, "attention launch");
         unsigned long long* acc = m->oacc + (size_t)l * m->oacc_stride;
         unsigned long long* zacc = m->oacc + (size_t)m->fo_prev[l] * m->oacc_stride;
-        if (dk_attn_o(w.part, a->NH, a->NKV, a->max_t, *a->wo, acc, zacc, (int)m->oacc_stride, st))
+        if (dk_attn_o(w.part, a->NH, a->NKV, a->HD, a->max_t, *a->wo, acc, zacc, (int)m->oacc_stride, st))
             return fail(-1, "attention o launch");
+        if (m->moe[l])  // the router forms base + the o projection into w.xm (its norm input, the down's residual)
+            return draco_moe_layer_enqueue(m->moe[l], base, m->fnorm[l], eps, w.x, nullptr, st,
+                                           reinterpret_cast<const float*>(acc), w.xm, true);
         if (int rc = enqueue_gateup(f, w, base, 1, m->fnorm[l], eps, st, reinterpret_cast<const float*>(acc), w.xm, 8))
             return rc;
     } else if (dk_attention(w.q, a->kc, a->vc, w.part, w.cnt, w.att, m->state, l, a->NH, a->NKV, a->HD, a->max_t,

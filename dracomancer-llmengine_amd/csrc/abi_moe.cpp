@@ -130,9 +130,9 @@ int moe_work(MoeWork& w, int n_in, int n_exp, int n_used, int inter, int n_out) 
 // (RMSNorm with norm_w, eps), which the expert launches read
 int enqueue_moe(ExpertSet* s, const float* x, float* out, const float* resid, MoeWork& w, int n_exp, int n_used,
                 int inter, int n_in, int n_out, hipStream_t st, const float* norm_w = nullptr, float eps = 0.f,
-                float* xn = nullptr, const float* pend = nullptr, float* xs = nullptr) {
+                float* xn = nullptr, const float* pend = nullptr, float* xs = nullptr, bool pend_fx = false) {
     if (draco_moe_logits_launch(x, (const float*)s->router->dev, n_exp, n_in, w.logits, st, norm_w, eps, xn, pend,
-                                xs))
+                                xs, pend_fx))
         return fail(-1, "moe router launch rejected");
     if (pend) resid = xs;  // the formed input is the residual
     MoeArgs a = {};
@@ -483,7 +483,7 @@ MoeLayer* draco_moe_layer(const DracoMoeP* p) {
 bool draco_moe_layer_pend_ok(const MoeLayer* m, const float* norm_w) { return m->snap.n_in <= 4096 && norm_w; }
 
 int draco_moe_layer_enqueue(MoeLayer* m, const float* x, const float* norm_w, float eps, float* out,
-                            const float* resid, hipStream_t st, const float* pend, float* xs) {
+                            const float* resid, hipStream_t st, const float* pend, float* xs, bool pend_fx) {
     const DracoMoeP& p = m->snap;
     if (!draco_moe_layer_pend_ok(m, norm_w)) {  // wider than the router's norm prologue, or no norm weight
         if (pend) return fail(-1, "moe layer: a pending residual needs the router's RMSNorm prologue");
@@ -492,7 +492,7 @@ int draco_moe_layer_enqueue(MoeLayer* m, const float* x, const float* norm_w, fl
     }
     if (pend && !xs) return fail(-1, "moe layer: a pending residual needs its sum buffer");
     return enqueue_moe(m->set, x, out, resid, m->w, p.n_exp, p.n_used, p.inter, p.n_in, p.n_out, st, norm_w, eps,
-                       m->xn, pend, xs);
+                       m->xn, pend, xs, pend_fx);
 }
 
 int draco_moe_layer_enqueue_xn(MoeLayer* m, const float* xn, float* out, const float* resid, hipStream_t st) {

@@ -47,8 +47,9 @@ void dk_rope_append(float* q, const float* k, const float* v, float* kc, float* 
 int dk_attention(const float* q, const float* kc, const float* vc, float* part, unsigned* count, float* out,
                  const int* state, int layer, int NH, int NKV, int HD, int max_t, float scale, hipStream_t st,
                  const float* gate = nullptr, int gstride = 0);
-// The per-head attention's split partials only (head dim 64, the shapes the
-// per-head kernel serves); -1 otherwise.  part as dk_attention.
+// The split partials only (the grouped or per-head kernel dk_attention would
+// run, without the merge); -1 for the shapes only the generic kernel serves.
+// part as dk_attention.
 int dk_attention_parts(const float* q, const float* kc, const float* vc, float* part, const int* state, int layer,
                        int NH, int NKV, int HD, int max_t, float scale, hipStream_t st);
 // Their merge fused with the o projection wo (n_in = NH * 64; Q4_K / Q6_K:
@@ -57,7 +58,7 @@ int dk_attention_parts(const float* q, const float* kc, const float* vc, float* 
 // (int64 fixed point; acc must start at zero), acc[n_out] set when a
 // contribution is not finite; zacc[0 .. zn) is cleared.  -1 for another
 // shape.
-int dk_attn_o(const float* part, int NH, int NKV, int max_t, const DracoMat& wo, unsigned long long* acc,
+int dk_attn_o(const float* part, int NH, int NKV, int HD, int max_t, const DracoMat& wo, unsigned long long* acc,
               unsigned long long* zacc, int zn, hipStream_t st);
 // qwen35 full attention q/k head RMSNorm + rope (NH q heads, 2 k heads of 256).
 void dk_fa_prep(const float* QG, float* Qr, const float* kin, float* kout, const float* qn, const float* kn,

@@ -485,13 +485,16 @@ __global__ __launch_bounds__(256) void k_attn_combine(const float* __restrict__ 
     out[(size_t)h * HD + tid] = r;
 }
 
-// The per-head kernel's split merge fused with the o projection (head dim
-// 64: q heads 4c .. 4c+3 are input super-block c of the o rows; Q4_K / Q6_K
-// tile layout).  Block b takes chunk c = b % NC and row tiles 4 (b / NC) ..
-// +3.  Wave w first requests its tile's item c (the weights stream while the
-// merge runs), then merges the splits of head 4c + w as k_attn_combine does
-// (statistics and partials in one round trip); wave 0 digitises the 256
-// merged values (as k_dq's prologue) and every wave multiplies its tile.
+// The split merge fused with the o projection (Q4_K / Q6_K tile layout):
+// input super-block c of the o rows is chunk c, the 256 attention outputs
+// 256 c .. 256 c + 255 (q heads 4c .. 4c+3 at head dim 64, 2c, 2c+1 at 128,
+// c at 256).  Block b takes chunk c = b % NC and row tiles 4 (b / NC) .. +3.
+// Wave w first requests its tile's item c (the weights stream while the
+// merge runs), then merges outputs 256 c + 64 w .. + 63 (one head's 64 dims,
+// or a quarter / half of one, with that head's split statistics) as
+// k_attn_combine does (statistics and partials in one round trip); wave 0
+// digitises the 256 merged values (as k_dq's prologue) and every wave
+// multiplies its tile.
 // The chunks' contributions W[row, 256c .. 256c + 255] . att[256c ..] meet
 // in acc[row] as 64-bit fixed point (round(v * 2^32), agent-scope atomic
 // adds): integer addition is associative, so the sum is the same bit for
@@ -503,12 +506,12 @@ __global__ __launch_bounds__(256) void k_attn_combine(const float* __restrict__ 
 // before this launch).  With NC = 8 kv groups of 4 heads block b
 // runs on XCD b mod 8, the XCD that ran the splits of kv head c (k_attn_part's
 // block (c, s) is linear block c + 8 s).
-template <int FM, int MAXS>
+template <int FM, int MAXS, int HD>
 __global__ __launch_bounds__(256) void k_attn_o(const float* __restrict__ part, int nsplit,
                                                 const uint8_t* __restrict__ wo, int nb, int n_out, int NC,
                                                 unsigned long long* __restrict__ acc,
                                                 unsigned long long* __restrict__ zacc, int zn) {
-    constexpr int HD = 64;
+    static_assert(HD == 64 || HD == 128 || HD == 256, "chunk = whole heads or parts of one");
     constexpr size_t IB = FM == 1 ? DRACO_Q4T_ITEM : DRACO_Q6T_ITEM;
     __shared__ __align__(16) float att[256];
     __shared__ __align__(16) int8_t xd[1024];
@@ -522,13 +525,15 @@ __global__ __launch_bounds__(256) void k_attn_o(const float* __restrict__ part, 
     const uint8_t* item = wo + ((size_t)Tc * nb + c) * IB;
     if (FM == 1) load_q4(item, lane, f);
     else load_q6(item, lane, f);
-    // merge head 4c + w: every load unconditional (clamped split index)
-    const float* ph = part + (size_t)(4 * c + w) * nsplit * (HD + 2);
+    // merge outputs 256 c + 64 w + lane: head (256 c + 64 w) / HD, dim
+    // (64 w) % HD + lane; every load unconditional (clamped split index)
+    const int hh = (256 * c + 64 * w) / HD, dd = (64 * w) % HD + lane;
+    const float* ph = part + (size_t)hh * nsplit * (HD + 2);
     const int kl = min(lane, nsplit - 1);
     const float m0 = ph[kl * (HD + 2) + HD], l0 = ph[kl * (HD + 2) + HD + 1];
     float pv[MAXS];
 #pragma unroll
-    for (int k = 0; k < MAXS; k++) pv[k] = ph[min(k, nsplit - 1) * (HD + 2) + lane];
+    for (int k = 0; k < MAXS; k++) pv[k] = ph[min(k, nsplit - 1) * (HD + 2) + dd];
     reinterpret_cast<uint32_t*>(zero)[tid] = 0u;
     for (int i = b * 256 + tid; i < zn; i += gridDim.x * 256) zacc[i] = 0ull;
     const float m = lane < nsplit ? m0 : -INFINITY;
@@ -540,7 +545,7 @@ __global__ __launch_bounds__(256) void k_attn_o(const float* __restrict__ part, 
 #pragma unroll
     for (int k = 0; k < MAXS; k++)  // lanes k >= nsplit carry weight 0
         s = fmaf(pv[k], __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wk), k)), s);
-    att[w * HD + lane] = s * (1.f / L);
+    att[w * 64 + lane] = s * (1.f / L);
     lds_barrier();
     if (w == 0) digits4(reinterpret_cast<const float4*>(att)[lane], lane, xd, xsm);
     lds_barrier();
@@ -892,20 +897,42 @@ int dk_attention(const float* q, const float* kc, const float* vc, float* part, 
 
 int dk_attention_parts(const float* q, const float* kc, const float* vc, float* part, const int* state, int layer,
                        int NH, int NKV, int HD, int max_t, float scale, hipStream_t st) {
-    if (HD != 64 || !attn_per_head(NH, NKV, HD) || attn_grouped(NH, NKV, HD)) return -1;
     const int nsplit = attn_nsplit(max_t, NH, NKV, HD);
+    if (attn_grouped(NH, NKV, HD)) {
+        const int rep = NH / NKV;
+        const dim3 grid(NKV, nsplit);
+#define GQA_CASE(H_, R_)                                                                                  \
+    if (HD == H_ && rep == R_) {                                                                          \
+        hipLaunchKernelGGL((k_attn_gqa<H_, R_>), grid, dim3(256), 0, st, q, kc, vc, part, state, layer, NKV, \
+                           nsplit, scale);                                                                \
+    } else
+        GQA_CASE(128, 2) GQA_CASE(128, 4) GQA_CASE(128, 8)
+        GQA_CASE(256, 2) GQA_CASE(256, 4) GQA_CASE(256, 8) GQA_CASE(256, 16) return -1;
+#undef GQA_CASE
+        return 0;
+    }
+    if (!attn_per_head(NH, NKV, HD)) return -1;
     const dim3 grid(NKV, nsplit), block(64 * (NH / NKV));
-    hipLaunchKernelGGL(k_attn_part<64>, grid, block, 0, st, q, kc, vc, part, state, layer, NH, NKV, nsplit, scale);
+    if (HD == 64)
+        hipLaunchKernelGGL(k_attn_part<64>, grid, block, 0, st, q, kc, vc, part, state, layer, NH, NKV, nsplit, scale);
+    else if (HD == 128)
+        hipLaunchKernelGGL(k_attn_part<128>, grid, block, 0, st, q, kc, vc, part, state, layer, NH, NKV, nsplit,
+                           scale);
+    else if (HD == 256)
+        hipLaunchKernelGGL(k_attn_part<256>, grid, block, 0, st, q, kc, vc, part, state, layer, NH, NKV, nsplit,
+                           scale);
+    else
+        return -1;
     return 0;
 }
 
-int dk_attn_o(const float* part, int NH, int NKV, int max_t, const DracoMat& wo, unsigned long long* acc,
+int dk_attn_o(const float* part, int NH, int NKV, int HD, int max_t, const DracoMat& wo, unsigned long long* acc,
               unsigned long long* zacc, int zn, hipStream_t st) {
-    const int nsplit = attn_nsplit(max_t, NH, NKV, 64);
+    const int nsplit = attn_nsplit(max_t, NH, NKV, HD);
     if (wo.L.code == DRACO_Q8_0) {
         // chunks = kv groups of REP q heads, 2 REP blocks of every o row
         const int REP = NKV > 0 && NH % NKV == 0 ? NH / NKV : 0;
-        if (REP < 1 || REP > 4 || wo.L.n_in != NH * 64 || wo.L.nb != 2 * NH || nsplit > 64) return -1;
+        if (HD != 64 || REP < 1 || REP > 4 || wo.L.n_in != NH * 64 || wo.L.nb != 2 * NH || nsplit > 64) return -1;
         const dim3 grid(NKV * ((wo.L.n_out + 31) / 32)), block(256);
         const uint8_t* qs = wo.dev + wo.L.off[0];
         const uint8_t* ds = wo.dev + wo.L.off[1];
@@ -928,25 +955,36 @@ int dk_attn_o(const float* part, int NH, int NKV, int max_t, const DracoMat& wo,
 #undef AO8_CASE
         return 0;
     }
-    const int NC = NH / 4;
-    if (NH % 4 || wo.L.n_in != NH * 64 || wo.L.nb != NC || nsplit > 64 ||
+    // K-quants: one chunk per o input super-block (256 attention outputs)
+    if (HD != 64 && HD != 128 && HD != 256) return -1;
+    const int NC = NH * HD / 256;
+    if ((NH * HD) % 256 || wo.L.n_in != NH * HD || wo.L.nb != NC || nsplit > 64 ||
         (wo.L.code != DRACO_Q4_K && wo.L.code != DRACO_Q6_K))
         return -1;
     const int ntiles = (wo.L.n_out + 15) / 16;
     const dim3 grid(NC * ((ntiles + 3) / 4)), block(256);
     const bool q4 = wo.L.code == DRACO_Q4_K;
-#define AO_CASE(S_)                                                                                              \
-    if (q4) hipLaunchKernelGGL((k_attn_o<1, S_>), grid, block, 0, st, part, nsplit, wo.dev, wo.L.nb, wo.L.n_out, NC, \
-                               acc, zacc, zn);                                                                   \
-    else hipLaunchKernelGGL((k_attn_o<2, S_>), grid, block, 0, st, part, nsplit, wo.dev, wo.L.nb, wo.L.n_out, NC, \
-                            acc, zacc, zn);
-    if (nsplit <= 16) {
-        AO_CASE(16)
-    } else if (nsplit <= 32) {
-        AO_CASE(32)
-    } else {
-        AO_CASE(64)
+#define AO_CASE(S_, H_)                                                                                          \
+    if (q4) hipLaunchKernelGGL((k_attn_o<1, S_, H_>), grid, block, 0, st, part, nsplit, wo.dev, wo.L.nb, wo.L.n_out, \
+                               NC, acc, zacc, zn);                                                               \
+    else hipLaunchKernelGGL((k_attn_o<2, S_, H_>), grid, block, 0, st, part, nsplit, wo.dev, wo.L.nb, wo.L.n_out, \
+                            NC, acc, zacc, zn);
+#define AO_HD(S_)                \
+    if (HD == 64) {              \
+        AO_CASE(S_, 64)          \
+    } else if (HD == 128) {      \
+        AO_CASE(S_, 128)         \
+    } else {                     \
+        AO_CASE(S_, 256)         \
     }
+    if (nsplit <= 16) {
+        AO_HD(16)
+    } else if (nsplit <= 32) {
+        AO_HD(32)
+    } else {
+        AO_HD(64)
+    }
+#undef AO_HD
 #undef AO_CASE
     return 0;
 }

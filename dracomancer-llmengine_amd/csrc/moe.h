@@ -39,10 +39,13 @@ struct MoeArgs {
 
 // norm_w set (n_in <= 4096): x is normalised first, xn = (x * rms^-1) * norm_w
 // (eps), and stored to xn_out for the expert launches.  pend (norm_w set):
-// the input is x + pend[0..n_in) + pend[n_in..2 n_in), stored to xs_out.
+// the input is x + pend[0..n_in) + pend[n_in..2 n_in), or with pend_fx
+// x + 2^-32 pend_i (int64 fixed point, a flag at [n_in] making it NaN),
+// stored to xs_out.
 int draco_moe_logits_launch(const float* x, const float* gate_inp, int n_exp, int n_in, float* logits,
                             hipStream_t st, const float* norm_w = nullptr, float eps = 0.f,
-                            float* xn_out = nullptr, const float* pend = nullptr, float* xs_out = nullptr);
+                            float* xn_out = nullptr, const float* pend = nullptr, float* xs_out = nullptr,
+                            bool pend_fx = false);
 // fm: 1 = Q4_K, 2 = Q6_K.  route (+dual): gate/up of the routed experts;
 // otherwise the grouped GEMV (xper: per-slot x).
 int draco_moe_grp_launch(MoeArgs& a, int fm, bool dual, bool xper, bool route, hipStream_t st);
@@ -68,11 +71,14 @@ MoeLayer* draco_moe_layer(const DracoMoeP* p);
 // out = resid + MoE(RMSNorm(x) * norm_w), device pointers; out may alias x
 // and resid (x is read by the norm launch before anything is written).
 // With pend ([2][n_in], the o projection's split-K partials) the input is
-// x + pend[0..n_in) + pend[n_in..2 n_in), formed by the router launch and
-// stored to xs, which is then the residual (resid is not read); pend needs
-// the router's RMSNorm prologue (draco_moe_layer_pend_ok).
+// x + pend[0..n_in) + pend[n_in..2 n_in) (with pend_fx: the fused attention
+// merge + o projection's int64 fixed-point sums, x + 2^-32 pend_i), formed by
+// the router launch and stored to xs, which is then the residual (resid is
+// not read); pend needs the router's RMSNorm prologue
+// (draco_moe_layer_pend_ok).
 int draco_moe_layer_enqueue(MoeLayer* m, const float* x, const float* norm_w, float eps, float* out,
-                            const float* resid, hipStream_t st, const float* pend = nullptr, float* xs = nullptr);
+                            const float* resid, hipStream_t st, const float* pend = nullptr, float* xs = nullptr,
+                            bool pend_fx = false);
 bool draco_moe_layer_pend_ok(const MoeLayer* m, const float* norm_w);
 // out = resid + MoE(xn) for an input that is already normalised (the qwen35
 // FFN input x2n, src/qwen35_engine.py:325)

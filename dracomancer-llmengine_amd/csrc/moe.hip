@@ -44,10 +44,12 @@ constexpr int XP_MAXV = 4;
 // every block gets the same xn); block 0 also stores xn for the expert
 // launches, which then need no RMSNorm launch of their own.
 // PRES (with NORM): x is a pending residual, x + pend[0..n_in) +
-// pend[n_in..2 n_in) (the split-K partials of the o projection), formed in
-// every block in that order; block 0 also stores the sum to xs_out (the
-// residual of the expert down launch).
-template <bool NORM, bool PRES = false>
+// pend[n_in..2 n_in) (PRES 1: the split-K partials of the o projection) or
+// x + 2^-32 pend_i (PRES 2: the fused attention merge + o projection's int64
+// fixed-point sums, a flag at [n_in] making the input NaN), formed in every
+// block; block 0 also stores the sum to xs_out (the residual of the expert
+// down launch).
+template <bool NORM, int PRES = 0>
 __global__ __launch_bounds__(256) void k_moe_logits(const float* __restrict__ x, const float* __restrict__ gi,
                                                     int n_exp, int n_in, float* __restrict__ logits,
                                                     const float* __restrict__ norm_w, float eps,
@@ -58,27 +60,45 @@ __global__ __launch_bounds__(256) void k_moe_logits(const float* __restrict__ x,
     const int e = blockIdx.x, tid = threadIdx.x;
     const float* w = gi + (size_t)e * n_in;
     float acc = 0.f;
+    const long long pflag = PRES == 2 ? reinterpret_cast<const long long*>(pend)[n_in] : 0;
     for (int i0 = tid * 4; i0 < n_in; i0 += U * 1024) {
         float4 a[U], b[U], nw[U], p0[U], p1[U];
+        longlong2 q0[PRES == 2 ? U : 1], q1[PRES == 2 ? U : 1];
 #pragma unroll
         for (int u = 0; u < U; u++) {
             const int i = i0 + u * 1024;
             a[u] = i < n_in ? ld4(x + i) : make_float4(0.f, 0.f, 0.f, 0.f);
             b[u] = i < n_in ? ld4(w + i) : make_float4(0.f, 0.f, 0.f, 0.f);
             if (NORM) nw[u] = i < n_in ? ld4(norm_w + i) : make_float4(0.f, 0.f, 0.f, 0.f);
-            if (PRES) {
+            if (PRES == 1) {
                 p0[u] = i < n_in ? ld4(pend + i) : make_float4(0.f, 0.f, 0.f, 0.f);
                 p1[u] = i < n_in ? ld4(pend + n_in + i) : make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+            if constexpr (PRES == 2) {
+                const int ic = i < n_in ? i : 0;
+                const longlong2* A = reinterpret_cast<const longlong2*>(pend) + ic / 2;
+                q0[u] = A[0];
+                q1[u] = A[1];
             }
         }
         if (PRES) {
 #pragma unroll
             for (int u = 0; u < U; u++) {
-                a[u].x = (a[u].x + p0[u].x) + p1[u].x;
-                a[u].y = (a[u].y + p0[u].y) + p1[u].y;
-                a[u].z = (a[u].z + p0[u].z) + p1[u].z;
-                a[u].w = (a[u].w + p0[u].w) + p1[u].w;
                 const int i = i0 + u * 1024;
+                if constexpr (PRES == 1) {
+                    a[u].x = (a[u].x + p0[u].x) + p1[u].x;
+                    a[u].y = (a[u].y + p0[u].y) + p1[u].y;
+                    a[u].z = (a[u].z + p0[u].z) + p1[u].z;
+                    a[u].w = (a[u].w + p0[u].w) + p1[u].w;
+                } else if (i < n_in) {
+                    constexpr float S = 2.3283064365386963e-10f;  // 2^-32
+                    if (pflag) {
+                        a[u].x = a[u].y = a[u].z = a[u].w = __builtin_nanf("");
+                    } else {
+                        a[u].x += (float)q0[u].x * S; a[u].y += (float)q0[u].y * S;
+                        a[u].z += (float)q1[u].x * S; a[u].w += (float)q1[u].y * S;
+                    }
+                }
                 if (e == 0 && i < n_in) *reinterpret_cast<float4*>(xs_out + i) = a[u];
             }
         }
@@ -615,13 +635,16 @@ int dispatch_grp(const MoeArgs& a, int fm, bool dual, bool xper, bool route, int
 
 int draco_moe_logits_launch(const float* x, const float* gate_inp, int n_exp, int n_in, float* logits,
                             hipStream_t st, const float* norm_w, float eps, float* xn_out, const float* pend,
-                            float* xs_out) {
+                            float* xs_out, bool pend_fx) {
     if (n_exp < 1 || n_exp > MOE_EXP_MAX || n_in % 4) return -1;
     if (pend && (!norm_w || !xs_out)) return -1;
     if (norm_w) {
         if (n_in > 4096 || !xn_out) return -1;
-        if (pend)
-            hipLaunchKernelGGL((k_moe_logits<true, true>), dim3(n_exp), dim3(256), 0, st, x, gate_inp, n_exp, n_in,
+        if (pend && pend_fx)
+            hipLaunchKernelGGL((k_moe_logits<true, 2>), dim3(n_exp), dim3(256), 0, st, x, gate_inp, n_exp, n_in,
+                               logits, norm_w, eps, xn_out, pend, xs_out);
+        else if (pend)
+            hipLaunchKernelGGL((k_moe_logits<true, 1>), dim3(n_exp), dim3(256), 0, st, x, gate_inp, n_exp, n_in,
                                logits, norm_w, eps, xn_out, pend, xs_out);
         else
             hipLaunchKernelGGL((k_moe_logits<true>), dim3(n_exp), dim3(256), 0, st, x, gate_inp, n_exp, n_in, logits,

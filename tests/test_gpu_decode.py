@@ -427,6 +427,63 @@ def test_moe_stack_device_generate(use_graph):
     assert np.max(np.abs(hidden - g["hidden"])) <= hid_tol(g["hidden"])
 
 
+@pytest.mark.parametrize("fusion", [1, 0])
+@pytest.mark.parametrize("use_graph", [False, True])
+def test_moe_stack_attn_o_fusion(fusion, use_graph):
+    """configs[3]'s layer (attention 32 q / 4 kv x 128, Q6_K o of 16 chunks)
+    with the attention split merge fused with the o projection (int64 fixed
+    point into the MoE router's prologue) and with the two-launch form: both
+    give the compiled reference's tokens and hidden state, in the device loop
+    and through the per-token drop-in path."""
+    from dracohip import lib
+    g = golden("moe_tiny.npz")
+    L = lib.load()
+    old = L.draco_set_attn_o_fusion(fusion)
+    try:
+        cfg, model, drv = _driver("moe-tiny")
+        print(f"[decode] moe stack attn-o fusion {fusion} graph={use_graph}", flush=True)
+        toks, hidden, _ = drv.generate_device(model.prompt(), cfg.n_gen, use_graph=use_graph)
+        assert toks == list(g["tokens"])
+        assert np.max(np.abs(hidden - g["hidden"])) <= hid_tol(g["hidden"])
+        L.draco_reset()
+        drv2 = LlamaDriver(model, hip_engine_lib())
+        t2, h2, _ = drv2.greedy(model.prompt(), cfg.n_gen)
+        assert t2 == list(g["tokens"])
+        assert np.max(np.abs(h2 - g["hidden"])) <= hid_tol(g["hidden"])
+    finally:
+        L.draco_set_attn_o_fusion(old)
+
+
+MOE_FUSED_SHAPES = [  # (q heads, kv heads, head dim, max_t): per-head HD 64; grouped HD 256; 64 splits at HD 128
+    (16, 4, 64, 64), (8, 2, 256, 64), (32, 8, 128, 2048)]
+
+
+@pytest.mark.parametrize("shape", MOE_FUSED_SHAPES, ids=[f"{s[0]}q{s[1]}kv-hd{s[2]}-t{s[3]}" for s in MOE_FUSED_SHAPES])
+def test_moe_attn_o_fusion_shapes(oracle, shape):
+    """The fused merge + o projection ahead of the MoE router at the other
+    head dims it serves (per-head kernel at 64, grouped at 256, 64 splits at
+    128) against the oracle engine: greedy tokens identical, hidden state
+    within the decode bar (device loop, graph-replayed)."""
+    import dataclasses
+    from tests_oracle_engine import oracle_engine
+    from dracohip import lib
+    nh, nkv, hd, max_t = shape
+    cfg = dataclasses.replace(models.MOE_TINY, name=f"moe-fused-{nh}-{nkv}-{hd}", hidden=1024, n_head=nh, n_kv=nkv,
+                              head_dim=hd, n_exp=16, n_used=4, exp_ff=512, vocab=512, n_prompt=10, n_gen=8,
+                              max_t=max_t, wscale=0.05)
+    model = models.build_llama(cfg, 43)
+    ref = LlamaDriver(model, oracle_engine(oracle))
+    rt, rh, _ = ref.greedy(model.prompt(), cfg.n_gen)
+    L = lib.load()
+    assert L.draco_set_attn_o_fusion(-1) == 1
+    L.draco_reset()
+    drv = LlamaDriver(model, hip_engine_lib())
+    print(f"[decode] moe attn-o fusion {shape}", flush=True)
+    toks, hidden_dev, _ = drv.generate_device(model.prompt(), cfg.n_gen, use_graph=True)
+    assert toks == rt
+    assert np.max(np.abs(hidden_dev - rh)) <= hid_tol(rh)
+
+
 def test_smol360m_device_generate():
     """SmolLM2-360M-shaped Q8_0, 32 prompt + 64 greedy tokens."""
     g = golden("smol360m.npz")
