@@ -57,23 +57,34 @@ def q4k_gemv_roofline(lib, n_copies=10, iters=200):
 
     Average launch duration = one HIP event pair around a graph replay of
     `iters` launches rotating over `n_copies` weight copies (330 MB > the
-    256 MB MALL), so kernels run back to back on the launch stream.
+    256 MB MALL), so kernels run back to back on the launch stream.  The
+    other configs[1] shape (4096x14336, fp32 x) is timed the same way and
+    reported under "other_shape"; the top-level figures are the 14336x4096
+    launch's.
     """
-    n_out, n_in = 14336, 4096
-    rng = np.random.default_rng(1)
-    W = lib.quantize(5, rng.standard_normal((n_out, n_in), dtype=np.float32) * np.float32(0.02))
-    out = np.zeros(8, np.float32)
-    rc = lib.load().draco_bench_gemv(5, lib.pu8(W), n_out, n_in, n_copies, iters, lib.pf(out))
-    if rc != 0:
-        raise RuntimeError(lib.last_error())
-    us = float(out[4])
-    alg_bytes = W.nbytes + 4 * n_in + 4 * n_out  # weights + fp32 x + fp32 y
+    def one(n_out, n_in):
+        rng = np.random.default_rng(1)
+        W = lib.quantize(5, rng.standard_normal((n_out, n_in), dtype=np.float32) * np.float32(0.02))
+        out = np.zeros(8, np.float32)
+        rc = lib.load().draco_bench_gemv(5, lib.pu8(W), n_out, n_in, n_copies, iters, lib.pf(out))
+        if rc != 0:
+            raise RuntimeError(lib.last_error())
+        us = float(out[4])
+        alg_bytes = W.nbytes + 4 * n_in + 4 * n_out  # weights + fp32 x + fp32 y
+        return us, alg_bytes, float(out[0])
+
+    us, alg_bytes, us_ev = one(14336, 4096)
     gbs = alg_bytes / us / 1e3
+    us2, alg2, _ = one(4096, 14336)
+    gbs2 = alg2 / us2 / 1e3
     return {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
             "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": TRAFFIC_BYTES,
             "kernel": "k_dq<8,1,false> (W 14336x4096 Q4_K, fp32 x, 10 rotating copies)",
             "alg_bytes_per_launch": alg_bytes, "us_per_launch": round(us, 3),
-            "us_per_launch_event_pairs": round(float(out[0]), 3)}
+            "us_per_launch_event_pairs": round(us_ev, 3),
+            "other_shape": {"shape": "4096x14336", "kernel": "k_dq<16,1,false> (W 4096x14336 Q4_K, fp32 x)",
+                            "alg_bytes_per_launch": alg2, "us_per_launch": round(us2, 3),
+                            "achieved": round(gbs2, 1), "frac": round(gbs2 / PEAK_HBM_GBS, 4)}}
 
 
 def q8k_gemv_configs1(lib, n_copies=10, iters=200):
@@ -92,10 +103,14 @@ def q8k_gemv_configs1(lib, n_copies=10, iters=200):
                 raise RuntimeError(lib.last_error())
             alg = W.nbytes + nvec * (n_in // 256) * 292 + 4 * nvec * n_out
             us = float(o[0])
-            out[f"{n_out}x{n_in}_bs{nvec}"] = {
-                "us_per_launch": round(us, 3), "GB_s": round(alg / us / 1e3, 1),
-                "frac_of_peak": round(alg / us / 1e3 / PEAK_HBM_GBS, 4),
-                "us_quantize_plus_gemv": round(float(o[1]), 3), "alg_bytes": alg}
+            rec = {"us_per_launch": round(us, 3), "GB_s": round(alg / us / 1e3, 1),
+                   "frac_of_peak": round(alg / us / 1e3 / PEAK_HBM_GBS, 4),
+                   "us_quantize_plus_gemv": round(float(o[1]), 3), "alg_bytes": alg}
+            if nvec == 1 and o[2] > 0:
+                # the fp32-x path draco_gemv_q8k_f32 runs for rows up to 4096 wide:
+                # one launch that quantizes x itself
+                rec["us_fp32_x_fused"] = round(float(o[2]), 3)
+            out[f"{n_out}x{n_in}_bs{nvec}"] = rec
     return out
 
 
@@ -588,7 +603,8 @@ def main():
 
     if args.roofline_only:
         roof = q4k_gemv_roofline(lib)
-        log(f"Q4_K GEMV 14336x4096: {roof['us_per_launch']} us/launch, {roof['achieved']} GB/s")
+        log(f"Q4_K GEMV 14336x4096: {roof['us_per_launch']} us/launch, {roof['achieved']} GB/s; 4096x14336: "
+            f"{roof['other_shape']['us_per_launch']} us/launch, {roof['other_shape']['achieved']} GB/s")
         q8 = q8k_gemv_configs1(lib)
         for k, v in q8.items():
             log(f"Q4_K x Q8_K GEMV {k}: {v['us_per_launch']} us, {v['GB_s']} GB/s")
@@ -669,7 +685,8 @@ def main():
     roof = q8 = moe = shx = gdn = pre = qw = None
     if not args.no_roofline:
         roof = q4k_gemv_roofline(lib)
-        log(f"Q4_K GEMV 14336x4096: {roof['us_per_launch']} us/launch, {roof['achieved']} GB/s")
+        log(f"Q4_K GEMV 14336x4096: {roof['us_per_launch']} us/launch, {roof['achieved']} GB/s; 4096x14336: "
+            f"{roof['other_shape']['us_per_launch']} us/launch, {roof['other_shape']['achieved']} GB/s")
         q8 = q8k_gemv_configs1(lib)
         for k, v in q8.items():
             log(f"Q4_K x Q8_K GEMV {k}: {v['us_per_launch']} us, {v['GB_s']} GB/s")

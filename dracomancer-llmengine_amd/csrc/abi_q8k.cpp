@@ -90,14 +90,18 @@ int draco_gemv_q8k_f32(int code, const float* x, int nvec, const uint8_t* W, int
     if (!dx || !dq || !dy) return -2;
     hipStream_t st = stream();
     DRACO_HIP(hipMemcpyAsync(dx, x, sizeof(float) * (size_t)n_in * nvec, hipMemcpyHostToDevice, st));
-    // the quantizer writes the GEMV's image of the blocks (same values)
-    if (draco_q8k_quantize_launch(dx, n_in, nvec, dq, st, true)) return fail(-1, "q8k quantize launch rejected");
     Q8Launch a = {};
     a.base = m->dev;
     a.L = m->L;
     a.n_in = n_in;
-    a.xq = dq;
-    a.img = true;
+    if (nvec == 1 && draco_gemv_q8k_fused_ok(code, n_in)) {
+        a.xf = dx;  // one vector: the GEMV launch quantizes it itself
+    } else {
+        // the quantizer writes the GEMV's image of the blocks (same values)
+        if (draco_q8k_quantize_launch(dx, n_in, nvec, dq, st, true)) return fail(-1, "q8k quantize launch rejected");
+        a.xq = dq;
+        a.img = true;
+    }
     a.y = dy;
     a.y_stride = n_out;
     if (draco_gemv_q8k_launch(a, nvec, false, st)) return fail(-1, "q8k gemv launch rejected");
@@ -188,13 +192,26 @@ int draco_bench_gemv_q8k(int code, const uint8_t* W, int n_out, int n_in, int nv
     hipEvent_t e0, e1;
     DRACO_HIP(hipEventCreate(&e0));
     DRACO_HIP(hipEventCreate(&e1));
-    for (int mode = 0; mode < 2; mode++) {
+    auto gemv_fx = [&](int i) {  // as draco_gemv_q8k_f32 at nvec 1: the GEMV quantizes x itself
+        Q8Launch a = {};
+        a.base = dev[i % n_copies];
+        a.L = L;
+        a.n_in = n_in;
+        a.xf = dx;
+        a.y = dy;
+        a.y_stride = n_out;
+        return draco_gemv_q8k_launch(a, 1, false, st);
+    };
+    out[2] = 0.f;
+    const bool fx = nvec == 1 && draco_gemv_q8k_fused_ok(code, n_in);
+    for (int mode = 0; mode < (fx ? 3 : 2); mode++) {
         hipGraph_t graph;
         hipGraphExec_t exec;
         DRACO_HIP(hipStreamBeginCapture(st, hipStreamCaptureModeRelaxed));
         for (int i = 0; i < iters; i++) {
             if (mode == 1) draco_q8k_quantize_launch(dx, n_in, nvec, dq, st, true);
-            gemv(i);
+            if (mode == 2) gemv_fx(i);
+            else gemv(i);
         }
         DRACO_HIP(hipStreamEndCapture(st, &graph));
         DRACO_HIP(hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0));

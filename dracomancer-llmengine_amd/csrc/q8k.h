@@ -13,6 +13,8 @@ struct Q8Launch {
     const uint8_t* xq;    // nvec * (n_in/256) Q8_K blocks, vector-major (device);
                           // with img: the GEMV image of those blocks (below)
     bool img;
+    const float* xf;      // optional (nvec 1, not img / isums): fp32 x, quantized to
+                          // Q8_K inside the GEMV launch (xq unused)
     float* y;             // y[v * y_stride + row]
     int y_stride;
     int row0, row1;       // rows computed (row1 == 0: n_out)
@@ -36,3 +38,9 @@ int draco_gemv_q8k_launch(Q8Launch& a, int nvec, bool isums, hipStream_t st);
 // Q8_K image of x and the block's reduction space fit the CU's 160 KiB of
 // LDS), checked before anything is enqueued.
 int draco_gemv_q8k_shape_ok(int code, int n_in, int nvec, bool img, bool isums);
+// Whether one vector of rows n_in wide can be quantized inside the GEMV
+// launch (Q8Launch.xf): the block's half-waves cover the row's super-blocks
+// in one pass (n_in <= 4096 at 8 waves, 8192 at 16).  Longer rows measured
+// slower fused than as a quantizer launch plus the GEMV (4096x14336:
+// 14.5 us against 10.6 us).
+int draco_gemv_q8k_fused_ok(int code, int n_in);

@@ -91,7 +91,14 @@ __global__ __launch_bounds__(256) void k_q8k_quantize(const float* __restrict__ 
 // write each (row, super-block)'s integer sums (NB == 1).  IMG: xq is the
 // GEMV image (q8 [NB][n_in], bsums [nb][NB][16] f16, d [nb][NB]), which is
 // the LDS layout itself, so the prologue is a flat 16-byte copy; otherwise
-// the prologue scatters the Q8_K blocks into that layout.
+// the prologue scatters the Q8_K blocks into that layout.  QX (NB == 1):
+// a.xf is the fp32 vector and the prologue quantizes it into the image
+// itself, with k_q8k_quantize's operations (so the bytes are the same):
+// 32 threads per super-block, 8 consecutive values each; the first index of
+// the largest |x| by am_merge within the thread and across the 32 lanes, the
+// signed maximum from its lane by a sum of one non-zero term, the group sums
+// of 16 values over two lanes.  One launch instead of two (the quantizer's
+// launch and its dependency).
 //
 // Per item (16 rows x one super-block) and lane (row j, lane group g) the
 // int8 MFMAs give the exact group dots C of the lane's four groups with every
@@ -116,8 +123,9 @@ __device__ __forceinline__ uint32_t pk_h2(float a, float b) {
            ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)b) << 16);
 }
 
-template <int NW, int FM, int NB, bool ISUMS, bool IMG>
+template <int NW, int FM, int NB, bool ISUMS, bool IMG, bool QX = false>
 __global__ __launch_bounds__(64 * NW) void k_dq8(const Q8Launch a) {
+    static_assert(!QX || (NB == 1 && !IMG && !ISUMS), "the in-block quantizer serves one vector");
     extern __shared__ __align__(16) uint8_t smem[];
     constexpr int NT = 64 * NW, NH = NB >= 4 ? NB / 4 : 1;
     const int n_in = a.n_in, nb = n_in >> 8;
@@ -154,7 +162,68 @@ __global__ __launch_bounds__(64 * NW) void k_dq8(const Q8Launch a) {
         uint4* dst = reinterpret_cast<uint4*>(smem);
         for (int i = tid; i < n16; i += NT) dst[i] = src[i];
     }
-    const int ndw = IMG ? 0 : NB * nb * (Q8K_BLOCK_BYTES / 4);
+    if constexpr (QX) {
+        constexpr int SPP = NT / 32;                 // super-blocks per pass
+        constexpr int MP = (64 + SPP - 1) / SPP;     // passes for rows of up to 64 super-blocks (16384 values)
+        const int l32 = tid & 31;
+        // every pass's x requested before the first wait (clamped super-block)
+        float4 u[2 * MP];
+#pragma unroll
+        for (int p = 0; p < MP; p++) {
+            if (p * SPP >= nb) break;  // uniform
+            const int b = p * SPP + tid / 32, bc = b < nb ? b : nb - 1;
+            const float* xp = a.xf + (size_t)bc * 256 + l32 * 8;
+            u[2 * p] = ld4(xp);
+            u[2 * p + 1] = ld4(xp + 4);
+        }
+#pragma unroll
+        for (int p = 0; p < MP; p++) {
+            if (p * SPP >= nb) break;
+            const int b = p * SPP + tid / 32;  // whole half-waves past the end compute and discard
+            const float4 u0 = u[2 * p], u1 = u[2 * p + 1];
+            const float xv[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
+            float ax = fabsf(xv[0]);
+            int idx = l32 * 8;
+#pragma unroll
+            for (int k = 1; k < 8; k++) am_merge(ax, idx, fabsf(xv[k]), l32 * 8 + k);
+            group_argmax<32>(ax, idx);
+            float own = 0.f;  // the signed maximum, from the lane that holds it
+#pragma unroll
+            for (int k = 0; k < 8; k++)
+                if (idx == l32 * 8 + k) own = xv[k];
+            const float sown = group_sum<32>(own);  // every lane of the group active
+            const float mx = ax > 0.f ? sown : 0.f;
+            int q[8];
+            float d = 0.f;
+#pragma unroll
+            for (int k = 0; k < 8; k++) q[k] = 0;
+            if (mx != 0.f) {
+                const float iscale = -127.f / mx;
+#pragma unroll
+                for (int k = 0; k < 8; k++) {
+                    const int qq = (int)rintf(iscale * xv[k]);
+                    q[k] = qq < 127 ? qq : 127;
+                }
+                d = 1.f / iscale;
+            }
+            int part = 0;
+#pragma unroll
+            for (int k = 0; k < 8; k++) part += q[k];
+            const int gs = part + dpp<DPP_XOR1>(part);  // the 16 values of lanes 2m, 2m + 1
+            if (b < nb) {
+                uint32_t p0 = 0, p1 = 0;
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    p0 |= (uint32_t)(uint8_t)(int8_t)q[k] << (8 * k);
+                    p1 |= (uint32_t)(uint8_t)(int8_t)q[4 + k] << (8 * k);
+                }
+                *reinterpret_cast<uint2*>(q8 + (size_t)b * 256 + l32 * 8) = make_uint2(p0, p1);
+                if ((l32 & 1) == 0) bsf[(size_t)b * 16 + (l32 >> 1)] = __builtin_bit_cast(uint16_t, (_Float16)gs);
+                if (l32 == 0) d8[b] = d;
+            }
+        }
+    }
+    const int ndw = (IMG || QX) ? 0 : NB * nb * (Q8K_BLOCK_BYTES / 4);
     for (int i = tid; i < ndw; i += NT) {
         const int blk = i / (Q8K_BLOCK_BYTES / 4), k = i % (Q8K_BLOCK_BYTES / 4);
         const int v = blk / nb, b = blk % nb;
@@ -390,18 +459,21 @@ int cu_count() {
     return n;
 }
 
-template <int NW, int FM, int NB, bool IS, bool IMG>
+template <int NW, int FM, int NB, bool IS, bool IMG, bool QX = false>
 void launch_dq8i(const Q8Launch& a, int grid, size_t lds, hipStream_t st) {
     static std::once_flag once;
     std::call_once(once, [] {
-        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&k_dq8<NW, FM, NB, IS, IMG>),
+        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&k_dq8<NW, FM, NB, IS, IMG, QX>),
                                   hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
     });
-    hipLaunchKernelGGL((k_dq8<NW, FM, NB, IS, IMG>), dim3(grid), dim3(64 * NW), lds, st, a);
+    hipLaunchKernelGGL((k_dq8<NW, FM, NB, IS, IMG, QX>), dim3(grid), dim3(64 * NW), lds, st, a);
 }
 
 template <int NW, int FM, int NB, bool IS>
 void launch_dq8(const Q8Launch& a, int grid, size_t lds, hipStream_t st) {
+    if constexpr (NB == 1 && !IS) {
+        if (a.xf) return launch_dq8i<NW, FM, 1, false, false, true>(a, grid, lds, st);
+    }
     if (a.img && !IS) launch_dq8i<NW, FM, NB, false, true>(a, grid, lds, st);
     else launch_dq8i<NW, FM, NB, IS, false>(a, grid, lds, st);
 }
@@ -464,12 +536,21 @@ int draco_gemv_q8k_shape_ok(int code, int n_in, int nvec, bool img, bool isums) 
     return q8k_shape(code, n_in, nvec, img, isums, &nw, &lds) == 0;
 }
 
+int draco_gemv_q8k_fused_ok(int code, int n_in) {
+    int nw;
+    size_t lds;
+    return q8k_shape(code, n_in, 1, false, false, &nw, &lds) == 0 && n_in / 256 <= 2 * nw;
+}
+
 int draco_gemv_q8k_launch(Q8Launch& a, int nvec, bool isums, hipStream_t st) {
     const int code = a.L.code;
     const int n_in = a.n_in;
     int nw;
     size_t lds;
     if (n_in != a.L.n_in || q8k_shape(code, n_in, nvec, a.img, isums, &nw, &lds)) return -1;
+    // the in-block quantizer: one vector, plain GEMV, one pass of the block's
+    // half-waves over the row's super-blocks
+    if (a.xf && (nvec != 1 || isums || a.img || n_in / 256 > 2 * nw)) return -1;
     if (a.row1 <= 0) a.row1 = a.L.n_out;
     if (a.row0 < 0 || a.row1 > a.L.n_out || a.row0 >= a.row1) return -1;
     a.tile0 = a.row0 / 16;

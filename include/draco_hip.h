@@ -405,7 +405,9 @@ int draco_qwen_state_push(const void* layers, int n_layer, int rows);
 int draco_q8k_quantize(const float* x, int n, int nvec, uint8_t* out);
 /* y[v * n_out + r] for v < nvec, nvec in {1, 4, 8}; xq as above. */
 int draco_gemv_q8k(int code, const uint8_t* xq, int nvec, const uint8_t* W, int n_out, int n_in, float* y);
-/* x fp32 (nvec vectors of n_in), quantized to Q8_K on the device first. */
+/* x fp32 (nvec vectors of n_in), quantized to Q8_K on the device (one vector
+ * of rows up to 4096 wide: inside the GEMV launch, with the quantizer's
+ * operations; otherwise a quantizer launch first). */
 int draco_gemv_q8k_f32(int code, const float* x, int nvec, const uint8_t* W, int n_out, int n_in, float* y);
 /* Integer super-block sums of one vector: isc[r * nb + b], imn[r * nb + b]. */
 int draco_q8k_isums(int code, const uint8_t* xq, const uint8_t* W, int n_out, int n_in, int32_t* isc,
@@ -425,8 +427,11 @@ int draco_q8k_isums(int code, const uint8_t* xq, const uint8_t* W, int n_out, in
 int draco_gemv_q8k_f32_noalloc(int code, const float* x, int nvec, const uint8_t* W, int n_out, int n_in, float* y,
                                void* stream);
 size_t draco_noalloc_capacity(void);
-/* out[0] us per Q8_K GEMV launch, out[1] us per (quantize + GEMV) pair, both
- * from a graph replay of `iters` launches over n_copies weight copies. */
+/* out[0] us per Q8_K GEMV launch, out[1] us per (quantize + GEMV) pair,
+ * out[2] (nvec 1, rows up to 4096 wide; else 0) us per GEMV launch that
+ * quantizes fp32 x itself (what draco_gemv_q8k_f32 runs for one vector of
+ * such rows), all from a graph replay of `iters`
+ * launches over n_copies weight copies.  out holds 3 floats. */
 int draco_bench_gemv_q8k(int code, const uint8_t* W, int n_out, int n_in, int nvec, int n_copies, int iters,
                          float* out);
 

@@ -81,6 +81,43 @@ def test_gemv_q8k_vs_oracle(hip, oracle, code, n_out, n_in, nvec):
         assert np.array_equal(y2[v * n_out:(v + 1) * n_out], y[v * n_out:(v + 1) * n_out])
 
 
+@pytest.mark.parametrize("code", [4, 5])
+def test_gemv_q8k_f32_in_block_quantizer_edge_cases(hip, oracle, code):
+    """One vector through draco_gemv_q8k_f32 (the GEMV launch quantizes x
+    itself) equals the GEMV over the oracle's Q8_K bytes bit for bit on the
+    quantizer's edge cases: an all-zero super-block (d = 0), a largest |x|
+    held twice with opposite signs (the first index sets the sign), a negative
+    maximum, products exactly halfway between integers (round half to even)
+    and a value that clamps at 127."""
+    from dracohip import lib
+    n_out, n_in = 256, 1536
+    rng = np.random.default_rng(5)
+    W = lib.quantize(code, rng.standard_normal((n_out, n_in), dtype=np.float32) * np.float32(0.02))
+    x = rng.standard_normal(n_in).astype(np.float32)
+    x[256:512] = 0.0                                    # all zero
+    b = x[512:768]
+    b[:] = rng.uniform(-1, 1, 256).astype(np.float32)
+    b[10], b[200] = 3.0, -3.0                           # tie: +3 first
+    c = x[768:1024]
+    c[:] = rng.uniform(-1, 1, 256).astype(np.float32)
+    c[77], c[78] = -3.0, 3.0                            # tie: -3 first
+    d = x[1024:1280]
+    d[:] = np.arange(256, dtype=np.float32) % 64 - 31.5  # iscale * x = n + 0.5 for m = -127
+    d[5] = -127.0                                       # m = -127: iscale = 1
+    e = x[1280:1536]
+    e[:] = rng.uniform(-1, 1, 256).astype(np.float32)
+    e[3] = -1.5                                         # negative max: iscale > 0, x = +1.5 -> ... clamps
+    e[9] = 1.4999999
+    xq = oracle.quantize_q8k(x)
+    y = np.zeros(n_out, np.float32)
+    lib.check(hip.draco_gemv_q8k(code, lib.pu8(xq), 1, lib.pu8(W), n_out, n_in, lib.pf(y)), "draco_gemv_q8k")
+    y2 = np.zeros_like(y)
+    lib.check(hip.draco_gemv_q8k_f32(code, lib.pf(x), 1, lib.pu8(W), n_out, n_in, lib.pf(y2)),
+              "draco_gemv_q8k_f32")
+    assert np.array_equal(y, y2)
+    assert rel_err(y, oracle.gemv_q8k(code, xq, W, n_out, n_in)) <= TOL
+
+
 def test_gemv_q8k_rejects_bad_input(hip):
     from dracohip import lib
     W = np.zeros(144 * 4, np.uint8)
