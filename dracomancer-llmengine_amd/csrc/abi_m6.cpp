@@ -631,6 +631,23 @@ int plan_fusion(DevModel* m, hipStream_t st) {
 
 bool fused_o(const DevModel* m, int l) { return l >= 0 && l < (int)m->fo.size() && m->fo[l]; }
 
+// Whether MoE layer l's expert down launch leaves its two halves' sums
+// pending (split_out into w.pd), for layer l + 1's q/k/v launch to form
+// w.xm + half 0 + half 1: the MoE input is materialised in w.xm (a fused or
+// split-K o projection whose router stored it), the next layer's q/k/v are
+// all K-quants (the launch that takes the pending sum) and the down launch
+// serves the halves (an even number of experts, at most 16).  A 2048x768
+// down of 8 experts runs 256 blocks of 4 waves instead of 128 of 8.
+// draco_set_moe_split switches it (on by default).
+int g_moe_split = 1;
+bool moe_split(const DevModel* m, int l) {
+    if (!g_moe_split || l + 1 >= m->n_layer || !m->moe[l] || !draco_moe_layer_split_ok(m->moe[l])) return false;
+    if (!fused_o(m, l) && !ksplit_o(m, l)) return false;
+    const DevAttn* n = m->attn[l + 1];
+    auto kq = [](const DracoMat* x) { return x->L.code == DRACO_Q4_K || x->L.code == DRACO_Q6_K; };
+    return kq(n->wq) && kq(n->wk) && kq(n->wv);
+}
+
 // enqueue one llama layer on the device (x in w.x, updated in place; with
 // xin set the layer reads its input from xin and leaves its output in w.x):
 // qkv(+norm,+rope,+append), attention, merge, wo(+residual),
@@ -646,10 +663,12 @@ int enqueue_layer(DevModel* m, int l, float eps, hipStream_t st, const float* xi
     Work& w = m->w;
     const int H = m->h;
     const float* x0 = xin ? xin : w.x;
-    const bool pending = !xin && l > 0 && ksplit_down(m, l - 1);
+    const bool pending = !xin && l > 0 && (ksplit_down(m, l - 1) || moe_split(m, l - 1));
     // a pending input's materialised part: w.xm after a split-K or fused o
-    // projection (the previous layer's FFN input)
-    const float* xq = pending && (fused_o(m, l - 1) || ksplit_o_dense(m, l - 1)) ? w.xm : x0;
+    // projection (the previous layer's FFN input; for a split MoE layer
+    // always, moe_split requires it)
+    const float* xq =
+        pending && (fused_o(m, l - 1) || ksplit_o_dense(m, l - 1) || moe_split(m, l - 1)) ? w.xm : x0;
     if (int rc = enqueue_qkv(a, w, xq, 1, m->anorm[l], eps, m->state, l, st, pending)) return rc;
     const float* base = pending ? w.xs : x0;  // this layer's input
     const bool fo = fused_o(m, l);
@@ -665,7 +684,8 @@ int enqueue_layer(DevModel* m, int l, float eps, hipStream_t st, const float* xi
             return fail(-1, "attention o launch");
         if (m->moe[l])  // the router forms base + the o projection into w.xm (its norm input, the down's residual)
             return draco_moe_layer_enqueue(m->moe[l], base, m->fnorm[l], eps, w.x, nullptr, st,
-                                           reinterpret_cast<const float*>(acc), w.xm, true);
+                                           reinterpret_cast<const float*>(acc), w.xm, true,
+                                           moe_split(m, l) ? w.pd : nullptr);
         if (int rc = enqueue_gateup(f, w, base, 1, m->fnorm[l], eps, st, reinterpret_cast<const float*>(acc), w.xm, 8))
             return rc;
     } else if (dk_attention(w.q, a->kc, a->vc, w.part, w.cnt, w.att, m->state, l, a->NH, a->NKV, a->HD, a->max_t,
@@ -688,7 +708,10 @@ int enqueue_layer(DevModel* m, int l, float eps, hipStream_t st, const float* xi
         d.y = w.pd;
         d.epi = EPI_STORE;
         if (draco_seg_launch(s, st)) return fail(-1, "gemv o (split-K)");
-        return draco_moe_layer_enqueue(m->moe[l], base, m->fnorm[l], eps, w.x, nullptr, st, w.pd, w.xm);
+        // (the o partials in w.pd are consumed by the router before the
+        // down launch writes its halves there)
+        return draco_moe_layer_enqueue(m->moe[l], base, m->fnorm[l], eps, w.x, nullptr, st, w.pd, w.xm, false,
+                                       moe_split(m, l) ? w.pd : nullptr);
     }
     const bool kso = !fo && !m->moe[l] && ksplit_o_dense(m, l);
     if (fo) {
@@ -1411,6 +1434,13 @@ int draco_llama_generate(const void* layers_v, int n_layer, int h, float eps, co
 // on, the default; 0 = the split merge and the o projection as two launches).
 // Returns the previous setting; on < 0 only queries.  Captured decode graphs
 // are per call, so a change applies to the next call.
+int draco_set_moe_split(int on) {
+    std::lock_guard<std::recursive_mutex> g(api_mutex());
+    const int old = g_moe_split;
+    if (on >= 0) g_moe_split = on ? 1 : 0;
+    return old;
+}
+
 int draco_set_attn_o_fusion(int on) {
     std::lock_guard<std::recursive_mutex> g(api_mutex());
     const int old = g_attn_o_fusion;

@@ -130,7 +130,8 @@ int moe_work(MoeWork& w, int n_in, int n_exp, int n_used, int inter, int n_out) 
 // (RMSNorm with norm_w, eps), which the expert launches read
 int enqueue_moe(ExpertSet* s, const float* x, float* out, const float* resid, MoeWork& w, int n_exp, int n_used,
                 int inter, int n_in, int n_out, hipStream_t st, const float* norm_w = nullptr, float eps = 0.f,
-                float* xn = nullptr, const float* pend = nullptr, float* xs = nullptr, bool pend_fx = false) {
+                float* xn = nullptr, const float* pend = nullptr, float* xs = nullptr, bool pend_fx = false,
+                float* split_out = nullptr) {
     if (draco_moe_logits_launch(x, (const float*)s->router->dev, n_exp, n_in, w.logits, st, norm_w, eps, xn, pend,
                                 xs, pend_fx))
         return fail(-1, "moe router launch rejected");
@@ -152,8 +153,9 @@ int enqueue_moe(ExpertSet* s, const float* x, float* out, const float* resid, Mo
     if (draco_moe_grp_launch(a, s->fm_gu, true, false, true, st)) return fail(-1, "moe gate/up launch rejected");
     a.inter = inter;
     a.n_out = n_out;
-    a.out = out;
-    a.resid = resid;
+    a.out = split_out ? split_out : out;
+    a.resid = split_out ? nullptr : resid;
+    a.split = split_out ? 1 : 0;
     if (draco_moe_down_launch(a, s->fm_d, st)) return fail(-1, "moe down launch rejected");
     return 0;
 }
@@ -482,8 +484,11 @@ MoeLayer* draco_moe_layer(const DracoMoeP* p) {
 
 bool draco_moe_layer_pend_ok(const MoeLayer* m, const float* norm_w) { return m->snap.n_in <= 4096 && norm_w; }
 
+bool draco_moe_layer_split_ok(const MoeLayer* m) { return m->snap.n_used % 2 == 0 && m->snap.n_used <= 16; }
+
 int draco_moe_layer_enqueue(MoeLayer* m, const float* x, const float* norm_w, float eps, float* out,
-                            const float* resid, hipStream_t st, const float* pend, float* xs, bool pend_fx) {
+                            const float* resid, hipStream_t st, const float* pend, float* xs, bool pend_fx,
+                            float* split_out) {
     const DracoMoeP& p = m->snap;
     if (!draco_moe_layer_pend_ok(m, norm_w)) {  // wider than the router's norm prologue, or no norm weight
         if (pend) return fail(-1, "moe layer: a pending residual needs the router's RMSNorm prologue");
@@ -491,8 +496,9 @@ int draco_moe_layer_enqueue(MoeLayer* m, const float* x, const float* norm_w, fl
         return enqueue_moe(m->set, m->xn, out, resid, m->w, p.n_exp, p.n_used, p.inter, p.n_in, p.n_out, st);
     }
     if (pend && !xs) return fail(-1, "moe layer: a pending residual needs its sum buffer");
+    if (split_out && !draco_moe_layer_split_ok(m)) return fail(-1, "moe layer: %d experts cannot split", p.n_used);
     return enqueue_moe(m->set, x, out, resid, m->w, p.n_exp, p.n_used, p.inter, p.n_in, p.n_out, st, norm_w, eps,
-                       m->xn, pend, xs, pend_fx);
+                       m->xn, pend, xs, pend_fx, split_out);
 }
 
 int draco_moe_layer_enqueue_xn(MoeLayer* m, const float* xn, float* out, const float* resid, hipStream_t st) {

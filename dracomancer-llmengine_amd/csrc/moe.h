@@ -35,6 +35,7 @@ struct MoeArgs {
     int n_out;
     float* out;
     const float* resid;      // optional: out = resid + sum
+    int split;               // 1: two halves of the slots, sums to out[0..n_out) and out[n_out..2 n_out), no resid
 };
 
 // norm_w set (n_in <= 4096): x is normalised first, xn = (x * rms^-1) * norm_w
@@ -76,9 +77,14 @@ MoeLayer* draco_moe_layer(const DracoMoeP* p);
 // the router launch and stored to xs, which is then the residual (resid is
 // not read); pend needs the router's RMSNorm prologue
 // (draco_moe_layer_pend_ok).
+// With split_out ([2][n_out]; an even number of selected experts, at most
+// 16) the down launch writes the weighted sums of the two halves of the
+// slots there instead of out = resid + sum: the caller's consumer forms
+// resid + half 0 + half 1 (draco_moe_layer_split_ok).
 int draco_moe_layer_enqueue(MoeLayer* m, const float* x, const float* norm_w, float eps, float* out,
                             const float* resid, hipStream_t st, const float* pend = nullptr, float* xs = nullptr,
-                            bool pend_fx = false);
+                            bool pend_fx = false, float* split_out = nullptr);
+bool draco_moe_layer_split_ok(const MoeLayer* m);
 bool draco_moe_layer_pend_ok(const MoeLayer* m, const float* norm_w);
 // out = resid + MoE(xn) for an input that is already normalised (the qwen35
 // FFN input x2n, src/qwen35_engine.py:325)

@@ -427,14 +427,20 @@ __global__ __launch_bounds__(64 * NW) void k_moe_grp(const MoeArgs a) {
 // one 16-row output tile at a time; wave j (< n_used) = expert slot j, which
 // walks the nb super-blocks of its down rows over act_j's digits, three
 // super-blocks in flight; the first three are requested before act_j is
-// read and digitized.
-template <int NW, int FM>
+// read and digitized.  SPLIT: twice the blocks, block b = tile b % tiles of
+// half h = b / tiles, whose waves take slots h n/2 .. h n/2 + n/2 - 1 and
+// whose weighted sum (slot order) goes to out[h n_out + row], no residual:
+// the consumer forms resid + half 0 + half 1.
+template <int NW, int FM, bool SPLIT = false>
 __global__ __launch_bounds__(64 * NW) void k_moe_down(const MoeArgs a) {
     extern __shared__ __align__(16) uint8_t smem[];
     constexpr int NT = 64 * NW;
     constexpr size_t IB = FM == 1 ? DRACO_Q4T_ITEM : DRACO_Q6T_ITEM;
     const int inter = a.inter, nb = inter >> 8, ng = inter >> 4, n4 = inter >> 2;
-    const int n_used = a.n_slots;
+    const int tiles = a.n_out >> 4;
+    const int half = SPLIT ? (int)blockIdx.x / tiles : 0;
+    const int n_used = SPLIT ? a.n_slots / 2 : a.n_slots;  // this block's slots
+    const int so = half * n_used;                            // its first slot
     int8_t* xd = reinterpret_cast<int8_t*>(smem);                      // [n_used][ng][64]
     int8_t* zero = xd + (size_t)n_used * ng * 64;
     float2* xsm = reinterpret_cast<float2*>(zero + 1024);              // [n_used][ng]
@@ -443,10 +449,9 @@ __global__ __launch_bounds__(64 * NW) void k_moe_down(const MoeArgs a) {
 
     const int tid = threadIdx.x, lane = tid & 63, j = lane & 15, g = lane >> 4;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int tiles = a.n_out >> 4;
     const bool active = w < n_used;
     // this wave's expert base (routing published by k_moe_grp)
-    const uint8_t* base = a.seld[active ? w : 0];
+    const uint8_t* base = a.seld[so + (active ? w : 0)];
     // item b of tile t (b clamped: a repeated item is already in flight)
     auto ld = [&](int t, int b, Frag& f) {
         const uint8_t* p = base + ((size_t)t * nb + (b < nb ? b : nb - 1)) * IB;
@@ -464,15 +469,15 @@ __global__ __launch_bounds__(64 * NW) void k_moe_down(const MoeArgs a) {
         for (int k = 0; k < AB; k++) {
             const int i4 = b0 + tid + k * NT, ic = i4 < nvals4 ? i4 : nvals4 - 1;
             const int s = ic / n4, o = ic - s * n4;
-            av[k] = ld4(a.act + (size_t)s * inter + 4 * o);
+            av[k] = ld4(a.act + (size_t)(so + s) * inter + 4 * o);
         }
     };
     act_batch(0);
-    const float swv = a.selw[tid < n_used ? tid : n_used - 1];
+    const float swv = a.selw[so + (tid < n_used ? tid : n_used - 1)];
     // requested unconditionally (a wave past the used slots or a block past
     // the tiles re-reads real items), so the act waits above count exactly
     Frag P0, P1, P2;
-    int t = blockIdx.x;
+    int t = SPLIT ? (int)blockIdx.x - half * tiles : (int)blockIdx.x;
     {
         const int tl = t < tiles ? t : tiles - 1;
         ld(tl, 0, P0);
@@ -511,7 +516,7 @@ __global__ __launch_bounds__(64 * NW) void k_moe_down(const MoeArgs a) {
                     aD += dot_q6(f, xa, ms, b * 16 + gl6);
                 }
             };
-            const int tn = t + (int)gridDim.x;  // the next tile's first items follow this tile's last
+            const int tn = SPLIT ? tiles : t + (int)gridDim.x;  // the next tile's first items follow this tile's last
             for (int b = 0; b < nb; b += 3) {
                 dot(P0, b);
                 if (b + 3 < nb) ld(t, b + 3, P0);
@@ -536,9 +541,11 @@ __global__ __launch_bounds__(64 * NW) void k_moe_down(const MoeArgs a) {
             float o = 0.f;
             for (int s = 0; s < n_used; s++) o += swt[s] * red[s * 16 + tid];  // j order, like the reference
             const int row = t * 16 + tid;
-            a.out[row] = a.resid ? a.resid[row] + o : o;
+            if (SPLIT) a.out[(size_t)half * a.n_out + row] = o;
+            else a.out[row] = a.resid ? a.resid[row] + o : o;
         }
         lds_barrier();
+        if (SPLIT) break;  // one tile per block
     }
 }
 
@@ -593,11 +600,11 @@ void launch_grp(const MoeArgs& a, int grid, size_t lds, hipStream_t st) {
     hipLaunchKernelGGL((k_moe_grp<NW, FM, DUAL, XPER, ROUTE>), dim3(grid), dim3(64 * NW), lds, st, a);
 }
 
-template <int NW, int FM>
+template <int NW, int FM, bool SPLIT = false>
 void launch_down(const MoeArgs& a, int grid, size_t lds, hipStream_t st) {
     static std::once_flag once;
-    std::call_once(once, [] { allow_big_lds(&k_moe_down<NW, FM>); });
-    hipLaunchKernelGGL((k_moe_down<NW, FM>), dim3(grid), dim3(64 * NW), lds, st, a);
+    std::call_once(once, [] { allow_big_lds(&k_moe_down<NW, FM, SPLIT>); });
+    hipLaunchKernelGGL((k_moe_down<NW, FM, SPLIT>), dim3(grid), dim3(64 * NW), lds, st, a);
 }
 
 int grp_nw(int n_in) {
@@ -712,6 +719,25 @@ int moe_down_chunk(const MoeArgs& a, int fm, hipStream_t st) {
 // (out = ((resid + S_0..15) + S_16..31) + ...).
 int draco_moe_down_launch(MoeArgs& a, int fm, hipStream_t st) {
     if (a.inter % 256 || a.n_out % 16 || a.n_slots < 1 || a.n_slots > MOE_USED_MAX) return -1;
+    if (a.split) {
+        // two halves of the slots, one launch of twice the tiles; each half's
+        // weighted sum to out[h n_out ..] (no residual)
+        const int nh = a.n_slots / 2;
+        if (a.n_slots % 2 || nh > 8 || nh * (a.inter / 4) > 4096 * 4) return -1;
+        const int nw = nh <= 4 ? 4 : 8;
+        const size_t lds = (size_t)nh * (a.inter / 16) * 72 + 1024 + (size_t)nw * 16 * 4 + MOE_USED_MAX * 4;
+        if (lds > 160 * 1024) return -1;
+        const int grid = 2 * (a.n_out / 16);
+        if (nw == 4) {
+            if (fm == 1) launch_down<4, 1, true>(a, grid, lds, st);
+            else launch_down<4, 2, true>(a, grid, lds, st);
+        } else if (fm == 1) {
+            launch_down<8, 1, true>(a, grid, lds, st);
+        } else {
+            launch_down<8, 2, true>(a, grid, lds, st);
+        }
+        return 0;
+    }
     for (int c0 = 0; c0 < a.n_slots; c0 += 16) {
         MoeArgs c = a;
         c.n_slots = a.n_slots - c0 < 16 ? a.n_slots - c0 : 16;

@@ -152,6 +152,11 @@ int draco_set_prefill_chunk(int n);
  * dim 64, 32 q heads, K-quant o and gate/up) or run as two launches (0).
  * Returns the previous setting; on < 0 only queries. */
 int draco_set_attn_o_fusion(int on);
+/* No reference counterpart: MoE decode layers followed by a K-quant layer
+ * leave their expert down launch's two half sums pending for the next
+ * layer's q/k/v launch to add (1, the default) or add them with the residual
+ * themselves (0).  Returns the previous setting; on < 0 only queries. */
+int draco_set_moe_split(int on);
 
 /* ---- library utilities (no reference counterpart) ----------------------- */
 

@@ -427,18 +427,21 @@ def test_moe_stack_device_generate(use_graph):
     assert np.max(np.abs(hidden - g["hidden"])) <= hid_tol(g["hidden"])
 
 
-@pytest.mark.parametrize("fusion", [1, 0])
+@pytest.mark.parametrize("fusion,split", [(1, 1), (1, 0), (0, 1), (0, 0)])
 @pytest.mark.parametrize("use_graph", [False, True])
-def test_moe_stack_attn_o_fusion(fusion, use_graph):
+def test_moe_stack_attn_o_fusion(fusion, split, use_graph):
     """configs[3]'s layer (attention 32 q / 4 kv x 128, Q6_K o of 16 chunks)
     with the attention split merge fused with the o projection (int64 fixed
     point into the MoE router's prologue) and with the two-launch form: both
     give the compiled reference's tokens and hidden state, in the device loop
-    and through the per-token drop-in path."""
+    and through the per-token drop-in path; with and without the first
+    layer's expert down leaving its two half sums pending for the second
+    layer's q/k/v launch."""
     from dracohip import lib
     g = golden("moe_tiny.npz")
     L = lib.load()
     old = L.draco_set_attn_o_fusion(fusion)
+    old_split = L.draco_set_moe_split(split)
     try:
         cfg, model, drv = _driver("moe-tiny")
         print(f"[decode] moe stack attn-o fusion {fusion} graph={use_graph}", flush=True)
@@ -452,6 +455,7 @@ def test_moe_stack_attn_o_fusion(fusion, use_graph):
         assert np.max(np.abs(h2 - g["hidden"])) <= hid_tol(g["hidden"])
     finally:
         L.draco_set_attn_o_fusion(old)
+        L.draco_set_moe_split(old_split)
 
 
 MOE_FUSED_SHAPES = [  # (q heads, kv heads, head dim, max_t): per-head HD 64; grouped HD 256; 64 splits at HD 128
