@@ -129,6 +129,8 @@ struct DevModel {
     std::vector<int> fo_prev;
     unsigned long long* oacc = nullptr;
     size_t oacc_stride = 0, oacc_n = 0;
+    // the longest cache (rows) a layer reaches in the current call
+    int call_rows = 0;
 };
 
 struct RopeTab {
@@ -558,6 +560,10 @@ bool ksplit_o_dense(const DevModel* m, int l) {
 // The attention split merge fused with the o projection (dk_attn_o), on by
 // default; draco_set_attn_o_fusion switches it.
 int g_attn_o_fusion = 1;
+// With it, Q8_0 layers whose caches stay within DK_ATT_SHORT_T rows in a call
+// run the whole attention inside the o projection (dk_attn_o8_short); on by
+// default, draco_set_attn_short switches it.
+int g_attn_short = 1;
 
 // Whether dense layer l's attention split merge rides on its o projection
 // (dk_attn_o: one launch fewer per layer) and the o projection's chunk sums
@@ -601,8 +607,10 @@ bool fused_o_shape(const DevModel* m, int l) {
 // launch, ran before), so every accumulator is zero when its layer starts,
 // call after call; fewer than two fused layers run unfused (a layer cannot
 // clear its own).  Called by every entry point before it enqueues layers.
-int plan_fusion(DevModel* m, hipStream_t st) {
+int plan_fusion(DevModel* m, hipStream_t st, int n_steps) {
     const int L = m->n_layer;
+    m->call_rows = 0;
+    for (int l = 0; l < L; l++) m->call_rows = std::max(m->call_rows, *m->attn[l]->snap.tlen + n_steps);
     m->fo.assign(L, 0);
     m->fo_prev.assign(L, -1);
     std::vector<int> ls;
@@ -673,15 +681,23 @@ int enqueue_layer(DevModel* m, int l, float eps, hipStream_t st, const float* xi
     const float* base = pending ? w.xs : x0;  // this layer's input
     const bool fo = fused_o(m, l);
     if (fo) {
-        // split partials, then their merge + the o projection into eight
-        // partials, which the gate/up launch adds to the input (into w.xm)
-        if (dk_attention_parts(w.q, a->kc, a->vc, w.part, m->state, l, a->NH, a->NKV, a->HD, a->max_t, a->scale,
-                               st))
-            return fail(-1, "attention launch");
+        // split partials, then their merge + the o projection into the int64
+        // accumulator, which the next launch adds to the input (into w.xm);
+        // Q8_0 layers with short caches run the whole attention inside the
+        // o projection's blocks (one launch)
         unsigned long long* acc = m->oacc + (size_t)l * m->oacc_stride;
         unsigned long long* zacc = m->oacc + (size_t)m->fo_prev[l] * m->oacc_stride;
-        if (dk_attn_o(w.part, a->NH, a->NKV, a->HD, a->max_t, *a->wo, acc, zacc, (int)m->oacc_stride, st))
-            return fail(-1, "attention o launch");
+        if (g_attn_short && a->wo->L.code == DRACO_Q8_0 && m->call_rows <= DK_ATT_SHORT_T) {
+            if (dk_attn_o8_short(w.q, a->kc, a->vc, m->state, l, a->NH, a->NKV, a->HD, a->scale,
+                                 std::min(m->call_rows, a->max_t), *a->wo, acc, zacc, (int)m->oacc_stride, st))
+                return fail(-1, "short attention o launch");
+        } else {
+            if (dk_attention_parts(w.q, a->kc, a->vc, w.part, m->state, l, a->NH, a->NKV, a->HD, a->max_t, a->scale,
+                                   st))
+                return fail(-1, "attention launch");
+            if (dk_attn_o(w.part, a->NH, a->NKV, a->HD, a->max_t, *a->wo, acc, zacc, (int)m->oacc_stride, st))
+                return fail(-1, "attention o launch");
+        }
         if (m->moe[l])  // the router forms base + the o projection into w.xm (its norm input, the down's residual)
             return draco_moe_layer_enqueue(m->moe[l], base, m->fnorm[l], eps, w.x, nullptr, st,
                                            reinterpret_cast<const float*>(acc), w.xm, true,
@@ -987,7 +1003,7 @@ int m6_forward_token(float* x, int h, float eps, int pos, const M6LayerDesc* lay
     if (int rc = ensure_init()) return report(rc, "m6_forward_token");
     DevModel* m = resolve_model(layers, n_layer, h);
     if (!m) return report(-1, "m6_forward_token");
-    if (int rc = plan_fusion(m, stream())) return report(rc, "m6_forward_token");
+    if (int rc = plan_fusion(m, stream(), 1)) return report(rc, "m6_forward_token");
     if (int rc = check_positions(m, pos, 1)) return report(rc, "m6_forward_token");
     hipStream_t st = stream();
     if (int rc = upload_state(m, pos, st)) return report(rc, "m6_forward_token");
@@ -1263,7 +1279,7 @@ int draco_llama_generate(const void* layers_v, int n_layer, int h, float eps, co
             return report(fail(-1, "prompt token id %d out of range", prompt[i]), "draco_llama_generate");
     DevModel* m = resolve_model(layers, n_layer, h);
     if (!m) return report(-1, "draco_llama_generate");
-    if (int rc = plan_fusion(m, stream())) return report(rc, "draco_llama_generate");
+    if (int rc = plan_fusion(m, stream(), n_prompt + n_gen)) return report(rc, "draco_llama_generate");
     const DracoMat* hm = get_mat(head_w, head_code, vocab, h);
     const DracoMat* em = get_mat(emb_w, emb_code, vocab, h);
     const float* nw = norm_dev(final_norm, h);
@@ -1434,6 +1450,13 @@ int draco_llama_generate(const void* layers_v, int n_layer, int h, float eps, co
 // on, the default; 0 = the split merge and the o projection as two launches).
 // Returns the previous setting; on < 0 only queries.  Captured decode graphs
 // are per call, so a change applies to the next call.
+int draco_set_attn_short(int on) {
+    std::lock_guard<std::recursive_mutex> g(api_mutex());
+    const int old = g_attn_short;
+    if (on >= 0) g_attn_short = on ? 1 : 0;
+    return old;
+}
+
 int draco_set_moe_split(int on) {
     std::lock_guard<std::recursive_mutex> g(api_mutex());
     const int old = g_moe_split;
@@ -1472,7 +1495,7 @@ int draco_llama_prefill(const void* layers_v, int n_layer, int h, float eps, con
         if (ids[i] < 0 || ids[i] >= vocab) return report(fail(-1, "token id %d out of range", ids[i]), "draco_llama_prefill");
     DevModel* m = resolve_model(layers, n_layer, h);
     if (!m) return report(-1, "draco_llama_prefill");
-    if (int rc = plan_fusion(m, stream())) return report(rc, "draco_llama_prefill");
+    if (int rc = plan_fusion(m, stream(), n)) return report(rc, "draco_llama_prefill");
     const DracoMat* em = get_mat(emb_w, emb_code, vocab, h);
     if (!em) return report(-1, "draco_llama_prefill");
     for (int l = 0; l < n_layer; l++) {

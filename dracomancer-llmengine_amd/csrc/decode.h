@@ -58,6 +58,14 @@ int dk_attention_parts(const float* q, const float* kc, const float* vc, float* 
 // (int64 fixed point; acc must start at zero), acc[n_out] set when a
 // contribution is not finite; zacc[0 .. zn) is cleared.  -1 for another
 // shape.
+// Short caches: the whole attention of every kv group fused with the Q8_0 o
+// projection (head dim 64, NH / NKV <= 4), for caches of at most tcap <= 128
+// rows (tcap also bounds the rows read: the call's longest cache); acc as
+// dk_attn_o.  -1 for another shape.
+constexpr int DK_ATT_SHORT_T = 128;
+int dk_attn_o8_short(const float* q, const float* kc, const float* vc, const int* state, int layer, int NH, int NKV,
+                     int HD, float scale, int tcap, const DracoMat& wo, unsigned long long* acc,
+                     unsigned long long* zacc, int zn, hipStream_t st);
 int dk_attn_o(const float* part, int NH, int NKV, int HD, int max_t, const DracoMat& wo, unsigned long long* acc,
               unsigned long long* zacc, int zn, hipStream_t st);
 // qwen35 full attention q/k head RMSNorm + rope (NH q heads, 2 k heads of 256).

@@ -643,6 +643,138 @@ __global__ __launch_bounds__(256) void k_attn_o8(const float* __restrict__ part,
     }
 }
 
+// Short caches (at most ATT_SHORT_T rows in this call): the whole attention of
+// kv group c runs inside every o-projection block of chunk c, with no splits
+// and no merge, and the Q8_0 o projection follows as in k_attn_o8 (one launch
+// instead of the split attention and k_attn_o8).  Each of the NKV chunks is
+// recomputed by its ceil(n_out / 32) row groups from L2-resident K / V rows
+// (the row groups of one chunk read the same rows).  Block b: chunk c = b % NC,
+// rows 32 (b / NC) .. + 31.  All loads are requested first: the o rows'
+// quants (lane (r, k) as k_attn_o8), the group's q (into LDS), K row t =
+// 32 w + lane / 2 for lane pair half lane & 1 (32 dims, 8 float4), V rows
+// t = w + 4 i (i < 32) at dim lane, every row index clamped below tcap.
+// Then: scores of the REP heads for the wave's K rows (a 2-lane sum; rows at
+// or past the cache length are -inf), softmax per head over the rows by wave
+// h (max, exp, sum; the probabilities unnormalised in LDS), P.V of each
+// wave's V rows for every head, the 4 waves' sums added in LDS and divided
+// by the head's sum.  Results agree with the split form to fp32 rounding.
+constexpr int ATT_SHORT_T = 128;
+
+template <int REP>
+__global__ __launch_bounds__(256) void k_attn_o8s(const float* __restrict__ q, const float* __restrict__ kc,
+                                                  const float* __restrict__ vc, const int* __restrict__ st, int layer,
+                                                  float scale, int tcap, const uint8_t* __restrict__ qs,
+                                                  const uint8_t* __restrict__ ds, int nb, int n_out, int NC,
+                                                  unsigned long long* __restrict__ acc,
+                                                  unsigned long long* __restrict__ zacc, int zn) {
+    constexpr int HD = 64, KB = 2 * REP;
+    __shared__ __align__(16) float qsh[REP * HD];
+    __shared__ float psh[REP][ATT_SHORT_T];
+    __shared__ float lsh[REP];
+    __shared__ __align__(16) float osh[4][REP][HD];
+    __shared__ __align__(16) float att[8 * 36];
+    const int b = blockIdx.x, c = b % NC, rb = b / NC;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, r = lane >> 3, k = lane & 7;
+    const int KD = NC * HD;  // NC = NKV: one chunk per kv group
+    // o rows' quants (as k_attn_o8)
+    const int row = rb * 32 + w * 8 + r, rc = row < n_out ? row : n_out - 1;
+    const int kcb = k < KB ? k : KB - 1;
+    const size_t blk = (size_t)rc * nb + (size_t)c * KB + kcb;
+    const uint4 q0 = ldnt4(qs + blk * 32), q1 = ldnt4(qs + blk * 32 + 16);
+    const uint16_t dh = *reinterpret_cast<const uint16_t*>(ds + blk * 2);
+    // the group's q (REP heads of 64): one float4 per thread of the first REP * 16
+    const int qi = tid < REP * 16 ? tid : 0;
+    const float4 qv4 = ld4(q + (size_t)c * REP * HD + 4 * qi);
+    // K: row tk = 32 w + lane / 2, dims 32 (lane & 1) .. + 31
+    const int tk = 32 * w + (lane >> 1), half = lane & 1;
+    const int tkc = tk < tcap ? tk : tcap - 1;
+    float4 kx[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) kx[i] = ld4(kc + (size_t)tkc * KD + c * HD + 32 * half + 4 * i);
+    // V: rows w + 4 i at dim lane
+    float vv[ATT_SHORT_T / 4];
+#pragma unroll
+    for (int i = 0; i < ATT_SHORT_T / 4; i++) {
+        const int t = w + 4 * i, tc = t < tcap ? t : tcap - 1;
+        vv[i] = vc[(size_t)tc * KD + c * HD + lane];
+    }
+    const int Tn = st[1 + layer] + 1;
+    __builtin_amdgcn_sched_barrier(0);  // every request before the first wait
+    for (int i = b * 256 + tid; i < zn; i += gridDim.x * 256) zacc[i] = 0ull;
+    if (tid < REP * 16) reinterpret_cast<float4*>(qsh)[tid] = qv4;
+    lds_barrier();
+    // scores of the wave's K rows for the REP heads
+    const bool kval = tk < Tn;
+#pragma unroll
+    for (int h = 0; h < REP; h++) {
+        const float4* qh = reinterpret_cast<const float4*>(qsh + h * HD + 32 * half);
+        float s = 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const float4 a = qh[i];
+            s = fmaf(a.x, kx[i].x, s);
+            s = fmaf(a.y, kx[i].y, s);
+            s = fmaf(a.z, kx[i].z, s);
+            s = fmaf(a.w, kx[i].w, s);
+        }
+        s = group_sum<2>(s);
+        if (half == 0) psh[h][tk] = kval ? s * scale : -INFINITY;
+    }
+    lds_barrier();
+    // softmax of head h over the rows (wave h; lanes hold rows lane, lane + 64)
+    if (w < REP) {
+        const float s0 = psh[w][lane], s1 = psh[w][lane + 64];
+        const float m = wave_max(fmaxf(s0, s1));
+        const float p0 = s0 == -INFINITY ? 0.f : expf(s0 - m), p1 = s1 == -INFINITY ? 0.f : expf(s1 - m);
+        const float l = wave_sum(p0 + p1);
+        psh[w][lane] = p0;
+        psh[w][lane + 64] = p1;
+        if (lane == 0) lsh[w] = l;
+    }
+    lds_barrier();
+    // P.V over the wave's V rows, every head
+    float o[REP];
+#pragma unroll
+    for (int h = 0; h < REP; h++) o[h] = 0.f;
+#pragma unroll
+    for (int i = 0; i < ATT_SHORT_T / 4; i++) {
+        const int t = w + 4 * i;
+        const float v = t < Tn ? vv[i] : 0.f;  // rows past the length may hold anything
+#pragma unroll
+        for (int h = 0; h < REP; h++) o[h] = fmaf(psh[h][t], v, o[h]);
+    }
+#pragma unroll
+    for (int h = 0; h < REP; h++) osh[w][h][lane] = o[h];
+    lds_barrier();
+    if (w < REP) {
+        const float sum = (osh[0][w][lane] + osh[1][w][lane]) + (osh[2][w][lane] + osh[3][w][lane]);
+        att[(2 * w + (lane >> 5)) * 36 + (lane & 31)] = sum * (1.f / lsh[w]);
+    }
+    lds_barrier();
+    // the o projection of the chunk (as k_attn_o8)
+    const float* xa = att + kcb * 36;
+    const uint32_t Q[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+    float d = 0.f;
+#pragma unroll
+    for (int dw = 0; dw < 8; dw++) {
+        const float4 x4 = *reinterpret_cast<const float4*>(xa + 4 * dw);
+        d = fmaf(sbyte_f(Q[dw], 0), x4.x, d);
+        d = fmaf(sbyte_f(Q[dw], 1), x4.y, d);
+        d = fmaf(sbyte_f(Q[dw], 2), x4.z, d);
+        d = fmaf(sbyte_f(Q[dw], 3), x4.w, d);
+    }
+    float v = k < KB ? h2f(dh) * d : 0.f;
+    v = group_sum<8>(v);
+    if (k == 0 && row < n_out) {
+        const float sv = v * 4294967296.f;  // 2^32
+        if (fabsf(sv) < 9.0e18f) {
+            atomicAdd(acc + row, (unsigned long long)(long long)rintf(sv));
+        } else {
+            atomicOr(acc + n_out, 1ull);
+        }
+    }
+}
+
 // qwen35 full attention, per-head RMSNorm over 256 dims and rope on the pairs
 // (t, t + 32), t < 32 (src/m6_layer.c:427-457).  Blocks 0..NH-1 normalise q
 // head b from QG[b * 512 .. + 256] into Qr[b * 256] as (x * r) * q_norm; blocks
@@ -986,6 +1118,27 @@ int dk_attn_o(const float* part, int NH, int NKV, int HD, int max_t, const Draco
     }
 #undef AO_HD
 #undef AO_CASE
+    return 0;
+}
+
+int dk_attn_o8_short(const float* q, const float* kc, const float* vc, const int* state, int layer, int NH, int NKV,
+                     int HD, float scale, int tcap, const DracoMat& wo, unsigned long long* acc,
+                     unsigned long long* zacc, int zn, hipStream_t st) {
+    const int REP = NKV > 0 && NH % NKV == 0 ? NH / NKV : 0;
+    if (HD != 64 || REP < 1 || REP > 4 || tcap < 1 || tcap > ATT_SHORT_T || wo.L.code != DRACO_Q8_0 ||
+        wo.L.n_in != NH * 64 || wo.L.nb != 2 * NH)
+        return -1;
+    const dim3 grid(NKV * ((wo.L.n_out + 31) / 32)), block(256);
+    const uint8_t* qs = wo.dev + wo.L.off[0];
+    const uint8_t* ds = wo.dev + wo.L.off[1];
+#define AOS_CASE(R_)                                                                                            \
+    hipLaunchKernelGGL((k_attn_o8s<R_>), grid, block, 0, st, q, kc, vc, state, layer, scale, tcap, qs, ds, wo.L.nb, \
+                       wo.L.n_out, NKV, acc, zacc, zn)
+    if (REP == 1) AOS_CASE(1);
+    else if (REP == 2) AOS_CASE(2);
+    else if (REP == 3) AOS_CASE(3);
+    else AOS_CASE(4);
+#undef AOS_CASE
     return 0;
 }
 

@@ -157,6 +157,12 @@ int draco_set_attn_o_fusion(int on);
  * layer's q/k/v launch to add (1, the default) or add them with the residual
  * themselves (0).  Returns the previous setting; on < 0 only queries. */
 int draco_set_moe_split(int on);
+/* No reference counterpart: with the attention merge fused (above), Q8_0
+ * llama layers whose caches stay within 128 rows during a call run the whole
+ * attention inside the o projection's launch (1, the default) instead of a
+ * split attention launch before it (0).  Returns the previous setting; on < 0
+ * only queries. */
+int draco_set_attn_short(int on);
 
 /* ---- library utilities (no reference counterpart) ----------------------- */
 

@@ -150,12 +150,13 @@ def test_attn_o8_fusion_matches_oracle(oracle, shape, use_graph):
     ref = LlamaDriver(model, oracle_engine(oracle))
     rt, rh, _ = ref.greedy(model.prompt(), cfg.n_gen)
     L = lib.load()
-    for fusion in ([1, 0] if hidden == 960 else [1]):
+    for fusion, short in ([(1, 1), (1, 0), (0, 1)] if hidden == 960 else [(1, 1), (1, 0)]):
         old = L.draco_set_attn_o_fusion(fusion)
+        old_short = L.draco_set_attn_short(short)
         try:
             L.draco_reset()
             drv = LlamaDriver(model, hip_engine_lib())
-            print(f"[decode] q8 attn-o fusion {fusion} {shape} graph={use_graph}", flush=True)
+            print(f"[decode] q8 attn-o fusion {fusion} short {short} {shape} graph={use_graph}", flush=True)
             toks, hidden_dev, _ = drv.generate_device(model.prompt(), cfg.n_gen, use_graph=use_graph)
             assert toks == rt
             assert np.max(np.abs(hidden_dev - rh)) <= hid_tol(rh)
@@ -166,6 +167,36 @@ def test_attn_o8_fusion_matches_oracle(oracle, shape, use_graph):
             assert np.max(np.abs(h2 - rh)) <= hid_tol(rh)
         finally:
             L.draco_set_attn_o_fusion(old)
+            L.draco_set_attn_short(old_short)
+
+
+@pytest.mark.parametrize("dropin", [False, True])
+def test_attn_o8_short_to_split_crossing(oracle, dropin):
+    """configs[0]'s formats and head shape with a 120-token prompt and 16
+    greedy tokens: the per-token drop-in path runs the whole attention inside
+    the o projection while the cache holds at most 128 rows and the split
+    attention beyond; the device loop (whose call reaches 136 rows) runs the
+    split form throughout.  Greedy tokens equal the oracle engine's, hidden
+    state within the decode bar."""
+    import dataclasses
+    from tests_oracle_engine import oracle_engine
+    from dracohip import lib
+    cfg = dataclasses.replace(models.SMOL360M, name="q8-short-cross", n_layer=2, vocab=1024, n_prompt=120, n_gen=16,
+                              max_t=256)
+    model = models.build_llama(cfg, 44)
+    ref = LlamaDriver(model, oracle_engine(oracle))
+    rt, rh, _ = ref.greedy(model.prompt(), cfg.n_gen)
+    L = lib.load()
+    assert L.draco_set_attn_short(-1) == 1 and L.draco_set_attn_o_fusion(-1) == 1
+    L.draco_reset()
+    drv = LlamaDriver(model, hip_engine_lib())
+    print(f"[decode] q8 short/split crossing dropin={dropin}", flush=True)
+    if dropin:
+        toks, hidden_dev, _ = drv.greedy(model.prompt(), cfg.n_gen)
+    else:
+        toks, hidden_dev, _ = drv.generate_device(model.prompt(), cfg.n_gen, use_graph=True)
+    assert toks == rt
+    assert np.max(np.abs(hidden_dev - rh)) <= hid_tol(rh)
 
 
 def test_attn_o_fusion_is_deterministic():
