@@ -272,14 +272,19 @@ __global__ __launch_bounds__(256) void k_attn_any(const float* __restrict__ q, c
 // Each (q head, split) writes (o[HD], m, l) for k_attn_merge.
 constexpr int GQ_CH = 32;
 
-template <int HD, int REP>
-__global__ __launch_bounds__(256) void k_attn_gqa(const float* __restrict__ q, const float* __restrict__ kc,
-                                                  const float* __restrict__ vc, float* __restrict__ part,
-                                                  const int* __restrict__ st, int layer, int NKV, int nsplit,
-                                                  float scale) {
-    constexpr int DPL = HD / 64, HPT = REP * HD / 256, RPW = GQ_CH / 4;
+template <int HD, int REP, int NWV>
+__global__ __launch_bounds__(64 * NWV) void k_attn_gqa(const float* __restrict__ q, const float* __restrict__ kc,
+                                                       const float* __restrict__ vc, float* __restrict__ part,
+                                                       const int* __restrict__ st, int layer, int NKV, int nsplit,
+                                                       float scale) {
+    // NWV waves: scores take rows w, w + NWV, ...; for P.V the threads past
+    // the first 256 take further row ranges (RQ of them), whose sums meet in
+    // LDS after the last sub-chunk
+    constexpr int DPL = HD / 64, HPT = REP * HD / 256, RPW = GQ_CH / NWV, RQ = NWV / 4, RPQ = GQ_CH / RQ;
+    static_assert(NWV == 4 || NWV == 8 || NWV == 16, "4, 8 or 16 waves");
     __shared__ float sc[GQ_CH * REP];
     __shared__ float mrun[REP], lrun[REP], corr[REP];
+    __shared__ float ored[RQ > 1 ? (RQ - 1) * 256 * HPT : 1];
     const int g = blockIdx.x, s = blockIdx.y, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int KD = NKV * HD;
     const int Tn = st[1 + layer] + 1;
@@ -290,7 +295,7 @@ __global__ __launch_bounds__(256) void k_attn_gqa(const float* __restrict__ q, c
     for (int h = 0; h < REP; h++)
 #pragma unroll
         for (int e = 0; e < DPL; e++) qv[h][e] = q[(size_t)(g * REP + h) * HD + DPL * lane + e];
-    const int d = tid % HD, hg = tid / HD;
+    const int tb = tid & 255, rq = tid >> 8, d = tb % HD, hg = tb / HD;
     float o[HPT];
 #pragma unroll
     for (int i = 0; i < HPT; i++) o[i] = 0.f;
@@ -302,17 +307,18 @@ __global__ __launch_bounds__(256) void k_attn_gqa(const float* __restrict__ q, c
     const float* vg = vc + (size_t)g * HD + d;
     for (int c0 = t0; c0 < t1; c0 += GQ_CH) {
         const int nr = min(GQ_CH, t1 - c0);
-        // all loads of the sub-chunk first: K for this wave's rows, V for this thread's dim
+        // all loads of the sub-chunk first: K for this wave's rows, V for this
+        // thread's dim over its row range
         float kx[RPW][DPL];
 #pragma unroll
         for (int i = 0; i < RPW; i++) {
-            const int t = min(c0 + w + 4 * i, t1 - 1);
+            const int t = min(c0 + w + NWV * i, t1 - 1);
 #pragma unroll
             for (int e = 0; e < DPL; e++) kx[i][e] = kg[(size_t)t * KD + e];
         }
-        float vv[GQ_CH];
+        float vv[RPQ];
 #pragma unroll
-        for (int r = 0; r < GQ_CH; r++) vv[r] = vg[(size_t)min(c0 + r, t1 - 1) * KD];
+        for (int r = 0; r < RPQ; r++) vv[r] = vg[(size_t)min(c0 + rq * RPQ + r, t1 - 1) * KD];
         __builtin_amdgcn_sched_barrier(0);  // every request of the sub-chunk before the first wait
         // reduce-scatter over the heads: each stage halves the heads a lane
         // holds and pairs it (lane_flip) with a lane keeping the other half;
@@ -345,12 +351,12 @@ __global__ __launch_bounds__(256) void k_attn_gqa(const float* __restrict__ q, c
         for (int i = 0; i < RPW; i++) pd[i][0] = group_sum<64 / REP>(pd[i][0]);
 #pragma unroll
         for (int i = 0; i < RPW; i++) {
-            const int r = w + 4 * i;
+            const int r = w + NWV * i;
             if ((lane & (64 / REP - 1)) == 0) sc[r * REP + hs] = r < nr ? pd[i][0] * scale : -INFINITY;
         }
         lds_barrier();
-        // softmax: wave w takes heads 2w (lanes 0-31) and 2w+1 (lanes 32-63), then +8
-        for (int h = 2 * w + (lane >> 5); h < REP; h += 8) {
+        // softmax: wave w takes heads 2w (lanes 0-31) and 2w+1 (lanes 32-63), then + 2 NWV
+        for (int h = 2 * w + (lane >> 5); h < REP; h += 2 * NWV) {
             const int r = lane & 31;
             const float sv = sc[r * REP + h];
             const float cm = group_max<32>(sv);
@@ -370,11 +376,23 @@ __global__ __launch_bounds__(256) void k_attn_gqa(const float* __restrict__ q, c
 #pragma unroll
         for (int i = 0; i < HPT; i++) o[i] *= corr[hg * HPT + i];
 #pragma unroll
-        for (int r = 0; r < GQ_CH; r++) {
+        for (int r = 0; r < RPQ; r++) {
 #pragma unroll
-            for (int i = 0; i < HPT; i++) o[i] = fmaf(sc[r * REP + hg * HPT + i], vv[r], o[i]);
+            for (int i = 0; i < HPT; i++) o[i] = fmaf(sc[(rq * RPQ + r) * REP + hg * HPT + i], vv[r], o[i]);
         }
         lds_barrier();  // sc / corr / mrun are rewritten by the next sub-chunk
+    }
+    if (RQ > 1) {
+        if (rq > 0) {
+#pragma unroll
+            for (int i = 0; i < HPT; i++) ored[((rq - 1) * HPT + i) * 256 + tb] = o[i];
+        }
+        lds_barrier();
+        if (rq > 0) return;
+#pragma unroll
+        for (int j = 0; j < RQ - 1; j++)
+#pragma unroll
+            for (int i = 0; i < HPT; i++) o[i] += ored[(j * HPT + i) * 256 + tb];
     }
 #pragma unroll
     for (int i = 0; i < HPT; i++) part[((size_t)(g * REP + hg * HPT + i) * nsplit + s) * (HD + 2) + d] = o[i];
@@ -978,6 +996,17 @@ void dk_rope_append(float* q, const float* k, const float* v, float* kc, float* 
                        NKV, HD, rot);
 }
 
+// Waves per block of k_attn_gqa.  8 measured best on MI355X: configs[3]
+// (head dim 128, 8 q heads per kv head, 16 splits) 595 -> 601 tok/s against
+// 4 waves, configs[4] (head dim 256, 130 splits) within its spread; 16 no
+// better than 4.
+static int g_gqa_waves = 8;
+extern "C" int draco_set_gqa_waves(int n) {
+    const int old = g_gqa_waves;
+    if (n == 4 || n == 8 || n == 16) g_gqa_waves = n;
+    return old;
+}
+
 int dk_attention(const float* q, const float* kc, const float* vc, float* part, unsigned* count, float* out,
                  const int* state, int layer, int NH, int NKV, int HD, int max_t, float scale, hipStream_t st,
                  const float* gate, int gstride) {
@@ -994,8 +1023,15 @@ int dk_attention(const float* q, const float* kc, const float* vc, float* part, 
         const dim3 grid(NKV, nsplit);
 #define GQA_CASE(H_, R_)                                                                                  \
     if (HD == H_ && rep == R_) {                                                                          \
-        hipLaunchKernelGGL((k_attn_gqa<H_, R_>), grid, dim3(256), 0, st, q, kc, vc, part, state, layer, NKV, \
-                           nsplit, scale);                                                                \
+        if (g_gqa_waves == 16)                                                                            \
+            hipLaunchKernelGGL((k_attn_gqa<H_, R_, 16>), grid, dim3(1024), 0, st, q, kc, vc, part, state, \
+                               layer, NKV, nsplit, scale);                                                \
+        else if (g_gqa_waves == 8)                                                                        \
+            hipLaunchKernelGGL((k_attn_gqa<H_, R_, 8>), grid, dim3(512), 0, st, q, kc, vc, part, state,   \
+                               layer, NKV, nsplit, scale);                                                \
+        else                                                                                              \
+            hipLaunchKernelGGL((k_attn_gqa<H_, R_, 4>), grid, dim3(256), 0, st, q, kc, vc, part, state,   \
+                               layer, NKV, nsplit, scale);                                                \
     } else
         // the shapes attn_grouped sends here: head dim 128 with GQA <= 8
         // (llama attention) and head dim 256 with GQA <= 16 (qwen35 full
@@ -1035,8 +1071,15 @@ int dk_attention_parts(const float* q, const float* kc, const float* vc, float* 
         const dim3 grid(NKV, nsplit);
 #define GQA_CASE(H_, R_)                                                                                  \
     if (HD == H_ && rep == R_) {                                                                          \
-        hipLaunchKernelGGL((k_attn_gqa<H_, R_>), grid, dim3(256), 0, st, q, kc, vc, part, state, layer, NKV, \
-                           nsplit, scale);                                                                \
+        if (g_gqa_waves == 16)                                                                            \
+            hipLaunchKernelGGL((k_attn_gqa<H_, R_, 16>), grid, dim3(1024), 0, st, q, kc, vc, part, state, \
+                               layer, NKV, nsplit, scale);                                                \
+        else if (g_gqa_waves == 8)                                                                        \
+            hipLaunchKernelGGL((k_attn_gqa<H_, R_, 8>), grid, dim3(512), 0, st, q, kc, vc, part, state,   \
+                               layer, NKV, nsplit, scale);                                                \
+        else                                                                                              \
+            hipLaunchKernelGGL((k_attn_gqa<H_, R_, 4>), grid, dim3(256), 0, st, q, kc, vc, part, state,   \
+                               layer, NKV, nsplit, scale);                                                \
     } else
         GQA_CASE(128, 2) GQA_CASE(128, 4) GQA_CASE(128, 8)
         GQA_CASE(256, 2) GQA_CASE(256, 4) GQA_CASE(256, 8) GQA_CASE(256, 16) return -1;

@@ -882,6 +882,140 @@ __global__ __launch_bounds__(256) void k_seg(const SegKArgs a) {
     }
 }
 
+// Persistent Q8_0 GEMV for long single-segment launches (the vocabulary
+// head, store or argmax epilogue).  k_seg gives every block 8 rows, so the
+// head's 6144 blocks each repeat the x prologue for 2 KB of weights per wave;
+// here a block stages x (RMS-normalised when NORM) in LDS once and then takes
+// row groups gi = blockIdx.x, + gridDim.x, ... of 4 waves x RPW rows.  A
+// wave's lanes cover the (row, block) pairs p = lane + 64 k of its RPW rows
+// (PASSES passes); the next group's weights are requested before the current
+// group is dotted (loads clamped to real pairs, so they are unconditional and
+// in bounds).  Row dots, the 1/rms scaling and the argmax merge are k_seg's.
+template <int RPW, int PASSES, bool NORM>
+__global__ __launch_bounds__(256) void k_seg_rows(const SegKArgs a) {
+    using F = FQ80;
+    extern __shared__ float xsh[];
+    __shared__ float red[4];
+    __shared__ float amv[4];
+    __shared__ int ami[4];
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const SegK& s = a.seg[0];
+    const int n_out = s.n_out, U = s.nb, npair = RPW * U;
+    const int n_groups = (n_out + 4 * RPW - 1) / (4 * RPW);
+    const bool argmax = s.epi == EPI_ARGMAX;
+    auto load_group = [&](int gi, typename F::W (&w)[PASSES]) {
+        const int r0 = gi * 4 * RPW + wv * RPW;
+#pragma unroll
+        for (int k = 0; k < PASSES; k++) {
+            const int p0 = lane + 64 * k, p = p0 < npair ? p0 : npair - 1;
+            const int i = p / U, u = p - i * U;
+            w[k] = F::load(s, r0 + i < n_out ? r0 + i : n_out - 1, u);
+        }
+    };
+    int gi = blockIdx.x;
+    typename F::W cur[PASSES], nxt[PASSES];
+    load_group(gi < n_groups ? gi : n_groups - 1, cur);
+
+    // prologue as k_seg's: x (times the norm weight) into LDS with the sum of
+    // squares through one LDS-only barrier
+    const int n4 = a.n_in >> 2;
+    constexpr int XB = 4;
+    const float* nwp = a.norm_w ? a.norm_w : a.x;
+    float4 xv[XB], nv[XB];
+#pragma unroll
+    for (int q = 0; q < XB; q++) {
+        const int i4 = tid + q * 256, ic = i4 < n4 ? i4 : n4 - 1;
+        xv[q] = ld4(a.x + 4 * ic);
+        if (NORM) nv[q] = ld4(nwp + 4 * ic);
+    }
+    float ss = 0.f;
+    auto stage = [&](int i4, float4 v, const float4 w) {
+        if (NORM) {
+            ss = fmaf(v.x, v.x, ss);
+            ss = fmaf(v.y, v.y, ss);
+            ss = fmaf(v.z, v.z, ss);
+            ss = fmaf(v.w, v.w, ss);
+            if (a.norm_w) {
+                v.x *= w.x; v.y *= w.y; v.z *= w.z; v.w *= w.w;
+            }
+        }
+        *reinterpret_cast<float4*>(xsh + 4 * i4) = v;
+    };
+#pragma unroll
+    for (int q = 0; q < XB; q++)
+        if (tid + q * 256 < n4) stage(tid + q * 256, xv[q], nv[q]);
+    for (int i4 = tid + XB * 256; i4 < n4; i4 += 256) stage(i4, ld4(a.x + 4 * i4), NORM ? ld4(nwp + 4 * i4) : xv[0]);
+    float inv = 1.f;
+    if (NORM) {
+        ss = wave_sum(ss);
+        if (lane == 0) red[wv] = ss;
+    }
+    lds_barrier();  // LDS only: the weight loads above stay in flight
+    if (NORM) {
+        const float tot = (red[0] + red[1]) + (red[2] + red[3]);
+        inv = 1.f / sqrtf(tot / (float)a.n_in + a.eps);
+        if (a.xn_out && blockIdx.x == 0) {  // the normalised x, (x / rms) * w as the reference
+            for (int i4 = tid; i4 < n4; i4 += 256) {
+                float4 v = ld4(a.x + 4 * i4);
+                if (a.norm_w) {
+                    const float4 w = ld4(a.norm_w + 4 * i4);
+                    v.x = v.x * inv * w.x; v.y = v.y * inv * w.y; v.z = v.z * inv * w.z; v.w = v.w * inv * w.w;
+                } else {
+                    v.x *= inv; v.y *= inv; v.z *= inv; v.w *= inv;
+                }
+                *reinterpret_cast<float4*>(a.xn_out + 4 * i4) = v;
+            }
+        }
+    }
+
+    float am_v = -INFINITY;
+    int am_i = 0x7fffffff;
+    for (; gi < n_groups; gi += gridDim.x) {
+        const int gn = gi + (int)gridDim.x < n_groups ? gi + (int)gridDim.x : n_groups - 1;
+        load_group(gn, nxt);  // the last group re-requests itself: in bounds, unused
+        const int r0 = gi * 4 * RPW + wv * RPW;
+        float acc[RPW];
+#pragma unroll
+        for (int r = 0; r < RPW; r++) acc[r] = 0.f;
+#pragma unroll
+        for (int k = 0; k < PASSES; k++) {
+            const int p0 = lane + 64 * k, p = p0 < npair ? p0 : npair - 1;
+            const int i = p / U, u = p - i * U;
+            float xs[F::NX], sx[F::NS];
+            F::xslice(xsh, u, xs, sx);
+            const float d = F::dotw(cur[k], xs, sx);
+#pragma unroll
+            for (int r = 0; r < RPW; r++)
+                if (p0 < npair && r == i) acc[r] += d;
+        }
+#pragma unroll
+        for (int r = 0; r < RPW; r++) acc[r] = wave_sum(acc[r]) * inv;
+        if (lane == 0) {
+#pragma unroll
+            for (int r = 0; r < RPW; r++)
+                if (r0 + r < n_out) {
+                    s.y[r0 + r] = acc[r];
+                    am_merge(am_v, am_i, acc[r], r0 + r);
+                }
+        }
+#pragma unroll
+        for (int k = 0; k < PASSES; k++) cur[k] = nxt[k];
+    }
+    if (!argmax) return;
+    if (lane == 0) {
+        amv[wv] = am_v;
+        ami[wv] = am_i;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        float v = amv[0];
+        int idx = ami[0];
+        for (int i = 1; i < 4; i++) am_merge(v, idx, amv[i], ami[i]);
+        a.am_val[blockIdx.x] = v;
+        a.am_idx[blockIdx.x] = idx;
+    }
+}
+
 // Reduce the head's per-block argmax partials (np.argmax semantics: first
 // index of the maximum), write tokens[*cursor + 1] and advance the token
 // state.  With emb_out set, also decode the new token's embedding row into
@@ -1231,6 +1365,8 @@ void launch_seg(dim3 g, size_t shm, hipStream_t st, const SegKArgs& k) {
     }
 }
 
+int g_seg_rows = 2;  // blocks per CU of the persistent Q8_0 head kernel; 0: k_seg
+
 // Q8_0 segments (k_seg).
 int seg_launch_q8(SegLaunch& a, hipStream_t st) {
     // one row per wave for rows wider than 32 blocks when no segment needs
@@ -1274,6 +1410,32 @@ int seg_launch_q8(SegLaunch& a, hipStream_t st) {
     const SegKArgs k = seg_kargs(a, true);
     // passes of 64 (row, block) pairs per wave; the first NP preloaded
     const int passes = (R * (a.n_in / 32) + 63) / 64;
+    // long single-segment launches (the head): the persistent row-group kernel
+    const int n_out0 = a.seg[0].L.n_out;
+    if (g_seg_rows > 0 && a.nseg == 1 && (a.seg[0].epi == EPI_STORE || a.seg[0].epi == EPI_ARGMAX) &&
+        n_out0 >= 16384 && a.n_in <= 4096 && a.do_norm <= 1) {
+        constexpr int RPW = 8;
+        const int npair = RPW * (a.n_in / 32);
+        const int n_groups = (n_out0 + 4 * RPW - 1) / (4 * RPW);
+        const int grid = n_groups < 256 * g_seg_rows ? n_groups : 256 * g_seg_rows;
+        const dim3 gr(grid);
+        auto go = [&](void (*kern)(SegKArgs)) { hipLaunchKernelGGL(kern, gr, dim3(256), shm, st, k); };
+        if (npair <= 128) {
+            if (a.do_norm) go(k_seg_rows<RPW, 2, true>); else go(k_seg_rows<RPW, 2, false>);
+        } else if (npair <= 256) {
+            if (a.do_norm) go(k_seg_rows<RPW, 4, true>); else go(k_seg_rows<RPW, 4, false>);
+        } else if (npair <= 512) {
+            if (a.do_norm) go(k_seg_rows<RPW, 8, true>); else go(k_seg_rows<RPW, 8, false>);
+        } else {
+            goto plain;
+        }
+        if (a.seg[0].epi == EPI_ARGMAX)
+            hipLaunchKernelGGL(k_argmax_finalize, dim3(finalize_blocks(a.emb_out, a.emb_L.n_in)), dim3(256), 0, st,
+                               a.am_val, a.am_idx, grid, a.tokens, const_cast<int*>(a.cursor), a.advance_state,
+                               a.advance_layers, a.emb, a.emb_L, a.emb_out);
+        return 0;
+    }
+plain:
     if (R == 1) {
         if (passes <= 1) launch_seg1<false, 1, false, 1>(g, shm, st, k);
         else if (passes <= 2) launch_seg1<false, 2, false, 1>(g, shm, st, k);
@@ -1294,6 +1456,12 @@ int seg_launch_q8(SegLaunch& a, hipStream_t st) {
 }
 
 }  // namespace
+
+extern "C" int draco_set_seg_rows(int n) {
+    const int old = g_seg_rows;
+    if (n >= 0 && n <= 8) g_seg_rows = n;
+    return old;
+}
 
 int draco_dq_ksplit_waves(int n_in, int do_norm) {
     if (n_in <= 0 || n_in % 512) return 0;

@@ -163,6 +163,15 @@ int draco_set_moe_split(int on);
  * split attention launch before it (0).  Returns the previous setting; on < 0
  * only queries. */
 int draco_set_attn_short(int on);
+/* No reference counterpart: waves per block of the group-shared decode
+ * attention kernel (head dims 128 / 256): 4, 8 (the default) or 16; other
+ * values only query.  Returns the previous setting. */
+int draco_set_gqa_waves(int n);
+/* No reference counterpart: blocks per CU of the persistent Q8_0 GEMV that
+ * serves single-matrix launches of at least 16384 rows (the vocabulary
+ * head; 2, the default), or 0 for the 8-rows-per-block kernel.  Values
+ * outside 0..8 only query.  Returns the previous setting. */
+int draco_set_seg_rows(int n);
 
 /* ---- library utilities (no reference counterpart) ----------------------- */
 

@@ -393,41 +393,55 @@ def test_attn_op_long_cache_match_oracle(oracle, hd, nh, nkv, max_t, ocode):
     print(f"[attn_op] long cache hd {hd} nh {nh} nkv {nkv} max_t {max_t}: worst {worst:.2e}")
 
 
-@pytest.mark.parametrize("nh,nkv", [(4, 2), (8, 2), (32, 4)])
-def test_attn_op_grouped_head_dim_128_match_oracle(oracle, nh, nkv):
+GQA128_CASES = [  # (q heads, kv heads, cache capacity, first length, tokens, waves per block (0: default))
+    (4, 2, 256, 200, 40, 0), (8, 2, 256, 200, 40, 0), (32, 4, 256, 200, 40, 0),
+    (8, 2, 256, 200, 12, 4), (32, 4, 256, 200, 12, 16),
+    # 128 splits (the cap at 4 kv heads) of 64 rows: two sub-chunks per block
+    (16, 4, 8192, 8000, 8, 4), (16, 4, 8192, 8000, 8, 8), (16, 4, 8192, 8000, 8, 16)]
+
+
+@pytest.mark.parametrize("nh,nkv,max_t,t0,steps,waves", GQA128_CASES,
+                         ids=[f"{c[0]}q{c[1]}kv-t{c[2]}-w{c[5]}" for c in GQA128_CASES])
+def test_attn_op_grouped_head_dim_128_match_oracle(oracle, nh, nkv, max_t, t0, steps, waves):
     """The group-shared attention kernel at head dim 128 for every GQA ratio
-    m6_llama_attn_op sends to it (2, 4, 8): 40 tokens from a 200-row cache of
-    256 (8 splits) through m6_llama_attn_op, against the oracle after every
-    token."""
+    m6_llama_attn_op sends to it (2, 4, 8), in blocks of 4, 8 (the default)
+    and 16 waves: tokens from a cache filled to t0 rows through
+    m6_llama_attn_op, against the oracle after every token; at 8192 rows the
+    split count is capped, so every block runs two 32-row sub-chunks."""
     import dataclasses
     from tests_oracle_engine import oracle_engine
     from dracohip import lib
-    cfg = dataclasses.replace(models.TINY_Q8, name=f"gqa-128-{nh}-{nkv}", head_dim=128, n_head=nh, n_kv=nkv,
-                              hidden=256, max_t=256)
+    L0 = lib.load()
+    cfg = dataclasses.replace(models.TINY_Q8, name=f"gqa-128-{nh}-{nkv}-{max_t}", head_dim=128, n_head=nh, n_kv=nkv,
+                              hidden=256, max_t=max_t)
     model = models.build_llama(cfg, 1)
-    lib.load().draco_reset()
-    drv = LlamaDriver(model, hip_engine_lib())
-    ref = LlamaDriver(model, oracle_engine(oracle))
-    rng = np.random.default_rng(9)
-    kd = nkv * 128
-    rows = rng.standard_normal((2, 200 * kd), dtype=np.float32)
-    for d in (drv, ref):
-        d.kc[0][:rows.shape[1]] = rows[0]
-        d.vc[0][:rows.shape[1]] = rows[1]
-        d.tl[0][0] = 200
-    L = drv.engine.cdll
-    worst = 0.0
-    for step in range(40):
-        xn = rng.standard_normal(cfg.hidden, dtype=np.float32)
-        out = np.zeros(cfg.hidden, np.float32)
-        outr = np.zeros(cfg.hidden, np.float32)
-        print(f"[attn_op] grouped hd 128 nh {nh} nkv {nkv} step {step}", flush=True)
-        L.m6_llama_attn_op(pf(xn), drv.descs[0].attn_p, 200 + step, pf(out))
-        oracle.lib.or_llama_attn_op(pf(xn), ref.descs[0].attn_p, 200 + step, pf(outr))
-        e = rel_err(out, outr)
-        worst = max(worst, e)
-        assert e <= 1e-5, (step, e)
-    print(f"[attn_op] grouped hd 128 nh {nh} nkv {nkv}: worst {worst:.2e}")
+    L0.draco_reset()
+    old = L0.draco_set_gqa_waves(waves if waves else 8)
+    try:
+        drv = LlamaDriver(model, hip_engine_lib())
+        ref = LlamaDriver(model, oracle_engine(oracle))
+        rng = np.random.default_rng(9)
+        kd = nkv * 128
+        rows = rng.standard_normal((2, t0 * kd), dtype=np.float32)
+        for d in (drv, ref):
+            d.kc[0][:rows.shape[1]] = rows[0]
+            d.vc[0][:rows.shape[1]] = rows[1]
+            d.tl[0][0] = t0
+        L = drv.engine.cdll
+        worst = 0.0
+        for step in range(steps):
+            xn = rng.standard_normal(cfg.hidden, dtype=np.float32)
+            out = np.zeros(cfg.hidden, np.float32)
+            outr = np.zeros(cfg.hidden, np.float32)
+            print(f"[attn_op] grouped hd 128 nh {nh} nkv {nkv} max_t {max_t} waves {waves} step {step}", flush=True)
+            L.m6_llama_attn_op(pf(xn), drv.descs[0].attn_p, t0 + step, pf(out))
+            oracle.lib.or_llama_attn_op(pf(xn), ref.descs[0].attn_p, t0 + step, pf(outr))
+            e = rel_err(out, outr)
+            worst = max(worst, e)
+            assert e <= 1e-5, (step, e)
+    finally:
+        L0.draco_set_gqa_waves(old)
+    print(f"[attn_op] grouped hd 128 nh {nh} nkv {nkv} max_t {max_t} waves {waves}: worst {worst:.2e}")
 
 
 def test_moe_stack_dropin_per_token():

@@ -139,3 +139,61 @@ def test_all_nan_logits_give_token_zero(use_graph):
     toks, _, _ = drv.generate_device(model.prompt(), cfg.n_gen, use_graph=use_graph)
     assert toks == [0] * cfg.n_gen
     assert drv.tl[0][0] == cfg.n_prompt + cfg.n_gen - 1
+
+
+Q8_HEADS = [(960, 15, 5, 16403), (2048, 32, 8, 20000)]  # 30 / 64 Q8_0 blocks per row, ragged last row group
+
+
+def _q8_nan_rows(model, rows):
+    """Q8_0 head rows whose first block scale is the f16 NaN 0x7e00 (the
+    block's first two bytes): those logits are NaN, the others finite."""
+    buf, code = model.head()[:2]
+    assert code == models.Q8_0
+    rb = buf.nbytes // model.cfg.vocab
+    for r in rows:
+        buf[r * rb:r * rb + 2] = np.frombuffer(np.uint16(0x7E00).tobytes(), np.uint8)
+
+
+@pytest.mark.parametrize("hidden,nh,nkv,vocab", Q8_HEADS, ids=[f"h{s[0]}-v{s[3]}" for s in Q8_HEADS])
+def test_q8_head_row_groups_match_oracle(oracle, hidden, nh, nkv, vocab):
+    """Q8_0 heads of at least 16384 rows run the persistent row-group kernel
+    (x staged once per block, row groups of 32 rows): the per-token drop-in
+    path's logits within 1e-5 of the oracle engine's with the kernel on and
+    off (k_seg), greedy tokens equal; the device loop's fused argmax gives the
+    oracle engine's tokens, also with NaN rows in the head (the first NaN
+    wins, as np.argmax)."""
+    from tests_oracle_engine import oracle_engine
+    from dracohip import lib
+    L = lib.load()
+    cfg = dataclasses.replace(models.SMOL360M, name=f"q8-head-{hidden}-{vocab}", hidden=hidden, n_head=nh, n_kv=nkv,
+                              n_layer=2, n_ff=1024, vocab=vocab, tied=False, n_prompt=8, n_gen=6, max_t=64)
+    model = models.build_llama(cfg, 51)
+    ref = LlamaDriver(model, oracle_engine(oracle))
+    rt, _, rl = ref.greedy(model.prompt(), cfg.n_gen, collect_logits=(0, 3))
+    old = L.draco_set_seg_rows(-1)
+    try:
+        for rows in (2, 0):
+            L.draco_set_seg_rows(rows)
+            L.draco_reset()
+            drv = LlamaDriver(model, hip_engine_lib())
+            print(f"[shapes] q8 head h{hidden} v{vocab} seg_rows {rows}", flush=True)
+            toks, _, lg = drv.greedy(model.prompt(), cfg.n_gen, collect_logits=(0, 3))
+            assert toks == rt
+            for s in (0, 3):
+                assert rel_err(lg[s], rl[s]) <= 1e-5
+            L.draco_reset()
+            drv = LlamaDriver(model, hip_engine_lib())
+            toks, _, _ = drv.generate_device(model.prompt(), cfg.n_gen, use_graph=True)
+            assert toks == rt
+        _q8_nan_rows(model, (vocab - 5, 40))
+        ref = LlamaDriver(model, oracle_engine(oracle))
+        rt, _, _ = ref.greedy(model.prompt(), cfg.n_gen)
+        assert rt[0] == 40
+        L.draco_set_seg_rows(2)
+        L.draco_reset()
+        drv = LlamaDriver(model, hip_engine_lib())
+        print(f"[shapes] q8 head h{hidden} v{vocab} NaN rows", flush=True)
+        toks, _, _ = drv.generate_device(model.prompt(), cfg.n_gen, use_graph=True)
+        assert toks == rt
+    finally:
+        L.draco_set_seg_rows(old)
