@@ -14,6 +14,7 @@ CSRC = os.path.join(HERE, "csrc")
 LIBDIR = os.path.join(HERE, "lib")
 OBJDIR = os.path.join(HERE, "_build")
 LIB = os.path.join(LIBDIR, "libdraco_hip.so")
+TIMELINE_LIB = os.path.join(LIBDIR, "libdraco_hip_timeline.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = os.environ.get("DRACO_ARCH", "gfx950")
 
@@ -37,9 +38,10 @@ def _sources():
     return out
 
 
-def _compile(src):
-    obj = os.path.join(OBJDIR, os.path.basename(src) + ".o")
-    cmd = [HIPCC] + COMMON + DEVICE_CONTRACT + FILE_FLAGS.get(os.path.basename(src), []) + ["-c", src, "-o", obj]
+def _compile(src, objdir=OBJDIR, extra=()):
+    obj = os.path.join(objdir, os.path.basename(src) + ".o")
+    cmd = ([HIPCC] + COMMON + DEVICE_CONTRACT + FILE_FLAGS.get(os.path.basename(src), []) + list(extra) +
+           ["-c", src, "-o", obj])
     if src.endswith(".hip"):
         cmd[1:1] = ["-x", "hip"]
     r = subprocess.run(cmd, capture_output=True, text=True)
@@ -48,23 +50,29 @@ def _compile(src):
     return obj
 
 
-def build(verbose=False):
+def build(verbose=False, timeline=False):
+    """timeline: the profiling variant (-DDRACO_TIMELINE: per-wave stamps in
+    the roofline GEMV launch, read by timeline.py) as lib/libdraco_hip_timeline.so,
+    objects in _build_timeline/; the product library is not touched."""
+    lib = TIMELINE_LIB if timeline else LIB
+    objdir = OBJDIR + "_timeline" if timeline else OBJDIR
+    extra = ["-DDRACO_TIMELINE"] if timeline else []
     os.makedirs(LIBDIR, exist_ok=True)
-    os.makedirs(OBJDIR, exist_ok=True)
+    os.makedirs(objdir, exist_ok=True)
     srcs = _sources()
     with cf.ThreadPoolExecutor(max_workers=min(8, len(srcs))) as ex:
-        objs = list(ex.map(_compile, srcs))
-    tmp = LIB + ".tmp"
+        objs = list(ex.map(lambda f: _compile(f, objdir, extra), srcs))
+    tmp = lib + ".tmp"
     cmd = [HIPCC, "-shared", "-fPIC", f"--offload-arch={ARCH}", "-fopenmp", "-o", tmp] + objs
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stderr[-6000:]}")
-    os.replace(tmp, LIB)
+    os.replace(tmp, lib)
     if verbose:
-        print(f"[build] {LIB} ({os.path.getsize(LIB)} bytes) from {len(srcs)} sources")
-    return LIB
+        print(f"[build] {lib} ({os.path.getsize(lib)} bytes) from {len(srcs)} sources")
+    return lib
 
 
 if __name__ == "__main__":
-    build(verbose=True)
+    build(verbose=True, timeline="--timeline" in sys.argv[1:])
     sys.exit(0)

@@ -169,6 +169,19 @@ __device__ __forceinline__ auto seg_pick(const SegKArgs& a, int si, F f) -> decl
 // KS: split-K launch (one EPI_STORE segment, no prologue norm): tiles
 // [0, a.rot) multiply the first half of every row's super-blocks and store
 // to y, tiles [a.rot, 2 a.rot) the second half and store to y + a.kv_dim.
+// Per-wave timeline of the roofline launch (k_dq<8, 1, false, false, 0, 0,
+// ...>: one Q4_K segment, fp32 x, no prologue norm), compiled only with
+// -DDRACO_TIMELINE (build.py --timeline, timeline.py): lane 0 of each wave
+// stores s_memrealtime stamps (100 MHz) at the wave's start, x digitised in
+// LDS, after each of its first four items (the second and fourth end a tile,
+// with its reduction and store) and the end, plus its XCC id, into g_tl.
+// Product builds compile none of it.
+#ifdef DRACO_TIMELINE
+constexpr bool TL_BUILD = true;
+__device__ unsigned long long g_tl[1024 * 16 * 8];
+#else
+constexpr bool TL_BUILD = false;
+#endif
 constexpr int EPI_RT = -1, EPI_QKV = -2;
 // GD: the launch carries row dots (a.gdot, RMSNorm prologues only).
 template <int NW, int FM, bool DUAL, bool MULTI, int EPI, int NORM, bool IPT1, bool KS = false, bool GD = false>
@@ -183,6 +196,10 @@ __global__ __launch_bounds__(64 * NW) void k_dq(const SegKArgs a) {
 
     const int tid = threadIdx.x, lane = tid & 63, j = lane & 15, g = lane >> 4;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    constexpr bool TSON = TL_BUILD && NW == 8 && FM == 1 && !DUAL && !MULTI && NORM == 0 && !KS && !GD && EPI == 0 &&
+                          !IPT1;
+    unsigned long long ts0 = 0, ts1 = 0, ts2 = 0, ts3 = 0, ts4 = 0, ts5 = 0;
+    if (TSON) ts0 = __builtin_amdgcn_s_memrealtime();
     const int bx = blockIdx.x, G = gridDim.x;
     const int total = a.total_tiles;
     const int ipt = IPT1 ? 1 : (KS ? (nb >> 1) / NW : (nb + NW - 1) / NW);  // IPT1: one item per wave and tile
@@ -387,6 +404,7 @@ __global__ __launch_bounds__(64 * NW) void k_dq(const SegKArgs a) {
         }
         digits4(v, i4, xd, xsm);
     }
+    if (TSON) ts1 = __builtin_amdgcn_s_memrealtime();
     if (RMS) {
         ss = wave_sum(ss);
         if (GD && gr >= 0) gp = wave_sum(gp);
@@ -588,13 +606,36 @@ __global__ __launch_bounds__(64 * NW) void k_dq(const SegKArgs a) {
     };
     for (int i = 0; i < n_items; i += 2) {
         step(P0, P1, Q0, Q1);
+        if (TSON) {
+            const unsigned long long now = __builtin_amdgcn_s_memrealtime();
+            if (i == 0) ts2 = now;
+            if (i == 2) ts4 = now;
+        }
         if (i + 1 >= n_items) break;
         step(P1, P0, Q1, Q0);
+        if (TSON) {
+            const unsigned long long now = __builtin_amdgcn_s_memrealtime();
+            if (i == 0) ts3 = now;
+            if (i == 2) ts5 = now;
+        }
     }
     if ((EPI >= 0 ? EPI : (EPI == EPI_QKV ? EPI_ROPE_Q : a.seg[0].epi)) == EPI_ARGMAX && tid == 0) {
         a.am_val[bx] = am_v;
         a.am_idx[bx] = am_i;
     }
+#ifdef DRACO_TIMELINE
+    if (TSON) {
+        const unsigned long long ts6 = __builtin_amdgcn_s_memrealtime();
+        unsigned xcc;
+        asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+        if (lane == 0 && bx < 1024) {
+            unsigned long long* o = g_tl + ((size_t)bx * NW + w) * 8;
+            o[0] = ts0; o[1] = ts1; o[2] = ts2; o[3] = ts3; o[4] = ts4; o[5] = ts5; o[6] = ts6; o[7] = xcc;
+        }
+    }
+#else
+    (void)ts0; (void)ts1; (void)ts2; (void)ts3; (void)ts4; (void)ts5;
+#endif
 }
 
 // ------------------------------------------------------------------ Q8_0 --
@@ -1456,6 +1497,18 @@ plain:
 }
 
 }  // namespace
+
+#ifdef DRACO_TIMELINE
+// Timeline builds only: copy out / clear the stamps of the last roofline launch.
+extern "C" int draco_timeline_read(unsigned long long* host) {
+    return hipMemcpyFromSymbol(host, HIP_SYMBOL(g_tl), sizeof(unsigned long long) * 1024 * 16 * 8) == hipSuccess
+               ? 0 : -1;
+}
+extern "C" int draco_timeline_clear() {
+    static unsigned long long z[1024 * 16 * 8];
+    return hipMemcpyToSymbol(HIP_SYMBOL(g_tl), z, sizeof(z)) == hipSuccess ? 0 : -1;
+}
+#endif
 
 extern "C" int draco_set_seg_rows(int n) {
     const int old = g_seg_rows;
