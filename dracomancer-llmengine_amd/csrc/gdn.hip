@@ -306,6 +306,113 @@ __global__ __launch_bounds__(64 * NW) void k_gdn_scan(const GdnArgs a) {
         }
 }
 
+// Decode step (T = 1) with the gates' dots from the in-projection (a.glog),
+// without block barriers: 16 waves per V head (blockIdx.y * NW + w = wg),
+// wave wg owning columns 8 wg .. 8 wg + 7 in k_gdn_scan's lane layout (KQ = 8
+// lanes per column, 16 rows per lane), and every wave recomputing the conv +
+// silu + l2 norms of its q / k head's 256 channels itself (lane l: channels
+// l and l + 64 of q and of k; lanes 0-7 also its v column l's channel), so
+// no wave waits for another.  The normalised q / k pass between the lanes of
+// a wave through the wave's own LDS rows.  The per-element operations are
+// k_gdn_scan's; the l2 norms' sums of squares reduce in another tree order
+// (fp32 rounding).  Outputs as k_gdn_scan's split form: ON and the 16
+// per-wave sums of squares in PSS.  Tails: a v channel's by its wave, the
+// q / k channels' by wave 0 of V head h < nhq (as k_gdn_scan's split 0).
+template <int NW>
+__global__ __launch_bounds__(64 * NW) void k_gdn_dec(const GdnArgs a) {
+    constexpr int CPW = 8, KQ = 8, RPL = SV / KQ;
+    __shared__ float qk[NW][2 * SV];
+    __shared__ float cvs[NW][CPW];
+    const int h = blockIdx.x, lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int wg = blockIdx.y * NW + w;
+    const int NHQ = a.nhq, n_vh = a.n_vh;
+    const int j = h % NHQ;
+    // every load first: gates' dots, conv weights / tails / inputs of the 5
+    // channels, z, norm weight and the state slice
+    const float gdb = a.glog[h], gda = a.glog[n_vh + h];
+    int ch[5];
+    ch[0] = j * SV + lane;
+    ch[1] = ch[0] + 64;
+    ch[2] = NHQ * SV + j * SV + lane;
+    ch[3] = ch[2] + 64;
+    ch[4] = 2 * NHQ * SV + h * SV + CPW * wg + (lane & (CPW - 1));
+    float w0[5], w1[5], w2[5], w3[5], t0[5], t1[5], t2[5], xi[5];
+#pragma unroll
+    for (int r = 0; r < 5; r++) {
+        const float4 cw = ld4(a.conv + (size_t)ch[r] * 4);
+        w0[r] = cw.x;
+        w1[r] = cw.y;
+        w2[r] = cw.z;
+        w3[r] = cw.w;
+        t0[r] = a.tail[(size_t)ch[r] * 3];
+        t1[r] = a.tail[(size_t)ch[r] * 3 + 1];
+        t2[r] = a.tail[(size_t)ch[r] * 3 + 2];
+        xi[r] = a.QKV[ch[r]];
+    }
+    const int vl = lane / KQ, kq = lane % KQ, v = CPW * wg + vl;
+    float* Sh = a.S + (size_t)h * SV * SV;
+    const float nw = a.ssm_norm[v];
+    const float z = a.Z[(size_t)h * SV + v];
+    float s[RPL];
+#pragma unroll
+    for (int i = 0; i < RPL; i++) s[i] = Sh[(size_t)(RPL * kq + i) * SV + v];
+    float b, g;
+    GdnGates<NW>::gates_of(a, h, gdb, gda, &b, &g);
+    // (1) conv + silu (src/m6_gdn_scan.c:30-38), (2) the l2 norms of q and k
+    float c[5];
+#pragma unroll
+    for (int r = 0; r < 5; r++) {
+        const float acc = w0[r] * t0[r] + w1[r] * t1[r] + w2[r] * t2[r] + w3[r] * xi[r];
+        c[r] = silu(acc);
+    }
+    const float sqq = wave_sum(c[0] * c[0] + c[1] * c[1]);
+    const float sqk = wave_sum(c[2] * c[2] + c[3] * c[3]);
+    const float rq = sqrtf(sqq), rk = sqrtf(sqk);
+    const float iq = 1.f / (rq > EPS ? rq : EPS), ik = 1.f / (rk > EPS ? rk : EPS);
+    float* cq = qk[w];
+    float* ck = qk[w] + SV;
+    cq[lane] = c[0] * iq;
+    cq[lane + 64] = c[1] * iq;
+    ck[lane] = c[2] * ik;
+    ck[lane + 64] = c[3] * ik;
+    if (lane < CPW) cvs[w][lane] = c[4];
+    // the wave's own LDS rows: its writes ordered before its reads
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+    // (3) delta rule on this lane's 16 rows of column v
+    float sk = 0.f;
+#pragma unroll
+    for (int i = 0; i < RPL; i++) {
+        s[i] = s[i] * g;
+        sk = sk + s[i] * ck[RPL * kq + i];
+    }
+    sk = group_sum<KQ>(sk);
+    const float d = (cvs[w][vl] - sk) * b;
+    float o = 0.f;
+#pragma unroll
+    for (int i = 0; i < RPL; i++) {
+        s[i] = s[i] + ck[RPL * kq + i] * d;
+        o = o + s[i] * cq[RPL * kq + i];
+    }
+    o = group_sum<KQ>(o);
+    // (4) o / sqrt(128) and the wave's sum of squares for the gated rms
+    o = o * (1.f / sqrtf((float)SV));
+    const float o2 = wave_sum(kq == 0 ? o * o : 0.f);
+    if (kq == 0) a.ON[(size_t)h * SV + v] = a.defer_gnorm ? o * nw * silu(z) : o;
+    if (lane == 0) a.PSS[(size_t)h * GDN_PSS_STRIDE + wg] = o2;
+#pragma unroll
+    for (int i = 0; i < RPL; i++) Sh[(size_t)(RPL * kq + i) * SV + v] = s[i];
+    const bool own_qk = h < NHQ && wg == 0;
+#pragma unroll
+    for (int r = 0; r < 5; r++)
+        if (r == 4 ? lane < CPW : own_qk) {
+            a.tail[(size_t)ch[r] * 3] = t1[r];
+            a.tail[(size_t)ch[r] * 3 + 1] = t2[r];
+            a.tail[(size_t)ch[r] * 3 + 2] = xi[r];
+        }
+}
+
 // The gated rms of split scans, in place: for token t and V head h,
 // ON[t][h][v] = o * rsqrt(sum of the NP wave partials / 128 + eps) *
 // ssm_norm[v] * silu(Z[t][h][v]), the reference's order (src/m6_layer.c:
@@ -324,12 +431,19 @@ __global__ __launch_bounds__(128) void k_gdn_gnorm(const GdnArgs a) {
 
 // A split decode step leaves NSPL * NW = 16 partials (the ssm_out GEMV's
 // GNORM prologue reads 16); scans of several tokens use 8 waves per block.
+// k_gdn_dec's waves per block (1 or 2; 0: k_gdn_scan<true, 2, 8>)
+int g_dec_waves = 2;
+
 template <bool DEC>
 int launch_scan(const GdnArgs& a, int nspl, hipStream_t st) {
     if (nspl > 1 && !a.PSS) return -1;
     const dim3 g(a.n_vh, nspl);
     int np = 16;
-    if (DEC || nspl == 1) {
+    if (DEC && nspl == 8 && a.glog && g_dec_waves) {
+        // the barrier-free decode step: 16 waves per V head in blocks of 1 or 2
+        if (g_dec_waves == 1) hipLaunchKernelGGL(k_gdn_dec<1>, dim3(a.n_vh, 16), dim3(64), 0, st, a);
+        else hipLaunchKernelGGL(k_gdn_dec<2>, dim3(a.n_vh, 8), dim3(128), 0, st, a);
+    } else if (DEC || nspl == 1) {
         switch (nspl) {
         case 1: hipLaunchKernelGGL((k_gdn_scan<DEC, 8, 1>), g, dim3(512), 0, st, a); return 0;
         case 2: hipLaunchKernelGGL((k_gdn_scan<DEC, 8, 2>), g, dim3(512), 0, st, a); break;
@@ -375,6 +489,15 @@ int draco_gdn_split(bool decode) { return decode ? g_split_dec : g_split_scan; }
 // Blocks per V head of the GDN decode step and of multi-token scans (1, 2, 4
 // or 8; a negative argument keeps the setting).  Returns the previous values
 // as decode * 16 + scan.
+// Waves per block of the barrier-free GDN decode step (1 or 2), or 0 for
+// the split scan kernel's decode form; other values only query.  Returns the
+// previous value.
+extern "C" int draco_set_gdn_dec(int waves) {
+    const int old = g_dec_waves;
+    if (waves >= 0 && waves <= 2) g_dec_waves = waves;
+    return old;
+}
+
 extern "C" int draco_set_gdn_split(int decode_split, int scan_split) {
     const int old = g_split_dec * 16 + g_split_scan;
     auto ok = [](int n) { return n == 1 || n == 2 || n == 4 || n == 8; };

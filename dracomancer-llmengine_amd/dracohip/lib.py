@@ -64,6 +64,7 @@ SIGNATURES = {
     "draco_set_attn_short": (ct.c_int, [ct.c_int]),
     "draco_set_gqa_waves": (ct.c_int, [ct.c_int]),
     "draco_set_seg_rows": (ct.c_int, [ct.c_int]),
+    "draco_set_gdn_dec": (ct.c_int, [ct.c_int]),
     "draco_llama_prefill": (ct.c_int, [ct.c_void_p, ct.c_int, ct.c_int, ct.c_float, ct.c_void_p, ct.c_int, ct.c_int,
                                        i32p, ct.c_int, ct.c_int, f32p]),
     # qwen35 hybrid layers (src/m6_layer.c:189-518)

@@ -172,6 +172,11 @@ int draco_set_gqa_waves(int n);
  * head; 2, the default), or 0 for the 8-rows-per-block kernel.  Values
  * outside 0..8 only query.  Returns the previous setting. */
 int draco_set_seg_rows(int n);
+/* No reference counterpart: the GDN decode step at 8 blocks per V head with
+ * the gates' dots from the in-projection runs the barrier-free kernel in
+ * blocks of 1 or 2 (the default) waves, or (0) the split scan kernel's decode
+ * form.  Other values only query.  Returns the previous setting. */
+int draco_set_gdn_dec(int waves);
 
 /* ---- library utilities (no reference counterpart) ----------------------- */
 

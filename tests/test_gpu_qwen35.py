@@ -44,6 +44,23 @@ def test_gdn_attn_decode_split(hip, oracle, tag, split):
         hip.draco_set_gdn_split(old // 16, old % 16)
 
 
+@pytest.mark.parametrize("waves", [0, 1, 2])
+@pytest.mark.parametrize("tag", [c[0] for c in gg.QWEN_GDN_CASES])
+def test_gdn_attn_decode_step_kernels(hip, oracle, tag, waves):
+    """The decode step at 8 blocks per V head in the barrier-free kernel
+    (every wave recomputes its q / k head's conv and l2 norms; blocks of 1 or
+    2 waves) and in the split scan kernel's decode form (0): the compiled
+    reference's outputs, and the oracle's state and conv tail after the
+    case's tokens."""
+    old = hip.draco_set_gdn_dec(waves)
+    old_split = hip.draco_set_gdn_split(8, -1)
+    try:
+        _gdn_attn_case(hip, oracle, tag)
+    finally:
+        hip.draco_set_gdn_dec(old)
+        hip.draco_set_gdn_split(old_split // 16, old_split % 16)
+
+
 def _gdn_attn_case(hip, oracle, tag):
     from dracohip import qwen35 as Q
     g = golden("qwen35.npz")
