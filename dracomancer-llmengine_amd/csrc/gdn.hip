@@ -20,8 +20,8 @@
 // LDS and no barrier.  The conv runs on the block's threads, channel c =
 // tid + r * threads (q and k of head j in every block: the l2 norms need
 // them whole; v only for the block's columns), the tails in registers; only
-// the block that owns a channel writes its tail back (q/k channels: split 0
-// of a head with h < NHQ).  The l2 norms reduce across the block's waves
+// the block that owns a channel writes its tail back (q/k channels: the last
+// block of the head's readers to count itself in g_qk_cnt).  The l2 norms reduce across the block's waves
 // through LDS.  The gated rms needs all 128 columns of a head: with one
 // block per head (NW = 8) it is finished in the block; split across blocks,
 // each wave writes its columns' o / sqrt(128) to ON and the sum of their
@@ -43,6 +43,19 @@ namespace {
 
 constexpr int SV = 128;
 constexpr float EPS = 1e-6f;
+
+// The q / k channels of a q/k head's conv are read by every block (wave) of
+// each V head that uses the head and updated once.  The last reader writes
+// the new tails: each reader adds 1 to its head's counter here once its tail
+// loads have returned; the one that brings it to the number of readers
+// writes the tails and puts the counter back to 0 for the next launch.  A
+// fixed writer could overwrite a tail before a reader's queued load of it
+// had been served (the readers of a head run on the same XCD, so such a load
+// would hit the new value in L2).
+// One counter per q/k head, 4 KB apart: atomics on one line serialise.
+constexpr int QK_CNT_STRIDE = 1024;
+constexpr int QK_CNT_MAX = 64;  // q/k heads
+__device__ unsigned g_qk_cnt[QK_CNT_MAX * QK_CNT_STRIDE];
 
 __device__ __forceinline__ float silu(float a) { return a / (1.f + expf(-a)); }
 
@@ -174,7 +187,7 @@ __global__ __launch_bounds__(64 * NW) void k_gdn_scan(const GdnArgs a) {
         else if (c < CH) cc = 2 * NHQ * SV + h * SV + col0 + (c - 2 * SV);
         const bool live = c < CH;
         ch[r] = live ? cc : -1;
-        own[r] = c >= 2 * SV ? true : (h < NHQ && sp == 0);
+        own[r] = c >= 2 * SV;  // q / k channels: the head's last reader block (below)
         const float4 cw = ld4(a.conv + (size_t)cc * 4);
         const float ta = a.tail[(size_t)cc * 3], tb = a.tail[(size_t)cc * 3 + 1], tc = a.tail[(size_t)cc * 3 + 2];
         const float xi = a.QKV[cc];
@@ -198,6 +211,12 @@ __global__ __launch_bounds__(64 * NW) void k_gdn_scan(const GdnArgs a) {
     for (int i = 0; i < RPL; i++) s[i] = Sh[(size_t)(RPL * kq + i) * SV + v];
     const float scale = 1.f / sqrtf((float)SV);
 
+    // every load above (the tails among them) has returned: count this block
+    // as a reader of its q / k head's tails
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __shared__ unsigned qk_prev;
+    unsigned prev = 0;  // thread 0's; passed on after the token loop, so its round trip overlaps the scan
+    if (tid == 0) prev = __hip_atomic_fetch_add(&g_qk_cnt[j * QK_CNT_STRIDE], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     float gin = 0.f, bin = 0.f;
     if constexpr (DEC) {
         if (a.glog) GdnGates<NW>::gates_of(a, h, gdb, gda, &bin, &gin);
@@ -297,9 +316,13 @@ __global__ __launch_bounds__(64 * NW) void k_gdn_scan(const GdnArgs a) {
     }
 #pragma unroll
     for (int i = 0; i < RPL; i++) Sh[(size_t)(RPL * kq + i) * SV + v] = s[i];
+    if (tid == 0) qk_prev = prev;
+    lds_barrier();
+    const bool last = qk_prev + 1 == (unsigned)(NSPL * ((n_vh - 1 - j) / NHQ + 1));
+    if (last && tid == 0) __hip_atomic_store(&g_qk_cnt[j * QK_CNT_STRIDE], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 #pragma unroll
     for (int r = 0; r < R; r++)
-        if (ch[r] >= 0 && own[r]) {
+        if (ch[r] >= 0 && (own[r] || last)) {
             a.tail[(size_t)ch[r] * 3] = t0[r];
             a.tail[(size_t)ch[r] * 3 + 1] = t1[r];
             a.tail[(size_t)ch[r] * 3 + 2] = t2[r];
@@ -317,7 +340,7 @@ __global__ __launch_bounds__(64 * NW) void k_gdn_scan(const GdnArgs a) {
 // k_gdn_scan's; the l2 norms' sums of squares reduce in another tree order
 // (fp32 rounding).  Outputs as k_gdn_scan's split form: ON and the 16
 // per-wave sums of squares in PSS.  Tails: a v channel's by its wave, the
-// q / k channels' by wave 0 of V head h < nhq (as k_gdn_scan's split 0).
+// q / k channels' by the head's last reader (g_qk_cnt).
 template <int NW>
 __global__ __launch_bounds__(64 * NW) void k_gdn_dec(const GdnArgs a) {
     constexpr int CPW = 8, KQ = 8, RPL = SV / KQ;
@@ -365,6 +388,11 @@ __global__ __launch_bounds__(64 * NW) void k_gdn_dec(const GdnArgs a) {
         const float acc = w0[r] * t0[r] + w1[r] * t1[r] + w2[r] * t2[r] + w3[r] * xi[r];
         c[r] = silu(acc);
     }
+    // every load above (the tails among them) has returned: count this wave
+    // as a reader of its q / k head's tails
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    unsigned prev = 0;  // lane 0's; read at the end, so its round trip overlaps the step
+    if (lane == 0) prev = __hip_atomic_fetch_add(&g_qk_cnt[j * QK_CNT_STRIDE], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     const float sqq = wave_sum(c[0] * c[0] + c[1] * c[1]);
     const float sqk = wave_sum(c[2] * c[2] + c[3] * c[3]);
     const float rq = sqrtf(sqq), rk = sqrtf(sqk);
@@ -403,7 +431,9 @@ __global__ __launch_bounds__(64 * NW) void k_gdn_dec(const GdnArgs a) {
     if (lane == 0) a.PSS[(size_t)h * GDN_PSS_STRIDE + wg] = o2;
 #pragma unroll
     for (int i = 0; i < RPL; i++) Sh[(size_t)(RPL * kq + i) * SV + v] = s[i];
-    const bool own_qk = h < NHQ && wg == 0;
+    // the last of the head's 16 * (V heads using it) reader waves writes the q / k tails
+    const bool own_qk = __builtin_amdgcn_readfirstlane(prev) + 1 == 16u * (unsigned)((n_vh - 1 - j) / NHQ + 1);
+    if (own_qk && lane == 0) __hip_atomic_store(&g_qk_cnt[j * QK_CNT_STRIDE], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 #pragma unroll
     for (int r = 0; r < 5; r++)
         if (r == 4 ? lane < CPW : own_qk) {
@@ -507,13 +537,15 @@ extern "C" int draco_set_gdn_split(int decode_split, int scan_split) {
 }
 
 int draco_gdn_scan_launch(const GdnArgs& a, hipStream_t st) {
-    if (a.n_vh < 1 || a.nhq < 1 || a.n_qkv != a.n_vh * SV + 2 * a.nhq * SV || a.T < 0) return -1;
+    if (a.n_vh < 1 || a.nhq < 1 || a.nhq > QK_CNT_MAX || a.n_qkv != a.n_vh * SV + 2 * a.nhq * SV || a.T < 0)
+        return -1;
     if (a.T == 0) return 0;
     return launch_scan<false>(a, a.nspl < 1 ? 1 : a.nspl, st);
 }
 
 int draco_gdn_step_launch(const GdnArgs& a, hipStream_t st) {
-    if (a.n_vh < 1 || a.nhq < 1 || a.n_qkv != a.n_vh * SV + 2 * a.nhq * SV || a.T != 1) return -1;
+    if (a.n_vh < 1 || a.nhq < 1 || a.nhq > QK_CNT_MAX || a.n_qkv != a.n_vh * SV + 2 * a.nhq * SV || a.T != 1)
+        return -1;
     if (a.H < 4 || a.H > 4096 || a.H % 4 || !a.h1 || !a.attn_norm || !a.bw || !a.aw || !a.ssm_a || !a.ssm_dt)
         return -1;
     return launch_scan<true>(a, a.nspl < 1 ? 1 : a.nspl, st);
