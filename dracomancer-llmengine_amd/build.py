@@ -27,7 +27,11 @@ DEVICE_CONTRACT = ["-fno-gpu-flush-denormals-to-zero"]
 # Per-file flags.  The prefill GEMM post-processes every MFMA result on the VALU;
 # the VGPR form of the MFMA writes them where the VALU reads them, instead of to
 # accumulation registers that each need a v_accvgpr_read first.
-FILE_FLAGS = {"gemm.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
+FILE_FLAGS = {"gemm.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
+              # the scan kernels' reader counters: one lane's atomic whose result is
+              # used only at the kernel's end (the optimizer's wave-level rewrite
+              # would wait for it where it is issued)
+              "gdn.hip": ["-mllvm", "-amdgpu-atomic-optimizer-strategy=None"]}
 
 
 def _sources():

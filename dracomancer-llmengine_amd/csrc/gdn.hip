@@ -211,12 +211,8 @@ __global__ __launch_bounds__(64 * NW) void k_gdn_scan(const GdnArgs a) {
     for (int i = 0; i < RPL; i++) s[i] = Sh[(size_t)(RPL * kq + i) * SV + v];
     const float scale = 1.f / sqrtf((float)SV);
 
-    // every load above (the tails among them) has returned: count this block
-    // as a reader of its q / k head's tails
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __shared__ unsigned qk_prev;
-    unsigned prev = 0;  // thread 0's; passed on after the token loop, so its round trip overlaps the scan
-    if (tid == 0) prev = __hip_atomic_fetch_add(&g_qk_cnt[j * QK_CNT_STRIDE], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    unsigned prev = 0;  // thread 0's: the block's count as a reader of its q / k head's tails (below)
     float gin = 0.f, bin = 0.f;
     if constexpr (DEC) {
         if (a.glog) GdnGates<NW>::gates_of(a, h, gdb, gda, &bin, &gin);
@@ -262,6 +258,12 @@ __global__ __launch_bounds__(64 * NW) void k_gdn_scan(const GdnArgs a) {
             red[1][w] = sqk;
         }
         lds_barrier();
+        // every wave has used its tails in the first token's conv (their loads
+        // have returned): count the block as a reader of its q / k head's
+        // tails; the result is read after the token loop, so the atomic's
+        // round trip overlaps the scan
+        if (t == 0 && tid == 0)
+            prev = __hip_atomic_fetch_add(&g_qk_cnt[j * QK_CNT_STRIDE], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         float nq = 0.f, nk = 0.f;
 #pragma unroll
         for (int q = 0; q < NW; q++) {
@@ -388,10 +390,21 @@ __global__ __launch_bounds__(64 * NW) void k_gdn_dec(const GdnArgs a) {
         const float acc = w0[r] * t0[r] + w1[r] * t1[r] + w2[r] * t2[r] + w3[r] * xi[r];
         c[r] = silu(acc);
     }
-    // every load above (the tails among them) has returned: count this wave
-    // as a reader of its q / k head's tails
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    unsigned prev = 0;  // lane 0's; read at the end, so its round trip overlaps the step
+    // Count the wave as a reader of its q / k head's tails once every load
+    // above has returned: the empty asm statements read every loaded value,
+    // so the compiler waits for all of them here (they are all needed from
+    // here on) and no wait after the atomic is for anything but the atomic,
+    // whose result is read at the end: its round trip overlaps the step.
+    // (gdn.hip is built without the atomic optimizer, whose wave-level
+    // rewrite waits for the result where the atomic is.)
+#pragma unroll
+    for (int r = 0; r < 5; r++)
+        asm volatile("" ::"v"(w0[r]), "v"(w1[r]), "v"(w2[r]), "v"(w3[r]), "v"(t0[r]), "v"(t1[r]), "v"(t2[r]),
+                     "v"(xi[r]));
+#pragma unroll
+    for (int i = 0; i < RPL; i += 4) asm volatile("" ::"v"(s[i]), "v"(s[i + 1]), "v"(s[i + 2]), "v"(s[i + 3]));
+    asm volatile("" ::"v"(z), "v"(nw) : "memory");
+    unsigned prev = 0;  // lane 0's
     if (lane == 0) prev = __hip_atomic_fetch_add(&g_qk_cnt[j * QK_CNT_STRIDE], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     const float sqq = wave_sum(c[0] * c[0] + c[1] * c[1]);
     const float sqk = wave_sum(c[2] * c[2] + c[3] * c[3]);
