@@ -170,6 +170,28 @@ __device__ __forceinline__ void lds_barrier() {
 
 __device__ __forceinline__ float4 ld4(const float* p) { return *reinterpret_cast<const float4*>(p); }
 
+// The pending accumulator's flag (a uniform int64) through a vector load at
+// an opaque per-lane offset of 0: a plain uniform load becomes a scalar load
+// that the compiler schedules after the vector loads and then waits for.
+__device__ __forceinline__ long long load_flag(const long long* p) {
+    int z;
+    asm volatile("v_mov_b32 %0, 0" : "=v"(z));
+    return p[z];
+}
+
+// x + acc * 2^-32 for a pending residual held as int64 fixed point (acc of
+// four inputs in a, b), or NaN in every lane when the accumulator's flag is
+// set.  Branch-free: under an if / else the compiler moves the x and acc
+// loads into the branch, behind the flag's load, which costs a memory round
+// trip.
+__device__ __forceinline__ float4 fx_pending(float4 v, longlong2 a, longlong2 b, bool bad) {
+    constexpr float S = 2.3283064365386963e-10f;  // 2^-32
+    const float n = __builtin_nanf("");
+    const float x = v.x + (float)a.x * S, y = v.y + (float)a.y * S;
+    const float z = v.z + (float)b.x * S, w = v.w + (float)b.y * S;
+    return make_float4(bad ? n : x, bad ? n : y, bad ? n : z, bad ? n : w);
+}
+
 
 // Streaming load of data read once per launch (quantized weights): the
 // non-temporal hint marks the lines for early eviction, so a weight stream

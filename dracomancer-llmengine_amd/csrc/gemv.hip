@@ -739,6 +739,7 @@ __global__ __launch_bounds__(256) void k_seg(const SegKArgs a) {
     float4 xv[XB], nv[XB];
     longlong2 pa[PEND ? XB : 1], pb[PEND ? XB : 1];
     long long pflag = 0;
+    if constexpr (PEND) pflag = load_flag(reinterpret_cast<const long long*>(a.am_val) + a.n_in);
 #pragma unroll
     for (int q = 0; q < XB; q++) {
         const int i4 = tid + q * 256, ic = i4 < n4 ? i4 : n4 - 1;
@@ -751,17 +752,9 @@ __global__ __launch_bounds__(256) void k_seg(const SegKArgs a) {
         }
     }
     if constexpr (PEND) {
-        pflag = reinterpret_cast<const long long*>(a.am_val)[a.n_in];
 #pragma unroll
         for (int q = 0; q < XB; q++) {
-            constexpr float S = 2.3283064365386963e-10f;  // 2^-32
-            float4 v = xv[q];
-            if (pflag) {
-                v.x = v.y = v.z = v.w = __builtin_nanf("");
-            } else {
-                v.x += (float)pa[q].x * S; v.y += (float)pa[q].y * S;
-                v.z += (float)pb[q].x * S; v.w += (float)pb[q].y * S;
-            }
+            const float4 v = fx_pending(xv[q], pa[q], pb[q], pflag != 0);
             xv[q] = v;
             if (a.xn_out && blockIdx.x == 0 && tid + q * 256 < n4)
                 *reinterpret_cast<float4*>(a.xn_out + 4 * (tid + q * 256)) = v;
