@@ -18,7 +18,12 @@ TIMELINE_LIB = os.path.join(LIBDIR, "libdraco_hip_timeline.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = os.environ.get("DRACO_ARCH", "gfx950")
 
+# Kernel-argument preloading: the dispatcher places the first 14 dwords of
+# the arguments in SGPRs, so a kernel issues its first loads after fewer
+# dependent scalar loads of its arguments (configs[2] 2327 -> 2376 tok/s,
+# configs[3] 600 -> 614 same-box; configs[0] / [4] flat).
 COMMON = ["-O3", "-fPIC", "-std=c++17", f"--offload-arch={ARCH}", "-ffp-contract=off",
+          "-mllvm", "-amdgpu-kernarg-preload-count=16",
           "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
           "-fopenmp", "-Wno-unused-result", f"-I{CSRC}"]
 # Contraction is off everywhere: kernels call fmaf where they want a fused op, and
