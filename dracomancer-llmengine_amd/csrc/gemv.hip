@@ -58,31 +58,40 @@ constexpr int XP_MAXV = 4;                // float4s of x per thread held by the
 // +0.4 us per launch, same kernel code), so the host request -- four full
 // layouts and fields only the host or the finalize launch needs -- is not
 // passed as is.
+// Field order: the kernels receive the first 14 dwords of the argument
+// block in SGPRs (kernel-argument preloading), so what the prologue's first
+// loads need comes first -- x, the norm weight, the pending accumulator, the
+// row width and tile count, then segment 0's weight base, first tile and tile
+// offset -- and those loads need no scalar load of an argument.
 struct SegK {
     const uint8_t* base;  // K-quant tiles; Q8_0: the quants (layout off[0])
+    int first;            // first global tile (K-quants) or first grid block (Q8_0)
+    int tile0;
+    int code, n_out;
     const uint8_t* aux;   // Q8_0: the fp16 scales (layout off[1])
     float* y;
     const float* yadd;
-    int code, n_out, nb, epi;
+    int nb, epi;
     int row0, row1;
-    int first;  // first global tile (K-quants) or first grid block (Q8_0)
-    int tile0;
 };
 
 struct SegKArgs {
-    SegK seg[SEG_MAX];
     const float* x;
     const float* norm_w;
+    float* am_val;
+    int n_in, total_tiles;
+    int rot;  // also the split-K launches' tile count per half
+    int nseg;
+    SegK seg[SEG_MAX];
     float* xn_out;
     const float* rope_tab;
     const int* state;
     float* kc;
     float* vc;
-    float* am_val;
     int* am_idx;
-    int nseg, total_tiles, n_in, do_norm;
+    int do_norm;
     float eps;
-    int layer, head_dim, rot, kv_dim;
+    int layer, head_dim, kv_dim;
     // row dots (SegLaunch.gdot_*): launches that carry them have no rope or
     // KV epilogue and no GNORM prologue, so their rows ride in rope_tab (w0)
     // and kc (w1) and the dots go to vc (the argument block stays 368 bytes)
@@ -184,11 +193,18 @@ constexpr bool TL_BUILD = false;
 #endif
 constexpr int EPI_RT = -1, EPI_QKV = -2;
 // GD: the launch carries row dots (a.gdot, RMSNorm prologues only).
+// The prologue's arguments come first, as scalars (agrid = the launch's
+// grid size): the dispatcher preloads the first 14 argument dwords into
+// SGPRs (a struct argument is never preloaded), so the first x and weight
+// loads wait for no argument load.
 template <int NW, int FM, bool DUAL, bool MULTI, int EPI, int NORM, bool IPT1, bool KS = false, bool GD = false>
-__global__ __launch_bounds__(64 * NW) void k_dq(const SegKArgs a) {
+__global__ __launch_bounds__(64 * NW) void k_dq(const float* __restrict__ ax, const float* __restrict__ anw,
+                                                 float* __restrict__ aacc, int an_in, int atotal, int arot,
+                                                 int agrid, const uint8_t* __restrict__ abase0, int afirst0,
+                                                 int atile00, const SegKArgs a) {
     extern __shared__ __align__(16) uint8_t smem[];
     constexpr int NT = 64 * NW;
-    const int n_in = a.n_in, nb = n_in >> 8, ng = n_in >> 4, n4 = n_in >> 2;
+    const int n_in = an_in, nb = n_in >> 8, ng = n_in >> 4, n4 = n_in >> 2;
     int8_t* xd = reinterpret_cast<int8_t*>(smem);                           // [ng][4 digits][16]
     int8_t* zero = xd + (size_t)ng * 64;                                    // 1 KB of zeros
     float2* xsm = reinterpret_cast<float2*>(smem + (size_t)ng * 64 + 1024);  // [ng] (2^(k-7), sum x)
@@ -200,11 +216,11 @@ __global__ __launch_bounds__(64 * NW) void k_dq(const SegKArgs a) {
                           !IPT1;
     unsigned long long ts0 = 0, ts1 = 0, ts2 = 0, ts3 = 0, ts4 = 0, ts5 = 0;
     if (TSON) ts0 = __builtin_amdgcn_s_memrealtime();
-    const int bx = blockIdx.x, G = gridDim.x;
-    const int total = a.total_tiles;
+    const int bx = blockIdx.x, G = agrid;
+    const int total = atotal;
     const int ipt = IPT1 ? 1 : (KS ? (nb >> 1) / NW : (nb + NW - 1) / NW);  // IPT1: one item per wave and tile
     // KS: the half of tile T (0 or 1) and its first super-block
-    auto khalf = [&](int T) { return KS && T >= a.rot ? 1 : 0; };
+    auto khalf = [&](int T) { return KS && T >= arot ? 1 : 0; };
     auto kfirst = [&](int T) { return KS ? khalf(T) * (nb >> 1) : 0; };
     const int my_tiles = bx < total ? (total - bx + G - 1) / G : 0;
     const int n_items = my_tiles * ipt;
@@ -217,15 +233,16 @@ __global__ __launch_bounds__(64 * NW) void k_dq(const SegKArgs a) {
         bool q4;
     };
     auto tile_ref = [&](int T) {
-        if (KS) T -= khalf(T) * a.rot;
+        if (KS) T -= khalf(T) * arot;
         const int si = MULTI ? seg_of_tile(a, T) : 0;
         const bool q4 = FM == 3 ? seg_pick(a, si, [](const SegK& d) { return d.code; }) == DRACO_Q4_K : FM == 1;
         const size_t ib = FM == 4 ? DRACO_Q5T_ITEM : (q4 ? DRACO_Q4T_ITEM : DRACO_Q6T_ITEM);
-        const int tl = T - seg_pick(a, si, [](const SegK& d) { return d.first; }) +
-                       seg_pick(a, si, [](const SegK& d) { return d.tile0; });
+        // segment 0's fields from the preloaded arguments
+        const int tl = T - (si == 0 ? afirst0 : seg_pick(a, si, [](const SegK& d) { return d.first; })) +
+                       (si == 0 ? atile00 : seg_pick(a, si, [](const SegK& d) { return d.tile0; }));
         const size_t off = (size_t)tl * nb * ib;
         TileRef r;
-        r.p = seg_pick(a, si, [](const SegK& d) { return d.base; }) + off;
+        r.p = (si == 0 ? abase0 : seg_pick(a, si, [](const SegK& d) { return d.base; })) + off;
         r.p2 = DUAL ? seg_pick(a, si + 1, [](const SegK& d) { return d.base; }) + off : r.p;
         r.q4 = q4;
         return r;
@@ -246,12 +263,12 @@ __global__ __launch_bounds__(64 * NW) void k_dq(const SegKArgs a) {
     constexpr int XPV = NORM == 4 ? 1 : XP_MAXV;               // float4s of x per thread
     float4 xv[XPV], wv[XPV];
     // NORM 4 (PRES8): the pending residual's int64 fixed-point accumulator at
-    // a.am_val ([n_in] sums of round(2^32 p), then a flag at [n_in], set when
+    // aacc ([n_in] sums of round(2^32 p), then a flag at [n_in], set when
     // a contribution was not finite)
     longlong2 pq[NORM == 4 ? 2 : 1];
     long long pflag = 0;
     // NORM 2 (GNORM): the group partials [n_in / 128][64] = a.kc (16 used)
-    // NORM 3 (PRES): the pending residual's two split-K partials at a.am_val
+    // NORM 3 (PRES): the pending residual's two split-K partials at aacc
     // ([2][n_in]); x = (x + p0) + p1, written to a.xn_out by block 0
     float4 pv0[NORM == 2 || NORM == 3 ? XP_MAXV : 1], pv1[NORM == 2 || NORM == 3 ? XP_MAXV : 1],
         pv2[NORM == 2 ? XP_MAXV : 1], pv3[NORM == 2 ? XP_MAXV : 1];
@@ -264,17 +281,17 @@ __global__ __launch_bounds__(64 * NW) void k_dq(const SegKArgs a) {
     for (int q = 0; q < XPV; q++) {
         const int i4 = tid + q * NT;
         if (i4 < n4 && q >= kq_lo && q < kq_lo + kq_n) {
-            xv[q] = ld4(a.x + 4 * i4);
-            if (RMS && a.norm_w) wv[q] = ld4(a.norm_w + 4 * i4);
+            xv[q] = ld4(ax + 4 * i4);
+            if (RMS && anw) wv[q] = ld4(anw + 4 * i4);
             if constexpr (NORM == 4) {
-                const longlong2* A = reinterpret_cast<const longlong2*>(a.am_val) + 2 * i4;
+                const longlong2* A = reinterpret_cast<const longlong2*>(aacc) + 2 * i4;
                 pq[0] = A[0];
                 pq[1] = A[1];
-                pflag = reinterpret_cast<const long long*>(a.am_val)[n_in];
+                pflag = reinterpret_cast<const long long*>(aacc)[n_in];
             }
             if constexpr (NORM == 3) {
-                pv0[q] = ld4(a.am_val + 4 * i4);
-                pv1[q] = ld4(a.am_val + n_in + 4 * i4);
+                pv0[q] = ld4(aacc + 4 * i4);
+                pv1[q] = ld4(aacc + n_in + 4 * i4);
             }
             if constexpr (NORM == 2) {
                 const float* pp = a.kc + ((4 * i4) >> 7) * 64;
@@ -390,7 +407,7 @@ __global__ __launch_bounds__(64 * NW) void k_dq(const SegKArgs a) {
             ss = fmaf(v.y, v.y, ss);
             ss = fmaf(v.z, v.z, ss);
             ss = fmaf(v.w, v.w, ss);
-            if (a.norm_w) {
+            if (anw) {
                 const float4 nw = wv[q];
                 v.x *= nw.x; v.y *= nw.y; v.z *= nw.z; v.w *= nw.w;
             }
@@ -442,7 +459,7 @@ __global__ __launch_bounds__(64 * NW) void k_dq(const SegKArgs a) {
                 const int i4 = tid + q * NT;
                 if (i4 >= n4) break;
                 float4 v = xv[q];
-                if (a.norm_w) {
+                if (anw) {
                     const float4 nw = wv[q];
                     v.x = v.x * inv * nw.x; v.y = v.y * inv * nw.y; v.z = v.z * inv * nw.z; v.w = v.w * inv * nw.w;
                 } else {
@@ -473,7 +490,7 @@ __global__ __launch_bounds__(64 * NW) void k_dq(const SegKArgs a) {
             const int si = MULTI ? seg_of_tile(a, ct) : 0;
             if constexpr (EPI == EPI_QKV) c_epi = si == 0 ? EPI_ROPE_Q : (si == 1 ? EPI_ROPE_K : EPI_V_APPEND);
             else c_epi = EPI != EPI_RT ? EPI : seg_pick(a, si, [](const SegK& d) { return d.epi; });
-            c_row = (ct - khalf(ct) * a.rot - seg_pick(a, si, [](const SegK& d) { return d.first; }) +
+            c_row = (ct - khalf(ct) * arot - seg_pick(a, si, [](const SegK& d) { return d.first; }) +
                      seg_pick(a, si, [](const SegK& d) { return d.tile0; })) * 16;
             c_r0 = seg_pick(a, si, [](const SegK& d) { return d.row0; });
             c_r1 = seg_pick(a, si, [](const SegK& d) { return d.row1; });
@@ -486,8 +503,8 @@ __global__ __launch_bounds__(64 * NW) void k_dq(const SegKArgs a) {
                 const float* src = nullptr;
                 if (c_epi == EPI_RESID) {
                     src = seg_pick(a, si, [](const SegK& d) { return d.yadd; }) + rr;
-                } else if ((c_epi == EPI_ROPE_Q || c_epi == EPI_ROPE_K) && rr % a.head_dim < a.rot) {
-                    src = a.rope_tab + ((size_t)pos * (a.rot / 2) + (rr % a.head_dim) / 2) * 2;
+                } else if ((c_epi == EPI_ROPE_Q || c_epi == EPI_ROPE_K) && rr % a.head_dim < arot) {
+                    src = a.rope_tab + ((size_t)pos * (arot / 2) + (rr % a.head_dim) / 2) * 2;
                 }
                 const float2 e =
                     src ? make_float2(src[0], c_epi == EPI_RESID ? 0.f : src[1]) : make_float2(0.f, 0.f);
@@ -568,7 +585,7 @@ __global__ __launch_bounds__(64 * NW) void k_dq(const SegKArgs a) {
                     // pairs (2i, 2i+1) of a head, src/m6_engine.c:134-143
                     const float pv = dpp<DPP_XOR1>(v);
                     float o = v;
-                    if (row % a.head_dim < a.rot) {
+                    if (row % a.head_dim < arot) {
                         const float c = ep0, sn = ep1;
                         o = (row & 1) ? pv * sn + v * c : v * c - pv * sn;
                     }
@@ -620,7 +637,7 @@ __global__ __launch_bounds__(64 * NW) void k_dq(const SegKArgs a) {
         }
     }
     if ((EPI >= 0 ? EPI : (EPI == EPI_QKV ? EPI_ROPE_Q : a.seg[0].epi)) == EPI_ARGMAX && tid == 0) {
-        a.am_val[bx] = am_v;
+        aacc[bx] = am_v;
         a.am_idx[bx] = am_i;
     }
 #ifdef DRACO_TIMELINE
@@ -1178,8 +1195,10 @@ void launch_dq1(SegLaunch& a, int grid, hipStream_t st) {
             reinterpret_cast<const void*>(&k_dq<NW, FM, DUAL, MULTI, EPI, NORM, IPT1, KS, GD>),
             hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
     });
+    const SegKArgs k = seg_kargs(a, false);
     hipLaunchKernelGGL((k_dq<NW, FM, DUAL, MULTI, EPI, NORM, IPT1, KS, GD>), dim3(grid), dim3(64 * NW),
-                       dq_lds_bytes(a.n_in, NW), st, seg_kargs(a, false));
+                       dq_lds_bytes(a.n_in, NW), st, k.x, k.norm_w, k.am_val, k.n_in, k.total_tiles, k.rot, grid,
+                       k.seg[0].base, k.seg[0].first, k.seg[0].tile0, k);
 }
 
 // launches carrying row dots: 8 waves, several store / residual segments
