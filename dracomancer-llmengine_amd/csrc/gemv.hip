@@ -709,19 +709,46 @@ struct FQ80 {
 // round(2^32 p), then a flag at [n_in], set when a contribution was not
 // finite: the input is then NaN), the fused attention merge + o projection's
 // output; block 0 stores the sum (not normalised) to a.xn_out.
+// The prologue's arguments come first, as scalars the dispatcher preloads
+// into SGPRs (x, norm weight, pending accumulator, width, the first blocks
+// of segments 1 and 2, segment 0's quants / scales / rows); the block's
+// segment (at most 3) is picked branch-free from the preloaded first blocks
+// (unused slots start at block 1 << 30), segment 0's blocks read no further
+// argument before their first loads, and the other segments' fields go out
+// together instead of one load per segment.
 template <class F, bool DUAL, int NP, bool NORM, int R, bool PEND = false>
-__global__ __launch_bounds__(256) void k_seg(const SegKArgs a) {
+__global__ __launch_bounds__(256) void k_seg(const float* __restrict__ ax, const float* __restrict__ anw,
+                                             float* __restrict__ aacc, int an_in, int afirst1,
+                                             const uint8_t* __restrict__ abase0, const uint8_t* __restrict__ aaux0,
+                                             int an_out0, int afirst2, const SegKArgs a) {
     extern __shared__ float xsh[];  // the block's x, n_in floats (normalised when do_norm)
     __shared__ float red[4];
     __shared__ float amv[4 * R];
     __shared__ int ami[4 * R];
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    int si = 0;
-    for (int i = 1; i < a.nseg; i++)
-        if ((int)blockIdx.x >= a.seg[i].first) si = i;
-    const SegK& s = a.seg[si];
-    const SegK& s2 = a.seg[DUAL ? si + 1 : si];
-    const int r0 = ((int)blockIdx.x - s.first) * (4 * R) + wv * R;
+    const int bx = blockIdx.x;
+    const int si = (bx >= afirst1) + (bx >= afirst2);  // Q8_0 launches have at most 3 segments
+    SegK s, s2;
+    if (si == 0) {  // wave-uniform: segment 0's blocks use the preloaded fields only
+        s.base = abase0;
+        s.aux = aaux0;
+        s.n_out = an_out0;
+        s.first = 0;
+    } else {
+        s.base = seg_pick(a, si, [](const SegK& d) { return d.base; });
+        s.aux = seg_pick(a, si, [](const SegK& d) { return d.aux; });
+        s.n_out = seg_pick(a, si, [](const SegK& d) { return d.n_out; });
+        s.first = si == 1 ? afirst1 : afirst2;
+    }
+    s.nb = an_in / F::NX;  // the epilogue's fields are picked where they are used
+    if (DUAL) {
+        s2.base = seg_pick(a, si + 1, [](const SegK& d) { return d.base; });
+        s2.aux = seg_pick(a, si + 1, [](const SegK& d) { return d.aux; });
+        s2.nb = s.nb;
+    } else {
+        s2 = s;
+    }
+    const int r0 = (bx - s.first) * (4 * R) + wv * R;
     const int n_out = s.n_out, U = s.nb * F::UPB, npair = R * U, passes = (npair + 63) / 64;
     // pass k of this lane: row index i within the wave's rows, block u; live
     // when the pair exists and its row is in range
@@ -750,20 +777,20 @@ __global__ __launch_bounds__(256) void k_seg(const SegKArgs a) {
     // are requested together and unconditionally (clamped index; a null norm
     // weight re-reads x), so the wait for them does not wait for the
     // weights; longer rows take further batches.
-    const int n4 = a.n_in >> 2;
+    const int n4 = an_in >> 2;
     constexpr int XB = 4;  // float4s per thread per batch
-    const float* nwp = a.norm_w ? a.norm_w : a.x;
+    const float* nwp = anw ? anw : ax;
     float4 xv[XB], nv[XB];
     longlong2 pa[PEND ? XB : 1], pb[PEND ? XB : 1];
     long long pflag = 0;
-    if constexpr (PEND) pflag = load_flag(reinterpret_cast<const long long*>(a.am_val) + a.n_in);
+    if constexpr (PEND) pflag = load_flag(reinterpret_cast<const long long*>(aacc) + an_in);
 #pragma unroll
     for (int q = 0; q < XB; q++) {
         const int i4 = tid + q * 256, ic = i4 < n4 ? i4 : n4 - 1;
-        xv[q] = ld4(a.x + 4 * ic);
+        xv[q] = ld4(ax + 4 * ic);
         if (NORM) nv[q] = ld4(nwp + 4 * ic);
         if constexpr (PEND) {
-            const longlong2* A = reinterpret_cast<const longlong2*>(a.am_val) + 2 * ic;
+            const longlong2* A = reinterpret_cast<const longlong2*>(aacc) + 2 * ic;
             pa[q] = A[0];
             pb[q] = A[1];
         }
@@ -784,7 +811,7 @@ __global__ __launch_bounds__(256) void k_seg(const SegKArgs a) {
             ss = fmaf(v.y, v.y, ss);
             ss = fmaf(v.z, v.z, ss);
             ss = fmaf(v.w, v.w, ss);
-            if (a.norm_w) {
+            if (anw) {
                 v.x *= w.x; v.y *= w.y; v.z *= w.z; v.w *= w.w;
             }
         }
@@ -793,7 +820,7 @@ __global__ __launch_bounds__(256) void k_seg(const SegKArgs a) {
 #pragma unroll
     for (int q = 0; q < XB; q++)
         if (tid + q * 256 < n4) stage(tid + q * 256, xv[q], nv[q]);
-    for (int i4 = tid + XB * 256; i4 < n4; i4 += 256) stage(i4, ld4(a.x + 4 * i4), NORM ? ld4(nwp + 4 * i4) : xv[0]);
+    for (int i4 = tid + XB * 256; i4 < n4; i4 += 256) stage(i4, ld4(ax + 4 * i4), NORM ? ld4(nwp + 4 * i4) : xv[0]);
     float inv = 1.f;
     if (NORM) {
         ss = wave_sum(ss);
@@ -802,10 +829,10 @@ __global__ __launch_bounds__(256) void k_seg(const SegKArgs a) {
     lds_barrier();  // LDS only: the weight loads above stay in flight
     if (NORM) {
         const float tot = (red[0] + red[1]) + (red[2] + red[3]);
-        inv = 1.f / sqrtf(tot / (float)a.n_in + a.eps);
+        inv = 1.f / sqrtf(tot / (float)an_in + a.eps);
         if (!PEND && a.xn_out && blockIdx.x == 0) {  // the normalised x, (x / rms) * w as the reference
             auto put = [&](int i4, float4 v, const float4 w) {
-                if (a.norm_w) {
+                if (anw) {
                     v.x = v.x * inv * w.x; v.y = v.y * inv * w.y; v.z = v.z * inv * w.z; v.w = v.w * inv * w.w;
                 } else {
                     v.x *= inv; v.y *= inv; v.z *= inv; v.w *= inv;
@@ -815,7 +842,7 @@ __global__ __launch_bounds__(256) void k_seg(const SegKArgs a) {
 #pragma unroll
             for (int q = 0; q < XB; q++)
                 if (tid + q * 256 < n4) put(tid + q * 256, xv[q], nv[q]);
-            for (int i4 = tid + XB * 256; i4 < n4; i4 += 256) put(i4, ld4(a.x + 4 * i4), ld4(nwp + 4 * i4));
+            for (int i4 = tid + XB * 256; i4 < n4; i4 += 256) put(i4, ld4(ax + 4 * i4), ld4(nwp + 4 * i4));
         }
     }
 
@@ -860,6 +887,9 @@ __global__ __launch_bounds__(256) void k_seg(const SegKArgs a) {
 #pragma unroll
     for (int i = 0; i < (DUAL ? 2 : 1) * R; i++) acc[i] = wave_sum(acc[i]) * inv;
 
+    s.epi = seg_pick(a, si, [](const SegK& d) { return d.epi; });
+    s.y = seg_pick(a, si, [](const SegK& d) { return d.y; });
+    s.yadd = seg_pick(a, si, [](const SegK& d) { return d.yadd; });
     switch (s.epi) {
     case EPI_STORE:
     case EPI_ARGMAX:
@@ -928,7 +958,7 @@ __global__ __launch_bounds__(256) void k_seg(const SegKArgs a) {
         int idx = ami[0];
         for (int i = 1; i < 4 * R; i++) am_merge(v, idx, amv[i], ami[i]);
         const int bi = (int)blockIdx.x - s.first;
-        a.am_val[bi] = v;
+        aacc[bi] = v;
         a.am_idx[bi] = idx;
     }
 }
@@ -943,14 +973,23 @@ __global__ __launch_bounds__(256) void k_seg(const SegKArgs a) {
 // group is dotted (loads clamped to real pairs, so they are unconditional and
 // in bounds).  Row dots, the 1/rms scaling and the argmax merge are k_seg's.
 template <int RPW, int PASSES, bool NORM>
-__global__ __launch_bounds__(256) void k_seg_rows(const SegKArgs a) {
+__global__ __launch_bounds__(256) void k_seg_rows(const float* __restrict__ ax, const float* __restrict__ anw,
+                                                  int an_in, int an_out0, const uint8_t* __restrict__ abase0,
+                                                  const uint8_t* __restrict__ aaux0, float* __restrict__ ay0,
+                                                  int aepi0, const SegKArgs a) {
     using F = FQ80;
     extern __shared__ float xsh[];
     __shared__ float red[4];
     __shared__ float amv[4];
     __shared__ int ami[4];
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    const SegK& s = a.seg[0];
+    SegK s;  // the one segment, from the preloaded arguments
+    s.base = abase0;
+    s.aux = aaux0;
+    s.n_out = an_out0;
+    s.nb = an_in / F::NX;
+    s.epi = aepi0;
+    s.y = ay0;
     const int n_out = s.n_out, U = s.nb, npair = RPW * U;
     const int n_groups = (n_out + 4 * RPW - 1) / (4 * RPW);
     const bool argmax = s.epi == EPI_ARGMAX;
@@ -969,14 +1008,14 @@ __global__ __launch_bounds__(256) void k_seg_rows(const SegKArgs a) {
 
     // prologue as k_seg's: x (times the norm weight) into LDS with the sum of
     // squares through one LDS-only barrier
-    const int n4 = a.n_in >> 2;
+    const int n4 = an_in >> 2;
     constexpr int XB = 4;
-    const float* nwp = a.norm_w ? a.norm_w : a.x;
+    const float* nwp = anw ? anw : ax;
     float4 xv[XB], nv[XB];
 #pragma unroll
     for (int q = 0; q < XB; q++) {
         const int i4 = tid + q * 256, ic = i4 < n4 ? i4 : n4 - 1;
-        xv[q] = ld4(a.x + 4 * ic);
+        xv[q] = ld4(ax + 4 * ic);
         if (NORM) nv[q] = ld4(nwp + 4 * ic);
     }
     float ss = 0.f;
@@ -986,7 +1025,7 @@ __global__ __launch_bounds__(256) void k_seg_rows(const SegKArgs a) {
             ss = fmaf(v.y, v.y, ss);
             ss = fmaf(v.z, v.z, ss);
             ss = fmaf(v.w, v.w, ss);
-            if (a.norm_w) {
+            if (anw) {
                 v.x *= w.x; v.y *= w.y; v.z *= w.z; v.w *= w.w;
             }
         }
@@ -995,7 +1034,7 @@ __global__ __launch_bounds__(256) void k_seg_rows(const SegKArgs a) {
 #pragma unroll
     for (int q = 0; q < XB; q++)
         if (tid + q * 256 < n4) stage(tid + q * 256, xv[q], nv[q]);
-    for (int i4 = tid + XB * 256; i4 < n4; i4 += 256) stage(i4, ld4(a.x + 4 * i4), NORM ? ld4(nwp + 4 * i4) : xv[0]);
+    for (int i4 = tid + XB * 256; i4 < n4; i4 += 256) stage(i4, ld4(ax + 4 * i4), NORM ? ld4(nwp + 4 * i4) : xv[0]);
     float inv = 1.f;
     if (NORM) {
         ss = wave_sum(ss);
@@ -1004,12 +1043,12 @@ __global__ __launch_bounds__(256) void k_seg_rows(const SegKArgs a) {
     lds_barrier();  // LDS only: the weight loads above stay in flight
     if (NORM) {
         const float tot = (red[0] + red[1]) + (red[2] + red[3]);
-        inv = 1.f / sqrtf(tot / (float)a.n_in + a.eps);
+        inv = 1.f / sqrtf(tot / (float)an_in + a.eps);
         if (a.xn_out && blockIdx.x == 0) {  // the normalised x, (x / rms) * w as the reference
             for (int i4 = tid; i4 < n4; i4 += 256) {
-                float4 v = ld4(a.x + 4 * i4);
-                if (a.norm_w) {
-                    const float4 w = ld4(a.norm_w + 4 * i4);
+                float4 v = ld4(ax + 4 * i4);
+                if (anw) {
+                    const float4 w = ld4(anw + 4 * i4);
                     v.x = v.x * inv * w.x; v.y = v.y * inv * w.y; v.z = v.z * inv * w.z; v.w = v.w * inv * w.w;
                 } else {
                     v.x *= inv; v.y *= inv; v.z *= inv; v.w *= inv;
@@ -1404,7 +1443,8 @@ void launch_seg1(dim3 g, size_t shm, hipStream_t st, const SegKArgs& k) {
         (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&k_seg<FQ80, DUAL, NP, NORM, R, PEND>),
                                   hipFuncAttributeMaxDynamicSharedMemorySize, 128 * 1024);
     });
-    hipLaunchKernelGGL((k_seg<FQ80, DUAL, NP, NORM, R, PEND>), g, dim3(256), shm, st, k);
+    hipLaunchKernelGGL((k_seg<FQ80, DUAL, NP, NORM, R, PEND>), g, dim3(256), shm, st, k.x, k.norm_w, k.am_val, k.n_in,
+                       k.seg[1].first, k.seg[0].base, k.seg[0].aux, k.seg[0].n_out, k.seg[2].first, k);
 }
 
 template <bool DUAL, int NP>
@@ -1452,6 +1492,8 @@ int seg_launch_q8(SegLaunch& a, hipStream_t st) {
     bool dual = false;
     for (int i = 0; i < a.nseg; i++) dual = dual || a.seg[i].epi == EPI_SWIGLU;
     if (dual && a.nseg != 2) return -1;
+    if (a.nseg > 3) return -1;  // k_seg picks among 3 segments
+    for (int i = a.nseg; i < SEG_MAX; i++) a.seg[i].first_block = 1 << 30;  // never selected
     // the fixed-point pending residual: a SwiGLU pair whose rows fit one
     // batch of the prologue (4 float4s per thread), with its accumulator
     if (a.do_norm == 4 && (!dual || a.n_in > 4096 || !a.am_val)) return -1;
@@ -1472,7 +1514,11 @@ int seg_launch_q8(SegLaunch& a, hipStream_t st) {
         const int n_groups = (n_out0 + 4 * RPW - 1) / (4 * RPW);
         const int grid = n_groups < 256 * g_seg_rows ? n_groups : 256 * g_seg_rows;
         const dim3 gr(grid);
-        auto go = [&](void (*kern)(SegKArgs)) { hipLaunchKernelGGL(kern, gr, dim3(256), shm, st, k); };
+        auto go = [&](void (*kern)(const float*, const float*, int, int, const uint8_t*, const uint8_t*, float*, int,
+                                   SegKArgs)) {
+            hipLaunchKernelGGL(kern, gr, dim3(256), shm, st, k.x, k.norm_w, k.n_in, k.seg[0].n_out, k.seg[0].base,
+                               k.seg[0].aux, k.seg[0].y, k.seg[0].epi, k);
+        };
         if (npair <= 128) {
             if (a.do_norm) go(k_seg_rows<RPW, 2, true>); else go(k_seg_rows<RPW, 2, false>);
         } else if (npair <= 256) {
