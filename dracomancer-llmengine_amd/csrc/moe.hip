@@ -194,11 +194,20 @@ __device__ __forceinline__ int rank_part(const float* sp, int e, int f0, int spa
 // (DUAL) with SwiGLU into a.act; otherwise e_s = a.idx[s] and y[s][row].
 // XPER: slot s reads x + s * x_stride (digits of every slot in LDS).
 template <int NW, int FM, bool DUAL, bool XPER, bool ROUTE>
-__global__ __launch_bounds__(64 * NW) void k_moe_grp(const MoeArgs a) {
+// The prologue's arguments come first as scalars the dispatcher preloads
+// into SGPRs (a struct argument is never preloaded): x, the norm weight
+// (null: none), the logits, the three expert base tables, the width and the
+// expert count.
+__global__ __launch_bounds__(64 * NW) void k_moe_grp(const float* __restrict__ px, const float* __restrict__ pnw,
+                                                     const float* __restrict__ plog,
+                                                     const uint8_t* const* __restrict__ pb0,
+                                                     const uint8_t* const* __restrict__ pb1,
+                                                     const uint8_t* const* __restrict__ pb2, int pn_in, int pn_exp,
+                                                     const MoeArgs a) {
     extern __shared__ __align__(16) uint8_t smem[];
     constexpr int NT = 64 * NW;
     constexpr size_t IB = FM == 1 ? DRACO_Q4T_ITEM : DRACO_Q6T_ITEM;
-    const int n_in = a.n_in, nb = n_in >> 8, ng = n_in >> 4, n4 = n_in >> 2;
+    const int n_in = pn_in, nb = n_in >> 8, ng = n_in >> 4, n4 = n_in >> 2;
     const int nx = XPER ? a.n_slots : 1;  // digit sets
     int8_t* xd = reinterpret_cast<int8_t*>(smem);                            // [nx][ng][4][16]
     int8_t* zero = xd + (size_t)nx * ng * 64;                                // 1 KB of zeros
@@ -213,12 +222,7 @@ __global__ __launch_bounds__(64 * NW) void k_moe_grp(const MoeArgs a) {
 
     const int tid = threadIdx.x, lane = tid & 63, j = lane & 15, g = lane >> 4;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int bx = blockIdx.x, G = gridDim.x;
-    const int n_slots = a.n_slots, tpe = a.n_out_e >> 4;
-    const int total = n_slots * tpe;
-    const int ipt = (nb + NW - 1) / NW;
-    const int my_tiles = bx < total ? (total - bx + G - 1) / G : 0;
-    const int n_items = my_tiles * ipt;
+    const int bx = blockIdx.x;
 
     // x loads first (independent of the routing)
     float4 xv[XP_MAXV], wv[XP_MAXV];
@@ -228,8 +232,8 @@ __global__ __launch_bounds__(64 * NW) void k_moe_grp(const MoeArgs a) {
         const int i4 = tid + q * NT;
         if (i4 < nvals4) {
             const int s = XPER ? i4 / n4 : 0, o = i4 - s * n4;
-            xv[q] = ld4(a.x + (size_t)s * a.x_stride + 4 * o);
-            if (a.do_norm && a.norm_w) wv[q] = ld4(a.norm_w + 4 * o);
+            xv[q] = ld4(px + (size_t)s * a.x_stride + 4 * o);
+            if (pnw) wv[q] = ld4(pnw + 4 * o);
         }
     }
     // routing / expert bases
@@ -248,28 +252,29 @@ __global__ __launch_bounds__(64 * NW) void k_moe_grp(const MoeArgs a) {
 #pragma unroll
         for (int k = 0; k < NPASS; k++) {
             const int e = (tid >> 2) + k * EPP;
-            const bool mine = part == 0 && e < a.n_exp;
-            rb0[k] = mine ? a.base0[e] : nullptr;
-            rb1[k] = (DUAL && mine) ? a.base1[e] : nullptr;
-            rb2[k] = (bx == 0 && mine) ? a.base2[e] : nullptr;
+            const bool mine = part == 0 && e < pn_exp;
+            rb0[k] = mine ? pb0[e] : nullptr;
+            rb1[k] = (DUAL && mine) ? pb1[e] : nullptr;
+            rb2[k] = (bx == 0 && mine) ? pb2[e] : nullptr;
         }
+        const int n_slots = a.n_slots;  // read after the loads above are issued
         if (tid < n_slots) {
             sidx[tid] = 0;
             swt[tid] = 0.f;
-            sb0[tid] = a.base0[0];
-            if (DUAL) sb1[tid] = a.base1[0];
-            if (bx == 0) sb2[tid] = a.base2[0];
+            sb0[tid] = pb0[0];
+            if (DUAL) sb1[tid] = pb1[0];
+            if (bx == 0) sb2[tid] = pb2[0];
         }
-        if (w == 0) softmax_wave(a.logits, a.n_exp, sp);
+        if (w == 0) softmax_wave(plog, pn_exp, sp);
         lds_barrier();
-        const int span = ((a.n_exp + 15) >> 4) << 2;  // a quarter, rounded up to whole float4s
+        const int span = ((pn_exp + 15) >> 4) << 2;  // a quarter, rounded up to whole float4s
 #pragma unroll
         for (int k = 0; k < NPASS; k++) {
-            if (k * EPP >= a.n_exp) break;  // uniform
+            if (k * EPP >= pn_exp) break;  // uniform
             const int e = (tid >> 2) + k * EPP;
-            int r = e < a.n_exp ? rank_part(sp, e, part * span, span) : 0;
+            int r = e < pn_exp ? rank_part(sp, e, part * span, span) : 0;
             r = group_reduce<4>(r, OpAdd{});
-            if (part == 0 && e < a.n_exp && r < n_slots) {
+            if (part == 0 && e < pn_exp && r < n_slots) {
                 sidx[r] = e;
                 swt[r] = sp[e];
                 sb0[r] = rb0[k];
@@ -277,12 +282,19 @@ __global__ __launch_bounds__(64 * NW) void k_moe_grp(const MoeArgs a) {
                 if (bx == 0) sb2[r] = rb2[k];
             }
         }
-    } else if (tid < n_slots) {
-        sb0[tid] = a.base0[tid];
-        if (DUAL) sb1[tid] = a.base1[tid];
+    } else if (tid < a.n_slots) {
+        sb0[tid] = pb0[tid];
+        if (DUAL) sb1[tid] = pb1[tid];
     }
     for (int i = tid; i < 256; i += NT) reinterpret_cast<uint32_t*>(zero)[i] = 0u;
     lds_barrier();
+    // the tile walk (its arguments read after the prologue's loads are issued)
+    const int G = gridDim.x;
+    const int n_slots = a.n_slots, tpe = a.n_out_e >> 4;
+    const int total = n_slots * tpe;
+    const int ipt = (nb + NW - 1) / NW;
+    const int my_tiles = bx < total ? (total - bx + G - 1) / G : 0;
+    const int n_items = my_tiles * ipt;
 
     auto load = [&](int T, int b, Frag& f, Frag& f2) {
         const int s = T / tpe, lt = T - s * tpe;
@@ -325,7 +337,7 @@ __global__ __launch_bounds__(64 * NW) void k_moe_grp(const MoeArgs a) {
         if (i4 >= nvals4) break;
         float4 v = xv[q];
         if (a.do_norm) {
-            if (a.norm_w) {
+            if (pnw) {
                 const float4 nw = wv[q];
                 v.x = v.x * inv * nw.x; v.y = v.y * inv * nw.y; v.z = v.z * inv * nw.z; v.w = v.w * inv * nw.w;
             } else {
@@ -432,14 +444,20 @@ __global__ __launch_bounds__(64 * NW) void k_moe_grp(const MoeArgs a) {
 // whose weighted sum (slot order) goes to out[h n_out + row], no residual:
 // the consumer forms resid + half 0 + half 1.
 template <int NW, int FM, bool SPLIT = false>
-__global__ __launch_bounds__(64 * NW) void k_moe_down(const MoeArgs a) {
+// Leading scalars as k_moe_grp's (preloaded): the selected experts' down
+// bases, the activations, the routing weights, the output and residual, the
+// inner width, the output rows and the slot count.
+__global__ __launch_bounds__(64 * NW) void k_moe_down(const uint8_t* const* __restrict__ pseld,
+                                                      const float* __restrict__ pact, const float* __restrict__ pselw,
+                                                      float* __restrict__ pout, const float* __restrict__ presid,
+                                                      int pinter, int pn_out, int pn_slots, const MoeArgs a) {
     extern __shared__ __align__(16) uint8_t smem[];
     constexpr int NT = 64 * NW;
     constexpr size_t IB = FM == 1 ? DRACO_Q4T_ITEM : DRACO_Q6T_ITEM;
-    const int inter = a.inter, nb = inter >> 8, ng = inter >> 4, n4 = inter >> 2;
-    const int tiles = a.n_out >> 4;
+    const int inter = pinter, nb = inter >> 8, ng = inter >> 4, n4 = inter >> 2;
+    const int tiles = pn_out >> 4;
     const int half = SPLIT ? (int)blockIdx.x / tiles : 0;
-    const int n_used = SPLIT ? a.n_slots / 2 : a.n_slots;  // this block's slots
+    const int n_used = SPLIT ? pn_slots / 2 : pn_slots;  // this block's slots
     const int so = half * n_used;                            // its first slot
     int8_t* xd = reinterpret_cast<int8_t*>(smem);                      // [n_used][ng][64]
     int8_t* zero = xd + (size_t)n_used * ng * 64;
@@ -451,7 +469,7 @@ __global__ __launch_bounds__(64 * NW) void k_moe_down(const MoeArgs a) {
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const bool active = w < n_used;
     // this wave's expert base (routing published by k_moe_grp)
-    const uint8_t* base = a.seld[so + (active ? w : 0)];
+    const uint8_t* base = pseld[so + (active ? w : 0)];
     // item b of tile t (b clamped: a repeated item is already in flight)
     auto ld = [&](int t, int b, Frag& f) {
         const uint8_t* p = base + ((size_t)t * nb + (b < nb ? b : nb - 1)) * IB;
@@ -469,11 +487,11 @@ __global__ __launch_bounds__(64 * NW) void k_moe_down(const MoeArgs a) {
         for (int k = 0; k < AB; k++) {
             const int i4 = b0 + tid + k * NT, ic = i4 < nvals4 ? i4 : nvals4 - 1;
             const int s = ic / n4, o = ic - s * n4;
-            av[k] = ld4(a.act + (size_t)(so + s) * inter + 4 * o);
+            av[k] = ld4(pact + (size_t)(so + s) * inter + 4 * o);
         }
     };
     act_batch(0);
-    const float swv = a.selw[so + (tid < n_used ? tid : n_used - 1)];
+    const float swv = pselw[so + (tid < n_used ? tid : n_used - 1)];
     // requested unconditionally (a wave past the used slots or a block past
     // the tiles re-reads real items), so the act waits above count exactly
     Frag P0, P1, P2;
@@ -541,8 +559,8 @@ __global__ __launch_bounds__(64 * NW) void k_moe_down(const MoeArgs a) {
             float o = 0.f;
             for (int s = 0; s < n_used; s++) o += swt[s] * red[s * 16 + tid];  // j order, like the reference
             const int row = t * 16 + tid;
-            if (SPLIT) a.out[(size_t)half * a.n_out + row] = o;
-            else a.out[row] = a.resid ? a.resid[row] + o : o;
+            if (SPLIT) pout[(size_t)half * pn_out + row] = o;
+            else pout[row] = presid ? presid[row] + o : o;
         }
         lds_barrier();
         if (SPLIT) break;  // one tile per block
@@ -597,14 +615,16 @@ template <int NW, int FM, bool DUAL, bool XPER, bool ROUTE>
 void launch_grp(const MoeArgs& a, int grid, size_t lds, hipStream_t st) {
     static std::once_flag once;
     std::call_once(once, [] { allow_big_lds(&k_moe_grp<NW, FM, DUAL, XPER, ROUTE>); });
-    hipLaunchKernelGGL((k_moe_grp<NW, FM, DUAL, XPER, ROUTE>), dim3(grid), dim3(64 * NW), lds, st, a);
+    hipLaunchKernelGGL((k_moe_grp<NW, FM, DUAL, XPER, ROUTE>), dim3(grid), dim3(64 * NW), lds, st, a.x,
+                       a.do_norm ? a.norm_w : nullptr, a.logits, a.base0, a.base1, a.base2, a.n_in, a.n_exp, a);
 }
 
 template <int NW, int FM, bool SPLIT = false>
 void launch_down(const MoeArgs& a, int grid, size_t lds, hipStream_t st) {
     static std::once_flag once;
     std::call_once(once, [] { allow_big_lds(&k_moe_down<NW, FM, SPLIT>); });
-    hipLaunchKernelGGL((k_moe_down<NW, FM, SPLIT>), dim3(grid), dim3(64 * NW), lds, st, a);
+    hipLaunchKernelGGL((k_moe_down<NW, FM, SPLIT>), dim3(grid), dim3(64 * NW), lds, st, a.seld, a.act, a.selw, a.out,
+                       a.resid, a.inter, a.n_out, a.n_slots, a);
 }
 
 int grp_nw(int n_in) {
