@@ -678,14 +678,18 @@ __global__ __launch_bounds__(256) void k_attn_o8(const float* __restrict__ part,
 // by the head's sum.  Results agree with the split form to fp32 rounding.
 constexpr int ATT_SHORT_T = 128;
 
+// Every argument the first loads need comes within the 14 dwords the
+// dispatcher preloads into SGPRs: ncn packs NC (bits 0-7) and n_out (from
+// bit 8), tn points at the layer's cache length (state + 1 + layer), and the
+// row stride in blocks is NC * KB (the o projection's n_in is NC * REP * 64).
 template <int REP>
-__global__ __launch_bounds__(256) void k_attn_o8s(const float* __restrict__ q, const float* __restrict__ kc,
-                                                  const float* __restrict__ vc, const int* __restrict__ st, int layer,
-                                                  float scale, int tcap, const uint8_t* __restrict__ qs,
-                                                  const uint8_t* __restrict__ ds, int nb, int n_out, int NC,
-                                                  unsigned long long* __restrict__ acc,
+__global__ __launch_bounds__(256) void k_attn_o8s(const uint8_t* __restrict__ qs, const uint8_t* __restrict__ ds,
+                                                  int ncn, const float* __restrict__ q, const float* __restrict__ kc,
+                                                  const float* __restrict__ vc, int tcap, const int* __restrict__ tn,
+                                                  float scale, unsigned long long* __restrict__ acc,
                                                   unsigned long long* __restrict__ zacc, int zn) {
     constexpr int HD = 64, KB = 2 * REP;
+    const int NC = ncn & 255, n_out = ncn >> 8, nb = NC * KB;
     __shared__ __align__(16) float qsh[REP * HD];
     __shared__ float psh[REP][ATT_SHORT_T];
     __shared__ float lsh[REP];
@@ -716,7 +720,7 @@ __global__ __launch_bounds__(256) void k_attn_o8s(const float* __restrict__ q, c
         const int t = w + 4 * i, tc = t < tcap ? t : tcap - 1;
         vv[i] = vc[(size_t)tc * KD + c * HD + lane];
     }
-    const int Tn = st[1 + layer] + 1;
+    const int Tn = *tn + 1;
     __builtin_amdgcn_sched_barrier(0);  // every request before the first wait
     for (int i = b * 256 + tid; i < zn; i += gridDim.x * 256) zacc[i] = 0ull;
     if (tid < REP * 16) reinterpret_cast<float4*>(qsh)[tid] = qv4;
@@ -1169,14 +1173,14 @@ int dk_attn_o8_short(const float* q, const float* kc, const float* vc, const int
                      unsigned long long* zacc, int zn, hipStream_t st) {
     const int REP = NKV > 0 && NH % NKV == 0 ? NH / NKV : 0;
     if (HD != 64 || REP < 1 || REP > 4 || tcap < 1 || tcap > ATT_SHORT_T || wo.L.code != DRACO_Q8_0 ||
-        wo.L.n_in != NH * 64 || wo.L.nb != 2 * NH)
+        wo.L.n_in != NH * 64 || wo.L.nb != 2 * NH || NKV > 255 || wo.L.n_out >= (1 << 23))
         return -1;
     const dim3 grid(NKV * ((wo.L.n_out + 31) / 32)), block(256);
     const uint8_t* qs = wo.dev + wo.L.off[0];
     const uint8_t* ds = wo.dev + wo.L.off[1];
 #define AOS_CASE(R_)                                                                                            \
-    hipLaunchKernelGGL((k_attn_o8s<R_>), grid, block, 0, st, q, kc, vc, state, layer, scale, tcap, qs, ds, wo.L.nb, \
-                       wo.L.n_out, NKV, acc, zacc, zn)
+    hipLaunchKernelGGL((k_attn_o8s<R_>), grid, block, 0, st, qs, ds, NKV | (wo.L.n_out << 8), q, kc, vc, tcap, \
+                       state + 1 + layer, scale, acc, zacc, zn)
     if (REP == 1) AOS_CASE(1);
     else if (REP == 2) AOS_CASE(2);
     else if (REP == 3) AOS_CASE(3);
