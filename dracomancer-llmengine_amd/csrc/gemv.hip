@@ -247,14 +247,22 @@ __global__ __launch_bounds__(64 * NW) void k_dq(const float* __restrict__ ax, co
         r.q4 = q4;
         return r;
     };
+    // Buffer loads for the K-quant items: with global loads the compiler
+    // formed each item's 64-bit VGPR address in the loop and waited for every
+    // load in flight (vmcnt(0)) before issuing the next item's, and a launch
+    // mixing Q4_K and Q6_K tiles loaded under a per-tile branch, which
+    // forced the same full waits (configs[2] decode 2438 -> 2520 tok/s,
+    // configs[4] 1062 -> 1084 same-box).
     auto load_at = [&](const uint8_t* p, const uint8_t* p2, bool q4, Frag& f, Frag& f2) {
         if (FM == 4) load_q5(p, lane, f);
-        else if (q4) load_q4(p, lane, f);
-        else load_q6(p, lane, f);
+        else if (FM == 3) load_q46b(p, q4, lane, f);
+        else if (q4) load_q4b(p, lane, f);
+        else load_q6b(p, lane, f);
         if (DUAL) {
             if (FM == 4) load_q5(p2, lane, f2);
-            else if (q4) load_q4(p2, lane, f2);
-            else load_q6(p2, lane, f2);
+            else if (FM == 3) load_q46b(p2, q4, lane, f2);
+            else if (q4) load_q4b(p2, lane, f2);
+            else load_q6b(p2, lane, f2);
         }
     };
 

@@ -42,6 +42,49 @@ __device__ __forceinline__ void load_q6(const uint8_t* item, int lane, Frag& f) 
     f.d = *gptr<uint16_t>(item + 3328 + 2 * (lane & 15));
 }
 
+// The same items through buffer loads: the item's address is one SGPR
+// descriptor (range = the item's bytes), each lane's offset a fixed VGPR, so
+// a loop that walks items forms no per-item VGPR address.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t item_rsrc(const uint8_t* item, int bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(item), (short)0, bytes, 0x00020000);
+}
+
+__device__ __forceinline__ uint4 bufnt4(__amdgpu_buffer_rsrc_t r, int off) {
+    const v4u32 v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 2);  // aux 2: non-temporal
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+__device__ __forceinline__ void load_q4b(const uint8_t* item, int lane, Frag& f) {
+    const __amdgpu_buffer_rsrc_t r = item_rsrc(item, DRACO_Q4T_ITEM);
+    f.a = bufnt4(r, 16 * lane);
+    f.b = bufnt4(r, 1024 + 16 * lane);
+    f.c = bufnt4(r, 2048 + 16 * (lane & 15));
+    f.sc = 0u;
+    f.d = 0u;
+}
+
+__device__ __forceinline__ void load_q6b(const uint8_t* item, int lane, Frag& f) {
+    const __amdgpu_buffer_rsrc_t r = item_rsrc(item, DRACO_Q6T_ITEM);
+    f.a = bufnt4(r, 16 * lane);
+    f.b = bufnt4(r, 1024 + 16 * lane);
+    f.c = bufnt4(r, 2048 + 16 * lane);
+    f.sc = __builtin_amdgcn_raw_buffer_load_b32(r, 3072 + 4 * lane, 0, 0);
+    f.d = __builtin_amdgcn_raw_buffer_load_b16(r, 3328 + 2 * (lane & 15), 0, 0);
+}
+
+// Either format with the same five loads and no branch (a launch that mixes
+// Q4_K and Q6_K tiles): the descriptor's range is the item's bytes, so for a
+// Q4_K item the two Q6_K-only loads fall past the range and read zero
+// without touching memory.
+__device__ __forceinline__ void load_q46b(const uint8_t* item, bool q4, int lane, Frag& f) {
+    const __amdgpu_buffer_rsrc_t r = item_rsrc(item, q4 ? DRACO_Q4T_ITEM : DRACO_Q6T_ITEM);
+    f.a = bufnt4(r, 16 * lane);
+    f.b = bufnt4(r, 1024 + 16 * lane);
+    f.c = bufnt4(r, 2048 + 16 * (q4 ? lane & 15 : lane));
+    f.sc = __builtin_amdgcn_raw_buffer_load_b32(r, 3072 + 4 * lane, 0, 0);
+    f.d = __builtin_amdgcn_raw_buffer_load_b16(r, 3328 + 2 * (lane & 15), 0, 0);
+}
+
 __device__ __forceinline__ float fold(const v4i C) {
     const int i0 = (C[0] << 7) + C[1], i1 = (C[2] << 7) + C[3];
     return fmaf((float)i1, 6.103515625e-05f, (float)i0);
