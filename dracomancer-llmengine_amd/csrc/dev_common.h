@@ -211,6 +211,17 @@ __device__ __forceinline__ uint4 ldu4(const uint8_t* p) {
     const v4u32 v = *gptr<v4u32>(p);
     return make_uint4(v.x, v.y, v.z, v.w);
 }
+// Lane s's pointer (s wave-uniform) read into SGPRs: a table of up to 64
+// pointers held one per lane is indexed without writing a VGPR (a VGPR
+// temporary can land on the destination of a load still in flight, and the
+// compiler then waits for every load before writing it).
+__device__ __forceinline__ const uint8_t* lane_ptr(const uint8_t* p, int s) {
+    const unsigned long long v = reinterpret_cast<unsigned long long>(p);
+    const unsigned lo = __builtin_amdgcn_readlane((unsigned)v, s);
+    const unsigned hi = __builtin_amdgcn_readlane((unsigned)(v >> 32), s);
+    return reinterpret_cast<const uint8_t*>(((unsigned long long)hi << 32) | lo);
+}
+
 __device__ __forceinline__ uint4 ldnt4(const uint8_t* p) {
     const v4u32 v = __builtin_nontemporal_load(gptr<v4u32>(p));
     return make_uint4(v.x, v.y, v.z, v.w);

@@ -296,14 +296,21 @@ __global__ __launch_bounds__(64 * NW) void k_moe_grp(const float* __restrict__ p
     const int my_tiles = bx < total ? (total - bx + G - 1) / G : 0;
     const int n_items = my_tiles * ipt;
 
+    // the slots' bases, one per lane (n_slots <= MOE_USED_MAX = 64)
+    static_assert(MOE_USED_MAX <= 64, "one slot per lane");
+    const int ls = lane < n_slots ? lane : 0;
+    const uint8_t* lb0 = sb0[ls];
+    const uint8_t* lb1 = DUAL ? sb1[ls] : lb0;
     auto load = [&](int T, int b, Frag& f, Frag& f2) {
         const int s = T / tpe, lt = T - s * tpe;
         const size_t off = ((size_t)lt * nb + b) * IB;
-        if (FM == 1) load_q4(sb0[s] + off, lane, f);
-        else load_q6(sb0[s] + off, lane, f);
+        const uint8_t* p0 = lane_ptr(lb0, s) + off;
+        if (FM == 1) load_q4b(p0, lane, f);
+        else load_q6b(p0, lane, f);
         if (DUAL) {
-            if (FM == 1) load_q4(sb1[s] + off, lane, f2);
-            else load_q6(sb1[s] + off, lane, f2);
+            const uint8_t* p1 = lane_ptr(lb1, s) + off;
+            if (FM == 1) load_q4b(p1, lane, f2);
+            else load_q6b(p1, lane, f2);
         }
     };
     Frag P0, P1, Q0, Q1;
@@ -473,8 +480,8 @@ __global__ __launch_bounds__(64 * NW) void k_moe_down(const uint8_t* const* __re
     // item b of tile t (b clamped: a repeated item is already in flight)
     auto ld = [&](int t, int b, Frag& f) {
         const uint8_t* p = base + ((size_t)t * nb + (b < nb ? b : nb - 1)) * IB;
-        if (FM == 1) load_q4(p, lane, f);
-        else load_q6(p, lane, f);
+        if (FM == 1) load_q4b(p, lane, f);
+        else load_q6b(p, lane, f);
     };
     // act loads (all slots; every float4 of a batch requested together,
     // clamped index) and the combine weight before the expert weights: the
