@@ -735,7 +735,8 @@ __global__ __launch_bounds__(256) void k_seg(const float* __restrict__ ax, const
     __shared__ int ami[4 * R];
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int bx = blockIdx.x;
-    const int si = (bx >= afirst1) + (bx >= afirst2);  // Q8_0 launches have at most 3 segments
+    // Q8_0 launches have at most 3 segments; a dual launch is one pair (segments 0 and 1)
+    const int si = DUAL ? 0 : (bx >= afirst1) + (bx >= afirst2);
     SegK s, s2;
     if (si == 0) {  // wave-uniform: segment 0's blocks use the preloaded fields only
         s.base = abase0;
@@ -750,8 +751,8 @@ __global__ __launch_bounds__(256) void k_seg(const float* __restrict__ ax, const
     }
     s.nb = an_in / F::NX;  // the epilogue's fields are picked where they are used
     if (DUAL) {
-        s2.base = seg_pick(a, si + 1, [](const SegK& d) { return d.base; });
-        s2.aux = seg_pick(a, si + 1, [](const SegK& d) { return d.aux; });
+        s2.base = a.seg[1].base;
+        s2.aux = a.seg[1].aux;
         s2.nb = s.nb;
     } else {
         s2 = s;
@@ -774,7 +775,6 @@ __global__ __launch_bounds__(256) void k_seg(const float* __restrict__ ax, const
         int i, u;
         pair(k, i, u);
         wa[k] = F::load(s, row_of(i), u);
-        if (DUAL) wb[k] = F::load(s2, row_of(i), u);
     }
 
     // prologue: x into LDS, every block the same way.  With the RMSNorm the
@@ -801,6 +801,19 @@ __global__ __launch_bounds__(256) void k_seg(const float* __restrict__ ax, const
             const longlong2* A = reinterpret_cast<const longlong2*>(aacc) + 2 * ic;
             pa[q] = A[0];
             pb[q] = A[1];
+        }
+    }
+    if (DUAL) {
+        // the pair's second half reads its pointers from the struct argument:
+        // its loads follow the first half's and x's, which need no argument
+        // load (the barrier only where the assembly shows it costs no register
+        // copies of loads in flight: the pending-input prologue)
+        if constexpr (PEND) __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int k = 0; k < NP; k++) {
+            int i, u;
+            pair(k, i, u);
+            wb[k] = F::load(s2, row_of(i), u);
         }
     }
     if constexpr (PEND) {
