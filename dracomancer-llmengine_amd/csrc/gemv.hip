@@ -770,12 +770,6 @@ __global__ __launch_bounds__(256) void k_seg(const float* __restrict__ ax, const
     };
     auto row_of = [&](int i) { return r0 + i < n_out ? r0 + i : n_out - 1; };
     typename F::W wa[NP], wb[NP];
-#pragma unroll
-    for (int k = 0; k < NP; k++) {
-        int i, u;
-        pair(k, i, u);
-        wa[k] = F::load(s, row_of(i), u);
-    }
 
     // prologue: x into LDS, every block the same way.  With the RMSNorm the
     // block stages x * w and reduces the sum of squares of x through the same
@@ -802,6 +796,14 @@ __global__ __launch_bounds__(256) void k_seg(const float* __restrict__ ax, const
             pa[q] = A[0];
             pb[q] = A[1];
         }
+    }
+    // the weights after x, so x (needed first) returns first
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int k = 0; k < NP; k++) {
+        int i, u;
+        pair(k, i, u);
+        wa[k] = F::load(s, row_of(i), u);
     }
     if (DUAL) {
         // the pair's second half reads its pointers from the struct argument:
