@@ -698,12 +698,6 @@ __global__ __launch_bounds__(256) void k_attn_o8s(const uint8_t* __restrict__ qs
     const int b = blockIdx.x, c = b % NC, rb = b / NC;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, r = lane >> 3, k = lane & 7;
     const int KD = NC * HD;  // NC = NKV: one chunk per kv group
-    // o rows' quants (as k_attn_o8)
-    const int row = rb * 32 + w * 8 + r, rc = row < n_out ? row : n_out - 1;
-    const int kcb = k < KB ? k : KB - 1;
-    const size_t blk = (size_t)rc * nb + (size_t)c * KB + kcb;
-    const uint4 q0 = ldnt4(qs + blk * 32), q1 = ldnt4(qs + blk * 32 + 16);
-    const uint16_t dh = *reinterpret_cast<const uint16_t*>(ds + blk * 2);
     // the group's q (REP heads of 64): one float4 per thread of the first REP * 16
     const int qi = tid < REP * 16 ? tid : 0;
     const float4 qv4 = ld4(q + (size_t)c * REP * HD + 4 * qi);
@@ -721,6 +715,13 @@ __global__ __launch_bounds__(256) void k_attn_o8s(const uint8_t* __restrict__ qs
         vv[i] = vc[(size_t)tc * KD + c * HD + lane];
     }
     const int Tn = *tn + 1;
+    // o rows' quants (as k_attn_o8), requested last: the scores need q and
+    // K first, the o dot these
+    const int row = rb * 32 + w * 8 + r, rc = row < n_out ? row : n_out - 1;
+    const int kcb = k < KB ? k : KB - 1;
+    const size_t blk = (size_t)rc * nb + (size_t)c * KB + kcb;
+    const uint4 q0 = ldnt4(qs + blk * 32), q1 = ldnt4(qs + blk * 32 + 16);
+    const uint16_t dh = *reinterpret_cast<const uint16_t*>(ds + blk * 2);
     __builtin_amdgcn_sched_barrier(0);  // every request before the first wait
     for (int i = b * 256 + tid; i < zn; i += gridDim.x * 256) zacc[i] = 0ull;
     if (tid < REP * 16) reinterpret_cast<float4*>(qsh)[tid] = qv4;

@@ -1027,10 +1027,10 @@ __global__ __launch_bounds__(256) void k_seg_rows(const float* __restrict__ ax, 
     };
     int gi = blockIdx.x;
     typename F::W cur[PASSES], nxt[PASSES];
-    load_group(gi < n_groups ? gi : n_groups - 1, cur);
 
     // prologue as k_seg's: x (times the norm weight) into LDS with the sum of
-    // squares through one LDS-only barrier
+    // squares through one LDS-only barrier; x requested before the first
+    // group's weights, so it returns first
     const int n4 = an_in >> 2;
     constexpr int XB = 4;
     const float* nwp = anw ? anw : ax;
@@ -1041,6 +1041,8 @@ __global__ __launch_bounds__(256) void k_seg_rows(const float* __restrict__ ax, 
         xv[q] = ld4(ax + 4 * ic);
         if (NORM) nv[q] = ld4(nwp + 4 * ic);
     }
+    __builtin_amdgcn_sched_barrier(0);
+    load_group(gi < n_groups ? gi : n_groups - 1, cur);
     float ss = 0.f;
     auto stage = [&](int i4, float4 v, const float4 w) {
         if (NORM) {
