@@ -536,13 +536,10 @@ __global__ __launch_bounds__(256) void k_attn_o(const float* __restrict__ part, 
     __shared__ __align__(16) int8_t zero[1024];
     __shared__ float2 xsm[16];
     const int b = blockIdx.x, c = b % NC, rr = b / NC;
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, j = lane & 15, g = lane >> 4;
+    const int tid = threadIdx.x, lane = tid & 63, j = lane & 15, g = lane >> 4;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: the item's descriptor in SGPRs
     const int ntiles = (n_out + 15) >> 4;
     const int T = rr * 4 + w, Tc = T < ntiles ? T : ntiles - 1;
-    Frag f;
-    const uint8_t* item = wo + ((size_t)Tc * nb + c) * IB;
-    if (FM == 1) load_q4(item, lane, f);
-    else load_q6(item, lane, f);
     // merge outputs 256 c + 64 w + lane: head (256 c + 64 w) / HD, dim
     // (64 w) % HD + lane; every load unconditional (clamped split index)
     const int hh = (256 * c + 64 * w) / HD, dd = (64 * w) % HD + lane;
@@ -552,6 +549,13 @@ __global__ __launch_bounds__(256) void k_attn_o(const float* __restrict__ part, 
     float pv[MAXS];
 #pragma unroll
     for (int k = 0; k < MAXS; k++) pv[k] = ph[min(k, nsplit - 1) * (HD + 2) + dd];
+    // the o item after the partials: the merge needs them first, the dot
+    // this (requested before the first wait all the same)
+    __builtin_amdgcn_sched_barrier(0);
+    Frag f;
+    const uint8_t* item = wo + ((size_t)Tc * nb + c) * IB;
+    if (FM == 1) load_q4b(item, lane, f);
+    else load_q6b(item, lane, f);
     reinterpret_cast<uint32_t*>(zero)[tid] = 0u;
     for (int i = b * 256 + tid; i < zn; i += gridDim.x * 256) zacc[i] = 0ull;
     const float m = lane < nsplit ? m0 : -INFINITY;
