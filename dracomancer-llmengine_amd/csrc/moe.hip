@@ -49,18 +49,19 @@ constexpr int XP_MAXV = 4;
 // fixed-point sums, a flag at [n_in] making the input NaN), formed in every
 // block; block 0 also stores the sum to xs_out (the residual of the expert
 // down launch).
+// The pointers the first loads need lead the arguments (the first 14
+// dwords arrive in SGPRs), and the flag is read by a vector load, so no
+// argument or flag load is waited for before the x and row requests.
 template <bool NORM, int PRES = 0>
-__global__ __launch_bounds__(256) void k_moe_logits(const float* __restrict__ x, const float* __restrict__ gi,
-                                                    int n_exp, int n_in, float* __restrict__ logits,
-                                                    const float* __restrict__ norm_w, float eps,
-                                                    float* __restrict__ xn_out, const float* __restrict__ pend,
-                                                    float* __restrict__ xs_out) {
+__global__ __launch_bounds__(256) void k_moe_logits(const float* __restrict__ x, const float* __restrict__ pend,
+                                                    const float* __restrict__ norm_w, const float* __restrict__ gi,
+                                                    int n_in, int n_exp, float* __restrict__ logits, float eps,
+                                                    float* __restrict__ xn_out, float* __restrict__ xs_out) {
     __shared__ float part[4], sq[4];
     constexpr int U = 4;
     const int e = blockIdx.x, tid = threadIdx.x;
     const float* w = gi + (size_t)e * n_in;
     float acc = 0.f;
-    const long long pflag = PRES == 2 ? reinterpret_cast<const long long*>(pend)[n_in] : 0;
     for (int i0 = tid * 4; i0 < n_in; i0 += U * 1024) {
         float4 a[U], b[U], nw[U], p0[U], p1[U];
         longlong2 q0[PRES == 2 ? U : 1], q1[PRES == 2 ? U : 1];
@@ -81,6 +82,9 @@ __global__ __launch_bounds__(256) void k_moe_logits(const float* __restrict__ x,
                 q1[u] = A[1];
             }
         }
+        // the flag after the batch's loads (a vector load: it is waited for
+        // where it is used, behind them)
+        const long long pflag = PRES == 2 ? load_flag(reinterpret_cast<const long long*>(pend) + n_in) : 0;
         if (PRES) {
 #pragma unroll
             for (int u = 0; u < U; u++) {
@@ -675,18 +679,18 @@ int draco_moe_logits_launch(const float* x, const float* gate_inp, int n_exp, in
     if (norm_w) {
         if (n_in > 4096 || !xn_out) return -1;
         if (pend && pend_fx)
-            hipLaunchKernelGGL((k_moe_logits<true, 2>), dim3(n_exp), dim3(256), 0, st, x, gate_inp, n_exp, n_in,
-                               logits, norm_w, eps, xn_out, pend, xs_out);
+            hipLaunchKernelGGL((k_moe_logits<true, 2>), dim3(n_exp), dim3(256), 0, st, x, pend, norm_w, gate_inp,
+                               n_in, n_exp, logits, eps, xn_out, xs_out);
         else if (pend)
-            hipLaunchKernelGGL((k_moe_logits<true, 1>), dim3(n_exp), dim3(256), 0, st, x, gate_inp, n_exp, n_in,
-                               logits, norm_w, eps, xn_out, pend, xs_out);
+            hipLaunchKernelGGL((k_moe_logits<true, 1>), dim3(n_exp), dim3(256), 0, st, x, pend, norm_w, gate_inp,
+                               n_in, n_exp, logits, eps, xn_out, xs_out);
         else
-            hipLaunchKernelGGL((k_moe_logits<true>), dim3(n_exp), dim3(256), 0, st, x, gate_inp, n_exp, n_in, logits,
-                               norm_w, eps, xn_out, nullptr, nullptr);
+            hipLaunchKernelGGL((k_moe_logits<true>), dim3(n_exp), dim3(256), 0, st, x, nullptr, norm_w, gate_inp,
+                               n_in, n_exp, logits, eps, xn_out, nullptr);
         return 0;
     }
-    hipLaunchKernelGGL((k_moe_logits<false>), dim3(n_exp), dim3(256), 0, st, x, gate_inp, n_exp, n_in, logits,
-                       nullptr, 0.f, nullptr, nullptr, nullptr);
+    hipLaunchKernelGGL((k_moe_logits<false>), dim3(n_exp), dim3(256), 0, st, x, nullptr, nullptr, gate_inp, n_in,
+                       n_exp, logits, 0.f, nullptr, nullptr);
     return 0;
 }
 
