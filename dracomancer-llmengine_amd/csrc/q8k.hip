@@ -147,8 +147,8 @@ __global__ __launch_bounds__(64 * NW) void k_dq8(const Q8Launch a) {
 
     auto load = [&](int T, int b, Frag& f) {
         const uint8_t* p = a.base + ((size_t)(T + a.tile0) * nb + b) * IB;
-        if (FM == 1) load_q4b(p, lane, f);
-        else load_q6b(p, lane, f);
+        if (FM == 1) load_q4(p, lane, f);
+        else load_q6(p, lane, f);
     };
     Frag P0, P1;
     int ct = bx, cb = w, cp = 0;
