@@ -343,18 +343,23 @@ __global__ __launch_bounds__(64 * NW) void k_gdn_scan(const GdnArgs a) {
 // (fp32 rounding).  Outputs as k_gdn_scan's split form: ON and the 16
 // per-wave sums of squares in PSS.  Tails: a v channel's by its wave, the
 // q / k channels' by the head's last reader (g_qk_cnt).
+// The prologue's operands come first as scalars the dispatcher preloads into
+// SGPRs (a struct argument is never preloaded).
 template <int NW>
-__global__ __launch_bounds__(64 * NW) void k_gdn_dec(const GdnArgs a) {
+__global__ __launch_bounds__(64 * NW) void k_gdn_dec(float* __restrict__ pS, const float* __restrict__ pconv,
+                                                     float* __restrict__ ptail, const float* __restrict__ pqkv,
+                                                     const float* __restrict__ pglog, int pnhq, int pnvh,
+                                                     const float* __restrict__ pZ, const GdnArgs a) {
     constexpr int CPW = 8, KQ = 8, RPL = SV / KQ;
     __shared__ float qk[NW][2 * SV];
     __shared__ float cvs[NW][CPW];
     const int h = blockIdx.x, lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int wg = blockIdx.y * NW + w;
-    const int NHQ = a.nhq, n_vh = a.n_vh;
+    const int NHQ = pnhq, n_vh = pnvh;
     const int j = h % NHQ;
     // every load first: gates' dots, conv weights / tails / inputs of the 5
     // channels, z, norm weight and the state slice
-    const float gdb = a.glog[h], gda = a.glog[n_vh + h];
+    const float gdb = pglog[h], gda = pglog[n_vh + h];
     int ch[5];
     ch[0] = j * SV + lane;
     ch[1] = ch[0] + 64;
@@ -364,20 +369,20 @@ __global__ __launch_bounds__(64 * NW) void k_gdn_dec(const GdnArgs a) {
     float w0[5], w1[5], w2[5], w3[5], t0[5], t1[5], t2[5], xi[5];
 #pragma unroll
     for (int r = 0; r < 5; r++) {
-        const float4 cw = ld4(a.conv + (size_t)ch[r] * 4);
+        const float4 cw = ld4(pconv + (size_t)ch[r] * 4);
         w0[r] = cw.x;
         w1[r] = cw.y;
         w2[r] = cw.z;
         w3[r] = cw.w;
-        t0[r] = a.tail[(size_t)ch[r] * 3];
-        t1[r] = a.tail[(size_t)ch[r] * 3 + 1];
-        t2[r] = a.tail[(size_t)ch[r] * 3 + 2];
-        xi[r] = a.QKV[ch[r]];
+        t0[r] = ptail[(size_t)ch[r] * 3];
+        t1[r] = ptail[(size_t)ch[r] * 3 + 1];
+        t2[r] = ptail[(size_t)ch[r] * 3 + 2];
+        xi[r] = pqkv[ch[r]];
     }
     const int vl = lane / KQ, kq = lane % KQ, v = CPW * wg + vl;
-    float* Sh = a.S + (size_t)h * SV * SV;
+    float* Sh = pS + (size_t)h * SV * SV;
     const float nw = a.ssm_norm[v];
-    const float z = a.Z[(size_t)h * SV + v];
+    const float z = pZ[(size_t)h * SV + v];
     float s[RPL];
 #pragma unroll
     for (int i = 0; i < RPL; i++) s[i] = Sh[(size_t)(RPL * kq + i) * SV + v];
@@ -450,9 +455,9 @@ __global__ __launch_bounds__(64 * NW) void k_gdn_dec(const GdnArgs a) {
 #pragma unroll
     for (int r = 0; r < 5; r++)
         if (r == 4 ? lane < CPW : own_qk) {
-            a.tail[(size_t)ch[r] * 3] = t1[r];
-            a.tail[(size_t)ch[r] * 3 + 1] = t2[r];
-            a.tail[(size_t)ch[r] * 3 + 2] = xi[r];
+            ptail[(size_t)ch[r] * 3] = t1[r];
+            ptail[(size_t)ch[r] * 3 + 1] = t2[r];
+            ptail[(size_t)ch[r] * 3 + 2] = xi[r];
         }
 }
 
@@ -484,8 +489,12 @@ int launch_scan(const GdnArgs& a, int nspl, hipStream_t st) {
     int np = 16;
     if (DEC && nspl == 8 && a.glog && g_dec_waves) {
         // the barrier-free decode step: 16 waves per V head in blocks of 1 or 2
-        if (g_dec_waves == 1) hipLaunchKernelGGL(k_gdn_dec<1>, dim3(a.n_vh, 16), dim3(64), 0, st, a);
-        else hipLaunchKernelGGL(k_gdn_dec<2>, dim3(a.n_vh, 8), dim3(128), 0, st, a);
+        if (g_dec_waves == 1)
+            hipLaunchKernelGGL(k_gdn_dec<1>, dim3(a.n_vh, 16), dim3(64), 0, st, a.S, a.conv, a.tail, a.QKV, a.glog,
+                               a.nhq, a.n_vh, a.Z, a);
+        else
+            hipLaunchKernelGGL(k_gdn_dec<2>, dim3(a.n_vh, 8), dim3(128), 0, st, a.S, a.conv, a.tail, a.QKV, a.glog,
+                               a.nhq, a.n_vh, a.Z, a);
     } else if (DEC || nspl == 1) {
         switch (nspl) {
         case 1: hipLaunchKernelGGL((k_gdn_scan<DEC, 8, 1>), g, dim3(512), 0, st, a); return 0;

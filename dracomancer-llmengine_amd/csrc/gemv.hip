@@ -275,7 +275,9 @@ __global__ __launch_bounds__(64 * NW) void k_dq(const float* __restrict__ ax, co
     // a contribution was not finite)
     longlong2 pq[NORM == 4 ? 2 : 1];
     long long pflag = 0;
-    // NORM 2 (GNORM): the group partials [n_in / 128][64] = a.kc (16 used)
+    // NORM 2 (GNORM): the group partials [n_in / 128][64] (16 used), passed in
+    // the preloaded aacc slot (the launch's a.kc; GNORM launches have no
+    // accumulator)
     // NORM 3 (PRES): the pending residual's two split-K partials at aacc
     // ([2][n_in]); x = (x + p0) + p1, written to a.xn_out by block 0
     float4 pv0[NORM == 2 || NORM == 3 ? XP_MAXV : 1], pv1[NORM == 2 || NORM == 3 ? XP_MAXV : 1],
@@ -302,7 +304,7 @@ __global__ __launch_bounds__(64 * NW) void k_dq(const float* __restrict__ ax, co
                 pv1[q] = ld4(aacc + n_in + 4 * i4);
             }
             if constexpr (NORM == 2) {
-                const float* pp = a.kc + ((4 * i4) >> 7) * 64;
+                const float* pp = aacc + ((4 * i4) >> 7) * 64;
                 pv0[q] = ld4(pp);
                 pv1[q] = ld4(pp + 4);
                 pv2[q] = ld4(pp + 8);
@@ -1261,7 +1263,8 @@ void launch_dq1(SegLaunch& a, int grid, hipStream_t st) {
     });
     const SegKArgs k = seg_kargs(a, false);
     hipLaunchKernelGGL((k_dq<NW, FM, DUAL, MULTI, EPI, NORM, IPT1, KS, GD>), dim3(grid), dim3(64 * NW),
-                       dq_lds_bytes(a.n_in, NW), st, k.x, k.norm_w, k.am_val, k.n_in, k.total_tiles, k.rot, grid,
+                       dq_lds_bytes(a.n_in, NW), st, k.x, k.norm_w, NORM == 2 ? k.kc : k.am_val, k.n_in,
+                       k.total_tiles, k.rot, grid,
                        k.seg[0].base, k.seg[0].first, k.seg[0].tile0, k);
 }
 
