@@ -839,25 +839,27 @@ __global__ __launch_bounds__(256) void k_fa_prep(const float* __restrict__ QG, f
 // kin[t] into kc row r and copies v head g of vin[t] into vc row r.  The
 // rope's cos / sin come from cs_tab row p (64 floats: the reference's
 // (float)pos * rope_inv[t] angle, computed on the host).
-__global__ __launch_bounds__(256) void k_fa_prep_rows(const float* __restrict__ QG, int qg_stride,
-                                                      float* __restrict__ Qr, const float* __restrict__ kin,
-                                                      const float* __restrict__ vin, float* __restrict__ kc,
-                                                      float* __restrict__ vc, const float* __restrict__ qn,
-                                                      const float* __restrict__ kn,
-                                                      const float* __restrict__ cs_tab, const int* __restrict__ state,
-                                                      int pos0, int row0, int NH) {
+// The operands of the first loads lead the arguments (the first 14 dwords
+// arrive in SGPRs); the head's value, its norm weight and the v value are
+// requested before the position is read from the state, whose rope row
+// follows (the one dependent load).
+__global__ __launch_bounds__(256) void k_fa_prep_rows(const float* __restrict__ QG, const float* __restrict__ kin,
+                                                      const float* __restrict__ vin, const float* __restrict__ qn,
+                                                      const float* __restrict__ kn, const int* __restrict__ state,
+                                                      int qg_stride, int NH, const float* __restrict__ cs_tab,
+                                                      float* __restrict__ Qr, float* __restrict__ kc,
+                                                      float* __restrict__ vc, int pos0, int row0) {
     __shared__ float red[4];
     const int b = blockIdx.x, tok = blockIdx.y, t = threadIdx.x, lane = t & 63, w = t >> 6;
-    const int pos = (state ? state[0] : pos0) + tok, row = (state ? state[1] : row0) + tok;
     const bool isq = b < NH;
     const int g = b - NH;
-    // every operand requested before the first wait (one memory round trip):
-    // the head's value, its norm weight, the rope row (every wave; wave 0
-    // uses it) and, for q blocks too, a v value (k blocks copy it)
     const float* xp = isq ? QG + (size_t)tok * qg_stride + (size_t)b * 512 : kin + (size_t)tok * 512 + g * 256;
     const float* vp = vin + (size_t)tok * 512 + (isq ? 0 : g * 256);
-    const float* cs = cs_tab + (size_t)pos * 64;
     const float x = xp[t], nwt = (isq ? qn : kn)[t], vv = vp[t];
+    // state[0..1] in one 8-byte load (the device state array is 8-byte aligned)
+    const int2 pr = state ? *reinterpret_cast<const int2*>(state) : make_int2(pos0, row0);
+    const int pos = pr.x + tok, row = pr.y + tok;
+    const float* cs = cs_tab + (size_t)pos * 64;
     const float c = cs[2 * (lane & 31)], sn = cs[2 * (lane & 31) + 1];
     if (!isq) vc[(size_t)row * 512 + g * 256 + t] = vv;
     const float s = wave_sum(x * x);
@@ -1202,8 +1204,8 @@ void dk_fa_prep(const float* QG, float* Qr, const float* kin, float* kout, const
 void dk_fa_prep_rows(const float* QG, int qg_stride, float* Qr, const float* kin, const float* vin, float* kc,
                      float* vc, const float* qn, const float* kn, const float* cs_tab, const int* state, int pos0,
                      int row0, int NH, int T, hipStream_t st) {
-    hipLaunchKernelGGL(k_fa_prep_rows, dim3(NH + 2, T), dim3(256), 0, st, QG, qg_stride, Qr, kin, vin, kc, vc, qn, kn,
-                       cs_tab, state, pos0, row0, NH);
+    hipLaunchKernelGGL(k_fa_prep_rows, dim3(NH + 2, T), dim3(256), 0, st, QG, kin, vin, qn, kn, state, qg_stride, NH,
+                       cs_tab, Qr, kc, vc, pos0, row0);
 }
 
 void dk_swiglu(float* g, const float* u, int n, hipStream_t st) {
