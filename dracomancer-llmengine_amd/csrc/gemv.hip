@@ -148,7 +148,7 @@ SegKArgs seg_kargs(const SegLaunch& a, bool q80) {
 // the "up" half of a SwiGLU pair) hold 1 << 30, so three comparisons against
 // kernel-argument values (loaded once, kept in SGPRs) replace a loop.
 __device__ __forceinline__ int seg_of_tile(const SegKArgs& a, int T) {
-    return (T >= a.seg[1].first) + (T >= a.seg[2].first) + (T >= a.seg[3].first);
+    return (T >= a.seg[1].first) + (T >= a.seg[2].first);  // k_dq launches have at most 3 segments
 }
 
 // Fields of segment si picked with selects over compile-time indices (no
@@ -159,6 +159,16 @@ __device__ __forceinline__ auto seg_pick(const SegKArgs& a, int si, F f) -> decl
     if (si == 1) r = f(a.seg[1]);
     if (si == 2) r = f(a.seg[2]);
     if (si == 3) r = f(a.seg[3]);
+    return r;
+}
+
+// k_dq's pick: at most 3 segments (seg_launch_dq refuses more), so the
+// fields of a fourth are never loaded
+template <class F>
+__device__ __forceinline__ auto seg_pick3(const SegKArgs& a, int si, F f) -> decltype(f(a.seg[0])) {
+    auto r = f(a.seg[0]);
+    if (si == 1) r = f(a.seg[1]);
+    if (si == 2) r = f(a.seg[2]);
     return r;
 }
 
@@ -235,15 +245,15 @@ __global__ __launch_bounds__(64 * NW) void k_dq(const float* __restrict__ ax, co
     auto tile_ref = [&](int T) {
         if (KS) T -= khalf(T) * arot;
         const int si = MULTI ? seg_of_tile(a, T) : 0;
-        const bool q4 = FM == 3 ? seg_pick(a, si, [](const SegK& d) { return d.code; }) == DRACO_Q4_K : FM == 1;
+        const bool q4 = FM == 3 ? seg_pick3(a, si, [](const SegK& d) { return d.code; }) == DRACO_Q4_K : FM == 1;
         const size_t ib = FM == 4 ? DRACO_Q5T_ITEM : (q4 ? DRACO_Q4T_ITEM : DRACO_Q6T_ITEM);
         // segment 0's fields from the preloaded arguments
-        const int tl = T - (si == 0 ? afirst0 : seg_pick(a, si, [](const SegK& d) { return d.first; })) +
-                       (si == 0 ? atile00 : seg_pick(a, si, [](const SegK& d) { return d.tile0; }));
+        const int tl = T - (si == 0 ? afirst0 : seg_pick3(a, si, [](const SegK& d) { return d.first; })) +
+                       (si == 0 ? atile00 : seg_pick3(a, si, [](const SegK& d) { return d.tile0; }));
         const size_t off = (size_t)tl * nb * ib;
         TileRef r;
-        r.p = (si == 0 ? abase0 : seg_pick(a, si, [](const SegK& d) { return d.base; })) + off;
-        r.p2 = DUAL ? seg_pick(a, si + 1, [](const SegK& d) { return d.base; }) + off : r.p;
+        r.p = (si == 0 ? abase0 : seg_pick3(a, si, [](const SegK& d) { return d.base; })) + off;
+        r.p2 = DUAL ? seg_pick3(a, si + 1, [](const SegK& d) { return d.base; }) + off : r.p;
         r.q4 = q4;
         return r;
     };
@@ -499,20 +509,20 @@ __global__ __launch_bounds__(64 * NW) void k_dq(const float* __restrict__ ax, co
         if (cp == 0) {
             const int si = MULTI ? seg_of_tile(a, ct) : 0;
             if constexpr (EPI == EPI_QKV) c_epi = si == 0 ? EPI_ROPE_Q : (si == 1 ? EPI_ROPE_K : EPI_V_APPEND);
-            else c_epi = EPI != EPI_RT ? EPI : seg_pick(a, si, [](const SegK& d) { return d.epi; });
-            c_row = (ct - khalf(ct) * arot - seg_pick(a, si, [](const SegK& d) { return d.first; }) +
-                     seg_pick(a, si, [](const SegK& d) { return d.tile0; })) * 16;
-            c_r0 = seg_pick(a, si, [](const SegK& d) { return d.row0; });
-            c_r1 = seg_pick(a, si, [](const SegK& d) { return d.row1; });
-            c_y = seg_pick(a, si, [](const SegK& d) { return d.y; }) + (KS ? (size_t)khalf(ct) * a.kv_dim : 0);
-            if (FM == 3) cq4 = seg_pick(a, si, [](const SegK& d) { return d.code; }) == DRACO_Q4_K;
+            else c_epi = EPI != EPI_RT ? EPI : seg_pick3(a, si, [](const SegK& d) { return d.epi; });
+            c_row = (ct - khalf(ct) * arot - seg_pick3(a, si, [](const SegK& d) { return d.first; }) +
+                     seg_pick3(a, si, [](const SegK& d) { return d.tile0; })) * 16;
+            c_r0 = seg_pick3(a, si, [](const SegK& d) { return d.row0; });
+            c_r1 = seg_pick3(a, si, [](const SegK& d) { return d.row1; });
+            c_y = seg_pick3(a, si, [](const SegK& d) { return d.y; }) + (KS ? (size_t)khalf(ct) * a.kv_dim : 0);
+            if (FM == 3) cq4 = seg_pick3(a, si, [](const SegK& d) { return d.code; }) == DRACO_Q4_K;
             if (tid < 16) {
-                const int n_out = seg_pick(a, si, [](const SegK& d) { return d.n_out; });
+                const int n_out = seg_pick3(a, si, [](const SegK& d) { return d.n_out; });
                 const int row = c_row + tid;
                 const int rr = row < n_out ? row : n_out - 1;
                 const float* src = nullptr;
                 if (c_epi == EPI_RESID) {
-                    src = seg_pick(a, si, [](const SegK& d) { return d.yadd; }) + rr;
+                    src = seg_pick3(a, si, [](const SegK& d) { return d.yadd; }) + rr;
                 } else if ((c_epi == EPI_ROPE_Q || c_epi == EPI_ROPE_K) && rr % a.head_dim < arot) {
                     src = a.rope_tab + ((size_t)pos * (arot / 2) + (rr % a.head_dim) / 2) * 2;
                 }
@@ -1419,6 +1429,7 @@ int seg_launch_dq(SegLaunch& a, hipStream_t st) {
     }
     a.total_tiles = tiles;
     const int grid = sh.grid;
+    if (a.nseg > 3) return -1;  // k_dq picks among 3 segments
     a.gdot_done = sh.gd;
     if (sh.ks) {
         // tiles [0, tiles) take each row's first half, [tiles, 2 tiles) the second
