@@ -11,8 +11,9 @@ events on the decode stream).  configs2_prefill reports the prompt's chunked
 prefill time (and the token-serial time of the same prompt for scale).
 
 roofline: the Q4_K GEMV of configs[1] (W 14336x4096 from seed 1, fp32 x),
-one HIP event pair around a graph replay of 200 launches rotating 10
-distinct weight copies (330 MB > the 256 MB MALL).  decode_roofline: the
+one HIP event pair around each graph replay of 200 launches rotating 10
+distinct weight copies (330 MB > the 256 MB MALL), the median of five
+replays after a warm one.  decode_roofline: the
 configs[2] decode's bytes per token x tok/s against the same HBM peak.
 Further legs: configs[0], [1], [3] and [4] (see each function).
 
@@ -57,7 +58,8 @@ def q4k_gemv_roofline(lib, n_copies=10, iters=200):
 
     Average launch duration = one HIP event pair around a graph replay of
     `iters` launches rotating over `n_copies` weight copies (330 MB > the
-    256 MB MALL), so kernels run back to back on the launch stream.  The
+    256 MB MALL), so kernels run back to back on the launch stream; the
+    median of five replays after a warm one.  The
     other configs[1] shape (4096x14336, fp32 x) is timed the same way and
     reported under "other_shape"; the top-level figures are the 14336x4096
     launch's.

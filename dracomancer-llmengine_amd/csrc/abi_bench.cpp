@@ -23,9 +23,10 @@ extern "C" {
 // out[1] us per launch from one event pair around the whole loop
 // out[2] min us, out[3] median us (per-launch pairs)
 // out[4] us per launch of the same `iters` launches captured in a HIP graph
-//        and replayed (one event pair around the replay): back-to-back
-//        kernels with no host gaps, the figure comparable to a profiler's
-//        per-kernel duration.  `out` holds at least 5 floats.
+//        and replayed (one event pair around each replay; the median of
+//        five replays after a warm one): back-to-back kernels with no host
+//        gaps, the figure comparable to a profiler's per-kernel duration.
+//        `out` holds at least 5 floats.
 int draco_bench_gemv(int code, const uint8_t* W, int n_out, int n_in, int n_copies, int iters,
                      float* out) {
     std::lock_guard<std::recursive_mutex> g(api_mutex());
@@ -78,12 +79,16 @@ int draco_bench_gemv(int code, const uint8_t* W, int n_out, int n_in, int n_copi
     DRACO_HIP(hipStreamEndCapture(st, &graph));
     DRACO_HIP(hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0));
     DRACO_HIP(hipGraphLaunch(exec, st));  // warm
-    DRACO_HIP(hipEventRecord(ev[0], st));
-    DRACO_HIP(hipGraphLaunch(exec, st));
-    DRACO_HIP(hipEventRecord(ev[1], st));
-    DRACO_HIP(hipStreamSynchronize(st));
-    float gms = 0;
-    DRACO_HIP(hipEventElapsedTime(&gms, ev[0], ev[1]));
+    float reps[5];
+    for (int r = 0; r < 5; r++) {
+        DRACO_HIP(hipEventRecord(ev[0], st));
+        DRACO_HIP(hipGraphLaunch(exec, st));
+        DRACO_HIP(hipEventRecord(ev[1], st));
+        DRACO_HIP(hipStreamSynchronize(st));
+        DRACO_HIP(hipEventElapsedTime(&reps[r], ev[0], ev[1]));
+    }
+    std::sort(reps, reps + 5);
+    const float gms = reps[2];
     hipGraphExecDestroy(exec);
     hipGraphDestroy(graph);
     // calibration for hardware byte counters: one device-to-device copy of a
