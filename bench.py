@@ -42,9 +42,9 @@ import numpy as np  # noqa: E402
 PEAK_HBM_GBS = 8000.0
 # HBM bytes per launch of the roofline kernel from the FETCH_SIZE / WRITE_SIZE
 # counter passes (rocprofv3 --pmc, scaled by a device copy of known size:
-# 2046.5 B per FETCH_SIZE unit, 1024 B per WRITE_SIZE unit): 16291.2 * 2046.48
+# 2046.5 B per FETCH_SIZE unit, 1024 B per WRITE_SIZE unit): 16299.2 * 2046.48
 # + 56.0 * 1024 bytes (profiles/gemv_q4k_14336x4096_roofline.md)
-TRAFFIC_BYTES = 33396915
+TRAFFIC_BYTES = 33413287
 CTX_START = 960
 MAX_DECODE = 64  # positions 960..1023 (max_t 1024)
 
