@@ -504,6 +504,8 @@ __global__ __launch_bounds__(64 * NW) void k_dq(const float* __restrict__ ax, co
     float* c_y = nullptr;
     bool cq4 = FM != 2;
     float ep0 = 0.f, ep1 = 0.f;  // epilogue inputs, loaded at tile start (off the tile-end critical path)
+    constexpr bool RB2 = !DUAL && !MULTI && EPI == EPI_STORE && !IPT1 && !KS;
+    int rpar = 0;  // RB2: the half of red this tile's partials use
 
     auto step = [&](Frag& cur, Frag& nxt, Frag& cur2, Frag& nxt2) {
         if (cp == 0) {
@@ -572,8 +574,18 @@ __global__ __launch_bounds__(64 * NW) void k_dq(const float* __restrict__ ax, co
             float acc = aD - aM, acc2 = aD2 - aM2;
             acc = rows_sum(acc);
             if (DUAL) acc2 = rows_sum(acc2);
+            // RB2 (plain GEMV launches -- one store segment, several items per
+            // wave, no split-K: the drop-in GEMV calls): the tiles alternate
+            // between the two halves of red, so
+            // the next tile's partials never overwrite the half wave 0 is
+            // still summing: tile k + 2 reuses tile k's half only after tile
+            // k + 1's barrier, which wave 0 reaches once tile k's epilogue is
+            // done -- and the barrier after the epilogue goes (the 14336x4096
+            // launch 7.7-8.1 -> 7.5-7.8 us same-box; configs[2]'s decode launches
+            // measured 0.25-0.3% slower with it and keep the barrier)
+            float* rb = RB2 ? red + rpar * NW * 16 : red;
             if (lane < 16) {
-                red[w * 16 + j] = acc;
+                rb[w * 16 + j] = acc;
                 if (DUAL) red[(NW + w) * 16 + j] = acc2;
             }
             lds_barrier();
@@ -581,7 +593,7 @@ __global__ __launch_bounds__(64 * NW) void k_dq(const float* __restrict__ ax, co
                 float v = 0.f, v2 = 0.f;
 #pragma unroll
                 for (int q = 0; q < NW; q++) {
-                    v += red[q * 16 + tid];
+                    v += rb[q * 16 + tid];
                     if (DUAL) v2 += red[(NW + q) * 16 + tid];
                 }
                 if (RMS) {
@@ -630,7 +642,8 @@ __global__ __launch_bounds__(64 * NW) void k_dq(const float* __restrict__ ax, co
                     break;
                 }
             }
-            lds_barrier();
+            if (!RB2) lds_barrier();
+            rpar ^= 1;
             aD = aM = aD2 = aM2 = 0.f;
         }
         cp++;
